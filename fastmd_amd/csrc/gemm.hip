@@ -1,0 +1,339 @@
+// (d) Wide edge GEMM on CDNA4 matrix cores.
+//
+// C[M,N] = A[M,K] * op(B) (+ bias) (+ C), fp32 output, MFMA accumulation in fp32:
+//   fp32: v_mfma_f32_32x32x2_f32   (A/B operands fp32; 157 TFLOP/s dense peak on MI355X)
+//   bf16: v_mfma_f32_32x32x16_bf16 (A/B operands bf16; 2.5 PFLOP/s dense peak)
+// Workgroup: 256 threads = 4 waves in a 2x2 arrangement; block tile 128x128, each wave owns a
+// 64x64 sub-tile (2x2 MFMA 32x32 blocks, 64 accumulator registers per lane). The K dimension
+// is staged through LDS in BK-wide slices; the next slice's global loads are issued before
+// the MFMAs of the current one (register double buffering). Any M, N, K (tails are zero-filled
+// in LDS), so K = 2F+8 (136, 264, 520) needs no padding by the caller.
+// MFMA operand layouts (32x32, one block):
+//   A operand: lane l holds A[l%32][k0 + (l/32)*KPL .. +KPL)   (KPL = 1 fp32 / 8 bf16)
+//   B operand: lane l holds B[k0 + (l/32)*KPL .. +KPL)[l%32]
+//   D: lane l, register v holds D[(v/4)*8 + (l/32)*4 + v%4][l%32]
+#include "common.h"
+
+namespace {
+
+constexpr int BM = 128, BN = 128, kThreads = 256;
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+template <typename Store>
+__device__ __forceinline__ void epilogue(const f32x16 (&acc)[2][2], int64_t row0, int64_t col0, int64_t m, int64_t n,
+                                         const float* bias, float* c, int64_t ldc, int accumulate, int act) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj) {
+      const int64_t col = col0 + bj * 32 + (lane & 31);
+      if (col >= n) continue;
+      const float b = bias ? bias[col] : 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = row0 + bi * 32 + (v / 4) * 8 + (lane / 32) * 4 + (v % 4);
+        if (row >= m) continue;
+        float x = acc[bi][bj][v] + b;
+        float* dst = c + row * ldc + col;
+        if (accumulate) x = *dst + x;
+        if (act == 1) x = silu(x);
+        *dst = x;
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------- fp32
+constexpr int BK32 = 16;
+constexpr int LDA32 = BM + 4;  // LDS row of one k: BM floats (+pad)
+
+// A tile [BM x BK] -> LDS As[k][i]; B tile -> Bs[k][j]
+template <int BLAYOUT>
+__global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restrict__ a, int64_t lda,
+                                                            const float* __restrict__ b, int64_t ldb,
+                                                            const float* __restrict__ bias, float* c, int64_t ldc,
+                                                            int64_t m, int64_t n, int64_t k, int accumulate, int act) {
+  __shared__ float As[BK32][LDA32];
+  __shared__ float Bs[BK32][LDA32];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t row_blk = (int64_t)blockIdx.x * BM, col_blk = (int64_t)blockIdx.y * BN;
+
+  // loader mapping: 128 rows x 16 k = 512 float4; 2 per thread
+  float4 ra[2], rb[2];
+  auto load_a = [&](int64_t k0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int id = t + q * kThreads;  // 0..511
+      const int r = id >> 2, kc = (id & 3) * 4;
+      const int64_t gr = row_blk + r, gk = k0 + kc;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (gr < m) {
+        const float* p = a + gr * lda + gk;
+        if (gk + 3 < k && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
+          v = *reinterpret_cast<const float4*>(p);
+        } else {
+          v.x = gk < k ? p[0] : 0.f;
+          v.y = gk + 1 < k ? p[1] : 0.f;
+          v.z = gk + 2 < k ? p[2] : 0.f;
+          v.w = gk + 3 < k ? p[3] : 0.f;
+        }
+      }
+      ra[q] = v;
+    }
+  };
+  auto load_b = [&](int64_t k0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int id = t + q * kThreads;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (BLAYOUT == 0) {  // B [N, K]: row j, 4 consecutive k
+        const int r = id >> 2, kc = (id & 3) * 4;
+        const int64_t gj = col_blk + r, gk = k0 + kc;
+        if (gj < n) {
+          const float* p = b + gj * ldb + gk;
+          if (gk + 3 < k && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
+            v = *reinterpret_cast<const float4*>(p);
+          } else {
+            v.x = gk < k ? p[0] : 0.f;
+            v.y = gk + 1 < k ? p[1] : 0.f;
+            v.z = gk + 2 < k ? p[2] : 0.f;
+            v.w = gk + 3 < k ? p[3] : 0.f;
+          }
+        }
+      } else {  // B [K, N]: row k, 4 consecutive j
+        const int kr = id >> 5, jc = (id & 31) * 4;
+        const int64_t gk = k0 + kr, gj = col_blk + jc;
+        if (gk < k) {
+          const float* p = b + gk * ldb + gj;
+          if (gj + 3 < n && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
+            v = *reinterpret_cast<const float4*>(p);
+          } else {
+            v.x = gj < n ? p[0] : 0.f;
+            v.y = gj + 1 < n ? p[1] : 0.f;
+            v.z = gj + 2 < n ? p[2] : 0.f;
+            v.w = gj + 3 < n ? p[3] : 0.f;
+          }
+        }
+      }
+      rb[q] = v;
+    }
+  };
+  auto store_tiles = [&]() {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int id = t + q * kThreads;
+      const int r = id >> 2, kc = (id & 3) * 4;
+      As[kc + 0][r] = ra[q].x;
+      As[kc + 1][r] = ra[q].y;
+      As[kc + 2][r] = ra[q].z;
+      As[kc + 3][r] = ra[q].w;
+      if (BLAYOUT == 0) {
+        Bs[kc + 0][r] = rb[q].x;
+        Bs[kc + 1][r] = rb[q].y;
+        Bs[kc + 2][r] = rb[q].z;
+        Bs[kc + 3][r] = rb[q].w;
+      } else {
+        const int kr = id >> 5, jc = (id & 31) * 4;
+        *reinterpret_cast<float4*>(&Bs[kr][jc]) = rb[q];
+      }
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int64_t nk = fmd_cdiv(k, BK32);
+  load_a(0);
+  load_b(0);
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    __syncthreads();
+    store_tiles();
+    __syncthreads();
+    if (kt + 1 < nk) {
+      load_a((kt + 1) * BK32);
+      load_b((kt + 1) * BK32);
+    }
+#pragma unroll
+    for (int kk = 0; kk < BK32; kk += 2) {
+      const int kr = kk + (lane >> 5);
+      float av[2], bv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) av[i] = As[kr][wm * 64 + i * 32 + (lane & 31)];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bv[j] = Bs[kr][wn * 64 + j * 32 + (lane & 31)];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  epilogue<int>(acc, row_blk + wm * 64, col_blk + wn * 64, m, n, bias, c, ldc, accumulate, act);
+}
+
+// ---------------------------------------------------------------------------------------- bf16
+constexpr int BK16 = 32;
+constexpr int LDK16 = BK16 + 8;  // bf16 elements per LDS row (+pad, keeps 16-byte alignment)
+
+template <int BLAYOUT>
+__global__ void __launch_bounds__(kThreads) gemm_bf16_kernel(const uint16_t* __restrict__ a, int64_t lda,
+                                                             const uint16_t* __restrict__ b, int64_t ldb,
+                                                             const float* __restrict__ bias, float* c, int64_t ldc,
+                                                             int64_t m, int64_t n, int64_t k, int accumulate,
+                                                             int act) {
+  // As[i][k], Bs[j][k]: k contiguous so a lane reads its 8 k values as one 16-byte load
+  __shared__ uint16_t As[BM][LDK16];
+  __shared__ uint16_t Bs[BN][LDK16];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t row_blk = (int64_t)blockIdx.x * BM, col_blk = (int64_t)blockIdx.y * BN;
+
+  // A: 128 rows x 32 k = 512 chunks of 8 bf16; 2 per thread
+  uint4 ra[2], rb[2];
+  auto load_rowmajor = [&](const uint16_t* base, int64_t ld, int64_t rows_total, int64_t r0, int64_t k0, uint4* out) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int id = t + q * kThreads;
+      const int r = id >> 2, kc = (id & 3) * 8;
+      const int64_t gr = r0 + r, gk = k0 + kc;
+      uint16_t e[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (gr < rows_total) {
+        const uint16_t* p = base + gr * ld + gk;
+        if (gk + 7 < k && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
+          out[q] = *reinterpret_cast<const uint4*>(p);
+          continue;
+        }
+#pragma unroll
+        for (int x = 0; x < 8; ++x) e[x] = (gk + x < k) ? p[x] : (uint16_t)0;
+      }
+      out[q] = make_uint4(e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16), e[4] | ((uint32_t)e[5] << 16),
+                          e[6] | ((uint32_t)e[7] << 16));
+    }
+  };
+  // B [K, N] (layout 1): 32 k rows x 128 j; each thread gathers 8 k of one j column
+  auto load_b_kn = [&](int64_t k0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int id = t + q * kThreads;
+      const int j = id >> 2, kc = (id & 3) * 8;
+      const int64_t gj = col_blk + j;
+      uint16_t e[8];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        const int64_t gk = k0 + kc + x;
+        e[x] = (gj < n && gk < k) ? b[gk * ldb + gj] : (uint16_t)0;
+      }
+      rb[q] = make_uint4(e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16), e[4] | ((uint32_t)e[5] << 16),
+                         e[6] | ((uint32_t)e[7] << 16));
+    }
+  };
+  auto store_tiles = [&]() {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int id = t + q * kThreads;
+      const int r = id >> 2, kc = (id & 3) * 8;
+      *reinterpret_cast<uint4*>(&As[r][kc]) = ra[q];
+      *reinterpret_cast<uint4*>(&Bs[r][kc]) = rb[q];
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int64_t nk = fmd_cdiv(k, BK16);
+  auto issue = [&](int64_t k0) {
+    load_rowmajor(a, lda, m, row_blk, k0, ra);
+    if (BLAYOUT == 0)
+      load_rowmajor(b, ldb, n, col_blk, k0, rb);
+    else
+      load_b_kn(k0);
+  };
+  issue(0);
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    __syncthreads();
+    store_tiles();
+    __syncthreads();
+    if (kt + 1 < nk) issue((kt + 1) * BK16);
+#pragma unroll
+    for (int kk = 0; kk < BK16; kk += 16) {
+      const int kc = kk + (lane >> 5) * 8;
+      bf16x8 av[2], bv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        uint4 raw = *reinterpret_cast<const uint4*>(&As[wm * 64 + i * 32 + (lane & 31)][kc]);
+        av[i] = __builtin_bit_cast(bf16x8, raw);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        uint4 raw = *reinterpret_cast<const uint4*>(&Bs[wn * 64 + j * 32 + (lane & 31)][kc]);
+        bv[j] = __builtin_bit_cast(bf16x8, raw);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  epilogue<int>(acc, row_blk + wm * 64, col_blk + wn * 64, m, n, bias, c, ldc, accumulate, act);
+}
+
+}  // namespace
+
+extern "C" {
+
+int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32_t b_layout, const float* bias,
+                 float* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int32_t accumulate, int32_t epilogue_kind,
+                 hipStream_t stream) {
+  FMD_REQUIRE(m >= 0 && n >= 0 && k >= 0 && c && ldc >= n);
+  FMD_REQUIRE(b_layout == 0 || b_layout == 1);
+  FMD_REQUIRE(epilogue_kind == 0 || epilogue_kind == 1);
+  if (m == 0 || n == 0) return FMD_OK;
+  FMD_REQUIRE(k == 0 || (a && b && lda >= k && ldb >= (b_layout == 0 ? k : n)));
+  FMD_REQUIRE(fmd_cdiv(m, BM) < (int64_t(1) << 31) && fmd_cdiv(n, BN) < 65536);
+  dim3 grid((unsigned)fmd_cdiv(m, BM), (unsigned)fmd_cdiv(n, BN));
+  if (b_layout == 0)
+    hipLaunchKernelGGL(gemm_f32_kernel<0>, grid, dim3(kThreads), 0, stream, a, lda, b, ldb, bias, c, ldc, m, n, k,
+                       accumulate, epilogue_kind);
+  else
+    hipLaunchKernelGGL(gemm_f32_kernel<1>, grid, dim3(kThreads), 0, stream, a, lda, b, ldb, bias, c, ldc, m, n, k,
+                       accumulate, epilogue_kind);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int32_t b_layout, const float* bias,
+                  float* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int32_t accumulate, int32_t epilogue_kind,
+                  hipStream_t stream) {
+  FMD_REQUIRE(m >= 0 && n >= 0 && k >= 0 && c && ldc >= n);
+  FMD_REQUIRE(b_layout == 0 || b_layout == 1);
+  FMD_REQUIRE(epilogue_kind == 0 || epilogue_kind == 1);
+  if (m == 0 || n == 0) return FMD_OK;
+  FMD_REQUIRE(k == 0 || (a && b && lda >= k && ldb >= (b_layout == 0 ? k : n)));
+  FMD_REQUIRE(fmd_cdiv(m, BM) < (int64_t(1) << 31) && fmd_cdiv(n, BN) < 65536);
+  dim3 grid((unsigned)fmd_cdiv(m, BM), (unsigned)fmd_cdiv(n, BN));
+  if (b_layout == 0)
+    hipLaunchKernelGGL(gemm_bf16_kernel<0>, grid, dim3(kThreads), 0, stream, a, lda, b, ldb, bias, c, ldc, m, n, k,
+                       accumulate, epilogue_kind);
+  else
+    hipLaunchKernelGGL(gemm_bf16_kernel<1>, grid, dim3(kThreads), 0, stream, a, lda, b, ldb, bias, c, ldc, m, n, k,
+                       accumulate, epilogue_kind);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,286 @@
+// (e) Nose-Hoover chain velocity Verlet (ASE NoseHooverChainNVT) on the float64 state.
+//
+// One workgroup integrates all atoms (no inter-block synchronization): the thermostat chain
+// is a handful of fp64 scalars in LDS that thread 0 advances (the other threads read the
+// momentum scale factor it publishes), and the only reduction, ke2 = sum(p*p/m), is formed per
+// thread in a fixed order, then over the wave by a butterfly and over the waves in wave order,
+// so every thread sees the same bits. The operation order follows ASE / the reference port
+// (gpu_nhc.py:315-425): p_eta_j sweeps backward, eta update, p scaling by exp(-delta p_eta0/Q0),
+// ke2 recomputed, p_eta_j sweep forward; per Suzuki-Yoshida coefficient, tloop times.
+// FP contraction is off (each op rounded like NumPy); exp is the HIP device library's.
+// Momenta live in registers (KPT <= 4 atoms per thread, no spills) up to 4096 atoms; beyond
+// that they are scaled in place in global memory (L2 resident) pass by pass.
+#pragma clang fp contract(off)
+
+#include "common.h"
+
+namespace {
+
+constexpr int kMaxChain = 8;
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / FMD_WAVE;
+
+// Thermostat chain in LDS; thread 0 advances it, the other threads read the scale factor.
+struct Chain {
+  double eta[kMaxChain], pe[kMaxChain], Q[kMaxChain];
+  double scale;
+  int M;
+};
+
+__device__ __forceinline__ double block_sum(double v, double* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & (FMD_WAVE - 1), wave = threadIdx.x / FMD_WAVE;
+  __syncthreads();  // red[] may still be read from the previous reduction
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  const int nw = (blockDim.x + FMD_WAVE - 1) / FMD_WAVE;
+  double s = red[0];
+  for (int w = 1; w < nw; ++w) s = s + red[w];
+  return s;
+}
+
+// ASE _integrate_p_eta_j (thread 0 only)
+__device__ __forceinline__ void p_eta_j(Chain& c, int j, double ke2, double kT, double ndof_kT, double delta2,
+                                        double neg_delta4) {
+  double pj = c.pe[j];
+  double s = 1.0;
+  const bool inner = j < c.M - 1;
+  if (inner) {
+    s = exp((neg_delta4 * c.pe[j + 1]) / c.Q[j + 1]);
+    pj = pj * s;
+  }
+  double g;
+  if (j == 0)
+    g = ke2 - ndof_kT;
+  else
+    g = (c.pe[j - 1] * c.pe[j - 1]) / c.Q[j - 1] - kT;
+  pj = pj + delta2 * g;
+  if (inner) pj = pj * s;
+  c.pe[j] = pj;
+}
+
+// Momentum storage: registers (KPT > 0) or global memory (KPT == 0).
+template <int KPT>
+struct Momenta {
+  double p[KPT > 0 ? KPT : 1][3];
+  double* gp;
+  const double* m;
+  int64_t n;
+
+  __device__ void load(double* p_ptr, const double* masses, int64_t n_atoms) {
+    gp = p_ptr;
+    m = masses;
+    n = n_atoms;
+    if constexpr (KPT > 0) {
+#pragma unroll
+      for (int r = 0; r < KPT; ++r) {
+        const int64_t a = threadIdx.x + (int64_t)r * blockDim.x;
+#pragma unroll
+        for (int d = 0; d < 3; ++d) p[r][d] = a < n ? p_ptr[3 * a + d] : 0.0;
+      }
+    }
+  }
+  template <typename F>
+  __device__ __forceinline__ void for_each(F f) {  // f(atom, double (&)[3] p)
+    if constexpr (KPT > 0) {
+#pragma unroll
+      for (int r = 0; r < KPT; ++r) {
+        const int64_t a = threadIdx.x + (int64_t)r * blockDim.x;
+        if (a < n) f(a, p[r]);
+      }
+    } else {
+      for (int64_t a = threadIdx.x; a < n; a += blockDim.x) {
+        double v[3] = {gp[3 * a], gp[3 * a + 1], gp[3 * a + 2]};
+        f(a, v);
+        gp[3 * a] = v[0];
+        gp[3 * a + 1] = v[1];
+        gp[3 * a + 2] = v[2];
+      }
+    }
+  }
+  __device__ void store() {
+    if constexpr (KPT > 0) {
+#pragma unroll
+      for (int r = 0; r < KPT; ++r) {
+        const int64_t a = threadIdx.x + (int64_t)r * blockDim.x;
+        if (a < n) {
+#pragma unroll
+          for (int d = 0; d < 3; ++d) gp[3 * a + d] = p[r][d];
+        }
+      }
+    }
+  }
+};
+
+template <int KPT>
+__device__ double ke2_of(Momenta<KPT>& mom, double* red) {
+  double s = 0.0;
+  mom.for_each([&](int64_t a, double (&p)[3]) {
+    const double m = mom.m[a];
+    s = s + (p[0] * p[0]) / m;
+    s = s + (p[1] * p[1]) / m;
+    s = s + (p[2] * p[2]) / m;
+  });
+  return block_sum(s, red);
+}
+
+// ASE integrate_nhc over half a time step.
+template <int KPT>
+__device__ void nhc_half(Momenta<KPT>& mom, Chain& c, const double* consts, int tloop, double* red) {
+  const double kT = consts[2], ndof_kT = consts[3];
+  const bool lead = threadIdx.x == 0;
+  double ke2 = ke2_of(mom, red);
+  for (int tl = 0; tl < tloop; ++tl) {
+    for (int k = 0; k < 3; ++k) {
+      const double delta = consts[4 + 4 * k], delta2 = consts[5 + 4 * k];
+      const double neg_delta4 = consts[6 + 4 * k], neg_delta = consts[7 + 4 * k];
+      if (lead) {
+        for (int jj = 0; jj < c.M; ++jj) p_eta_j(c, c.M - 1 - jj, ke2, kT, ndof_kT, delta2, neg_delta4);
+        for (int j = 0; j < c.M; ++j) c.eta[j] = c.eta[j] + (delta * c.pe[j]) / c.Q[j];
+        c.scale = exp((neg_delta * c.pe[0]) / c.Q[0]);
+      }
+      __syncthreads();
+      const double scale = c.scale;
+      mom.for_each([&](int64_t, double (&p)[3]) {
+        p[0] = p[0] * scale;
+        p[1] = p[1] * scale;
+        p[2] = p[2] * scale;
+      });
+      ke2 = ke2_of(mom, red);  // its barriers also order the read of c.scale before the next write
+      if (lead)
+        for (int j = 0; j < c.M; ++j) p_eta_j(c, j, ke2, kT, ndof_kT, delta2, neg_delta4);
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ void load_chain(Chain& c, int M, const double* eta, const double* pe,
+                                           const double* consts) {
+  if (threadIdx.x == 0) {
+    c.M = M;
+    for (int j = 0; j < kMaxChain; ++j) {
+      c.eta[j] = j < M ? eta[j] : 0.0;
+      c.pe[j] = j < M ? pe[j] : 0.0;
+      c.Q[j] = j < M ? consts[16 + j] : 1.0;
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ void store_chain(const Chain& c, double* eta, double* pe) {
+  if (threadIdx.x == 0) {
+    for (int j = 0; j < c.M; ++j) {
+      eta[j] = c.eta[j];
+      pe[j] = c.pe[j];
+    }
+  }
+}
+
+__device__ __forceinline__ double kick_of(double dt2, double f, int f32_kick) {
+  if (f32_kick) return (double)((float)dt2 * (float)f);
+  return dt2 * f;
+}
+
+template <int KPT>
+__global__ void __launch_bounds__(kThreads) nhc_pre_kernel(double* q, double* p, const double* f, const double* masses,
+                                                           double* eta, double* pe, const double* consts, int64_t n,
+                                                           int M, int tloop, int f32_kick) {
+  __shared__ double red[kWaves];
+  __shared__ Chain c;
+  load_chain(c, M, eta, pe, consts);
+  Momenta<KPT> mom;
+  mom.load(p, masses, n);
+  nhc_half(mom, c, consts, tloop, red);
+  const double dt = consts[0], dt2 = consts[1];
+  mom.for_each([&](int64_t a, double (&pv)[3]) {
+    const double m = masses[a];
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+      pv[d] = pv[d] + kick_of(dt2, f[3 * a + d], f32_kick);
+      q[3 * a + d] = q[3 * a + d] + (dt * pv[d]) / m;
+    }
+  });
+  mom.store();
+  store_chain(c, eta, pe);
+}
+
+template <int KPT>
+__global__ void __launch_bounds__(kThreads) nhc_post_kernel(double* p, const void* f_in, int f_in_64, double* f_cache,
+                                                            const double* masses, double* eta, double* pe,
+                                                            const double* consts, const void* e_in, int e_kind,
+                                                            double* e_out, int64_t n, int M, int tloop, int f32_kick) {
+  __shared__ double red[kWaves];
+  __shared__ Chain c;
+  load_chain(c, M, eta, pe, consts);
+  Momenta<KPT> mom;
+  mom.load(p, masses, n);
+  const double dt2 = consts[1];
+  mom.for_each([&](int64_t a, double (&pv)[3]) {
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+      const double fv = f_in_64 ? static_cast<const double*>(f_in)[3 * a + d]
+                                : (double)static_cast<const float*>(f_in)[3 * a + d];
+      pv[d] = pv[d] + kick_of(dt2, fv, f32_kick);
+      f_cache[3 * a + d] = fv;
+    }
+  });
+  nhc_half(mom, c, consts, tloop, red);
+  mom.store();
+  store_chain(c, eta, pe);
+  if (threadIdx.x == 0 && e_kind != 0)
+    e_out[0] = e_kind == 2 ? static_cast<const double*>(e_in)[0] : (double)static_cast<const float*>(e_in)[0];
+}
+
+int pick_kpt(int64_t n, int threads) {
+  const int64_t per = fmd_cdiv(n, threads);
+  if (per <= 1) return 1;
+  if (per <= 2) return 2;
+  if (per <= 4) return 4;
+  return 0;
+}
+
+int nhc_threads(int64_t n) {
+  int64_t t = fmd_cdiv(n, FMD_WAVE) * FMD_WAVE;
+  return (int)(t < kThreads ? (t < FMD_WAVE ? FMD_WAVE : t) : kThreads);
+}
+
+}  // namespace
+
+#define FMD_NHC_DISPATCH(KERNEL, ...)                                                                    \
+  switch (kpt) {                                                                                         \
+    case 1: hipLaunchKernelGGL(KERNEL<1>, dim3(1), dim3(threads), 0, stream, __VA_ARGS__); break;       \
+    case 2: hipLaunchKernelGGL(KERNEL<2>, dim3(1), dim3(threads), 0, stream, __VA_ARGS__); break;       \
+    case 4: hipLaunchKernelGGL(KERNEL<4>, dim3(1), dim3(threads), 0, stream, __VA_ARGS__); break;       \
+    default: hipLaunchKernelGGL(KERNEL<0>, dim3(1), dim3(threads), 0, stream, __VA_ARGS__); break;      \
+  }
+
+extern "C" {
+
+int fmd_nhc_pre_force(double* q, double* p, const double* f, const double* masses, double* eta, double* p_eta,
+                      const double* consts, int64_t n_atoms, int32_t tchain, int32_t tloop, int32_t f32_kick,
+                      hipStream_t stream) {
+  FMD_REQUIRE(q && p && f && masses && eta && p_eta && consts && n_atoms > 0);
+  FMD_REQUIRE(tchain >= 1 && tchain <= kMaxChain && tloop >= 1);
+  const int threads = nhc_threads(n_atoms);
+  const int kpt = pick_kpt(n_atoms, threads);
+  FMD_NHC_DISPATCH(nhc_pre_kernel, q, p, f, masses, eta, p_eta, consts, n_atoms, tchain, tloop, f32_kick);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_nhc_post_force(double* p, const void* f_in, int32_t f_in_is_f64, double* f_cache, const double* masses,
+                       double* eta, double* p_eta, const double* consts, const void* e_in, int32_t e_kind,
+                       double* e_out, int64_t n_atoms, int32_t tchain, int32_t tloop, int32_t f32_kick,
+                       hipStream_t stream) {
+  FMD_REQUIRE(p && f_in && f_cache && masses && eta && p_eta && consts && n_atoms > 0);
+  FMD_REQUIRE(tchain >= 1 && tchain <= kMaxChain && tloop >= 1);
+  FMD_REQUIRE(e_kind == 0 || (e_in && e_out && (e_kind == 1 || e_kind == 2)));
+  const int threads = nhc_threads(n_atoms);
+  const int kpt = pick_kpt(n_atoms, threads);
+  FMD_NHC_DISPATCH(nhc_post_kernel, p, f_in, f_in_is_f64, f_cache, masses, eta, p_eta, consts, e_in, e_kind, e_out,
+                   n_atoms, tchain, tloop, f32_kick);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,833 @@
+// (a) Neighbour list of the GPU-resident MD step: candidate cell list (rare refresh path) and
+// the per-step exact re-filter build over the candidates (count -> scan -> materialize ->
+// pad -> flags), bit-exact against the CPU oracle.
+//
+// Arithmetic contract (shared with oracle/nl.py): every float32 operation below is a single
+// IEEE round-to-nearest operation in the written order, with no contraction into FMAs (this
+// file is compiled with -ffp-contract=off and the pragma below):
+//   frac_a   = (x*inv[0][a] + y*inv[1][a]) + z*inv[2][a]          (small_matmul, geometry.py:7-34)
+//   wrap_a   = floor(frac_a);  frac_a -= wrap_a
+//   wrapped_c = (f0*cell[0][c] + f1*cell[1][c]) + f2*cell[2][c]
+//   d_c      = (((p_j,c - p_i,c) + sx*cell[0][c]) + sy*cell[1][c]) + sz*cell[2][c]
+//   d2       = (dx*dx + dy*dy) + dz*dz,    edge iff d2 < rc2        (fixed_capacity_builder.py:163-171)
+// Candidates are stored per atom in ascending (neighbour, sx, sy, sz) order, so the rows the
+// build materializes at edge_offsets[i] + rank are already in the canonical (centre,
+// neighbour, image) order that the reference obtains with a global torch.sort
+// (fixed_capacity_builder.py:1968-1999): image = shift + wrap_delta[j] - wrap_delta[i] is a
+// per-neighbour constant offset of the shift, so the per-row order is preserved.
+#pragma clang fp contract(off)
+
+#include "common.h"
+
+namespace {
+
+constexpr int kSmallThreads = 1024;   // fused single-workgroup build
+constexpr int kSmallMaxAtoms = 1024;  // LDS-resident wrapped coordinates up to this many atoms
+constexpr int kBlock = 256;           // multi-block kernels: 4 waves, one atom per wave
+
+struct Mat3 {
+  float m[9];
+};
+
+__device__ __forceinline__ Mat3 load_mat3(const float* p) {
+  Mat3 r;
+#pragma unroll
+  for (int k = 0; k < 9; ++k) r.m[k] = p[k];
+  return r;
+}
+
+__device__ __forceinline__ void load_position(const void* positions, int is64, int64_t i, float& x,
+                                              float& y, float& z) {
+  if (is64) {
+    const double* p = static_cast<const double*>(positions) + 3 * i;
+    x = (float)p[0];
+    y = (float)p[1];
+    z = (float)p[2];
+  } else {
+    const float* p = static_cast<const float*>(positions) + 3 * i;
+    x = p[0];
+    y = p[1];
+    z = p[2];
+  }
+}
+
+// pos -> fractional coordinates in [0,1), integer wraps and the wrapped Cartesian position.
+__device__ __forceinline__ void wrap_position(float x, float y, float z, const Mat3& inv, const Mat3& cell,
+                                              float f[3], int w[3], float wr[3]) {
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    float t = x * inv.m[a];
+    t = t + y * inv.m[3 + a];
+    t = t + z * inv.m[6 + a];
+    float fl = floorf(t);
+    w[a] = (int)fl;
+    f[a] = t - fl;
+  }
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    float t = f[0] * cell.m[c];
+    t = t + f[1] * cell.m[3 + c];
+    t = t + f[2] * cell.m[6 + c];
+    wr[c] = t;
+  }
+}
+
+__device__ __forceinline__ float pair_d2(float xi, float yi, float zi, float xj, float yj, float zj, float sx,
+                                         float sy, float sz, const Mat3& cell) {
+  float dx = xj - xi;
+  dx = dx + sx * cell.m[0];
+  dx = dx + sy * cell.m[3];
+  dx = dx + sz * cell.m[6];
+  float dy = yj - yi;
+  dy = dy + sx * cell.m[1];
+  dy = dy + sy * cell.m[4];
+  dy = dy + sz * cell.m[7];
+  float dz = zj - zi;
+  dz = dz + sx * cell.m[2];
+  dz = dz + sy * cell.m[5];
+  dz = dz + sz * cell.m[8];
+  float d2 = dx * dx;
+  d2 = d2 + dy * dy;
+  d2 = d2 + dz * dz;
+  return d2;
+}
+
+__device__ __forceinline__ float displacement_norm(float x, float y, float z, const float* ref) {
+  float dx = x - ref[0], dy = y - ref[1], dz = z - ref[2];
+  float s = dx * dx;
+  s = s + dy * dy;
+  s = s + dz * dz;
+  return sqrtf(s);
+}
+
+// ------------------------------------------------------------------------------------------
+// wrap (refresh flavour)
+// ------------------------------------------------------------------------------------------
+__global__ void nl_wrap_kernel(const void* positions, int is64, const float* inv_cell, const float* cell,
+                               int64_t n, float* frac, int32_t* wraps, float* wrapped, float* ref_pos,
+                               int32_t* ref_wraps, int32_t* wrap_delta) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  Mat3 inv = load_mat3(inv_cell), cm = load_mat3(cell);
+  float x, y, z, f[3], wr[3];
+  int w[3];
+  load_position(positions, is64, i, x, y, z);
+  wrap_position(x, y, z, inv, cm, f, w, wr);
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    if (frac) frac[3 * i + a] = f[a];
+    if (wraps) wraps[3 * i + a] = w[a];
+    if (wrapped) wrapped[3 * i + a] = wr[a];
+    if (ref_wraps) ref_wraps[3 * i + a] = w[a];
+    if (wrap_delta) wrap_delta[3 * i + a] = 0;
+  }
+  if (ref_pos) {
+    ref_pos[3 * i] = x;
+    ref_pos[3 * i + 1] = y;
+    ref_pos[3 * i + 2] = z;
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// candidate cell list
+// ------------------------------------------------------------------------------------------
+__device__ __forceinline__ int cell_coord(float f, int nc) {
+  int c = (int)floorf(f * (float)nc);
+  c = c < 0 ? 0 : c;
+  return c >= nc ? nc - 1 : c;
+}
+
+__global__ void cells_reset_kernel(int32_t* cell_count, int64_t ncell, uint8_t* capacity_valid) {
+  int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c < ncell) cell_count[c] = 0;
+  if (c == 0) capacity_valid[0] = 1;
+}
+
+__global__ void cells_count_kernel(const float* frac, int64_t n, int n0, int n1, int n2, int32_t* cell_count) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int c0 = cell_coord(frac[3 * i], n0), c1 = cell_coord(frac[3 * i + 1], n1), c2 = cell_coord(frac[3 * i + 2], n2);
+  atomicAdd(&cell_count[(c0 * n1 + c1) * n2 + c2], 1);
+}
+
+// Exclusive scan of the cell counts (one workgroup); leaves the counts zeroed as cursors.
+__global__ void cells_scan_kernel(int32_t* cell_count, int32_t* cell_start, int64_t ncell) {
+  __shared__ int32_t partial[1024];
+  const int t = threadIdx.x, T = blockDim.x;
+  const int64_t chunk = fmd_cdiv(ncell, T);
+  const int64_t lo = t * chunk, hi = lo + chunk < ncell ? lo + chunk : ncell;
+  int32_t s = 0;
+  for (int64_t c = lo; c < hi; ++c) s += cell_count[c];
+  partial[t] = s;
+  __syncthreads();
+  if (t == 0) {
+    int32_t run = 0;
+    for (int k = 0; k < T; ++k) {
+      int32_t v = partial[k];
+      partial[k] = run;
+      run += v;
+    }
+    cell_start[ncell] = run;
+  }
+  __syncthreads();
+  int32_t run = partial[t];
+  for (int64_t c = lo; c < hi; ++c) {
+    int32_t v = cell_count[c];
+    cell_start[c] = run;
+    run += v;
+    cell_count[c] = 0;
+  }
+}
+
+__global__ void cells_place_kernel(const float* frac, int64_t n, int n0, int n1, int n2, int32_t* cursor,
+                                   const int32_t* cell_start, int32_t* cell_atoms) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int c0 = cell_coord(frac[3 * i], n0), c1 = cell_coord(frac[3 * i + 1], n1), c2 = cell_coord(frac[3 * i + 2], n2);
+  int cid = (c0 * n1 + c1) * n2 + c2;
+  int slot = atomicAdd(&cursor[cid], 1);
+  cell_atoms[cell_start[cid] + slot] = (int32_t)i;
+}
+
+__device__ __forceinline__ uint64_t cand_key(int32_t j, int sx, int sy, int sz) {
+  return ((uint64_t)(uint32_t)j << 24) | ((uint64_t)(sx + 128) << 16) | ((uint64_t)(sy + 128) << 8) |
+         (uint64_t)(sz + 128);
+}
+
+// One workgroup per atom: test every atom of the cells within reach (all periodic images),
+// collect the candidate keys in LDS, bitonic-sort them and write the row.
+__global__ void __launch_bounds__(256) cells_query_kernel(const float* wrapped, const float* frac, const float* cell,
+                                                          int64_t n, float cutoff2, int n0, int n1, int n2, int r0,
+                                                          int r1, int r2, int32_t bmax, int lcap,
+                                                          const int32_t* cell_start, const int32_t* cell_atoms,
+                                                          int32_t* neighbor_matrix, int32_t* neighbor_shifts,
+                                                          int32_t* num_neighbors, uint8_t* capacity_valid) {
+  extern __shared__ uint64_t keys[];
+  __shared__ int counter;
+  const int64_t i = blockIdx.x;
+  const int t = threadIdx.x;
+  if (t == 0) counter = 0;
+  __syncthreads();
+  Mat3 cm = load_mat3(cell);
+  const float xi = wrapped[3 * i], yi = wrapped[3 * i + 1], zi = wrapped[3 * i + 2];
+  const int c0 = cell_coord(frac[3 * i], n0), c1 = cell_coord(frac[3 * i + 1], n1), c2 = cell_coord(frac[3 * i + 2], n2);
+  const int span0 = 2 * r0 + 1, span1 = 2 * r1 + 1, span2 = 2 * r2 + 1;
+  const int noff = span0 * span1 * span2;
+  for (int q = t; q < noff; q += blockDim.x) {
+    const int d0 = q / (span1 * span2) - r0;
+    const int d1 = (q / span2) % span1 - r1;
+    const int d2 = q % span2 - r2;
+    int t0 = c0 + d0, t1 = c1 + d1, t2 = c2 + d2;
+    // floor division into (cell, image shift)
+    int s0 = (t0 >= 0) ? t0 / n0 : -((-t0 + n0 - 1) / n0);
+    int s1 = (t1 >= 0) ? t1 / n1 : -((-t1 + n1 - 1) / n1);
+    int s2 = (t2 >= 0) ? t2 / n2 : -((-t2 + n2 - 1) / n2);
+    t0 -= s0 * n0;
+    t1 -= s1 * n1;
+    t2 -= s2 * n2;
+    const int cid = (t0 * n1 + t1) * n2 + t2;
+    const float sx = (float)s0, sy = (float)s1, sz = (float)s2;
+    for (int p = cell_start[cid]; p < cell_start[cid + 1]; ++p) {
+      const int32_t j = cell_atoms[p];
+      if (j == i && s0 == 0 && s1 == 0 && s2 == 0) continue;
+      const float d2v = pair_d2(xi, yi, zi, wrapped[3 * j], wrapped[3 * j + 1], wrapped[3 * j + 2], sx, sy, sz, cm);
+      if (d2v < cutoff2) {
+        int slot = atomicAdd(&counter, 1);
+        if (slot < lcap) keys[slot] = cand_key(j, s0, s1, s2);
+      }
+    }
+  }
+  __syncthreads();
+  const int count = counter;
+  const int stored = count < lcap ? count : lcap;
+  int P = 1;
+  while (P < stored) P <<= 1;
+  for (int k = stored + t; k < P; k += blockDim.x) keys[k] = ~0ull;
+  __syncthreads();
+  // bitonic sort of keys[0, P)
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int k = t; k < P / 2; k += blockDim.x) {
+        const int lo = 2 * k - (k & (stride - 1));
+        const int hi = lo + stride;
+        const bool up = ((lo & size) == 0);
+        const uint64_t a = keys[lo], b = keys[hi];
+        if ((a > b) == up) {
+          keys[lo] = b;
+          keys[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  int32_t* nrow = neighbor_matrix + i * bmax;
+  int32_t* srow = neighbor_shifts + i * bmax * 3;
+  for (int s = t; s < bmax; s += blockDim.x) {
+    int32_t j = (int32_t)n;
+    int sx = 0, sy = 0, sz = 0;
+    if (s < stored) {
+      const uint64_t key = keys[s];
+      j = (int32_t)(key >> 24);
+      sx = (int)((key >> 16) & 0xff) - 128;
+      sy = (int)((key >> 8) & 0xff) - 128;
+      sz = (int)(key & 0xff) - 128;
+    }
+    nrow[s] = j;
+    srow[3 * s] = sx;
+    srow[3 * s + 1] = sy;
+    srow[3 * s + 2] = sz;
+  }
+  if (t == 0) {
+    num_neighbors[i] = count;
+    if (count > bmax) capacity_valid[0] = 0;
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// per-step build
+// ------------------------------------------------------------------------------------------
+struct BuildArgs {
+  const void* positions;
+  int pos64;
+  const float* inv_cell;
+  const float* cell;
+  int64_t n;
+  const int32_t* nbr;
+  const int32_t* shifts;
+  const int32_t* num;
+  int32_t bmax;
+  const float* ref_pos;
+  const int32_t* ref_wraps;
+  const uint8_t* capacity_valid;
+  float rc2;
+  float skin_limit;
+  int pad_ix, pad_iy, pad_iz;
+  int64_t e_cap;
+  int64_t* work;
+  float* frac;
+  int32_t* wrap_delta;
+  float* wrapped_out;
+  int64_t* edge_counts;
+  int64_t* edge_offsets;
+  int32_t* center;
+  int32_t* neighbor;
+  int32_t* images;
+  float* distances;
+  int32_t* edge_index;
+  float* edge_image;
+  float* max_disp;
+  uint8_t* cand_valid;
+  uint8_t* overflow;
+  int32_t* isolated;
+};
+
+__device__ __forceinline__ void write_row(const BuildArgs& a, int64_t row, int32_t c, int32_t j, int ix, int iy,
+                                          int iz, float dist, bool real) {
+  a.center[row] = c;
+  a.neighbor[row] = j;
+  a.images[3 * row] = ix;
+  a.images[3 * row + 1] = iy;
+  a.images[3 * row + 2] = iz;
+  if (real) a.distances[row] = dist;
+  if (a.edge_index) {
+    a.edge_index[2 * row] = c;
+    a.edge_index[2 * row + 1] = j;
+  }
+  if (a.edge_image) {
+    a.edge_image[3 * row] = (float)ix;
+    a.edge_image[3 * row + 1] = (float)iy;
+    a.edge_image[3 * row + 2] = (float)iz;
+  }
+}
+
+// Validity of candidate slot s of atom i, given the atom's wrapped position and wrap delta and
+// a functor giving (wrapped_j, wrap_delta_j).
+template <typename NeighborFn>
+__device__ __forceinline__ bool slot_edge(const BuildArgs& a, const Mat3& cm, int64_t i, int s, float xi, float yi,
+                                          float zi, const int wdi[3], NeighborFn nbr_state, int32_t& j, int img[3],
+                                          float& d2) {
+  j = a.nbr[i * a.bmax + s];
+  j = j < (int32_t)a.n - 1 ? j : (int32_t)a.n - 1;
+  const int32_t* sh = a.shifts + (i * a.bmax + s) * 3;
+  float xj, yj, zj;
+  int wdj[3];
+  nbr_state(j, xj, yj, zj, wdj);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) img[k] = sh[k] + wdj[k] - wdi[k];
+  d2 = pair_d2(xi, yi, zi, xj, yj, zj, (float)img[0], (float)img[1], (float)img[2], cm);
+  return d2 < a.rc2;
+}
+
+__device__ __forceinline__ void pad_rows(const BuildArgs& a, int64_t total, int64_t start, int64_t step) {
+  const int64_t ec = total < a.e_cap ? total : a.e_cap;
+  for (int64_t row = ec + start; row < a.e_cap; row += step) {
+    const int32_t atom = (int32_t)((row - ec) % a.n);
+    write_row(a, row, atom, atom, a.pad_ix, a.pad_iy, a.pad_iz, 0.f, false);
+  }
+}
+
+// Fused build of small systems in ONE workgroup (no inter-block dependency): prologue, counts,
+// scan, materialization, padding and flags, with the wrapped coordinates in LDS.
+__global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs a) {
+  __shared__ float s_pos[kSmallMaxAtoms * 3];
+  __shared__ int32_t s_wd[kSmallMaxAtoms * 3];
+  __shared__ int32_t s_cnt[kSmallMaxAtoms + 1];
+  __shared__ float s_red[kSmallThreads / FMD_WAVE];
+  __shared__ int32_t s_iso[kSmallThreads / FMD_WAVE];
+  __shared__ int32_t s_scan[kSmallThreads];
+  const int t = threadIdx.x, T = blockDim.x;
+  const int lane = t & (FMD_WAVE - 1), wave = t / FMD_WAVE, nwaves = T / FMD_WAVE;
+  const int n = (int)a.n;
+  Mat3 inv = load_mat3(a.inv_cell), cm = load_mat3(a.cell);
+
+  // (1) prologue
+  float dmax = 0.f;
+  for (int i = t; i < n; i += T) {
+    float x, y, z, f[3], wr[3];
+    int w[3];
+    load_position(a.positions, a.pos64, i, x, y, z);
+    wrap_position(x, y, z, inv, cm, f, w, wr);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const int wd = w[k] - a.ref_wraps[3 * i + k];
+      a.frac[3 * i + k] = f[k];
+      a.wrap_delta[3 * i + k] = wd;
+      if (a.wrapped_out) a.wrapped_out[3 * i + k] = wr[k];
+      s_pos[3 * i + k] = wr[k];
+      s_wd[3 * i + k] = wd;
+    }
+    dmax = nan_max(dmax, displacement_norm(x, y, z, a.ref_pos + 3 * i));
+  }
+  dmax = wave_nan_max(dmax);
+  if (lane == 0) s_red[wave] = dmax;
+  __syncthreads();
+
+  auto nbr_state = [&](int32_t j, float& xj, float& yj, float& zj, int wdj[3]) {
+    xj = s_pos[3 * j];
+    yj = s_pos[3 * j + 1];
+    zj = s_pos[3 * j + 2];
+    wdj[0] = s_wd[3 * j];
+    wdj[1] = s_wd[3 * j + 1];
+    wdj[2] = s_wd[3 * j + 2];
+  };
+
+  // (2) counts, one wave per atom
+  int iso = 0;
+  for (int i = wave; i < n; i += nwaves) {
+    const float xi = s_pos[3 * i], yi = s_pos[3 * i + 1], zi = s_pos[3 * i + 2];
+    const int wdi[3] = {s_wd[3 * i], s_wd[3 * i + 1], s_wd[3 * i + 2]};
+    int cnt = a.num[i];
+    cnt = cnt < a.bmax ? cnt : a.bmax;
+    int total = 0;
+    for (int base = 0; base < cnt; base += FMD_WAVE) {
+      const int s = base + lane;
+      bool e = false;
+      if (s < cnt) {
+        int32_t j;
+        int img[3];
+        float d2;
+        e = slot_edge(a, cm, i, s, xi, yi, zi, wdi, nbr_state, j, img, d2);
+      }
+      total += __popcll(__ballot(e));
+    }
+    if (lane == 0) {
+      s_cnt[i] = total;
+      a.edge_counts[i] = total;
+      iso += (total == 0);
+    }
+  }
+  if (lane == 0) s_iso[wave] = iso;
+  __syncthreads();
+
+  // (3) exclusive scan of the counts (chunk per thread, then a serial pass over the threads)
+  {
+    const int chunk = (n + T - 1) / T;
+    const int lo = t * chunk, hi = lo + chunk < n ? lo + chunk : n;
+    int s = 0;
+    for (int k = lo; k < hi; ++k) s += s_cnt[k];
+    s_scan[t] = s;
+    __syncthreads();
+    if (t == 0) {
+      int run = 0;
+      for (int k = 0; k < T; ++k) {
+        const int v = s_scan[k];
+        s_scan[k] = run;
+        run += v;
+      }
+      s_cnt[kSmallMaxAtoms] = run;
+      float m = s_red[0];
+      int isol = s_iso[0];
+      for (int k = 1; k < nwaves; ++k) {
+        m = nan_max(m, s_red[k]);
+        isol += s_iso[k];
+      }
+      const bool valid = (m * 2.0f <= a.skin_limit) && (a.capacity_valid[0] != 0);
+      a.max_disp[0] = m;
+      a.cand_valid[0] = valid ? 1 : 0;
+      a.overflow[0] = ((int64_t)run > a.e_cap || !valid) ? 1 : 0;
+      a.isolated[0] = isol;
+      a.edge_offsets[n] = run;
+    }
+    __syncthreads();
+    int run = s_scan[t];
+    for (int k = lo; k < hi; ++k) {
+      const int v = s_cnt[k];
+      s_cnt[k] = run;  // now the offset
+      a.edge_offsets[k] = run;
+      run += v;
+    }
+  }
+  __syncthreads();
+  const int64_t total = s_cnt[kSmallMaxAtoms];
+
+  // (4) materialize in candidate (= canonical) order
+  for (int i = wave; i < n; i += nwaves) {
+    const float xi = s_pos[3 * i], yi = s_pos[3 * i + 1], zi = s_pos[3 * i + 2];
+    const int wdi[3] = {s_wd[3 * i], s_wd[3 * i + 1], s_wd[3 * i + 2]};
+    int cnt = a.num[i];
+    cnt = cnt < a.bmax ? cnt : a.bmax;
+    int64_t row0 = s_cnt[i];
+    for (int base = 0; base < cnt; base += FMD_WAVE) {
+      const int s = base + lane;
+      bool e = false;
+      int32_t j = 0;
+      int img[3] = {0, 0, 0};
+      float d2 = 0.f;
+      if (s < cnt) e = slot_edge(a, cm, i, s, xi, yi, zi, wdi, nbr_state, j, img, d2);
+      const uint64_t m = __ballot(e);
+      const int64_t row = row0 + lane_prefix(m);
+      if (e && row < a.e_cap) write_row(a, row, (int32_t)i, j, img[0], img[1], img[2], sqrtf(d2), true);
+      row0 += __popcll(m);
+    }
+  }
+  // (5) padding rows
+  pad_rows(a, total, t, T);
+}
+
+// Multi-block path, kernel 1: prologue of atom i (own wrap) and its edge count; the
+// neighbours' wrapped coordinates are recomputed from their positions with the same
+// arithmetic (bitwise the values kernel 1 publishes for them).
+__global__ void __launch_bounds__(kBlock) nl_count_kernel(BuildArgs a) {
+  __shared__ float s_red[kBlock / FMD_WAVE];
+  __shared__ int32_t s_iso[kBlock / FMD_WAVE];
+  const int lane = threadIdx.x & (FMD_WAVE - 1), wave = threadIdx.x / FMD_WAVE;
+  const int64_t i = (int64_t)blockIdx.x * (kBlock / FMD_WAVE) + wave;
+  Mat3 inv = load_mat3(a.inv_cell), cm = load_mat3(a.cell);
+  float dmax = 0.f;
+  int iso = 0;
+  if (i < a.n) {
+    float x, y, z, f[3], wr[3];
+    int w[3], wdi[3];
+    load_position(a.positions, a.pos64, i, x, y, z);
+    wrap_position(x, y, z, inv, cm, f, w, wr);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) wdi[k] = w[k] - a.ref_wraps[3 * i + k];
+    if (lane < 3) {
+      a.frac[3 * i + lane] = f[lane];
+      a.wrap_delta[3 * i + lane] = wdi[lane];
+      if (a.wrapped_out) a.wrapped_out[3 * i + lane] = wr[lane];
+    }
+    dmax = displacement_norm(x, y, z, a.ref_pos + 3 * i);
+    auto nbr_state = [&](int32_t j, float& xj, float& yj, float& zj, int wdj[3]) {
+      float px, py, pz, fj[3], wj[3];
+      int ww[3];
+      load_position(a.positions, a.pos64, j, px, py, pz);
+      wrap_position(px, py, pz, inv, cm, fj, ww, wj);
+      xj = wj[0];
+      yj = wj[1];
+      zj = wj[2];
+      wdj[0] = ww[0] - a.ref_wraps[3 * j];
+      wdj[1] = ww[1] - a.ref_wraps[3 * j + 1];
+      wdj[2] = ww[2] - a.ref_wraps[3 * j + 2];
+    };
+    int cnt = a.num[i];
+    cnt = cnt < a.bmax ? cnt : a.bmax;
+    int total = 0;
+    for (int base = 0; base < cnt; base += FMD_WAVE) {
+      const int s = base + lane;
+      bool e = false;
+      if (s < cnt) {
+        int32_t j;
+        int img[3];
+        float d2;
+        e = slot_edge(a, cm, i, s, wr[0], wr[1], wr[2], wdi, nbr_state, j, img, d2);
+      }
+      total += __popcll(__ballot(e));
+    }
+    if (lane == 0) a.edge_counts[i] = total;
+    iso = (total == 0);
+  }
+  if (lane == 0) {
+    s_red[wave] = dmax;
+    s_iso[wave] = iso;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float m = s_red[0];
+    int isol = s_iso[0];
+    for (int k = 1; k < kBlock / FMD_WAVE; ++k) {
+      m = nan_max(m, s_red[k]);
+      isol += s_iso[k];
+    }
+    const int64_t nb = gridDim.x;
+    float* red = reinterpret_cast<float*>(a.work);
+    red[blockIdx.x] = m;
+    reinterpret_cast<int32_t*>(a.work + fmd_cdiv(nb, 2))[blockIdx.x] = isol;
+  }
+}
+
+// Kernel 2 (one workgroup): exclusive scan of the counts, the flags and the reductions.
+__global__ void __launch_bounds__(1024) nl_scan_kernel(BuildArgs a, int64_t nblocks) {
+  __shared__ int64_t s_scan[1024];
+  const int t = threadIdx.x, T = blockDim.x;
+  const int64_t n = a.n;
+  const int64_t chunk = fmd_cdiv(n, T);
+  const int64_t lo = t * chunk, hi = lo + chunk < n ? lo + chunk : n;
+  int64_t s = 0;
+  for (int64_t k = lo; k < hi; ++k) s += a.edge_counts[k];
+  s_scan[t] = s;
+  __syncthreads();
+  if (t == 0) {
+    int64_t run = 0;
+    for (int k = 0; k < T; ++k) {
+      const int64_t v = s_scan[k];
+      s_scan[k] = run;
+      run += v;
+    }
+    const float* red = reinterpret_cast<const float*>(a.work);
+    const int32_t* isop = reinterpret_cast<const int32_t*>(a.work + fmd_cdiv(nblocks, 2));
+    float m = red[0];
+    int32_t isol = 0;
+    for (int64_t b = 0; b < nblocks; ++b) {
+      m = nan_max(m, red[b]);
+      isol += isop[b];
+    }
+    const bool valid = (m * 2.0f <= a.skin_limit) && (a.capacity_valid[0] != 0);
+    a.max_disp[0] = m;
+    a.cand_valid[0] = valid ? 1 : 0;
+    a.overflow[0] = (run > a.e_cap || !valid) ? 1 : 0;
+    a.isolated[0] = isol;
+    a.edge_offsets[n] = run;
+  }
+  __syncthreads();
+  int64_t run = s_scan[t];
+  for (int64_t k = lo; k < hi; ++k) {
+    const int64_t v = a.edge_counts[k];
+    a.edge_offsets[k] = run;
+    run += v;
+  }
+}
+
+// Kernel 3: materialization (one wave per atom, neighbours' state from kernel 1's output)
+// and, in the trailing blocks, the padding rows.
+__global__ void __launch_bounds__(kBlock) nl_materialize_kernel(BuildArgs a, int64_t atom_blocks) {
+  const int lane = threadIdx.x & (FMD_WAVE - 1), wave = threadIdx.x / FMD_WAVE;
+  if ((int64_t)blockIdx.x >= atom_blocks) {
+    const int64_t total = a.edge_offsets[a.n];
+    const int64_t pb = blockIdx.x - atom_blocks, npb = gridDim.x - atom_blocks;
+    pad_rows(a, total, pb * kBlock + threadIdx.x, npb * kBlock);
+    return;
+  }
+  const int64_t i = (int64_t)blockIdx.x * (kBlock / FMD_WAVE) + wave;
+  if (i >= a.n) return;
+  Mat3 cm = load_mat3(a.cell);
+  // atom i's own wrapped position: recomputed (kernel 1 may not have published it)
+  Mat3 inv = load_mat3(a.inv_cell);
+  float x, y, z, f[3], wr[3];
+  int w[3];
+  load_position(a.positions, a.pos64, i, x, y, z);
+  wrap_position(x, y, z, inv, cm, f, w, wr);
+  const int wdi[3] = {a.wrap_delta[3 * i], a.wrap_delta[3 * i + 1], a.wrap_delta[3 * i + 2]};
+  auto nbr_state = [&](int32_t j, float& xj, float& yj, float& zj, int wdj[3]) {
+    float px, py, pz, fj[3], wj[3];
+    int ww[3];
+    load_position(a.positions, a.pos64, j, px, py, pz);
+    wrap_position(px, py, pz, inv, cm, fj, ww, wj);
+    xj = wj[0];
+    yj = wj[1];
+    zj = wj[2];
+    wdj[0] = a.wrap_delta[3 * j];
+    wdj[1] = a.wrap_delta[3 * j + 1];
+    wdj[2] = a.wrap_delta[3 * j + 2];
+  };
+  int cnt = a.num[i];
+  cnt = cnt < a.bmax ? cnt : a.bmax;
+  int64_t row0 = a.edge_offsets[i];
+  for (int base = 0; base < cnt; base += FMD_WAVE) {
+    const int s = base + lane;
+    bool e = false;
+    int32_t j = 0;
+    int img[3] = {0, 0, 0};
+    float d2 = 0.f;
+    if (s < cnt) e = slot_edge(a, cm, i, s, wr[0], wr[1], wr[2], wdi, nbr_state, j, img, d2);
+    const uint64_t m = __ballot(e);
+    const int64_t row = row0 + lane_prefix(m);
+    if (e && row < a.e_cap) write_row(a, row, (int32_t)i, j, img[0], img[1], img[2], sqrtf(d2), true);
+    row0 += __popcll(m);
+  }
+}
+
+__global__ void nl_reverse_kernel(const int32_t* center, const int32_t* neighbor, const int32_t* images,
+                                  const int64_t* off, int64_t n, int64_t e_cap, int32_t* reverse) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = off[n];
+  const int64_t ec = total < e_cap ? total : e_cap;
+  if (e >= e_cap) return;
+  if (e >= ec) {
+    reverse[e] = -1;
+    return;
+  }
+  const int32_t c = center[e], j = neighbor[e];
+  const int ix = -images[3 * e], iy = -images[3 * e + 1], iz = -images[3 * e + 2];
+  int64_t lo = off[j], hi = off[j + 1];
+  hi = hi < ec ? hi : ec;
+  lo = lo < hi ? lo : hi;
+  // first row of the block of j whose (neighbor, image) >= (c, -image)
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    const int32_t mj = neighbor[mid];
+    const int mx = images[3 * mid], my = images[3 * mid + 1], mz = images[3 * mid + 2];
+    const bool less = (mj < c) || (mj == c && (mx < ix || (mx == ix && (my < iy || (my == iy && mz < iz)))));
+    if (less)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  int32_t r = -1;
+  int64_t end = off[j + 1] < ec ? off[j + 1] : ec;
+  if (lo < end && neighbor[lo] == c && images[3 * lo] == ix && images[3 * lo + 1] == iy && images[3 * lo + 2] == iz)
+    r = (int32_t)lo;
+  reverse[e] = r;
+}
+
+__global__ void nl_window_flags_kernel(const int64_t* edge_count, const uint8_t* invalid_pairs,
+                                       const uint8_t* overflow, const int32_t* isolated, int64_t e_cap,
+                                       int check_isolated, uint8_t* w_over, uint8_t* w_cap, int64_t* w_edges,
+                                       int32_t* w_iso) {
+  if (threadIdx.x != 0) return;
+  const int64_t edges = edge_count[0];
+  const int32_t iso = isolated[0];
+  bool flag = overflow[0] != 0;
+  if (check_isolated) flag = flag || iso > 0;
+  w_over[0] = (w_over[0] != 0 || flag) ? 1 : 0;
+  const bool cap = edges > e_cap || (invalid_pairs && invalid_pairs[0] != 0);
+  w_cap[0] = (w_cap[0] != 0 || cap) ? 1 : 0;
+  w_edges[0] = edges > w_edges[0] ? edges : w_edges[0];
+  w_iso[0] = iso > w_iso[0] ? iso : w_iso[0];
+}
+
+}  // namespace
+
+extern "C" {
+
+int fmd_nl_wrap(const void* positions, int32_t pos_is_f64, const float* inv_cell, const float* cell,
+                int64_t n_atoms, float* frac, int32_t* wraps, float* wrapped, float* reference_positions,
+                int32_t* reference_wraps, int32_t* wrap_delta, hipStream_t stream) {
+  FMD_REQUIRE(n_atoms >= 0 && positions && inv_cell && cell);
+  if (n_atoms == 0) return FMD_OK;
+  const int threads = 256;
+  hipLaunchKernelGGL(nl_wrap_kernel, dim3((unsigned)fmd_cdiv(n_atoms, threads)), dim3(threads), 0, stream,
+                     positions, pos_is_f64, inv_cell, cell, n_atoms, frac, wraps, wrapped, reference_positions,
+                     reference_wraps, wrap_delta);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_nl_candidates(const float* wrapped, const float* frac, const float* cell, int64_t n_atoms, float cutoff2,
+                      const int32_t* ncells, const int32_t* reach, int32_t bmax, int32_t* cell_count,
+                      int32_t* cell_start, int32_t* cell_atoms, int32_t* neighbor_matrix, int32_t* neighbor_shifts,
+                      int32_t* num_neighbors, uint8_t* capacity_valid, hipStream_t stream) {
+  FMD_REQUIRE(n_atoms > 0 && bmax > 0 && ncells && reach);
+  const int n0 = ncells[0], n1 = ncells[1], n2 = ncells[2];
+  const int r0 = reach[0], r1 = reach[1], r2 = reach[2];
+  FMD_REQUIRE(n0 > 0 && n1 > 0 && n2 > 0 && r0 >= 0 && r1 >= 0 && r2 >= 0);
+  // image shifts are packed in 8 bits: |shift| <= reach / ncells + 1 must stay below 127
+  FMD_REQUIRE(r0 / n0 + 2 < 127 && r1 / n1 + 2 < 127 && r2 / n2 + 2 < 127);
+  FMD_REQUIRE(n_atoms < (int64_t(1) << 31));
+  int lcap = 64;
+  while (lcap < bmax) lcap <<= 1;
+  if (lcap > 8192) return FMD_EUNSUPPORTED;
+  const int64_t ncell = (int64_t)n0 * n1 * n2;
+  const int threads = 256;
+  hipLaunchKernelGGL(cells_reset_kernel, dim3((unsigned)fmd_cdiv(ncell, threads)), dim3(threads), 0, stream,
+                     cell_count, ncell, capacity_valid);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(cells_count_kernel, dim3((unsigned)fmd_cdiv(n_atoms, threads)), dim3(threads), 0, stream, frac,
+                     n_atoms, n0, n1, n2, cell_count);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(cells_scan_kernel, dim3(1), dim3(1024), 0, stream, cell_count, cell_start, ncell);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(cells_place_kernel, dim3((unsigned)fmd_cdiv(n_atoms, threads)), dim3(threads), 0, stream, frac,
+                     n_atoms, n0, n1, n2, cell_count, cell_start, cell_atoms);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(cells_query_kernel, dim3((unsigned)n_atoms), dim3(256), (size_t)lcap * sizeof(uint64_t), stream,
+                     wrapped, frac, cell, n_atoms, cutoff2, n0, n1, n2, r0, r1, r2, bmax, lcap, cell_start, cell_atoms,
+                     neighbor_matrix, neighbor_shifts, num_neighbors, capacity_valid);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int64_t fmd_nl_build_work_size(int64_t n_atoms) {
+  const int64_t nb = fmd_cdiv(n_atoms > 0 ? n_atoms : 1, kBlock / FMD_WAVE);
+  return 2 * fmd_cdiv(nb, 2) + 2;
+}
+
+int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cell, const float* cell, int64_t n_atoms,
+                 const int32_t* neighbor_matrix, const int32_t* neighbor_shifts, const int32_t* num_neighbors,
+                 int32_t bmax, const float* reference_positions, const int32_t* reference_wraps,
+                 const uint8_t* capacity_valid, float rc2, float skin_limit, int32_t pad_ix, int32_t pad_iy,
+                 int32_t pad_iz, int64_t e_cap, int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
+                 int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor, int32_t* images,
+                 float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
+                 uint8_t* candidate_valid, uint8_t* overflow, int32_t* isolated, hipStream_t stream) {
+  FMD_REQUIRE(n_atoms > 0 && n_atoms < (int64_t(1) << 31) && e_cap > 0 && bmax > 0);
+  FMD_REQUIRE(positions && inv_cell && cell && neighbor_matrix && neighbor_shifts && num_neighbors);
+  FMD_REQUIRE(reference_positions && reference_wraps && capacity_valid && work && frac && wrap_delta);
+  FMD_REQUIRE(edge_counts && edge_offsets && center && neighbor && images && distances);
+  FMD_REQUIRE(max_displacement && candidate_valid && overflow && isolated);
+  BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
+              reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, pad_ix, pad_iy, pad_iz, e_cap,
+              work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
+              edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated};
+  if (n_atoms <= kSmallMaxAtoms && n_atoms <= 1024) {
+    hipLaunchKernelGGL(nl_build_small_kernel, dim3(1), dim3(kSmallThreads), 0, stream, a);
+    FMD_CHECK_LAUNCH();
+    return FMD_OK;
+  }
+  const int64_t atom_blocks = fmd_cdiv(n_atoms, kBlock / FMD_WAVE);
+  hipLaunchKernelGGL(nl_count_kernel, dim3((unsigned)atom_blocks), dim3(kBlock), 0, stream, a);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(nl_scan_kernel, dim3(1), dim3(1024), 0, stream, a, atom_blocks);
+  FMD_CHECK_LAUNCH();
+  int64_t pad_blocks = fmd_cdiv(e_cap, (int64_t)kBlock * 4);
+  pad_blocks = pad_blocks < 1 ? 1 : (pad_blocks > 1024 ? 1024 : pad_blocks);
+  hipLaunchKernelGGL(nl_materialize_kernel, dim3((unsigned)(atom_blocks + pad_blocks)), dim3(kBlock), 0, stream, a,
+                     atom_blocks);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_nl_reverse(const int32_t* center, const int32_t* neighbor, const int32_t* images, const int64_t* edge_offsets,
+                   int64_t n_atoms, int64_t e_cap, int32_t* reverse, hipStream_t stream) {
+  FMD_REQUIRE(n_atoms > 0 && e_cap > 0 && center && neighbor && images && edge_offsets && reverse);
+  const int threads = 256;
+  hipLaunchKernelGGL(nl_reverse_kernel, dim3((unsigned)fmd_cdiv(e_cap, threads)), dim3(threads), 0, stream, center,
+                     neighbor, images, edge_offsets, n_atoms, e_cap, reverse);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_nl_window_flags(const int64_t* edge_count, const uint8_t* invalid_pairs, const uint8_t* overflow,
+                        const int32_t* isolated, int64_t e_cap, int32_t check_isolated, uint8_t* window_overflow,
+                        uint8_t* window_capacity_overflow, int64_t* window_max_edges, int32_t* window_max_isolated,
+                        hipStream_t stream) {
+  FMD_REQUIRE(edge_count && overflow && isolated && window_overflow && window_capacity_overflow &&
+              window_max_edges && window_max_isolated);
+  hipLaunchKernelGGL(nl_window_flags_kernel, dim3(1), dim3(64), 0, stream, edge_count, invalid_pairs, overflow,
+                     isolated, e_cap, check_isolated, window_overflow, window_capacity_overflow, window_max_edges,
+                     window_max_isolated);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,304 @@
+"""(a) Capture-safe fixed-capacity neighbour list for GPU-resident MD (HIP kernels).
+
+Same interface as the reference's ``FixedCapacityGraphBuilder``
+(fastmd/graph/fixed_capacity_builder.py:1030-2366) for the edges-only single-system path:
+persistent buffers published as a ``GraphBatch``, a rare eager candidate refresh (cell list
+within ``candidate_cutoff = cutoff + skin``) and a per-step exact re-filter ``build`` that is
+a fixed sequence of kernels with device-side status flags (no host sync, capturable).
+
+MI355X design: the candidate rows are written sorted by (neighbour, shift) at refresh, so the
+per-step rows come out in the canonical (centre, neighbour, image) order directly (the
+reference's per-build ``torch.sort`` of e_cap keys, :1968-1999, is gone); a build is one
+fused single-workgroup kernel up to 1024 atoms, three kernels beyond (count, scan,
+materialize+pad), plus the reverse-edge index that the deterministic VJPs use.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Any, Callable
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from fastmd_amd import _abi
+from fastmd_amd._device import require_cuda
+from fastmd_amd.adapters.protocol import GraphBatch, PaddingRule
+from fastmd_amd.graph.neighbor_list_backend import (NeighborOverflowError, cell_list_shape,
+                                                    estimate_max_neighbors)
+
+_FAR_SELF_LOOPS = PaddingRule("far_self_loops")
+
+
+@dataclass
+class FixedCapacityGraphStatus:
+    """Device-side status of one build (fixed_capacity_builder.py:756-767)."""
+
+    edge_count: Tensor
+    triplet_count: Tensor
+    overflow: Tensor
+    invalid_pairs: Tensor
+    candidate_valid: Tensor
+    max_displacement: Tensor
+    isolated_atom_count: Tensor
+    candidate_capacity_valid: Tensor | None = None
+
+    @property
+    def undirected_count(self) -> Tensor:
+        return self.edge_count // 2
+
+
+def fixed_capacity_exceeded(status, builder) -> Tensor:
+    """Device predicate: the real graph does not fit (fixed_capacity_builder.py:796-814). An
+    edges-only builder fits up to ``e_capacity`` inclusive; with a line graph, equality is an
+    overflow too."""
+    if getattr(builder, "edges_only", False):
+        return (status.edge_count[0] > builder.e_capacity) | status.invalid_pairs[0]
+    return ((status.edge_count[0] >= builder.e_capacity) | (status.triplet_count[0] > builder.t_capacity)
+            | status.invalid_pairs[0])
+
+
+def self_loop_padding(padding: PaddingRule, cell: Tensor, cutoff: float):
+    """(integer image, length, override vector) of the padded self-loops
+    (fixed_capacity_builder.py:1004-1027). Host only."""
+    if padding.kind == "exact_rc_loops":
+        vector = tuple(map(float, padding.pad_vector or (cutoff, 0.0, 0.0)))
+        length = float(torch.linalg.vector_norm(torch.tensor(vector, dtype=torch.float32)))
+        if not length >= float(torch.tensor(cutoff, dtype=torch.float32)) or length == 0.0:
+            raise ValueError(f"exact_rc_loops: pad_vector {vector} is shorter than the cutoff {cutoff}")
+        return (0, 0, 0), length, vector
+    if padding.kind != "far_self_loops":
+        raise ValueError(f"{padding.kind} padding has no self-loops")
+    lengths = cell.detach().cpu().double().norm(dim=1)
+    axis = int(torch.argmax(lengths))
+    longest = float(lengths[axis])
+    if not longest > 0.0:
+        raise ValueError("far self-loop padding needs a cell with a nonzero lattice vector")
+    multiple = max(1, math.ceil(max(padding.min_length, 2.0 * cutoff) / longest))
+    image = [0, 0, 0]
+    image[axis] = multiple
+    return (image[0], image[1], image[2]), multiple * longest, None
+
+
+def _batch_itself(batch: GraphBatch) -> GraphBatch:
+    return batch
+
+
+class FixedCapacityGraphBuilder:
+    """Single-system, edges-only fixed-capacity builder (see the module docstring).
+
+    Unsupported reference options (line graph, ghost rows, sink padding, shared candidates,
+    minimum-image wraps, float64 published positions) raise ``NotImplementedError``.
+    ``sorted_edges=False`` is accepted: the rows are always in the canonical order, which is
+    also grouped by centre."""
+
+    def __init__(self, *, cell: Tensor, atomic_numbers: Tensor, u_capacity: int, t_capacity: int = 0,
+                 pbc: Tensor | None = None, atom_graph_cutoff: float = 6.0, line_graph_cutoff: float | None = None,
+                 n_dummy: int = 64, device: torch.device | str = "cuda", composition: str | None = None,
+                 candidate_cutoff: float | None = None, ghosts=None, minimum_image: bool = False,
+                 candidates_from=None, padding: PaddingRule | None = None,
+                 prepare: Callable[[GraphBatch], Any] | None = None, positions_dtype: torch.dtype = torch.float32,
+                 sorted_edges: bool = True, max_neighbor_count: Tensor | None = None,
+                 publish_positions: bool = False) -> None:
+        if line_graph_cutoff is not None or t_capacity != 0:
+            raise NotImplementedError("line graphs (three-body topologies) are not built by this builder")
+        if ghosts is not None or candidates_from is not None or minimum_image:
+            raise NotImplementedError("ghost rows, shared candidates and minimum-image wraps are not supported")
+        if positions_dtype != torch.float32:
+            raise NotImplementedError("float64 published positions are not supported")
+        padding = _FAR_SELF_LOOPS if padding is None else padding
+        if padding.kind != "far_self_loops":
+            raise NotImplementedError(f"{padding.kind} padding is not supported (far_self_loops only)")
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("the fixed-capacity builder runs on the GPU")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        _abi.load()
+        if pbc is not None and not bool(torch.as_tensor(pbc).all()):
+            raise NotImplementedError("non-periodic axes are not supported")
+        self.edges_only = True
+        self.padding = padding
+        self.sorted_edges = True
+        self.max_neighbor_count = max_neighbor_count
+        self.cell = cell.to(device=self.device, dtype=torch.float32).contiguous()
+        self.inv_cell = torch.linalg.inv(self.cell.double().cpu()).float().to(self.device).contiguous()
+        self.atomic_numbers_real = atomic_numbers.to(device=self.device, dtype=torch.int32)
+        self.n_real = int(self.atomic_numbers_real.shape[0])
+        if self.n_real <= 0:
+            raise ValueError("a builder needs at least one atom")
+        self.n_dummy = 0
+        self.u_capacity = int(u_capacity)
+        if self.u_capacity <= 0:
+            raise ValueError("an edges-only builder needs u_capacity > 0 and t_capacity == 0")
+        self.e_capacity = 2 * self.u_capacity
+        self.t_capacity = 0
+        self.atom_graph_cutoff = float(atom_graph_cutoff)
+        self.line_graph_cutoff = None
+        self.candidate_cutoff = float(candidate_cutoff or (self.atom_graph_cutoff + 1.0e-6))
+        if self.candidate_cutoff < self.atom_graph_cutoff:
+            raise ValueError("candidate_cutoff must not be below the pair cutoff")
+        self.skin = self.candidate_cutoff - self.atom_graph_cutoff
+        self.composition = composition or ""
+        self.buffer_max = int(estimate_max_neighbors(cutoff=self.candidate_cutoff, safety_factor=2.0))
+        self._rc2 = float(np.float32(self.atom_graph_cutoff * self.atom_graph_cutoff))
+        self._cand2 = float(np.float32(self.candidate_cutoff * self.candidate_cutoff))
+        self._skin_limit = float(np.float32(self.skin + 1.0e-6))
+        self._pad_loop = self_loop_padding(padding, self.cell, self.atom_graph_cutoff)
+        self._ncells, self._reach = cell_list_shape(self.cell.cpu().numpy(), self.candidate_cutoff)
+        n, dev = self.n_real, self.device
+        i32 = dict(dtype=torch.int32, device=dev)
+        f32 = dict(dtype=torch.float32, device=dev)
+        i64 = dict(dtype=torch.int64, device=dev)
+        u8 = dict(dtype=torch.uint8, device=dev)
+        ncell = self._ncells[0] * self._ncells[1] * self._ncells[2]
+        self._cell_count = torch.zeros(ncell, **i32)
+        self._cell_start = torch.zeros(ncell + 1, **i32)
+        self._cell_atoms = torch.zeros(n, **i32)
+        self.neighbor_matrix = torch.full((n, self.buffer_max), n, **i32)
+        self.neighbor_shifts = torch.zeros((n, self.buffer_max, 3), **i32)
+        self.num_neighbors = torch.zeros(n, **i32)
+        self.reference_positions = torch.zeros((n, 3), **f32)
+        self.reference_wraps = torch.zeros((n, 3), **i32)
+        self.wrap_delta = torch.zeros((n, 3), **i32)
+        self._wraps = torch.zeros((n, 3), **i32)
+        self._wrapped_refresh = torch.zeros((n, 3), **f32)
+        self._candidate_capacity_valid = torch.zeros(1, **u8)
+        self._candidate_initialized = False
+        self.frac_coords = torch.zeros((n, 3), **f32)
+        self.edge_counts = torch.zeros(n, **i64)
+        self.edge_offsets = torch.zeros(n + 1, **i64)
+        self.pair_offsets = torch.zeros(1, **i64)
+        e = self.e_capacity
+        self.center = torch.zeros(e, **i32)
+        self.neighbor = torch.zeros(e, **i32)
+        self.images = torch.zeros((e, 3), **i32)
+        self.distances = torch.zeros(e, **f32)
+        self.edge_reverse = torch.full((e,), -1, **i32)
+        self._work = torch.zeros(int(_abi.load().fmd_nl_build_work_size(n)), **i64)
+        self._max_displacement = torch.zeros(1, **f32)
+        self._candidate_valid = torch.zeros(1, **u8)
+        self._overflow = torch.zeros(1, **u8)
+        self._isolated_atom_count = torch.zeros(1, **i32)
+        self._invalid_pairs = torch.zeros(1, dtype=torch.bool, device=dev)
+        self.positions = torch.zeros((n, 3), **f32)
+        self.batch = GraphBatch(
+            positions=self.positions,
+            frac_coords=self.frac_coords,
+            cell=self.cell,
+            species=self.atomic_numbers_real,
+            n_real=n,
+            edge_index=torch.zeros((e, 2), **i32),
+            edge_image=torch.zeros((e, 3), **f32),
+            n_edges=self.edge_offsets[-1:],
+            cutoff=self.atom_graph_cutoff,
+            padding=padding,
+            composition=self.composition,
+            edge_offsets=self.edge_offsets,
+            edge_reverse=self.edge_reverse,
+        )
+        self.graph = (prepare or _batch_itself)(self.batch)
+
+    # ------------------------------------------------------------------ candidates
+    def _stream(self) -> int:
+        return _abi.stream_handle(self.device)
+
+    @torch.no_grad()
+    def refresh_candidates(self, positions: Tensor) -> None:
+        """Refresh the cell-list candidates from ``positions`` (eager, rare path): the reference
+        positions and wraps are reset and the wrap delta zeroed (fixed_capacity_builder.py:1674-1685)."""
+        positions = self._positions_arg(positions)
+        is64 = 1 if positions.dtype == torch.float64 else 0
+        n = self.n_real
+        _abi.call("fmd_nl_wrap", positions.data_ptr(), is64, self.inv_cell.data_ptr(), self.cell.data_ptr(), n,
+                  self.frac_coords.data_ptr(), self._wraps.data_ptr(), self._wrapped_refresh.data_ptr(),
+                  self.reference_positions.data_ptr(), self.reference_wraps.data_ptr(),
+                  self.wrap_delta.data_ptr(), self._stream())
+        _abi.call("fmd_nl_candidates", self._wrapped_refresh.data_ptr(), self.frac_coords.data_ptr(),
+                  self.cell.data_ptr(), n, self._cand2, _abi.array(_abi._i32, self._ncells),
+                  _abi.array(_abi._i32, self._reach), self.buffer_max, self._cell_count.data_ptr(),
+                  self._cell_start.data_ptr(), self._cell_atoms.data_ptr(), self.neighbor_matrix.data_ptr(),
+                  self.neighbor_shifts.data_ptr(), self.num_neighbors.data_ptr(),
+                  self._candidate_capacity_valid.data_ptr(), self._stream())
+        self._candidate_initialized = True
+
+    def assert_candidate_capacity(self) -> None:
+        """Raise (host sync) if a candidate row was truncated (fixed_capacity_builder.py:1665-1672)."""
+        if bool(self._candidate_capacity_valid.item()):
+            return
+        raise NeighborOverflowError(self.buffer_max, int(self.num_neighbors.max().item()))
+
+    def _positions_arg(self, positions: Tensor) -> Tensor:
+        if positions.shape != (self.n_real, 3):
+            raise ValueError(f"positions must have shape {(self.n_real, 3)}, got {tuple(positions.shape)}")
+        if positions.device != self.device:
+            positions = positions.to(self.device)
+        if positions.dtype not in (torch.float32, torch.float64):
+            positions = positions.to(torch.float32)
+        return positions.contiguous()
+
+    # ------------------------------------------------------------------ build
+    @torch.no_grad()
+    def build(self, positions: Tensor, *, rebuild_candidates: bool = True, predicate=None):
+        """Build into the persistent buffers; returns ``(prepare(batch), status)``
+        (fixed_capacity_builder.py:2180-2298). ``positions`` float32 or float64 [N, 3]."""
+        if predicate is not None:
+            raise NotImplementedError("caller predicates belong to ghost-row builders")
+        positions = self._positions_arg(positions)
+        if rebuild_candidates:
+            self.refresh_candidates(positions)
+        elif not self._candidate_initialized:
+            raise RuntimeError("refresh_candidates must run before candidate reuse")
+        is64 = 1 if positions.dtype == torch.float64 else 0
+        image = self._pad_loop[0]
+        _abi.call("fmd_nl_build", positions.data_ptr(), is64, self.inv_cell.data_ptr(), self.cell.data_ptr(),
+                  self.n_real, self.neighbor_matrix.data_ptr(), self.neighbor_shifts.data_ptr(),
+                  self.num_neighbors.data_ptr(), self.buffer_max, self.reference_positions.data_ptr(),
+                  self.reference_wraps.data_ptr(), self._candidate_capacity_valid.data_ptr(), self._rc2,
+                  self._skin_limit, image[0], image[1], image[2], self.e_capacity, self._work.data_ptr(),
+                  self.frac_coords.data_ptr(), self.wrap_delta.data_ptr(), self.positions.data_ptr(),
+                  self.edge_counts.data_ptr(), self.edge_offsets.data_ptr(), self.center.data_ptr(),
+                  self.neighbor.data_ptr(), self.images.data_ptr(), self.distances.data_ptr(),
+                  self.batch.edge_index.data_ptr(), self.batch.edge_image.data_ptr(),
+                  self._max_displacement.data_ptr(), self._candidate_valid.data_ptr(), self._overflow.data_ptr(),
+                  self._isolated_atom_count.data_ptr(), self._stream())
+        _abi.call("fmd_nl_reverse", self.center.data_ptr(), self.neighbor.data_ptr(), self.images.data_ptr(),
+                  self.edge_offsets.data_ptr(), self.n_real, self.e_capacity, self.edge_reverse.data_ptr(),
+                  self._stream())
+        if self.max_neighbor_count is not None:
+            torch.maximum(self.max_neighbor_count, self.edge_counts.max().reshape(1), out=self.max_neighbor_count)
+        return self.graph, self.status
+
+    @property
+    def status(self) -> FixedCapacityGraphStatus:
+        return FixedCapacityGraphStatus(
+            edge_count=self.edge_offsets[-1:],
+            triplet_count=self.pair_offsets[-1:],
+            overflow=self._overflow,
+            invalid_pairs=self._invalid_pairs,
+            candidate_valid=self._candidate_valid,
+            max_displacement=self._max_displacement,
+            isolated_atom_count=self._isolated_atom_count,
+            candidate_capacity_valid=self._candidate_capacity_valid,
+        )
+
+    def accumulate_window(self, status: FixedCapacityGraphStatus, *, window_overflow: Tensor,
+                          window_capacity_overflow: Tensor, window_max_edges: Tensor, window_max_isolated: Tensor,
+                          check_isolated: bool) -> None:
+        """Fold one build's status into a whole-step window's flags in one kernel
+        (fixed_capacity_builder.py:2300-2312, 430-455). Flags are uint8 [1]."""
+        for t, dt in ((window_overflow, torch.uint8), (window_capacity_overflow, torch.uint8),
+                      (window_max_edges, torch.int64), (window_max_isolated, torch.int32)):
+            if t.dtype != dt:
+                raise ValueError(f"window flag dtype {t.dtype}, expected {dt}")
+        _abi.call("fmd_nl_window_flags", status.edge_count.data_ptr(), None, status.overflow.data_ptr(),
+                  status.isolated_atom_count.data_ptr(), self.e_capacity, 1 if check_isolated else 0,
+                  window_overflow.data_ptr(), window_capacity_overflow.data_ptr(), window_max_edges.data_ptr(),
+                  window_max_isolated.data_ptr(), self._stream())
+
+    # ------------------------------------------------------------------ host views (tests, eager)
+    def real_edges(self) -> tuple[Tensor, Tensor, Tensor]:
+        """(center, neighbor, images) of the real rows (host sync)."""
+        count = min(int(self.edge_offsets[-1].item()), self.e_capacity)
+        return self.center[:count], self.neighbor[:count], self.images[:count]

@@ -1,0 +1,209 @@
+/*
+ * fastmd_hip.h - C ABI of the MI355X (gfx950) kernels of the GPU-resident MD step.
+ *
+ * Every entry point takes plain device pointers, sizes and the hipStream_t to launch on
+ * (torch's current stream), never allocates or frees memory, never synchronizes the host
+ * and returns 0 on success or a nonzero status (a hipError_t, or one of the FMD_E* codes
+ * below) that fmd_error_string() describes. Argument validation happens in the Python
+ * wrappers before the launch; the checks here only reject launches that could not be
+ * in bounds (negative sizes, null buffers that a kernel would dereference).
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   (a) fastmd/graph/fixed_capacity_builder.py, fastmd/graph/gpu_graph_builder.py
+ *   (b) fastmd/models/matris/op/triton_gather_cat.py
+ *   (c) fastmd/models/matris/op/triton_csr_segment_sum.py, fastmd/engine/kernels/segment.py
+ *   (d) fastmd/engine/kernels/triton_wide_gemm.py
+ *   (e) fastmd/execution/gpu_nhc.py
+ * Line citations sit beside each declaration.
+ */
+#ifndef FASTMD_HIP_H
+#define FASTMD_HIP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FMD_ABI_VERSION 1
+
+/* Status codes beyond hipError_t (hipError_t values stay below 10000). */
+#define FMD_OK 0
+#define FMD_EINVAL 10001      /* a size or pointer argument no launch could honour */
+#define FMD_EUNSUPPORTED 10002 /* a configuration this build does not implement */
+
+int fmd_abi_version(void);
+const char* fmd_error_string(int status);
+
+/* ----------------------------------------------------------------------------------------
+ * (a) Neighbour list
+ * -------------------------------------------------------------------------------------- */
+
+/* Candidate refresh: the cell-list candidates of every atom within `cutoff` (the builder's
+ * candidate cutoff = pair cutoff + skin), over all periodic images, from the WRAPPED float32
+ * coordinates. Row i of `neighbor_matrix`/`neighbor_shifts` (row stride bmax) holds the first
+ * bmax candidates of atom i in ascending (neighbour, sx, sy, sz) order; `num_neighbors[i]`
+ * counts every candidate (a count above bmax means truncation; `capacity_valid[0]` = all
+ * counts <= bmax). Unused slots keep neighbour n_atoms and shift 0.
+ * ncells/reach: cells per lattice axis and the cell search reach per axis (host computed).
+ * Replaces nvalchemiops batch_build_cell_list/batch_query_cell_list as called at
+ * fastmd/graph/fixed_capacity_builder.py:1519-1554 (FixedCapacityGraphBuilder._build_candidates). */
+int fmd_nl_candidates(const float* wrapped, const float* frac, const float* cell, int64_t n_atoms,
+                      float cutoff2, const int32_t* ncells, const int32_t* reach, int32_t bmax,
+                      int32_t* cell_count, int32_t* cell_start, int32_t* cell_atoms,
+                      int32_t* neighbor_matrix, int32_t* neighbor_shifts, int32_t* num_neighbors,
+                      uint8_t* capacity_valid, hipStream_t stream);
+
+/* Wrap (refresh flavour): float32 positions -> fractional coordinates in [0,1), integer
+ * wraps and wrapped Cartesian coordinates; optionally resets the reference positions/wraps
+ * and the wrap delta (refresh). `positions` are float32 (pos_is_f64 = 0) or float64 (1, cast
+ * to float32 first). Replaces fixed_capacity_builder.py:1674-1685 (refresh_candidates). */
+int fmd_nl_wrap(const void* positions, int32_t pos_is_f64, const float* inv_cell, const float* cell,
+                int64_t n_atoms, float* frac, int32_t* wraps, float* wrapped,
+                float* reference_positions, int32_t* reference_wraps, int32_t* wrap_delta,
+                hipStream_t stream);
+
+/* One exact re-filter build over the candidate list (the per-step path of a fixed-capacity,
+ * edges-only builder): wrap + wrap delta + skin test, per-atom edge counts, exclusive scan,
+ * materialization of the rows at edge_offsets[i] + rank (rows >= e_cap dropped), far
+ * self-loop padding of rows [min(E, e_cap), e_cap), overflow flag and the published batch
+ * buffers. The candidates are sorted per atom, so the rows come out in the canonical
+ * (centre, neighbour, image) order of fixed_capacity_builder.py:1968-1999 without a sort.
+ * Replaces FixedCapacityGraphBuilder.build(rebuild_candidates=False)
+ * fixed_capacity_builder.py:2180-2298 with _count_neighbors_kernel :97-185,
+ * _materialize_neighbors_kernel :188-288, _pad_self_loops_kernel :323-366, _sort_edges
+ * :1968-1999 and the batch copies :2260-2282.
+ *   positions      float32 or float64 [n,3] (pos_is_f64)
+ *   inv_cell, cell float32 [3,3] (row = lattice vector)
+ *   neighbor_matrix/neighbor_shifts/num_neighbors: the refresh's candidates (bmax stride)
+ *   reference_positions [n,3] f32, reference_wraps [n,3] i32: state of the last refresh
+ *   capacity_valid  uint8[1] from the refresh
+ *   rc2             float32 square of the pair cutoff
+ *   skin_limit      float32: the build is valid iff 2 * max displacement <= skin_limit
+ *   pad_image       integer image of the padded self-loops
+ *   work            int64 scratch of fmd_nl_build_work_size(n) elements
+ * Outputs: frac [n,3] f32, wrap_delta [n,3] i32, wrapped_out [n,3] f32 (published
+ * positions, may be null), edge_counts [n] i64, edge_offsets [n+1] i64, center/neighbor
+ * [e_cap] i32, images [e_cap,3] i32, distances [e_cap] f32, edge_index [e_cap,2] i32 and
+ * edge_image [e_cap,3] f32 (published, may be null), status: max_displacement f32[1],
+ * candidate_valid u8[1], overflow u8[1], isolated i32[1]. */
+int64_t fmd_nl_build_work_size(int64_t n_atoms);
+int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cell, const float* cell,
+                 int64_t n_atoms, const int32_t* neighbor_matrix, const int32_t* neighbor_shifts,
+                 const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,
+                 const int32_t* reference_wraps, const uint8_t* capacity_valid, float rc2,
+                 float skin_limit, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz, int64_t e_cap,
+                 int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
+                 int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor,
+                 int32_t* images, float* distances, int32_t* edge_index, float* edge_image,
+                 float* max_displacement, uint8_t* candidate_valid, uint8_t* overflow,
+                 int32_t* isolated, hipStream_t stream);
+
+/* Reverse edge of every real row e < min(E, e_cap): the row of (neighbour, centre, -image),
+ * or -1 when it is not stored (overflowed build). Gives the sender-side CSR of the sorted
+ * edge list (perm = reverse, off = edge_offsets), used by the deterministic VJPs. No
+ * counterpart in the reference, which scatters with atomics instead
+ * (triton_gather_cat.py:58-72). */
+int fmd_nl_reverse(const int32_t* center, const int32_t* neighbor, const int32_t* images,
+                   const int64_t* edge_offsets, int64_t n_atoms, int64_t e_cap, int32_t* reverse,
+                   hipStream_t stream);
+
+/* Window flag fold of one build (fixed_capacity_builder.py:430-455, _window_flags_kernel). */
+int fmd_nl_window_flags(const int64_t* edge_count, const uint8_t* invalid_pairs, const uint8_t* overflow,
+                        const int32_t* isolated, int64_t e_cap, int32_t check_isolated,
+                        uint8_t* window_overflow, uint8_t* window_capacity_overflow,
+                        int64_t* window_max_edges, int32_t* window_max_isolated, hipStream_t stream);
+
+/* ----------------------------------------------------------------------------------------
+ * (b) Gather-cat
+ * -------------------------------------------------------------------------------------- */
+
+/* out[e] = cat(part_0[e'], ..., part_{n-1}[e']) over n_parts <= 4 column blocks, where part k
+ * reads row index_k[e] of src_k (gathered) or row e (index_k null, aligned), width w_k, row
+ * stride ld_k; out row stride ld_out. Replaces aligned_gather_cat3/4
+ * (triton_gather_cat.py:29-43,181-199,202-232,353-374) and the north-star form
+ * gather_cat(x, src, dst, rbf) = cat(x[src], x[dst], rbf). Index arrays are int32. */
+int fmd_gather_cat_f32(int32_t n_parts, const float* const* srcs, const int32_t* const* indices,
+                       const int64_t* lds, const int32_t* widths, int64_t rows, float* out,
+                       int64_t ld_out, hipStream_t stream);
+
+/* ----------------------------------------------------------------------------------------
+ * (c) Deterministic CSR segment sums
+ * -------------------------------------------------------------------------------------- */
+
+/* out[s, :] = sum over terms t of  scale_t * sum_{j in [off_t[s], off_t[s+1]) ∩ [0, rows_t)}
+ *             [w_t[r]*] v_t[r, col_t + :]   with r = perm_t ? perm_t[j] : j (r < 0 skipped)
+ * for up to 2 terms, width `dim`, fixed summation order (deterministic, no atomics); the
+ * per-term arrays (values, ld_values, col_offsets, weights, scales, perms, offs, rows) are
+ * host arrays of n_terms entries (weights, scales, perms may be null: none, 1, identity).
+ * `skip_segment` >= 0 writes 0 to that segment. accumulate != 0 adds into out.
+ * Replaces csr_segment_sum (triton_csr_segment_sum.py:70-120,433-479) and the gather-cat VJP
+ * scatters (triton_gather_cat.py:58-72) by two CSRs. */
+int fmd_segsum_csr_f32(int32_t n_terms, const float* const* values, const int64_t* ld_values,
+                       const int64_t* col_offsets, const float* const* weights, const float* scales,
+                       const int32_t* const* perms, const int64_t* const* offs,
+                       const int64_t* rows, int64_t num_segment, int64_t dim, int64_t skip_segment,
+                       int32_t accumulate, float* out, int64_t ld_out, hipStream_t stream);
+
+/* Transpose (VJP) of one term: for j in the run of s, r = perm ? perm[j] : j,
+ *   gvalue[r] = gout[s] (* weight[r]),  gweight[r] = gout[s] * value[r];
+ * rows of [0, n_rows) in no run (padding) get 0. skip_segment's rows get 0.
+ * Replaces _csr_segsum_bwd_runs / _csr_segsum_bwd_rows (triton_csr_segment_sum.py:123-230). */
+int fmd_segsum_csr_t_f32(const float* gout, int64_t ld_gout, const float* value, const float* weight,
+                         int64_t ld_value, const int32_t* perm, const int64_t* off, int64_t num_segment,
+                         int64_t n_rows, int64_t dim, int64_t skip_segment, float* gvalue,
+                         float* gweight, hipStream_t stream);
+
+/* ----------------------------------------------------------------------------------------
+ * (d) Edge GEMM on MFMA
+ * -------------------------------------------------------------------------------------- */
+
+/* C[M,N] (ldc) = A[M,K] (lda) * op(B) (+ bias[N]) (+ C if accumulate), fp32 in/out, fp32
+ * MFMA (v_mfma_f32_32x32x2_f32). b_layout 0: B is [N,K] (ldb), op(B) = B^T (F.linear weight);
+ * 1: B is [K,N] (ldb), op(B) = B. epilogue 0: none, 1: SiLU. Replaces linear / linear_into /
+ * matmul (triton_wide_gemm.py:482-553), whose 3xTF32 kernels decline K % 16 != 0 (:235) and
+ * fall back to F.linear. */
+int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32_t b_layout,
+                 const float* bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                 int32_t accumulate, int32_t epilogue, hipStream_t stream);
+
+/* As fmd_gemm_f32 with bf16 operands (uint16 storage), fp32 accumulate and fp32 output, on
+ * v_mfma_f32_32x32x16_bf16. Not in the reference (which has no bf16 GEMM on this path). */
+int fmd_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int32_t b_layout,
+                  const float* bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                  int32_t accumulate, int32_t epilogue, hipStream_t stream);
+
+/* ----------------------------------------------------------------------------------------
+ * (e) Nose-Hoover chain velocity Verlet (ASE NoseHooverChainNVT), float64 state
+ * -------------------------------------------------------------------------------------- */
+
+/* consts layout (float64): [dt, dt/2, kT, 3N*kT, 3 x (delta, delta/2, -(delta/4), -delta),
+ * Q[tchain], 1/Q[tchain]] (gpu_nhc.py:113-133,273-275).
+ * pre: NHC(dt/2); p += dt/2 * F (cached forces, float64; f32_kick: the float32 product of
+ * NumPy NEP 50); q += dt * p / m. Replaces _nhc_pre_force_kernel (gpu_nhc.py:359-391). */
+int fmd_nhc_pre_force(double* q, double* p, const double* f, const double* masses, double* eta,
+                      double* p_eta, const double* consts, int64_t n_atoms, int32_t tchain,
+                      int32_t tloop, int32_t f32_kick, hipStream_t stream);
+
+/* post: p += dt/2 * F_in; NHC(dt/2); cache F_in as float64 in f_cache; copy the energy.
+ * f_in_is_f64 selects float32/float64 forces, e_kind 0: no energy, 1: float32, 2: float64.
+ * Replaces _nhc_post_force_kernel (gpu_nhc.py:393-425). */
+int fmd_nhc_post_force(double* p, const void* f_in, int32_t f_in_is_f64, double* f_cache,
+                       const double* masses, double* eta, double* p_eta, const double* consts,
+                       const void* e_in, int32_t e_kind, double* e_out, int64_t n_atoms,
+                       int32_t tchain, int32_t tloop, int32_t f32_kick, hipStream_t stream);
+
+/* ----------------------------------------------------------------------------------------
+ * Small deterministic reductions used around the step
+ * -------------------------------------------------------------------------------------- */
+
+/* out[0] = sum_{i<n} (double)x[i] in a fixed order (x float32 if x_is_f64 == 0). The FP64
+ * energy sum of EnergyDerivative (fastmd/engine/energy_derivative.py:131-133). */
+int fmd_sum_f64(const void* x, int32_t x_is_f64, int64_t n, double* out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FASTMD_HIP_H */

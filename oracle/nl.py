@@ -1,0 +1,275 @@
+"""Neighbour-list oracle (test infrastructure only; see oracle/__init__.py).
+
+Restates, in NumPy float32 with the operation order of ``fastmd_amd/csrc/nl.hip``:
+  * the wrap of FixedCapacityGraphBuilder.build / refresh_candidates
+    (fastmd/graph/fixed_capacity_builder.py:1674-1685, 2199-2252; small_matmul geometry.py:7-34)
+  * the candidate list of the cell-list refresh (nvalchemiops' role at
+    fixed_capacity_builder.py:1519-1554), as the full set of (j, shift) within the candidate
+    cutoff, sorted by (j, sx, sy, sz), first bmax stored, all counted
+  * _count_neighbors_kernel / _materialize_neighbors_kernel (:97-288), the exclusive scan
+    (:1814-1815), far self-loop padding (_pad_self_loops_kernel :323-366, self_loop_padding
+    :1004-1027), the canonical sort (_sort_edges :1968-1999) and the overflow flag
+  * fixed_capacity_exceeded (:796-814) and the window flag fold (:430-455)
+  * estimate_max_neighbors (fastmd/graph/neighbor_list_backend.py:77-88) and the ragged
+    builder's slot growth rule (fastmd/graph/gpu_graph_builder.py:74-85)
+and an FP64 brute-force pair set (tests/test_fixed_capacity_boundary.py:86-102) that pins it.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+F32 = np.float32
+
+
+def estimate_max_neighbors(cutoff: float, atomic_density: float = 0.35, safety_factor: float = 5.0) -> int:
+    """neighbor_list_backend.py:77-88."""
+    if cutoff <= 0:
+        return 0
+    volume = atomic_density * (4.0 / 3.0) * math.pi * (cutoff ** 3)
+    expected = max(1, safety_factor * volume)
+    return int(math.ceil(expected / 16)) * 16
+
+
+def grown_max_neighbors(capacity: int, max_count: int, quantum: int = 16) -> int:
+    """gpu_graph_builder.py:83-85."""
+    return max(2 * capacity, -(-max_count // quantum) * quantum)
+
+
+def wrap(positions, inv_cell, cell):
+    """(frac, wraps, wrapped) in float32 (nl.hip wrap_position)."""
+    x = np.asarray(positions).astype(F32)
+    inv = np.asarray(inv_cell, dtype=F32)
+    c = np.asarray(cell, dtype=F32)
+    t = x[:, 0:1] * inv[0]
+    t = t + x[:, 1:2] * inv[1]
+    t = t + x[:, 2:3] * inv[2]
+    fl = np.floor(t)
+    wraps = fl.astype(np.int32)
+    frac = (t - fl).astype(F32)
+    w = frac[:, 0:1] * c[0]
+    w = w + frac[:, 1:2] * c[1]
+    w = w + frac[:, 2:3] * c[2]
+    return frac, wraps, w.astype(F32)
+
+
+def pair_d2(pi, pj, img, cell):
+    """float32 squared distance of rows pi -> pj + img @ cell in nl.hip's order; returns (d2, d)."""
+    c = np.asarray(cell, dtype=F32)
+    s = np.asarray(img).astype(F32)
+    d = []
+    for k in range(3):
+        v = pj[:, k] - pi[:, k]
+        v = v + s[:, 0] * c[0, k]
+        v = v + s[:, 1] * c[1, k]
+        v = v + s[:, 2] * c[2, k]
+        d.append(v.astype(F32))
+    d2 = d[0] * d[0]
+    d2 = d2 + d[1] * d[1]
+    d2 = d2 + d[2] * d[2]
+    return d2.astype(F32), np.stack(d, 1)
+
+
+def cell_heights(cell) -> np.ndarray:
+    c = np.asarray(cell, dtype=np.float64)
+    volume = abs(np.linalg.det(c))
+    return np.array([volume / np.linalg.norm(np.cross(c[(k + 1) % 3], c[(k + 2) % 3])) for k in range(3)])
+
+
+def _candidate_pairs(wrapped, cell, cutoff):
+    """A superset of the directed (i, j, shift) pairs within `cutoff` (float64 search)."""
+    n = wrapped.shape[0]
+    reach = [int(math.ceil(cutoff / h)) + 1 for h in cell_heights(cell)]
+    images = np.array(np.meshgrid(*[np.arange(-r, r + 1) for r in reach], indexing="ij")).reshape(3, -1).T
+    pos = wrapped.astype(np.float64)
+    cell64 = np.asarray(cell, dtype=np.float64)
+    margin = cutoff + 0.05
+    out_i, out_j, out_s = [], [], []
+    if n * n * len(images) <= 4_000_000:
+        for s in images:
+            v = pos[None, :, :] + (s @ cell64)[None, None, :] - pos[:, None, :]
+            d = np.sqrt((v * v).sum(-1))
+            ii, jj = np.nonzero(d < margin)
+            out_i.append(ii)
+            out_j.append(jj)
+            out_s.append(np.broadcast_to(s, (ii.size, 3)))
+    else:
+        from scipy.spatial import cKDTree
+
+        tree = cKDTree(pos)
+        for s in images:
+            shifted = pos + s @ cell64
+            pairs = cKDTree(shifted).query_ball_tree(tree, margin)  # pairs[j] = atoms i near image j
+            jj = np.repeat(np.arange(n), [len(p) for p in pairs])
+            ii = np.fromiter((i for p in pairs for i in p), dtype=np.int64, count=jj.size)
+            out_i.append(ii)
+            out_j.append(jj)
+            out_s.append(np.broadcast_to(s, (ii.size, 3)))
+    i = np.concatenate(out_i).astype(np.int64)
+    j = np.concatenate(out_j).astype(np.int64)
+    s = np.concatenate(out_s).astype(np.int32)
+    return i, j, s
+
+
+@dataclass
+class Candidates:
+    neighbor_matrix: np.ndarray  # int32 [n, bmax], pad n
+    neighbor_shifts: np.ndarray  # int32 [n, bmax, 3]
+    num_neighbors: np.ndarray  # int32 [n]
+    capacity_valid: bool
+
+
+def candidates(wrapped, cell, cutoff2, bmax: int) -> Candidates:
+    """The refresh's candidate rows (see module docstring); `wrapped` are the wrapped float32
+    coordinates, `cutoff2` the float32 square of the candidate cutoff."""
+    wrapped = np.asarray(wrapped, dtype=F32)
+    n = wrapped.shape[0]
+    cutoff2 = F32(cutoff2)
+    i, j, s = _candidate_pairs(wrapped, cell, float(np.sqrt(np.float64(cutoff2))))
+    d2, _ = pair_d2(wrapped[i], wrapped[j], s, cell)
+    keep = (d2 < cutoff2) & ~((i == j) & (s == 0).all(1))
+    i, j, s = i[keep], j[keep], s[keep]
+    order = np.lexsort((s[:, 2], s[:, 1], s[:, 0], j, i))
+    i, j, s = i[order], j[order], s[order]
+    counts = np.bincount(i, minlength=n).astype(np.int32)
+    starts = np.concatenate([[0], np.cumsum(counts)])
+    rank = np.arange(i.size) - starts[i]
+    stored = rank < bmax
+    nm = np.full((n, bmax), n, dtype=np.int32)
+    ns = np.zeros((n, bmax, 3), dtype=np.int32)
+    nm[i[stored], rank[stored]] = j[stored]
+    ns[i[stored], rank[stored]] = s[stored]
+    return Candidates(nm, ns, counts, bool((counts <= bmax).all()))
+
+
+def self_loop_image(cell, cutoff: float, min_length: float = 0.0):
+    """Far self-loop padding image and length (fixed_capacity_builder.py:1004-1027)."""
+    lengths = np.linalg.norm(np.asarray(cell, dtype=np.float64), axis=1)
+    axis = int(np.argmax(lengths))
+    longest = float(lengths[axis])
+    if not longest > 0.0:
+        raise ValueError("far self-loop padding needs a cell with a nonzero lattice vector")
+    multiple = max(1, math.ceil(max(min_length, 2.0 * cutoff) / longest))
+    image = [0, 0, 0]
+    image[axis] = multiple
+    return tuple(image), multiple * longest
+
+
+@dataclass
+class Build:
+    frac: np.ndarray
+    wrap_delta: np.ndarray
+    wrapped: np.ndarray
+    edge_counts: np.ndarray  # int64 [n]
+    edge_offsets: np.ndarray  # int64 [n+1]
+    center: np.ndarray  # int32 [e_cap]
+    neighbor: np.ndarray
+    images: np.ndarray  # int32 [e_cap, 3]
+    distances: np.ndarray  # float32 [e_cap] (rows >= real rows undefined: NaN here)
+    max_displacement: np.float32
+    candidate_valid: bool
+    overflow: bool
+    isolated: int
+
+    @property
+    def n_edges(self) -> int:
+        return int(self.edge_offsets[-1])
+
+
+def build(positions, inv_cell, cell, cand: Candidates, reference_positions, reference_wraps, rc2, skin_limit,
+          pad_image, e_cap: int) -> Build:
+    """One edges-only build over the candidate list (see module docstring)."""
+    pos = np.asarray(positions).astype(F32)
+    n = pos.shape[0]
+    frac, wraps, wrapped = wrap(pos, inv_cell, cell)
+    wd = (wraps - np.asarray(reference_wraps, dtype=np.int32)).astype(np.int32)
+    disp = pos - np.asarray(reference_positions, dtype=F32)
+    s = disp[:, 0] * disp[:, 0]
+    s = s + disp[:, 1] * disp[:, 1]
+    s = s + disp[:, 2] * disp[:, 2]
+    norms = np.sqrt(s.astype(F32))
+    max_disp = F32(np.max(norms)) if n else F32(0)
+    valid = bool((max_disp * F32(2.0) <= F32(skin_limit)) and cand.capacity_valid)
+
+    bmax = cand.neighbor_matrix.shape[1]
+    cnt = np.minimum(cand.num_neighbors, bmax)
+    slot = np.arange(bmax)[None, :] < cnt[:, None]
+    ii, ss = np.nonzero(slot)  # row-major: ascending (atom, slot)
+    jj = np.minimum(cand.neighbor_matrix[ii, ss], n - 1)
+    img = cand.neighbor_shifts[ii, ss] + wd[jj] - wd[ii]
+    d2, _ = pair_d2(wrapped[ii], wrapped[jj], img, cell)
+    edge = d2 < F32(rc2)
+    ii, jj, img, d2 = ii[edge], jj[edge], img[edge], d2[edge]
+    counts = np.bincount(ii, minlength=n).astype(np.int64)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    total = int(offsets[-1])
+    ec = min(total, e_cap)
+    center = np.empty(e_cap, np.int32)
+    neighbor = np.empty(e_cap, np.int32)
+    images = np.empty((e_cap, 3), np.int32)
+    distances = np.full(e_cap, np.nan, F32)
+    center[:ec] = ii[:ec]
+    neighbor[:ec] = jj[:ec]
+    images[:ec] = img[:ec]
+    distances[:ec] = np.sqrt(d2[:ec])
+    pad = np.arange(ec, e_cap)
+    atoms = ((pad - ec) % n).astype(np.int32)
+    center[ec:] = atoms
+    neighbor[ec:] = atoms
+    images[ec:] = np.asarray(pad_image, dtype=np.int32)
+    return Build(frac, wd, wrapped, counts, offsets, center, neighbor, images, distances, max_disp, valid,
+                 bool(total > e_cap or not valid), int((counts == 0).sum()))
+
+
+def canonical_order_ok(center, neighbor, images, n_atoms: int, max_image: int = 10) -> bool:
+    """The reference's canonical key (fixed_capacity_builder.py:1980-1987) is strictly increasing."""
+    radix = 2 * max_image + 1
+    key = ((center.astype(np.int64) * n_atoms + neighbor) * radix ** 3 + (images[:, 0] + max_image) * radix * radix
+           + (images[:, 1] + max_image) * radix + images[:, 2] + max_image)
+    return bool(np.all(np.diff(key) > 0))
+
+
+def reverse(center, neighbor, images, edge_offsets, e_cap: int) -> np.ndarray:
+    """Row of (neighbour, centre, -image) for each real row, -1 if not stored."""
+    total = int(edge_offsets[-1])
+    ec = min(total, e_cap)
+    rows = {(int(center[e]), int(neighbor[e]), *map(int, images[e])): e for e in range(ec)}
+    out = np.full(e_cap, -1, np.int32)
+    for e in range(ec):
+        out[e] = rows.get((int(neighbor[e]), int(center[e]), *(-int(v) for v in images[e])), -1)
+    return out
+
+
+def dense_pairs(wrapped, cell, cutoff: float) -> dict:
+    """FP64 O(N^2 x images) directed edges {(i, j, nx, ny, nz): distance}
+    (tests/test_fixed_capacity_boundary.py:86-102)."""
+    pos = np.asarray(wrapped, dtype=np.float64)
+    c = np.asarray(cell, dtype=np.float64)
+    reach = [int(np.ceil(cutoff / h)) + 1 for h in cell_heights(c)]
+    pairs = {}
+    for s in np.array(np.meshgrid(*[np.arange(-r, r + 1) for r in reach], indexing="ij")).reshape(3, -1).T:
+        v = pos[None, :, :] + (s @ c)[None, None, :] - pos[:, None, :]
+        d = np.sqrt((v * v).sum(-1))
+        for i, j in zip(*np.nonzero(d < cutoff)):
+            if i != j or np.abs(s).sum() > 0:
+                pairs[(int(i), int(j), *map(int, s))] = float(d[i, j])
+    return pairs
+
+
+def fixed_capacity_exceeded(edge_count: int, invalid_pairs: bool, e_capacity: int) -> bool:
+    """Edges-only rule of fixed_capacity_builder.py:796-814 (fits up to e_capacity inclusive)."""
+    return bool(edge_count > e_capacity or invalid_pairs)
+
+
+def window_fold(state: dict, edges: int, invalid_pairs: bool, overflow: bool, isolated: int, e_cap: int,
+                check_isolated: bool) -> dict:
+    """_window_flags_kernel (fixed_capacity_builder.py:430-455)."""
+    flag = overflow or (check_isolated and isolated > 0)
+    return {
+        "overflow": state["overflow"] or flag,
+        "capacity_overflow": state["capacity_overflow"] or edges > e_cap or invalid_pairs,
+        "max_edges": max(state["max_edges"], edges),
+        "max_isolated": max(state["max_isolated"], isolated),
+    }

@@ -1,0 +1,306 @@
+"""(a) Neighbour list: the oracle pinned against the reference's own checks (CPU), and the HIP
+builder bit-exact against the oracle (GPU)."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import nl as onl
+from fastmd_amd import systems
+
+F32 = np.float32
+
+
+def _crystal():
+    """Perturbed 3x3x3 simple-cubic crystal in a slightly triclinic cell
+    (tests/test_fixed_capacity_boundary.py:43-53 of the reference, seed 1234)."""
+    rng = np.random.default_rng(1234)
+    cell = np.array([[6.0, 0.0, 0.0], [0.3, 6.1, 0.0], [0.2, -0.25, 5.9]])
+    grid = np.stack(np.meshgrid(*(np.arange(3),) * 3, indexing="ij"), -1).reshape(-1, 3)
+    frac = (grid + 0.5 + rng.uniform(-0.08, 0.08, grid.shape)) / 3.0
+    return cell, frac @ cell
+
+
+def _lattice(n_side, spacing, jitter, seed):
+    """tests/test_ragged_builder_overflow.py:33-43 of the reference (positions float32)."""
+    rng = np.random.default_rng(seed)
+    grid = np.stack(np.meshgrid(*(np.arange(n_side),) * 3, indexing="ij"), -1)
+    positions = (grid.reshape(-1, 3) + 0.5) * spacing
+    positions = positions + rng.uniform(-jitter, jitter, positions.shape)
+    return np.eye(3) * n_side * spacing, positions.astype(np.float32).astype(np.float64)
+
+
+def _oracle_build(cell, positions, cutoff, skin, e_cap, pad=None, ref_positions=None):
+    cell32 = cell.astype(F32)
+    inv = np.linalg.inv(cell).astype(F32)
+    ref = positions if ref_positions is None else ref_positions
+    _, wraps, wrapped = onl.wrap(ref, inv, cell32)
+    bmax = onl.estimate_max_neighbors(cutoff + skin, safety_factor=2.0)
+    cand = onl.candidates(wrapped, cell32, F32((cutoff + skin) ** 2), bmax)
+    if pad is None:
+        pad, _ = onl.self_loop_image(cell, cutoff)
+    b = onl.build(positions, inv, cell32, cand, np.asarray(ref, dtype=F32), wraps, F32(cutoff * cutoff),
+                  F32(skin + 1e-6), pad, e_cap)
+    return cand, b, wrapped
+
+
+# ------------------------------------------------------------------------------- CPU: oracle pins
+def test_estimate_max_neighbors_known_answers():
+    # tests/test_ragged_builder_overflow.py:328-336 of the reference
+    for cutoff, expected in ((6.0 + 1e-6, 640), (5.0, 368), (3.0, 80), (0.0, 0)):
+        assert onl.estimate_max_neighbors(cutoff=cutoff, safety_factor=2.0) == expected
+    from fastmd_amd.graph.neighbor_list_backend import estimate_max_neighbors
+
+    for cutoff in np.linspace(0.5, 12.0, 50):
+        assert estimate_max_neighbors(float(cutoff), safety_factor=2.0) == onl.estimate_max_neighbors(
+            float(cutoff), safety_factor=2.0)
+    assert onl.estimate_max_neighbors(8.0, safety_factor=2.0) == 1504
+
+
+def test_growth_rule():
+    from fastmd_amd.graph.gpu_graph_builder import grown_max_neighbors
+
+    for cap, mx in ((8, 9), (8, 100), (80, 81), (16, 17), (1, 1)):
+        assert grown_max_neighbors(cap, mx) == max(2 * cap, math.ceil(mx / 16) * 16) == onl.grown_max_neighbors(cap, mx)
+
+
+@pytest.mark.parametrize("case", ["perovskite", "crystal", "lattice"])
+def test_oracle_edges_equal_fp64_brute_force(case):
+    """The oracle's real edges are the FP64 dense pair set, up to pairs within 1e-5 A of the
+    cutoff (tests/test_fixed_capacity_boundary.py:358-365 of the reference)."""
+    if case == "perovskite":
+        s = systems.perovskite(3)
+        cell, pos, cutoff = s.cell, s.positions, 6.0
+    elif case == "crystal":
+        cell, pos = _crystal()
+        cutoff = 3.0
+    else:
+        cell, pos = _lattice(5, 1.6, 0.15, 0)
+        cutoff = 3.0
+    cand, b, wrapped = _oracle_build(cell, pos, cutoff, 1.0, 100000)
+    e = b.n_edges
+    got = {(int(c), int(n), *map(int, i)): float(d) for c, n, i, d in
+           zip(b.center[:e], b.neighbor[:e], b.images[:e], b.distances[:e])}
+    dense = onl.dense_pairs(wrapped, cell.astype(F32), cutoff)
+    near = {k for k, d in dense.items() if abs(d - cutoff) < 1e-5} | {k for k, d in got.items() if abs(d - cutoff) < 1e-5}
+    assert set(got) - near == set(dense) - near
+    assert onl.canonical_order_ok(b.center[:e], b.neighbor[:e], b.images[:e], pos.shape[0])
+    for k, d in got.items():  # distances are the rows' own
+        assert abs(d - dense.get(k, d)) < 1e-4
+
+
+def test_perovskite_edge_statistics():
+    """15.21 edges/atom at a = 6.2, rc = 6 (E = 2 054 at 135 atoms), 50 candidates at 8 A."""
+    s = systems.perovskite(3)
+    cand, b, _ = _oracle_build(s.cell, s.positions, 6.0, 2.0, 2176)
+    assert b.n_edges == 2054 and not b.overflow and b.isolated == 0
+    assert cand.num_neighbors.max() == 52 and cand.capacity_valid
+
+
+def test_padding_layout_and_overflow_flag():
+    s = systems.perovskite(3)
+    cell = s.cell
+    image, length = onl.self_loop_image(cell, 6.0)
+    assert image == (1, 0, 0) and length == pytest.approx(18.6)  # m = 1: |a| = 18.6 >= 2 rc
+    _, b, _ = _oracle_build(cell, s.positions, 6.0, 2.0, 2176)
+    rows = np.arange(b.n_edges, 2176)
+    assert np.array_equal(b.center[rows], (rows - b.n_edges) % 135)  # round robin
+    assert np.array_equal(b.neighbor[rows], b.center[rows])
+    assert (b.images[rows] == np.array(image)).all()
+    _, small, _ = _oracle_build(cell, s.positions, 6.0, 2.0, 1000)
+    assert small.overflow and small.n_edges == 2054
+    assert onl.fixed_capacity_exceeded(2054, False, 1000)
+
+
+def test_fixed_capacity_truth_table():
+    # tests/test_fixed_capacity_boundary.py:111-120 of the reference (edges only)
+    for edges, invalid, expected in ((31, False, False), (32, False, False), (33, False, True),
+                                     (34, False, True), (30, True, True)):
+        assert onl.fixed_capacity_exceeded(edges, invalid, 32) == expected
+
+
+def test_padding_rule_validation_table():
+    # tests/test_fixed_capacity_boundary.py:121-129 of the reference
+    from fastmd_amd.adapters.protocol import PaddingRule
+
+    for kwargs, message in (({"kind": "zero_loops"}, "unknown kind"), ({"min_length": -1.0}, "min_length"),
+                            ({"min_length": float("nan")}, "min_length"),
+                            ({"kind": "sink_atoms", "min_length": 1.0}, "far_self_loops only"),
+                            ({"kind": "far_self_loops", "pad_vector": (1.0, 0.0, 0.0)}, "exact_rc_loops only"),
+                            ({"kind": "exact_rc_loops", "pad_vector": (1.0, 0.0)}, "three finite"),
+                            ({"placement": "one_row"}, "unknown placement")):
+        with pytest.raises(ValueError, match=message):
+            PaddingRule(**kwargs)
+
+
+def test_reused_candidates_equal_fresh_build():
+    """A build over reused candidates equals a fresh build bitwise after moves within the skin
+    (tests/test_fixed_capacity_boundary.py:439-461 of the reference), across wrap changes."""
+    s = systems.perovskite(3)
+    rng = np.random.default_rng(5)
+    moved = s.positions + rng.normal(0, 0.2, s.positions.shape)
+    moved[:, 0] -= s.positions[:, 0].min() + 0.05  # atoms of the x = 0 face leave the cell: wraps change
+    earlier = moved - rng.normal(0, 0.1, moved.shape)  # the refresh's positions, within the skin
+    _, reused, _ = _oracle_build(s.cell, moved, 6.0, 2.0, 2400, ref_positions=earlier)
+    _, fresh, _ = _oracle_build(s.cell, moved, 6.0, 2.0, 2400)
+    assert reused.candidate_valid and not reused.overflow
+    assert (reused.wrap_delta != 0).any()
+    e = fresh.n_edges
+    assert reused.n_edges == e
+    for a, b in ((reused.center, fresh.center), (reused.neighbor, fresh.neighbor), (reused.images, fresh.images)):
+        assert np.array_equal(a[:e], b[:e])
+    # a lattice jump of the unwrapped coordinate is motion for this builder: the skin test fails
+    jumped = moved.copy()
+    jumped[:3] += s.cell[0]
+    _, bad, _ = _oracle_build(s.cell, jumped, 6.0, 2.0, 2400, ref_positions=moved)
+    assert not bad.candidate_valid and bad.overflow
+
+
+def test_window_fold():
+    st = {"overflow": False, "capacity_overflow": False, "max_edges": 0, "max_isolated": 0}
+    st = onl.window_fold(st, 10, False, False, 0, 32, True)
+    st = onl.window_fold(st, 40, False, True, 2, 32, False)
+    assert st == {"overflow": True, "capacity_overflow": True, "max_edges": 40, "max_isolated": 2}
+
+
+# ------------------------------------------------------------------------------- GPU: HIP vs oracle
+def _gpu_builder(cell, n, cutoff, skin, u_cap, device):
+    import torch
+
+    from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
+
+    return FixedCapacityGraphBuilder(cell=torch.tensor(cell, dtype=torch.float32), atomic_numbers=torch.ones(n),
+                                     u_capacity=u_cap, atom_graph_cutoff=cutoff, candidate_cutoff=cutoff + skin,
+                                     device=device)
+
+
+def _assert_build_equal(builder, ob, cand=None):
+    n = builder.n_real
+    e_cap = builder.e_capacity
+    off = builder.edge_offsets.cpu().numpy()
+    assert np.array_equal(off, ob.edge_offsets)
+    assert np.array_equal(builder.edge_counts.cpu().numpy(), ob.edge_counts)
+    ec = min(ob.n_edges, e_cap)
+    assert np.array_equal(builder.center.cpu().numpy(), ob.center)
+    assert np.array_equal(builder.neighbor.cpu().numpy(), ob.neighbor)
+    assert np.array_equal(builder.images.cpu().numpy(), ob.images)
+    assert np.array_equal(builder.distances.cpu().numpy()[:ec], ob.distances[:ec])
+    assert np.array_equal(builder.frac_coords.cpu().numpy(), ob.frac)
+    assert np.array_equal(builder.wrap_delta.cpu().numpy(), ob.wrap_delta)
+    assert np.array_equal(builder.positions.cpu().numpy(), ob.wrapped)
+    assert builder._max_displacement.cpu().numpy()[0] == ob.max_displacement
+    assert bool(builder._candidate_valid.item()) == ob.candidate_valid
+    assert bool(builder._overflow.item()) == ob.overflow
+    assert int(builder._isolated_atom_count.item()) == ob.isolated
+    ei = builder.batch.edge_index.cpu().numpy()
+    assert np.array_equal(ei[:, 0], ob.center) and np.array_equal(ei[:, 1], ob.neighbor)
+    assert np.array_equal(builder.batch.edge_image.cpu().numpy(), ob.images.astype(F32))
+    rev = builder.edge_reverse.cpu().numpy()
+    assert np.array_equal(rev, onl.reverse(ob.center, ob.neighbor, ob.images, ob.edge_offsets, e_cap))
+    if cand is not None:
+        assert np.array_equal(builder.num_neighbors.cpu().numpy(), cand.num_neighbors)
+        assert np.array_equal(builder.neighbor_matrix.cpu().numpy(), cand.neighbor_matrix)
+        assert np.array_equal(builder.neighbor_shifts.cpu().numpy(), cand.neighbor_shifts)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n_atoms", [135, 1080, 3430, 10000])
+def test_builder_bit_exact(device, n_atoms):
+    """Candidates, rows, flags and published buffers bit-exact vs the oracle, on the fused
+    single-workgroup path (<= 1024 atoms) and the multi-block path, fresh and with reused
+    candidates after seeded moves (wraps change, skin still valid)."""
+    import torch
+
+    print(f"[nl] n_atoms={n_atoms}", flush=True)
+    s = systems.perovskite_atoms(n_atoms)
+    cutoff, skin = 6.0, 2.0
+    u_cap = int(round(15.3 * n_atoms / 2)) + 64
+    builder = _gpu_builder(s.cell, n_atoms, cutoff, skin, u_cap, device)
+    pos = torch.tensor(s.positions, dtype=torch.float64, device=device)
+    builder.build(pos, rebuild_candidates=True)
+    cand, ob, _ = _oracle_build(s.cell, s.positions, cutoff, skin, builder.e_capacity)
+    torch.cuda.synchronize()
+    _assert_build_equal(builder, ob, cand)
+    cell32 = s.cell.astype(F32)
+    inv = np.linalg.inv(s.cell).astype(F32)
+    _, wraps, _ = onl.wrap(s.positions, inv, cell32)
+    rng = np.random.default_rng(7)
+    for sigma, jump, valid in ((0.08, False, True), (0.25, True, False)):
+        moved = s.positions + rng.normal(0, sigma, s.positions.shape)
+        if jump:
+            moved[: n_atoms // 10] += s.cell[1]
+        builder.build(torch.tensor(moved, device=device), rebuild_candidates=False)
+        ob2 = onl.build(moved, inv, cell32, cand, s.positions.astype(F32), wraps, F32(36.0), F32(2.0 + 1e-6),
+                        onl.self_loop_image(s.cell, cutoff)[0], builder.e_capacity)
+        torch.cuda.synchronize()
+        _assert_build_equal(builder, ob2)
+        assert ob2.candidate_valid == valid
+
+
+@pytest.mark.gpu
+def test_builder_overflow_and_triclinic(device):
+    """An edge count above e_cap sets the overflow flag and keeps every stored index in range;
+    a triclinic crystal with a cutoff above half the cell (many images) stays bit-exact."""
+    import torch
+
+    s = systems.perovskite(3)
+    builder = _gpu_builder(s.cell, 135, 6.0, 2.0, 500, device)
+    builder.build(torch.tensor(s.positions, device=device))
+    cand, ob, _ = _oracle_build(s.cell, s.positions, 6.0, 2.0, 1000)
+    torch.cuda.synchronize()
+    _assert_build_equal(builder, ob, cand)
+    assert ob.overflow and bool(builder._overflow.item())
+    cell, pos = _crystal()
+    builder = _gpu_builder(cell, pos.shape[0], 3.0, 1.0, 1500, device)
+    builder.build(torch.tensor(pos, device=device))
+    cand, ob, _ = _oracle_build(cell, pos, 3.0, 1.0, 3000)
+    torch.cuda.synchronize()
+    _assert_build_equal(builder, ob, cand)
+
+
+@pytest.mark.gpu
+def test_window_flags_kernel(device):
+    import torch
+
+    s = systems.perovskite(3)
+    builder = _gpu_builder(s.cell, 135, 6.0, 2.0, 1100, device)
+    _, status = builder.build(torch.tensor(s.positions, device=device))
+    wo = torch.zeros(1, dtype=torch.uint8, device=device)
+    wc = torch.zeros(1, dtype=torch.uint8, device=device)
+    we = torch.zeros(1, dtype=torch.int64, device=device)
+    wi = torch.zeros(1, dtype=torch.int32, device=device)
+    builder.accumulate_window(status, window_overflow=wo, window_capacity_overflow=wc, window_max_edges=we,
+                              window_max_isolated=wi, check_isolated=True)
+    assert (int(wo.item()), int(wc.item()), int(we.item()), int(wi.item())) == (0, 0, 2054, 0)
+    small = _gpu_builder(s.cell, 135, 6.0, 2.0, 500, device)
+    _, st2 = small.build(torch.tensor(s.positions, device=device))
+    small.accumulate_window(st2, window_overflow=wo, window_capacity_overflow=wc, window_max_edges=we,
+                            window_max_isolated=wi, check_isolated=True)
+    assert (int(wo.item()), int(wc.item()), int(we.item())) == (1, 1, 2054)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("max_neighbors", [1, 8, 16, None])
+def test_ragged_builder_growth_is_bitwise_identical(device, max_neighbors):
+    """Forced tiny slot counts rebuild to the same graph (tests/test_ragged_builder_overflow.py:
+    158-213 of the reference); the ragged rows equal the oracle's."""
+    import torch
+
+    from fastmd_amd.graph.gpu_graph_builder import TensorGraphBuilder
+
+    s = systems.perovskite(3)
+    b = TensorGraphBuilder(cell=torch.tensor(s.cell), atomic_numbers=torch.tensor(s.numbers), atom_graph_cutoff=6.0,
+                           max_neighbors=max_neighbors, device=device)
+    g = b.build(torch.tensor(s.positions, device=device))
+    assert max_neighbors is None or b.max_neighbors >= 20
+    cell32 = s.cell.astype(F32)
+    inv = np.linalg.inv(s.cell).astype(F32)
+    _, wraps, wrapped = onl.wrap(s.positions, inv, cell32)
+    cand = onl.candidates(wrapped, cell32, F32((6.0 + 1e-6) ** 2), 640)
+    ob = onl.build(s.positions, inv, cell32, cand, s.positions.astype(F32), wraps, F32(36.0), F32(1e-6),
+                   (0, 0, 1), int(cand.num_neighbors.sum()))
+    e = ob.n_edges
+    ei = g.edge_index.cpu().numpy()
+    assert int(g.n_edges.item()) == e == ei.shape[0]
+    assert np.array_equal(ei[:, 0], ob.center[:e]) and np.array_equal(ei[:, 1], ob.neighbor[:e])
+    assert np.array_equal(g.edge_image.cpu().numpy(), ob.images[:e].astype(F32))

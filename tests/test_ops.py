@@ -1,0 +1,179 @@
+"""(b) gather-cat, (c) CSR segment sums, (d) MFMA GEMM: HIP kernels vs the oracle."""
+import numpy as np
+import pytest
+
+from oracle import ops as oops
+from oracle import nl as onl
+from fastmd_amd import systems
+
+
+def test_relative_metric():
+    assert oops.relative([1.0, 2.0], [1.0, 2.0]) == 0.0
+    assert oops.relative([1.0, 2.5], [1.0, 2.0]) == pytest.approx(0.25)
+
+
+def test_oracle_segment_sum_closed_form():
+    value = np.arange(12, dtype=np.float64).reshape(6, 2)
+    seg = np.array([0, 0, 2, 2, 2, 1])
+    out = oops.segment_sum(value, seg, 3)
+    assert np.array_equal(out, [[2, 4], [10, 11], [18, 21]])
+    gv, gw = oops.segment_sum_vjp(np.ones((3, 2)) * [[1], [2], [3]], seg, weight=2.0, value=value)
+    assert np.array_equal(gv[:, 0], [2, 2, 6, 6, 6, 4])
+
+
+def _edge_list(n_atoms=135, cutoff=6.0):
+    s = systems.perovskite_atoms(n_atoms)
+    cell32 = s.cell.astype(np.float32)
+    inv = np.linalg.inv(s.cell).astype(np.float32)
+    _, wraps, wrapped = onl.wrap(s.positions, inv, cell32)
+    cand = onl.candidates(wrapped, cell32, np.float32(cutoff ** 2 + 1e-3), 64)
+    b = onl.build(s.positions, inv, cell32, cand, s.positions.astype(np.float32), wraps, np.float32(cutoff ** 2),
+                  np.float32(1.0), (1, 0, 0), 10 ** 8)
+    e = b.n_edges
+    rev = onl.reverse(b.center, b.neighbor, b.images, b.edge_offsets, e)
+    return b.center[:e], b.neighbor[:e], b.edge_offsets, rev, wrapped, b.distances[:e]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("F", [64, 128, 256])
+def test_gather_cat_forward_bitwise_and_vjp(device, F):
+    import torch
+
+    from fastmd_amd.ops.csr_segment_sum import Csr
+    from fastmd_amd.ops.gather_cat import aligned_gather_cat3, gather_cat
+
+    print(f"[gather_cat] F={F}", flush=True)
+    center, neighbor, off, rev, _, dist = _edge_list()
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(135, F, generator=g)
+    rbf = torch.randn(center.size, 8, generator=g)
+    src = torch.tensor(neighbor, dtype=torch.int32)
+    dst = torch.tensor(center, dtype=torch.int32)
+    xd, rbfd = x.to(device).requires_grad_(), rbf.to(device).requires_grad_()
+    csr_dst = Csr(torch.tensor(off, device=device))
+    csr_src = Csr(torch.tensor(off, device=device), torch.tensor(rev, device=device))
+    out = gather_cat(xd, src.to(device), dst.to(device), rbfd, src_csr=csr_src, dst_csr=csr_dst)
+    ref = oops.gather_cat([(x.numpy(), neighbor), (x.numpy(), center), (rbf.numpy(), None)])
+    assert out.shape == (center.size, 2 * F + 8)
+    assert np.array_equal(out.detach().cpu().numpy(), ref.astype(np.float32))
+    gout = torch.randn(out.shape, generator=g)
+    out.backward(gout.to(device))
+    gx_ref = (oops.segment_sum(gout[:, :F].numpy(), neighbor, 135) + oops.segment_sum(gout[:, F:2 * F].numpy(), center, 135))
+    assert oops.relative(xd.grad.cpu().numpy(), gx_ref) < 1e-6
+    assert np.array_equal(rbfd.grad.cpu().numpy(), gout[:, 2 * F:].numpy())
+    # deterministic: the same VJP twice, bitwise
+    g1 = xd.grad.clone()
+    xd.grad = None
+    gather_cat(xd, src.to(device), dst.to(device), rbfd, src_csr=csr_src, dst_csr=csr_dst).backward(gout.to(device))
+    assert torch.equal(g1, xd.grad)
+    # reference form, CSRs built from the indices
+    aligned = torch.randn(center.size, F, generator=g)
+    a = aligned_gather_cat3(aligned.to(device), x.to(device), dst.to(device), src.to(device))
+    assert np.array_equal(a.cpu().numpy(), oops.gather_cat([(aligned.numpy(), None), (x.numpy(), center),
+                                                            (x.numpy(), neighbor)]).astype(np.float32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("F", [1, 3, 64, 128, 256, 512])
+def test_segment_sum_identity_and_perm_csr(device, F):
+    import torch
+
+    from fastmd_amd.ops.csr_segment_sum import Csr, csr_segment_sum, segment_sum_csr
+
+    print(f"[segsum] F={F}", flush=True)
+    center, neighbor, off, rev, _, _ = _edge_list()
+    e = center.size
+    g = torch.Generator().manual_seed(1)
+    v = torch.randn(e, F, generator=g)
+    w = torch.randn(e, F, generator=g)
+    seg = torch.tensor(center, dtype=torch.int64)
+    ref = oops.segment_sum(v.numpy(), center, 135)
+    vd = v.to(device).requires_grad_()
+    wd = w.to(device).requires_grad_()
+    offd = torch.tensor(off, device=device)
+    out = csr_segment_sum(vd, seg.to(device), 135, off=offd, identity_perm=True)
+    assert oops.relative(out.detach().cpu().numpy(), ref) < 1e-5
+    out2 = csr_segment_sum(vd, seg.to(device), 135, off=offd, identity_perm=True)
+    assert torch.equal(out, out2)  # bitwise run to run
+    # weighted, CSR built from the segment (permutation path), with the VJP
+    outw = csr_segment_sum(vd, torch.tensor(neighbor, device=device), 135, weight=wd)
+    refw = oops.segment_sum(v.numpy(), neighbor, 135, weight=w.numpy())
+    assert oops.relative(outw.detach().cpu().numpy(), refw) < 1e-5
+    gout = torch.randn(135, F, generator=g)
+    outw.backward(gout.to(device))
+    gv_ref, gw_ref = oops.segment_sum_vjp(gout.numpy(), neighbor, weight=w.numpy(), value=v.numpy())
+    assert oops.relative(vd.grad.cpu().numpy(), gv_ref) < 1e-6
+    assert oops.relative(wd.grad.cpu().numpy(), gw_ref) < 1e-6
+    # two-term sum over the reverse CSR with a sign: sum_{src = i} v - sum_{dst = i} v
+    both = segment_sum_csr([(v.to(device), Csr(offd, torch.tensor(rev, device=device)), 0, 1.0, None),
+                            (v.to(device), Csr(offd), 0, -1.0, None)], 135, F)
+    ref2 = oops.segment_sum(v.numpy(), neighbor, 135) - oops.segment_sum(v.numpy(), center, 135)
+    assert oops.relative(both.cpu().numpy(), ref2) < 1e-5
+    # skip_segment: zero output row and zero gradient for its rows
+    vd.grad = None
+    out3 = csr_segment_sum(vd, seg.to(device), 135, off=offd, identity_perm=True, skip_segment=7)
+    assert float(out3[7].abs().max()) == 0.0
+    out3.sum().backward()
+    rows7 = center == 7
+    assert float(vd.grad[torch.tensor(rows7, device=device)].abs().max()) == 0.0
+
+
+@pytest.mark.gpu
+def test_segment_sum_padding_rows_excluded(device):
+    """Rows past off[-1] (fixed-capacity padding) add nothing and get zero gradient."""
+    import torch
+
+    from fastmd_amd.ops.csr_segment_sum import csr_segment_sum
+
+    off = torch.tensor([0, 2, 3], device=device)
+    v = torch.arange(10.0, device=device).reshape(5, 2).requires_grad_()
+    out = csr_segment_sum(v, None, 2, off=off, identity_perm=True)
+    assert out.tolist() == [[2.0, 4.0], [4.0, 5.0]]
+    out.sum().backward()
+    assert v.grad.tolist() == [[1, 1], [1, 1], [1, 1], [0, 0], [0, 0]]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("F", [64, 128, 256])
+@pytest.mark.parametrize("m", [1, 100, 2054])
+def test_gemm_fp32_against_fp64(device, F, m):
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import edge_gemm, linear, matmul
+
+    print(f"[gemm] F={F} m={m}", flush=True)
+    g = torch.Generator().manual_seed(2)
+    k, n = 2 * F + 8, 4 * F
+    a = torch.randn(m, k, generator=g)
+    w = torch.randn(k, n, generator=g) / k ** 0.5
+    ref = a.double() @ w.double()
+    y = edge_gemm(a.to(device), w.to(device))
+    assert oops.relative(y.cpu().numpy(), ref.numpy()) < 1e-5
+    wl = w.t().contiguous()  # F.linear layout [N, K]
+    b = torch.randn(n, generator=g)
+    ad = a.to(device).requires_grad_()
+    yl = linear(ad, wl.to(device), b.to(device))
+    assert oops.relative(yl.detach().cpu().numpy(), (ref + b.double()).numpy()) < 1e-5
+    gy = torch.randn(m, n, generator=g)
+    yl.backward(gy.to(device))
+    assert oops.relative(ad.grad.cpu().numpy(), (gy.double() @ wl.double()).numpy()) < 1e-5
+    mm = matmul(gy.to(device), wl.to(device))
+    assert oops.relative(mm.cpu().numpy(), (gy.double() @ wl.double()).numpy()) < 1e-5
+    ys = edge_gemm(a.to(device), w.to(device), epilogue="silu")
+    assert oops.relative(ys.cpu().numpy(), torch.nn.functional.silu(ref).numpy()) < 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("F", [64, 128])
+def test_gemm_bf16_against_fp64_of_rounded_inputs(device, F):
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import edge_gemm
+
+    g = torch.Generator().manual_seed(3)
+    m, k, n = 777, 2 * F + 8, 4 * F
+    a = torch.randn(m, k, generator=g)
+    w = torch.randn(k, n, generator=g) / k ** 0.5
+    y = edge_gemm(a.to(device), w.to(device), dtype=torch.bfloat16)
+    ref = a.bfloat16().double() @ w.bfloat16().double()  # products of bf16 values are exact in fp32
+    assert oops.relative(y.cpu().numpy(), ref.numpy()) < 1e-5
