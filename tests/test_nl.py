@@ -30,9 +30,14 @@ def _lattice(n_side, spacing, jitter, seed):
     return np.eye(3) * n_side * spacing, positions.astype(np.float32).astype(np.float64)
 
 
-def _oracle_build(cell, positions, cutoff, skin, e_cap, pad=None, ref_positions=None):
+def _inv32(cell):
+    """The builders' inverse: of the float32-rounded cell, in float64, rounded to float32."""
+    return np.linalg.inv(np.asarray(cell, dtype=F32).astype(np.float64)).astype(F32)
+
+
+def _oracle_build(cell, positions, cutoff, skin, e_cap, pad=None, ref_positions=None, inv=None):
     cell32 = cell.astype(F32)
-    inv = np.linalg.inv(cell).astype(F32)
+    inv = _inv32(cell) if inv is None else inv
     ref = positions if ref_positions is None else ref_positions
     _, wraps, wrapped = onl.wrap(ref, inv, cell32)
     bmax = onl.estimate_max_neighbors(cutoff + skin, safety_factor=2.0)
@@ -218,11 +223,11 @@ def test_builder_bit_exact(device, n_atoms):
     builder = _gpu_builder(s.cell, n_atoms, cutoff, skin, u_cap, device)
     pos = torch.tensor(s.positions, dtype=torch.float64, device=device)
     builder.build(pos, rebuild_candidates=True)
-    cand, ob, _ = _oracle_build(s.cell, s.positions, cutoff, skin, builder.e_capacity)
+    inv = builder.inv_cell.cpu().numpy()
+    cand, ob, _ = _oracle_build(s.cell, s.positions, cutoff, skin, builder.e_capacity, inv=inv)
     torch.cuda.synchronize()
     _assert_build_equal(builder, ob, cand)
     cell32 = s.cell.astype(F32)
-    inv = np.linalg.inv(s.cell).astype(F32)
     _, wraps, _ = onl.wrap(s.positions, inv, cell32)
     rng = np.random.default_rng(7)
     for sigma, jump, valid in ((0.08, False, True), (0.25, True, False)):
@@ -246,14 +251,14 @@ def test_builder_overflow_and_triclinic(device):
     s = systems.perovskite(3)
     builder = _gpu_builder(s.cell, 135, 6.0, 2.0, 500, device)
     builder.build(torch.tensor(s.positions, device=device))
-    cand, ob, _ = _oracle_build(s.cell, s.positions, 6.0, 2.0, 1000)
+    cand, ob, _ = _oracle_build(s.cell, s.positions, 6.0, 2.0, 1000, inv=builder.inv_cell.cpu().numpy())
     torch.cuda.synchronize()
     _assert_build_equal(builder, ob, cand)
     assert ob.overflow and bool(builder._overflow.item())
     cell, pos = _crystal()
     builder = _gpu_builder(cell, pos.shape[0], 3.0, 1.0, 1500, device)
     builder.build(torch.tensor(pos, device=device))
-    cand, ob, _ = _oracle_build(cell, pos, 3.0, 1.0, 3000)
+    cand, ob, _ = _oracle_build(cell, pos, 3.0, 1.0, 3000, inv=builder.inv_cell.cpu().numpy())
     torch.cuda.synchronize()
     _assert_build_equal(builder, ob, cand)
 
@@ -294,7 +299,7 @@ def test_ragged_builder_growth_is_bitwise_identical(device, max_neighbors):
     g = b.build(torch.tensor(s.positions, device=device))
     assert max_neighbors is None or b.max_neighbors >= 20
     cell32 = s.cell.astype(F32)
-    inv = np.linalg.inv(s.cell).astype(F32)
+    inv = b.inv_cell.cpu().numpy()
     _, wraps, wrapped = onl.wrap(s.positions, inv, cell32)
     cand = onl.candidates(wrapped, cell32, F32((6.0 + 1e-6) ** 2), 640)
     ob = onl.build(s.positions, inv, cell32, cand, s.positions.astype(F32), wraps, F32(36.0), F32(1e-6),
