@@ -32,8 +32,8 @@ SIGNATURES: dict[str, tuple] = {
                                     _i32, _i32, _i32, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                     _p, _p, _p, _p, _p, _p]),
     "fmd_nl_reverse": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i64, _p, _p]),
-    "fmd_nl_window_flags": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _p, _p, _p, _p, _p]),
-    "fmd_gather_cat_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _i64, _p, _i64, _p]),
+    "fmd_nl_window_flags": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p]),
+    "fmd_gather_cat_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _i64, _p, _i64, _p]),
     "fmd_segsum_csr_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32,
                                           _p, _i64, _p]),
     "fmd_segsum_csr_t_f32": (ctypes.c_int, [_p, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _p,
@@ -44,6 +44,18 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_nhc_post_force": (ctypes.c_int, [_p, _p, _i32, _p, _p, _p, _p, _p, _p, _i32, _p, _i64, _i32, _i32,
                                           _i32, _p]),
     "fmd_sum_f64": (ctypes.c_int, [_p, _i32, _i64, _p, _p]),
+    "fmd_edge_geometry_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _f32, _i32, _p, _p, _p, _p]),
+    "fmd_edge_geometry_bwd_f32": (ctypes.c_int, [_p, _p, _i32, _p, _i64, _p, _i64, _p, _p, _i64, _p, _p]),
+    "fmd_mace_message_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _f32, _p, _p, _p]),
+    "fmd_mace_message_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _p, _p, _f32,
+                                                _p, _p, _i32, _p, _p, _i32, _p]),
+    "fmd_mace_symcon_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p]),
+    "fmd_mace_symcon_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p]),
+    "fmd_mace_energy_f32": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _p, _p, _f32, _f32, _i64, _p, _p]),
+    "fmd_mace_energy_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _f32, _i64, _p, _p, _p]),
+    "fmd_embed_f32": (ctypes.c_int, [_p, _p, _i64, _i32, _p, _p]),
+    "fmd_morse_f32": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _f32, _f32, _f32, _f32, _f32, _p, _p, _p]),
+    "fmd_morse_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _p, _p]),
 }
 
 _lock = threading.Lock()

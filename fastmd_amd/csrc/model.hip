@@ -1,0 +1,682 @@
+// Model kernels of the MD step: edge geometry + radial basis, the MACE-like interaction
+// (fused message + receiver aggregation, symmetric contraction, readout) and their explicit
+// VJPs, and the Morse pair potential. fp32, deterministic (no float atomics: receiver sums walk
+// the centre CSR, sender sums walk the reverse-edge CSR).
+//
+// Edge rows: real rows [0, min(n_edges, e_cap)), n_edges read from device memory (a captured
+// graph replays them with the current count); rows past it are fixed-capacity padding and are
+// skipped (their contributions are exactly zero by the padding contract: far self-loops lie
+// beyond the cutoff, where the envelope and its derivative vanish).
+// Channel layout: a wavefront owns a node or an edge; lane l holds channels l*CPL .. +CPL
+// (C = 64 * CPL). Node features: h0 [N, C], h1 [N, 3, C]. Per edge z [E, 4C] = the four path
+// weight blocks (a | b | c | d) before the SiLU.
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / FMD_WAVE;
+constexpr float kPi = 3.14159265358979323846f;
+
+__device__ __forceinline__ int64_t real_rows(const int64_t* n_edges, int64_t e_cap) {
+  const int64_t e = n_edges[0];
+  return e < e_cap ? e : e_cap;
+}
+
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// ------------------------------------------------------------------------------------------
+// edge geometry: geo[e] = (ux, uy, uz, r, fcut, dfcut, 0, 0); ef[e, n] = b_n(r) fcut(r);
+// def[e, n] = d ef / dr. b_n = sqrt(2/rc) sin(n pi r / rc) / r (n = 1..NB), fcut the p = 5
+// polynomial envelope 1 - 21 x^5 + 35 x^6 - 15 x^7 (x = r / rc < 1, else 0).
+// vec = (pos[j] + image @ cell) - pos[c], image @ cell formed row by row.
+// ------------------------------------------------------------------------------------------
+__global__ void edge_geometry_kernel(const float* pos, const float* cell, const int32_t* edge_index,
+                                     const float* edge_image, const int64_t* n_edges, int64_t e_cap, float rc, int nb,
+                                     float* geo, float* ef, float* def) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= e_cap) return;
+  const int64_t rows = real_rows(n_edges, e_cap);
+  float* g = geo + 8 * e;
+  if (e >= rows) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) g[k] = 0.f;
+    g[3] = 1.f;
+    for (int n = 0; n < nb; ++n) {
+      ef[e * nb + n] = 0.f;
+      def[e * nb + n] = 0.f;
+    }
+    return;
+  }
+  const int32_t c = edge_index[2 * e], j = edge_index[2 * e + 1];
+  const float ix = edge_image[3 * e], iy = edge_image[3 * e + 1], iz = edge_image[3 * e + 2];
+  float v[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    float s = ix * cell[k];
+    s = s + iy * cell[3 + k];
+    s = s + iz * cell[6 + k];
+    v[k] = (pos[3 * j + k] + s) - pos[3 * c + k];
+  }
+  const float r = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+  const float inv_r = 1.0f / r;
+  const float x = r / rc;
+  float fc = 0.f, dfc = 0.f;
+  if (x < 1.0f) {
+    const float x2 = x * x, x4 = x2 * x2, x5 = x4 * x;
+    fc = 1.0f - 21.0f * x5 + 35.0f * x5 * x - 15.0f * x5 * x2;
+    const float omx = 1.0f - x;
+    dfc = -105.0f * x4 * omx * omx / rc;
+  }
+  g[0] = v[0] * inv_r;
+  g[1] = v[1] * inv_r;
+  g[2] = v[2] * inv_r;
+  g[3] = r;
+  g[4] = fc;
+  g[5] = dfc;
+  g[6] = 0.f;
+  g[7] = 0.f;
+  const float pref = sqrtf(2.0f / rc);
+  for (int n = 1; n <= nb; ++n) {
+    const float k = (float)n * kPi / rc;
+    const float sn = sinf(k * r), cs = cosf(k * r);
+    const float b = pref * sn * inv_r;
+    const float db = pref * (k * cs * inv_r - sn * inv_r * inv_r);
+    ef[e * nb + (n - 1)] = b * fc;
+    def[e * nb + (n - 1)] = db * fc + b * dfc;
+  }
+}
+
+// g_vec[e] = g_r u + (g_u - (g_u . u) u) / r with g_r = sum_n g_ef[e,n] def[e,n] (over up to two
+// g_ef sources) + g_fcut dfcut; g_geo[e] = (g_ux, g_uy, g_uz, g_fcut).
+__global__ void edge_geometry_bwd_kernel(const float* geo, const float* def, int nb, const float* gef0, int64_t ld0,
+                                         const float* gef1, int64_t ld1, const float* ggeo, const int64_t* n_edges,
+                                         int64_t e_cap, float* gvec) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= e_cap) return;
+  const int64_t rows = real_rows(n_edges, e_cap);
+  if (e >= rows) {
+    gvec[3 * e] = gvec[3 * e + 1] = gvec[3 * e + 2] = 0.f;
+    return;
+  }
+  const float* g = geo + 8 * e;
+  float gr = 0.f;
+  for (int n = 0; n < nb; ++n) {
+    float ge = 0.f;
+    if (gef0) ge += gef0[e * ld0 + n];
+    if (gef1) ge += gef1[e * ld1 + n];
+    gr += ge * def[e * nb + n];
+  }
+  float gu[3] = {0.f, 0.f, 0.f};
+  if (ggeo) {
+    gu[0] = ggeo[4 * e];
+    gu[1] = ggeo[4 * e + 1];
+    gu[2] = ggeo[4 * e + 2];
+    gr += ggeo[4 * e + 3] * g[5];
+  }
+  const float inv_r = 1.0f / g[3];
+  const float gdotu = gu[0] * g[0] + gu[1] * g[1] + gu[2] * g[2];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) gvec[3 * e + k] = gr * g[k] + (gu[k] - gdotu * g[k]) * inv_r;
+}
+
+// ------------------------------------------------------------------------------------------
+// interaction: forward message + receiver sum. One wave per centre node i.
+//   w = silu(z_e) * fcut_e; proj = h1_j . u; m0 = wa h0_j + wc proj; m1_x = wb h0_j u_x + wd h1_j,x
+//   A0_i = inv_avg * sum_e m0, A1_i = inv_avg * sum_e m1
+// ------------------------------------------------------------------------------------------
+template <int CPL, bool H1>
+__global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const float* geo, const int32_t* edge_index,
+                                                           const int64_t* off, const int64_t* n_edges, int64_t e_cap,
+                                                           int64_t n, const float* h0, const float* h1, float inv_avg,
+                                                           float* A0, float* A1) {
+  constexpr int C = 64 * CPL;
+  const int lane = threadIdx.x & 63;
+  const int64_t i = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64;
+  if (i >= n) return;
+  const int64_t rows = real_rows(n_edges, e_cap);
+  int64_t lo = off[i], hi = off[i + 1];
+  hi = hi < rows ? hi : rows;
+  lo = lo < hi ? lo : hi;
+  float a0[CPL], a1[3][CPL];
+#pragma unroll
+  for (int q = 0; q < CPL; ++q) {
+    a0[q] = 0.f;
+    a1[0][q] = a1[1][q] = a1[2][q] = 0.f;
+  }
+  const int c0 = lane * CPL;
+  for (int64_t e = lo; e < hi; ++e) {
+    const float* g = geo + 8 * e;
+    const float ux = g[0], uy = g[1], uz = g[2], fc = g[4];
+    const int64_t j = edge_index[2 * e + 1];
+    const float* ze = z + e * 4 * C + c0;
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) {
+      const float za = ze[q], zb = ze[C + q];
+      const float wa = za * sigmoid(za) * fc, wb = zb * sigmoid(zb) * fc;
+      const float hj = h0[j * C + c0 + q];
+      float m0 = wa * hj;
+      const float t = wb * hj;
+      float m1x = t * ux, m1y = t * uy, m1z = t * uz;
+      if (H1) {
+        const float zc = ze[2 * C + q], zd = ze[3 * C + q];
+        const float wc = zc * sigmoid(zc) * fc, wd = zd * sigmoid(zd) * fc;
+        const float hx = h1[(j * 3 + 0) * C + c0 + q], hy = h1[(j * 3 + 1) * C + c0 + q],
+                    hz = h1[(j * 3 + 2) * C + c0 + q];
+        m0 += wc * (hx * ux + hy * uy + hz * uz);
+        m1x += wd * hx;
+        m1y += wd * hy;
+        m1z += wd * hz;
+      }
+      a0[q] += m0;
+      a1[0][q] += m1x;
+      a1[1][q] += m1y;
+      a1[2][q] += m1z;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < CPL; ++q) {
+    A0[i * C + c0 + q] = a0[q] * inv_avg;
+    A1[(i * 3 + 0) * C + c0 + q] = a1[0][q] * inv_avg;
+    A1[(i * 3 + 1) * C + c0 + q] = a1[1][q] * inv_avg;
+    A1[(i * 3 + 2) * C + c0 + q] = a1[2][q] * inv_avg;
+  }
+}
+
+// VJP, edge side (one wave per centre node i, its rows e): with gA = inv_avg * (gA0_i, gA1_i),
+//   g_wa = gA0 h0_j, g_wb = h0_j (gA1 . u), g_wc = gA0 proj, g_wd = sum_x gA1_x h1_j,x
+//   g_z = g_w * fcut * silu'(z)            -> gz [E, 4C]
+//   g_fcut = sum_ch g_w * silu(z), g_u_x = sum_ch (gA0 wc h1_j,x + gA1_x wb h0_j)  -> ggeo [E, 4]
+template <int CPL, bool H1>
+__global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
+    const float* z, const float* geo, const int32_t* edge_index, const int64_t* off, const int64_t* n_edges,
+    int64_t e_cap, int64_t n, const float* h0, const float* h1, const float* gA0, const float* gA1, float inv_avg,
+    float* gz, float* ggeo, int accumulate_geo) {
+  constexpr int C = 64 * CPL;
+  const int lane = threadIdx.x & 63;
+  const int64_t i = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64;
+  if (i >= n) return;
+  const int64_t rows = real_rows(n_edges, e_cap);
+  int64_t lo = off[i], hi = off[i + 1];
+  hi = hi < rows ? hi : rows;
+  lo = lo < hi ? lo : hi;
+  const int c0 = lane * CPL;
+  float g0[CPL], g1[3][CPL];
+#pragma unroll
+  for (int q = 0; q < CPL; ++q) {
+    g0[q] = gA0[i * C + c0 + q] * inv_avg;
+    g1[0][q] = gA1[(i * 3 + 0) * C + c0 + q] * inv_avg;
+    g1[1][q] = gA1[(i * 3 + 1) * C + c0 + q] * inv_avg;
+    g1[2][q] = gA1[(i * 3 + 2) * C + c0 + q] * inv_avg;
+  }
+  for (int64_t e = lo; e < hi; ++e) {
+    const float* g = geo + 8 * e;
+    const float ux = g[0], uy = g[1], uz = g[2], fc = g[4];
+    const int64_t j = edge_index[2 * e + 1];
+    const float* ze = z + e * 4 * C + c0;
+    float* gze = gz + e * 4 * C + c0;
+    float sf = 0.f, su0 = 0.f, su1 = 0.f, su2 = 0.f;
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) {
+      const float hj = h0[j * C + c0 + q];
+      const float gu = g1[0][q] * ux + g1[1][q] * uy + g1[2][q] * uz;
+      const float za = ze[q], zb = ze[C + q];
+      const float sa = sigmoid(za), sb = sigmoid(zb);
+      const float gwa = g0[q] * hj, gwb = hj * gu;
+      gze[q] = gwa * fc * sa * (1.0f + za * (1.0f - sa));
+      gze[C + q] = gwb * fc * sb * (1.0f + zb * (1.0f - sb));
+      sf += gwa * za * sa + gwb * zb * sb;
+      const float wb = zb * sb * fc;
+      su0 += g1[0][q] * wb * hj;
+      su1 += g1[1][q] * wb * hj;
+      su2 += g1[2][q] * wb * hj;
+      if (H1) {
+        const float hx = h1[(j * 3 + 0) * C + c0 + q], hy = h1[(j * 3 + 1) * C + c0 + q],
+                    hz = h1[(j * 3 + 2) * C + c0 + q];
+        const float zc = ze[2 * C + q], zd = ze[3 * C + q];
+        const float sc = sigmoid(zc), sd = sigmoid(zd);
+        const float proj = hx * ux + hy * uy + hz * uz;
+        const float gwc = g0[q] * proj, gwd = g1[0][q] * hx + g1[1][q] * hy + g1[2][q] * hz;
+        gze[2 * C + q] = gwc * fc * sc * (1.0f + zc * (1.0f - sc));
+        gze[3 * C + q] = gwd * fc * sd * (1.0f + zd * (1.0f - sd));
+        sf += gwc * zc * sc + gwd * zd * sd;
+        const float t = g0[q] * zc * sc * fc;
+        su0 += t * hx;
+        su1 += t * hy;
+        su2 += t * hz;
+      } else {
+        gze[2 * C + q] = 0.f;
+        gze[3 * C + q] = 0.f;
+      }
+    }
+    sf = wave_sum(sf);
+    su0 = wave_sum(su0);
+    su1 = wave_sum(su1);
+    su2 = wave_sum(su2);
+    if (lane == 0) {
+      float* gg = ggeo + 4 * e;
+      if (accumulate_geo) {
+        gg[0] += su0;
+        gg[1] += su1;
+        gg[2] += su2;
+        gg[3] += sf;
+      } else {
+        gg[0] = su0;
+        gg[1] = su1;
+        gg[2] = su2;
+        gg[3] = sf;
+      }
+    }
+  }
+}
+
+// VJP, sender side (one wave per node j, over the reverse rows e = reverse[e'] of its rows e'
+// as a centre; the receiver of e is i = neighbor[e']):
+//   g_h0_j += gA0_i wa_e + wb_e (gA1_i . u_e);  g_h1_j,x += gA0_i wc_e u_e,x + gA1_i,x wd_e
+template <int CPL, bool H1>
+__global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
+    const float* z, const float* geo, const int32_t* edge_index, const int32_t* reverse, const int64_t* off,
+    const int64_t* n_edges, int64_t e_cap, int64_t n, const float* gA0, const float* gA1, float inv_avg, float* gh0,
+    float* gh1, int accumulate) {
+  constexpr int C = 64 * CPL;
+  const int lane = threadIdx.x & 63;
+  const int64_t jn = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64;
+  if (jn >= n) return;
+  const int64_t rows = real_rows(n_edges, e_cap);
+  int64_t lo = off[jn], hi = off[jn + 1];
+  hi = hi < rows ? hi : rows;
+  lo = lo < hi ? lo : hi;
+  const int c0 = lane * CPL;
+  float a0[CPL], a1[3][CPL];
+#pragma unroll
+  for (int q = 0; q < CPL; ++q) a0[q] = a1[0][q] = a1[1][q] = a1[2][q] = 0.f;
+  for (int64_t ep = lo; ep < hi; ++ep) {
+    const int64_t e = reverse[ep];
+    if (e < 0) continue;
+    const int64_t i = edge_index[2 * ep + 1];
+    const float* g = geo + 8 * e;
+    const float ux = g[0], uy = g[1], uz = g[2], fc = g[4];
+    const float* ze = z + e * 4 * C + c0;
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) {
+      const float g0 = gA0[i * C + c0 + q];
+      const float gx = gA1[(i * 3 + 0) * C + c0 + q], gy = gA1[(i * 3 + 1) * C + c0 + q],
+                  gzv = gA1[(i * 3 + 2) * C + c0 + q];
+      const float za = ze[q], zb = ze[C + q];
+      const float wa = za * sigmoid(za) * fc, wb = zb * sigmoid(zb) * fc;
+      a0[q] += g0 * wa + wb * (gx * ux + gy * uy + gzv * uz);
+      if (H1) {
+        const float zc = ze[2 * C + q], zd = ze[3 * C + q];
+        const float wc = zc * sigmoid(zc) * fc, wd = zd * sigmoid(zd) * fc;
+        const float t = g0 * wc;
+        a1[0][q] += t * ux + gx * wd;
+        a1[1][q] += t * uy + gy * wd;
+        a1[2][q] += t * uz + gzv * wd;
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < CPL; ++q) {
+    float* d0 = gh0 + jn * C + c0 + q;
+    const float v0 = a0[q] * inv_avg;
+    *d0 = accumulate ? *d0 + v0 : v0;
+    if (H1 && gh1) {
+      for (int x = 0; x < 3; ++x) {
+        float* d1 = gh1 + (jn * 3 + x) * C + c0 + q;
+        const float v1 = a1[x][q] * inv_avg;
+        *d1 = accumulate ? *d1 + v1 : v1;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// symmetric contraction (correlation order 3, L <= 1), per node and channel, element weights
+//   n1 = |P1|^2;  B0 = c1 P0 + c2 P0^2 + c3 n1 + c4 P0^3 + c5 P0 n1
+//   B1_x = (d1 + d2 P0 + d3 P0^2 + d4 n1) P1_x
+// Wc [nel, 5, C], Wd [nel, 4, C]; elem[i] the element index of node i.
+// ------------------------------------------------------------------------------------------
+__global__ void symcon_kernel(const float* P0, const float* P1, const int32_t* elem, const float* Wc,
+                              const float* Wd, int64_t n, int C, float* B0, float* B1) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= n * C) return;
+  const int64_t i = k / C;
+  const int ch = (int)(k - i * C);
+  const int el = elem[i];
+  const float p0 = P0[k];
+  const float px = P1[(i * 3 + 0) * C + ch], py = P1[(i * 3 + 1) * C + ch], pz = P1[(i * 3 + 2) * C + ch];
+  const float n1 = px * px + py * py + pz * pz;
+  const float* c = Wc + (int64_t)el * 5 * C + ch;
+  B0[k] = c[0] * p0 + c[C] * p0 * p0 + c[2 * C] * n1 + c[3 * C] * p0 * p0 * p0 + c[4 * C] * p0 * n1;
+  if (B1) {
+    const float* d = Wd + (int64_t)el * 4 * C + ch;
+    const float q = d[0] + d[C] * p0 + d[2 * C] * p0 * p0 + d[3 * C] * n1;
+    B1[(i * 3 + 0) * C + ch] = q * px;
+    B1[(i * 3 + 1) * C + ch] = q * py;
+    B1[(i * 3 + 2) * C + ch] = q * pz;
+  }
+}
+
+__global__ void symcon_bwd_kernel(const float* P0, const float* P1, const int32_t* elem, const float* Wc,
+                                  const float* Wd, const float* gB0, const float* gB1, int64_t n, int C, float* gP0,
+                                  float* gP1) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= n * C) return;
+  const int64_t i = k / C;
+  const int ch = (int)(k - i * C);
+  const int el = elem[i];
+  const float p0 = P0[k];
+  const float p[3] = {P1[(i * 3 + 0) * C + ch], P1[(i * 3 + 1) * C + ch], P1[(i * 3 + 2) * C + ch]};
+  const float n1 = p[0] * p[0] + p[1] * p[1] + p[2] * p[2];
+  const float* c = Wc + (int64_t)el * 5 * C + ch;
+  const float gb0 = gB0[k];
+  float gp0 = gb0 * (c[0] + 2.0f * c[C] * p0 + 3.0f * c[3 * C] * p0 * p0 + c[4 * C] * n1);
+  float gn1 = gb0 * (c[2 * C] + c[4 * C] * p0);
+  float gp[3] = {0.f, 0.f, 0.f};
+  if (gB1) {
+    const float* d = Wd + (int64_t)el * 4 * C + ch;
+    const float q = d[0] + d[C] * p0 + d[2 * C] * p0 * p0 + d[3 * C] * n1;
+    float gq = 0.f;
+#pragma unroll
+    for (int x = 0; x < 3; ++x) {
+      const float g = gB1[(i * 3 + x) * C + ch];
+      gp[x] = g * q;
+      gq += g * p[x];
+    }
+    gp0 += gq * (d[C] + 2.0f * d[2 * C] * p0);
+    gn1 += gq * d[3 * C];
+  }
+  gP0[k] = gp0;
+#pragma unroll
+  for (int x = 0; x < 3; ++x) gP1[(i * 3 + x) * C + ch] = gp[x] + 2.0f * gn1 * p[x];
+}
+
+// ------------------------------------------------------------------------------------------
+// readout and node energy: one wave per node
+//   E_i = E0[elem_i] + scale * (h_a,i . wr1 + sum_k silu(y_i,k) wr2b_k) + shift
+// VJP: gha_i = scale gE_i wr1, gy_i,k = scale gE_i wr2b_k silu'(y_i,k)
+// ------------------------------------------------------------------------------------------
+__global__ void energy_kernel(const float* ha, const float* wr1, const float* y, const float* wr2b, int C, int H,
+                              const int32_t* elem, const float* e0, float scale, float shift, int64_t n, float* energy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64;
+  if (i >= n) return;
+  float s = 0.f;
+  for (int c = lane; c < C; c += 64) s += ha[i * C + c] * wr1[c];
+  for (int k = lane; k < H; k += 64) {
+    const float v = y[i * H + k];
+    s += v * sigmoid(v) * wr2b[k];
+  }
+  s = wave_sum(s);
+  if (lane == 0) energy[i] = e0[elem[i]] + scale * s + shift;
+}
+
+__global__ void energy_bwd_kernel(const float* gE, const float* wr1, const float* y, const float* wr2b, int C, int H,
+                                  float scale, int64_t n, float* gha, float* gy) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = n * (C + H);
+  if (k >= total) return;
+  const int64_t i = k / (C + H);
+  const int c = (int)(k - i * (C + H));
+  const float g = scale * gE[i];
+  if (c < C) {
+    gha[i * C + c] = g * wr1[c];
+  } else {
+    const int h = c - C;
+    const float v = y[i * H + h];
+    const float sg = sigmoid(v);
+    gy[i * H + h] = g * wr2b[h] * sg * (1.0f + v * (1.0f - sg));
+  }
+}
+
+// h0[i] = table[elem[i]]  (element embedding)
+__global__ void embed_kernel(const int32_t* elem, const float* table, int64_t n, int C, float* h0) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= n * C) return;
+  const int64_t i = k / C;
+  h0[k] = table[(int64_t)elem[i] * C + (k - i * C)];
+}
+
+// ------------------------------------------------------------------------------------------
+// Morse pair potential, shifted to zero at the cutoff: per centre node (one thread per node):
+//   E_i = 1/2 sum_e V(r_e),  V = D[(1 - exp(-a(r - r0)))^2 - 1] - V_rc (r < rc, else 0)
+//   dvdr[e] = V'(r_e) (0 beyond the cutoff)
+// ------------------------------------------------------------------------------------------
+__global__ void morse_kernel(const float* geo, const int64_t* off, const int64_t* n_edges, int64_t e_cap, int64_t n,
+                             float D, float a, float r0, float rc, float vshift, float* energy, float* dvdr) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t rows = real_rows(n_edges, e_cap);
+  int64_t lo = off[i], hi = off[i + 1];
+  hi = hi < rows ? hi : rows;
+  lo = lo < hi ? lo : hi;
+  float s = 0.f;
+  for (int64_t e = lo; e < hi; ++e) {
+    const float r = geo[8 * e + 3];
+    float v = 0.f, dv = 0.f;
+    if (r < rc) {
+      const float ex = __expf(-a * (r - r0));
+      const float om = 1.0f - ex;
+      v = D * (om * om - 1.0f) - vshift;
+      dv = 2.0f * D * om * a * ex;
+    }
+    s += v;
+    dvdr[e] = dv;
+  }
+  energy[i] = 0.5f * s;
+}
+
+// g_geo[e] = (0, 0, 0, 0) and g_r folded into g_vec directly: gvec[e] = 0.5 gE[c] V'(r) u
+__global__ void morse_bwd_kernel(const float* geo, const float* dvdr, const int32_t* edge_index, const float* gE,
+                                 const int64_t* n_edges, int64_t e_cap, float* gvec) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= e_cap) return;
+  const int64_t rows = real_rows(n_edges, e_cap);
+  if (e >= rows) {
+    gvec[3 * e] = gvec[3 * e + 1] = gvec[3 * e + 2] = 0.f;
+    return;
+  }
+  const float g = 0.5f * gE[edge_index[2 * e]] * dvdr[e];
+  gvec[3 * e] = g * geo[8 * e];
+  gvec[3 * e + 1] = g * geo[8 * e + 1];
+  gvec[3 * e + 2] = g * geo[8 * e + 2];
+}
+
+template <int CPL>
+int launch_message(bool h1, dim3 grid, hipStream_t s, const float* z, const float* geo, const int32_t* ei,
+                   const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const float* h0,
+                   const float* h1p, float inv_avg, float* A0, float* A1) {
+  if (h1)
+    hipLaunchKernelGGL((message_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, geo, ei, off, ne, e_cap, n, h0, h1p,
+                       inv_avg, A0, A1);
+  else
+    hipLaunchKernelGGL((message_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, geo, ei, off, ne, e_cap, n, h0,
+                       h1p, inv_avg, A0, A1);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+}  // namespace
+
+#define FMD_CPL_DISPATCH(C, FN, ...)                 \
+  switch ((C) / 64) {                                \
+    case 1: return FN<1>(__VA_ARGS__);               \
+    case 2: return FN<2>(__VA_ARGS__);               \
+    case 4: return FN<4>(__VA_ARGS__);               \
+    default: return FMD_EUNSUPPORTED;                \
+  }
+
+namespace {
+template <int CPL>
+int launch_bwd_edge(bool h1, dim3 grid, hipStream_t s, const float* z, const float* geo, const int32_t* ei,
+                    const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const float* h0,
+                    const float* h1p, const float* gA0, const float* gA1, float inv_avg, float* gz, float* ggeo,
+                    int acc) {
+  if (h1)
+    hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, geo, ei, off, ne, e_cap,
+                       n, h0, h1p, gA0, gA1, inv_avg, gz, ggeo, acc);
+  else
+    hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, geo, ei, off, ne, e_cap,
+                       n, h0, h1p, gA0, gA1, inv_avg, gz, ggeo, acc);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+template <int CPL>
+int launch_bwd_src(bool h1, dim3 grid, hipStream_t s, const float* z, const float* geo, const int32_t* ei,
+                   const int32_t* rev, const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n,
+                   const float* gA0, const float* gA1, float inv_avg, float* gh0, float* gh1, int acc) {
+  if (h1)
+    hipLaunchKernelGGL((message_bwd_src_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, geo, ei, rev, off, ne,
+                       e_cap, n, gA0, gA1, inv_avg, gh0, gh1, acc);
+  else
+    hipLaunchKernelGGL((message_bwd_src_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, geo, ei, rev, off, ne,
+                       e_cap, n, gA0, gA1, inv_avg, gh0, gh1, acc);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int fmd_edge_geometry_f32(const float* positions, const float* cell, const int32_t* edge_index,
+                          const float* edge_image, const int64_t* n_edges, int64_t e_cap, float rc, int32_t nb,
+                          float* geo, float* ef, float* def, hipStream_t stream) {
+  FMD_REQUIRE(positions && cell && edge_index && edge_image && n_edges && geo && ef && def);
+  FMD_REQUIRE(e_cap >= 0 && nb > 0 && rc > 0.f);
+  if (e_cap == 0) return FMD_OK;
+  hipLaunchKernelGGL(edge_geometry_kernel, dim3((unsigned)fmd_cdiv(e_cap, 256)), dim3(256), 0, stream, positions,
+                     cell, edge_index, edge_image, n_edges, e_cap, rc, nb, geo, ef, def);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, const float* gef0, int64_t ld0,
+                              const float* gef1, int64_t ld1, const float* ggeo, const int64_t* n_edges,
+                              int64_t e_cap, float* gvec, hipStream_t stream) {
+  FMD_REQUIRE(geo && def && n_edges && gvec && e_cap >= 0 && nb > 0);
+  if (e_cap == 0) return FMD_OK;
+  hipLaunchKernelGGL(edge_geometry_bwd_kernel, dim3((unsigned)fmd_cdiv(e_cap, 256)), dim3(256), 0, stream, geo, def,
+                     nb, gef0, ld0, gef1, ld1, ggeo, n_edges, e_cap, gvec);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_mace_message_f32(const float* z, const float* geo, const int32_t* edge_index, const int64_t* edge_offsets,
+                         const int64_t* n_edges, int64_t e_cap, int64_t n_atoms, int32_t channels, const float* h0,
+                         const float* h1, float inv_avg, float* A0, float* A1, hipStream_t stream) {
+  FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && A0 && A1 && n_atoms >= 0);
+  if (n_atoms == 0) return FMD_OK;
+  dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
+  FMD_CPL_DISPATCH(channels, launch_message, h1 != nullptr, grid, stream, z, geo, edge_index, edge_offsets, n_edges,
+                   e_cap, n_atoms, h0, h1, inv_avg, A0, A1);
+}
+
+int fmd_mace_message_bwd_f32(const float* z, const float* geo, const int32_t* edge_index, const int32_t* reverse,
+                             const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
+                             int32_t channels, const float* h0, const float* h1, const float* gA0, const float* gA1,
+                             float inv_avg, float* gz, float* ggeo, int32_t accumulate_geo, float* gh0, float* gh1,
+                             int32_t accumulate_h, hipStream_t stream) {
+  FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && gA0 && gA1 && gz && ggeo && n_atoms >= 0);
+  FMD_REQUIRE(!gh0 || reverse);
+  if (n_atoms == 0) return FMD_OK;
+  dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
+  int rc = FMD_OK;
+  switch (channels / 64) {
+    case 1: rc = launch_bwd_edge<1>(h1 != nullptr, grid, stream, z, geo, edge_index, edge_offsets, n_edges, e_cap,
+                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, ggeo, accumulate_geo); break;
+    case 2: rc = launch_bwd_edge<2>(h1 != nullptr, grid, stream, z, geo, edge_index, edge_offsets, n_edges, e_cap,
+                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, ggeo, accumulate_geo); break;
+    case 4: rc = launch_bwd_edge<4>(h1 != nullptr, grid, stream, z, geo, edge_index, edge_offsets, n_edges, e_cap,
+                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, ggeo, accumulate_geo); break;
+    default: return FMD_EUNSUPPORTED;
+  }
+  if (rc != FMD_OK || !gh0) return rc;
+  switch (channels / 64) {
+    case 1: return launch_bwd_src<1>(h1 != nullptr, grid, stream, z, geo, edge_index, reverse, edge_offsets, n_edges,
+                                     e_cap, n_atoms, gA0, gA1, inv_avg, gh0, gh1, accumulate_h);
+    case 2: return launch_bwd_src<2>(h1 != nullptr, grid, stream, z, geo, edge_index, reverse, edge_offsets, n_edges,
+                                     e_cap, n_atoms, gA0, gA1, inv_avg, gh0, gh1, accumulate_h);
+    case 4: return launch_bwd_src<4>(h1 != nullptr, grid, stream, z, geo, edge_index, reverse, edge_offsets, n_edges,
+                                     e_cap, n_atoms, gA0, gA1, inv_avg, gh0, gh1, accumulate_h);
+    default: return FMD_EUNSUPPORTED;
+  }
+}
+
+int fmd_mace_symcon_f32(const float* P0, const float* P1, const int32_t* elem, const float* Wc, const float* Wd,
+                        int64_t n_atoms, int32_t channels, float* B0, float* B1, hipStream_t stream) {
+  FMD_REQUIRE(P0 && P1 && elem && Wc && B0 && (!B1 || Wd) && n_atoms >= 0 && channels > 0);
+  if (n_atoms == 0) return FMD_OK;
+  const int64_t total = n_atoms * channels;
+  hipLaunchKernelGGL(symcon_kernel, dim3((unsigned)fmd_cdiv(total, 256)), dim3(256), 0, stream, P0, P1, elem, Wc, Wd,
+                     n_atoms, channels, B0, B1);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_mace_symcon_bwd_f32(const float* P0, const float* P1, const int32_t* elem, const float* Wc, const float* Wd,
+                            const float* gB0, const float* gB1, int64_t n_atoms, int32_t channels, float* gP0,
+                            float* gP1, hipStream_t stream) {
+  FMD_REQUIRE(P0 && P1 && elem && Wc && gB0 && gP0 && gP1 && (!gB1 || Wd) && n_atoms >= 0 && channels > 0);
+  if (n_atoms == 0) return FMD_OK;
+  const int64_t total = n_atoms * channels;
+  hipLaunchKernelGGL(symcon_bwd_kernel, dim3((unsigned)fmd_cdiv(total, 256)), dim3(256), 0, stream, P0, P1, elem, Wc,
+                     Wd, gB0, gB1, n_atoms, channels, gP0, gP1);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_mace_energy_f32(const float* ha, const float* wr1, const float* y, const float* wr2b, int32_t channels,
+                        int32_t hidden, const int32_t* elem, const float* e0, float scale, float shift,
+                        int64_t n_atoms, float* energy, hipStream_t stream) {
+  FMD_REQUIRE(ha && wr1 && y && wr2b && elem && e0 && energy && n_atoms >= 0);
+  if (n_atoms == 0) return FMD_OK;
+  hipLaunchKernelGGL(energy_kernel, dim3((unsigned)fmd_cdiv(n_atoms, kWaves)), dim3(kThreads), 0, stream, ha, wr1, y,
+                     wr2b, channels, hidden, elem, e0, scale, shift, n_atoms, energy);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_mace_energy_bwd_f32(const float* gE, const float* wr1, const float* y, const float* wr2b, int32_t channels,
+                            int32_t hidden, float scale, int64_t n_atoms, float* gha, float* gy, hipStream_t stream) {
+  FMD_REQUIRE(gE && wr1 && y && wr2b && gha && gy && n_atoms >= 0);
+  if (n_atoms == 0) return FMD_OK;
+  const int64_t total = n_atoms * (channels + hidden);
+  hipLaunchKernelGGL(energy_bwd_kernel, dim3((unsigned)fmd_cdiv(total, 256)), dim3(256), 0, stream, gE, wr1, y, wr2b,
+                     channels, hidden, scale, n_atoms, gha, gy);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_embed_f32(const int32_t* elem, const float* table, int64_t n_atoms, int32_t channels, float* h0,
+                  hipStream_t stream) {
+  FMD_REQUIRE(elem && table && h0 && n_atoms >= 0 && channels > 0);
+  if (n_atoms == 0) return FMD_OK;
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)fmd_cdiv(n_atoms * channels, 256)), dim3(256), 0, stream, elem,
+                     table, n_atoms, channels, h0);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_morse_f32(const float* geo, const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap,
+                  int64_t n_atoms, float D, float a, float r0, float rc, float vshift, float* energy, float* dvdr,
+                  hipStream_t stream) {
+  FMD_REQUIRE(geo && edge_offsets && n_edges && energy && dvdr && n_atoms >= 0);
+  if (n_atoms == 0) return FMD_OK;
+  hipLaunchKernelGGL(morse_kernel, dim3((unsigned)fmd_cdiv(n_atoms, 256)), dim3(256), 0, stream, geo, edge_offsets,
+                     n_edges, e_cap, n_atoms, D, a, r0, rc, vshift, energy, dvdr);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_morse_bwd_f32(const float* geo, const float* dvdr, const int32_t* edge_index, const float* gE,
+                      const int64_t* n_edges, int64_t e_cap, float* gvec, hipStream_t stream) {
+  FMD_REQUIRE(geo && dvdr && edge_index && gE && n_edges && gvec && e_cap >= 0);
+  if (e_cap == 0) return FMD_OK;
+  hipLaunchKernelGGL(morse_bwd_kernel, dim3((unsigned)fmd_cdiv(e_cap, 256)), dim3(256), 0, stream, geo, dvdr,
+                     edge_index, gE, n_edges, e_cap, gvec);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+}  // extern "C"

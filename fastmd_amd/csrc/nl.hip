@@ -703,17 +703,31 @@ __global__ void nl_reverse_kernel(const int32_t* center, const int32_t* neighbor
 __global__ void nl_window_flags_kernel(const int64_t* edge_count, const uint8_t* invalid_pairs,
                                        const uint8_t* overflow, const int32_t* isolated, int64_t e_cap,
                                        int check_isolated, uint8_t* w_over, uint8_t* w_cap, int64_t* w_edges,
-                                       int32_t* w_iso) {
+                                       int32_t* w_iso, const float* max_disp, double* stats) {
   if (threadIdx.x != 0) return;
   const int64_t edges = edge_count[0];
   const int32_t iso = isolated[0];
   bool flag = overflow[0] != 0;
   if (check_isolated) flag = flag || iso > 0;
-  w_over[0] = (w_over[0] != 0 || flag) ? 1 : 0;
+  const uint8_t wo = (w_over[0] != 0 || flag) ? 1 : 0;
+  w_over[0] = wo;
   const bool cap = edges > e_cap || (invalid_pairs && invalid_pairs[0] != 0);
-  w_cap[0] = (w_cap[0] != 0 || cap) ? 1 : 0;
-  w_edges[0] = edges > w_edges[0] ? edges : w_edges[0];
+  const uint8_t wc = (w_cap[0] != 0 || cap) ? 1 : 0;
+  w_cap[0] = wc;
+  const int64_t we = edges > w_edges[0] ? edges : w_edges[0];
+  w_edges[0] = we;
   w_iso[0] = iso > w_iso[0] ? iso : w_iso[0];
+  if (stats) {
+    // the window's statistics after this build: (overflow, edges, triplets, max displacement,
+    // capacity overflow, max edges, max isolated)
+    stats[0] = (double)wo;
+    stats[1] = (double)edges;
+    stats[2] = 0.0;
+    stats[3] = max_disp ? (double)max_disp[0] : 0.0;
+    stats[4] = (double)wc;
+    stats[5] = (double)we;
+    stats[6] = (double)w_iso[0];
+  }
 }
 
 }  // namespace
@@ -820,12 +834,12 @@ int fmd_nl_reverse(const int32_t* center, const int32_t* neighbor, const int32_t
 int fmd_nl_window_flags(const int64_t* edge_count, const uint8_t* invalid_pairs, const uint8_t* overflow,
                         const int32_t* isolated, int64_t e_cap, int32_t check_isolated, uint8_t* window_overflow,
                         uint8_t* window_capacity_overflow, int64_t* window_max_edges, int32_t* window_max_isolated,
-                        hipStream_t stream) {
+                        const float* max_displacement, double* stats, hipStream_t stream) {
   FMD_REQUIRE(edge_count && overflow && isolated && window_overflow && window_capacity_overflow &&
               window_max_edges && window_max_isolated);
   hipLaunchKernelGGL(nl_window_flags_kernel, dim3(1), dim3(64), 0, stream, edge_count, invalid_pairs, overflow,
                      isolated, e_cap, check_isolated, window_overflow, window_capacity_overflow, window_max_edges,
-                     window_max_isolated);
+                     window_max_isolated, max_displacement, stats);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

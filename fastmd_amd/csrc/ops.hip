@@ -17,6 +17,7 @@ constexpr int kMaxTerms = 2;
 struct CatParts {
   const float* src[kMaxParts];
   const int32_t* idx[kMaxParts];
+  int64_t istride[kMaxParts];
   int64_t ld[kMaxParts];
   int32_t width[kMaxParts];  // in VEC units
   int32_t start[kMaxParts + 1];
@@ -58,7 +59,7 @@ __global__ void __launch_bounds__(kThreads) gather_cat_kernel(CatParts p, int64_
   for (int64_t e = wave; e < rows; e += nwaves) {
     int64_t srow[kMaxParts];
 #pragma unroll
-    for (int k = 0; k < kMaxParts; ++k) srow[k] = (k < p.n && p.idx[k]) ? (int64_t)p.idx[k][e] : e;
+    for (int k = 0; k < kMaxParts; ++k) srow[k] = (k < p.n && p.idx[k]) ? (int64_t)p.idx[k][e * p.istride[k]] : e;
     V* orow = reinterpret_cast<V*>(out + e * ld_out);
     for (int c = lane; c < total; c += FMD_WAVE) {
       int k = 0;
@@ -210,8 +211,9 @@ int lanes_per_row(int64_t dimv) {
 
 extern "C" {
 
-int fmd_gather_cat_f32(int32_t n_parts, const float* const* srcs, const int32_t* const* indices, const int64_t* lds,
-                       const int32_t* widths, int64_t rows, float* out, int64_t ld_out, hipStream_t stream) {
+int fmd_gather_cat_f32(int32_t n_parts, const float* const* srcs, const int32_t* const* indices,
+                       const int64_t* index_strides, const int64_t* lds, const int32_t* widths, int64_t rows,
+                       float* out, int64_t ld_out, hipStream_t stream) {
   FMD_REQUIRE(n_parts >= 1 && n_parts <= kMaxParts && rows >= 0 && out && srcs && lds && widths);
   if (rows == 0) return FMD_OK;
   bool vec = aligned16(out) && ld_out % 4 == 0;
@@ -229,6 +231,8 @@ int fmd_gather_cat_f32(int32_t n_parts, const float* const* srcs, const int32_t*
   for (int k = 0; k < n_parts; ++k) {
     p.src[k] = srcs[k];
     p.idx[k] = indices ? indices[k] : nullptr;
+    p.istride[k] = index_strides ? index_strides[k] : 1;
+    FMD_REQUIRE(p.istride[k] >= 1);
     p.ld[k] = lds[k];
     p.width[k] = widths[k] / div;
     p.start[k + 1] = p.start[k] + p.width[k];

@@ -1,0 +1,80 @@
+"""The engine-owned derivative: forces of a model that returns per-atom energies only.
+
+Same contract as the reference's ``EnergyDerivative`` (fastmd/engine/energy_derivative.py:87-140):
+the leaf is a detached view of ``batch.positions`` (no copy), the energy is the FP64 sum of the
+real rows' energies, one ``torch.autograd.grad`` gives F = -dE/dx, and nothing synchronizes the
+host, so the whole-step runner captures it. The FP64 sum is a HIP kernel with a fixed summation
+order (deterministic and free of library reductions inside a captured graph).
+"""
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+from torch.autograd import Function
+
+from fastmd_amd import _abi
+from fastmd_amd.adapters.protocol import EnergyTap, GraphBatch
+
+
+class _SumF64(Function):
+    @staticmethod
+    def forward(ctx, x: Tensor) -> Tensor:
+        x = x.detach().contiguous()
+        if x.dtype not in (torch.float32, torch.float64):
+            raise ValueError(f"energies must be float32 or float64, got {x.dtype}")
+        out = torch.empty(1, dtype=torch.float64, device=x.device)
+        _abi.call("fmd_sum_f64", x.data_ptr(), 1 if x.dtype == torch.float64 else 0, x.numel(), out.data_ptr(),
+                  _abi.stream_handle())
+        ctx.shape, ctx.dtype = x.shape, x.dtype
+        return out.reshape(())
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        return g.to(ctx.dtype).expand(ctx.shape).contiguous()
+
+
+def sum_f64(x: Tensor) -> Tensor:
+    """sum(x) in float64 in a fixed order (0-dim), differentiable."""
+    return _SumF64.apply(x)
+
+
+def engine_derivative(adapter) -> "EnergyDerivative | None":
+    """The derivative the runtime runs for ``adapter`` (energy_derivative.py:51-60)."""
+    if hasattr(adapter, "node_energy"):
+        return EnergyDerivative(adapter)
+    if hasattr(adapter, "evaluate"):
+        return None
+    raise TypeError(f"model adapter {getattr(adapter, 'name', adapter)!r} has neither a model-owned derivative "
+                    "nor an energy tap (node_energy)")
+
+
+def edges_only_builder_options(adapter) -> dict:
+    """Builder options beyond the defaults (energy_derivative.py:63-73): none are needed here (edges
+    are always in the canonical order, which is also grouped by centre)."""
+    topology = adapter.topology_spec()
+    if topology.model_dtype != "float32":
+        raise NotImplementedError("float64 models are not supported by the fp32 kernels")
+    return {}
+
+
+class EnergyDerivative:
+    """``derivative(batch, inputs, task="ef", n_real=None) -> {"e": [1] f64, "f": [forces [rows, 3]]}``."""
+
+    stress_unit = "eV/A^3"
+
+    def __init__(self, adapter: EnergyTap) -> None:
+        self.adapter = adapter
+
+    def extensive_energy(self, energy: Tensor, atom_counts) -> Tensor:
+        return energy
+
+    def __call__(self, batch: GraphBatch, inputs, *, task: str = "ef", n_real: int | None = None) -> dict:
+        if "s" in task:
+            raise NotImplementedError("stress is not supported by this build's models")
+        with torch.enable_grad():
+            leaf = batch.positions.detach().requires_grad_(True)
+            energies = self.adapter.node_energy(inputs, leaf, batch.cell)
+            rows = energies.shape[0] if n_real is None else n_real
+            energy = sum_f64(energies[:rows])
+            (grad,) = torch.autograd.grad(energy, (leaf,))
+        return {"e": energy.detach().reshape(1), "f": [-grad]}

@@ -1,0 +1,263 @@
+"""(f) The whole MD step captured as ONE hipGraph and replayed per window.
+
+Same contract as the reference's ``WholeStepGraphRunner``
+(fastmd/execution/whole_step_cuda_graph.py:56-736) for a stateful (NHC) integrator and an
+edges-only builder: a window is a transaction -- the integrator's one-copy backup, the window
+flags reset, then ``steps_per_launch`` x (``step_pre_force`` -> exact re-filter build ->
+engine-owned derivative -> ``step_post_force`` -> flag fold) -- captured once (after
+side-stream warmup windows that are rolled back) and replayed; after a replay the host reads
+one small statistics buffer and settles the window:
+
+* capacity overflow (edges > e_cap): roll back and raise ``FixedCapacityOverflow`` (the driver
+  grows the capacity and recaptures);
+* an invalid candidate list (an atom moved more than half the skin, or a truncated row): roll
+  back, refresh the candidates at the window's start state and replay (recovery), falling back
+  to eager steps with fresh candidates if that fails again;
+* a proactive candidate refresh when the largest displacement reached
+  ``proactive_refresh_fraction`` of the skin;
+* non-finite state (NaN displacement) raises.
+
+Every kernel of the body is a HIP kernel of this package launched on torch's current stream
+(captured by torch.cuda.CUDAGraph = hipStreamBeginCapture/hipGraphInstantiate); the flags are
+cleared by fill kernels, never memsets.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor
+
+from fastmd_amd.engine.energy_derivative import engine_derivative
+from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
+from fastmd_amd.graph.gpu_graph_builder import raise_if_isolated_atoms
+
+
+class FixedCapacityOverflow(RuntimeError):
+    def __init__(self, edge_count: int, triplet_count: int = 0) -> None:
+        super().__init__(f"fixed graph capacity exceeded: edges={edge_count}, triplets={triplet_count}")
+        self.edge_count = edge_count
+        self.triplet_count = triplet_count
+
+
+def _require_finite_displacement(displacement: float, launch: int) -> None:
+    """whole_step_cuda_graph.py:25-35: NaN positions show as a NaN maximum displacement."""
+    if not math.isfinite(displacement):
+        raise ValueError(f"non-finite MD state after whole-step launch {launch}: max displacement {displacement}")
+
+
+@dataclass
+class WindowStats:
+    overflow: bool
+    edge_count: int
+    max_displacement: float
+    capacity_overflow: bool
+    max_edges: int
+    max_isolated: int
+
+
+class WholeStepGraphRunner:
+    """Capture integrator + exact graph re-filter + model forces (see the module docstring)."""
+
+    def __init__(self, *, model, builder: FixedCapacityGraphBuilder, integrator, positions: Tensor | None = None,
+                 momenta: Tensor | None = None, forces: Tensor | None = None, task: str = "ef",
+                 steps_per_launch: int = 1, warmup: int = 3, proactive_refresh_fraction: float = 0.25,
+                 graph_pool=None, validate_isolated_atoms: bool = False, config=None, recapture: bool = False,
+                 capture: bool = True) -> None:
+        if steps_per_launch <= 0:
+            raise ValueError("steps_per_launch must be positive")
+        if not 0.0 < proactive_refresh_fraction < 0.5:
+            raise ValueError("proactive_refresh_fraction must be in (0, 0.5)")
+        if "s" in task:
+            raise NotImplementedError("stress windows are not supported")
+        self.adapter = model
+        self._derivative = engine_derivative(model)
+        if self._derivative is None:
+            raise NotImplementedError("model-owned derivatives are not supported: the model needs an EnergyTap")
+        self.builder = builder
+        self.integrator = integrator
+        self.task = task
+        self.steps_per_launch = int(steps_per_launch)
+        self.warmup = 1 if recapture else int(warmup)
+        self.proactive_refresh_fraction = float(proactive_refresh_fraction)
+        self.graph_pool = graph_pool
+        self.validate_isolated_atoms = bool(validate_isolated_atoms) or model.isolated_atom_policy() == "error"
+        self.n_real = builder.n_real
+        self.device = builder.device
+        dev = self.device
+        self.window_overflow = torch.zeros(1, dtype=torch.uint8, device=dev)
+        self.window_capacity_overflow = torch.zeros(1, dtype=torch.uint8, device=dev)
+        self.window_max_edges = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.window_max_isolated = torch.zeros(1, dtype=torch.int32, device=dev)
+        self._window_stats = torch.zeros(7, dtype=torch.float64, device=dev)
+        self._stats_host = torch.zeros(7, dtype=torch.float64, pin_memory=True)
+        self._stats_event = None
+        self.graph = None
+        self.fallback_windows = 0
+        self.candidate_refreshes = 0
+        self.recovery_replays = 0
+        self.launches = 0
+        self.max_edge_count = 0
+        self.max_displacement_seen = 0.0
+        self.last_edge_count = 0
+        self.warmup_runs = 0
+        if positions is not None:
+            integrator.set_state(positions=positions)
+        if momenta is not None:
+            integrator.set_state(momenta=momenta)
+        # candidates at the current state, then the initial evaluation F(q0)
+        self.builder.refresh_candidates(integrator.positions)
+        self.candidate_refreshes += 1
+        self.builder.assert_candidate_capacity()
+        f0, e0, status = self._evaluate(integrator.positions)
+        if int(status.edge_count.item()) > builder.e_capacity:
+            raise FixedCapacityOverflow(int(status.edge_count.item()))
+        if self.validate_isolated_atoms:
+            raise_if_isolated_atoms(int(status.isolated_atom_count.item()))
+        if forces is None:
+            integrator.set_forces(f0.detach(), energy=e0.detach())
+        else:
+            integrator.set_forces(forces.to(device=dev, dtype=torch.float64))
+        if capture:
+            self._capture()
+
+    # ------------------------------------------------------------------ body
+    def _evaluate(self, positions: Tensor):
+        graph, status = self.builder.build(positions, rebuild_candidates=False)
+        out = self._derivative(self.builder.batch, graph, task=self.task, n_real=self.n_real)
+        forces = out["f"][0][: self.n_real]
+        energy = out["e"].reshape(-1)[:1]
+        return forces, energy, status
+
+    def _step_body(self, last: bool) -> None:
+        integrator = self.integrator
+        positions = integrator.step_pre_force()
+        forces, energy, status = self._evaluate(positions)
+        with torch.no_grad():
+            integrator.step_post_force(forces.detach(), energy=energy.detach())
+        self.builder.accumulate_window(status, window_overflow=self.window_overflow,
+                                       window_capacity_overflow=self.window_capacity_overflow,
+                                       window_max_edges=self.window_max_edges,
+                                       window_max_isolated=self.window_max_isolated,
+                                       check_isolated=self.validate_isolated_atoms,
+                                       stats=self._window_stats if last else None)
+
+    def _window_body(self) -> None:
+        self.integrator.backup()
+        self.window_overflow.zero_()
+        self.window_capacity_overflow.zero_()
+        self.window_max_edges.zero_()
+        self.window_max_isolated.zero_()
+        for k in range(self.steps_per_launch):
+            self._step_body(last=k == self.steps_per_launch - 1)
+
+    def _capture(self) -> None:
+        integrator = self.integrator
+        saved = integrator.snapshot()
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        try:
+            with torch.cuda.stream(side):
+                for _ in range(self.warmup):
+                    self._window_body()
+                    integrator.load_snapshot(saved)
+                    self.warmup_runs += 1
+            torch.cuda.current_stream(self.device).wait_stream(side)
+            torch.cuda.synchronize(self.device)
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph, pool=self.graph_pool, capture_error_mode="thread_local"):
+                self._window_body()
+        except BaseException:
+            torch.cuda.current_stream(self.device).wait_stream(side)
+            integrator.load_snapshot(saved)
+            raise
+        integrator.load_snapshot(saved)
+        torch.cuda.synchronize(self.device)
+
+    # ------------------------------------------------------------------ replay
+    def launch(self) -> None:
+        """Replay one window and start the asynchronous copy of its statistics."""
+        if self.graph is None:
+            self._window_body()
+        else:
+            self.graph.replay()
+        self.launches += 1
+        self._stats_host.copy_(self._window_stats, non_blocking=True)
+        self._stats_event = torch.cuda.Event()
+        self._stats_event.record()
+
+    def read_stats(self) -> WindowStats:
+        """Wait for the last launched window's statistics (the one host sync per window)."""
+        self._stats_event.synchronize()
+        s = self._stats_host.tolist()
+        return WindowStats(bool(s[0]), int(s[1]), float(s[3]), bool(s[4]), int(s[5]), int(s[6]))
+
+    def settle(self, stats: WindowStats) -> None:
+        """Act on a window's flags (whole_step_cuda_graph.py:540-584)."""
+        _require_finite_displacement(stats.max_displacement, self.launches)
+        self.last_edge_count = stats.edge_count
+        self.max_edge_count = max(self.max_edge_count, stats.max_edges)
+        self.max_displacement_seen = max(self.max_displacement_seen, stats.max_displacement)
+        if stats.capacity_overflow:
+            self.integrator.restore()
+            raise FixedCapacityOverflow(stats.max_edges)
+        if stats.overflow:
+            self._fallback()
+            return
+        if stats.max_displacement >= self.proactive_refresh_fraction * self.builder.skin:
+            self.builder.refresh_candidates(self.integrator.positions)
+            self.candidate_refreshes += 1
+            self.builder.assert_candidate_capacity()
+
+    def _fallback(self) -> None:
+        """Roll the window back, refresh the candidates at its start state and replay it; if the
+        replay is invalid again, run its steps eagerly with a fresh candidate list per step."""
+        self.fallback_windows += 1
+        self.integrator.restore()
+        self.builder.refresh_candidates(self.integrator.positions)
+        self.candidate_refreshes += 1
+        self.builder.assert_candidate_capacity()
+        self.launch()
+        stats = self.read_stats()
+        self.recovery_replays += 1
+        if stats.capacity_overflow:
+            self.integrator.restore()
+            raise FixedCapacityOverflow(stats.max_edges)
+        if not stats.overflow:
+            return
+        self.integrator.restore()
+        for _ in range(self.steps_per_launch):
+            self.builder.refresh_candidates(self.integrator.positions)
+            self.candidate_refreshes += 1
+            self._step_body(last=True)
+            stats = self._read_now()
+            if stats.capacity_overflow:
+                raise FixedCapacityOverflow(stats.max_edges)
+        _require_finite_displacement(stats.max_displacement, self.launches)
+
+    def _read_now(self) -> WindowStats:
+        s = self._window_stats.tolist()
+        return WindowStats(bool(s[0]), int(s[1]), float(s[3]), bool(s[4]), int(s[5]), int(s[6]))
+
+    def replay(self) -> WindowStats:
+        """One window: launch, read its statistics, settle."""
+        self.launch()
+        stats = self.read_stats()
+        self.settle(stats)
+        return stats
+
+    def stats(self) -> dict:
+        """whole_step_cuda_graph.py:724-736."""
+        return {
+            "launches": self.launches,
+            "steps_per_launch": self.steps_per_launch,
+            "candidate_refreshes": self.candidate_refreshes,
+            "fallback_windows": self.fallback_windows,
+            "recovery_replays": self.recovery_replays,
+            "max_edge_count": self.max_edge_count,
+            "last_edge_count": self.last_edge_count,
+            "max_displacement": self.max_displacement_seen,
+            "e_capacity": self.builder.e_capacity,
+            "warmup_runs": self.warmup_runs,
+        }

@@ -285,9 +285,12 @@ class FixedCapacityGraphBuilder:
 
     def accumulate_window(self, status: FixedCapacityGraphStatus, *, window_overflow: Tensor,
                           window_capacity_overflow: Tensor, window_max_edges: Tensor, window_max_isolated: Tensor,
-                          check_isolated: bool) -> None:
+                          check_isolated: bool, stats: Tensor | None = None) -> None:
         """Fold one build's status into a whole-step window's flags in one kernel
-        (fixed_capacity_builder.py:2300-2312, 430-455). Flags are uint8 [1]."""
+        (fixed_capacity_builder.py:2300-2312, 430-455). Flags are uint8 [1]; ``stats`` (float64 [7])
+        receives the window's statistics after this build."""
+        if stats is not None and (stats.dtype != torch.float64 or stats.numel() < 7):
+            raise ValueError("stats must be a float64 tensor of at least 7 entries")
         for t, dt in ((window_overflow, torch.uint8), (window_capacity_overflow, torch.uint8),
                       (window_max_edges, torch.int64), (window_max_isolated, torch.int32)):
             if t.dtype != dt:
@@ -295,7 +298,8 @@ class FixedCapacityGraphBuilder:
         _abi.call("fmd_nl_window_flags", status.edge_count.data_ptr(), None, status.overflow.data_ptr(),
                   status.isolated_atom_count.data_ptr(), self.e_capacity, 1 if check_isolated else 0,
                   window_overflow.data_ptr(), window_capacity_overflow.data_ptr(), window_max_edges.data_ptr(),
-                  window_max_isolated.data_ptr(), self._stream())
+                  window_max_isolated.data_ptr(), status.max_displacement.data_ptr(),
+                  None if stats is None else stats.data_ptr(), self._stream())
 
     # ------------------------------------------------------------------ host views (tests, eager)
     def real_edges(self) -> tuple[Tensor, Tensor, Tensor]:

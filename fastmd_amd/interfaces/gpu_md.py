@@ -1,0 +1,225 @@
+"""GPU-resident molecular dynamics on one MI355X: the drop-in driver of the MD step.
+
+Interface of the reference's ``GPUResidentMolecularDynamics`` (fastmd/interfaces/gpu_md.py:
+135-462 constructor, ``step`` :1789-1830, ``run`` :1866-1880, ``evaluate`` :1500-1529,
+``conserved_energy`` :1999-2004, ``thermodynamics`` :2169-2204, ``whole_step_stats`` :2007) for
+the Nose-Hoover chain ensemble and an energy-tap model adapter. ``atoms`` is an ASE-like object
+(``get_positions``/``get_cell``/``get_atomic_numbers``/``get_masses`` and optionally
+``get_momenta``) or a ``fastmd_amd.systems.System``; ASE itself is not a dependency.
+
+Execution modes (``InferenceConfig.execution``):
+  ``eager``       per step: ragged exact neighbour list (host syncs) -> model -> NHC halves;
+  ``whole_step``  the whole step captured as one hipGraph per capacity tier, replayed per
+                  window of ``steps_per_launch`` steps (``auto`` selects it);
+  ``model_graph`` is the reference's bucketed model graph; it is not offered (ValueError).
+Units: ``timestep``, ``tdamp`` in fs, ``temperature`` in K (ASE units inside).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from fastmd_amd import units
+from fastmd_amd.config import InferenceConfig
+from fastmd_amd.engine.capacity_policy import JointCapacityPolicy, held_demand, whole_step_headroom
+from fastmd_amd.engine.energy_derivative import engine_derivative
+from fastmd_amd.execution.gpu_nhc import GPUNoseHooverChainNVT, maxwell_boltzmann_momenta
+from fastmd_amd.execution.whole_step_cuda_graph import FixedCapacityOverflow, WholeStepGraphRunner
+from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
+from fastmd_amd.graph.gpu_graph_builder import TensorGraphBuilder, raise_if_isolated_atoms
+
+
+def _atoms_arrays(atoms):
+    if hasattr(atoms, "get_positions"):
+        positions = np.asarray(atoms.get_positions(), dtype=np.float64)
+        cell = np.asarray(getattr(atoms.get_cell(), "array", atoms.get_cell()), dtype=np.float64)
+        numbers = np.asarray(atoms.get_atomic_numbers(), dtype=np.int32)
+        masses = np.asarray(atoms.get_masses(), dtype=np.float64)
+        momenta = np.asarray(atoms.get_momenta(), dtype=np.float64) if hasattr(atoms, "get_momenta") else None
+        if momenta is not None and not np.any(momenta):
+            momenta = None
+        return positions, cell, numbers, masses, momenta
+    return (np.asarray(atoms.positions, dtype=np.float64), np.asarray(atoms.cell, dtype=np.float64),
+            np.asarray(atoms.numbers, dtype=np.int32), np.asarray(atoms.masses, dtype=np.float64),
+            getattr(atoms, "momenta", None))
+
+
+class GPUResidentMolecularDynamics:
+    def __init__(self, atoms, model=None, *, device: torch.device | str = "cuda", ensemble: str = "nvt_nhc",
+                 temperature: float = 300.0, timestep: float = 1.0, taut: float = 100.0, tdamp: float | None = None,
+                 tchain: int = 3, tloop: int = 1, config: InferenceConfig | None = None, steps_per_launch: int = 1,
+                 momenta=None, seed: int = 0, task: str = "ef", validate_isolated_atoms: bool = False) -> None:
+        if ensemble.lower() != "nvt_nhc":
+            raise NotImplementedError("this build integrates the Nose-Hoover chain ensemble (ensemble='nvt_nhc')")
+        if model is None or not hasattr(model, "node_energy"):
+            raise TypeError("model must be a model adapter with an energy tap (node_energy)")
+        if isinstance(steps_per_launch, bool) or not isinstance(steps_per_launch, int) or steps_per_launch < 1:
+            raise ValueError("GPUResidentMolecularDynamics: steps_per_launch must be a positive integer")
+        self.config = config or InferenceConfig()
+        self.execution = self.config.resolved_execution
+        if self.execution == "model_graph":
+            raise ValueError("execution='model_graph' is not offered by this build: use 'whole_step' or 'eager'")
+        self.device = torch.device(device)
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.adapter = model
+        self.derivative = engine_derivative(model)
+        self.task = task
+        self.steps_per_launch = int(steps_per_launch)
+        self.validate_isolated_atoms = bool(validate_isolated_atoms)
+        positions, cell, numbers, masses, atom_momenta = _atoms_arrays(atoms)
+        self.n_atoms = int(positions.shape[0])
+        self.cell = torch.tensor(cell, dtype=torch.float64)
+        self.numbers = torch.tensor(numbers, dtype=torch.int32)
+        self.masses = masses
+        self.temperature = float(temperature)
+        if momenta is None:
+            momenta = atom_momenta if atom_momenta is not None else maxwell_boltzmann_momenta(masses, temperature, seed)
+        tdamp = taut if tdamp is None else tdamp
+        self.integrator = GPUNoseHooverChainNVT(
+            masses, positions, np.asarray(momenta, dtype=np.float64), temperature_K=temperature,
+            timestep=timestep * units.fs, tdamp=tdamp * units.fs, tchain=tchain, tloop=tloop, device=self.device,
+            force_dtype=torch.float32)
+        topology = model.topology_spec()
+        self.cutoff = float(topology.cutoff)
+        self.graph_builder = TensorGraphBuilder(cell=self.cell, atomic_numbers=self.numbers,
+                                                atom_graph_cutoff=self.cutoff, device=self.device,
+                                                check_isolated_atoms=False)
+        self.steps = 0
+        self.whole_step_runner: WholeStepGraphRunner | None = None
+        self.capacity_policy = None
+        self._capacity = None
+        self.whole_step_capacity_history: list[int] = []
+        self._graph_pool = None
+        # F(q0) for the first pre-force half
+        forces, energy = self.evaluate(self.integrator.positions)
+        self.integrator.set_forces(forces, energy=energy)
+        if self.execution == "whole_step":
+            self.enable_whole_step_cuda_graph()
+
+    # ------------------------------------------------------------------ eager evaluation
+    def evaluate(self, positions: Tensor | None = None) -> tuple[Tensor, Tensor]:
+        """(forces float32 [N, 3], energy float64 [1]) at ``positions`` (default: the current
+        state), through a ragged exact neighbour list (eager, host syncs)."""
+        q = self.integrator.positions if positions is None else positions
+        batch = self.graph_builder.build(q)
+        if self.validate_isolated_atoms:
+            counts = torch.diff(batch.edge_offsets)
+            raise_if_isolated_atoms(int((counts == 0).sum().item()))
+        inputs = self.adapter.prepare(batch)
+        out = self.derivative(batch, inputs, task=self.task, n_real=self.n_atoms)
+        return out["f"][0][: self.n_atoms].detach(), out["e"].detach()
+
+    def step(self) -> None:
+        """One eager MD step (integrator halves around a fresh evaluation)."""
+        if self.whole_step_runner is not None:
+            raise RuntimeError("step() is the eager path; the whole-step mode runs windows through run()")
+        q = self.integrator.step_pre_force()
+        forces, energy = self.evaluate(q)
+        self.integrator.step_post_force(forces, energy=energy)
+        self.steps += 1
+
+    # ------------------------------------------------------------------ whole step
+    def _make_runner(self, u_capacity: int, recapture: bool) -> WholeStepGraphRunner:
+        builder = FixedCapacityGraphBuilder(cell=self.cell, atomic_numbers=self.numbers, u_capacity=u_capacity,
+                                            atom_graph_cutoff=self.cutoff,
+                                            candidate_cutoff=self.cutoff + self.config.capacity.candidate_skin,
+                                            padding=self.adapter.padding_rule(), prepare=self.adapter.prepare,
+                                            device=self.device)
+        return WholeStepGraphRunner(model=self.adapter, builder=builder, integrator=self.integrator, task=self.task,
+                                    steps_per_launch=self.steps_per_launch, warmup=self.config.capacity.warmup,
+                                    graph_pool=self._graph_pool, validate_isolated_atoms=self.validate_isolated_atoms,
+                                    recapture=recapture)
+
+    def _capacity_step(self):
+        cap = self.config.capacity
+        step = getattr(self.adapter, "capacity_step", None)
+        if step is not None and (cap.u_step, cap.min_pad_u) == (512, 256):
+            s = step()
+            return s.u_step, s.min_pad_u, s.u_thermal_factor
+        return cap.u_step, cap.min_pad_u, 1.0
+
+    def enable_whole_step_cuda_graph(self) -> None:
+        """Size the capacity from a ragged build (gpu_md.py:591-711) and capture the window."""
+        if self.whole_step_runner is not None:
+            return
+        sample = self.graph_builder.build(self.integrator.positions)
+        demand = int(sample.edge_index.shape[0]) // 2
+        u_step, min_pad, factor = self._capacity_step()
+        self.capacity_policy = JointCapacityPolicy(u_step=u_step, min_pad_u=min_pad)
+        self._capacity = self.capacity_policy.start(held_demand(demand, whole_step_headroom(demand, u_step), factor))
+        self._graph_pool = torch.cuda.graph_pool_handle()
+        while True:
+            try:
+                self.whole_step_runner = self._make_runner(self._capacity.u_capacity, recapture=False)
+                break
+            except FixedCapacityOverflow as overflow:
+                self._grow(overflow.edge_count)
+        self.whole_step_capacity_history.append(self._capacity.u_capacity)
+
+    def _grow(self, edge_count: int) -> None:
+        u_step, _, factor = self._capacity_step()
+        demand = (int(edge_count) + 1) // 2
+        self._capacity = self.capacity_policy.grow(self._capacity, held_demand(demand, whole_step_headroom(
+            demand, u_step), factor))
+
+    def _grow_whole_step_runner(self, edge_count: int) -> None:
+        """Capacity growth after an overflowed window: a larger tier, recaptured (gpu_md.py:1355-1410)."""
+        old = self.whole_step_runner
+        self._grow(edge_count)
+        self.whole_step_runner = None
+        del old
+        self.whole_step_runner = self._make_runner(self._capacity.u_capacity, recapture=True)
+        self.whole_step_capacity_history.append(self._capacity.u_capacity)
+
+    def run(self, steps: int) -> None:
+        """``steps`` MD steps (a multiple of ``steps_per_launch`` in the whole-step mode)."""
+        steps = int(steps)
+        if self.whole_step_runner is None:
+            for _ in range(steps):
+                self.step()
+            return
+        if steps % self.steps_per_launch:
+            raise ValueError(f"steps ({steps}) must be a multiple of steps_per_launch ({self.steps_per_launch})")
+        windows = steps // self.steps_per_launch
+        done = 0
+        while done < windows:
+            try:
+                self.whole_step_runner.replay()
+            except FixedCapacityOverflow as overflow:
+                self._grow_whole_step_runner(overflow.edge_count)
+                continue
+            done += 1
+            self.steps += self.steps_per_launch
+
+    # ------------------------------------------------------------------ observables
+    @property
+    def positions(self) -> Tensor:
+        return self.integrator.positions
+
+    @property
+    def momenta(self) -> Tensor:
+        return self.integrator.momenta
+
+    @property
+    def forces(self) -> Tensor:
+        return self.integrator.forces
+
+    def conserved_energy(self) -> float:
+        return float(self.integrator.conserved_energy())
+
+    def thermodynamics(self) -> dict:
+        """One download of the scalars (gpu_md.py:2169-2204)."""
+        epot = self.integrator.potential_energy[0]
+        ekin = self.integrator.kinetic_energy()
+        values = torch.stack([epot, ekin, self.integrator.temperature(), self.integrator.conserved_energy()]).tolist()
+        return {"step": self.steps, "epot": values[0], "ekin": values[1], "temperature": values[2],
+                "etotal": values[0] + values[1], "conserved": values[3]}
+
+    def whole_step_stats(self) -> dict | None:
+        if self.whole_step_runner is None:
+            return None
+        stats = self.whole_step_runner.stats()
+        stats["capacity_history"] = list(self.whole_step_capacity_history)
+        return stats

@@ -1,0 +1,320 @@
+"""A MACE-like equivariant interatomic potential whose forward and backward run as HIP kernels.
+
+The reference's MACE family is third-party (mace-torch 0.3.16, wrapped by
+fastmd/models/mace.py:254-477); it is not available here, so this build defines its own
+"2-layer, 128-channel, L_max = 1, correlation-order-3, 8-Bessel" model with the same plugin
+surface (``MACEAdapter``-shaped adapter: far self-loop padding, CapacityStep(32, 32, 1.02),
+an EnergyTap the engine differentiates) and puts the configs' operators on its path:
+the gather-cat (b), the wide edge GEMM (d) and the receiver segment sums (c).
+
+Model (per interaction layer t, node features h0 [N, C] scalars and h1 [N, 3, C] vectors):
+  edge e = (centre i <- neighbour j), vec = pos_j + image @ cell - pos_i, r = |vec|, u = vec / r
+  ef_n   = sqrt(2/rc) sin(n pi r / rc) / r * fcut(r),  n = 1..8;  fcut = 1 - 21x^5 + 35x^6 - 15x^7
+  a_e    = [h0_j | h0_i | ef_e]                                 (gather-cat, [E, 2C + 8])
+  z_e    = a_e @ W1                                              (edge GEMM, [2C+8, 4C])
+  w_e    = silu(z_e) * fcut(r)  = (wa | wb | wc | wd)
+  m0     = wa h0_j + wc (h1_j . u),  m1_x = wb h0_j u_x + wd h1_j,x
+  A0_i, A1_i = (1 / avg_num_neighbors) * sum over the rows of i   (segment sums)
+  P0 = A0 Wm0, P1_x = A1_x Wm1;  n1 = |P1|^2
+  B0 = c1 P0 + c2 P0^2 + c3 n1 + c4 P0^3 + c5 P0 n1          (element-dependent c, d)
+  B1_x = (d1 + d2 P0 + d3 P0^2 + d4 n1) P1_x
+  h0' = B0 Wo0 + h0 Wsc0,  h1'_x = B1_x Wo1                    (last layer: scalars only)
+readout: E_i = E0[Z_i] + scale * (h0^(1) . wr1 + silu(h0^(2) Wr2a) . wr2b) + shift.
+Initial h0 = embedding[Z], h1 = 0. Random init from ``torch.manual_seed(seed)``.
+
+The gradient dE/dpos is formed by explicit VJP kernels (fmd_mace_*_bwd), not by autograd of
+many small ops: the whole model is ONE autograd node whose backward launches ~25 kernels.
+Padding rows (far self-loops beyond the cutoff) contribute exactly zero and are skipped.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+from torch import Tensor, nn
+from torch.autograd import Function
+
+from fastmd_amd import _abi
+from fastmd_amd.adapters.protocol import CapacityStep, CaptureContract, GraphBatch, PaddingRule, TopologySpec
+from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr
+from fastmd_amd.ops.wide_gemm import gemm
+
+_ELEMENTS = 118
+_CAPACITY_STEP = CapacityStep(u_step=32, min_pad_u=32, u_thermal_factor=1.02)
+
+
+@dataclass(frozen=True)
+class MaceLikeConfig:
+    channels: int = 128
+    num_interactions: int = 2
+    n_basis: int = 8
+    cutoff: float = 6.0
+    avg_num_neighbors: float = 15.0
+    readout_hidden: int = 16
+    elements: tuple = (55, 50, 53)
+    scale: float = 1.0
+    shift: float = 0.0
+    seed: int = 0
+
+
+class MaceLike(nn.Module):
+    """Parameters of the model (frozen, float32). Node-side matrices are stored [in, out]; the
+    edge GEMM weight W1 is [2C + 8, 4C]."""
+
+    def __init__(self, config: MaceLikeConfig = MaceLikeConfig()) -> None:
+        super().__init__()
+        self.config = config
+        C, nb, H = config.channels, config.n_basis, config.readout_hidden
+        if C % 64 or C // 64 not in (1, 2, 4):
+            raise ValueError("channels must be 64, 128 or 256")
+        nel = len(config.elements)
+        gen = torch.Generator().manual_seed(config.seed)
+
+        def rnd(*shape, fan_in=None):
+            std = 1.0 / math.sqrt(fan_in) if fan_in else 1.0
+            return nn.Parameter(torch.randn(*shape, generator=gen) * std, requires_grad=False)
+
+        self.embedding = rnd(nel, C)
+        self.layers = nn.ModuleList()
+        for t in range(config.num_interactions):
+            layer = nn.Module()
+            layer.W1 = rnd(2 * C + nb, 4 * C, fan_in=2 * C + nb)
+            layer.Wm0 = rnd(C, C, fan_in=C)
+            layer.Wm1 = rnd(C, C, fan_in=C)
+            layer.Wc = rnd(nel, 5, C, fan_in=5)
+            layer.Wd = rnd(nel, 4, C, fan_in=4)
+            layer.Wo0 = rnd(C, C, fan_in=C)
+            layer.Wo1 = rnd(C, C, fan_in=C)
+            layer.Wsc0 = rnd(C, C, fan_in=C)
+            self.layers.append(layer)
+        self.wr1 = rnd(C, fan_in=C)
+        self.Wr2a = rnd(C, H, fan_in=C)
+        self.wr2b = rnd(H, fan_in=H)
+        self.e0 = nn.Parameter(-1.0 - torch.rand(nel, generator=gen), requires_grad=False)
+        table = torch.full((_ELEMENTS + 1,), -1, dtype=torch.int32)
+        for k, z in enumerate(config.elements):
+            table[z] = k
+        self.register_buffer("z_table", table)
+
+    @property
+    def r_max(self) -> float:
+        return self.config.cutoff
+
+    @property
+    def num_interactions(self) -> int:
+        return self.config.num_interactions
+
+
+@dataclass
+class MaceLikeInput:
+    batch: GraphBatch
+    elem: Tensor  # int32 [rows] element index of every atom row
+    csr_dst: Csr = field(default=None)
+    csr_src: Csr = field(default=None)
+
+
+def _call(name, *args):
+    _abi.call(name, *args, _abi.stream_handle())
+
+
+def _empty(*shape, device, dtype=torch.float32):
+    return torch.empty(*shape, dtype=dtype, device=device)
+
+
+def _gather_edge_rows(h0: Tensor, ef: Tensor, edge_index: Tensor, out: Tensor) -> None:
+    """out[e] = [h0[src e] | h0[dst e] | ef[e]] (src = neighbour column 1, dst = centre column 0)."""
+    C, nb = h0.shape[1], ef.shape[1]
+    rows = out.shape[0]
+    col_src = edge_index[:, 1]
+    col_dst = edge_index[:, 0]
+    _abi.call("fmd_gather_cat_f32", 3, _abi.ptr_array([h0.data_ptr(), h0.data_ptr(), ef.data_ptr()]),
+              _abi.ptr_array([col_src.data_ptr(), col_dst.data_ptr(), None]),
+              _abi.array(_abi._i64, [edge_index.stride(0), edge_index.stride(0), 1]),
+              _abi.array(_abi._i64, [C, C, nb]), _abi.array(_abi._i32, [C, C, nb]), rows, out.data_ptr(),
+              out.stride(0), _abi.stream_handle())
+
+
+class _MaceLikeEnergy(Function):
+    """positions -> node energies [rows]; backward: dE/dpos by the VJP kernels."""
+
+    @staticmethod
+    def forward(ctx, positions, cell, model: MaceLike, inputs: MaceLikeInput):
+        cfg = model.config
+        batch = inputs.batch
+        dev = positions.device
+        C, nb, H = cfg.channels, cfg.n_basis, cfg.readout_hidden
+        n = positions.shape[0]
+        e_cap = batch.edge_index.shape[0]
+        if positions.dtype != torch.float32:
+            raise ValueError("the MACE-like model runs in float32")
+        positions = positions.detach().contiguous()
+        cell = cell.detach().to(torch.float32).contiguous()
+        n_edges, off, ei = batch.n_edges, batch.edge_offsets, batch.edge_index
+        elem = inputs.elem
+        inv_avg = 1.0 / cfg.avg_num_neighbors
+        geo = _empty(e_cap, 8, device=dev)
+        ef = _empty(e_cap, nb, device=dev)
+        de = _empty(e_cap, nb, device=dev)
+        _call("fmd_edge_geometry_f32", positions.data_ptr(), cell.data_ptr(), ei.data_ptr(),
+              batch.edge_image.data_ptr(), n_edges.data_ptr(), e_cap, float(cfg.cutoff), nb, geo.data_ptr(),
+              ef.data_ptr(), de.data_ptr())
+        h0 = _empty(n, C, device=dev)
+        _call("fmd_embed_f32", elem.data_ptr(), model.embedding.data_ptr(), n, C, h0.data_ptr())
+        h1 = None
+        saved = []
+        h_first = None
+        L = len(model.layers)
+        a = _empty(e_cap, 2 * C + nb, device=dev)
+        for t, layer in enumerate(model.layers):
+            last = t == L - 1
+            _gather_edge_rows(h0, ef, ei, a)
+            z = gemm(a, layer.W1, b_layout=1)  # [E, 4C]
+            A0 = _empty(n, C, device=dev)
+            A1 = _empty(n, 3, C, device=dev)
+            _call("fmd_mace_message_f32", z.data_ptr(), geo.data_ptr(), ei.data_ptr(), off.data_ptr(),
+                  n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), inv_avg, A0.data_ptr(), A1.data_ptr())
+            P0 = gemm(A0, layer.Wm0, b_layout=1)
+            P1 = gemm(A1.view(3 * n, C), layer.Wm1, b_layout=1).view(n, 3, C)
+            B0 = _empty(n, C, device=dev)
+            B1 = None if last else _empty(n, 3, C, device=dev)
+            _call("fmd_mace_symcon_f32", P0.data_ptr(), P1.data_ptr(), elem.data_ptr(), layer.Wc.data_ptr(),
+                  layer.Wd.data_ptr(), n, C, B0.data_ptr(), _abi.ptr(B1))
+            h0n = gemm(B0, layer.Wo0, b_layout=1)
+            gemm(h0, layer.Wsc0, b_layout=1, out=h0n, accumulate=True)
+            h1n = None if last else gemm(B1.view(3 * n, C), layer.Wo1, b_layout=1).view(n, 3, C)
+            saved.append((h0, h1, z, P0, P1))
+            if t == 0:
+                h_first = h0n
+            h0, h1 = h0n, h1n
+        y = gemm(h0, model.Wr2a, b_layout=1)  # [N, H]
+        energy = _empty(n, device=dev)
+        _call("fmd_mace_energy_f32", h_first.data_ptr(), model.wr1.data_ptr(), y.data_ptr(), model.wr2b.data_ptr(),
+              C, H, elem.data_ptr(), model.e0.data_ptr(), float(cfg.scale), float(cfg.shift), n, energy.data_ptr())
+        ctx.model, ctx.inputs, ctx.saved = model, inputs, saved
+        ctx.geo, ctx.de, ctx.y = geo, de, y
+        ctx.n, ctx.e_cap = n, e_cap
+        return energy
+
+    @staticmethod
+    def backward(ctx, gE):
+        model, inputs = ctx.model, ctx.inputs
+        cfg = model.config
+        batch = inputs.batch
+        C, nb, H = cfg.channels, cfg.n_basis, cfg.readout_hidden
+        n, e_cap = ctx.n, ctx.e_cap
+        dev = gE.device
+        gE = gE.detach().to(torch.float32).contiguous()
+        inv_avg = 1.0 / cfg.avg_num_neighbors
+        n_edges, off, ei, rev = batch.n_edges, batch.edge_offsets, batch.edge_index, batch.edge_reverse
+        # readouts: gha = dE/d(first layer's h0 out), gy -> dE/d(last layer's h0 out)
+        gy = _empty(n, H, device=dev)
+        gha = _empty(n, C, device=dev)
+        _call("fmd_mace_energy_bwd_f32", gE.data_ptr(), model.wr1.data_ptr(), ctx.y.data_ptr(), model.wr2b.data_ptr(),
+              C, H, float(cfg.scale), n, gha.data_ptr(), gy.data_ptr())
+        g_out0 = gemm(gy, model.Wr2a, b_layout=0)  # dE/dh0 out of the last layer
+        g_out1 = None  # dE/dh1 out of the current layer (the last layer's h1 out is unused)
+        ggeo = _empty(e_cap, 4, device=dev)
+        gefs = []
+        L = len(model.layers)
+        for t in reversed(range(L)):
+            layer = model.layers[t]
+            h0, h1, z, P0, P1 = ctx.saved[t]
+            if t == 0:
+                g_out0 = g_out0 + gha
+            gB0 = gemm(g_out0, layer.Wo0, b_layout=0)
+            gB1 = None if g_out1 is None else gemm(g_out1.reshape(3 * n, C), layer.Wo1, b_layout=0)
+            gP0 = _empty(n, C, device=dev)
+            gP1 = _empty(n, 3, C, device=dev)
+            _call("fmd_mace_symcon_bwd_f32", P0.data_ptr(), P1.data_ptr(), inputs.elem.data_ptr(),
+                  layer.Wc.data_ptr(), layer.Wd.data_ptr(), gB0.data_ptr(), _abi.ptr(gB1), n, C, gP0.data_ptr(),
+                  gP1.data_ptr())
+            gA0 = gemm(gP0, layer.Wm0, b_layout=0)
+            gA1 = gemm(gP1.view(3 * n, C), layer.Wm1, b_layout=0)
+            gz = _empty(e_cap, 4 * C, device=dev)
+            acc_geo = 1 if t < L - 1 else 0
+            if t == 0:
+                # the first layer's inputs are the element embedding (no position dependence)
+                _call("fmd_mace_message_bwd_f32", z.data_ptr(), ctx.geo.data_ptr(), ei.data_ptr(), rev.data_ptr(),
+                      off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(),
+                      gA1.data_ptr(), inv_avg, gz.data_ptr(), ggeo.data_ptr(), acc_geo, None, None, 0)
+                # only the radial-basis block of the gather-cat rows carries a position gradient
+                gefs.append((gemm(gz, layer.W1[2 * C:], b_layout=0), nb))
+                break
+            # this layer's inputs: residual, sender side of the messages, gather-cat rows
+            g_in0 = gemm(g_out0, layer.Wsc0, b_layout=0)
+            g_in1 = torch.zeros(n, 3, C, dtype=torch.float32, device=dev) if h1 is not None else None
+            _call("fmd_mace_message_bwd_f32", z.data_ptr(), ctx.geo.data_ptr(), ei.data_ptr(), rev.data_ptr(),
+                  off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(),
+                  gA1.data_ptr(), inv_avg, gz.data_ptr(), ggeo.data_ptr(), acc_geo, g_in0.data_ptr(),
+                  _abi.ptr(g_in1), 1)
+            ga = gemm(gz, layer.W1, b_layout=0)  # [E, 2C + nb]
+            segment_sum_csr([(ga, inputs.csr_src, 0, 1.0, None), (ga, inputs.csr_dst, C, 1.0, None)], n, C,
+                            out=g_in0, accumulate=True)
+            gefs.append((ga[:, 2 * C:], 2 * C + nb))
+            g_out0, g_out1 = g_in0, g_in1
+        gvec = _empty(e_cap, 3, device=dev)
+        (g0, ld0) = gefs[0]
+        (g1, ld1) = gefs[1] if len(gefs) > 1 else (None, 0)
+        _call("fmd_edge_geometry_bwd_f32", ctx.geo.data_ptr(), ctx.de.data_ptr(), nb, g0.data_ptr(), ld0,
+              _abi.ptr(g1), ld1, ggeo.data_ptr(), n_edges.data_ptr(), e_cap, gvec.data_ptr())
+        gpos = segment_sum_csr([(gvec, inputs.csr_src, 0, 1.0, None), (gvec, inputs.csr_dst, 0, -1.0, None)], n, 3)
+        return gpos, None, None, None
+
+
+class MaceLikeAdapter:
+    """The MACE-like model as a ModelAdapter with an EnergyTap (mace.py:254-477's surface)."""
+
+    name = "mace_like"
+    compiled = False
+
+    def __init__(self, module: MaceLike | None = None, *, config: MaceLikeConfig | None = None,
+                 device: torch.device | str = "cuda") -> None:
+        module = module if module is not None else MaceLike(config or MaceLikeConfig())
+        self.module = module.to(device).eval()
+        for p in self.module.parameters():
+            p.requires_grad_(False)
+
+    def topology_spec(self) -> TopologySpec:
+        cfg = self.module.config
+        return TopologySpec(cutoff=float(cfg.cutoff), num_interactions=int(cfg.num_interactions),
+                            model_dtype="float32", edge_order="sorted")
+
+    def padding_rule(self) -> PaddingRule:
+        return PaddingRule("far_self_loops")
+
+    def capacity_step(self) -> CapacityStep:
+        return _CAPACITY_STEP
+
+    def capture_contract(self) -> CaptureContract:
+        return CaptureContract(sync_free=True, exact_cutoff=True, accuracy_class="fp32_noise",
+                               force_mode="engine_autograd", stress_unit="eV/A^3", compiled="none")
+
+    def isolated_atom_policy(self) -> str:
+        return "model"
+
+    def reference_energies(self) -> Tensor:
+        row = torch.full((1, _ELEMENTS), float("nan"), dtype=torch.float64)
+        for k, z in enumerate(self.module.config.elements):
+            row[0, z - 1] = float(self.module.e0[k])
+        return row
+
+    def prepare(self, batch: GraphBatch) -> MaceLikeInput:
+        """Aliases of the batch plus the element index of every row (host check of the species,
+        outside any graph) and the two CSRs of the edge list."""
+        if batch.positions is None or batch.edge_offsets is None or batch.edge_reverse is None:
+            raise ValueError("the MACE-like model needs an edges-only batch with its CSR (edge_offsets, edge_reverse)")
+        species = batch.species.long()
+        table = self.module.z_table.to(species.device)
+        if bool(((species < 1) | (species > _ELEMENTS)).any()) or bool((table[species.clamp(1, _ELEMENTS)] < 0).any()):
+            raise ValueError(f"the MACE-like model supports atomic numbers {list(self.module.config.elements)}")
+        elem = table[species].to(torch.int32).contiguous()
+        rows = batch.edge_index.shape[0]
+        return MaceLikeInput(batch=batch, elem=elem, csr_dst=Csr(batch.edge_offsets, None, rows),
+                             csr_src=Csr(batch.edge_offsets, batch.edge_reverse, rows))
+
+    def node_energy(self, inputs: MaceLikeInput, positions: Tensor, cell: Tensor) -> Tensor:
+        """Per-atom energies [rows] (float32) at ``positions``; differentiable w.r.t. positions."""
+        if cell.requires_grad:
+            raise NotImplementedError("stress (a strained cell) is not supported by the MACE-like kernels")
+        return _MaceLikeEnergy.apply(positions, cell, self.module, inputs)

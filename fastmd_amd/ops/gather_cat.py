@@ -24,14 +24,18 @@ from fastmd_amd.ops.csr_segment_sum import Csr, csr_from_segment, segment_sum_cs
 
 def _launch(parts, rows: int, out: Tensor) -> None:
     """parts: list of (src matrix, index or None)."""
-    srcs, idx, lds, widths, keep = [], [], [], [], []
+    srcs, idx, strides, lds, widths, keep = [], [], [], [], [], []
     for src, index in parts:
         if src.dtype != torch.float32:
             raise ValueError(f"gather_cat takes float32 blocks, got {src.dtype}")
         src, ld = rows_view(src)
+        stride = 1
         if index is not None:
-            if index.dtype != torch.int32 or not index.is_contiguous():
-                index = index.to(torch.int32).contiguous()
+            if index.dtype != torch.int32 or index.dim() != 1:
+                index = index.to(torch.int32).reshape(-1).contiguous()
+            stride = index.stride(0) if index.numel() > 1 else 1
+            if stride < 1:
+                index, stride = index.contiguous(), 1
             if index.numel() != rows:
                 raise ValueError(f"index has {index.numel()} entries for {rows} rows")
         elif src.shape[0] != rows:
@@ -39,10 +43,11 @@ def _launch(parts, rows: int, out: Tensor) -> None:
         keep += [src, index]
         srcs.append(src.data_ptr())
         idx.append(None if index is None else index.data_ptr())
+        strides.append(stride)
         lds.append(ld)
         widths.append(src.shape[1])
     _abi.call("fmd_gather_cat_f32", len(parts), _abi.ptr_array(srcs), _abi.ptr_array(idx),
-              _abi.array(_abi._i64, lds), _abi.array(_abi._i32, widths), rows, out.data_ptr(), out.stride(0),
+              _abi.array(_abi._i64, strides), _abi.array(_abi._i64, lds), _abi.array(_abi._i32, widths), rows, out.data_ptr(), out.stride(0),
               stream())
 
 

@@ -109,24 +109,29 @@ int fmd_nl_reverse(const int32_t* center, const int32_t* neighbor, const int32_t
                    const int64_t* edge_offsets, int64_t n_atoms, int64_t e_cap, int32_t* reverse,
                    hipStream_t stream);
 
-/* Window flag fold of one build (fixed_capacity_builder.py:430-455, _window_flags_kernel). */
+/* Window flag fold of one build (fixed_capacity_builder.py:430-455, _window_flags_kernel); with
+ * `stats` (float64 [7], may be null) also the window's statistics after this build: (overflow,
+ * edges, triplets = 0, max displacement, capacity overflow, max edges, max isolated), the one
+ * buffer the host reads per window (whole_step_cuda_graph.py:353-356). */
 int fmd_nl_window_flags(const int64_t* edge_count, const uint8_t* invalid_pairs, const uint8_t* overflow,
                         const int32_t* isolated, int64_t e_cap, int32_t check_isolated,
                         uint8_t* window_overflow, uint8_t* window_capacity_overflow,
-                        int64_t* window_max_edges, int32_t* window_max_isolated, hipStream_t stream);
+                        int64_t* window_max_edges, int32_t* window_max_isolated,
+                        const float* max_displacement, double* stats, hipStream_t stream);
 
 /* ----------------------------------------------------------------------------------------
  * (b) Gather-cat
  * -------------------------------------------------------------------------------------- */
 
 /* out[e] = cat(part_0[e'], ..., part_{n-1}[e']) over n_parts <= 4 column blocks, where part k
- * reads row index_k[e] of src_k (gathered) or row e (index_k null, aligned), width w_k, row
- * stride ld_k; out row stride ld_out. Replaces aligned_gather_cat3/4
+ * reads row index_k[e * index_stride_k] of src_k (gathered) or row e (index_k null, aligned),
+ * width w_k, row stride ld_k; out row stride ld_out. Per-part arrays are host arrays
+ * (index_strides may be null: 1). Replaces aligned_gather_cat3/4
  * (triton_gather_cat.py:29-43,181-199,202-232,353-374) and the north-star form
  * gather_cat(x, src, dst, rbf) = cat(x[src], x[dst], rbf). Index arrays are int32. */
 int fmd_gather_cat_f32(int32_t n_parts, const float* const* srcs, const int32_t* const* indices,
-                       const int64_t* lds, const int32_t* widths, int64_t rows, float* out,
-                       int64_t ld_out, hipStream_t stream);
+                       const int64_t* index_strides, const int64_t* lds, const int32_t* widths, int64_t rows,
+                       float* out, int64_t ld_out, hipStream_t stream);
 
 /* ----------------------------------------------------------------------------------------
  * (c) Deterministic CSR segment sums
@@ -201,6 +206,57 @@ int fmd_nhc_post_force(double* p, const void* f_in, int32_t f_in_is_f64, double*
 /* out[0] = sum_{i<n} (double)x[i] in a fixed order (x float32 if x_is_f64 == 0). The FP64
  * energy sum of EnergyDerivative (fastmd/engine/energy_derivative.py:131-133). */
 int fmd_sum_f64(const void* x, int32_t x_is_f64, int64_t n, double* out, hipStream_t stream);
+
+/* ----------------------------------------------------------------------------------------
+ * Model kernels (the MACE-like interaction and the Morse pair potential of the benchmark
+ * configurations). Edge rows are the real rows [0, min(*n_edges, e_cap)) of the builder's
+ * sorted list (n_edges read on the device); node sums walk the centre CSR (edge_offsets),
+ * sender sums the reverse-edge CSR. The reference's model arithmetic is third-party
+ * (mace-torch, wrapped by fastmd/models/mace.py:356-388); these kernels implement this
+ * build's own MACE-like model, specified in fastmd_amd/models/mace_like.py.
+ * -------------------------------------------------------------------------------------- */
+
+/* geo[e] = (u, r, fcut, dfcut, 0, 0) [E,8]; ef[e,n] = Bessel_n(r) fcut(r), def = d ef / dr [E,nb]. */
+int fmd_edge_geometry_f32(const float* positions, const float* cell, const int32_t* edge_index,
+                          const float* edge_image, const int64_t* n_edges, int64_t e_cap, float rc, int32_t nb,
+                          float* geo, float* ef, float* def, hipStream_t stream);
+/* gvec[e] = dE/dvec from dE/def (up to two sources, row strides ld0/ld1) and dE/d(u, fcut) (ggeo [E,4]). */
+int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, const float* gef0, int64_t ld0,
+                              const float* gef1, int64_t ld1, const float* ggeo, const int64_t* n_edges,
+                              int64_t e_cap, float* gvec, hipStream_t stream);
+/* A0[i], A1[i] = inv_avg * sum over the rows of centre i of the messages (h1 may be null). */
+int fmd_mace_message_f32(const float* z, const float* geo, const int32_t* edge_index, const int64_t* edge_offsets,
+                         const int64_t* n_edges, int64_t e_cap, int64_t n_atoms, int32_t channels, const float* h0,
+                         const float* h1, float inv_avg, float* A0, float* A1, hipStream_t stream);
+/* VJP of fmd_mace_message_f32: gz [E,4C], ggeo [E,4] (= or += ), and if gh0: the sender-side
+ * gh0/gh1 (= or +=) over the reverse CSR. */
+int fmd_mace_message_bwd_f32(const float* z, const float* geo, const int32_t* edge_index, const int32_t* reverse,
+                             const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
+                             int32_t channels, const float* h0, const float* h1, const float* gA0, const float* gA1,
+                             float inv_avg, float* gz, float* ggeo, int32_t accumulate_geo, float* gh0, float* gh1,
+                             int32_t accumulate_h, hipStream_t stream);
+/* Symmetric contraction (correlation 3, L <= 1) and its VJP. */
+int fmd_mace_symcon_f32(const float* P0, const float* P1, const int32_t* elem, const float* Wc, const float* Wd,
+                        int64_t n_atoms, int32_t channels, float* B0, float* B1, hipStream_t stream);
+int fmd_mace_symcon_bwd_f32(const float* P0, const float* P1, const int32_t* elem, const float* Wc, const float* Wd,
+                            const float* gB0, const float* gB1, int64_t n_atoms, int32_t channels, float* gP0,
+                            float* gP1, hipStream_t stream);
+/* Node energies E_i = E0[elem] + scale (ha . wr1 + sum_k silu(y_k) wr2b_k) + shift, and the VJP. */
+int fmd_mace_energy_f32(const float* ha, const float* wr1, const float* y, const float* wr2b, int32_t channels,
+                        int32_t hidden, const int32_t* elem, const float* e0, float scale, float shift,
+                        int64_t n_atoms, float* energy, hipStream_t stream);
+int fmd_mace_energy_bwd_f32(const float* gE, const float* wr1, const float* y, const float* wr2b, int32_t channels,
+                            int32_t hidden, float scale, int64_t n_atoms, float* gha, float* gy, hipStream_t stream);
+/* h0[i] = table[elem[i]]. */
+int fmd_embed_f32(const int32_t* elem, const float* table, int64_t n_atoms, int32_t channels, float* h0,
+                  hipStream_t stream);
+/* Morse pair potential (shifted to 0 at rc): E_i = 1/2 sum V(r_e) over the rows of centre i,
+ * dvdr[e] = V'(r_e); VJP gvec[e] = 1/2 gE[centre] V'(r) u. */
+int fmd_morse_f32(const float* geo, const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap,
+                  int64_t n_atoms, float D, float a, float r0, float rc, float vshift, float* energy, float* dvdr,
+                  hipStream_t stream);
+int fmd_morse_bwd_f32(const float* geo, const float* dvdr, const int32_t* edge_index, const float* gE,
+                      const int64_t* n_edges, int64_t e_cap, float* gvec, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,102 @@
+"""Model oracle (test infrastructure and the timed CPU baseline; see oracle/__init__.py).
+
+PyTorch-CPU eager restatements, differentiated by autograd exactly as the reference's
+engine-owned derivative does (fastmd/engine/energy_derivative.py:110-140: positions leaf, FP64
+energy sum over the real rows, one ``torch.autograd.grad``, F = -dE/dx), with the reference's
+CPU op forms: ``index_select`` gathers, ``index_add_`` receiver sums
+(triton_csr_segment_sum.py:463-479) and dense ``matmul`` GEMMs (triton_wide_gemm.py:488-489).
+
+* ``morse_node_energy``: the configs[0] Morse pair potential (D, a, r0, cutoff), shifted to zero at
+  the cutoff, E_i = 1/2 sum_j V(r_ij).
+* ``mace_like_node_energy``: the MACE-like model specified in fastmd_amd/models/mace_like.py
+  (its parameters are passed in as a dict of tensors; the oracle does not import the product).
+Edges are the real rows (centre, neighbour, image) of a neighbour list; vec = pos[neighbour] +
+image @ cell - pos[centre].
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+from torch import Tensor
+
+
+def edge_vectors(positions: Tensor, cell: Tensor, center: Tensor, neighbor: Tensor, images: Tensor) -> Tensor:
+    img = images.to(positions.dtype)
+    shift = img[:, 0:1] * cell[0] + img[:, 1:2] * cell[1] + img[:, 2:3] * cell[2]
+    return (positions.index_select(0, neighbor) + shift) - positions.index_select(0, center)
+
+
+def morse_node_energy(positions, cell, center, neighbor, images, *, D=0.3, a=1.5, r0=3.0, cutoff=6.0):
+    vec = edge_vectors(positions, cell, center, neighbor, images)
+    r = vec.norm(dim=1)
+    vshift = D * ((1 - math.exp(-a * (cutoff - r0))) ** 2 - 1)
+    v = D * ((1 - torch.exp(-a * (r - r0))) ** 2 - 1) - vshift
+    v = torch.where(r < cutoff, v, torch.zeros_like(v))
+    return 0.5 * torch.zeros(positions.shape[0], dtype=positions.dtype).index_add_(0, center, v)
+
+
+def radial_basis(r: Tensor, cutoff: float, n_basis: int):
+    n = torch.arange(1, n_basis + 1, dtype=r.dtype)
+    bessel = math.sqrt(2.0 / cutoff) * torch.sin(n[None, :] * math.pi * r[:, None] / cutoff) / r[:, None]
+    x = r / cutoff
+    fcut = 1 - 21 * x ** 5 + 35 * x ** 6 - 15 * x ** 7
+    fcut = torch.where(x < 1, fcut, torch.zeros_like(fcut))
+    return bessel * fcut[:, None], fcut
+
+
+def mace_like_node_energy(params: dict, config: dict, positions, cell, elem, center, neighbor, images):
+    """Per-atom energies of the MACE-like model (see the module docstring)."""
+    dt = positions.dtype
+    p = {k: v.to(dt) for k, v in params.items()}
+    C, nb = config["channels"], config["n_basis"]
+    L = config["num_interactions"]
+    n_atoms = positions.shape[0]
+    vec = edge_vectors(positions, cell.to(dt), center, neighbor, images)
+    r = vec.norm(dim=1)
+    u = vec / r[:, None]
+    ef, fcut = radial_basis(r, config["cutoff"], nb)
+    elem = elem.long()
+    h0 = p["embedding"].index_select(0, elem)
+    h1 = torch.zeros(n_atoms, 3, C, dtype=dt)
+    h_first = None
+    for t in range(L):
+        W = {k.split(".", 2)[2]: v for k, v in p.items() if k.startswith(f"layers.{t}.")}
+        last = t == L - 1
+        hj = h0.index_select(0, neighbor)
+        a = torch.cat([hj, h0.index_select(0, center), ef], dim=1)
+        z = a @ W["W1"]
+        w = torch.nn.functional.silu(z) * fcut[:, None]
+        wa, wb, wc, wd = w[:, :C], w[:, C:2 * C], w[:, 2 * C:3 * C], w[:, 3 * C:]
+        h1j = h1.index_select(0, neighbor)
+        proj = (h1j * u[:, :, None]).sum(1)
+        m0 = wa * hj + wc * proj
+        m1 = (wb * hj)[:, None, :] * u[:, :, None] + wd[:, None, :] * h1j
+        A0 = torch.zeros(n_atoms, C, dtype=dt).index_add_(0, center, m0) / config["avg_num_neighbors"]
+        A1 = torch.zeros(n_atoms, 3, C, dtype=dt).index_add_(0, center, m1) / config["avg_num_neighbors"]
+        P0 = A0 @ W["Wm0"]
+        P1 = A1 @ W["Wm1"]
+        n1 = (P1 * P1).sum(1)
+        c = W["Wc"].index_select(0, elem)
+        B0 = c[:, 0] * P0 + c[:, 1] * P0 ** 2 + c[:, 2] * n1 + c[:, 3] * P0 ** 3 + c[:, 4] * P0 * n1
+        h0n = B0 @ W["Wo0"] + h0 @ W["Wsc0"]
+        if not last:
+            d = W["Wd"].index_select(0, elem)
+            q = d[:, 0] + d[:, 1] * P0 + d[:, 2] * P0 ** 2 + d[:, 3] * n1
+            h1 = (q[:, None, :] * P1) @ W["Wo1"]
+        if t == 0:
+            h_first = h0n
+        h0 = h0n
+    y = h0 @ p["Wr2a"]
+    e = h_first @ p["wr1"] + torch.nn.functional.silu(y) @ p["wr2b"]
+    return p["e0"].index_select(0, elem) + config["scale"] * e + config["shift"]
+
+
+def energy_and_forces(node_energy_fn, positions, *args, n_real=None, **kwargs):
+    """The engine-owned derivative (energy_derivative.py:110-140): FP64 sum, one autograd.grad."""
+    leaf = positions.detach().clone().requires_grad_(True)
+    energies = node_energy_fn(leaf, *args, **kwargs)
+    rows = energies.shape[0] if n_real is None else n_real
+    energy = energies[:rows].to(torch.float64).sum()
+    (grad,) = torch.autograd.grad(energy, leaf)
+    return energy.detach(), -grad, energies.detach()

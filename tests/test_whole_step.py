@@ -1,0 +1,137 @@
+"""(f) The whole MD step as a hipGraph: replays equal the eager MD bitwise (the reference's own
+check with a deterministic pair potential, tests/test_fixed_capacity_boundary.py:497-536), also
+through capacity growth (recapture) and candidate refresh / fallback windows; the MD is
+checked against the CPU oracle (NHC + Morse) over many steps."""
+import numpy as np
+import pytest
+
+from fastmd_amd import systems
+from fastmd_amd.config import CapacityConfig, InferenceConfig
+
+
+def test_inference_config_contract():
+    assert InferenceConfig().resolved_execution == "whole_step"
+    assert InferenceConfig(execution="eager").resolved_execution == "eager"
+    with pytest.raises(ValueError):
+        InferenceConfig(execution="fast")
+    with pytest.raises(ValueError):
+        CapacityConfig(u_step=0)
+    with pytest.raises(ValueError):
+        CapacityConfig(candidate_skin=-1.0)
+
+
+def test_capacity_tiers_known_answers():
+    from fastmd_amd.engine.capacity_policy import JointCapacityPolicy, held_demand, tier, whole_step_headroom
+
+    assert tier(1000, 512, 256) == 1536 and tier(1100, 512, 256) == 1536 and tier(1300, 512, 256) == 2048
+    assert held_demand(1000, 8, 1.0) == 1008 and held_demand(1000, 8, 1.02) == 1020
+    assert whole_step_headroom(77000, 32) == 576 and whole_step_headroom(1027, 32) == 0
+    p = JointCapacityPolicy(u_step=32, min_pad_u=32)
+    k = p.start(held_demand(1027, 0, 1.02))
+    assert k.u_capacity == 1088  # 135-atom perovskite, MACE capacity step (1 088)
+    assert p.grow(k, 900).u_capacity == 1088 and p.grow(k, 1100).u_capacity > 1088
+
+
+def _md(model, execution, device, steps_per_launch=1, capacity=None, system=None, temperature=500.0):
+    from fastmd_amd.interfaces.gpu_md import GPUResidentMolecularDynamics
+
+    s = system or systems.perovskite(3)
+    return GPUResidentMolecularDynamics(s, model=model, device=device, temperature=temperature, timestep=0.25,
+                                        tdamp=25.0, config=InferenceConfig(execution=execution,
+                                                                           capacity=capacity or CapacityConfig()),
+                                        steps_per_launch=steps_per_launch)
+
+
+def _state(md):
+    import torch
+
+    torch.cuda.synchronize()
+    return md.integrator.state.flat.detach().cpu().clone()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("model_name", ["morse", "mace_like"])
+@pytest.mark.parametrize("steps_per_launch", [1, 5])
+def test_whole_step_equals_eager_bitwise(device, model_name, steps_per_launch):
+    import torch
+
+    from fastmd_amd.models.mace_like import MaceLikeAdapter
+    from fastmd_amd.models.pair_potential import MorsePairAdapter
+
+    print(f"[whole_step] {model_name} spl={steps_per_launch}", flush=True)
+    make = (lambda: MorsePairAdapter(device=device)) if model_name == "morse" else (
+        lambda: MaceLikeAdapter(device=device))
+    eager = _md(make(), "eager", device)
+    graph = _md(make(), "whole_step", device, steps_per_launch=steps_per_launch)
+    assert torch.equal(_state(eager), _state(graph))
+    eager.run(20)
+    graph.run(20)
+    a, b = _state(eager), _state(graph)
+    assert torch.equal(a, b), float((a - b).abs().max())
+    stats = graph.whole_step_stats()
+    assert stats["launches"] == 20 // steps_per_launch and stats["fallback_windows"] == 0
+
+
+@pytest.mark.gpu
+def test_whole_step_capacity_growth_and_refresh_paths(device):
+    """A tiny capacity step forces overflow -> growth -> recapture; a tiny skin forces candidate
+    refreshes and fallback windows. The trajectory stays the eager one, bitwise."""
+    import torch
+
+    from fastmd_amd.models.pair_potential import MorsePairAdapter
+
+    s = systems.perovskite(3)
+    eager = _md(MorsePairAdapter(device=device), "eager", device, system=s)
+    tight = CapacityConfig(u_step=1, min_pad_u=0, candidate_skin=0.05)
+    graph = _md(MorsePairAdapter(device=device), "whole_step", device, steps_per_launch=2, capacity=tight, system=s)
+    eager.run(30)
+    graph.run(30)
+    assert torch.equal(_state(eager), _state(graph))
+    st = graph.whole_step_stats()
+    print(st, flush=True)
+    assert st["candidate_refreshes"] > 2
+
+
+@pytest.mark.gpu
+def test_whole_step_morse_md_matches_cpu_oracle(device):
+    """configs[0] plumbing: Morse MD (NHC 500 K, dt 0.25 fs) for 200 steps on the GPU vs the CPU
+    oracle (numpy NHC + PyTorch-CPU Morse forces in float32, like the GPU): positions agree to fp32
+    noise, and the conserved quantity drifts no more than the oracle's."""
+    import torch
+
+    from oracle import models as om
+    from oracle import nhc as onhc
+    from oracle import nl as onl
+    from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
+    from fastmd_amd.models.pair_potential import MorsePairAdapter
+
+    s = systems.perovskite(3)
+    md = _md(MorsePairAdapter(device=device), "whole_step", device, steps_per_launch=10, system=s)
+    cell32 = s.cell.astype(np.float32)
+    inv = np.linalg.inv(cell32.astype(np.float64)).astype(np.float32)
+
+    def forces(q):
+        _, wraps, wrapped = onl.wrap(q, inv, cell32)
+        cand = onl.candidates(wrapped, cell32, np.float32(36.0 + 1e-3), 200)
+        b = onl.build(q, inv, cell32, cand, q.astype(np.float32), wraps, np.float32(36.0), np.float32(1.0), (1, 0, 0),
+                      10 ** 6)
+        e = b.n_edges
+        pos = torch.tensor(b.wrapped)
+        energy, f, _ = om.energy_and_forces(om.morse_node_energy, pos, torch.tensor(cell32), torch.tensor(
+            b.center[:e].astype(np.int64)), torch.tensor(b.neighbor[:e].astype(np.int64)), torch.tensor(b.images[:e]))
+        return f.numpy().astype(np.float32), float(energy)
+
+    p0 = maxwell_boltzmann_momenta(s.masses, 500.0, seed=0)
+    f0, e0 = forces(s.positions)
+    o = onhc.NHC(s.masses, s.positions, p0, temperature_K=500.0, timestep=0.25 * onhc.FS, tdamp=25 * onhc.FS,
+                 f32_kick=True, forces=f0, energy=e0)
+    c0_gpu, c0_cpu = md.conserved_energy(), o.conserved_energy()
+    assert abs(c0_gpu - c0_cpu) < 1e-4 * s.n_atoms
+    for _ in range(200):
+        o.step(forces)
+    md.run(200)
+    q = md.positions.cpu().numpy()
+    assert np.max(np.abs(q - o.q)) < 1e-3
+    drift_gpu = abs(md.conserved_energy() - c0_gpu)
+    drift_cpu = abs(o.conserved_energy() - c0_cpu)
+    assert drift_gpu <= 2 * drift_cpu + 1e-6 * s.n_atoms, (drift_gpu, drift_cpu)
