@@ -58,3 +58,37 @@ __device__ __forceinline__ int lane_prefix(uint64_t mask) {
   const int lane = threadIdx.x & (FMD_WAVE - 1);
   return __popcll(mask & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
 }
+
+// Exclusive prefix sum of one integer per thread over the workgroup (blockDim a multiple of
+// 64, at most 1024): wave inclusive scans by shuffles, then a scan of the wave totals by wave 0.
+// Returns the thread's exclusive prefix; *total receives the block total in every thread.
+// `s_wave` is LDS scratch of at least 16 entries. Integer sums are exact: the result does not
+// depend on the order.
+template <typename T>
+__device__ __forceinline__ T block_exclusive_scan(T v, T* s_wave, T* total) {
+  const int lane = threadIdx.x & (FMD_WAVE - 1), wave = threadIdx.x / FMD_WAVE;
+  const int nw = blockDim.x / FMD_WAVE;
+  T incl = v;
+#pragma unroll
+  for (int off = 1; off < FMD_WAVE; off <<= 1) {
+    const T o = __shfl_up(incl, off, FMD_WAVE);
+    if (lane >= off) incl += o;
+  }
+  __syncthreads();  // s_wave may be in use by a previous call
+  if (lane == FMD_WAVE - 1) s_wave[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    T w = lane < nw ? s_wave[lane] : T(0);
+    T wi = w;
+#pragma unroll
+    for (int off = 1; off < FMD_WAVE; off <<= 1) {
+      const T o = __shfl_up(wi, off, FMD_WAVE);
+      if (lane >= off) wi += o;
+    }
+    if (lane < nw) s_wave[lane] = wi - w;  // exclusive offsets of the waves
+    if (lane == nw - 1) s_wave[FMD_WAVE / 4] = wi;  // total (slot 16)
+  }
+  __syncthreads();
+  *total = s_wave[FMD_WAVE / 4];
+  return s_wave[wave] + incl - v;
+}

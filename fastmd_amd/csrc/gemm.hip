@@ -3,11 +3,11 @@
 // C[M,N] = A[M,K] * op(B) (+ bias) (+ C), fp32 output, MFMA accumulation in fp32:
 //   fp32: v_mfma_f32_32x32x2_f32   (A/B operands fp32; 157 TFLOP/s dense peak on MI355X)
 //   bf16: v_mfma_f32_32x32x16_bf16 (A/B operands bf16; 2.5 PFLOP/s dense peak)
-// Workgroup: 256 threads = 4 waves in a 2x2 arrangement; block tile 128x128, each wave owns a
-// 64x64 sub-tile (2x2 MFMA 32x32 blocks, 64 accumulator registers per lane). The K dimension
-// is staged through LDS in BK-wide slices; the next slice's global loads are issued before
-// the MFMAs of the current one (register double buffering). Any M, N, K (tails are zero-filled
-// in LDS), so K = 2F+8 (136, 264, 520) needs no padding by the caller.
+// Workgroup: 256 threads = 4 waves in a 2x2 arrangement; block tile 128x128 (each wave a 64x64
+// sub-tile: 2x2 MFMA 32x32 blocks, 64 accumulator registers per lane) or 64x64 for small
+// problems. The K dimension is staged through LDS in BK-wide slices; the next slice's global
+// loads are issued before the MFMAs of the current one. Any M, N, K (tails are zero-filled in
+// LDS), so K = 2F+8 (136, 264, 520) needs no padding by the caller.
 // MFMA operand layouts (32x32, one block):
 //   A operand: lane l holds A[l%32][k0 + (l/32)*KPL .. +KPL)   (KPL = 1 fp32 / 8 bf16)
 //   B operand: lane l holds B[k0 + (l/32)*KPL .. +KPL)[l%32]
@@ -23,14 +23,14 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 
-template <typename Store>
-__device__ __forceinline__ void epilogue(const f32x16 (&acc)[2][2], int64_t row0, int64_t col0, int64_t m, int64_t n,
-                                         const float* bias, float* c, int64_t ldc, int accumulate, int act) {
+template <int WM, int WN>
+__device__ __forceinline__ void epilogue(const f32x16 (&acc)[WM][WN], int64_t row0, int64_t col0, int64_t m,
+                                         int64_t n, const float* bias, float* c, int64_t ldc, int accumulate, int act) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int bi = 0; bi < 2; ++bi)
+  for (int bi = 0; bi < WM; ++bi)
 #pragma unroll
-    for (int bj = 0; bj < 2; ++bj) {
+    for (int bj = 0; bj < WN; ++bj) {
       const int64_t col = col0 + bj * 32 + (lane & 31);
       if (col >= n) continue;
       const float b = bias ? bias[col] : 0.f;
@@ -48,136 +48,129 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[2][2], int64_t row0
 }
 
 // ---------------------------------------------------------------------------------------- fp32
-constexpr int BK32 = 16;
-constexpr int LDA32 = BM + 4;  // LDS row of one k: BM floats (+pad)
+// Block tile BM x BN (64 or 128 each), K staged in BK = 32 slices through a double-buffered LDS
+// (one barrier per slice: the next slice is stored into the other buffer while this one feeds
+// the MFMAs). 4 waves in 2 x 2; wave tile (BM/2) x (BN/2) = WM x WN MFMA blocks of 32 x 32.
+// LDS holds both operands k-major (As[k][i], Bs[k][j]) so a lane's MFMA operand is one
+// ds_read_b32 at a conflict-free address (consecutive lanes, consecutive i / j).
+constexpr int BK32 = 32;
 
-// A tile [BM x BK] -> LDS As[k][i]; B tile -> Bs[k][j]
-template <int BLAYOUT>
+template <int BM, int BN, int BLAYOUT>
 __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restrict__ a, int64_t lda,
                                                             const float* __restrict__ b, int64_t ldb,
                                                             const float* __restrict__ bias, float* c, int64_t ldc,
                                                             int64_t m, int64_t n, int64_t k, int accumulate, int act) {
-  __shared__ float As[BK32][LDA32];
-  __shared__ float Bs[BK32][LDA32];
+  constexpr int WM = BM / 64, WN = BN / 64;           // MFMA blocks per wave
+  constexpr int LDA = BM + 4, LDB = BN + 4;           // padded LDS rows
+  constexpr int A_VEC = BM * BK32 / 4 / kThreads;     // float4 loads per thread (A)
+  constexpr int B_VEC = BN * BK32 / 4 / kThreads;     // float4 loads per thread (B)
+  __shared__ float As[2][BK32][LDA];
+  __shared__ float Bs[2][BK32][LDB];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t row_blk = (int64_t)blockIdx.x * BM, col_blk = (int64_t)blockIdx.y * BN;
 
-  // loader mapping: 128 rows x 16 k = 512 float4; 2 per thread
-  float4 ra[2], rb[2];
+  float4 ra[A_VEC], rb[B_VEC];
+  auto load4 = [&](const float* p, bool in_rows, int64_t kk, int64_t kmax) -> float4 {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (!in_rows) return v;
+    if (kk + 3 < kmax && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) return *reinterpret_cast<const float4*>(p);
+    v.x = kk < kmax ? p[0] : 0.f;
+    v.y = kk + 1 < kmax ? p[1] : 0.f;
+    v.z = kk + 2 < kmax ? p[2] : 0.f;
+    v.w = kk + 3 < kmax ? p[3] : 0.f;
+    return v;
+  };
+  // A tile: BM rows x 32 k; id -> (row id / 8, k (id % 8) * 4)
   auto load_a = [&](int64_t k0) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int id = t + q * kThreads;  // 0..511
-      const int r = id >> 2, kc = (id & 3) * 4;
+    for (int q = 0; q < A_VEC; ++q) {
+      const int id = t + q * kThreads;
+      const int r = id >> 3, kc = (id & 7) * 4;
       const int64_t gr = row_blk + r, gk = k0 + kc;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (gr < m) {
-        const float* p = a + gr * lda + gk;
-        if (gk + 3 < k && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
-          v = *reinterpret_cast<const float4*>(p);
-        } else {
-          v.x = gk < k ? p[0] : 0.f;
-          v.y = gk + 1 < k ? p[1] : 0.f;
-          v.z = gk + 2 < k ? p[2] : 0.f;
-          v.w = gk + 3 < k ? p[3] : 0.f;
-        }
-      }
-      ra[q] = v;
+      ra[q] = load4(a + gr * lda + gk, gr < m, gk, k);
     }
   };
   auto load_b = [&](int64_t k0) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < B_VEC; ++q) {
       const int id = t + q * kThreads;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (BLAYOUT == 0) {  // B [N, K]: row j, 4 consecutive k
-        const int r = id >> 2, kc = (id & 3) * 4;
+        const int r = id >> 3, kc = (id & 7) * 4;
         const int64_t gj = col_blk + r, gk = k0 + kc;
-        if (gj < n) {
-          const float* p = b + gj * ldb + gk;
-          if (gk + 3 < k && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
-            v = *reinterpret_cast<const float4*>(p);
-          } else {
-            v.x = gk < k ? p[0] : 0.f;
-            v.y = gk + 1 < k ? p[1] : 0.f;
-            v.z = gk + 2 < k ? p[2] : 0.f;
-            v.w = gk + 3 < k ? p[3] : 0.f;
-          }
-        }
+        rb[q] = load4(b + gj * ldb + gk, gj < n, gk, k);
       } else {  // B [K, N]: row k, 4 consecutive j
-        const int kr = id >> 5, jc = (id & 31) * 4;
+        constexpr int JV = BN / 4;
+        const int kr = id / JV, jc = (id % JV) * 4;
         const int64_t gk = k0 + kr, gj = col_blk + jc;
-        if (gk < k) {
-          const float* p = b + gk * ldb + gj;
-          if (gj + 3 < n && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) {
-            v = *reinterpret_cast<const float4*>(p);
-          } else {
-            v.x = gj < n ? p[0] : 0.f;
-            v.y = gj + 1 < n ? p[1] : 0.f;
-            v.z = gj + 2 < n ? p[2] : 0.f;
-            v.w = gj + 3 < n ? p[3] : 0.f;
-          }
-        }
+        rb[q] = load4(b + gk * ldb + gj, gk < k, gj, n);
       }
-      rb[q] = v;
     }
   };
-  auto store_tiles = [&]() {
+  auto store_tiles = [&](int st) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < A_VEC; ++q) {
       const int id = t + q * kThreads;
-      const int r = id >> 2, kc = (id & 3) * 4;
-      As[kc + 0][r] = ra[q].x;
-      As[kc + 1][r] = ra[q].y;
-      As[kc + 2][r] = ra[q].z;
-      As[kc + 3][r] = ra[q].w;
+      const int r = id >> 3, kc = (id & 7) * 4;
+      As[st][kc + 0][r] = ra[q].x;
+      As[st][kc + 1][r] = ra[q].y;
+      As[st][kc + 2][r] = ra[q].z;
+      As[st][kc + 3][r] = ra[q].w;
+    }
+#pragma unroll
+    for (int q = 0; q < B_VEC; ++q) {
+      const int id = t + q * kThreads;
       if (BLAYOUT == 0) {
-        Bs[kc + 0][r] = rb[q].x;
-        Bs[kc + 1][r] = rb[q].y;
-        Bs[kc + 2][r] = rb[q].z;
-        Bs[kc + 3][r] = rb[q].w;
+        const int r = id >> 3, kc = (id & 7) * 4;
+        Bs[st][kc + 0][r] = rb[q].x;
+        Bs[st][kc + 1][r] = rb[q].y;
+        Bs[st][kc + 2][r] = rb[q].z;
+        Bs[st][kc + 3][r] = rb[q].w;
       } else {
-        const int kr = id >> 5, jc = (id & 31) * 4;
-        *reinterpret_cast<float4*>(&Bs[kr][jc]) = rb[q];
+        constexpr int JV = BN / 4;
+        const int kr = id / JV, jc = (id % JV) * 4;
+        *reinterpret_cast<float4*>(&Bs[st][kr][jc]) = rb[q];
       }
     }
   };
 
-  f32x16 acc[2][2];
+  f32x16 acc[WM][WN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < WN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   const int64_t nk = fmd_cdiv(k, BK32);
   load_a(0);
   load_b(0);
+  store_tiles(0);
+  __syncthreads();
   for (int64_t kt = 0; kt < nk; ++kt) {
-    __syncthreads();
-    store_tiles();
-    __syncthreads();
-    if (kt + 1 < nk) {
+    const int st = (int)(kt & 1);
+    const bool more = kt + 1 < nk;
+    if (more) {
       load_a((kt + 1) * BK32);
       load_b((kt + 1) * BK32);
     }
 #pragma unroll
     for (int kk = 0; kk < BK32; kk += 2) {
       const int kr = kk + (lane >> 5);
-      float av[2], bv[2];
+      float av[WM], bv[WN];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) av[i] = As[kr][wm * 64 + i * 32 + (lane & 31)];
+      for (int i = 0; i < WM; ++i) av[i] = As[st][kr][wm * (BM / 2) + i * 32 + (lane & 31)];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bv[j] = Bs[kr][wn * 64 + j * 32 + (lane & 31)];
+      for (int j = 0; j < WN; ++j) bv[j] = Bs[st][kr][wn * (BN / 2) + j * 32 + (lane & 31)];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < WN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
+    if (more) store_tiles(st ^ 1);
+    __syncthreads();
   }
-  epilogue<int>(acc, row_blk + wm * 64, col_blk + wn * 64, m, n, bias, c, ldc, accumulate, act);
+  epilogue<WM, WN>(acc, row_blk + wm * (BM / 2), col_blk + wn * (BN / 2), m, n, bias, c, ldc, accumulate, act);
 }
 
 // ---------------------------------------------------------------------------------------- bf16
@@ -289,7 +282,23 @@ __global__ void __launch_bounds__(kThreads) gemm_bf16_kernel(const uint16_t* __r
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
   }
-  epilogue<int>(acc, row_blk + wm * 64, col_blk + wn * 64, m, n, bias, c, ldc, accumulate, act);
+  epilogue<2, 2>(acc, row_blk + wm * 64, col_blk + wn * 64, m, n, bias, c, ldc, accumulate, act);
+}
+
+// Tile choice: 128 x 128 when that still gives two workgroups per CU (256 CUs), else 64 x 64
+// (small node-side GEMMs and the 135-atom edge GEMM: 4x more workgroups, 4x less serial K work
+// per wave).
+template <int BM, int BN>
+void launch_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32_t b_layout,
+                            const float* bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k,
+                            int32_t accumulate, int32_t act, hipStream_t stream) {
+  dim3 grid((unsigned)fmd_cdiv(m, BM), (unsigned)fmd_cdiv(n, BN));
+  if (b_layout == 0)
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, 0>), grid, dim3(kThreads), 0, stream, a, lda, b, ldb, bias, c, ldc, m,
+                       n, k, accumulate, act);
+  else
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, 1>), grid, dim3(kThreads), 0, stream, a, lda, b, ldb, bias, c, ldc, m,
+                       n, k, accumulate, act);
 }
 
 }  // namespace
@@ -304,14 +313,12 @@ int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32
   FMD_REQUIRE(epilogue_kind == 0 || epilogue_kind == 1);
   if (m == 0 || n == 0) return FMD_OK;
   FMD_REQUIRE(k == 0 || (a && b && lda >= k && ldb >= (b_layout == 0 ? k : n)));
-  FMD_REQUIRE(fmd_cdiv(m, BM) < (int64_t(1) << 31) && fmd_cdiv(n, BN) < 65536);
-  dim3 grid((unsigned)fmd_cdiv(m, BM), (unsigned)fmd_cdiv(n, BN));
-  if (b_layout == 0)
-    hipLaunchKernelGGL(gemm_f32_kernel<0>, grid, dim3(kThreads), 0, stream, a, lda, b, ldb, bias, c, ldc, m, n, k,
-                       accumulate, epilogue_kind);
+  FMD_REQUIRE(fmd_cdiv(m, 64) < (int64_t(1) << 31) && fmd_cdiv(n, 64) < 65536);
+  const int64_t big_tiles = fmd_cdiv(m, 128) * fmd_cdiv(n, 128);
+  if (big_tiles >= 512)
+    launch_gemm_f32<128, 128>(a, lda, b, ldb, b_layout, bias, c, ldc, m, n, k, accumulate, epilogue_kind, stream);
   else
-    hipLaunchKernelGGL(gemm_f32_kernel<1>, grid, dim3(kThreads), 0, stream, a, lda, b, ldb, bias, c, ldc, m, n, k,
-                       accumulate, epilogue_kind);
+    launch_gemm_f32<64, 64>(a, lda, b, ldb, b_layout, bias, c, ldc, m, n, k, accumulate, epilogue_kind, stream);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -187,13 +187,23 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
 //   g_wa = gA0 h0_j, g_wb = h0_j (gA1 . u), g_wc = gA0 proj, g_wd = sum_x gA1_x h1_j,x
 //   g_z = g_w * fcut * silu'(z)            -> gz [E, 4C]
 //   g_fcut = sum_ch g_w * silu(z), g_u_x = sum_ch (gA0 wc h1_j,x + gA1_x wb h0_j)  -> ggeo [E, 4]
+// With w1ef (the radial-basis rows of the edge GEMM weight, [nb, 4C]) the kernel also forms
+// gef[e, n] = sum_k gz[e, k] w1ef[n, k] (the radial block of the gather-cat row gradient) and
+// gz itself may be null (not stored): the first layer needs no other part of gz @ W1^T.
+constexpr int kMaxBasis = 16;
+
 template <int CPL, bool H1>
 __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     const float* z, const float* geo, const int32_t* edge_index, const int64_t* off, const int64_t* n_edges,
     int64_t e_cap, int64_t n, const float* h0, const float* h1, const float* gA0, const float* gA1, float inv_avg,
-    float* gz, float* ggeo, int accumulate_geo) {
+    float* gz, float* ggeo, int accumulate_geo, const float* w1ef, int nb, float* gef) {
   constexpr int C = 64 * CPL;
+  __shared__ float s_w[kMaxBasis * 4 * C];
   const int lane = threadIdx.x & 63;
+  if (w1ef) {
+    for (int k = threadIdx.x; k < nb * 4 * C; k += blockDim.x) s_w[k] = w1ef[k];
+    __syncthreads();
+  }
   const int64_t i = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64;
   if (i >= n) return;
   const int64_t rows = real_rows(n_edges, e_cap);
@@ -214,7 +224,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     const float ux = g[0], uy = g[1], uz = g[2], fc = g[4];
     const int64_t j = edge_index[2 * e + 1];
     const float* ze = z + e * 4 * C + c0;
-    float* gze = gz + e * 4 * C + c0;
+    float gzl[4][CPL];
     float sf = 0.f, su0 = 0.f, su1 = 0.f, su2 = 0.f;
 #pragma unroll
     for (int q = 0; q < CPL; ++q) {
@@ -223,8 +233,8 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
       const float za = ze[q], zb = ze[C + q];
       const float sa = sigmoid(za), sb = sigmoid(zb);
       const float gwa = g0[q] * hj, gwb = hj * gu;
-      gze[q] = gwa * fc * sa * (1.0f + za * (1.0f - sa));
-      gze[C + q] = gwb * fc * sb * (1.0f + zb * (1.0f - sb));
+      gzl[0][q] = gwa * fc * sa * (1.0f + za * (1.0f - sa));
+      gzl[1][q] = gwb * fc * sb * (1.0f + zb * (1.0f - sb));
       sf += gwa * za * sa + gwb * zb * sb;
       const float wb = zb * sb * fc;
       su0 += g1[0][q] * wb * hj;
@@ -237,16 +247,34 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
         const float sc = sigmoid(zc), sd = sigmoid(zd);
         const float proj = hx * ux + hy * uy + hz * uz;
         const float gwc = g0[q] * proj, gwd = g1[0][q] * hx + g1[1][q] * hy + g1[2][q] * hz;
-        gze[2 * C + q] = gwc * fc * sc * (1.0f + zc * (1.0f - sc));
-        gze[3 * C + q] = gwd * fc * sd * (1.0f + zd * (1.0f - sd));
+        gzl[2][q] = gwc * fc * sc * (1.0f + zc * (1.0f - sc));
+        gzl[3][q] = gwd * fc * sd * (1.0f + zd * (1.0f - sd));
         sf += gwc * zc * sc + gwd * zd * sd;
         const float t = g0[q] * zc * sc * fc;
         su0 += t * hx;
         su1 += t * hy;
         su2 += t * hz;
       } else {
-        gze[2 * C + q] = 0.f;
-        gze[3 * C + q] = 0.f;
+        gzl[2][q] = 0.f;
+        gzl[3][q] = 0.f;
+      }
+    }
+    if (gz) {
+      float* gze = gz + e * 4 * C + c0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) gze[b * C + q] = gzl[b][q];
+    }
+    if (w1ef) {
+      for (int nn = 0; nn < nb; ++nn) {
+        float acc = 0.f;
+#pragma unroll
+        for (int b = 0; b < (H1 ? 4 : 2); ++b)
+#pragma unroll
+          for (int q = 0; q < CPL; ++q) acc += gzl[b][q] * s_w[nn * 4 * C + b * C + c0 + q];
+        acc = wave_sum(acc);
+        if (lane == 0) gef[e * nb + nn] = acc;
       }
     }
     sf = wave_sum(sf);
@@ -511,13 +539,13 @@ template <int CPL>
 int launch_bwd_edge(bool h1, dim3 grid, hipStream_t s, const float* z, const float* geo, const int32_t* ei,
                     const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const float* h0,
                     const float* h1p, const float* gA0, const float* gA1, float inv_avg, float* gz, float* ggeo,
-                    int acc) {
+                    int acc, const float* w1ef, int nb, float* gef) {
   if (h1)
     hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, geo, ei, off, ne, e_cap,
-                       n, h0, h1p, gA0, gA1, inv_avg, gz, ggeo, acc);
+                       n, h0, h1p, gA0, gA1, inv_avg, gz, ggeo, acc, w1ef, nb, gef);
   else
     hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, geo, ei, off, ne, e_cap,
-                       n, h0, h1p, gA0, gA1, inv_avg, gz, ggeo, acc);
+                       n, h0, h1p, gA0, gA1, inv_avg, gz, ggeo, acc, w1ef, nb, gef);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -576,19 +604,21 @@ int fmd_mace_message_bwd_f32(const float* z, const float* geo, const int32_t* ed
                              const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
                              int32_t channels, const float* h0, const float* h1, const float* gA0, const float* gA1,
                              float inv_avg, float* gz, float* ggeo, int32_t accumulate_geo, float* gh0, float* gh1,
-                             int32_t accumulate_h, hipStream_t stream) {
-  FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && gA0 && gA1 && gz && ggeo && n_atoms >= 0);
+                             int32_t accumulate_h, const float* w1ef, int32_t nb, float* gef, hipStream_t stream) {
+  FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && gA0 && gA1 && ggeo && n_atoms >= 0);
+  FMD_REQUIRE(gz || w1ef);
+  FMD_REQUIRE(!w1ef || (gef && nb > 0 && nb <= kMaxBasis));
   FMD_REQUIRE(!gh0 || reverse);
   if (n_atoms == 0) return FMD_OK;
   dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
   int rc = FMD_OK;
   switch (channels / 64) {
     case 1: rc = launch_bwd_edge<1>(h1 != nullptr, grid, stream, z, geo, edge_index, edge_offsets, n_edges, e_cap,
-                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, ggeo, accumulate_geo); break;
+                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, ggeo, accumulate_geo, w1ef, nb, gef); break;
     case 2: rc = launch_bwd_edge<2>(h1 != nullptr, grid, stream, z, geo, edge_index, edge_offsets, n_edges, e_cap,
-                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, ggeo, accumulate_geo); break;
+                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, ggeo, accumulate_geo, w1ef, nb, gef); break;
     case 4: rc = launch_bwd_edge<4>(h1 != nullptr, grid, stream, z, geo, edge_index, edge_offsets, n_edges, e_cap,
-                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, ggeo, accumulate_geo); break;
+                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, ggeo, accumulate_geo, w1ef, nb, gef); break;
     default: return FMD_EUNSUPPORTED;
   }
   if (rc != FMD_OK || !gh0) return rc;

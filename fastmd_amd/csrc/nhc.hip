@@ -9,7 +9,7 @@
 // ke2 recomputed, p_eta_j sweep forward; per Suzuki-Yoshida coefficient, tloop times.
 // FP contraction is off (each op rounded like NumPy); exp is the HIP device library's.
 // Momenta live in registers (KPT <= 4 atoms per thread, no spills) up to 4096 atoms; beyond
-// that they are scaled in place in global memory (L2 resident) pass by pass.
+// that the multi-block path below runs (three grid kernels per half step).
 #pragma clang fp contract(off)
 
 #include "common.h"
@@ -231,6 +231,117 @@ __global__ void __launch_bounds__(kThreads) nhc_post_kernel(double* p, const voi
     e_out[0] = e_kind == 2 ? static_cast<const double*>(e_in)[0] : (double)static_cast<const float*>(e_in)[0];
 }
 
+
+// ------------------------------------------------------------------------------------------
+// Multi-block path (systems beyond the register path): a half step is three grid kernels --
+// per-block partial sums of p*p/m (fixed order) -> one workgroup reduces them in block order
+// and integrates the chain, recording the momentum scale factor of every Suzuki-Yoshida
+// sub-step -> an elementwise pass multiplies p by those factors in sequence (the same roundings
+// as the single-workgroup path). After a scaling, ke2 is updated as ke2 * s^2 instead of a new
+// reduction (the reference's "scaled" ke2 update, gpu_nhc.py:520-706), which differs from the
+// recomputed sum in the last bits only.
+// work layout (float64): [0, kMaxScales) scale factors, then the block partials.
+// ------------------------------------------------------------------------------------------
+constexpr int kMbThreads = 256;
+constexpr int kMaxScales = 3 * 16;
+
+__device__ __forceinline__ double block_sum_mb(double v, double* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & (FMD_WAVE - 1), wave = threadIdx.x / FMD_WAVE;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  double s = red[0];
+  for (int w = 1; w < (int)(blockDim.x / FMD_WAVE); ++w) s = s + red[w];
+  return s;
+}
+
+// p += kick (post half: kick first, cache F) then the block partial of p*p/m
+__global__ void __launch_bounds__(kMbThreads) nhc_mb_partials_kernel(double* p, const void* f_in, int f_in_64,
+                                                                     double* f_cache, const double* masses,
+                                                                     const double* consts, int kick,
+                                                                     int f32_kick, int64_t n, double* work) {
+  __shared__ double red[kMbThreads / FMD_WAVE];
+  const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  double s = 0.0;
+  if (a < n) {
+    const double m = masses[a];
+    const double dt2 = consts[1];
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+      double pv = p[3 * a + d];
+      if (kick) {
+        const double fv = f_in_64 ? static_cast<const double*>(f_in)[3 * a + d]
+                                  : (double)static_cast<const float*>(f_in)[3 * a + d];
+        pv = pv + kick_of(dt2, fv, f32_kick);
+        p[3 * a + d] = pv;
+        f_cache[3 * a + d] = fv;
+      }
+      s = s + (pv * pv) / m;
+    }
+  }
+  s = block_sum_mb(s, red);
+  if (threadIdx.x == 0) work[kMaxScales + blockIdx.x] = s;
+}
+
+// one workgroup: ke2 from the partials, the chain half step, the scale factors
+__global__ void __launch_bounds__(FMD_WAVE) nhc_mb_chain_kernel(double* eta, double* pe, const double* consts, int M,
+                                                                int tloop, int64_t nblocks, double* work) {
+  double s = 0.0;
+  for (int64_t b = threadIdx.x; b < nblocks; b += FMD_WAVE) s = s + work[kMaxScales + b];
+  s = wave_sum(s);
+  if (threadIdx.x != 0) return;
+  Chain c;
+  c.M = M;
+  for (int j = 0; j < kMaxChain; ++j) {
+    c.eta[j] = j < M ? eta[j] : 0.0;
+    c.pe[j] = j < M ? pe[j] : 0.0;
+    c.Q[j] = j < M ? consts[16 + j] : 1.0;
+  }
+  const double kT = consts[2], ndof_kT = consts[3];
+  double ke2 = s;
+  int ns = 0;
+  for (int tl = 0; tl < tloop; ++tl) {
+    for (int k = 0; k < 3; ++k) {
+      const double delta = consts[4 + 4 * k], delta2 = consts[5 + 4 * k];
+      const double neg_delta4 = consts[6 + 4 * k], neg_delta = consts[7 + 4 * k];
+      for (int jj = 0; jj < c.M; ++jj) p_eta_j(c, c.M - 1 - jj, ke2, kT, ndof_kT, delta2, neg_delta4);
+      for (int j = 0; j < c.M; ++j) c.eta[j] = c.eta[j] + (delta * c.pe[j]) / c.Q[j];
+      const double scale = exp((neg_delta * c.pe[0]) / c.Q[0]);
+      work[ns++] = scale;
+      ke2 = ke2 * (scale * scale);
+      for (int j = 0; j < c.M; ++j) p_eta_j(c, j, ke2, kT, ndof_kT, delta2, neg_delta4);
+    }
+  }
+  for (int j = 0; j < M; ++j) {
+    eta[j] = c.eta[j];
+    pe[j] = c.pe[j];
+  }
+}
+
+// p *= scale factors in sequence; pre half: then kick with the cached F and drift
+__global__ void __launch_bounds__(kMbThreads) nhc_mb_apply_kernel(double* q, double* p, const double* f,
+                                                                  const double* masses, const double* consts,
+                                                                  int nscale, int pre, int f32_kick, int64_t n,
+                                                                  const double* work, const void* e_in, int e_kind,
+                                                                  double* e_out) {
+  const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (a == 0 && e_kind != 0)
+    e_out[0] = e_kind == 2 ? static_cast<const double*>(e_in)[0] : (double)static_cast<const float*>(e_in)[0];
+  if (a >= n) return;
+  const double m = masses[a];
+  const double dt = consts[0], dt2 = consts[1];
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    double pv = p[3 * a + d];
+    for (int k = 0; k < nscale; ++k) pv = pv * work[k];
+    if (pre) {
+      pv = pv + kick_of(dt2, f[3 * a + d], f32_kick);
+      q[3 * a + d] = q[3 * a + d] + (dt * pv) / m;
+    }
+    p[3 * a + d] = pv;
+  }
+}
+
 int pick_kpt(int64_t n, int threads) {
   const int64_t per = fmd_cdiv(n, threads);
   if (per <= 1) return 1;
@@ -251,18 +362,34 @@ int nhc_threads(int64_t n) {
     case 1: hipLaunchKernelGGL(KERNEL<1>, dim3(1), dim3(threads), 0, stream, __VA_ARGS__); break;       \
     case 2: hipLaunchKernelGGL(KERNEL<2>, dim3(1), dim3(threads), 0, stream, __VA_ARGS__); break;       \
     case 4: hipLaunchKernelGGL(KERNEL<4>, dim3(1), dim3(threads), 0, stream, __VA_ARGS__); break;       \
-    default: hipLaunchKernelGGL(KERNEL<0>, dim3(1), dim3(threads), 0, stream, __VA_ARGS__); break;      \
+    default: return FMD_EUNSUPPORTED;                                                                    \
   }
 
 extern "C" {
 
+int64_t fmd_nhc_work_size(int64_t n_atoms) { return kMaxScales + fmd_cdiv(n_atoms > 0 ? n_atoms : 1, kMbThreads); }
+
 int fmd_nhc_pre_force(double* q, double* p, const double* f, const double* masses, double* eta, double* p_eta,
                       const double* consts, int64_t n_atoms, int32_t tchain, int32_t tloop, int32_t f32_kick,
-                      hipStream_t stream) {
+                      double* work, hipStream_t stream) {
   FMD_REQUIRE(q && p && f && masses && eta && p_eta && consts && n_atoms > 0);
   FMD_REQUIRE(tchain >= 1 && tchain <= kMaxChain && tloop >= 1);
   const int threads = nhc_threads(n_atoms);
   const int kpt = pick_kpt(n_atoms, threads);
+  if (kpt == 0) {
+    FMD_REQUIRE(work && 3 * tloop <= kMaxScales);
+    const int64_t nb = fmd_cdiv(n_atoms, kMbThreads);
+    hipLaunchKernelGGL(nhc_mb_partials_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, p, (const void*)f, 1,
+                       (double*)nullptr, masses, consts, 0, f32_kick, n_atoms, work);
+    FMD_CHECK_LAUNCH();
+    hipLaunchKernelGGL(nhc_mb_chain_kernel, dim3(1), dim3(FMD_WAVE), 0, stream, eta, p_eta, consts, tchain, tloop, nb,
+                       work);
+    FMD_CHECK_LAUNCH();
+    hipLaunchKernelGGL(nhc_mb_apply_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, q, p, f, masses, consts,
+                       3 * tloop, 1, f32_kick, n_atoms, (const double*)work, (const void*)nullptr, 0, (double*)nullptr);
+    FMD_CHECK_LAUNCH();
+    return FMD_OK;
+  }
   FMD_NHC_DISPATCH(nhc_pre_kernel, q, p, f, masses, eta, p_eta, consts, n_atoms, tchain, tloop, f32_kick);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
@@ -270,13 +397,28 @@ int fmd_nhc_pre_force(double* q, double* p, const double* f, const double* masse
 
 int fmd_nhc_post_force(double* p, const void* f_in, int32_t f_in_is_f64, double* f_cache, const double* masses,
                        double* eta, double* p_eta, const double* consts, const void* e_in, int32_t e_kind,
-                       double* e_out, int64_t n_atoms, int32_t tchain, int32_t tloop, int32_t f32_kick,
+                       double* e_out, int64_t n_atoms, int32_t tchain, int32_t tloop, int32_t f32_kick, double* work,
                        hipStream_t stream) {
   FMD_REQUIRE(p && f_in && f_cache && masses && eta && p_eta && consts && n_atoms > 0);
   FMD_REQUIRE(tchain >= 1 && tchain <= kMaxChain && tloop >= 1);
   FMD_REQUIRE(e_kind == 0 || (e_in && e_out && (e_kind == 1 || e_kind == 2)));
   const int threads = nhc_threads(n_atoms);
   const int kpt = pick_kpt(n_atoms, threads);
+  if (kpt == 0) {
+    FMD_REQUIRE(work && 3 * tloop <= kMaxScales);
+    const int64_t nb = fmd_cdiv(n_atoms, kMbThreads);
+    hipLaunchKernelGGL(nhc_mb_partials_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, p, f_in, f_in_is_f64,
+                       f_cache, masses, consts, 1, f32_kick, n_atoms, work);
+    FMD_CHECK_LAUNCH();
+    hipLaunchKernelGGL(nhc_mb_chain_kernel, dim3(1), dim3(FMD_WAVE), 0, stream, eta, p_eta, consts, tchain, tloop, nb,
+                       work);
+    FMD_CHECK_LAUNCH();
+    hipLaunchKernelGGL(nhc_mb_apply_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, (double*)nullptr, p,
+                       (const double*)nullptr, masses, consts, 3 * tloop, 0, f32_kick, n_atoms, (const double*)work,
+                       e_in, e_kind, e_out);
+    FMD_CHECK_LAUNCH();
+    return FMD_OK;
+  }
   FMD_NHC_DISPATCH(nhc_post_kernel, p, f_in, f_in_is_f64, f_cache, masses, eta, p_eta, consts, e_in, e_kind, e_out,
                    n_atoms, tchain, tloop, f32_kick);
   FMD_CHECK_LAUNCH();

@@ -439,21 +439,16 @@ __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs
   if (lane == 0) s_iso[wave] = iso;
   __syncthreads();
 
-  // (3) exclusive scan of the counts (chunk per thread, then a serial pass over the threads)
+  // (3) exclusive scan of the counts (chunk per thread, then a block scan over the threads)
   {
     const int chunk = (n + T - 1) / T;
     const int lo = t * chunk, hi = lo + chunk < n ? lo + chunk : n;
     int s = 0;
     for (int k = lo; k < hi; ++k) s += s_cnt[k];
-    s_scan[t] = s;
-    __syncthreads();
+    int total = 0;
+    const int mine = block_exclusive_scan<int>(s, s_scan, &total);
     if (t == 0) {
-      int run = 0;
-      for (int k = 0; k < T; ++k) {
-        const int v = s_scan[k];
-        s_scan[k] = run;
-        run += v;
-      }
+      const int run = total;
       s_cnt[kSmallMaxAtoms] = run;
       float m = s_red[0];
       int isol = s_iso[0];
@@ -469,7 +464,7 @@ __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs
       a.edge_offsets[n] = run;
     }
     __syncthreads();
-    int run = s_scan[t];
+    int run = mine;
     for (int k = lo; k < hi; ++k) {
       const int v = s_cnt[k];
       s_cnt[k] = run;  // now the offset
@@ -578,39 +573,52 @@ __global__ void __launch_bounds__(kBlock) nl_count_kernel(BuildArgs a) {
 
 // Kernel 2 (one workgroup): exclusive scan of the counts, the flags and the reductions.
 __global__ void __launch_bounds__(1024) nl_scan_kernel(BuildArgs a, int64_t nblocks) {
-  __shared__ int64_t s_scan[1024];
+  __shared__ float s_max[1024 / FMD_WAVE];
+  __shared__ int32_t s_iso[1024 / FMD_WAVE];
   const int t = threadIdx.x, T = blockDim.x;
+  const int lane = t & (FMD_WAVE - 1), wave = t / FMD_WAVE;
   const int64_t n = a.n;
   const int64_t chunk = fmd_cdiv(n, T);
   const int64_t lo = t * chunk, hi = lo + chunk < n ? lo + chunk : n;
   int64_t s = 0;
   for (int64_t k = lo; k < hi; ++k) s += a.edge_counts[k];
-  s_scan[t] = s;
-  __syncthreads();
-  if (t == 0) {
-    int64_t run = 0;
-    for (int k = 0; k < T; ++k) {
-      const int64_t v = s_scan[k];
-      s_scan[k] = run;
-      run += v;
-    }
+  // block partials of kernel 1 (max displacement, isolated atoms): strided per thread, then
+  // over the wave and over the waves, in a fixed order
+  {
     const float* red = reinterpret_cast<const float*>(a.work);
     const int32_t* isop = reinterpret_cast<const int32_t*>(a.work + fmd_cdiv(nblocks, 2));
-    float m = red[0];
-    int32_t isol = 0;
-    for (int64_t b = 0; b < nblocks; ++b) {
+    float m = 0.f;
+    int32_t iso = 0;
+    for (int64_t b = t; b < nblocks; b += T) {
       m = nan_max(m, red[b]);
-      isol += isop[b];
+      iso += isop[b];
+    }
+    m = wave_nan_max(m);
+    iso = wave_sum(iso);
+    if (lane == 0) {
+      s_max[wave] = m;
+      s_iso[wave] = iso;
+    }
+  }
+  __syncthreads();
+  __shared__ int64_t s_wtot[17];
+  int64_t total = 0;
+  const int64_t mine = block_exclusive_scan<int64_t>(s, s_wtot, &total);
+  if (t == 0) {
+    float m = s_max[0];
+    int32_t isol = s_iso[0];
+    for (int w = 1; w < T / FMD_WAVE; ++w) {
+      m = nan_max(m, s_max[w]);
+      isol += s_iso[w];
     }
     const bool valid = (m * 2.0f <= a.skin_limit) && (a.capacity_valid[0] != 0);
     a.max_disp[0] = m;
     a.cand_valid[0] = valid ? 1 : 0;
-    a.overflow[0] = (run > a.e_cap || !valid) ? 1 : 0;
+    a.overflow[0] = (total > a.e_cap || !valid) ? 1 : 0;
     a.isolated[0] = isol;
-    a.edge_offsets[n] = run;
+    a.edge_offsets[n] = total;
   }
-  __syncthreads();
-  int64_t run = s_scan[t];
+  int64_t run = mine;
   for (int64_t k = lo; k < hi; ++k) {
     const int64_t v = a.edge_counts[k];
     a.edge_offsets[k] = run;

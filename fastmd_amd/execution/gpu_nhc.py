@@ -5,9 +5,9 @@ for the single-device protocol: the float64 state lives in ONE flat device buffe
 ``[q 3N | p 3N | F 3N | eta tchain | p_eta tchain | E 1]`` (NHCState, :216-267) so a
 transactional backup/restore is one copy; a step is ``step_pre_force`` (NHC(dt/2), kick with
 the cached F(q_n), drift) then ``step_post_force(F, E)`` (kick, NHC(dt/2), cache F), each ONE
-kernel launch (``fmd_nhc_pre_force`` / ``fmd_nhc_post_force``) for every system size (the
-reference's fused kernels are single-CTA and limited to 3N <= 16 384, :96,839-849, beyond which
-it runs several hundred torch ops per step). Constants: ``nhc_constants`` forms ASE's scalars
+kernel launch (``fmd_nhc_pre_force`` / ``fmd_nhc_post_force``) up to 4096 atoms and three
+grid-wide kernels beyond (the reference's fused kernels are single-CTA and limited to
+3N <= 16 384, :96,839-849, beyond which it runs several hundred torch ops per step). Constants: ``nhc_constants`` forms ASE's scalars
 with ASE's own Python expressions (:113-133) and ``set_temperature`` rewrites them on the device
 without a host sync. ``backend="torch"`` is not offered: the CPU restatement of the algorithm is
 the test oracle (oracle/nhc.py), not a product path.
@@ -165,6 +165,7 @@ class GPUNoseHooverChainNVT(StatefulIntegrator):
         self.masses = torch.tensor(masses_np, dtype=torch.float64, device=self.device).reshape(n, 1).contiguous()
         self.state = NHCState.allocate(n, self.tchain, self.device)
         self._backup = NHCState.allocate(n, self.tchain, self.device)
+        self._work = torch.zeros(int(_abi.load().fmd_nhc_work_size(n)), dtype=torch.float64, device=self.device)
         self.set_state(positions=positions, momenta=momenta, forces=forces, potential_energy=potential_energy)
 
     # -------------------------------------------------------------- constants
@@ -274,7 +275,8 @@ class GPUNoseHooverChainNVT(StatefulIntegrator):
         st = self.state if state is None else state
         _abi.call("fmd_nhc_pre_force", st.positions.data_ptr(), st.momenta.data_ptr(), st.forces.data_ptr(),
                   self.masses.data_ptr(), st.eta.data_ptr(), st.p_eta.data_ptr(), self.consts.data_ptr(),
-                  self.n_atoms, self.tchain, self.tloop, 1 if self.f32_kick else 0, _abi.stream_handle(self.device))
+                  self.n_atoms, self.tchain, self.tloop, 1 if self.f32_kick else 0, self._work.data_ptr(),
+                  _abi.stream_handle(self.device))
         return st.positions
 
     def step_post_force(self, forces: Tensor, energy: Tensor | None = None, state: NHCState | None = None) -> None:
@@ -297,7 +299,7 @@ class GPUNoseHooverChainNVT(StatefulIntegrator):
                   1 if forces.dtype == torch.float64 else 0, st.forces.data_ptr(), self.masses.data_ptr(),
                   st.eta.data_ptr(), st.p_eta.data_ptr(), self.consts.data_ptr(), _abi.ptr(energy), e_kind,
                   st.potential_energy.data_ptr(), self.n_atoms, self.tchain, self.tloop,
-                  1 if self.f32_kick else 0, _abi.stream_handle(self.device))
+                  1 if self.f32_kick else 0, self._work.data_ptr(), _abi.stream_handle(self.device))
 
     def step(self, force_fn, state: NHCState | None = None):
         st = self.state if state is None else state

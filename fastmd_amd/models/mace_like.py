@@ -231,23 +231,27 @@ class _MaceLikeEnergy(Function):
                   gP1.data_ptr())
             gA0 = gemm(gP0, layer.Wm0, b_layout=0)
             gA1 = gemm(gP1.view(3 * n, C), layer.Wm1, b_layout=0)
-            gz = _empty(e_cap, 4 * C, device=dev)
             acc_geo = 1 if t < L - 1 else 0
             if t == 0:
-                # the first layer's inputs are the element embedding (no position dependence)
+                # the first layer's inputs are the element embedding (no position dependence): only
+                # the radial-basis block of its gather-cat row gradient is needed, formed in the
+                # kernel from W1's radial rows (gz is not stored)
+                gef = _empty(e_cap, nb, device=dev)
+                w1ef = layer.W1[2 * C:]
                 _call("fmd_mace_message_bwd_f32", z.data_ptr(), ctx.geo.data_ptr(), ei.data_ptr(), rev.data_ptr(),
                       off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(),
-                      gA1.data_ptr(), inv_avg, gz.data_ptr(), ggeo.data_ptr(), acc_geo, None, None, 0)
-                # only the radial-basis block of the gather-cat rows carries a position gradient
-                gefs.append((gemm(gz, layer.W1[2 * C:], b_layout=0), nb))
+                      gA1.data_ptr(), inv_avg, None, ggeo.data_ptr(), acc_geo, None, None, 0, w1ef.data_ptr(), nb,
+                      gef.data_ptr())
+                gefs.append((gef, nb))
                 break
+            gz = _empty(e_cap, 4 * C, device=dev)
             # this layer's inputs: residual, sender side of the messages, gather-cat rows
             g_in0 = gemm(g_out0, layer.Wsc0, b_layout=0)
             g_in1 = torch.zeros(n, 3, C, dtype=torch.float32, device=dev) if h1 is not None else None
             _call("fmd_mace_message_bwd_f32", z.data_ptr(), ctx.geo.data_ptr(), ei.data_ptr(), rev.data_ptr(),
                   off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(),
                   gA1.data_ptr(), inv_avg, gz.data_ptr(), ggeo.data_ptr(), acc_geo, g_in0.data_ptr(),
-                  _abi.ptr(g_in1), 1)
+                  _abi.ptr(g_in1), 1, None, 0, None)
             ga = gemm(gz, layer.W1, b_layout=0)  # [E, 2C + nb]
             segment_sum_csr([(ga, inputs.csr_src, 0, 1.0, None), (ga, inputs.csr_dst, C, 1.0, None)], n, C,
                             out=g_in0, accumulate=True)

@@ -184,12 +184,13 @@ int fmd_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb
  * -------------------------------------------------------------------------------------- */
 
 /* consts layout (float64): [dt, dt/2, kT, 3N*kT, 3 x (delta, delta/2, -(delta/4), -delta),
- * Q[tchain], 1/Q[tchain]] (gpu_nhc.py:113-133,273-275).
+ * Q[tchain], 1/Q[tchain]] (gpu_nhc.py:113-133,273-275). Up to 4096 atoms one workgroup runs a
+ * half step with every ke2 = sum(p^2/m) recomputed (ASE's order); beyond, see fmd_nhc_work_size.
  * pre: NHC(dt/2); p += dt/2 * F (cached forces, float64; f32_kick: the float32 product of
  * NumPy NEP 50); q += dt * p / m. Replaces _nhc_pre_force_kernel (gpu_nhc.py:359-391). */
 int fmd_nhc_pre_force(double* q, double* p, const double* f, const double* masses, double* eta,
                       double* p_eta, const double* consts, int64_t n_atoms, int32_t tchain,
-                      int32_t tloop, int32_t f32_kick, hipStream_t stream);
+                      int32_t tloop, int32_t f32_kick, double* work, hipStream_t stream);
 
 /* post: p += dt/2 * F_in; NHC(dt/2); cache F_in as float64 in f_cache; copy the energy.
  * f_in_is_f64 selects float32/float64 forces, e_kind 0: no energy, 1: float32, 2: float64.
@@ -197,7 +198,13 @@ int fmd_nhc_pre_force(double* q, double* p, const double* f, const double* masse
 int fmd_nhc_post_force(double* p, const void* f_in, int32_t f_in_is_f64, double* f_cache,
                        const double* masses, double* eta, double* p_eta, const double* consts,
                        const void* e_in, int32_t e_kind, double* e_out, int64_t n_atoms,
-                       int32_t tchain, int32_t tloop, int32_t f32_kick, hipStream_t stream);
+                       int32_t tchain, int32_t tloop, int32_t f32_kick, double* work, hipStream_t stream);
+
+/* float64 elements of the `work` buffer the NHC entry points need for n_atoms (systems of more
+ * than 4096 atoms run the multi-block path: per-block partial sums, one chain workgroup, an
+ * elementwise pass; after each momentum scaling ke2 is updated as ke2 * s^2, the reference's
+ * "scaled" update of gpu_nhc.py:520-706, instead of a fresh reduction). May be null below. */
+int64_t fmd_nhc_work_size(int64_t n_atoms);
 
 /* ----------------------------------------------------------------------------------------
  * Small deterministic reductions used around the step
@@ -228,13 +235,14 @@ int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, co
 int fmd_mace_message_f32(const float* z, const float* geo, const int32_t* edge_index, const int64_t* edge_offsets,
                          const int64_t* n_edges, int64_t e_cap, int64_t n_atoms, int32_t channels, const float* h0,
                          const float* h1, float inv_avg, float* A0, float* A1, hipStream_t stream);
-/* VJP of fmd_mace_message_f32: gz [E,4C], ggeo [E,4] (= or += ), and if gh0: the sender-side
- * gh0/gh1 (= or +=) over the reverse CSR. */
+/* VJP of fmd_mace_message_f32: gz [E,4C] (may be null when w1ef is given), ggeo [E,4] (= or +=),
+ * with w1ef ([nb, 4C], the radial rows of the edge GEMM weight) also gef[e] = gz[e] @ w1ef^T
+ * [E,nb], and if gh0: the sender-side gh0/gh1 (= or +=) over the reverse CSR. */
 int fmd_mace_message_bwd_f32(const float* z, const float* geo, const int32_t* edge_index, const int32_t* reverse,
                              const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
                              int32_t channels, const float* h0, const float* h1, const float* gA0, const float* gA1,
                              float inv_avg, float* gz, float* ggeo, int32_t accumulate_geo, float* gh0, float* gh1,
-                             int32_t accumulate_h, hipStream_t stream);
+                             int32_t accumulate_h, const float* w1ef, int32_t nb, float* gef, hipStream_t stream);
 /* Symmetric contraction (correlation 3, L <= 1) and its VJP. */
 int fmd_mace_symcon_f32(const float* P0, const float* P1, const int32_t* elem, const float* Wc, const float* Wd,
                         int64_t n_atoms, int32_t channels, float* B0, float* B1, hipStream_t stream);

@@ -164,6 +164,32 @@ def test_gemm_fp32_against_fp64(device, F, m):
 
 
 @pytest.mark.gpu
+def test_gemm_fp32_large_tiles(device):
+    """The 10k-atom edge GEMM shape (ragged M, K = 2F+8, N = 4F) takes the 128x128 tile path:
+    both B layouts, the bias/SiLU epilogue and accumulate against float64."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm
+
+    g = torch.Generator().manual_seed(5)
+    m, k, n = 66001, 264, 512
+    a = torch.randn(m, k, generator=g)
+    w = torch.randn(k, n, generator=g) / k ** 0.5
+    bias = torch.randn(n, generator=g)
+    ref = a.double() @ w.double()
+    ad, wd = a.to(device), w.to(device)
+    y = gemm(ad, wd, b_layout=1)
+    assert oops.relative(y.cpu().numpy(), ref.numpy()) < 1e-5
+    wt = w.t().contiguous().to(device)
+    ys = gemm(ad, wt, b_layout=0, bias=bias.to(device), epilogue="silu")
+    assert oops.relative(ys.cpu().numpy(), torch.nn.functional.silu(ref + bias.double()).numpy()) < 1e-5
+    c0 = torch.randn(m, n, generator=g)
+    out = c0.to(device)
+    gemm(ad, wd, b_layout=1, out=out, accumulate=True)
+    assert oops.relative(out.cpu().numpy(), (ref + c0.double()).numpy()) < 1e-5
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("F", [64, 128])
 def test_gemm_bf16_against_fp64_of_rounded_inputs(device, F):
     import torch

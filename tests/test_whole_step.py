@@ -114,7 +114,7 @@ def test_whole_step_morse_md_matches_cpu_oracle(device):
         _, wraps, wrapped = onl.wrap(q, inv, cell32)
         cand = onl.candidates(wrapped, cell32, np.float32(36.0 + 1e-3), 200)
         b = onl.build(q, inv, cell32, cand, q.astype(np.float32), wraps, np.float32(36.0), np.float32(1.0), (1, 0, 0),
-                      10 ** 6)
+                      int(cand.num_neighbors.sum()))
         e = b.n_edges
         pos = torch.tensor(b.wrapped)
         energy, f, _ = om.energy_and_forces(om.morse_node_energy, pos, torch.tensor(cell32), torch.tensor(
