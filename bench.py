@@ -8,7 +8,7 @@ model, NVT Nose-Hoover chain at 500 K (tdamp 25 fs, tchain 3, tloop 1, dt 0.25 f
 F = 128) are reported beside it, with the dominant kernel's roofline and the CPU baseline (the
 PyTorch-CPU eager oracle on this host's cores, a bounded sample of the same workload).
 
-  python bench.py [--gpus 1] [--steps 200] [--warmup 3] [--no-cpu] [--quick]
+  python bench.py [--gpus 1] [--steps 200] [--warmup 200] [--no-cpu] [--quick]
 """
 from __future__ import annotations
 
@@ -48,16 +48,25 @@ def build_md(n_atoms: int, steps_per_launch: int):
                                         steps_per_launch=steps_per_launch)
 
 
-def time_md(md, steps: int, warmup_windows: int) -> float:
-    """Seconds for exactly ``steps`` MD steps (barrier + synchronize on both sides)."""
+def time_md(md, steps: int, warmup_steps: int) -> float:
+    """Seconds for exactly ``steps`` MD steps after ``warmup_steps`` untimed ones (rounded up to
+    whole windows), synchronized on both sides (one process, one GPU: no barrier to take)."""
     import torch
 
-    md.run(warmup_windows * md.steps_per_launch)
+    spl = md.steps_per_launch
+    md.run(-(-warmup_steps // spl) * spl)
+    before = md.whole_step_stats()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     md.run(steps)
     torch.cuda.synchronize()
-    return time.perf_counter() - t0
+    elapsed = time.perf_counter() - t0
+    after = md.whole_step_stats()
+    # events inside the timed region (each is part of the measured time)
+    md.timed_events = {"capacity_growths": len(after["capacity_history"]) - len(before["capacity_history"]),
+                       "fallback_windows": after["fallback_windows"] - before["fallback_windows"],
+                       "candidate_refreshes": after["candidate_refreshes"] - before["candidate_refreshes"]}
+    return elapsed
 
 
 def time_kernel(fn, reps: int = 20) -> float:
@@ -78,32 +87,55 @@ def time_kernel(fn, reps: int = 20) -> float:
 
 def gemm_roofline(md) -> dict:
     """The dominant kernel of the 10 000-atom step, the fp32 MFMA edge GEMM z = a @ W1
-    ([e_cap, 2C+8] x [2C+8, 4C]), timed live; algorithmic flops = 2 M K N per launch."""
+    ([e_cap, 2C+8] x [2C+8, 4C], W1 stored K-contiguous: gemm_f32_nt_kernel), timed live on the
+    stream it is launched on; algorithmic flops = 2 M K N per launch."""
     import torch
 
     from fastmd_amd.ops.wide_gemm import gemm
 
-    layer = md.adapter.module.layers[0]
+    w = md.adapter.module.w1_t(0)  # [4C, 2C+8]
     m = md.whole_step_runner.builder.e_capacity
-    k, n = layer.W1.shape
+    n, k = w.shape
     a = torch.randn(m, k, device=md.device)
     out = torch.empty(m, n, device=md.device)
-    t = time_kernel(lambda: gemm(a, layer.W1, b_layout=1, out=out))
+    t = time_kernel(lambda: gemm(a, w, b_layout=0, out=out), reps=50)
     flops = 2.0 * m * k * n
     achieved = flops / t / 1e12
     return {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None, "kernel": "gemm_f32_kernel<1>",
-            "launch_ms": round(t * 1e3, 4), "flops_per_launch": flops, "shape": [m, k, n]}
+            "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": _traffic("gemm_f32_nt_kernel", [m, k, n]),
+            "kernel": "gemm_f32_nt_kernel", "launch_us": round(t * 1e6, 2), "flops_per_launch": flops,
+            "algorithmic_bytes_per_launch": 4 * (m * k + n * k + m * n), "shape_mkn": [m, k, n]}
 
 
-def segment_sum_bench(n_atoms: int = 40000, F: int = 128) -> dict:
-    """configs[1] segment sum [E, F] -> [N, F] over the sorted (identity) CSR of the 40 000-atom
-    perovskite at rc = 6 A; algorithmic bytes E F 4 + N F 4 + (N + 1) 8."""
+def _traffic(kernel: str, shape: list):
+    """HBM bytes per launch of ``kernel`` at ``shape`` from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or None if none matches."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            table = json.load(f)
+    except (OSError, ValueError):
+        return None
+    row = table.get(kernel)
+    if not row or row.get("shape", [None])[1:] != shape[1:]:
+        return None
+    # the measured shape's HBM bytes, scaled to this launch's M (the A read and C write are per row)
+    return int(row["bytes_per_launch"] * shape[0] / row["shape"][0])
+
+
+def hbm_ops_bench(n_atoms: int = 40000, F: int = 128) -> dict:
+    """configs[1] memory-bound operators on the 40 000-atom perovskite at rc = 6 A (sorted edge
+    list, 15.2 edges/atom), F = 128, fp32, each timed live with HIP events. Algorithmic bytes:
+      segment_sum [E,F] -> [N,F]:          E F 4 + N F 4 + (N + 1) 8
+      segment_sum transpose [N,F] -> [E,F]: 2 E F 4 + E 4   (gout row per edge + gvalue + perm)
+      gather_cat [E, 2F + 8]:               E (16 F + 72)    (two F rows + 8 basis + 2 indices in,
+                                                              the 2F + 8 row out)"""
     import torch
 
     from fastmd_amd import systems
     from fastmd_amd.graph.gpu_graph_builder import TensorGraphBuilder
-    from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr
+    from fastmd_amd.models.mace_like import _gather_edge_rows
+    from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr, segment_sum_t
 
     device = torch.device("cuda", 0)
     s = systems.perovskite_atoms(n_atoms)
@@ -112,14 +144,24 @@ def segment_sum_bench(n_atoms: int = 40000, F: int = 128) -> dict:
     e = int(g.n_edges.item())
     gen = torch.Generator(device="cpu").manual_seed(0)
     v = torch.randn(e, F, generator=gen).to(device)
+    x = torch.randn(n_atoms, F, generator=gen).to(device)
+    rbf = torch.randn(e, 8, generator=gen).to(device)
     out = torch.empty(n_atoms, F, device=device)
+    rows = torch.empty(e, 2 * F + 8, device=device)
     csr = Csr(g.edge_offsets)
-    t = time_kernel(lambda: segment_sum_csr([(v, csr, 0, 1.0, None)], n_atoms, F, out=out), reps=50)
-    nbytes = e * F * 4 + n_atoms * F * 4 + (n_atoms + 1) * 8
-    gbps = nbytes / t / 1e9
-    return {"segment_sum_GBps": round(gbps, 1), "segment_sum_frac_of_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4),
-            "segment_sum_us": round(t * 1e6, 2), "segment_sum_edges": e, "segment_sum_F": F,
-            "segment_sum_atoms": n_atoms}
+    ei = g.edge_index[:e]
+    res = {"atoms": n_atoms, "edges": e, "F": F}
+
+    def put(name, t, nbytes):
+        gbps = nbytes / t / 1e9
+        res[name] = {"us": round(t * 1e6, 2), "GBps": round(gbps, 1), "frac_of_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4),
+                     "algorithmic_bytes": nbytes}
+
+    put("segment_sum", time_kernel(lambda: segment_sum_csr([(v, csr, 0, 1.0, None)], n_atoms, F, out=out), reps=50),
+        e * F * 4 + n_atoms * F * 4 + (n_atoms + 1) * 8)
+    put("segment_sum_transpose", time_kernel(lambda: segment_sum_t(x, csr, e), reps=50), 2 * e * F * 4 + e * 4)
+    put("gather_cat", time_kernel(lambda: _gather_edge_rows(x, rbf, ei, rows), reps=50), e * (16 * F + 72))
+    return res
 
 
 def cpu_baseline(n_atoms: int, budget_s: float) -> dict:
@@ -183,11 +225,14 @@ def main() -> int:
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=200)
-    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--warmup", type=int, default=200,
+                        help="untimed MD steps before timing (thermalisation: the edge count settles)")
     parser.add_argument("--steps-small", type=int, default=2000)
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--quick", action="store_true", help="short run (profiling): no CPU baseline, fewer steps")
+    parser.add_argument("--roofline-only", action="store_true",
+                        help="only the dominant kernel at the 10 000-atom shape plus a 256 MiB copy (--pmc runs)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs the MD step on one MI355X; --gpus {args.gpus} is not supported "
@@ -202,6 +247,18 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     steps_small = 200 if args.quick else args.steps_small
+    if args.roofline_only:
+        # the run profiled with rocprofv3 --pmc for the GEMM's HBM traffic: the dominant kernel at
+        # the 10 000-atom shape, then a plain 256 MiB device copy (the counters' calibration)
+        md = build_md(10000, STEPS_PER_LAUNCH)
+        roof = gemm_roofline(md)
+        src = torch.empty(64 << 20, device=md.device)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"roofline": roof, "copy_bytes": src.numel() * 4}), flush=True)
+        return 0
 
     log("10 000 atoms: capture")
     md = build_md(10000, STEPS_PER_LAUNCH)
@@ -209,7 +266,8 @@ def main() -> int:
     t_big = time_md(md, args.steps, args.warmup)
     ms_big = t_big / args.steps * 1e3
     stats_big = md.whole_step_stats()
-    log(f"10 000 atoms: {ms_big:.3f} ms/step")
+    events_big = md.timed_events
+    log(f"10 000 atoms: {ms_big:.3f} ms/step {events_big}")
     roof = gemm_roofline(md)
     del md
     torch.cuda.empty_cache()
@@ -219,12 +277,13 @@ def main() -> int:
     t_small = time_md(md, steps_small, args.warmup)
     ms_small = t_small / steps_small * 1e3
     stats_small = md.whole_step_stats()
-    log(f"135 atoms: {ms_small:.4f} ms/step")
+    events_small = md.timed_events
+    log(f"135 atoms: {ms_small:.4f} ms/step {events_small}")
     del md
     torch.cuda.empty_cache()
 
-    log("segment sum microbenchmark")
-    seg = segment_sum_bench()
+    log("memory-bound operator microbenchmarks")
+    seg = hbm_ops_bench()
     cpu = None
     if not (args.no_cpu or args.quick):
         log("CPU baseline (oracle)")
@@ -254,10 +313,12 @@ def main() -> int:
         "md_steps_per_s": round(1e3 / ms_big, 2),
         "small_system": {"atoms": 135, "ms_per_step": round(ms_small, 5), "md_steps_per_s": round(1e3 / ms_small, 1),
                          "atom_steps_per_s": round(135 / (ms_small / 1e3), 1), "steps": steps_small,
-                         "e_capacity": stats_small["e_capacity"]},
-        "segment_sum": seg,
-        "whole_step_stats_10k": {k: stats_big[k] for k in ("candidate_refreshes", "fallback_windows",
-                                                           "max_edge_count", "capacity_history")},
+                         "e_capacity": stats_small["e_capacity"], "timed_events": events_small},
+        "segment_sum_GBps": seg["segment_sum"]["GBps"],
+        "hbm_ops_40k": seg,
+        "whole_step_stats_10k": {**{k: stats_big[k] for k in ("candidate_refreshes", "fallback_windows",
+                                                              "max_edge_count", "capacity_history")},
+                                 "timed_events": events_big},
     }
     print(json.dumps(line), flush=True)
     return 0

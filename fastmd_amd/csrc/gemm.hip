@@ -173,6 +173,144 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restr
   epilogue<WM, WN>(acc, row_blk + wm * (BM / 2), col_blk + wn * (BN / 2), m, n, bias, c, ldc, accumulate, act);
 }
 
+// ------------------------------------------------------------------------- fp32, both K-major
+// The edge GEMMs of the MD step (z = a W1 with W1 stored transposed, and its VJP gz W1^T) have
+// both operands K-contiguous ("NT": A [M,K], B [N,K]). This kernel is built for that case (each
+// choice below was timed against the alternatives at the 10 000-atom shapes):
+//  * LDS rows hold one operand row each in natural k order (pitch 36 floats: 16-byte aligned
+//    float4 stores, conflict-free b128 reads). The 32 k of a slice are fed to the 16 MFMAs as
+//    k = 16 h + 4 q + p at step (q, p) (h = lane / 32), so the values a lane needs are contiguous:
+//    4 ds_read_b128 per operand block instead of 16 ds_read_b32 (the MFMA sums its two k slots,
+//    so any bijection (q, p, h) -> k shared by A and B gives the same product).
+//  * one LDS buffer (36 KB) and one register stage: the next slice's float4 loads are in flight
+//    during the current slice's 64 MFMAs per wave, and three workgroups fit on a CU (12 waves).
+//    Interior slices use unconditional loads (rows past M/N are clamped to the last row: computed,
+//    never stored); a partial last slice is masked on a workgroup-uniform branch, and only its
+//    first ceil(kv / 4) step groups are issued (K = 2F + 8 leaves kv = 8: 2 of 4).
+//  * tiles are assigned XCD-aware: workgroups are dispatched round-robin over the 8 XCDs, and
+//    the linear id is remapped so that each XCD walks a contiguous run of tiles (N fastest), so
+//    the N tiles sharing one A tile run on the same XCD and read it from its L2.
+//  * interior wave tiles without bias/accumulate/activation store straight from the
+//    accumulators with incremental row pointers; the general epilogue handles the rest.
+constexpr int NT_PITCH = 36;
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int64_t xcd_tile(int64_t w, int64_t g) {
+  const int64_t xcd = w % kXcds, slot = w / kXcds, q = g / kXcds, r = g % kXcds;
+  return xcd * q + (xcd < r ? xcd : r) + slot;
+}
+
+constexpr int NT_V = 128 * BK32 / 4 / kThreads;  // float4 per thread per operand and slice (4)
+
+__global__ void __launch_bounds__(kThreads) gemm_f32_nt_kernel(const float* __restrict__ a, int64_t lda,
+                                                               const float* __restrict__ b, int64_t ldb,
+                                                               const float* __restrict__ bias, float* c, int64_t ldc,
+                                                               int64_t m, int64_t n, int64_t k, int accumulate,
+                                                               int act, int vec_ok, int64_t n_tiles) {
+  constexpr int TM = 128, TN = 128;
+  __shared__ float As[TM][NT_PITCH];
+  __shared__ float Bs[TN][NT_PITCH];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t row_blk = (tile / n_tiles) * TM, col_blk = (tile % n_tiles) * TN;
+
+  // thread -> (row, 4 consecutive k) of a 128 x 32 slice: 8 lanes cover one row's 128 bytes
+  const int kc = (t & 7) * 4;
+  int64_t arow[NT_V], brow[NT_V];
+#pragma unroll
+  for (int q = 0; q < NT_V; ++q) {
+    const int r = (t + q * kThreads) >> 3;
+    arow[q] = min(row_blk + r, m - 1) * lda + kc;
+    brow[q] = min(col_blk + r, n - 1) * ldb + kc;
+  }
+  float4 ra[NT_V], rb[NT_V];
+  auto load = [&](int64_t k0) {
+    if (vec_ok && k0 + BK32 <= k) {
+#pragma unroll
+      for (int q = 0; q < NT_V; ++q) {
+        ra[q] = *reinterpret_cast<const float4*>(a + arow[q] + k0);
+        rb[q] = *reinterpret_cast<const float4*>(b + brow[q] + k0);
+      }
+    } else {
+      const int64_t g = k0 + kc;
+#pragma unroll
+      for (int q = 0; q < NT_V; ++q) {
+        const float* pa = a + arow[q] + k0;
+        const float* pb = b + brow[q] + k0;
+        ra[q] = make_float4(g < k ? pa[0] : 0.f, g + 1 < k ? pa[1] : 0.f, g + 2 < k ? pa[2] : 0.f,
+                            g + 3 < k ? pa[3] : 0.f);
+        rb[q] = make_float4(g < k ? pb[0] : 0.f, g + 1 < k ? pb[1] : 0.f, g + 2 < k ? pb[2] : 0.f,
+                            g + 3 < k ? pb[3] : 0.f);
+      }
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int q = 0; q < NT_V; ++q) {
+      const int r = (t + q * kThreads) >> 3;
+      *reinterpret_cast<float4*>(&As[r][kc]) = ra[q];
+      *reinterpret_cast<float4*>(&Bs[r][kc]) = rb[q];
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  auto compute = [&](int nq) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (q >= nq) break;
+      float4 av[2], bv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        av[i] = *reinterpret_cast<const float4*>(&As[wm * 64 + i * 32 + (lane & 31)][h * 16 + q * 4]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bv[j] = *reinterpret_cast<const float4*>(&Bs[wn * 64 + j * 32 + (lane & 31)][h * 16 + q * 4]);
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][p], bv[j][p], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  const int64_t nk = fmd_cdiv(k, BK32);
+  const int kv_last = (int)(k - (nk - 1) * BK32);  // real k in the last slice (1..32)
+  // the last slice's real k sit at slots 0..kv-1, all with h = 0 when kv <= 16
+  const int nq_last = kv_last <= 16 ? (kv_last + 3) / 4 : 4;
+  load(0);
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    if (kt) __syncthreads();  // every wave is done reading the previous slice
+    store();
+    __syncthreads();
+    if (kt + 1 < nk) load((kt + 1) * BK32);
+    compute(kt + 1 < nk ? 4 : nq_last);
+  }
+  const int64_t row0 = row_blk + wm * 64, col0 = col_blk + wn * 64;
+  if (!bias && !accumulate && act == 0 && row0 + 64 <= m && col0 + 64 <= n) {
+    float* base = c + (row0 + h * 4) * ldc + col0 + (lane & 31);
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        float* rp = base + (int64_t)(bi * 32 + (v / 4) * 8 + (v % 4)) * ldc;
+        rp[0] = acc[bi][0][v];
+        rp[32] = acc[bi][1][v];
+      }
+    return;
+  }
+  epilogue<2, 2>(acc, row0, col0, m, n, bias, c, ldc, accumulate, act);
+}
+
 // ---------------------------------------------------------------------------------------- bf16
 constexpr int BK16 = 32;
 constexpr int LDK16 = BK16 + 8;  // bf16 elements per LDS row (+pad, keeps 16-byte alignment)
@@ -315,7 +453,13 @@ int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32
   FMD_REQUIRE(k == 0 || (a && b && lda >= k && ldb >= (b_layout == 0 ? k : n)));
   FMD_REQUIRE(fmd_cdiv(m, 64) < (int64_t(1) << 31) && fmd_cdiv(n, 64) < 65536);
   const int64_t big_tiles = fmd_cdiv(m, 128) * fmd_cdiv(n, 128);
-  if (big_tiles >= 512)
+  if (big_tiles >= 512 && b_layout == 0) {
+    FMD_REQUIRE(big_tiles < (int64_t(1) << 31));
+    const int vec_ok = (lda % 4 == 0) && (ldb % 4 == 0) && ((reinterpret_cast<uintptr_t>(a) & 15) == 0) &&
+                       ((reinterpret_cast<uintptr_t>(b) & 15) == 0);
+    hipLaunchKernelGGL(gemm_f32_nt_kernel, dim3((unsigned)big_tiles), dim3(kThreads), 0, stream, a, lda, b, ldb, bias,
+                       c, ldc, m, n, k, accumulate, epilogue_kind, vec_ok, fmd_cdiv(n, 128));
+  } else if (big_tiles >= 512)
     launch_gemm_f32<128, 128>(a, lda, b, ldb, b_layout, bias, c, ldc, m, n, k, accumulate, epilogue_kind, stream);
   else
     launch_gemm_f32<64, 64>(a, lda, b, ldb, b_layout, bias, c, ldc, m, n, k, accumulate, epilogue_kind, stream);

@@ -267,14 +267,22 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
         for (int q = 0; q < CPL; ++q) gze[b * C + q] = gzl[b][q];
     }
     if (w1ef) {
-      for (int nn = 0; nn < nb; ++nn) {
-        float acc = 0.f;
+      for (int n0 = 0; n0 < nb; n0 += 8) {
+        float acc[8];
 #pragma unroll
-        for (int b = 0; b < (H1 ? 4 : 2); ++b)
+        for (int t = 0; t < 8; ++t) {
+          acc[t] = 0.f;
+          if (n0 + t < nb) {
+            const float* w = s_w + (n0 + t) * 4 * C + c0;
 #pragma unroll
-          for (int q = 0; q < CPL; ++q) acc += gzl[b][q] * s_w[nn * 4 * C + b * C + c0 + q];
-        acc = wave_sum(acc);
-        if (lane == 0) gef[e * nb + nn] = acc;
+            for (int b = 0; b < (H1 ? 4 : 2); ++b)
+#pragma unroll
+              for (int q = 0; q < CPL; ++q) acc[t] += gzl[b][q] * w[b * C + q];
+          }
+        }
+        const float tot = wave_sum8(acc);
+        const int t = wave_sum8_index(lane);
+        if ((lane & 7) == 0 && n0 + t < nb) gef[e * nb + n0 + t] = tot;
       }
     }
     sf = wave_sum(sf);
@@ -301,6 +309,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
 // VJP, sender side (one wave per node j, over the reverse rows e = reverse[e'] of its rows e'
 // as a centre; the receiver of e is i = neighbor[e']):
 //   g_h0_j += gA0_i wa_e + wb_e (gA1_i . u_e);  g_h1_j,x += gA0_i wc_e u_e,x + gA1_i,x wd_e
+// accumulate: bit 0 adds into gh0, bit 1 into gh1 (else they are overwritten).
 template <int CPL, bool H1>
 __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
     const float* z, const float* geo, const int32_t* edge_index, const int32_t* reverse, const int64_t* off,
@@ -347,12 +356,12 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
   for (int q = 0; q < CPL; ++q) {
     float* d0 = gh0 + jn * C + c0 + q;
     const float v0 = a0[q] * inv_avg;
-    *d0 = accumulate ? *d0 + v0 : v0;
+    *d0 = (accumulate & 1) ? *d0 + v0 : v0;
     if (H1 && gh1) {
       for (int x = 0; x < 3; ++x) {
         float* d1 = gh1 + (jn * 3 + x) * C + c0 + q;
         const float v1 = a1[x][q] * inv_avg;
-        *d1 = accumulate ? *d1 + v1 : v1;
+        *d1 = (accumulate & 2) ? *d1 + v1 : v1;
       }
     }
   }
@@ -446,7 +455,7 @@ __global__ void energy_bwd_kernel(const float* gE, const float* wr1, const float
   if (k >= total) return;
   const int64_t i = k / (C + H);
   const int c = (int)(k - i * (C + H));
-  const float g = scale * gE[i];
+  const float g = gE ? scale * gE[i] : scale;  // null gE: dE/dE_i = 1 for every row
   if (c < C) {
     gha[i * C + c] = g * wr1[c];
   } else {
@@ -669,7 +678,7 @@ int fmd_mace_energy_f32(const float* ha, const float* wr1, const float* y, const
 
 int fmd_mace_energy_bwd_f32(const float* gE, const float* wr1, const float* y, const float* wr2b, int32_t channels,
                             int32_t hidden, float scale, int64_t n_atoms, float* gha, float* gy, hipStream_t stream) {
-  FMD_REQUIRE(gE && wr1 && y && wr2b && gha && gy && n_atoms >= 0);
+  FMD_REQUIRE(wr1 && y && wr2b && gha && gy && n_atoms >= 0);
   if (n_atoms == 0) return FMD_OK;
   const int64_t total = n_atoms * (channels + hidden);
   hipLaunchKernelGGL(energy_bwd_kernel, dim3((unsigned)fmd_cdiv(total, 256)), dim3(256), 0, stream, gE, wr1, y, wr2b,

@@ -38,6 +38,15 @@ def sum_f64(x: Tensor) -> Tensor:
     return _SumF64.apply(x)
 
 
+def sum_f64_into(x: Tensor) -> Tensor:
+    """sum(x) in float64 in the same fixed order as ``sum_f64``, as a [1] tensor, no autograd."""
+    x = x.detach().contiguous()
+    out = torch.empty(1, dtype=torch.float64, device=x.device)
+    _abi.call("fmd_sum_f64", x.data_ptr(), 1 if x.dtype == torch.float64 else 0, x.numel(), out.data_ptr(),
+              _abi.stream_handle())
+    return out
+
+
 def engine_derivative(adapter) -> "EnergyDerivative | None":
     """The derivative the runtime runs for ``adapter`` (energy_derivative.py:51-60)."""
     if hasattr(adapter, "node_energy"):
@@ -71,6 +80,12 @@ class EnergyDerivative:
     def __call__(self, batch: GraphBatch, inputs, *, task: str = "ef", n_real: int | None = None) -> dict:
         if "s" in task:
             raise NotImplementedError("stress is not supported by this build's models")
+        explicit = getattr(self.adapter, "energy_and_forces", None)
+        if explicit is not None and (n_real is None or n_real == batch.positions.shape[0]):
+            # the adapter's explicit VJP: the same kernels as the autograd path below without the
+            # autograd seed / cast / negation launches (one graph node each per step)
+            energy, forces = explicit(inputs, batch.positions, batch.cell)
+            return {"e": energy, "f": [forces]}
         with torch.enable_grad():
             leaf = batch.positions.detach().requires_grad_(True)
             energies = self.adapter.node_energy(inputs, leaf, batch.cell)

@@ -101,6 +101,18 @@ class MaceLike(nn.Module):
     def r_max(self) -> float:
         return self.config.cutoff
 
+    def w1_t(self, t: int) -> Tensor:
+        """W1 of layer t stored K-contiguous ([4C, 2C + 8]) for the edge GEMM, which is fastest with
+        both operands K-contiguous; rebuilt when W1 is changed in place (version counter)."""
+        w = self.layers[t].W1
+        key = (w.data_ptr(), w._version, w.device)
+        cache = self.__dict__.setdefault("_w1t_cache", {})
+        hit = cache.get(t)
+        if hit is None or hit[0] != key:
+            hit = (key, w.detach().t().contiguous())
+            cache[t] = hit
+        return hit[1]
+
     @property
     def num_interactions(self) -> int:
         return self.config.num_interactions
@@ -169,7 +181,7 @@ class _MaceLikeEnergy(Function):
         for t, layer in enumerate(model.layers):
             last = t == L - 1
             _gather_edge_rows(h0, ef, ei, a)
-            z = gemm(a, layer.W1, b_layout=1)  # [E, 4C]
+            z = gemm(a, model.w1_t(t), b_layout=0)  # [E, 4C] = a @ W1
             A0 = _empty(n, C, device=dev)
             A1 = _empty(n, 3, C, device=dev)
             _call("fmd_mace_message_f32", z.data_ptr(), geo.data_ptr(), ei.data_ptr(), off.data_ptr(),
@@ -198,72 +210,83 @@ class _MaceLikeEnergy(Function):
 
     @staticmethod
     def backward(ctx, gE):
-        model, inputs = ctx.model, ctx.inputs
-        cfg = model.config
-        batch = inputs.batch
-        C, nb, H = cfg.channels, cfg.n_basis, cfg.readout_hidden
-        n, e_cap = ctx.n, ctx.e_cap
-        dev = gE.device
         gE = gE.detach().to(torch.float32).contiguous()
-        inv_avg = 1.0 / cfg.avg_num_neighbors
-        n_edges, off, ei, rev = batch.n_edges, batch.edge_offsets, batch.edge_index, batch.edge_reverse
-        # readouts: gha = dE/d(first layer's h0 out), gy -> dE/d(last layer's h0 out)
-        gy = _empty(n, H, device=dev)
-        gha = _empty(n, C, device=dev)
-        _call("fmd_mace_energy_bwd_f32", gE.data_ptr(), model.wr1.data_ptr(), ctx.y.data_ptr(), model.wr2b.data_ptr(),
-              C, H, float(cfg.scale), n, gha.data_ptr(), gy.data_ptr())
-        g_out0 = gemm(gy, model.Wr2a, b_layout=0)  # dE/dh0 out of the last layer
-        g_out1 = None  # dE/dh1 out of the current layer (the last layer's h1 out is unused)
-        ggeo = _empty(e_cap, 4, device=dev)
-        gefs = []
-        L = len(model.layers)
-        for t in reversed(range(L)):
-            layer = model.layers[t]
-            h0, h1, z, P0, P1 = ctx.saved[t]
-            if t == 0:
-                g_out0 = g_out0 + gha
-            gB0 = gemm(g_out0, layer.Wo0, b_layout=0)
-            gB1 = None if g_out1 is None else gemm(g_out1.reshape(3 * n, C), layer.Wo1, b_layout=0)
-            gP0 = _empty(n, C, device=dev)
-            gP1 = _empty(n, 3, C, device=dev)
-            _call("fmd_mace_symcon_bwd_f32", P0.data_ptr(), P1.data_ptr(), inputs.elem.data_ptr(),
-                  layer.Wc.data_ptr(), layer.Wd.data_ptr(), gB0.data_ptr(), _abi.ptr(gB1), n, C, gP0.data_ptr(),
-                  gP1.data_ptr())
-            gA0 = gemm(gP0, layer.Wm0, b_layout=0)
-            gA1 = gemm(gP1.view(3 * n, C), layer.Wm1, b_layout=0)
-            acc_geo = 1 if t < L - 1 else 0
-            if t == 0:
-                # the first layer's inputs are the element embedding (no position dependence): only
-                # the radial-basis block of its gather-cat row gradient is needed, formed in the
-                # kernel from W1's radial rows (gz is not stored)
-                gef = _empty(e_cap, nb, device=dev)
-                w1ef = layer.W1[2 * C:]
-                _call("fmd_mace_message_bwd_f32", z.data_ptr(), ctx.geo.data_ptr(), ei.data_ptr(), rev.data_ptr(),
-                      off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(),
-                      gA1.data_ptr(), inv_avg, None, ggeo.data_ptr(), acc_geo, None, None, 0, w1ef.data_ptr(), nb,
-                      gef.data_ptr())
-                gefs.append((gef, nb))
-                break
-            gz = _empty(e_cap, 4 * C, device=dev)
-            # this layer's inputs: residual, sender side of the messages, gather-cat rows
-            g_in0 = gemm(g_out0, layer.Wsc0, b_layout=0)
-            g_in1 = torch.zeros(n, 3, C, dtype=torch.float32, device=dev) if h1 is not None else None
+        return _vjp(ctx, gE, 1.0), None, None, None
+
+
+class _Saved:
+    """What the forward keeps for the VJP (the autograd ctx, or this holder outside autograd)."""
+
+
+def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
+    """``sign * dE/dpos`` [rows, 3] with E = sum_i gE_i E_i (gE None: all ones), by the VJP kernels."""
+    model, inputs = ctx.model, ctx.inputs
+    cfg = model.config
+    batch = inputs.batch
+    C, nb, H = cfg.channels, cfg.n_basis, cfg.readout_hidden
+    n, e_cap = ctx.n, ctx.e_cap
+    dev = ctx.geo.device
+    inv_avg = 1.0 / cfg.avg_num_neighbors
+    n_edges, off, ei, rev = batch.n_edges, batch.edge_offsets, batch.edge_index, batch.edge_reverse
+    # readouts: gha = dE/d(first layer's h0 out), gy -> dE/d(last layer's h0 out)
+    gy = _empty(n, H, device=dev)
+    gha = _empty(n, C, device=dev)
+    _call("fmd_mace_energy_bwd_f32", _abi.ptr(gE), model.wr1.data_ptr(), ctx.y.data_ptr(), model.wr2b.data_ptr(),
+          C, H, float(cfg.scale), n, gha.data_ptr(), gy.data_ptr())
+    # dE/dh0 out of the last layer (with one layer, the first readout's gradient joins here)
+    L = len(model.layers)
+    g_out0 = gemm(gy, model.Wr2a, b_layout=0, out=gha if L == 1 else None, accumulate=L == 1)
+    g_out1 = None  # dE/dh1 out of the current layer (the last layer's h1 out is unused)
+    ggeo = _empty(e_cap, 4, device=dev)
+    gefs = []
+    for t in reversed(range(L)):
+        layer = model.layers[t]
+        h0, h1, z, P0, P1 = ctx.saved[t]
+        gB0 = gemm(g_out0, layer.Wo0, b_layout=0)
+        gB1 = None if g_out1 is None else gemm(g_out1.reshape(3 * n, C), layer.Wo1, b_layout=0)
+        gP0 = _empty(n, C, device=dev)
+        gP1 = _empty(n, 3, C, device=dev)
+        _call("fmd_mace_symcon_bwd_f32", P0.data_ptr(), P1.data_ptr(), inputs.elem.data_ptr(),
+              layer.Wc.data_ptr(), layer.Wd.data_ptr(), gB0.data_ptr(), _abi.ptr(gB1), n, C, gP0.data_ptr(),
+              gP1.data_ptr())
+        gA0 = gemm(gP0, layer.Wm0, b_layout=0)
+        gA1 = gemm(gP1.view(3 * n, C), layer.Wm1, b_layout=0)
+        acc_geo = 1 if t < L - 1 else 0
+        if t == 0:
+            # the first layer's inputs are the element embedding (no position dependence): only
+            # the radial-basis block of its gather-cat row gradient is needed, formed in the
+            # kernel from W1's radial rows (gz is not stored)
+            gef = _empty(e_cap, nb, device=dev)
+            w1ef = layer.W1[2 * C:]
             _call("fmd_mace_message_bwd_f32", z.data_ptr(), ctx.geo.data_ptr(), ei.data_ptr(), rev.data_ptr(),
                   off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(),
-                  gA1.data_ptr(), inv_avg, gz.data_ptr(), ggeo.data_ptr(), acc_geo, g_in0.data_ptr(),
-                  _abi.ptr(g_in1), 1, None, 0, None)
-            ga = gemm(gz, layer.W1, b_layout=0)  # [E, 2C + nb]
-            segment_sum_csr([(ga, inputs.csr_src, 0, 1.0, None), (ga, inputs.csr_dst, C, 1.0, None)], n, C,
-                            out=g_in0, accumulate=True)
-            gefs.append((ga[:, 2 * C:], 2 * C + nb))
-            g_out0, g_out1 = g_in0, g_in1
-        gvec = _empty(e_cap, 3, device=dev)
-        (g0, ld0) = gefs[0]
-        (g1, ld1) = gefs[1] if len(gefs) > 1 else (None, 0)
-        _call("fmd_edge_geometry_bwd_f32", ctx.geo.data_ptr(), ctx.de.data_ptr(), nb, g0.data_ptr(), ld0,
-              _abi.ptr(g1), ld1, ggeo.data_ptr(), n_edges.data_ptr(), e_cap, gvec.data_ptr())
-        gpos = segment_sum_csr([(gvec, inputs.csr_src, 0, 1.0, None), (gvec, inputs.csr_dst, 0, -1.0, None)], n, 3)
-        return gpos, None, None, None
+                  gA1.data_ptr(), inv_avg, None, ggeo.data_ptr(), acc_geo, None, None, 0, w1ef.data_ptr(), nb,
+                  gef.data_ptr())
+            gefs.append((gef, nb))
+            break
+        gz = _empty(e_cap, 4 * C, device=dev)
+        gef = _empty(e_cap, nb, device=dev)
+        # this layer's inputs: residual (plus, in the second layer, the first readout's
+        # gradient of the first layer's output), sender side of the messages, gather-cat rows
+        g_in0 = gemm(g_out0, layer.Wsc0, b_layout=0, out=gha if t == 1 else None, accumulate=t == 1)
+        g_in1 = _empty(n, 3, C, device=dev) if h1 is not None else None
+        w1ef = layer.W1[2 * C:]
+        _call("fmd_mace_message_bwd_f32", z.data_ptr(), ctx.geo.data_ptr(), ei.data_ptr(), rev.data_ptr(),
+              off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(),
+              gA1.data_ptr(), inv_avg, gz.data_ptr(), ggeo.data_ptr(), acc_geo, g_in0.data_ptr(),
+              _abi.ptr(g_in1), 1, w1ef.data_ptr(), nb, gef.data_ptr())
+        # the node blocks of the gather-cat row gradient (the radial block is gef)
+        ga = gemm(gz, layer.W1[:2 * C], b_layout=0)  # [E, 2C]
+        segment_sum_csr([(ga, inputs.csr_src, 0, 1.0, None), (ga, inputs.csr_dst, C, 1.0, None)], n, C,
+                        out=g_in0, accumulate=True)
+        gefs.append((gef, nb))
+        g_out0, g_out1 = g_in0, g_in1
+    gvec = _empty(e_cap, 3, device=dev)
+    (g0, ld0) = gefs[0]
+    (g1, ld1) = gefs[1] if len(gefs) > 1 else (None, 0)
+    _call("fmd_edge_geometry_bwd_f32", ctx.geo.data_ptr(), ctx.de.data_ptr(), nb, g0.data_ptr(), ld0,
+          _abi.ptr(g1), ld1, ggeo.data_ptr(), n_edges.data_ptr(), e_cap, gvec.data_ptr())
+    return segment_sum_csr([(gvec, inputs.csr_src, 0, sign, None), (gvec, inputs.csr_dst, 0, -sign, None)], n, 3)
 
 
 class MaceLikeAdapter:
@@ -322,3 +345,14 @@ class MaceLikeAdapter:
         if cell.requires_grad:
             raise NotImplementedError("stress (a strained cell) is not supported by the MACE-like kernels")
         return _MaceLikeEnergy.apply(positions, cell, self.module, inputs)
+
+    def energy_and_forces(self, inputs: MaceLikeInput, positions: Tensor, cell: Tensor) -> tuple[Tensor, Tensor]:
+        """(E [1] float64 = the fixed-order sum of the node energies, F = -dE/dpos [rows, 3]) without
+        autograd: the same forward and VJP kernels as ``node_energy`` + ``torch.autograd.grad``, minus
+        the autograd seed, cast and negation kernels."""
+        from fastmd_amd.engine.energy_derivative import sum_f64_into
+
+        saved = _Saved()
+        energies = _MaceLikeEnergy.forward(saved, positions.detach(), cell.detach(), self.module, inputs)
+        energy = sum_f64_into(energies)
+        return energy, _vjp(saved, None, -1.0)

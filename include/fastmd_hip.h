@@ -237,7 +237,8 @@ int fmd_mace_message_f32(const float* z, const float* geo, const int32_t* edge_i
                          const float* h1, float inv_avg, float* A0, float* A1, hipStream_t stream);
 /* VJP of fmd_mace_message_f32: gz [E,4C] (may be null when w1ef is given), ggeo [E,4] (= or +=),
  * with w1ef ([nb, 4C], the radial rows of the edge GEMM weight) also gef[e] = gz[e] @ w1ef^T
- * [E,nb], and if gh0: the sender-side gh0/gh1 (= or +=) over the reverse CSR. */
+ * [E,nb], and if gh0: the sender-side gh0/gh1 over the reverse CSR (accumulate_h bit 0: gh0 +=,
+ * bit 1: gh1 +=; otherwise =). */
 int fmd_mace_message_bwd_f32(const float* z, const float* geo, const int32_t* edge_index, const int32_t* reverse,
                              const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
                              int32_t channels, const float* h0, const float* h1, const float* gA0, const float* gA1,
@@ -249,7 +250,8 @@ int fmd_mace_symcon_f32(const float* P0, const float* P1, const int32_t* elem, c
 int fmd_mace_symcon_bwd_f32(const float* P0, const float* P1, const int32_t* elem, const float* Wc, const float* Wd,
                             const float* gB0, const float* gB1, int64_t n_atoms, int32_t channels, float* gP0,
                             float* gP1, hipStream_t stream);
-/* Node energies E_i = E0[elem] + scale (ha . wr1 + sum_k silu(y_k) wr2b_k) + shift, and the VJP. */
+/* Node energies E_i = E0[elem] + scale (ha . wr1 + sum_k silu(y_k) wr2b_k) + shift, and the VJP
+ * (gE null: dE/dE_i = 1 for every row). */
 int fmd_mace_energy_f32(const float* ha, const float* wr1, const float* y, const float* wr2b, int32_t channels,
                         int32_t hidden, const int32_t* elem, const float* e0, float scale, float shift,
                         int64_t n_atoms, float* energy, hipStream_t stream);

@@ -134,6 +134,16 @@ def test_mace_like_gpu_matches_oracle(device, n_cells, channels):
     assert float((f_gpu - f_ref).abs().max()) < 1e-4
     assert float(f_ref.abs().max()) > 1e-2
     assert float((f_gpu - f_ref).abs().max()) / float(f_ref.abs().max()) < 1e-4
+    # the engine takes the adapter's explicit VJP; the autograd route over node_energy (the
+    # reference engine's route) runs the same kernels and gives the same bits
+    with torch.enable_grad():
+        leaf = builder.batch.positions.detach().requires_grad_(True)
+        from fastmd_amd.engine.energy_derivative import sum_f64
+
+        energy = sum_f64(adapter.node_energy(inputs, leaf, builder.batch.cell)[:n])
+        (grad,) = torch.autograd.grad(energy, (leaf,))
+    assert torch.equal(energy.detach().reshape(1), out["e"])
+    assert torch.equal(-grad, out["f"][0])
 
 
 @pytest.mark.gpu

@@ -187,6 +187,17 @@ def test_gemm_fp32_large_tiles(device):
     out = c0.to(device)
     gemm(ad, wd, b_layout=1, out=out, accumulate=True)
     assert oops.relative(out.cpu().numpy(), (ref + c0.double()).numpy()) < 1e-5
+    # the VJP shape (N = 2F+8: a partial last N tile) and a row pitch that is not a multiple of 4
+    # (masked loads on every K slice)
+    gz = torch.randn(m, n, generator=g)
+    gref = gz.double() @ w.double().t()
+    gy = gemm(gz.to(device), wd, b_layout=0)
+    assert oops.relative(gy.cpu().numpy(), gref.numpy()) < 1e-5
+    wide = torch.zeros(m, k + 3)
+    wide[:, :k] = a
+    aw = wide.to(device)[:, :k]
+    yw = gemm(aw, wt, b_layout=0)
+    assert oops.relative(yw.cpu().numpy(), ref.numpy()) < 1e-5
 
 
 @pytest.mark.gpu
