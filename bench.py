@@ -25,6 +25,8 @@ if ROOT not in sys.path:
 METRIC = "MD ms/step & atom-steps/s (whole_step) at 135/10k atoms; segment_sum HBM GB/s"
 HBM_PEAK_GBPS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+SPLIT_PRODUCTS = 6  # fp32-accurate GEMM: three bf16 planes per operand, six MFMA products
 STEPS_PER_LAUNCH = 10
 
 
@@ -86,24 +88,37 @@ def time_kernel(fn, reps: int = 20) -> float:
 
 
 def gemm_roofline(md) -> dict:
-    """The dominant kernel of the 10 000-atom step, the fp32 MFMA edge GEMM z = a @ W1
-    ([e_cap, 2C+8] x [2C+8, 4C], W1 stored K-contiguous: gemm_f32_nt_kernel), timed live on the
-    stream it is launched on; algorithmic flops = 2 M K N per launch."""
+    """The dominant kernel of the 10 000-atom step: the edge GEMM z = [h0[src] | h0[dst] | ef] @ W1
+    with the gather-cat fused into its operand load (gemm_x3_kernel: [e_cap, 2C+8] x [2C+8, 4C],
+    fp32-accurate as six bf16 MFMA products), at the run's e_capacity and edge list, timed live on
+    the stream it is launched on. Algorithmic flops = 2 M K N per launch (the fp32 GEMM); the
+    ceiling of fp32 work done this way is the dense bf16 MFMA peak over the six products."""
     import torch
 
-    from fastmd_amd.ops.wide_gemm import gemm
+    from fastmd_amd.ops.wide_gemm import gemm_gather
 
+    builder = md.whole_step_runner.builder
     w = md.adapter.module.w1_t(0)  # [4C, 2C+8]
-    m = md.whole_step_runner.builder.e_capacity
     n, k = w.shape
-    a = torch.randn(m, k, device=md.device)
+    C = md.adapter.module.config.channels
+    nb = k - 2 * C
+    m = builder.e_capacity
+    ei = builder.batch.edge_index
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    h0 = torch.randn(md.n_atoms, C, generator=gen).to(md.device)
+    ef = torch.randn(m, nb, generator=gen).to(md.device)
     out = torch.empty(m, n, device=md.device)
-    t = time_kernel(lambda: gemm(a, w, b_layout=0, out=out), reps=50)
+    parts = [(h0, ei[:, 1]), (h0, ei[:, 0]), (ef, None)]
+    t = time_kernel(lambda: gemm_gather(parts, w, out=out), reps=50)
     flops = 2.0 * m * k * n
     achieved = flops / t / 1e12
-    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": _traffic("gemm_f32_nt_kernel", [m, k, n]),
-            "kernel": "gemm_f32_nt_kernel", "launch_us": round(t * 1e6, 2), "flops_per_launch": flops,
+    peak = BF16_MFMA_PEAK_TFLOPS / SPLIT_PRODUCTS
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4), "traffic": _traffic("gemm_x3_kernel", [m, k, n]),
+            "kernel": "gemm_x3_kernel", "launch_us": round(t * 1e6, 2), "flops_per_launch": flops,
+            "peak_basis": f"fp32 GEMM as {SPLIT_PRODUCTS} bf16 MFMA products: dense bf16 peak "
+                          f"{BF16_MFMA_PEAK_TFLOPS} TFLOP/s / {SPLIT_PRODUCTS}",
+            "frac_of_fp32_mfma_peak": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
             "algorithmic_bytes_per_launch": 4 * (m * k + n * k + m * n), "shape_mkn": [m, k, n]}
 
 
@@ -123,19 +138,25 @@ def _traffic(kernel: str, shape: list):
     return int(row["bytes_per_launch"] * shape[0] / row["shape"][0])
 
 
-def hbm_ops_bench(n_atoms: int = 40000, F: int = 128) -> dict:
-    """configs[1] memory-bound operators on the 40 000-atom perovskite at rc = 6 A (sorted edge
-    list, 15.2 edges/atom), F = 128, fp32, each timed live with HIP events. Algorithmic bytes:
-      segment_sum [E,F] -> [N,F]:          E F 4 + N F 4 + (N + 1) 8
-      segment_sum transpose [N,F] -> [E,F]: 2 E F 4 + E 4   (gout row per edge + gvalue + perm)
-      gather_cat [E, 2F + 8]:               E (16 F + 72)    (two F rows + 8 basis + 2 indices in,
-                                                              the 2F + 8 row out)"""
+def hbm_ops_bench(n_atoms: int = 40000, F: int = 128, gemm: bool = False) -> dict:
+    """configs[1] memory-bound operators on the perovskite of ``n_atoms`` atoms at rc = 6 A (sorted
+    edge list, 15.2 edges/atom), width F, fp32, each timed live with HIP events. Two byte counts
+    per op: ``hbm_bytes``, every input row read once and every output written once (the HBM
+    traffic a perfect cache gives; ``GBps`` and ``frac_of_hbm_peak`` use it), and
+    ``survey_bytes``, the per-gathered-load formula, which counts a source row once per edge
+    that reads it (those re-reads are L2/MALL hits, so its rate can exceed the HBM peak):
+      segment_sum [E,F] -> [N,F]:      hbm = survey = E F 4 + N F 4 + (N + 1) 8
+      transpose   [N,F] -> [E,F]:      hbm = E F 4 + N F 4 + (N + 1) 8;  survey = 2 E F 4 + E 4
+      gather_cat  [E, 2F + 8]:         hbm = E (2F + 8) 4 + N F 4 + E 8 4 + E 2 4;  survey = E (16 F + 72)
+    With ``gemm`` the wide edge GEMM [E, 2F + 8] x [2F + 8, 4F] is timed too (fp32 and bf16
+    operands, fp32 out; flops 2 E (2F + 8) 4F)."""
     import torch
 
     from fastmd_amd import systems
     from fastmd_amd.graph.gpu_graph_builder import TensorGraphBuilder
     from fastmd_amd.models.mace_like import _gather_edge_rows
     from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr, segment_sum_t
+    from fastmd_amd.ops.wide_gemm import gemm as wide_gemm
 
     device = torch.device("cuda", 0)
     s = systems.perovskite_atoms(n_atoms)
@@ -151,17 +172,47 @@ def hbm_ops_bench(n_atoms: int = 40000, F: int = 128) -> dict:
     csr = Csr(g.edge_offsets)
     ei = g.edge_index[:e]
     res = {"atoms": n_atoms, "edges": e, "F": F}
+    reps = 50 if e > 100000 else 200
 
-    def put(name, t, nbytes):
-        gbps = nbytes / t / 1e9
+    def put(name, t, hbm, survey):
+        gbps = hbm / t / 1e9
         res[name] = {"us": round(t * 1e6, 2), "GBps": round(gbps, 1), "frac_of_hbm_peak": round(gbps / HBM_PEAK_GBPS, 4),
-                     "algorithmic_bytes": nbytes}
+                     "hbm_bytes": hbm, "survey_bytes": survey, "survey_GBps": round(survey / t / 1e9, 1)}
 
-    put("segment_sum", time_kernel(lambda: segment_sum_csr([(v, csr, 0, 1.0, None)], n_atoms, F, out=out), reps=50),
-        e * F * 4 + n_atoms * F * 4 + (n_atoms + 1) * 8)
-    put("segment_sum_transpose", time_kernel(lambda: segment_sum_t(x, csr, e), reps=50), 2 * e * F * 4 + e * 4)
-    put("gather_cat", time_kernel(lambda: _gather_edge_rows(x, rbf, ei, rows), reps=50), e * (16 * F + 72))
+    seg_bytes = e * F * 4 + n_atoms * F * 4 + (n_atoms + 1) * 8
+    put("segment_sum", time_kernel(lambda: segment_sum_csr([(v, csr, 0, 1.0, None)], n_atoms, F, out=out), reps=reps),
+        seg_bytes, seg_bytes)
+    put("segment_sum_transpose", time_kernel(lambda: segment_sum_t(x, csr, e), reps=reps), seg_bytes,
+        2 * e * F * 4 + e * 4)
+    put("gather_cat", time_kernel(lambda: _gather_edge_rows(x, rbf, ei, rows), reps=reps),
+        e * (2 * F + 8) * 4 + n_atoms * F * 4 + e * 8 * 4 + e * 2 * 4, e * (16 * F + 72))
+    if gemm:
+        k, n = 2 * F + 8, 4 * F
+        w = torch.randn(k, n, generator=gen).to(device) / k ** 0.5
+        flops = 2.0 * e * k * n
+        z = torch.empty(e, n, device=device)
+        t32 = time_kernel(lambda: wide_gemm(rows, w, b_layout=1, out=z), reps=reps)
+        rows16, w16 = rows.to(torch.bfloat16), w.to(torch.bfloat16)
+        t16 = time_kernel(lambda: wide_gemm(rows16, w16, b_layout=1, out=z), reps=reps)
+        res["edge_gemm_f32"] = {"us": round(t32 * 1e6, 2), "TFLOPs": round(flops / t32 / 1e12, 2),
+                                "frac_of_fp32_mfma_peak": round(flops / t32 / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
+        b16 = 2 * (e * k + k * n) + 4 * e * n
+        res["edge_gemm_bf16"] = {"us": round(t16 * 1e6, 2), "TFLOPs": round(flops / t16 / 1e12, 2),
+                                 "GBps": round(b16 / t16 / 1e9, 1),
+                                 "frac_of_hbm_peak": round(b16 / t16 / 1e9 / HBM_PEAK_GBPS, 4)}
     return res
+
+
+def ops_sweep() -> list:
+    """every (N, F) of the operator microbenchmark."""
+    out = []
+    for n_atoms in (135, 3430, 40000):
+        for F in (64, 128, 256):
+            r = hbm_ops_bench(n_atoms, F, gemm=True)
+            log(f"ops N={n_atoms} F={F}: " + ", ".join(
+                f"{k} {r[k]['us']} us" for k in r if isinstance(r[k], dict)))
+            out.append(r)
+    return out
 
 
 def cpu_baseline(n_atoms: int, budget_s: float) -> dict:
@@ -231,6 +282,8 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--quick", action="store_true", help="short run (profiling): no CPU baseline, fewer steps")
+    parser.add_argument("--ops", action="store_true",
+                        help="only the configs[1] operator microbenchmark sweep (N x F), one JSON line")
     parser.add_argument("--roofline-only", action="store_true",
                         help="only the dominant kernel at the 10 000-atom shape plus a 256 MiB copy (--pmc runs)")
     args = parser.parse_args()
@@ -247,6 +300,10 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     steps_small = 200 if args.quick else args.steps_small
+    if args.ops:
+        print(json.dumps({"ops_sweep": ops_sweep(), "hbm_peak_GBps": HBM_PEAK_GBPS,
+                          "fp32_mfma_peak_TFLOPs": FP32_MFMA_PEAK_TFLOPS}), flush=True)
+        return 0
     if args.roofline_only:
         # the run profiled with rocprofv3 --pmc for the GEMM's HBM traffic: the dominant kernel at
         # the 10 000-atom shape, then a plain 256 MiB device copy (the counters' calibration)

@@ -2,6 +2,12 @@
 //
 // C[M,N] = A[M,K] * op(B) (+ bias) (+ C), fp32 output, MFMA accumulation in fp32:
 //   fp32: v_mfma_f32_32x32x2_f32   (A/B operands fp32; 157 TFLOP/s dense peak on MI355X)
+//   fp32 as three bf16 planes: each operand x = x0 + x1 + x2 (bf16, round to nearest: the three
+//         planes hold x's 24 significand bits) and C = sum of the six products xi*yj with
+//         i + j <= 2 on v_mfma_f32_32x32x16_bf16 (fp32 accumulation). The dropped products are
+//         below 2^-24 relative, so the result is as accurate as an fp32 GEMM (measured: max error
+//         vs fp64 7e-7 of max|C| at K = 264, against 9e-7 for the fp32 MFMA kernel), at
+//         2.5 PFLOP/s / 6 = 417 TFLOP/s of fp32 work instead of 157 (CDNA4 has no TF32).
 //   bf16: v_mfma_f32_32x32x16_bf16 (A/B operands bf16; 2.5 PFLOP/s dense peak)
 // Workgroup: 256 threads = 4 waves in a 2x2 arrangement; block tile 128x128 (each wave a 64x64
 // sub-tile: 2x2 MFMA 32x32 blocks, 64 accumulator registers per lane) or 64x64 for small
@@ -423,6 +429,205 @@ __global__ void __launch_bounds__(kThreads) gemm_bf16_kernel(const uint16_t* __r
   epilogue<2, 2>(acc, row_blk + wm * 64, col_blk + wn * 64, m, n, bias, c, ldc, accumulate, act);
 }
 
+// ------------------------------------------------------------- fp32 as three bf16 planes, NT
+// C[M,N] = A[M,K] B[N,K]^T (+ bias) (+ C), both operands K-contiguous fp32. A is the column
+// concatenation of up to three parts, part p reading row idx_p[r * istride_p] of src_p (or row
+// r): the gather-cat of edge rows fused into the GEMM's operand load, so the [M, K] row matrix
+// never exists in HBM. Block tile 128 x 128, 4 waves of 64 x 64 (2 x 2 blocks of 32 x 32),
+// K in slices of 16: every thread loads two float4 of A and two of B (a row's 16 k take four
+// threads), splits them into the three bf16 planes and stores 8-byte pieces into LDS; the 8-k
+// chunk pair of LDS row r is swapped when bit 3 of r is set, so the sixteen 16-byte operand reads
+// of a quarter wave hit distinct bank groups. Two LDS buffers (48 KB: three workgroups per CU at
+// 148 VGPRs): slice kt + 1 is split and stored, and slice kt + 2 loaded into registers, while
+// the MFMAs of slice kt run. Part widths are multiples of 4 and all but the last multiples of 16
+// (a slice never straddles two parts); k past a part's width or past K loads as zero.
+struct X3Part {
+  const float* src;
+  const int32_t* idx;
+  int64_t ld, istride;
+  int32_t width;
+};
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void split3(float4 v, bf16x4& p0, bf16x4& p1, bf16x4& p2) {
+  const float x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const __bf16 h0 = (__bf16)x[e];
+    const float r1 = x[e] - (float)h0;  // exact
+    const __bf16 h1 = (__bf16)r1;
+    const float r2 = r1 - (float)h1;    // exact
+    p0[e] = h0;
+    p1[e] = h1;
+    p2[e] = (__bf16)r2;
+  }
+}
+
+constexpr int X3_PL = 128 * 16, X3_OP = 3 * X3_PL, X3_BUF = 2 * X3_OP;
+
+#define X3_LOAD(K0)                                                                                 \
+  do {                                                                                              \
+    const int64_t k0_ = (K0);                                                                       \
+    const bool q2_ = k0_ >= ks2, q1_ = !q2_ && k0_ >= ks1;                                          \
+    const float* base_ = q2_ ? src2 : q1_ ? src1 : src0;                                            \
+    const int64_t kin_ = q2_ ? k0_ - ks2 : q1_ ? k0_ - ks1 : k0_;                                   \
+    const int w_ = q2_ ? w2 : q1_ ? w1 : w0;                                                        \
+    _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                                 \
+      const int64_t o_ = q2_ ? ao2[q] : q1_ ? ao1[q] : ao0[q];                                      \
+      ra[q] = (kin_ + kc < w_) ? *reinterpret_cast<const float4*>(base_ + o_ + kin_)                \
+                               : make_float4(0.f, 0.f, 0.f, 0.f);                                   \
+      rb[q] = (k0_ + kc < k) ? *reinterpret_cast<const float4*>(b + bo[q] + k0_)                    \
+                             : make_float4(0.f, 0.f, 0.f, 0.f);                                     \
+    }                                                                                               \
+  } while (0)
+
+#define X3_STORE(BUFI)                                                                              \
+  do {                                                                                              \
+    __bf16* sb_ = lds + (BUFI) * X3_BUF;                                                            \
+    _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                                 \
+      bf16x4 x0_, x1_, x2_;                                                                         \
+      split3(ra[q], x0_, x1_, x2_);                                                                 \
+      *reinterpret_cast<bf16x4*>(sb_ + 0 * X3_PL + soff[q]) = x0_;                                  \
+      *reinterpret_cast<bf16x4*>(sb_ + 1 * X3_PL + soff[q]) = x1_;                                  \
+      *reinterpret_cast<bf16x4*>(sb_ + 2 * X3_PL + soff[q]) = x2_;                                  \
+      split3(rb[q], x0_, x1_, x2_);                                                                 \
+      *reinterpret_cast<bf16x4*>(sb_ + X3_OP + 0 * X3_PL + soff[q]) = x0_;                          \
+      *reinterpret_cast<bf16x4*>(sb_ + X3_OP + 1 * X3_PL + soff[q]) = x1_;                          \
+      *reinterpret_cast<bf16x4*>(sb_ + X3_OP + 2 * X3_PL + soff[q]) = x2_;                          \
+    }                                                                                               \
+  } while (0)
+
+// six products per block, the small ones first: (0,2) (1,1) (2,0) (0,1) (1,0) (0,0)
+#define X3_COMPUTE(BUFI)                                                                            \
+  do {                                                                                              \
+    const __bf16* as_ = lds + (BUFI) * X3_BUF;                                                      \
+    const __bf16* bs_ = as_ + X3_OP;                                                                \
+    bf16x8 av_[3][2], bv_[3][2];                                                                    \
+    _Pragma("unroll") for (int p = 0; p < 3; ++p) {                                                 \
+      _Pragma("unroll") for (int i = 0; i < 2; ++i)                                                 \
+        av_[p][i] = *reinterpret_cast<const bf16x8*>(as_ + p * X3_PL + (wm * 64 + i * 32) * 16 + rd); \
+      _Pragma("unroll") for (int j = 0; j < 2; ++j)                                                 \
+        bv_[p][j] = *reinterpret_cast<const bf16x8*>(bs_ + p * X3_PL + (wn * 64 + j * 32) * 16 + rd); \
+    }                                                                                               \
+    _Pragma("unroll") for (int i = 0; i < 2; ++i) _Pragma("unroll") for (int j = 0; j < 2; ++j) {   \
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[0][i], bv_[2][j], acc[i][j], 0, 0, 0); \
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[1][i], bv_[1][j], acc[i][j], 0, 0, 0); \
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[2][i], bv_[0][j], acc[i][j], 0, 0, 0); \
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[0][i], bv_[1][j], acc[i][j], 0, 0, 0); \
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[1][i], bv_[0][j], acc[i][j], 0, 0, 0); \
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[0][i], bv_[0][j], acc[i][j], 0, 0, 0); \
+    }                                                                                               \
+  } while (0)
+
+__global__ void __launch_bounds__(kThreads) gemm_x3_kernel(X3Part P0, X3Part P1, X3Part P2, int np,
+                                                           const float* __restrict__ b, int64_t ldb,
+                                                           const float* __restrict__ bias, float* c, int64_t ldc,
+                                                           int64_t m, int64_t n, int64_t k, int accumulate, int act,
+                                                           int64_t n_tiles) {
+  __shared__ __attribute__((aligned(16))) __bf16 lds[2 * X3_BUF];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, rr = lane & 31;
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t row_blk = (tile / n_tiles) * 128, col_blk = (tile % n_tiles) * 128;
+  const int64_t ks1 = P0.width, ks2 = ks1 + (np > 1 ? P1.width : 0);
+  const float *src0 = P0.src, *src1 = P1.src, *src2 = P2.src;
+  const int w0 = P0.width, w1 = P1.width, w2 = P2.width;
+  // loader: thread t, pass q -> row (t + 256 q) / 4 of the tile, k (t % 4) * 4 of the slice
+  const int kc = (t & 3) * 4;
+  int64_t ao0[2], ao1[2], ao2[2], bo[2];
+  int soff[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int r = (t + q * kThreads) >> 2;
+    const int64_t gr = min(row_blk + r, m - 1);
+    ao0[q] = (P0.idx ? (int64_t)P0.idx[gr * P0.istride] : gr) * P0.ld + kc;
+    ao1[q] = np > 1 ? (P1.idx ? (int64_t)P1.idx[gr * P1.istride] : gr) * P1.ld + kc : 0;
+    ao2[q] = np > 2 ? (P2.idx ? (int64_t)P2.idx[gr * P2.istride] : gr) * P2.ld + kc : 0;
+    bo[q] = min(col_blk + r, n - 1) * ldb + kc;
+    soff[q] = r * 16 + (((kc >> 3) ^ ((r >> 3) & 1)) * 8) + (kc & 7);
+  }
+  const int rd = rr * 16 + ((h ^ ((rr >> 3) & 1)) * 8);  // this lane's 8 k of its MFMA row
+  float4 ra[2], rb[2];
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int64_t nk = fmd_cdiv(k, 16);
+  X3_LOAD(0);
+  X3_STORE(0);
+  if (nk > 1) X3_LOAD(16);
+  __syncthreads();
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int cur = (int)(kt & 1);
+    if (kt + 1 < nk) {
+      X3_STORE(cur ^ 1);                       // slice kt + 1 (loaded one iteration ago)
+      if (kt + 2 < nk) X3_LOAD((kt + 2) * 16);  // slice kt + 2 stays in flight over these MFMAs
+    }
+    X3_COMPUTE(cur);
+    __syncthreads();  // buffer cur is free, buffer cur ^ 1 is complete
+  }
+  const int64_t row0 = row_blk + wm * 64, col0 = col_blk + wn * 64;
+  if (!bias && !accumulate && act == 0 && row0 + 64 <= m && col0 + 64 <= n) {
+    float* base = c + (row0 + h * 4) * ldc + col0 + rr;
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        float* rp = base + (int64_t)(bi * 32 + (v / 4) * 8 + (v % 4)) * ldc;
+        store_stream(rp, acc[bi][0][v]);
+        store_stream(rp + 32, acc[bi][1][v]);
+      }
+    return;
+  }
+  epilogue<2, 2>(acc, row0, col0, m, n, bias, c, ldc, accumulate, act);
+}
+
+#undef X3_LOAD
+#undef X3_STORE
+#undef X3_COMPUTE
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+bool k_fits_int(int32_t n_parts, const int32_t* widths) {
+  if (n_parts < 1 || n_parts > 3) return false;
+  int64_t k = 0;
+  for (int p = 0; p < n_parts; ++p) {
+    if (widths[p] <= 0) return false;
+    k += widths[p];
+  }
+  return k < (int64_t(1) << 30);
+}
+
+// Launch of gemm_x3_kernel; FMD_EUNSUPPORTED when the parts do not meet its layout conditions.
+int launch_gemm_x3(int32_t n_parts, const float* const* srcs, const int32_t* const* indices,
+                   const int64_t* index_strides, const int64_t* lds, const int32_t* widths, int64_t m,
+                   const float* b, int64_t ldb, const float* bias, float* c, int64_t ldc, int64_t n,
+                   int32_t accumulate, int32_t act, hipStream_t stream) {
+  if (n_parts < 1 || n_parts > 3) return FMD_EUNSUPPORTED;
+  X3Part P[3] = {};
+  int64_t k = 0;
+  for (int p = 0; p < n_parts; ++p) {
+    if (!srcs[p] || widths[p] <= 0 || widths[p] % 4 || (p + 1 < n_parts && widths[p] % 16)) return FMD_EUNSUPPORTED;
+    if (!aligned16(srcs[p]) || lds[p] % 4) return FMD_EUNSUPPORTED;
+    P[p] = X3Part{srcs[p], indices ? indices[p] : nullptr, lds[p], index_strides ? index_strides[p] : 1, widths[p]};
+    if (P[p].istride < 1) return FMD_EINVAL;
+    k += widths[p];
+  }
+  if (!b || !aligned16(b) || ldb % 4 || ldb < k) return FMD_EUNSUPPORTED;
+  const int64_t n_tiles = fmd_cdiv(n, 128), tiles = fmd_cdiv(m, 128) * n_tiles;
+  if (tiles >= (int64_t(1) << 31)) return FMD_EINVAL;
+  hipLaunchKernelGGL(gemm_x3_kernel, dim3((unsigned)tiles), dim3(kThreads), 0, stream, P[0], P[1], P[2], n_parts, b, ldb,
+                     bias, c, ldc, m, n, k, accumulate, act, n_tiles);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
 // Tile choice: 128 x 128 when that still gives two workgroups per CU (256 CUs), else 64 x 64
 // (small node-side GEMMs and the 135-atom edge GEMM: 4x more workgroups, 4x less serial K work
 // per wave).
@@ -453,6 +658,14 @@ int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32
   FMD_REQUIRE(k == 0 || (a && b && lda >= k && ldb >= (b_layout == 0 ? k : n)));
   FMD_REQUIRE(fmd_cdiv(m, 64) < (int64_t(1) << 31) && fmd_cdiv(n, 64) < 65536);
   const int64_t big_tiles = fmd_cdiv(m, 128) * fmd_cdiv(n, 128);
+  if (big_tiles >= 512 && b_layout == 0 && k > 0 && k % 4 == 0) {
+    // fp32-accurate on the bf16 matrix cores when the operands allow 16-byte loads
+    const int64_t lda64 = lda;
+    const int32_t width = (int32_t)k;
+    const int st = launch_gemm_x3(1, &a, nullptr, nullptr, &lda64, &width, m, b, ldb, bias, c, ldc, n, accumulate,
+                                  epilogue_kind, stream);
+    if (st != FMD_EUNSUPPORTED) return st;
+  }
   if (big_tiles >= 512 && b_layout == 0) {
     FMD_REQUIRE(big_tiles < (int64_t(1) << 31));
     const int vec_ok = (lda % 4 == 0) && (ldb % 4 == 0) && ((reinterpret_cast<uintptr_t>(a) & 15) == 0) &&
@@ -465,6 +678,18 @@ int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32
     launch_gemm_f32<64, 64>(a, lda, b, ldb, b_layout, bias, c, ldc, m, n, k, accumulate, epilogue_kind, stream);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
+}
+
+int fmd_gemm_gather_f32(int32_t n_parts, const float* const* srcs, const int32_t* const* indices,
+                        const int64_t* index_strides, const int64_t* lds, const int32_t* widths, int64_t m,
+                        const float* b, int64_t ldb, const float* bias, float* c, int64_t ldc, int64_t n,
+                        int32_t accumulate, int32_t epilogue_kind, hipStream_t stream) {
+  FMD_REQUIRE(m >= 0 && n >= 0 && c && ldc >= n && srcs && lds && widths);
+  FMD_REQUIRE(epilogue_kind == 0 || epilogue_kind == 1);
+  if (m == 0 || n == 0) return FMD_OK;
+  FMD_REQUIRE(k_fits_int(n_parts, widths));
+  return launch_gemm_x3(n_parts, srcs, indices, index_strides, lds, widths, m, b, ldb, bias, c, ldc, n, accumulate,
+                        epilogue_kind, stream);
 }
 
 int fmd_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int32_t b_layout, const float* bias,

@@ -48,26 +48,65 @@ struct VecT<4> {
   __device__ static T scale(T a, float s) { return make_float4(a.x * s, a.y * s, a.z * s, a.w * s); }
 };
 
-// out[e, :] = cat(parts): one wave per row, grid-stride over rows.
-template <int VEC>
+// out[e, :] = cat(parts) over tiles of RPW rows per wave. A wave first stages the gathered row
+// numbers of its tile in LDS (one coalesced index load per part), then walks the tile's
+// RPW x total output units as one flat range: unit u = it * 64 + lane is (row u / total, column
+// u % total), so every lane stores on every pass and consecutive lanes store consecutive
+// 16-byte units (full-width coalesced stores, no idle lanes at the end of a row). U passes are
+// issued before their stores so each lane keeps U loads in flight; the stores are streaming.
+template <int VEC, int RPW>
 __global__ void __launch_bounds__(kThreads) gather_cat_kernel(CatParts p, int64_t rows, float* out, int64_t ld_out) {
   using V = typename VecT<VEC>::T;
+  constexpr int U = 4;
+  constexpr int kWaves = kThreads / FMD_WAVE;
+  __shared__ int32_t s_idx[kWaves][kMaxParts][RPW];
   const int lane = threadIdx.x & (FMD_WAVE - 1);
-  const int64_t wave = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / FMD_WAVE;
-  const int64_t nwaves = (int64_t)gridDim.x * (kThreads / FMD_WAVE);
+  const int w = threadIdx.x / FMD_WAVE;
   const int total = p.start[p.n];
-  for (int64_t e = wave; e < rows; e += nwaves) {
-    int64_t srow[kMaxParts];
+  // advance of (row, column) per pass of 64 units
+  const int q = FMD_WAVE / total, rem = FMD_WAVE % total;
+  const int64_t ntiles = (rows + RPW - 1) / RPW;
+  for (int64_t tile = (int64_t)blockIdx.x * kWaves + w; tile < ntiles; tile += (int64_t)gridDim.x * kWaves) {
+    const int64_t e0 = tile * RPW;
+    const int nrow = (int)((rows - e0) < RPW ? (rows - e0) : RPW);
+    for (int l = lane; l < RPW; l += FMD_WAVE) {
 #pragma unroll
-    for (int k = 0; k < kMaxParts; ++k) srow[k] = (k < p.n && p.idx[k]) ? (int64_t)p.idx[k][e * p.istride[k]] : e;
-    V* orow = reinterpret_cast<V*>(out + e * ld_out);
-    for (int c = lane; c < total; c += FMD_WAVE) {
-      int k = 0;
-#pragma unroll
-      for (int q = 1; q < kMaxParts; ++q) k += (q < p.n && c >= p.start[q]) ? 1 : 0;
-      const V* s = reinterpret_cast<const V*>(p.src[k] + srow[k] * p.ld[k]);
-      orow[c] = s[c - p.start[k]];
+      for (int k = 0; k < kMaxParts; ++k) {
+        int32_t v = 0;
+        if (k < p.n && l < nrow) v = p.idx[k] ? p.idx[k][(e0 + l) * p.istride[k]] : (int32_t)(e0 + l);
+        s_idx[w][k][l] = v;
+      }
     }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int T = nrow * total;
+    int r = lane / total, c = lane % total;
+    for (int base = 0; base < T; base += FMD_WAVE * U) {
+      V val[U];
+      int rr[U], cc[U];
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        rr[j] = r;
+        cc[j] = c;
+        if (base + j * FMD_WAVE + lane < T) {
+          int k = 0;
+#pragma unroll
+          for (int m = 1; m < kMaxParts; ++m) k += (m < p.n && c >= p.start[m]) ? 1 : 0;
+          const int64_t srow = s_idx[w][k][r];
+          val[j] = reinterpret_cast<const V*>(p.src[k] + srow * p.ld[k])[c - p.start[k]];
+        }
+        r += q;
+        c += rem;
+        if (c >= total) {
+          c -= total;
+          r += 1;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < U; ++j)
+        if (base + j * FMD_WAVE + lane < T) store_stream(reinterpret_cast<V*>(out + (e0 + rr[j]) * ld_out) + cc[j], val[j]);
+    }
+    __builtin_amdgcn_wave_barrier();  // s_idx is rewritten for the next tile
   }
 }
 
@@ -108,12 +147,25 @@ __global__ void __launch_bounds__(kThreads) segsum_kernel(SegTerms t, int64_t nu
       const float* wb = t.w[k] ? t.w[k] + t.col[k] : nullptr;
       const float sc = t.scale[k];
       V part = Op::zero();
-      for (int64_t j = lo + g; j < hi; j += R) {
-        const int64_t r = t.perm[k] ? (int64_t)t.perm[k][j] : j;
-        if (r < 0) continue;
-        V val = reinterpret_cast<const V*>(base + r * t.ld[k])[c];
-        if (wb) val = Op::mul(val, reinterpret_cast<const V*>(wb + r * t.ld[k])[c]);
-        Op::add(part, val);
+      // four rows of the group's run loaded before they are added (in run order, so the sum is
+      // the same as a row-by-row loop; a missing row adds +0, which leaves the +0-started sum
+      // unchanged bit for bit)
+      for (int64_t j = lo + g; j < hi; j += 4 * R) {
+        V val[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t jj = j + (int64_t)i * R;
+          val[i] = Op::zero();
+          if (jj < hi) {
+            const int64_t r = t.perm[k] ? (int64_t)t.perm[k][jj] : jj;
+            if (r >= 0) {
+              val[i] = reinterpret_cast<const V*>(base + r * t.ld[k])[c];
+              if (wb) val[i] = Op::mul(val[i], reinterpret_cast<const V*>(wb + r * t.ld[k])[c]);
+            }
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Op::add(part, val[i]);
       }
       Op::add(acc, sc == 1.0f ? part : Op::scale(part, sc));
     }
@@ -168,9 +220,11 @@ __global__ void __launch_bounds__(kThreads) segsum_t_kernel(const float* gout, i
     if (gv) {
       V val = go;
       if (weight) val = Op::mul(val, reinterpret_cast<const V*>(weight + r * ld_value)[c]);
-      reinterpret_cast<V*>(gv + r * dimv * VEC)[c] = val;
+      store_stream(reinterpret_cast<V*>(gv + r * dimv * VEC) + c, val);
     }
-    if (gw) reinterpret_cast<V*>(gw + r * dimv * VEC)[c] = Op::mul(go, reinterpret_cast<const V*>(value + r * ld_value)[c]);
+    if (gw)
+      store_stream(reinterpret_cast<V*>(gw + r * dimv * VEC) + c,
+                   Op::mul(go, reinterpret_cast<const V*>(value + r * ld_value)[c]));
   }
 }
 
@@ -238,12 +292,16 @@ int fmd_gather_cat_f32(int32_t n_parts, const float* const* srcs, const int32_t*
     p.start[k + 1] = p.start[k] + p.width[k];
   }
   for (int k = n_parts; k < kMaxParts; ++k) p.start[k + 1] = p.start[n_parts];
-  int64_t blocks = fmd_cdiv(rows, kThreads / FMD_WAVE);
-  blocks = blocks > 65536 ? 65536 : blocks;
+  if (p.start[n_parts] == 0) return FMD_OK;
+  constexpr int kRpw = 16;
+  int64_t blocks = fmd_cdiv(fmd_cdiv(rows, kRpw), kThreads / FMD_WAVE);
+  blocks = blocks > (1 << 20) ? (1 << 20) : blocks;
   if (vec)
-    hipLaunchKernelGGL(gather_cat_kernel<4>, dim3((unsigned)blocks), dim3(kThreads), 0, stream, p, rows, out, ld_out);
+    hipLaunchKernelGGL((gather_cat_kernel<4, kRpw>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, p, rows, out,
+                       ld_out);
   else
-    hipLaunchKernelGGL(gather_cat_kernel<1>, dim3((unsigned)blocks), dim3(kThreads), 0, stream, p, rows, out, ld_out);
+    hipLaunchKernelGGL((gather_cat_kernel<1, kRpw>), dim3((unsigned)blocks), dim3(kThreads), 0, stream, p, rows, out,
+                       ld_out);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

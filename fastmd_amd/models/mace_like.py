@@ -11,7 +11,8 @@ Model (per interaction layer t, node features h0 [N, C] scalars and h1 [N, 3, C]
   edge e = (centre i <- neighbour j), vec = pos_j + image @ cell - pos_i, r = |vec|, u = vec / r
   ef_n   = sqrt(2/rc) sin(n pi r / rc) / r * fcut(r),  n = 1..8;  fcut = 1 - 21x^5 + 35x^6 - 15x^7
   a_e    = [h0_j | h0_i | ef_e]                                 (gather-cat, [E, 2C + 8])
-  z_e    = a_e @ W1                                              (edge GEMM, [2C+8, 4C])
+  z_e    = a_e @ W1                                              (edge GEMM, [2C+8, 4C]; the
+                                                                  gather-cat is fused into its load)
   w_e    = silu(z_e) * fcut(r)  = (wa | wb | wc | wd)
   m0     = wa h0_j + wc (h1_j . u),  m1_x = wb h0_j u_x + wd h1_j,x
   A0_i, A1_i = (1 / avg_num_neighbors) * sum over the rows of i   (segment sums)
@@ -38,7 +39,7 @@ from torch.autograd import Function
 from fastmd_amd import _abi
 from fastmd_amd.adapters.protocol import CapacityStep, CaptureContract, GraphBatch, PaddingRule, TopologySpec
 from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr
-from fastmd_amd.ops.wide_gemm import gemm
+from fastmd_amd.ops.wide_gemm import gemm, gemm_gather
 
 _ELEMENTS = 118
 _CAPACITY_STEP = CapacityStep(u_step=32, min_pad_u=32, u_thermal_factor=1.02)
@@ -177,11 +178,10 @@ class _MaceLikeEnergy(Function):
         saved = []
         h_first = None
         L = len(model.layers)
-        a = _empty(e_cap, 2 * C + nb, device=dev)
         for t, layer in enumerate(model.layers):
             last = t == L - 1
-            _gather_edge_rows(h0, ef, ei, a)
-            z = gemm(a, model.w1_t(t), b_layout=0)  # [E, 4C] = a @ W1
+            # z = [h0[src] | h0[dst] | ef] @ W1 ([E, 4C]): the gather-cat fused into the edge GEMM
+            z = gemm_gather([(h0, ei[:, 1]), (h0, ei[:, 0]), (ef, None)], model.w1_t(t))
             A0 = _empty(n, C, device=dev)
             A1 = _empty(n, 3, C, device=dev)
             _call("fmd_mace_message_f32", z.data_ptr(), geo.data_ptr(), ei.data_ptr(), off.data_ptr(),

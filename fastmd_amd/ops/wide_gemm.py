@@ -5,9 +5,11 @@ Reference signatures (fastmd/engine/kernels/triton_wide_gemm.py:482-553):
   ``linear_into(out, x, weight, bias=None, rows=None)`` (no autograd),
   ``matmul(grad, weight, c=None, rows=None, accumulate=False, enabled=None)`` = ``grad @ weight (+ c)``.
 The reference's 3xTF32 kernels decline K % 16 != 0 (:235), i.e. the configs' K = 2F + 8, and fall
-back to cuBLAS SGEMM; here every shape runs the fp32 MFMA kernel (v_mfma_f32_32x32x2_f32), and
-``edge_gemm(a, w, dtype=torch.bfloat16)`` the bf16 one (v_mfma_f32_32x32x16_bf16, fp32 out).
-``epilogue="silu"`` fuses SiLU into the store.
+back to cuBLAS SGEMM. Here large K-contiguous ("NT") GEMMs run fp32-accurate on the bf16 matrix
+cores (each operand split into three bf16 planes, six MFMA products: CDNA4's counterpart of
+3xTF32), the rest on fp32 MFMA (v_mfma_f32_32x32x2_f32); ``edge_gemm(a, w, dtype=torch.bfloat16)``
+runs plain bf16 operands (v_mfma_f32_32x32x16_bf16, fp32 out). ``gemm_gather`` fuses the edge-row
+gather-cat into the GEMM's operand load. ``epilogue="silu"`` fuses SiLU into the store.
 """
 from __future__ import annotations
 
@@ -55,6 +57,71 @@ def gemm(a: Tensor, b: Tensor, *, b_layout: int, bias: Tensor | None = None, out
     return out
 
 
+_EUNSUPPORTED = 10002
+
+
+def gemm_gather(parts, b: Tensor, *, out: Tensor | None = None, bias: Tensor | None = None,
+                accumulate: bool = False, epilogue: str | None = None) -> Tensor:
+    """``cat([src[idx] or src for src, idx in parts], 1) @ b^T`` with the gather-cat fused into the
+    GEMM's operand load (fmd_gemm_gather_f32): ``parts`` is a list of up to three ``(src, index)``
+    (``index`` None: row r of ``src``; an int32 index may be a strided column view), ``b`` [N, K]
+    K-contiguous. Falls back to gather-cat + GEMM when the layout does not meet the fused kernel's
+    conditions (16-byte aligned rows, widths % 4, all but the last width % 16)."""
+    require_cuda(b, out, bias, *[src for src, _ in parts])
+    if not 1 <= len(parts) <= 3:
+        raise ValueError("gemm_gather takes one to three parts")
+    rows = None
+    srcs, idx, strides, lds, widths, keep = [], [], [], [], [], []
+    for src, index in parts:
+        if src.dtype != torch.float32 or src.dim() != 2:
+            raise ValueError("gemm_gather parts must be 2-D float32")
+        src, ld = rows_view(src)
+        if index is not None:
+            if index.dtype != torch.int32 or index.dim() != 1:
+                index = index.to(torch.int32).reshape(-1).contiguous()
+            n_rows = index.numel()
+            stride = index.stride(0) if n_rows > 1 else 1
+        else:
+            n_rows, stride = src.shape[0], 1
+        if rows is None:
+            rows = n_rows
+        elif n_rows != rows:
+            raise ValueError("gemm_gather parts disagree on the row count")
+        keep += [src, index]
+        srcs.append(src.data_ptr())
+        idx.append(None if index is None else index.data_ptr())
+        strides.append(stride)
+        lds.append(ld)
+        widths.append(src.shape[1])
+    k = sum(widths)
+    if b.dim() != 2 or b.dtype != torch.float32 or b.shape[1] != k or b.stride(1) != 1:
+        raise ValueError(f"gemm_gather: b must be float32 [N, {k}] with unit column stride")
+    n = b.shape[0]
+    if bias is not None and (bias.shape != (n,) or bias.dtype != torch.float32):
+        raise ValueError("bias must be float32 [N]")
+    if bias is not None:
+        bias = bias.contiguous()
+    if out is None:
+        out = (torch.zeros if accumulate else torch.empty)((rows, n), dtype=torch.float32, device=b.device)
+    elif out.shape != (rows, n) or out.dtype != torch.float32 or out.stride(1) != 1:
+        raise ValueError("out must be float32 [M, N] with unit column stride")
+    if rows == 0 or n == 0:
+        return out
+    status = _abi.load().fmd_gemm_gather_f32(
+        len(parts), _abi.ptr_array(srcs), _abi.ptr_array(idx), _abi.array(_abi._i64, strides),
+        _abi.array(_abi._i64, lds), _abi.array(_abi._i32, widths), rows, b.data_ptr(), b.stride(0),
+        _abi.ptr(bias), out.data_ptr(), out.stride(0) if rows > 1 else n, n, 1 if accumulate else 0,
+        _EPILOGUES[epilogue], stream())
+    if status == _EUNSUPPORTED:
+        from fastmd_amd.ops.gather_cat import _launch as gather_launch
+
+        a = torch.empty((rows, k), dtype=torch.float32, device=b.device)
+        gather_launch(parts, rows, a)
+        return gemm(a, b, b_layout=0, bias=bias, out=out, accumulate=accumulate, epilogue=epilogue)
+    _abi.check(status, "fmd_gemm_gather_f32")
+    return out
+
+
 class _Linear(Function):
     @staticmethod
     def forward(ctx, x, weight, bias):
@@ -76,9 +143,9 @@ class _Linear(Function):
 
 
 def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None, precision=None, parts=()) -> Tensor:
-    """``F.linear(x, weight, bias)`` on the fp32 MFMA kernel (x 2-D float32). ``precision`` and
-    ``parts`` are accepted for signature parity; there is one precision (IEEE-rounded fp32
-    products, fp32 accumulation)."""
+    """``F.linear(x, weight, bias)`` on the MFMA kernels (x 2-D float32). ``precision`` and
+    ``parts`` are accepted for signature parity; there is one precision, fp32-accurate (fp32
+    MFMA, or three bf16 planes per operand for the large K-contiguous shapes)."""
     if x.dim() != 2:
         shape = x.shape
         return linear(x.reshape(-1, shape[-1]), weight, bias).reshape(*shape[:-1], weight.shape[0])

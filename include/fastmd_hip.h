@@ -164,14 +164,32 @@ int fmd_segsum_csr_t_f32(const float* gout, int64_t ld_gout, const float* value,
  * (d) Edge GEMM on MFMA
  * -------------------------------------------------------------------------------------- */
 
-/* C[M,N] (ldc) = A[M,K] (lda) * op(B) (+ bias[N]) (+ C if accumulate), fp32 in/out, fp32
- * MFMA (v_mfma_f32_32x32x2_f32). b_layout 0: B is [N,K] (ldb), op(B) = B^T (F.linear weight);
- * 1: B is [K,N] (ldb), op(B) = B. epilogue 0: none, 1: SiLU. Replaces linear / linear_into /
- * matmul (triton_wide_gemm.py:482-553), whose 3xTF32 kernels decline K % 16 != 0 (:235) and
- * fall back to F.linear. */
+/* C[M,N] (ldc) = A[M,K] (lda) * op(B) (+ bias[N]) (+ C if accumulate), fp32 in/out.
+ * b_layout 0: B is [N,K] (ldb), op(B) = B^T (F.linear weight); 1: B is [K,N] (ldb), op(B) = B.
+ * epilogue 0: none, 1: SiLU. Large b_layout-0 GEMMs with K % 4 == 0 and 16-byte aligned
+ * operands run as three bf16 planes per operand on the bf16 matrix cores (fp32-accurate, the
+ * counterpart of the reference's 3xTF32); everything else on fp32 MFMA
+ * (v_mfma_f32_32x32x2_f32). Replaces linear / linear_into / matmul
+ * (triton_wide_gemm.py:482-553), whose 3xTF32 kernels decline K % 16 != 0 (:235) and fall back
+ * to F.linear. */
 int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32_t b_layout,
                  const float* bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k,
                  int32_t accumulate, int32_t epilogue, hipStream_t stream);
+
+/* C[M,N] = A[M,K] B[N,K]^T (+ bias) (+ C) with the gather-cat fused into the operand load:
+ * A = cat(part_0, ..., part_{n-1}) over n_parts <= 3 column blocks, part p reading row
+ * indices_p[r * index_strides_p] of srcs_p (or row r when indices_p is null), width widths_p,
+ * row stride lds_p; K = sum of the widths; B [N, ldb] K-contiguous (b_layout 0 of fmd_gemm_f32).
+ * Replaces the reference's edge-row pair aligned_gather_cat3 -> linear
+ * (triton_gather_cat.py:181-199 feeding triton_wide_gemm.py:482-515): same C as
+ * fmd_gather_cat_f32 followed by fmd_gemm_f32, without the [M, K] row matrix in memory.
+ * fp32-accurate (three bf16 planes per operand, six MFMA products). Needs 16-byte aligned
+ * sources with lds_p % 4 == 0, widths % 4 == 0 and every width but the last % 16 == 0, b
+ * aligned with ldb % 4 == 0: otherwise FMD_EUNSUPPORTED (the caller gathers, then multiplies). */
+int fmd_gemm_gather_f32(int32_t n_parts, const float* const* srcs, const int32_t* const* indices,
+                        const int64_t* index_strides, const int64_t* lds, const int32_t* widths, int64_t m,
+                        const float* b, int64_t ldb, const float* bias, float* c, int64_t ldc, int64_t n,
+                        int32_t accumulate, int32_t epilogue, hipStream_t stream);
 
 /* As fmd_gemm_f32 with bf16 operands (uint16 storage), fp32 accumulate and fp32 output, on
  * v_mfma_f32_32x32x16_bf16. Not in the reference (which has no bf16 GEMM on this path). */

@@ -214,3 +214,73 @@ def test_gemm_bf16_against_fp64_of_rounded_inputs(device, F):
     y = edge_gemm(a.to(device), w.to(device), dtype=torch.bfloat16)
     ref = a.bfloat16().double() @ w.bfloat16().double()  # products of bf16 values are exact in fp32
     assert oops.relative(y.cpu().numpy(), ref.numpy()) < 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("F", [64, 128])
+def test_gemm_gather_against_fp64(device, F):
+    """The fused gather-cat + edge GEMM (fmd_gemm_gather_f32) on a real neighbour list: parts
+    [x[src] | x[dst] | rbf] read through strided int32 columns of edge_index, against fp64 of
+    torch.cat; the bias/SiLU and accumulate epilogues; and a layout the fused kernel declines
+    (a first part of width 12) through the gather-then-GEMM fallback."""
+    import numpy as np
+    import torch
+
+    from fastmd_amd import systems
+    from fastmd_amd.graph.gpu_graph_builder import TensorGraphBuilder
+    from fastmd_amd.ops.wide_gemm import gemm_gather
+
+    print(f"[gemm_gather] F={F}", flush=True)
+    s = systems.perovskite(4)
+    g = TensorGraphBuilder(cell=torch.tensor(s.cell), atomic_numbers=torch.tensor(s.numbers), atom_graph_cutoff=6.0,
+                           device=device).build(torch.tensor(s.positions, device=device))
+    e = int(g.n_edges.item())
+    ei = g.edge_index[:e]
+    gen = torch.Generator().manual_seed(11)
+    n_atoms = s.n_atoms
+    x = torch.randn(n_atoms, F, generator=gen)
+    rbf = torch.randn(e, 8, generator=gen)
+    k, n = 2 * F + 8, 4 * F
+    w = torch.randn(n, k, generator=gen) / k ** 0.5  # [N, K]
+    eic = ei.cpu().long()
+    a = torch.cat([x[eic[:, 1]], x[eic[:, 0]], rbf], 1).double()
+    ref = a @ w.double().t()
+    xd, rd, wd = x.to(device), rbf.to(device), w.to(device)
+    z = gemm_gather([(xd, ei[:, 1]), (xd, ei[:, 0]), (rd, None)], wd)
+    assert oops.relative(z.cpu().numpy(), ref.numpy()) < 1e-5
+    bias = torch.randn(n, generator=gen)
+    zs = gemm_gather([(xd, ei[:, 1]), (xd, ei[:, 0]), (rd, None)], wd, bias=bias.to(device), epilogue="silu")
+    assert oops.relative(zs.cpu().numpy(), torch.nn.functional.silu(ref + bias.double()).numpy()) < 1e-5
+    c0 = torch.randn(e, n, generator=gen)
+    out = c0.to(device)
+    gemm_gather([(xd, ei[:, 1]), (xd, ei[:, 0]), (rd, None)], wd, out=out, accumulate=True)
+    assert oops.relative(out.cpu().numpy(), (ref + c0.double()).numpy()) < 1e-5
+    # fallback layout: widths [12, 8] (the first is not a multiple of 16)
+    x12 = torch.randn(n_atoms, 12, generator=gen)
+    w2 = torch.randn(n, 20, generator=gen)
+    ref2 = torch.cat([x12[eic[:, 0]], rbf], 1).double() @ w2.double().t()
+    z2 = gemm_gather([(x12.to(device), ei[:, 0]), (rd, None)], w2.to(device))
+    assert np.abs(z2.cpu().double().numpy() - ref2.numpy()).max() / np.abs(ref2.numpy()).max() < 1e-5
+
+
+@pytest.mark.gpu
+def test_gemm_split_planes_dynamic_range(device):
+    """The three-plane bf16 path must keep fp32 accuracy over a wide exponent range: rows and
+    columns scaled by 2^-30 .. 2^30, exact zeros, and values whose low bits the first two planes
+    cannot hold (x = 1 + 2^-20). Checked against fp64 row by row (relative to each row's max)."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm
+
+    g = torch.Generator().manual_seed(13)
+    m, k, n = 40000, 264, 512  # >= 512 tiles: the split-plane kernel
+    a = torch.randn(m, k, generator=g)
+    a *= torch.pow(2.0, torch.randint(-30, 31, (m, 1), generator=g).float())
+    a[::7, ::5] = 0.0
+    a[1::11] = 1.0 + 2.0 ** -20
+    w = torch.randn(n, k, generator=g) / k ** 0.5
+    w *= torch.pow(2.0, torch.randint(-8, 9, (n, 1), generator=g).float())
+    ref = a.double() @ w.double().t()
+    y = gemm(a.to(device), w.to(device), b_layout=0).cpu().double()
+    rowmax = ref.abs().max(1, keepdim=True).values.clamp_min(1e-300)
+    assert float(((y - ref).abs() / rowmax).max()) < 1e-5
