@@ -88,28 +88,32 @@ def time_kernel(fn, reps: int = 20) -> float:
 
 
 def gemm_roofline(md) -> dict:
-    """The dominant kernel of the 10 000-atom step: the edge GEMM z = [h0[src] | h0[dst] | ef] @ W1
-    with the gather-cat fused into its operand load (gemm_x3_kernel: [e_cap, 2C+8] x [2C+8, 4C],
-    fp32-accurate as six bf16 MFMA products), at the run's e_capacity and edge list, timed live on
-    the stream it is launched on. Algorithmic flops = 2 M K N per launch (the fp32 GEMM); the
-    ceiling of fp32 work done this way is the dense bf16 MFMA peak over the six products."""
+    """The dominant kernel of the 10 000-atom step: the edge GEMM of the interaction,
+    z = [h0[src] | ef] @ W1[sender and radial rows] + Q[dst] (Q = h0 @ W1[receiver rows], formed per
+    atom and added in the epilogue), with the gather-cat fused into the operand load
+    (gemm_x3_kernel: [e_cap, C+8] x [C+8, 4C], fp32-accurate as six bf16 MFMA products), at the
+    run's e_capacity and edge list, timed live on the stream it is launched on. Algorithmic flops =
+    2 M K N per launch; the ceiling of fp32 work done this way is the dense bf16 MFMA peak over the
+    six products."""
     import torch
 
-    from fastmd_amd.ops.wide_gemm import gemm_gather
+    from fastmd_amd.ops.wide_gemm import gemm, gemm_gather
 
     builder = md.whole_step_runner.builder
-    w = md.adapter.module.w1_t(0)  # [4C, 2C+8]
+    module = md.adapter.module
+    w = module.w1_sender_t(0)  # [4C, C+8]
     n, k = w.shape
-    C = md.adapter.module.config.channels
-    nb = k - 2 * C
+    C = module.config.channels
+    nb = k - C
     m = builder.e_capacity
     ei = builder.batch.edge_index
     gen = torch.Generator(device="cpu").manual_seed(0)
     h0 = torch.randn(md.n_atoms, C, generator=gen).to(md.device)
     ef = torch.randn(m, nb, generator=gen).to(md.device)
+    q = gemm(h0, module.layers[0].W1[C:2 * C], b_layout=1)
     out = torch.empty(m, n, device=md.device)
-    parts = [(h0, ei[:, 1]), (h0, ei[:, 0]), (ef, None)]
-    t = time_kernel(lambda: gemm_gather(parts, w, out=out), reps=50)
+    parts = [(h0, ei[:, 1]), (ef, None)]
+    t = time_kernel(lambda: gemm_gather(parts, w, out=out, row_add=(q, ei[:, 0])), reps=50)
     flops = 2.0 * m * k * n
     achieved = flops / t / 1e12
     peak = BF16_MFMA_PEAK_TFLOPS / SPLIT_PRODUCTS
@@ -148,8 +152,9 @@ def hbm_ops_bench(n_atoms: int = 40000, F: int = 128, gemm: bool = False) -> dic
       segment_sum [E,F] -> [N,F]:      hbm = survey = E F 4 + N F 4 + (N + 1) 8
       transpose   [N,F] -> [E,F]:      hbm = E F 4 + N F 4 + (N + 1) 8;  survey = 2 E F 4 + E 4
       gather_cat  [E, 2F + 8]:         hbm = E (2F + 8) 4 + N F 4 + E 8 4 + E 2 4;  survey = E (16 F + 72)
-    With ``gemm`` the wide edge GEMM [E, 2F + 8] x [2F + 8, 4F] is timed too (fp32 and bf16
-    operands, fp32 out; flops 2 E (2F + 8) 4F)."""
+    With ``gemm`` the wide edge GEMM [E, 2F + 8] x [2F + 8, 4F] is timed too (fp32-accurate on
+    prebuilt rows, the same with the gather-cat fused into its operand load, and bf16 operands;
+    fp32 out; flops 2 E (2F + 8) 4F)."""
     import torch
 
     from fastmd_amd import systems
@@ -157,6 +162,7 @@ def hbm_ops_bench(n_atoms: int = 40000, F: int = 128, gemm: bool = False) -> dic
     from fastmd_amd.models.mace_like import _gather_edge_rows
     from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr, segment_sum_t
     from fastmd_amd.ops.wide_gemm import gemm as wide_gemm
+    from fastmd_amd.ops.wide_gemm import gemm_gather
 
     device = torch.device("cuda", 0)
     s = systems.perovskite_atoms(n_atoms)
@@ -191,11 +197,16 @@ def hbm_ops_bench(n_atoms: int = 40000, F: int = 128, gemm: bool = False) -> dic
         w = torch.randn(k, n, generator=gen).to(device) / k ** 0.5
         flops = 2.0 * e * k * n
         z = torch.empty(e, n, device=device)
-        t32 = time_kernel(lambda: wide_gemm(rows, w, b_layout=1, out=z), reps=reps)
-        rows16, w16 = rows.to(torch.bfloat16), w.to(torch.bfloat16)
-        t16 = time_kernel(lambda: wide_gemm(rows16, w16, b_layout=1, out=z), reps=reps)
-        res["edge_gemm_f32"] = {"us": round(t32 * 1e6, 2), "TFLOPs": round(flops / t32 / 1e12, 2),
-                                "frac_of_fp32_mfma_peak": round(flops / t32 / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
+        wt = w.t().contiguous()  # [4F, 2F+8]: the weight layout of F.linear (K-contiguous)
+        t32 = time_kernel(lambda: wide_gemm(rows, wt, b_layout=0, out=z), reps=reps)
+        tfused = time_kernel(lambda: gemm_gather([(x, ei[:, 1]), (x, ei[:, 0]), (rbf, None)], wt, out=z), reps=reps)
+        rows16, w16 = rows.to(torch.bfloat16), wt.to(torch.bfloat16)
+        t16 = time_kernel(lambda: wide_gemm(rows16, w16, b_layout=0, out=z), reps=reps)
+        split_peak = BF16_MFMA_PEAK_TFLOPS / SPLIT_PRODUCTS
+        for name, t in (("edge_gemm_f32", t32), ("gather_cat_edge_gemm_f32_fused", tfused)):
+            res[name] = {"us": round(t * 1e6, 2), "TFLOPs": round(flops / t / 1e12, 2),
+                         "frac_of_split_ceiling": round(flops / t / 1e12 / split_peak, 4),
+                         "frac_of_fp32_mfma_peak": round(flops / t / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
         b16 = 2 * (e * k + k * n) + 4 * e * n
         res["edge_gemm_bf16"] = {"us": round(t16 * 1e6, 2), "TFLOPs": round(flops / t16 / 1e12, 2),
                                  "GBps": round(b16 / t16 / 1e9, 1),

@@ -39,8 +39,8 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_segsum_csr_t_f32": (ctypes.c_int, [_p, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _p,
                                             _p]),
     "fmd_gemm_f32": (ctypes.c_int, [_p, _i64, _p, _i64, _i32, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p]),
-    "fmd_gemm_gather_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _p, _i64, _i64, _i32, _i32,
-                                           _p]),
+    "fmd_gemm_gather_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _p, _i64, _i64, _p, _p, _i64,
+                                           _i64, _i32, _i32, _p]),
     "fmd_gemm_bf16": (ctypes.c_int, [_p, _i64, _p, _i64, _i32, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p]),
     "fmd_nhc_pre_force": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _p, _p]),
     "fmd_nhc_post_force": (ctypes.c_int, [_p, _p, _i32, _p, _p, _p, _p, _p, _p, _i32, _p, _i64, _i32, _i32,
@@ -49,9 +49,9 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_sum_f64": (ctypes.c_int, [_p, _i32, _i64, _p, _p]),
     "fmd_edge_geometry_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _f32, _i32, _p, _p, _p, _p]),
     "fmd_edge_geometry_bwd_f32": (ctypes.c_int, [_p, _p, _i32, _p, _i64, _p, _i64, _p, _p, _i64, _p, _p]),
-    "fmd_mace_message_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _f32, _p, _p, _p]),
-    "fmd_mace_message_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _p, _p, _f32,
-                                                _p, _p, _i32, _p, _p, _i32, _p, _i32, _p, _p]),
+    "fmd_mace_message_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _f32, _p, _p, _p]),
+    "fmd_mace_message_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _p, _p, _f32,
+                                                _p, _p, _p, _i32, _p, _p, _i32, _p, _i32, _p, _p]),
     "fmd_mace_symcon_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p]),
     "fmd_mace_symcon_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p]),
     "fmd_mace_energy_f32": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _p, _p, _f32, _f32, _i64, _p, _p]),

@@ -440,7 +440,9 @@ __global__ void __launch_bounds__(kThreads) gemm_bf16_kernel(const uint16_t* __r
 // of a quarter wave hit distinct bank groups. Two LDS buffers (48 KB: three workgroups per CU at
 // 148 VGPRs): slice kt + 1 is split and stored, and slice kt + 2 loaded into registers, while
 // the MFMAs of slice kt run. Part widths are multiples of 4 and all but the last multiples of 16
-// (a slice never straddles two parts); k past a part's width or past K loads as zero.
+// (a slice never straddles two parts); k past a part's width or past K loads as zero. An optional
+// gathered row is added to each output row before the epilogue (C[r] += Q[idx[r]]: the receiver
+// block of an edge GEMM formed once per atom).
 struct X3Part {
   const float* src;
   const int32_t* idx;
@@ -521,7 +523,7 @@ constexpr int X3_PL = 128 * 16, X3_OP = 3 * X3_PL, X3_BUF = 2 * X3_OP;
   } while (0)
 
 __global__ void __launch_bounds__(kThreads) gemm_x3_kernel(X3Part P0, X3Part P1, X3Part P2, int np,
-                                                           const float* __restrict__ b, int64_t ldb,
+                                                           const float* __restrict__ b, int64_t ldb, X3Part radd,
                                                            const float* __restrict__ bias, float* c, int64_t ldc,
                                                            int64_t m, int64_t n, int64_t k, int accumulate, int act,
                                                            int64_t n_tiles) {
@@ -573,6 +575,21 @@ __global__ void __launch_bounds__(kThreads) gemm_x3_kernel(X3Part P0, X3Part P1,
     __syncthreads();  // buffer cur is free, buffer cur ^ 1 is complete
   }
   const int64_t row0 = row_blk + wm * 64, col0 = col_blk + wn * 64;
+  if (radd.src) {
+    // C[r, :] += radd[radd.idx[r], :] (a gathered row added to the product)
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = min(row0 + bi * 32 + (v / 4) * 8 + h * 4 + (v % 4), m - 1);
+        const float* qr = radd.src + (radd.idx ? (int64_t)radd.idx[row * radd.istride] : row) * radd.ld;
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) {
+          const int64_t col = min(col0 + bj * 32 + rr, n - 1);
+          acc[bi][bj][v] += qr[col];
+        }
+      }
+  }
   if (!bias && !accumulate && act == 0 && row0 + 64 <= m && col0 + 64 <= n) {
     float* base = c + (row0 + h * 4) * ldc + col0 + rr;
 #pragma unroll
@@ -607,8 +624,9 @@ bool k_fits_int(int32_t n_parts, const int32_t* widths) {
 // Launch of gemm_x3_kernel; FMD_EUNSUPPORTED when the parts do not meet its layout conditions.
 int launch_gemm_x3(int32_t n_parts, const float* const* srcs, const int32_t* const* indices,
                    const int64_t* index_strides, const int64_t* lds, const int32_t* widths, int64_t m,
-                   const float* b, int64_t ldb, const float* bias, float* c, int64_t ldc, int64_t n,
-                   int32_t accumulate, int32_t act, hipStream_t stream) {
+                   const float* b, int64_t ldb, const float* row_add, const int32_t* row_add_index,
+                   int64_t row_add_index_stride, int64_t ld_row_add, const float* bias, float* c, int64_t ldc,
+                   int64_t n, int32_t accumulate, int32_t act, hipStream_t stream) {
   if (n_parts < 1 || n_parts > 3) return FMD_EUNSUPPORTED;
   X3Part P[3] = {};
   int64_t k = 0;
@@ -620,10 +638,12 @@ int launch_gemm_x3(int32_t n_parts, const float* const* srcs, const int32_t* con
     k += widths[p];
   }
   if (!b || !aligned16(b) || ldb % 4 || ldb < k) return FMD_EUNSUPPORTED;
+  X3Part radd{row_add, row_add_index, ld_row_add, row_add_index_stride, 0};
+  if (row_add && (ld_row_add < n || row_add_index_stride < 1)) return FMD_EINVAL;
   const int64_t n_tiles = fmd_cdiv(n, 128), tiles = fmd_cdiv(m, 128) * n_tiles;
   if (tiles >= (int64_t(1) << 31)) return FMD_EINVAL;
   hipLaunchKernelGGL(gemm_x3_kernel, dim3((unsigned)tiles), dim3(kThreads), 0, stream, P[0], P[1], P[2], n_parts, b, ldb,
-                     bias, c, ldc, m, n, k, accumulate, act, n_tiles);
+                     radd, bias, c, ldc, m, n, k, accumulate, act, n_tiles);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -658,12 +678,13 @@ int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32
   FMD_REQUIRE(k == 0 || (a && b && lda >= k && ldb >= (b_layout == 0 ? k : n)));
   FMD_REQUIRE(fmd_cdiv(m, 64) < (int64_t(1) << 31) && fmd_cdiv(n, 64) < 65536);
   const int64_t big_tiles = fmd_cdiv(m, 128) * fmd_cdiv(n, 128);
-  if (big_tiles >= 512 && b_layout == 0 && k > 0 && k % 4 == 0) {
-    // fp32-accurate on the bf16 matrix cores when the operands allow 16-byte loads
+  if (big_tiles >= 256 && b_layout == 0 && k > 0 && k % 4 == 0) {
+    // fp32-accurate on the bf16 matrix cores when the operands allow 16-byte loads (from 256
+    // tiles of 128 x 128: below that the 64 x 64 fp32 kernel's four times more workgroups win)
     const int64_t lda64 = lda;
     const int32_t width = (int32_t)k;
-    const int st = launch_gemm_x3(1, &a, nullptr, nullptr, &lda64, &width, m, b, ldb, bias, c, ldc, n, accumulate,
-                                  epilogue_kind, stream);
+    const int st = launch_gemm_x3(1, &a, nullptr, nullptr, &lda64, &width, m, b, ldb, nullptr, nullptr, 1, 0, bias, c,
+                                  ldc, n, accumulate, epilogue_kind, stream);
     if (st != FMD_EUNSUPPORTED) return st;
   }
   if (big_tiles >= 512 && b_layout == 0) {
@@ -682,14 +703,15 @@ int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32
 
 int fmd_gemm_gather_f32(int32_t n_parts, const float* const* srcs, const int32_t* const* indices,
                         const int64_t* index_strides, const int64_t* lds, const int32_t* widths, int64_t m,
-                        const float* b, int64_t ldb, const float* bias, float* c, int64_t ldc, int64_t n,
-                        int32_t accumulate, int32_t epilogue_kind, hipStream_t stream) {
+                        const float* b, int64_t ldb, const float* row_add, const int32_t* row_add_index,
+                        int64_t row_add_index_stride, int64_t ld_row_add, const float* bias, float* c, int64_t ldc,
+                        int64_t n, int32_t accumulate, int32_t epilogue_kind, hipStream_t stream) {
   FMD_REQUIRE(m >= 0 && n >= 0 && c && ldc >= n && srcs && lds && widths);
   FMD_REQUIRE(epilogue_kind == 0 || epilogue_kind == 1);
   if (m == 0 || n == 0) return FMD_OK;
   FMD_REQUIRE(k_fits_int(n_parts, widths));
-  return launch_gemm_x3(n_parts, srcs, indices, index_strides, lds, widths, m, b, ldb, bias, c, ldc, n, accumulate,
-                        epilogue_kind, stream);
+  return launch_gemm_x3(n_parts, srcs, indices, index_strides, lds, widths, m, b, ldb, row_add, row_add_index,
+                        row_add_index_stride, ld_row_add, bias, c, ldc, n, accumulate, epilogue_kind, stream);
 }
 
 int fmd_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int32_t b_layout, const float* bias,

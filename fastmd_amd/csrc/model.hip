@@ -126,10 +126,11 @@ __global__ void edge_geometry_bwd_kernel(const float* geo, const float* def, int
 //   A0_i = inv_avg * sum_e m0, A1_i = inv_avg * sum_e m1
 // ------------------------------------------------------------------------------------------
 template <int CPL, bool H1>
-__global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const float* geo, const int32_t* edge_index,
-                                                           const int64_t* off, const int64_t* n_edges, int64_t e_cap,
-                                                           int64_t n, const float* h0, const float* h1, float inv_avg,
-                                                           float* A0, float* A1) {
+__global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const float* zq, const float* geo,
+                                                           const int32_t* edge_index, const int64_t* off,
+                                                           const int64_t* n_edges, int64_t e_cap, int64_t n,
+                                                           const float* h0, const float* h1, float inv_avg, float* A0,
+                                                           float* A1) {
   constexpr int C = 64 * CPL;
   const int lane = threadIdx.x & 63;
   const int64_t i = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64;
@@ -145,6 +146,11 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
     a1[0][q] = a1[1][q] = a1[2][q] = 0.f;
   }
   const int c0 = lane * CPL;
+  float qz[4][CPL];  // the centre's receiver block of z (zq[i]), 0 when z is complete
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) qz[b][q] = zq ? zq[i * 4 * C + b * C + c0 + q] : 0.f;
   for (int64_t e = lo; e < hi; ++e) {
     const float* g = geo + 8 * e;
     const float ux = g[0], uy = g[1], uz = g[2], fc = g[4];
@@ -152,14 +158,14 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
     const float* ze = z + e * 4 * C + c0;
 #pragma unroll
     for (int q = 0; q < CPL; ++q) {
-      const float za = ze[q], zb = ze[C + q];
+      const float za = ze[q] + qz[0][q], zb = ze[C + q] + qz[1][q];
       const float wa = za * sigmoid(za) * fc, wb = zb * sigmoid(zb) * fc;
       const float hj = h0[j * C + c0 + q];
       float m0 = wa * hj;
       const float t = wb * hj;
       float m1x = t * ux, m1y = t * uy, m1z = t * uz;
       if (H1) {
-        const float zc = ze[2 * C + q], zd = ze[3 * C + q];
+        const float zc = ze[2 * C + q] + qz[2][q], zd = ze[3 * C + q] + qz[3][q];
         const float wc = zc * sigmoid(zc) * fc, wd = zd * sigmoid(zd) * fc;
         const float hx = h1[(j * 3 + 0) * C + c0 + q], hy = h1[(j * 3 + 1) * C + c0 + q],
                     hz = h1[(j * 3 + 2) * C + c0 + q];
@@ -194,9 +200,10 @@ constexpr int kMaxBasis = 16;
 
 template <int CPL, bool H1>
 __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
-    const float* z, const float* geo, const int32_t* edge_index, const int64_t* off, const int64_t* n_edges,
-    int64_t e_cap, int64_t n, const float* h0, const float* h1, const float* gA0, const float* gA1, float inv_avg,
-    float* gz, float* ggeo, int accumulate_geo, const float* w1ef, int nb, float* gef) {
+    const float* z, const float* zq, const float* geo, const int32_t* edge_index, const int64_t* off,
+    const int64_t* n_edges, int64_t e_cap, int64_t n, const float* h0, const float* h1, const float* gA0,
+    const float* gA1, float inv_avg, float* gz, float* gzsum, float* ggeo, int accumulate_geo, const float* w1ef,
+    int nb, float* gef) {
   constexpr int C = 64 * CPL;
   __shared__ float s_w[kMaxBasis * 4 * C];
   const int lane = threadIdx.x & 63;
@@ -219,6 +226,15 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     g1[1][q] = gA1[(i * 3 + 1) * C + c0 + q] * inv_avg;
     g1[2][q] = gA1[(i * 3 + 2) * C + c0 + q] * inv_avg;
   }
+  float gs[4][CPL];  // sum of gz over the centre's rows (in row order)
+  float qz[4][CPL];  // the centre's receiver block of z (zq[i]), 0 when z is complete
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) {
+      gs[b][q] = 0.f;
+      qz[b][q] = zq ? zq[i * 4 * C + b * C + c0 + q] : 0.f;
+    }
   for (int64_t e = lo; e < hi; ++e) {
     const float* g = geo + 8 * e;
     const float ux = g[0], uy = g[1], uz = g[2], fc = g[4];
@@ -230,7 +246,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     for (int q = 0; q < CPL; ++q) {
       const float hj = h0[j * C + c0 + q];
       const float gu = g1[0][q] * ux + g1[1][q] * uy + g1[2][q] * uz;
-      const float za = ze[q], zb = ze[C + q];
+      const float za = ze[q] + qz[0][q], zb = ze[C + q] + qz[1][q];
       const float sa = sigmoid(za), sb = sigmoid(zb);
       const float gwa = g0[q] * hj, gwb = hj * gu;
       gzl[0][q] = gwa * fc * sa * (1.0f + za * (1.0f - sa));
@@ -243,7 +259,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
       if (H1) {
         const float hx = h1[(j * 3 + 0) * C + c0 + q], hy = h1[(j * 3 + 1) * C + c0 + q],
                     hz = h1[(j * 3 + 2) * C + c0 + q];
-        const float zc = ze[2 * C + q], zd = ze[3 * C + q];
+        const float zc = ze[2 * C + q] + qz[2][q], zd = ze[3 * C + q] + qz[3][q];
         const float sc = sigmoid(zc), sd = sigmoid(zd);
         const float proj = hx * ux + hy * uy + hz * uz;
         const float gwc = g0[q] * proj, gwd = g1[0][q] * hx + g1[1][q] * hy + g1[2][q] * hz;
@@ -264,7 +280,13 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
 #pragma unroll
       for (int b = 0; b < 4; ++b)
 #pragma unroll
-        for (int q = 0; q < CPL; ++q) gze[b * C + q] = gzl[b][q];
+        for (int q = 0; q < CPL; ++q) store_stream(gze + b * C + q, gzl[b][q]);
+    }
+    if (gzsum) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) gs[b][q] += gzl[b][q];
     }
     if (w1ef) {
       for (int n0 = 0; n0 < nb; n0 += 8) {
@@ -304,6 +326,13 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
       }
     }
   }
+  if (gzsum) {
+    float* d = gzsum + i * 4 * C + c0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int q = 0; q < CPL; ++q) d[b * C + q] = gs[b][q];
+  }
 }
 
 // VJP, sender side (one wave per node j, over the reverse rows e = reverse[e'] of its rows e'
@@ -312,9 +341,9 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
 // accumulate: bit 0 adds into gh0, bit 1 into gh1 (else they are overwritten).
 template <int CPL, bool H1>
 __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
-    const float* z, const float* geo, const int32_t* edge_index, const int32_t* reverse, const int64_t* off,
-    const int64_t* n_edges, int64_t e_cap, int64_t n, const float* gA0, const float* gA1, float inv_avg, float* gh0,
-    float* gh1, int accumulate) {
+    const float* z, const float* zq, const float* geo, const int32_t* edge_index, const int32_t* reverse,
+    const int64_t* off, const int64_t* n_edges, int64_t e_cap, int64_t n, const float* gA0, const float* gA1,
+    float inv_avg, float* gh0, float* gh1, int accumulate) {
   constexpr int C = 64 * CPL;
   const int lane = threadIdx.x & 63;
   const int64_t jn = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64;
@@ -334,16 +363,17 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
     const float* g = geo + 8 * e;
     const float ux = g[0], uy = g[1], uz = g[2], fc = g[4];
     const float* ze = z + e * 4 * C + c0;
+    const float* qe = zq ? zq + i * 4 * C + c0 : nullptr;  // the receiver block of z[e] (row i)
 #pragma unroll
     for (int q = 0; q < CPL; ++q) {
       const float g0 = gA0[i * C + c0 + q];
       const float gx = gA1[(i * 3 + 0) * C + c0 + q], gy = gA1[(i * 3 + 1) * C + c0 + q],
                   gzv = gA1[(i * 3 + 2) * C + c0 + q];
-      const float za = ze[q], zb = ze[C + q];
+      const float za = ze[q] + (qe ? qe[q] : 0.f), zb = ze[C + q] + (qe ? qe[C + q] : 0.f);
       const float wa = za * sigmoid(za) * fc, wb = zb * sigmoid(zb) * fc;
       a0[q] += g0 * wa + wb * (gx * ux + gy * uy + gzv * uz);
       if (H1) {
-        const float zc = ze[2 * C + q], zd = ze[3 * C + q];
+        const float zc = ze[2 * C + q] + (qe ? qe[2 * C + q] : 0.f), zd = ze[3 * C + q] + (qe ? qe[3 * C + q] : 0.f);
         const float wc = zc * sigmoid(zc) * fc, wd = zd * sigmoid(zd) * fc;
         const float t = g0 * wc;
         a1[0][q] += t * ux + gx * wd;
@@ -520,15 +550,16 @@ __global__ void morse_bwd_kernel(const float* geo, const float* dvdr, const int3
 }
 
 template <int CPL>
-int launch_message(bool h1, dim3 grid, hipStream_t s, const float* z, const float* geo, const int32_t* ei,
+int launch_message(bool h1, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
+                   const int32_t* ei,
                    const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const float* h0,
                    const float* h1p, float inv_avg, float* A0, float* A1) {
   if (h1)
-    hipLaunchKernelGGL((message_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, geo, ei, off, ne, e_cap, n, h0, h1p,
-                       inv_avg, A0, A1);
-  else
-    hipLaunchKernelGGL((message_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, geo, ei, off, ne, e_cap, n, h0,
+    hipLaunchKernelGGL((message_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, off, ne, e_cap, n, h0,
                        h1p, inv_avg, A0, A1);
+  else
+    hipLaunchKernelGGL((message_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, off, ne, e_cap, n,
+                       h0, h1p, inv_avg, A0, A1);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -545,29 +576,31 @@ int launch_message(bool h1, dim3 grid, hipStream_t s, const float* z, const floa
 
 namespace {
 template <int CPL>
-int launch_bwd_edge(bool h1, dim3 grid, hipStream_t s, const float* z, const float* geo, const int32_t* ei,
+int launch_bwd_edge(bool h1, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
+                    const int32_t* ei,
                     const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const float* h0,
-                    const float* h1p, const float* gA0, const float* gA1, float inv_avg, float* gz, float* ggeo,
-                    int acc, const float* w1ef, int nb, float* gef) {
+                    const float* h1p, const float* gA0, const float* gA1, float inv_avg, float* gz, float* gzsum,
+                    float* ggeo, int acc, const float* w1ef, int nb, float* gef) {
   if (h1)
-    hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, geo, ei, off, ne, e_cap,
-                       n, h0, h1p, gA0, gA1, inv_avg, gz, ggeo, acc, w1ef, nb, gef);
+    hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, off, ne, e_cap,
+                       n, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef);
   else
-    hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, geo, ei, off, ne, e_cap,
-                       n, h0, h1p, gA0, gA1, inv_avg, gz, ggeo, acc, w1ef, nb, gef);
+    hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, off, ne, e_cap,
+                       n, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
 
 template <int CPL>
-int launch_bwd_src(bool h1, dim3 grid, hipStream_t s, const float* z, const float* geo, const int32_t* ei,
+int launch_bwd_src(bool h1, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
+                   const int32_t* ei,
                    const int32_t* rev, const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n,
                    const float* gA0, const float* gA1, float inv_avg, float* gh0, float* gh1, int acc) {
   if (h1)
-    hipLaunchKernelGGL((message_bwd_src_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, geo, ei, rev, off, ne,
+    hipLaunchKernelGGL((message_bwd_src_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, rev, off, ne,
                        e_cap, n, gA0, gA1, inv_avg, gh0, gh1, acc);
   else
-    hipLaunchKernelGGL((message_bwd_src_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, geo, ei, rev, off, ne,
+    hipLaunchKernelGGL((message_bwd_src_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, rev, off, ne,
                        e_cap, n, gA0, gA1, inv_avg, gh0, gh1, acc);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
@@ -599,21 +632,24 @@ int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, co
   return FMD_OK;
 }
 
-int fmd_mace_message_f32(const float* z, const float* geo, const int32_t* edge_index, const int64_t* edge_offsets,
-                         const int64_t* n_edges, int64_t e_cap, int64_t n_atoms, int32_t channels, const float* h0,
-                         const float* h1, float inv_avg, float* A0, float* A1, hipStream_t stream) {
+int fmd_mace_message_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
+                         const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
+                         int32_t channels, const float* h0, const float* h1, float inv_avg, float* A0, float* A1,
+                         hipStream_t stream) {
   FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && A0 && A1 && n_atoms >= 0);
   if (n_atoms == 0) return FMD_OK;
   dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
-  FMD_CPL_DISPATCH(channels, launch_message, h1 != nullptr, grid, stream, z, geo, edge_index, edge_offsets, n_edges,
-                   e_cap, n_atoms, h0, h1, inv_avg, A0, A1);
+  FMD_CPL_DISPATCH(channels, launch_message, h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets,
+                   n_edges, e_cap, n_atoms, h0, h1, inv_avg, A0, A1);
 }
 
-int fmd_mace_message_bwd_f32(const float* z, const float* geo, const int32_t* edge_index, const int32_t* reverse,
+int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
+                             const int32_t* reverse,
                              const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
                              int32_t channels, const float* h0, const float* h1, const float* gA0, const float* gA1,
-                             float inv_avg, float* gz, float* ggeo, int32_t accumulate_geo, float* gh0, float* gh1,
-                             int32_t accumulate_h, const float* w1ef, int32_t nb, float* gef, hipStream_t stream) {
+                             float inv_avg, float* gz, float* gzsum, float* ggeo, int32_t accumulate_geo, float* gh0,
+                             float* gh1, int32_t accumulate_h, const float* w1ef, int32_t nb, float* gef,
+                             hipStream_t stream) {
   FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && gA0 && gA1 && ggeo && n_atoms >= 0);
   FMD_REQUIRE(gz || w1ef);
   FMD_REQUIRE(!w1ef || (gef && nb > 0 && nb <= kMaxBasis));
@@ -622,21 +658,21 @@ int fmd_mace_message_bwd_f32(const float* z, const float* geo, const int32_t* ed
   dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
   int rc = FMD_OK;
   switch (channels / 64) {
-    case 1: rc = launch_bwd_edge<1>(h1 != nullptr, grid, stream, z, geo, edge_index, edge_offsets, n_edges, e_cap,
-                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, ggeo, accumulate_geo, w1ef, nb, gef); break;
-    case 2: rc = launch_bwd_edge<2>(h1 != nullptr, grid, stream, z, geo, edge_index, edge_offsets, n_edges, e_cap,
-                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, ggeo, accumulate_geo, w1ef, nb, gef); break;
-    case 4: rc = launch_bwd_edge<4>(h1 != nullptr, grid, stream, z, geo, edge_index, edge_offsets, n_edges, e_cap,
-                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, ggeo, accumulate_geo, w1ef, nb, gef); break;
+    case 1: rc = launch_bwd_edge<1>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges, e_cap,
+                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
+    case 2: rc = launch_bwd_edge<2>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges, e_cap,
+                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
+    case 4: rc = launch_bwd_edge<4>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges, e_cap,
+                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
     default: return FMD_EUNSUPPORTED;
   }
   if (rc != FMD_OK || !gh0) return rc;
   switch (channels / 64) {
-    case 1: return launch_bwd_src<1>(h1 != nullptr, grid, stream, z, geo, edge_index, reverse, edge_offsets, n_edges,
+    case 1: return launch_bwd_src<1>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets, n_edges,
                                      e_cap, n_atoms, gA0, gA1, inv_avg, gh0, gh1, accumulate_h);
-    case 2: return launch_bwd_src<2>(h1 != nullptr, grid, stream, z, geo, edge_index, reverse, edge_offsets, n_edges,
+    case 2: return launch_bwd_src<2>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets, n_edges,
                                      e_cap, n_atoms, gA0, gA1, inv_avg, gh0, gh1, accumulate_h);
-    case 4: return launch_bwd_src<4>(h1 != nullptr, grid, stream, z, geo, edge_index, reverse, edge_offsets, n_edges,
+    case 4: return launch_bwd_src<4>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets, n_edges,
                                      e_cap, n_atoms, gA0, gA1, inv_avg, gh0, gh1, accumulate_h);
     default: return FMD_EUNSUPPORTED;
   }

@@ -43,6 +43,9 @@ from fastmd_amd.ops.wide_gemm import gemm, gemm_gather
 
 _ELEMENTS = 118
 _CAPACITY_STEP = CapacityStep(u_step=32, min_pad_u=32, u_thermal_factor=1.02)
+# edge lists from this many rows form the receiver block of the edge GEMM per atom (below it the
+# two extra node GEMMs cost more launch latency than the halved edge GEMM saves)
+HOIST_MIN_ROWS = 16384
 
 
 @dataclass(frozen=True)
@@ -114,6 +117,31 @@ class MaceLike(nn.Module):
             cache[t] = hit
         return hit[1]
 
+    def w1_receiver_t(self, t: int) -> Tensor:
+        """The receiver rows of W1 ([C, 2C)) stored K-contiguous ([4C, C])."""
+        w = self.layers[t].W1
+        C = self.config.channels
+        key = (w.data_ptr(), w._version, w.device)
+        cache = self.__dict__.setdefault("_w1r_cache", {})
+        hit = cache.get(t)
+        if hit is None or hit[0] != key:
+            hit = (key, w.detach()[C:2 * C].t().contiguous())
+            cache[t] = hit
+        return hit[1]
+
+    def w1_sender_t(self, t: int) -> Tensor:
+        """The sender and radial rows of W1 ([0, C) and [2C, 2C + nb)) stored K-contiguous
+        ([4C, C + nb]): the edge GEMM's weight once the receiver block is formed per atom."""
+        w = self.layers[t].W1
+        C = self.config.channels
+        key = (w.data_ptr(), w._version, w.device)
+        cache = self.__dict__.setdefault("_w1s_cache", {})
+        hit = cache.get(t)
+        if hit is None or hit[0] != key:
+            hit = (key, torch.cat([w.detach()[:C], w.detach()[2 * C:]], 0).t().contiguous())
+            cache[t] = hit
+        return hit[1]
+
     @property
     def num_interactions(self) -> int:
         return self.config.num_interactions
@@ -180,11 +208,19 @@ class _MaceLikeEnergy(Function):
         L = len(model.layers)
         for t, layer in enumerate(model.layers):
             last = t == L - 1
-            # z = [h0[src] | h0[dst] | ef] @ W1 ([E, 4C]): the gather-cat fused into the edge GEMM
-            z = gemm_gather([(h0, ei[:, 1]), (h0, ei[:, 0]), (ef, None)], model.w1_t(t))
+            # z = [h0[src] | h0[dst] | ef] @ W1 ([E, 4C]), the gather-cat fused into the edge GEMM's
+            # operand load. On large edge lists the receiver block h0[dst] @ W1[C:2C], the same for
+            # every row of a centre, is formed once per atom (q, [N, 4C]) and added by the message
+            # kernels, and the edge GEMM multiplies [h0[src] | ef] (K = C + nb).
+            if e_cap >= HOIST_MIN_ROWS:
+                q = gemm(h0, model.w1_receiver_t(t), b_layout=0)
+                z = gemm_gather([(h0, ei[:, 1]), (ef, None)], model.w1_sender_t(t))
+            else:
+                q = None
+                z = gemm_gather([(h0, ei[:, 1]), (h0, ei[:, 0]), (ef, None)], model.w1_t(t))
             A0 = _empty(n, C, device=dev)
             A1 = _empty(n, 3, C, device=dev)
-            _call("fmd_mace_message_f32", z.data_ptr(), geo.data_ptr(), ei.data_ptr(), off.data_ptr(),
+            _call("fmd_mace_message_f32", z.data_ptr(), _abi.ptr(q), geo.data_ptr(), ei.data_ptr(), off.data_ptr(),
                   n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), inv_avg, A0.data_ptr(), A1.data_ptr())
             P0 = gemm(A0, layer.Wm0, b_layout=1)
             P1 = gemm(A1.view(3 * n, C), layer.Wm1, b_layout=1).view(n, 3, C)
@@ -195,7 +231,7 @@ class _MaceLikeEnergy(Function):
             h0n = gemm(B0, layer.Wo0, b_layout=1)
             gemm(h0, layer.Wsc0, b_layout=1, out=h0n, accumulate=True)
             h1n = None if last else gemm(B1.view(3 * n, C), layer.Wo1, b_layout=1).view(n, 3, C)
-            saved.append((h0, h1, z, P0, P1))
+            saved.append((h0, h1, z, q, P0, P1))
             if t == 0:
                 h_first = h0n
             h0, h1 = h0n, h1n
@@ -241,7 +277,7 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
     gefs = []
     for t in reversed(range(L)):
         layer = model.layers[t]
-        h0, h1, z, P0, P1 = ctx.saved[t]
+        h0, h1, z, q, P0, P1 = ctx.saved[t]
         gB0 = gemm(g_out0, layer.Wo0, b_layout=0)
         gB1 = None if g_out1 is None else gemm(g_out1.reshape(3 * n, C), layer.Wo1, b_layout=0)
         gP0 = _empty(n, C, device=dev)
@@ -258,27 +294,35 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
             # kernel from W1's radial rows (gz is not stored)
             gef = _empty(e_cap, nb, device=dev)
             w1ef = layer.W1[2 * C:]
-            _call("fmd_mace_message_bwd_f32", z.data_ptr(), ctx.geo.data_ptr(), ei.data_ptr(), rev.data_ptr(),
-                  off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(),
-                  gA1.data_ptr(), inv_avg, None, ggeo.data_ptr(), acc_geo, None, None, 0, w1ef.data_ptr(), nb,
-                  gef.data_ptr())
+            _call("fmd_mace_message_bwd_f32", z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(), ei.data_ptr(),
+                  rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1),
+                  gA0.data_ptr(), gA1.data_ptr(), inv_avg, None, None, ggeo.data_ptr(), acc_geo, None, None, 0,
+                  w1ef.data_ptr(), nb, gef.data_ptr())
             gefs.append((gef, nb))
             break
         gz = _empty(e_cap, 4 * C, device=dev)
+        gzs = _empty(n, 4 * C, device=dev) if q is not None else None
         gef = _empty(e_cap, nb, device=dev)
         # this layer's inputs: residual (plus, in the second layer, the first readout's
         # gradient of the first layer's output), sender side of the messages, gather-cat rows
         g_in0 = gemm(g_out0, layer.Wsc0, b_layout=0, out=gha if t == 1 else None, accumulate=t == 1)
         g_in1 = _empty(n, 3, C, device=dev) if h1 is not None else None
         w1ef = layer.W1[2 * C:]
-        _call("fmd_mace_message_bwd_f32", z.data_ptr(), ctx.geo.data_ptr(), ei.data_ptr(), rev.data_ptr(),
-              off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(),
-              gA1.data_ptr(), inv_avg, gz.data_ptr(), ggeo.data_ptr(), acc_geo, g_in0.data_ptr(),
-              _abi.ptr(g_in1), 1, w1ef.data_ptr(), nb, gef.data_ptr())
+        _call("fmd_mace_message_bwd_f32", z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(), ei.data_ptr(),
+              rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1),
+              gA0.data_ptr(), gA1.data_ptr(), inv_avg, gz.data_ptr(), _abi.ptr(gzs), ggeo.data_ptr(), acc_geo,
+              g_in0.data_ptr(), _abi.ptr(g_in1), 1, w1ef.data_ptr(), nb, gef.data_ptr())
         # the node blocks of the gather-cat row gradient (the radial block is gef)
-        ga = gemm(gz, layer.W1[:2 * C], b_layout=0)  # [E, 2C]
-        segment_sum_csr([(ga, inputs.csr_src, 0, 1.0, None), (ga, inputs.csr_dst, C, 1.0, None)], n, C,
-                        out=g_in0, accumulate=True)
+        if q is not None:
+            # sender block row by row (edge GEMM, then the sender segment sum); receiver block
+            # from the per-centre sums of gz: sum_e gz[e] W1[C:2C]^T = (sum_e gz[e]) W1[C:2C]^T
+            ga = gemm(gz, layer.W1[:C], b_layout=0)  # [E, C]
+            segment_sum_csr([(ga, inputs.csr_src, 0, 1.0, None)], n, C, out=g_in0, accumulate=True)
+            gemm(gzs, layer.W1[C:2 * C], b_layout=0, out=g_in0, accumulate=True)
+        else:
+            ga = gemm(gz, layer.W1[:2 * C], b_layout=0)  # [E, 2C]
+            segment_sum_csr([(ga, inputs.csr_src, 0, 1.0, None), (ga, inputs.csr_dst, C, 1.0, None)], n, C,
+                            out=g_in0, accumulate=True)
         gefs.append((gef, nb))
         g_out0, g_out1 = g_in0, g_in1
     gvec = _empty(e_cap, 3, device=dev)

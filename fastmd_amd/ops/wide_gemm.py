@@ -61,12 +61,14 @@ _EUNSUPPORTED = 10002
 
 
 def gemm_gather(parts, b: Tensor, *, out: Tensor | None = None, bias: Tensor | None = None,
-                accumulate: bool = False, epilogue: str | None = None) -> Tensor:
-    """``cat([src[idx] or src for src, idx in parts], 1) @ b^T`` with the gather-cat fused into the
-    GEMM's operand load (fmd_gemm_gather_f32): ``parts`` is a list of up to three ``(src, index)``
-    (``index`` None: row r of ``src``; an int32 index may be a strided column view), ``b`` [N, K]
-    K-contiguous. Falls back to gather-cat + GEMM when the layout does not meet the fused kernel's
-    conditions (16-byte aligned rows, widths % 4, all but the last width % 16)."""
+                accumulate: bool = False, epilogue: str | None = None, row_add=None) -> Tensor:
+    """``cat([src[idx] or src for src, idx in parts], 1) @ b^T (+ q[qidx])`` with the gather-cat
+    fused into the GEMM's operand load (fmd_gemm_gather_f32): ``parts`` is a list of up to three
+    ``(src, index)`` (``index`` None: row r of ``src``; an int32 index may be a strided column
+    view), ``b`` [N, K] K-contiguous, ``row_add`` an optional ``(q [*, N], qidx or None)`` whose
+    gathered row is added to each output row. Falls back to gather-cat + GEMM (+ add) when the
+    layout does not meet the fused kernel's conditions (16-byte aligned rows, widths % 4, all but
+    the last width % 16)."""
     require_cuda(b, out, bias, *[src for src, _ in parts])
     if not 1 <= len(parts) <= 3:
         raise ValueError("gemm_gather takes one to three parts")
@@ -105,19 +107,37 @@ def gemm_gather(parts, b: Tensor, *, out: Tensor | None = None, bias: Tensor | N
         out = (torch.zeros if accumulate else torch.empty)((rows, n), dtype=torch.float32, device=b.device)
     elif out.shape != (rows, n) or out.dtype != torch.float32 or out.stride(1) != 1:
         raise ValueError("out must be float32 [M, N] with unit column stride")
+    q, qidx, qstride, ldq = None, None, 1, 0
+    if row_add is not None:
+        q, qidx = row_add
+        require_cuda(q, qidx)
+        if q.dim() != 2 or q.dtype != torch.float32 or q.shape[1] != n or q.stride(1) != 1:
+            raise ValueError(f"row_add must be float32 [*, {n}] with unit column stride")
+        ldq = q.stride(0)
+        if qidx is not None:
+            if qidx.dtype != torch.int32 or qidx.dim() != 1 or qidx.numel() != rows:
+                raise ValueError(f"row_add index must be int32 [{rows}]")
+            qstride = qidx.stride(0) if rows > 1 else 1
+        elif q.shape[0] != rows:
+            raise ValueError(f"row_add without an index needs {rows} rows")
     if rows == 0 or n == 0:
         return out
     status = _abi.load().fmd_gemm_gather_f32(
         len(parts), _abi.ptr_array(srcs), _abi.ptr_array(idx), _abi.array(_abi._i64, strides),
         _abi.array(_abi._i64, lds), _abi.array(_abi._i32, widths), rows, b.data_ptr(), b.stride(0),
-        _abi.ptr(bias), out.data_ptr(), out.stride(0) if rows > 1 else n, n, 1 if accumulate else 0,
-        _EPILOGUES[epilogue], stream())
+        _abi.ptr(q), _abi.ptr(qidx), qstride, ldq, _abi.ptr(bias), out.data_ptr(),
+        out.stride(0) if rows > 1 else n, n, 1 if accumulate else 0, _EPILOGUES[epilogue], stream())
     if status == _EUNSUPPORTED:
         from fastmd_amd.ops.gather_cat import _launch as gather_launch
 
+        if row_add is not None and (bias is not None or accumulate or epilogue not in (None, "none")):
+            raise ValueError("gemm_gather fallback: row_add with bias/accumulate/epilogue is not supported")
         a = torch.empty((rows, k), dtype=torch.float32, device=b.device)
         gather_launch(parts, rows, a)
-        return gemm(a, b, b_layout=0, bias=bias, out=out, accumulate=accumulate, epilogue=epilogue)
+        gemm(a, b, b_layout=0, bias=bias, out=out, accumulate=accumulate, epilogue=epilogue)
+        if row_add is not None:
+            out += q if qidx is None else q.index_select(0, qidx.long())
+        return out
     _abi.check(status, "fmd_gemm_gather_f32")
     return out
 
@@ -180,4 +200,6 @@ def edge_gemm(a: Tensor, w: Tensor, dtype: torch.dtype = torch.float32, *, bias:
             return gemm(a.to(torch.bfloat16), w.to(torch.bfloat16), b_layout=1, bias=bias, epilogue=epilogue)
         if dtype != torch.float32:
             raise ValueError(f"edge_gemm dtype must be float32 or bfloat16, got {dtype}")
-        return gemm(a, w, b_layout=1, bias=bias, epilogue=epilogue)
+        # the weight transposed once to K-contiguous [4F, 2F+8]: the layout of the fp32-accurate
+        # split-plane kernel
+        return gemm(a, w.t().contiguous(), b_layout=0, bias=bias, epilogue=epilogue)

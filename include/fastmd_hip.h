@@ -183,13 +183,18 @@ int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32
  * Replaces the reference's edge-row pair aligned_gather_cat3 -> linear
  * (triton_gather_cat.py:181-199 feeding triton_wide_gemm.py:482-515): same C as
  * fmd_gather_cat_f32 followed by fmd_gemm_f32, without the [M, K] row matrix in memory.
- * fp32-accurate (three bf16 planes per operand, six MFMA products). Needs 16-byte aligned
- * sources with lds_p % 4 == 0, widths % 4 == 0 and every width but the last % 16 == 0, b
- * aligned with ldb % 4 == 0: otherwise FMD_EUNSUPPORTED (the caller gathers, then multiplies). */
+ * fp32-accurate (three bf16 planes per operand, six MFMA products). row_add (optional, ld
+ * ld_row_add >= N) adds row row_add_index[r * row_add_index_stride] (or row r) of row_add to
+ * output row r before bias/accumulate/epilogue: a block of the gather-cat that depends only on
+ * an index (the receiver's features) multiplied once per node instead of once per edge. Needs
+ * 16-byte aligned sources with lds_p % 4 == 0, widths % 4 == 0 and every width but the last
+ * % 16 == 0, b aligned with ldb % 4 == 0: otherwise FMD_EUNSUPPORTED (the caller gathers, then
+ * multiplies). */
 int fmd_gemm_gather_f32(int32_t n_parts, const float* const* srcs, const int32_t* const* indices,
                         const int64_t* index_strides, const int64_t* lds, const int32_t* widths, int64_t m,
-                        const float* b, int64_t ldb, const float* bias, float* c, int64_t ldc, int64_t n,
-                        int32_t accumulate, int32_t epilogue, hipStream_t stream);
+                        const float* b, int64_t ldb, const float* row_add, const int32_t* row_add_index,
+                        int64_t row_add_index_stride, int64_t ld_row_add, const float* bias, float* c,
+                        int64_t ldc, int64_t n, int32_t accumulate, int32_t epilogue, hipStream_t stream);
 
 /* As fmd_gemm_f32 with bf16 operands (uint16 storage), fp32 accumulate and fp32 output, on
  * v_mfma_f32_32x32x16_bf16. Not in the reference (which has no bf16 GEMM on this path). */
@@ -249,19 +254,25 @@ int fmd_edge_geometry_f32(const float* positions, const float* cell, const int32
 int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, const float* gef0, int64_t ld0,
                               const float* gef1, int64_t ld1, const float* ggeo, const int64_t* n_edges,
                               int64_t e_cap, float* gvec, hipStream_t stream);
-/* A0[i], A1[i] = inv_avg * sum over the rows of centre i of the messages (h1 may be null). */
-int fmd_mace_message_f32(const float* z, const float* geo, const int32_t* edge_index, const int64_t* edge_offsets,
-                         const int64_t* n_edges, int64_t e_cap, int64_t n_atoms, int32_t channels, const float* h0,
-                         const float* h1, float inv_avg, float* A0, float* A1, hipStream_t stream);
-/* VJP of fmd_mace_message_f32: gz [E,4C] (may be null when w1ef is given), ggeo [E,4] (= or +=),
- * with w1ef ([nb, 4C], the radial rows of the edge GEMM weight) also gef[e] = gz[e] @ w1ef^T
- * [E,nb], and if gh0: the sender-side gh0/gh1 over the reverse CSR (accumulate_h bit 0: gh0 +=,
- * bit 1: gh1 +=; otherwise =). */
-int fmd_mace_message_bwd_f32(const float* z, const float* geo, const int32_t* edge_index, const int32_t* reverse,
+/* A0[i], A1[i] = inv_avg * sum over the rows of centre i of the messages (h1 may be null). The
+ * edge pre-activations are z[e] + zq[i] when zq ([N, 4C], the receiver block of the edge GEMM
+ * formed once per atom) is given, else z[e]. */
+int fmd_mace_message_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
+                         const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
+                         int32_t channels, const float* h0, const float* h1, float inv_avg, float* A0, float* A1,
+                         hipStream_t stream);
+/* VJP of fmd_mace_message_f32 (z, zq as there): gz [E,4C] (may be null when w1ef is given), gzsum [N,4C] (may be
+ * null: the sum of gz over each centre's rows, in row order), ggeo [E,4] (= or +=), with w1ef
+ * ([nb, 4C], the radial rows of the edge GEMM weight) also gef[e] = gz[e] @ w1ef^T [E,nb], and if
+ * gh0: the sender-side gh0/gh1 over the reverse CSR (accumulate_h bit 0: gh0 +=, bit 1: gh1 +=;
+ * otherwise =). */
+int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
+                             const int32_t* reverse,
                              const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
                              int32_t channels, const float* h0, const float* h1, const float* gA0, const float* gA1,
-                             float inv_avg, float* gz, float* ggeo, int32_t accumulate_geo, float* gh0, float* gh1,
-                             int32_t accumulate_h, const float* w1ef, int32_t nb, float* gef, hipStream_t stream);
+                             float inv_avg, float* gz, float* gzsum, float* ggeo, int32_t accumulate_geo, float* gh0,
+                             float* gh1, int32_t accumulate_h, const float* w1ef, int32_t nb, float* gef,
+                             hipStream_t stream);
 /* Symmetric contraction (correlation 3, L <= 1) and its VJP. */
 int fmd_mace_symcon_f32(const float* P0, const float* P1, const int32_t* elem, const float* Wc, const float* Wd,
                         int64_t n_atoms, int32_t channels, float* B0, float* B1, hipStream_t stream);
