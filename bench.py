@@ -226,6 +226,48 @@ def ops_sweep() -> list:
     return out
 
 
+def scaling_sweep(steps: int, warmup: int) -> list:
+    """the configs[2] model and 500 K NHC on k x k x k perovskite supercells,
+    k in {3, 6, 10, 15, 20} (135 .. 40 000 atoms), ``steps`` whole-step steps each after ``warmup``
+    untimed ones; beside each, the ragged (eager) builder at max_neighbors = 96 (one build) and
+    forced through its overflow-rebuild path from 8 slots (the slot count grows, the edges are
+    identical)."""
+    import torch
+
+    from fastmd_amd import systems
+    from fastmd_amd.graph.gpu_graph_builder import TensorGraphBuilder
+
+    out = []
+    for k in (3, 6, 10, 15, 20):
+        n_atoms = 5 * k ** 3
+        md = build_md(n_atoms, STEPS_PER_LAUNCH)
+        t = time_md(md, steps, warmup)
+        stats = md.whole_step_stats()
+        row = {"k": k, "atoms": n_atoms, "steps": steps, "ms_per_step": round(t / steps * 1e3, 4),
+               "md_steps_per_s": round(steps / t, 1), "atom_steps_per_s": round(n_atoms * steps / t, 1),
+               "e_capacity": stats["e_capacity"], "timed_events": md.timed_events}
+        del md
+        torch.cuda.empty_cache()
+        s = systems.perovskite(k)
+        pos = torch.tensor(s.positions, device="cuda")
+        for slots, key in ((96, "ragged_build_96"), (8, "ragged_build_overflow_from_8")):
+            def build(slots=slots):
+                b = TensorGraphBuilder(cell=torch.tensor(s.cell), atomic_numbers=torch.tensor(s.numbers),
+                                       atom_graph_cutoff=6.0, device="cuda", max_neighbors=slots)
+                g = b.build(pos)
+                return b, g
+            build()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            b, g = build()
+            torch.cuda.synchronize()
+            row[key] = {"ms": round((time.perf_counter() - t0) * 1e3, 3), "slots_after": b.max_neighbors,
+                        "edges": int(g.n_edges.item())}
+        log(f"scaling k={k} N={n_atoms}: {row['ms_per_step']} ms/step, ragged {row['ragged_build_96']}")
+        out.append(row)
+    return out
+
+
 def cpu_baseline(n_atoms: int, budget_s: float) -> dict:
     """The CPU oracle (PyTorch-CPU eager model forward+backward with index_select/index_add_/matmul,
     NumPy neighbour list and NHC) on this host, whole MD steps until ``budget_s`` elapsed."""
@@ -293,6 +335,9 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--quick", action="store_true", help="short run (profiling): no CPU baseline, fewer steps")
+    parser.add_argument("--scaling", action="store_true",
+                        help="only the configs[3] size sweep (135 .. 40 000 atoms, --steps-scaling steps each)")
+    parser.add_argument("--steps-scaling", type=int, default=1000)
     parser.add_argument("--ops", action="store_true",
                         help="only the configs[1] operator microbenchmark sweep (N x F), one JSON line")
     parser.add_argument("--roofline-only", action="store_true",
@@ -311,6 +356,9 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     steps_small = 200 if args.quick else args.steps_small
+    if args.scaling:
+        print(json.dumps({"scaling": scaling_sweep(args.steps_scaling, args.warmup)}), flush=True)
+        return 0
     if args.ops:
         print(json.dumps({"ops_sweep": ops_sweep(), "hbm_peak_GBps": HBM_PEAK_GBPS,
                           "fp32_mfma_peak_TFLOPs": FP32_MFMA_PEAK_TFLOPS}), flush=True)

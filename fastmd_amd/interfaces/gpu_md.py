@@ -45,6 +45,10 @@ def _atoms_arrays(atoms):
             getattr(atoms, "momenta", None))
 
 
+# runner counters summed over the runners a capacity growth retires (whole_step_stats covers the run)
+_CUMULATIVE_STATS = ("launches", "candidate_refreshes", "fallback_windows", "recovery_replays", "warmup_runs")
+
+
 class GPUResidentMolecularDynamics:
     def __init__(self, atoms, model=None, *, device: torch.device | str = "cuda", ensemble: str = "nvt_nhc",
                  temperature: float = 300.0, timestep: float = 1.0, taut: float = 100.0, tdamp: float | None = None,
@@ -91,6 +95,7 @@ class GPUResidentMolecularDynamics:
         self.capacity_policy = None
         self._capacity = None
         self.whole_step_capacity_history: list[int] = []
+        self._retired_stats: dict = {}
         self._graph_pool = None
         # F(q0) for the first pre-force half
         forces, energy = self.evaluate(self.integrator.positions)
@@ -167,6 +172,12 @@ class GPUResidentMolecularDynamics:
     def _grow_whole_step_runner(self, edge_count: int) -> None:
         """Capacity growth after an overflowed window: a larger tier, recaptured (gpu_md.py:1355-1410)."""
         old = self.whole_step_runner
+        # the retired runner's counters carry over into whole_step_stats()
+        for key, value in old.stats().items():
+            if key in _CUMULATIVE_STATS:
+                self._retired_stats[key] = self._retired_stats.get(key, 0) + value
+        self._retired_stats["max_edge_count"] = max(self._retired_stats.get("max_edge_count", 0),
+                                                    old.stats()["max_edge_count"])
         self._grow(edge_count)
         self.whole_step_runner = None
         del old
@@ -221,5 +232,8 @@ class GPUResidentMolecularDynamics:
         if self.whole_step_runner is None:
             return None
         stats = self.whole_step_runner.stats()
+        for key in _CUMULATIVE_STATS:
+            stats[key] += self._retired_stats.get(key, 0)
+        stats["max_edge_count"] = max(stats["max_edge_count"], self._retired_stats.get("max_edge_count", 0))
         stats["capacity_history"] = list(self.whole_step_capacity_history)
         return stats

@@ -284,3 +284,40 @@ def test_gemm_split_planes_dynamic_range(device):
     y = gemm(a.to(device), w.to(device), b_layout=0).cpu().double()
     rowmax = ref.abs().max(1, keepdim=True).values.clamp_min(1e-300)
     assert float(((y - ref).abs() / rowmax).max()) < 1e-5
+
+
+@pytest.mark.gpu
+def test_weighted_segment_sum_aggregate_and_count(device):
+    """weighted_segment_sum / aggregate / segment_count (the reference's index_add_ and atomic
+    variants) against float64 index_add_ on the CPU, on an unsorted segment index with empty
+    segments; the weighted form's VJP against float64 autograd."""
+    import torch
+
+    from fastmd_amd.ops.segment import aggregate, segment_count, weighted_segment_sum
+
+    g = torch.Generator().manual_seed(21)
+    rows, dim, nseg = 5000, 48, 700
+    seg = torch.randint(0, nseg - 50, (rows,), generator=g)  # the last 50 segments are empty
+    v = torch.randn(rows, dim, generator=g)
+    w = torch.randn(rows, dim, generator=g)
+    ref = torch.zeros(nseg, dim, dtype=torch.float64).index_add_(0, seg, (w * v).double())
+    vd, wd = v.to(device).requires_grad_(), w.to(device).requires_grad_()
+    out = weighted_segment_sum(wd, vd, seg.to(device), nseg)
+    assert oops.relative(out.detach().cpu().numpy(), ref.numpy()) < 1e-5
+    gout = torch.randn(nseg, dim, generator=g)
+    out.backward(gout.to(device))
+    assert oops.relative(vd.grad.cpu().numpy(), (gout[seg] * w).numpy()) < 1e-6
+    assert oops.relative(wd.grad.cpu().numpy(), (gout[seg] * v).numpy()) < 1e-6
+    w1 = torch.randn(rows, 1, generator=g)
+    out1 = weighted_segment_sum(w1.to(device), v.to(device), seg.to(device), nseg)
+    ref1 = torch.zeros(nseg, dim, dtype=torch.float64).index_add_(0, seg, (w1 * v).double())
+    assert oops.relative(out1.cpu().numpy(), ref1.numpy()) < 1e-5
+    counts = segment_count(seg.to(device), nseg).cpu()
+    assert torch.equal(counts, torch.bincount(seg, minlength=nseg))
+    mean = aggregate(v.to(device), seg.to(device), num_segment=nseg).cpu().double()
+    ref_sum = torch.zeros(nseg, dim, dtype=torch.float64).index_add_(0, seg, v.double())
+    ref_mean = ref_sum / counts.clamp_min(1).double()[:, None]
+    assert oops.relative(mean.numpy(), ref_mean.numpy()) < 1e-5
+    total = aggregate(v.to(device), seg.to(device), average=False).cpu().double()
+    assert total.shape[0] == int(seg.max()) + 1
+    assert oops.relative(total.numpy(), ref_sum[: total.shape[0]].numpy()) < 1e-5
