@@ -52,6 +52,10 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_mace_message_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _f32, _p, _p, _p]),
     "fmd_mace_message_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _p, _p, _f32,
                                                 _p, _p, _p, _i32, _p, _p, _i32, _p, _i32, _p, _p]),
+    "fmd_mace_node_fwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p, _p, _p,
+                                             _p, _p]),
+    "fmd_mace_node_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32,
+                                             _p, _p, _p, _p, _p]),
     "fmd_mace_symcon_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p]),
     "fmd_mace_symcon_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p]),
     "fmd_mace_energy_f32": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _p, _p, _f32, _f32, _i64, _p, _p]),

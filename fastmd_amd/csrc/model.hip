@@ -11,6 +11,7 @@
 // (C = 64 * CPL). Node features: h0 [N, C], h1 [N, 3, C]. Per edge z [E, 4C] = the four path
 // weight blocks (a | b | c | d) before the SiLU.
 #include "common.h"
+#include "mace_math.h"
 
 namespace {
 
@@ -413,11 +414,9 @@ __global__ void symcon_kernel(const float* P0, const float* P1, const int32_t* e
   const float p0 = P0[k];
   const float px = P1[(i * 3 + 0) * C + ch], py = P1[(i * 3 + 1) * C + ch], pz = P1[(i * 3 + 2) * C + ch];
   const float n1 = px * px + py * py + pz * pz;
-  const float* c = Wc + (int64_t)el * 5 * C + ch;
-  B0[k] = c[0] * p0 + c[C] * p0 * p0 + c[2 * C] * n1 + c[3 * C] * p0 * p0 * p0 + c[4 * C] * p0 * n1;
+  B0[k] = symcon_b0(p0, n1, Wc + (int64_t)el * 5 * C + ch, C);
   if (B1) {
-    const float* d = Wd + (int64_t)el * 4 * C + ch;
-    const float q = d[0] + d[C] * p0 + d[2 * C] * p0 * p0 + d[3 * C] * n1;
+    const float q = symcon_q(p0, n1, Wd + (int64_t)el * 4 * C + ch, C);
     B1[(i * 3 + 0) * C + ch] = q * px;
     B1[(i * 3 + 1) * C + ch] = q * py;
     B1[(i * 3 + 2) * C + ch] = q * pz;
@@ -432,30 +431,16 @@ __global__ void symcon_bwd_kernel(const float* P0, const float* P1, const int32_
   const int64_t i = k / C;
   const int ch = (int)(k - i * C);
   const int el = elem[i];
-  const float p0 = P0[k];
   const float p[3] = {P1[(i * 3 + 0) * C + ch], P1[(i * 3 + 1) * C + ch], P1[(i * 3 + 2) * C + ch]};
-  const float n1 = p[0] * p[0] + p[1] * p[1] + p[2] * p[2];
-  const float* c = Wc + (int64_t)el * 5 * C + ch;
-  const float gb0 = gB0[k];
-  float gp0 = gb0 * (c[0] + 2.0f * c[C] * p0 + 3.0f * c[3 * C] * p0 * p0 + c[4 * C] * n1);
-  float gn1 = gb0 * (c[2 * C] + c[4 * C] * p0);
-  float gp[3] = {0.f, 0.f, 0.f};
-  if (gB1) {
-    const float* d = Wd + (int64_t)el * 4 * C + ch;
-    const float q = d[0] + d[C] * p0 + d[2 * C] * p0 * p0 + d[3 * C] * n1;
-    float gq = 0.f;
-#pragma unroll
-    for (int x = 0; x < 3; ++x) {
-      const float g = gB1[(i * 3 + x) * C + ch];
-      gp[x] = g * q;
-      gq += g * p[x];
-    }
-    gp0 += gq * (d[C] + 2.0f * d[2 * C] * p0);
-    gn1 += gq * d[3 * C];
-  }
+  float gb1[3] = {0.f, 0.f, 0.f};
+  if (gB1)
+    for (int x = 0; x < 3; ++x) gb1[x] = gB1[(i * 3 + x) * C + ch];
+  float gp0, gp[3];
+  symcon_vjp(P0[k], p, Wc + (int64_t)el * 5 * C + ch, Wd + (int64_t)el * 4 * C + ch, C, gB0[k], gB1 != nullptr, gb1,
+             gp0, gp);
   gP0[k] = gp0;
 #pragma unroll
-  for (int x = 0; x < 3; ++x) gP1[(i * 3 + x) * C + ch] = gp[x] + 2.0f * gn1 * p[x];
+  for (int x = 0; x < 3; ++x) gP1[(i * 3 + x) * C + ch] = gp[x];
 }
 
 // ------------------------------------------------------------------------------------------

@@ -46,6 +46,12 @@ _CAPACITY_STEP = CapacityStep(u_step=32, min_pad_u=32, u_thermal_factor=1.02)
 # edge lists from this many rows form the receiver block of the edge GEMM per atom (below it the
 # two extra node GEMMs cost more launch latency than the halved edge GEMM saves)
 HOIST_MIN_ROWS = 16384
+# the node side of each layer (two GEMMs, the contraction, three GEMMs; and its VJP) as one fused
+# launch per direction (fmd_mace_node_fwd/bwd_f32) instead of the chain of six. Off: each 32-atom
+# tile walks its phases' 24 K-slices one after the other, which measured slower (50 us per launch
+# at 135 atoms, 73 / 117 us at 10 000) than the six short launches it replaces; kept tested
+# against the oracle beside the chain.
+FUSED_NODE = False
 
 
 @dataclass(frozen=True)
@@ -114,6 +120,26 @@ class MaceLike(nn.Module):
         hit = cache.get(t)
         if hit is None or hit[0] != key:
             hit = (key, w.detach().t().contiguous())
+            cache[t] = hit
+        return hit[1]
+
+    def node_weights(self, t: int) -> dict:
+        """Layer t's node-side weights in the layouts of the fused node kernels ([columns, K],
+        K-contiguous): wm0t = Wm0^T, wm1t = Wm1^T, wout0 = [Wo0; Wsc0]^T, wout1 = [Wo1; 0]^T (forward)
+        and wo0st = [Wo0; Wsc0], wo1st = [Wo1; 0] (VJP); rebuilt when a weight changes in place."""
+        layer = self.layers[t]
+        mats = (layer.Wm0, layer.Wm1, layer.Wo0, layer.Wo1, layer.Wsc0)
+        key = tuple((w.data_ptr(), w._version, w.device) for w in mats)
+        cache = self.__dict__.setdefault("_node_w_cache", {})
+        hit = cache.get(t)
+        if hit is None or hit[0] != key:
+            wm0, wm1, wo0, wo1, wsc0 = (w.detach() for w in mats)
+            zero = torch.zeros_like(wo1)
+            hit = (key, {"wm0t": wm0.t().contiguous(), "wm1t": wm1.t().contiguous(),
+                         "wout0": torch.cat([wo0, wsc0], 0).t().contiguous(),
+                         "wout1": torch.cat([wo1, zero], 0).t().contiguous(),
+                         "wo0st": torch.cat([wo0, wsc0], 0).contiguous(),
+                         "wo1st": torch.cat([wo1, zero], 0).contiguous()})
             cache[t] = hit
         return hit[1]
 
@@ -222,15 +248,27 @@ class _MaceLikeEnergy(Function):
             A1 = _empty(n, 3, C, device=dev)
             _call("fmd_mace_message_f32", z.data_ptr(), _abi.ptr(q), geo.data_ptr(), ei.data_ptr(), off.data_ptr(),
                   n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), inv_avg, A0.data_ptr(), A1.data_ptr())
-            P0 = gemm(A0, layer.Wm0, b_layout=1)
-            P1 = gemm(A1.view(3 * n, C), layer.Wm1, b_layout=1).view(n, 3, C)
             B0 = _empty(n, C, device=dev)
             B1 = None if last else _empty(n, 3, C, device=dev)
-            _call("fmd_mace_symcon_f32", P0.data_ptr(), P1.data_ptr(), elem.data_ptr(), layer.Wc.data_ptr(),
-                  layer.Wd.data_ptr(), n, C, B0.data_ptr(), _abi.ptr(B1))
-            h0n = gemm(B0, layer.Wo0, b_layout=1)
-            gemm(h0, layer.Wsc0, b_layout=1, out=h0n, accumulate=True)
-            h1n = None if last else gemm(B1.view(3 * n, C), layer.Wo1, b_layout=1).view(n, 3, C)
+            if FUSED_NODE:
+                # the node side of the layer in one launch per 32-atom tile
+                w = model.node_weights(t)
+                P0 = _empty(n, C, device=dev)
+                P1 = _empty(n, 3, C, device=dev)
+                h0n = _empty(n, C, device=dev)
+                h1n = None if last else _empty(n, 3, C, device=dev)
+                _call("fmd_mace_node_fwd_f32", A0.data_ptr(), A1.data_ptr(), h0.data_ptr(), elem.data_ptr(),
+                      w["wm0t"].data_ptr(), w["wm1t"].data_ptr(), layer.Wc.data_ptr(), layer.Wd.data_ptr(),
+                      w["wout0"].data_ptr(), w["wout1"].data_ptr(), n, C, P0.data_ptr(), P1.data_ptr(),
+                      B0.data_ptr(), _abi.ptr(B1), h0n.data_ptr(), _abi.ptr(h1n))
+            else:
+                P0 = gemm(A0, layer.Wm0, b_layout=1)
+                P1 = gemm(A1.view(3 * n, C), layer.Wm1, b_layout=1).view(n, 3, C)
+                _call("fmd_mace_symcon_f32", P0.data_ptr(), P1.data_ptr(), elem.data_ptr(), layer.Wc.data_ptr(),
+                      layer.Wd.data_ptr(), n, C, B0.data_ptr(), _abi.ptr(B1))
+                h0n = gemm(B0, layer.Wo0, b_layout=1)
+                gemm(h0, layer.Wsc0, b_layout=1, out=h0n, accumulate=True)
+                h1n = None if last else gemm(B1.view(3 * n, C), layer.Wo1, b_layout=1).view(n, 3, C)
             saved.append((h0, h1, z, q, P0, P1))
             if t == 0:
                 h_first = h0n
@@ -278,15 +316,33 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
     for t in reversed(range(L)):
         layer = model.layers[t]
         h0, h1, z, q, P0, P1 = ctx.saved[t]
-        gB0 = gemm(g_out0, layer.Wo0, b_layout=0)
-        gB1 = None if g_out1 is None else gemm(g_out1.reshape(3 * n, C), layer.Wo1, b_layout=0)
         gP0 = _empty(n, C, device=dev)
         gP1 = _empty(n, 3, C, device=dev)
-        _call("fmd_mace_symcon_bwd_f32", P0.data_ptr(), P1.data_ptr(), inputs.elem.data_ptr(),
-              layer.Wc.data_ptr(), layer.Wd.data_ptr(), gB0.data_ptr(), _abi.ptr(gB1), n, C, gP0.data_ptr(),
-              gP1.data_ptr())
-        gA0 = gemm(gP0, layer.Wm0, b_layout=0)
-        gA1 = gemm(gP1.view(3 * n, C), layer.Wm1, b_layout=0)
+        g_in0 = None
+        if FUSED_NODE:
+            # node side of the layer's VJP in one launch per 32-atom tile; with t > 0 it also forms
+            # this layer's input gradient through the residual, g_in0 = g_out0 Wsc0^T (added to the
+            # first readout's gradient in the second layer)
+            w = model.node_weights(t)
+            gB0 = _empty(n, C, device=dev)
+            gB1 = None if g_out1 is None else _empty(n, 3, C, device=dev)
+            gA0 = _empty(n, C, device=dev)
+            gA1 = _empty(n, 3, C, device=dev)
+            if t > 0:
+                g_in0 = gha if t == 1 else _empty(n, C, device=dev)
+            _call("fmd_mace_node_bwd_f32", g_out0.data_ptr(), _abi.ptr(g_out1), P0.data_ptr(), P1.data_ptr(),
+                  inputs.elem.data_ptr(), w["wo0st"].data_ptr(), w["wo1st"].data_ptr(), layer.Wc.data_ptr(),
+                  layer.Wd.data_ptr(), layer.Wm0.data_ptr(), layer.Wm1.data_ptr(), n, C, gB0.data_ptr(),
+                  _abi.ptr(gB1), _abi.ptr(g_in0), 1 if t == 1 else 0, gP0.data_ptr(), gP1.data_ptr(),
+                  gA0.data_ptr(), gA1.data_ptr())
+        else:
+            gB0 = gemm(g_out0, layer.Wo0, b_layout=0)
+            gB1 = None if g_out1 is None else gemm(g_out1.reshape(3 * n, C), layer.Wo1, b_layout=0)
+            _call("fmd_mace_symcon_bwd_f32", P0.data_ptr(), P1.data_ptr(), inputs.elem.data_ptr(),
+                  layer.Wc.data_ptr(), layer.Wd.data_ptr(), gB0.data_ptr(), _abi.ptr(gB1), n, C, gP0.data_ptr(),
+                  gP1.data_ptr())
+            gA0 = gemm(gP0, layer.Wm0, b_layout=0)
+            gA1 = gemm(gP1.view(3 * n, C), layer.Wm1, b_layout=0)
         acc_geo = 1 if t < L - 1 else 0
         if t == 0:
             # the first layer's inputs are the element embedding (no position dependence): only
@@ -305,7 +361,8 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
         gef = _empty(e_cap, nb, device=dev)
         # this layer's inputs: residual (plus, in the second layer, the first readout's
         # gradient of the first layer's output), sender side of the messages, gather-cat rows
-        g_in0 = gemm(g_out0, layer.Wsc0, b_layout=0, out=gha if t == 1 else None, accumulate=t == 1)
+        if g_in0 is None:
+            g_in0 = gemm(g_out0, layer.Wsc0, b_layout=0, out=gha if t == 1 else None, accumulate=t == 1)
         g_in1 = _empty(n, 3, C, device=dev) if h1 is not None else None
         w1ef = layer.W1[2 * C:]
         _call("fmd_mace_message_bwd_f32", z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(), ei.data_ptr(),

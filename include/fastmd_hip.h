@@ -273,6 +273,25 @@ int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, 
                              float inv_avg, float* gz, float* gzsum, float* ggeo, int32_t accumulate_geo, float* gh0,
                              float* gh1, int32_t accumulate_h, const float* w1ef, int32_t nb, float* gef,
                              hipStream_t stream);
+/* The node side of one interaction layer fused per 32-atom tile (one launch instead of six),
+ * fp32-accurate on the bf16 matrix cores: P0 = A0 Wm0, P1_x = A1_x Wm1, the symmetric
+ * contraction (B0, B1: workspace, [N,C] and [N,3,C]), h0n = B0 Wo0 + h0 Wsc0, h1n_x = B1_x Wo1
+ * (h1n null: last layer, no vector output). Weights laid out [columns, K] K-contiguous:
+ * wm0t = Wm0^T, wm1t = Wm1^T [C, C]; wout0 = [Wo0; Wsc0]^T, wout1 = [Wo1; 0]^T [C, 2C]. Same
+ * results as fmd_gemm_f32 + fmd_mace_symcon_f32 chains to fp32 rounding. No reference
+ * counterpart: it replaces the model's node-side chain (mace.py:386 runs mace-torch there). */
+int fmd_mace_node_fwd_f32(const float* A0, const float* A1, const float* h0, const int32_t* elem, const float* wm0t,
+                          const float* wm1t, const float* Wc, const float* Wd, const float* wout0, const float* wout1,
+                          int64_t n_atoms, int32_t channels, float* P0, float* P1, float* B0, float* B1, float* h0n,
+                          float* h1n, hipStream_t stream);
+/* VJP of fmd_mace_node_fwd_f32 per 32-atom tile: gB0 = g0 Wo0^T, gB1_x = g1_x Wo1^T (g1 null: no
+ * vector input gradient), g_in0 (=, or += when accumulate_in0; null: not formed) = g0 Wsc0^T,
+ * the contraction VJP (gP0, gP1), gA0 = gP0 Wm0^T, gA1_x = gP1_x Wm1^T. wo0st = [Wo0; Wsc0]
+ * [2C, C], wo1st = [Wo1; 0] [2C, C], wm0 = Wm0, wm1 = Wm1 [C, C] (row-major [in, out] as stored). */
+int fmd_mace_node_bwd_f32(const float* g0, const float* g1, const float* P0, const float* P1, const int32_t* elem,
+                          const float* wo0st, const float* wo1st, const float* Wc, const float* Wd, const float* wm0,
+                          const float* wm1, int64_t n_atoms, int32_t channels, float* gB0, float* gB1, float* gin0,
+                          int32_t accumulate_in0, float* gP0, float* gP1, float* gA0, float* gA1, hipStream_t stream);
 /* Symmetric contraction (correlation 3, L <= 1) and its VJP. */
 int fmd_mace_symcon_f32(const float* P0, const float* P1, const int32_t* elem, const float* Wc, const float* Wd,
                         int64_t n_atoms, int32_t channels, float* B0, float* B1, hipStream_t stream);
