@@ -52,6 +52,10 @@ HOIST_MIN_ROWS = 16384
 # at 135 atoms, 73 / 117 us at 10 000) than the six short launches it replaces; kept tested
 # against the oracle beside the chain.
 FUSED_NODE = False
+# Timing hook of the edge GEMM launches: when a list, each eager (uncaptured) forward appends
+# (start event, end event, (M, K, N)) recorded around its edge GEMMs on the current stream. The
+# benchmark uses it to time the dominant kernel in the context of the step; None in normal runs.
+EDGE_GEMM_EVENTS: list | None = None
 
 
 @dataclass(frozen=True)
@@ -238,12 +242,20 @@ class _MaceLikeEnergy(Function):
             # operand load. On large edge lists the receiver block h0[dst] @ W1[C:2C], the same for
             # every row of a centre, is formed once per atom (q, [N, 4C]) and added by the message
             # kernels, and the edge GEMM multiplies [h0[src] | ef] (K = C + nb).
+            timed = EDGE_GEMM_EVENTS is not None and not torch.cuda.is_current_stream_capturing()
             if e_cap >= HOIST_MIN_ROWS:
                 q = gemm(h0, model.w1_receiver_t(t), b_layout=0)
-                z = gemm_gather([(h0, ei[:, 1]), (ef, None)], model.w1_sender_t(t))
+                parts, w1 = [(h0, ei[:, 1]), (ef, None)], model.w1_sender_t(t)
             else:
                 q = None
-                z = gemm_gather([(h0, ei[:, 1]), (h0, ei[:, 0]), (ef, None)], model.w1_t(t))
+                parts, w1 = [(h0, ei[:, 1]), (h0, ei[:, 0]), (ef, None)], model.w1_t(t)
+            if timed:
+                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                ev[0].record()
+            z = gemm_gather(parts, w1)
+            if timed:
+                ev[1].record()
+                EDGE_GEMM_EVENTS.append((ev[0], ev[1], (e_cap, w1.shape[1], w1.shape[0])))
             A0 = _empty(n, C, device=dev)
             A1 = _empty(n, 3, C, device=dev)
             _call("fmd_mace_message_f32", z.data_ptr(), _abi.ptr(q), geo.data_ptr(), ei.data_ptr(), off.data_ptr(),
