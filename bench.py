@@ -27,6 +27,7 @@ HBM_PEAK_GBPS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 SPLIT_PRODUCTS = 6  # fp32-accurate GEMM: three bf16 planes per operand, six MFMA products
+SPIN_CYCLES = 20_000_000  # GPU clock cycles of torch.cuda._sleep (several ms)
 STEPS_PER_LAUNCH = 10
 
 
@@ -91,12 +92,13 @@ def gemm_roofline(md) -> dict:
     """The dominant kernel of the 10 000-atom step: the edge GEMM of the interaction,
     z = [h0[src] | ef] @ W1[sender and radial rows] (the receiver block h0[dst] @ W1[C:2C] is formed
     per atom and added by the message kernels), with the gather-cat fused into the operand load
-    (gemm_x3_kernel: [e_cap, C+8] x [C+8, 4C], fp32-accurate as six bf16 MFMA products). It is
-    timed in the context of the step: HIP events on torch's current stream (the stream it is
-    launched on) around every edge GEMM of 10 eager force evaluations at the run's final state
-    (its edge list, capacity and features), the model's own timing hook. Algorithmic flops =
-    2 M K N per launch; the ceiling of fp32 work done this way is the dense bf16 MFMA peak over
-    the six products. ``isolated_launch_us`` is the same launch repeated back to back."""
+    (gemm_x3_kernel: [e_cap, C+8] x [C+8, 4C] in the second layer, fp32-accurate as six bf16 MFMA
+    products). It is timed in the context of the step: HIP events on torch's current stream (the
+    stream it is launched on) around every edge GEMM of 10 eager force evaluations at the run's
+    final state (its edge list, capacity and features), the model's own timing hook; each
+    evaluation is queued behind a spin kernel so that no host latency falls inside the event
+    pairs. Algorithmic flops = 2 M K N per launch; the ceiling of fp32 work done this way is the
+    dense bf16 MFMA peak over the six products. ``isolated_launch_us`` is the same launch repeated back to back."""
     import torch
 
     from fastmd_amd.models import mace_like
@@ -108,6 +110,10 @@ def gemm_roofline(md) -> dict:
     mace_like.EDGE_GEMM_EVENTS = events = []
     try:
         for _ in range(10):
+            # a spin kernel ahead of each evaluation keeps the GPU busy while the host enqueues
+            # the evaluation's ~40 launches, so the GPU runs them back to back as in the captured
+            # step (no host-latency gaps inside the event pairs)
+            torch.cuda._sleep(SPIN_CYCLES)
             runner._evaluate(md.integrator.positions)
         torch.cuda.synchronize()
     finally:

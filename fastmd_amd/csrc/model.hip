@@ -13,6 +13,8 @@
 #include "common.h"
 #include "mace_math.h"
 
+#include <initializer_list>
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -24,7 +26,8 @@ __device__ __forceinline__ int64_t real_rows(const int64_t* n_edges, int64_t e_c
   return e < e_cap ? e : e_cap;
 }
 
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// 1 / (1 + e^-x) with the hardware reciprocal (1 ulp): the saturated ends give exactly 0 and 1
+__device__ __forceinline__ float sigmoid(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 // ------------------------------------------------------------------------------------------
 // edge geometry: geo[e] = (ux, uy, uz, r, fcut, dfcut, 0, 0); ef[e, n] = b_n(r) fcut(r);
@@ -125,7 +128,70 @@ __global__ void edge_geometry_bwd_kernel(const float* geo, const float* def, int
 // interaction: forward message + receiver sum. One wave per centre node i.
 //   w = silu(z_e) * fcut_e; proj = h1_j . u; m0 = wa h0_j + wc proj; m1_x = wb h0_j u_x + wd h1_j,x
 //   A0_i = inv_avg * sum_e m0, A1_i = inv_avg * sum_e m1
+// Without h1 (a layer whose vector features are zero, where wc and wd meet only zeros) z holds
+// just the a | b blocks: [E, 2C]. zq, when given, is the receiver block of z per atom ([N, the
+// same width]), added to every row of the centre.
+//
+// Latency: per 64 rows the wave loads the rows' neighbour index and geometry once (one row per
+// lane, coalesced) and broadcasts them with readlane; each group of kGroup rows then issues all
+// of its z, h0[j] and h1[j] loads before any arithmetic, so a group costs one memory round trip
+// instead of two per row. Rows are accumulated in row order (deterministic).
 // ------------------------------------------------------------------------------------------
+constexpr int kGroup = 4;
+
+__device__ __forceinline__ int bcast(int v, int s) { return __builtin_amdgcn_readlane(v, s); }
+__device__ __forceinline__ float bcast(float v, int s) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), s));
+}
+
+// CPL consecutive floats (4 * CPL-byte aligned)
+template <int CPL>
+__device__ __forceinline__ void load_ch(const float* p, float (&v)[CPL]) {
+  if constexpr (CPL == 4) {
+    const float4 t = *reinterpret_cast<const float4*>(p);
+    v[0] = t.x;
+    v[1] = t.y;
+    v[2] = t.z;
+    v[3] = t.w;
+  } else if constexpr (CPL == 2) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    v[0] = t.x;
+    v[1] = t.y;
+  } else {
+    v[0] = p[0];
+  }
+}
+
+// one row's neighbour index and geometry (zeros for ok == false)
+struct RowGeo {
+  int j;
+  float ux, uy, uz, fc;
+};
+
+__device__ __forceinline__ RowGeo row_geo(const float* geo, const int32_t* edge_index, int64_t e, bool ok) {
+  RowGeo r{0, 0.f, 0.f, 0.f, 0.f};
+  if (ok) {
+    r.j = edge_index[2 * e + 1];
+    const float4 g = *reinterpret_cast<const float4*>(geo + 8 * e);
+    r.ux = g.x;
+    r.uy = g.y;
+    r.uz = g.z;
+    r.fc = geo[8 * e + 4];
+  }
+  return r;
+}
+
+// the wave's node (uniform) and its real rows [lo, hi)
+__device__ __forceinline__ int64_t wave_rows(const int64_t* off, const int64_t* n_edges, int64_t e_cap, int64_t i,
+                                             int64_t& lo) {
+  const int64_t rows = real_rows(n_edges, e_cap);
+  int64_t hi = off[i + 1];
+  lo = off[i];
+  hi = hi < rows ? hi : rows;
+  lo = lo < hi ? lo : hi;
+  return hi;
+}
+
 template <int CPL, bool H1>
 __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const float* zq, const float* geo,
                                                            const int32_t* edge_index, const int64_t* off,
@@ -133,13 +199,12 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
                                                            const float* h0, const float* h1, float inv_avg, float* A0,
                                                            float* A1) {
   constexpr int C = 64 * CPL;
+  constexpr int NZ = H1 ? 4 : 2;  // z blocks in a row
   const int lane = threadIdx.x & 63;
-  const int64_t i = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64;
+  const int64_t i = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   if (i >= n) return;
-  const int64_t rows = real_rows(n_edges, e_cap);
-  int64_t lo = off[i], hi = off[i + 1];
-  hi = hi < rows ? hi : rows;
-  lo = lo < hi ? lo : hi;
+  int64_t lo;
+  const int64_t hi = wave_rows(off, n_edges, e_cap, i, lo);
   float a0[CPL], a1[3][CPL];
 #pragma unroll
   for (int q = 0; q < CPL; ++q) {
@@ -147,38 +212,67 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
     a1[0][q] = a1[1][q] = a1[2][q] = 0.f;
   }
   const int c0 = lane * CPL;
-  float qz[4][CPL];  // the centre's receiver block of z (zq[i]), 0 when z is complete
+  float qz[NZ][CPL];  // the centre's receiver block of z (zq[i]), 0 when z is complete
 #pragma unroll
-  for (int b = 0; b < 4; ++b)
+  for (int b = 0; b < NZ; ++b) {
+    if (zq) {
+      load_ch<CPL>(zq + i * NZ * C + b * C + c0, qz[b]);
+    } else {
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) qz[b][q] = zq ? zq[i * 4 * C + b * C + c0 + q] : 0.f;
-  for (int64_t e = lo; e < hi; ++e) {
-    const float* g = geo + 8 * e;
-    const float ux = g[0], uy = g[1], uz = g[2], fc = g[4];
-    const int64_t j = edge_index[2 * e + 1];
-    const float* ze = z + e * 4 * C + c0;
+      for (int q = 0; q < CPL; ++q) qz[b][q] = 0.f;
+    }
+  }
+  for (int64_t base = lo; base < hi; base += 64) {
+    const int cnt = (int)(hi - base < 64 ? hi - base : 64);
+    const RowGeo m = row_geo(geo, edge_index, base + lane, lane < cnt);
+    for (int u0 = 0; u0 < cnt; u0 += kGroup) {
+      float zr[kGroup][NZ][CPL], hj[kGroup][CPL], hv[kGroup][3][CPL];
+      float ux[kGroup], uy[kGroup], uz[kGroup], fc[kGroup];
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) {
-      const float za = ze[q] + qz[0][q], zb = ze[C + q] + qz[1][q];
-      const float wa = za * sigmoid(za) * fc, wb = zb * sigmoid(zb) * fc;
-      const float hj = h0[j * C + c0 + q];
-      float m0 = wa * hj;
-      const float t = wb * hj;
-      float m1x = t * ux, m1y = t * uy, m1z = t * uz;
-      if (H1) {
-        const float zc = ze[2 * C + q] + qz[2][q], zd = ze[3 * C + q] + qz[3][q];
-        const float wc = zc * sigmoid(zc) * fc, wd = zd * sigmoid(zd) * fc;
-        const float hx = h1[(j * 3 + 0) * C + c0 + q], hy = h1[(j * 3 + 1) * C + c0 + q],
-                    hz = h1[(j * 3 + 2) * C + c0 + q];
-        m0 += wc * (hx * ux + hy * uy + hz * uz);
-        m1x += wd * hx;
-        m1y += wd * hy;
-        m1z += wd * hz;
+      for (int u = 0; u < kGroup; ++u) {
+        const int s = u0 + u < cnt ? u0 + u : cnt - 1;
+        const int64_t j = bcast(m.j, s);
+        ux[u] = bcast(m.ux, s);
+        uy[u] = bcast(m.uy, s);
+        uz[u] = bcast(m.uz, s);
+        fc[u] = u0 + u < cnt ? bcast(m.fc, s) : 0.f;  // a row past the end adds exact zeros
+        const float* ze = z + (base + s) * (NZ * C) + c0;
+#pragma unroll
+        for (int b = 0; b < NZ; ++b) load_ch<CPL>(ze + b * C, zr[u][b]);
+        load_ch<CPL>(h0 + j * C + c0, hj[u]);
+        if (H1) {
+#pragma unroll
+          for (int x = 0; x < 3; ++x) load_ch<CPL>(h1 + (j * 3 + x) * C + c0, hv[u][x]);
+        }
       }
-      a0[q] += m0;
-      a1[0][q] += m1x;
-      a1[1][q] += m1y;
-      a1[2][q] += m1z;
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        // no early exit for the rows past the end (fc = 0): a branch here would let the compiler
+        // move the group's loads behind it, one round trip per row again
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) {
+          const float za = zr[u][0][q] + qz[0][q], zb = zr[u][1][q] + qz[1][q];
+          const float wa = za * sigmoid(za) * fc[u], wb = zb * sigmoid(zb) * fc[u];
+          const float hjq = hj[u][q];
+          float m0 = wa * hjq;
+          const float t = wb * hjq;
+          float m1x = t * ux[u], m1y = t * uy[u], m1z = t * uz[u];
+          if (H1) {
+            const float zc = zr[u][NZ > 2 ? 2 : 0][q] + qz[NZ > 2 ? 2 : 0][q];
+            const float zd = zr[u][NZ > 2 ? 3 : 0][q] + qz[NZ > 2 ? 3 : 0][q];
+            const float wc = zc * sigmoid(zc) * fc[u], wd = zd * sigmoid(zd) * fc[u];
+            const float hx = hv[u][0][q], hy = hv[u][1][q], hz = hv[u][2][q];
+            m0 += wc * (hx * ux[u] + hy * uy[u] + hz * uz[u]);
+            m1x += wd * hx;
+            m1y += wd * hy;
+            m1z += wd * hz;
+          }
+          a0[q] += m0;
+          a1[0][q] += m1x;
+          a1[1][q] += m1y;
+          a1[2][q] += m1z;
+        }
+      }
     }
   }
 #pragma unroll
@@ -192,11 +286,13 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
 
 // VJP, edge side (one wave per centre node i, its rows e): with gA = inv_avg * (gA0_i, gA1_i),
 //   g_wa = gA0 h0_j, g_wb = h0_j (gA1 . u), g_wc = gA0 proj, g_wd = sum_x gA1_x h1_j,x
-//   g_z = g_w * fcut * silu'(z)            -> gz [E, 4C]
+//   g_z = g_w * fcut * silu'(z)            -> gz [E, NZ C] (NZ = 4 with h1, else 2)
 //   g_fcut = sum_ch g_w * silu(z), g_u_x = sum_ch (gA0 wc h1_j,x + gA1_x wb h0_j)  -> ggeo [E, 4]
 // With w1ef (the radial-basis rows of the edge GEMM weight, [nb, 4C]) the kernel also forms
 // gef[e, n] = sum_k gz[e, k] w1ef[n, k] (the radial block of the gather-cat row gradient) and
 // gz itself may be null (not stored): the first layer needs no other part of gz @ W1^T.
+// gzsum[i] = sum over the centre's rows of gz (the receiver block's gradient when zq is formed
+// per atom). Row loads as in message_kernel.
 constexpr int kMaxBasis = 16;
 
 template <int CPL, bool H1>
@@ -206,131 +302,199 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     const float* gA1, float inv_avg, float* gz, float* gzsum, float* ggeo, int accumulate_geo, const float* w1ef,
     int nb, float* gef) {
   constexpr int C = 64 * CPL;
-  __shared__ float s_w[kMaxBasis * 4 * C];
+  constexpr int NZ = H1 ? 4 : 2;
+  extern __shared__ float s_w[];  // w1ef [nb, 4C] when given (dynamic: nb * 4C floats)
   const int lane = threadIdx.x & 63;
   if (w1ef) {
     for (int k = threadIdx.x; k < nb * 4 * C; k += blockDim.x) s_w[k] = w1ef[k];
     __syncthreads();
   }
-  const int64_t i = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64;
+  const int64_t i = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   if (i >= n) return;
-  const int64_t rows = real_rows(n_edges, e_cap);
-  int64_t lo = off[i], hi = off[i + 1];
-  hi = hi < rows ? hi : rows;
-  lo = lo < hi ? lo : hi;
+  int64_t lo;
+  const int64_t hi = wave_rows(off, n_edges, e_cap, i, lo);
   const int c0 = lane * CPL;
   float g0[CPL], g1[3][CPL];
+  load_ch<CPL>(gA0 + i * C + c0, g0);
+#pragma unroll
+  for (int x = 0; x < 3; ++x) load_ch<CPL>(gA1 + (i * 3 + x) * C + c0, g1[x]);
 #pragma unroll
   for (int q = 0; q < CPL; ++q) {
-    g0[q] = gA0[i * C + c0 + q] * inv_avg;
-    g1[0][q] = gA1[(i * 3 + 0) * C + c0 + q] * inv_avg;
-    g1[1][q] = gA1[(i * 3 + 1) * C + c0 + q] * inv_avg;
-    g1[2][q] = gA1[(i * 3 + 2) * C + c0 + q] * inv_avg;
+    g0[q] *= inv_avg;
+    g1[0][q] *= inv_avg;
+    g1[1][q] *= inv_avg;
+    g1[2][q] *= inv_avg;
   }
-  float gs[4][CPL];  // sum of gz over the centre's rows (in row order)
-  float qz[4][CPL];  // the centre's receiver block of z (zq[i]), 0 when z is complete
+  float gs[NZ][CPL];  // sum of gz over the centre's rows (in row order)
+  float qz[NZ][CPL];  // the centre's receiver block of z (zq[i]), 0 when z is complete
 #pragma unroll
-  for (int b = 0; b < 4; ++b)
+  for (int b = 0; b < NZ; ++b) {
+    if (zq) {
+      load_ch<CPL>(zq + i * NZ * C + b * C + c0, qz[b]);
+    } else {
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) {
-      gs[b][q] = 0.f;
-      qz[b][q] = zq ? zq[i * 4 * C + b * C + c0 + q] : 0.f;
+      for (int q = 0; q < CPL; ++q) qz[b][q] = 0.f;
     }
-  for (int64_t e = lo; e < hi; ++e) {
-    const float* g = geo + 8 * e;
-    const float ux = g[0], uy = g[1], uz = g[2], fc = g[4];
-    const int64_t j = edge_index[2 * e + 1];
-    const float* ze = z + e * 4 * C + c0;
-    float gzl[4][CPL];
-    float sf = 0.f, su0 = 0.f, su1 = 0.f, su2 = 0.f;
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) {
-      const float hj = h0[j * C + c0 + q];
-      const float gu = g1[0][q] * ux + g1[1][q] * uy + g1[2][q] * uz;
-      const float za = ze[q] + qz[0][q], zb = ze[C + q] + qz[1][q];
-      const float sa = sigmoid(za), sb = sigmoid(zb);
-      const float gwa = g0[q] * hj, gwb = hj * gu;
-      gzl[0][q] = gwa * fc * sa * (1.0f + za * (1.0f - sa));
-      gzl[1][q] = gwb * fc * sb * (1.0f + zb * (1.0f - sb));
-      sf += gwa * za * sa + gwb * zb * sb;
-      const float wb = zb * sb * fc;
-      su0 += g1[0][q] * wb * hj;
-      su1 += g1[1][q] * wb * hj;
-      su2 += g1[2][q] * wb * hj;
-      if (H1) {
-        const float hx = h1[(j * 3 + 0) * C + c0 + q], hy = h1[(j * 3 + 1) * C + c0 + q],
-                    hz = h1[(j * 3 + 2) * C + c0 + q];
-        const float zc = ze[2 * C + q] + qz[2][q], zd = ze[3 * C + q] + qz[3][q];
-        const float sc = sigmoid(zc), sd = sigmoid(zd);
-        const float proj = hx * ux + hy * uy + hz * uz;
-        const float gwc = g0[q] * proj, gwd = g1[0][q] * hx + g1[1][q] * hy + g1[2][q] * hz;
-        gzl[2][q] = gwc * fc * sc * (1.0f + zc * (1.0f - sc));
-        gzl[3][q] = gwd * fc * sd * (1.0f + zd * (1.0f - sd));
-        sf += gwc * zc * sc + gwd * zd * sd;
-        const float t = g0[q] * zc * sc * fc;
-        su0 += t * hx;
-        su1 += t * hy;
-        su2 += t * hz;
-      } else {
-        gzl[2][q] = 0.f;
-        gzl[3][q] = 0.f;
+    for (int q = 0; q < CPL; ++q) gs[b][q] = 0.f;
+  }
+  const bool fused_red = nb <= 8 || !w1ef;  // radial gradients and geometry sums in one reduction
+  for (int64_t base = lo; base < hi; base += 64) {
+    const int cnt = (int)(hi - base < 64 ? hi - base : 64);
+    const RowGeo m = row_geo(geo, edge_index, base + lane, lane < cnt);
+    float og[4] = {0.f, 0.f, 0.f, 0.f};  // ggeo of the lane's row before this kernel (accumulating)
+    if (accumulate_geo && fused_red && lane < cnt) {
+      const float4 t = *reinterpret_cast<const float4*>(ggeo + 4 * (base + lane));
+      og[0] = t.x;
+      og[1] = t.y;
+      og[2] = t.z;
+      og[3] = t.w;
+    }
+    for (int u0 = 0; u0 < cnt; u0 += kGroup) {
+      float zr[kGroup][NZ][CPL], hj[kGroup][CPL], hv[kGroup][3][CPL];
+      float ux[kGroup], uy[kGroup], uz[kGroup], fc[kGroup];
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        const int s = u0 + u < cnt ? u0 + u : cnt - 1;
+        const int64_t j = bcast(m.j, s);
+        ux[u] = bcast(m.ux, s);
+        uy[u] = bcast(m.uy, s);
+        uz[u] = bcast(m.uz, s);
+        fc[u] = u0 + u < cnt ? bcast(m.fc, s) : 0.f;  // a row past the end adds exact zeros
+        const float* ze = z + (base + s) * (NZ * C) + c0;
+#pragma unroll
+        for (int b = 0; b < NZ; ++b) load_ch<CPL>(ze + b * C, zr[u][b]);
+        load_ch<CPL>(h0 + j * C + c0, hj[u]);
+        if (H1) {
+#pragma unroll
+          for (int x = 0; x < 3; ++x) load_ch<CPL>(h1 + (j * 3 + x) * C + c0, hv[u][x]);
+        }
       }
-    }
-    if (gz) {
-      float* gze = gz + e * 4 * C + c0;
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
+      for (int u = 0; u < kGroup; ++u) {
+        // rows past the end (fc = 0) are computed and not stored: a branch around them would let
+        // the compiler move the group's loads behind it
+        const bool valid = u0 + u < cnt;
+        const int64_t e = base + u0 + u;
+        float gzl[NZ][CPL];
+        float sf = 0.f, su0 = 0.f, su1 = 0.f, su2 = 0.f;
 #pragma unroll
-        for (int q = 0; q < CPL; ++q) store_stream(gze + b * C + q, gzl[b][q]);
-    }
-    if (gzsum) {
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-#pragma unroll
-        for (int q = 0; q < CPL; ++q) gs[b][q] += gzl[b][q];
-    }
-    if (w1ef) {
-      for (int n0 = 0; n0 < nb; n0 += 8) {
-        float acc[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          acc[t] = 0.f;
-          if (n0 + t < nb) {
-            const float* w = s_w + (n0 + t) * 4 * C + c0;
-#pragma unroll
-            for (int b = 0; b < (H1 ? 4 : 2); ++b)
-#pragma unroll
-              for (int q = 0; q < CPL; ++q) acc[t] += gzl[b][q] * w[b * C + q];
+        for (int q = 0; q < CPL; ++q) {
+          const float hjq = hj[u][q];
+          const float gu = g1[0][q] * ux[u] + g1[1][q] * uy[u] + g1[2][q] * uz[u];
+          const float za = zr[u][0][q] + qz[0][q], zb = zr[u][1][q] + qz[1][q];
+          const float sa = sigmoid(za), sb = sigmoid(zb);
+          const float gwa = g0[q] * hjq, gwb = hjq * gu;
+          gzl[0][q] = gwa * fc[u] * sa * (1.0f + za * (1.0f - sa));
+          gzl[1][q] = gwb * fc[u] * sb * (1.0f + zb * (1.0f - sb));
+          sf += gwa * za * sa + gwb * zb * sb;
+          const float wb = zb * sb * fc[u];
+          su0 += g1[0][q] * wb * hjq;
+          su1 += g1[1][q] * wb * hjq;
+          su2 += g1[2][q] * wb * hjq;
+          if (H1) {
+            constexpr int BC = NZ > 2 ? 2 : 0, BD = NZ > 2 ? 3 : 0;
+            const float hx = hv[u][0][q], hy = hv[u][1][q], hz = hv[u][2][q];
+            const float zc = zr[u][BC][q] + qz[BC][q], zd = zr[u][BD][q] + qz[BD][q];
+            const float sc = sigmoid(zc), sd = sigmoid(zd);
+            const float proj = hx * ux[u] + hy * uy[u] + hz * uz[u];
+            const float gwc = g0[q] * proj, gwd = g1[0][q] * hx + g1[1][q] * hy + g1[2][q] * hz;
+            gzl[BC][q] = gwc * fc[u] * sc * (1.0f + zc * (1.0f - sc));
+            gzl[BD][q] = gwd * fc[u] * sd * (1.0f + zd * (1.0f - sd));
+            sf += gwc * zc * sc + gwd * zd * sd;
+            const float t = g0[q] * zc * sc * fc[u];
+            su0 += t * hx;
+            su1 += t * hy;
+            su2 += t * hz;
           }
         }
-        const float tot = wave_sum8(acc);
-        const int t = wave_sum8_index(lane);
-        if ((lane & 7) == 0 && n0 + t < nb) gef[e * nb + n0 + t] = tot;
-      }
-    }
-    sf = wave_sum(sf);
-    su0 = wave_sum(su0);
-    su1 = wave_sum(su1);
-    su2 = wave_sum(su2);
-    if (lane == 0) {
-      float* gg = ggeo + 4 * e;
-      if (accumulate_geo) {
-        gg[0] += su0;
-        gg[1] += su1;
-        gg[2] += su2;
-        gg[3] += sf;
-      } else {
-        gg[0] = su0;
-        gg[1] = su1;
-        gg[2] = su2;
-        gg[3] = sf;
+        if (gz && valid) {
+          float* gze = gz + e * NZ * C + c0;
+#pragma unroll
+          for (int b = 0; b < NZ; ++b)
+#pragma unroll
+            for (int q = 0; q < CPL; ++q) store_stream(gze + b * C + q, gzl[b][q]);
+        }
+        if (gzsum) {
+#pragma unroll
+          for (int b = 0; b < NZ; ++b)
+#pragma unroll
+            for (int q = 0; q < CPL; ++q) gs[b][q] += gzl[b][q];
+        }
+        if (fused_red) {
+          float red[16];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            red[t] = 0.f;
+            if (w1ef && t < nb) {
+              const float* w = s_w + t * 4 * C + c0;
+#pragma unroll
+              for (int b = 0; b < NZ; ++b)
+#pragma unroll
+                for (int q = 0; q < CPL; ++q) red[t] += gzl[b][q] * w[b * C + q];
+            }
+          }
+          red[8] = su0;
+          red[9] = su1;
+          red[10] = su2;
+          red[11] = sf;
+          red[12] = red[13] = red[14] = red[15] = 0.f;
+          const float tot = wave_sum16(red);
+          const int t = wave_sum16_index(lane);
+          const int s = valid ? u0 + u : cnt - 1;
+          const float o0 = bcast(og[0], s), o1 = bcast(og[1], s), o2 = bcast(og[2], s), o3 = bcast(og[3], s);
+          if (valid && (lane & 3) == 0) {
+            if (t < 8) {
+              if (w1ef && t < nb) gef[e * nb + t] = tot;
+            } else if (t < 12) {
+              const float old = t == 8 ? o0 : t == 9 ? o1 : t == 10 ? o2 : o3;
+              ggeo[4 * e + (t - 8)] = accumulate_geo ? old + tot : tot;
+            }
+          }
+        } else if (valid) {
+          for (int n0 = 0; n0 < nb; n0 += 8) {
+            float acc[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+              acc[t] = 0.f;
+              if (n0 + t < nb) {
+                const float* w = s_w + (n0 + t) * 4 * C + c0;
+#pragma unroll
+                for (int b = 0; b < NZ; ++b)
+#pragma unroll
+                  for (int q = 0; q < CPL; ++q) acc[t] += gzl[b][q] * w[b * C + q];
+              }
+            }
+            const float tot = wave_sum8(acc);
+            const int t = wave_sum8_index(lane);
+            if ((lane & 7) == 0 && n0 + t < nb) gef[e * nb + n0 + t] = tot;
+          }
+          sf = wave_sum(sf);
+          su0 = wave_sum(su0);
+          su1 = wave_sum(su1);
+          su2 = wave_sum(su2);
+          if (lane == 0) {
+            float* gg = ggeo + 4 * e;
+            if (accumulate_geo) {
+              gg[0] += su0;
+              gg[1] += su1;
+              gg[2] += su2;
+              gg[3] += sf;
+            } else {
+              gg[0] = su0;
+              gg[1] = su1;
+              gg[2] = su2;
+              gg[3] = sf;
+            }
+          }
+        }
       }
     }
   }
   if (gzsum) {
-    float* d = gzsum + i * 4 * C + c0;
+    float* d = gzsum + i * NZ * C + c0;
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < NZ; ++b)
 #pragma unroll
       for (int q = 0; q < CPL; ++q) d[b * C + q] = gs[b][q];
   }
@@ -339,47 +503,90 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
 // VJP, sender side (one wave per node j, over the reverse rows e = reverse[e'] of its rows e'
 // as a centre; the receiver of e is i = neighbor[e']):
 //   g_h0_j += gA0_i wa_e + wb_e (gA1_i . u_e);  g_h1_j,x += gA0_i wc_e u_e,x + gA1_i,x wd_e
-// accumulate: bit 0 adds into gh0, bit 1 into gh1 (else they are overwritten).
+// accumulate: bit 0 adds into gh0, bit 1 into gh1 (else they are overwritten). Per 64 rows the
+// wave loads reverse[e'], the receiver and the geometry of e once (a lane per row); each group
+// of kGroup rows issues its z[e], zq[i], gA0[i] and gA1[i] loads before any arithmetic.
 template <int CPL, bool H1>
 __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
     const float* z, const float* zq, const float* geo, const int32_t* edge_index, const int32_t* reverse,
     const int64_t* off, const int64_t* n_edges, int64_t e_cap, int64_t n, const float* gA0, const float* gA1,
     float inv_avg, float* gh0, float* gh1, int accumulate) {
   constexpr int C = 64 * CPL;
+  constexpr int NZ = H1 ? 4 : 2;
   const int lane = threadIdx.x & 63;
-  const int64_t jn = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64;
+  const int64_t jn = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   if (jn >= n) return;
-  const int64_t rows = real_rows(n_edges, e_cap);
-  int64_t lo = off[jn], hi = off[jn + 1];
-  hi = hi < rows ? hi : rows;
-  lo = lo < hi ? lo : hi;
+  int64_t lo;
+  const int64_t hi = wave_rows(off, n_edges, e_cap, jn, lo);
   const int c0 = lane * CPL;
   float a0[CPL], a1[3][CPL];
 #pragma unroll
   for (int q = 0; q < CPL; ++q) a0[q] = a1[0][q] = a1[1][q] = a1[2][q] = 0.f;
-  for (int64_t ep = lo; ep < hi; ++ep) {
-    const int64_t e = reverse[ep];
-    if (e < 0) continue;
-    const int64_t i = edge_index[2 * ep + 1];
-    const float* g = geo + 8 * e;
-    const float ux = g[0], uy = g[1], uz = g[2], fc = g[4];
-    const float* ze = z + e * 4 * C + c0;
-    const float* qe = zq ? zq + i * 4 * C + c0 : nullptr;  // the receiver block of z[e] (row i)
+  for (int64_t base = lo; base < hi; base += 64) {
+    const int cnt = (int)(hi - base < 64 ? hi - base : 64);
+    int me = -1, mi = 0;
+    float mux = 0.f, muy = 0.f, muz = 0.f, mfc = 0.f;
+    if (lane < cnt) {
+      const int64_t ep = base + lane;
+      me = reverse[ep];
+      mi = edge_index[2 * ep + 1];
+      if (me >= 0) {
+        const float4 g = *reinterpret_cast<const float4*>(geo + 8 * (int64_t)me);
+        mux = g.x;
+        muy = g.y;
+        muz = g.z;
+        mfc = geo[8 * (int64_t)me + 4];
+      }
+    }
+    for (int u0 = 0; u0 < cnt; u0 += kGroup) {
+      float zr[kGroup][NZ][CPL], qe[kGroup][NZ][CPL], ga[kGroup][4][CPL];
+      float ux[kGroup], uy[kGroup], uz[kGroup], fc[kGroup];
+      int er[kGroup];
 #pragma unroll
-    for (int q = 0; q < CPL; ++q) {
-      const float g0 = gA0[i * C + c0 + q];
-      const float gx = gA1[(i * 3 + 0) * C + c0 + q], gy = gA1[(i * 3 + 1) * C + c0 + q],
-                  gzv = gA1[(i * 3 + 2) * C + c0 + q];
-      const float za = ze[q] + (qe ? qe[q] : 0.f), zb = ze[C + q] + (qe ? qe[C + q] : 0.f);
-      const float wa = za * sigmoid(za) * fc, wb = zb * sigmoid(zb) * fc;
-      a0[q] += g0 * wa + wb * (gx * ux + gy * uy + gzv * uz);
-      if (H1) {
-        const float zc = ze[2 * C + q] + (qe ? qe[2 * C + q] : 0.f), zd = ze[3 * C + q] + (qe ? qe[3 * C + q] : 0.f);
-        const float wc = zc * sigmoid(zc) * fc, wd = zd * sigmoid(zd) * fc;
-        const float t = g0 * wc;
-        a1[0][q] += t * ux + gx * wd;
-        a1[1][q] += t * uy + gy * wd;
-        a1[2][q] += t * uz + gzv * wd;
+      for (int u = 0; u < kGroup; ++u) {
+        const int s = u0 + u < cnt ? u0 + u : cnt - 1;
+        er[u] = bcast(me, s);
+        const int64_t i = bcast(mi, s);
+        const int64_t e = er[u] < 0 ? 0 : er[u];  // a missing reverse row reads row 0, weight 0
+        ux[u] = bcast(mux, s);
+        uy[u] = bcast(muy, s);
+        uz[u] = bcast(muz, s);
+        // rows past the end and missing reverse rows add exact zeros (fc = 0)
+        fc[u] = u0 + u < cnt && er[u] >= 0 ? bcast(mfc, s) : 0.f;
+        const float* ze = z + e * (NZ * C) + c0;
+#pragma unroll
+        for (int b = 0; b < NZ; ++b) {
+          load_ch<CPL>(ze + b * C, zr[u][b]);
+          if (zq) {
+            load_ch<CPL>(zq + i * (NZ * C) + b * C + c0, qe[u][b]);  // the receiver block of z[e] (row i)
+          } else {
+#pragma unroll
+            for (int q = 0; q < CPL; ++q) qe[u][b][q] = 0.f;
+          }
+        }
+        load_ch<CPL>(gA0 + i * C + c0, ga[u][0]);
+#pragma unroll
+        for (int x = 0; x < 3; ++x) load_ch<CPL>(gA1 + (i * 3 + x) * C + c0, ga[u][1 + x]);
+      }
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        // no branch around the zero rows: it would let the compiler move the loads behind it
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) {
+          const float g0 = ga[u][0][q], gx = ga[u][1][q], gy = ga[u][2][q], gzv = ga[u][3][q];
+          const float za = zr[u][0][q] + qe[u][0][q], zb = zr[u][1][q] + qe[u][1][q];
+          const float wa = za * sigmoid(za) * fc[u], wb = zb * sigmoid(zb) * fc[u];
+          a0[q] += g0 * wa + wb * (gx * ux[u] + gy * uy[u] + gzv * uz[u]);
+          if (H1) {
+            constexpr int BC = NZ > 2 ? 2 : 0, BD = NZ > 2 ? 3 : 0;
+            const float zc = zr[u][BC][q] + qe[u][BC][q], zd = zr[u][BD][q] + qe[u][BD][q];
+            const float wc = zc * sigmoid(zc) * fc[u], wd = zd * sigmoid(zd) * fc[u];
+            const float t = g0 * wc;
+            a1[0][q] += t * ux[u] + gx * wd;
+            a1[1][q] += t * uy[u] + gy * wd;
+            a1[2][q] += t * uz[u] + gzv * wd;
+          }
+        }
       }
     }
   }
@@ -551,6 +758,16 @@ int launch_message(bool h1, dim3 grid, hipStream_t s, const float* z, const floa
 
 }  // namespace
 
+// the message kernels load a lane's CPL = C / 64 channels as one vector: the per-node and per-row
+// arrays start on 4 * CPL-byte boundaries, geo and ggeo on 16 bytes
+static bool aligned_to(uintptr_t a, std::initializer_list<const void*> ptrs) {
+  for (const void* p : ptrs)
+    if (p && ((uintptr_t)p % a) != 0) return false;
+  return true;
+}
+
+static uintptr_t channel_alignment(int channels) { return 4 * (uintptr_t)(channels >= 64 ? channels / 64 : 1); }
+
 #define FMD_CPL_DISPATCH(C, FN, ...)                 \
   switch ((C) / 64) {                                \
     case 1: return FN<1>(__VA_ARGS__);               \
@@ -566,12 +783,13 @@ int launch_bwd_edge(bool h1, dim3 grid, hipStream_t s, const float* z, const flo
                     const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const float* h0,
                     const float* h1p, const float* gA0, const float* gA1, float inv_avg, float* gz, float* gzsum,
                     float* ggeo, int acc, const float* w1ef, int nb, float* gef) {
+  const size_t lds = w1ef ? (size_t)nb * 4 * 64 * CPL * sizeof(float) : 0;
   if (h1)
-    hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, off, ne, e_cap,
-                       n, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef);
+    hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, true>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne,
+                       e_cap, n, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef);
   else
-    hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, off, ne, e_cap,
-                       n, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef);
+    hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, false>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne,
+                       e_cap, n, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -622,6 +840,7 @@ int fmd_mace_message_f32(const float* z, const float* zq, const float* geo, cons
                          int32_t channels, const float* h0, const float* h1, float inv_avg, float* A0, float* A1,
                          hipStream_t stream) {
   FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && A0 && A1 && n_atoms >= 0);
+  FMD_REQUIRE(aligned_to(channel_alignment(channels), {z, zq, h0, h1, A0, A1}) && aligned_to(16, {geo}));
   if (n_atoms == 0) return FMD_OK;
   dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
   FMD_CPL_DISPATCH(channels, launch_message, h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets,
@@ -639,6 +858,8 @@ int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, 
   FMD_REQUIRE(gz || w1ef);
   FMD_REQUIRE(!w1ef || (gef && nb > 0 && nb <= kMaxBasis));
   FMD_REQUIRE(!gh0 || reverse);
+  FMD_REQUIRE(aligned_to(channel_alignment(channels), {z, zq, h0, h1, gA0, gA1, gz, gzsum, gh0, gh1}) &&
+              aligned_to(16, {geo, ggeo}));
   if (n_atoms == 0) return FMD_OK;
   dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
   int rc = FMD_OK;

@@ -13,7 +13,7 @@ Model (per interaction layer t, node features h0 [N, C] scalars and h1 [N, 3, C]
   a_e    = [h0_j | h0_i | ef_e]                                 (gather-cat, [E, 2C + 8])
   z_e    = a_e @ W1                                              (edge GEMM, [2C+8, 4C]; the
                                                                   gather-cat is fused into its load)
-  w_e    = silu(z_e) * fcut(r)  = (wa | wb | wc | wd)
+  w_e    = silu(z_e) * fcut(r)  = (wa | wb | wc | wd)             (h1 = 0: wa | wb only)
   m0     = wa h0_j + wc (h1_j . u),  m1_x = wb h0_j u_x + wd h1_j,x
   A0_i, A1_i = (1 / avg_num_neighbors) * sum over the rows of i   (segment sums)
   P0 = A0 Wm0, P1_x = A1_x Wm1;  n1 = |P1|^2
@@ -242,13 +242,16 @@ class _MaceLikeEnergy(Function):
             # operand load. On large edge lists the receiver block h0[dst] @ W1[C:2C], the same for
             # every row of a centre, is formed once per atom (q, [N, 4C]) and added by the message
             # kernels, and the edge GEMM multiplies [h0[src] | ef] (K = C + nb).
+            # Without vector features (h1 = 0, the first layer) wc and wd multiply only zeros: z keeps
+            # just its a | b blocks ([E, 2C], the first 2C columns of W1).
             timed = EDGE_GEMM_EVENTS is not None and not torch.cuda.is_current_stream_capturing()
+            nz = 4 * C if h1 is not None else 2 * C
             if e_cap >= HOIST_MIN_ROWS:
-                q = gemm(h0, model.w1_receiver_t(t), b_layout=0)
-                parts, w1 = [(h0, ei[:, 1]), (ef, None)], model.w1_sender_t(t)
+                q = gemm(h0, model.w1_receiver_t(t)[:nz], b_layout=0)
+                parts, w1 = [(h0, ei[:, 1]), (ef, None)], model.w1_sender_t(t)[:nz]
             else:
                 q = None
-                parts, w1 = [(h0, ei[:, 1]), (h0, ei[:, 0]), (ef, None)], model.w1_t(t)
+                parts, w1 = [(h0, ei[:, 1]), (h0, ei[:, 0]), (ef, None)], model.w1_t(t)[:nz]
             if timed:
                 ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                 ev[0].record()

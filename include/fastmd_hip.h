@@ -254,18 +254,21 @@ int fmd_edge_geometry_f32(const float* positions, const float* cell, const int32
 int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, const float* gef0, int64_t ld0,
                               const float* gef1, int64_t ld1, const float* ggeo, const int64_t* n_edges,
                               int64_t e_cap, float* gvec, hipStream_t stream);
-/* A0[i], A1[i] = inv_avg * sum over the rows of centre i of the messages (h1 may be null). The
- * edge pre-activations are z[e] + zq[i] when zq ([N, 4C], the receiver block of the edge GEMM
- * formed once per atom) is given, else z[e]. */
+/* A0[i], A1[i] = inv_avg * sum over the rows of centre i of the messages. z [E, W] holds the
+ * edge pre-activation blocks a | b | c | d (W = 4C) when h1 is given; with h1 null (zero vector
+ * features, where c and d meet only zeros) z holds a | b only (W = 2C). The pre-activations are
+ * z[e] + zq[i] when zq ([N, W], the receiver block of the edge GEMM formed once per atom) is
+ * given, else z[e]. z, zq, h0, h1, A0, A1 start on 4 * (C / 64)-byte boundaries, geo on 16. */
 int fmd_mace_message_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
                          const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
                          int32_t channels, const float* h0, const float* h1, float inv_avg, float* A0, float* A1,
                          hipStream_t stream);
-/* VJP of fmd_mace_message_f32 (z, zq as there): gz [E,4C] (may be null when w1ef is given), gzsum [N,4C] (may be
- * null: the sum of gz over each centre's rows, in row order), ggeo [E,4] (= or +=), with w1ef
- * ([nb, 4C], the radial rows of the edge GEMM weight) also gef[e] = gz[e] @ w1ef^T [E,nb], and if
- * gh0: the sender-side gh0/gh1 over the reverse CSR (accumulate_h bit 0: gh0 +=, bit 1: gh1 +=;
- * otherwise =). */
+/* VJP of fmd_mace_message_f32 (z, zq and the width W as there): gz [E,W] (may be null when w1ef
+ * is given), gzsum [N,W] (may be null: the sum of gz over each centre's rows, in row order), ggeo
+ * [E,4] (= or +=), with w1ef ([nb, 4C], the radial rows of the edge GEMM weight; its first W
+ * columns enter) also gef[e] = gz[e] @ w1ef[:, :W]^T [E,nb], and if gh0: the sender-side gh0/gh1
+ * over the reverse CSR (accumulate_h bit 0: gh0 +=, bit 1: gh1 +=; otherwise =). Alignment as
+ * there (gA0, gA1, gz, gzsum, gh0, gh1 like h0; ggeo on 16 bytes). */
 int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
                              const int32_t* reverse,
                              const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
