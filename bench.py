@@ -347,8 +347,8 @@ def cpu_baseline(n_atoms: int, budget_s: float) -> dict:
 def main() -> int:
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=200)
-    parser.add_argument("--warmup", type=int, default=600,
+    parser.add_argument("--steps", type=int, default=1000)
+    parser.add_argument("--warmup", type=int, default=1000,
                         help="untimed MD steps before timing (thermalisation: the edge count settles)")
     parser.add_argument("--steps-small", type=int, default=2000)
     parser.add_argument("--no-cpu", action="store_true")

@@ -21,12 +21,55 @@
 
 __host__ __device__ static inline int64_t fmd_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// gfx950 cross-lane moves that bypass the LDS crossbar: v_permlane32_swap / v_permlane16_swap
+// trade the upper half of every 64 / 32 lanes of one register with the lower half of another, and
+// DPP reads a partner lane inside a row of 16 as an operand of the consuming instruction.
+__device__ __forceinline__ void swap_halves32(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ void swap_halves16(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
+constexpr int kDppQuadXor1 = 0xB1;    // quad_perm [1,0,3,2]: lane l reads l ^ 1
+constexpr int kDppQuadXor2 = 0x4E;    // quad_perm [2,3,0,1]: lane l reads l ^ 2
+constexpr int kDppRowRor8 = 0x128;    // row_ror:8: lane l reads (l + 8) mod 16 of its row = l ^ 8
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror: lane l reads 7 - l of its 8 (bit 2 flips)
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_read(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
 // Wavefront (64 lanes) reductions in a fixed butterfly order: every lane ends with the same
-// value, and the order depends on nothing but the lane layout (deterministic).
+// value, and the order depends on nothing but the lane layout (deterministic). Called with the
+// whole wave active.
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, FMD_WAVE);
+  return v;
+}
+
+// float: lanes l and l ^ 32, then l ^ 16 (half swaps of the value with itself), then l ^ 8, the
+// mirror lane in 8, l ^ 1 and l ^ 2 (DPP) - 64 lanes in six steps without the LDS crossbar
+template <>
+__device__ __forceinline__ float wave_sum<float>(float v) {
+  float w = v;
+  swap_halves32(v, w);
+  v = v + w;
+  w = v;
+  swap_halves16(v, w);
+  v = v + w;
+  v = v + dpp_read<kDppRowRor8>(v);
+  v = v + dpp_read<kDppHalfMirror>(v);
+  v = v + dpp_read<kDppQuadXor1>(v);
+  v = v + dpp_read<kDppQuadXor2>(v);
   return v;
 }
 
@@ -40,60 +83,67 @@ __device__ __forceinline__ T wave_max(T v) {
   return v;
 }
 
-// Eight wave sums at once: a transposing butterfly (halve the value set at each of the first three
-// exchanges, then reduce the last value over the remaining three) uses 10 exchanges instead of 48.
-// On return every lane holds the total of value index 4*b5 + 2*b4 + b3 (b_i: bit i of the lane),
-// see wave_sum8_index. The order of additions is fixed by the lane layout (deterministic).
+// Eight wave sums at once: a transposing butterfly (each of the first three exchanges halves the
+// value set: a lane keeps one half and adds its partner's copy of it, the partner keeps the other
+// half), then a full sum of the last value over the remaining 8 lanes. On return every lane holds
+// the total of value index 4*b5 + 2*b4 + b3 (b_i: bit i of the lane), see wave_sum8_index. The
+// order of additions is fixed by the lane layout (deterministic).
 __device__ __forceinline__ float wave_sum8(const float (&v)[8]) {
   const int lane = threadIdx.x & (FMD_WAVE - 1);
-  const bool h5 = lane & 32, h4 = lane & 16, h3 = lane & 8;
-  float w[4], x[2];
+  const bool h3 = lane & 8;
+  float a[4], b[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float keep = h5 ? v[i + 4] : v[i], send = h5 ? v[i] : v[i + 4];
-    w[i] = keep + __shfl_xor(send, 32, FMD_WAVE);
+  for (int i = 0; i < 4; ++i) {  // lanes with bit 5 set keep index i + 4
+    float x = v[i], y = v[i + 4];
+    swap_halves32(x, y);
+    a[i] = x + y;
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const float keep = h4 ? w[i + 2] : w[i], send = h4 ? w[i] : w[i + 2];
-    x[i] = keep + __shfl_xor(send, 16, FMD_WAVE);
+  for (int i = 0; i < 2; ++i) {  // bit 4 set: index i + 2
+    float x = a[i], y = a[i + 2];
+    swap_halves16(x, y);
+    b[i] = x + y;
   }
-  float y = (h3 ? x[1] : x[0]) + __shfl_xor(h3 ? x[0] : x[1], 8, FMD_WAVE);
-#pragma unroll
-  for (int off = 4; off >= 1; off >>= 1) y += __shfl_xor(y, off, FMD_WAVE);
-  return y;
+  float t = (h3 ? b[1] : b[0]) + dpp_read<kDppRowRor8>(h3 ? b[0] : b[1]);
+  t = t + dpp_read<kDppHalfMirror>(t);
+  t = t + dpp_read<kDppQuadXor1>(t);
+  t = t + dpp_read<kDppQuadXor2>(t);
+  return t;
 }
 
 __device__ __forceinline__ int wave_sum8_index(int lane) {
   return ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
 }
 
-// Sixteen wave sums at once (the same transposing butterfly over four halving exchanges, then two
-// full ones): 17 exchanges instead of 96. On return every lane holds the total of value index
-// 8*b5 + 4*b4 + 2*b3 + b2 (wave_sum16_index). Fixed order (deterministic).
+// Sixteen wave sums at once (the same transposing butterfly over four halving exchanges, the
+// fourth with the mirror lane in 8, then l ^ 1 and l ^ 2): on return every lane holds the total of
+// value index 8*b5 + 4*b4 + 2*b3 + b2 (wave_sum16_index). Fixed order (deterministic).
 __device__ __forceinline__ float wave_sum16(const float (&v)[16]) {
   const int lane = threadIdx.x & (FMD_WAVE - 1);
-  const bool h5 = lane & 32, h4 = lane & 16, h3 = lane & 8, h2 = lane & 4;
+  const bool h3 = lane & 8, h2 = lane & 4;
   float a[8], b[4], c[2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float keep = h5 ? v[i + 8] : v[i], send = h5 ? v[i] : v[i + 8];
-    a[i] = keep + __shfl_xor(send, 32, FMD_WAVE);
+  for (int i = 0; i < 8; ++i) {  // bit 5 set: index i + 8
+    float x = v[i], y = v[i + 8];
+    swap_halves32(x, y);
+    a[i] = x + y;
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float keep = h4 ? a[i + 4] : a[i], send = h4 ? a[i] : a[i + 4];
-    b[i] = keep + __shfl_xor(send, 16, FMD_WAVE);
+  for (int i = 0; i < 4; ++i) {  // bit 4 set: index i + 4
+    float x = a[i], y = a[i + 4];
+    swap_halves16(x, y);
+    b[i] = x + y;
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < 2; ++i) {  // bit 3 set: index i + 2 (partner l ^ 8)
     const float keep = h3 ? b[i + 2] : b[i], send = h3 ? b[i] : b[i + 2];
-    c[i] = keep + __shfl_xor(send, 8, FMD_WAVE);
+    c[i] = keep + dpp_read<kDppRowRor8>(send);
   }
-  float y = (h2 ? c[1] : c[0]) + __shfl_xor(h2 ? c[0] : c[1], 4, FMD_WAVE);
-  y += __shfl_xor(y, 2, FMD_WAVE);
-  y += __shfl_xor(y, 1, FMD_WAVE);
-  return y;
+  // bit 2 set: index 1 (partner: the mirror lane in 8, whose bit 2 is the other)
+  float t = (h2 ? c[1] : c[0]) + dpp_read<kDppHalfMirror>(h2 ? c[0] : c[1]);
+  t = t + dpp_read<kDppQuadXor1>(t);
+  t = t + dpp_read<kDppQuadXor2>(t);
+  return t;
 }
 
 __device__ __forceinline__ int wave_sum16_index(int lane) {

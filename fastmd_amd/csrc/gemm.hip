@@ -61,11 +61,14 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[WM][WN], int64_t ro
 // ds_read_b32 at a conflict-free address (consecutive lanes, consecutive i / j).
 constexpr int BK32 = 32;
 
+// One BM x BN tile at (row_blk, col_blk). A may be split along K: columns [0, ksplit) from a,
+// [ksplit, k) from a2 (ksplit a multiple of BK32), i.e. [a | a2] @ op(b) in one accumulation.
 template <int BM, int BN, int BLAYOUT>
-__global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restrict__ a, int64_t lda,
-                                                            const float* __restrict__ b, int64_t ldb,
-                                                            const float* __restrict__ bias, float* c, int64_t ldc,
-                                                            int64_t m, int64_t n, int64_t k, int accumulate, int act) {
+__device__ __forceinline__ void gemm_f32_tile(const float* __restrict__ a, int64_t lda, const float* __restrict__ a2,
+                                              int64_t lda2, int64_t ksplit, const float* __restrict__ b, int64_t ldb,
+                                              const float* __restrict__ bias, float* c, int64_t ldc, int64_t m,
+                                              int64_t n, int64_t k, int accumulate, int act, int64_t row_blk,
+                                              int64_t col_blk) {
   constexpr int WM = BM / 64, WN = BN / 64;           // MFMA blocks per wave
   constexpr int LDA = BM + 4, LDB = BN + 4;           // padded LDS rows
   constexpr int A_VEC = BM * BK32 / 4 / kThreads;     // float4 loads per thread (A)
@@ -74,7 +77,6 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restr
   __shared__ float Bs[2][BK32][LDB];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t row_blk = (int64_t)blockIdx.x * BM, col_blk = (int64_t)blockIdx.y * BN;
 
   float4 ra[A_VEC], rb[B_VEC];
   auto load4 = [&](const float* p, bool in_rows, int64_t kk, int64_t kmax) -> float4 {
@@ -94,7 +96,8 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restr
       const int id = t + q * kThreads;
       const int r = id >> 3, kc = (id & 7) * 4;
       const int64_t gr = row_blk + r, gk = k0 + kc;
-      ra[q] = load4(a + gr * lda + gk, gr < m, gk, k);
+      const float* src = k0 < ksplit ? a + gr * lda + gk : a2 + gr * lda2 + (gk - ksplit);
+      ra[q] = load4(src, gr < m, gk, k);
     }
   };
   auto load_b = [&](int64_t k0) {
@@ -177,6 +180,49 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restr
     __syncthreads();
   }
   epilogue<WM, WN>(acc, row_blk + wm * (BM / 2), col_blk + wn * (BN / 2), m, n, bias, c, ldc, accumulate, act);
+}
+
+template <int BM, int BN, int BLAYOUT>
+__global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restrict__ a, int64_t lda,
+                                                            const float* __restrict__ b, int64_t ldb,
+                                                            const float* __restrict__ bias, float* c, int64_t ldc,
+                                                            int64_t m, int64_t n, int64_t k, int accumulate, int act) {
+  gemm_f32_tile<BM, BN, BLAYOUT>(a, lda, a, lda, k, b, ldb, bias, c, ldc, m, n, k, accumulate, act,
+                                 (int64_t)blockIdx.x * BM, (int64_t)blockIdx.y * BN);
+}
+
+// Several independent GEMMs of one b layout in one launch (the node side of an interaction
+// layer: fewer, fuller launches). Workgroup w takes problem g with tile0[g] <= w < tile0[g + 1],
+// tile (w - tile0[g]) in row-major order of its 64 x 64 tiles. Each problem's result is the one
+// fmd_gemm_f32's 64 x 64 kernel gives (same K order), with [a | a2] when a2 is set.
+constexpr int kMaxGroup = 4;
+struct GemmDesc {
+  const float* a;
+  const float* a2;
+  const float* b;
+  const float* bias;
+  float* c;
+  int64_t lda, lda2, ksplit, ldb, ldc, m, n, k, tiles_n, tile0;
+  int accumulate;
+};
+struct GemmGroup {
+  GemmDesc d[kMaxGroup];
+  int count;
+  int act;
+};
+
+template <int BLAYOUT>
+__global__ void __launch_bounds__(kThreads) gemm_f32_group_kernel(const GemmGroup grp) {
+  const int64_t w = blockIdx.x;
+  int g = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxGroup; ++q)
+    if (q < grp.count && w >= grp.d[q].tile0) g = q;
+  const GemmDesc& d = grp.d[g];
+  const int64_t t = w - d.tile0;
+  const int64_t tm = t / d.tiles_n, tn = t - tm * d.tiles_n;
+  gemm_f32_tile<64, 64, BLAYOUT>(d.a, d.lda, d.a2 ? d.a2 : d.a, d.a2 ? d.lda2 : d.lda, d.a2 ? d.ksplit : d.k, d.b,
+                                 d.ldb, d.bias, d.c, d.ldc, d.m, d.n, d.k, d.accumulate, grp.act, tm * 64, tn * 64);
 }
 
 // ------------------------------------------------------------------------- fp32, both K-major
@@ -697,6 +743,56 @@ int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32
     launch_gemm_f32<128, 128>(a, lda, b, ldb, b_layout, bias, c, ldc, m, n, k, accumulate, epilogue_kind, stream);
   else
     launch_gemm_f32<64, 64>(a, lda, b, ldb, b_layout, bias, c, ldc, m, n, k, accumulate, epilogue_kind, stream);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda, const float* const* a2,
+                       const int64_t* lda2, const int64_t* ksplit, const float* const* b, const int64_t* ldb,
+                       int32_t b_layout, const float* const* bias, float* const* c, const int64_t* ldc,
+                       const int64_t* m, const int64_t* n, const int64_t* k, const int32_t* accumulate,
+                       int32_t epilogue_kind, hipStream_t stream) {
+  FMD_REQUIRE(count >= 1 && count <= kMaxGroup && a && lda && b && ldb && c && ldc && m && n && k);
+  FMD_REQUIRE(b_layout == 0 || b_layout == 1);
+  FMD_REQUIRE(epilogue_kind == 0 || epilogue_kind == 1);
+  GemmGroup grp{};
+  grp.act = epilogue_kind;
+  int64_t tiles = 0;
+  for (int g = 0; g < count; ++g) {
+    GemmDesc& d = grp.d[grp.count];
+    FMD_REQUIRE(m[g] >= 0 && n[g] >= 0 && k[g] >= 0);
+    if (m[g] == 0 || n[g] == 0) continue;  // (an empty output may have a null pointer)
+    FMD_REQUIRE(c[g] && ldc[g] >= n[g]);
+    const bool split = a2 && a2[g];
+    const int64_t ks = split ? ksplit[g] : k[g];
+    FMD_REQUIRE(k[g] == 0 || (a[g] && b[g] && ldb[g] >= (b_layout == 0 ? k[g] : n[g])));
+    FMD_REQUIRE(k[g] == 0 || lda[g] >= ks);
+    FMD_REQUIRE(!split || (lda2 && ks > 0 && ks < k[g] && ks % BK32 == 0 && lda2[g] >= k[g] - ks));
+    d.a = a[g];
+    d.a2 = split ? a2[g] : nullptr;
+    d.lda = lda[g];
+    d.lda2 = split ? lda2[g] : 0;
+    d.ksplit = ks;
+    d.b = b[g];
+    d.ldb = ldb[g];
+    d.bias = bias ? bias[g] : nullptr;
+    d.c = c[g];
+    d.ldc = ldc[g];
+    d.m = m[g];
+    d.n = n[g];
+    d.k = k[g];
+    d.accumulate = accumulate ? accumulate[g] : 0;
+    d.tiles_n = fmd_cdiv(n[g], 64);
+    d.tile0 = tiles;
+    tiles += fmd_cdiv(m[g], 64) * d.tiles_n;
+    ++grp.count;
+  }
+  if (grp.count == 0) return FMD_OK;
+  FMD_REQUIRE(tiles < (int64_t(1) << 31));
+  if (b_layout == 0)
+    hipLaunchKernelGGL(gemm_f32_group_kernel<0>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
+  else
+    hipLaunchKernelGGL(gemm_f32_group_kernel<1>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

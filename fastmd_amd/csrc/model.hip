@@ -295,7 +295,7 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
 // per atom). Row loads as in message_kernel.
 constexpr int kMaxBasis = 16;
 
-template <int CPL, bool H1>
+template <int CPL, bool H1, int RB>
 __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     const float* z, const float* zq, const float* geo, const int32_t* edge_index, const int64_t* off,
     const int64_t* n_edges, int64_t e_cap, int64_t n, const float* h0, const float* h1, const float* gA0,
@@ -303,12 +303,13 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     int nb, float* gef) {
   constexpr int C = 64 * CPL;
   constexpr int NZ = H1 ? 4 : 2;
-  extern __shared__ float s_w[];  // w1ef [nb, 4C] when given (dynamic: nb * 4C floats)
+  // w1ef's rows padded to RB (8 or 16) with zero rows (all zero without w1ef): the radial sums
+  // run over RB rows without a branch per row
+  extern __shared__ float s_w[];  // [RB, 4C]
   const int lane = threadIdx.x & 63;
-  if (w1ef) {
-    for (int k = threadIdx.x; k < nb * 4 * C; k += blockDim.x) s_w[k] = w1ef[k];
-    __syncthreads();
-  }
+  const int nbv = w1ef ? nb : 0;
+  for (int k = threadIdx.x; k < RB * 4 * C; k += blockDim.x) s_w[k] = k < nbv * 4 * C ? w1ef[k] : 0.f;
+  __syncthreads();
   const int64_t i = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   if (i >= n) return;
   int64_t lo;
@@ -338,12 +339,11 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
 #pragma unroll
     for (int q = 0; q < CPL; ++q) gs[b][q] = 0.f;
   }
-  const bool fused_red = nb <= 8 || !w1ef;  // radial gradients and geometry sums in one reduction
   for (int64_t base = lo; base < hi; base += 64) {
     const int cnt = (int)(hi - base < 64 ? hi - base : 64);
     const RowGeo m = row_geo(geo, edge_index, base + lane, lane < cnt);
     float og[4] = {0.f, 0.f, 0.f, 0.f};  // ggeo of the lane's row before this kernel (accumulating)
-    if (accumulate_geo && fused_red && lane < cnt) {
+    if (accumulate_geo && lane < cnt) {
       const float4 t = *reinterpret_cast<const float4*>(ggeo + 4 * (base + lane));
       og[0] = t.x;
       og[1] = t.y;
@@ -421,19 +421,26 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
 #pragma unroll
             for (int q = 0; q < CPL; ++q) gs[b][q] += gzl[b][q];
         }
-        if (fused_red) {
-          float red[16];
+        // the radial-basis gradients and the four geometry sums, reduced over the wave together.
+        // The LDS offset is opaque to the compiler, which would otherwise keep all of w1ef in
+        // registers across the loop (RB * NZ * CPL of them: fewer waves per SIMD)
+        int woff = c0;
+        asm volatile("" : "+v"(woff));
+        float red[16];
 #pragma unroll
-          for (int t = 0; t < 8; ++t) {
-            red[t] = 0.f;
-            if (w1ef && t < nb) {
-              const float* w = s_w + t * 4 * C + c0;
+        for (int t = 0; t < (RB == 8 ? 8 : 16); ++t) {
+          const float* w = s_w + t * 4 * C + woff;
+          red[t] = 0.f;
 #pragma unroll
-              for (int b = 0; b < NZ; ++b)
+          for (int b = 0; b < NZ; ++b)
 #pragma unroll
-                for (int q = 0; q < CPL; ++q) red[t] += gzl[b][q] * w[b * C + q];
-            }
-          }
+            for (int q = 0; q < CPL; ++q) red[t] += gzl[b][q] * w[b * C + q];
+        }
+        const int s = valid ? u0 + u : cnt - 1;
+        const float o0 = bcast(og[0], s), o1 = bcast(og[1], s), o2 = bcast(og[2], s), o3 = bcast(og[3], s);
+        float tg;  // the geometry sum this lane writes (index tgi), if any
+        int tgi;
+        if constexpr (RB == 8) {
           red[8] = su0;
           red[9] = su1;
           red[10] = su2;
@@ -441,52 +448,21 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
           red[12] = red[13] = red[14] = red[15] = 0.f;
           const float tot = wave_sum16(red);
           const int t = wave_sum16_index(lane);
-          const int s = valid ? u0 + u : cnt - 1;
-          const float o0 = bcast(og[0], s), o1 = bcast(og[1], s), o2 = bcast(og[2], s), o3 = bcast(og[3], s);
-          if (valid && (lane & 3) == 0) {
-            if (t < 8) {
-              if (w1ef && t < nb) gef[e * nb + t] = tot;
-            } else if (t < 12) {
-              const float old = t == 8 ? o0 : t == 9 ? o1 : t == 10 ? o2 : o3;
-              ggeo[4 * e + (t - 8)] = accumulate_geo ? old + tot : tot;
-            }
-          }
-        } else if (valid) {
-          for (int n0 = 0; n0 < nb; n0 += 8) {
-            float acc[8];
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-              acc[t] = 0.f;
-              if (n0 + t < nb) {
-                const float* w = s_w + (n0 + t) * 4 * C + c0;
-#pragma unroll
-                for (int b = 0; b < NZ; ++b)
-#pragma unroll
-                  for (int q = 0; q < CPL; ++q) acc[t] += gzl[b][q] * w[b * C + q];
-              }
-            }
-            const float tot = wave_sum8(acc);
-            const int t = wave_sum8_index(lane);
-            if ((lane & 7) == 0 && n0 + t < nb) gef[e * nb + n0 + t] = tot;
-          }
-          sf = wave_sum(sf);
-          su0 = wave_sum(su0);
-          su1 = wave_sum(su1);
-          su2 = wave_sum(su2);
-          if (lane == 0) {
-            float* gg = ggeo + 4 * e;
-            if (accumulate_geo) {
-              gg[0] += su0;
-              gg[1] += su1;
-              gg[2] += su2;
-              gg[3] += sf;
-            } else {
-              gg[0] = su0;
-              gg[1] = su1;
-              gg[2] = su2;
-              gg[3] = sf;
-            }
-          }
+          if (valid && (lane & 3) == 0 && t < nbv) gef[e * nb + t] = tot;
+          tg = tot;
+          tgi = (lane & 3) == 0 && t >= 8 && t < 12 ? t - 8 : -1;
+        } else {
+          const float tot = wave_sum16(red);
+          const int t = wave_sum16_index(lane);
+          if (valid && (lane & 3) == 0 && t < nbv) gef[e * nb + t] = tot;
+          float g8[8] = {su0, su1, su2, sf, 0.f, 0.f, 0.f, 0.f};
+          tg = wave_sum8(g8);
+          const int t8 = wave_sum8_index(lane);
+          tgi = (lane & 7) == 0 && t8 < 4 ? t8 : -1;
+        }
+        if (valid && tgi >= 0) {
+          const float old = tgi == 0 ? o0 : tgi == 1 ? o1 : tgi == 2 ? o2 : o3;
+          ggeo[4 * e + tgi] = accumulate_geo ? old + tg : tg;
         }
       }
     }
@@ -783,13 +759,20 @@ int launch_bwd_edge(bool h1, dim3 grid, hipStream_t s, const float* z, const flo
                     const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const float* h0,
                     const float* h1p, const float* gA0, const float* gA1, float inv_avg, float* gz, float* gzsum,
                     float* ggeo, int acc, const float* w1ef, int nb, float* gef) {
-  const size_t lds = w1ef ? (size_t)nb * 4 * 64 * CPL * sizeof(float) : 0;
-  if (h1)
-    hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, true>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne,
-                       e_cap, n, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef);
+  const bool wide = w1ef && nb > 8;  // radial rows padded to 16 instead of 8
+  const size_t lds = (size_t)(wide ? 16 : 8) * 4 * 64 * CPL * sizeof(float);
+#define FMD_BWD_EDGE(H, RB)                                                                                         \
+  hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, H, RB>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne,  \
+                     e_cap, n, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef)
+  if (h1 && wide)
+    FMD_BWD_EDGE(true, 16);
+  else if (h1)
+    FMD_BWD_EDGE(true, 8);
+  else if (wide)
+    FMD_BWD_EDGE(false, 16);
   else
-    hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, false>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne,
-                       e_cap, n, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef);
+    FMD_BWD_EDGE(false, 8);
+#undef FMD_BWD_EDGE
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

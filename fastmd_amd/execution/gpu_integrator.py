@@ -57,9 +57,11 @@ class StatefulIntegrator(Protocol):
 
     def set_forces(self, forces, energy=None) -> None: ...
 
-    def backup(self) -> None: ...
+    def backup(self, state=None) -> None: ...  # state (default: the live one) into the backup
 
-    def restore(self) -> None: ...
+    def restore(self, state=None) -> None: ...  # the backup into state (default: the live one)
+
+    def new_state(self): ...  # a state of the same shape (the runner's held window start)
 
     def snapshot(self) -> tuple: ...
 

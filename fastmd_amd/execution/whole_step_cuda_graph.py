@@ -91,8 +91,20 @@ class WholeStepGraphRunner:
         self.window_max_edges = torch.zeros(1, dtype=torch.int64, device=dev)
         self.window_max_isolated = torch.zeros(1, dtype=torch.int32, device=dev)
         self._window_stats = torch.zeros(7, dtype=torch.float64, device=dev)
-        self._stats_host = torch.zeros(7, dtype=torch.float64, pin_memory=True)
-        self._stats_event = None
+        # two host slots for the statistics of launched windows (one settled while the window
+        # launched behind it runs), each with the event of its copy
+        self._slots = [[torch.zeros(7, dtype=torch.float64, pin_memory=True), None] for _ in range(2)]
+        self._next_slot = 0
+        self._last_slot = None
+        # launch(behind=True): the unsettled window's start state (its integrator backup, which the
+        # window behind overwrites), kept for rewind()
+        self._held = None
+        # what refresh_unlikely() reads: the last settled window's largest displacement, whether it
+        # fell back, and the largest growth of the displacement per window with the current and the
+        # previous candidate list
+        self._settled_displacement = 0.0
+        self._settled_fallback = False
+        self._displacement_growth = [None, None]
         self.graph = None
         self.fallback_windows = 0
         self.candidate_refreshes = 0
@@ -176,22 +188,78 @@ class WholeStepGraphRunner:
         torch.cuda.synchronize(self.device)
 
     # ------------------------------------------------------------------ replay
-    def launch(self) -> None:
-        """Replay one window and start the asynchronous copy of its statistics."""
+    def launch(self, *, behind: bool = False) -> int:
+        """Replay one window without settling it and start the asynchronous copy of its statistics
+        into a host slot (no host synchronization); returns the slot for :meth:`launched_stats`.
+        ``behind``: the previously launched window is not settled yet; its start state, which this
+        window's backup overwrites, is kept first for :meth:`rewind` (whole_step_cuda_graph.py:598-627)."""
+        if behind:
+            if self._held is None:
+                self._held = self.integrator.new_state()
+            self.integrator.restore(self._held)  # its backup (the unsettled window's start) into held
         if self.graph is None:
             self._window_body()
         else:
             self.graph.replay()
         self.launches += 1
-        self._stats_host.copy_(self._window_stats, non_blocking=True)
-        self._stats_event = torch.cuda.Event()
-        self._stats_event.record()
+        slot = self._next_slot
+        self._next_slot ^= 1
+        host = self._slots[slot][0]
+        host.copy_(self._window_stats, non_blocking=True)
+        event = torch.cuda.Event()
+        event.record()
+        self._slots[slot][1] = event
+        self._last_slot = slot
+        return slot
+
+    def launched_stats(self, slot: int) -> WindowStats:
+        """The statistics of the window :meth:`launch` copied into ``slot``, once that copy is done
+        (waits for that window only)."""
+        host, event = self._slots[slot]
+        event.synchronize()
+        s = host.tolist()
+        return WindowStats(bool(s[0]), int(s[1]), float(s[3]), bool(s[4]), int(s[5]), int(s[6]))
 
     def read_stats(self) -> WindowStats:
         """Wait for the last launched window's statistics (the one host sync per window)."""
-        self._stats_event.synchronize()
-        s = self._stats_host.tolist()
-        return WindowStats(bool(s[0]), int(s[1]), float(s[3]), bool(s[4]), int(s[5]), int(s[6]))
+        return self.launched_stats(self._last_slot)
+
+    def settling_work(self, stats: WindowStats) -> str | None:
+        """What settling a window with these statistics changes beyond host bookkeeping
+        (whole_step_cuda_graph.py:629-639): "overflow" (rollback and growth, or the fallback replay),
+        "refresh" (new candidates; also a non-finite state, which raises), else None."""
+        if stats.capacity_overflow or stats.overflow:
+            return "overflow"
+        if not math.isfinite(stats.max_displacement):
+            return "refresh"
+        return "refresh" if stats.max_displacement >= self.proactive_refresh_fraction * self.builder.skin else None
+
+    def refresh_unlikely(self) -> bool:
+        """Whether the window in flight will likely neither refresh the candidates nor fall back
+        (whole_step_cuda_graph.py:586-596): the last settled window did not fall back, and its largest
+        displacement plus twice the largest growth per window seen with this or the previous
+        candidate list stays below the refresh threshold. A window launched behind one that does is
+        rolled back (one window of GPU time), so the driver launches none behind a likely one."""
+        growth = [g for g in self._displacement_growth if g is not None]
+        if not growth or self._settled_fallback:
+            return False
+        threshold = self.builder.skin * self.proactive_refresh_fraction
+        return self._settled_displacement + 2.0 * max(growth) < threshold
+
+    def rewind(self) -> None:
+        """Roll back the unsettled window and the one launched behind it to the unsettled window's
+        start (kept by ``launch(behind=True)``), which is also the backup again: settling the
+        unsettled window (its fallback or capacity rollback) then proceeds as if nothing had been
+        launched behind it."""
+        self.integrator.backup(self._held)  # the held start into the backup, then into the state
+        self.integrator.restore()
+        self.launches -= 1
+
+    def drop(self) -> None:
+        """Roll back the window launched last (behind another) to its start, the previous window's
+        end."""
+        self.integrator.restore()
+        self.launches -= 1
 
     def settle(self, stats: WindowStats) -> None:
         """Act on a window's flags (whole_step_cuda_graph.py:540-584)."""
@@ -204,11 +272,22 @@ class WholeStepGraphRunner:
             raise FixedCapacityOverflow(stats.max_edges)
         if stats.overflow:
             self._fallback()
+            # fresh candidates at the window's start: the displacement restarts (an upper bound of
+            # the growth follows from the next window), and none is launched behind the next one
+            self._settled_fallback = True
+            self._settled_displacement = 0.0
+            self._displacement_growth = [None, self._displacement_growth[0]]
             return
+        self._settled_fallback = False
+        growth = stats.max_displacement - self._settled_displacement
+        self._displacement_growth[0] = max(growth, self._displacement_growth[0] or 0.0)
+        self._settled_displacement = stats.max_displacement
         if stats.max_displacement >= self.proactive_refresh_fraction * self.builder.skin:
             self.builder.refresh_candidates(self.integrator.positions)
             self.candidate_refreshes += 1
             self.builder.assert_candidate_capacity()
+            self._settled_displacement = 0.0
+            self._displacement_growth = [None, self._displacement_growth[0]]
 
     def _fallback(self) -> None:
         """Roll the window back, refresh the candidates at its start state and replay it; if the

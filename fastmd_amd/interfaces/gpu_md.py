@@ -71,6 +71,11 @@ class GPUResidentMolecularDynamics:
         self.derivative = engine_derivative(model)
         self.task = task
         self.steps_per_launch = int(steps_per_launch)
+        # run(): launch each next whole-step window before the host reads the flags of the one in
+        # flight (see run); counters of the windows launched so and of those rolled back
+        self.launch_behind = True
+        self.windows_ahead = 0
+        self.windows_rolled_back = 0
         self.validate_isolated_atoms = bool(validate_isolated_atoms)
         positions, cell, numbers, masses, atom_momenta = _atoms_arrays(atoms)
         self.n_atoms = int(positions.shape[0])
@@ -185,7 +190,15 @@ class GPUResidentMolecularDynamics:
         self.whole_step_capacity_history.append(self._capacity.u_capacity)
 
     def run(self, steps: int) -> None:
-        """``steps`` MD steps (a multiple of ``steps_per_launch`` in the whole-step mode)."""
+        """``steps`` MD steps (a multiple of ``steps_per_launch`` in the whole-step mode).
+
+        Whole-step windows are pipelined as the reference's ``_run_windows``
+        (gpu_md.py:1882-1975): the next window is launched before the host reads the flags of the
+        one in flight, unless that one will likely refresh the candidates, so the GPU does not wait
+        for the host (graph submission, flag read) between windows. When the settled window needs
+        more than bookkeeping, the window behind it is rolled back: to the settled window's end
+        before a candidate refresh, to its start before a fallback or a capacity growth; the
+        trajectory is the one of windows settled one at a time, bitwise."""
         steps = int(steps)
         if self.whole_step_runner is None:
             for _ in range(steps):
@@ -195,14 +208,41 @@ class GPUResidentMolecularDynamics:
             raise ValueError(f"steps ({steps}) must be a multiple of steps_per_launch ({self.steps_per_launch})")
         windows = steps // self.steps_per_launch
         done = 0
-        while done < windows:
-            try:
-                self.whole_step_runner.replay()
-            except FixedCapacityOverflow as overflow:
-                self._grow_whole_step_runner(overflow.edge_count)
-                continue
-            done += 1
-            self.steps += self.steps_per_launch
+        ahead = None  # the slot of the window launched behind the one being settled
+        runner = None
+        try:
+            while done < windows:
+                runner = self.whole_step_runner
+                slot, ahead = (runner.launch() if ahead is None else ahead), None
+                # the next window goes into the stream before the host reads this one's flags (so the
+                # GPU does not wait for the host between windows), unless this one will likely
+                # refresh the candidates (gpu_md.py:1882-1975)
+                if self.launch_behind and done + 1 < windows and runner.refresh_unlikely():
+                    ahead = runner.launch(behind=True)
+                    self.windows_ahead += 1
+                stats = runner.launched_stats(slot)
+                work = runner.settling_work(stats)
+                if ahead is not None and work is not None:
+                    # the window behind ran on what this one's settling changes: roll it back (to this
+                    # window's end for a candidate refresh, to this window's start for a fallback or
+                    # a growth) and settle this one as if nothing had been launched behind it
+                    if work == "refresh":
+                        runner.drop()
+                    else:
+                        runner.rewind()
+                    ahead = None
+                    self.windows_rolled_back += 1
+                try:
+                    runner.settle(stats)
+                except FixedCapacityOverflow as overflow:
+                    self._grow_whole_step_runner(overflow.edge_count)
+                    continue
+                done += 1
+                self.steps += self.steps_per_launch
+        except BaseException:
+            if ahead is not None:  # back to the end of the window settled (or being settled)
+                runner.drop()
+            raise
 
     # ------------------------------------------------------------------ observables
     @property
@@ -236,4 +276,6 @@ class GPUResidentMolecularDynamics:
             stats[key] += self._retired_stats.get(key, 0)
         stats["max_edge_count"] = max(stats["max_edge_count"], self._retired_stats.get("max_edge_count", 0))
         stats["capacity_history"] = list(self.whole_step_capacity_history)
+        stats["windows_ahead"] = self.windows_ahead
+        stats["windows_rolled_back"] = self.windows_rolled_back
         return stats

@@ -39,7 +39,7 @@ from torch.autograd import Function
 from fastmd_amd import _abi
 from fastmd_amd.adapters.protocol import CapacityStep, CaptureContract, GraphBatch, PaddingRule, TopologySpec
 from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr
-from fastmd_amd.ops.wide_gemm import gemm, gemm_gather
+from fastmd_amd.ops.wide_gemm import gemm, gemm_gather, gemm_group
 
 _ELEMENTS = 118
 _CAPACITY_STEP = CapacityStep(u_step=32, min_pad_u=32, u_thermal_factor=1.02)
@@ -277,13 +277,20 @@ class _MaceLikeEnergy(Function):
                       w["wout0"].data_ptr(), w["wout1"].data_ptr(), n, C, P0.data_ptr(), P1.data_ptr(),
                       B0.data_ptr(), _abi.ptr(B1), h0n.data_ptr(), _abi.ptr(h1n))
             else:
-                P0 = gemm(A0, layer.Wm0, b_layout=1)
-                P1 = gemm(A1.view(3 * n, C), layer.Wm1, b_layout=1).view(n, 3, C)
+                # the node side as two grouped GEMM launches around the contraction:
+                # (P0 = A0 Wm0, P1 = A1 Wm1), then (h0n = [B0 | h0] [Wo0; Wsc0], h1n = B1 Wo1)
+                P0 = _empty(n, C, device=dev)
+                P1 = _empty(n, 3, C, device=dev)
+                gemm_group([{"a": A0, "b": layer.Wm0, "out": P0},
+                            {"a": A1.view(3 * n, C), "b": layer.Wm1, "out": P1.view(3 * n, C)}], b_layout=1)
                 _call("fmd_mace_symcon_f32", P0.data_ptr(), P1.data_ptr(), elem.data_ptr(), layer.Wc.data_ptr(),
                       layer.Wd.data_ptr(), n, C, B0.data_ptr(), _abi.ptr(B1))
-                h0n = gemm(B0, layer.Wo0, b_layout=1)
-                gemm(h0, layer.Wsc0, b_layout=1, out=h0n, accumulate=True)
-                h1n = None if last else gemm(B1.view(3 * n, C), layer.Wo1, b_layout=1).view(n, 3, C)
+                h0n = _empty(n, C, device=dev)
+                h1n = None if last else _empty(n, 3, C, device=dev)
+                probs = [{"a": B0, "a2": h0, "b": model.node_weights(t)["wo0st"], "out": h0n}]
+                if not last:
+                    probs.append({"a": B1.view(3 * n, C), "b": layer.Wo1, "out": h1n.view(3 * n, C)})
+                gemm_group(probs, b_layout=1)
             saved.append((h0, h1, z, q, P0, P1))
             if t == 0:
                 h_first = h0n
@@ -351,13 +358,26 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
                   _abi.ptr(gB1), _abi.ptr(g_in0), 1 if t == 1 else 0, gP0.data_ptr(), gP1.data_ptr(),
                   gA0.data_ptr(), gA1.data_ptr())
         else:
-            gB0 = gemm(g_out0, layer.Wo0, b_layout=0)
-            gB1 = None if g_out1 is None else gemm(g_out1.reshape(3 * n, C), layer.Wo1, b_layout=0)
+            # two grouped GEMM launches around the contraction's VJP: (gB0 = g_out0 Wo0^T,
+            # gB1 = g_out1 Wo1^T, and with t > 0 this layer's input gradient through the residual,
+            # g_in0 = g_out0 Wsc0^T, added to the first readout's gradient in the second layer),
+            # then (gA0 = gP0 Wm0^T, gA1 = gP1 Wm1^T)
+            gB0 = _empty(n, C, device=dev)
+            gB1 = None if g_out1 is None else _empty(n, 3, C, device=dev)
+            probs = [{"a": g_out0, "b": layer.Wo0, "out": gB0}]
+            if gB1 is not None:
+                probs.append({"a": g_out1.reshape(3 * n, C), "b": layer.Wo1, "out": gB1.view(3 * n, C)})
+            if t > 0:
+                g_in0 = gha if t == 1 else _empty(n, C, device=dev)
+                probs.append({"a": g_out0, "b": layer.Wsc0, "out": g_in0, "accumulate": t == 1})
+            gemm_group(probs, b_layout=0)
             _call("fmd_mace_symcon_bwd_f32", P0.data_ptr(), P1.data_ptr(), inputs.elem.data_ptr(),
                   layer.Wc.data_ptr(), layer.Wd.data_ptr(), gB0.data_ptr(), _abi.ptr(gB1), n, C, gP0.data_ptr(),
                   gP1.data_ptr())
-            gA0 = gemm(gP0, layer.Wm0, b_layout=0)
-            gA1 = gemm(gP1.view(3 * n, C), layer.Wm1, b_layout=0)
+            gA0 = _empty(n, C, device=dev)
+            gA1 = _empty(n, 3, C, device=dev)
+            gemm_group([{"a": gP0, "b": layer.Wm0, "out": gA0},
+                        {"a": gP1.view(3 * n, C), "b": layer.Wm1, "out": gA1.view(3 * n, C)}], b_layout=0)
         acc_geo = 1 if t < L - 1 else 0
         if t == 0:
             # the first layer's inputs are the element embedding (no position dependence): only

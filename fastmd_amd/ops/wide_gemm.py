@@ -57,6 +57,63 @@ def gemm(a: Tensor, b: Tensor, *, b_layout: int, bias: Tensor | None = None, out
     return out
 
 
+def gemm_group(problems, *, b_layout: int, epilogue: str | None = None) -> list:
+    """Up to four independent ``gemm`` problems of one ``b_layout`` in one launch
+    (fmd_gemm_group_f32). Each problem is a dict with ``a``, ``b``, ``out`` (float32, preallocated,
+    unit column stride) and optionally ``a2`` (extra K columns: ``[a | a2] @ op(b)``, a's width a
+    multiple of 32), ``bias``, ``accumulate``. Returns the outputs."""
+    if not 1 <= len(problems) <= 4:
+        raise ValueError("gemm_group takes one to four problems")
+    cols = {k: [] for k in ("a", "lda", "a2", "lda2", "ksplit", "b", "ldb", "bias", "c", "ldc", "m", "n", "k", "acc")}
+    keep = []
+    for p in problems:
+        a, b, out, a2, bias = p["a"], p["b"], p["out"], p.get("a2"), p.get("bias")
+        require_cuda(a, b, out, a2, bias)
+        for t in (a, b, out) + ((a2,) if a2 is not None else ()):
+            if t.dim() != 2 or t.dtype != torch.float32:
+                raise ValueError("gemm_group operands must be 2-D float32")
+        a, lda = rows_view(a)
+        b, ldb = rows_view(b)
+        m, ka = a.shape
+        k2 = 0
+        if a2 is not None:
+            a2, lda2 = rows_view(a2)
+            if a2.shape[0] != m or ka % 32 != 0:
+                raise ValueError("gemm_group: a2 must have a's rows and a's width must be a multiple of 32")
+            k2 = a2.shape[1]
+        k = ka + k2
+        n = b.shape[0] if b_layout == 0 else b.shape[1]
+        if (b.shape[1] if b_layout == 0 else b.shape[0]) != k:
+            raise ValueError(f"gemm_group shape mismatch: K {k} vs b {tuple(b.shape)} (layout {b_layout})")
+        if out.shape != (m, n) or out.stride(1) != 1:
+            raise ValueError(f"gemm_group: out must be [{m}, {n}] with unit column stride")
+        if bias is not None:
+            if bias.shape != (n,) or bias.dtype != torch.float32:
+                raise ValueError("bias must be float32 [N]")
+            bias = bias.contiguous()
+        keep += [a, b, out, a2, bias]
+        cols["a"].append(a.data_ptr())
+        cols["lda"].append(lda)
+        cols["a2"].append(None if a2 is None else a2.data_ptr())
+        cols["lda2"].append(0 if a2 is None else lda2)
+        cols["ksplit"].append(ka if a2 is not None else k)
+        cols["b"].append(b.data_ptr())
+        cols["ldb"].append(ldb)
+        cols["bias"].append(None if bias is None else bias.data_ptr())
+        cols["c"].append(out.data_ptr())
+        cols["ldc"].append(out.stride(0) if m > 1 else n)
+        cols["m"].append(m)
+        cols["n"].append(n)
+        cols["k"].append(k)
+        cols["acc"].append(1 if p.get("accumulate") else 0)
+    i64 = lambda key: _abi.array(_abi._i64, cols[key])  # noqa: E731
+    _abi.call("fmd_gemm_group_f32", len(problems), _abi.ptr_array(cols["a"]), i64("lda"), _abi.ptr_array(cols["a2"]),
+              i64("lda2"), i64("ksplit"), _abi.ptr_array(cols["b"]), i64("ldb"), b_layout,
+              _abi.ptr_array(cols["bias"]), _abi.ptr_array(cols["c"]), i64("ldc"), i64("m"), i64("n"), i64("k"),
+              _abi.array(_abi._i32, cols["acc"]), _EPILOGUES[epilogue], stream())
+    return [p["out"] for p in problems]
+
+
 _EUNSUPPORTED = 10002
 
 

@@ -176,6 +176,19 @@ int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32
                  const float* bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k,
                  int32_t accumulate, int32_t epilogue, hipStream_t stream);
 
+/* Up to four independent fmd_gemm_f32 problems of one b_layout in one launch (arrays of length
+ * count, problem g: C_g = [A_g | A2_g] op(B_g) (+ bias_g) (+ C_g if accumulate_g)). A2_g (may be
+ * null, or the a2 array itself null) supplies K columns [ksplit_g, K_g) with row stride lda2_g;
+ * ksplit_g % 32 == 0. Every problem runs the 64 x 64 fp32 MFMA tiles of fmd_gemm_f32 (same K
+ * order). Replaces several linear / matmul calls on independent operands
+ * (triton_wide_gemm.py:482-553) with one launch: the node side of an interaction layer, whose
+ * per-layer GEMMs are each too small to fill the chip. bias and accumulate may be null. */
+int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda, const float* const* a2,
+                       const int64_t* lda2, const int64_t* ksplit, const float* const* b, const int64_t* ldb,
+                       int32_t b_layout, const float* const* bias, float* const* c, const int64_t* ldc,
+                       const int64_t* m, const int64_t* n, const int64_t* k, const int32_t* accumulate,
+                       int32_t epilogue, hipStream_t stream);
+
 /* C[M,N] = A[M,K] B[N,K]^T (+ bias) (+ C) with the gather-cat fused into the operand load:
  * A = cat(part_0, ..., part_{n-1}) over n_parts <= 3 column blocks, part p reading row
  * indices_p[r * index_strides_p] of srcs_p (or row r when indices_p is null), width widths_p,

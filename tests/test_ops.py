@@ -201,6 +201,62 @@ def test_gemm_fp32_large_tiles(device):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("b_layout", [0, 1])
+def test_gemm_group_matches_single_gemms_and_fp64(device, b_layout):
+    """fmd_gemm_group_f32: four problems of mixed shapes (ragged M, an empty one, a K split
+    [a | a2], accumulate and bias) in one launch, each bitwise equal to the same problem through
+    fmd_gemm_f32's 64 x 64 kernel (same K order) and within fp32 of float64."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm, gemm_group
+
+    g = torch.Generator().manual_seed(11)
+
+    def weight(k, n):
+        w = torch.randn(k, n, generator=g) / k ** 0.5
+        return w if b_layout == 1 else w.t().contiguous()  # stored [K, N] or [N, K]
+
+    def ref_of(a, w):
+        wk = w if b_layout == 1 else w.t()
+        return a.double() @ wk.double()
+
+    shapes = [(135, 128, 128), (405, 128, 128), (0, 128, 64), (1000, 64, 192)]
+    probs, refs, singles = [], [], []
+    for (m, k, n) in shapes:
+        a = torch.randn(m, k, generator=g)
+        w = weight(k, n)
+        ref = ref_of(a, w)
+        out = torch.empty(m, n, device=device)
+        probs.append({"a": a.to(device), "b": w.to(device), "out": out})
+        refs.append(ref)
+        singles.append(gemm(a.to(device), w.to(device), b_layout=b_layout))
+    # accumulate + bias on the last problem
+    c0 = torch.randn(1000, 192, generator=g)
+    bias = torch.randn(192, generator=g)
+    probs[3]["out"] = c0.to(device)
+    probs[3]["accumulate"] = True
+    probs[3]["bias"] = bias.to(device)
+    refs[3] = refs[3] + c0.double() + bias.double()
+    out_single = c0.to(device)
+    gemm(probs[3]["a"], probs[3]["b"], b_layout=b_layout, out=out_single, accumulate=True, bias=bias.to(device))
+    singles[3] = out_single
+    gemm_group(probs, b_layout=b_layout)
+    for p, ref, single in zip(probs, refs, singles):
+        assert torch.equal(p["out"], single)
+        if ref.numel():
+            assert oops.relative(p["out"].cpu().numpy(), ref.numpy()) < 1e-5
+    # K split: [a | a2] @ [W0; W1] in one accumulation
+    m, k1, k2, n = 777, 128, 128, 128
+    a, a2 = torch.randn(m, k1, generator=g), torch.randn(m, k2, generator=g)
+    w = weight(k1 + k2, n)
+    out = torch.empty(m, n, device=device)
+    gemm_group([{"a": a.to(device), "a2": a2.to(device), "b": w.to(device), "out": out}], b_layout=b_layout)
+    single = gemm(torch.cat([a, a2], 1).to(device), w.to(device), b_layout=b_layout)
+    assert torch.equal(out, single)
+    assert oops.relative(out.cpu().numpy(), ref_of(torch.cat([a, a2], 1), w).numpy()) < 1e-5
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("F", [64, 128])
 def test_gemm_bf16_against_fp64_of_rounded_inputs(device, F):
     import torch

@@ -93,6 +93,40 @@ def test_whole_step_capacity_growth_and_refresh_paths(device):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("model_name", ["morse", "mace_like"])
+def test_windows_launched_behind_match_settled_windows_bitwise(device, model_name, monkeypatch):
+    """run() launches each next window before the host reads the flags of the one in flight. With
+    a launch behind EVERY window (refresh_unlikely forced true) and a tiny skin and capacity step
+    (candidate refreshes, fallbacks and a capacity growth behind which windows were launched),
+    the rollbacks (drop to the window's end, rewind to its start) give the trajectory of windows
+    settled one at a time, bitwise."""
+    import torch
+
+    from fastmd_amd.execution.whole_step_cuda_graph import WholeStepGraphRunner
+    from fastmd_amd.models.mace_like import MaceLikeAdapter
+    from fastmd_amd.models.pair_potential import MorsePairAdapter
+
+    print(f"[launch behind] {model_name}", flush=True)
+    make = (lambda: MorsePairAdapter(device=device)) if model_name == "morse" else (
+        lambda: MaceLikeAdapter(device=device))
+    s = systems.perovskite(3)
+    tight = CapacityConfig(u_step=1, min_pad_u=0, candidate_skin=0.05)
+    settled = _md(make(), "whole_step", device, steps_per_launch=2, capacity=tight, system=s)
+    settled.launch_behind = False
+    settled.run(40)
+    monkeypatch.setattr(WholeStepGraphRunner, "refresh_unlikely", lambda self: True)
+    behind = _md(make(), "whole_step", device, steps_per_launch=2, capacity=tight, system=s)
+    behind.run(40)
+    a, b = _state(settled), _state(behind)
+    assert torch.equal(a, b), float((a - b).abs().max())
+    sa, sb = settled.whole_step_stats(), behind.whole_step_stats()
+    print(sa, sb, flush=True)
+    assert sb["windows_ahead"] >= 19 and sb["windows_rolled_back"] > 0 and sa["windows_ahead"] == 0
+    for key in ("launches", "candidate_refreshes", "fallback_windows", "capacity_history"):
+        assert sa[key] == sb[key], key
+
+
+@pytest.mark.gpu
 def test_whole_step_morse_md_matches_cpu_oracle(device):
     """configs[0] plumbing: Morse MD (NHC 500 K, dt 0.25 fs) for 200 steps on the GPU vs the CPU
     oracle (numpy NHC + PyTorch-CPU Morse forces in float32, like the GPU): positions agree to fp32
