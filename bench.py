@@ -8,7 +8,7 @@ model, NVT Nose-Hoover chain at 500 K (tdamp 25 fs, tchain 3, tloop 1, dt 0.25 f
 F = 128) are reported beside it, with the dominant kernel's roofline and the CPU baseline (the
 PyTorch-CPU eager oracle on this host's cores, a bounded sample of the same workload).
 
-  python bench.py [--gpus 1] [--steps 200] [--warmup 600] [--no-cpu] [--quick] [--ops] [--scaling]
+  python bench.py [--gpus 1] [--steps 1000] [--warmup 1000] [--no-cpu] [--quick] [--ops] [--scaling]
 """
 from __future__ import annotations
 
@@ -28,6 +28,7 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 SPLIT_PRODUCTS = 6  # fp32-accurate GEMM: three bf16 planes per operand, six MFMA products
 SPIN_CYCLES = 20_000_000  # GPU clock cycles of torch.cuda._sleep (several ms)
+ROOFLINE_KERNEL = "gemm_x3p_kernel<true>"
 STEPS_PER_LAUNCH = 10
 
 
@@ -89,20 +90,21 @@ def time_kernel(fn, reps: int = 20) -> float:
 
 
 def gemm_roofline(md) -> dict:
-    """The dominant kernel of the 10 000-atom step: the edge GEMM of the interaction,
+    """The dominant kernel of the 10 000-atom step: the second layer's edge GEMM,
     z = [h0[src] | ef] @ W1[sender and radial rows] (the receiver block h0[dst] @ W1[C:2C] is formed
     per atom and added by the message kernels), with the gather-cat fused into the operand load
-    (gemm_x3_kernel: [e_cap, C+8] x [C+8, 4C] in the second layer, fp32-accurate as six bf16 MFMA
-    products). It is timed in the context of the step: HIP events on torch's current stream (the
-    stream it is launched on) around every edge GEMM of 10 eager force evaluations at the run's
-    final state (its edge list, capacity and features), the model's own timing hook; each
-    evaluation is queued behind a spin kernel so that no host latency falls inside the event
-    pairs. Algorithmic flops = 2 M K N per launch; the ceiling of fp32 work done this way is the
-    dense bf16 MFMA peak over the six products. ``isolated_launch_us`` is the same launch repeated back to back."""
+    and the operands pre-split into bf16 planes (gemm_x3p_kernel<true>: [e_cap, C+8] x [C+8, 4C],
+    fp32-accurate as six bf16 MFMA products). It is timed in the context of the step: HIP events on
+    torch's current stream (the stream it is launched on) around every edge GEMM of 10 eager force
+    evaluations at the run's final state (its edge list, capacity and features), the model's own
+    timing hook; each evaluation is queued behind a spin kernel so that no host latency falls
+    inside the event pairs. Algorithmic flops = 2 M K N per launch; the ceiling of fp32 work done
+    this way is the dense bf16 MFMA peak over the six products. ``isolated_launch_us`` is the same
+    launch repeated back to back."""
     import torch
 
     from fastmd_amd.models import mace_like
-    from fastmd_amd.ops.wide_gemm import gemm_gather
+    from fastmd_amd.ops.wide_gemm import gemm_planes, split_planes
 
     runner = md.whole_step_runner
     torch.cuda.synchronize()
@@ -127,17 +129,17 @@ def gemm_roofline(md) -> dict:
     C = module.config.channels
     ei = runner.builder.batch.edge_index
     gen = torch.Generator(device="cpu").manual_seed(0)
-    h0 = torch.randn(md.n_atoms, C, generator=gen).to(md.device)
-    ef = torch.randn(m, k - C, generator=gen).to(md.device)
+    h0p = split_planes(torch.randn(md.n_atoms, C, generator=gen).to(md.device))
+    efp = split_planes(torch.randn(m, k - C, generator=gen).to(md.device))
     out = torch.empty(m, n, device=md.device)
-    w = module.w1_sender_t(0)
-    t_iso = time_kernel(lambda: gemm_gather([(h0, ei[:, 1]), (ef, None)], w, out=out), reps=20)
+    w = module.w1_planes(len(module.layers) - 1, "sender", n)
+    t_iso = time_kernel(lambda: gemm_planes([(h0p, ei[:, 1]), (efp, None)], w, a_planes=True, out=out), reps=20)
     flops = 2.0 * m * k * n
     achieved = flops / t / 1e12
     peak = BF16_MFMA_PEAK_TFLOPS / SPLIT_PRODUCTS
     return {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
-            "frac": round(achieved / peak, 4), "traffic": _traffic("gemm_x3_kernel", [m, k, n]),
-            "kernel": "gemm_x3_kernel", "launch_us": round(t * 1e6, 2), "launches_timed": len(durations),
+            "frac": round(achieved / peak, 4), "traffic": _traffic(ROOFLINE_KERNEL, [m, k, n]),
+            "kernel": ROOFLINE_KERNEL, "launch_us": round(t * 1e6, 2), "launches_timed": len(durations),
             "isolated_launch_us": round(t_iso * 1e6, 2), "flops_per_launch": flops,
             "peak_basis": f"fp32 GEMM as {SPLIT_PRODUCTS} bf16 MFMA products: dense bf16 peak "
                           f"{BF16_MFMA_PEAK_TFLOPS} TFLOP/s / {SPLIT_PRODUCTS}",

@@ -483,8 +483,8 @@ __global__ void __launch_bounds__(kThreads) gemm_bf16_kernel(const uint16_t* __r
 // K in slices of 16: every thread loads two float4 of A and two of B (a row's 16 k take four
 // threads), splits them into the three bf16 planes and stores 8-byte pieces into LDS; the 8-k
 // chunk pair of LDS row r is swapped when bit 3 of r is set, so the sixteen 16-byte operand reads
-// of a quarter wave hit distinct bank groups. Two LDS buffers (48 KB: three workgroups per CU at
-// 148 VGPRs): slice kt + 1 is split and stored, and slice kt + 2 loaded into registers, while
+// of a quarter wave hit distinct bank groups. Two LDS buffers (48 KB: three workgroups per CU,
+// the register budget held to three waves per SIMD): slice kt + 1 is split and stored, and slice kt + 2 loaded into registers, while
 // the MFMAs of slice kt run. Part widths are multiples of 4 and all but the last multiples of 16
 // (a slice never straddles two parts); k past a part's width or past K loads as zero. An optional
 // gathered row is added to each output row before the epilogue (C[r] += Q[idx[r]]: the receiver
@@ -558,17 +558,17 @@ constexpr int X3_PL = 128 * 16, X3_OP = 3 * X3_PL, X3_BUF = 2 * X3_OP;
       _Pragma("unroll") for (int j = 0; j < 2; ++j)                                                 \
         bv_[p][j] = *reinterpret_cast<const bf16x8*>(bs_ + p * X3_PL + (wn * 64 + j * 32) * 16 + rd); \
     }                                                                                               \
-    _Pragma("unroll") for (int i = 0; i < 2; ++i) _Pragma("unroll") for (int j = 0; j < 2; ++j) {   \
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[0][i], bv_[2][j], acc[i][j], 0, 0, 0); \
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[1][i], bv_[1][j], acc[i][j], 0, 0, 0); \
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[2][i], bv_[0][j], acc[i][j], 0, 0, 0); \
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[0][i], bv_[1][j], acc[i][j], 0, 0, 0); \
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[1][i], bv_[0][j], acc[i][j], 0, 0, 0); \
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[0][i], bv_[0][j], acc[i][j], 0, 0, 0); \
+    /* product-major: consecutive MFMAs go to the four accumulators in turn (four independent   \
+       chains in flight); each accumulator still takes its six products in the same order */     \
+    _Pragma("unroll") for (int pr = 0; pr < 6; ++pr) {                                              \
+      const int pa_ = pr == 0 ? 0 : pr == 1 ? 1 : pr == 2 ? 2 : pr == 3 ? 0 : pr == 4 ? 1 : 0;      \
+      const int pb_ = pr == 0 ? 2 : pr == 1 ? 1 : pr == 2 ? 0 : pr == 3 ? 1 : pr == 4 ? 0 : 0;      \
+      _Pragma("unroll") for (int i = 0; i < 2; ++i) _Pragma("unroll") for (int j = 0; j < 2; ++j)   \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[pa_][i], bv_[pb_][j], acc[i][j], 0, 0, 0); \
     }                                                                                               \
   } while (0)
 
-__global__ void __launch_bounds__(kThreads) gemm_x3_kernel(X3Part P0, X3Part P1, X3Part P2, int np,
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) gemm_x3_kernel(X3Part P0, X3Part P1, X3Part P2, int np,
                                                            const float* __restrict__ b, int64_t ldb, X3Part radd,
                                                            const float* __restrict__ bias, float* c, int64_t ldc,
                                                            int64_t m, int64_t n, int64_t k, int accumulate, int act,
@@ -651,6 +651,205 @@ __global__ void __launch_bounds__(kThreads) gemm_x3_kernel(X3Part P0, X3Part P1,
   epilogue<2, 2>(acc, row0, col0, m, n, bias, c, ldc, accumulate, act);
 }
 
+// ------------------------------------------------- fp32 as three bf16 planes, pre-split operands
+// The same product as gemm_x3_kernel (same planes, same six MFMA products in the same order, same
+// K order: bitwise the same C) with the operands split into their bf16 planes beforehand
+// (split3_kernel): B always (a weight, split once), A either split (APRE: the planes of per-atom
+// features and per-edge radial rows, split once per evaluation instead of once per column tile)
+// or fp32 split here. Plane arrays are slice-interleaved, [rows][S][3][16] bf16 (S = width / 16
+// rounded up, zero past the width): the three planes of a row's 16-k slice are 96 contiguous
+// bytes, so a slice of a gathered row is one contiguous read. The loader copies them into LDS
+// without arithmetic: the 768 16-byte chunks of an operand slice (128 rows x 3 planes x 2 halves)
+// go to the 256 threads three each, consecutive threads on consecutive chunks of a row.
+struct X3PPart {
+  const void* src;
+  const int32_t* idx;
+  int64_t ld, istride;  // ld: row stride in elements (48 S for planes)
+  int32_t width;
+};
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// XP_LOAD(K0, S): slice K0 into register stage S (pa##S / pb##S, or ra##S for fp32 A);
+// XP_STORE(BUFI, S): stage S into LDS buffer BUFI
+#define XP_LOAD(K0, S)                                                                              \
+  do {                                                                                              \
+    const int64_t k0_ = (K0);                                                                       \
+    if constexpr (APRE) {                                                                           \
+      const bool q2_ = k0_ >= ks2, q1_ = !q2_ && k0_ >= ks1;                                        \
+      const __bf16* base_ = q2_ ? ap2 : q1_ ? ap1 : ap0;                                            \
+      const int64_t kin_ = q2_ ? k0_ - ks2 : q1_ ? k0_ - ks1 : k0_;                                 \
+      const bool ok_ = kin_ < (q2_ ? w2 : q1_ ? w1 : w0);                                           \
+      _Pragma("unroll") for (int j = 0; j < 3; ++j) {                                               \
+        const int64_t o_ = (q2_ ? ao2[j] : q1_ ? ao1[j] : ao0[j]) + kin_ * 3;                       \
+        pa##S[j] = ok_ ? *reinterpret_cast<const u32x4*>(base_ + o_) : u32x4{0, 0, 0, 0};           \
+      }                                                                                             \
+    } else {                                                                                        \
+      const bool q2_ = k0_ >= ks2, q1_ = !q2_ && k0_ >= ks1;                                        \
+      const float* base_ = q2_ ? fa2 : q1_ ? fa1 : fa0;                                             \
+      const int64_t kin_ = q2_ ? k0_ - ks2 : q1_ ? k0_ - ks1 : k0_;                                 \
+      const int w_ = q2_ ? w2 : q1_ ? w1 : w0;                                                      \
+      _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                               \
+        const int64_t o_ = q2_ ? ao2[q] : q1_ ? ao1[q] : ao0[q];                                    \
+        ra##S[q] = (kin_ + kc < w_) ? *reinterpret_cast<const float4*>(base_ + o_ + kin_)           \
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);                              \
+      }                                                                                             \
+    }                                                                                               \
+    _Pragma("unroll") for (int j = 0; j < 3; ++j)                                                   \
+      pb##S[j] = *reinterpret_cast<const u32x4*>(bp + bo[j] + k0_ * 3);                            \
+  } while (0)
+
+#define XP_STORE(BUFI, S)                                                                           \
+  do {                                                                                              \
+    __bf16* sb_ = lds + (BUFI) * X3_BUF;                                                            \
+    if constexpr (APRE) {                                                                           \
+      _Pragma("unroll") for (int j = 0; j < 3; ++j)                                                 \
+        *reinterpret_cast<u32x4*>(sb_ + soffp[j]) = pa##S[j];                                       \
+    } else {                                                                                        \
+      _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                               \
+        bf16x4 x0_, x1_, x2_;                                                                       \
+        split3(ra##S[q], x0_, x1_, x2_);                                                            \
+        *reinterpret_cast<bf16x4*>(sb_ + 0 * X3_PL + soff[q]) = x0_;                                \
+        *reinterpret_cast<bf16x4*>(sb_ + 1 * X3_PL + soff[q]) = x1_;                                \
+        *reinterpret_cast<bf16x4*>(sb_ + 2 * X3_PL + soff[q]) = x2_;                                \
+      }                                                                                             \
+    }                                                                                               \
+    _Pragma("unroll") for (int j = 0; j < 3; ++j)                                                   \
+      *reinterpret_cast<u32x4*>(sb_ + X3_OP + soffp[j]) = pb##S[j];                                 \
+  } while (0)
+
+// Two register stages (loads issued two slices ahead) measured no faster than one at two waves
+// per SIMD instead of three, so the kernel keeps one stage: slice kt + 1 is stored into LDS and
+// slice kt + 2 loaded into the stage while the MFMAs of slice kt run.
+template <bool APRE>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) gemm_x3p_kernel(
+    X3PPart P0, X3PPart P1, X3PPart P2, int np, const __bf16* __restrict__ bp, int64_t ldb, X3Part radd,
+    const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int accumulate, int act,
+    int64_t n_tiles) {
+  __shared__ __attribute__((aligned(16))) __bf16 lds[2 * X3_BUF];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, rr = lane & 31;
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t row_blk = (tile / n_tiles) * 128, col_blk = (tile % n_tiles) * 128;
+  const int64_t ks1 = P0.width, ks2 = ks1 + (np > 1 ? P1.width : 0);
+  const int w0 = P0.width, w1 = P1.width, w2 = P2.width;
+  const __bf16 *ap0 = static_cast<const __bf16*>(P0.src), *ap1 = static_cast<const __bf16*>(P1.src),
+               *ap2 = static_cast<const __bf16*>(P2.src);
+  const float *fa0 = static_cast<const float*>(P0.src), *fa1 = static_cast<const float*>(P1.src),
+              *fa2 = static_cast<const float*>(P2.src);
+  // plane loader: chunk t + 256 j = (row, plane, half) of the slice: row c / 6, plane (c % 6) / 2,
+  // half c % 2; its 8 k sit at 8 (c % 6) in the row's 48-element slice block
+  int soffp[3];
+  int64_t bo[3], ao0[3], ao1[3], ao2[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int cidx = t + j * kThreads, r = cidx / 6, sub = cidx - r * 6, pl = sub >> 1, hf = sub & 1;
+    soffp[j] = pl * X3_PL + r * 16 + ((hf ^ ((r >> 3) & 1)) * 8);
+    bo[j] = min(col_blk + r, n - 1) * ldb + sub * 8;
+    if (APRE) {
+      const int64_t gr = min(row_blk + r, m - 1);
+      ao0[j] = (P0.idx ? (int64_t)P0.idx[gr * P0.istride] : gr) * P0.ld + sub * 8;
+      ao1[j] = np > 1 ? (P1.idx ? (int64_t)P1.idx[gr * P1.istride] : gr) * P1.ld + sub * 8 : 0;
+      ao2[j] = np > 2 ? (P2.idx ? (int64_t)P2.idx[gr * P2.istride] : gr) * P2.ld + sub * 8 : 0;
+    }
+  }
+  // fp32 loader (!APRE): row (t + 256 q) / 4, k (t % 4) * 4
+  const int kc = (t & 3) * 4;
+  int soff[2];
+  if (!APRE) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int r = (t + q * kThreads) >> 2;
+      const int64_t gr = min(row_blk + r, m - 1);
+      ao0[q] = (P0.idx ? (int64_t)P0.idx[gr * P0.istride] : gr) * P0.ld + kc;
+      ao1[q] = np > 1 ? (P1.idx ? (int64_t)P1.idx[gr * P1.istride] : gr) * P1.ld + kc : 0;
+      ao2[q] = np > 2 ? (P2.idx ? (int64_t)P2.idx[gr * P2.istride] : gr) * P2.ld + kc : 0;
+      soff[q] = r * 16 + (((kc >> 3) ^ ((r >> 3) & 1)) * 8) + (kc & 7);
+    }
+  }
+  const int rd = rr * 16 + ((h ^ ((rr >> 3) & 1)) * 8);  // this lane's 8 k of its MFMA row
+  u32x4 pa0[3], pb0[3];
+  float4 ra0[2];
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int64_t nk = fmd_cdiv(k, 16);
+  XP_LOAD(0, 0);
+  XP_STORE(0, 0);
+  if (nk > 1) XP_LOAD(16, 0);
+  __syncthreads();
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int cur = (int)(kt & 1);
+    if (kt + 1 < nk) {
+      XP_STORE(cur ^ 1, 0);                       // slice kt + 1 (loaded one iteration ago)
+      if (kt + 2 < nk) XP_LOAD((kt + 2) * 16, 0);  // slice kt + 2 stays in flight over these MFMAs
+    }
+    X3_COMPUTE(cur);
+    __syncthreads();  // buffer cur is free, buffer cur ^ 1 is complete
+  }
+  const int64_t row0 = row_blk + wm * 64, col0 = col_blk + wn * 64;
+  if (radd.src) {
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = min(row0 + bi * 32 + (v / 4) * 8 + h * 4 + (v % 4), m - 1);
+        const float* qr = radd.src + (radd.idx ? (int64_t)radd.idx[row * radd.istride] : row) * radd.ld;
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) {
+          const int64_t col = min(col0 + bj * 32 + rr, n - 1);
+          acc[bi][bj][v] += qr[col];
+        }
+      }
+  }
+  if (!bias && !accumulate && act == 0 && row0 + 64 <= m && col0 + 64 <= n) {
+    float* base = c + (row0 + h * 4) * ldc + col0 + rr;
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        float* rp = base + (int64_t)(bi * 32 + (v / 4) * 8 + (v % 4)) * ldc;
+        store_stream(rp, acc[bi][0][v]);
+        store_stream(rp + 32, acc[bi][1][v]);
+      }
+    return;
+  }
+  epilogue<2, 2>(acc, row0, col0, m, n, bias, c, ldc, accumulate, act);
+}
+
+#undef XP_LOAD
+#undef XP_STORE
+
+// planes[r][s][p][0, 16) = the bf16 planes of src[r][16 s, 16 s + 16) (split3), zero past the
+// width (the slice-interleaved operand format of gemm_x3p_kernel); one thread per 8 elements
+__global__ void split3_kernel(const float* __restrict__ src, int64_t ld, int64_t rows, int width, __bf16* planes,
+                              int64_t slices) {
+  const int64_t chunks = slices * 2;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= rows * chunks) return;
+  const int64_t r = id / chunks;
+  const int c = (int)(id - r * chunks), k0 = c * 8;
+  const float* s = src + r * ld + k0;
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = k0 + e < width ? s[e] : 0.f;
+  bf16x4 p[3][2];
+  split3(make_float4(x[0], x[1], x[2], x[3]), p[0][0], p[1][0], p[2][0]);
+  split3(make_float4(x[4], x[5], x[6], x[7]), p[0][1], p[1][1], p[2][1]);
+  __bf16* d = planes + r * slices * 48 + (c >> 1) * 48 + (c & 1) * 8;
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    *reinterpret_cast<bf16x4*>(d + q * 16) = p[q][0];
+    *reinterpret_cast<bf16x4*>(d + q * 16 + 4) = p[q][1];
+  }
+}
+
 #undef X3_LOAD
 #undef X3_STORE
 #undef X3_COMPUTE
@@ -710,9 +909,72 @@ void launch_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, i
                        n, k, accumulate, act);
 }
 
+// Launch of gemm_x3p_kernel (B as slice-interleaved planes, row stride ldb = 48 ceil(K / 16)); A
+// parts as planes (a_planes, row stride 48 ceil(width / 16)) or fp32 (the conditions of
+// launch_gemm_x3); FMD_EUNSUPPORTED otherwise.
+int launch_gemm_x3p(int32_t a_planes, int32_t n_parts, const void* const* srcs, const int32_t* const* indices,
+                    const int64_t* index_strides, const int64_t* lds, const int32_t* widths, int64_t m,
+                    const uint16_t* bp, int64_t ldb, int64_t k_b, const float* row_add, const int32_t* row_add_index,
+                    int64_t row_add_index_stride, int64_t ld_row_add, const float* bias, float* c, int64_t ldc,
+                    int64_t n, int32_t accumulate, int32_t act, hipStream_t stream) {
+  if (n_parts < 1 || n_parts > 3) return FMD_EUNSUPPORTED;
+  X3PPart P[3] = {};
+  int64_t k = 0;
+  for (int p = 0; p < n_parts; ++p) {
+    if (!srcs[p] || widths[p] <= 0 || !aligned16(srcs[p])) return FMD_EUNSUPPORTED;
+    if (p + 1 < n_parts && widths[p] % 16) return FMD_EUNSUPPORTED;
+    if (a_planes ? (widths[p] % 8 || lds[p] != 48 * fmd_cdiv(widths[p], 16)) : (widths[p] % 4 || lds[p] % 4))
+      return FMD_EUNSUPPORTED;
+    P[p] = X3PPart{srcs[p], indices ? indices[p] : nullptr, lds[p], index_strides ? index_strides[p] : 1, widths[p]};
+    if (P[p].istride < 1) return FMD_EINVAL;
+    k += widths[p];
+  }
+  if (k != k_b) return FMD_EINVAL;
+  if (!bp || !aligned16(bp) || ldb != 48 * fmd_cdiv(k, 16)) return FMD_EUNSUPPORTED;
+  X3Part radd{row_add, row_add_index, ld_row_add, row_add_index_stride, 0};
+  if (row_add && (ld_row_add < n || row_add_index_stride < 1)) return FMD_EINVAL;
+  const int64_t n_tiles = fmd_cdiv(n, 128), tiles = fmd_cdiv(m, 128) * n_tiles;
+  if (tiles >= (int64_t(1) << 31)) return FMD_EINVAL;
+  const __bf16* b = reinterpret_cast<const __bf16*>(bp);
+  if (a_planes)
+    hipLaunchKernelGGL(gemm_x3p_kernel<true>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, P[0], P[1], P[2],
+                       n_parts, b, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, n_tiles);
+  else
+    hipLaunchKernelGGL(gemm_x3p_kernel<false>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, P[0], P[1], P[2],
+                       n_parts, b, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, n_tiles);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int fmd_split3_f32(const float* src, int64_t ld, int64_t rows, int32_t width, uint16_t* planes, hipStream_t stream) {
+  FMD_REQUIRE(rows >= 0 && width > 0 && ld >= width);
+  if (rows == 0) return FMD_OK;
+  FMD_REQUIRE(src && planes && aligned16(planes));
+  const int64_t slices = fmd_cdiv(width, 16), threads = rows * slices * 2;
+  hipLaunchKernelGGL(split3_kernel, dim3((unsigned)fmd_cdiv(threads, 256)), dim3(256), 0, stream, src, ld, rows, width,
+                     reinterpret_cast<__bf16*>(planes), slices);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_gemm_x3_planes_f32(int32_t a_planes, int32_t n_parts, const void* const* srcs, const int32_t* const* indices,
+                           const int64_t* index_strides, const int64_t* lds, const int32_t* widths, int64_t m,
+                           const uint16_t* b_planes, int64_t ldb, int64_t k, const float* row_add,
+                           const int32_t* row_add_index, int64_t row_add_index_stride, int64_t ld_row_add,
+                           const float* bias, float* c, int64_t ldc, int64_t n, int32_t accumulate,
+                           int32_t epilogue_kind, hipStream_t stream) {
+  FMD_REQUIRE(m >= 0 && n >= 0 && c && ldc >= n && srcs && lds && widths);
+  FMD_REQUIRE(epilogue_kind == 0 || epilogue_kind == 1);
+  if (m == 0 || n == 0) return FMD_OK;
+  FMD_REQUIRE(k_fits_int(n_parts, widths));
+  return launch_gemm_x3p(a_planes, n_parts, srcs, indices, index_strides, lds, widths, m, b_planes, ldb, k, row_add,
+                         row_add_index, row_add_index_stride, ld_row_add, bias, c, ldc, n, accumulate, epilogue_kind,
+                         stream);
+}
 
 int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32_t b_layout, const float* bias,
                  float* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int32_t accumulate, int32_t epilogue_kind,

@@ -39,7 +39,7 @@ from torch.autograd import Function
 from fastmd_amd import _abi
 from fastmd_amd.adapters.protocol import CapacityStep, CaptureContract, GraphBatch, PaddingRule, TopologySpec
 from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr
-from fastmd_amd.ops.wide_gemm import gemm, gemm_gather, gemm_group
+from fastmd_amd.ops.wide_gemm import Planes, gemm, gemm_gather, gemm_group, gemm_planes, split_planes
 
 _ELEMENTS = 118
 _CAPACITY_STEP = CapacityStep(u_step=32, min_pad_u=32, u_thermal_factor=1.02)
@@ -172,6 +172,29 @@ class MaceLike(nn.Module):
             cache[t] = hit
         return hit[1]
 
+    def w1_planes(self, t: int, which: str, nz: int = 0) -> Planes:
+        """bf16 planes (split once per W1 version) of the weights of layer t's edge GEMMs when the
+        operands come pre-split: "receiver" / "sender" = the first nz rows of w1_receiver_t /
+        w1_sender_t (the forward's [nz, K] B operands), "sender_rows" = W1[:C] ([C, 4C], the B
+        operand of the VJP's sender-block GEMM gz @ W1[:C]^T)."""
+        w = self.layers[t].W1
+        key = (w.data_ptr(), w._version, w.device)
+        cache = self.__dict__.setdefault("_w1p_cache", {})
+        hit = cache.get((t, which, nz))
+        if hit is None or hit[0] != key:
+            C = self.config.channels
+            if which == "receiver":
+                src = self.w1_receiver_t(t)[:nz]
+            elif which == "sender":
+                src = self.w1_sender_t(t)[:nz]
+            elif which == "sender_rows":
+                src = w.detach()[:C]
+            else:
+                raise ValueError(f"unknown W1 block {which!r}")
+            hit = (key, split_planes(src))
+            cache[(t, which, nz)] = hit
+        return hit[1]
+
     @property
     def num_interactions(self) -> int:
         return self.config.num_interactions
@@ -236,6 +259,11 @@ class _MaceLikeEnergy(Function):
         saved = []
         h_first = None
         L = len(model.layers)
+        # On large edge lists the edge GEMMs take pre-split operands: the radial rows once per
+        # evaluation here, h0 once per layer, the weights once per version (bitwise the same z as
+        # splitting inside the GEMM, without the splitting arithmetic per output tile)
+        hoist = e_cap >= HOIST_MIN_ROWS
+        efp = split_planes(ef) if hoist else None
         for t, layer in enumerate(model.layers):
             last = t == L - 1
             # z = [h0[src] | h0[dst] | ef] @ W1 ([E, 4C]), the gather-cat fused into the edge GEMM's
@@ -246,19 +274,25 @@ class _MaceLikeEnergy(Function):
             # just its a | b blocks ([E, 2C], the first 2C columns of W1).
             timed = EDGE_GEMM_EVENTS is not None and not torch.cuda.is_current_stream_capturing()
             nz = 4 * C if h1 is not None else 2 * C
-            if e_cap >= HOIST_MIN_ROWS:
-                q = gemm(h0, model.w1_receiver_t(t)[:nz], b_layout=0)
-                parts, w1 = [(h0, ei[:, 1]), (ef, None)], model.w1_sender_t(t)[:nz]
+            if hoist:
+                h0p = split_planes(h0)
+                q = gemm_planes([(h0p, None)], model.w1_planes(t, "receiver", nz), a_planes=True)
+                w1p = model.w1_planes(t, "sender", nz)
+                shape = (e_cap, w1p.width, nz)
             else:
                 q = None
                 parts, w1 = [(h0, ei[:, 1]), (h0, ei[:, 0]), (ef, None)], model.w1_t(t)[:nz]
+                shape = (e_cap, w1.shape[1], nz)
             if timed:
                 ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                 ev[0].record()
-            z = gemm_gather(parts, w1)
+            if hoist:
+                z = gemm_planes([(h0p, ei[:, 1]), (efp, None)], w1p, a_planes=True)
+            else:
+                z = gemm_gather(parts, w1)
             if timed:
                 ev[1].record()
-                EDGE_GEMM_EVENTS.append((ev[0], ev[1], (e_cap, w1.shape[1], w1.shape[0])))
+                EDGE_GEMM_EVENTS.append((ev[0], ev[1], shape))
             A0 = _empty(n, C, device=dev)
             A1 = _empty(n, 3, C, device=dev)
             _call("fmd_mace_message_f32", z.data_ptr(), _abi.ptr(q), geo.data_ptr(), ei.data_ptr(), off.data_ptr(),
@@ -408,7 +442,7 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
         if q is not None:
             # sender block row by row (edge GEMM, then the sender segment sum); receiver block
             # from the per-centre sums of gz: sum_e gz[e] W1[C:2C]^T = (sum_e gz[e]) W1[C:2C]^T
-            ga = gemm(gz, layer.W1[:C], b_layout=0)  # [E, C]
+            ga = gemm_planes([(gz, None)], model.w1_planes(t, "sender_rows"), a_planes=False)  # [E, C]
             segment_sum_csr([(ga, inputs.csr_src, 0, 1.0, None)], n, C, out=g_in0, accumulate=True)
             gemm(gzs, layer.W1[C:2 * C], b_layout=0, out=g_in0, accumulate=True)
         else:

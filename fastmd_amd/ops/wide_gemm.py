@@ -114,6 +114,111 @@ def gemm_group(problems, *, b_layout: int, epilogue: str | None = None) -> list:
     return [p["out"] for p in problems]
 
 
+class Planes:
+    """The three bf16 planes of a float32 matrix [rows, width] (fmd_split3_f32), slice-interleaved:
+    ``data`` [rows, S, 3, 16] bfloat16 (S = ceil(width / 16), zero past ``width``), x = p0 + p1 + p2."""
+
+    __slots__ = ("data", "width")
+
+    def __init__(self, data: Tensor, width: int) -> None:
+        self.data, self.width = data, int(width)
+
+    @property
+    def ld(self) -> int:
+        """Row stride in elements (48 S)."""
+        return self.data.shape[1] * 48
+
+    def dense(self) -> Tensor:
+        """[rows, 3, 16 S] view order of the planes (a copy), for checks."""
+        rows, slices = self.data.shape[:2]
+        return self.data.permute(0, 2, 1, 3).reshape(rows, 3, slices * 16)
+
+
+def split_planes(x: Tensor, *, out: Planes | None = None) -> Planes:
+    """The bf16 planes of a 2-D float32 ``x`` (fmd_split3_f32)."""
+    require_cuda(x)
+    if x.dim() != 2 or x.dtype != torch.float32:
+        raise ValueError("split_planes takes a 2-D float32 tensor")
+    x, ld = rows_view(x)
+    rows, width = x.shape
+    slices = -(-width // 16)
+    if out is None:
+        out = Planes(torch.empty((rows, slices, 3, 16), dtype=torch.bfloat16, device=x.device), width)
+    elif out.data.shape != (rows, slices, 3, 16) or out.width != width:
+        raise ValueError("split_planes: out does not match")
+    if rows:
+        _abi.call("fmd_split3_f32", x.data_ptr(), ld, rows, width, out.data.data_ptr(), stream())
+    return out
+
+
+def gemm_planes(parts, b: Planes, *, a_planes: bool, out: Tensor | None = None, bias: Tensor | None = None,
+                accumulate: bool = False, epilogue: str | None = None, row_add=None) -> Tensor:
+    """``gemm_gather`` with pre-split operands (fmd_gemm_x3_planes_f32): ``b`` the planes of the
+    K-contiguous weight [N, K] (``split_planes(w)``), ``parts`` a list of up to three
+    ``(src, index)`` with ``src`` Planes (``a_planes``) or float32 [rows, width]. Bitwise equal to
+    ``gemm_gather`` on the unsplit operands."""
+    if not 1 <= len(parts) <= 3:
+        raise ValueError("gemm_planes takes one to three parts")
+    require_cuda(b.data, out, bias)
+    rows = None
+    srcs, idx, strides, lds, widths, keep = [], [], [], [], [], []
+    for src, index in parts:
+        if a_planes:
+            if not isinstance(src, Planes):
+                raise ValueError("gemm_planes(a_planes=True) takes Planes parts")
+            data, ld, width, n_src = src.data, src.ld, src.width, src.data.shape[0]
+        else:
+            if src.dtype != torch.float32 or src.dim() != 2:
+                raise ValueError("gemm_planes parts must be 2-D float32")
+            data, ld = rows_view(src)
+            width, n_src = data.shape[1], data.shape[0]
+        require_cuda(data)
+        if index is not None:
+            if index.dtype != torch.int32 or index.dim() != 1:
+                index = index.to(torch.int32).reshape(-1).contiguous()
+            n_rows = index.numel()
+            stride = index.stride(0) if n_rows > 1 else 1
+        else:
+            n_rows, stride = n_src, 1
+        if rows is None:
+            rows = n_rows
+        elif n_rows != rows:
+            raise ValueError("gemm_planes parts disagree on the row count")
+        keep += [data, index]
+        srcs.append(data.data_ptr())
+        idx.append(None if index is None else index.data_ptr())
+        strides.append(stride)
+        lds.append(ld)
+        widths.append(width)
+    k = sum(widths)
+    if b.width != k:
+        raise ValueError(f"gemm_planes: b has K = {b.width}, the parts {k}")
+    n = b.data.shape[0]
+    if bias is not None:
+        if bias.shape != (n,) or bias.dtype != torch.float32:
+            raise ValueError("bias must be float32 [N]")
+        bias = bias.contiguous()
+    if out is None:
+        out = (torch.zeros if accumulate else torch.empty)((rows, n), dtype=torch.float32, device=b.data.device)
+    elif out.shape != (rows, n) or out.dtype != torch.float32 or out.stride(1) != 1:
+        raise ValueError("out must be float32 [M, N] with unit column stride")
+    q, qidx, qstride, ldq = None, None, 1, 0
+    if row_add is not None:
+        q, qidx = row_add
+        if q.dim() != 2 or q.dtype != torch.float32 or q.shape[1] != n or q.stride(1) != 1:
+            raise ValueError(f"row_add must be float32 [*, {n}] with unit column stride")
+        ldq = q.stride(0)
+        if qidx is not None:
+            qstride = qidx.stride(0) if rows > 1 else 1
+    if rows == 0 or n == 0:
+        return out
+    _abi.call("fmd_gemm_x3_planes_f32", 1 if a_planes else 0, len(parts), _abi.ptr_array(srcs), _abi.ptr_array(idx),
+              _abi.array(_abi._i64, strides), _abi.array(_abi._i64, lds), _abi.array(_abi._i32, widths), rows,
+              b.data.data_ptr(), b.ld, k, _abi.ptr(q), _abi.ptr(qidx), qstride, ldq, _abi.ptr(bias), out.data_ptr(),
+              out.stride(0) if rows > 1 else n, n, 1 if accumulate else 0, _EPILOGUES[epilogue], stream())
+    return out
+
+
 _EUNSUPPORTED = 10002
 
 

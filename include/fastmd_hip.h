@@ -209,6 +209,30 @@ int fmd_gemm_gather_f32(int32_t n_parts, const float* const* srcs, const int32_t
                         int64_t row_add_index_stride, int64_t ld_row_add, const float* bias, float* c,
                         int64_t ldc, int64_t n, int32_t accumulate, int32_t epilogue, hipStream_t stream);
 
+/* The three bf16 planes of a float32 matrix src [rows, width] (row stride ld), slice-interleaved:
+ * planes [rows][S][3][16] (bf16 as uint16, S = ceil(width / 16), 16-byte aligned), plane p of
+ * columns [16 s, 16 s + 16) of row r at (r S + s) 48 + 16 p, with x = p0 + p1 + p2 exactly
+ * (p0 = bf16(x), p1 = bf16(x - p0), p2 = bf16(x - p0 - p1), round to nearest even) and zeros past
+ * the width. The operand format of fmd_gemm_x3_planes_f32. Counterpart of the reference's
+ * once-per-weight-version operand split (_split_kernel / _split, triton_wide_gemm.py:12-15,
+ * 131-199: hi/lo TF32 pairs there, three bf16 planes here). */
+int fmd_split3_f32(const float* src, int64_t ld, int64_t rows, int32_t width, uint16_t* planes, hipStream_t stream);
+/* fmd_gemm_gather_f32 with pre-split operands: B [N, K] as planes (fmd_split3_f32, ldb =
+ * 48 ceil(K / 16)), and with a_planes the parts as planes too (srcs_p planes of width widths_p,
+ * lds_p = 48 ceil(widths_p / 16); widths multiples of 8, all but the last of 16); a_planes 0: the
+ * parts are fp32 as in fmd_gemm_gather_f32. Bitwise the same C as fmd_gemm_gather_f32 on the
+ * unsplit operands (same planes, products and order), without the splitting arithmetic in the
+ * GEMM: a weight is split once, a per-atom feature once per evaluation instead of once per output
+ * tile, and a row's 16-k slice is one contiguous 96-byte read. Replaces the same reference calls
+ * as fmd_gemm_gather_f32 (triton_gather_cat.py:181-199 feeding triton_wide_gemm.py:482-515).
+ * FMD_EUNSUPPORTED when a layout condition fails. */
+int fmd_gemm_x3_planes_f32(int32_t a_planes, int32_t n_parts, const void* const* srcs, const int32_t* const* indices,
+                           const int64_t* index_strides, const int64_t* lds, const int32_t* widths, int64_t m,
+                           const uint16_t* b_planes, int64_t ldb, int64_t k, const float* row_add,
+                           const int32_t* row_add_index, int64_t row_add_index_stride, int64_t ld_row_add,
+                           const float* bias, float* c, int64_t ldc, int64_t n, int32_t accumulate,
+                           int32_t epilogue, hipStream_t stream);
+
 /* As fmd_gemm_f32 with bf16 operands (uint16 storage), fp32 accumulate and fp32 output, on
  * v_mfma_f32_32x32x16_bf16. Not in the reference (which has no bf16 GEMM on this path). */
 int fmd_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int32_t b_layout,

@@ -320,6 +320,52 @@ def test_gemm_gather_against_fp64(device, F):
 
 
 @pytest.mark.gpu
+def test_gemm_planes_bitwise_equal_to_in_kernel_split(device):
+    """fmd_split3_f32 gives x = p0 + p1 + p2 exactly (zero padding past the width), and the GEMM on
+    pre-split planes (A gathered from plane rows, or fp32 A with pre-split B) is bitwise the GEMM
+    that splits inside (same planes, products and order), including bias, accumulate and a
+    gathered row add; and within fp32 of float64."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm_gather, gemm_planes, split_planes
+
+    g = torch.Generator().manual_seed(21)
+    n_atoms, E, C, nb, N = 3001, 40000, 128, 8, 512
+    h0 = torch.randn(n_atoms, C, generator=g)
+    ef = torch.randn(E, nb, generator=g) * 1e-3
+    src = torch.randint(0, n_atoms, (E,), generator=g, dtype=torch.int32)
+    w = torch.randn(N, C + nb, generator=g) / (C + nb) ** 0.5
+    hp = split_planes(h0.to(device))
+    total = hp.dense().double().sum(1)[:, :C].cpu()
+    assert torch.equal(total, h0.double())
+    efp = split_planes(ef.to(device))
+    assert efp.ld == 48 and torch.equal(efp.dense().double().sum(1)[:, :nb].cpu(), ef.double())
+    assert float(efp.dense()[:, :, nb:].abs().max()) == 0.0
+    wp = split_planes(w.to(device))
+    assert wp.ld == 48 * 9 and float(wp.dense()[:, :, C + nb:].abs().max()) == 0.0
+    ref = gemm_gather([(h0.to(device), src.to(device)), (ef.to(device), None)], w.to(device))
+    got = gemm_planes([(hp, src.to(device)), (efp, None)], wp, a_planes=True)
+    assert torch.equal(got, ref)
+    exact = torch.cat([h0[src.long()], ef], 1).double() @ w.double().t()
+    assert oops.relative(got.cpu().numpy(), exact.numpy()) < 1e-5
+    # bias + accumulate + gathered row add
+    q = torch.randn(n_atoms, N, generator=g).to(device)
+    qi = torch.randint(0, n_atoms, (E,), generator=g, dtype=torch.int32).to(device)
+    c0 = torch.randn(E, N, generator=g).to(device)
+    bias = torch.randn(N, generator=g).to(device)
+    ref2 = gemm_gather([(h0.to(device), src.to(device)), (ef.to(device), None)], w.to(device), out=c0.clone(),
+                       bias=bias, accumulate=True, row_add=(q, qi))
+    got2 = gemm_planes([(hp, src.to(device)), (efp, None)], wp, a_planes=True, out=c0.clone(), bias=bias,
+                       accumulate=True, row_add=(q, qi))
+    assert torch.equal(got2, ref2)
+    # fp32 A (split in the kernel) with pre-split B: the VJP shape [E, 4C] x [4C, C]
+    gz = torch.randn(E, 4 * C, generator=g).to(device)
+    wv = (torch.randn(C, 4 * C, generator=g) / (4 * C) ** 0.5).to(device)
+    got3 = gemm_planes([(gz, None)], split_planes(wv), a_planes=False)
+    assert torch.equal(got3, gemm_gather([(gz, None)], wv))
+
+
+@pytest.mark.gpu
 def test_gemm_split_planes_dynamic_range(device):
     """The three-plane bf16 path must keep fp32 accuracy over a wide exponent range: rows and
     columns scaled by 2^-30 .. 2^30, exact zeros, and values whose low bits the first two planes
