@@ -44,6 +44,8 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_split3_f32": (ctypes.c_int, [_p, _i64, _i64, _i32, _p, _p]),
     "fmd_gemm_x3_planes_f32": (ctypes.c_int, [_i32, _i32, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _p, _p, _i64,
                                               _i64, _p, _p, _i64, _i64, _i32, _i32, _p]),
+    "fmd_gemm_splitk_f32": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i64, _i64, _i64, _i64,
+                                           _i32, _i32, _p, _p]),
     "fmd_gemm_gather_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _p, _i64, _i64, _p, _p, _i64,
                                            _i64, _i32, _i32, _p]),
     "fmd_gemm_bf16": (ctypes.c_int, [_p, _i64, _p, _i64, _i32, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p]),
@@ -56,7 +58,7 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_edge_geometry_bwd_f32": (ctypes.c_int, [_p, _p, _i32, _p, _i64, _p, _i64, _p, _p, _i64, _p, _p]),
     "fmd_mace_message_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _f32, _p, _p, _p]),
     "fmd_mace_message_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _p, _p, _f32,
-                                                _p, _p, _p, _i32, _p, _p, _i32, _p, _i32, _p, _p]),
+                                                _p, _p, _p, _p, _i32, _p, _p, _i32, _p, _i32, _p, _p]),
     "fmd_mace_node_fwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p, _p, _p,
                                              _p, _p]),
     "fmd_mace_node_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32,

@@ -150,6 +150,46 @@ __device__ __forceinline__ int wave_sum16_index(int lane) {
   return ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
 }
 
+// Sixteen sums over each half-wave (lanes 0-31 and 32-63 separately, each reducing its own
+// values): the transposing butterfly over l ^ 16 (half swap), l ^ 8 (row_ror:8), the mirror lane
+// in 8 and l ^ 2, then a full sum with l ^ 1. On return lanes l and l ^ 1 of a half hold the total
+// of value index 8*b4 + 4*b3 + 2*b2 + b1 (half_sum16_index). Fixed order (deterministic).
+__device__ __forceinline__ float half_sum16(const float (&v)[16]) {
+  const int lane = threadIdx.x & (FMD_WAVE - 1);
+  const bool h3 = lane & 8, h2 = lane & 4, h1 = lane & 2;
+  float a[8], b[4], c[2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {  // bit 4 set: index i + 8
+    float x = v[i], y = v[i + 8];
+    swap_halves16(x, y);
+    a[i] = x + y;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // bit 3 set: index i + 4 (partner l ^ 8)
+    const float keep = h3 ? a[i + 4] : a[i], send = h3 ? a[i] : a[i + 4];
+    b[i] = keep + dpp_read<kDppRowRor8>(send);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {  // bit 2 set: index i + 2 (partner: the mirror lane in 8)
+    const float keep = h2 ? b[i + 2] : b[i], send = h2 ? b[i] : b[i + 2];
+    c[i] = keep + dpp_read<kDppHalfMirror>(send);
+  }
+  float t = (h1 ? c[1] : c[0]) + dpp_read<kDppQuadXor2>(h1 ? c[0] : c[1]);  // bit 1 set: index 1
+  t = t + dpp_read<kDppQuadXor1>(t);
+  return t;
+}
+
+__device__ __forceinline__ int half_sum16_index(int lane) {
+  return ((lane >> 4) & 1) * 8 + ((lane >> 3) & 1) * 4 + ((lane >> 2) & 1) * 2 + ((lane >> 1) & 1);
+}
+
+// x of lane l plus x of lane l ^ 32, the same value (same order of the two terms) in both lanes
+__device__ __forceinline__ float add_halves(float x) {
+  float y = x;
+  swap_halves32(x, y);
+  return x + y;
+}
+
 // Streaming stores (the `nt` bit): outputs written once and not re-read by the same kernel. On
 // gfx950 they sustain ~5.9 TB/s for a gather-and-write stream against ~3.4 TB/s for plain
 // stores, which keep the lines in L2 and the last-level cache on their way out.

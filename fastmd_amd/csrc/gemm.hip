@@ -211,6 +211,38 @@ struct GemmGroup {
   int act;
 };
 
+// Deterministic split-K for tall-K node GEMMs (few output tiles, long K): workgroup (tile, s)
+// multiplies K slice s ([s ks, (s + 1) ks), inside one of the parts a | a2) into the workspace
+// partial ws[s] ([M, N]); splitk_sum_kernel adds the partials in the order s = 0, 1, ...
+template <int BLAYOUT>
+__global__ void __launch_bounds__(kThreads) gemm_f32_splitk_kernel(const float* __restrict__ a, int64_t lda,
+                                                                   const float* __restrict__ a2, int64_t lda2,
+                                                                   int64_t ksplit, const float* __restrict__ b,
+                                                                   int64_t ldb, float* ws, int64_t m, int64_t n,
+                                                                   int64_t ks, int64_t tiles_n, int64_t tiles) {
+  const int64_t w = blockIdx.x, s = w / tiles, t = w - s * tiles;
+  const int64_t tm = t / tiles_n, tn = t - tm * tiles_n;
+  const int64_t k0 = s * ks;
+  const bool second = k0 >= ksplit;
+  const float* ap = second ? a2 + (k0 - ksplit) : a + k0;
+  const int64_t la = second ? lda2 : lda;
+  const float* bp = BLAYOUT == 0 ? b + k0 : b + k0 * ldb;
+  gemm_f32_tile<64, 64, BLAYOUT>(ap, la, ap, la, ks, bp, ldb, nullptr, ws + s * m * n, n, m, n, ks, 0, 0, tm * 64,
+                                 tn * 64);
+}
+
+__global__ void splitk_sum_kernel(const float* __restrict__ ws, int splits, int64_t m, int64_t n,
+                                  const float* __restrict__ bias, float* c, int64_t ldc, int accumulate) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= m * n) return;
+  const int64_t r = id / n, col = id - r * n;
+  float x = ws[id];
+  for (int sp = 1; sp < splits; ++sp) x += ws[sp * m * n + id];
+  if (bias) x += bias[col];
+  float* d = c + r * ldc + col;
+  *d = accumulate ? *d + x : x;
+}
+
 template <int BLAYOUT>
 __global__ void __launch_bounds__(kThreads) gemm_f32_group_kernel(const GemmGroup grp) {
   const int64_t w = blockIdx.x;
@@ -1055,6 +1087,33 @@ int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda,
     hipLaunchKernelGGL(gemm_f32_group_kernel<0>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
   else
     hipLaunchKernelGGL(gemm_f32_group_kernel<1>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_gemm_splitk_f32(const float* a, int64_t lda, const float* a2, int64_t lda2, int64_t ksplit, const float* b,
+                        int64_t ldb, int32_t b_layout, const float* bias, float* c, int64_t ldc, int64_t m, int64_t n,
+                        int64_t k, int32_t accumulate, int32_t splits, float* workspace, hipStream_t stream) {
+  FMD_REQUIRE(m >= 0 && n >= 0 && k > 0 && splits >= 1 && (b_layout == 0 || b_layout == 1));
+  if (m == 0 || n == 0) return FMD_OK;
+  FMD_REQUIRE(a && b && c && workspace && ldc >= n && k % splits == 0);
+  const int64_t ks = k / splits;
+  const int64_t ksp = a2 ? ksplit : k;
+  FMD_REQUIRE(ks % 32 == 0 && ksp % ks == 0 && lda >= ksp && (!a2 || lda2 >= k - ksp));
+  FMD_REQUIRE(ldb >= (b_layout == 0 ? k : n));
+  const int64_t tiles_n = fmd_cdiv(n, 64), tiles = fmd_cdiv(m, 64) * tiles_n;
+  FMD_REQUIRE(tiles * splits < (int64_t(1) << 31));
+  const float* a2p = a2 ? a2 : a;
+  const int64_t lda2p = a2 ? lda2 : lda;
+  if (b_layout == 0)
+    hipLaunchKernelGGL(gemm_f32_splitk_kernel<0>, dim3((unsigned)(tiles * splits)), dim3(kThreads), 0, stream, a, lda,
+                       a2p, lda2p, ksp, b, ldb, workspace, m, n, ks, tiles_n, tiles);
+  else
+    hipLaunchKernelGGL(gemm_f32_splitk_kernel<1>, dim3((unsigned)(tiles * splits)), dim3(kThreads), 0, stream, a, lda,
+                       a2p, lda2p, ksp, b, ldb, workspace, m, n, ks, tiles_n, tiles);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(splitk_sum_kernel, dim3((unsigned)fmd_cdiv(m * n, 256)), dim3(256), 0, stream, workspace, splits, m,
+                     n, bias, c, ldc, accumulate);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -132,33 +132,69 @@ __global__ void edge_geometry_bwd_kernel(const float* geo, const float* def, int
 // just the a | b blocks: [E, 2C]. zq, when given, is the receiver block of z per atom ([N, the
 // same width]), added to every row of the centre.
 //
-// Latency: per 64 rows the wave loads the rows' neighbour index and geometry once (one row per
-// lane, coalesced) and broadcasts them with readlane; each group of kGroup rows then issues all
-// of its z, h0[j] and h1[j] loads before any arithmetic, so a group costs one memory round trip
-// instead of two per row. Rows are accumulated in row order (deterministic).
+// Layout: a half-wave per row (lane l of a half holds channels CPL l .. + CPL, CPL = C / 32), so
+// every load of a row's block or of a node row is 16 bytes per lane (the texture path costs the
+// same per instruction for 8 and 16 bytes) and one instruction serves two rows. Half h of the
+// wave takes rows lo + h, lo + h + 2, ... of the centre. Per 64 rows the wave loads their
+// neighbour index and geometry once (one row per lane, coalesced) and each half reads its row's
+// with readlane; each group of kPairs row pairs issues all of its loads before any arithmetic
+// (one memory round trip per group). The two halves' sums are added at the end (fixed order:
+// deterministic).
 // ------------------------------------------------------------------------------------------
-constexpr int kGroup = 4;
+constexpr int kPairs = 2;
 
 __device__ __forceinline__ int bcast(int v, int s) { return __builtin_amdgcn_readlane(v, s); }
 __device__ __forceinline__ float bcast(float v, int s) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), s));
 }
+// lane s0's v in the lower half-wave, lane s1's in the upper one (s0, s1 uniform)
+__device__ __forceinline__ int bcast2(int v, int s0, int s1, bool upper) {
+  const int a = bcast(v, s0), b = bcast(v, s1);
+  return upper ? b : a;
+}
+__device__ __forceinline__ float bcast2(float v, int s0, int s1, bool upper) {
+  const float a = bcast(v, s0), b = bcast(v, s1);
+  return upper ? b : a;
+}
 
-// CPL consecutive floats (4 * CPL-byte aligned)
+// CPL consecutive floats (CPL 2: 8-byte, 4 and 8: 16-byte aligned)
 template <int CPL>
 __device__ __forceinline__ void load_ch(const float* p, float (&v)[CPL]) {
-  if constexpr (CPL == 4) {
-    const float4 t = *reinterpret_cast<const float4*>(p);
-    v[0] = t.x;
-    v[1] = t.y;
-    v[2] = t.z;
-    v[3] = t.w;
-  } else if constexpr (CPL == 2) {
+  if constexpr (CPL == 2) {
     const float2 t = *reinterpret_cast<const float2*>(p);
     v[0] = t.x;
     v[1] = t.y;
   } else {
-    v[0] = p[0];
+#pragma unroll
+    for (int q = 0; q < CPL; q += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(p + q);
+      v[q] = t.x;
+      v[q + 1] = t.y;
+      v[q + 2] = t.z;
+      v[q + 3] = t.w;
+    }
+  }
+}
+
+template <int CPL>
+__device__ __forceinline__ void store_ch(float* p, const float (&v)[CPL]) {
+  if constexpr (CPL == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < CPL; q += 4) *reinterpret_cast<float4*>(p + q) = make_float4(v[q], v[q + 1], v[q + 2], v[q + 3]);
+  }
+}
+
+template <int CPL>
+__device__ __forceinline__ void store_ch_stream(float* p, const float (&v)[CPL]) {
+  if constexpr (CPL == 2) {
+    store_stream(p, v[0]);
+    store_stream(p + 1, v[1]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < CPL; q += 4)
+      store_stream(reinterpret_cast<float4*>(p + q), make_float4(v[q], v[q + 1], v[q + 2], v[q + 3]));
   }
 }
 
@@ -192,26 +228,28 @@ __device__ __forceinline__ int64_t wave_rows(const int64_t* off, const int64_t* 
   return hi;
 }
 
-template <int CPL, bool H1>
+// CPL64 = C / 64 (the dispatch parameter); a lane holds CPL = 2 CPL64 channels of a half-wave's row
+template <int CPL64, bool H1>
 __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const float* zq, const float* geo,
                                                            const int32_t* edge_index, const int64_t* off,
                                                            const int64_t* n_edges, int64_t e_cap, int64_t n,
                                                            const float* h0, const float* h1, float inv_avg, float* A0,
                                                            float* A1) {
-  constexpr int C = 64 * CPL;
+  constexpr int CPL = 2 * CPL64, C = 32 * CPL;
   constexpr int NZ = H1 ? 4 : 2;  // z blocks in a row
   const int lane = threadIdx.x & 63;
+  const bool upper = lane >= 32;
   const int64_t i = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   if (i >= n) return;
   int64_t lo;
   const int64_t hi = wave_rows(off, n_edges, e_cap, i, lo);
+  const int c0 = (lane & 31) * CPL;
   float a0[CPL], a1[3][CPL];
 #pragma unroll
   for (int q = 0; q < CPL; ++q) {
     a0[q] = 0.f;
     a1[0][q] = a1[1][q] = a1[2][q] = 0.f;
   }
-  const int c0 = lane * CPL;
   float qz[NZ][CPL];  // the centre's receiver block of z (zq[i]), 0 when z is complete
 #pragma unroll
   for (int b = 0; b < NZ; ++b) {
@@ -225,44 +263,47 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
   for (int64_t base = lo; base < hi; base += 64) {
     const int cnt = (int)(hi - base < 64 ? hi - base : 64);
     const RowGeo m = row_geo(geo, edge_index, base + lane, lane < cnt);
-    for (int u0 = 0; u0 < cnt; u0 += kGroup) {
-      float zr[kGroup][NZ][CPL], hj[kGroup][CPL], hv[kGroup][3][CPL];
-      float ux[kGroup], uy[kGroup], uz[kGroup], fc[kGroup];
+    for (int u0 = 0; u0 < cnt; u0 += 2 * kPairs) {
+      float zr[kPairs][NZ][CPL], hj[kPairs][CPL], hv[kPairs][3][CPL];
+      float ux[kPairs], uy[kPairs], uz[kPairs], fc[kPairs];
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u) {
-        const int s = u0 + u < cnt ? u0 + u : cnt - 1;
-        const int64_t j = bcast(m.j, s);
-        ux[u] = bcast(m.ux, s);
-        uy[u] = bcast(m.uy, s);
-        uz[u] = bcast(m.uz, s);
-        fc[u] = u0 + u < cnt ? bcast(m.fc, s) : 0.f;  // a row past the end adds exact zeros
+      for (int g = 0; g < kPairs; ++g) {
+        const int r0 = u0 + 2 * g, s0 = r0 < cnt ? r0 : cnt - 1, s1 = r0 + 1 < cnt ? r0 + 1 : cnt - 1;
+        const bool valid = r0 + (upper ? 1 : 0) < cnt;
+        const int s = upper ? s1 : s0;
+        const int64_t j = bcast2(m.j, s0, s1, upper);
+        ux[g] = bcast2(m.ux, s0, s1, upper);
+        uy[g] = bcast2(m.uy, s0, s1, upper);
+        uz[g] = bcast2(m.uz, s0, s1, upper);
+        const float f = bcast2(m.fc, s0, s1, upper);
+        fc[g] = valid ? f : 0.f;  // a row past the end adds exact zeros
         const float* ze = z + (base + s) * (NZ * C) + c0;
 #pragma unroll
-        for (int b = 0; b < NZ; ++b) load_ch<CPL>(ze + b * C, zr[u][b]);
-        load_ch<CPL>(h0 + j * C + c0, hj[u]);
+        for (int b = 0; b < NZ; ++b) load_ch<CPL>(ze + b * C, zr[g][b]);
+        load_ch<CPL>(h0 + j * C + c0, hj[g]);
         if (H1) {
 #pragma unroll
-          for (int x = 0; x < 3; ++x) load_ch<CPL>(h1 + (j * 3 + x) * C + c0, hv[u][x]);
+          for (int x = 0; x < 3; ++x) load_ch<CPL>(h1 + (j * 3 + x) * C + c0, hv[g][x]);
         }
       }
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u) {
+      for (int g = 0; g < kPairs; ++g) {
         // no early exit for the rows past the end (fc = 0): a branch here would let the compiler
         // move the group's loads behind it, one round trip per row again
 #pragma unroll
         for (int q = 0; q < CPL; ++q) {
-          const float za = zr[u][0][q] + qz[0][q], zb = zr[u][1][q] + qz[1][q];
-          const float wa = za * sigmoid(za) * fc[u], wb = zb * sigmoid(zb) * fc[u];
-          const float hjq = hj[u][q];
+          const float za = zr[g][0][q] + qz[0][q], zb = zr[g][1][q] + qz[1][q];
+          const float wa = za * sigmoid(za) * fc[g], wb = zb * sigmoid(zb) * fc[g];
+          const float hjq = hj[g][q];
           float m0 = wa * hjq;
           const float t = wb * hjq;
-          float m1x = t * ux[u], m1y = t * uy[u], m1z = t * uz[u];
+          float m1x = t * ux[g], m1y = t * uy[g], m1z = t * uz[g];
           if (H1) {
-            const float zc = zr[u][NZ > 2 ? 2 : 0][q] + qz[NZ > 2 ? 2 : 0][q];
-            const float zd = zr[u][NZ > 2 ? 3 : 0][q] + qz[NZ > 2 ? 3 : 0][q];
-            const float wc = zc * sigmoid(zc) * fc[u], wd = zd * sigmoid(zd) * fc[u];
-            const float hx = hv[u][0][q], hy = hv[u][1][q], hz = hv[u][2][q];
-            m0 += wc * (hx * ux[u] + hy * uy[u] + hz * uz[u]);
+            constexpr int BC = NZ > 2 ? 2 : 0, BD = NZ > 2 ? 3 : 0;
+            const float zc = zr[g][BC][q] + qz[BC][q], zd = zr[g][BD][q] + qz[BD][q];
+            const float wc = zc * sigmoid(zc) * fc[g], wd = zd * sigmoid(zd) * fc[g];
+            const float hx = hv[g][0][q], hy = hv[g][1][q], hz = hv[g][2][q];
+            m0 += wc * (hx * ux[g] + hy * uy[g] + hz * uz[g]);
             m1x += wd * hx;
             m1y += wd * hy;
             m1z += wd * hz;
@@ -277,10 +318,18 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
   }
 #pragma unroll
   for (int q = 0; q < CPL; ++q) {
-    A0[i * C + c0 + q] = a0[q] * inv_avg;
-    A1[(i * 3 + 0) * C + c0 + q] = a1[0][q] * inv_avg;
-    A1[(i * 3 + 1) * C + c0 + q] = a1[1][q] * inv_avg;
-    A1[(i * 3 + 2) * C + c0 + q] = a1[2][q] * inv_avg;
+    a0[q] = add_halves(a0[q]) * inv_avg;
+    a1[0][q] = add_halves(a1[0][q]) * inv_avg;
+    a1[1][q] = add_halves(a1[1][q]) * inv_avg;
+    a1[2][q] = add_halves(a1[2][q]) * inv_avg;
+  }
+  // the lower half writes A0 and the x row of A1, the upper half the y and z rows
+  if (!upper) {
+    store_ch<CPL>(A0 + i * C + c0, a0);
+    store_ch<CPL>(A1 + (i * 3 + 0) * C + c0, a1[0]);
+  } else {
+    store_ch<CPL>(A1 + (i * 3 + 1) * C + c0, a1[1]);
+    store_ch<CPL>(A1 + (i * 3 + 2) * C + c0, a1[2]);
   }
 }
 
@@ -292,21 +341,24 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
 // gef[e, n] = sum_k gz[e, k] w1ef[n, k] (the radial block of the gather-cat row gradient) and
 // gz itself may be null (not stored): the first layer needs no other part of gz @ W1^T.
 // gzsum[i] = sum over the centre's rows of gz (the receiver block's gradient when zq is formed
-// per atom). Row loads as in message_kernel.
+// per atom). Rows and loads as in message_kernel (a half-wave per row); the channel sums of a
+// row (radial gradients and geometry) are reduced over its half-wave.
 constexpr int kMaxBasis = 16;
 
-template <int CPL, bool H1, int RB>
+template <int CPL64, bool H1, int RB>
 __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     const float* z, const float* zq, const float* geo, const int32_t* edge_index, const int64_t* off,
     const int64_t* n_edges, int64_t e_cap, int64_t n, const float* h0, const float* h1, const float* gA0,
     const float* gA1, float inv_avg, float* gz, float* gzsum, float* ggeo, int accumulate_geo, const float* w1ef,
     int nb, float* gef) {
-  constexpr int C = 64 * CPL;
+  constexpr int CPL = 2 * CPL64, C = 32 * CPL;
   constexpr int NZ = H1 ? 4 : 2;
+  constexpr int kPairs = H1 ? 1 : 2;  // row pairs per load group (registers: three waves per SIMD)
   // w1ef's rows padded to RB (8 or 16) with zero rows (all zero without w1ef): the radial sums
   // run over RB rows without a branch per row
   extern __shared__ float s_w[];  // [RB, 4C]
   const int lane = threadIdx.x & 63;
+  const bool upper = lane >= 32;
   const int nbv = w1ef ? nb : 0;
   for (int k = threadIdx.x; k < RB * 4 * C; k += blockDim.x) s_w[k] = k < nbv * 4 * C ? w1ef[k] : 0.f;
   __syncthreads();
@@ -314,7 +366,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
   if (i >= n) return;
   int64_t lo;
   const int64_t hi = wave_rows(off, n_edges, e_cap, i, lo);
-  const int c0 = lane * CPL;
+  const int c0 = (lane & 31) * CPL;
   float g0[CPL], g1[3][CPL];
   load_ch<CPL>(gA0 + i * C + c0, g0);
 #pragma unroll
@@ -326,7 +378,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     g1[1][q] *= inv_avg;
     g1[2][q] *= inv_avg;
   }
-  float gs[NZ][CPL];  // sum of gz over the centre's rows (in row order)
+  float gs[NZ][CPL];  // sum of gz over this half's rows (in row order)
   float qz[NZ][CPL];  // the centre's receiver block of z (zq[i]), 0 when z is complete
 #pragma unroll
   for (int b = 0; b < NZ; ++b) {
@@ -339,6 +391,8 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
 #pragma unroll
     for (int q = 0; q < CPL; ++q) gs[b][q] = 0.f;
   }
+  const int t_red = half_sum16_index(lane);
+  const bool writer = (lane & 1) == 0;
   for (int64_t base = lo; base < hi; base += 64) {
     const int cnt = (int)(hi - base < 64 ? hi - base : 64);
     const RowGeo m = row_geo(geo, edge_index, base + lane, lane < cnt);
@@ -350,59 +404,63 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
       og[2] = t.z;
       og[3] = t.w;
     }
-    for (int u0 = 0; u0 < cnt; u0 += kGroup) {
-      float zr[kGroup][NZ][CPL], hj[kGroup][CPL], hv[kGroup][3][CPL];
-      float ux[kGroup], uy[kGroup], uz[kGroup], fc[kGroup];
+    for (int u0 = 0; u0 < cnt; u0 += 2 * kPairs) {
+      float zr[kPairs][NZ][CPL], hj[kPairs][CPL], hv[kPairs][3][CPL];
+      float ux[kPairs], uy[kPairs], uz[kPairs], fc[kPairs];
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u) {
-        const int s = u0 + u < cnt ? u0 + u : cnt - 1;
-        const int64_t j = bcast(m.j, s);
-        ux[u] = bcast(m.ux, s);
-        uy[u] = bcast(m.uy, s);
-        uz[u] = bcast(m.uz, s);
-        fc[u] = u0 + u < cnt ? bcast(m.fc, s) : 0.f;  // a row past the end adds exact zeros
+      for (int g = 0; g < kPairs; ++g) {
+        const int r0 = u0 + 2 * g, s0 = r0 < cnt ? r0 : cnt - 1, s1 = r0 + 1 < cnt ? r0 + 1 : cnt - 1;
+        const bool valid = r0 + (upper ? 1 : 0) < cnt;
+        const int s = upper ? s1 : s0;
+        const int64_t j = bcast2(m.j, s0, s1, upper);
+        ux[g] = bcast2(m.ux, s0, s1, upper);
+        uy[g] = bcast2(m.uy, s0, s1, upper);
+        uz[g] = bcast2(m.uz, s0, s1, upper);
+        const float f = bcast2(m.fc, s0, s1, upper);
+        fc[g] = valid ? f : 0.f;  // a row past the end adds exact zeros
         const float* ze = z + (base + s) * (NZ * C) + c0;
 #pragma unroll
-        for (int b = 0; b < NZ; ++b) load_ch<CPL>(ze + b * C, zr[u][b]);
-        load_ch<CPL>(h0 + j * C + c0, hj[u]);
+        for (int b = 0; b < NZ; ++b) load_ch<CPL>(ze + b * C, zr[g][b]);
+        load_ch<CPL>(h0 + j * C + c0, hj[g]);
         if (H1) {
 #pragma unroll
-          for (int x = 0; x < 3; ++x) load_ch<CPL>(h1 + (j * 3 + x) * C + c0, hv[u][x]);
+          for (int x = 0; x < 3; ++x) load_ch<CPL>(h1 + (j * 3 + x) * C + c0, hv[g][x]);
         }
       }
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u) {
+      for (int g = 0; g < kPairs; ++g) {
         // rows past the end (fc = 0) are computed and not stored: a branch around them would let
         // the compiler move the group's loads behind it
-        const bool valid = u0 + u < cnt;
-        const int64_t e = base + u0 + u;
+        const int r0 = u0 + 2 * g, s0 = r0 < cnt ? r0 : cnt - 1, s1 = r0 + 1 < cnt ? r0 + 1 : cnt - 1;
+        const bool valid = r0 + (upper ? 1 : 0) < cnt;
+        const int64_t e = base + (upper ? s1 : s0);
         float gzl[NZ][CPL];
         float sf = 0.f, su0 = 0.f, su1 = 0.f, su2 = 0.f;
 #pragma unroll
         for (int q = 0; q < CPL; ++q) {
-          const float hjq = hj[u][q];
-          const float gu = g1[0][q] * ux[u] + g1[1][q] * uy[u] + g1[2][q] * uz[u];
-          const float za = zr[u][0][q] + qz[0][q], zb = zr[u][1][q] + qz[1][q];
+          const float hjq = hj[g][q];
+          const float gu = g1[0][q] * ux[g] + g1[1][q] * uy[g] + g1[2][q] * uz[g];
+          const float za = zr[g][0][q] + qz[0][q], zb = zr[g][1][q] + qz[1][q];
           const float sa = sigmoid(za), sb = sigmoid(zb);
           const float gwa = g0[q] * hjq, gwb = hjq * gu;
-          gzl[0][q] = gwa * fc[u] * sa * (1.0f + za * (1.0f - sa));
-          gzl[1][q] = gwb * fc[u] * sb * (1.0f + zb * (1.0f - sb));
+          gzl[0][q] = gwa * fc[g] * sa * (1.0f + za * (1.0f - sa));
+          gzl[1][q] = gwb * fc[g] * sb * (1.0f + zb * (1.0f - sb));
           sf += gwa * za * sa + gwb * zb * sb;
-          const float wb = zb * sb * fc[u];
+          const float wb = zb * sb * fc[g];
           su0 += g1[0][q] * wb * hjq;
           su1 += g1[1][q] * wb * hjq;
           su2 += g1[2][q] * wb * hjq;
           if (H1) {
             constexpr int BC = NZ > 2 ? 2 : 0, BD = NZ > 2 ? 3 : 0;
-            const float hx = hv[u][0][q], hy = hv[u][1][q], hz = hv[u][2][q];
-            const float zc = zr[u][BC][q] + qz[BC][q], zd = zr[u][BD][q] + qz[BD][q];
+            const float hx = hv[g][0][q], hy = hv[g][1][q], hz = hv[g][2][q];
+            const float zc = zr[g][BC][q] + qz[BC][q], zd = zr[g][BD][q] + qz[BD][q];
             const float sc = sigmoid(zc), sd = sigmoid(zd);
-            const float proj = hx * ux[u] + hy * uy[u] + hz * uz[u];
+            const float proj = hx * ux[g] + hy * uy[g] + hz * uz[g];
             const float gwc = g0[q] * proj, gwd = g1[0][q] * hx + g1[1][q] * hy + g1[2][q] * hz;
-            gzl[BC][q] = gwc * fc[u] * sc * (1.0f + zc * (1.0f - sc));
-            gzl[BD][q] = gwd * fc[u] * sd * (1.0f + zd * (1.0f - sd));
+            gzl[BC][q] = gwc * fc[g] * sc * (1.0f + zc * (1.0f - sc));
+            gzl[BD][q] = gwd * fc[g] * sd * (1.0f + zd * (1.0f - sd));
             sf += gwc * zc * sc + gwd * zd * sd;
-            const float t = g0[q] * zc * sc * fc[u];
+            const float t = g0[q] * zc * sc * fc[g];
             su0 += t * hx;
             su1 += t * hy;
             su2 += t * hz;
@@ -411,9 +469,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
         if (gz && valid) {
           float* gze = gz + e * NZ * C + c0;
 #pragma unroll
-          for (int b = 0; b < NZ; ++b)
-#pragma unroll
-            for (int q = 0; q < CPL; ++q) store_stream(gze + b * C + q, gzl[b][q]);
+          for (int b = 0; b < NZ; ++b) store_ch_stream<CPL>(gze + b * C, gzl[b]);
         }
         if (gzsum) {
 #pragma unroll
@@ -421,9 +477,9 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
 #pragma unroll
             for (int q = 0; q < CPL; ++q) gs[b][q] += gzl[b][q];
         }
-        // the radial-basis gradients and the four geometry sums, reduced over the wave together.
-        // The LDS offset is opaque to the compiler, which would otherwise keep all of w1ef in
-        // registers across the loop (RB * NZ * CPL of them: fewer waves per SIMD)
+        // the radial-basis gradients and the four geometry sums, reduced over the half-wave
+        // together. The LDS offset is opaque to the compiler, which would otherwise keep all of
+        // w1ef in registers across the loop (RB * NZ * CPL of them: fewer waves per SIMD)
         int woff = c0;
         asm volatile("" : "+v"(woff));
         float red[16];
@@ -432,12 +488,15 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
           const float* w = s_w + t * 4 * C + woff;
           red[t] = 0.f;
 #pragma unroll
-          for (int b = 0; b < NZ; ++b)
+          for (int b = 0; b < NZ; ++b) {
+            float wv[CPL];
+            load_ch<CPL>(w + b * C, wv);
 #pragma unroll
-            for (int q = 0; q < CPL; ++q) red[t] += gzl[b][q] * w[b * C + q];
+            for (int q = 0; q < CPL; ++q) red[t] += gzl[b][q] * wv[q];
+          }
         }
-        const int s = valid ? u0 + u : cnt - 1;
-        const float o0 = bcast(og[0], s), o1 = bcast(og[1], s), o2 = bcast(og[2], s), o3 = bcast(og[3], s);
+        const float o0 = bcast2(og[0], s0, s1, upper), o1 = bcast2(og[1], s0, s1, upper),
+                    o2 = bcast2(og[2], s0, s1, upper), o3 = bcast2(og[3], s0, s1, upper);
         float tg;  // the geometry sum this lane writes (index tgi), if any
         int tgi;
         if constexpr (RB == 8) {
@@ -446,19 +505,16 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
           red[10] = su2;
           red[11] = sf;
           red[12] = red[13] = red[14] = red[15] = 0.f;
-          const float tot = wave_sum16(red);
-          const int t = wave_sum16_index(lane);
-          if (valid && (lane & 3) == 0 && t < nbv) gef[e * nb + t] = tot;
+          const float tot = half_sum16(red);
+          if (valid && writer && t_red < nbv) gef[e * nb + t_red] = tot;
           tg = tot;
-          tgi = (lane & 3) == 0 && t >= 8 && t < 12 ? t - 8 : -1;
+          tgi = writer && t_red >= 8 && t_red < 12 ? t_red - 8 : -1;
         } else {
-          const float tot = wave_sum16(red);
-          const int t = wave_sum16_index(lane);
-          if (valid && (lane & 3) == 0 && t < nbv) gef[e * nb + t] = tot;
-          float g8[8] = {su0, su1, su2, sf, 0.f, 0.f, 0.f, 0.f};
-          tg = wave_sum8(g8);
-          const int t8 = wave_sum8_index(lane);
-          tgi = (lane & 7) == 0 && t8 < 4 ? t8 : -1;
+          const float tot = half_sum16(red);
+          if (valid && writer && t_red < nbv) gef[e * nb + t_red] = tot;
+          float g16[16] = {su0, su1, su2, sf, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          tg = half_sum16(g16);
+          tgi = writer && t_red < 4 ? t_red : -1;
         }
         if (valid && tgi >= 0) {
           const float old = tgi == 0 ? o0 : tgi == 1 ? o1 : tgi == 2 ? o2 : o3;
@@ -468,36 +524,64 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     }
   }
   if (gzsum) {
-    float* d = gzsum + i * NZ * C + c0;
 #pragma unroll
     for (int b = 0; b < NZ; ++b)
 #pragma unroll
-      for (int q = 0; q < CPL; ++q) d[b * C + q] = gs[b][q];
+      for (int q = 0; q < CPL; ++q) gs[b][q] = add_halves(gs[b][q]);
+    // the lower half writes blocks 0 .. NZ / 2 - 1, the upper half the rest
+    float* d = gzsum + i * NZ * C + c0;
+#pragma unroll
+    for (int b = 0; b < NZ; ++b)
+      if ((b < NZ / 2) != upper) store_ch<CPL>(d + b * C, gs[b]);
   }
 }
 
 // VJP, sender side (one wave per node j, over the reverse rows e = reverse[e'] of its rows e'
 // as a centre; the receiver of e is i = neighbor[e']):
 //   g_h0_j += gA0_i wa_e + wb_e (gA1_i . u_e);  g_h1_j,x += gA0_i wc_e u_e,x + gA1_i,x wd_e
-// accumulate: bit 0 adds into gh0, bit 1 into gh1 (else they are overwritten). Per 64 rows the
-// wave loads reverse[e'], the receiver and the geometry of e once (a lane per row); each group
-// of kGroup rows issues its z[e], zq[i], gA0[i] and gA1[i] loads before any arithmetic.
-template <int CPL, bool H1>
+// and, with gzsum_src, the sender sums of the edge pre-activation gradient,
+//   gzsum_src[j] = sum over the rows e with sender j of g_z[e]   ([N, NZ C], g_z as in
+// message_bwd_edge_kernel, recomputed here from z[e], zq[i], gA[i] and the sender's own h0_j,
+// h1_j): the sender block of the gather-cat row gradient then is gzsum_src @ W1[:C]^T, one node
+// GEMM, instead of the edge GEMM gz @ W1[:C]^T and a segment sum over [E, C] (the same sum by
+// linearity) and without g_z ever in memory.
+// accumulate: bit 0 adds into gh0, bit 1 into gh1 (else they are overwritten). A half-wave per
+// row as in message_kernel: per 64 rows the wave loads reverse[e'], the receiver and the
+// geometry of e once (a lane per row); each group of kPairs row pairs issues its z[e], zq[i],
+// gA0[i] and gA1[i] loads before any arithmetic.
+template <int CPL64, bool H1>
 __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
     const float* z, const float* zq, const float* geo, const int32_t* edge_index, const int32_t* reverse,
-    const int64_t* off, const int64_t* n_edges, int64_t e_cap, int64_t n, const float* gA0, const float* gA1,
-    float inv_avg, float* gh0, float* gh1, int accumulate) {
-  constexpr int C = 64 * CPL;
+    const int64_t* off, const int64_t* n_edges, int64_t e_cap, int64_t n, const float* h0, const float* h1,
+    const float* gA0, const float* gA1, float inv_avg, float* gh0, float* gh1, int accumulate, float* gzsum_src) {
+  constexpr int CPL = 2 * CPL64, C = 32 * CPL;
   constexpr int NZ = H1 ? 4 : 2;
+  constexpr int kPairs = H1 ? 1 : 2;  // row pairs per load group (registers: three waves per SIMD)
   const int lane = threadIdx.x & 63;
+  const bool upper = lane >= 32;
   const int64_t jn = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   if (jn >= n) return;
   int64_t lo;
   const int64_t hi = wave_rows(off, n_edges, e_cap, jn, lo);
-  const int c0 = lane * CPL;
-  float a0[CPL], a1[3][CPL];
+  const int c0 = (lane & 31) * CPL;
+  float a0[CPL], a1[3][CPL], gsum[NZ][CPL];
 #pragma unroll
   for (int q = 0; q < CPL; ++q) a0[q] = a1[0][q] = a1[1][q] = a1[2][q] = 0.f;
+#pragma unroll
+  for (int b = 0; b < NZ; ++b)
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) gsum[b][q] = 0.f;
+  // the sender's own features (the h0_j / h1_j of every row here), for the g_z sums
+  float hs[CPL], hsv[3][CPL];
+#pragma unroll
+  for (int q = 0; q < CPL; ++q) hs[q] = hsv[0][q] = hsv[1][q] = hsv[2][q] = 0.f;
+  if (gzsum_src) {
+    load_ch<CPL>(h0 + jn * C + c0, hs);
+    if (H1) {
+#pragma unroll
+      for (int x = 0; x < 3; ++x) load_ch<CPL>(h1 + (jn * 3 + x) * C + c0, hsv[x]);
+    }
+  }
   for (int64_t base = lo; base < hi; base += 64) {
     const int cnt = (int)(hi - base < 64 ? hi - base : 64);
     int me = -1, mi = 0;
@@ -514,53 +598,69 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
         mfc = geo[8 * (int64_t)me + 4];
       }
     }
-    for (int u0 = 0; u0 < cnt; u0 += kGroup) {
-      float zr[kGroup][NZ][CPL], qe[kGroup][NZ][CPL], ga[kGroup][4][CPL];
-      float ux[kGroup], uy[kGroup], uz[kGroup], fc[kGroup];
-      int er[kGroup];
+    for (int u0 = 0; u0 < cnt; u0 += 2 * kPairs) {
+      float zr[kPairs][NZ][CPL], qe[kPairs][NZ][CPL], ga[kPairs][4][CPL];
+      float ux[kPairs], uy[kPairs], uz[kPairs], fc[kPairs];
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u) {
-        const int s = u0 + u < cnt ? u0 + u : cnt - 1;
-        er[u] = bcast(me, s);
-        const int64_t i = bcast(mi, s);
-        const int64_t e = er[u] < 0 ? 0 : er[u];  // a missing reverse row reads row 0, weight 0
-        ux[u] = bcast(mux, s);
-        uy[u] = bcast(muy, s);
-        uz[u] = bcast(muz, s);
+      for (int g = 0; g < kPairs; ++g) {
+        const int r0 = u0 + 2 * g, s0 = r0 < cnt ? r0 : cnt - 1, s1 = r0 + 1 < cnt ? r0 + 1 : cnt - 1;
+        const bool valid = r0 + (upper ? 1 : 0) < cnt;
+        const int er = bcast2(me, s0, s1, upper);
+        const int64_t i = bcast2(mi, s0, s1, upper);
+        const int64_t e = er < 0 ? 0 : er;  // a missing reverse row reads row 0, weight 0
+        ux[g] = bcast2(mux, s0, s1, upper);
+        uy[g] = bcast2(muy, s0, s1, upper);
+        uz[g] = bcast2(muz, s0, s1, upper);
+        const float f = bcast2(mfc, s0, s1, upper);
         // rows past the end and missing reverse rows add exact zeros (fc = 0)
-        fc[u] = u0 + u < cnt && er[u] >= 0 ? bcast(mfc, s) : 0.f;
+        fc[g] = valid && er >= 0 ? f : 0.f;
         const float* ze = z + e * (NZ * C) + c0;
 #pragma unroll
         for (int b = 0; b < NZ; ++b) {
-          load_ch<CPL>(ze + b * C, zr[u][b]);
+          load_ch<CPL>(ze + b * C, zr[g][b]);
           if (zq) {
-            load_ch<CPL>(zq + i * (NZ * C) + b * C + c0, qe[u][b]);  // the receiver block of z[e] (row i)
+            load_ch<CPL>(zq + i * (NZ * C) + b * C + c0, qe[g][b]);  // the receiver block of z[e] (row i)
           } else {
 #pragma unroll
-            for (int q = 0; q < CPL; ++q) qe[u][b][q] = 0.f;
+            for (int q = 0; q < CPL; ++q) qe[g][b][q] = 0.f;
           }
         }
-        load_ch<CPL>(gA0 + i * C + c0, ga[u][0]);
+        load_ch<CPL>(gA0 + i * C + c0, ga[g][0]);
 #pragma unroll
-        for (int x = 0; x < 3; ++x) load_ch<CPL>(gA1 + (i * 3 + x) * C + c0, ga[u][1 + x]);
+        for (int x = 0; x < 3; ++x) load_ch<CPL>(gA1 + (i * 3 + x) * C + c0, ga[g][1 + x]);
       }
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u) {
+      for (int g = 0; g < kPairs; ++g) {
         // no branch around the zero rows: it would let the compiler move the loads behind it
 #pragma unroll
         for (int q = 0; q < CPL; ++q) {
-          const float g0 = ga[u][0][q], gx = ga[u][1][q], gy = ga[u][2][q], gzv = ga[u][3][q];
-          const float za = zr[u][0][q] + qe[u][0][q], zb = zr[u][1][q] + qe[u][1][q];
-          const float wa = za * sigmoid(za) * fc[u], wb = zb * sigmoid(zb) * fc[u];
-          a0[q] += g0 * wa + wb * (gx * ux[u] + gy * uy[u] + gzv * uz[u]);
+          const float g0 = ga[g][0][q], gx = ga[g][1][q], gy = ga[g][2][q], gzv = ga[g][3][q];
+          const float za = zr[g][0][q] + qe[g][0][q], zb = zr[g][1][q] + qe[g][1][q];
+          const float sa = sigmoid(za), sb = sigmoid(zb);
+          const float wa = za * sa * fc[g], wb = zb * sb * fc[g];
+          const float gu = gx * ux[g] + gy * uy[g] + gzv * uz[g];
+          a0[q] += g0 * wa + wb * gu;
+          if (gzsum_src) {
+            const float gwa = g0 * hs[q], gwb = hs[q] * gu;
+            gsum[0][q] += gwa * fc[g] * sa * (1.0f + za * (1.0f - sa));
+            gsum[1][q] += gwb * fc[g] * sb * (1.0f + zb * (1.0f - sb));
+          }
           if (H1) {
             constexpr int BC = NZ > 2 ? 2 : 0, BD = NZ > 2 ? 3 : 0;
-            const float zc = zr[u][BC][q] + qe[u][BC][q], zd = zr[u][BD][q] + qe[u][BD][q];
-            const float wc = zc * sigmoid(zc) * fc[u], wd = zd * sigmoid(zd) * fc[u];
+            const float zc = zr[g][BC][q] + qe[g][BC][q], zd = zr[g][BD][q] + qe[g][BD][q];
+            const float sc = sigmoid(zc), sd = sigmoid(zd);
+            const float wc = zc * sc * fc[g], wd = zd * sd * fc[g];
             const float t = g0 * wc;
-            a1[0][q] += t * ux[u] + gx * wd;
-            a1[1][q] += t * uy[u] + gy * wd;
-            a1[2][q] += t * uz[u] + gzv * wd;
+            a1[0][q] += t * ux[g] + gx * wd;
+            a1[1][q] += t * uy[g] + gy * wd;
+            a1[2][q] += t * uz[g] + gzv * wd;
+            if (gzsum_src) {
+              const float hx = hsv[0][q], hy = hsv[1][q], hz = hsv[2][q];
+              const float gwc = g0 * (hx * ux[g] + hy * uy[g] + hz * uz[g]);
+              const float gwd = gx * hx + gy * hy + gzv * hz;
+              gsum[BC][q] += gwc * fc[g] * sc * (1.0f + zc * (1.0f - sc));
+              gsum[BD][q] += gwd * fc[g] * sd * (1.0f + zd * (1.0f - sd));
+            }
           }
         }
       }
@@ -568,16 +668,54 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
   }
 #pragma unroll
   for (int q = 0; q < CPL; ++q) {
-    float* d0 = gh0 + jn * C + c0 + q;
-    const float v0 = a0[q] * inv_avg;
-    *d0 = (accumulate & 1) ? *d0 + v0 : v0;
-    if (H1 && gh1) {
-      for (int x = 0; x < 3; ++x) {
-        float* d1 = gh1 + (jn * 3 + x) * C + c0 + q;
-        const float v1 = a1[x][q] * inv_avg;
-        *d1 = (accumulate & 2) ? *d1 + v1 : v1;
-      }
+    a0[q] = add_halves(a0[q]) * inv_avg;
+    if (H1) {
+      a1[0][q] = add_halves(a1[0][q]) * inv_avg;
+      a1[1][q] = add_halves(a1[1][q]) * inv_avg;
+      a1[2][q] = add_halves(a1[2][q]) * inv_avg;
     }
+  }
+  // the lower half writes gh0 and the x row of gh1, the upper half the y and z rows
+  if (gh0 && !upper) {
+    float* d0 = gh0 + jn * C + c0;
+    float v0[CPL];
+    if (accumulate & 1) {
+      load_ch<CPL>(d0, v0);
+#pragma unroll
+      for (int q = 0; q < CPL; ++q) v0[q] += a0[q];
+    } else {
+#pragma unroll
+      for (int q = 0; q < CPL; ++q) v0[q] = a0[q];
+    }
+    store_ch<CPL>(d0, v0);
+  }
+  if (H1 && gh1) {
+#pragma unroll
+    for (int x = 0; x < 3; ++x) {
+      if ((x == 0) == upper) continue;
+      float* d1 = gh1 + (jn * 3 + x) * C + c0;
+      float v1[CPL];
+      if (accumulate & 2) {
+        load_ch<CPL>(d1, v1);
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) v1[q] += a1[x][q];
+      } else {
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) v1[q] = a1[x][q];
+      }
+      store_ch<CPL>(d1, v1);
+    }
+  }
+  if (gzsum_src) {
+#pragma unroll
+    for (int b = 0; b < NZ; ++b)
+#pragma unroll
+      for (int q = 0; q < CPL; ++q) gsum[b][q] = add_halves(gsum[b][q]) * inv_avg;
+    // the lower half writes blocks 0 .. NZ / 2 - 1, the upper half the rest
+    float* d = gzsum_src + jn * NZ * C + c0;
+#pragma unroll
+    for (int b = 0; b < NZ; ++b)
+      if ((b < NZ / 2) != upper) store_ch<CPL>(d + b * C, gsum[b]);
   }
 }
 
@@ -734,15 +872,16 @@ int launch_message(bool h1, dim3 grid, hipStream_t s, const float* z, const floa
 
 }  // namespace
 
-// the message kernels load a lane's CPL = C / 64 channels as one vector: the per-node and per-row
-// arrays start on 4 * CPL-byte boundaries, geo and ggeo on 16 bytes
+// the message kernels load a lane's channels as vectors: the per-node and per-row arrays start on
+// 8-byte (C = 64) or 16-byte boundaries, geo and ggeo on 16 bytes
 static bool aligned_to(uintptr_t a, std::initializer_list<const void*> ptrs) {
   for (const void* p : ptrs)
     if (p && ((uintptr_t)p % a) != 0) return false;
   return true;
 }
 
-static uintptr_t channel_alignment(int channels) { return 4 * (uintptr_t)(channels >= 64 ? channels / 64 : 1); }
+// a lane's CPL = C / 32 channels: 8-byte loads for C = 64, 16-byte loads above
+static uintptr_t channel_alignment(int channels) { return channels <= 64 ? 8 : 16; }
 
 #define FMD_CPL_DISPATCH(C, FN, ...)                 \
   switch ((C) / 64) {                                \
@@ -760,7 +899,7 @@ int launch_bwd_edge(bool h1, dim3 grid, hipStream_t s, const float* z, const flo
                     const float* h1p, const float* gA0, const float* gA1, float inv_avg, float* gz, float* gzsum,
                     float* ggeo, int acc, const float* w1ef, int nb, float* gef) {
   const bool wide = w1ef && nb > 8;  // radial rows padded to 16 instead of 8
-  const size_t lds = (size_t)(wide ? 16 : 8) * 4 * 64 * CPL * sizeof(float);
+  const size_t lds = (size_t)(wide ? 16 : 8) * 4 * 64 * CPL * sizeof(float);  // RB x 4C floats
 #define FMD_BWD_EDGE(H, RB)                                                                                         \
   hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, H, RB>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne,  \
                      e_cap, n, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef)
@@ -779,15 +918,15 @@ int launch_bwd_edge(bool h1, dim3 grid, hipStream_t s, const float* z, const flo
 
 template <int CPL>
 int launch_bwd_src(bool h1, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
-                   const int32_t* ei,
-                   const int32_t* rev, const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n,
-                   const float* gA0, const float* gA1, float inv_avg, float* gh0, float* gh1, int acc) {
+                   const int32_t* ei, const int32_t* rev, const int64_t* off, const int64_t* ne, int64_t e_cap,
+                   int64_t n, const float* h0, const float* h1p, const float* gA0, const float* gA1, float inv_avg,
+                   float* gh0, float* gh1, int acc, float* gzsum_src) {
   if (h1)
     hipLaunchKernelGGL((message_bwd_src_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, rev, off, ne,
-                       e_cap, n, gA0, gA1, inv_avg, gh0, gh1, acc);
+                       e_cap, n, h0, h1p, gA0, gA1, inv_avg, gh0, gh1, acc, gzsum_src);
   else
     hipLaunchKernelGGL((message_bwd_src_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, rev, off, ne,
-                       e_cap, n, gA0, gA1, inv_avg, gh0, gh1, acc);
+                       e_cap, n, h0, h1p, gA0, gA1, inv_avg, gh0, gh1, acc, gzsum_src);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -834,14 +973,14 @@ int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, 
                              const int32_t* reverse,
                              const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
                              int32_t channels, const float* h0, const float* h1, const float* gA0, const float* gA1,
-                             float inv_avg, float* gz, float* gzsum, float* ggeo, int32_t accumulate_geo, float* gh0,
-                             float* gh1, int32_t accumulate_h, const float* w1ef, int32_t nb, float* gef,
-                             hipStream_t stream) {
+                             float inv_avg, float* gz, float* gzsum, float* gzsum_src, float* ggeo,
+                             int32_t accumulate_geo, float* gh0, float* gh1, int32_t accumulate_h, const float* w1ef,
+                             int32_t nb, float* gef, hipStream_t stream) {
   FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && gA0 && gA1 && ggeo && n_atoms >= 0);
-  FMD_REQUIRE(gz || w1ef);
+  FMD_REQUIRE(gz || w1ef || gzsum);
   FMD_REQUIRE(!w1ef || (gef && nb > 0 && nb <= kMaxBasis));
-  FMD_REQUIRE(!gh0 || reverse);
-  FMD_REQUIRE(aligned_to(channel_alignment(channels), {z, zq, h0, h1, gA0, gA1, gz, gzsum, gh0, gh1}) &&
+  FMD_REQUIRE(!(gh0 || gzsum_src) || reverse);
+  FMD_REQUIRE(aligned_to(channel_alignment(channels), {z, zq, h0, h1, gA0, gA1, gz, gzsum, gzsum_src, gh0, gh1}) &&
               aligned_to(16, {geo, ggeo}));
   if (n_atoms == 0) return FMD_OK;
   dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
@@ -855,14 +994,14 @@ int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, 
                                     n_atoms, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
     default: return FMD_EUNSUPPORTED;
   }
-  if (rc != FMD_OK || !gh0) return rc;
+  if (rc != FMD_OK || !(gh0 || gzsum_src)) return rc;
   switch (channels / 64) {
     case 1: return launch_bwd_src<1>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets, n_edges,
-                                     e_cap, n_atoms, gA0, gA1, inv_avg, gh0, gh1, accumulate_h);
+                                     e_cap, n_atoms, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h, gzsum_src);
     case 2: return launch_bwd_src<2>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets, n_edges,
-                                     e_cap, n_atoms, gA0, gA1, inv_avg, gh0, gh1, accumulate_h);
+                                     e_cap, n_atoms, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h, gzsum_src);
     case 4: return launch_bwd_src<4>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets, n_edges,
-                                     e_cap, n_atoms, gA0, gA1, inv_avg, gh0, gh1, accumulate_h);
+                                     e_cap, n_atoms, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h, gzsum_src);
     default: return FMD_EUNSUPPORTED;
   }
 }

@@ -39,7 +39,8 @@ from torch.autograd import Function
 from fastmd_amd import _abi
 from fastmd_amd.adapters.protocol import CapacityStep, CaptureContract, GraphBatch, PaddingRule, TopologySpec
 from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr
-from fastmd_amd.ops.wide_gemm import Planes, gemm, gemm_gather, gemm_group, gemm_planes, split_planes
+from fastmd_amd.ops.wide_gemm import (Planes, gemm, gemm_gather, gemm_group, gemm_planes, gemm_splitk,
+                                     split_planes)
 
 _ELEMENTS = 118
 _CAPACITY_STEP = CapacityStep(u_step=32, min_pad_u=32, u_thermal_factor=1.02)
@@ -175,8 +176,7 @@ class MaceLike(nn.Module):
     def w1_planes(self, t: int, which: str, nz: int = 0) -> Planes:
         """bf16 planes (split once per W1 version) of the weights of layer t's edge GEMMs when the
         operands come pre-split: "receiver" / "sender" = the first nz rows of w1_receiver_t /
-        w1_sender_t (the forward's [nz, K] B operands), "sender_rows" = W1[:C] ([C, 4C], the B
-        operand of the VJP's sender-block GEMM gz @ W1[:C]^T)."""
+        w1_sender_t (the forward's [nz, K] B operands)."""
         w = self.layers[t].W1
         key = (w.data_ptr(), w._version, w.device)
         cache = self.__dict__.setdefault("_w1p_cache", {})
@@ -187,12 +187,24 @@ class MaceLike(nn.Module):
                 src = self.w1_receiver_t(t)[:nz]
             elif which == "sender":
                 src = self.w1_sender_t(t)[:nz]
-            elif which == "sender_rows":
-                src = w.detach()[:C]
             else:
                 raise ValueError(f"unknown W1 block {which!r}")
             hit = (key, split_planes(src))
             cache[(t, which, nz)] = hit
+        return hit[1]
+
+    def w1_node_blocks(self, t: int) -> Tensor:
+        """[W1[:C] | W1[C:2C]] ([C, 8C]): the B operand ([N, K], b_layout 0) of the VJP's node
+        GEMM [gzs_src | gzs] @ B^T, the sender and receiver blocks of the gather-cat row gradient;
+        rebuilt when W1 is changed in place."""
+        w = self.layers[t].W1
+        C = self.config.channels
+        key = (w.data_ptr(), w._version, w.device)
+        cache = self.__dict__.setdefault("_w1nb_cache", {})
+        hit = cache.get(t)
+        if hit is None or hit[0] != key:
+            hit = (key, torch.cat([w.detach()[:C], w.detach()[C:2 * C]], 1).contiguous())
+            cache[t] = hit
         return hit[1]
 
     @property
@@ -421,12 +433,15 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
             w1ef = layer.W1[2 * C:]
             _call("fmd_mace_message_bwd_f32", z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(), ei.data_ptr(),
                   rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1),
-                  gA0.data_ptr(), gA1.data_ptr(), inv_avg, None, None, ggeo.data_ptr(), acc_geo, None, None, 0,
-                  w1ef.data_ptr(), nb, gef.data_ptr())
+                  gA0.data_ptr(), gA1.data_ptr(), inv_avg, None, None, None, ggeo.data_ptr(), acc_geo, None, None,
+                  0, w1ef.data_ptr(), nb, gef.data_ptr())
             gefs.append((gef, nb))
             break
-        gz = _empty(e_cap, 4 * C, device=dev)
-        gzs = _empty(n, 4 * C, device=dev) if q is not None else None
+        # the gather-cat row gradient's node blocks come from per-node sums of g_z (never stored):
+        # over each centre's rows (receiver, gzs) and over each sender's rows (gzs_src, formed by
+        # the sender-side kernel); by linearity sum_e g_z[e] W^T = (sum_e g_z[e]) W^T
+        gzs = _empty(n, 4 * C, device=dev)
+        gzs_src = _empty(n, 4 * C, device=dev)
         gef = _empty(e_cap, nb, device=dev)
         # this layer's inputs: residual (plus, in the second layer, the first readout's
         # gradient of the first layer's output), sender side of the messages, gather-cat rows
@@ -436,19 +451,10 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
         w1ef = layer.W1[2 * C:]
         _call("fmd_mace_message_bwd_f32", z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(), ei.data_ptr(),
               rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1),
-              gA0.data_ptr(), gA1.data_ptr(), inv_avg, gz.data_ptr(), _abi.ptr(gzs), ggeo.data_ptr(), acc_geo,
-              g_in0.data_ptr(), _abi.ptr(g_in1), 1, w1ef.data_ptr(), nb, gef.data_ptr())
-        # the node blocks of the gather-cat row gradient (the radial block is gef)
-        if q is not None:
-            # sender block row by row (edge GEMM, then the sender segment sum); receiver block
-            # from the per-centre sums of gz: sum_e gz[e] W1[C:2C]^T = (sum_e gz[e]) W1[C:2C]^T
-            ga = gemm_planes([(gz, None)], model.w1_planes(t, "sender_rows"), a_planes=False)  # [E, C]
-            segment_sum_csr([(ga, inputs.csr_src, 0, 1.0, None)], n, C, out=g_in0, accumulate=True)
-            gemm(gzs, layer.W1[C:2 * C], b_layout=0, out=g_in0, accumulate=True)
-        else:
-            ga = gemm(gz, layer.W1[:2 * C], b_layout=0)  # [E, 2C]
-            segment_sum_csr([(ga, inputs.csr_src, 0, 1.0, None), (ga, inputs.csr_dst, C, 1.0, None)], n, C,
-                            out=g_in0, accumulate=True)
+              gA0.data_ptr(), gA1.data_ptr(), inv_avg, None, gzs.data_ptr(), gzs_src.data_ptr(), ggeo.data_ptr(),
+              acc_geo, g_in0.data_ptr(), _abi.ptr(g_in1), 1, w1ef.data_ptr(), nb, gef.data_ptr())
+        # g_in0 += [gzs_src | gzs] [W1[:C] | W1[C:2C]]^T (sender and receiver blocks, one node GEMM)
+        gemm_splitk(gzs_src, model.w1_node_blocks(t), b_layout=0, out=g_in0, a2=gzs, accumulate=True)
         gefs.append((gef, nb))
         g_out0, g_out1 = g_in0, g_in1
     gvec = _empty(e_cap, 3, device=dev)

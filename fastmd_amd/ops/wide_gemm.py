@@ -114,6 +114,34 @@ def gemm_group(problems, *, b_layout: int, epilogue: str | None = None) -> list:
     return [p["out"] for p in problems]
 
 
+def gemm_splitk(a: Tensor, b: Tensor, *, b_layout: int, out: Tensor, a2: Tensor | None = None,
+                bias: Tensor | None = None, accumulate: bool = False, splits: int = 8) -> Tensor:
+    """``out (+)= [a | a2] @ op(b) (+ bias)`` with K cut into ``splits`` slices multiplied by separate
+    workgroups and summed in slice order (fmd_gemm_splitk_f32): tall-K, few-tile GEMMs."""
+    require_cuda(a, b, out, a2, bias)
+    a, lda = rows_view(a)
+    b, ldb = rows_view(b)
+    m, ka = a.shape
+    k = ka + (a2.shape[1] if a2 is not None else 0)
+    n = b.shape[0] if b_layout == 0 else b.shape[1]
+    if (b.shape[1] if b_layout == 0 else b.shape[0]) != k or out.shape != (m, n) or out.stride(1) != 1:
+        raise ValueError("gemm_splitk shape mismatch")
+    lda2 = 0
+    if a2 is not None:
+        a2, lda2 = rows_view(a2)
+        if a2.shape[0] != m:
+            raise ValueError("gemm_splitk: a2 must have a's rows")
+    while splits > 1 and (k % splits or (k // splits) % 32 or (a2 is not None and ka % (k // splits))):
+        splits //= 2
+    ws = torch.empty((splits, m, n), dtype=torch.float32, device=out.device)
+    if bias is not None:
+        bias = bias.contiguous()
+    _abi.call("fmd_gemm_splitk_f32", a.data_ptr(), lda, _abi.ptr(a2), lda2, ka, b.data_ptr(), ldb, b_layout,
+              _abi.ptr(bias), out.data_ptr(), out.stride(0) if m > 1 else n, m, n, k, 1 if accumulate else 0, splits,
+              ws.data_ptr(), stream())
+    return out
+
+
 class Planes:
     """The three bf16 planes of a float32 matrix [rows, width] (fmd_split3_f32), slice-interleaved:
     ``data`` [rows, S, 3, 16] bfloat16 (S = ceil(width / 16), zero past ``width``), x = p0 + p1 + p2."""

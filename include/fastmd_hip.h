@@ -189,6 +189,16 @@ int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda,
                        const int64_t* m, const int64_t* n, const int64_t* k, const int32_t* accumulate,
                        int32_t epilogue, hipStream_t stream);
 
+/* C = [A | A2] op(B) (+ bias) (+ C if accumulate) as fmd_gemm_f32, with K cut into `splits` equal
+ * slices (multiples of 32, none straddling ksplit, the width of A; A2 may be null) multiplied by
+ * separate workgroups into workspace [splits, M, N] and then summed in slice order
+ * (deterministic): the tall-K node GEMMs (K = 8C) that fmd_gemm_f32's tiles would leave to a few
+ * hundred long-running workgroups. Replaces the reference's matmul (triton_wide_gemm.py:542-553)
+ * for that shape. */
+int fmd_gemm_splitk_f32(const float* a, int64_t lda, const float* a2, int64_t lda2, int64_t ksplit, const float* b,
+                        int64_t ldb, int32_t b_layout, const float* bias, float* c, int64_t ldc, int64_t m, int64_t n,
+                        int64_t k, int32_t accumulate, int32_t splits, float* workspace, hipStream_t stream);
+
 /* C[M,N] = A[M,K] B[N,K]^T (+ bias) (+ C) with the gather-cat fused into the operand load:
  * A = cat(part_0, ..., part_{n-1}) over n_parts <= 3 column blocks, part p reading row
  * indices_p[r * index_strides_p] of srcs_p (or row r when indices_p is null), width widths_p,
@@ -295,24 +305,29 @@ int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, co
  * edge pre-activation blocks a | b | c | d (W = 4C) when h1 is given; with h1 null (zero vector
  * features, where c and d meet only zeros) z holds a | b only (W = 2C). The pre-activations are
  * z[e] + zq[i] when zq ([N, W], the receiver block of the edge GEMM formed once per atom) is
- * given, else z[e]. z, zq, h0, h1, A0, A1 start on 4 * (C / 64)-byte boundaries, geo on 16. */
+ * given, else z[e]. z, zq, h0, h1, A0, A1 start on 16-byte boundaries (8 for C = 64), geo on 16.
+ * Every row of a centre is taken by a half-wave (C / 32 channels per lane). */
 int fmd_mace_message_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
                          const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
                          int32_t channels, const float* h0, const float* h1, float inv_avg, float* A0, float* A1,
                          hipStream_t stream);
-/* VJP of fmd_mace_message_f32 (z, zq and the width W as there): gz [E,W] (may be null when w1ef
- * is given), gzsum [N,W] (may be null: the sum of gz over each centre's rows, in row order), ggeo
- * [E,4] (= or +=), with w1ef ([nb, 4C], the radial rows of the edge GEMM weight; its first W
- * columns enter) also gef[e] = gz[e] @ w1ef[:, :W]^T [E,nb], and if gh0: the sender-side gh0/gh1
- * over the reverse CSR (accumulate_h bit 0: gh0 +=, bit 1: gh1 +=; otherwise =). Alignment as
- * there (gA0, gA1, gz, gzsum, gh0, gh1 like h0; ggeo on 16 bytes). */
+/* VJP of fmd_mace_message_f32 (z, zq and the width W as there): gz [E,W] (may be null), gzsum
+ * [N,W] (may be null: the sum of gz over each centre's rows, in row order), gzsum_src [N,W] (may
+ * be null: the sum of gz over the rows whose sender is the node, over the reverse CSR, without gz
+ * in memory), ggeo [E,4] (= or +=), with w1ef ([nb, 4C], the radial rows of the edge GEMM weight;
+ * its first W columns enter) also gef[e] = gz[e] @ w1ef[:, :W]^T [E,nb], and if gh0: the
+ * sender-side gh0/gh1 over the reverse CSR (accumulate_h bit 0: gh0 +=, bit 1: gh1 +=; otherwise
+ * =). The gather-cat row gradient's node blocks are then gzsum_src @ W1[:C]^T (sender) and
+ * gzsum @ W1[C:2C]^T (receiver), node GEMMs (by linearity the same sums as gz @ W1^T summed per
+ * sender / receiver). Alignment as there (gA0, gA1, gz, gzsum, gzsum_src, gh0, gh1 like h0; ggeo
+ * on 16 bytes). */
 int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
                              const int32_t* reverse,
                              const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
                              int32_t channels, const float* h0, const float* h1, const float* gA0, const float* gA1,
-                             float inv_avg, float* gz, float* gzsum, float* ggeo, int32_t accumulate_geo, float* gh0,
-                             float* gh1, int32_t accumulate_h, const float* w1ef, int32_t nb, float* gef,
-                             hipStream_t stream);
+                             float inv_avg, float* gz, float* gzsum, float* gzsum_src, float* ggeo,
+                             int32_t accumulate_geo, float* gh0, float* gh1, int32_t accumulate_h, const float* w1ef,
+                             int32_t nb, float* gef, hipStream_t stream);
 /* The node side of one interaction layer fused per 32-atom tile (one launch instead of six),
  * fp32-accurate on the bf16 matrix cores: P0 = A0 Wm0, P1_x = A1_x Wm1, the symmetric
  * contraction (B0, B1: workspace, [N,C] and [N,3,C]), h0n = B0 Wo0 + h0 Wsc0, h1n_x = B1_x Wo1

@@ -320,6 +320,33 @@ def test_gemm_gather_against_fp64(device, F):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("b_layout", [0, 1])
+def test_gemm_splitk_against_fp64_and_run_to_run(device, b_layout):
+    """fmd_gemm_splitk_f32: [a | a2] op(b) (+ bias) (+ C) with K in slices summed in slice order:
+    within fp32 of float64 (ragged M and N), and bitwise the same on a second call."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm_splitk
+
+    g = torch.Generator().manual_seed(23)
+    m, k1, k2, n = 10001, 512, 512, 130
+    a, a2 = torch.randn(m, k1, generator=g), torch.randn(m, k2, generator=g)
+    w = torch.randn(k1 + k2, n, generator=g) / (k1 + k2) ** 0.5
+    wb = w if b_layout == 1 else w.t().contiguous()
+    c0 = torch.randn(m, n, generator=g)
+    bias = torch.randn(n, generator=g)
+    ref = torch.cat([a, a2], 1).double() @ w.double() + c0.double() + bias.double()
+    outs = []
+    for _ in range(2):
+        out = c0.to(device)
+        gemm_splitk(a.to(device), wb.to(device), b_layout=b_layout, out=out, a2=a2.to(device), bias=bias.to(device),
+                    accumulate=True)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+    assert oops.relative(outs[0].cpu().numpy(), ref.numpy()) < 1e-5
+
+
+@pytest.mark.gpu
 def test_gemm_planes_bitwise_equal_to_in_kernel_split(device):
     """fmd_split3_f32 gives x = p0 + p1 + p2 exactly (zero padding past the width), and the GEMM on
     pre-split planes (A gathered from plane rows, or fp32 A with pre-split B) is bitwise the GEMM
