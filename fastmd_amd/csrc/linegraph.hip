@@ -1,0 +1,322 @@
+// Three-body line graph of the fixed-capacity builder: undirected pairs of the directed edge rows,
+// the short-bond lists per atom and the triplet rows (fixed_capacity_builder.py:2001-2161, the
+// torch steps of _materialize_pairs / _materialize_line_graph and _line_graph_kernel :680-753).
+// Integer work, bit-exact with the reference's rules on the same rows:
+//   pair leader: a real row e whose reverse row r exists and e <= r; the pair id of e is the
+//     number of leaders up to min(e, r), minus one (d2u); u2d[u] = the leader row of pair u;
+//     padding rows / pairs follow the far self-loop rule (pair u >= real_u is the rows
+//     ec + 2 (u - real_u) and ec + 2 (u - real_u) + 1); invalid_pairs = odd edge count, a leader
+//     count other than half the edges, or a real row without a reverse row
+//   short lists: the rows of atom i with the short-bond flag, in row order, in
+//     short_edge_matrix[i, 0..s_i) (the rest e_cap); pair_offsets = exclusive scan of s (s - 1)
+//   overflow = edges >= e_cap | triplets > t_cap | invalid_pairs | !candidate_valid
+//   triplet row t (< min(triplets, t_cap)): atom a = the last atom with pair_offsets[a] <= t,
+//     local = t - pair_offsets[a], first = local / (s_a - 1), second = local % (s_a - 1) skipping
+//     first; (a, d2u[row1], row1, d2u[row2], row2) with row = short_edge_matrix[a, .]; padding
+//     triplets use padding pair real_u + (t - t_real) % (u_cap - real_u) on atom pair % n;
+//     on overflow every triplet is the all-loop topology (u = t u_cap / t_cap, row 2 u, atom u % n)
+//     and d2u / u2d are the all-loop pairs (e / 2, 2 u).
+// The scans are multi-block (block sums, one workgroup over the blocks, block-local scans):
+// deterministic, no atomics.
+#include "common.h"
+
+namespace {
+
+constexpr int kLgBlock = 1024;
+
+__device__ __forceinline__ int64_t real_rows_of(const int64_t* edge_offsets, int64_t n, int64_t e_cap) {
+  const int64_t t = edge_offsets[n];
+  return t < e_cap ? t : e_cap;
+}
+
+// block-wide inclusive scan of one int64 per thread (1024 threads), through LDS
+__device__ __forceinline__ int64_t block_inclusive_scan(int64_t v, int64_t* sh) {
+  const int t = threadIdx.x;
+  sh[t] = v;
+  __syncthreads();
+  for (int off = 1; off < kLgBlock; off <<= 1) {
+    const int64_t add = t >= off ? sh[t - off] : 0;
+    __syncthreads();
+    sh[t] += add;
+    __syncthreads();
+  }
+  const int64_t r = sh[t];
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ void leader_of(const int32_t* reverse, int64_t e, int64_t ec, bool& leader, bool& unmatched,
+                                          int64_t& canon) {
+  const bool real = e < ec;
+  const int64_t r = real ? (int64_t)reverse[e] : -1;
+  const bool matched = real && r >= 0;
+  leader = matched && e <= r;
+  unmatched = real && !matched;
+  canon = matched && r < e ? r : e;
+}
+
+// K1: per block of rows, the leader and unmatched counts -> work[b], work[nb + b]
+__global__ void __launch_bounds__(kLgBlock) lg_leader_count_kernel(const int32_t* reverse, const int64_t* edge_offsets,
+                                                                    int64_t n, int64_t e_cap, int64_t nb,
+                                                                    int64_t* work) {
+  __shared__ int64_t sh[kLgBlock];
+  const int64_t e = (int64_t)blockIdx.x * kLgBlock + threadIdx.x;
+  const int64_t ec = real_rows_of(edge_offsets, n, e_cap);
+  bool leader, unmatched;
+  int64_t canon;
+  leader_of(reverse, e, ec, leader, unmatched, canon);
+  const int64_t packed = (leader ? 1 : 0) + (unmatched ? (int64_t(1) << 32) : 0);
+  const int64_t tot = block_inclusive_scan(packed, sh);
+  if (threadIdx.x == kLgBlock - 1) {
+    work[blockIdx.x] = tot & 0xffffffffLL;
+    work[nb + blockIdx.x] = tot >> 32;
+  }
+}
+
+// K2: one workgroup: exclusive scan of the block leader counts (in place), the invalid-pairs flag
+__global__ void __launch_bounds__(kLgBlock) lg_leader_scan_kernel(const int64_t* edge_offsets, int64_t n, int64_t nb,
+                                                                   int64_t* work, uint8_t* invalid_pairs) {
+  __shared__ int64_t sh[kLgBlock];
+  __shared__ int64_t chunk;
+  int64_t carry = 0, unmatched = 0;
+  for (int64_t base = 0; base < nb; base += kLgBlock) {
+    const int64_t b = base + threadIdx.x;
+    const int64_t v = b < nb ? work[b] : 0;
+    unmatched += b < nb ? work[nb + b] : 0;
+    const int64_t inc = block_inclusive_scan(v, sh);
+    if (b < nb) work[b] = carry + inc - v;
+    if (threadIdx.x == kLgBlock - 1) chunk = inc;  // the chunk's total
+    __syncthreads();
+    carry += chunk;
+    __syncthreads();
+  }
+  const int64_t um = block_inclusive_scan(unmatched, sh);
+  if (threadIdx.x == kLgBlock - 1) {
+    const int64_t total = edge_offsets[n];
+    work[2 * nb] = carry;  // number of leaders
+    invalid_pairs[0] = (total % 2 != 0) || (carry != total / 2) || (um > 0) ? 1 : 0;
+  }
+}
+
+// K3: per block: the inclusive leader prefix of every row -> pfx[e] (int64)
+__global__ void __launch_bounds__(kLgBlock) lg_leader_apply_kernel(const int32_t* reverse, const int64_t* edge_offsets,
+                                                                    int64_t n, int64_t e_cap, const int64_t* work,
+                                                                    int64_t* pfx) {
+  __shared__ int64_t sh[kLgBlock];
+  const int64_t e = (int64_t)blockIdx.x * kLgBlock + threadIdx.x;
+  const int64_t ec = real_rows_of(edge_offsets, n, e_cap);
+  bool leader, unmatched;
+  int64_t canon;
+  leader_of(reverse, e, ec, leader, unmatched, canon);
+  const int64_t inc = block_inclusive_scan(leader ? 1 : 0, sh);
+  if (e < e_cap) pfx[e] = work[blockIdx.x] + inc;
+}
+
+// K4: one wave per atom: its short rows in row order, their count
+__global__ void __launch_bounds__(256) lg_short_kernel(const uint8_t* short_flags, const int64_t* edge_offsets,
+                                                       int64_t n, int64_t e_cap, int32_t bmax, int64_t* short_counts,
+                                                       int32_t* sem) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  if (i >= n) return;
+  const int64_t ec = real_rows_of(edge_offsets, n, e_cap);
+  int64_t lo = edge_offsets[i], hi = edge_offsets[i + 1];
+  hi = hi < ec ? hi : ec;
+  lo = lo < hi ? lo : hi;
+  int64_t s = 0;
+  int32_t* row = sem + i * bmax;
+  for (int64_t base = lo; base < hi; base += 64) {
+    const int64_t e = base + lane;
+    const bool f = e < hi && short_flags[e] != 0;
+    const uint64_t mask = __ballot(f);
+    const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+    if (f && s + rank < bmax) row[s + rank] = (int32_t)e;
+    s += __popcll(mask);
+  }
+  for (int64_t k = (s < bmax ? s : bmax) + lane; k < bmax; k += 64) row[k] = (int32_t)e_cap;
+  if (lane == 0) short_counts[i] = s;
+}
+
+// K5: one workgroup: exclusive scans of s and s (s - 1) over the atoms, the overflow flag
+__global__ void __launch_bounds__(kLgBlock) lg_pairs_scan_kernel(const int64_t* short_counts, const int64_t* edge_offsets,
+                                                                  const uint8_t* invalid_pairs,
+                                                                  const uint8_t* candidate_valid, int64_t n,
+                                                                  int64_t e_cap, int64_t t_cap, int64_t* short_offsets,
+                                                                  int64_t* pair_offsets, uint8_t* overflow) {
+  __shared__ int64_t sh[kLgBlock];
+  __shared__ int64_t tot[2];
+  int64_t carry_s = 0, carry_p = 0;
+  for (int64_t base = 0; base < n; base += kLgBlock) {
+    const int64_t i = base + threadIdx.x;
+    const int64_t s = i < n ? short_counts[i] : 0;
+    const int64_t p = s * (s - 1);
+    const int64_t inc_s = block_inclusive_scan(s, sh);
+    if (threadIdx.x == kLgBlock - 1) tot[0] = inc_s;
+    const int64_t inc_p = block_inclusive_scan(p, sh);
+    if (threadIdx.x == kLgBlock - 1) tot[1] = inc_p;
+    __syncthreads();
+    if (i < n) {
+      short_offsets[i] = carry_s + inc_s - s;
+      pair_offsets[i] = carry_p + inc_p - p;
+    }
+    carry_s += tot[0];
+    carry_p += tot[1];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    short_offsets[n] = carry_s;
+    pair_offsets[n] = carry_p;
+    const int64_t total = edge_offsets[n];
+    overflow[0] = (total >= e_cap) || (carry_p > t_cap) || invalid_pairs[0] || !candidate_valid[0] ? 1 : 0;
+  }
+}
+
+// K6: d2u per row and u2d per pair (written by the pair's leader row, padding pairs by index)
+__global__ void lg_pairs_index_kernel(const int32_t* reverse, const int64_t* edge_offsets, const int64_t* pfx,
+                                      const uint8_t* overflow, int64_t n, int64_t e_cap, int64_t u_cap, int32_t* d2u,
+                                      int32_t* u2d) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const bool ovf = overflow[0] != 0;
+  const int64_t ec = real_rows_of(edge_offsets, n, e_cap);
+  const int64_t real_u = ec / 2;
+  if (k < e_cap) {
+    const int64_t e = k;
+    bool leader, unmatched;
+    int64_t canon;
+    leader_of(reverse, e, ec, leader, unmatched, canon);
+    int64_t u;
+    if (ovf) {
+      u = e / 2;
+    } else if (e < ec) {
+      u = pfx[canon] - 1;
+    } else {
+      u = real_u + (e - ec) / 2;
+    }
+    u = u < 0 ? 0 : (u > u_cap - 1 ? u_cap - 1 : u);
+    d2u[e] = (int32_t)u;
+    if (!ovf && leader) {
+      const int64_t id = pfx[e] - 1;
+      if (id >= 0 && id < u_cap) u2d[id] = (int32_t)(e < e_cap - 1 ? e : e_cap - 1);
+    }
+  }
+  if (k < u_cap) {
+    int64_t v = -1;
+    if (ovf)
+      v = 2 * k;
+    else if (k >= real_u)
+      v = ec + 2 * (k - real_u);
+    if (v >= 0) u2d[k] = (int32_t)(v < e_cap - 1 ? v : e_cap - 1);
+  }
+}
+
+// K7: the triplet rows
+__global__ void lg_line_graph_kernel(const int64_t* pair_offsets, const int64_t* short_counts, const int32_t* sem,
+                                     const int32_t* d2u, const int64_t* edge_offsets, const uint8_t* overflow,
+                                     int64_t n, int64_t e_cap, int64_t u_cap, int64_t t_cap, int32_t bmax,
+                                     int32_t* line_graph) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= t_cap) return;
+  int32_t* out = line_graph + t * 5;
+  if (overflow[0]) {
+    int64_t u = t * u_cap / t_cap;
+    u = u < u_cap - 1 ? u : u_cap - 1;
+    const int32_t atom = (int32_t)(u % n);
+    out[0] = atom;
+    out[1] = (int32_t)u;
+    out[2] = (int32_t)(2 * u);
+    out[3] = (int32_t)u;
+    out[4] = (int32_t)(2 * u);
+    return;
+  }
+  const int64_t total_t = pair_offsets[n];
+  const int64_t t_real = total_t < t_cap ? total_t : t_cap;
+  const int64_t ec = real_rows_of(edge_offsets, n, e_cap);
+  if (t < t_real) {
+    // the last atom with pair_offsets[atom] <= t
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi + 1) / 2;
+      if (pair_offsets[mid] <= t)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const int64_t atom = lo < n - 1 ? lo : n - 1;
+    const int64_t local = t - pair_offsets[atom];
+    int64_t denom = short_counts[atom] - 1;
+    denom = denom > 1 ? denom : 1;
+    const int64_t first = local / denom;
+    const int64_t second_raw = local - first * denom;
+    const int64_t second = second_raw + (second_raw >= first ? 1 : 0);
+    const int64_t de1 = sem[atom * bmax + (first < bmax - 1 ? first : bmax - 1)];
+    const int64_t de2 = sem[atom * bmax + (second < bmax - 1 ? second : bmax - 1)];
+    const int64_t c1 = de1 < 0 ? 0 : (de1 > e_cap - 1 ? e_cap - 1 : de1);
+    const int64_t c2 = de2 < 0 ? 0 : (de2 > e_cap - 1 ? e_cap - 1 : de2);
+    out[0] = (int32_t)atom;
+    out[1] = d2u[c1];
+    out[2] = (int32_t)de1;
+    out[3] = d2u[c2];
+    out[4] = (int32_t)de2;
+  } else {
+    const int64_t real_u = ec / 2;
+    const int64_t pad_id = t - t_real;
+    const int64_t free_u = u_cap - real_u > 1 ? u_cap - real_u : 1;
+    const int64_t pad_pair = pad_id % free_u;
+    const int32_t pu = (int32_t)(real_u + pad_pair), pde = (int32_t)(ec + 2 * pad_pair);
+    out[0] = (int32_t)(pad_pair % n);
+    out[1] = pu;
+    out[2] = pde;
+    out[3] = pu;
+    out[4] = pde;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t fmd_nl_line_graph_work_size(int64_t n_atoms, int64_t e_cap) {
+  const int64_t nb = fmd_cdiv(e_cap, kLgBlock);
+  return 2 * nb + 8 + e_cap;
+}
+
+int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const uint8_t* short_flags,
+                      const int64_t* edge_offsets, const uint8_t* candidate_valid, int64_t n_atoms, int64_t e_cap,
+                      int64_t u_cap, int64_t t_cap, int32_t bmax, int64_t* work, int32_t* d2u, int32_t* u2d,
+                      uint8_t* invalid_pairs, int64_t* short_counts, int64_t* short_offsets,
+                      int32_t* short_edge_matrix, int64_t* pair_offsets, uint8_t* overflow, int32_t* line_graph,
+                      hipStream_t stream) {
+  FMD_REQUIRE(n_atoms > 0 && e_cap > 0 && u_cap > 0 && t_cap > 0 && bmax > 0 && e_cap == 2 * u_cap);
+  FMD_REQUIRE(e_cap < (int64_t(1) << 31) && t_cap < (int64_t(1) << 31) && n_atoms < (int64_t(1) << 31));
+  FMD_REQUIRE(edge_reverse && short_flags && edge_offsets && candidate_valid && work && d2u && u2d && invalid_pairs);
+  FMD_REQUIRE(short_counts && short_offsets && short_edge_matrix && pair_offsets && overflow && line_graph);
+  (void)center;
+  const int64_t nb = fmd_cdiv(e_cap, kLgBlock);
+  int64_t* pfx = work + 2 * nb + 8;
+  hipLaunchKernelGGL(lg_leader_count_kernel, dim3((unsigned)nb), dim3(kLgBlock), 0, stream, edge_reverse, edge_offsets,
+                     n_atoms, e_cap, nb, work);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(lg_leader_scan_kernel, dim3(1), dim3(kLgBlock), 0, stream, edge_offsets, n_atoms, nb, work,
+                     invalid_pairs);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(lg_leader_apply_kernel, dim3((unsigned)nb), dim3(kLgBlock), 0, stream, edge_reverse, edge_offsets,
+                     n_atoms, e_cap, work, pfx);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(lg_short_kernel, dim3((unsigned)fmd_cdiv(n_atoms, 4)), dim3(256), 0, stream, short_flags,
+                     edge_offsets, n_atoms, e_cap, bmax, short_counts, short_edge_matrix);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(lg_pairs_scan_kernel, dim3(1), dim3(kLgBlock), 0, stream, short_counts, edge_offsets,
+                     invalid_pairs, candidate_valid, n_atoms, e_cap, t_cap, short_offsets, pair_offsets, overflow);
+  FMD_CHECK_LAUNCH();
+  const int64_t idx = e_cap > u_cap ? e_cap : u_cap;
+  hipLaunchKernelGGL(lg_pairs_index_kernel, dim3((unsigned)fmd_cdiv(idx, 256)), dim3(256), 0, stream, edge_reverse,
+                     edge_offsets, pfx, overflow, n_atoms, e_cap, u_cap, d2u, u2d);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(lg_line_graph_kernel, dim3((unsigned)fmd_cdiv(t_cap, 256)), dim3(256), 0, stream, pair_offsets,
+                     short_counts, short_edge_matrix, d2u, edge_offsets, overflow, n_atoms, e_cap, u_cap, t_cap, bmax,
+                     line_graph);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+}  // extern "C"

@@ -319,16 +319,21 @@ struct BuildArgs {
   uint8_t* cand_valid;
   uint8_t* overflow;
   int32_t* isolated;
+  float line2;           // line-graph (bond) cutoff squared, float32
+  uint8_t* short_flags;  // [e_cap]: real row with d2 < line2 (null: not written)
 };
 
+// d2: the row's squared distance (the edge decision's own value: the short-bond decision uses the
+// same bits, fixed_capacity_builder.py:258-260)
 __device__ __forceinline__ void write_row(const BuildArgs& a, int64_t row, int32_t c, int32_t j, int ix, int iy,
-                                          int iz, float dist, bool real) {
+                                          int iz, float d2, bool real) {
   a.center[row] = c;
   a.neighbor[row] = j;
   a.images[3 * row] = ix;
   a.images[3 * row + 1] = iy;
   a.images[3 * row + 2] = iz;
-  if (real) a.distances[row] = dist;
+  if (real) a.distances[row] = sqrtf(d2);
+  if (a.short_flags) a.short_flags[row] = real && d2 < a.line2 ? 1 : 0;
   if (a.edge_index) {
     a.edge_index[2 * row] = c;
     a.edge_index[2 * row + 1] = j;
@@ -491,7 +496,7 @@ __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs
       if (s < cnt) e = slot_edge(a, cm, i, s, xi, yi, zi, wdi, nbr_state, j, img, d2);
       const uint64_t m = __ballot(e);
       const int64_t row = row0 + lane_prefix(m);
-      if (e && row < a.e_cap) write_row(a, row, (int32_t)i, j, img[0], img[1], img[2], sqrtf(d2), true);
+      if (e && row < a.e_cap) write_row(a, row, (int32_t)i, j, img[0], img[1], img[2], d2, true);
       row0 += __popcll(m);
     }
   }
@@ -670,7 +675,7 @@ __global__ void __launch_bounds__(kBlock) nl_materialize_kernel(BuildArgs a, int
     if (s < cnt) e = slot_edge(a, cm, i, s, wr[0], wr[1], wr[2], wdi, nbr_state, j, img, d2);
     const uint64_t m = __ballot(e);
     const int64_t row = row0 + lane_prefix(m);
-    if (e && row < a.e_cap) write_row(a, row, (int32_t)i, j, img[0], img[1], img[2], sqrtf(d2), true);
+    if (e && row < a.e_cap) write_row(a, row, (int32_t)i, j, img[0], img[1], img[2], d2, true);
     row0 += __popcll(m);
   }
 }
@@ -801,7 +806,8 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  int32_t pad_iz, int64_t e_cap, int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
                  int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor, int32_t* images,
                  float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
-                 uint8_t* candidate_valid, uint8_t* overflow, int32_t* isolated, hipStream_t stream) {
+                 uint8_t* candidate_valid, uint8_t* overflow, int32_t* isolated, float line2, uint8_t* short_flags,
+                 hipStream_t stream) {
   FMD_REQUIRE(n_atoms > 0 && n_atoms < (int64_t(1) << 31) && e_cap > 0 && bmax > 0);
   FMD_REQUIRE(positions && inv_cell && cell && neighbor_matrix && neighbor_shifts && num_neighbors);
   FMD_REQUIRE(reference_positions && reference_wraps && capacity_valid && work && frac && wrap_delta);
@@ -810,7 +816,7 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
               reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, pad_ix, pad_iy, pad_iz, e_cap,
               work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
-              edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated};
+              edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags};
   if (n_atoms <= kSmallMaxAtoms && n_atoms <= 1024) {
     hipLaunchKernelGGL(nl_build_small_kernel, dim3(1), dim3(kSmallThreads), 0, stream, a);
     FMD_CHECK_LAUNCH();

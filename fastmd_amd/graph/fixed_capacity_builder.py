@@ -86,12 +86,14 @@ def _batch_itself(batch: GraphBatch) -> GraphBatch:
 
 
 class FixedCapacityGraphBuilder:
-    """Single-system, edges-only fixed-capacity builder (see the module docstring).
+    """Single-system fixed-capacity builder (see the module docstring): edges only, or with the
+    three-body line graph when ``line_graph_cutoff`` and ``t_capacity`` are given (undirected
+    pairs, short-bond lists and triplet rows, fmd_nl_line_graph, published as
+    ``batch.pair_d2u`` / ``pair_u2d`` / ``triplets``).
 
-    Unsupported reference options (line graph, ghost rows, sink padding, shared candidates,
-    minimum-image wraps, float64 published positions) raise ``NotImplementedError``.
-    ``sorted_edges=False`` is accepted: the rows are always in the canonical order, which is
-    also grouped by centre."""
+    Unsupported reference options (ghost rows, sink padding, shared candidates, minimum-image
+    wraps, float64 published positions) raise ``NotImplementedError``. ``sorted_edges=False`` is
+    accepted: the rows are always in the canonical order, which is also grouped by centre."""
 
     def __init__(self, *, cell: Tensor, atomic_numbers: Tensor, u_capacity: int, t_capacity: int = 0,
                  pbc: Tensor | None = None, atom_graph_cutoff: float = 6.0, line_graph_cutoff: float | None = None,
@@ -101,8 +103,11 @@ class FixedCapacityGraphBuilder:
                  prepare: Callable[[GraphBatch], Any] | None = None, positions_dtype: torch.dtype = torch.float32,
                  sorted_edges: bool = True, max_neighbor_count: Tensor | None = None,
                  publish_positions: bool = False) -> None:
-        if line_graph_cutoff is not None or t_capacity != 0:
-            raise NotImplementedError("line graphs (three-body topologies) are not built by this builder")
+        line_graph = line_graph_cutoff is not None
+        if line_graph and (t_capacity <= 0 or not 0.0 < float(line_graph_cutoff) <= float(atom_graph_cutoff)):
+            raise ValueError("a line-graph builder needs t_capacity > 0 and 0 < line_graph_cutoff <= the atom cutoff")
+        if not line_graph and t_capacity != 0:
+            raise ValueError("t_capacity needs a line_graph_cutoff")
         if ghosts is not None or candidates_from is not None or minimum_image:
             raise NotImplementedError("ghost rows, shared candidates and minimum-image wraps are not supported")
         if positions_dtype != torch.float32:
@@ -118,7 +123,7 @@ class FixedCapacityGraphBuilder:
         _abi.load()
         if pbc is not None and not bool(torch.as_tensor(pbc).all()):
             raise NotImplementedError("non-periodic axes are not supported")
-        self.edges_only = True
+        self.edges_only = not line_graph
         self.padding = padding
         self.sorted_edges = True
         self.max_neighbor_count = max_neighbor_count
@@ -131,11 +136,13 @@ class FixedCapacityGraphBuilder:
         self.n_dummy = 0
         self.u_capacity = int(u_capacity)
         if self.u_capacity <= 0:
-            raise ValueError("an edges-only builder needs u_capacity > 0 and t_capacity == 0")
+            raise ValueError("a builder needs u_capacity > 0")
         self.e_capacity = 2 * self.u_capacity
-        self.t_capacity = 0
+        self.t_capacity = int(t_capacity) if line_graph else 0
         self.atom_graph_cutoff = float(atom_graph_cutoff)
-        self.line_graph_cutoff = None
+        self.line_graph_cutoff = float(line_graph_cutoff) if line_graph else None
+        # the short-bond decision d2 < float32(cutoff^2), on the edge decision's own d2
+        self._line2 = float(np.float32(self.line_graph_cutoff * self.line_graph_cutoff)) if line_graph else 0.0
         self.candidate_cutoff = float(candidate_cutoff or (self.atom_graph_cutoff + 1.0e-6))
         if self.candidate_cutoff < self.atom_graph_cutoff:
             raise ValueError("candidate_cutoff must not be below the pair cutoff")
@@ -182,6 +189,18 @@ class FixedCapacityGraphBuilder:
         self._overflow = torch.zeros(1, **u8)
         self._isolated_atom_count = torch.zeros(1, **i32)
         self._invalid_pairs = torch.zeros(1, dtype=torch.bool, device=dev)
+        self.short_flags = self.directed2undirected = self.undirected2directed = self.line_graph = None
+        self.short_counts = self.short_offsets = self.short_edge_matrix = None
+        if line_graph:
+            self.short_flags = torch.zeros(e, **u8)
+            self.directed2undirected = torch.zeros(e, **i32)
+            self.undirected2directed = torch.zeros(self.u_capacity, **i32)
+            self.short_counts = torch.zeros(n, **i64)
+            self.short_offsets = torch.zeros(n + 1, **i64)
+            self.short_edge_matrix = torch.zeros((n, self.buffer_max), **i32)
+            self.pair_offsets = torch.zeros(n + 1, **i64)
+            self.line_graph = torch.zeros((self.t_capacity, 5), **i32)
+            self._lg_work = torch.zeros(int(_abi.load().fmd_nl_line_graph_work_size(n, e)), **i64)
         self.positions = torch.zeros((n, 3), **f32)
         self.batch = GraphBatch(
             positions=self.positions,
@@ -197,6 +216,10 @@ class FixedCapacityGraphBuilder:
             composition=self.composition,
             edge_offsets=self.edge_offsets,
             edge_reverse=self.edge_reverse,
+            triplet_cutoff=self.line_graph_cutoff,
+            pair_d2u=self.directed2undirected,
+            pair_u2d=self.undirected2directed,
+            triplets=self.line_graph,
         )
         self.graph = (prepare or _batch_itself)(self.batch)
 
@@ -262,10 +285,21 @@ class FixedCapacityGraphBuilder:
                   self.neighbor.data_ptr(), self.images.data_ptr(), self.distances.data_ptr(),
                   self.batch.edge_index.data_ptr(), self.batch.edge_image.data_ptr(),
                   self._max_displacement.data_ptr(), self._candidate_valid.data_ptr(), self._overflow.data_ptr(),
-                  self._isolated_atom_count.data_ptr(), self._stream())
+                  self._isolated_atom_count.data_ptr(), self._line2, _abi.ptr(self.short_flags), self._stream())
         _abi.call("fmd_nl_reverse", self.center.data_ptr(), self.neighbor.data_ptr(), self.images.data_ptr(),
                   self.edge_offsets.data_ptr(), self.n_real, self.e_capacity, self.edge_reverse.data_ptr(),
                   self._stream())
+        if not self.edges_only:
+            # pairs, short-bond lists and triplets; the overflow flag becomes the line-graph rule
+            # (edges >= e_capacity | triplets > t_capacity | invalid pairs | invalid candidates)
+            _abi.call("fmd_nl_line_graph", self.center.data_ptr(), self.edge_reverse.data_ptr(),
+                      self.short_flags.data_ptr(), self.edge_offsets.data_ptr(), self._candidate_valid.data_ptr(),
+                      self.n_real, self.e_capacity, self.u_capacity, self.t_capacity, self.buffer_max,
+                      self._lg_work.data_ptr(), self.directed2undirected.data_ptr(),
+                      self.undirected2directed.data_ptr(), self._invalid_pairs.data_ptr(),
+                      self.short_counts.data_ptr(), self.short_offsets.data_ptr(),
+                      self.short_edge_matrix.data_ptr(), self.pair_offsets.data_ptr(), self._overflow.data_ptr(),
+                      self.line_graph.data_ptr(), self._stream())
         if self.max_neighbor_count is not None:
             torch.maximum(self.max_neighbor_count, self.edge_counts.max().reshape(1), out=self.max_neighbor_count)
         return self.graph, self.status

@@ -87,7 +87,9 @@ int fmd_nl_wrap(const void* positions, int32_t pos_is_f64, const float* inv_cell
  * positions, may be null), edge_counts [n] i64, edge_offsets [n+1] i64, center/neighbor
  * [e_cap] i32, images [e_cap,3] i32, distances [e_cap] f32, edge_index [e_cap,2] i32 and
  * edge_image [e_cap,3] f32 (published, may be null), status: max_displacement f32[1],
- * candidate_valid u8[1], overflow u8[1], isolated i32[1]. */
+ * candidate_valid u8[1], overflow u8[1], isolated i32[1]; short_flags [e_cap] u8 (may be null:
+ * a line-graph build's short-bond flag, real rows with the same d2 < line2, line2 the float32
+ * square of the bond cutoff, fixed_capacity_builder.py:258-260; padding rows 0). */
 int64_t fmd_nl_build_work_size(int64_t n_atoms);
 int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cell, const float* cell,
                  int64_t n_atoms, const int32_t* neighbor_matrix, const int32_t* neighbor_shifts,
@@ -98,7 +100,25 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor,
                  int32_t* images, float* distances, int32_t* edge_index, float* edge_image,
                  float* max_displacement, uint8_t* candidate_valid, uint8_t* overflow,
-                 int32_t* isolated, hipStream_t stream);
+                 int32_t* isolated, float line2, uint8_t* short_flags, hipStream_t stream);
+
+/* The three-body line graph over a build's rows (FixedCapacityGraphBuilder._materialize_pairs
+ * / _materialize_line_graph / _line_graph_kernel, fixed_capacity_builder.py:2001-2161,680-753),
+ * far self-loop padding: directed2undirected d2u [e_cap] i32 and undirected2directed u2d
+ * [u_cap] i32 (e_cap = 2 u_cap), invalid_pairs u8[1], short_counts [n] i64, short_offsets and
+ * pair_offsets [n+1] i64 (exclusive scans of s and s (s - 1)), short_edge_matrix [n, bmax] i32
+ * (an atom's short rows in row order, then e_cap), overflow u8[1] (set to edges >= e_cap |
+ * triplets > t_cap | invalid_pairs | !candidate_valid), line_graph [t_cap, 5] i32 rows
+ * (atom, u1, row1, u2, row2), the all-loop topology on overflow. Inputs: edge_reverse from
+ * fmd_nl_reverse, short_flags from fmd_nl_build, work of fmd_nl_line_graph_work_size int64.
+ * center is unused (kept for the reference's argument order). */
+int64_t fmd_nl_line_graph_work_size(int64_t n_atoms, int64_t e_cap);
+int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const uint8_t* short_flags,
+                      const int64_t* edge_offsets, const uint8_t* candidate_valid, int64_t n_atoms, int64_t e_cap,
+                      int64_t u_cap, int64_t t_cap, int32_t bmax, int64_t* work, int32_t* d2u, int32_t* u2d,
+                      uint8_t* invalid_pairs, int64_t* short_counts, int64_t* short_offsets,
+                      int32_t* short_edge_matrix, int64_t* pair_offsets, uint8_t* overflow, int32_t* line_graph,
+                      hipStream_t stream);
 
 /* Reverse edge of every real row e < min(E, e_cap): the row of (neighbour, centre, -image),
  * or -1 when it is not stored (overflowed build). Gives the sender-side CSR of the sorted

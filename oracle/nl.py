@@ -10,6 +10,11 @@ Restates, in NumPy float32 with the operation order of ``fastmd_amd/csrc/nl.hip`
     (:1814-1815), far self-loop padding (_pad_self_loops_kernel :323-366, self_loop_padding
     :1004-1027), the canonical sort (_sort_edges :1968-1999) and the overflow flag
   * fixed_capacity_exceeded (:796-814) and the window flag fold (:430-455)
+  * the three-body line graph: the short-bond flags of the materialization (:258-260), the
+    undirected pairs of _materialize_pairs (:2001-2084), the short lists, pair offsets and
+    overflow rule of _materialize_line_graph (:2086-2161) and the triplet rows of
+    _line_graph_kernel (:680-753), far self-loop padding (LOOP_PADDING), with the all-loop
+    overflow topology of _allocate_overflow_topology (:1474-1513)
   * estimate_max_neighbors (fastmd/graph/neighbor_list_backend.py:77-88) and the ragged
     builder's slot growth rule (fastmd/graph/gpu_graph_builder.py:74-85)
 and an FP64 brute-force pair set (tests/test_fixed_capacity_boundary.py:86-102) that pins it.
@@ -172,6 +177,7 @@ class Build:
     candidate_valid: bool
     overflow: bool
     isolated: int
+    short: np.ndarray | None = None  # bool [e_cap]: real rows with d2 < line2 (line-graph builds)
 
     @property
     def n_edges(self) -> int:
@@ -179,8 +185,9 @@ class Build:
 
 
 def build(positions, inv_cell, cell, cand: Candidates, reference_positions, reference_wraps, rc2, skin_limit,
-          pad_image, e_cap: int) -> Build:
-    """One edges-only build over the candidate list (see module docstring)."""
+          pad_image, e_cap: int, line2: float | None = None) -> Build:
+    """One build over the candidate list (see module docstring); with ``line2`` (the float32
+    square of the bond cutoff) also the short-bond flag of every row."""
     pos = np.asarray(positions).astype(F32)
     n = pos.shape[0]
     frac, wraps, wrapped = wrap(pos, inv_cell, cell)
@@ -219,8 +226,89 @@ def build(positions, inv_cell, cell, cand: Candidates, reference_positions, refe
     center[ec:] = atoms
     neighbor[ec:] = atoms
     images[ec:] = np.asarray(pad_image, dtype=np.int32)
+    short = None
+    if line2 is not None:
+        short = np.zeros(e_cap, bool)
+        short[:ec] = d2[:ec] < F32(line2)
     return Build(frac, wd, wrapped, counts, offsets, center, neighbor, images, distances, max_disp, valid,
-                 bool(total > e_cap or not valid), int((counts == 0).sum()))
+                 bool(total > e_cap or not valid), int((counts == 0).sum()), short)
+
+
+def line_graph(b: Build, rev, n: int, e_cap: int, u_cap: int, t_cap: int, bmax: int) -> dict:
+    """The line graph of a build (module docstring): d2u, u2d, invalid_pairs, short_counts,
+    short_offsets, short_edge_matrix, pair_offsets, overflow and the triplet rows."""
+    total = b.n_edges
+    ec = min(total, e_cap)
+    ids = np.arange(e_cap, dtype=np.int64)
+    rev = np.asarray(rev, dtype=np.int64)
+    real = ids < ec
+    matched = real & (rev >= 0)
+    leader = matched & (ids <= rev)
+    canon = np.where(matched & (rev < ids), rev, ids)
+    prefix = np.cumsum(leader.astype(np.int64))
+    real_u = ec // 2
+    d2u = np.where(real, prefix[canon] - 1, real_u + np.maximum(ids - ec, 0) // 2)
+    d2u = np.clip(d2u, 0, u_cap - 1)
+    u2d = np.full(u_cap, e_cap - 1, np.int64)
+    lead_ids = (prefix - 1)[leader]
+    ok = (lead_ids >= 0) & (lead_ids < u_cap)
+    u2d[lead_ids[ok]] = np.minimum(ids[leader][ok], e_cap - 1)
+    u = np.arange(u_cap)
+    u2d = np.where(u >= real_u, np.minimum(ec + 2 * (u - real_u), e_cap - 1), u2d)
+    invalid = bool(total % 2 != 0 or int(leader.sum()) != total // 2 or bool((real & ~matched).any()))
+    short = b.short & real
+    s = np.bincount(b.center[short], minlength=n).astype(np.int64)
+    short_offsets = np.concatenate([[0], np.cumsum(s)]).astype(np.int64)
+    sem = np.full((n, bmax), e_cap, np.int64)
+    rows = np.nonzero(short)[0]
+    for i in range(n):
+        mine = rows[b.center[rows] == i][:bmax]
+        sem[i, :len(mine)] = mine
+    pair_offsets = np.concatenate([[0], np.cumsum(s * (s - 1))]).astype(np.int64)
+    overflow = bool(total >= e_cap or pair_offsets[-1] > t_cap or invalid or not b.candidate_valid)
+    lg = np.zeros((t_cap, 5), np.int64)
+    t_ids = np.arange(t_cap, dtype=np.int64)
+    if overflow:
+        lu = np.minimum(t_ids * u_cap // t_cap, u_cap - 1)
+        lg[:] = np.stack([lu % n, lu, 2 * lu, lu, 2 * lu], 1)
+        d2u = ids // 2
+        u2d = 2 * u
+    else:
+        t_real = min(int(pair_offsets[-1]), t_cap)
+        tr = t_ids[:t_real]
+        atom = np.searchsorted(pair_offsets, tr, side="right") - 1
+        atom = np.minimum(atom, n - 1)
+        local = tr - pair_offsets[atom]
+        denom = np.maximum(s[atom] - 1, 1)
+        first = local // denom
+        second_raw = local - first * denom
+        second = second_raw + (second_raw >= first)
+        de1 = sem[atom, np.minimum(first, bmax - 1)]
+        de2 = sem[atom, np.minimum(second, bmax - 1)]
+        lg[:t_real] = np.stack([atom, d2u[np.clip(de1, 0, e_cap - 1)], de1, d2u[np.clip(de2, 0, e_cap - 1)], de2], 1)
+        pad_id = t_ids[t_real:] - t_real
+        pad_pair = pad_id % max(u_cap - real_u, 1)
+        pu, pde = real_u + pad_pair, ec + 2 * pad_pair
+        lg[t_real:] = np.stack([pad_pair % n, pu, pde, pu, pde], 1)
+    return {"d2u": d2u.astype(np.int32), "u2d": u2d.astype(np.int32), "invalid_pairs": invalid,
+            "short_counts": s, "short_offsets": short_offsets, "short_edge_matrix": sem.astype(np.int32),
+            "pair_offsets": pair_offsets, "overflow": overflow, "line_graph": lg.astype(np.int32)}
+
+
+def triplet_set(center, neighbor, images, short, n_edges: int) -> set:
+    """Brute force: every ordered pair of two distinct short bonds at a common centre, as
+    (centre, (neighbour, image) of the first, (neighbour, image) of the second)."""
+    by_atom: dict = {}
+    for e in range(n_edges):
+        if short[e]:
+            by_atom.setdefault(int(center[e]), []).append((int(neighbor[e]), *map(int, images[e])))
+    out = set()
+    for a, bonds in by_atom.items():
+        for x in bonds:
+            for y in bonds:
+                if x != y:
+                    out.add((a, x, y))
+    return out
 
 
 def canonical_order_ok(center, neighbor, images, n_atoms: int, max_image: int = 10) -> bool:

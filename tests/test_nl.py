@@ -309,3 +309,147 @@ def test_ragged_builder_growth_is_bitwise_identical(device, max_neighbors):
     assert int(g.n_edges.item()) == e == ei.shape[0]
     assert np.array_equal(ei[:, 0], ob.center[:e]) and np.array_equal(ei[:, 1], ob.neighbor[:e])
     assert np.array_equal(g.edge_image.cpu().numpy(), ob.images[:e].astype(F32))
+
+
+# ------------------------------------------------------------------ line graph (three-body)
+def _oracle_line(cell, positions, cutoff, skin, u_cap, t_cap, line_cutoff, inv=None):
+    cell32 = cell.astype(F32)
+    inv = _inv32(cell) if inv is None else inv
+    _, wraps, wrapped = onl.wrap(positions, inv, cell32)
+    bmax = onl.estimate_max_neighbors(cutoff + skin, safety_factor=2.0)
+    cand = onl.candidates(wrapped, cell32, F32((cutoff + skin) ** 2), bmax)
+    pad, _ = onl.self_loop_image(cell, cutoff)
+    b = onl.build(positions, inv, cell32, cand, np.asarray(positions, dtype=F32), wraps, F32(cutoff * cutoff),
+                  F32(skin + 1e-6), pad, 2 * u_cap, line2=F32(line_cutoff * line_cutoff))
+    rev = onl.reverse(b.center, b.neighbor, b.images, b.edge_offsets, 2 * u_cap)
+    lg = onl.line_graph(b, rev, positions.shape[0], 2 * u_cap, u_cap, t_cap, bmax)
+    return cand, b, rev, lg, wrapped
+
+
+def _edge_key(b, e):
+    return (int(b.neighbor[e]), *map(int, b.images[e]))
+
+
+@pytest.mark.parametrize("line_cutoff", [3.0, 3.5])
+def test_oracle_line_graph_pinned(line_cutoff):
+    """The oracle's pairs and triplets against independent formulations: the short-bond flags
+    against FP64 distances (away from the cutoff), the triplet rows against the brute-force set
+    of ordered bond pairs per centre, and the pair ids against their invariants (a row and its
+    reverse share a pair, u2d is the lower row, leaders numbered in row order), plus the padding
+    rule and the reference's capacity-boundary answers (tests/test_fixed_capacity_boundary.py:
+    155-237): edges > or == e_capacity overflow, one padding pair leaves no overflow and takes
+    every padding triplet."""
+    s = systems.perovskite(3)
+    cutoff, skin = 6.0, 2.0
+    _, b0, _, _, wrapped = _oracle_line(s.cell, s.positions, cutoff, skin, 4096, 65536, line_cutoff)
+    edges = b0.n_edges
+    real_u = edges // 2
+    d64 = np.linalg.norm(wrapped.astype(np.float64)[b0.neighbor[:edges]] + b0.images[:edges].astype(np.float64)
+                         @ s.cell.astype(F32).astype(np.float64) - wrapped.astype(np.float64)[b0.center[:edges]], axis=1)
+    far = np.abs(d64 - line_cutoff) > 1e-4
+    assert np.array_equal(b0.short[:edges][far], (d64 < line_cutoff)[far])
+    triplets = int(sum(int(c) * (int(c) - 1) for c in np.bincount(b0.center[:edges][b0.short[:edges]], minlength=135)))
+    assert triplets > 0
+    t_cap = triplets + 32
+    for u_cap, expect in ((real_u - 1, True), (real_u, True), (real_u + 1, False)):
+        _, b, rev, lg, _ = _oracle_line(s.cell, s.positions, cutoff, skin, u_cap, t_cap, line_cutoff)
+        assert lg["overflow"] == expect
+        line = lg["line_graph"].astype(np.int64)
+        assert line[:, [1, 3]].max() < u_cap and line[:, [2, 4]].max() < 2 * u_cap and line.min() >= 0
+        assert lg["d2u"].max() < u_cap and lg["u2d"].max() < 2 * u_cap
+        if expect:
+            lu = np.minimum(np.arange(t_cap) * u_cap // t_cap, u_cap - 1)
+            assert np.array_equal(line[:, 1], lu) and np.array_equal(line[:, 2], 2 * lu)
+            continue
+        assert int(lg["pair_offsets"][-1]) == triplets and not lg["invalid_pairs"]
+        # every padding triplet uses the single padding pair
+        assert (line[triplets:, [1, 3]] == real_u).all() and (line[triplets:, [2, 4]] == edges).all()
+        got = {(int(r[0]), _edge_key(b, r[2]), _edge_key(b, r[4])) for r in line[:triplets]}
+        assert len(got) == triplets
+        assert got == onl.triplet_set(b.center, b.neighbor, b.images, b.short, edges)
+        assert all(b.center[r[2]] == r[0] and b.center[r[4]] == r[0] for r in line[:triplets])
+        d2u, u2d = lg["d2u"].astype(np.int64), lg["u2d"].astype(np.int64)
+        rows = np.arange(edges)
+        assert np.array_equal(d2u[rows], d2u[rev[rows]])
+        assert np.array_equal(u2d[d2u[rows]], np.minimum(rows, rev[rows]))
+        leaders = rows[rows <= rev[rows]]
+        assert np.array_equal(d2u[leaders], np.arange(real_u))
+        pad_rows = np.arange(edges, 2 * u_cap)
+        assert np.array_equal(d2u[pad_rows], np.minimum(real_u + (pad_rows - edges) // 2, u_cap - 1))
+        assert np.array_equal(line[:triplets, 1], d2u[line[:triplets, 2]])
+    # triplets above t_capacity overflow too
+    _, _, _, lg, _ = _oracle_line(s.cell, s.positions, cutoff, skin, real_u + 64, triplets - 1, line_cutoff)
+    assert lg["overflow"]
+
+
+def _gpu_line_builder(cell, n, cutoff, skin, u_cap, t_cap, line_cutoff, device):
+    import torch
+
+    from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
+
+    return FixedCapacityGraphBuilder(cell=torch.tensor(cell, dtype=torch.float32), atomic_numbers=torch.ones(n),
+                                     u_capacity=u_cap, t_capacity=t_cap, atom_graph_cutoff=cutoff,
+                                     line_graph_cutoff=line_cutoff, candidate_cutoff=cutoff + skin, device=device)
+
+
+def _assert_line_equal(builder, b, lg):
+    assert np.array_equal(builder.short_flags.cpu().numpy().astype(bool), b.short)
+    for name, buf in (("d2u", builder.directed2undirected), ("u2d", builder.undirected2directed),
+                      ("short_counts", builder.short_counts), ("short_offsets", builder.short_offsets),
+                      ("short_edge_matrix", builder.short_edge_matrix), ("pair_offsets", builder.pair_offsets),
+                      ("line_graph", builder.line_graph)):
+        assert np.array_equal(buf.cpu().numpy(), lg[name]), name
+    assert bool(builder._invalid_pairs.item()) == lg["invalid_pairs"]
+    assert bool(builder._overflow.item()) == lg["overflow"]
+    assert builder.batch.triplets is builder.line_graph and builder.batch.pair_d2u is builder.directed2undirected
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n_atoms,line_cutoff", [(135, 3.5), (1080, 3.0), (5000, 3.0), (5000, 3.5)])
+def test_line_graph_builder_bit_exact(device, n_atoms, line_cutoff):
+    """The HIP line graph (short-bond flags, undirected pairs, short lists, pair offsets, triplet
+    rows, flags) bit-exact vs the oracle on the fused (<= 1 024 atoms) and multi-block builds."""
+    import torch
+
+    print(f"[line graph] n_atoms={n_atoms} cutoff={line_cutoff}", flush=True)
+    s = systems.perovskite_atoms(n_atoms)
+    cutoff, skin = 6.0, 2.0
+    u_cap = int(round(15.3 * n_atoms / 2)) + 64
+    t_cap = 40 * n_atoms
+    builder = _gpu_line_builder(s.cell, n_atoms, cutoff, skin, u_cap, t_cap, line_cutoff, device)
+    builder.build(torch.tensor(s.positions, dtype=torch.float64, device=device))
+    inv = builder.inv_cell.cpu().numpy()
+    cand, b, rev, lg, _ = _oracle_line(s.cell, s.positions, cutoff, skin, u_cap, t_cap, line_cutoff, inv=inv)
+    torch.cuda.synchronize()
+    assert np.array_equal(builder.center.cpu().numpy(), b.center)
+    assert np.array_equal(builder.edge_reverse.cpu().numpy(), rev)
+    _assert_line_equal(builder, b, lg)
+    assert not lg["overflow"] and int(lg["pair_offsets"][-1]) > 0
+
+
+@pytest.mark.gpu
+def test_line_graph_builder_capacity_boundary(device):
+    """The reference's boundary cases on the GPU (tests/test_fixed_capacity_boundary.py:155-237):
+    edges > e_capacity and == e_capacity overflow (all-loop topology), one padding pair does not,
+    triplets > t_capacity overflow; every index in range; bit-exact vs the oracle throughout."""
+    import torch
+
+    s = systems.perovskite(3)
+    cutoff, skin, lc = 6.0, 2.0, 3.5
+    _, b0, _, _, _ = _oracle_line(s.cell, s.positions, cutoff, skin, 4096, 65536, lc)
+    real_u = b0.n_edges // 2
+    triplets = int(sum(int(c) * (int(c) - 1) for c in np.bincount(b0.center[:b0.n_edges][b0.short[:b0.n_edges]],
+                                                                  minlength=135)))
+    for u_cap, t_cap, expect in ((real_u - 1, triplets + 32, True), (real_u, triplets + 32, True),
+                                 (real_u + 1, triplets + 32, False), (real_u + 8, triplets - 1, True)):
+        print(f"[line graph boundary] u_cap={u_cap} t_cap={t_cap}", flush=True)
+        builder = _gpu_line_builder(s.cell, 135, cutoff, skin, u_cap, t_cap, lc, device)
+        builder.build(torch.tensor(s.positions, device=device))
+        inv = builder.inv_cell.cpu().numpy()
+        _, b, rev, lg, _ = _oracle_line(s.cell, s.positions, cutoff, skin, u_cap, t_cap, lc, inv=inv)
+        torch.cuda.synchronize()
+        _assert_line_equal(builder, b, lg)
+        assert lg["overflow"] == expect
+        line = builder.line_graph.long()
+        assert int(line[:, [1, 3]].max()) < u_cap and int(line[:, [2, 4]].max()) < 2 * u_cap
+        assert int(line.min()) >= 0 and int(line[:, 0].max()) < 135
