@@ -115,7 +115,7 @@ __global__ void __launch_bounds__(kLgBlock) lg_leader_apply_kernel(const int32_t
 // K4: one wave per atom: its short rows in row order, their count
 __global__ void __launch_bounds__(256) lg_short_kernel(const uint8_t* short_flags, const int64_t* edge_offsets,
                                                        int64_t n, int64_t e_cap, int32_t bmax, int64_t* short_counts,
-                                                       int32_t* sem) {
+                                                       int32_t* sem, int32_t* short_rank) {
   const int lane = threadIdx.x & 63;
   const int64_t i = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   if (i >= n) return;
@@ -131,6 +131,7 @@ __global__ void __launch_bounds__(256) lg_short_kernel(const uint8_t* short_flag
     const uint64_t mask = __ballot(f);
     const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
     if (f && s + rank < bmax) row[s + rank] = (int32_t)e;
+    if (e < hi) short_rank[e] = (int32_t)(s + rank);  // short rows of the atom before e
     s += __popcll(mask);
   }
   for (int64_t k = (s < bmax ? s : bmax) + lane; k < bmax; k += 64) row[k] = (int32_t)e_cap;
@@ -209,6 +210,36 @@ __global__ void lg_pairs_index_kernel(const int32_t* reverse, const int64_t* edg
   }
 }
 
+// K8: the angle -> bond CSR over the directed rows (row e's triplets as first bond:
+// [off[e], off[e + 1]) = pair_offsets[i] + rank_e (s_i - 1) + [0, s_i - 1) for a short row, empty
+// otherwise; padding rows empty at the end; clamped to t_cap) and the compact short-bond rows
+// (bond_rows[short_offsets[i] + rank_e] = e, the rest -1)
+__global__ void lg_edge_offsets_kernel(const int32_t* center, const uint8_t* short_flags, const int32_t* short_rank,
+                                       const int64_t* short_counts, const int64_t* short_offsets,
+                                       const int64_t* pair_offsets, const int64_t* edge_offsets, int64_t n,
+                                       int64_t e_cap, int64_t t_cap, int64_t* edge_tri_off, int32_t* bond_rows) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e > e_cap) return;
+  const int64_t ec = real_rows_of(edge_offsets, n, e_cap);
+  int64_t o;
+  if (e < ec) {
+    const int64_t i = center[e];
+    const int64_t sc = short_counts[i];
+    o = pair_offsets[i] + (int64_t)short_rank[e] * (sc > 0 ? sc - 1 : 0);
+  } else {
+    o = pair_offsets[n];
+  }
+  edge_tri_off[e] = o < t_cap ? o : t_cap;
+  if (e < e_cap) {
+    const int64_t nshort = short_offsets[n];
+    if (e < ec && short_flags[e]) {
+      const int64_t b = short_offsets[center[e]] + short_rank[e];
+      if (b < e_cap) bond_rows[b] = (int32_t)e;
+    }
+    if (e >= nshort) bond_rows[e] = -1;
+  }
+}
+
 // K7: the triplet rows
 __global__ void lg_line_graph_kernel(const int64_t* pair_offsets, const int64_t* short_counts, const int32_t* sem,
                                      const int32_t* d2u, const int64_t* edge_offsets, const uint8_t* overflow,
@@ -277,7 +308,7 @@ extern "C" {
 
 int64_t fmd_nl_line_graph_work_size(int64_t n_atoms, int64_t e_cap) {
   const int64_t nb = fmd_cdiv(e_cap, kLgBlock);
-  return 2 * nb + 8 + e_cap;
+  return 2 * nb + 8 + e_cap + fmd_cdiv(e_cap, 2);  // block sums, leader prefix, short ranks (int32)
 }
 
 int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const uint8_t* short_flags,
@@ -285,14 +316,15 @@ int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const 
                       int64_t u_cap, int64_t t_cap, int32_t bmax, int64_t* work, int32_t* d2u, int32_t* u2d,
                       uint8_t* invalid_pairs, int64_t* short_counts, int64_t* short_offsets,
                       int32_t* short_edge_matrix, int64_t* pair_offsets, uint8_t* overflow, int32_t* line_graph,
-                      hipStream_t stream) {
+                      int64_t* edge_triplet_offsets, int32_t* bond_rows, hipStream_t stream) {
   FMD_REQUIRE(n_atoms > 0 && e_cap > 0 && u_cap > 0 && t_cap > 0 && bmax > 0 && e_cap == 2 * u_cap);
   FMD_REQUIRE(e_cap < (int64_t(1) << 31) && t_cap < (int64_t(1) << 31) && n_atoms < (int64_t(1) << 31));
   FMD_REQUIRE(edge_reverse && short_flags && edge_offsets && candidate_valid && work && d2u && u2d && invalid_pairs);
   FMD_REQUIRE(short_counts && short_offsets && short_edge_matrix && pair_offsets && overflow && line_graph);
-  (void)center;
+  FMD_REQUIRE(center && edge_triplet_offsets && bond_rows);
   const int64_t nb = fmd_cdiv(e_cap, kLgBlock);
   int64_t* pfx = work + 2 * nb + 8;
+  int32_t* short_rank = reinterpret_cast<int32_t*>(pfx + e_cap);
   hipLaunchKernelGGL(lg_leader_count_kernel, dim3((unsigned)nb), dim3(kLgBlock), 0, stream, edge_reverse, edge_offsets,
                      n_atoms, e_cap, nb, work);
   FMD_CHECK_LAUNCH();
@@ -303,7 +335,7 @@ int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const 
                      n_atoms, e_cap, work, pfx);
   FMD_CHECK_LAUNCH();
   hipLaunchKernelGGL(lg_short_kernel, dim3((unsigned)fmd_cdiv(n_atoms, 4)), dim3(256), 0, stream, short_flags,
-                     edge_offsets, n_atoms, e_cap, bmax, short_counts, short_edge_matrix);
+                     edge_offsets, n_atoms, e_cap, bmax, short_counts, short_edge_matrix, short_rank);
   FMD_CHECK_LAUNCH();
   hipLaunchKernelGGL(lg_pairs_scan_kernel, dim3(1), dim3(kLgBlock), 0, stream, short_counts, edge_offsets,
                      invalid_pairs, candidate_valid, n_atoms, e_cap, t_cap, short_offsets, pair_offsets, overflow);
@@ -311,6 +343,10 @@ int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const 
   const int64_t idx = e_cap > u_cap ? e_cap : u_cap;
   hipLaunchKernelGGL(lg_pairs_index_kernel, dim3((unsigned)fmd_cdiv(idx, 256)), dim3(256), 0, stream, edge_reverse,
                      edge_offsets, pfx, overflow, n_atoms, e_cap, u_cap, d2u, u2d);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(lg_edge_offsets_kernel, dim3((unsigned)fmd_cdiv(e_cap + 1, 256)), dim3(256), 0, stream, center,
+                     short_flags, short_rank, short_counts, short_offsets, pair_offsets, edge_offsets, n_atoms, e_cap,
+                     t_cap, edge_triplet_offsets, bond_rows);
   FMD_CHECK_LAUNCH();
   hipLaunchKernelGGL(lg_line_graph_kernel, dim3((unsigned)fmd_cdiv(t_cap, 256)), dim3(256), 0, stream, pair_offsets,
                      short_counts, short_edge_matrix, d2u, edge_offsets, overflow, n_atoms, e_cap, u_cap, t_cap, bmax,

@@ -111,14 +111,44 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
  * triplets > t_cap | invalid_pairs | !candidate_valid), line_graph [t_cap, 5] i32 rows
  * (atom, u1, row1, u2, row2), the all-loop topology on overflow. Inputs: edge_reverse from
  * fmd_nl_reverse, short_flags from fmd_nl_build, work of fmd_nl_line_graph_work_size int64.
- * center is unused (kept for the reference's argument order). */
+ * Also the segment layouts of the angle -> bond -> atom sums: edge_triplet_offsets [e_cap + 1]
+ * i64, a CSR over the directed rows whose run for row e holds the triplets with e as their first
+ * bond (empty for other rows; clamped to t_cap), and bond_rows [e_cap] i32, the short rows in
+ * (atom, rank) order (then -1), the rows of the CSR short_offsets over the atoms. */
 int64_t fmd_nl_line_graph_work_size(int64_t n_atoms, int64_t e_cap);
 int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const uint8_t* short_flags,
                       const int64_t* edge_offsets, const uint8_t* candidate_valid, int64_t n_atoms, int64_t e_cap,
                       int64_t u_cap, int64_t t_cap, int32_t bmax, int64_t* work, int32_t* d2u, int32_t* u2d,
                       uint8_t* invalid_pairs, int64_t* short_counts, int64_t* short_offsets,
                       int32_t* short_edge_matrix, int64_t* pair_offsets, uint8_t* overflow, int32_t* line_graph,
-                      hipStream_t stream);
+                      int64_t* edge_triplet_offsets, int32_t* bond_rows, hipStream_t stream);
+
+/* The three-body Fourier angle basis (threebody_fourier_basis, triton_threebody_fourier.py:45-80,
+ * :230-260): out[t] = [1/sqrt(2), sin(theta f_k), cos(theta f_k)] / scale (1 + 2 n_freq columns),
+ * theta = acos((u[target[t]] . u[source[t]]) (1 - 1e-6)), u rows of stride ld_unit. */
+int fmd_threebody_fourier_f32(const float* unit_vec, int64_t ld_unit, const int32_t* target_index,
+                              const int32_t* source_index, int64_t rows, const float* freqs, int32_t n_freq,
+                              float scale, float* out, hipStream_t stream);
+/* Its per-row VJP terms: contrib[t] = (g to u[target[t]], g to u[source[t]]) [rows, 6]; the caller
+ * sums them per vector row in a fixed order (the reference's atomics, :121-127, are not used). */
+int fmd_threebody_fourier_bwd_rows_f32(const float* gout, const float* unit_vec, int64_t ld_unit,
+                                       const int32_t* target_index, const int32_t* source_index, int64_t rows,
+                                       const float* freqs, int32_t n_freq, float scale, float* contrib,
+                                       hipStream_t stream);
+/* The basis over a line graph of fmd_nl_line_graph (target = first bond, source = second bond of
+ * each triplet row; padding rows from line_graph) and its VJP over the real triplets,
+ * deterministic: one wave per atom forms its bonds' gradients (grad_unit rows of the short bonds,
+ * = or += with accumulate) from its triplets in triplet order. overflow (nullable) is the build's
+ * flag: set, every row is read from line_graph and the VJP is zero. */
+int fmd_threebody_fourier_line_f32(const float* unit_vec, int64_t ld_unit, const int64_t* pair_offsets,
+                                   const int64_t* short_counts, const int32_t* short_edge_matrix, int32_t bmax,
+                                   const int32_t* line_graph, const uint8_t* overflow, int64_t n_atoms, int64_t t_cap,
+                                   const float* freqs, int32_t n_freq, float scale, float* out, hipStream_t stream);
+int fmd_threebody_fourier_line_bwd_f32(const float* gout, const float* unit_vec, int64_t ld_unit,
+                                       const int64_t* pair_offsets, const int64_t* short_counts,
+                                       const int32_t* short_edge_matrix, int32_t bmax, const uint8_t* overflow,
+                                       int64_t n_atoms, int64_t t_cap, const float* freqs, int32_t n_freq, float scale,
+                                       float* grad_unit, int64_t ld_grad, int32_t accumulate, hipStream_t stream);
 
 /* Reverse edge of every real row e < min(E, e_cap): the row of (neighbour, centre, -image),
  * or -1 when it is not stored (overflowed build). Gives the sender-side CSR of the sorted

@@ -290,9 +290,21 @@ def line_graph(b: Build, rev, n: int, e_cap: int, u_cap: int, t_cap: int, bmax: 
         pad_pair = pad_id % max(u_cap - real_u, 1)
         pu, pde = real_u + pad_pair, ec + 2 * pad_pair
         lg[t_real:] = np.stack([pad_pair % n, pu, pde, pu, pde], 1)
+    # segment layouts of the angle -> bond -> atom sums: row e (short, rank r among its atom's short
+    # rows) is the first bond of triplets pair_offsets[i] + r (s_i - 1) + [0, s_i - 1)
+    before = np.concatenate([[0], np.cumsum(short.astype(np.int64))])[:e_cap]  # short rows before e
+    centre = np.asarray(b.center[:e_cap], np.int64) if len(b.center) else np.zeros(0, np.int64)
+    centre = np.concatenate([centre, np.zeros(e_cap - len(centre), np.int64)])
+    rank = before - short_offsets[np.clip(centre, 0, n - 1)]
+    eto = np.full(e_cap + 1, pair_offsets[-1], np.int64)
+    eto[:ec] = pair_offsets[centre[:ec]] + rank[:ec] * np.maximum(s[centre[:ec]] - 1, 0)
+    eto = np.minimum(eto, t_cap)
+    bond_rows = np.full(e_cap, -1, np.int64)
+    bond_rows[:len(rows)] = rows  # rows are in (atom, rank) order: the builder's rows are sorted by atom
     return {"d2u": d2u.astype(np.int32), "u2d": u2d.astype(np.int32), "invalid_pairs": invalid,
             "short_counts": s, "short_offsets": short_offsets, "short_edge_matrix": sem.astype(np.int32),
-            "pair_offsets": pair_offsets, "overflow": overflow, "line_graph": lg.astype(np.int32)}
+            "pair_offsets": pair_offsets, "overflow": overflow, "line_graph": lg.astype(np.int32),
+            "edge_triplet_offsets": eto, "bond_rows": bond_rows.astype(np.int32)}
 
 
 def triplet_set(center, neighbor, images, short, n_edges: int) -> set:

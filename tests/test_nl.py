@@ -377,6 +377,15 @@ def test_oracle_line_graph_pinned(line_cutoff):
         pad_rows = np.arange(edges, 2 * u_cap)
         assert np.array_equal(d2u[pad_rows], np.minimum(real_u + (pad_rows - edges) // 2, u_cap - 1))
         assert np.array_equal(line[:triplets, 1], d2u[line[:triplets, 2]])
+        # the angle -> bond CSR: row e's run holds exactly the triplets whose first bond is e
+        eto = lg["edge_triplet_offsets"]
+        assert eto[0] == 0 and (np.diff(eto) >= 0).all() and eto[-1] == triplets
+        first = np.repeat(np.arange(len(eto) - 1), np.diff(eto))
+        assert np.array_equal(first, line[:triplets, 2])
+        # the bond -> atom CSR: short_offsets over bond_rows lists each atom's short rows
+        br, so = lg["bond_rows"].astype(np.int64), lg["short_offsets"]
+        assert np.array_equal(br[:so[-1]], np.nonzero(b.short[:edges])[0]) and (br[so[-1]:] == -1).all()
+        assert np.array_equal(b.center[br[:so[-1]]], np.repeat(np.arange(135), np.diff(so)))
     # triplets above t_capacity overflow too
     _, _, _, lg, _ = _oracle_line(s.cell, s.positions, cutoff, skin, real_u + 64, triplets - 1, line_cutoff)
     assert lg["overflow"]
@@ -397,7 +406,8 @@ def _assert_line_equal(builder, b, lg):
     for name, buf in (("d2u", builder.directed2undirected), ("u2d", builder.undirected2directed),
                       ("short_counts", builder.short_counts), ("short_offsets", builder.short_offsets),
                       ("short_edge_matrix", builder.short_edge_matrix), ("pair_offsets", builder.pair_offsets),
-                      ("line_graph", builder.line_graph)):
+                      ("line_graph", builder.line_graph), ("edge_triplet_offsets", builder.edge_triplet_offsets),
+                      ("bond_rows", builder.bond_rows)):
         assert np.array_equal(buf.cpu().numpy(), lg[name]), name
     assert bool(builder._invalid_pairs.item()) == lg["invalid_pairs"]
     assert bool(builder._overflow.item()) == lg["overflow"]
