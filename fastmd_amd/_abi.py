@@ -33,13 +33,21 @@ SIGNATURES: dict[str, tuple] = {
                                     _p, _p, _p, _p, _p, _f32, _p, _p]),
     "fmd_nl_line_graph_work_size": (_i64, [_i64, _i64]),
     "fmd_nl_line_graph": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _p,
-                                         _p, _p, _p, _p, _p, _p, _p, _p]),
+                                         _p, _p, _p, _p, _p, _p, _p, _p, _p]),
     "fmd_threebody_fourier_f32": (ctypes.c_int, [_p, _i64, _p, _p, _i64, _p, _i32, _f32, _p, _p]),
     "fmd_threebody_fourier_bwd_rows_f32": (ctypes.c_int, [_p, _p, _i64, _p, _p, _i64, _p, _i32, _f32, _p, _p]),
     "fmd_threebody_fourier_line_f32": (ctypes.c_int, [_p, _i64, _p, _p, _p, _i32, _p, _p, _i64, _i64, _p, _i32, _f32,
                                                       _p, _p]),
     "fmd_threebody_fourier_line_bwd_f32": (ctypes.c_int, [_p, _p, _i64, _p, _p, _p, _i32, _p, _i64, _i64, _p, _i32,
                                                           _f32, _p, _i64, _i32, _p]),
+    "fmd_tb_bond_envelope_f32": (ctypes.c_int, [_p, _p, _p, _i64, _f32, _p]),
+    "fmd_tb_gated_sum_f32": (ctypes.c_int, [_p, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _p, _i64, _f32, _p, _i64,
+                                            _i32, _p]),
+    "fmd_tb_gated_sum_bwd_f32": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _p, _i64,
+                                                _f32, _p, _i64, _p, _i64, _p, _i64, _i32, _p]),
+    "fmd_tb_readout_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _i64, _p, _p]),
+    "fmd_tb_readout_bwd_f32": (ctypes.c_int, [_p, _f32, _p, _i32, _i64, _p, _i64, _p]),
+    "fmd_tb_geometry_bwd_f32": (ctypes.c_int, [_p, _p, _i32, _p, _i64, _p, _i64, _p, _p, _p, _i64, _p, _p]),
     "fmd_nl_reverse": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i64, _p, _p]),
     "fmd_nl_window_flags": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p]),
     "fmd_gather_cat_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _i64, _p, _i64, _p]),

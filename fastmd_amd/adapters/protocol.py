@@ -94,6 +94,7 @@ class GraphBatch:
     systems: Any = None
     edge_offsets: Tensor | None = None
     edge_reverse: Tensor | None = None
+    line: Any = None  # the line graph's arrays (fastmd_amd.ops.threebody.LineGraph) when built
 
     @property
     def edge_dst(self) -> Tensor:

@@ -244,10 +244,14 @@ __global__ void lg_edge_offsets_kernel(const int32_t* center, const uint8_t* sho
 __global__ void lg_line_graph_kernel(const int64_t* pair_offsets, const int64_t* short_counts, const int32_t* sem,
                                      const int32_t* d2u, const int64_t* edge_offsets, const uint8_t* overflow,
                                      int64_t n, int64_t e_cap, int64_t u_cap, int64_t t_cap, int32_t bmax,
-                                     int32_t* line_graph) {
+                                     int32_t* line_graph, int32_t* second_perm) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= t_cap) return;
   int32_t* out = line_graph + t * 5;
+  // the second-bond CSR: its entries past the real triplets (and all of an overflowed build's) are
+  // -1; a real triplet's own entry is written below
+  const int64_t total_all = pair_offsets[n];
+  if (overflow[0] || t >= (total_all < t_cap ? total_all : t_cap)) second_perm[t] = -1;
   if (overflow[0]) {
     int64_t u = t * u_cap / t_cap;
     u = u < u_cap - 1 ? u : u_cap - 1;
@@ -288,6 +292,9 @@ __global__ void lg_line_graph_kernel(const int64_t* pair_offsets, const int64_t*
     out[2] = (int32_t)de1;
     out[3] = d2u[c2];
     out[4] = (int32_t)de2;
+    // triplets with bond (atom, second) as their second bond, by first bond: slot first (or
+    // first - 1 past the bond itself) of that bond's run pair_offsets + second (s - 1)
+    second_perm[pair_offsets[atom] + second * denom + (first < second ? first : first - 1)] = (int32_t)t;
   } else {
     const int64_t real_u = ec / 2;
     const int64_t pad_id = t - t_real;
@@ -316,12 +323,12 @@ int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const 
                       int64_t u_cap, int64_t t_cap, int32_t bmax, int64_t* work, int32_t* d2u, int32_t* u2d,
                       uint8_t* invalid_pairs, int64_t* short_counts, int64_t* short_offsets,
                       int32_t* short_edge_matrix, int64_t* pair_offsets, uint8_t* overflow, int32_t* line_graph,
-                      int64_t* edge_triplet_offsets, int32_t* bond_rows, hipStream_t stream) {
+                      int64_t* edge_triplet_offsets, int32_t* bond_rows, int32_t* second_perm, hipStream_t stream) {
   FMD_REQUIRE(n_atoms > 0 && e_cap > 0 && u_cap > 0 && t_cap > 0 && bmax > 0 && e_cap == 2 * u_cap);
   FMD_REQUIRE(e_cap < (int64_t(1) << 31) && t_cap < (int64_t(1) << 31) && n_atoms < (int64_t(1) << 31));
   FMD_REQUIRE(edge_reverse && short_flags && edge_offsets && candidate_valid && work && d2u && u2d && invalid_pairs);
   FMD_REQUIRE(short_counts && short_offsets && short_edge_matrix && pair_offsets && overflow && line_graph);
-  FMD_REQUIRE(center && edge_triplet_offsets && bond_rows);
+  FMD_REQUIRE(center && edge_triplet_offsets && bond_rows && second_perm);
   const int64_t nb = fmd_cdiv(e_cap, kLgBlock);
   int64_t* pfx = work + 2 * nb + 8;
   int32_t* short_rank = reinterpret_cast<int32_t*>(pfx + e_cap);
@@ -350,7 +357,7 @@ int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const 
   FMD_CHECK_LAUNCH();
   hipLaunchKernelGGL(lg_line_graph_kernel, dim3((unsigned)fmd_cdiv(t_cap, 256)), dim3(256), 0, stream, pair_offsets,
                      short_counts, short_edge_matrix, d2u, edge_offsets, overflow, n_atoms, e_cap, u_cap, t_cap, bmax,
-                     line_graph);
+                     line_graph, second_perm);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

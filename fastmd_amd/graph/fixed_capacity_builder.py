@@ -191,7 +191,7 @@ class FixedCapacityGraphBuilder:
         self._invalid_pairs = torch.zeros(1, dtype=torch.bool, device=dev)
         self.short_flags = self.directed2undirected = self.undirected2directed = self.line_graph = None
         self.short_counts = self.short_offsets = self.short_edge_matrix = None
-        self.edge_triplet_offsets = self.bond_rows = None
+        self.edge_triplet_offsets = self.bond_rows = self.second_perm = None
         if line_graph:
             self.short_flags = torch.zeros(e, **u8)
             self.directed2undirected = torch.zeros(e, **i32)
@@ -203,6 +203,8 @@ class FixedCapacityGraphBuilder:
             self.line_graph = torch.zeros((self.t_capacity, 5), **i32)
             self.edge_triplet_offsets = torch.zeros(e + 1, **i64)  # angle -> bond CSR over the rows
             self.bond_rows = torch.full((e,), -1, **i32)  # short rows in (atom, rank) order
+            # with edge_triplet_offsets: the triplets of each row as their second bond
+            self.second_perm = torch.full((self.t_capacity,), -1, **i32)
             self._lg_work = torch.zeros(int(_abi.load().fmd_nl_line_graph_work_size(n, e)), **i64)
         self.positions = torch.zeros((n, 3), **f32)
         self.batch = GraphBatch(
@@ -223,8 +225,16 @@ class FixedCapacityGraphBuilder:
             pair_d2u=self.directed2undirected,
             pair_u2d=self.undirected2directed,
             triplets=self.line_graph,
+            line=self._line_layout(),
         )
         self.graph = (prepare or _batch_itself)(self.batch)
+
+    def _line_layout(self):
+        if self.line_graph is None:
+            return None
+        from fastmd_amd.ops.threebody import LineGraph
+
+        return LineGraph.from_builder(self)
 
     # ------------------------------------------------------------------ candidates
     def _stream(self) -> int:
@@ -303,7 +313,7 @@ class FixedCapacityGraphBuilder:
                       self.short_counts.data_ptr(), self.short_offsets.data_ptr(),
                       self.short_edge_matrix.data_ptr(), self.pair_offsets.data_ptr(), self._overflow.data_ptr(),
                       self.line_graph.data_ptr(), self.edge_triplet_offsets.data_ptr(), self.bond_rows.data_ptr(),
-                      self._stream())
+                      self.second_perm.data_ptr(), self._stream())
         if self.max_neighbor_count is not None:
             torch.maximum(self.max_neighbor_count, self.edge_counts.max().reshape(1), out=self.max_neighbor_count)
         return self.graph, self.status

@@ -132,6 +132,12 @@ class LineGraph:
     line_graph: Tensor  # int32 [t_cap, 5]
     e_cap: int
     overflow: Tensor | None = None  # uint8 [1]: the build's overflow flag (all rows padding when set)
+    # the segment layouts of the angle -> bond -> atom sums (fmd_nl_line_graph); None when not needed
+    short_flags: Tensor | None = None  # uint8 [e_cap]
+    short_offsets: Tensor | None = None  # int64 [n_atoms + 1]: CSR of the atoms over bond_rows
+    edge_triplet_offsets: Tensor | None = None  # int64 [e_cap + 1]: triplets of each row as first bond
+    bond_rows: Tensor | None = None  # int32 [e_cap]: short rows in (atom, rank) order, then -1
+    second_perm: Tensor | None = None  # int32 [t_cap]: with edge_triplet_offsets, as second bond
 
     @property
     def n_atoms(self) -> int:
@@ -150,7 +156,8 @@ class LineGraph:
         if builder.line_graph is None:
             raise ValueError("the builder has no line graph (line_graph_cutoff and t_capacity > 0)")
         return cls(builder.pair_offsets, builder.short_counts, builder.short_edge_matrix, builder.line_graph,
-                   builder.e_capacity, builder._overflow)
+                   builder.e_capacity, builder._overflow, builder.short_flags, builder.short_offsets,
+                   builder.edge_triplet_offsets, builder.bond_rows, builder.second_perm)
 
     def check(self, n_vec: int) -> None:
         if self.pair_offsets.dtype != torch.int64 or self.short_counts.dtype != torch.int64:

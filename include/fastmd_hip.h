@@ -113,15 +113,17 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
  * fmd_nl_reverse, short_flags from fmd_nl_build, work of fmd_nl_line_graph_work_size int64.
  * Also the segment layouts of the angle -> bond -> atom sums: edge_triplet_offsets [e_cap + 1]
  * i64, a CSR over the directed rows whose run for row e holds the triplets with e as their first
- * bond (empty for other rows; clamped to t_cap), and bond_rows [e_cap] i32, the short rows in
- * (atom, rank) order (then -1), the rows of the CSR short_offsets over the atoms. */
+ * bond (empty for other rows; clamped to t_cap), bond_rows [e_cap] i32, the short rows in
+ * (atom, rank) order (then -1), the rows of the CSR short_offsets over the atoms, and second_perm
+ * [t_cap] i32, the permutation that with edge_triplet_offsets lists for row e the triplets with e
+ * as their second bond, by first bond (-1 past the real triplets and throughout an overflowed build). */
 int64_t fmd_nl_line_graph_work_size(int64_t n_atoms, int64_t e_cap);
 int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const uint8_t* short_flags,
                       const int64_t* edge_offsets, const uint8_t* candidate_valid, int64_t n_atoms, int64_t e_cap,
                       int64_t u_cap, int64_t t_cap, int32_t bmax, int64_t* work, int32_t* d2u, int32_t* u2d,
                       uint8_t* invalid_pairs, int64_t* short_counts, int64_t* short_offsets,
                       int32_t* short_edge_matrix, int64_t* pair_offsets, uint8_t* overflow, int32_t* line_graph,
-                      int64_t* edge_triplet_offsets, int32_t* bond_rows, hipStream_t stream);
+                      int64_t* edge_triplet_offsets, int32_t* bond_rows, int32_t* second_perm, hipStream_t stream);
 
 /* The three-body Fourier angle basis (threebody_fourier_basis, triton_threebody_fourier.py:45-80,
  * :230-260): out[t] = [1/sqrt(2), sin(theta f_k), cos(theta f_k)] / scale (1 + 2 n_freq columns),
@@ -149,6 +151,45 @@ int fmd_threebody_fourier_line_bwd_f32(const float* gout, const float* unit_vec,
                                        const int32_t* short_edge_matrix, int32_t bmax, const uint8_t* overflow,
                                        int64_t n_atoms, int64_t t_cap, const float* freqs, int32_t n_freq, float scale,
                                        float* grad_unit, int64_t ld_grad, int32_t accumulate, hipStream_t stream);
+
+/* ---- three-body (CHGNet/MatRIS-style) model kernels. The reference runs CHGNet (upstream
+ * chgnet, fastmd/models/chgnet.py:1-60) and MatRIS (fastmd/models/matris/interaction_block.py)
+ * through their own modules; these are the pieces of this package's configs[4] model: the bond
+ * envelope of the line graph, the gated segment sums of its angle -> bond and edge -> atom updates
+ * (the reference's triplet gather + segment sums, fastmd/models/matris/op/
+ * triton_weighted_segment_sum.py, triton_csr_segment_sum.py:433-479), the readout and the
+ * geometry VJP. */
+
+/* geo [e_cap, 8] rows (u, r, fc, dfc, s, ds) of fmd_edge_geometry_f32: writes s, ds, the polynomial
+ * envelope 1 - 21x^5 + 35x^6 - 15x^7 (x = r / rb) of each real short row and its r-derivative (0
+ * elsewhere). */
+int fmd_tb_bond_envelope_f32(float* geo, const uint8_t* short_flags, const int64_t* n_edges, int64_t e_cap, float rb,
+                             hipStream_t stream);
+/* out[s] (+)= scale * sum_{r in [offsets[s], offsets[s+1]) and r < rows} silu(z[r]) * w(r),
+ * w(r) = w[r], w[index1[r]] or w[index1[r]] * w[index2[r]] (index rows of stride ld_index, w of
+ * stride ldw); one wave per segment, rows in order. channels <= 256. */
+int fmd_tb_gated_sum_f32(const float* z, int64_t ldz, int64_t rows, int32_t channels, const float* w, int64_t ldw,
+                         const int32_t* index1, const int32_t* index2, int64_t ld_index, const int64_t* offsets,
+                         int64_t n_segments, float scale, float* out, int64_t ldo, int32_t accumulate,
+                         hipStream_t stream);
+/* Its VJP: gz[r] = scale gout[s] w(r) silu'(z[r]) for every row (0 past the last run); gsum[s] =
+ * sum_r gz[r] (nullable); gw[r] (nullable) = sum_c scale gout[s] silu(z[r]), as (gw w2, gw w1) for
+ * the two-index weight, stored or (accumulate_gw) added. */
+int fmd_tb_gated_sum_bwd_f32(const float* gout, int64_t ldg, const float* z, int64_t ldz, int64_t rows,
+                             int32_t channels, const float* w, int64_t ldw, const int32_t* index1,
+                             const int32_t* index2, int64_t ld_index, const int64_t* offsets, int64_t n_segments,
+                             float scale, float* gz, int64_t ldgz, float* gsum, int64_t ldgs, float* gw, int64_t ldgw,
+                             int32_t accumulate_gw, hipStream_t stream);
+/* energy[i] = e0[elem[i]] + h[i] . wr, and its VJP gh[i] = (gE ? gE[i] : sign) * wr. */
+int fmd_tb_readout_f32(const float* h, int64_t ldh, int32_t channels, const float* wr, const int32_t* elem,
+                       const float* e0, int64_t n, float* energy, hipStream_t stream);
+int fmd_tb_readout_bwd_f32(const float* gE, float sign, const float* wr, int32_t channels, int64_t n, float* gh,
+                           int64_t ldgh, hipStream_t stream);
+/* gvec [e_cap, 3] = gr u + (gu - (gu . u) u) / r per real row (0 on padding), gr = sum_n gef def +
+ * gfc dfc + gs ds (each term nullable). */
+int fmd_tb_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, const float* gef, int64_t ldgef,
+                            const float* gu, int64_t ldgu, const float* gfc, const float* gs, const int64_t* n_edges,
+                            int64_t e_cap, float* gvec, hipStream_t stream);
 
 /* Reverse edge of every real row e < min(E, e_cap): the row of (neighbour, centre, -image),
  * or -1 when it is not stored (overflowed build). Gives the sender-side CSR of the sorted

@@ -10,6 +10,10 @@ CPU op forms: ``index_select`` gathers, ``index_add_`` receiver sums
   the cutoff, E_i = 1/2 sum_j V(r_ij).
 * ``mace_like_node_energy``: the MACE-like model specified in fastmd_amd/models/mace_like.py
   (its parameters are passed in as a dict of tensors; the oracle does not import the product).
+* ``threebody_like_node_energy``: the three-body model of fastmd_amd/models/threebody_like.py, its
+  triplets formed here by brute force (every ordered pair of distinct bonds at a centre) and its
+  angle basis by torch's own acos / sin / cos (parity of the model's data path and kernels; the
+  model itself is this package's, the reference's CHGNet / MatRIS weights being unavailable).
 Edges are the real rows (centre, neighbour, image) of a neighbour list; vec = pos[neighbour] +
 image @ cell - pos[centre].
 """
@@ -90,6 +94,65 @@ def mace_like_node_energy(params: dict, config: dict, positions, cell, elem, cen
     y = h0 @ p["Wr2a"]
     e = h_first @ p["wr1"] + torch.nn.functional.silu(y) @ p["wr2b"]
     return p["e0"].index_select(0, elem) + config["scale"] * e + config["shift"]
+
+
+def poly_cutoff(r: Tensor, rc: float) -> Tensor:
+    x = r / rc
+    f = 1 - 21 * x ** 5 + 35 * x ** 6 - 15 * x ** 7
+    return torch.where(x < 1, f, torch.zeros_like(f))
+
+
+def triplets_of(center: Tensor, bonds: Tensor):
+    """Every ordered pair (b1, b2) of two distinct bonds (edge rows in ``bonds``) with a common
+    centre, as (centre, b1, b2) int64 tensors; brute force by centre."""
+    by_atom: dict = {}
+    for e in bonds.tolist():
+        by_atom.setdefault(int(center[e]), []).append(e)
+    a, b1, b2 = [], [], []
+    for i, rows in by_atom.items():
+        for x in rows:
+            for y in rows:
+                if x != y:
+                    a.append(i)
+                    b1.append(x)
+                    b2.append(y)
+    as_t = lambda v: torch.tensor(v, dtype=torch.int64)  # noqa: E731
+    return as_t(a), as_t(b1), as_t(b2)
+
+
+def threebody_like_node_energy(params: dict, config: dict, positions, cell, elem, center, neighbor, images,
+                               bond_rows=None):
+    """Per-atom energies of the three-body model specified in fastmd_amd/models/threebody_like.py.
+    Bonds are the edges shorter than the bond cutoff (``bond_rows`` to fix the set, e.g. to the
+    builder's float32 decision; a row at the cutoff has a zero envelope either way)."""
+    dt = positions.dtype
+    p = {k: v.to(dt) for k, v in params.items()}
+    C, nb, L, F = config["channels"], config["n_basis"], config["num_interactions"], config["n_freq"]
+    rb = config["bond_cutoff"]
+    n_atoms = positions.shape[0]
+    vec = edge_vectors(positions, cell.to(dt), center, neighbor, images)
+    r = vec.norm(dim=1)
+    u = vec / r[:, None]
+    ef, fc = radial_basis(r, config["cutoff"], nb)
+    if bond_rows is None:
+        bond_rows = torch.nonzero(r.detach() < rb).flatten()
+    s = torch.zeros_like(r).index_copy(0, bond_rows, poly_cutoff(r.index_select(0, bond_rows), rb))
+    atom, b1, b2 = triplets_of(center, bond_rows)
+    cos = (u.index_select(0, b1) * u.index_select(0, b2)).sum(1) * (1 - 1e-6)
+    theta = torch.arccos(cos)
+    ph = theta[:, None] * torch.arange(1, F + 1, dtype=dt)[None, :]
+    alpha = torch.cat([torch.full_like(theta[:, None], 2 ** -0.5), torch.sin(ph), torch.cos(ph)], 1) / math.sqrt(math.pi)
+    elem = elem.long()
+    h = p["embedding"].index_select(0, elem)
+    eps = ef @ p["We"]
+    w3 = s.index_select(0, b1) * s.index_select(0, b2)
+    for t in range(L):
+        W3, W2 = p[f"layers.{t}.W3"], p[f"layers.{t}.W2"]
+        z3 = torch.cat([eps.index_select(0, b1), eps.index_select(0, b2), h.index_select(0, atom), alpha], 1) @ W3
+        eps = eps.index_add(0, b1, torch.nn.functional.silu(z3) * w3[:, None] / config["avg_num_angles"])
+        z2 = torch.cat([h.index_select(0, neighbor), h.index_select(0, center), eps], 1) @ W2
+        h = h.index_add(0, center, torch.nn.functional.silu(z2) * fc[:, None] / config["avg_num_neighbors"])
+    return p["e0"].index_select(0, elem) + h @ p["wr"]
 
 
 def energy_and_forces(node_energy_fn, positions, *args, n_real=None, **kwargs):

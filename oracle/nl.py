@@ -299,12 +299,20 @@ def line_graph(b: Build, rev, n: int, e_cap: int, u_cap: int, t_cap: int, bmax: 
     eto = np.full(e_cap + 1, pair_offsets[-1], np.int64)
     eto[:ec] = pair_offsets[centre[:ec]] + rank[:ec] * np.maximum(s[centre[:ec]] - 1, 0)
     eto = np.minimum(eto, t_cap)
+    # the second-bond CSR's permutation: for row e, by first bond, the triplets with e second
+    second_perm = np.full(t_cap, -1, np.int64)
+    if not overflow:
+        t_real = int(pair_offsets[-1])
+        line = lg[:t_real]
+        key = np.lexsort((line[:, 2], line[:, 4]))  # by second row, then first row
+        second_perm[:t_real] = np.arange(t_real)[key]
     bond_rows = np.full(e_cap, -1, np.int64)
     bond_rows[:len(rows)] = rows  # rows are in (atom, rank) order: the builder's rows are sorted by atom
     return {"d2u": d2u.astype(np.int32), "u2d": u2d.astype(np.int32), "invalid_pairs": invalid,
             "short_counts": s, "short_offsets": short_offsets, "short_edge_matrix": sem.astype(np.int32),
             "pair_offsets": pair_offsets, "overflow": overflow, "line_graph": lg.astype(np.int32),
-            "edge_triplet_offsets": eto, "bond_rows": bond_rows.astype(np.int32)}
+            "edge_triplet_offsets": eto, "bond_rows": bond_rows.astype(np.int32),
+            "second_perm": second_perm.astype(np.int32)}
 
 
 def triplet_set(center, neighbor, images, short, n_edges: int) -> set:

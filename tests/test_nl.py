@@ -382,6 +382,10 @@ def test_oracle_line_graph_pinned(line_cutoff):
         assert eto[0] == 0 and (np.diff(eto) >= 0).all() and eto[-1] == triplets
         first = np.repeat(np.arange(len(eto) - 1), np.diff(eto))
         assert np.array_equal(first, line[:triplets, 2])
+        # the second-bond CSR: row e's run through second_perm holds the triplets with e second
+        sp = lg["second_perm"].astype(np.int64)
+        assert np.array_equal(np.sort(sp[:triplets]), np.arange(triplets)) and (sp[triplets:] == -1).all()
+        assert np.array_equal(line[sp[:triplets], 4], first)
         # the bond -> atom CSR: short_offsets over bond_rows lists each atom's short rows
         br, so = lg["bond_rows"].astype(np.int64), lg["short_offsets"]
         assert np.array_equal(br[:so[-1]], np.nonzero(b.short[:edges])[0]) and (br[so[-1]:] == -1).all()
@@ -407,7 +411,7 @@ def _assert_line_equal(builder, b, lg):
                       ("short_counts", builder.short_counts), ("short_offsets", builder.short_offsets),
                       ("short_edge_matrix", builder.short_edge_matrix), ("pair_offsets", builder.pair_offsets),
                       ("line_graph", builder.line_graph), ("edge_triplet_offsets", builder.edge_triplet_offsets),
-                      ("bond_rows", builder.bond_rows)):
+                      ("bond_rows", builder.bond_rows), ("second_perm", builder.second_perm)):
         assert np.array_equal(buf.cpu().numpy(), lg[name]), name
     assert bool(builder._invalid_pairs.item()) == lg["invalid_pairs"]
     assert bool(builder._overflow.item()) == lg["overflow"]
