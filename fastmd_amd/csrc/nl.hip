@@ -716,7 +716,8 @@ __global__ void nl_reverse_kernel(const int32_t* center, const int32_t* neighbor
 __global__ void nl_window_flags_kernel(const int64_t* edge_count, const uint8_t* invalid_pairs,
                                        const uint8_t* overflow, const int32_t* isolated, int64_t e_cap,
                                        int check_isolated, uint8_t* w_over, uint8_t* w_cap, int64_t* w_edges,
-                                       int32_t* w_iso, const float* max_disp, double* stats) {
+                                       int32_t* w_iso, const float* max_disp, double* stats,
+                                       const int64_t* triplet_count, int64_t t_cap, int64_t* w_triplets) {
   if (threadIdx.x != 0) return;
   const int64_t edges = edge_count[0];
   const int32_t iso = isolated[0];
@@ -724,7 +725,16 @@ __global__ void nl_window_flags_kernel(const int64_t* edge_count, const uint8_t*
   if (check_isolated) flag = flag || iso > 0;
   const uint8_t wo = (w_over[0] != 0 || flag) ? 1 : 0;
   w_over[0] = wo;
-  const bool cap = edges > e_cap || (invalid_pairs && invalid_pairs[0] != 0);
+  // a line-graph build (triplet_count given) overflows its pairs at edges == e_cap (no padding
+  // pair left), and its triplets above t_cap
+  const int64_t triplets = triplet_count ? triplet_count[0] : 0;
+  const bool cap = (triplet_count ? edges >= e_cap : edges > e_cap) || (invalid_pairs && invalid_pairs[0] != 0) ||
+                   (triplet_count && triplets > t_cap);
+  int64_t wt = 0;
+  if (w_triplets) {
+    wt = triplets > w_triplets[0] ? triplets : w_triplets[0];
+    w_triplets[0] = wt;
+  }
   const uint8_t wc = (w_cap[0] != 0 || cap) ? 1 : 0;
   w_cap[0] = wc;
   const int64_t we = edges > w_edges[0] ? edges : w_edges[0];
@@ -735,7 +745,7 @@ __global__ void nl_window_flags_kernel(const int64_t* edge_count, const uint8_t*
     // capacity overflow, max edges, max isolated)
     stats[0] = (double)wo;
     stats[1] = (double)edges;
-    stats[2] = 0.0;
+    stats[2] = (double)wt;
     stats[3] = max_disp ? (double)max_disp[0] : 0.0;
     stats[4] = (double)wc;
     stats[5] = (double)we;
@@ -848,12 +858,14 @@ int fmd_nl_reverse(const int32_t* center, const int32_t* neighbor, const int32_t
 int fmd_nl_window_flags(const int64_t* edge_count, const uint8_t* invalid_pairs, const uint8_t* overflow,
                         const int32_t* isolated, int64_t e_cap, int32_t check_isolated, uint8_t* window_overflow,
                         uint8_t* window_capacity_overflow, int64_t* window_max_edges, int32_t* window_max_isolated,
-                        const float* max_displacement, double* stats, hipStream_t stream) {
+                        const float* max_displacement, double* stats, const int64_t* triplet_count, int64_t t_cap,
+                        int64_t* window_max_triplets, hipStream_t stream) {
   FMD_REQUIRE(edge_count && overflow && isolated && window_overflow && window_capacity_overflow &&
               window_max_edges && window_max_isolated);
+  FMD_REQUIRE(!triplet_count || t_cap > 0);
   hipLaunchKernelGGL(nl_window_flags_kernel, dim3(1), dim3(64), 0, stream, edge_count, invalid_pairs, overflow,
                      isolated, e_cap, check_isolated, window_overflow, window_capacity_overflow, window_max_edges,
-                     window_max_isolated, max_displacement, stats);
+                     window_max_isolated, max_displacement, stats, triplet_count, t_cap, window_max_triplets);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

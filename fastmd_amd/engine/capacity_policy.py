@@ -32,22 +32,28 @@ class CapacityKey:
 
 
 class JointCapacityPolicy:
-    """Edges-only capacity tiers with monotonic growth (capacity_policy.py:267-316)."""
+    """Pair (and, with a triplet step, triplet) capacity tiers with monotonic growth
+    (capacity_policy.py:267-316): each count takes its own tier, growth keeps the larger."""
 
-    def __init__(self, *, u_step: int = 512, min_pad_u: int = 256) -> None:
+    def __init__(self, *, u_step: int = 512, min_pad_u: int = 256, t_step: int | None = None,
+                 min_pad_t: int | None = None) -> None:
         self.u_step, self.min_pad_u = int(u_step), int(min_pad_u)
+        self.t_step = None if t_step is None else int(t_step)
+        self.min_pad_t = int(min_pad_t if min_pad_t is not None else (t_step or 0))
         self.capacity_history: list[CapacityKey] = []
 
-    def key_for(self, u: int) -> CapacityKey:
-        return CapacityKey(tier(u, self.u_step, self.min_pad_u), 0)
+    def key_for(self, u: int, t: int = 0) -> CapacityKey:
+        return CapacityKey(tier(u, self.u_step, self.min_pad_u),
+                           tier(t, self.t_step, self.min_pad_t) if self.t_step else 0)
 
-    def start(self, u: int) -> CapacityKey:
-        key = self.key_for(u)
+    def start(self, u: int, t: int = 0) -> CapacityKey:
+        key = self.key_for(u, t)
         self.capacity_history.append(key)
         return key
 
-    def grow(self, current: CapacityKey, u: int) -> CapacityKey:
-        grown = CapacityKey(max(current.u_capacity, self.key_for(u).u_capacity), 0)
+    def grow(self, current: CapacityKey, u: int, t: int = 0) -> CapacityKey:
+        want = self.key_for(u, t)
+        grown = CapacityKey(max(current.u_capacity, want.u_capacity), max(current.t_capacity, want.t_capacity))
         if grown != current:
             self.capacity_history.append(grown)
         return grown

@@ -34,6 +34,16 @@ from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
 from fastmd_amd.graph.gpu_graph_builder import raise_if_isolated_atoms
 
 
+def _capacity_exceeded(builder, status) -> bool:
+    """A build's capacity overflow, read on the host (initial evaluation): edges above e_capacity;
+    for a line-graph build also edges at e_capacity, invalid pairs or triplets above t_capacity."""
+    edges = int(status.edge_count.item())
+    if builder.line_graph is None:
+        return edges > builder.e_capacity
+    return (edges >= builder.e_capacity or bool(status.invalid_pairs.item())
+            or int(status.triplet_count.item()) > builder.t_capacity)
+
+
 class FixedCapacityOverflow(RuntimeError):
     def __init__(self, edge_count: int, triplet_count: int = 0) -> None:
         super().__init__(f"fixed graph capacity exceeded: edges={edge_count}, triplets={triplet_count}")
@@ -55,6 +65,7 @@ class WindowStats:
     capacity_overflow: bool
     max_edges: int
     max_isolated: int
+    max_triplets: int = 0
 
 
 class WholeStepGraphRunner:
@@ -90,6 +101,7 @@ class WholeStepGraphRunner:
         self.window_capacity_overflow = torch.zeros(1, dtype=torch.uint8, device=dev)
         self.window_max_edges = torch.zeros(1, dtype=torch.int64, device=dev)
         self.window_max_isolated = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.window_max_triplets = torch.zeros(1, dtype=torch.int64, device=dev)
         self._window_stats = torch.zeros(7, dtype=torch.float64, device=dev)
         # two host slots for the statistics of launched windows (one settled while the window
         # launched behind it runs), each with the event of its copy
@@ -123,8 +135,8 @@ class WholeStepGraphRunner:
         self.candidate_refreshes += 1
         self.builder.assert_candidate_capacity()
         f0, e0, status = self._evaluate(integrator.positions)
-        if int(status.edge_count.item()) > builder.e_capacity:
-            raise FixedCapacityOverflow(int(status.edge_count.item()))
+        if _capacity_exceeded(builder, status):
+            raise FixedCapacityOverflow(int(status.edge_count.item()), int(status.triplet_count.item()))
         if self.validate_isolated_atoms:
             raise_if_isolated_atoms(int(status.isolated_atom_count.item()))
         if forces is None:
@@ -153,7 +165,8 @@ class WholeStepGraphRunner:
                                        window_max_edges=self.window_max_edges,
                                        window_max_isolated=self.window_max_isolated,
                                        check_isolated=self.validate_isolated_atoms,
-                                       stats=self._window_stats if last else None)
+                                       stats=self._window_stats if last else None,
+                                       window_max_triplets=self.window_max_triplets)
 
     def _window_body(self) -> None:
         self.integrator.backup()
@@ -161,6 +174,7 @@ class WholeStepGraphRunner:
         self.window_capacity_overflow.zero_()
         self.window_max_edges.zero_()
         self.window_max_isolated.zero_()
+        self.window_max_triplets.zero_()
         for k in range(self.steps_per_launch):
             self._step_body(last=k == self.steps_per_launch - 1)
 
@@ -218,7 +232,7 @@ class WholeStepGraphRunner:
         host, event = self._slots[slot]
         event.synchronize()
         s = host.tolist()
-        return WindowStats(bool(s[0]), int(s[1]), float(s[3]), bool(s[4]), int(s[5]), int(s[6]))
+        return WindowStats(bool(s[0]), int(s[1]), float(s[3]), bool(s[4]), int(s[5]), int(s[6]), int(s[2]))
 
     def read_stats(self) -> WindowStats:
         """Wait for the last launched window's statistics (the one host sync per window)."""
@@ -269,7 +283,7 @@ class WholeStepGraphRunner:
         self.max_displacement_seen = max(self.max_displacement_seen, stats.max_displacement)
         if stats.capacity_overflow:
             self.integrator.restore()
-            raise FixedCapacityOverflow(stats.max_edges)
+            raise FixedCapacityOverflow(stats.max_edges, stats.max_triplets)
         if stats.overflow:
             self._fallback()
             # fresh candidates at the window's start: the displacement restarts (an upper bound of
@@ -302,7 +316,7 @@ class WholeStepGraphRunner:
         self.recovery_replays += 1
         if stats.capacity_overflow:
             self.integrator.restore()
-            raise FixedCapacityOverflow(stats.max_edges)
+            raise FixedCapacityOverflow(stats.max_edges, stats.max_triplets)
         if not stats.overflow:
             return
         self.integrator.restore()
@@ -312,12 +326,12 @@ class WholeStepGraphRunner:
             self._step_body(last=True)
             stats = self._read_now()
             if stats.capacity_overflow:
-                raise FixedCapacityOverflow(stats.max_edges)
+                raise FixedCapacityOverflow(stats.max_edges, stats.max_triplets)
         _require_finite_displacement(stats.max_displacement, self.launches)
 
     def _read_now(self) -> WindowStats:
         s = self._window_stats.tolist()
-        return WindowStats(bool(s[0]), int(s[1]), float(s[3]), bool(s[4]), int(s[5]), int(s[6]))
+        return WindowStats(bool(s[0]), int(s[1]), float(s[3]), bool(s[4]), int(s[5]), int(s[6]), int(s[2]))
 
     def replay(self) -> WindowStats:
         """One window: launch, read its statistics, settle."""

@@ -333,21 +333,29 @@ class FixedCapacityGraphBuilder:
 
     def accumulate_window(self, status: FixedCapacityGraphStatus, *, window_overflow: Tensor,
                           window_capacity_overflow: Tensor, window_max_edges: Tensor, window_max_isolated: Tensor,
-                          check_isolated: bool, stats: Tensor | None = None) -> None:
+                          check_isolated: bool, stats: Tensor | None = None,
+                          window_max_triplets: Tensor | None = None) -> None:
         """Fold one build's status into a whole-step window's flags in one kernel
         (fixed_capacity_builder.py:2300-2312, 430-455). Flags are uint8 [1]; ``stats`` (float64 [7])
-        receives the window's statistics after this build."""
+        receives the window's statistics after this build. A line-graph build also folds its
+        triplet count (capacity overflow above t_capacity, pairs full at e_capacity edges) and
+        its invalid-pair flag."""
+        if window_max_triplets is not None and window_max_triplets.dtype != torch.int64:
+            raise ValueError("window_max_triplets must be int64")
+        line = self.line_graph is not None
         if stats is not None and (stats.dtype != torch.float64 or stats.numel() < 7):
             raise ValueError("stats must be a float64 tensor of at least 7 entries")
         for t, dt in ((window_overflow, torch.uint8), (window_capacity_overflow, torch.uint8),
                       (window_max_edges, torch.int64), (window_max_isolated, torch.int32)):
             if t.dtype != dt:
                 raise ValueError(f"window flag dtype {t.dtype}, expected {dt}")
-        _abi.call("fmd_nl_window_flags", status.edge_count.data_ptr(), None, status.overflow.data_ptr(),
+        _abi.call("fmd_nl_window_flags", status.edge_count.data_ptr(),
+                  status.invalid_pairs.data_ptr() if line else None, status.overflow.data_ptr(),
                   status.isolated_atom_count.data_ptr(), self.e_capacity, 1 if check_isolated else 0,
                   window_overflow.data_ptr(), window_capacity_overflow.data_ptr(), window_max_edges.data_ptr(),
                   window_max_isolated.data_ptr(), status.max_displacement.data_ptr(),
-                  None if stats is None else stats.data_ptr(), self._stream())
+                  None if stats is None else stats.data_ptr(), status.triplet_count.data_ptr() if line else None,
+                  self.t_capacity, _abi.ptr(window_max_triplets) if line else None, self._stream())
 
     # ------------------------------------------------------------------ host views (tests, eager)
     def real_edges(self) -> tuple[Tensor, Tensor, Tensor]:

@@ -25,7 +25,8 @@ from fastmd_amd.config import InferenceConfig
 from fastmd_amd.engine.capacity_policy import JointCapacityPolicy, held_demand, whole_step_headroom
 from fastmd_amd.engine.energy_derivative import engine_derivative
 from fastmd_amd.execution.gpu_nhc import GPUNoseHooverChainNVT, maxwell_boltzmann_momenta
-from fastmd_amd.execution.whole_step_cuda_graph import FixedCapacityOverflow, WholeStepGraphRunner
+from fastmd_amd.execution.whole_step_cuda_graph import (FixedCapacityOverflow, WholeStepGraphRunner,
+                                                        _capacity_exceeded)
 from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
 from fastmd_amd.graph.gpu_graph_builder import TensorGraphBuilder, raise_if_isolated_atoms
 
@@ -92,14 +93,18 @@ class GPUResidentMolecularDynamics:
             force_dtype=torch.float32)
         topology = model.topology_spec()
         self.cutoff = float(topology.cutoff)
+        # a three-body model reads the line graph of bonds shorter than this (None: edges only)
+        self.triplet_cutoff = None if topology.triplet_cutoff is None else float(topology.triplet_cutoff)
         self.graph_builder = TensorGraphBuilder(cell=self.cell, atomic_numbers=self.numbers,
                                                 atom_graph_cutoff=self.cutoff, device=self.device,
                                                 check_isolated_atoms=False)
+        self._eager_line = None  # the eager path's line-graph builder and its capacity
         self.steps = 0
         self.whole_step_runner: WholeStepGraphRunner | None = None
         self.capacity_policy = None
         self._capacity = None
         self.whole_step_capacity_history: list[int] = []
+        self.whole_step_triplet_capacity_history: list[int] = []
         self._retired_stats: dict = {}
         self._graph_pool = None
         # F(q0) for the first pre-force half
@@ -113,7 +118,7 @@ class GPUResidentMolecularDynamics:
         """(forces float32 [N, 3], energy float64 [1]) at ``positions`` (default: the current
         state), through a ragged exact neighbour list (eager, host syncs)."""
         q = self.integrator.positions if positions is None else positions
-        batch = self.graph_builder.build(q)
+        batch = self._eager_batch(q)
         if self.validate_isolated_atoms:
             counts = torch.diff(batch.edge_offsets)
             raise_if_isolated_atoms(int((counts == 0).sum().item()))
@@ -130,13 +135,54 @@ class GPUResidentMolecularDynamics:
         self.integrator.step_post_force(forces, energy=energy)
         self.steps += 1
 
+    def _demand(self, batch) -> tuple[int, int]:
+        """(undirected pairs, triplets) of a ragged build: the pairs from its edge count, the
+        triplets from its bonds (squared float32 length below the bond cutoff's, the builder's
+        own test) as sum s (s - 1) over the centres."""
+        u = int(batch.edge_index.shape[0]) // 2
+        if self.triplet_cutoff is None:
+            return u, 0
+        ei = batch.edge_index.long()
+        cell = batch.cell.to(torch.float32)
+        pos = batch.positions.to(torch.float32)
+        vec = pos.index_select(0, ei[:, 1]) + batch.edge_image.to(torch.float32) @ cell - pos.index_select(0, ei[:, 0])
+        short = (vec * vec).sum(1) < float(np.float32(self.triplet_cutoff * self.triplet_cutoff))
+        s = torch.bincount(ei[short, 0], minlength=self.n_atoms)
+        return u, int((s * (s - 1)).sum().item())
+
+    def _eager_batch(self, q: Tensor):
+        """The batch of an eager evaluation: the ragged exact list, or for a three-body model a
+        line-graph build at a capacity held above the ragged list's demand (regrown when short)."""
+        batch = self.graph_builder.build(q)
+        if self.triplet_cutoff is None:
+            return batch
+        u, t = self._demand(batch)
+        policy = self._policy()
+        want = policy.key_for(*self._held(u, t))
+        while True:
+            if self._eager_line is None or (self._eager_line[1].u_capacity < want.u_capacity
+                                            or self._eager_line[1].t_capacity < want.t_capacity):
+                key = want if self._eager_line is None else policy.grow(self._eager_line[1], *self._held(u, t))
+                self._eager_line = (self._line_builder(key, prepare=None), key)
+            builder = self._eager_line[0]
+            builder.refresh_candidates(q)
+            _, status = builder.build(q, rebuild_candidates=False)
+            if not _capacity_exceeded(builder, status):
+                return builder.batch
+            u = max(u, (int(status.edge_count.item()) + 1) // 2)
+            t = max(t, int(status.triplet_count.item()))
+            want = policy.grow(self._eager_line[1], *self._held(u, t))
+
     # ------------------------------------------------------------------ whole step
-    def _make_runner(self, u_capacity: int, recapture: bool) -> WholeStepGraphRunner:
-        builder = FixedCapacityGraphBuilder(cell=self.cell, atomic_numbers=self.numbers, u_capacity=u_capacity,
-                                            atom_graph_cutoff=self.cutoff,
-                                            candidate_cutoff=self.cutoff + self.config.capacity.candidate_skin,
-                                            padding=self.adapter.padding_rule(), prepare=self.adapter.prepare,
-                                            device=self.device)
+    def _line_builder(self, key, prepare):
+        return FixedCapacityGraphBuilder(cell=self.cell, atomic_numbers=self.numbers, u_capacity=key.u_capacity,
+                                         t_capacity=key.t_capacity if self.triplet_cutoff is not None else 0,
+                                         atom_graph_cutoff=self.cutoff, line_graph_cutoff=self.triplet_cutoff,
+                                         candidate_cutoff=self.cutoff + self.config.capacity.candidate_skin,
+                                         padding=self.adapter.padding_rule(), prepare=prepare, device=self.device)
+
+    def _make_runner(self, key, recapture: bool) -> WholeStepGraphRunner:
+        builder = self._line_builder(key, prepare=self.adapter.prepare)
         return WholeStepGraphRunner(model=self.adapter, builder=builder, integrator=self.integrator, task=self.task,
                                     steps_per_launch=self.steps_per_launch, warmup=self.config.capacity.warmup,
                                     graph_pool=self._graph_pool, validate_isolated_atoms=self.validate_isolated_atoms,
@@ -150,31 +196,54 @@ class GPUResidentMolecularDynamics:
             return s.u_step, s.min_pad_u, s.u_thermal_factor
         return cap.u_step, cap.min_pad_u, 1.0
 
+    def _triplet_step(self):
+        """(t_step, min_pad_t, t_factor): the model's triplet tiers, else 128 / 128 / 1.06."""
+        step = getattr(self.adapter, "capacity_step", None)
+        s = step() if step is not None else None
+        if s is None or not s.t_step:
+            return 128, 128, 1.06
+        return int(s.t_step), int(s.min_pad_t or s.t_step), float(s.t_thermal_factor)
+
+    def _policy(self) -> JointCapacityPolicy:
+        if self.capacity_policy is None:
+            u_step, min_pad, _ = self._capacity_step()
+            t_step, t_pad, _ = self._triplet_step() if self.triplet_cutoff is not None else (None, None, 1.0)
+            self.capacity_policy = JointCapacityPolicy(u_step=u_step, min_pad_u=min_pad, t_step=t_step, min_pad_t=t_pad)
+        return self.capacity_policy
+
+    def _held(self, u: int, t: int) -> tuple[int, int]:
+        """The pair and triplet counts a capture holds for a demand (headroom, thermal factors)."""
+        u_step, _, factor = self._capacity_step()
+        held_u = held_demand(u, whole_step_headroom(u, u_step), factor)
+        if self.triplet_cutoff is None:
+            return held_u, 0
+        t_step, _, t_factor = self._triplet_step()
+        return held_u, held_demand(t, whole_step_headroom(t, t_step), t_factor)
+
     def enable_whole_step_cuda_graph(self) -> None:
         """Size the capacity from a ragged build (gpu_md.py:591-711) and capture the window."""
         if self.whole_step_runner is not None:
             return
         sample = self.graph_builder.build(self.integrator.positions)
-        demand = int(sample.edge_index.shape[0]) // 2
-        u_step, min_pad, factor = self._capacity_step()
-        self.capacity_policy = JointCapacityPolicy(u_step=u_step, min_pad_u=min_pad)
-        self._capacity = self.capacity_policy.start(held_demand(demand, whole_step_headroom(demand, u_step), factor))
+        u, t = self._demand(sample)
+        self._capacity = self._policy().start(*self._held(u, t))
         self._graph_pool = torch.cuda.graph_pool_handle()
         while True:
             try:
-                self.whole_step_runner = self._make_runner(self._capacity.u_capacity, recapture=False)
+                self.whole_step_runner = self._make_runner(self._capacity, recapture=False)
                 break
             except FixedCapacityOverflow as overflow:
-                self._grow(overflow.edge_count)
+                self._grow(overflow.edge_count, overflow.triplet_count)
         self.whole_step_capacity_history.append(self._capacity.u_capacity)
+        self.whole_step_triplet_capacity_history.append(self._capacity.t_capacity)
 
-    def _grow(self, edge_count: int) -> None:
-        u_step, _, factor = self._capacity_step()
-        demand = (int(edge_count) + 1) // 2
-        self._capacity = self.capacity_policy.grow(self._capacity, held_demand(demand, whole_step_headroom(
-            demand, u_step), factor))
+    def _grow(self, edge_count: int, triplet_count: int = 0) -> None:
+        """A larger tier for a window's largest counts (a pair overflow truncates the triplets it
+        counted: their tier grows again if the next window still overflows)."""
+        u = (int(edge_count) + 1) // 2
+        self._capacity = self._policy().grow(self._capacity, *self._held(u, int(triplet_count)))
 
-    def _grow_whole_step_runner(self, edge_count: int) -> None:
+    def _grow_whole_step_runner(self, edge_count: int, triplet_count: int = 0) -> None:
         """Capacity growth after an overflowed window: a larger tier, recaptured (gpu_md.py:1355-1410)."""
         old = self.whole_step_runner
         # the retired runner's counters carry over into whole_step_stats()
@@ -183,11 +252,12 @@ class GPUResidentMolecularDynamics:
                 self._retired_stats[key] = self._retired_stats.get(key, 0) + value
         self._retired_stats["max_edge_count"] = max(self._retired_stats.get("max_edge_count", 0),
                                                     old.stats()["max_edge_count"])
-        self._grow(edge_count)
+        self._grow(edge_count, triplet_count)
         self.whole_step_runner = None
         del old
-        self.whole_step_runner = self._make_runner(self._capacity.u_capacity, recapture=True)
+        self.whole_step_runner = self._make_runner(self._capacity, recapture=True)
         self.whole_step_capacity_history.append(self._capacity.u_capacity)
+        self.whole_step_triplet_capacity_history.append(self._capacity.t_capacity)
 
     def run(self, steps: int) -> None:
         """``steps`` MD steps (a multiple of ``steps_per_launch`` in the whole-step mode).
@@ -235,7 +305,7 @@ class GPUResidentMolecularDynamics:
                 try:
                     runner.settle(stats)
                 except FixedCapacityOverflow as overflow:
-                    self._grow_whole_step_runner(overflow.edge_count)
+                    self._grow_whole_step_runner(overflow.edge_count, overflow.triplet_count)
                     continue
                 done += 1
                 self.steps += self.steps_per_launch
@@ -276,6 +346,8 @@ class GPUResidentMolecularDynamics:
             stats[key] += self._retired_stats.get(key, 0)
         stats["max_edge_count"] = max(stats["max_edge_count"], self._retired_stats.get("max_edge_count", 0))
         stats["capacity_history"] = list(self.whole_step_capacity_history)
+        if self.triplet_cutoff is not None:
+            stats["triplet_capacity_history"] = list(self.whole_step_triplet_capacity_history)
         stats["windows_ahead"] = self.windows_ahead
         stats["windows_rolled_back"] = self.windows_rolled_back
         return stats

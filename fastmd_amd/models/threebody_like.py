@@ -45,11 +45,10 @@ from fastmd_amd.ops.threebody import LineGraph, fourier_line_vjp
 from fastmd_amd.ops.wide_gemm import gemm, gemm_gather, gemm_splitk
 
 _ELEMENTS = 118
-# pairs in tiers of 32 with 32 of padding; triplets held at 1.06x their demand (the CHGNet adapter's
-# factors, fastmd/models/chgnet.py:25-30)
-_CAPACITY_STEP = CapacityStep(u_step=32, min_pad_u=32, u_thermal_factor=1.02)
-T_THERMAL_FACTOR = 1.06
-T_STEP = 128
+# pairs and triplets in tiers of 128 with at least 128 of padding, held at 1.01x the pair and 1.06x
+# the triplet demand (the CHGNet adapter's tiers, fastmd/models/chgnet.py:25-30)
+_CAPACITY_STEP = CapacityStep(u_step=128, min_pad_u=128, u_thermal_factor=1.01, t_step=128, min_pad_t=128,
+                              t_thermal_factor=1.06)
 
 
 @dataclass(frozen=True)

@@ -202,13 +202,17 @@ int fmd_nl_reverse(const int32_t* center, const int32_t* neighbor, const int32_t
 
 /* Window flag fold of one build (fixed_capacity_builder.py:430-455, _window_flags_kernel); with
  * `stats` (float64 [7], may be null) also the window's statistics after this build: (overflow,
- * edges, triplets = 0, max displacement, capacity overflow, max edges, max isolated), the one
- * buffer the host reads per window (whole_step_cuda_graph.py:353-356). */
+ * edges, max triplets, max displacement, capacity overflow, max edges, max isolated), the one
+ * buffer the host reads per window (whole_step_cuda_graph.py:353-356). A line-graph build passes
+ * its triplet count (pair_offsets[n]) and t_cap: capacity overflow is then edges >= e_cap (no
+ * padding pair), invalid pairs or triplets > t_cap, and window_max_triplets (nullable) keeps the
+ * window's largest triplet count. */
 int fmd_nl_window_flags(const int64_t* edge_count, const uint8_t* invalid_pairs, const uint8_t* overflow,
                         const int32_t* isolated, int64_t e_cap, int32_t check_isolated,
                         uint8_t* window_overflow, uint8_t* window_capacity_overflow,
                         int64_t* window_max_edges, int32_t* window_max_isolated,
-                        const float* max_displacement, double* stats, hipStream_t stream);
+                        const float* max_displacement, double* stats, const int64_t* triplet_count, int64_t t_cap,
+                        int64_t* window_max_triplets, hipStream_t stream);
 
 /* ----------------------------------------------------------------------------------------
  * (b) Gather-cat

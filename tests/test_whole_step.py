@@ -30,6 +30,12 @@ def test_capacity_tiers_known_answers():
     k = p.start(held_demand(1027, 0, 1.02))
     assert k.u_capacity == 1088  # 135-atom perovskite, MACE capacity step (1 088)
     assert p.grow(k, 900).u_capacity == 1088 and p.grow(k, 1100).u_capacity > 1088
+    # joint tiers: pairs and triplets each take their own tier, growth keeps the larger of each
+    j = JointCapacityPolicy(u_step=128, min_pad_u=128, t_step=128, min_pad_t=128)
+    k = j.start(1040, 980)
+    assert (k.u_capacity, k.t_capacity) == (1280, 1152)
+    g = j.grow(k, 1000, 1100)
+    assert (g.u_capacity, g.t_capacity) == (1280, 1280) and j.capacity_history == [k, g]
 
 
 def _md(model, execution, device, steps_per_launch=1, capacity=None, system=None, temperature=500.0):
@@ -42,6 +48,18 @@ def _md(model, execution, device, steps_per_launch=1, capacity=None, system=None
                                         steps_per_launch=steps_per_launch)
 
 
+def _adapter(model_name, device, bond_cutoff=3.5):
+    from fastmd_amd.models.mace_like import MaceLikeAdapter
+    from fastmd_amd.models.pair_potential import MorsePairAdapter
+    from fastmd_amd.models.threebody_like import ThreeBodyAdapter, ThreeBodyConfig
+
+    if model_name == "morse":
+        return MorsePairAdapter(device=device)
+    if model_name == "mace_like":
+        return MaceLikeAdapter(device=device)
+    return ThreeBodyAdapter(config=ThreeBodyConfig(bond_cutoff=bond_cutoff), device=device)
+
+
 def _state(md):
     import torch
 
@@ -50,17 +68,13 @@ def _state(md):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("model_name", ["morse", "mace_like"])
+@pytest.mark.parametrize("model_name", ["morse", "mace_like", "threebody"])
 @pytest.mark.parametrize("steps_per_launch", [1, 5])
 def test_whole_step_equals_eager_bitwise(device, model_name, steps_per_launch):
     import torch
 
-    from fastmd_amd.models.mace_like import MaceLikeAdapter
-    from fastmd_amd.models.pair_potential import MorsePairAdapter
-
     print(f"[whole_step] {model_name} spl={steps_per_launch}", flush=True)
-    make = (lambda: MorsePairAdapter(device=device)) if model_name == "morse" else (
-        lambda: MaceLikeAdapter(device=device))
+    make = lambda: _adapter(model_name, device)  # noqa: E731
     eager = _md(make(), "eager", device)
     graph = _md(make(), "whole_step", device, steps_per_launch=steps_per_launch)
     assert torch.equal(_state(eager), _state(graph))
@@ -93,7 +107,38 @@ def test_whole_step_capacity_growth_and_refresh_paths(device):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("model_name", ["morse", "mace_like"])
+def test_whole_step_threebody_triplet_capacity_growth(device):
+    """Triplet tiers of one triplet (a model whose capacity step is 1 / 0 / 1.0) with the bond
+    cutoff at the B-X distance (3.1 A, where bonds come and go at 3000 K): windows overflow their
+    triplets, the capacity grows and the step is recaptured; the trajectory stays the eager one,
+    bitwise."""
+    import torch
+
+    from fastmd_amd.adapters.protocol import CapacityStep
+    from fastmd_amd.models.threebody_like import ThreeBodyAdapter, ThreeBodyConfig
+
+    class Tight(ThreeBodyAdapter):
+        def capacity_step(self):
+            return CapacityStep(u_step=1, min_pad_u=0, u_thermal_factor=1.0, t_step=1, min_pad_t=0,
+                                t_thermal_factor=1.0)
+
+    s = systems.perovskite(3)
+    cfg = ThreeBodyConfig(bond_cutoff=3.1)
+    eager = _md(Tight(config=cfg, device=device), "eager", device, system=s, temperature=3000.0)
+    graph = _md(Tight(config=cfg, device=device), "whole_step", device, steps_per_launch=2, system=s,
+                temperature=3000.0)
+    eager.run(200)
+    graph.run(200)
+    a, b = _state(eager), _state(graph)
+    assert torch.equal(a, b), float((a - b).abs().max())
+    st = graph.whole_step_stats()
+    print(st, flush=True)
+    assert len(st["triplet_capacity_history"]) > 1
+    assert st["triplet_capacity_history"] == sorted(st["triplet_capacity_history"])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("model_name", ["morse", "mace_like", "threebody"])
 def test_windows_launched_behind_match_settled_windows_bitwise(device, model_name, monkeypatch):
     """run() launches each next window before the host reads the flags of the one in flight. With
     a launch behind EVERY window (refresh_unlikely forced true) and a tiny skin and capacity step
@@ -103,12 +148,9 @@ def test_windows_launched_behind_match_settled_windows_bitwise(device, model_nam
     import torch
 
     from fastmd_amd.execution.whole_step_cuda_graph import WholeStepGraphRunner
-    from fastmd_amd.models.mace_like import MaceLikeAdapter
-    from fastmd_amd.models.pair_potential import MorsePairAdapter
 
     print(f"[launch behind] {model_name}", flush=True)
-    make = (lambda: MorsePairAdapter(device=device)) if model_name == "morse" else (
-        lambda: MaceLikeAdapter(device=device))
+    make = lambda: _adapter(model_name, device)  # noqa: E731
     s = systems.perovskite(3)
     tight = CapacityConfig(u_step=1, min_pad_u=0, candidate_skin=0.05)
     settled = _md(make(), "whole_step", device, steps_per_launch=2, capacity=tight, system=s)
