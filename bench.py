@@ -36,17 +36,22 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_md(n_atoms: int, steps_per_launch: int):
+def build_md(n_atoms: int, steps_per_launch: int, bond_cutoff: float | None = None):
+    """The whole-step MD of a perovskite: the MACE-like model, or with ``bond_cutoff`` the
+    configs[4] three-body model (64 channels, 4 layers, that bond-graph cutoff)."""
     import torch
 
     from fastmd_amd import systems
     from fastmd_amd.config import InferenceConfig
     from fastmd_amd.interfaces.gpu_md import GPUResidentMolecularDynamics
     from fastmd_amd.models.mace_like import MaceLikeAdapter
+    from fastmd_amd.models.threebody_like import ThreeBodyAdapter, ThreeBodyConfig
 
     device = torch.device("cuda", 0)
     s = systems.perovskite_atoms(n_atoms)
-    return GPUResidentMolecularDynamics(s, model=MaceLikeAdapter(device=device), device=device, temperature=500.0,
+    model = (MaceLikeAdapter(device=device) if bond_cutoff is None else
+             ThreeBodyAdapter(config=ThreeBodyConfig(bond_cutoff=bond_cutoff), device=device))
+    return GPUResidentMolecularDynamics(s, model=model, device=device, temperature=500.0,
                                         timestep=0.25, tdamp=25.0, tchain=3, tloop=1,
                                         config=InferenceConfig(execution="whole_step"),
                                         steps_per_launch=steps_per_launch)
@@ -289,6 +294,29 @@ def scaling_sweep(steps: int, warmup: int) -> list:
     return out
 
 
+def threebody_bench(steps: int, warmup: int) -> list:
+    """the three-body model on the 5 000-atom perovskite (10 x 10 x 10 cells), 500 K NHC,
+    at the stated 3 A bond cutoff and at 3.5 A (where the B-X bonds, 3.1 A, enter the line graph)."""
+    import torch
+
+    out = []
+    for rb in (3.0, 3.5):
+        md = build_md(5000, STEPS_PER_LAUNCH, bond_cutoff=rb)
+        t = time_md(md, steps, warmup)
+        b = md.whole_step_runner.builder
+        stats = md.whole_step_stats()
+        row = {"atoms": 5000, "bond_cutoff": rb, "steps": steps, "warmup": warmup,
+               "ms_per_step": round(t / steps * 1e3, 4), "md_steps_per_s": round(steps / t, 1),
+               "atom_steps_per_s": round(5000 * steps / t, 1), "edges": int(b.edge_offsets[-1].item()),
+               "bonds": int(b.short_offsets[-1].item()), "triplets": int(b.pair_offsets[-1].item()),
+               "e_capacity": stats["e_capacity"], "t_capacity": b.t_capacity, "timed_events": md.timed_events}
+        log(f"three-body rb={rb}: {row['ms_per_step']} ms/step, {row['bonds']} bonds, {row['triplets']} triplets")
+        out.append(row)
+        del md, b
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(n_atoms: int, budget_s: float) -> dict:
     """The CPU oracle (PyTorch-CPU eager model forward+backward with index_select/index_add_/matmul,
     NumPy neighbour list and NHC) on this host, whole MD steps until ``budget_s`` elapsed."""
@@ -361,6 +389,9 @@ def main() -> int:
     parser.add_argument("--steps-scaling", type=int, default=1000)
     parser.add_argument("--ops", action="store_true",
                         help="only the configs[1] operator microbenchmark sweep (N x F), one JSON line")
+    parser.add_argument("--threebody", action="store_true",
+                        help="only the configs[4] three-body model (5 000 atoms, bond cutoffs 3 and 3.5 A)")
+    parser.add_argument("--steps-threebody", type=int, default=500)
     parser.add_argument("--roofline-only", action="store_true",
                         help="only the dominant kernel at the 10 000-atom shape plus a 256 MiB copy (--pmc runs)")
     args = parser.parse_args()
@@ -379,6 +410,9 @@ def main() -> int:
     steps_small = 200 if args.quick else args.steps_small
     if args.scaling:
         print(json.dumps({"scaling": scaling_sweep(args.steps_scaling, args.warmup)}), flush=True)
+        return 0
+    if args.threebody:
+        print(json.dumps({"threebody": threebody_bench(args.steps_threebody, args.warmup)}), flush=True)
         return 0
     if args.ops:
         print(json.dumps({"ops_sweep": ops_sweep(), "hbm_peak_GBps": HBM_PEAK_GBPS,
@@ -419,6 +453,9 @@ def main() -> int:
     del md
     torch.cuda.empty_cache()
 
+    log("configs[4]: three-body model, 5 000 atoms")
+    threebody = threebody_bench(200 if args.quick else args.steps_threebody, args.warmup)
+
     log("memory-bound operator microbenchmarks")
     seg = hbm_ops_bench()
     cpu = None
@@ -451,6 +488,7 @@ def main() -> int:
         "small_system": {"atoms": 135, "ms_per_step": round(ms_small, 5), "md_steps_per_s": round(1e3 / ms_small, 1),
                          "atom_steps_per_s": round(135 / (ms_small / 1e3), 1), "steps": steps_small,
                          "e_capacity": stats_small["e_capacity"], "timed_events": events_small},
+        "threebody_5000": threebody,
         "segment_sum_GBps": seg["segment_sum"]["GBps"],
         "hbm_ops_40k": seg,
         "whole_step_stats_10k": {**{k: stats_big[k] for k in ("candidate_refreshes", "fallback_windows",

@@ -69,10 +69,19 @@ __global__ void __launch_bounds__(256) tb_gated_sum_kernel(const float* z, int64
   run_of(off, s, rows, lo, hi);
   for (int c = lane; c < C; c += 64) {
     float acc = 0.f;
-#pragma unroll 4
-    for (int64_t r = lo; r < hi; ++r) {
-      const float x = z[r * ldz + c];
-      acc += x * tb_sigmoid(x) * (rw.w1(r) * rw.w2(r));
+    // four rows' loads in flight before their arithmetic (the sum stays in row order)
+    for (int64_t r = lo; r < hi; r += 4) {
+      const int m = hi - r >= 4 ? 4 : (int)(hi - r);
+      float x[4], w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j < m) {
+          x[j] = z[(r + j) * ldz + c];
+          w[j] = rw.w1(r + j) * rw.w2(r + j);
+        }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j < m) acc += x[j] * tb_sigmoid(x[j]) * w[j];
     }
     float* o = out + s * ldo + c;
     *o = accumulate ? *o + scale * acc : scale * acc;
@@ -114,30 +123,49 @@ __global__ void __launch_bounds__(256) tb_gated_sum_bwd_kernel(const float* gout
     g[k] = (k < nc && c < C) ? scale * gout[s * ldg + c] : 0.f;
     acc[k] = 0.f;
   }
-  for (int64_t r = lo; r < hi; ++r) {
-    const float a = rw.w1(r), b = rw.w2(r), w = a * b;
-    float p = 0.f;
+  for (int64_t r0 = lo; r0 < hi; r0 += 4) {
+    // four rows' loads in flight before their arithmetic (rows still handled in order)
+    const int m = hi - r0 >= 4 ? 4 : (int)(hi - r0);
+    float xs[4][4], wa[4], wb[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int c = lane + 64 * k;
-      if (k < nc && c < C) {
-        const float x = z[r * ldz + c];
-        const float sg = tb_sigmoid(x);
-        const float si = x * sg;
-        const float v = g[k] * w * (sg + si * (1.0f - sg));
-        gz[r * ldgz + c] = v;
-        acc[k] += v;
-        p += g[k] * si;
+    for (int j = 0; j < 4; ++j)
+      if (j < m) {
+        wa[j] = rw.w1(r0 + j);
+        wb[j] = rw.w2(r0 + j);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int c = lane + 64 * k;
+          xs[j][k] = (k < nc && c < C) ? z[(r0 + j) * ldz + c] : 0.f;
+        }
       }
-    }
-    if (gw) {
-      const float t = wave_sum(p);
-      if (lane == 0) {
-        if (rw.i2) {
-          gw[r * ldgw] = (acc_gw ? gw[r * ldgw] : 0.f) + t * b;
-          gw[r * ldgw + 1] = (acc_gw ? gw[r * ldgw + 1] : 0.f) + t * a;
-        } else {
-          gw[r * ldgw] = (acc_gw ? gw[r * ldgw] : 0.f) + t;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j >= m) break;
+      const int64_t r = r0 + j;
+      const float a = wa[j], b = wb[j], w = a * b;
+      float p = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int c = lane + 64 * k;
+        if (k < nc && c < C) {
+          const float x = xs[j][k];
+          const float sg = tb_sigmoid(x);
+          const float si = x * sg;
+          const float v = g[k] * w * (sg + si * (1.0f - sg));
+          gz[r * ldgz + c] = v;
+          acc[k] += v;
+          p += g[k] * si;
+        }
+      }
+      if (gw) {
+        const float t = wave_sum(p);
+        if (lane == 0) {
+          if (rw.i2) {
+            gw[r * ldgw] = (acc_gw ? gw[r * ldgw] : 0.f) + t * b;
+            gw[r * ldgw + 1] = (acc_gw ? gw[r * ldgw + 1] : 0.f) + t * a;
+          } else {
+            gw[r * ldgw] = (acc_gw ? gw[r * ldgw] : 0.f) + t;
+          }
         }
       }
     }
@@ -202,6 +230,163 @@ __global__ void tb_geometry_bwd_kernel(const float* geo, const float* def, int n
   for (int k = 0; k < 3; ++k) gvec[3 * e + k] = gr * g[k] + (v[k] - gdotu * g[k]) * inv_r;
 }
 
+// ---- angle -> bond sums over the line graph. The work is a few bonds and triplets per atom, far
+// fewer than the edge rows: each kernel runs a fixed grid of waves that strides over the real
+// bonds (bond_rows[0, short_offsets[n])) or triplets ([0, pair_offsets[n])), counts read on the
+// device, one bond or triplet per wave at a time (channels across the lanes). A bond's triplets
+// as first bond are the run [eto[b], eto[b+1]) of the line graph (contiguous), as second bond
+// the same run through second_perm.
+struct LineCsr {
+  const int64_t* short_offsets;  // [n + 1]: the bond count at [n]
+  const int32_t* bond_rows;      // [e_cap]
+  const int64_t* eto;            // edge_triplet_offsets [e_cap + 1]
+  const int32_t* second_perm;    // [t_cap]
+  const int32_t* line;           // line_graph [t_cap, 5]: (atom, pair 1, row 1, pair 2, row 2)
+  const int64_t* pair_offsets;   // [n + 1]: the triplet count at [n]
+  int64_t n;
+  int64_t t_cap;
+};
+
+constexpr int kStrideBlocks = 1024;  // 4096 waves (about four per SIMD)
+
+__device__ __forceinline__ int64_t wave_id() {
+  return (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+}
+
+// eps[b] += scale * sum over b's triplets (first bond), in order, of silu(z3[k]) s_b s_b2
+__global__ void __launch_bounds__(256) tb_bond_sum_kernel(LineCsr lc, const float* z3, int64_t ldz, int C,
+                                                           const float* geo, float scale, float* eps, int64_t lde) {
+  const int lane = threadIdx.x & 63;
+  const int nc = (C + 63) / 64;
+  const int64_t nb = lc.short_offsets[lc.n];
+  for (int64_t j = wave_id(); j < nb; j += (int64_t)gridDim.x * 4) {
+    const int64_t b = lc.bond_rows[j];
+    const float w1 = geo[8 * b + 6];
+    int64_t lo = lc.eto[b], hi = lc.eto[b + 1];
+    hi = hi < lc.t_cap ? hi : lc.t_cap;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    // four triplets' loads in flight before their arithmetic (the sum stays in triplet order)
+    for (int64_t k0 = lo; k0 < hi; k0 += 4) {
+      const int m = hi - k0 >= 4 ? 4 : (int)(hi - k0);
+      float x[4][4], w[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (q < m) {
+          w[q] = w1 * geo[8 * (int64_t)lc.line[5 * (k0 + q) + 4] + 6];
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc) {
+            const int c = lane + 64 * cc;
+            x[q][cc] = (cc < nc && c < C) ? z3[(k0 + q) * ldz + c] : 0.f;
+          }
+        }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (q < m)
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc) acc[cc] += x[q][cc] * tb_sigmoid(x[q][cc]) * w[q];
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const int c = lane + 64 * cc;
+      if (cc < nc && c < C) eps[b * lde + c] += scale * acc[cc];
+    }
+  }
+}
+
+// Per triplet k (one wave): with g = scale geps[b1], gz3[k] = g s_b1 s_b2 silu'(z3[k]) and
+// gw = sum_c g silu(z3[k]), stored as the envelope terms gsw[k] = (gw s_b2, gw s_b1). Rows past
+// the real triplets: gz3 = 0.
+__global__ void __launch_bounds__(256) tb_triplet_bwd_kernel(LineCsr lc, const float* geps, int64_t ldg,
+                                                              const float* z3, int64_t ldz, int C, const float* geo,
+                                                              float scale, float* gz3, int64_t ldgz, float* gsw) {
+  const int lane = threadIdx.x & 63;
+  const int nc = (C + 63) / 64;
+  const int64_t t_all = lc.pair_offsets[lc.n];
+  const int64_t t_real = t_all < lc.t_cap ? t_all : lc.t_cap;
+  for (int64_t k = wave_id(); k < lc.t_cap; k += (int64_t)gridDim.x * 4) {
+    if (k >= t_real) {
+      for (int c = lane; c < C; c += 64) gz3[k * ldgz + c] = 0.f;
+      continue;
+    }
+    const int64_t b1 = lc.line[5 * k + 2], b2 = lc.line[5 * k + 4];
+    const float w1 = geo[8 * b1 + 6], w2 = geo[8 * b2 + 6], w = w1 * w2;
+    float g[4], x[4];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const int c = lane + 64 * cc;
+      const bool ok = cc < nc && c < C;
+      g[cc] = ok ? scale * geps[b1 * ldg + c] : 0.f;
+      x[cc] = ok ? z3[k * ldz + c] : 0.f;
+    }
+    float p = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const int c = lane + 64 * cc;
+      if (cc < nc && c < C) {
+        const float sg = tb_sigmoid(x[cc]);
+        const float si = x[cc] * sg;
+        gz3[k * ldgz + c] = g[cc] * w * (sg + si * (1.0f - sg));
+        p += g[cc] * si;
+      }
+    }
+    const float gw = wave_sum(p);
+    if (lane == 0) {
+      gsw[2 * k] = gw * w2;
+      gsw[2 * k + 1] = gw * w1;
+    }
+  }
+}
+
+// Per bond b (one wave): geps[b] += sum over b's triplets as first bond of ga3[k, 0:C], then as
+// second bond of ga3[k, C:2C]; gs[b] += the same sums of gsw[k, 0] and gsw[k, 1].
+__global__ void __launch_bounds__(256) tb_bond_reduce_kernel(LineCsr lc, const float* ga3, int64_t lda, int C,
+                                                              const float* gsw, float* geps, int64_t ldg, float* gs) {
+  const int lane = threadIdx.x & 63;
+  const int nc = (C + 63) / 64;
+  const int64_t nb = lc.short_offsets[lc.n];
+  for (int64_t j = wave_id(); j < nb; j += (int64_t)gridDim.x * 4) {
+    const int64_t b = lc.bond_rows[j];
+    int64_t lo = lc.eto[b], hi = lc.eto[b + 1];
+    hi = hi < lc.t_cap ? hi : lc.t_cap;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float gsum = 0.f;
+    for (int role = 0; role < 2; ++role) {
+      for (int64_t p0 = lo; p0 < hi; p0 += 4) {
+        const int m = hi - p0 >= 4 ? 4 : (int)(hi - p0);
+        int64_t kk[4];
+        float x[4][4], sw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (q < m) kk[q] = role == 0 ? p0 + q : (int64_t)lc.second_perm[p0 + q];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (q < m) {
+            const bool real = kk[q] >= 0;
+            sw[q] = real ? gsw[2 * kk[q] + role] : 0.f;
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+              const int c = lane + 64 * cc;
+              x[q][cc] = (real && cc < nc && c < C) ? ga3[kk[q] * lda + role * C + c] : 0.f;
+            }
+          }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (q < m) {
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) acc[cc] += x[q][cc];
+            gsum += sw[q];
+          }
+      }
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const int c = lane + 64 * cc;
+      if (cc < nc && c < C) geps[b * ldg + c] += acc[cc];
+    }
+    if (lane == 0) gs[b] += gsum;
+  }
+}
+
 RowWeight make_weight(const float* w, int64_t ldw, const int32_t* i1, const int32_t* i2, int64_t ld_idx) {
   return RowWeight{w, ldw, i1, i2, ld_idx};
 }
@@ -253,6 +438,48 @@ int fmd_tb_gated_sum_bwd_f32(const float* gout, int64_t ldg, const float* z, int
   hipLaunchKernelGGL(tb_gated_sum_bwd_kernel, dim3((unsigned)(seg_blocks + tail_blocks)), dim3(256), 0, stream, gout,
                      ldg, z, ldz, rows, channels, make_weight(w, ldw, index1, index2, ld_index), offsets, n_segments,
                      scale, gz, ldgz, gsum, ldgs, gw, ldgw, accumulate_gw, seg_blocks);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_tb_bond_sum_f32(const float* z3, int64_t ldz, int32_t channels, const float* geo, const int64_t* short_offsets,
+                        const int32_t* bond_rows, const int64_t* edge_triplet_offsets, const int32_t* line_graph,
+                        int64_t n_atoms, int64_t t_cap, float scale, float* eps, int64_t lde, hipStream_t stream) {
+  FMD_REQUIRE(n_atoms >= 0 && t_cap >= 0 && channels > 0 && channels <= 256 && ldz >= channels && lde >= channels);
+  if (n_atoms == 0 || t_cap == 0) return FMD_OK;
+  FMD_REQUIRE(z3 && geo && short_offsets && bond_rows && edge_triplet_offsets && line_graph && eps);
+  LineCsr lc{short_offsets, bond_rows, edge_triplet_offsets, nullptr, line_graph, nullptr, n_atoms, t_cap};
+  hipLaunchKernelGGL(tb_bond_sum_kernel, dim3(kStrideBlocks), dim3(256), 0, stream, lc, z3, ldz, channels, geo, scale,
+                     eps, lde);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_tb_triplet_bwd_f32(const float* geps, int64_t ldg, const float* z3, int64_t ldz, int32_t channels,
+                           const float* geo, const int32_t* line_graph, const int64_t* pair_offsets, int64_t n_atoms,
+                           int64_t t_cap, float scale, float* gz3, int64_t ldgz, float* gsw, hipStream_t stream) {
+  FMD_REQUIRE(n_atoms >= 0 && t_cap >= 0 && channels > 0 && channels <= 256 && ldg >= channels && ldz >= channels &&
+              ldgz >= channels);
+  if (n_atoms == 0 || t_cap == 0) return FMD_OK;
+  FMD_REQUIRE(geps && z3 && geo && line_graph && pair_offsets && gz3 && gsw);
+  LineCsr lc{nullptr, nullptr, nullptr, nullptr, line_graph, pair_offsets, n_atoms, t_cap};
+  hipLaunchKernelGGL(tb_triplet_bwd_kernel, dim3(kStrideBlocks), dim3(256), 0, stream, lc, geps, ldg, z3, ldz,
+                     channels, geo, scale, gz3, ldgz, gsw);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_tb_bond_reduce_f32(const float* ga3, int64_t lda, int32_t channels, const float* gsw,
+                           const int64_t* short_offsets, const int32_t* bond_rows, const int64_t* edge_triplet_offsets,
+                           const int32_t* second_perm, int64_t n_atoms, int64_t t_cap, float* geps, int64_t ldg,
+                           float* gs, hipStream_t stream) {
+  FMD_REQUIRE(n_atoms >= 0 && t_cap >= 0 && channels > 0 && channels <= 256 && lda >= 2 * channels &&
+              ldg >= channels);
+  if (n_atoms == 0 || t_cap == 0) return FMD_OK;
+  FMD_REQUIRE(ga3 && gsw && short_offsets && bond_rows && edge_triplet_offsets && second_perm && geps && gs);
+  LineCsr lc{short_offsets, bond_rows, edge_triplet_offsets, second_perm, nullptr, nullptr, n_atoms, t_cap};
+  hipLaunchKernelGGL(tb_bond_reduce_kernel, dim3(kStrideBlocks), dim3(256), 0, stream, lc, ga3, lda, channels, gsw, geps,
+                     ldg, gs);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

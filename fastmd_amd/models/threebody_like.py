@@ -23,11 +23,13 @@ Model (per layer t; atom features h [N, C], bond features eps [E, C] on every di
   readout:     E_i = e0[Z_i] + h_i . wr
 Random init from ``torch.Generator().manual_seed(seed)``.
 
-dE/dpos is formed by explicit VJP kernels (one autograd node): per layer the gated-sum VJP
-gives the pre-activation gradients, their per-segment sums and the envelope / cutoff gradients;
-by linearity the node and bond gradients are products of those per-segment sums (first bond,
-second bond, centre atom, sender) with the weight blocks, so no [T, 3C] or [E, 3C] operand
-gradient is formed. The Fourier VJP runs once over all layers' angle gradients.
+dE/dpos is formed by explicit VJP kernels (one autograd node). Atom update: the gated-sum VJP
+gives the pre-activation gradients gz2, their per-centre sums and the cutoff gradient; by
+linearity the node gradient is the product of the per-centre and per-sender sums with the weight
+blocks, so only gz2 W2c^T is formed on the edge rows. Three-body update: per triplet gz3 and the
+envelope terms, ga3 = gz3 W3^T on the triplet rows (far fewer than the edges), then per bond the
+sums over its triplets as first and as second bond, per atom over its triplets. The Fourier VJP
+runs once over all layers' angle gradients.
 """
 from __future__ import annotations
 
@@ -42,7 +44,7 @@ from fastmd_amd import _abi
 from fastmd_amd.adapters.protocol import CapacityStep, CaptureContract, GraphBatch, PaddingRule, TopologySpec
 from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr
 from fastmd_amd.ops.threebody import LineGraph, fourier_line_vjp
-from fastmd_amd.ops.wide_gemm import gemm, gemm_gather, gemm_splitk
+from fastmd_amd.ops.wide_gemm import gemm, gemm_gather, gemm_group
 
 _ELEMENTS = 118
 # pairs and triplets in tiers of 128 with at least 128 of padding, held at 1.01x the pair and 1.06x
@@ -118,13 +120,14 @@ class ThreeBodyLike(nn.Module):
         C = self.config.channels
 
         def build():
-            out = {"w3t": [], "w2t": [], "w3_bonds": [], "w3_atom": [], "w2_nodes": [], "w2_eps": []}
+            out = {"w3t": [], "w2_je_t": [], "w2_i": [], "w3_vjp": [], "w2_nodes": [], "w2_eps": []}
             for layer in self.layers:
                 W3, W2 = layer.W3.detach(), layer.W2.detach()
                 out["w3t"].append(W3[:3 * C].t().contiguous())  # [C, 3C] (N, K): the triplet GEMM
-                out["w2t"].append(W2.t().contiguous())  # [C, 3C]: the edge GEMM
-                out["w3_bonds"].append(torch.cat([W3[:C], W3[C:2 * C]], 1).contiguous())  # [C, 2C] VJP
-                out["w3_atom"].append(W3[2 * C:3 * C].contiguous())  # [C, C] VJP
+                # the edge GEMM on [h_j | eps_e] ([C, 2C] (N, K)); the centre block h_i W2b per atom
+                out["w2_je_t"].append(torch.cat([W2[:C], W2[2 * C:]], 0).t().contiguous())
+                out["w2_i"].append(W2[C:2 * C].contiguous())  # [C, C] ([K, N])
+                out["w3_vjp"].append(W3[:3 * C].contiguous())  # [3C, C] (N, K): gz3 [W3a; W3b; W3c]^T
                 out["w2_nodes"].append(torch.cat([W2[:C], W2[C:2 * C]], 1).contiguous())  # [C, 2C] VJP
                 out["w2_eps"].append(W2[2 * C:].contiguous())  # [C, C] VJP
             out["w3d"] = torch.cat([layer.W3.detach()[3 * C:] for layer in self.layers], 1).contiguous()  # [A, L C]
@@ -194,10 +197,13 @@ def _forward(ctx, positions: Tensor, cell: Tensor, model: ThreeBodyLike, inputs:
         # three-body update of the bonds: gather-cat [eps_b1 | eps_b2 | h_i] fused into the GEMM's
         # load, the angle block added per row
         z3 = gemm_gather([(eps, row1), (eps, row2), (h, atom)], lay["w3t"][t], row_add=(aw[:, t * C:(t + 1) * C], None))
-        _call("fmd_tb_gated_sum_f32", z3.data_ptr(), C, t_cap, C, geo[:, 6:].data_ptr(), 8, row1.data_ptr(),
-              row2.data_ptr(), 5, lg.edge_triplet_offsets.data_ptr(), e_cap, inv_ang, eps.data_ptr(), C, 1)
-        # atom update
-        z2 = gemm_gather([(h, ei[:, 1]), (h, ei[:, 0]), (eps, None)], lay["w2t"][t])
+        _call("fmd_tb_bond_sum_f32", z3.data_ptr(), C, C, geo.data_ptr(), lg.short_offsets.data_ptr(),
+              lg.bond_rows.data_ptr(), lg.edge_triplet_offsets.data_ptr(), lg.line_graph.data_ptr(), lg.n_atoms,
+              t_cap, inv_ang, eps.data_ptr(), C)
+        # atom update: [h_j | eps_e] gathered into the GEMM's load, the centre block h_i W2b formed
+        # once per atom and added per row
+        q2 = gemm(h, lay["w2_i"][t], b_layout=1)
+        z2 = gemm_gather([(h, ei[:, 1]), (eps, None)], lay["w2_je_t"][t], row_add=(q2, ei[:, 0]))
         _call("fmd_tb_gated_sum_f32", z2.data_ptr(), C, e_cap, C, geo[:, 4:].data_ptr(), 8, None, None, 0,
               off.data_ptr(), n, inv_avg, h.data_ptr(), C, 1)
         saved.append((z3, z2))
@@ -220,45 +226,40 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
     dev = ctx.geo.device
     geo = ctx.geo
     lay = model.layouts()
-    line = lg.line_graph
-    row1, row2 = line[:, 2], line[:, 4]
     inv_ang, inv_avg = 1.0 / cfg.avg_num_angles, 1.0 / cfg.avg_num_neighbors
     off = batch.edge_offsets
-    first = Csr(lg.edge_triplet_offsets, None, t_cap)
-    second = Csr(lg.edge_triplet_offsets, lg.second_perm)
-    per_atom = Csr(lg.pair_offsets, None, t_cap)
 
     gh = _empty(n, C, device=dev)
     _call("fmd_tb_readout_bwd_f32", _abi.ptr(gE), 1.0, model.wr.data_ptr(), C, n, gh.data_ptr(), C)
     geps = torch.zeros(e_cap, C, device=dev)
     gfc = torch.zeros(e_cap, device=dev)
-    gs = torch.zeros(e_cap, 1, device=dev)
+    gs = torch.zeros(e_cap, device=dev)
     gz3_all = _empty(t_cap, L * C, device=dev)
     gz2 = _empty(e_cap, C, device=dev)
     s_dst = _empty(n, C, device=dev)
-    s1 = _empty(e_cap, C, device=dev)
     gsw = _empty(t_cap, 2, device=dev)
+    per_atom = Csr(lg.pair_offsets, None, t_cap)
     for t in reversed(range(L)):
         z3, z2 = ctx.saved[t]
         # atom update: gz2 and its per-centre sums; the cutoff's gradient accumulates over layers
         _call("fmd_tb_gated_sum_bwd_f32", gh.data_ptr(), C, z2.data_ptr(), C, e_cap, C, geo[:, 4:].data_ptr(), 8, None,
               None, 0, off.data_ptr(), n, inv_avg, gz2.data_ptr(), C, s_dst.data_ptr(), C, gfc.data_ptr(), 1, 1)
         s_src = segment_sum_csr([(gz2, inputs.csr_src, 0, 1.0, None)], n, C)
-        # gh += [S_src | S_dst] [W2a; W2b]^T, geps += gz2 W2c^T
-        gemm_splitk(s_src, lay["w2_nodes"][t], b_layout=0, out=gh, a2=s_dst, accumulate=True)
-        gemm(gz2, lay["w2_eps"][t], b_layout=0, out=geps, accumulate=True)
-        # three-body update: gz3 (this layer's column block), its first-bond sums, envelope terms
+        # gh += [S_src | S_dst] [W2a; W2b]^T and geps += gz2 W2c^T in one launch
+        gemm_group([{"a": s_src, "a2": s_dst, "b": lay["w2_nodes"][t], "out": gh, "accumulate": True},
+                    {"a": gz2, "b": lay["w2_eps"][t], "out": geps, "accumulate": True}], b_layout=0)
+        # three-body update: gz3 per triplet (this layer's column block) and its envelope terms,
+        # ga3 = gz3 [W3a; W3b; W3c]^T on the triplet rows, then per bond the sums of its triplets as
+        # first and second bond into geps (and gs), per atom those of its triplets into gh
         gz3 = gz3_all[:, t * C:(t + 1) * C]
-        _call("fmd_tb_gated_sum_bwd_f32", geps.data_ptr(), C, z3.data_ptr(), C, t_cap, C, geo[:, 6:].data_ptr(), 8,
-              row1.data_ptr(), row2.data_ptr(), 5, lg.edge_triplet_offsets.data_ptr(), e_cap, inv_ang,
-              gz3.data_ptr(), L * C, s1.data_ptr(), C, gsw.data_ptr(), 2, 0)
-        s2 = segment_sum_csr([(gz3, second, 0, 1.0, None)], e_cap, C)
-        s3 = segment_sum_csr([(gz3, per_atom, 0, 1.0, None)], n, C)
-        # geps += [S1 | S2] [W3a; W3b]^T, gh += S3 W3c^T, the envelopes' gradient
-        gemm_splitk(s1, lay["w3_bonds"][t], b_layout=0, out=geps, a2=s2, accumulate=True)
-        gemm(s3, lay["w3_atom"][t], b_layout=0, out=gh, accumulate=True)
-        segment_sum_csr([(gsw, first, 0, 1.0, None), (gsw, second, 1, 1.0, None)], e_cap, 1, out=gs,
-                        accumulate=True)
+        _call("fmd_tb_triplet_bwd_f32", geps.data_ptr(), C, z3.data_ptr(), C, C, geo.data_ptr(),
+              lg.line_graph.data_ptr(), lg.pair_offsets.data_ptr(), n, t_cap, inv_ang, gz3.data_ptr(), L * C,
+              gsw.data_ptr())
+        ga3 = gemm(gz3, lay["w3_vjp"][t], b_layout=0)  # [T, 3C]
+        _call("fmd_tb_bond_reduce_f32", ga3.data_ptr(), 3 * C, C, gsw.data_ptr(), lg.short_offsets.data_ptr(),
+              lg.bond_rows.data_ptr(), lg.edge_triplet_offsets.data_ptr(), lg.second_perm.data_ptr(), n, t_cap,
+              geps.data_ptr(), C, gs.data_ptr())
+        segment_sum_csr([(ga3, per_atom, 2 * C, 1.0, None)], n, C, out=gh, accumulate=True)
     # the angle basis: all layers' angle gradients at once, then the Fourier VJP (short rows)
     galpha = gemm(gz3_all, lay["w3d"], b_layout=0)  # [T, A]
     gu = torch.zeros(e_cap, 3, device=dev)

@@ -180,6 +180,26 @@ int fmd_tb_gated_sum_bwd_f32(const float* gout, int64_t ldg, const float* z, int
                              const int32_t* index2, int64_t ld_index, const int64_t* offsets, int64_t n_segments,
                              float scale, float* gz, int64_t ldgz, float* gsum, int64_t ldgs, float* gw, int64_t ldgw,
                              int32_t accumulate_gw, hipStream_t stream);
+/* The angle -> bond sums over a line graph of fmd_nl_line_graph (its segment layouts: the bonds
+ * bond_rows[0, short_offsets[n]), a bond's triplets as first bond the run [eto[b], eto[b+1]), as
+ * second bond the same run through second_perm), a fixed grid striding over the real bonds /
+ * triplets, every sum in triplet order. The reference's triplet gather + segment sums
+ * (fastmd/models/matris/op/triton_weighted_segment_sum.py, triton_csr_segment_sum.py:433-479).
+ * Forward: eps[b] += scale * sum over b's triplets k of silu(z3[k]) s_b s_b2 (s = geo column 6). */
+int fmd_tb_bond_sum_f32(const float* z3, int64_t ldz, int32_t channels, const float* geo, const int64_t* short_offsets,
+                        const int32_t* bond_rows, const int64_t* edge_triplet_offsets, const int32_t* line_graph,
+                        int64_t n_atoms, int64_t t_cap, float scale, float* eps, int64_t lde, hipStream_t stream);
+/* VJP per triplet: gz3[k] = scale geps[b1] s_b1 s_b2 silu'(z3[k]) (0 past the real triplets) and
+ * the envelope terms gsw [t_cap, 2] = (gw s_b2, gw s_b1), gw = sum_c scale geps[b1] silu(z3[k]). */
+int fmd_tb_triplet_bwd_f32(const float* geps, int64_t ldg, const float* z3, int64_t ldz, int32_t channels,
+                           const float* geo, const int32_t* line_graph, const int64_t* pair_offsets, int64_t n_atoms,
+                           int64_t t_cap, float scale, float* gz3, int64_t ldgz, float* gsw, hipStream_t stream);
+/* VJP per bond: geps[b] += sum over b's triplets as first bond of ga3[k, 0:C] + as second bond of
+ * ga3[k, C:2C] (ga3 = gz3 [W_b1; W_b2]^T); gs[b] += the same sums of gsw[k, 0] and gsw[k, 1]. */
+int fmd_tb_bond_reduce_f32(const float* ga3, int64_t lda, int32_t channels, const float* gsw,
+                           const int64_t* short_offsets, const int32_t* bond_rows, const int64_t* edge_triplet_offsets,
+                           const int32_t* second_perm, int64_t n_atoms, int64_t t_cap, float* geps, int64_t ldg,
+                           float* gs, hipStream_t stream);
 /* energy[i] = e0[elem[i]] + h[i] . wr, and its VJP gh[i] = (gE ? gE[i] : sign) * wr. */
 int fmd_tb_readout_f32(const float* h, int64_t ldh, int32_t channels, const float* wr, const int32_t* elem,
                        const float* e0, int64_t n, float* energy, hipStream_t stream);

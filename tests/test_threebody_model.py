@@ -174,3 +174,64 @@ def test_threebody_gpu_matches_oracle(device, n_cells, bond_cutoff):
         (grad,) = torch.autograd.grad(energy, (leaf,))
     assert torch.equal(energy.detach().reshape(1), out["e"])
     assert torch.equal(-grad, out["f"][0])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("two_index", [False, True])
+def test_gated_segment_sum_and_vjp(device, two_index):
+    """fmd_tb_gated_sum_f32 / _bwd_f32 (both weight forms) against float64 torch: the sums, the
+    pre-activation and weight gradients, the per-segment gradient sums; rows past the last run
+    get zero gradients."""
+    from fastmd_amd import _abi
+
+    gen = torch.Generator().manual_seed(3)
+    rows, n_seg, C, nw = 3000, 400, 128, 500
+    counts = torch.randint(0, 12, (n_seg,), generator=gen)
+    off = torch.zeros(n_seg + 1, dtype=torch.int64)
+    off[1:] = torch.cumsum(counts, 0)
+    used = int(off[-1])
+    assert used < rows
+    z = torch.randn(rows, C, generator=gen)
+    w = torch.rand(nw, 2, generator=gen)  # column 0 is the weight, stride 2
+    idx = torch.randint(0, nw, (rows, 3), generator=gen, dtype=torch.int32)
+    g = torch.randn(n_seg, C, generator=gen)
+    scale = 0.37
+    seg = torch.repeat_interleave(torch.arange(n_seg), counts)
+    z64 = z[:used].double().requires_grad_(True)
+    w64 = w[:, 0].double().requires_grad_(True)
+    wr = w64[idx[:used, 0].long()] * (w64[idx[:used, 2].long()] if two_index else 1.0)
+    out64 = torch.zeros(n_seg, C, dtype=torch.float64).index_add(
+        0, seg, torch.nn.functional.silu(z64) * wr[:, None]) * scale
+    (out64 * g.double()).sum().backward()
+    zd, wd, idd, offd, gd = (t.to(device) for t in (z, w, idx, off, g))
+    out = torch.full((n_seg, C), 1.5, device=device)
+    i2 = idd[:, 2].data_ptr() if two_index else None
+    _abi.call("fmd_tb_gated_sum_f32", zd.data_ptr(), C, rows, C, wd.data_ptr(), 2, idd[:, 0].data_ptr(), i2, 3,
+              offd.data_ptr(), n_seg, scale, out.data_ptr(), C, 1, _abi.stream_handle())
+    gz = torch.full((rows, C), 7.0, device=device)
+    gsum = torch.empty(n_seg, C, device=device)
+    gw = torch.full((rows, 2), 9.0, device=device)
+    _abi.call("fmd_tb_gated_sum_bwd_f32", gd.data_ptr(), C, zd.data_ptr(), C, rows, C, wd.data_ptr(), 2,
+              idd[:, 0].data_ptr(), i2, 3, offd.data_ptr(), n_seg, scale, gz.data_ptr(), C, gsum.data_ptr(), C,
+              gw.data_ptr(), 2, 0, _abi.stream_handle())
+    torch.cuda.synchronize()
+    assert torch.allclose(out.cpu().double() - 1.5, out64.detach(), atol=1e-5, rtol=1e-5)
+    assert torch.allclose(gz[:used].cpu().double(), z64.grad, atol=1e-5, rtol=1e-5)
+    assert not gz[used:].any()
+    assert torch.allclose(gsum.cpu().double(), torch.zeros(n_seg, C, dtype=torch.float64).index_add(
+        0, seg, z64.grad), atol=1e-4, rtol=1e-5)
+    # the weight's gradient from its per-row terms
+    silu_g = (torch.nn.functional.silu(z64.detach()) * (g.double() * scale)[seg]).sum(1)
+    if two_index:
+        a, b = w64.detach()[idx[:used, 0].long()], w64.detach()[idx[:used, 2].long()]
+        assert torch.allclose(gw[:used, 0].cpu().double(), silu_g * b, atol=1e-4, rtol=1e-5)
+        assert torch.allclose(gw[:used, 1].cpu().double(), silu_g * a, atol=1e-4, rtol=1e-5)
+        assert not gw[used:].any()
+    else:
+        assert torch.allclose(gw[:used, 0].cpu().double(), silu_g, atol=1e-4, rtol=1e-5)
+        assert not gw[used:, 0].any()
+    gw_total = torch.zeros(nw, dtype=torch.float64)
+    gw_total.index_add_(0, idx[:used, 0].long(), gw[:used, 0].cpu().double())
+    if two_index:
+        gw_total.index_add_(0, idx[:used, 2].long(), gw[:used, 1].cpu().double())
+    assert torch.allclose(gw_total, w64.grad, atol=1e-3, rtol=1e-5)
