@@ -205,7 +205,8 @@ __global__ void tb_readout_bwd_kernel(const float* ge, float sign, const float* 
 // gvec = gr u + (gu - (gu . u) u) / r with gr = sum_n gef def + gfc dfc + gs ds
 __global__ void tb_geometry_bwd_kernel(const float* geo, const float* def, int nb, const float* gef, int64_t ldgef,
                                        const float* gu, int64_t ldgu, const float* gfc, const float* gs,
-                                       const int64_t* n_edges, int64_t e_cap, float* gvec) {
+                                       const uint8_t* bond_flags, const int64_t* n_edges, int64_t e_cap,
+                                       float* gvec) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= e_cap) return;
   if (e >= tb_real_rows(n_edges, e_cap)) {
@@ -217,9 +218,11 @@ __global__ void tb_geometry_bwd_kernel(const float* geo, const float* def, int n
   if (gef)
     for (int n = 0; n < nb; ++n) gr += gef[e * ldgef + n] * def[e * nb + n];
   if (gfc) gr += gfc[e] * g[5];
-  if (gs) gr += gs[e] * g[7];
+  // gs and gu hold values on the bond rows only (with bond_flags; else on every row)
+  const bool bond = bond_flags ? bond_flags[e] != 0 : true;
+  if (gs && bond) gr += gs[e] * g[7];
   float v[3] = {0.f, 0.f, 0.f};
-  if (gu) {
+  if (gu && bond) {
     v[0] = gu[e * ldgu];
     v[1] = gu[e * ldgu + 1];
     v[2] = gu[e * ldgu + 2];
@@ -338,9 +341,11 @@ __global__ void __launch_bounds__(256) tb_triplet_bwd_kernel(LineCsr lc, const f
 }
 
 // Per bond b (one wave): geps[b] += sum over b's triplets as first bond of ga3[k, 0:C], then as
-// second bond of ga3[k, C:2C]; gs[b] += the same sums of gsw[k, 0] and gsw[k, 1].
+// second bond of ga3[k, C:2C]; gs[b] (+)= the same sums of gsw[k, 0] and gsw[k, 1] (stored, or
+// added with acc_gs).
 __global__ void __launch_bounds__(256) tb_bond_reduce_kernel(LineCsr lc, const float* ga3, int64_t lda, int C,
-                                                              const float* gsw, float* geps, int64_t ldg, float* gs) {
+                                                              const float* gsw, float* geps, int64_t ldg, float* gs,
+                                                              int acc_gs) {
   const int lane = threadIdx.x & 63;
   const int nc = (C + 63) / 64;
   const int64_t nb = lc.short_offsets[lc.n];
@@ -383,7 +388,7 @@ __global__ void __launch_bounds__(256) tb_bond_reduce_kernel(LineCsr lc, const f
       const int c = lane + 64 * cc;
       if (cc < nc && c < C) geps[b * ldg + c] += acc[cc];
     }
-    if (lane == 0) gs[b] += gsum;
+    if (lane == 0) gs[b] = (acc_gs ? gs[b] : 0.f) + gsum;
   }
 }
 
@@ -472,14 +477,14 @@ int fmd_tb_triplet_bwd_f32(const float* geps, int64_t ldg, const float* z3, int6
 int fmd_tb_bond_reduce_f32(const float* ga3, int64_t lda, int32_t channels, const float* gsw,
                            const int64_t* short_offsets, const int32_t* bond_rows, const int64_t* edge_triplet_offsets,
                            const int32_t* second_perm, int64_t n_atoms, int64_t t_cap, float* geps, int64_t ldg,
-                           float* gs, hipStream_t stream) {
+                           float* gs, int32_t accumulate_gs, hipStream_t stream) {
   FMD_REQUIRE(n_atoms >= 0 && t_cap >= 0 && channels > 0 && channels <= 256 && lda >= 2 * channels &&
               ldg >= channels);
   if (n_atoms == 0 || t_cap == 0) return FMD_OK;
   FMD_REQUIRE(ga3 && gsw && short_offsets && bond_rows && edge_triplet_offsets && second_perm && geps && gs);
   LineCsr lc{short_offsets, bond_rows, edge_triplet_offsets, second_perm, nullptr, nullptr, n_atoms, t_cap};
   hipLaunchKernelGGL(tb_bond_reduce_kernel, dim3(kStrideBlocks), dim3(256), 0, stream, lc, ga3, lda, channels, gsw, geps,
-                     ldg, gs);
+                     ldg, gs, accumulate_gs);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -507,15 +512,15 @@ int fmd_tb_readout_bwd_f32(const float* gE, float sign, const float* wr, int32_t
 }
 
 int fmd_tb_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, const float* gef, int64_t ldgef,
-                            const float* gu, int64_t ldgu, const float* gfc, const float* gs, const int64_t* n_edges,
-                            int64_t e_cap, float* gvec, hipStream_t stream) {
+                            const float* gu, int64_t ldgu, const float* gfc, const float* gs, const uint8_t* bond_flags,
+                            const int64_t* n_edges, int64_t e_cap, float* gvec, hipStream_t stream) {
   FMD_REQUIRE(e_cap >= 0 && nb > 0);
   if (e_cap == 0) return FMD_OK;
   FMD_REQUIRE(geo && def && n_edges && gvec);
   FMD_REQUIRE(!gef || ldgef >= nb);
   FMD_REQUIRE(!gu || ldgu >= 3);
   hipLaunchKernelGGL(tb_geometry_bwd_kernel, dim3((unsigned)fmd_cdiv(e_cap, 256)), dim3(256), 0, stream, geo, def, nb,
-                     gef, ldgef, gu, ldgu, gfc, gs, n_edges, e_cap, gvec);
+                     gef, ldgef, gu, ldgu, gfc, gs, bond_flags, n_edges, e_cap, gvec);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -231,9 +231,10 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
 
     gh = _empty(n, C, device=dev)
     _call("fmd_tb_readout_bwd_f32", _abi.ptr(gE), 1.0, model.wr.data_ptr(), C, n, gh.data_ptr(), C)
-    geps = torch.zeros(e_cap, C, device=dev)
-    gfc = torch.zeros(e_cap, device=dev)
-    gs = torch.zeros(e_cap, device=dev)
+    # stored by the first layer the loop takes (the last), added to by the others: no zero fills
+    geps = _empty(e_cap, C, device=dev)
+    gfc = _empty(e_cap, device=dev)
+    gs = _empty(e_cap, device=dev)  # written on the bond rows only (read there only)
     gz3_all = _empty(t_cap, L * C, device=dev)
     gz2 = _empty(e_cap, C, device=dev)
     s_dst = _empty(n, C, device=dev)
@@ -241,13 +242,15 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
     per_atom = Csr(lg.pair_offsets, None, t_cap)
     for t in reversed(range(L)):
         z3, z2 = ctx.saved[t]
+        first = t == L - 1
         # atom update: gz2 and its per-centre sums; the cutoff's gradient accumulates over layers
         _call("fmd_tb_gated_sum_bwd_f32", gh.data_ptr(), C, z2.data_ptr(), C, e_cap, C, geo[:, 4:].data_ptr(), 8, None,
-              None, 0, off.data_ptr(), n, inv_avg, gz2.data_ptr(), C, s_dst.data_ptr(), C, gfc.data_ptr(), 1, 1)
+              None, 0, off.data_ptr(), n, inv_avg, gz2.data_ptr(), C, s_dst.data_ptr(), C, gfc.data_ptr(), 1,
+              0 if first else 1)
         s_src = segment_sum_csr([(gz2, inputs.csr_src, 0, 1.0, None)], n, C)
         # gh += [S_src | S_dst] [W2a; W2b]^T and geps += gz2 W2c^T in one launch
         gemm_group([{"a": s_src, "a2": s_dst, "b": lay["w2_nodes"][t], "out": gh, "accumulate": True},
-                    {"a": gz2, "b": lay["w2_eps"][t], "out": geps, "accumulate": True}], b_layout=0)
+                    {"a": gz2, "b": lay["w2_eps"][t], "out": geps, "accumulate": not first}], b_layout=0)
         # three-body update: gz3 per triplet (this layer's column block) and its envelope terms,
         # ga3 = gz3 [W3a; W3b; W3c]^T on the triplet rows, then per bond the sums of its triplets as
         # first and second bond into geps (and gs), per atom those of its triplets into gh
@@ -258,16 +261,16 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
         ga3 = gemm(gz3, lay["w3_vjp"][t], b_layout=0)  # [T, 3C]
         _call("fmd_tb_bond_reduce_f32", ga3.data_ptr(), 3 * C, C, gsw.data_ptr(), lg.short_offsets.data_ptr(),
               lg.bond_rows.data_ptr(), lg.edge_triplet_offsets.data_ptr(), lg.second_perm.data_ptr(), n, t_cap,
-              geps.data_ptr(), C, gs.data_ptr())
+              geps.data_ptr(), C, gs.data_ptr(), 0 if first else 1)
         segment_sum_csr([(ga3, per_atom, 2 * C, 1.0, None)], n, C, out=gh, accumulate=True)
     # the angle basis: all layers' angle gradients at once, then the Fourier VJP (short rows)
     galpha = gemm(gz3_all, lay["w3d"], b_layout=0)  # [T, A]
-    gu = torch.zeros(e_cap, 3, device=dev)
+    gu = _empty(e_cap, 3, device=dev)  # written on the bond rows only (read there only)
     fourier_line_vjp(galpha, geo[:, :3], lg, model.freqs, model.fourier_scale, out=gu, accumulate=False)
     gef = gemm(geps, model.We, b_layout=0)  # [E, nb]
     gvec = _empty(e_cap, 3, device=dev)
     _call("fmd_tb_geometry_bwd_f32", geo.data_ptr(), ctx.de.data_ptr(), nb, gef.data_ptr(), nb, gu.data_ptr(), 3,
-          gfc.data_ptr(), gs.data_ptr(), batch.n_edges.data_ptr(), e_cap, gvec.data_ptr())
+          gfc.data_ptr(), gs.data_ptr(), lg.short_flags.data_ptr(), batch.n_edges.data_ptr(), e_cap, gvec.data_ptr())
     return segment_sum_csr([(gvec, inputs.csr_src, 0, sign, None), (gvec, inputs.csr_dst, 0, -sign, None)], n, 3)
 
 

@@ -195,21 +195,23 @@ int fmd_tb_triplet_bwd_f32(const float* geps, int64_t ldg, const float* z3, int6
                            const float* geo, const int32_t* line_graph, const int64_t* pair_offsets, int64_t n_atoms,
                            int64_t t_cap, float scale, float* gz3, int64_t ldgz, float* gsw, hipStream_t stream);
 /* VJP per bond: geps[b] += sum over b's triplets as first bond of ga3[k, 0:C] + as second bond of
- * ga3[k, C:2C] (ga3 = gz3 [W_b1; W_b2]^T); gs[b] += the same sums of gsw[k, 0] and gsw[k, 1]. */
+ * ga3[k, C:2C] (ga3 = gz3 [W_b1; W_b2]^T); gs[b] = (or += with accumulate_gs) the same sums of
+ * gsw[k, 0] and gsw[k, 1]. Rows that are no bond are not written. */
 int fmd_tb_bond_reduce_f32(const float* ga3, int64_t lda, int32_t channels, const float* gsw,
                            const int64_t* short_offsets, const int32_t* bond_rows, const int64_t* edge_triplet_offsets,
                            const int32_t* second_perm, int64_t n_atoms, int64_t t_cap, float* geps, int64_t ldg,
-                           float* gs, hipStream_t stream);
+                           float* gs, int32_t accumulate_gs, hipStream_t stream);
 /* energy[i] = e0[elem[i]] + h[i] . wr, and its VJP gh[i] = (gE ? gE[i] : sign) * wr. */
 int fmd_tb_readout_f32(const float* h, int64_t ldh, int32_t channels, const float* wr, const int32_t* elem,
                        const float* e0, int64_t n, float* energy, hipStream_t stream);
 int fmd_tb_readout_bwd_f32(const float* gE, float sign, const float* wr, int32_t channels, int64_t n, float* gh,
                            int64_t ldgh, hipStream_t stream);
 /* gvec [e_cap, 3] = gr u + (gu - (gu . u) u) / r per real row (0 on padding), gr = sum_n gef def +
- * gfc dfc + gs ds (each term nullable). */
+ * gfc dfc + gs ds (each term nullable); with bond_flags (nullable) gu and gs are read on the flagged
+ * rows only (the bonds of a line graph, the rows the three-body VJP writes). */
 int fmd_tb_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, const float* gef, int64_t ldgef,
-                            const float* gu, int64_t ldgu, const float* gfc, const float* gs, const int64_t* n_edges,
-                            int64_t e_cap, float* gvec, hipStream_t stream);
+                            const float* gu, int64_t ldgu, const float* gfc, const float* gs, const uint8_t* bond_flags,
+                            const int64_t* n_edges, int64_t e_cap, float* gvec, hipStream_t stream);
 
 /* Reverse edge of every real row e < min(E, e_cap): the row of (neighbour, centre, -image),
  * or -1 when it is not stored (overflowed build). Gives the sender-side CSR of the sorted
