@@ -36,9 +36,9 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_md(n_atoms: int, steps_per_launch: int, bond_cutoff: float | None = None):
-    """The whole-step MD of a perovskite: the MACE-like model, or with ``bond_cutoff`` the
-    configs[4] three-body model (64 channels, 4 layers, that bond-graph cutoff)."""
+def build_md(n_atoms: int, steps_per_launch: int, bond_cutoff: float | None = None, execution: str = "whole_step"):
+    """The MD of a perovskite (whole-step by default): the MACE-like model, or with
+    ``bond_cutoff`` the configs[4] three-body model (64 channels, 4 layers, that bond cutoff)."""
     import torch
 
     from fastmd_amd import systems
@@ -53,7 +53,7 @@ def build_md(n_atoms: int, steps_per_launch: int, bond_cutoff: float | None = No
              ThreeBodyAdapter(config=ThreeBodyConfig(bond_cutoff=bond_cutoff), device=device))
     return GPUResidentMolecularDynamics(s, model=model, device=device, temperature=500.0,
                                         timestep=0.25, tdamp=25.0, tchain=3, tloop=1,
-                                        config=InferenceConfig(execution="whole_step"),
+                                        config=InferenceConfig(execution=execution),
                                         steps_per_launch=steps_per_launch)
 
 
@@ -317,6 +317,31 @@ def threebody_bench(steps: int, warmup: int) -> list:
     return out
 
 
+def model_graph_bench(steps: int, warmup: int) -> list:
+    """The model_graph execution mode (ragged build and integrator eager, the model's forward + VJP
+    replayed per capacity bucket) of the MACE-like model at 135 and 10 000 atoms."""
+    import torch
+
+    out = []
+    for n_atoms in (135, 10000):
+        md = build_md(n_atoms, 1, execution="model_graph")
+        md.run(warmup)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        md.run(steps)
+        torch.cuda.synchronize()
+        t = time.perf_counter() - t0
+        st = md.model_graph_stats()
+        row = {"atoms": n_atoms, "steps": steps, "warmup": warmup, "ms_per_step": round(t / steps * 1e3, 4),
+               "atom_steps_per_s": round(n_atoms * steps / t, 1), "captures": st["captures"],
+               "cached_buckets": st["cached_buckets"]}
+        log(f"model_graph N={n_atoms}: {row['ms_per_step']} ms/step, {st['captures']} captures")
+        out.append(row)
+        del md
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(n_atoms: int, budget_s: float) -> dict:
     """The CPU oracle (PyTorch-CPU eager model forward+backward with index_select/index_add_/matmul,
     NumPy neighbour list and NHC) on this host, whole MD steps until ``budget_s`` elapsed."""
@@ -395,6 +420,8 @@ def main() -> int:
     parser.add_argument("--warmup-threebody", type=int, default=2000,
                         help="untimed three-body steps (the random-init potential keeps adding edges and triplets "
                              "for the first ~2 000 steps, each growth a recapture)")
+    parser.add_argument("--model-graph", action="store_true",
+                        help="only the model_graph execution mode (MACE-like, 135 and 10 000 atoms)")
     parser.add_argument("--roofline-only", action="store_true",
                         help="only the dominant kernel at the 10 000-atom shape plus a 256 MiB copy (--pmc runs)")
     args = parser.parse_args()
@@ -416,6 +443,9 @@ def main() -> int:
         return 0
     if args.threebody:
         print(json.dumps({"threebody": threebody_bench(args.steps_threebody, args.warmup_threebody)}), flush=True)
+        return 0
+    if args.model_graph:
+        print(json.dumps({"model_graph": model_graph_bench(200, 200)}), flush=True)
         return 0
     if args.ops:
         print(json.dumps({"ops_sweep": ops_sweep(), "hbm_peak_GBps": HBM_PEAK_GBPS,
@@ -460,6 +490,9 @@ def main() -> int:
     threebody = threebody_bench(200 if args.quick else args.steps_threebody,
                                 200 if args.quick else args.warmup_threebody)
 
+    log("model_graph mode")
+    model_graph = model_graph_bench(50 if args.quick else 200, 50 if args.quick else 200)
+
     log("memory-bound operator microbenchmarks")
     seg = hbm_ops_bench()
     cpu = None
@@ -493,6 +526,7 @@ def main() -> int:
                          "atom_steps_per_s": round(135 / (ms_small / 1e3), 1), "steps": steps_small,
                          "e_capacity": stats_small["e_capacity"], "timed_events": events_small},
         "threebody_5000": threebody,
+        "model_graph": model_graph,
         "segment_sum_GBps": seg["segment_sum"]["GBps"],
         "hbm_ops_40k": seg,
         "whole_step_stats_10k": {**{k: stats_big[k] for k in ("candidate_refreshes", "fallback_windows",

@@ -54,6 +54,7 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_tb_readout_bwd_f32": (ctypes.c_int, [_p, _f32, _p, _i32, _i64, _p, _i64, _p]),
     "fmd_tb_geometry_bwd_f32": (ctypes.c_int, [_p, _p, _i32, _p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _p, _p]),
     "fmd_nl_reverse": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i64, _p, _p]),
+    "fmd_nl_pad_rows": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p]),
     "fmd_nl_window_flags": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p]),
     "fmd_gather_cat_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _i64, _p, _i64, _p]),
     "fmd_segsum_csr_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32,

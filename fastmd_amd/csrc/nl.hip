@@ -845,6 +845,31 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
   return FMD_OK;
 }
 
+// padded rows of a bucket workspace: rows [e_real, e_cap) become far self-loops of atom
+// (row - e_real) mod n (the builder's own padding rule), with no reverse row
+__global__ void nl_pad_rows_kernel(int32_t* edge_index, float* edge_image, int32_t* edge_reverse, int64_t e_real,
+                                   int64_t e_cap, int64_t n, int32_t ix, int32_t iy, int32_t iz) {
+  const int64_t row = e_real + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= e_cap) return;
+  const int32_t atom = (int32_t)((row - e_real) % n);
+  edge_index[2 * row] = atom;
+  edge_index[2 * row + 1] = atom;
+  edge_image[3 * row] = (float)ix;
+  edge_image[3 * row + 1] = (float)iy;
+  edge_image[3 * row + 2] = (float)iz;
+  if (edge_reverse) edge_reverse[row] = -1;
+}
+
+int fmd_nl_pad_rows(int32_t* edge_index, float* edge_image, int32_t* edge_reverse, int64_t e_real, int64_t e_cap,
+                    int64_t n_atoms, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz, hipStream_t stream) {
+  FMD_REQUIRE(e_real >= 0 && e_real <= e_cap && n_atoms > 0 && edge_index && edge_image);
+  if (e_real == e_cap) return FMD_OK;
+  hipLaunchKernelGGL(nl_pad_rows_kernel, dim3((unsigned)fmd_cdiv(e_cap - e_real, 256)), dim3(256), 0, stream,
+                     edge_index, edge_image, edge_reverse, e_real, e_cap, n_atoms, pad_ix, pad_iy, pad_iz);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
 int fmd_nl_reverse(const int32_t* center, const int32_t* neighbor, const int32_t* images, const int64_t* edge_offsets,
                    int64_t n_atoms, int64_t e_cap, int32_t* reverse, hipStream_t stream) {
   FMD_REQUIRE(n_atoms > 0 && e_cap > 0 && center && neighbor && images && edge_offsets && reverse);

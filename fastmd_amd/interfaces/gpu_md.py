@@ -9,9 +9,11 @@ the Nose-Hoover chain ensemble and an energy-tap model adapter. ``atoms`` is an 
 
 Execution modes (``InferenceConfig.execution``):
   ``eager``       per step: ragged exact neighbour list (host syncs) -> model -> NHC halves;
+  ``model_graph`` per step: ragged build -> the model's forward + VJP replayed as the hipGraph of
+                  the capacity bucket that holds it (``execution.cuda_graph.BucketedGraphRunner``)
+                  -> NHC halves (gpu_md.py:435-446, 560-590);
   ``whole_step``  the whole step captured as one hipGraph per capacity tier, replayed per
-                  window of ``steps_per_launch`` steps (``auto`` selects it);
-  ``model_graph`` is the reference's bucketed model graph; it is not offered (ValueError).
+                  window of ``steps_per_launch`` steps (``auto`` selects it).
 Units: ``timestep``, ``tdamp`` in fs, ``temperature`` in K (ASE units inside).
 """
 from __future__ import annotations
@@ -63,8 +65,6 @@ class GPUResidentMolecularDynamics:
             raise ValueError("GPUResidentMolecularDynamics: steps_per_launch must be a positive integer")
         self.config = config or InferenceConfig()
         self.execution = self.config.resolved_execution
-        if self.execution == "model_graph":
-            raise ValueError("execution='model_graph' is not offered by this build: use 'whole_step' or 'eager'")
         self.device = torch.device(device)
         if self.device.index is None:
             self.device = torch.device("cuda", torch.cuda.current_device())
@@ -99,6 +99,7 @@ class GPUResidentMolecularDynamics:
                                                 atom_graph_cutoff=self.cutoff, device=self.device,
                                                 check_isolated_atoms=False)
         self._eager_line = None  # the eager path's line-graph builder and its capacity
+        self.model_runner = None  # model_graph: the bucketed model graphs
         self.steps = 0
         self.whole_step_runner: WholeStepGraphRunner | None = None
         self.capacity_policy = None
@@ -107,6 +108,8 @@ class GPUResidentMolecularDynamics:
         self.whole_step_triplet_capacity_history: list[int] = []
         self._retired_stats: dict = {}
         self._graph_pool = None
+        if self.execution == "model_graph":
+            self.enable_model_cuda_graph()
         # F(q0) for the first pre-force half
         forces, energy = self.evaluate(self.integrator.positions)
         self.integrator.set_forces(forces, energy=energy)
@@ -116,8 +119,22 @@ class GPUResidentMolecularDynamics:
     # ------------------------------------------------------------------ eager evaluation
     def evaluate(self, positions: Tensor | None = None) -> tuple[Tensor, Tensor]:
         """(forces float32 [N, 3], energy float64 [1]) at ``positions`` (default: the current
-        state), through a ragged exact neighbour list (eager, host syncs)."""
+        state), through a ragged exact neighbour list (eager, host syncs); in the model_graph
+        mode by the replay of the bucket's model graph (copies: the graph's outputs are reused)."""
+        forces, energy = self._evaluate(positions)
+        if self.model_runner is not None:
+            return forces.clone(), energy.clone()
+        return forces, energy
+
+    def _evaluate(self, positions: Tensor | None = None) -> tuple[Tensor, Tensor]:
         q = self.integrator.positions if positions is None else positions
+        if self.model_runner is not None:
+            batch = self.graph_builder.build(q)
+            if self.validate_isolated_atoms:
+                counts = torch.diff(batch.edge_offsets)
+                raise_if_isolated_atoms(int((counts == 0).sum().item()))
+            out, n = self.model_runner.run(batch, positions=q)
+            return out["f"][0][:n].detach(), out["e"].detach()
         batch = self._eager_batch(q)
         if self.validate_isolated_atoms:
             counts = torch.diff(batch.edge_offsets)
@@ -126,12 +143,33 @@ class GPUResidentMolecularDynamics:
         out = self.derivative(batch, inputs, task=self.task, n_real=self.n_atoms)
         return out["f"][0][: self.n_atoms].detach(), out["e"].detach()
 
+    def enable_model_cuda_graph(self) -> None:
+        """The model_graph mode (gpu_md.py:560-590): the model's forward + VJP as one graph per
+        capacity bucket, the ragged build and the integrator eager."""
+        if self.whole_step_runner is not None:
+            raise ValueError("cannot enable model replay with a whole-step runner")
+        if self.model_runner is not None:
+            return
+        from fastmd_amd.execution.cuda_graph import BucketedGraphRunner
+
+        cap = self.config.capacity
+        u_step, min_pad, _ = self._capacity_step()
+        t_step, t_pad, _ = self._triplet_step() if self.triplet_cutoff is not None else (cap.t_step, cap.min_pad_t, 1.0)
+        self.model_runner = BucketedGraphRunner(self.adapter, task=self.task, u_step=u_step, t_step=t_step,
+                                                n_dummy=cap.n_dummy, min_pad_u=min_pad, warmup=cap.warmup,
+                                                min_pad_t=t_pad, candidate_skin=cap.candidate_skin, device=self.device)
+
+    def model_graph_stats(self) -> dict:
+        if self.model_runner is None:
+            raise RuntimeError("the model_graph mode is not enabled")
+        return self.model_runner.stats()
+
     def step(self) -> None:
         """One eager MD step (integrator halves around a fresh evaluation)."""
         if self.whole_step_runner is not None:
             raise RuntimeError("step() is the eager path; the whole-step mode runs windows through run()")
         q = self.integrator.step_pre_force()
-        forces, energy = self.evaluate(q)
+        forces, energy = self._evaluate(q)
         self.integrator.step_post_force(forces, energy=energy)
         self.steps += 1
 

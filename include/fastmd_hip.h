@@ -213,6 +213,13 @@ int fmd_tb_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, cons
                             const float* gu, int64_t ldgu, const float* gfc, const float* gs, const uint8_t* bond_flags,
                             const int64_t* n_edges, int64_t e_cap, float* gvec, hipStream_t stream);
 
+/* The padded rows of a model-graph bucket workspace (gpu_md.py model_graph, cuda_graph.py:209-293
+ * _PaddedEdgesWorkspace.update): rows [e_real, e_cap) of a ragged build copied into a fixed
+ * capacity become the builder's far self-loops of atom (row - e_real) mod n_atoms with the pad
+ * image, edge_reverse -1 (nullable). */
+int fmd_nl_pad_rows(int32_t* edge_index, float* edge_image, int32_t* edge_reverse, int64_t e_real, int64_t e_cap,
+                    int64_t n_atoms, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz, hipStream_t stream);
+
 /* Reverse edge of every real row e < min(E, e_cap): the row of (neighbour, centre, -image),
  * or -1 when it is not stored (overflowed build). Gives the sender-side CSR of the sorted
  * edge list (perm = reverse, off = edge_offsets), used by the deterministic VJPs. No

@@ -12,6 +12,7 @@ from fastmd_amd.config import CapacityConfig, InferenceConfig
 def test_inference_config_contract():
     assert InferenceConfig().resolved_execution == "whole_step"
     assert InferenceConfig(execution="eager").resolved_execution == "eager"
+    assert InferenceConfig(execution="model_graph").resolved_execution == "model_graph"
     with pytest.raises(ValueError):
         InferenceConfig(execution="fast")
     with pytest.raises(ValueError):
@@ -104,6 +105,32 @@ def test_whole_step_capacity_growth_and_refresh_paths(device):
     st = graph.whole_step_stats()
     print(st, flush=True)
     assert st["candidate_refreshes"] > 2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("model_name", ["morse", "mace_like", "threebody"])
+def test_model_graph_equals_eager_bitwise(device, model_name):
+    """The model_graph mode (the model's forward + VJP replayed per capacity bucket, the ragged
+    build and the integrator eager) gives the eager trajectory bitwise; a tiny capacity step makes
+    the heating system leave its first bucket (new captures; smaller buckets reused)."""
+    import torch
+
+    print(f"[model_graph] {model_name}", flush=True)
+    tight = CapacityConfig(u_step=8, min_pad_u=0, t_step=8, min_pad_t=0, warmup=1)
+    s = systems.perovskite(3)
+    eager = _md(_adapter(model_name, device), "eager", device, system=s, temperature=3000.0)
+    graph = _md(_adapter(model_name, device), "model_graph", device, capacity=tight, system=s, temperature=3000.0)
+    assert torch.equal(_state(eager), _state(graph))
+    eager.run(60)
+    graph.run(60)
+    a, b = _state(eager), _state(graph)
+    assert torch.equal(a, b), float((a - b).abs().max())
+    st = graph.model_graph_stats()
+    print(st, flush=True)
+    assert st["replays"] == 61 and st["captures"] >= 2
+    f_eager, e_eager = eager.evaluate()
+    f_graph, e_graph = graph.evaluate()
+    assert torch.equal(f_eager, f_graph) and torch.equal(e_eager, e_graph)
 
 
 @pytest.mark.gpu
