@@ -56,7 +56,24 @@ class GPUResidentMolecularDynamics:
     def __init__(self, atoms, model=None, *, device: torch.device | str = "cuda", ensemble: str = "nvt_nhc",
                  temperature: float = 300.0, timestep: float = 1.0, taut: float = 100.0, tdamp: float | None = None,
                  tchain: int = 3, tloop: int = 1, config: InferenceConfig | None = None, steps_per_launch: int = 1,
-                 momenta=None, seed: int = 0, task: str = "ef", validate_isolated_atoms: bool = False) -> None:
+                 momenta=None, seed: int = 0, task: str = "ef", validate_isolated_atoms: bool = False,
+                 trajectory=None, logfile=None, loginterval: int = 1, append_trajectory: bool = False,
+                 logger_ring: int = 8, output_dir=None, thermo_interval: int = 0, xyz_interval: int = 0,
+                 restart_interval: int = 0, total_steps: int | None = None, restart=None) -> None:
+        intervals = (thermo_interval, xyz_interval, restart_interval, 0 if total_steps is None else total_steps)
+        if any(isinstance(v, bool) or not isinstance(v, int) or v < 0 for v in intervals):
+            raise ValueError("GPUResidentMolecularDynamics: output intervals and total_steps must be nonnegative "
+                             "integers")
+        if steps_per_launch > 1 if isinstance(steps_per_launch, int) else False:
+            # every output and log step must end a window (gpu_md.py:183-195)
+            logs = trajectory is not None or logfile is not None
+            cadence = {"loginterval": max(int(loginterval), 1) if logs else 0, "thermo_interval": thermo_interval,
+                       "xyz_interval": xyz_interval, "restart_interval": restart_interval,
+                       "total_steps": total_steps or 0, "restart step": 0 if restart is None else int(restart.step)}
+            off = {k: v for k, v in cadence.items() if v % steps_per_launch}
+            if off:
+                raise ValueError(f"GPUResidentMolecularDynamics: steps_per_launch={steps_per_launch} must divide "
+                                 f"{off} (a multi-step window's inner steps are not visible)")
         if ensemble.lower() != "nvt_nhc":
             raise NotImplementedError("this build integrates the Nose-Hoover chain ensemble (ensemble='nvt_nhc')")
         if model is None or not hasattr(model, "node_energy"):
@@ -87,6 +104,11 @@ class GPUResidentMolecularDynamics:
         if momenta is None:
             momenta = atom_momenta if atom_momenta is not None else maxwell_boltzmann_momenta(masses, temperature, seed)
         tdamp = taut if tdamp is None else tdamp
+        self.timestep_fs = float(timestep)
+        self.parameters = {"ensemble": "nvt_nhc", "temperature_K": float(temperature), "timestep_fs": float(timestep),
+                           "tdamp_fs": float(tdamp), "tchain": int(tchain), "tloop": int(tloop),
+                           "total_steps": total_steps, "model": getattr(model, "name", type(model).__name__),
+                           "n_atoms": int(positions.shape[0])}
         self.integrator = GPUNoseHooverChainNVT(
             masses, positions, np.asarray(momenta, dtype=np.float64), temperature_K=temperature,
             timestep=timestep * units.fs, tdamp=tdamp * units.fs, tchain=tchain, tloop=tloop, device=self.device,
@@ -110,9 +132,25 @@ class GPUResidentMolecularDynamics:
         self._graph_pool = None
         if self.execution == "model_graph":
             self.enable_model_cuda_graph()
-        # F(q0) for the first pre-force half
-        forces, energy = self.evaluate(self.integrator.positions)
-        self.integrator.set_forces(forces, energy=energy)
+        # F(q0) for the first pre-force half (a restart's cached evaluation: no re-evaluation)
+        if restart is not None:
+            self._load_restart(restart)
+        else:
+            forces, energy = self.evaluate(self.integrator.positions)
+            self.integrator.set_forces(forces, energy=energy)
+        # outputs: the trajectory / text logger and the thermo, frame and restart files
+        from fastmd_amd.execution.gpu_logging import AsyncGPUMDLogger, AtomsTemplate
+        from fastmd_amd.execution.md_protocol import MDOutputs
+
+        self.logger = AsyncGPUMDLogger(
+            AtomsTemplate(np.asarray(numbers), np.asarray(masses, np.float64), np.asarray(cell, np.float64),
+                          np.ones(3, bool)), self.device, trajectory=trajectory, logfile=logfile,
+            loginterval=loginterval, append_trajectory=append_trajectory, ring=logger_ring,
+            state_dtype=torch.float64, extras={"nhc_eta": int(tchain), "nhc_p_eta": int(tchain)})
+        self.outputs = MDOutputs(self, output_dir, thermo_interval, xyz_interval, restart_interval, total_steps,
+                                 None if restart is None else restart.offsets, engine="native")
+        if self.logger.should_log(self.steps) and restart is None:
+            self._log_current()
         if self.execution == "whole_step":
             self.enable_whole_step_cuda_graph()
 
@@ -172,6 +210,86 @@ class GPUResidentMolecularDynamics:
         forces, energy = self._evaluate(q)
         self.integrator.step_post_force(forces, energy=energy)
         self.steps += 1
+        self._after_steps()
+
+    # ------------------------------------------------------------------ outputs
+    @property
+    def nsteps(self) -> int:
+        return self.steps
+
+    def _output_due(self, step: int) -> bool:
+        return self.logger.should_log(step) or self.outputs.due(step)
+
+    def _log_current(self) -> None:
+        th = self.integrator
+        self.logger.enqueue(step=self.steps, time_ps=self.steps * self.timestep_fs / 1000.0, positions=th.positions,
+                            momenta=th.momenta, forces=th.forces, cell=self.cell, potential_energy=th.potential_energy,
+                            kinetic_energy=th.kinetic_energy(), temperature=th.temperature(),
+                            extras={"nhc_eta": th.eta, "nhc_p_eta": th.p_eta})
+
+    def _after_steps(self) -> None:
+        """The logger's frame and the output files due at the current step."""
+        if self.logger.should_log(self.steps):
+            self._log_current()
+        self.outputs.write()
+
+    def write_outputs(self) -> dict | None:
+        return self.outputs.write()
+
+    def log_frame(self, thermo: dict | None = None) -> None:
+        self.outputs.log_frame(thermo)
+
+    def save_restart(self, path=None) -> None:
+        self.outputs.save_restart(path)
+
+    def md_fields(self) -> dict:
+        """Views of the current state for output and restart (gpu_md.py:2118-2140), ids = arange(N)."""
+        th = self.integrator
+        if getattr(self, "_masses64", None) is None:
+            self._masses64 = torch.as_tensor(np.asarray(self.masses, np.float64), device=self.device)
+            table = self.adapter.reference_energies() if hasattr(self.adapter, "reference_energies") else None
+            ref = 0.0 if table is None else float(torch.nan_to_num(table[0, self.numbers.long() - 1]).sum())
+            self._reference_energy = torch.tensor(ref, dtype=torch.float32, device=self.device)
+        return {"ids": torch.arange(self.n_atoms, device=self.device), "numbers": self.numbers.to(self.device),
+                "positions": th.positions, "momenta": th.momenta, "masses": self._masses64, "forces": th.forces,
+                "energy": th.potential_energy.reshape(()), "reference_energy": self._reference_energy}
+
+    def thermostat_state(self) -> dict:
+        return self.integrator.state_dict()
+
+    def collective_check(self, error: str | None) -> None:
+        if error:
+            raise ValueError(f"GPUResidentMolecularDynamics outputs: {error}")
+
+    def close(self) -> None:
+        """Flush and close the logger and the output files."""
+        try:
+            self.logger.close()
+        finally:
+            self.outputs.close()
+
+    def _load_restart(self, restart) -> None:
+        if restart.numbers.shape[0] != self.n_atoms or not np.array_equal(restart.numbers, self.numbers.numpy()):
+            raise ValueError("the restart file's atoms are not this system's")
+        th = self.integrator
+        if restart.nhc_state is not None:
+            th.load_state_dict(restart.nhc_state)
+        th.set_state(positions=restart.positions, momenta=restart.momenta, forces=restart.forces,
+                     potential_energy=np.asarray(restart.energy, np.float64).reshape(1))
+        self.steps = int(restart.step)
+
+    @classmethod
+    def from_restart(cls, restart, model, **kwargs) -> "GPUResidentMolecularDynamics":
+        """Continue a run from a restart file (or RestartData): its atoms, state, thermostat and
+        step, the output files truncated to its offsets; the MD parameters come from ``kwargs``
+        (``resume_mismatch`` lists what changed)."""
+        from fastmd_amd.execution.md_protocol import read_restart
+        from fastmd_amd.systems import System
+
+        data = read_restart(restart) if not hasattr(restart, "positions") else restart
+        system = System(positions=np.asarray(data.positions, np.float64), cell=np.asarray(data.cell, np.float64),
+                        numbers=np.asarray(data.numbers), masses=np.asarray(data.masses, np.float64))
+        return cls(system, model=model, momenta=np.asarray(data.momenta, np.float64), restart=data, **kwargs)
 
     def _demand(self, batch) -> tuple[int, int]:
         """(undirected pairs, triplets) of a ragged build: the pairs from its edge count, the
@@ -325,7 +443,8 @@ class GPUResidentMolecularDynamics:
                 # the next window goes into the stream before the host reads this one's flags (so the
                 # GPU does not wait for the host between windows), unless this one will likely
                 # refresh the candidates (gpu_md.py:1882-1975)
-                if self.launch_behind and done + 1 < windows and runner.refresh_unlikely():
+                if (self.launch_behind and done + 1 < windows and runner.refresh_unlikely()
+                        and not self._output_due(self.steps + self.steps_per_launch)):
                     ahead = runner.launch(behind=True)
                     self.windows_ahead += 1
                 stats = runner.launched_stats(slot)
@@ -347,6 +466,7 @@ class GPUResidentMolecularDynamics:
                     continue
                 done += 1
                 self.steps += self.steps_per_launch
+                self._after_steps()
         except BaseException:
             if ahead is not None:  # back to the end of the window settled (or being settled)
                 runner.drop()
@@ -369,12 +489,23 @@ class GPUResidentMolecularDynamics:
         return float(self.integrator.conserved_energy())
 
     def thermodynamics(self) -> dict:
-        """One download of the scalars (gpu_md.py:2169-2204)."""
-        epot = self.integrator.potential_energy[0]
-        ekin = self.integrator.kinetic_energy()
-        values = torch.stack([epot, ekin, self.integrator.temperature(), self.integrator.conserved_energy()]).tolist()
-        return {"step": self.steps, "epot": values[0], "ekin": values[1], "temperature": values[2],
-                "etotal": values[0] + values[1], "conserved": values[3]}
+        """Observables of the current state, one download (gpu_md.py:2169-2204): step, time_fs,
+        target_temperature, potential / kinetic / total energy, temperature, momentum (the total),
+        dof, eta, p_eta, thermostat_energy and conserved_energy (ASE's get_conserved_energy)."""
+        th = self.integrator
+        values = torch.cat([th.potential_energy.reshape(1).to(torch.float64), th.kinetic_energy().reshape(1),
+                            th.temperature().reshape(1).to(torch.float64),
+                            th.momenta.to(torch.float64).sum(0), th.eta.reshape(-1), th.p_eta.reshape(-1),
+                            th.thermostat_energy().reshape(1).to(torch.float64)]).tolist()
+        tchain = self.parameters["tchain"]
+        potential, kinetic, temperature = values[0], values[1], values[2]
+        energy = values[6 + 2 * tchain]
+        return {"step": self.steps, "time_fs": self.steps * self.timestep_fs,
+                "target_temperature": float(th.temperature_K), "potential_energy": potential,
+                "kinetic_energy": kinetic, "total_energy": potential + kinetic, "temperature": temperature,
+                "momentum": values[3:6], "dof": 3 * self.n_atoms, "eta": values[6:6 + tchain],
+                "p_eta": values[6 + tchain:6 + 2 * tchain], "thermostat_energy": energy,
+                "conserved_energy": potential + kinetic + energy}
 
     def whole_step_stats(self) -> dict | None:
         if self.whole_step_runner is None:
