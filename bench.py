@@ -342,6 +342,36 @@ def frames_bench(steps: int, warmup: int) -> dict:
             "md_steps_per_s": round(steps / t, 1), "trajectory_bytes": size}
 
 
+def replica_bench(steps: int, warmup: int) -> list:
+    """Replica batching (replica_batch.py): R replicas of the 135-atom configs[2] system (MACE-like,
+    500 K NHC, their own momenta and chains) in one whole-step graph per window."""
+    import torch
+
+    from fastmd_amd import systems
+    from fastmd_amd.execution.replica_batch import ReplicaBatchedMD
+    from fastmd_amd.models.mace_like import MaceLikeAdapter
+
+    out = []
+    for replicas in (8, 32):
+        md = ReplicaBatchedMD(systems.perovskite_atoms(135), MaceLikeAdapter(device="cuda"), replicas=replicas,
+                              device="cuda", temperature=500.0, timestep=0.25, tdamp=25.0,
+                              steps_per_launch=STEPS_PER_LAUNCH)
+        md.run(-(-warmup // STEPS_PER_LAUNCH) * STEPS_PER_LAUNCH)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        md.run(steps)
+        torch.cuda.synchronize()
+        t = time.perf_counter() - t0
+        row = {"replicas": replicas, "atoms_per_replica": 135, "steps": steps, "warmup": warmup,
+               "ms_per_step": round(t / steps * 1e3, 4), "atom_steps_per_s": round(replicas * 135 * steps / t, 1),
+               "capacity_history": md.capacity_history}
+        log(f"replicas R={replicas}: {row['ms_per_step']} ms/step, {row['atom_steps_per_s']} atom-steps/s")
+        out.append(row)
+        del md
+        torch.cuda.empty_cache()
+    return out
+
+
 def model_graph_bench(steps: int, warmup: int) -> list:
     """The model_graph execution mode (ragged build and integrator eager, the model's forward + VJP
     replayed per capacity bucket) of the MACE-like model at 135 and 10 000 atoms."""
@@ -445,6 +475,8 @@ def main() -> int:
     parser.add_argument("--warmup-threebody", type=int, default=2000,
                         help="untimed three-body steps (the random-init potential keeps adding edges and triplets "
                              "for the first ~2 000 steps, each growth a recapture)")
+    parser.add_argument("--replicas", action="store_true",
+                        help="only replica batching (8 and 32 replicas of the 135-atom system)")
     parser.add_argument("--model-graph", action="store_true",
                         help="only the model_graph execution mode (MACE-like, 135 and 10 000 atoms)")
     parser.add_argument("--roofline-only", action="store_true",
@@ -471,6 +503,9 @@ def main() -> int:
         return 0
     if args.model_graph:
         print(json.dumps({"model_graph": model_graph_bench(200, 200)}), flush=True)
+        return 0
+    if args.replicas:
+        print(json.dumps({"replicas_135": replica_bench(1000, 1000)}), flush=True)
         return 0
     if args.ops:
         print(json.dumps({"ops_sweep": ops_sweep(), "hbm_peak_GBps": HBM_PEAK_GBPS,
@@ -519,6 +554,9 @@ def main() -> int:
     frames = frames_bench(200 if args.quick else steps_small, args.warmup)
     log(f"135 atoms + frames: {frames['ms_per_step']} ms/step")
 
+    log("replica batching")
+    replicas = replica_bench(200 if args.quick else 1000, 200 if args.quick else 1000)
+
     log("model_graph mode")
     model_graph = model_graph_bench(50 if args.quick else 200, 50 if args.quick else 200)
 
@@ -557,6 +595,7 @@ def main() -> int:
         "small_system_with_frames": frames,
         "threebody_5000": threebody,
         "model_graph": model_graph,
+        "replicas_135": replicas,
         "segment_sum_GBps": seg["segment_sum"]["GBps"],
         "hbm_ops_40k": seg,
         "whole_step_stats_10k": {**{k: stats_big[k] for k in ("candidate_refreshes", "fallback_windows",

@@ -25,7 +25,8 @@ _u8 = ctypes.c_uint8
 SIGNATURES: dict[str, tuple] = {
     "fmd_abi_version": (ctypes.c_int, []),
     "fmd_error_string": (ctypes.c_char_p, [ctypes.c_int]),
-    "fmd_nl_candidates": (ctypes.c_int, [_p, _p, _p, _i64, _f32, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _p]),
+    "fmd_nl_candidates": (ctypes.c_int, [_p, _p, _p, _i64, _f32, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _i64,
+                                         _p]),
     "fmd_nl_wrap": (ctypes.c_int, [_p, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p]),
     "fmd_nl_build_work_size": (_i64, [_i64]),
     "fmd_nl_build": (ctypes.c_int, [_p, _i32, _p, _p, _i64, _p, _p, _p, _i32, _p, _p, _p, _f32, _f32,

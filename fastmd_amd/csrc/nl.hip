@@ -201,7 +201,8 @@ __global__ void __launch_bounds__(256) cells_query_kernel(const float* wrapped, 
                                                           int r1, int r2, int32_t bmax, int lcap,
                                                           const int32_t* cell_start, const int32_t* cell_atoms,
                                                           int32_t* neighbor_matrix, int32_t* neighbor_shifts,
-                                                          int32_t* num_neighbors, uint8_t* capacity_valid) {
+                                                          int32_t* num_neighbors, uint8_t* capacity_valid,
+                                                          int64_t system_size) {
   extern __shared__ uint64_t keys[];
   __shared__ int counter;
   const int64_t i = blockIdx.x;
@@ -230,6 +231,8 @@ __global__ void __launch_bounds__(256) cells_query_kernel(const float* wrapped, 
     for (int p = cell_start[cid]; p < cell_start[cid + 1]; ++p) {
       const int32_t j = cell_atoms[p];
       if (j == i && s0 == 0 && s1 == 0 && s2 == 0) continue;
+      // replicas of one system side by side (atoms [k S, (k+1) S) each): no pair across them
+      if (system_size > 0 && (int64_t)j / system_size != i / system_size) continue;
       const float d2v = pair_d2(xi, yi, zi, wrapped[3 * j], wrapped[3 * j + 1], wrapped[3 * j + 2], sx, sy, sz, cm);
       if (d2v < cutoff2) {
         int slot = atomicAdd(&counter, 1);
@@ -773,8 +776,9 @@ int fmd_nl_wrap(const void* positions, int32_t pos_is_f64, const float* inv_cell
 int fmd_nl_candidates(const float* wrapped, const float* frac, const float* cell, int64_t n_atoms, float cutoff2,
                       const int32_t* ncells, const int32_t* reach, int32_t bmax, int32_t* cell_count,
                       int32_t* cell_start, int32_t* cell_atoms, int32_t* neighbor_matrix, int32_t* neighbor_shifts,
-                      int32_t* num_neighbors, uint8_t* capacity_valid, hipStream_t stream) {
+                      int32_t* num_neighbors, uint8_t* capacity_valid, int64_t system_size, hipStream_t stream) {
   FMD_REQUIRE(n_atoms > 0 && bmax > 0 && ncells && reach);
+  FMD_REQUIRE(system_size >= 0 && (system_size == 0 || n_atoms % system_size == 0));
   const int n0 = ncells[0], n1 = ncells[1], n2 = ncells[2];
   const int r0 = reach[0], r1 = reach[1], r2 = reach[2];
   FMD_REQUIRE(n0 > 0 && n1 > 0 && n2 > 0 && r0 >= 0 && r1 >= 0 && r2 >= 0);
@@ -799,7 +803,7 @@ int fmd_nl_candidates(const float* wrapped, const float* frac, const float* cell
   FMD_CHECK_LAUNCH();
   hipLaunchKernelGGL(cells_query_kernel, dim3((unsigned)n_atoms), dim3(256), (size_t)lcap * sizeof(uint64_t), stream,
                      wrapped, frac, cell, n_atoms, cutoff2, n0, n1, n2, r0, r1, r2, bmax, lcap, cell_start, cell_atoms,
-                     neighbor_matrix, neighbor_shifts, num_neighbors, capacity_valid);
+                     neighbor_matrix, neighbor_shifts, num_neighbors, capacity_valid, system_size);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -47,6 +47,23 @@ def sum_f64_into(x: Tensor) -> Tensor:
     return out
 
 
+def sum_f64_segments(x: Tensor, segments: int) -> Tensor:
+    """Per-segment ``sum_f64_into`` of ``segments`` equal contiguous slices ([segments] float64):
+    each slice summed in the order ``sum_f64`` sums a system of that size, so a replica's energy
+    is bitwise its single-system energy."""
+    if segments == 1:
+        return sum_f64_into(x)
+    x = x.detach().contiguous().reshape(-1)
+    if x.numel() % segments:
+        raise ValueError(f"{x.numel()} rows do not split into {segments} equal segments")
+    n = x.numel() // segments
+    out = torch.empty(segments, dtype=torch.float64, device=x.device)
+    for r in range(segments):
+        _abi.call("fmd_sum_f64", x[r * n:(r + 1) * n].data_ptr(), 1 if x.dtype == torch.float64 else 0, n,
+                  out[r:r + 1].data_ptr(), _abi.stream_handle())
+    return out
+
+
 def engine_derivative(adapter) -> "EnergyDerivative | None":
     """The derivative the runtime runs for ``adapter`` (energy_derivative.py:51-60)."""
     if hasattr(adapter, "node_energy"):
@@ -71,8 +88,11 @@ class EnergyDerivative:
 
     stress_unit = "eV/A^3"
 
-    def __init__(self, adapter: EnergyTap) -> None:
+    def __init__(self, adapter: EnergyTap, segments: int = 1) -> None:
         self.adapter = adapter
+        # replica batching: the rows are this many copies of one system; "e" then holds one energy
+        # per copy (each bitwise its single-system energy), the forces are unchanged
+        self.segments = int(segments)
 
     def extensive_energy(self, energy: Tensor, atom_counts) -> Tensor:
         return energy
@@ -84,12 +104,20 @@ class EnergyDerivative:
         if explicit is not None and (n_real is None or n_real == batch.positions.shape[0]):
             # the adapter's explicit VJP: the same kernels as the autograd path below without the
             # autograd seed / cast / negation launches (one graph node each per step)
-            energy, forces = explicit(inputs, batch.positions, batch.cell)
+            if self.segments == 1:
+                energy, forces = explicit(inputs, batch.positions, batch.cell)
+            else:
+                energy, forces = explicit(inputs, batch.positions, batch.cell, segments=self.segments)
             return {"e": energy, "f": [forces]}
         with torch.enable_grad():
             leaf = batch.positions.detach().requires_grad_(True)
             energies = self.adapter.node_energy(inputs, leaf, batch.cell)
             rows = energies.shape[0] if n_real is None else n_real
-            energy = sum_f64(energies[:rows])
-            (grad,) = torch.autograd.grad(energy, (leaf,))
-        return {"e": energy.detach().reshape(1), "f": [-grad]}
+            if self.segments == 1:
+                energy = sum_f64(energies[:rows])
+                (grad,) = torch.autograd.grad(energy, (leaf,))
+                return {"e": energy.detach().reshape(1), "f": [-grad]}
+            n = rows // self.segments
+            parts = torch.stack([sum_f64(energies[r * n:(r + 1) * n]) for r in range(self.segments)])
+            (grad,) = torch.autograd.grad(parts.sum(), (leaf,))
+        return {"e": parts.detach(), "f": [-grad]}

@@ -84,6 +84,10 @@ class WholeStepGraphRunner:
             raise NotImplementedError("stress windows are not supported")
         self.adapter = model
         self._derivative = engine_derivative(model)
+        replicas = int(getattr(integrator, "replicas", 1))
+        if replicas > 1 and self._derivative is not None:
+            # a replica batch: one energy per replica for its integrator
+            self._derivative.segments = replicas
         if self._derivative is None:
             raise NotImplementedError("model-owned derivatives are not supported: the model needs an EnergyTap")
         self.builder = builder
@@ -151,7 +155,7 @@ class WholeStepGraphRunner:
         graph, status = self.builder.build(positions, rebuild_candidates=False)
         out = self._derivative(self.builder.batch, graph, task=self.task, n_real=self.n_real)
         forces = out["f"][0][: self.n_real]
-        energy = out["e"].reshape(-1)[:1]
+        energy = out["e"].reshape(-1)  # one energy (or one per replica of a replica batch)
         return forces, energy, status
 
     def _step_body(self, last: bool) -> None:

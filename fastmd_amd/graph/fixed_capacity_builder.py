@@ -102,7 +102,7 @@ class FixedCapacityGraphBuilder:
                  candidates_from=None, padding: PaddingRule | None = None,
                  prepare: Callable[[GraphBatch], Any] | None = None, positions_dtype: torch.dtype = torch.float32,
                  sorted_edges: bool = True, max_neighbor_count: Tensor | None = None,
-                 publish_positions: bool = False) -> None:
+                 publish_positions: bool = False, system_size: int = 0) -> None:
         line_graph = line_graph_cutoff is not None
         if line_graph and (t_capacity <= 0 or not 0.0 < float(line_graph_cutoff) <= float(atom_graph_cutoff)):
             raise ValueError("a line-graph builder needs t_capacity > 0 and 0 < line_graph_cutoff <= the atom cutoff")
@@ -124,6 +124,9 @@ class FixedCapacityGraphBuilder:
         if pbc is not None and not bool(torch.as_tensor(pbc).all()):
             raise NotImplementedError("non-periodic axes are not supported")
         self.edges_only = not line_graph
+        # replica batching: the atoms are copies of one system of this many atoms, side by side;
+        # no edge joins two copies (0: one system)
+        self.system_size = int(system_size)
         self.padding = padding
         self.sorted_edges = True
         self.max_neighbor_count = max_neighbor_count
@@ -256,7 +259,7 @@ class FixedCapacityGraphBuilder:
                   _abi.array(_abi._i32, self._reach), self.buffer_max, self._cell_count.data_ptr(),
                   self._cell_start.data_ptr(), self._cell_atoms.data_ptr(), self.neighbor_matrix.data_ptr(),
                   self.neighbor_shifts.data_ptr(), self.num_neighbors.data_ptr(),
-                  self._candidate_capacity_valid.data_ptr(), self._stream())
+                  self._candidate_capacity_valid.data_ptr(), self.system_size, self._stream())
         self._candidate_initialized = True
 
     def assert_candidate_capacity(self) -> None:

@@ -119,7 +119,7 @@ class TensorGraphBuilder:
             _abi.call("fmd_nl_candidates", wrapped.data_ptr(), frac.data_ptr(), self.cell.data_ptr(), n, self._cand2,
                       _abi.array(_abi._i32, self._ncells), _abi.array(_abi._i32, self._reach), bmax,
                       self._cell_count.data_ptr(), self._cell_start.data_ptr(), self._cell_atoms.data_ptr(),
-                      nm.data_ptr(), ns.data_ptr(), num.data_ptr(), valid.data_ptr(), stream)
+                      nm.data_ptr(), ns.data_ptr(), num.data_ptr(), valid.data_ptr(), 0, stream)
             max_count, total = torch.stack([num.max().long(), num.clamp(max=bmax).long().sum()]).tolist()
             if max_count <= bmax:
                 break

@@ -48,12 +48,14 @@ const char* fmd_error_string(int status);
  * counts <= bmax). Unused slots keep neighbour n_atoms and shift 0.
  * ncells/reach: cells per lattice axis and the cell search reach per axis (host computed).
  * Replaces nvalchemiops batch_build_cell_list/batch_query_cell_list as called at
- * fastmd/graph/fixed_capacity_builder.py:1519-1554 (FixedCapacityGraphBuilder._build_candidates). */
+ * fastmd/graph/fixed_capacity_builder.py:1519-1554 (FixedCapacityGraphBuilder._build_candidates).
+ * system_size > 0: the atoms are replicas of one system, [k S, (k+1) S) each, and pairs across
+ * replicas are not candidates (the union graph of replica batching, replica_batch.py:126-180). */
 int fmd_nl_candidates(const float* wrapped, const float* frac, const float* cell, int64_t n_atoms,
                       float cutoff2, const int32_t* ncells, const int32_t* reach, int32_t bmax,
                       int32_t* cell_count, int32_t* cell_start, int32_t* cell_atoms,
                       int32_t* neighbor_matrix, int32_t* neighbor_shifts, int32_t* num_neighbors,
-                      uint8_t* capacity_valid, hipStream_t stream);
+                      uint8_t* capacity_valid, int64_t system_size, hipStream_t stream);
 
 /* Wrap (refresh flavour): float32 positions -> fractional coordinates in [0,1), integer
  * wraps and wrapped Cartesian coordinates; optionally resets the reference positions/wraps

@@ -1,0 +1,68 @@
+"""Replica batching: R replicas of one system in one whole-step graph; each replica's trajectory
+and energy equal the single-system run with its momenta, bitwise (the union graph has no edge
+across replicas and every per-replica reduction keeps its single-system order)."""
+import numpy as np
+import pytest
+
+from fastmd_amd import systems
+from fastmd_amd.config import InferenceConfig
+
+
+def test_replica_state_layout():
+    import torch
+
+    from fastmd_amd.execution.replica_batch import ReplicaNHCState
+
+    st = ReplicaNHCState.allocate(3, 5, 2, "cpu")
+    assert st.positions.shape == (15, 3) and st.eta.shape == (3, 2) and st.potential_energy.shape == (3,)
+    assert st.flat.numel() == 3 * 45 + 2 * 6 + 3
+    r1 = st.replica(1, 5)
+    r1.positions.fill_(7.0)
+    r1.eta.fill_(3.0)
+    r1.potential_energy.fill_(-1.0)
+    assert (st.positions[5:10] == 7).all() and (st.positions[:5] == 0).all() and (st.positions[10:] == 0).all()
+    assert (st.eta[1] == 3).all() and float(st.potential_energy[1]) == -1.0 and not st.eta[0].any()
+    assert torch.equal(r1.momenta, st.momenta[5:10])
+
+
+def _adapter(name, device):
+    from fastmd_amd.models.mace_like import MaceLikeAdapter
+    from fastmd_amd.models.pair_potential import MorsePairAdapter
+    from fastmd_amd.models.threebody_like import ThreeBodyAdapter, ThreeBodyConfig
+
+    return {"morse": lambda: MorsePairAdapter(device=device), "mace_like": lambda: MaceLikeAdapter(device=device),
+            "threebody": lambda: ThreeBodyAdapter(config=ThreeBodyConfig(bond_cutoff=3.5), device=device)}[name]()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("model_name", ["morse", "mace_like", "threebody"])
+def test_replicas_equal_single_runs_bitwise(device, model_name):
+    import torch
+
+    from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
+    from fastmd_amd.execution.replica_batch import ReplicaBatchedMD
+    from fastmd_amd.interfaces.gpu_md import GPUResidentMolecularDynamics
+
+    print(f"[replicas] {model_name}", flush=True)
+    s = systems.perovskite(3)
+    R = 3
+    momenta = np.stack([maxwell_boltzmann_momenta(s.masses, 500.0, seed) for seed in (11, 12, 13)])
+    batch = ReplicaBatchedMD(s, _adapter(model_name, device), replicas=R, device=device, temperature=500.0,
+                             timestep=0.25, tdamp=25.0, momenta=momenta, steps_per_launch=5)
+    batch.run(30)
+    torch.cuda.synchronize()
+    assert batch.runner.builder.system_size == s.n_atoms
+    for r in range(R):
+        single = GPUResidentMolecularDynamics(s, model=_adapter(model_name, device), device=device, temperature=500.0,
+                                              timestep=0.25, tdamp=25.0, momenta=momenta[r], steps_per_launch=5,
+                                              config=InferenceConfig(execution="whole_step"))
+        single.run(30)
+        torch.cuda.synchronize()
+        got = batch.replica_state(r)
+        th = single.integrator
+        for key in ("positions", "momenta", "forces"):
+            assert torch.equal(got[key], getattr(th, key)), (r, key)
+        assert torch.equal(got["potential_energy"].reshape(1), th.potential_energy.reshape(1)), r
+        assert torch.equal(batch.integrator.eta[r], th.eta) and torch.equal(batch.integrator.p_eta[r], th.p_eta)
+    thermo = batch.thermodynamics()
+    assert len(thermo) == R and len({round(t["temperature"], 6) for t in thermo}) == R  # distinct replicas
