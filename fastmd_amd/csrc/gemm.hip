@@ -194,7 +194,8 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restr
 // Several independent GEMMs of one b layout in one launch (the node side of an interaction
 // layer: fewer, fuller launches). Workgroup w takes problem g with tile0[g] <= w < tile0[g + 1],
 // tile (w - tile0[g]) in row-major order of its 64 x 64 tiles. Each problem's result is the one
-// fmd_gemm_f32's 64 x 64 kernel gives (same K order), with [a | a2] when a2 is set.
+// fmd_gemm_f32's 64 x 64 kernel gives (same K order), with [a | a2] when a2 is set. Large groups
+// of B [N, K] problems run as gemm_x3_group_kernel instead.
 constexpr int kMaxGroup = 4;
 struct GemmDesc {
   const float* a;
@@ -546,32 +547,36 @@ __device__ __forceinline__ void split3(float4 v, bf16x4& p0, bf16x4& p1, bf16x4&
 
 constexpr int X3_PL = 128 * 16, X3_OP = 3 * X3_PL, X3_BUF = 2 * X3_OP;
 
-#define X3_LOAD(K0)                                                                                 \
+#define X3_LOAD(K0, S)                                                                              \
   do {                                                                                              \
     const int64_t k0_ = (K0);                                                                       \
     const bool q2_ = k0_ >= ks2, q1_ = !q2_ && k0_ >= ks1;                                          \
     const float* base_ = q2_ ? src2 : q1_ ? src1 : src0;                                            \
     const int64_t kin_ = q2_ ? k0_ - ks2 : q1_ ? k0_ - ks1 : k0_;                                   \
     const int w_ = q2_ ? w2 : q1_ ? w1 : w0;                                                        \
-    _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                                 \
+    _Pragma("unroll") for (int q = 0; q < MB; ++q) {                                                \
       const int64_t o_ = q2_ ? ao2[q] : q1_ ? ao1[q] : ao0[q];                                      \
-      ra[q] = (kin_ + kc < w_) ? *reinterpret_cast<const float4*>(base_ + o_ + kin_)                \
+      ra##S[q] = (kin_ + kc < w_) ? *reinterpret_cast<const float4*>(base_ + o_ + kin_)                \
                                : make_float4(0.f, 0.f, 0.f, 0.f);                                   \
-      rb[q] = (k0_ + kc < k) ? *reinterpret_cast<const float4*>(b + bo[q] + k0_)                    \
-                             : make_float4(0.f, 0.f, 0.f, 0.f);                                     \
     }                                                                                               \
+    _Pragma("unroll") for (int q = 0; q < 2; ++q)                                                   \
+      rb##S[q] = (k0_ + kc < k) ? *reinterpret_cast<const float4*>(b + bo[q] + k0_)                    \
+                             : make_float4(0.f, 0.f, 0.f, 0.f);                                     \
   } while (0)
 
-#define X3_STORE(BUFI)                                                                              \
+#define X3_STORE(BUFI, S)                                                                           \
   do {                                                                                              \
     __bf16* sb_ = lds + (BUFI) * X3_BUF;                                                            \
-    _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                                 \
+    _Pragma("unroll") for (int q = 0; q < MB; ++q) {                                                \
       bf16x4 x0_, x1_, x2_;                                                                         \
-      split3(ra[q], x0_, x1_, x2_);                                                                 \
+      split3(ra##S[q], x0_, x1_, x2_);                                                                 \
       *reinterpret_cast<bf16x4*>(sb_ + 0 * X3_PL + soff[q]) = x0_;                                  \
       *reinterpret_cast<bf16x4*>(sb_ + 1 * X3_PL + soff[q]) = x1_;                                  \
       *reinterpret_cast<bf16x4*>(sb_ + 2 * X3_PL + soff[q]) = x2_;                                  \
-      split3(rb[q], x0_, x1_, x2_);                                                                 \
+    }                                                                                               \
+    _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                                 \
+      bf16x4 x0_, x1_, x2_;                                                                         \
+      split3(rb##S[q], x0_, x1_, x2_);                                                                 \
       *reinterpret_cast<bf16x4*>(sb_ + X3_OP + 0 * X3_PL + soff[q]) = x0_;                          \
       *reinterpret_cast<bf16x4*>(sb_ + X3_OP + 1 * X3_PL + soff[q]) = x1_;                          \
       *reinterpret_cast<bf16x4*>(sb_ + X3_OP + 2 * X3_PL + soff[q]) = x2_;                          \
@@ -579,14 +584,14 @@ constexpr int X3_PL = 128 * 16, X3_OP = 3 * X3_PL, X3_BUF = 2 * X3_OP;
   } while (0)
 
 // six products per block, the small ones first: (0,2) (1,1) (2,0) (0,1) (1,0) (0,0)
-#define X3_COMPUTE(BUFI)                                                                            \
+#define X3_COMPUTE(BUFI, MBV)                                                                       \
   do {                                                                                              \
     const __bf16* as_ = lds + (BUFI) * X3_BUF;                                                      \
     const __bf16* bs_ = as_ + X3_OP;                                                                \
     bf16x8 av_[3][2], bv_[3][2];                                                                    \
     _Pragma("unroll") for (int p = 0; p < 3; ++p) {                                                 \
-      _Pragma("unroll") for (int i = 0; i < 2; ++i)                                                 \
-        av_[p][i] = *reinterpret_cast<const bf16x8*>(as_ + p * X3_PL + (wm * 64 + i * 32) * 16 + rd); \
+      _Pragma("unroll") for (int i = 0; i < (MBV); ++i)                                             \
+        av_[p][i] = *reinterpret_cast<const bf16x8*>(as_ + p * X3_PL + (wm * 32 * (MBV) + i * 32) * 16 + rd); \
       _Pragma("unroll") for (int j = 0; j < 2; ++j)                                                 \
         bv_[p][j] = *reinterpret_cast<const bf16x8*>(bs_ + p * X3_PL + (wn * 64 + j * 32) * 16 + rd); \
     }                                                                                               \
@@ -595,22 +600,26 @@ constexpr int X3_PL = 128 * 16, X3_OP = 3 * X3_PL, X3_BUF = 2 * X3_OP;
     _Pragma("unroll") for (int pr = 0; pr < 6; ++pr) {                                              \
       const int pa_ = pr == 0 ? 0 : pr == 1 ? 1 : pr == 2 ? 2 : pr == 3 ? 0 : pr == 4 ? 1 : 0;      \
       const int pb_ = pr == 0 ? 2 : pr == 1 ? 1 : pr == 2 ? 0 : pr == 3 ? 1 : pr == 4 ? 0 : 0;      \
-      _Pragma("unroll") for (int i = 0; i < 2; ++i) _Pragma("unroll") for (int j = 0; j < 2; ++j)   \
+      _Pragma("unroll") for (int i = 0; i < (MBV); ++i) _Pragma("unroll") for (int j = 0; j < 2; ++j) \
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[pa_][i], bv_[pb_][j], acc[i][j], 0, 0, 0); \
     }                                                                                               \
   } while (0)
 
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) gemm_x3_kernel(X3Part P0, X3Part P1, X3Part P2, int np,
-                                                           const float* __restrict__ b, int64_t ldb, X3Part radd,
-                                                           const float* __restrict__ bias, float* c, int64_t ldc,
-                                                           int64_t m, int64_t n, int64_t k, int accumulate, int act,
-                                                           int64_t n_tiles) {
+// One (64 MB) x 128 tile of C at (row_blk, col_blk): A as up to three gathered column parts (K
+// order P0 | P1 | P2), B [N, K] K-contiguous, both split into their planes as they are staged.
+// Each wave computes (32 MB) x 64 of it (MB blocks of 32 x 32 by two); MB = 1 halves the rows per
+// workgroup for launches with too few 128-row tiles to keep three workgroups on every CU (every
+// product keeps its K order: the same C either way).
+// ST: register stages of the global loads (1 or 2 slices in flight beyond the one being stored).
+template <int MB, int ST>
+__device__ __forceinline__ void x3_tile(const X3Part& P0, const X3Part& P1, const X3Part& P2, int np,
+                                        const float* __restrict__ b, int64_t ldb, const X3Part& radd,
+                                        const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n,
+                                        int64_t k, int accumulate, int act, int64_t row_blk, int64_t col_blk) {
   __shared__ __attribute__((aligned(16))) __bf16 lds[2 * X3_BUF];
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, rr = lane & 31;
-  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
-  const int64_t row_blk = (tile / n_tiles) * 128, col_blk = (tile % n_tiles) * 128;
   const int64_t ks1 = P0.width, ks2 = ks1 + (np > 1 ? P1.width : 0);
   const float *src0 = P0.src, *src1 = P1.src, *src2 = P2.src;
   const int w0 = P0.width, w1 = P1.width, w2 = P2.width;
@@ -622,41 +631,64 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
   for (int q = 0; q < 2; ++q) {
     const int r = (t + q * kThreads) >> 2;
     const int64_t gr = min(row_blk + r, m - 1);
-    ao0[q] = (P0.idx ? (int64_t)P0.idx[gr * P0.istride] : gr) * P0.ld + kc;
-    ao1[q] = np > 1 ? (P1.idx ? (int64_t)P1.idx[gr * P1.istride] : gr) * P1.ld + kc : 0;
-    ao2[q] = np > 2 ? (P2.idx ? (int64_t)P2.idx[gr * P2.istride] : gr) * P2.ld + kc : 0;
+    if (q < MB) {
+      ao0[q] = (P0.idx ? (int64_t)P0.idx[gr * P0.istride] : gr) * P0.ld + kc;
+      ao1[q] = np > 1 ? (P1.idx ? (int64_t)P1.idx[gr * P1.istride] : gr) * P1.ld + kc : 0;
+      ao2[q] = np > 2 ? (P2.idx ? (int64_t)P2.idx[gr * P2.istride] : gr) * P2.ld + kc : 0;
+    }
     bo[q] = min(col_blk + r, n - 1) * ldb + kc;
     soff[q] = r * 16 + (((kc >> 3) ^ ((r >> 3) & 1)) * 8) + (kc & 7);
   }
   const int rd = rr * 16 + ((h ^ ((rr >> 3) & 1)) * 8);  // this lane's 8 k of its MFMA row
-  float4 ra[2], rb[2];
-  f32x16 acc[2][2];
+  float4 ra0[MB], rb0[2], ra1[MB], rb1[2];  // register stages (the second with ST = 2)
+  f32x16 acc[MB][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   const int64_t nk = fmd_cdiv(k, 16);
-  X3_LOAD(0);
-  X3_STORE(0);
-  if (nk > 1) X3_LOAD(16);
+  X3_LOAD(0, 0);
+  X3_STORE(0, 0);
+  if (nk > 1) X3_LOAD(16, 0);
+  if (ST == 2 && nk > 2) X3_LOAD(32, 1);
   __syncthreads();
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const int cur = (int)(kt & 1);
-    if (kt + 1 < nk) {
-      X3_STORE(cur ^ 1);                       // slice kt + 1 (loaded one iteration ago)
-      if (kt + 2 < nk) X3_LOAD((kt + 2) * 16);  // slice kt + 2 stays in flight over these MFMAs
+  if constexpr (ST == 1) {
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      const int cur = (int)(kt & 1);
+      if (kt + 1 < nk) {
+        X3_STORE(cur ^ 1, 0);                       // slice kt + 1 (loaded one iteration ago)
+        if (kt + 2 < nk) X3_LOAD((kt + 2) * 16, 0);  // slice kt + 2 stays in flight over these MFMAs
+      }
+      X3_COMPUTE(cur, MB);
+      __syncthreads();  // buffer cur is free, buffer cur ^ 1 is complete
     }
-    X3_COMPUTE(cur);
-    __syncthreads();  // buffer cur is free, buffer cur ^ 1 is complete
+  } else {
+    // two register stages (odd slices in stage 0, even ones from 2 on in stage 1): a slice's loads
+    // are issued two iterations before it is stored, for tiles with little MFMA work per slice
+    for (int64_t kt = 0; kt < nk; kt += 2) {
+      if (kt + 1 < nk) {
+        X3_STORE(1, 0);                              // slice kt + 1
+        if (kt + 3 < nk) X3_LOAD((kt + 3) * 16, 0);
+      }
+      X3_COMPUTE(0, MB);
+      __syncthreads();
+      if (kt + 1 >= nk) break;
+      if (kt + 2 < nk) {
+        X3_STORE(0, 1);                              // slice kt + 2
+        if (kt + 4 < nk) X3_LOAD((kt + 4) * 16, 1);
+      }
+      X3_COMPUTE(1, MB);
+      __syncthreads();
+    }
   }
-  const int64_t row0 = row_blk + wm * 64, col0 = col_blk + wn * 64;
+  const int64_t row0 = row_blk + wm * 32 * MB, col0 = col_blk + wn * 64;
   if (radd.src) {
     // C[r, :] += radd[radd.idx[r], :] (a gathered row added to the product)
 #pragma unroll
-    for (int bi = 0; bi < 2; ++bi)
+    for (int bi = 0; bi < MB; ++bi)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int64_t row = min(row0 + bi * 32 + (v / 4) * 8 + h * 4 + (v % 4), m - 1);
@@ -668,10 +700,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
         }
       }
   }
-  if (!bias && !accumulate && act == 0 && row0 + 64 <= m && col0 + 64 <= n) {
+  if (!bias && !accumulate && act == 0 && row0 + 32 * MB <= m && col0 + 64 <= n) {
     float* base = c + (row0 + h * 4) * ldc + col0 + rr;
 #pragma unroll
-    for (int bi = 0; bi < 2; ++bi)
+    for (int bi = 0; bi < MB; ++bi)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         float* rp = base + (int64_t)(bi * 32 + (v / 4) * 8 + (v % 4)) * ldc;
@@ -680,7 +712,50 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
       }
     return;
   }
-  epilogue<2, 2>(acc, row0, col0, m, n, bias, c, ldc, accumulate, act);
+  epilogue<MB, 2>(acc, row0, col0, m, n, bias, c, ldc, accumulate, act);
+}
+
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) gemm_x3_kernel(X3Part P0, X3Part P1, X3Part P2, int np,
+                                                           const float* __restrict__ b, int64_t ldb, X3Part radd,
+                                                           const float* __restrict__ bias, float* c, int64_t ldc,
+                                                           int64_t m, int64_t n, int64_t k, int accumulate, int act,
+                                                           int64_t n_tiles) {
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  x3_tile<2, 1>(P0, P1, P2, np, b, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, (tile / n_tiles) * 128,
+             (tile % n_tiles) * 128);
+}
+
+// Several independent split-plane GEMMs in one launch (the node side of an interaction layer at
+// thousands of atoms): problem g owns the tiles [tile0[g], tile0[g + 1]) of the XCD-aware order,
+// (64 MB) x 128 each, A = [a | a2] (a's width a multiple of 16). Each problem's C is bitwise the
+// one gemm_x3_kernel gives for it (same planes, same K order).
+struct X3GroupDesc {
+  X3Part p0, p1;
+  int np;
+  const float* b;
+  const float* bias;
+  float* c;
+  int64_t ldb, ldc, m, n, k, n_tiles, tile0;
+  int accumulate;
+};
+struct X3Group {
+  X3GroupDesc d[kMaxGroup];
+  int count;
+  int act;
+};
+
+template <int MB>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) gemm_x3_group_kernel(const X3Group grp) {
+  const int64_t w = xcd_tile(blockIdx.x, gridDim.x);
+  int g = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxGroup; ++q)
+    if (q < grp.count && w >= grp.d[q].tile0) g = q;
+  const X3GroupDesc& d = grp.d[g];
+  const int64_t t = w - d.tile0;
+  const X3Part none{};
+  x3_tile<MB, MB == 1 ? 2 : 1>(d.p0, d.p1, d.p1, d.np, d.b, d.ldb, none, d.bias, d.c, d.ldc, d.m, d.n, d.k, d.accumulate, grp.act,
+              (t / d.n_tiles) * (64 * MB), (t % d.n_tiles) * 128);
 }
 
 // ------------------------------------------------- fp32 as three bf16 planes, pre-split operands
@@ -721,7 +796,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
       const float* base_ = q2_ ? fa2 : q1_ ? fa1 : fa0;                                             \
       const int64_t kin_ = q2_ ? k0_ - ks2 : q1_ ? k0_ - ks1 : k0_;                                 \
       const int w_ = q2_ ? w2 : q1_ ? w1 : w0;                                                      \
-      _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                               \
+      _Pragma("unroll") for (int q = 0; q < MB; ++q) {                                              \
         const int64_t o_ = q2_ ? ao2[q] : q1_ ? ao1[q] : ao0[q];                                    \
         ra##S[q] = (kin_ + kc < w_) ? *reinterpret_cast<const float4*>(base_ + o_ + kin_)           \
                                     : make_float4(0.f, 0.f, 0.f, 0.f);                              \
@@ -738,7 +813,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
       _Pragma("unroll") for (int j = 0; j < 3; ++j)                                                 \
         *reinterpret_cast<u32x4*>(sb_ + soffp[j]) = pa##S[j];                                       \
     } else {                                                                                        \
-      _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                               \
+      _Pragma("unroll") for (int q = 0; q < MB; ++q) {                                              \
         bf16x4 x0_, x1_, x2_;                                                                       \
         split3(ra##S[q], x0_, x1_, x2_);                                                            \
         *reinterpret_cast<bf16x4*>(sb_ + 0 * X3_PL + soff[q]) = x0_;                                \
@@ -753,17 +828,17 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // Two register stages (loads issued two slices ahead) measured no faster than one at two waves
 // per SIMD instead of three, so the kernel keeps one stage: slice kt + 1 is stored into LDS and
 // slice kt + 2 loaded into the stage while the MFMAs of slice kt run.
-template <bool APRE>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) gemm_x3p_kernel(
-    X3PPart P0, X3PPart P1, X3PPart P2, int np, const __bf16* __restrict__ bp, int64_t ldb, X3Part radd,
-    const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int accumulate, int act,
-    int64_t n_tiles) {
+// One (64 MB) x 128 tile (MB as in x3_tile; MB = 1 with fp32 A only).
+template <bool APRE, int MB>
+__device__ __forceinline__ void x3p_tile(const X3PPart& P0, const X3PPart& P1, const X3PPart& P2, int np,
+                                         const __bf16* __restrict__ bp, int64_t ldb, const X3Part& radd,
+                                         const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n,
+                                         int64_t k, int accumulate, int act, int64_t row_blk, int64_t col_blk) {
+  static_assert(MB == 2 || !APRE, "64-row tiles take fp32 A");
   __shared__ __attribute__((aligned(16))) __bf16 lds[2 * X3_BUF];
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, rr = lane & 31;
-  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
-  const int64_t row_blk = (tile / n_tiles) * 128, col_blk = (tile % n_tiles) * 128;
   const int64_t ks1 = P0.width, ks2 = ks1 + (np > 1 ? P1.width : 0);
   const int w0 = P0.width, w1 = P1.width, w2 = P2.width;
   const __bf16 *ap0 = static_cast<const __bf16*>(P0.src), *ap1 = static_cast<const __bf16*>(P1.src),
@@ -791,7 +866,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
   int soff[2];
   if (!APRE) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < MB; ++q) {
       const int r = (t + q * kThreads) >> 2;
       const int64_t gr = min(row_blk + r, m - 1);
       ao0[q] = (P0.idx ? (int64_t)P0.idx[gr * P0.istride] : gr) * P0.ld + kc;
@@ -802,10 +877,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
   }
   const int rd = rr * 16 + ((h ^ ((rr >> 3) & 1)) * 8);  // this lane's 8 k of its MFMA row
   u32x4 pa0[3], pb0[3];
-  float4 ra0[2];
-  f32x16 acc[2][2];
+  float4 ra0[MB];
+  f32x16 acc[MB][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -822,13 +897,13 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
       XP_STORE(cur ^ 1, 0);                       // slice kt + 1 (loaded one iteration ago)
       if (kt + 2 < nk) XP_LOAD((kt + 2) * 16, 0);  // slice kt + 2 stays in flight over these MFMAs
     }
-    X3_COMPUTE(cur);
+    X3_COMPUTE(cur, MB);
     __syncthreads();  // buffer cur is free, buffer cur ^ 1 is complete
   }
-  const int64_t row0 = row_blk + wm * 64, col0 = col_blk + wn * 64;
+  const int64_t row0 = row_blk + wm * 32 * MB, col0 = col_blk + wn * 64;
   if (radd.src) {
 #pragma unroll
-    for (int bi = 0; bi < 2; ++bi)
+    for (int bi = 0; bi < MB; ++bi)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int64_t row = min(row0 + bi * 32 + (v / 4) * 8 + h * 4 + (v % 4), m - 1);
@@ -840,10 +915,10 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
         }
       }
   }
-  if (!bias && !accumulate && act == 0 && row0 + 64 <= m && col0 + 64 <= n) {
+  if (!bias && !accumulate && act == 0 && row0 + 32 * MB <= m && col0 + 64 <= n) {
     float* base = c + (row0 + h * 4) * ldc + col0 + rr;
 #pragma unroll
-    for (int bi = 0; bi < 2; ++bi)
+    for (int bi = 0; bi < MB; ++bi)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         float* rp = base + (int64_t)(bi * 32 + (v / 4) * 8 + (v % 4)) * ldc;
@@ -852,7 +927,51 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
       }
     return;
   }
-  epilogue<2, 2>(acc, row0, col0, m, n, bias, c, ldc, accumulate, act);
+  epilogue<MB, 2>(acc, row0, col0, m, n, bias, c, ldc, accumulate, act);
+}
+
+template <bool APRE>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) gemm_x3p_kernel(
+    X3PPart P0, X3PPart P1, X3PPart P2, int np, const __bf16* __restrict__ bp, int64_t ldb, X3Part radd,
+    const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int accumulate, int act,
+    int64_t n_tiles) {
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  x3p_tile<APRE, 2>(P0, P1, P2, np, bp, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, (tile / n_tiles) * 128,
+                    (tile % n_tiles) * 128);
+}
+
+// Several independent GEMMs with pre-split weights in one launch (the node side of an interaction
+// layer at thousands of atoms): problem g owns the tiles [tile0[g], tile0[g + 1]) of the XCD-aware
+// order, (64 MB) x 128 each; A = [a | a2] fp32 (a's width a multiple of 16), split as it is
+// staged; B the planes of a [N, K] weight. Each problem's C is bitwise the one gemm_x3_kernel
+// gives for it (same planes, same K order).
+struct X3PGroupDesc {
+  X3PPart p0, p1;
+  int np;
+  const __bf16* b;
+  const float* bias;
+  float* c;
+  int64_t ldb, ldc, m, n, k, n_tiles, tile0;
+  int accumulate;
+};
+struct X3PGroup {
+  X3PGroupDesc d[kMaxGroup];
+  int count;
+  int act;
+};
+
+template <int MB>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) gemm_x3p_group_kernel(const X3PGroup grp) {
+  const int64_t w = xcd_tile(blockIdx.x, gridDim.x);
+  int g = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxGroup; ++q)
+    if (q < grp.count && w >= grp.d[q].tile0) g = q;
+  const X3PGroupDesc& d = grp.d[g];
+  const int64_t t = w - d.tile0;
+  const X3Part none{};
+  x3p_tile<false, MB>(d.p0, d.p1, d.p1, d.np, d.b, d.ldb, none, d.bias, d.c, d.ldc, d.m, d.n, d.k, d.accumulate,
+                      grp.act, (t / d.n_tiles) * (64 * MB), (t % d.n_tiles) * 128);
 }
 
 #undef XP_LOAD
@@ -924,6 +1043,12 @@ int launch_gemm_x3(int32_t n_parts, const float* const* srcs, const int32_t* con
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
+
+// A grouped launch runs as split-plane GEMMs from this many 128 x 128 tiles in all (the node side
+// of a layer at ~5 000 atoms and above); below, the 64 x 64 fp32 kernel's four times more
+// workgroups win.
+constexpr int64_t kGroupX3MinTiles = 128;
+constexpr int64_t kGroupX3HalfTilesBelow = 3 * 256;
 
 // Tile choice: 128 x 128 when that still gives two workgroups per CU (256 CUs), else 64 x 64
 // (small node-side GEMMs and the 135-atom edge GEMM: 4x more workgroups, 4x less serial K work
@@ -1052,6 +1177,12 @@ int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda,
   GemmGroup grp{};
   grp.act = epilogue_kind;
   int64_t tiles = 0;
+  // the split-plane form, when every problem allows it: B [N, K], 16-byte aligned rows, K split at a
+  // multiple of 16
+  X3Group xg{};
+  xg.act = epilogue_kind;
+  bool x3_ok = b_layout == 0;
+  int64_t big = 0;
   for (int g = 0; g < count; ++g) {
     GemmDesc& d = grp.d[grp.count];
     FMD_REQUIRE(m[g] >= 0 && n[g] >= 0 && k[g] >= 0);
@@ -1080,13 +1211,101 @@ int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda,
     d.tile0 = tiles;
     tiles += fmd_cdiv(m[g], 64) * d.tiles_n;
     ++grp.count;
+    x3_ok = x3_ok && k[g] > 0 && k[g] < (int64_t(1) << 30) && k[g] % 4 == 0 && aligned16(a[g]) && lda[g] % 4 == 0 &&
+            aligned16(b[g]) && ldb[g] % 4 == 0 && (!split || (ks % 16 == 0 && aligned16(a2[g]) && lda2[g] % 4 == 0));
+    if (x3_ok) {
+      X3GroupDesc& x = xg.d[xg.count++];
+      x.p0 = X3Part{a[g], nullptr, lda[g], 1, (int32_t)ks};
+      x.p1 = split ? X3Part{a2[g], nullptr, lda2[g], 1, (int32_t)(k[g] - ks)} : X3Part{};
+      x.np = split ? 2 : 1;
+      x.b = b[g];
+      x.bias = d.bias;
+      x.c = c[g];
+      x.ldb = ldb[g];
+      x.ldc = ldc[g];
+      x.m = m[g];
+      x.n = n[g];
+      x.k = k[g];
+      x.n_tiles = fmd_cdiv(n[g], 128);
+      x.accumulate = d.accumulate;
+      big += fmd_cdiv(m[g], 128) * x.n_tiles;
+    }
   }
   if (grp.count == 0) return FMD_OK;
   FMD_REQUIRE(tiles < (int64_t(1) << 31));
+  if (x3_ok && big >= kGroupX3MinTiles) {
+    // 64-row tiles while 128-row ones would not give three workgroups per CU
+    const int mb = big < kGroupX3HalfTilesBelow ? 1 : 2;
+    int64_t t0 = 0;
+    for (int g = 0; g < xg.count; ++g) {
+      xg.d[g].tile0 = t0;
+      t0 += fmd_cdiv(xg.d[g].m, 64 * mb) * xg.d[g].n_tiles;
+    }
+    FMD_REQUIRE(t0 < (int64_t(1) << 31));
+    if (mb == 1)
+      hipLaunchKernelGGL(gemm_x3_group_kernel<1>, dim3((unsigned)t0), dim3(kThreads), 0, stream, xg);
+    else
+      hipLaunchKernelGGL(gemm_x3_group_kernel<2>, dim3((unsigned)t0), dim3(kThreads), 0, stream, xg);
+    FMD_CHECK_LAUNCH();
+    return FMD_OK;
+  }
   if (b_layout == 0)
     hipLaunchKernelGGL(gemm_f32_group_kernel<0>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
   else
     hipLaunchKernelGGL(gemm_f32_group_kernel<1>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_gemm_group_x3_planes_f32(int32_t count, const float* const* a, const int64_t* lda, const float* const* a2,
+                                 const int64_t* lda2, const int64_t* ksplit, const uint16_t* const* b_planes,
+                                 const int64_t* ldb, const float* const* bias, float* const* c, const int64_t* ldc,
+                                 const int64_t* m, const int64_t* n, const int64_t* k, const int32_t* accumulate,
+                                 int32_t epilogue_kind, hipStream_t stream) {
+  FMD_REQUIRE(count >= 1 && count <= kMaxGroup && a && lda && b_planes && ldb && c && ldc && m && n && k);
+  FMD_REQUIRE(epilogue_kind == 0 || epilogue_kind == 1);
+  X3PGroup grp{};
+  grp.act = epilogue_kind;
+  int64_t big = 0;
+  for (int g = 0; g < count; ++g) {
+    FMD_REQUIRE(m[g] >= 0 && n[g] >= 0 && k[g] >= 0);
+    if (m[g] == 0 || n[g] == 0) continue;
+    FMD_REQUIRE(c[g] && ldc[g] >= n[g]);
+    const bool split = a2 && a2[g];
+    const int64_t ks = split ? ksplit[g] : k[g];
+    FMD_REQUIRE(k[g] > 0 && k[g] < (int64_t(1) << 30) && a[g] && b_planes[g] && lda[g] >= ks);
+    FMD_REQUIRE(!split || (lda2 && ks > 0 && ks < k[g] && lda2[g] >= k[g] - ks));
+    if (!aligned16(a[g]) || lda[g] % 4 || ks % 4 || !aligned16(b_planes[g]) || ldb[g] != 48 * fmd_cdiv(k[g], 16))
+      return FMD_EUNSUPPORTED;
+    if (split && (ks % 16 || !aligned16(a2[g]) || lda2[g] % 4 || (k[g] - ks) % 4)) return FMD_EUNSUPPORTED;
+    X3PGroupDesc& d = grp.d[grp.count++];
+    d.p0 = X3PPart{a[g], nullptr, lda[g], 1, (int32_t)ks};
+    d.p1 = split ? X3PPart{a2[g], nullptr, lda2[g], 1, (int32_t)(k[g] - ks)} : X3PPart{};
+    d.np = split ? 2 : 1;
+    d.b = reinterpret_cast<const __bf16*>(b_planes[g]);
+    d.bias = bias ? bias[g] : nullptr;
+    d.c = c[g];
+    d.ldb = ldb[g];
+    d.ldc = ldc[g];
+    d.m = m[g];
+    d.n = n[g];
+    d.k = k[g];
+    d.n_tiles = fmd_cdiv(n[g], 128);
+    d.accumulate = accumulate ? accumulate[g] : 0;
+    big += fmd_cdiv(m[g], 128) * d.n_tiles;
+  }
+  if (grp.count == 0) return FMD_OK;
+  const int mb = big < kGroupX3HalfTilesBelow ? 1 : 2;
+  int64_t t0 = 0;
+  for (int g = 0; g < grp.count; ++g) {
+    grp.d[g].tile0 = t0;
+    t0 += fmd_cdiv(grp.d[g].m, 64 * mb) * grp.d[g].n_tiles;
+  }
+  FMD_REQUIRE(t0 < (int64_t(1) << 31));
+  if (mb == 1)
+    hipLaunchKernelGGL(gemm_x3p_group_kernel<1>, dim3((unsigned)t0), dim3(kThreads), 0, stream, grp);
+  else
+    hipLaunchKernelGGL(gemm_x3p_group_kernel<2>, dim3((unsigned)t0), dim3(kThreads), 0, stream, grp);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -131,7 +131,9 @@ class MaceLike(nn.Module):
     def node_weights(self, t: int) -> dict:
         """Layer t's node-side weights in the layouts of the fused node kernels ([columns, K],
         K-contiguous): wm0t = Wm0^T, wm1t = Wm1^T, wout0 = [Wo0; Wsc0]^T, wout1 = [Wo1; 0]^T (forward)
-        and wo0st = [Wo0; Wsc0], wo1st = [Wo1; 0] (VJP); rebuilt when a weight changes in place."""
+        and wo0st = [Wo0; Wsc0], wo1st = [Wo1; 0] (VJP), and wo1t = Wo1^T for the grouped forward
+        GEMMs; "planes" holds the bf16 planes of the grouped GEMMs' [N, K] weights (forward: wm0t,
+        wm1t, wout0, wo1t; VJP: Wo0, Wo1, Wsc0, Wm0, Wm1); rebuilt when a weight changes in place."""
         layer = self.layers[t]
         mats = (layer.Wm0, layer.Wm1, layer.Wo0, layer.Wo1, layer.Wsc0)
         key = tuple((w.data_ptr(), w._version, w.device) for w in mats)
@@ -140,11 +142,15 @@ class MaceLike(nn.Module):
         if hit is None or hit[0] != key:
             wm0, wm1, wo0, wo1, wsc0 = (w.detach() for w in mats)
             zero = torch.zeros_like(wo1)
-            hit = (key, {"wm0t": wm0.t().contiguous(), "wm1t": wm1.t().contiguous(),
-                         "wout0": torch.cat([wo0, wsc0], 0).t().contiguous(),
-                         "wout1": torch.cat([wo1, zero], 0).t().contiguous(),
-                         "wo0st": torch.cat([wo0, wsc0], 0).contiguous(),
-                         "wo1st": torch.cat([wo1, zero], 0).contiguous()})
+            w = {"wm0t": wm0.t().contiguous(), "wm1t": wm1.t().contiguous(),
+                 "wout0": torch.cat([wo0, wsc0], 0).t().contiguous(),
+                 "wout1": torch.cat([wo1, zero], 0).t().contiguous(),
+                 "wo0st": torch.cat([wo0, wsc0], 0).contiguous(),
+                 "wo1st": torch.cat([wo1, zero], 0).contiguous(), "wo1t": wo1.t().contiguous()}
+            src = {"wm0t": w["wm0t"], "wm1t": w["wm1t"], "wout0": w["wout0"], "wo1t": w["wo1t"], "Wo0": wo0,
+                   "Wo1": wo1, "Wsc0": wsc0, "Wm0": wm0, "Wm1": wm1}
+            w["planes"] = {name: split_planes(x.contiguous()) for name, x in src.items()}
+            hit = (key, w)
             cache[t] = hit
         return hit[1]
 
@@ -324,19 +330,24 @@ class _MaceLikeEnergy(Function):
                       B0.data_ptr(), _abi.ptr(B1), h0n.data_ptr(), _abi.ptr(h1n))
             else:
                 # the node side as two grouped GEMM launches around the contraction:
-                # (P0 = A0 Wm0, P1 = A1 Wm1), then (h0n = [B0 | h0] [Wo0; Wsc0], h1n = B1 Wo1)
+                # (P0 = A0 Wm0, P1 = A1 Wm1), then (h0n = [B0 | h0] [Wo0; Wsc0], h1n = B1 Wo1), with
+                # the weights K-contiguous (the split-plane form of a large group)
+                w = model.node_weights(t)
+                wp = w["planes"]
                 P0 = _empty(n, C, device=dev)
                 P1 = _empty(n, 3, C, device=dev)
-                gemm_group([{"a": A0, "b": layer.Wm0, "out": P0},
-                            {"a": A1.view(3 * n, C), "b": layer.Wm1, "out": P1.view(3 * n, C)}], b_layout=1)
+                gemm_group([{"a": A0, "b": w["wm0t"], "b_planes": wp["wm0t"], "out": P0},
+                            {"a": A1.view(3 * n, C), "b": w["wm1t"], "b_planes": wp["wm1t"],
+                             "out": P1.view(3 * n, C)}], b_layout=0)
                 _call("fmd_mace_symcon_f32", P0.data_ptr(), P1.data_ptr(), elem.data_ptr(), layer.Wc.data_ptr(),
                       layer.Wd.data_ptr(), n, C, B0.data_ptr(), _abi.ptr(B1))
                 h0n = _empty(n, C, device=dev)
                 h1n = None if last else _empty(n, 3, C, device=dev)
-                probs = [{"a": B0, "a2": h0, "b": model.node_weights(t)["wo0st"], "out": h0n}]
+                probs = [{"a": B0, "a2": h0, "b": w["wout0"], "b_planes": wp["wout0"], "out": h0n}]
                 if not last:
-                    probs.append({"a": B1.view(3 * n, C), "b": layer.Wo1, "out": h1n.view(3 * n, C)})
-                gemm_group(probs, b_layout=1)
+                    probs.append({"a": B1.view(3 * n, C), "b": w["wo1t"], "b_planes": wp["wo1t"],
+                                  "out": h1n.view(3 * n, C)})
+                gemm_group(probs, b_layout=0)
             saved.append((h0, h1, z, q, P0, P1))
             if t == 0:
                 h_first = h0n
@@ -408,22 +419,26 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
             # gB1 = g_out1 Wo1^T, and with t > 0 this layer's input gradient through the residual,
             # g_in0 = g_out0 Wsc0^T, added to the first readout's gradient in the second layer),
             # then (gA0 = gP0 Wm0^T, gA1 = gP1 Wm1^T)
+            wp = model.node_weights(t)["planes"]
             gB0 = _empty(n, C, device=dev)
             gB1 = None if g_out1 is None else _empty(n, 3, C, device=dev)
-            probs = [{"a": g_out0, "b": layer.Wo0, "out": gB0}]
+            probs = [{"a": g_out0, "b": layer.Wo0, "b_planes": wp["Wo0"], "out": gB0}]
             if gB1 is not None:
-                probs.append({"a": g_out1.reshape(3 * n, C), "b": layer.Wo1, "out": gB1.view(3 * n, C)})
+                probs.append({"a": g_out1.reshape(3 * n, C), "b": layer.Wo1, "b_planes": wp["Wo1"],
+                              "out": gB1.view(3 * n, C)})
             if t > 0:
                 g_in0 = gha if t == 1 else _empty(n, C, device=dev)
-                probs.append({"a": g_out0, "b": layer.Wsc0, "out": g_in0, "accumulate": t == 1})
+                probs.append({"a": g_out0, "b": layer.Wsc0, "b_planes": wp["Wsc0"], "out": g_in0,
+                              "accumulate": t == 1})
             gemm_group(probs, b_layout=0)
             _call("fmd_mace_symcon_bwd_f32", P0.data_ptr(), P1.data_ptr(), inputs.elem.data_ptr(),
                   layer.Wc.data_ptr(), layer.Wd.data_ptr(), gB0.data_ptr(), _abi.ptr(gB1), n, C, gP0.data_ptr(),
                   gP1.data_ptr())
             gA0 = _empty(n, C, device=dev)
             gA1 = _empty(n, 3, C, device=dev)
-            gemm_group([{"a": gP0, "b": layer.Wm0, "out": gA0},
-                        {"a": gP1.view(3 * n, C), "b": layer.Wm1, "out": gA1.view(3 * n, C)}], b_layout=0)
+            gemm_group([{"a": gP0, "b": layer.Wm0, "b_planes": wp["Wm0"], "out": gA0},
+                        {"a": gP1.view(3 * n, C), "b": layer.Wm1, "b_planes": wp["Wm1"],
+                         "out": gA1.view(3 * n, C)}], b_layout=0)
         acc_geo = 1 if t < L - 1 else 0
         if t == 0:
             # the first layer's inputs are the element embedding (no position dependence): only

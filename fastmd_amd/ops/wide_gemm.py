@@ -57,11 +57,19 @@ def gemm(a: Tensor, b: Tensor, *, b_layout: int, bias: Tensor | None = None, out
     return out
 
 
+# 128 x 128 tiles from which a grouped launch takes the split-plane form (the C library's own
+# threshold for fmd_gemm_group_f32)
+GROUP_X3_MIN_TILES = 128
+
+
 def gemm_group(problems, *, b_layout: int, epilogue: str | None = None) -> list:
     """Up to four independent ``gemm`` problems of one ``b_layout`` in one launch
     (fmd_gemm_group_f32). Each problem is a dict with ``a``, ``b``, ``out`` (float32, preallocated,
     unit column stride) and optionally ``a2`` (extra K columns: ``[a | a2] @ op(b)``, a's width a
-    multiple of 32), ``bias``, ``accumulate``. Returns the outputs."""
+    multiple of 32), ``bias``, ``accumulate``, and ``b_planes`` (``split_planes(b)`` of a
+    ``b_layout`` 0 weight): when every problem has them and the group is large enough for the
+    split-plane form, the launch reads the planes (fmd_gemm_group_x3_planes_f32; the same bits
+    as splitting ``b`` in the kernel). Returns the outputs."""
     if not 1 <= len(problems) <= 4:
         raise ValueError("gemm_group takes one to four problems")
     cols = {k: [] for k in ("a", "lda", "a2", "lda2", "ksplit", "b", "ldb", "bias", "c", "ldc", "m", "n", "k", "acc")}
@@ -107,6 +115,22 @@ def gemm_group(problems, *, b_layout: int, epilogue: str | None = None) -> list:
         cols["k"].append(k)
         cols["acc"].append(1 if p.get("accumulate") else 0)
     i64 = lambda key: _abi.array(_abi._i64, cols[key])  # noqa: E731
+    planes = [p.get("b_planes") for p in problems]
+    tiles = sum(-(-m // 128) * -(-n // 128) for m, n in zip(cols["m"], cols["n"]))
+    if b_layout == 0 and all(q is not None for q in planes) and tiles >= GROUP_X3_MIN_TILES:
+        for q, p in zip(planes, problems):
+            require_cuda(q.data)
+            if q.width != p["b"].shape[1] or q.data.shape[0] != p["b"].shape[0]:
+                raise ValueError("gemm_group: b_planes are not the planes of b")
+        status = _abi.load().fmd_gemm_group_x3_planes_f32(
+            len(problems), _abi.ptr_array(cols["a"]), i64("lda"), _abi.ptr_array(cols["a2"]), i64("lda2"),
+            i64("ksplit"), _abi.ptr_array([q.data.data_ptr() for q in planes]),
+            _abi.array(_abi._i64, [q.ld for q in planes]), _abi.ptr_array(cols["bias"]), _abi.ptr_array(cols["c"]),
+            i64("ldc"), i64("m"), i64("n"), i64("k"), _abi.array(_abi._i32, cols["acc"]), _EPILOGUES[epilogue],
+            stream())
+        if status != _EUNSUPPORTED:
+            _abi.check(status, "fmd_gemm_group_x3_planes_f32")
+            return [p["out"] for p in problems]
     _abi.call("fmd_gemm_group_f32", len(problems), _abi.ptr_array(cols["a"]), i64("lda"), _abi.ptr_array(cols["a2"]),
               i64("lda2"), i64("ksplit"), _abi.ptr_array(cols["b"]), i64("ldb"), b_layout,
               _abi.ptr_array(cols["bias"]), _abi.ptr_array(cols["c"]), i64("ldc"), i64("m"), i64("n"), i64("k"),

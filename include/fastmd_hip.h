@@ -305,8 +305,10 @@ int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32
 /* Up to four independent fmd_gemm_f32 problems of one b_layout in one launch (arrays of length
  * count, problem g: C_g = [A_g | A2_g] op(B_g) (+ bias_g) (+ C_g if accumulate_g)). A2_g (may be
  * null, or the a2 array itself null) supplies K columns [ksplit_g, K_g) with row stride lda2_g;
- * ksplit_g % 32 == 0. Every problem runs the 64 x 64 fp32 MFMA tiles of fmd_gemm_f32 (same K
- * order). Replaces several linear / matmul calls on independent operands
+ * ksplit_g % 32 == 0. Small groups run the 64 x 64 fp32 MFMA tiles of fmd_gemm_f32 (same K
+ * order); from 128 tiles of 128 x 128 in all, a group with b_layout 0, K % 4 == 0 and 16-byte
+ * aligned rows runs as fp32-accurate split-plane GEMMs (three bf16 planes per operand, the
+ * product of fmd_gemm_f32's split-plane tiles). Replaces several linear / matmul calls on independent operands
  * (triton_wide_gemm.py:482-553) with one launch: the node side of an interaction layer, whose
  * per-layer GEMMs are each too small to fill the chip. bias and accumulate may be null. */
 int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda, const float* const* a2,
@@ -314,6 +316,20 @@ int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda,
                        int32_t b_layout, const float* const* bias, float* const* c, const int64_t* ldc,
                        const int64_t* m, const int64_t* n, const int64_t* k, const int32_t* accumulate,
                        int32_t epilogue, hipStream_t stream);
+
+/* fmd_gemm_group_f32 with b_layout 0 and each weight given as its bf16 planes (fmd_split3_f32 of
+ * the [N_g, K_g] weight, row stride ldb_g = 48 ceil(K_g / 16)): the split-plane product of
+ * fmd_gemm_f32 (bitwise the same C), without splitting the weights again in every workgroup.
+ * Tiles of 64 x 128 while the group has fewer than 768 tiles of 128 x 128. Conditions: A_g, A2_g
+ * and the planes 16-byte aligned, lda_g, lda2_g, ksplit_g and K_g - ksplit_g multiples of 4,
+ * ksplit_g a multiple of 16 when A2_g is set; FMD_EUNSUPPORTED otherwise (nothing launched).
+ * Replaces the same linear / matmul calls as fmd_gemm_group_f32 (triton_wide_gemm.py:482-553). */
+int fmd_gemm_group_x3_planes_f32(int32_t count, const float* const* a, const int64_t* lda,
+                                 const float* const* a2, const int64_t* lda2, const int64_t* ksplit,
+                                 const uint16_t* const* b_planes, const int64_t* ldb,
+                                 const float* const* bias, float* const* c, const int64_t* ldc,
+                                 const int64_t* m, const int64_t* n, const int64_t* k,
+                                 const int32_t* accumulate, int32_t epilogue, hipStream_t stream);
 
 /* C = [A | A2] op(B) (+ bias) (+ C if accumulate) as fmd_gemm_f32, with K cut into `splits` equal
  * slices (multiples of 32, none straddling ksplit, the width of A; A2 may be null) multiplied by

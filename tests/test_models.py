@@ -104,13 +104,15 @@ def _gpu_builder(s, u_cap, device):
 @pytest.mark.parametrize("n_cells,channels,hoist,fused", [
     (3, 128, None, True), (3, 64, None, True), (3, 256, None, True), ((6, 6, 6), 128, None, True),
     (3, 64, 0, True), (3, 128, 0, True), (3, 256, 0, True), ((6, 6, 6), 128, 10 ** 9, True),
-    (3, 64, None, False), (3, 128, None, False), (3, 256, None, False), ((6, 6, 6), 128, None, False)])
+    (3, 64, None, False), (3, 128, None, False), (3, 256, None, False), ((6, 6, 6), 128, None, False),
+    ((10, 10, 10), 128, None, False)])
 def test_mace_like_gpu_matches_oracle(device, n_cells, channels, hoist, fused, monkeypatch):
     """Energies within 1e-5 eV/atom and forces within 1e-4 eV/A of the FP64 oracle, through the
     fixed-capacity builder (padding rows present), bitwise reproducible. ``hoist`` overrides the
     edge-list size from which the receiver block of the edge GEMM is formed per atom (0: always,
     10**9: never), so both evaluation orders of z are checked at every width; ``fused`` selects the
-    fused node kernels or the unfused chain of GEMMs and contraction kernels."""
+    fused node kernels or the unfused chain of GEMMs and contraction kernels; at 5 000 atoms the
+    unfused node GEMMs take their split-plane grouped form."""
     from fastmd_amd.engine.energy_derivative import EnergyDerivative
     from fastmd_amd.models import mace_like
     from fastmd_amd.models.mace_like import MaceLikeAdapter

@@ -257,6 +257,62 @@ def test_gemm_group_matches_single_gemms_and_fp64(device, b_layout):
 
 
 @pytest.mark.gpu
+def test_gemm_group_split_plane_form(device):
+    """A large fmd_gemm_group_f32 group with B [N, K] (the node side of a layer at 10 000 atoms:
+    >= 128 tiles of 128 x 128) runs as split-plane GEMMs: each problem within fp32 of float64 and
+    bitwise equal to fmd_gemm_f32's split-plane kernel on the same problem (M large enough that it
+    takes that kernel; a K split at 128 gives the concatenated operand's bits), in the 64-row and
+    the 128-row tile forms, with the weights split in the kernel or given as planes."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm, gemm_group
+
+    g = torch.Generator().manual_seed(12)
+    C = 128
+    a0, a1 = torch.randn(33000, C, generator=g), torch.randn(33000, C, generator=g)
+    w0 = torch.randn(C, C, generator=g) / C ** 0.5
+    w1 = torch.randn(C, 2 * C, generator=g) / (2 * C) ** 0.5  # [N, K]: [a0 | a1] W1^T
+    c1 = torch.randn(33000, C, generator=g)
+    bias = torch.randn(C, generator=g)
+    d = lambda t: t.to(device)  # noqa: E731
+    out0 = torch.empty(33000, C, device=device)
+    out1 = d(c1)
+    gemm_group([{"a": d(a0), "b": d(w0), "out": out0},
+                {"a": d(a0), "a2": d(a1), "b": d(w1), "out": out1, "accumulate": True, "bias": d(bias)}], b_layout=0)
+    ref0 = a0.double() @ w0.double().t()
+    ref1 = torch.cat([a0, a1], 1).double() @ w1.double().t() + c1.double() + bias.double()
+    assert oops.relative(out0.cpu().numpy(), ref0.numpy()) < 1e-5
+    assert oops.relative(out1.cpu().numpy(), ref1.numpy()) < 1e-5
+    assert torch.equal(out0, gemm(d(a0), d(w0), b_layout=0))
+    single = d(c1)
+    gemm(d(torch.cat([a0, a1], 1)), d(w1), b_layout=0, out=single, accumulate=True, bias=d(bias))
+    assert torch.equal(out1, single)
+    # with the weights' planes given (split once, fmd_gemm_group_x3_planes_f32): the same bits
+    from fastmd_amd.ops.wide_gemm import split_planes
+
+    out0p, out1p = torch.empty(33000, C, device=device), d(c1)
+    gemm_group([{"a": d(a0), "b": d(w0), "b_planes": split_planes(d(w0)), "out": out0p},
+                {"a": d(a0), "a2": d(a1), "b": d(w1), "b_planes": split_planes(d(w1)), "out": out1p,
+                 "accumulate": True, "bias": d(bias)}], b_layout=0)
+    assert torch.equal(out0p, out0) and torch.equal(out1p, out1)
+    # 128-row tiles once a group has three per CU (782 here): the same bits as the 64-row form
+    a2 = torch.randn(100000, C, generator=g)
+    out2 = torch.empty(100000, C, device=device)
+    gemm_group([{"a": d(a2), "b": d(w0), "out": out2}], b_layout=0)
+    assert torch.equal(out2, gemm(d(a2), d(w0), b_layout=0))
+    assert torch.equal(out2[:33000], gemm(d(a2[:33000]), d(w0), b_layout=0))
+    assert oops.relative(out2.cpu().numpy(), (a2.double() @ w0.double().t()).numpy()) < 1e-5
+    out2p = torch.empty(100000, C, device=device)
+    gemm_group([{"a": d(a2), "b": d(w0), "b_planes": split_planes(d(w0)), "out": out2p}], b_layout=0)
+    assert torch.equal(out2p, out2)
+    # the fp32 form of the same group (B [K, N]) agrees to fp32 rounding
+    out0f = torch.empty(33000, C, device=device)
+    gemm_group([{"a": d(a0), "b": d(w0.t().contiguous()), "out": out0f}], b_layout=1)
+    assert oops.relative(out0f.cpu().numpy(), ref0.numpy()) < 1e-5
+    assert not torch.equal(out0f, out0)  # a different product: the form switch is real
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("F", [64, 128])
 def test_gemm_bf16_against_fp64_of_rounded_inputs(device, F):
     import torch
