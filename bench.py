@@ -28,7 +28,7 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 SPLIT_PRODUCTS = 6  # fp32-accurate GEMM: three bf16 planes per operand, six MFMA products
 SPIN_CYCLES = 20_000_000  # GPU clock cycles of torch.cuda._sleep (several ms)
-ROOFLINE_KERNEL = "gemm_x3p_kernel<true>"
+ROOFLINE_KERNEL = "gemm_x3p_dma_kernel"
 STEPS_PER_LAUNCH = 10
 
 
@@ -99,7 +99,7 @@ def gemm_roofline(md) -> dict:
     """The dominant kernel of the 10 000-atom step: the second layer's edge GEMM,
     z = [h0[src] | ef] @ W1[sender and radial rows] (the receiver block h0[dst] @ W1[C:2C] is formed
     per atom and added by the message kernels), with the gather-cat fused into the operand load
-    and the operands pre-split into bf16 planes (gemm_x3p_kernel<true>: [e_cap, C+8] x [C+8, 4C],
+    and the operands pre-split into bf16 planes (gemm_x3p_dma_kernel: [e_cap, C+8] x [C+8, 4C],
     fp32-accurate as six bf16 MFMA products). It is timed in the context of the step: HIP events on
     torch's current stream (the stream it is launched on) around every edge GEMM of 10 eager force
     evaluations at the run's final state (its edge list, capacity and features), the model's own

@@ -605,6 +605,42 @@ constexpr int X3_PL = 128 * 16, X3_OP = 3 * X3_PL, X3_BUF = 2 * X3_OP;
     }                                                                                               \
   } while (0)
 
+// The end of a split-plane tile: C (+)= acc (+ radd[radd.idx[r]]) (+ bias), then the activation;
+// interior wave tiles without bias / accumulate / activation store straight from the accumulators.
+template <int MB>
+__device__ __forceinline__ void x3_finish(f32x16 (&acc)[MB][2], const X3Part& radd, const float* __restrict__ bias,
+                                          float* c, int64_t ldc, int64_t m, int64_t n, int accumulate, int act,
+                                          int64_t row0, int64_t col0, int h, int rr) {
+  if (radd.src) {
+    // C[r, :] += radd[radd.idx[r], :] (a gathered row added to the product)
+#pragma unroll
+    for (int bi = 0; bi < MB; ++bi)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = min(row0 + bi * 32 + (v / 4) * 8 + h * 4 + (v % 4), m - 1);
+        const float* qr = radd.src + (radd.idx ? (int64_t)radd.idx[row * radd.istride] : row) * radd.ld;
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) {
+          const int64_t col = min(col0 + bj * 32 + rr, n - 1);
+          acc[bi][bj][v] += qr[col];
+        }
+      }
+  }
+  if (!bias && !accumulate && act == 0 && row0 + 32 * MB <= m && col0 + 64 <= n) {
+    float* base = c + (row0 + h * 4) * ldc + col0 + rr;
+#pragma unroll
+    for (int bi = 0; bi < MB; ++bi)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        float* rp = base + (int64_t)(bi * 32 + (v / 4) * 8 + (v % 4)) * ldc;
+        store_stream(rp, acc[bi][0][v]);
+        store_stream(rp + 32, acc[bi][1][v]);
+      }
+    return;
+  }
+  epilogue<MB, 2>(acc, row0, col0, m, n, bias, c, ldc, accumulate, act);
+}
+
 // One (64 MB) x 128 tile of C at (row_blk, col_blk): A as up to three gathered column parts (K
 // order P0 | P1 | P2), B [N, K] K-contiguous, both split into their planes as they are staged.
 // Each wave computes (32 MB) x 64 of it (MB blocks of 32 x 32 by two); MB = 1 halves the rows per
@@ -685,34 +721,7 @@ __device__ __forceinline__ void x3_tile(const X3Part& P0, const X3Part& P1, cons
     }
   }
   const int64_t row0 = row_blk + wm * 32 * MB, col0 = col_blk + wn * 64;
-  if (radd.src) {
-    // C[r, :] += radd[radd.idx[r], :] (a gathered row added to the product)
-#pragma unroll
-    for (int bi = 0; bi < MB; ++bi)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t row = min(row0 + bi * 32 + (v / 4) * 8 + h * 4 + (v % 4), m - 1);
-        const float* qr = radd.src + (radd.idx ? (int64_t)radd.idx[row * radd.istride] : row) * radd.ld;
-#pragma unroll
-        for (int bj = 0; bj < 2; ++bj) {
-          const int64_t col = min(col0 + bj * 32 + rr, n - 1);
-          acc[bi][bj][v] += qr[col];
-        }
-      }
-  }
-  if (!bias && !accumulate && act == 0 && row0 + 32 * MB <= m && col0 + 64 <= n) {
-    float* base = c + (row0 + h * 4) * ldc + col0 + rr;
-#pragma unroll
-    for (int bi = 0; bi < MB; ++bi)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        float* rp = base + (int64_t)(bi * 32 + (v / 4) * 8 + (v % 4)) * ldc;
-        store_stream(rp, acc[bi][0][v]);
-        store_stream(rp + 32, acc[bi][1][v]);
-      }
-    return;
-  }
-  epilogue<MB, 2>(acc, row0, col0, m, n, bias, c, ldc, accumulate, act);
+  x3_finish<MB>(acc, radd, bias, c, ldc, m, n, accumulate, act, row0, col0, h, rr);
 }
 
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) gemm_x3_kernel(X3Part P0, X3Part P1, X3Part P2, int np,
@@ -761,13 +770,15 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
 // ------------------------------------------------- fp32 as three bf16 planes, pre-split operands
 // The same product as gemm_x3_kernel (same planes, same six MFMA products in the same order, same
 // K order: bitwise the same C) with the operands split into their bf16 planes beforehand
-// (split3_kernel): B always (a weight, split once), A either split (APRE: the planes of per-atom
-// features and per-edge radial rows, split once per evaluation instead of once per column tile)
-// or fp32 split here. Plane arrays are slice-interleaved, [rows][S][3][16] bf16 (S = width / 16
-// rounded up, zero past the width): the three planes of a row's 16-k slice are 96 contiguous
-// bytes, so a slice of a gathered row is one contiguous read. The loader copies them into LDS
-// without arithmetic: the 768 16-byte chunks of an operand slice (128 rows x 3 planes x 2 halves)
-// go to the 256 threads three each, consecutive threads on consecutive chunks of a row.
+// (split3_kernel): B always (a weight, split once), A either as planes (the planes of per-atom
+// features and per-edge radial rows, split once per evaluation instead of once per column tile:
+// gemm_x3p_dma_kernel) or fp32 split here (gemm_x3p_kernel). Plane arrays are slice-interleaved,
+// [rows][S][3][16] bf16 (S = width / 16 rounded up, zero past the width): the three planes of a
+// row's 16-k slice are 96 contiguous bytes, so a slice of a gathered row is one contiguous read.
+// An operand slice in LDS is 768 16-byte slots: slot s holds plane s / 256 of row (s / 2) % 128,
+// stored half s % 2 (logical k-half (s % 2) ^ ((row / 8) % 2), the swizzle X3_COMPUTE reads).
+// Plane loads copy 16-byte chunks without arithmetic, slot s by thread s % 256 (consecutive
+// lanes on consecutive slots: conflict-free LDS stores).
 struct X3PPart {
   const void* src;
   const int32_t* idx;
@@ -777,30 +788,19 @@ struct X3PPart {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-// XP_LOAD(K0, S): slice K0 into register stage S (pa##S / pb##S, or ra##S for fp32 A);
+// XP_LOAD(K0, S): slice K0 into register stage S (ra##S for A, pb##S for B's planes);
 // XP_STORE(BUFI, S): stage S into LDS buffer BUFI
 #define XP_LOAD(K0, S)                                                                              \
   do {                                                                                              \
     const int64_t k0_ = (K0);                                                                       \
-    if constexpr (APRE) {                                                                           \
-      const bool q2_ = k0_ >= ks2, q1_ = !q2_ && k0_ >= ks1;                                        \
-      const __bf16* base_ = q2_ ? ap2 : q1_ ? ap1 : ap0;                                            \
-      const int64_t kin_ = q2_ ? k0_ - ks2 : q1_ ? k0_ - ks1 : k0_;                                 \
-      const bool ok_ = kin_ < (q2_ ? w2 : q1_ ? w1 : w0);                                           \
-      _Pragma("unroll") for (int j = 0; j < 3; ++j) {                                               \
-        const int64_t o_ = (q2_ ? ao2[j] : q1_ ? ao1[j] : ao0[j]) + kin_ * 3;                       \
-        pa##S[j] = ok_ ? *reinterpret_cast<const u32x4*>(base_ + o_) : u32x4{0, 0, 0, 0};           \
-      }                                                                                             \
-    } else {                                                                                        \
-      const bool q2_ = k0_ >= ks2, q1_ = !q2_ && k0_ >= ks1;                                        \
-      const float* base_ = q2_ ? fa2 : q1_ ? fa1 : fa0;                                             \
-      const int64_t kin_ = q2_ ? k0_ - ks2 : q1_ ? k0_ - ks1 : k0_;                                 \
-      const int w_ = q2_ ? w2 : q1_ ? w1 : w0;                                                      \
-      _Pragma("unroll") for (int q = 0; q < MB; ++q) {                                              \
-        const int64_t o_ = q2_ ? ao2[q] : q1_ ? ao1[q] : ao0[q];                                    \
-        ra##S[q] = (kin_ + kc < w_) ? *reinterpret_cast<const float4*>(base_ + o_ + kin_)           \
-                                    : make_float4(0.f, 0.f, 0.f, 0.f);                              \
-      }                                                                                             \
+    const bool q2_ = k0_ >= ks2, q1_ = !q2_ && k0_ >= ks1;                                          \
+    const float* base_ = q2_ ? fa2 : q1_ ? fa1 : fa0;                                               \
+    const int64_t kin_ = q2_ ? k0_ - ks2 : q1_ ? k0_ - ks1 : k0_;                                   \
+    const int w_ = q2_ ? w2 : q1_ ? w1 : w0;                                                        \
+    _Pragma("unroll") for (int q = 0; q < MB; ++q) {                                                \
+      const int64_t o_ = q2_ ? ao2[q] : q1_ ? ao1[q] : ao0[q];                                      \
+      ra##S[q] = (kin_ + kc < w_) ? *reinterpret_cast<const float4*>(base_ + o_ + kin_)             \
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);                                \
     }                                                                                               \
     _Pragma("unroll") for (int j = 0; j < 3; ++j)                                                   \
       pb##S[j] = *reinterpret_cast<const u32x4*>(bp + bo[j] + k0_ * 3);                            \
@@ -809,74 +809,56 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 #define XP_STORE(BUFI, S)                                                                           \
   do {                                                                                              \
     __bf16* sb_ = lds + (BUFI) * X3_BUF;                                                            \
-    if constexpr (APRE) {                                                                           \
-      _Pragma("unroll") for (int j = 0; j < 3; ++j)                                                 \
-        *reinterpret_cast<u32x4*>(sb_ + soffp[j]) = pa##S[j];                                       \
-    } else {                                                                                        \
-      _Pragma("unroll") for (int q = 0; q < MB; ++q) {                                              \
-        bf16x4 x0_, x1_, x2_;                                                                       \
-        split3(ra##S[q], x0_, x1_, x2_);                                                            \
-        *reinterpret_cast<bf16x4*>(sb_ + 0 * X3_PL + soff[q]) = x0_;                                \
-        *reinterpret_cast<bf16x4*>(sb_ + 1 * X3_PL + soff[q]) = x1_;                                \
-        *reinterpret_cast<bf16x4*>(sb_ + 2 * X3_PL + soff[q]) = x2_;                                \
-      }                                                                                             \
+    _Pragma("unroll") for (int q = 0; q < MB; ++q) {                                                \
+      bf16x4 x0_, x1_, x2_;                                                                         \
+      split3(ra##S[q], x0_, x1_, x2_);                                                              \
+      *reinterpret_cast<bf16x4*>(sb_ + 0 * X3_PL + soff[q]) = x0_;                                  \
+      *reinterpret_cast<bf16x4*>(sb_ + 1 * X3_PL + soff[q]) = x1_;                                  \
+      *reinterpret_cast<bf16x4*>(sb_ + 2 * X3_PL + soff[q]) = x2_;                                  \
     }                                                                                               \
     _Pragma("unroll") for (int j = 0; j < 3; ++j)                                                   \
-      *reinterpret_cast<u32x4*>(sb_ + X3_OP + soffp[j]) = pb##S[j];                                 \
+      *reinterpret_cast<u32x4*>(sb_ + X3_OP + (t + j * kThreads) * 8) = pb##S[j];                  \
   } while (0)
 
-// Two register stages (loads issued two slices ahead) measured no faster than one at two waves
-// per SIMD instead of three, so the kernel keeps one stage: slice kt + 1 is stored into LDS and
-// slice kt + 2 loaded into the stage while the MFMAs of slice kt run.
-// One (64 MB) x 128 tile (MB as in x3_tile; MB = 1 with fp32 A only).
-template <bool APRE, int MB>
+// One (64 MB) x 128 tile with fp32 A (MB as in x3_tile) and B's planes. Two register stages
+// (loads issued two slices ahead) measured no faster than one at two waves per SIMD instead of
+// three, so the tile keeps one stage: slice kt + 1 is stored into LDS and slice kt + 2 loaded into
+// the stage while the MFMAs of slice kt run.
+template <int MB>
 __device__ __forceinline__ void x3p_tile(const X3PPart& P0, const X3PPart& P1, const X3PPart& P2, int np,
                                          const __bf16* __restrict__ bp, int64_t ldb, const X3Part& radd,
                                          const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n,
                                          int64_t k, int accumulate, int act, int64_t row_blk, int64_t col_blk) {
-  static_assert(MB == 2 || !APRE, "64-row tiles take fp32 A");
   __shared__ __attribute__((aligned(16))) __bf16 lds[2 * X3_BUF];
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, rr = lane & 31;
   const int64_t ks1 = P0.width, ks2 = ks1 + (np > 1 ? P1.width : 0);
   const int w0 = P0.width, w1 = P1.width, w2 = P2.width;
-  const __bf16 *ap0 = static_cast<const __bf16*>(P0.src), *ap1 = static_cast<const __bf16*>(P1.src),
-               *ap2 = static_cast<const __bf16*>(P2.src);
   const float *fa0 = static_cast<const float*>(P0.src), *fa1 = static_cast<const float*>(P1.src),
               *fa2 = static_cast<const float*>(P2.src);
-  // plane loader: chunk t + 256 j = (row, plane, half) of the slice: row c / 6, plane (c % 6) / 2,
-  // half c % 2; its 8 k sit at 8 (c % 6) in the row's 48-element slice block
-  int soffp[3];
-  int64_t bo[3], ao0[3], ao1[3], ao2[3];
+  // B planes: slot t + 256 j (plane j)
+  int64_t bo[3];
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
-    const int cidx = t + j * kThreads, r = cidx / 6, sub = cidx - r * 6, pl = sub >> 1, hf = sub & 1;
-    soffp[j] = pl * X3_PL + r * 16 + ((hf ^ ((r >> 3) & 1)) * 8);
-    bo[j] = min(col_blk + r, n - 1) * ldb + sub * 8;
-    if (APRE) {
-      const int64_t gr = min(row_blk + r, m - 1);
-      ao0[j] = (P0.idx ? (int64_t)P0.idx[gr * P0.istride] : gr) * P0.ld + sub * 8;
-      ao1[j] = np > 1 ? (P1.idx ? (int64_t)P1.idx[gr * P1.istride] : gr) * P1.ld + sub * 8 : 0;
-      ao2[j] = np > 2 ? (P2.idx ? (int64_t)P2.idx[gr * P2.istride] : gr) * P2.ld + sub * 8 : 0;
-    }
+    const int r = (t >> 1) & 127, hf = (t & 1) ^ ((r >> 3) & 1);
+    bo[j] = min(col_blk + r, n - 1) * ldb + j * 16 + hf * 8;
   }
-  // fp32 loader (!APRE): row (t + 256 q) / 4, k (t % 4) * 4
+  // fp32 A: row (t + 256 q) / 4, k (t % 4) * 4
   const int kc = (t & 3) * 4;
+  int64_t ao0[2], ao1[2], ao2[2];
   int soff[2];
-  if (!APRE) {
 #pragma unroll
-    for (int q = 0; q < MB; ++q) {
-      const int r = (t + q * kThreads) >> 2;
-      const int64_t gr = min(row_blk + r, m - 1);
-      ao0[q] = (P0.idx ? (int64_t)P0.idx[gr * P0.istride] : gr) * P0.ld + kc;
-      ao1[q] = np > 1 ? (P1.idx ? (int64_t)P1.idx[gr * P1.istride] : gr) * P1.ld + kc : 0;
-      ao2[q] = np > 2 ? (P2.idx ? (int64_t)P2.idx[gr * P2.istride] : gr) * P2.ld + kc : 0;
-      soff[q] = r * 16 + (((kc >> 3) ^ ((r >> 3) & 1)) * 8) + (kc & 7);
-    }
+  for (int q = 0; q < MB; ++q) {
+    const int r = (t + q * kThreads) >> 2;
+    const int64_t gr = min(row_blk + r, m - 1);
+    ao0[q] = (P0.idx ? (int64_t)P0.idx[gr * P0.istride] : gr) * P0.ld + kc;
+    ao1[q] = np > 1 ? (P1.idx ? (int64_t)P1.idx[gr * P1.istride] : gr) * P1.ld + kc : 0;
+    ao2[q] = np > 2 ? (P2.idx ? (int64_t)P2.idx[gr * P2.istride] : gr) * P2.ld + kc : 0;
+    soff[q] = r * 16 + (((kc >> 3) ^ ((r >> 3) & 1)) * 8) + (kc & 7);
   }
   const int rd = rr * 16 + ((h ^ ((rr >> 3) & 1)) * 8);  // this lane's 8 k of its MFMA row
-  u32x4 pa0[3], pb0[3];
+  u32x4 pb0[3];
   float4 ra0[MB];
   f32x16 acc[MB][2];
 #pragma unroll
@@ -901,44 +883,117 @@ __device__ __forceinline__ void x3p_tile(const X3PPart& P0, const X3PPart& P1, c
     __syncthreads();  // buffer cur is free, buffer cur ^ 1 is complete
   }
   const int64_t row0 = row_blk + wm * 32 * MB, col0 = col_blk + wn * 64;
-  if (radd.src) {
-#pragma unroll
-    for (int bi = 0; bi < MB; ++bi)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t row = min(row0 + bi * 32 + (v / 4) * 8 + h * 4 + (v % 4), m - 1);
-        const float* qr = radd.src + (radd.idx ? (int64_t)radd.idx[row * radd.istride] : row) * radd.ld;
-#pragma unroll
-        for (int bj = 0; bj < 2; ++bj) {
-          const int64_t col = min(col0 + bj * 32 + rr, n - 1);
-          acc[bi][bj][v] += qr[col];
-        }
-      }
-  }
-  if (!bias && !accumulate && act == 0 && row0 + 32 * MB <= m && col0 + 64 <= n) {
-    float* base = c + (row0 + h * 4) * ldc + col0 + rr;
-#pragma unroll
-    for (int bi = 0; bi < MB; ++bi)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        float* rp = base + (int64_t)(bi * 32 + (v / 4) * 8 + (v % 4)) * ldc;
-        store_stream(rp, acc[bi][0][v]);
-        store_stream(rp + 32, acc[bi][1][v]);
-      }
-    return;
-  }
-  epilogue<MB, 2>(acc, row0, col0, m, n, bias, c, ldc, accumulate, act);
+  x3_finish<MB>(acc, radd, bias, c, ldc, m, n, accumulate, act, row0, col0, h, rr);
 }
 
-template <bool APRE>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) gemm_x3p_kernel(
     X3PPart P0, X3PPart P1, X3PPart P2, int np, const __bf16* __restrict__ bp, int64_t ldb, X3Part radd,
     const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int accumulate, int act,
     int64_t n_tiles) {
   const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
-  x3p_tile<APRE, 2>(P0, P1, P2, np, bp, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, (tile / n_tiles) * 128,
+  x3p_tile<2>(P0, P1, P2, np, bp, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, (tile / n_tiles) * 128,
                     (tile % n_tiles) * 128);
 }
+
+// The product with both operands as planes, copied straight into LDS by the memory system
+// (global_load_lds_dwordx4: no register stage, no VALU, no LDS bank conflicts), three LDS stages
+// (72 KB, two workgroups per CU): the loads of slice kt + 2 are in flight while slice kt feeds the
+// MFMAs. Wave w's load instruction j fills the slots (3 w + j) * 64 + lane of an operand's region
+// (the slot layout above). The three stages are separate arrays and every slice issues its loads
+// unconditionally (the tail re-loads the last slice into a free stage), so the compiler's wait
+// tracking for LDS-bound loads stays exact; the waits between stages are explicit vmcnt counts
+// (six loads per wave per slice, returned in order). Same planes, same products, same K order:
+// bitwise the C of gemm_x3_kernel. Measured at the 10 000-atom edge GEMM: 6 % faster than staging
+// the planes through registers (waves spend half as long waiting), with three stages at two
+// workgroups per CU.
+constexpr int XD_STAGE = 2 * X3_OP;                      // bf16 elements per stage (A then B region)
+constexpr int kVmcnt6 = 6 | (7 << 4) | (15 << 8);         // s_waitcnt vmcnt(6): the older slice landed
+constexpr int kVmcnt0 = 0 | (7 << 4) | (15 << 8);         // s_waitcnt vmcnt(0)
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void lds_dma16(const __bf16* g, __bf16* l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void_t*)l, 16, 0, 0);
+}
+
+#define XD_ISSUE(K0, STAGE)                                                                         \
+  do {                                                                                              \
+    const int64_t k0_ = (K0);                                                                       \
+    const bool q2_ = k0_ >= ks2, q1_ = !q2_ && k0_ >= ks1;                                          \
+    const __bf16* base_ = q2_ ? ap2 : q1_ ? ap1 : ap0;                                              \
+    const int64_t kin_ = q2_ ? k0_ - ks2 : q1_ ? k0_ - ks1 : k0_;                                   \
+    __bf16* sa_ = (STAGE) + dst0;                                                                   \
+    _Pragma("unroll") for (int j = 0; j < 3; ++j)                                                   \
+      lds_dma16(base_ + (q2_ ? ao2[j] : q1_ ? ao1[j] : ao0[j]) + kin_ * 3, sa_ + j * 512);          \
+    _Pragma("unroll") for (int j = 0; j < 3; ++j)                                                   \
+      lds_dma16(bp + bo[j] + k0_ * 3, sa_ + X3_OP + j * 512);                                       \
+  } while (0)
+
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) gemm_x3p_dma_kernel(
+    X3PPart P0, X3PPart P1, X3PPart P2, int np, const __bf16* __restrict__ bp, int64_t ldb, X3Part radd,
+    const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int accumulate, int act,
+    int64_t n_tiles) {
+  __shared__ __attribute__((aligned(16))) __bf16 st0[XD_STAGE];
+  __shared__ __attribute__((aligned(16))) __bf16 st1[XD_STAGE];
+  __shared__ __attribute__((aligned(16))) __bf16 st2[XD_STAGE];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, rr = lane & 31;
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t row_blk = (tile / n_tiles) * 128, col_blk = (tile % n_tiles) * 128;
+  const int64_t ks1 = P0.width, ks2 = ks1 + (np > 1 ? P1.width : 0);
+  const __bf16 *ap0 = static_cast<const __bf16*>(P0.src), *ap1 = static_cast<const __bf16*>(P1.src),
+               *ap2 = static_cast<const __bf16*>(P2.src);
+  int64_t ao0[3], ao1[3], ao2[3], bo[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int sl = (wave * 3 + j) * 64 + lane, pl = sl >> 8, r = (sl >> 1) & 127;
+    const int sub = pl * 16 + (((sl & 1) ^ ((r >> 3) & 1)) * 8);
+    const int64_t gr = min(row_blk + r, m - 1);
+    ao0[j] = (P0.idx ? (int64_t)P0.idx[gr * P0.istride] : gr) * P0.ld + sub;
+    ao1[j] = np > 1 ? (P1.idx ? (int64_t)P1.idx[gr * P1.istride] : gr) * P1.ld + sub : 0;
+    ao2[j] = np > 2 ? (P2.idx ? (int64_t)P2.idx[gr * P2.istride] : gr) * P2.ld + sub : 0;
+    bo[j] = min(col_blk + r, n - 1) * ldb + sub;
+  }
+  const int dst0 = wave * 3 * 512;  // element offset of this wave's first slot in a region
+  const int rd = rr * 16 + ((h ^ ((rr >> 3) & 1)) * 8);
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int64_t nk = fmd_cdiv(k, 16), last = (nk - 1) * 16;
+  XD_ISSUE(0, st0);
+  XD_ISSUE(min((int64_t)16, last), st1);
+#define XD_BLOCK(NEXT, ISSUE_STAGE, STAGE)                                                          \
+  do {                                                                                              \
+    __builtin_amdgcn_s_waitcnt(kVmcnt6);                                                            \
+    __builtin_amdgcn_s_barrier();                                                                   \
+    XD_ISSUE(min((NEXT) * 16, last), ISSUE_STAGE);                                                  \
+    const __bf16* lds = STAGE;                                                                      \
+    X3_COMPUTE(0, 2);                                                                               \
+  } while (0)
+  // stage 0 holds slice kt, stage 1 slice kt + 1; each block issues slice kt + 2 into the stage
+  // freed by the block before
+  int64_t kt = 0;
+  for (; kt + 3 <= nk; kt += 3) {
+    XD_BLOCK(kt + 2, st2, st0);
+    XD_BLOCK(kt + 3, st0, st1);
+    XD_BLOCK(kt + 4, st1, st2);
+  }
+  if (kt < nk) XD_BLOCK(kt + 2, st2, st0);
+  if (kt + 1 < nk) XD_BLOCK(kt + 3, st0, st1);
+#undef XD_BLOCK
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);  // no load into LDS outlives the workgroup
+  constexpr int MB = 2;
+  const int64_t row0 = row_blk + wm * 64, col0 = col_blk + wn * 64;
+  x3_finish<MB>(acc, radd, bias, c, ldc, m, n, accumulate, act, row0, col0, h, rr);
+}
+
+#undef XD_ISSUE
 
 // Several independent GEMMs with pre-split weights in one launch (the node side of an interaction
 // layer at thousands of atoms): problem g owns the tiles [tile0[g], tile0[g + 1]) of the XCD-aware
@@ -970,7 +1025,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
   const X3PGroupDesc& d = grp.d[g];
   const int64_t t = w - d.tile0;
   const X3Part none{};
-  x3p_tile<false, MB>(d.p0, d.p1, d.p1, d.np, d.b, d.ldb, none, d.bias, d.c, d.ldc, d.m, d.n, d.k, d.accumulate,
+  x3p_tile<MB>(d.p0, d.p1, d.p1, d.np, d.b, d.ldb, none, d.bias, d.c, d.ldc, d.m, d.n, d.k, d.accumulate,
                       grp.act, (t / d.n_tiles) * (64 * MB), (t % d.n_tiles) * 128);
 }
 
@@ -1094,10 +1149,10 @@ int launch_gemm_x3p(int32_t a_planes, int32_t n_parts, const void* const* srcs, 
   if (tiles >= (int64_t(1) << 31)) return FMD_EINVAL;
   const __bf16* b = reinterpret_cast<const __bf16*>(bp);
   if (a_planes)
-    hipLaunchKernelGGL(gemm_x3p_kernel<true>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, P[0], P[1], P[2],
+    hipLaunchKernelGGL(gemm_x3p_dma_kernel, dim3((unsigned)tiles), dim3(kThreads), 0, stream, P[0], P[1], P[2],
                        n_parts, b, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, n_tiles);
   else
-    hipLaunchKernelGGL(gemm_x3p_kernel<false>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, P[0], P[1], P[2],
+    hipLaunchKernelGGL(gemm_x3p_kernel, dim3((unsigned)tiles), dim3(kThreads), 0, stream, P[0], P[1], P[2],
                        n_parts, b, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, n_tiles);
   FMD_CHECK_LAUNCH();
   return FMD_OK;

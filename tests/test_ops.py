@@ -449,6 +449,31 @@ def test_gemm_planes_bitwise_equal_to_in_kernel_split(device):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("C,nb,N,E", [(48, 8, 200, 3001), (64, 8, 256, 5000), (256, 8, 384, 4099)])
+def test_gemm_planes_gathered_k_tails(device, C, nb, N, E):
+    """The gathered pre-split GEMM over K = C + nb of 56, 72 and 264 (4, 5 and 17 slices of 16: the
+    three-stage pipeline's loop and both tail lengths), ragged M and N: bitwise the in-kernel split
+    and within fp32 of float64."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm_gather, gemm_planes, split_planes
+
+    g = torch.Generator().manual_seed(C + N)
+    n_atoms = 777
+    h0 = torch.randn(n_atoms, C, generator=g)
+    ef = torch.randn(E, nb, generator=g)
+    src = torch.randint(0, n_atoms, (E,), generator=g, dtype=torch.int32)
+    w = torch.randn(N, C + nb, generator=g) / (C + nb) ** 0.5
+    d = lambda t: t.to(device)  # noqa: E731
+    got = gemm_planes([(split_planes(d(h0)), d(src)), (split_planes(d(ef)), None)], split_planes(d(w)),
+                      a_planes=True)
+    ref = gemm_gather([(d(h0), d(src)), (d(ef), None)], d(w))
+    assert torch.equal(got, ref)
+    exact = torch.cat([h0[src.long()], ef], 1).double() @ w.double().t()
+    assert oops.relative(got.cpu().numpy(), exact.numpy()) < 1e-5
+
+
+@pytest.mark.gpu
 def test_gemm_split_planes_dynamic_range(device):
     """The three-plane bf16 path must keep fp32 accuracy over a wide exponent range: rows and
     columns scaled by 2^-30 .. 2^30, exact zeros, and values whose low bits the first two planes
