@@ -194,8 +194,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restr
 // Several independent GEMMs of one b layout in one launch (the node side of an interaction
 // layer: fewer, fuller launches). Workgroup w takes problem g with tile0[g] <= w < tile0[g + 1],
 // tile (w - tile0[g]) in row-major order of its 64 x 64 tiles. Each problem's result is the one
-// fmd_gemm_f32's 64 x 64 kernel gives (same K order), with [a | a2] when a2 is set. Large groups
-// of B [N, K] problems run as gemm_x3_group_kernel instead.
+// fmd_gemm_f32's 64 x 64 kernel gives (same K order), with [a | a2] when a2 is set.
 constexpr int kMaxGroup = 4;
 struct GemmDesc {
   const float* a;
@@ -643,11 +642,10 @@ __device__ __forceinline__ void x3_finish(f32x16 (&acc)[MB][2], const X3Part& ra
 
 // One (64 MB) x 128 tile of C at (row_blk, col_blk): A as up to three gathered column parts (K
 // order P0 | P1 | P2), B [N, K] K-contiguous, both split into their planes as they are staged.
-// Each wave computes (32 MB) x 64 of it (MB blocks of 32 x 32 by two); MB = 1 halves the rows per
-// workgroup for launches with too few 128-row tiles to keep three workgroups on every CU (every
-// product keeps its K order: the same C either way).
-// ST: register stages of the global loads (1 or 2 slices in flight beyond the one being stored).
-template <int MB, int ST>
+// Each wave computes (32 MB) x 64 of it (MB blocks of 32 x 32 by two). The staging macros and
+// X3_COMPUTE take MB; x3p_tile uses MB = 1 for launches with too few 128-row tiles to keep three
+// workgroups on every CU (every product keeps its K order: the same C either way).
+template <int MB>
 __device__ __forceinline__ void x3_tile(const X3Part& P0, const X3Part& P1, const X3Part& P2, int np,
                                         const float* __restrict__ b, int64_t ldb, const X3Part& radd,
                                         const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n,
@@ -676,7 +674,7 @@ __device__ __forceinline__ void x3_tile(const X3Part& P0, const X3Part& P1, cons
     soff[q] = r * 16 + (((kc >> 3) ^ ((r >> 3) & 1)) * 8) + (kc & 7);
   }
   const int rd = rr * 16 + ((h ^ ((rr >> 3) & 1)) * 8);  // this lane's 8 k of its MFMA row
-  float4 ra0[MB], rb0[2], ra1[MB], rb1[2];  // register stages (the second with ST = 2)
+  float4 ra0[MB], rb0[2];
   f32x16 acc[MB][2];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
@@ -689,36 +687,15 @@ __device__ __forceinline__ void x3_tile(const X3Part& P0, const X3Part& P1, cons
   X3_LOAD(0, 0);
   X3_STORE(0, 0);
   if (nk > 1) X3_LOAD(16, 0);
-  if (ST == 2 && nk > 2) X3_LOAD(32, 1);
   __syncthreads();
-  if constexpr (ST == 1) {
-    for (int64_t kt = 0; kt < nk; ++kt) {
-      const int cur = (int)(kt & 1);
-      if (kt + 1 < nk) {
-        X3_STORE(cur ^ 1, 0);                       // slice kt + 1 (loaded one iteration ago)
-        if (kt + 2 < nk) X3_LOAD((kt + 2) * 16, 0);  // slice kt + 2 stays in flight over these MFMAs
-      }
-      X3_COMPUTE(cur, MB);
-      __syncthreads();  // buffer cur is free, buffer cur ^ 1 is complete
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int cur = (int)(kt & 1);
+    if (kt + 1 < nk) {
+      X3_STORE(cur ^ 1, 0);                       // slice kt + 1 (loaded one iteration ago)
+      if (kt + 2 < nk) X3_LOAD((kt + 2) * 16, 0);  // slice kt + 2 stays in flight over these MFMAs
     }
-  } else {
-    // two register stages (odd slices in stage 0, even ones from 2 on in stage 1): a slice's loads
-    // are issued two iterations before it is stored, for tiles with little MFMA work per slice
-    for (int64_t kt = 0; kt < nk; kt += 2) {
-      if (kt + 1 < nk) {
-        X3_STORE(1, 0);                              // slice kt + 1
-        if (kt + 3 < nk) X3_LOAD((kt + 3) * 16, 0);
-      }
-      X3_COMPUTE(0, MB);
-      __syncthreads();
-      if (kt + 1 >= nk) break;
-      if (kt + 2 < nk) {
-        X3_STORE(0, 1);                              // slice kt + 2
-        if (kt + 4 < nk) X3_LOAD((kt + 4) * 16, 1);
-      }
-      X3_COMPUTE(1, MB);
-      __syncthreads();
-    }
+    X3_COMPUTE(cur, MB);
+    __syncthreads();  // buffer cur is free, buffer cur ^ 1 is complete
   }
   const int64_t row0 = row_blk + wm * 32 * MB, col0 = col_blk + wn * 64;
   x3_finish<MB>(acc, radd, bias, c, ldc, m, n, accumulate, act, row0, col0, h, rr);
@@ -730,41 +707,8 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
                                                            int64_t m, int64_t n, int64_t k, int accumulate, int act,
                                                            int64_t n_tiles) {
   const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
-  x3_tile<2, 1>(P0, P1, P2, np, b, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, (tile / n_tiles) * 128,
+  x3_tile<2>(P0, P1, P2, np, b, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, (tile / n_tiles) * 128,
              (tile % n_tiles) * 128);
-}
-
-// Several independent split-plane GEMMs in one launch (the node side of an interaction layer at
-// thousands of atoms): problem g owns the tiles [tile0[g], tile0[g + 1]) of the XCD-aware order,
-// (64 MB) x 128 each, A = [a | a2] (a's width a multiple of 16). Each problem's C is bitwise the
-// one gemm_x3_kernel gives for it (same planes, same K order).
-struct X3GroupDesc {
-  X3Part p0, p1;
-  int np;
-  const float* b;
-  const float* bias;
-  float* c;
-  int64_t ldb, ldc, m, n, k, n_tiles, tile0;
-  int accumulate;
-};
-struct X3Group {
-  X3GroupDesc d[kMaxGroup];
-  int count;
-  int act;
-};
-
-template <int MB>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) gemm_x3_group_kernel(const X3Group grp) {
-  const int64_t w = xcd_tile(blockIdx.x, gridDim.x);
-  int g = 0;
-#pragma unroll
-  for (int q = 1; q < kMaxGroup; ++q)
-    if (q < grp.count && w >= grp.d[q].tile0) g = q;
-  const X3GroupDesc& d = grp.d[g];
-  const int64_t t = w - d.tile0;
-  const X3Part none{};
-  x3_tile<MB, MB == 1 ? 2 : 1>(d.p0, d.p1, d.p1, d.np, d.b, d.ldb, none, d.bias, d.c, d.ldc, d.m, d.n, d.k, d.accumulate, grp.act,
-              (t / d.n_tiles) * (64 * MB), (t % d.n_tiles) * 128);
 }
 
 // ------------------------------------------------- fp32 as three bf16 planes, pre-split operands
@@ -1099,10 +1043,8 @@ int launch_gemm_x3(int32_t n_parts, const float* const* srcs, const int32_t* con
   return FMD_OK;
 }
 
-// A grouped launch runs as split-plane GEMMs from this many 128 x 128 tiles in all (the node side
-// of a layer at ~5 000 atoms and above); below, the 64 x 64 fp32 kernel's four times more
-// workgroups win.
-constexpr int64_t kGroupX3MinTiles = 128;
+// Grouped split-plane launches use 64-row tiles below this many tiles of 128 x 128 (three
+// workgroups per CU).
 constexpr int64_t kGroupX3HalfTilesBelow = 3 * 256;
 
 // Tile choice: 128 x 128 when that still gives two workgroups per CU (256 CUs), else 64 x 64
@@ -1232,12 +1174,6 @@ int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda,
   GemmGroup grp{};
   grp.act = epilogue_kind;
   int64_t tiles = 0;
-  // the split-plane form, when every problem allows it: B [N, K], 16-byte aligned rows, K split at a
-  // multiple of 16
-  X3Group xg{};
-  xg.act = epilogue_kind;
-  bool x3_ok = b_layout == 0;
-  int64_t big = 0;
   for (int g = 0; g < count; ++g) {
     GemmDesc& d = grp.d[grp.count];
     FMD_REQUIRE(m[g] >= 0 && n[g] >= 0 && k[g] >= 0);
@@ -1266,44 +1202,9 @@ int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda,
     d.tile0 = tiles;
     tiles += fmd_cdiv(m[g], 64) * d.tiles_n;
     ++grp.count;
-    x3_ok = x3_ok && k[g] > 0 && k[g] < (int64_t(1) << 30) && k[g] % 4 == 0 && aligned16(a[g]) && lda[g] % 4 == 0 &&
-            aligned16(b[g]) && ldb[g] % 4 == 0 && (!split || (ks % 16 == 0 && aligned16(a2[g]) && lda2[g] % 4 == 0));
-    if (x3_ok) {
-      X3GroupDesc& x = xg.d[xg.count++];
-      x.p0 = X3Part{a[g], nullptr, lda[g], 1, (int32_t)ks};
-      x.p1 = split ? X3Part{a2[g], nullptr, lda2[g], 1, (int32_t)(k[g] - ks)} : X3Part{};
-      x.np = split ? 2 : 1;
-      x.b = b[g];
-      x.bias = d.bias;
-      x.c = c[g];
-      x.ldb = ldb[g];
-      x.ldc = ldc[g];
-      x.m = m[g];
-      x.n = n[g];
-      x.k = k[g];
-      x.n_tiles = fmd_cdiv(n[g], 128);
-      x.accumulate = d.accumulate;
-      big += fmd_cdiv(m[g], 128) * x.n_tiles;
-    }
   }
   if (grp.count == 0) return FMD_OK;
   FMD_REQUIRE(tiles < (int64_t(1) << 31));
-  if (x3_ok && big >= kGroupX3MinTiles) {
-    // 64-row tiles while 128-row ones would not give three workgroups per CU
-    const int mb = big < kGroupX3HalfTilesBelow ? 1 : 2;
-    int64_t t0 = 0;
-    for (int g = 0; g < xg.count; ++g) {
-      xg.d[g].tile0 = t0;
-      t0 += fmd_cdiv(xg.d[g].m, 64 * mb) * xg.d[g].n_tiles;
-    }
-    FMD_REQUIRE(t0 < (int64_t(1) << 31));
-    if (mb == 1)
-      hipLaunchKernelGGL(gemm_x3_group_kernel<1>, dim3((unsigned)t0), dim3(kThreads), 0, stream, xg);
-    else
-      hipLaunchKernelGGL(gemm_x3_group_kernel<2>, dim3((unsigned)t0), dim3(kThreads), 0, stream, xg);
-    FMD_CHECK_LAUNCH();
-    return FMD_OK;
-  }
   if (b_layout == 0)
     hipLaunchKernelGGL(gemm_f32_group_kernel<0>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
   else

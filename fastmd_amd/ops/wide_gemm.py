@@ -57,8 +57,8 @@ def gemm(a: Tensor, b: Tensor, *, b_layout: int, bias: Tensor | None = None, out
     return out
 
 
-# 128 x 128 tiles from which a grouped launch takes the split-plane form (the C library's own
-# threshold for fmd_gemm_group_f32)
+# 128 x 128 tiles from which a group with pre-split weights takes the split-plane form (below,
+# the fp32 kernel's 64 x 64 tiles give four times more workgroups)
 GROUP_X3_MIN_TILES = 128
 
 

@@ -305,10 +305,8 @@ int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32
 /* Up to four independent fmd_gemm_f32 problems of one b_layout in one launch (arrays of length
  * count, problem g: C_g = [A_g | A2_g] op(B_g) (+ bias_g) (+ C_g if accumulate_g)). A2_g (may be
  * null, or the a2 array itself null) supplies K columns [ksplit_g, K_g) with row stride lda2_g;
- * ksplit_g % 32 == 0. Small groups run the 64 x 64 fp32 MFMA tiles of fmd_gemm_f32 (same K
- * order); from 128 tiles of 128 x 128 in all, a group with b_layout 0, K % 4 == 0 and 16-byte
- * aligned rows runs as fp32-accurate split-plane GEMMs (three bf16 planes per operand, the
- * product of fmd_gemm_f32's split-plane tiles). Replaces several linear / matmul calls on independent operands
+ * ksplit_g % 32 == 0. Every problem runs the 64 x 64 fp32 MFMA tiles of fmd_gemm_f32 (same K
+ * order); large groups with pre-split weights go to fmd_gemm_group_x3_planes_f32. Replaces several linear / matmul calls on independent operands
  * (triton_wide_gemm.py:482-553) with one launch: the node side of an interaction layer, whose
  * per-layer GEMMs are each too small to fill the chip. bias and accumulate may be null. */
 int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda, const float* const* a2,

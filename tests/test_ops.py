@@ -258,14 +258,15 @@ def test_gemm_group_matches_single_gemms_and_fp64(device, b_layout):
 
 @pytest.mark.gpu
 def test_gemm_group_split_plane_form(device):
-    """A large fmd_gemm_group_f32 group with B [N, K] (the node side of a layer at 10 000 atoms:
-    >= 128 tiles of 128 x 128) runs as split-plane GEMMs: each problem within fp32 of float64 and
-    bitwise equal to fmd_gemm_f32's split-plane kernel on the same problem (M large enough that it
-    takes that kernel; a K split at 128 gives the concatenated operand's bits), in the 64-row and
-    the 128-row tile forms, with the weights split in the kernel or given as planes."""
+    """A large fmd_gemm_group_f32 group with B [N, K] and the weights' planes (the node side of a
+    layer at 10 000 atoms: >= 128 tiles of 128 x 128) runs as split-plane GEMMs
+    (fmd_gemm_group_x3_planes_f32): each problem within fp32 of float64 and bitwise equal to
+    fmd_gemm_f32's split-plane kernel on the same problem (M large enough that it takes that
+    kernel; a K split at 128 gives the concatenated operand's bits), in the 64-row and the 128-row
+    tile forms. Without planes the group keeps the fp32 tiles."""
     import torch
 
-    from fastmd_amd.ops.wide_gemm import gemm, gemm_group
+    from fastmd_amd.ops.wide_gemm import gemm, gemm_group, split_planes
 
     g = torch.Generator().manual_seed(12)
     C = 128
@@ -277,8 +278,9 @@ def test_gemm_group_split_plane_form(device):
     d = lambda t: t.to(device)  # noqa: E731
     out0 = torch.empty(33000, C, device=device)
     out1 = d(c1)
-    gemm_group([{"a": d(a0), "b": d(w0), "out": out0},
-                {"a": d(a0), "a2": d(a1), "b": d(w1), "out": out1, "accumulate": True, "bias": d(bias)}], b_layout=0)
+    gemm_group([{"a": d(a0), "b": d(w0), "b_planes": split_planes(d(w0)), "out": out0},
+                {"a": d(a0), "a2": d(a1), "b": d(w1), "b_planes": split_planes(d(w1)), "out": out1,
+                 "accumulate": True, "bias": d(bias)}], b_layout=0)
     ref0 = a0.double() @ w0.double().t()
     ref1 = torch.cat([a0, a1], 1).double() @ w1.double().t() + c1.double() + bias.double()
     assert oops.relative(out0.cpu().numpy(), ref0.numpy()) < 1e-5
@@ -287,29 +289,18 @@ def test_gemm_group_split_plane_form(device):
     single = d(c1)
     gemm(d(torch.cat([a0, a1], 1)), d(w1), b_layout=0, out=single, accumulate=True, bias=d(bias))
     assert torch.equal(out1, single)
-    # with the weights' planes given (split once, fmd_gemm_group_x3_planes_f32): the same bits
-    from fastmd_amd.ops.wide_gemm import split_planes
-
-    out0p, out1p = torch.empty(33000, C, device=device), d(c1)
-    gemm_group([{"a": d(a0), "b": d(w0), "b_planes": split_planes(d(w0)), "out": out0p},
-                {"a": d(a0), "a2": d(a1), "b": d(w1), "b_planes": split_planes(d(w1)), "out": out1p,
-                 "accumulate": True, "bias": d(bias)}], b_layout=0)
-    assert torch.equal(out0p, out0) and torch.equal(out1p, out1)
     # 128-row tiles once a group has three per CU (782 here): the same bits as the 64-row form
     a2 = torch.randn(100000, C, generator=g)
     out2 = torch.empty(100000, C, device=device)
-    gemm_group([{"a": d(a2), "b": d(w0), "out": out2}], b_layout=0)
+    gemm_group([{"a": d(a2), "b": d(w0), "b_planes": split_planes(d(w0)), "out": out2}], b_layout=0)
     assert torch.equal(out2, gemm(d(a2), d(w0), b_layout=0))
     assert torch.equal(out2[:33000], gemm(d(a2[:33000]), d(w0), b_layout=0))
     assert oops.relative(out2.cpu().numpy(), (a2.double() @ w0.double().t()).numpy()) < 1e-5
-    out2p = torch.empty(100000, C, device=device)
-    gemm_group([{"a": d(a2), "b": d(w0), "b_planes": split_planes(d(w0)), "out": out2p}], b_layout=0)
-    assert torch.equal(out2p, out2)
-    # the fp32 form of the same group (B [K, N]) agrees to fp32 rounding
+    # without planes: the fp32 tiles (within fp32 rounding of the same product, not its bits)
     out0f = torch.empty(33000, C, device=device)
-    gemm_group([{"a": d(a0), "b": d(w0.t().contiguous()), "out": out0f}], b_layout=1)
+    gemm_group([{"a": d(a0), "b": d(w0), "out": out0f}], b_layout=0)
     assert oops.relative(out0f.cpu().numpy(), ref0.numpy()) < 1e-5
-    assert not torch.equal(out0f, out0)  # a different product: the form switch is real
+    assert not torch.equal(out0f, out0)
 
 
 @pytest.mark.gpu
