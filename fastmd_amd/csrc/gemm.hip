@@ -553,12 +553,12 @@ constexpr int X3_PL = 128 * 16, X3_OP = 3 * X3_PL, X3_BUF = 2 * X3_OP;
     const float* base_ = q2_ ? src2 : q1_ ? src1 : src0;                                            \
     const int64_t kin_ = q2_ ? k0_ - ks2 : q1_ ? k0_ - ks1 : k0_;                                   \
     const int w_ = q2_ ? w2 : q1_ ? w1 : w0;                                                        \
-    _Pragma("unroll") for (int q = 0; q < MB; ++q) {                                                \
+    _Pragma("unroll") for (int q = 0; q < AQ; ++q) {                                                \
       const int64_t o_ = q2_ ? ao2[q] : q1_ ? ao1[q] : ao0[q];                                      \
       ra##S[q] = (kin_ + kc < w_) ? *reinterpret_cast<const float4*>(base_ + o_ + kin_)                \
                                : make_float4(0.f, 0.f, 0.f, 0.f);                                   \
     }                                                                                               \
-    _Pragma("unroll") for (int q = 0; q < 2; ++q)                                                   \
+    _Pragma("unroll") for (int q = 0; q < BQ; ++q)                                                   \
       rb##S[q] = (k0_ + kc < k) ? *reinterpret_cast<const float4*>(b + bo[q] + k0_)                    \
                              : make_float4(0.f, 0.f, 0.f, 0.f);                                     \
   } while (0)
@@ -566,14 +566,14 @@ constexpr int X3_PL = 128 * 16, X3_OP = 3 * X3_PL, X3_BUF = 2 * X3_OP;
 #define X3_STORE(BUFI, S)                                                                           \
   do {                                                                                              \
     __bf16* sb_ = lds + (BUFI) * X3_BUF;                                                            \
-    _Pragma("unroll") for (int q = 0; q < MB; ++q) {                                                \
+    _Pragma("unroll") for (int q = 0; q < AQ; ++q) {                                                \
       bf16x4 x0_, x1_, x2_;                                                                         \
       split3(ra##S[q], x0_, x1_, x2_);                                                                 \
       *reinterpret_cast<bf16x4*>(sb_ + 0 * X3_PL + soff[q]) = x0_;                                  \
       *reinterpret_cast<bf16x4*>(sb_ + 1 * X3_PL + soff[q]) = x1_;                                  \
       *reinterpret_cast<bf16x4*>(sb_ + 2 * X3_PL + soff[q]) = x2_;                                  \
     }                                                                                               \
-    _Pragma("unroll") for (int q = 0; q < 2; ++q) {                                                 \
+    _Pragma("unroll") for (int q = 0; q < BQ; ++q) {                                                 \
       bf16x4 x0_, x1_, x2_;                                                                         \
       split3(rb##S[q], x0_, x1_, x2_);                                                                 \
       *reinterpret_cast<bf16x4*>(sb_ + X3_OP + 0 * X3_PL + soff[q]) = x0_;                          \
@@ -640,20 +640,21 @@ __device__ __forceinline__ void x3_finish(f32x16 (&acc)[MB][2], const X3Part& ra
   epilogue<MB, 2>(acc, row0, col0, m, n, bias, c, ldc, accumulate, act);
 }
 
-// One (64 MB) x 128 tile of C at (row_blk, col_blk): A as up to three gathered column parts (K
-// order P0 | P1 | P2), B [N, K] K-contiguous, both split into their planes as they are staged.
-// Each wave computes (32 MB) x 64 of it (MB blocks of 32 x 32 by two). The staging macros and
-// X3_COMPUTE take MB; x3p_tile uses MB = 1 for launches with too few 128-row tiles to keep three
-// workgroups on every CU (every product keeps its K order: the same C either way).
-template <int MB>
+// One 128 x BN tile of C at (row_blk, col_blk): A as up to three gathered column parts (K order
+// P0 | P1 | P2), B [N, K] K-contiguous, both split into their planes as they are staged. BN = 128:
+// waves 2 x 2, each 64 x 64 (MB = 2 blocks of 32 rows); BN = 64 (N <= 64, where a 128-wide tile
+// would leave half its MFMAs idle): waves 4 x 1, each 32 x 64 (MB = 1). AQ / BQ: the loader's
+// passes over A's 128 and B's BN rows. Every product keeps its K order: the same C either way.
+template <int BN>
 __device__ __forceinline__ void x3_tile(const X3Part& P0, const X3Part& P1, const X3Part& P2, int np,
                                         const float* __restrict__ b, int64_t ldb, const X3Part& radd,
                                         const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n,
                                         int64_t k, int accumulate, int act, int64_t row_blk, int64_t col_blk) {
+  constexpr int MB = BN / 64, AQ = 2, BQ = BN / 64;
   __shared__ __attribute__((aligned(16))) __bf16 lds[2 * X3_BUF];
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, rr = lane & 31;
+  const int wm = BN == 128 ? wave >> 1 : wave, wn = BN == 128 ? wave & 1 : 0, h = lane >> 5, rr = lane & 31;
   const int64_t ks1 = P0.width, ks2 = ks1 + (np > 1 ? P1.width : 0);
   const float *src0 = P0.src, *src1 = P1.src, *src2 = P2.src;
   const int w0 = P0.width, w1 = P1.width, w2 = P2.width;
@@ -665,16 +666,14 @@ __device__ __forceinline__ void x3_tile(const X3Part& P0, const X3Part& P1, cons
   for (int q = 0; q < 2; ++q) {
     const int r = (t + q * kThreads) >> 2;
     const int64_t gr = min(row_blk + r, m - 1);
-    if (q < MB) {
-      ao0[q] = (P0.idx ? (int64_t)P0.idx[gr * P0.istride] : gr) * P0.ld + kc;
-      ao1[q] = np > 1 ? (P1.idx ? (int64_t)P1.idx[gr * P1.istride] : gr) * P1.ld + kc : 0;
-      ao2[q] = np > 2 ? (P2.idx ? (int64_t)P2.idx[gr * P2.istride] : gr) * P2.ld + kc : 0;
-    }
+    ao0[q] = (P0.idx ? (int64_t)P0.idx[gr * P0.istride] : gr) * P0.ld + kc;
+    ao1[q] = np > 1 ? (P1.idx ? (int64_t)P1.idx[gr * P1.istride] : gr) * P1.ld + kc : 0;
+    ao2[q] = np > 2 ? (P2.idx ? (int64_t)P2.idx[gr * P2.istride] : gr) * P2.ld + kc : 0;
     bo[q] = min(col_blk + r, n - 1) * ldb + kc;
     soff[q] = r * 16 + (((kc >> 3) ^ ((r >> 3) & 1)) * 8) + (kc & 7);
   }
   const int rd = rr * 16 + ((h ^ ((rr >> 3) & 1)) * 8);  // this lane's 8 k of its MFMA row
-  float4 ra0[MB], rb0[2];
+  float4 ra0[AQ], rb0[BQ];
   f32x16 acc[MB][2];
 #pragma unroll
   for (int i = 0; i < MB; ++i)
@@ -701,14 +700,15 @@ __device__ __forceinline__ void x3_tile(const X3Part& P0, const X3Part& P1, cons
   x3_finish<MB>(acc, radd, bias, c, ldc, m, n, accumulate, act, row0, col0, h, rr);
 }
 
+template <int BN>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) gemm_x3_kernel(X3Part P0, X3Part P1, X3Part P2, int np,
                                                            const float* __restrict__ b, int64_t ldb, X3Part radd,
                                                            const float* __restrict__ bias, float* c, int64_t ldc,
                                                            int64_t m, int64_t n, int64_t k, int accumulate, int act,
                                                            int64_t n_tiles) {
   const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
-  x3_tile<2>(P0, P1, P2, np, b, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, (tile / n_tiles) * 128,
-             (tile % n_tiles) * 128);
+  x3_tile<BN>(P0, P1, P2, np, b, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, (tile / n_tiles) * 128,
+              (tile % n_tiles) * BN);
 }
 
 // ------------------------------------------------- fp32 as three bf16 planes, pre-split operands
@@ -1035,10 +1035,16 @@ int launch_gemm_x3(int32_t n_parts, const float* const* srcs, const int32_t* con
   if (!b || !aligned16(b) || ldb % 4 || ldb < k) return FMD_EUNSUPPORTED;
   X3Part radd{row_add, row_add_index, ld_row_add, row_add_index_stride, 0};
   if (row_add && (ld_row_add < n || row_add_index_stride < 1)) return FMD_EINVAL;
-  const int64_t n_tiles = fmd_cdiv(n, 128), tiles = fmd_cdiv(m, 128) * n_tiles;
+  // 128 x 64 tiles for N <= 64 (the three-body model's edge rows): no idle half tile
+  const int64_t bn = n <= 64 ? 64 : 128;
+  const int64_t n_tiles = fmd_cdiv(n, bn), tiles = fmd_cdiv(m, 128) * n_tiles;
   if (tiles >= (int64_t(1) << 31)) return FMD_EINVAL;
-  hipLaunchKernelGGL(gemm_x3_kernel, dim3((unsigned)tiles), dim3(kThreads), 0, stream, P[0], P[1], P[2], n_parts, b, ldb,
-                     radd, bias, c, ldc, m, n, k, accumulate, act, n_tiles);
+  if (bn == 64)
+    hipLaunchKernelGGL(gemm_x3_kernel<64>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, P[0], P[1], P[2], n_parts,
+                       b, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, n_tiles);
+  else
+    hipLaunchKernelGGL(gemm_x3_kernel<128>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, P[0], P[1], P[2], n_parts,
+                       b, ldb, radd, bias, c, ldc, m, n, k, accumulate, act, n_tiles);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -465,6 +465,37 @@ def test_gemm_planes_gathered_k_tails(device, C, nb, N, E):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("N", [64, 40])
+def test_gemm_gather_narrow_tile(device, N):
+    """N <= 64 takes 128 x 64 split-plane tiles (the three-body model's edge rows): bitwise the
+    columns of the same product on 128-wide tiles (the weight padded with more rows), and within
+    fp32 of float64; with a gathered row add and accumulate."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm_gather
+
+    g = torch.Generator().manual_seed(N)
+    n_atoms, E, C = 500, 7001, 64
+    h = torch.randn(n_atoms, C, generator=g)
+    eps = torch.randn(E, C, generator=g)
+    src = torch.randint(0, n_atoms, (E,), generator=g, dtype=torch.int32)
+    w = torch.randn(N, 2 * C, generator=g) / (2 * C) ** 0.5
+    wide = torch.cat([w, torch.randn(128 - N, 2 * C, generator=g)], 0)
+    d = lambda t: t.to(device)  # noqa: E731
+    got = gemm_gather([(d(h), d(src)), (d(eps), None)], d(w))
+    ref = gemm_gather([(d(h), d(src)), (d(eps), None)], d(wide))[:, :N]
+    assert torch.equal(got, ref)
+    exact = torch.cat([h[src.long()], eps], 1).double() @ w.double().t()
+    assert oops.relative(got.cpu().numpy(), exact.numpy()) < 1e-5
+    q = torch.randn(n_atoms, N, generator=g)
+    qi = torch.randint(0, n_atoms, (E,), generator=g, dtype=torch.int32)
+    c0 = torch.randn(E, N, generator=g)
+    got2 = gemm_gather([(d(h), d(src)), (d(eps), None)], d(w), out=d(c0), accumulate=True, row_add=(d(q), d(qi)))
+    exact2 = exact + c0.double() + q.double()[qi.long()]
+    assert oops.relative(got2.cpu().numpy(), exact2.numpy()) < 1e-5
+
+
+@pytest.mark.gpu
 def test_gemm_split_planes_dynamic_range(device):
     """The three-plane bf16 path must keep fp32 accuracy over a wide exponent range: rows and
     columns scaled by 2^-30 .. 2^30, exact zeros, and values whose low bits the first two planes
