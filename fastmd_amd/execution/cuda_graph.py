@@ -27,7 +27,9 @@ from fastmd_amd import _abi
 from fastmd_amd.adapters.protocol import GraphBatch, PaddingRule
 from fastmd_amd.engine.capacity_policy import held_demand, tier
 from fastmd_amd.engine.energy_derivative import engine_derivative
+from fastmd_amd.execution.graph_capture import capture_graph
 from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder, self_loop_padding
+from fastmd_amd._roctx import roctx_ranged
 
 _FAR_SELF_LOOPS = PaddingRule("far_self_loops")
 
@@ -181,7 +183,7 @@ class BucketedGraphRunner:
         torch.cuda.current_stream(self.device).wait_stream(side)
         torch.cuda.synchronize(self.device)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, pool=self.pool, capture_error_mode="thread_local"):
+        with capture_graph(graph, pool=self.pool, name="model_graph_capture"):
             out = self._derivative(ws.batch, inputs, task=self.task, n_real=n)
         entry = {"graph": graph, "workspace": ws, "inputs": inputs, "out": out, "n_real": n}
         self.cache[key] = entry
@@ -198,6 +200,7 @@ class BucketedGraphRunner:
         t = triplet_demand(g, self.triplet_cutoff) if self.triplet_cutoff is not None else 0
         return int(g.n_real), _demand_u(g), t
 
+    @roctx_ranged("model_graph_run")
     def run(self, g: GraphBatch, positions: Tensor | None = None):
         """(out, n_real) of the model on the ragged build ``g``; ``out`` is valid until the next run.
         ``positions``: the coordinates ``g`` was built from, for a line-graph model's own build

@@ -22,6 +22,7 @@ from torch import Tensor
 
 from fastmd_amd import _abi, units
 from fastmd_amd.execution.gpu_integrator import StatefulIntegrator, _PinnedUpload
+from fastmd_amd._roctx import roctx_ranged
 
 FOURTH_ORDER_COEFFS = [
     1 / (2 - 2 ** (1 / 3)),
@@ -270,6 +271,7 @@ class GPUNoseHooverChainNVT(StatefulIntegrator):
                                       else self._as_f64(energy).reshape(1))
 
     # -------------------------------------------------------------- step halves
+    @roctx_ranged("gpu_integrator")
     def step_pre_force(self, state: NHCState | None = None) -> Tensor:
         """NHC(dt/2); p += dt/2 * F(q_n); q += dt * p / m. Returns the float64 positions view."""
         st = self.state if state is None else state
@@ -279,6 +281,7 @@ class GPUNoseHooverChainNVT(StatefulIntegrator):
                   _abi.stream_handle(self.device))
         return st.positions
 
+    @roctx_ranged("gpu_integrator")
     def step_post_force(self, forces: Tensor, energy: Tensor | None = None, state: NHCState | None = None) -> None:
         """p += dt/2 * F(q_{n+1}); NHC(dt/2); cache F (float64) and the energy."""
         st = self.state if state is None else state

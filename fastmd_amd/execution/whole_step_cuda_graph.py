@@ -30,8 +30,10 @@ import torch
 from torch import Tensor
 
 from fastmd_amd.engine.energy_derivative import engine_derivative
+from fastmd_amd.execution.graph_capture import capture_graph
 from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
 from fastmd_amd.graph.gpu_graph_builder import raise_if_isolated_atoms
+from fastmd_amd._roctx import roctx_ranged
 
 
 def _capacity_exceeded(builder, status) -> bool:
@@ -196,7 +198,7 @@ class WholeStepGraphRunner:
             torch.cuda.current_stream(self.device).wait_stream(side)
             torch.cuda.synchronize(self.device)
             self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph, pool=self.graph_pool, capture_error_mode="thread_local"):
+            with capture_graph(self.graph, pool=self.graph_pool, name="whole_step_capture"):
                 self._window_body()
         except BaseException:
             torch.cuda.current_stream(self.device).wait_stream(side)
@@ -206,6 +208,7 @@ class WholeStepGraphRunner:
         torch.cuda.synchronize(self.device)
 
     # ------------------------------------------------------------------ replay
+    @roctx_ranged("whole_step_launch")
     def launch(self, *, behind: bool = False) -> int:
         """Replay one window without settling it and start the asynchronous copy of its statistics
         into a host slot (no host synchronization); returns the slot for :meth:`launched_stats`.

@@ -24,6 +24,7 @@ from torch import Tensor
 
 from fastmd_amd import _abi
 from fastmd_amd._device import require_cuda
+from fastmd_amd._roctx import roctx_ranged
 from fastmd_amd.adapters.protocol import GraphBatch, PaddingRule
 from fastmd_amd.graph.neighbor_list_backend import (NeighborOverflowError, cell_list_shape,
                                                     estimate_max_neighbors)
@@ -244,6 +245,7 @@ class FixedCapacityGraphBuilder:
         return _abi.stream_handle(self.device)
 
     @torch.no_grad()
+    @roctx_ranged("fixed_capacity_refresh_candidates")
     def refresh_candidates(self, positions: Tensor) -> None:
         """Refresh the cell-list candidates from ``positions`` (eager, rare path): the reference
         positions and wraps are reset and the wrap delta zeroed (fixed_capacity_builder.py:1674-1685)."""
@@ -279,6 +281,7 @@ class FixedCapacityGraphBuilder:
 
     # ------------------------------------------------------------------ build
     @torch.no_grad()
+    @roctx_ranged("fixed_capacity_graph_build")
     def build(self, positions: Tensor, *, rebuild_candidates: bool = True, predicate=None):
         """Build into the persistent buffers; returns ``(prepare(batch), status)``
         (fixed_capacity_builder.py:2180-2298). ``positions`` float32 or float64 [N, 3]."""

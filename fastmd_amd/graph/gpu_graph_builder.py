@@ -16,6 +16,7 @@ from torch import Tensor
 from fastmd_amd import _abi
 from fastmd_amd.adapters.protocol import GraphBatch
 from fastmd_amd.graph.neighbor_list_backend import cell_list_shape, estimate_max_neighbors
+from fastmd_amd._roctx import roctx_ranged
 
 MAX_IMAGE = 10
 _NEIGHBOR_SLOT_QUANTUM = 16
@@ -87,6 +88,7 @@ class TensorGraphBuilder:
         self._cell_atoms = torch.zeros(n, dtype=torch.int32, device=dev)
 
     @torch.no_grad()
+    @roctx_ranged("neighbor_list")
     def build(self, positions: Tensor) -> GraphBatch:
         n, dev = self.n_atoms, self.device
         positions = positions.to(device=dev)

@@ -31,6 +31,7 @@ from fastmd_amd.execution.whole_step_cuda_graph import (FixedCapacityOverflow, W
                                                         _capacity_exceeded)
 from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
 from fastmd_amd.graph.gpu_graph_builder import TensorGraphBuilder, raise_if_isolated_atoms
+from fastmd_amd._roctx import roctx_ranged
 
 
 def _atoms_arrays(atoms):
@@ -100,6 +101,9 @@ class GPUResidentMolecularDynamics:
         self.cell = torch.tensor(cell, dtype=torch.float64)
         self.numbers = torch.tensor(numbers, dtype=torch.int32)
         self.masses = masses
+        # per-atom masses given explicitly (a System, or ASE atoms holding a masses array): frames
+        # then carry a masses column, as ASE's EXTXYZ writer does for such atoms
+        self.explicit_masses = not hasattr(atoms, "get_positions") or "masses" in getattr(atoms, "arrays", {})
         self.temperature = float(temperature)
         if momenta is None:
             momenta = atom_momenta if atom_momenta is not None else maxwell_boltzmann_momenta(masses, temperature, seed)
@@ -144,7 +148,7 @@ class GPUResidentMolecularDynamics:
 
         self.logger = AsyncGPUMDLogger(
             AtomsTemplate(np.asarray(numbers), np.asarray(masses, np.float64), np.asarray(cell, np.float64),
-                          np.ones(3, bool)), self.device, trajectory=trajectory, logfile=logfile,
+                          np.ones(3, bool), self.explicit_masses), self.device, trajectory=trajectory, logfile=logfile,
             loginterval=loginterval, append_trajectory=append_trajectory, ring=logger_ring,
             state_dtype=torch.float64, extras={"nhc_eta": int(tchain), "nhc_p_eta": int(tchain)})
         self.outputs = MDOutputs(self, output_dir, thermo_interval, xyz_interval, restart_interval, total_steps,
@@ -415,6 +419,7 @@ class GPUResidentMolecularDynamics:
         self.whole_step_capacity_history.append(self._capacity.u_capacity)
         self.whole_step_triplet_capacity_history.append(self._capacity.t_capacity)
 
+    @roctx_ranged("md_run")
     def run(self, steps: int) -> None:
         """``steps`` MD steps (a multiple of ``steps_per_launch`` in the whole-step mode).
 

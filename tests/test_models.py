@@ -1,5 +1,8 @@
-"""Models on the HIP kernels (MACE-like, Morse) vs the PyTorch-CPU oracle; the oracle pinned by
-finite differences, Newton's third law and exact-zero padding (CPU)."""
+"""Models on the HIP kernels (MACE-like, Morse) vs the PyTorch-CPU oracle (GPU, also on a rotated
+triclinic cell and at the 10 000-atom headline size); the oracle pinned on the CPU by finite
+differences, Newton's third law, exact-zero padding, rotation invariance with forces rotating,
+atom-permutation invariance, zero forces at inversion centres and a hand-reduced dimer closed
+form of the two-layer model."""
 import dataclasses
 
 import numpy as np
@@ -79,6 +82,156 @@ def test_mace_like_oracle_padding_adds_exactly_nothing():
     assert torch.equal(f1, f2)
 
 
+def _rotation(seed):
+    """A random proper rotation (det +1) from the QR of a seeded Gaussian matrix."""
+    q, r = np.linalg.qr(np.random.default_rng(seed).normal(size=(3, 3)))
+    q = q * np.sign(np.diag(r))
+    if np.linalg.det(q) < 0:
+        q[:, 0] = -q[:, 0]
+    return q
+
+
+def _triclinic_rotated(s, seed=7, shear=(0.12, -0.08, 0.05)):
+    """The same crystal (fractional coordinates kept) in a sheared cell, b' = b + s0 a and
+    c' = c + s1 a + s2 b, then rotated as a whole by a random rotation: a general cell matrix
+    with no zero entries and no axis along x, y or z."""
+    frac = s.positions @ np.linalg.inv(s.cell)
+    shear_m = np.array([[1.0, 0.0, 0.0], [shear[0], 1.0, 0.0], [shear[1], shear[2], 1.0]])
+    cell = (shear_m @ s.cell) @ _rotation(seed).T
+    return systems.System(frac @ cell, cell, s.numbers.copy(), s.masses.copy())
+
+
+def test_mace_like_oracle_rotation_invariant_and_forces_rotate():
+    """A common rotation R of the positions and of a triclinic cell (same edges and images)
+    leaves every per-atom energy unchanged and rotates the forces, F' = F R^T: the model sees
+    only lengths, u . h1 projections and |P1|^2, and carries h1 as a vector. A sign or index
+    mistake in u, the projection or the vector message breaks the second property."""
+    s = _triclinic_rotated(systems.perovskite(2, sigma=0.2), seed=3)
+    center, neighbor, images, pos = _edges(s)
+    _, params, cfg, elem_of = _mace_params(64)
+    elem = torch.tensor([elem_of[int(z)] for z in s.numbers])
+    cell = torch.tensor(s.cell)
+    e, f, node = om.energy_and_forces(_mace_fn(params, cfg, elem, center, neighbor, images, cell), pos)
+    assert float(f.abs().max()) > 1e-2
+    for seed in (11, 12):
+        rot = torch.tensor(_rotation(seed))
+        e_r, f_r, node_r = om.energy_and_forces(
+            _mace_fn(params, cfg, elem, center, neighbor, images, cell @ rot.T), pos @ rot.T)
+        assert float((node_r - node).abs().max()) < 1e-12 * float(node.abs().max())
+        assert abs(float(e_r - e)) < 1e-12 * abs(float(e))
+        assert float((f_r - f @ rot.T).abs().max()) < 1e-10 * float(f.abs().max())
+
+
+def test_mace_like_oracle_permutation_invariant():
+    """Relabelling the atoms (and listing the edge rows in another order) permutes the per-atom
+    energies and forces the same way and leaves the total unchanged."""
+    s = systems.perovskite(2, sigma=0.2)
+    center, neighbor, images, pos = _edges(s)
+    _, params, cfg, elem_of = _mace_params(64)
+    elem = torch.tensor([elem_of[int(z)] for z in s.numbers])
+    cell = torch.tensor(s.cell)
+    e, f, node = om.energy_and_forces(_mace_fn(params, cfg, elem, center, neighbor, images, cell), pos)
+    rng = np.random.default_rng(5)
+    perm = torch.tensor(rng.permutation(s.n_atoms))  # new atom k is old atom perm[k]
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(s.n_atoms)
+    rows = torch.tensor(rng.permutation(center.shape[0]))
+    fn_p = _mace_fn(params, cfg, elem[perm], inv[center[rows]], inv[neighbor[rows]], images[rows], cell)
+    e_p, f_p, node_p = om.energy_and_forces(fn_p, pos[perm])
+    assert abs(float(e_p - e)) < 1e-12 * abs(float(e))
+    assert float((node_p - node[perm]).abs().max()) < 1e-12 * float(node.abs().max())
+    assert float((f_p - f[perm]).abs().max()) < 1e-10 * float(f.abs().max())
+
+
+def test_mace_like_oracle_symmetric_sites_have_zero_forces():
+    """On the unjittered cubic perovskite every atom sits on an inversion centre, so every force
+    vanishes (to rounding) while the energy does not."""
+    s = systems.perovskite(2, sigma=0.0)
+    center, neighbor, images, _ = _edges(s)
+    pos = torch.tensor(s.positions)  # float64 sites (inside the cell, so no wrap): no float32 rounding
+    _, params, cfg, elem_of = _mace_params(64)
+    elem = torch.tensor([elem_of[int(z)] for z in s.numbers])
+    e, f, _ = om.energy_and_forces(_mace_fn(params, cfg, elem, center, neighbor, images, torch.tensor(s.cell)), pos)
+    assert abs(float(e)) > 1.0 and float(f.abs().max()) < 1e-11
+
+
+def _np_silu(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def _dimer_energy_closed_form(params, cfg, r, e_pair):
+    """Total energy of an isolated dimer at separation r written out from the model's definition
+    (per layer: gather-cat, edge GEMM, gated messages, contraction, node update; the readout), in
+    NumPy with the geometry reduced by hand. Atom i's only edge comes from the other atom j, and
+    u_1 = -u_0. Every vector feature stays parallel to the bond, h1_i = u_i (x) v_i, so
+      h1_j . u_i = -v_j,   m1_i = u_i (x) (wb h0_j - wd v_j),   |P1_i|^2 = ((wb h0_j - wd v_j)/avg Wm1)^2
+    and the model reduces to channel vectors only. Independent of the oracle's edge lists, index
+    sums and 3-vectors."""
+    p = {k: v.detach().double().numpy() for k, v in params.items()}
+    C, nb, L, rc, avg = cfg["channels"], cfg["n_basis"], cfg["num_interactions"], cfg["cutoff"], cfg["avg_num_neighbors"]
+    x = r / rc
+    fcut = 1 - 21 * x ** 5 + 35 * x ** 6 - 15 * x ** 7 if x < 1 else 0.0
+    n = np.arange(1, nb + 1)
+    ef = np.sqrt(2.0 / rc) * np.sin(n * np.pi * r / rc) / r * fcut
+    h = [p["embedding"][e_pair[0]], p["embedding"][e_pair[1]]]
+    v = [np.zeros(C), np.zeros(C)]
+    h_first = None
+    for t in range(L):
+        W = {k.split(".", 2)[2]: val for k, val in p.items() if k.startswith(f"layers.{t}.")}
+        new_h, new_v = [], []
+        for i in (0, 1):
+            j = 1 - i
+            z = np.concatenate([h[j], h[i], ef]) @ W["W1"]
+            w = _np_silu(z) * fcut
+            wa, wb, wc, wd = w[:C], w[C:2 * C], w[2 * C:3 * C], w[3 * C:]
+            P0 = ((wa * h[j] - wc * v[j]) / avg) @ W["Wm0"]
+            p1 = ((wb * h[j] - wd * v[j]) / avg) @ W["Wm1"]
+            n1 = p1 * p1
+            c = W["Wc"][e_pair[i]]
+            B0 = c[0] * P0 + c[1] * P0 ** 2 + c[2] * n1 + c[3] * P0 ** 3 + c[4] * P0 * n1
+            new_h.append(B0 @ W["Wo0"] + h[i] @ W["Wsc0"])
+            d = W["Wd"][e_pair[i]]
+            new_v.append(((d[0] + d[1] * P0 + d[2] * P0 ** 2 + d[3] * n1) * p1) @ W["Wo1"])
+        if t == 0:
+            h_first = new_h
+        h, v = new_h, new_v
+    total = 0.0
+    for i in (0, 1):
+        e_i = h_first[i] @ p["wr1"] + _np_silu(h[i] @ p["Wr2a"]) @ p["wr2b"]
+        total += p["e0"][e_pair[i]] + cfg["scale"] * e_i + cfg["shift"]
+    return total
+
+
+@pytest.mark.parametrize("r", [2.7, 4.1, 5.5])
+def test_mace_like_oracle_dimer_closed_form(r):
+    """The oracle on an isolated, randomly oriented Cs-I dimer (two layers, so the vector
+    features of the first layer feed the second) equals the hand-reduced closed form; its forces
+    are equal and opposite, along the bond, and equal -dE/dr of the closed form."""
+    _, params, cfg, elem_of = _mace_params(64)
+    e_pair = (elem_of[55], elem_of[53])
+    u = _rotation(9)[0]
+    pos = torch.tensor(np.array([[11.0, 12.0, 13.0], [11.0, 12.0, 13.0] + r * u]))
+    cell = torch.eye(3, dtype=torch.float64) * 40.0
+    fn = _mace_fn(params, cfg, torch.tensor(e_pair), torch.tensor([0, 1]), torch.tensor([1, 0]),
+                  torch.zeros(2, 3, dtype=torch.int32), cell)
+    e, f, _ = om.energy_and_forces(fn, pos)
+    closed = _dimer_energy_closed_form(params, cfg, r, e_pair)
+    assert abs(float(e) - closed) < 1e-12 * abs(closed)
+    h = 1e-5
+    dedr = (_dimer_energy_closed_form(params, cfg, r + h, e_pair)
+            - _dimer_energy_closed_form(params, cfg, r - h, e_pair)) / (2 * h)
+    assert abs(dedr) > 1e-3
+    f1 = f[1].numpy()
+    assert np.abs(f1 + dedr * u).max() < 1e-7 * max(1.0, abs(dedr))
+    assert np.abs(f[0].numpy() + f1).max() < 1e-12 * abs(dedr)
+    # one layer only: the vector features never enter, and the closed form still holds
+    cfg1 = dict(cfg, num_interactions=1)
+    p1 = {k: v for k, v in params.items() if not k.startswith("layers.1.")}
+    fn1 = _mace_fn(p1, cfg1, torch.tensor(e_pair), torch.tensor([0, 1]), torch.tensor([1, 0]),
+                   torch.zeros(2, 3, dtype=torch.int32), cell)
+    assert abs(float(fn1(pos).sum()) - _dimer_energy_closed_form(p1, cfg1, r, e_pair)) < 1e-12 * abs(closed)
+
+
 def test_morse_oracle_dimer_closed_form_and_gradient():
     cell = torch.eye(3, dtype=torch.float64) * 30.0
     pos = torch.tensor([[0.0, 0.0, 0.0], [3.5, 0.0, 0.0]], dtype=torch.float64)
@@ -101,18 +254,24 @@ def _gpu_builder(s, u_cap, device):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n_cells,channels,hoist,fused", [
-    (3, 128, None, True), (3, 64, None, True), (3, 256, None, True), ((6, 6, 6), 128, None, True),
-    (3, 64, 0, True), (3, 128, 0, True), (3, 256, 0, True), ((6, 6, 6), 128, 10 ** 9, True),
-    (3, 64, None, False), (3, 128, None, False), (3, 256, None, False), ((6, 6, 6), 128, None, False),
-    ((10, 10, 10), 128, None, False)])
-def test_mace_like_gpu_matches_oracle(device, n_cells, channels, hoist, fused, monkeypatch):
+@pytest.mark.parametrize("n_cells,channels,hoist,fused,geometry", [
+    (3, 128, None, True, "cubic"), (3, 64, None, True, "cubic"), (3, 256, None, True, "cubic"),
+    ((6, 6, 6), 128, None, True, "cubic"), (3, 64, 0, True, "cubic"), (3, 128, 0, True, "cubic"),
+    (3, 256, 0, True, "cubic"), ((6, 6, 6), 128, 10 ** 9, True, "cubic"), (3, 64, None, False, "cubic"),
+    (3, 128, None, False, "cubic"), (3, 256, None, False, "cubic"), ((6, 6, 6), 128, None, False, "cubic"),
+    ((10, 10, 10), 128, None, False, "cubic"),
+    (3, 128, None, False, "triclinic_rotated"), ((6, 6, 6), 128, None, False, "triclinic_rotated"),
+    ((6, 6, 6), 128, 0, False, "triclinic_rotated"),
+    ((10, 10, 20), 128, None, False, "cubic")])
+def test_mace_like_gpu_matches_oracle(device, n_cells, channels, hoist, fused, geometry, monkeypatch):
     """Energies within 1e-5 eV/atom and forces within 1e-4 eV/A of the FP64 oracle, through the
     fixed-capacity builder (padding rows present), bitwise reproducible. ``hoist`` overrides the
     edge-list size from which the receiver block of the edge GEMM is formed per atom (0: always,
     10**9: never), so both evaluation orders of z are checked at every width; ``fused`` selects the
     fused node kernels or the unfused chain of GEMMs and contraction kernels; at 5 000 atoms the
-    unfused node GEMMs take their split-plane grouped form."""
+    unfused node GEMMs take their split-plane grouped form. ``triclinic_rotated`` puts the crystal
+    in a sheared cell rotated as a whole (no cell axis along x, y or z); 10 x 10 x 20 cells is the
+    10 000-atom headline system."""
     from fastmd_amd.engine.energy_derivative import EnergyDerivative
     from fastmd_amd.models import mace_like
     from fastmd_amd.models.mace_like import MaceLikeAdapter
@@ -120,8 +279,10 @@ def test_mace_like_gpu_matches_oracle(device, n_cells, channels, hoist, fused, m
     if hoist is not None:
         monkeypatch.setattr(mace_like, "HOIST_MIN_ROWS", hoist)
     monkeypatch.setattr(mace_like, "FUSED_NODE", fused)
-    print(f"[mace] cells={n_cells} C={channels} hoist={hoist} fused={fused}", flush=True)
+    print(f"[mace] cells={n_cells} C={channels} hoist={hoist} fused={fused} {geometry}", flush=True)
     s = systems.perovskite(n_cells, sigma=0.2)  # displaced from the symmetric sites: sizeable forces
+    if geometry == "triclinic_rotated":
+        s = _triclinic_rotated(s)
     n = s.n_atoms
     m, params, cfg, elem_of = _mace_params(channels)
     adapter = MaceLikeAdapter(m, device=device)

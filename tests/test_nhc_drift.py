@@ -1,0 +1,170 @@
+"""The north-star drift gate: the NHC conserved quantity of the GPU's whole-step MD drifts no more
+than the CPU oracle's integration of the same system.
+
+The oracle's integrations (``tests/golden/make_nhc_drift.py``) are committed fixtures: 10 000
+Morse steps and 2 000 MACE-like steps, each from the momenta of seeds
+0, 1 and 2. The CPU tests pin each fixture to a short live run of the oracle. The trajectories of
+two chaotic runs decorrelate within a few hundred steps, so over the whole run the size of the
+drift is compared, not the path: with drift = max_t |C(t) - C(0)|, the gate is
+
+    mean over seeds (GPU drift) <= mean over seeds (oracle drift) + (max - min of the oracle drifts)
+
+i.e. the oracle's own spread across momenta seeds is the noise floor. Over the first steps, while
+the paths still agree, the positions themselves are compared.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from fastmd_amd import systems
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _fixture(name):
+    return np.load(os.path.join(GOLDEN, name))
+
+
+def _gate(gpu, oracle):
+    gpu, oracle = np.asarray(gpu), np.asarray(oracle)
+    return float(gpu.mean()), float(oracle.mean() + (oracle.max() - oracle.min()))
+
+
+def _mace_params():
+    import dataclasses
+
+    from fastmd_amd.models.mace_like import MaceLike, MaceLikeConfig
+
+    cfg = MaceLikeConfig()
+    return {k: v.detach().clone() for k, v in MaceLike(cfg).named_parameters()}, dataclasses.asdict(cfg)
+
+
+# ------------------------------------------------------------------------------------ CPU pins
+def test_morse_fixture_is_the_oracle_integration():
+    import md_oracle
+    from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
+
+    fx = _fixture("nhc_drift_morse_135.npz")
+    s = systems.perovskite(3)
+    assert tuple(fx["seeds"]) == (0, 1, 2) and fx["steps"][-1] == 10_000 and fx["conserved"].shape == (3, 101)
+    live = md_oracle.run_nhc(s, md_oracle.morse_forces(s), maxwell_boltzmann_momenta(s.masses, 500.0, 1), 300,
+                             sample_every=100)
+    np.testing.assert_allclose(live["conserved"], fx["conserved"][1, :4], rtol=0, atol=1e-9)
+
+
+def test_mace_like_fixture_is_the_oracle_integration():
+    import torch
+
+    import md_oracle
+    from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
+
+    fx = _fixture("nhc_drift_mace_like_135.npz")
+    s = systems.perovskite(3)
+    assert fx["conserved_f64"].shape == (3, 201) and fx["conserved_f32"].shape == (3, 201)
+    assert fx["positions_f64"].shape == (3, 6, s.n_atoms, 3)
+    params, cfg = _mace_params()
+    p0 = maxwell_boltzmann_momenta(s.masses, 500.0, 0)
+    for dtype, key in ((torch.float64, "conserved_f64"), (torch.float32, "conserved_f32")):
+        live = md_oracle.run_nhc(s, md_oracle.mace_like_forces(s, params, cfg, dtype=dtype), p0, 20,
+                                 positions_until=20)
+        np.testing.assert_allclose(live["conserved"], fx[key][0, :3], rtol=0, atol=1e-9)
+        if dtype == torch.float64:
+            np.testing.assert_allclose(live["positions"], fx["positions_f64"][0, :3], rtol=0, atol=1e-10)
+    # the oracle's float32 and float64 paths are the same trajectory to float32 noise early on
+    assert np.abs(fx["conserved_f32"][:, :6] - fx["conserved_f64"][:, :6]).max() < 1e-3
+
+
+def test_oracle_pair_list_matches_the_neighbour_list_oracle():
+    """The fixtures' brute-force skin pair list holds exactly the neighbour-list oracle's edges
+    (away from the cutoff) on a jittered, displaced system."""
+    import md_oracle
+    from oracle import nl as onl
+
+    s = systems.perovskite(3, sigma=0.2)
+    q = s.positions + np.random.default_rng(3).normal(0, 0.3, s.positions.shape)
+    ii, jj, img = md_oracle.PairList(s.cell).pairs(q)
+    cell32 = s.cell.astype(np.float32)
+    inv = np.linalg.inv(cell32.astype(np.float64)).astype(np.float32)
+    _, wraps, wrapped = onl.wrap(q, inv, cell32)
+    cand = onl.candidates(wrapped, cell32, np.float32(64.0), 1504)
+    b = onl.build(q, inv, cell32, cand, q.astype(np.float32), wraps, np.float32(36.0), np.float32(2.0), (1, 0, 0),
+                  10 ** 6)
+    e = b.n_edges
+    # the builder's images are in the frame of the wrapped positions: move them to q's frame
+    w = wraps.astype(np.int64)
+    nl_img = b.images[:e].astype(np.int64) - w[b.neighbor[:e]] + w[b.center[:e]]
+    ours = {(int(i), int(j), *map(int, k)) for i, j, k in zip(ii, jj, img)}
+    theirs = {(int(i), int(j), *map(int, k)) for i, j, k in zip(b.center[:e], b.neighbor[:e], nl_img)}
+    vec = lambda i, j, k: q[j] + np.asarray(k) @ s.cell - q[i]  # noqa: E731
+    near = {t for t in ours ^ theirs if abs(np.linalg.norm(vec(t[0], t[1], t[2:])) - 6.0) < 1e-5}
+    assert ours ^ theirs == near and len(ours) > 1000
+
+
+# ------------------------------------------------------------------------------------ GPU gates
+def _md(system, adapter, momenta, device):
+    from fastmd_amd.config import InferenceConfig
+    from fastmd_amd.interfaces.gpu_md import GPUResidentMolecularDynamics
+
+    return GPUResidentMolecularDynamics(system, model=adapter, device=device, temperature=500.0, timestep=0.25,
+                                        tdamp=25.0, momenta=momenta, steps_per_launch=10,
+                                        config=InferenceConfig(execution="whole_step"))
+
+
+@pytest.mark.gpu
+def test_nhc_conserved_quantity_drift_10k_steps_morse(device):
+    """10 000 whole-step NHC steps of Morse on the 135-atom perovskite at 500 K."""
+    from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
+    from fastmd_amd.models.pair_potential import MorsePairAdapter
+
+    fx = _fixture("nhc_drift_morse_135.npz")
+    s = systems.perovskite(3)
+    gpu, oracle = [], []
+    for k, seed in enumerate(fx["seeds"]):
+        md = _md(s, MorsePairAdapter(device=device), maxwell_boltzmann_momenta(s.masses, 500.0, int(seed)), device)
+        c0 = md.conserved_energy()
+        assert abs(c0 - fx["conserved"][k, 0]) < 1e-6 * s.n_atoms
+        series = [c0]
+        for _ in range(100):
+            md.run(100)
+            series.append(md.conserved_energy())
+        gpu.append(float(np.max(np.abs(np.array(series) - c0))))
+        oracle.append(float(np.max(np.abs(fx["conserved"][k] - fx["conserved"][k, 0]))))
+        print(f"[drift morse] seed {seed}: gpu {gpu[-1]:.3e} eV, oracle {oracle[-1]:.3e} eV", flush=True)
+    got, bound = _gate(gpu, oracle)
+    print(f"[drift morse] mean gpu {got:.3e} eV <= bound {bound:.3e} eV", flush=True)
+    assert got <= bound, (gpu, oracle)
+
+
+@pytest.mark.gpu
+def test_mace_like_nhc_2000_steps_vs_oracle(device):
+    """the MACE-like model (random init, seed 0) on the 135-atom perovskite, 2 000
+    whole-step NHC steps per seed. Positions follow the float64 oracle's trajectory over the first
+    50 steps (1e-4 A); the drift over the whole run is gated against the oracle's float32 runs (the
+    reference's arithmetic class; the float64 runs are reported beside them)."""
+    from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
+    from fastmd_amd.models.mace_like import MaceLikeAdapter
+
+    fx = _fixture("nhc_drift_mace_like_135.npz")
+    s = systems.perovskite(3)
+    gpu, o32, o64 = [], [], []
+    for k, seed in enumerate(fx["seeds"]):
+        md = _md(s, MaceLikeAdapter(device=device), maxwell_boltzmann_momenta(s.masses, 500.0, int(seed)), device)
+        c0 = md.conserved_energy()
+        assert abs(c0 - fx["conserved_f64"][k, 0]) < 1e-5 * s.n_atoms
+        series, dev = [c0], [0.0]
+        for block in range(200):
+            md.run(10)
+            series.append(md.conserved_energy())
+            if block < 5:
+                dev.append(float(np.abs(md.positions.cpu().numpy() - fx["positions_f64"][k, block + 1]).max()))
+        print(f"[mace 2000] seed {seed}: max |dq| over 50 steps {max(dev):.2e} A", flush=True)
+        assert max(dev) < 1e-4, dev
+        gpu.append(float(np.max(np.abs(np.array(series) - c0))))
+        o32.append(float(np.max(np.abs(fx["conserved_f32"][k] - fx["conserved_f32"][k, 0]))))
+        o64.append(float(np.max(np.abs(fx["conserved_f64"][k] - fx["conserved_f64"][k, 0]))))
+        print(f"[mace 2000] seed {seed}: drift gpu {gpu[-1]:.3e} eV, oracle f32 {o32[-1]:.3e} eV, "
+              f"oracle f64 {o64[-1]:.3e} eV", flush=True)
+    got, bound = _gate(gpu, o32)
+    print(f"[mace 2000] mean gpu {got:.3e} eV <= bound {bound:.3e} eV", flush=True)
+    assert got <= bound, (gpu, o32, o64)

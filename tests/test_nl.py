@@ -209,7 +209,7 @@ def _assert_build_equal(builder, ob, cand=None):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n_atoms", [135, 1080, 3430, 10000])
+@pytest.mark.parametrize("n_atoms", [135, 1080, 3430, 10000, 16875, 40000])
 def test_builder_bit_exact(device, n_atoms):
     """Candidates, rows, flags and published buffers bit-exact vs the oracle, on the fused
     single-workgroup path (<= 1024 atoms) and the multi-block path, fresh and with reused

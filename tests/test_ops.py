@@ -1,4 +1,6 @@
 """(b) gather-cat, (c) CSR segment sums, (d) MFMA GEMM: HIP kernels vs the oracle."""
+import functools
+
 import numpy as np
 import pytest
 
@@ -21,6 +23,7 @@ def test_oracle_segment_sum_closed_form():
     assert np.array_equal(gv[:, 0], [2, 2, 6, 6, 6, 4])
 
 
+@functools.lru_cache(maxsize=2)
 def _edge_list(n_atoms=135, cutoff=6.0):
     s = systems.perovskite_atoms(n_atoms)
     cell32 = s.cell.astype(np.float32)
@@ -116,6 +119,62 @@ def test_segment_sum_identity_and_perm_csr(device, F):
     out3.sum().backward()
     rows7 = center == 7
     assert float(vd.grad[torch.tensor(rows7, device=device)].abs().max()) == 0.0
+
+
+def _segment_sums_f64(value, segment, n_segments):
+    """fp64 sums of ``value`` rows by ``segment`` (stable sort, then one reduceat per run); every
+    segment of the perovskite edge lists is non-empty."""
+    order = np.argsort(segment, kind="stable")
+    counts = np.bincount(segment, minlength=n_segments)
+    assert counts.min() > 0
+    starts = np.concatenate([[0], np.cumsum(counts)[:-1]])
+    return np.add.reduceat(value[order].astype(np.float64), starts, axis=0)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n_atoms", [3430, 40000])
+@pytest.mark.parametrize("F", [64, 128, 256])
+def test_ops_at_configs_sizes(device, n_atoms, F):
+    """configs[1]'s sizes (N = 3 430 and 40 000, ~15 edges per atom at 6 A, F = 64 / 128 / 256),
+    where the large-grid paths run: gather-cat bitwise equal to the concatenated row gathers and
+    its VJP vs fp64 sums; the segment sum over the receiver CSR (identity permutation) and over the
+    sender CSR (reverse-edge permutation) vs fp64 sums formed by sorting; the transpose bitwise
+    equal to the row gather it is."""
+    import torch
+
+    from fastmd_amd.ops.csr_segment_sum import Csr, csr_segment_sum, segment_sum_t
+    from fastmd_amd.ops.gather_cat import gather_cat
+
+    print(f"[ops large] N={n_atoms} F={F}", flush=True)
+    center, neighbor, off, rev, _, _ = _edge_list(n_atoms)
+    e = center.size
+    g = torch.Generator().manual_seed(F)
+    x = torch.randn(n_atoms, F, generator=g)
+    rbf = torch.randn(e, 8, generator=g)
+    offd = torch.tensor(off, device=device)
+    dst_csr, src_csr = Csr(offd), Csr(offd, torch.tensor(rev, device=device))
+    src, dst = torch.tensor(neighbor, device=device), torch.tensor(center, device=device)
+    xd = x.to(device).requires_grad_()
+    out = gather_cat(xd, src, dst, rbf.to(device), src_csr=src_csr, dst_csr=dst_csr)
+    xn = x.numpy()
+    assert np.array_equal(out.detach().cpu().numpy(), np.concatenate([xn[neighbor], xn[center], rbf.numpy()], 1))
+    gout = torch.randn(e, 2 * F + 8, generator=g)
+    out.backward(gout.to(device))
+    del out
+    gx_ref = (_segment_sums_f64(gout[:, :F].numpy(), neighbor, n_atoms)
+              + _segment_sums_f64(gout[:, F:2 * F].numpy(), center, n_atoms))
+    assert oops.relative(xd.grad.cpu().numpy(), gx_ref) < 1e-6
+    v = gout[:, :F].contiguous()
+    vd = v.to(device)
+    by_dst = csr_segment_sum(vd, dst, n_atoms, off=offd, identity_perm=True)
+    assert oops.relative(by_dst.cpu().numpy(), _segment_sums_f64(v.numpy(), center, n_atoms)) < 1e-5
+    by_src = csr_segment_sum(vd, src, n_atoms, off=offd, perm=src_csr.perm)
+    assert oops.relative(by_src.cpu().numpy(), _segment_sums_f64(v.numpy(), neighbor, n_atoms)) < 1e-5
+    node = torch.randn(n_atoms, F, generator=g)
+    gv, _ = segment_sum_t(node.to(device), dst_csr, e)
+    assert np.array_equal(gv.cpu().numpy(), node.numpy()[center])
+    gv_src, _ = segment_sum_t(node.to(device), src_csr, e)
+    assert np.array_equal(gv_src.cpu().numpy(), node.numpy()[neighbor])
 
 
 @pytest.mark.gpu

@@ -45,6 +45,35 @@ def test_extxyz_round_trip(tmp_path):
     assert len(mp.read_extxyz(tmp_path / "t.extxyz")) == 3
 
 
+def test_extxyz_frame_text_is_the_ase_layout(tmp_path):
+    """A written frame, character for character, as ASE's extxyz writer lays out an Atoms with
+    explicit masses, velocities, a single-point calculator (energy, forces) and info entries:
+    Lattice, Properties, the info keys in insertion order, energy, pbc; ``%-2s`` species and
+    ``%16.8f`` columns (hand-written expected text)."""
+    frame = Frame(numbers=np.array([55, 53]), masses=np.array([2.0, 4.0]), cell=np.diag([6.2, 6.2, 6.3]),
+                  pbc=np.ones(3, bool), positions=np.array([[0.1, 0.2, 0.3], [3.1, 3.1, 0.0]]),
+                  momenta=np.array([[2.0, -4.0, 0.0], [4.0, 0.0, -2.0]]),
+                  forces=np.array([[0.5, -0.25, 0.0], [-0.5, 0.25, 1e-9]]), energy=-12.5,
+                  info={"step": np.array([10.0]), "time_fs": np.array([2.5]), "nhc_eta": np.array([0.1, 0.2, 0.3])},
+                  explicit_masses=True)
+    traj = mp.ExtxyzTrajectory(tmp_path / "one.extxyz", append=False)
+    traj.write(frame)
+    traj.close()
+    expected = (
+        "2\n"
+        'Lattice="6.2 0.0 0.0 0.0 6.2 0.0 0.0 0.0 6.3" '
+        "Properties=species:S:1:pos:R:3:masses:R:1:velocities:R:3:forces:R:3 "
+        'step=10 time_fs=2.5 nhc_eta="0.1 0.2 0.3" energy=-12.5 pbc="T T T"\n'
+        "Cs       0.10000000       0.20000000       0.30000000       2.00000000       1.00000000"
+        "      -2.00000000       0.00000000       0.50000000      -0.25000000       0.00000000\n"
+        "I        3.10000000       3.10000000       0.00000000       4.00000000       1.00000000"
+        "       0.00000000      -0.50000000      -0.50000000       0.25000000       0.00000000\n")
+    assert (tmp_path / "one.extxyz").read_text() == expected
+    back = mp.read_extxyz(tmp_path / "one.extxyz")[0]
+    assert back["keys"] == ["Lattice", "Properties", "step", "time_fs", "nhc_eta", "energy", "pbc"]
+    assert np.array_equal(back["masses"], [2.0, 4.0]) and np.allclose(back["velocities"], [[1, -2, 0], [1, 0, -0.5]])
+
+
 def test_restart_round_trip_and_format_check(tmp_path):
     rng = np.random.default_rng(1)
     data = mp.RestartData(ids=np.arange(4), numbers=np.array([55, 50, 53, 53]), masses=rng.random(4),
@@ -127,6 +156,22 @@ def test_whole_step_outputs_and_bitwise_resume(device, tmp_path):
     md.close()
     frames = mp.read_extxyz(out / mp.TRAJECTORY_FILE)
     assert [f["info"]["step"] for f in frames] == [0, 10, 20]
+    assert frames[0]["keys"] == ["Lattice", "Properties", "step", "time_fs", "target_temp_K", "nhc_eta", "nhc_p_eta",
+                                 "nhc_conserved_energy", "energy", "pbc"]
+    # the frames of steps 10 and 20 are the CPU oracle's integrated states (tests/md_oracle.py)
+    import md_oracle
+    from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
+
+    s = systems.perovskite(3)
+    o = md_oracle.run_nhc(s, md_oracle.morse_forces(s), maxwell_boltzmann_momenta(s.masses, 500.0, 0), 20,
+                          sample_every=10, positions_until=20)
+    for k in (1, 2):
+        assert np.abs(frames[k]["positions"] - o["positions"][k]).max() < 1e-4
+        assert np.abs(frames[k]["velocities"] - o["momenta"][k] / s.masses[:, None]).max() < 1e-6
+        assert np.abs(frames[k]["forces"] - o["forces"][k]).max() < 1e-4
+        assert np.array_equal(frames[k]["masses"], s.masses)
+        assert abs(frames[k]["energy"] - o["energy"][k]) < 1e-6 * s.n_atoms
+        assert abs(frames[k]["info"]["nhc_conserved_energy"] - o["conserved"][k]) < 1e-6 * s.n_atoms
     state = md.integrator
     assert np.allclose(frames[-1]["positions"], state.positions.cpu().numpy(), atol=1e-7)
     assert np.allclose(frames[-1]["forces"], state.forces.cpu().numpy(), atol=1e-7)

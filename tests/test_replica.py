@@ -66,3 +66,44 @@ def test_replicas_equal_single_runs_bitwise(device, model_name):
         assert torch.equal(batch.integrator.eta[r], th.eta) and torch.equal(batch.integrator.p_eta[r], th.p_eta)
     thermo = batch.thermodynamics()
     assert len(thermo) == R and len({round(t["temperature"], 6) for t in thermo}) == R  # distinct replicas
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("model_name", ["morse", "mace_like"])
+def test_replicas_follow_the_oracle_md(device, model_name):
+    """Each replica of a batch follows the CPU oracle's NHC integration (tests/md_oracle.py) from
+    that replica's momenta: positions to 1e-4 A and the conserved quantity's change since step 0
+    to 1e-7 eV per atom, at every 10th of 50 steps."""
+    import dataclasses
+
+    import md_oracle
+    from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
+    from fastmd_amd.execution.replica_batch import ReplicaBatchedMD
+
+    print(f"[replicas vs oracle] {model_name}", flush=True)
+    s = systems.perovskite(3)
+    seeds = (11, 12, 13)
+    momenta = np.stack([maxwell_boltzmann_momenta(s.masses, 500.0, seed) for seed in seeds])
+    if model_name == "morse":
+        make_forces = lambda: md_oracle.morse_forces(s)  # noqa: E731
+    else:
+        from fastmd_amd.models.mace_like import MaceLike, MaceLikeConfig
+
+        params = {k: v.detach().clone() for k, v in MaceLike(MaceLikeConfig()).named_parameters()}
+        cfg = dataclasses.asdict(MaceLikeConfig())
+        make_forces = lambda: md_oracle.mace_like_forces(s, params, cfg)  # noqa: E731
+    batch = ReplicaBatchedMD(s, _adapter(model_name, device), replicas=len(seeds), device=device, temperature=500.0,
+                             timestep=0.25, tdamp=25.0, momenta=momenta, steps_per_launch=5)
+    oracles = [md_oracle.run_nhc(s, make_forces(), momenta[r], 50, sample_every=10, positions_until=50)
+               for r in range(len(seeds))]
+    c0 = [t["conserved_energy"] for t in batch.thermodynamics()]
+    for k in range(1, 6):
+        batch.run(10)
+        thermo = batch.thermodynamics()
+        for r, o in enumerate(oracles):
+            q = batch.replica_state(r)["positions"].cpu().numpy()
+            dq = float(np.abs(q - o["positions"][k]).max())
+            dc = abs((thermo[r]["conserved_energy"] - c0[r]) - (o["conserved"][k] - o["conserved"][0]))
+            assert dq < 1e-4, (r, k, dq)
+            assert dc < 1e-7 * s.n_atoms, (r, k, dc)
+    print(f"[replicas vs oracle] {model_name}: step 50 ok", flush=True)

@@ -88,6 +88,24 @@ def test_whole_step_equals_eager_bitwise(device, model_name, steps_per_launch):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("k", [15, 20])
+def test_whole_step_equals_eager_bitwise_configs3_sizes(device, k):
+    """configs[3]'s largest supercells (16 875 and 40 000 atoms), MACE-like model: 20 whole-step
+    steps (windows of 10) give the eager trajectory bitwise, on the large-grid kernel paths."""
+    import torch
+
+    print(f"[whole_step configs3] k={k}", flush=True)
+    s = systems.perovskite(k)
+    eager = _md(_adapter("mace_like", device), "eager", device, system=s)
+    graph = _md(_adapter("mace_like", device), "whole_step", device, steps_per_launch=10, system=s)
+    eager.run(20)
+    graph.run(20)
+    a, b = _state(eager), _state(graph)
+    assert torch.equal(a, b), float((a - b).abs().max())
+    assert graph.whole_step_stats()["launches"] == 2
+
+
+@pytest.mark.gpu
 def test_whole_step_capacity_growth_and_refresh_paths(device):
     """A tiny capacity step forces overflow -> growth -> recapture; a tiny skin forces candidate
     refreshes and fallback windows. The trajectory stays the eager one, bitwise."""
@@ -196,97 +214,46 @@ def test_windows_launched_behind_match_settled_windows_bitwise(device, model_nam
 
 
 @pytest.mark.gpu
-def test_whole_step_morse_md_matches_cpu_oracle(device):
-    """configs[0] plumbing: Morse MD (NHC 500 K, dt 0.25 fs) for 200 steps on the GPU vs the CPU
-    oracle (numpy NHC + PyTorch-CPU Morse forces in float32, like the GPU): positions agree to fp32
-    noise, and the conserved quantity drifts no more than the oracle's."""
-    import torch
-
-    from oracle import models as om
-    from oracle import nhc as onhc
-    from oracle import nl as onl
+@pytest.mark.parametrize("execution", ["whole_step", "model_graph"])
+def test_morse_md_matches_cpu_oracle(device, execution):
+    """configs[0] plumbing: Morse MD (NHC 500 K, dt 0.25 fs) for 200 steps on the GPU, in the
+    whole-step and in the model_graph mode, against the CPU oracle's integration (NumPy NHC,
+    float64 Morse forces rounded to float32 like the GPU's, brute-force skin pair list): the
+    trajectories coincide, so the positions agree to float32 noise and so does the conserved
+    quantity at every sampled step (its change since step 0, which cancels the float32 rounding of
+    the initial energy)."""
+    import md_oracle
     from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
     from fastmd_amd.models.pair_potential import MorsePairAdapter
 
     s = systems.perovskite(3)
-    md = _md(MorsePairAdapter(device=device), "whole_step", device, steps_per_launch=10, system=s)
-    cell32 = s.cell.astype(np.float32)
-    inv = np.linalg.inv(cell32.astype(np.float64)).astype(np.float32)
-
-    def forces(q):
-        _, wraps, wrapped = onl.wrap(q, inv, cell32)
-        cand = onl.candidates(wrapped, cell32, np.float32(36.0 + 1e-3), 200)
-        b = onl.build(q, inv, cell32, cand, q.astype(np.float32), wraps, np.float32(36.0), np.float32(1.0), (1, 0, 0),
-                      int(cand.num_neighbors.sum()))
-        e = b.n_edges
-        pos = torch.tensor(b.wrapped)
-        energy, f, _ = om.energy_and_forces(om.morse_node_energy, pos, torch.tensor(cell32), torch.tensor(
-            b.center[:e].astype(np.int64)), torch.tensor(b.neighbor[:e].astype(np.int64)), torch.tensor(b.images[:e]))
-        return f.numpy().astype(np.float32), float(energy)
-
-    p0 = maxwell_boltzmann_momenta(s.masses, 500.0, seed=0)
-    f0, e0 = forces(s.positions)
-    o = onhc.NHC(s.masses, s.positions, p0, temperature_K=500.0, timestep=0.25 * onhc.FS, tdamp=25 * onhc.FS,
-                 f32_kick=True, forces=f0, energy=e0)
-    c0_gpu, c0_cpu = md.conserved_energy(), o.conserved_energy()
-    assert abs(c0_gpu - c0_cpu) < 1e-4 * s.n_atoms
-    for _ in range(200):
-        o.step(forces)
-    md.run(200)
-    q = md.positions.cpu().numpy()
-    assert np.max(np.abs(q - o.q)) < 1e-3
-    drift_gpu = abs(md.conserved_energy() - c0_gpu)
-    drift_cpu = abs(o.conserved_energy() - c0_cpu)
-    assert drift_gpu <= 2 * drift_cpu + 1e-6 * s.n_atoms, (drift_gpu, drift_cpu)
+    md = _md(MorsePairAdapter(device=device), execution, device, steps_per_launch=10, system=s)
+    oracle = md_oracle.run_nhc(s, md_oracle.morse_forces(s), maxwell_boltzmann_momenta(s.masses, 500.0, 0), 200,
+                               sample_every=10, positions_until=200)
+    c0 = md.conserved_energy()
+    assert abs(c0 - oracle["conserved"][0]) < 1e-6 * s.n_atoms
+    dq, dc = [], []
+    for k in range(1, 21):
+        md.run(10)
+        dq.append(float(np.abs(md.positions.cpu().numpy() - oracle["positions"][k]).max()))
+        dc.append(abs((md.conserved_energy() - c0) - (oracle["conserved"][k] - oracle["conserved"][0])))
+    print(f"[morse md {execution}] max |dq| {max(dq):.2e} A, max |dC| {max(dc):.2e} eV", flush=True)
+    assert max(dq) < 1e-4, dq
+    assert max(dc) < 1e-7 * s.n_atoms, dc
 
 
-def _morse_pairs_oracle(s, rc=6.0, skin=2.0):
-    """Vectorized float64 Morse forces for the drift test: candidate pairs (i, j, image) within
-    rc + skin, listed by brute force over the 27 neighbouring images (the 135-atom cell is 18.6 A
-    wide, so rc + skin = 8 A never needs a second shell) and rebuilt when an atom has moved more
-    than skin / 2 since the last listing (the reference's skin rule); every step keeps the pairs
-    with r < rc. Forces are returned as float32 like the GPU's."""
-    cell = s.cell
-    shifts = np.array([[a, b, c] for a in (-1, 0, 1) for b in (-1, 0, 1) for c in (-1, 0, 1)], dtype=np.float64)
-    D, a, r0 = 0.3, 1.5, 3.0
-    vrc = D * ((1 - np.exp(-a * (rc - r0))) ** 2 - 1)
-    state = {}
-
-    def listing(q):
-        d = q[None, :, None, :] + (shifts @ cell)[None, None, :, :] - q[:, None, None, :]
-        r = np.linalg.norm(d, axis=-1)
-        ii, jj, kk = np.nonzero((r < rc + skin) & (r > 1e-8))
-        state.update(q0=q.copy(), ii=ii, jj=jj, sh=(shifts @ cell)[kk])
-
-    def forces(q):
-        if not state or np.max(np.linalg.norm(q - state["q0"], axis=1)) >= skin / 2:
-            listing(q)
-        ii, jj, sh = state["ii"], state["jj"], state["sh"]
-        dv = q[jj] + sh - q[ii]
-        rr = np.linalg.norm(dv, axis=1)
-        m = rr < rc
-        ex = np.exp(-a * (rr - r0))
-        v = np.where(m, D * ((1 - ex) ** 2 - 1) - vrc, 0.0)
-        dvdr = np.where(m, 2 * D * (1 - ex) * a * ex, 0.0)
-        fij = (0.5 * dvdr / rr)[:, None] * dv  # each unordered pair appears twice (i-j and j-i)
-        f = np.zeros_like(q)
-        np.add.at(f, ii, fij)
-        np.add.at(f, jj, -fij)
-        return f.astype(np.float32), 0.5 * float(v.sum())
-
-    return forces
-
-
-def test_drift_oracle_forces_match_the_torch_oracle():
-    """The vectorized Morse forces of the drift test against the oracle's autograd Morse
-    (oracle/models.py) on the same positions: energies to 1e-6 eV, forces to 1e-5 eV/A."""
+def test_oracle_morse_forces_match_the_torch_oracle():
+    """The vectorized Morse forces of the MD oracle (tests/md_oracle.py) against the oracle's
+    autograd Morse (oracle/models.py) on the neighbour-list oracle's edges: energies to 1e-6 eV,
+    forces to 1e-5 eV/A."""
     import torch
 
+    import md_oracle
     from oracle import models as om
     from oracle import nl as onl
 
     s = systems.perovskite(3, sigma=0.2)
-    f_vec, e_vec = _morse_pairs_oracle(s)(s.positions)
+    f_vec, e_vec = md_oracle.morse_forces(s)(s.positions)
     cell32 = s.cell.astype(np.float32)
     inv = np.linalg.inv(cell32.astype(np.float64)).astype(np.float32)
     _, wraps, wrapped = onl.wrap(s.positions, inv, cell32)
@@ -300,34 +267,3 @@ def test_drift_oracle_forces_match_the_torch_oracle():
         torch.tensor(b.images[:e]))
     assert abs(float(energy) - e_vec) < 1e-6
     assert np.abs(f.numpy() - f_vec).max() < 1e-5
-
-
-@pytest.mark.gpu
-def test_nhc_conserved_quantity_drift_10k_steps(device):
-    """North-star gate: over 10 000 whole-step NHC steps (500 K, dt 0.25 fs, Morse on the 135-atom
-    perovskite) the GPU's conserved quantity drifts no more than the CPU oracle's integration of the
-    same system (ASE step order, float32 forces): max |C(t) - C(0)| sampled every 1 000 steps, GPU <=
-    2 x oracle + 2e-7 eV/atom (the trajectories decorrelate, so the fluctuations are compared, not
-    the paths)."""
-    from oracle import nhc as onhc
-    from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
-    from fastmd_amd.models.pair_potential import MorsePairAdapter
-
-    s = systems.perovskite(3)
-    forces = _morse_pairs_oracle(s)
-    p0 = maxwell_boltzmann_momenta(s.masses, 500.0, seed=0)
-    f0, e0 = forces(s.positions)
-    o = onhc.NHC(s.masses, s.positions, p0, temperature_K=500.0, timestep=0.25 * onhc.FS, tdamp=25 * onhc.FS,
-                 f32_kick=True, forces=f0, energy=e0)
-    md = _md(MorsePairAdapter(device=device), "whole_step", device, steps_per_launch=10, system=s)
-    c0_gpu, c0_cpu = md.conserved_energy(), o.conserved_energy()
-    assert abs(c0_gpu - c0_cpu) < 1e-4 * s.n_atoms
-    worst_gpu = worst_cpu = 0.0
-    for block in range(10):
-        for _ in range(1000):
-            o.step(forces)
-        md.run(1000)
-        worst_gpu = max(worst_gpu, abs(md.conserved_energy() - c0_gpu))
-        worst_cpu = max(worst_cpu, abs(o.conserved_energy() - c0_cpu))
-        print(f"[drift] step {1000 * (block + 1)}: gpu {worst_gpu:.3e} eV, oracle {worst_cpu:.3e} eV", flush=True)
-    assert worst_gpu <= 2.0 * worst_cpu + 2e-7 * s.n_atoms, (worst_gpu, worst_cpu)
