@@ -146,12 +146,30 @@ class MaceLike(nn.Module):
                  "wout0": torch.cat([wo0, wsc0], 0).t().contiguous(),
                  "wout1": torch.cat([wo1, zero], 0).t().contiguous(),
                  "wo0st": torch.cat([wo0, wsc0], 0).contiguous(),
-                 "wo1st": torch.cat([wo1, zero], 0).contiguous(), "wo1t": wo1.t().contiguous()}
+                 "wo1st": torch.cat([wo1, zero], 0).contiguous(), "wo1t": wo1.t().contiguous(),
+                 "wo0t": wo0.t().contiguous()}
             src = {"wm0t": w["wm0t"], "wm1t": w["wm1t"], "wout0": w["wout0"], "wo1t": w["wo1t"], "Wo0": wo0,
-                   "Wo1": wo1, "Wsc0": wsc0, "Wm0": wm0, "Wm1": wm1}
+                   "Wo1": wo1, "Wsc0": wsc0, "Wm0": wm0, "Wm1": wm1, "wo0t": w["wo0t"]}
             w["planes"] = {name: split_planes(x.contiguous()) for name, x in src.items()}
             hit = (key, w)
             cache[t] = hit
+        return hit[1]
+
+    def skip_table(self) -> Tensor:
+        """The first layer's residual term per element, embedding @ Wsc0 ([elements, C]), formed in
+        float64 and rounded once to float32; rebuilt when either weight changes in place. The
+        first layer's input is the embedding, so h0 @ Wsc0 is the same row for every atom of an
+        element and its float32 rounding error is the same for all of them: accumulated inside
+        the output GEMM that error grows with |B0 Wo0|, so it adds to the energy coherently over
+        the atoms and with a size that follows the configuration (an energy error the forces do
+        not share, seen as drift of the NHC conserved quantity)."""
+        mats = (self.embedding, self.layers[0].Wsc0)
+        key = tuple((w.data_ptr(), w._version, w.device) for w in mats)
+        hit = self.__dict__.get("_skip_cache")
+        if hit is None or hit[0] != key:
+            table = (self.embedding.detach().double() @ self.layers[0].Wsc0.detach().double()).float().contiguous()
+            hit = (key, table)
+            self.__dict__["_skip_cache"] = hit
         return hit[1]
 
     def w1_receiver_t(self, t: int) -> Tensor:
@@ -343,7 +361,13 @@ class _MaceLikeEnergy(Function):
                       layer.Wd.data_ptr(), n, C, B0.data_ptr(), _abi.ptr(B1))
                 h0n = _empty(n, C, device=dev)
                 h1n = None if last else _empty(n, 3, C, device=dev)
-                probs = [{"a": B0, "a2": h0, "b": w["wout0"], "b_planes": wp["wout0"], "out": h0n}]
+                if t == 0:
+                    # h0 is the embedding: the residual h0 Wsc0 is a per-element table (rounded
+                    # once), added to B0 Wo0 in the GEMM's epilogue
+                    _call("fmd_embed_f32", elem.data_ptr(), model.skip_table().data_ptr(), n, C, h0n.data_ptr())
+                    probs = [{"a": B0, "b": w["wo0t"], "b_planes": wp["wo0t"], "out": h0n, "accumulate": True}]
+                else:
+                    probs = [{"a": B0, "a2": h0, "b": w["wout0"], "b_planes": wp["wout0"], "out": h0n}]
                 if not last:
                     probs.append({"a": B1.view(3 * n, C), "b": w["wo1t"], "b_planes": wp["wo1t"],
                                   "out": h1n.view(3 * n, C)})

@@ -5,12 +5,19 @@ The oracle's integrations (``tests/golden/make_nhc_drift.py``) are committed fix
 Morse steps and 2 000 MACE-like steps, each from the momenta of seeds
 0, 1 and 2. The CPU tests pin each fixture to a short live run of the oracle. The trajectories of
 two chaotic runs decorrelate within a few hundred steps, so over the whole run the size of the
-drift is compared, not the path: with drift = max_t |C(t) - C(0)|, the gate is
+drift is compared, not the path.
 
-    mean over seeds (GPU drift) <= mean over seeds (oracle drift) + (max - min of the oracle drifts)
+Drift is the systematic change of C(t) over the run: the least-squares slope of the sampled C(t)
+times the run length, |b| * T. The largest excursion max_t |C(t) - C(0)| is not used as the
+gate: with a float32 model it is about four standard deviations of the energy's rounding noise
+(about 2e-6 eV at 135 atoms, five times the fitted drift of the float32 oracle over 2 000 steps)
+and so compares noise amplitudes, not drift. The gate is
 
-i.e. the oracle's own spread across momenta seeds is the noise floor. Over the first steps, while
-the paths still agree, the positions themselves are compared.
+    mean over seeds (GPU |b| T) <= mean over seeds (oracle |b| T) + (max - min of the oracle's |b| T)
+
+i.e. the oracle's own spread across momenta seeds is the noise floor. The excursion and the
+residual standard deviation about the fitted line are reported beside it. Over the first steps,
+while the paths still agree, the positions themselves are compared.
 """
 import os
 
@@ -26,9 +33,31 @@ def _fixture(name):
     return np.load(os.path.join(GOLDEN, name))
 
 
+def drift_stats(steps, conserved):
+    """(|b| T, residual std, max |C - C0|) of one sampled C(t) series: b is the least-squares slope
+    in eV per step, T the number of steps from the first to the last sample."""
+    t = np.asarray(steps, dtype=np.float64)
+    c = np.asarray(conserved, dtype=np.float64) - float(conserved[0])
+    design = np.stack([np.ones_like(t), t], axis=1)
+    coef = np.linalg.lstsq(design, c, rcond=None)[0]
+    resid = c - design @ coef
+    return abs(float(coef[1])) * float(t[-1] - t[0]), float(resid.std()), float(np.abs(c).max())
+
+
 def _gate(gpu, oracle):
     gpu, oracle = np.asarray(gpu), np.asarray(oracle)
     return float(gpu.mean()), float(oracle.mean() + (oracle.max() - oracle.min()))
+
+
+def _record(name, rows):
+    """Writes the per-seed drift figures of one gate to gpurun_out/ (the summary under profiles/
+    quotes them)."""
+    out = os.path.join(os.path.dirname(GOLDEN), os.pardir, "gpurun_out")
+    os.makedirs(out, exist_ok=True)
+    with open(os.path.join(out, f"drift_{name}.txt"), "w") as fh:
+        fh.write("seed run drift_|b|T_eV resid_std_eV max_excursion_eV\n")
+        for row in rows:
+            fh.write(" ".join(str(v) for v in row) + "\n")
 
 
 def _mace_params():
@@ -75,6 +104,18 @@ def test_mace_like_fixture_is_the_oracle_integration():
     assert np.abs(fx["conserved_f32"][:, :6] - fx["conserved_f64"][:, :6]).max() < 1e-3
 
 
+def test_drift_stats_separates_trend_from_noise():
+    """A planted linear trend of 1e-6 eV over 2 000 steps under 2e-6 eV of white noise is recovered
+    by the fitted |b| T to within its standard error, while the excursion is set by the noise."""
+    t = np.arange(201) * 10.0
+    noise = np.random.default_rng(0).normal(0.0, 2e-6, t.shape)
+    drift, resid, excursion = drift_stats(t, -5.0 + 5e-10 * t + noise)
+    se = 2e-6 * np.sqrt(12.0 / t.size)  # standard error of |b| T for white noise
+    assert abs(drift - 1e-6) < 3 * se
+    assert 1.8e-6 < resid < 2.2e-6 and excursion > 3 * drift
+    assert drift_stats(t, 2.0 - 1e-7 * t)[0] == pytest.approx(2e-4, rel=1e-12)
+
+
 def test_oracle_pair_list_matches_the_neighbour_list_oracle():
     """The fixtures' brute-force skin pair list holds exactly the neighbour-list oracle's edges
     (away from the cutoff) on a jittered, displaced system."""
@@ -119,7 +160,7 @@ def test_nhc_conserved_quantity_drift_10k_steps_morse(device):
 
     fx = _fixture("nhc_drift_morse_135.npz")
     s = systems.perovskite(3)
-    gpu, oracle = [], []
+    gpu, oracle, rows = [], [], []
     for k, seed in enumerate(fx["seeds"]):
         md = _md(s, MorsePairAdapter(device=device), maxwell_boltzmann_momenta(s.masses, 500.0, int(seed)), device)
         c0 = md.conserved_energy()
@@ -128,9 +169,14 @@ def test_nhc_conserved_quantity_drift_10k_steps_morse(device):
         for _ in range(100):
             md.run(100)
             series.append(md.conserved_energy())
-        gpu.append(float(np.max(np.abs(np.array(series) - c0))))
-        oracle.append(float(np.max(np.abs(fx["conserved"][k] - fx["conserved"][k, 0]))))
-        print(f"[drift morse] seed {seed}: gpu {gpu[-1]:.3e} eV, oracle {oracle[-1]:.3e} eV", flush=True)
+        g, o = drift_stats(fx["steps"], series), drift_stats(fx["steps"], fx["conserved"][k])
+        gpu.append(g[0])
+        oracle.append(o[0])
+        rows += [(int(seed), "gpu", *g), (int(seed), "oracle", *o)]
+        print(f"[drift morse] seed {seed}: |b|T gpu {g[0]:.3e} eV, oracle {o[0]:.3e} eV; "
+              f"residual std gpu {g[1]:.3e}, oracle {o[1]:.3e}; excursion gpu {g[2]:.3e}, oracle {o[2]:.3e}",
+              flush=True)
+    _record("morse_135_10000", rows)
     got, bound = _gate(gpu, oracle)
     print(f"[drift morse] mean gpu {got:.3e} eV <= bound {bound:.3e} eV", flush=True)
     assert got <= bound, (gpu, oracle)
@@ -147,7 +193,7 @@ def test_mace_like_nhc_2000_steps_vs_oracle(device):
 
     fx = _fixture("nhc_drift_mace_like_135.npz")
     s = systems.perovskite(3)
-    gpu, o32, o64 = [], [], []
+    gpu, o32, rows = [], [], []
     for k, seed in enumerate(fx["seeds"]):
         md = _md(s, MaceLikeAdapter(device=device), maxwell_boltzmann_momenta(s.masses, 500.0, int(seed)), device)
         c0 = md.conserved_energy()
@@ -160,11 +206,16 @@ def test_mace_like_nhc_2000_steps_vs_oracle(device):
                 dev.append(float(np.abs(md.positions.cpu().numpy() - fx["positions_f64"][k, block + 1]).max()))
         print(f"[mace 2000] seed {seed}: max |dq| over 50 steps {max(dev):.2e} A", flush=True)
         assert max(dev) < 1e-4, dev
-        gpu.append(float(np.max(np.abs(np.array(series) - c0))))
-        o32.append(float(np.max(np.abs(fx["conserved_f32"][k] - fx["conserved_f32"][k, 0]))))
-        o64.append(float(np.max(np.abs(fx["conserved_f64"][k] - fx["conserved_f64"][k, 0]))))
-        print(f"[mace 2000] seed {seed}: drift gpu {gpu[-1]:.3e} eV, oracle f32 {o32[-1]:.3e} eV, "
-              f"oracle f64 {o64[-1]:.3e} eV", flush=True)
+        g = drift_stats(fx["steps"], series)
+        f32 = drift_stats(fx["steps"], fx["conserved_f32"][k])
+        f64 = drift_stats(fx["steps"], fx["conserved_f64"][k])
+        gpu.append(g[0])
+        o32.append(f32[0])
+        rows += [(int(seed), "gpu", *g), (int(seed), "oracle_f32", *f32), (int(seed), "oracle_f64", *f64)]
+        print(f"[mace 2000] seed {seed}: |b|T gpu {g[0]:.3e} eV, oracle f32 {f32[0]:.3e} eV, oracle f64 "
+              f"{f64[0]:.3e} eV; residual std gpu {g[1]:.3e}, oracle f32 {f32[1]:.3e}; excursion gpu "
+              f"{g[2]:.3e}, oracle f32 {f32[2]:.3e}", flush=True)
+    _record("mace_like_135_2000", rows)
     got, bound = _gate(gpu, o32)
     print(f"[mace 2000] mean gpu {got:.3e} eV <= bound {bound:.3e} eV", flush=True)
-    assert got <= bound, (gpu, o32, o64)
+    assert got <= bound, (gpu, o32)

