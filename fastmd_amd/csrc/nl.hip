@@ -17,6 +17,8 @@
 // per-neighbour constant offset of the shift, so the per-row order is preserved.
 #pragma clang fp contract(off)
 
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -756,6 +758,61 @@ __global__ void nl_window_flags_kernel(const int64_t* edge_count, const uint8_t*
   }
 }
 
+// The build's launches (small systems: one fused workgroup; otherwise count -> scan ->
+// materialize, with the count kernel's per-block partials in a.work).
+int launch_build(const BuildArgs& a, hipStream_t stream) {
+  FMD_REQUIRE(a.n > 0 && a.n < (int64_t(1) << 31) && a.e_cap > 0 && a.bmax > 0);
+  FMD_REQUIRE(a.positions && a.inv_cell && a.cell && a.nbr && a.shifts && a.num);
+  FMD_REQUIRE(a.ref_pos && a.ref_wraps && a.capacity_valid && a.work && a.frac && a.wrap_delta);
+  FMD_REQUIRE(a.edge_counts && a.edge_offsets && a.center && a.neighbor && a.images && a.distances);
+  FMD_REQUIRE(a.max_disp && a.cand_valid && a.overflow && a.isolated);
+  if (a.n <= kSmallMaxAtoms && a.n <= 1024) {
+    hipLaunchKernelGGL(nl_build_small_kernel, dim3(1), dim3(kSmallThreads), 0, stream, a);
+    FMD_CHECK_LAUNCH();
+    return FMD_OK;
+  }
+  const int64_t atom_blocks = fmd_cdiv(a.n, kBlock / FMD_WAVE);
+  hipLaunchKernelGGL(nl_count_kernel, dim3((unsigned)atom_blocks), dim3(kBlock), 0, stream, a);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(nl_scan_kernel, dim3(1), dim3(1024), 0, stream, a, atom_blocks);
+  FMD_CHECK_LAUNCH();
+  int64_t pad_blocks = fmd_cdiv(a.e_cap, (int64_t)kBlock * 4);
+  pad_blocks = pad_blocks < 1 ? 1 : (pad_blocks > 1024 ? 1024 : pad_blocks);
+  hipLaunchKernelGGL(nl_materialize_kernel, dim3((unsigned)(atom_blocks + pad_blocks)), dim3(kBlock), 0, stream, a,
+                     atom_blocks);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+// Scratch of fmd_nl_build_noalloc: the count kernel's per-block partials (max displacement,
+// isolated atoms) for up to FMD_NL_BUILD_NOALLOC_MAX_ATOMS atoms. Every block writes its own
+// slot before the scan kernel reads it, so nothing in it has to start at zero. Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in for the symbol): its
+// device address is looked up once per device and kept in scratch_ptr.
+static __device__ __align__(256) int64_t scratch[FMD_NL_BUILD_NOALLOC_SCRATCH];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_lock;
+int64_t* scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch` (hipGetSymbolAddress on the first call per device).
+int noalloc_scratch(int64_t** out) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return (int)err;
+  if (device < 0 || device >= kMaxDevices) return FMD_EUNSUPPORTED;
+  std::lock_guard<std::mutex> guard(scratch_lock);
+  if (scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return (int)err;
+    if (ptr == nullptr) return FMD_EUNSUPPORTED;
+    scratch_ptr[device] = static_cast<int64_t*>(ptr);
+  }
+  *out = scratch_ptr[device];
+  return FMD_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -822,31 +879,33 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
                  uint8_t* candidate_valid, uint8_t* overflow, int32_t* isolated, float line2, uint8_t* short_flags,
                  hipStream_t stream) {
-  FMD_REQUIRE(n_atoms > 0 && n_atoms < (int64_t(1) << 31) && e_cap > 0 && bmax > 0);
-  FMD_REQUIRE(positions && inv_cell && cell && neighbor_matrix && neighbor_shifts && num_neighbors);
-  FMD_REQUIRE(reference_positions && reference_wraps && capacity_valid && work && frac && wrap_delta);
-  FMD_REQUIRE(edge_counts && edge_offsets && center && neighbor && images && distances);
-  FMD_REQUIRE(max_displacement && candidate_valid && overflow && isolated);
+  FMD_REQUIRE(work);
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
               reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, pad_ix, pad_iy, pad_iz, e_cap,
               work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
               edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags};
-  if (n_atoms <= kSmallMaxAtoms && n_atoms <= 1024) {
-    hipLaunchKernelGGL(nl_build_small_kernel, dim3(1), dim3(kSmallThreads), 0, stream, a);
-    FMD_CHECK_LAUNCH();
-    return FMD_OK;
-  }
-  const int64_t atom_blocks = fmd_cdiv(n_atoms, kBlock / FMD_WAVE);
-  hipLaunchKernelGGL(nl_count_kernel, dim3((unsigned)atom_blocks), dim3(kBlock), 0, stream, a);
-  FMD_CHECK_LAUNCH();
-  hipLaunchKernelGGL(nl_scan_kernel, dim3(1), dim3(1024), 0, stream, a, atom_blocks);
-  FMD_CHECK_LAUNCH();
-  int64_t pad_blocks = fmd_cdiv(e_cap, (int64_t)kBlock * 4);
-  pad_blocks = pad_blocks < 1 ? 1 : (pad_blocks > 1024 ? 1024 : pad_blocks);
-  hipLaunchKernelGGL(nl_materialize_kernel, dim3((unsigned)(atom_blocks + pad_blocks)), dim3(kBlock), 0, stream, a,
-                     atom_blocks);
-  FMD_CHECK_LAUNCH();
-  return FMD_OK;
+  return launch_build(a, stream);
+}
+
+int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float* inv_cell, const float* cell,
+                         int64_t n_atoms, const int32_t* neighbor_matrix, const int32_t* neighbor_shifts,
+                         const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,
+                         const int32_t* reference_wraps, const uint8_t* capacity_valid, float rc2, float skin_limit,
+                         int32_t pad_ix, int32_t pad_iy, int32_t pad_iz, int64_t e_cap, float* frac,
+                         int32_t* wrap_delta, float* wrapped_out, int64_t* edge_counts, int64_t* edge_offsets,
+                         int32_t* center, int32_t* neighbor, int32_t* images, float* distances, int32_t* edge_index,
+                         float* edge_image, float* max_displacement, uint8_t* candidate_valid, uint8_t* overflow,
+                         int32_t* isolated, float line2, uint8_t* short_flags, hipStream_t stream) {
+  if (n_atoms > FMD_NL_BUILD_NOALLOC_MAX_ATOMS) return FMD_ETOOLARGE;
+  FMD_REQUIRE(n_atoms > 0 && fmd_nl_build_work_size(n_atoms) <= FMD_NL_BUILD_NOALLOC_SCRATCH);
+  int64_t* work = nullptr;
+  const int status = noalloc_scratch(&work);
+  if (status != FMD_OK) return status;
+  BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
+              reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, pad_ix, pad_iy, pad_iz, e_cap,
+              work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
+              edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags};
+  return launch_build(a, stream);
 }
 
 // padded rows of a bucket workspace: rows [e_real, e_cap) become far self-loops of atom

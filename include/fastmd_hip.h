@@ -32,6 +32,7 @@ extern "C" {
 #define FMD_OK 0
 #define FMD_EINVAL 10001      /* a size or pointer argument no launch could honour */
 #define FMD_EUNSUPPORTED 10002 /* a configuration this build does not implement */
+#define FMD_ETOOLARGE 10003   /* a size beyond an allocation-free entry point's static scratch */
 
 int fmd_abi_version(void);
 const char* fmd_error_string(int status);
@@ -103,6 +104,28 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  int32_t* images, float* distances, int32_t* edge_index, float* edge_image,
                  float* max_displacement, uint8_t* candidate_valid, uint8_t* overflow,
                  int32_t* isolated, float line2, uint8_t* short_flags, hipStream_t stream);
+
+/* Allocation-free variant of fmd_nl_build. It has no counterpart in the reference: it is for
+ * callers that cannot call hipMalloc (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation). Same arguments, kernels and results as fmd_nl_build,
+ * without `work`: the per-block partials go to a static device array of
+ * FMD_NL_BUILD_NOALLOC_SCRATCH int64 words (2 MiB) that each GPU the library runs on holds until
+ * the process ends. n_atoms above FMD_NL_BUILD_NOALLOC_MAX_ATOMS returns FMD_ETOOLARGE with
+ * nothing launched. Every call on one GPU shares that GPU's array, which keeps the last call's
+ * contents (nothing in it must start at zero: each block writes its slot before it is read),
+ * so calls that overlap on one GPU (unordered streams) race. */
+#define FMD_NL_BUILD_NOALLOC_MAX_ATOMS (1 << 20)
+#define FMD_NL_BUILD_NOALLOC_SCRATCH 262146 /* fmd_nl_build_work_size(FMD_NL_BUILD_NOALLOC_MAX_ATOMS) */
+int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float* inv_cell, const float* cell,
+                         int64_t n_atoms, const int32_t* neighbor_matrix, const int32_t* neighbor_shifts,
+                         const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,
+                         const int32_t* reference_wraps, const uint8_t* capacity_valid, float rc2,
+                         float skin_limit, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz, int64_t e_cap,
+                         float* frac, int32_t* wrap_delta, float* wrapped_out, int64_t* edge_counts,
+                         int64_t* edge_offsets, int32_t* center, int32_t* neighbor, int32_t* images,
+                         float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
+                         uint8_t* candidate_valid, uint8_t* overflow, int32_t* isolated, float line2,
+                         uint8_t* short_flags, hipStream_t stream);
 
 /* The three-body line graph over a build's rows (FixedCapacityGraphBuilder._materialize_pairs
  * / _materialize_line_graph / _line_graph_kernel, fixed_capacity_builder.py:2001-2161,680-753),
