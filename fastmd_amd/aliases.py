@@ -48,6 +48,8 @@ ALIASES = {
     "fastmd.execution.whole_step_cuda_graph": "fastmd_amd.execution.whole_step_cuda_graph",
     "fastmd.execution.cuda_graph": "fastmd_amd.execution.cuda_graph",
     "fastmd.execution.replica_batch": "fastmd_amd.execution.replica_batch",
+    "fastmd.execution.skin_topology": "fastmd_amd.execution.skin_topology",
+    "fastmd.applications.skin_topology": "fastmd_amd.execution.skin_topology",
     "fastmd.execution.gpu_logging": "fastmd_amd.execution.gpu_logging",
     "fastmd.execution.md_protocol": "fastmd_amd.execution.md_protocol",
     "fastmd.interfaces.gpu_md": "fastmd_amd.interfaces.gpu_md",

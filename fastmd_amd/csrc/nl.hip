@@ -306,6 +306,7 @@ struct BuildArgs {
   const uint8_t* capacity_valid;
   float rc2;
   float skin_limit;
+  int minimum_image;  // a lattice jump since the refresh is no motion (see atom_motion)
   int pad_ix, pad_iy, pad_iz;
   int64_t e_cap;
   int64_t* work;
@@ -327,6 +328,42 @@ struct BuildArgs {
   float line2;           // line-graph (bond) cutoff squared, float32
   uint8_t* short_flags;  // [e_cap]: real row with d2 < line2 (null: not written)
 };
+
+// Skin-test motion of atom i since the refresh and its wrap delta wd = wraps - reference_wraps
+// (fixed_capacity_builder.py:2219-2251). With minimum_image a lattice jump L since the refresh
+// (the caller wrapped the atom, e.g. ASE's atoms.wrap()) is no motion: the displacement
+// d = pos - ref loses jumps = rint(d inv) (small_matmul order, round half to even), d -= jumps
+// cell, and the jump leaves the wrap delta, so the candidates' images stay exact.
+__device__ __forceinline__ float atom_motion(const BuildArgs& a, int64_t i, float x, float y, float z,
+                                             const int w[3], const Mat3& inv, const Mat3& cm, int wd[3]) {
+  const float* ref = a.ref_pos + 3 * i;
+  float d[3] = {x - ref[0], y - ref[1], z - ref[2]};
+#pragma unroll
+  for (int k = 0; k < 3; ++k) wd[k] = w[k] - a.ref_wraps[3 * i + k];
+  if (a.minimum_image) {
+    float jump[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      float t = d[0] * inv.m[c];
+      t = t + d[1] * inv.m[3 + c];
+      t = t + d[2] * inv.m[6 + c];
+      jump[c] = rintf(t);
+    }
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      float t = jump[0] * cm.m[c];
+      t = t + jump[1] * cm.m[3 + c];
+      t = t + jump[2] * cm.m[6 + c];
+      d[c] = d[c] - t;
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) wd[k] -= (int)jump[k];
+  }
+  float sq = d[0] * d[0];
+  sq = sq + d[1] * d[1];
+  sq = sq + d[2] * d[2];
+  return sqrtf(sq);
+}
 
 // d2: the row's squared distance (the edge decision's own value: the short-bond decision uses the
 // same bits, fixed_capacity_builder.py:258-260)
@@ -397,16 +434,17 @@ __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs
     int w[3];
     load_position(a.positions, a.pos64, i, x, y, z);
     wrap_position(x, y, z, inv, cm, f, w, wr);
+    int wd[3];
+    const float moved = atom_motion(a, i, x, y, z, w, inv, cm, wd);
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-      const int wd = w[k] - a.ref_wraps[3 * i + k];
       a.frac[3 * i + k] = f[k];
-      a.wrap_delta[3 * i + k] = wd;
+      a.wrap_delta[3 * i + k] = wd[k];
       if (a.wrapped_out) a.wrapped_out[3 * i + k] = wr[k];
       s_pos[3 * i + k] = wr[k];
-      s_wd[3 * i + k] = wd;
+      s_wd[3 * i + k] = wd[k];
     }
-    dmax = nan_max(dmax, displacement_norm(x, y, z, a.ref_pos + 3 * i));
+    dmax = nan_max(dmax, moved);
   }
   dmax = wave_nan_max(dmax);
   if (lane == 0) s_red[wave] = dmax;
@@ -525,14 +563,12 @@ __global__ void __launch_bounds__(kBlock) nl_count_kernel(BuildArgs a) {
     int w[3], wdi[3];
     load_position(a.positions, a.pos64, i, x, y, z);
     wrap_position(x, y, z, inv, cm, f, w, wr);
-#pragma unroll
-    for (int k = 0; k < 3; ++k) wdi[k] = w[k] - a.ref_wraps[3 * i + k];
+    dmax = atom_motion(a, i, x, y, z, w, inv, cm, wdi);
     if (lane < 3) {
       a.frac[3 * i + lane] = f[lane];
       a.wrap_delta[3 * i + lane] = wdi[lane];
       if (a.wrapped_out) a.wrapped_out[3 * i + lane] = wr[lane];
     }
-    dmax = displacement_norm(x, y, z, a.ref_pos + 3 * i);
     auto nbr_state = [&](int32_t j, float& xj, float& yj, float& zj, int wdj[3]) {
       float px, py, pz, fj[3], wj[3];
       int ww[3];
@@ -541,9 +577,7 @@ __global__ void __launch_bounds__(kBlock) nl_count_kernel(BuildArgs a) {
       xj = wj[0];
       yj = wj[1];
       zj = wj[2];
-      wdj[0] = ww[0] - a.ref_wraps[3 * j];
-      wdj[1] = ww[1] - a.ref_wraps[3 * j + 1];
-      wdj[2] = ww[2] - a.ref_wraps[3 * j + 2];
+      atom_motion(a, j, px, py, pz, ww, inv, cm, wdj);  // the wrap delta kernel 1 publishes for j
     };
     int cnt = a.num[i];
     cnt = cnt < a.bmax ? cnt : a.bmax;
@@ -873,15 +907,16 @@ int64_t fmd_nl_build_work_size(int64_t n_atoms) {
 int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cell, const float* cell, int64_t n_atoms,
                  const int32_t* neighbor_matrix, const int32_t* neighbor_shifts, const int32_t* num_neighbors,
                  int32_t bmax, const float* reference_positions, const int32_t* reference_wraps,
-                 const uint8_t* capacity_valid, float rc2, float skin_limit, int32_t pad_ix, int32_t pad_iy,
-                 int32_t pad_iz, int64_t e_cap, int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
+                 const uint8_t* capacity_valid, float rc2, float skin_limit, int32_t minimum_image, int32_t pad_ix,
+                 int32_t pad_iy, int32_t pad_iz, int64_t e_cap, int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
                  int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor, int32_t* images,
                  float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
                  uint8_t* candidate_valid, uint8_t* overflow, int32_t* isolated, float line2, uint8_t* short_flags,
                  hipStream_t stream) {
   FMD_REQUIRE(work);
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
-              reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, pad_ix, pad_iy, pad_iz, e_cap,
+              reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, minimum_image, pad_ix, pad_iy, pad_iz,
+              e_cap,
               work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
               edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags};
   return launch_build(a, stream);
@@ -891,7 +926,8 @@ int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float*
                          int64_t n_atoms, const int32_t* neighbor_matrix, const int32_t* neighbor_shifts,
                          const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,
                          const int32_t* reference_wraps, const uint8_t* capacity_valid, float rc2, float skin_limit,
-                         int32_t pad_ix, int32_t pad_iy, int32_t pad_iz, int64_t e_cap, float* frac,
+                         int32_t minimum_image, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz, int64_t e_cap,
+                         float* frac,
                          int32_t* wrap_delta, float* wrapped_out, int64_t* edge_counts, int64_t* edge_offsets,
                          int32_t* center, int32_t* neighbor, int32_t* images, float* distances, int32_t* edge_index,
                          float* edge_image, float* max_displacement, uint8_t* candidate_valid, uint8_t* overflow,
@@ -902,7 +938,8 @@ int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float*
   const int status = noalloc_scratch(&work);
   if (status != FMD_OK) return status;
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
-              reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, pad_ix, pad_iy, pad_iz, e_cap,
+              reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, minimum_image, pad_ix, pad_iy, pad_iz,
+              e_cap,
               work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
               edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags};
   return launch_build(a, stream);

@@ -86,14 +86,21 @@ def _batch_itself(batch: GraphBatch) -> GraphBatch:
     return batch
 
 
+# Candidate-list state a ``candidates_from`` builder shares with its source
+# (fixed_capacity_builder.py:665-675): the cell list, the candidates and the refresh's reference.
+_CANDIDATE_STATE = ("_cell_count", "_cell_start", "_cell_atoms", "neighbor_matrix", "neighbor_shifts",
+                    "num_neighbors", "reference_positions", "reference_wraps", "wrap_delta", "_wraps",
+                    "_wrapped_refresh", "_candidate_capacity_valid")
+
+
 class FixedCapacityGraphBuilder:
     """Single-system fixed-capacity builder (see the module docstring): edges only, or with the
     three-body line graph when ``line_graph_cutoff`` and ``t_capacity`` are given (undirected
     pairs, short-bond lists and triplet rows, fmd_nl_line_graph, published as
     ``batch.pair_d2u`` / ``pair_u2d`` / ``triplets``).
 
-    Unsupported reference options (ghost rows, sink padding, shared candidates, minimum-image
-    wraps, float64 published positions) raise ``NotImplementedError``. ``sorted_edges=False`` is
+    Unsupported reference options (ghost rows, sink padding, float64 published positions) raise
+    ``NotImplementedError``. ``sorted_edges=False`` is
     accepted: the rows are always in the canonical order, which is also grouped by centre."""
 
     def __init__(self, *, cell: Tensor, atomic_numbers: Tensor, u_capacity: int, t_capacity: int = 0,
@@ -109,8 +116,8 @@ class FixedCapacityGraphBuilder:
             raise ValueError("a line-graph builder needs t_capacity > 0 and 0 < line_graph_cutoff <= the atom cutoff")
         if not line_graph and t_capacity != 0:
             raise ValueError("t_capacity needs a line_graph_cutoff")
-        if ghosts is not None or candidates_from is not None or minimum_image:
-            raise NotImplementedError("ghost rows, shared candidates and minimum-image wraps are not supported")
+        if ghosts is not None:
+            raise NotImplementedError("ghost rows are not supported")
         if positions_dtype != torch.float32:
             raise NotImplementedError("float64 published positions are not supported")
         padding = _FAR_SELF_LOOPS if padding is None else padding
@@ -158,25 +165,43 @@ class FixedCapacityGraphBuilder:
         self._skin_limit = float(np.float32(self.skin + 1.0e-6))
         self._pad_loop = self_loop_padding(padding, self.cell, self.atom_graph_cutoff)
         self._ncells, self._reach = cell_list_shape(self.cell.cpu().numpy(), self.candidate_cutoff)
+        # minimum_image: the caller may hand in coordinates wrapped by any lattice vector since the
+        # refresh (ASE's atoms.wrap()); the skin test and the wrap delta remove the jump
+        # (fixed_capacity_builder.py:1071-1074,2233-2245)
+        self.minimum_image = bool(minimum_image)
         n, dev = self.n_real, self.device
         i32 = dict(dtype=torch.int32, device=dev)
         f32 = dict(dtype=torch.float32, device=dev)
         i64 = dict(dtype=torch.int64, device=dev)
         u8 = dict(dtype=torch.uint8, device=dev)
-        ncell = self._ncells[0] * self._ncells[1] * self._ncells[2]
-        self._cell_count = torch.zeros(ncell, **i32)
-        self._cell_start = torch.zeros(ncell + 1, **i32)
-        self._cell_atoms = torch.zeros(n, **i32)
-        self.neighbor_matrix = torch.full((n, self.buffer_max), n, **i32)
-        self.neighbor_shifts = torch.zeros((n, self.buffer_max, 3), **i32)
-        self.num_neighbors = torch.zeros(n, **i32)
-        self.reference_positions = torch.zeros((n, 3), **f32)
-        self.reference_wraps = torch.zeros((n, 3), **i32)
-        self.wrap_delta = torch.zeros((n, 3), **i32)
-        self._wraps = torch.zeros((n, 3), **i32)
-        self._wrapped_refresh = torch.zeros((n, 3), **f32)
-        self._candidate_capacity_valid = torch.zeros(1, **u8)
-        self._candidate_initialized = False
+        # candidates_from: read (and refresh) another builder's candidate list of the same system,
+        # with capacities of its own (fixed_capacity_builder.py:1075-1078,1228-1239)
+        self._candidate_source = None
+        if candidates_from is not None:
+            source = candidates_from._candidate_owner
+            if (source.device != self.device or source.n_real != self.n_real
+                    or source.candidate_cutoff != self.candidate_cutoff or source.minimum_image != self.minimum_image
+                    or source.system_size != self.system_size or not torch.equal(source.cell, self.cell)):
+                raise ValueError("candidates_from must be a single-system builder of the same system, "
+                                 "cell, pbc, candidate cutoff and minimum_image setting")
+            self._candidate_source = source
+            for name in _CANDIDATE_STATE:
+                setattr(self, name, getattr(source, name))
+        else:
+            ncell = self._ncells[0] * self._ncells[1] * self._ncells[2]
+            self._cell_count = torch.zeros(ncell, **i32)
+            self._cell_start = torch.zeros(ncell + 1, **i32)
+            self._cell_atoms = torch.zeros(n, **i32)
+            self.neighbor_matrix = torch.full((n, self.buffer_max), n, **i32)
+            self.neighbor_shifts = torch.zeros((n, self.buffer_max, 3), **i32)
+            self.num_neighbors = torch.zeros(n, **i32)
+            self.reference_positions = torch.zeros((n, 3), **f32)
+            self.reference_wraps = torch.zeros((n, 3), **i32)
+            self.wrap_delta = torch.zeros((n, 3), **i32)
+            self._wraps = torch.zeros((n, 3), **i32)
+            self._wrapped_refresh = torch.zeros((n, 3), **f32)
+            self._candidate_capacity_valid = torch.zeros(1, **u8)
+            self._candidate_initialized = False
         self.frac_coords = torch.zeros((n, 3), **f32)
         self.edge_counts = torch.zeros(n, **i64)
         self.edge_offsets = torch.zeros(n + 1, **i64)
@@ -241,6 +266,11 @@ class FixedCapacityGraphBuilder:
         return LineGraph.from_builder(self)
 
     # ------------------------------------------------------------------ candidates
+    @property
+    def _candidate_owner(self) -> "FixedCapacityGraphBuilder":
+        """The builder whose candidate list this one reads (itself unless ``candidates_from``)."""
+        return self._candidate_source or self
+
     def _stream(self) -> int:
         return _abi.stream_handle(self.device)
 
@@ -262,7 +292,7 @@ class FixedCapacityGraphBuilder:
                   self._cell_start.data_ptr(), self._cell_atoms.data_ptr(), self.neighbor_matrix.data_ptr(),
                   self.neighbor_shifts.data_ptr(), self.num_neighbors.data_ptr(),
                   self._candidate_capacity_valid.data_ptr(), self.system_size, self._stream())
-        self._candidate_initialized = True
+        self._candidate_owner._candidate_initialized = True
 
     def assert_candidate_capacity(self) -> None:
         """Raise (host sync) if a candidate row was truncated (fixed_capacity_builder.py:1665-1672)."""
@@ -290,7 +320,7 @@ class FixedCapacityGraphBuilder:
         positions = self._positions_arg(positions)
         if rebuild_candidates:
             self.refresh_candidates(positions)
-        elif not self._candidate_initialized:
+        elif not self._candidate_owner._candidate_initialized:
             raise RuntimeError("refresh_candidates must run before candidate reuse")
         is64 = 1 if positions.dtype == torch.float64 else 0
         image = self._pad_loop[0]
@@ -298,7 +328,8 @@ class FixedCapacityGraphBuilder:
                   self.n_real, self.neighbor_matrix.data_ptr(), self.neighbor_shifts.data_ptr(),
                   self.num_neighbors.data_ptr(), self.buffer_max, self.reference_positions.data_ptr(),
                   self.reference_wraps.data_ptr(), self._candidate_capacity_valid.data_ptr(), self._rc2,
-                  self._skin_limit, image[0], image[1], image[2], self.e_capacity, self._work.data_ptr(),
+                  self._skin_limit, 1 if self.minimum_image else 0, image[0], image[1], image[2], self.e_capacity,
+                  self._work.data_ptr(),
                   self.frac_coords.data_ptr(), self.wrap_delta.data_ptr(), self.positions.data_ptr(),
                   self.edge_counts.data_ptr(), self.edge_offsets.data_ptr(), self.center.data_ptr(),
                   self.neighbor.data_ptr(), self.images.data_ptr(), self.distances.data_ptr(),

@@ -84,6 +84,9 @@ int fmd_nl_wrap(const void* positions, int32_t pos_is_f64, const float* inv_cell
  *   capacity_valid  uint8[1] from the refresh
  *   rc2             float32 square of the pair cutoff
  *   skin_limit      float32: the build is valid iff 2 * max displacement <= skin_limit
+ *   minimum_image   1: a lattice jump since the refresh (the caller wrapped an atom) is no
+ *                   motion: the skin test takes the minimum-image displacement and the jump
+ *                   leaves the wrap delta (fixed_capacity_builder.py:2233-2245); 0: plain
  *   pad_image       integer image of the padded self-loops
  *   work            int64 scratch of fmd_nl_build_work_size(n) elements
  * Outputs: frac [n,3] f32, wrap_delta [n,3] i32, wrapped_out [n,3] f32 (published
@@ -98,8 +101,8 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  int64_t n_atoms, const int32_t* neighbor_matrix, const int32_t* neighbor_shifts,
                  const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,
                  const int32_t* reference_wraps, const uint8_t* capacity_valid, float rc2,
-                 float skin_limit, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz, int64_t e_cap,
-                 int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
+                 float skin_limit, int32_t minimum_image, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz,
+                 int64_t e_cap, int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
                  int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor,
                  int32_t* images, float* distances, int32_t* edge_index, float* edge_image,
                  float* max_displacement, uint8_t* candidate_valid, uint8_t* overflow,
@@ -120,8 +123,8 @@ int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float*
                          int64_t n_atoms, const int32_t* neighbor_matrix, const int32_t* neighbor_shifts,
                          const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,
                          const int32_t* reference_wraps, const uint8_t* capacity_valid, float rc2,
-                         float skin_limit, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz, int64_t e_cap,
-                         float* frac, int32_t* wrap_delta, float* wrapped_out, int64_t* edge_counts,
+                         float skin_limit, int32_t minimum_image, int32_t pad_ix, int32_t pad_iy,
+                         int32_t pad_iz, int64_t e_cap, float* frac, int32_t* wrap_delta, float* wrapped_out, int64_t* edge_counts,
                          int64_t* edge_offsets, int32_t* center, int32_t* neighbor, int32_t* images,
                          float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
                          uint8_t* candidate_valid, uint8_t* overflow, int32_t* isolated, float line2,

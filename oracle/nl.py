@@ -185,14 +185,29 @@ class Build:
 
 
 def build(positions, inv_cell, cell, cand: Candidates, reference_positions, reference_wraps, rc2, skin_limit,
-          pad_image, e_cap: int, line2: float | None = None) -> Build:
+          pad_image, e_cap: int, line2: float | None = None, minimum_image: bool = False) -> Build:
     """One build over the candidate list (see module docstring); with ``line2`` (the float32
-    square of the bond cutoff) also the short-bond flag of every row."""
+    square of the bond cutoff) also the short-bond flag of every row. ``minimum_image``
+    (fixed_capacity_builder.py:2233-2245): a lattice jump since the refresh is no motion; the
+    displacement d loses jumps = round(d @ inv_cell) (float32, half to even) times the cell, and
+    the jumps leave the wrap delta."""
     pos = np.asarray(positions).astype(F32)
     n = pos.shape[0]
     frac, wraps, wrapped = wrap(pos, inv_cell, cell)
     wd = (wraps - np.asarray(reference_wraps, dtype=np.int32)).astype(np.int32)
     disp = pos - np.asarray(reference_positions, dtype=F32)
+    if minimum_image:
+        inv = np.asarray(inv_cell, dtype=F32)
+        c = np.asarray(cell, dtype=F32)
+        t = disp[:, 0:1] * inv[0]
+        t = t + disp[:, 1:2] * inv[1]
+        t = t + disp[:, 2:3] * inv[2]
+        jumps = np.rint(t).astype(F32)
+        m = jumps[:, 0:1] * c[0]
+        m = m + jumps[:, 1:2] * c[1]
+        m = m + jumps[:, 2:3] * c[2]
+        disp = (disp - m).astype(F32)
+        wd = (wd - jumps.astype(np.int32)).astype(np.int32)
     s = disp[:, 0] * disp[:, 0]
     s = s + disp[:, 1] * disp[:, 1]
     s = s + disp[:, 2] * disp[:, 2]

@@ -31,6 +31,7 @@ REFERENCE_NAMES = {
     "fastmd.execution.whole_step_cuda_graph": ("WholeStepGraphRunner", "FixedCapacityOverflow"),
     "fastmd.execution.cuda_graph": ("BucketedGraphRunner",),
     "fastmd.execution.replica_batch": ("ReplicaNoseHooverChainNVT",),
+    "fastmd.execution.skin_topology": ("SkinTopologyRunner", "SkinTopologyUnavailable", "PROACTIVE_REFRESH_FRACTION"),
     "fastmd.execution.gpu_logging": ("AsyncGPUMDLogger",),
     "fastmd.execution.md_protocol": ("MDOutputs", "ExtxyzTrajectory", "RestartData", "read_restart", "write_restart",
                                      "resume_mismatch"),

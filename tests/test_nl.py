@@ -35,7 +35,8 @@ def _inv32(cell):
     return np.linalg.inv(np.asarray(cell, dtype=F32).astype(np.float64)).astype(F32)
 
 
-def _oracle_build(cell, positions, cutoff, skin, e_cap, pad=None, ref_positions=None, inv=None):
+def _oracle_build(cell, positions, cutoff, skin, e_cap, pad=None, ref_positions=None, inv=None,
+                  minimum_image=False):
     cell32 = cell.astype(F32)
     inv = _inv32(cell) if inv is None else inv
     ref = positions if ref_positions is None else ref_positions
@@ -45,7 +46,7 @@ def _oracle_build(cell, positions, cutoff, skin, e_cap, pad=None, ref_positions=
     if pad is None:
         pad, _ = onl.self_loop_image(cell, cutoff)
     b = onl.build(positions, inv, cell32, cand, np.asarray(ref, dtype=F32), wraps, F32(cutoff * cutoff),
-                  F32(skin + 1e-6), pad, e_cap)
+                  F32(skin + 1e-6), pad, e_cap, minimum_image=minimum_image)
     return cand, b, wrapped
 
 
@@ -161,6 +162,48 @@ def test_reused_candidates_equal_fresh_build():
     assert not bad.candidate_valid and bad.overflow
 
 
+def _edge_keys(b, wraps):
+    """The build's rows as (centre, neighbour, image) in the frame of the caller's coordinates."""
+    e = b.n_edges
+    w = wraps.astype(np.int64)
+    img = b.images[:e].astype(np.int64) - w[b.neighbor[:e]] + w[b.center[:e]]
+    return {(int(i), int(j), *map(int, k)) for i, j, k in zip(b.center[:e], b.neighbor[:e], img)}
+
+
+def test_minimum_image_build_ignores_lattice_jumps():
+    """fixed_capacity_builder.py:2233-2245: with minimum_image, atoms the caller wrapped by lattice
+    vectors since the refresh (ASE's atoms.wrap()) keep the skin test valid and give the FP64
+    brute-force pair set of the unwrapped coordinates (rows within 1e-4 A of the cutoff aside),
+    on a sheared cell; the jumps leave the wrap delta. Without it the skin test fails."""
+    import md_oracle
+
+    s = systems.perovskite(3)
+    cell = s.cell + np.array([[0.0, 0.0, 0.0], [0.9, 0.0, 0.0], [0.4, -0.6, 0.0]])
+    positions = (s.positions @ np.linalg.inv(s.cell)) @ cell
+    rng = np.random.default_rng(11)
+    moved = positions + rng.normal(0, 0.15, positions.shape)
+    jumps = rng.integers(-2, 3, size=positions.shape)
+    jumps[::3] = 0
+    jumped = moved + jumps @ cell
+    inv = _inv32(cell)
+    cell32 = cell.astype(F32)
+    _, plain, _ = _oracle_build(cell, moved, 6.0, 2.0, 4000, ref_positions=positions)
+    _, mi, _ = _oracle_build(cell, jumped, 6.0, 2.0, 4000, ref_positions=positions, minimum_image=True)
+    _, bad, _ = _oracle_build(cell, jumped, 6.0, 2.0, 4000, ref_positions=positions)
+    assert plain.candidate_valid and mi.candidate_valid and not bad.candidate_valid and not mi.overflow
+    assert abs(float(mi.max_displacement) - float(plain.max_displacement)) < 1e-4
+    # the minimum-image wrap delta is the unjumped one's shifted by the wrap change minus the jump
+    _, w_moved, _ = onl.wrap(moved, inv, cell32)
+    _, w_jumped, _ = onl.wrap(jumped, inv, cell32)
+    assert np.array_equal(mi.wrap_delta, plain.wrap_delta + (w_jumped - w_moved) - jumps)
+    ours = _edge_keys(mi, w_jumped.astype(np.int64) - jumps)
+    ii, jj, img = md_oracle.PairList(cell).pairs(moved)
+    brute = {(int(i), int(j), *map(int, k)) for i, j, k in zip(ii, jj, img)}
+    assert len(brute) > 1500
+    vec = lambda t: moved[t[1]] + np.asarray(t[2:]) @ cell - moved[t[0]]  # noqa: E731
+    assert all(abs(np.linalg.norm(vec(t)) - 6.0) < 1e-4 for t in ours ^ brute)
+
+
 def test_window_fold():
     st = {"overflow": False, "capacity_overflow": False, "max_edges": 0, "max_isolated": 0}
     st = onl.window_fold(st, 10, False, False, 0, 32, True)
@@ -261,6 +304,71 @@ def test_builder_overflow_and_triclinic(device):
     cand, ob, _ = _oracle_build(cell, pos, 3.0, 1.0, 3000, inv=builder.inv_cell.cpu().numpy())
     torch.cuda.synchronize()
     _assert_build_equal(builder, ob, cand)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n_atoms", [135, 3430])
+def test_builder_minimum_image_bit_exact(device, n_atoms):
+    """minimum_image builds bit-exact vs the oracle on the single-workgroup and the multi-block
+    path, with atoms wrapped by lattice vectors since the refresh."""
+    import torch
+
+    from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
+
+    print(f"[nl minimum image] n_atoms={n_atoms}", flush=True)
+    s = systems.perovskite_atoms(n_atoms)
+    builder = FixedCapacityGraphBuilder(cell=torch.tensor(s.cell, dtype=torch.float32),
+                                        atomic_numbers=torch.ones(n_atoms), u_capacity=9 * n_atoms + 64,
+                                        atom_graph_cutoff=6.0, candidate_cutoff=8.0, minimum_image=True,
+                                        device=device)
+    builder.build(torch.tensor(s.positions, dtype=torch.float64, device=device), rebuild_candidates=True)
+    inv = builder.inv_cell.cpu().numpy()
+    cell32 = s.cell.astype(F32)
+    _, wraps, wrapped = onl.wrap(s.positions, inv, cell32)
+    cand = onl.candidates(wrapped, cell32, F32(64.0), builder.buffer_max)
+    rng = np.random.default_rng(n_atoms)
+    moved = s.positions + rng.normal(0, 0.15, s.positions.shape)
+    jumps = rng.integers(-1, 2, size=s.positions.shape)
+    jumps[::2] = 0
+    jumped = moved + jumps @ s.cell
+    builder.build(torch.tensor(jumped, device=device), rebuild_candidates=False)
+    ob = onl.build(jumped, inv, cell32, cand, s.positions.astype(F32), wraps, F32(36.0), F32(2.0 + 1e-6),
+                   onl.self_loop_image(s.cell, 6.0)[0], builder.e_capacity, minimum_image=True)
+    torch.cuda.synchronize()
+    _assert_build_equal(builder, ob)
+    assert ob.candidate_valid and not ob.overflow
+
+
+@pytest.mark.gpu
+def test_shared_candidates_follow_the_owner(device):
+    """candidates_from: a builder of a larger capacity reads (and refreshes) the owner's candidate
+    list; its builds equal the owner's bitwise."""
+    import torch
+
+    from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
+
+    s = systems.perovskite(6)
+    n = s.n_atoms
+    kw = dict(cell=torch.tensor(s.cell, dtype=torch.float32), atomic_numbers=torch.ones(n), atom_graph_cutoff=6.0,
+              candidate_cutoff=8.0, device=device)
+    owner = FixedCapacityGraphBuilder(u_capacity=9 * n, **kw)
+    follower = FixedCapacityGraphBuilder(u_capacity=9 * n + 512, candidates_from=owner, **kw)
+    assert follower.neighbor_matrix.data_ptr() == owner.neighbor_matrix.data_ptr()
+    with pytest.raises(RuntimeError, match="refresh_candidates"):
+        follower.build(torch.tensor(s.positions, device=device), rebuild_candidates=False)
+    rng = np.random.default_rng(3)
+    for step in range(3):
+        q = torch.tensor(s.positions + rng.normal(0, 0.1, s.positions.shape), device=device)
+        (owner if step == 0 else follower).build(q, rebuild_candidates=step != 1)
+        owner.build(q, rebuild_candidates=False)
+        follower.build(q, rebuild_candidates=False)
+        e = int(owner.edge_offsets[-1])
+        for name in ("edge_offsets", "frac_coords", "positions"):
+            assert torch.equal(getattr(owner, name), getattr(follower, name)), name
+        for name in ("center", "neighbor", "images", "distances"):
+            assert torch.equal(getattr(owner, name)[:e], getattr(follower, name)[:e]), name
+    with pytest.raises(ValueError, match="same system"):
+        FixedCapacityGraphBuilder(u_capacity=9 * n, candidates_from=owner, **dict(kw, candidate_cutoff=7.0))
 
 
 @pytest.mark.gpu
