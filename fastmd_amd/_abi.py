@@ -26,14 +26,14 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_abi_version": (ctypes.c_int, []),
     "fmd_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "fmd_nl_candidates": (ctypes.c_int, [_p, _p, _p, _i64, _f32, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _i64,
-                                         _p]),
+                                         _i64, _p]),
     "fmd_nl_wrap": (ctypes.c_int, [_p, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p]),
     "fmd_nl_build_work_size": (_i64, [_i64]),
     "fmd_nl_build": (ctypes.c_int, [_p, _i32, _p, _p, _i64, _p, _p, _p, _i32, _p, _p, _p, _f32, _f32, _i32,
-                                    _i32, _i32, _i32, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                                    _i32, _i32, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                     _p, _p, _p, _p, _p, _f32, _p, _p]),
     "fmd_nl_build_noalloc": (ctypes.c_int, [_p, _i32, _p, _p, _i64, _p, _p, _p, _i32, _p, _p, _p, _f32, _f32, _i32,
-                                            _i32, _i32, _i32, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                                            _i32, _i32, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                             _p, _p, _p, _p, _p, _f32, _p, _p]),
     "fmd_nl_line_graph_work_size": (_i64, [_i64, _i64]),
     "fmd_nl_line_graph": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _p,
@@ -83,7 +83,7 @@ SIGNATURES: dict[str, tuple] = {
                                           _i32, _p, _p]),
     "fmd_nhc_work_size": (_i64, [_i64]),
     "fmd_sum_f64": (ctypes.c_int, [_p, _i32, _i64, _p, _p]),
-    "fmd_edge_geometry_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _f32, _i32, _p, _p, _p, _p]),
+    "fmd_edge_geometry_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _f32, _i32, _p, _p, _p, _p]),
     "fmd_edge_geometry_bwd_f32": (ctypes.c_int, [_p, _p, _i32, _p, _i64, _p, _i64, _p, _p, _i64, _p, _p]),
     "fmd_mace_message_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _f32, _p, _p, _p]),
     "fmd_mace_message_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _p, _p, _f32,

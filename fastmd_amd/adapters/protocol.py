@@ -60,6 +60,28 @@ class PaddingRule:
 
 
 @dataclass
+class SystemSegments:
+    """Several systems in one batch (protocol.py:123-141; the field names are the reference's).
+    System s owns the rows [row_ptr[s], row_ptr[s + 1]) (its slot); its atoms are the first
+    ``atoms[s]`` of them (None: all), the rest are vacant rows with no candidate and no real edge.
+    No edge joins two systems. ``cells`` [count, 3, 3] float32 holds each system's cell (None: the
+    batch's one cell). All are persistent device buffers."""
+
+    count: int
+    row_ptr: Tensor  # [count + 1] int64
+    system_of_row: Tensor  # [rows] int32
+    cells: Tensor | None = None
+    atoms: Tensor | None = None
+
+
+def system_rows(batch) -> int | None:
+    """Device address of the batch's per-row system index (None for one system): the argument
+    the edge-geometry kernel takes to form each edge's image in its own system's cell."""
+    systems = getattr(batch, "systems", None)
+    return None if systems is None or systems.cells is None else systems.system_of_row.data_ptr()
+
+
+@dataclass
 class GraphBatch:
     """The graph a builder publishes: engine-owned persistent buffers (protocol.py:144-211).
 

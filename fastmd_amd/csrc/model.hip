@@ -35,9 +35,9 @@ __device__ __forceinline__ float sigmoid(float x) { return __builtin_amdgcn_rcpf
 // polynomial envelope 1 - 21 x^5 + 35 x^6 - 15 x^7 (x = r / rc < 1, else 0).
 // vec = (pos[j] + image @ cell) - pos[c], image @ cell formed row by row.
 // ------------------------------------------------------------------------------------------
-__global__ void edge_geometry_kernel(const float* pos, const float* cell, const int32_t* edge_index,
-                                     const float* edge_image, const int64_t* n_edges, int64_t e_cap, float rc, int nb,
-                                     float* geo, float* ef, float* def) {
+__global__ void edge_geometry_kernel(const float* pos, const float* cell, const int32_t* system_of,
+                                     const int32_t* edge_index, const float* edge_image, const int64_t* n_edges,
+                                     int64_t e_cap, float rc, int nb, float* geo, float* ef, float* def) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= e_cap) return;
   const int64_t rows = real_rows(n_edges, e_cap);
@@ -54,6 +54,7 @@ __global__ void edge_geometry_kernel(const float* pos, const float* cell, const 
   }
   const int32_t c = edge_index[2 * e], j = edge_index[2 * e + 1];
   const float ix = edge_image[3 * e], iy = edge_image[3 * e + 1], iz = edge_image[3 * e + 2];
+  if (system_of) cell += 9 * (int64_t)system_of[c];  // a union of systems: the centre's cell
   float v[3];
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
@@ -934,14 +935,14 @@ int launch_bwd_src(bool h1, dim3 grid, hipStream_t s, const float* z, const floa
 
 extern "C" {
 
-int fmd_edge_geometry_f32(const float* positions, const float* cell, const int32_t* edge_index,
-                          const float* edge_image, const int64_t* n_edges, int64_t e_cap, float rc, int32_t nb,
-                          float* geo, float* ef, float* def, hipStream_t stream) {
+int fmd_edge_geometry_f32(const float* positions, const float* cell, const int32_t* system_of,
+                          const int32_t* edge_index, const float* edge_image, const int64_t* n_edges, int64_t e_cap,
+                          float rc, int32_t nb, float* geo, float* ef, float* def, hipStream_t stream) {
   FMD_REQUIRE(positions && cell && edge_index && edge_image && n_edges && geo && ef && def);
   FMD_REQUIRE(e_cap >= 0 && nb > 0 && rc > 0.f);
   if (e_cap == 0) return FMD_OK;
   hipLaunchKernelGGL(edge_geometry_kernel, dim3((unsigned)fmd_cdiv(e_cap, 256)), dim3(256), 0, stream, positions,
-                     cell, edge_index, edge_image, n_edges, e_cap, rc, nb, geo, ef, def);
+                     cell, system_of, edge_index, edge_image, n_edges, e_cap, rc, nb, geo, ef, def);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -204,7 +204,7 @@ __global__ void __launch_bounds__(256) cells_query_kernel(const float* wrapped, 
                                                           const int32_t* cell_start, const int32_t* cell_atoms,
                                                           int32_t* neighbor_matrix, int32_t* neighbor_shifts,
                                                           int32_t* num_neighbors, uint8_t* capacity_valid,
-                                                          int64_t system_size) {
+                                                          int64_t system_size, int64_t index_offset) {
   extern __shared__ uint64_t keys[];
   __shared__ int counter;
   const int64_t i = blockIdx.x;
@@ -244,7 +244,9 @@ __global__ void __launch_bounds__(256) cells_query_kernel(const float* wrapped, 
   }
   __syncthreads();
   const int count = counter;
-  const int stored = count < lcap ? count : lcap;
+  // a row whose candidates overflowed the LDS keys holds an arrival-order subset of them: it is
+  // stored empty instead (deterministic; the row is flagged invalid below since lcap >= bmax)
+  const int stored = count <= lcap ? count : 0;
   int P = 1;
   while (P < stored) P <<= 1;
   for (int k = stored + t; k < P; k += blockDim.x) keys[k] = ~0ull;
@@ -268,11 +270,11 @@ __global__ void __launch_bounds__(256) cells_query_kernel(const float* wrapped, 
   int32_t* nrow = neighbor_matrix + i * bmax;
   int32_t* srow = neighbor_shifts + i * bmax * 3;
   for (int s = t; s < bmax; s += blockDim.x) {
-    int32_t j = (int32_t)n;
+    int32_t j = (int32_t)(n + index_offset);
     int sx = 0, sy = 0, sz = 0;
     if (s < stored) {
       const uint64_t key = keys[s];
-      j = (int32_t)(key >> 24);
+      j = (int32_t)((int64_t)(key >> 24) + index_offset);
       sx = (int)((key >> 16) & 0xff) - 128;
       sy = (int)((key >> 8) & 0xff) - 128;
       sz = (int)(key & 0xff) - 128;
@@ -308,6 +310,10 @@ struct BuildArgs {
   float skin_limit;
   int minimum_image;  // a lattice jump since the refresh is no motion (see atom_motion)
   int pad_ix, pad_iy, pad_iz;
+  // several systems in one union (null: one system): the system of each row; then inv_cell and
+  // cell are [systems, 9] tables and pad_images [systems, 3] the far self-loop image of each
+  const int32_t* system_of;
+  const int32_t* pad_images;
   int64_t e_cap;
   int64_t* work;
   float* frac;
@@ -328,6 +334,13 @@ struct BuildArgs {
   float line2;           // line-graph (bond) cutoff squared, float32
   uint8_t* short_flags;  // [e_cap]: real row with d2 < line2 (null: not written)
 };
+
+// The cell and inverse cell of atom i (its system's, in a union of systems).
+__device__ __forceinline__ void atom_frame(const BuildArgs& a, int64_t i, Mat3& inv, Mat3& cm) {
+  const int64_t base = a.system_of ? 9 * (int64_t)a.system_of[i] : 0;
+  inv = load_mat3(a.inv_cell + base);
+  cm = load_mat3(a.cell + base);
+}
 
 // Skin-test motion of atom i since the refresh and its wrap delta wd = wraps - reference_wraps
 // (fixed_capacity_builder.py:2219-2251). With minimum_image a lattice jump L since the refresh
@@ -409,7 +422,12 @@ __device__ __forceinline__ void pad_rows(const BuildArgs& a, int64_t total, int6
   const int64_t ec = total < a.e_cap ? total : a.e_cap;
   for (int64_t row = ec + start; row < a.e_cap; row += step) {
     const int32_t atom = (int32_t)((row - ec) % a.n);
-    write_row(a, row, atom, atom, a.pad_ix, a.pad_iy, a.pad_iz, 0.f, false);
+    if (a.system_of) {
+      const int32_t* im = a.pad_images + 3 * a.system_of[atom];
+      write_row(a, row, atom, atom, im[0], im[1], im[2], 0.f, false);
+    } else {
+      write_row(a, row, atom, atom, a.pad_ix, a.pad_iy, a.pad_iz, 0.f, false);
+    }
   }
 }
 
@@ -425,13 +443,14 @@ __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs
   const int t = threadIdx.x, T = blockDim.x;
   const int lane = t & (FMD_WAVE - 1), wave = t / FMD_WAVE, nwaves = T / FMD_WAVE;
   const int n = (int)a.n;
-  Mat3 inv = load_mat3(a.inv_cell), cm = load_mat3(a.cell);
 
   // (1) prologue
   float dmax = 0.f;
   for (int i = t; i < n; i += T) {
     float x, y, z, f[3], wr[3];
     int w[3];
+    Mat3 inv, cm;
+    atom_frame(a, i, inv, cm);
     load_position(a.positions, a.pos64, i, x, y, z);
     wrap_position(x, y, z, inv, cm, f, w, wr);
     int wd[3];
@@ -464,6 +483,8 @@ __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs
   for (int i = wave; i < n; i += nwaves) {
     const float xi = s_pos[3 * i], yi = s_pos[3 * i + 1], zi = s_pos[3 * i + 2];
     const int wdi[3] = {s_wd[3 * i], s_wd[3 * i + 1], s_wd[3 * i + 2]};
+    Mat3 inv, cm;
+    atom_frame(a, i, inv, cm);
     int cnt = a.num[i];
     cnt = cnt < a.bmax ? cnt : a.bmax;
     int total = 0;
@@ -527,6 +548,8 @@ __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs
   for (int i = wave; i < n; i += nwaves) {
     const float xi = s_pos[3 * i], yi = s_pos[3 * i + 1], zi = s_pos[3 * i + 2];
     const int wdi[3] = {s_wd[3 * i], s_wd[3 * i + 1], s_wd[3 * i + 2]};
+    Mat3 inv, cm;
+    atom_frame(a, i, inv, cm);
     int cnt = a.num[i];
     cnt = cnt < a.bmax ? cnt : a.bmax;
     int64_t row0 = s_cnt[i];
@@ -555,10 +578,11 @@ __global__ void __launch_bounds__(kBlock) nl_count_kernel(BuildArgs a) {
   __shared__ int32_t s_iso[kBlock / FMD_WAVE];
   const int lane = threadIdx.x & (FMD_WAVE - 1), wave = threadIdx.x / FMD_WAVE;
   const int64_t i = (int64_t)blockIdx.x * (kBlock / FMD_WAVE) + wave;
-  Mat3 inv = load_mat3(a.inv_cell), cm = load_mat3(a.cell);
   float dmax = 0.f;
   int iso = 0;
   if (i < a.n) {
+    Mat3 inv, cm;
+    atom_frame(a, i, inv, cm);  // atom i's system's; its neighbours are of the same system
     float x, y, z, f[3], wr[3];
     int w[3], wdi[3];
     load_position(a.positions, a.pos64, i, x, y, z);
@@ -682,9 +706,9 @@ __global__ void __launch_bounds__(kBlock) nl_materialize_kernel(BuildArgs a, int
   }
   const int64_t i = (int64_t)blockIdx.x * (kBlock / FMD_WAVE) + wave;
   if (i >= a.n) return;
-  Mat3 cm = load_mat3(a.cell);
+  Mat3 inv, cm;
+  atom_frame(a, i, inv, cm);
   // atom i's own wrapped position: recomputed (kernel 1 may not have published it)
-  Mat3 inv = load_mat3(a.inv_cell);
   float x, y, z, f[3], wr[3];
   int w[3];
   load_position(a.positions, a.pos64, i, x, y, z);
@@ -800,6 +824,7 @@ int launch_build(const BuildArgs& a, hipStream_t stream) {
   FMD_REQUIRE(a.ref_pos && a.ref_wraps && a.capacity_valid && a.work && a.frac && a.wrap_delta);
   FMD_REQUIRE(a.edge_counts && a.edge_offsets && a.center && a.neighbor && a.images && a.distances);
   FMD_REQUIRE(a.max_disp && a.cand_valid && a.overflow && a.isolated);
+  FMD_REQUIRE(!a.system_of || a.pad_images);
   if (a.n <= kSmallMaxAtoms && a.n <= 1024) {
     hipLaunchKernelGGL(nl_build_small_kernel, dim3(1), dim3(kSmallThreads), 0, stream, a);
     FMD_CHECK_LAUNCH();
@@ -867,8 +892,10 @@ int fmd_nl_wrap(const void* positions, int32_t pos_is_f64, const float* inv_cell
 int fmd_nl_candidates(const float* wrapped, const float* frac, const float* cell, int64_t n_atoms, float cutoff2,
                       const int32_t* ncells, const int32_t* reach, int32_t bmax, int32_t* cell_count,
                       int32_t* cell_start, int32_t* cell_atoms, int32_t* neighbor_matrix, int32_t* neighbor_shifts,
-                      int32_t* num_neighbors, uint8_t* capacity_valid, int64_t system_size, hipStream_t stream) {
+                      int32_t* num_neighbors, uint8_t* capacity_valid, int64_t system_size, int64_t index_offset,
+                      hipStream_t stream) {
   FMD_REQUIRE(n_atoms > 0 && bmax > 0 && ncells && reach);
+  FMD_REQUIRE(index_offset >= 0 && n_atoms + index_offset < (int64_t(1) << 31));
   FMD_REQUIRE(system_size >= 0 && (system_size == 0 || n_atoms % system_size == 0));
   const int n0 = ncells[0], n1 = ncells[1], n2 = ncells[2];
   const int r0 = reach[0], r1 = reach[1], r2 = reach[2];
@@ -894,7 +921,7 @@ int fmd_nl_candidates(const float* wrapped, const float* frac, const float* cell
   FMD_CHECK_LAUNCH();
   hipLaunchKernelGGL(cells_query_kernel, dim3((unsigned)n_atoms), dim3(256), (size_t)lcap * sizeof(uint64_t), stream,
                      wrapped, frac, cell, n_atoms, cutoff2, n0, n1, n2, r0, r1, r2, bmax, lcap, cell_start, cell_atoms,
-                     neighbor_matrix, neighbor_shifts, num_neighbors, capacity_valid, system_size);
+                     neighbor_matrix, neighbor_shifts, num_neighbors, capacity_valid, system_size, index_offset);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -908,7 +935,8 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  const int32_t* neighbor_matrix, const int32_t* neighbor_shifts, const int32_t* num_neighbors,
                  int32_t bmax, const float* reference_positions, const int32_t* reference_wraps,
                  const uint8_t* capacity_valid, float rc2, float skin_limit, int32_t minimum_image, int32_t pad_ix,
-                 int32_t pad_iy, int32_t pad_iz, int64_t e_cap, int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
+                 int32_t pad_iy, int32_t pad_iz, const int32_t* system_of, const int32_t* pad_images, int64_t e_cap,
+                 int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
                  int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor, int32_t* images,
                  float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
                  uint8_t* candidate_valid, uint8_t* overflow, int32_t* isolated, float line2, uint8_t* short_flags,
@@ -916,8 +944,7 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
   FMD_REQUIRE(work);
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
               reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, minimum_image, pad_ix, pad_iy, pad_iz,
-              e_cap,
-              work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
+              system_of, pad_images, e_cap, work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
               edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags};
   return launch_build(a, stream);
 }
@@ -926,8 +953,8 @@ int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float*
                          int64_t n_atoms, const int32_t* neighbor_matrix, const int32_t* neighbor_shifts,
                          const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,
                          const int32_t* reference_wraps, const uint8_t* capacity_valid, float rc2, float skin_limit,
-                         int32_t minimum_image, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz, int64_t e_cap,
-                         float* frac,
+                         int32_t minimum_image, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz,
+                         const int32_t* system_of, const int32_t* pad_images, int64_t e_cap, float* frac,
                          int32_t* wrap_delta, float* wrapped_out, int64_t* edge_counts, int64_t* edge_offsets,
                          int32_t* center, int32_t* neighbor, int32_t* images, float* distances, int32_t* edge_index,
                          float* edge_image, float* max_displacement, uint8_t* candidate_valid, uint8_t* overflow,
@@ -939,8 +966,7 @@ int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float*
   if (status != FMD_OK) return status;
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
               reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, minimum_image, pad_ix, pad_iy, pad_iz,
-              e_cap,
-              work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
+              system_of, pad_images, e_cap, work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
               edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags};
   return launch_build(a, stream);
 }

@@ -169,6 +169,10 @@ class FixedCapacityGraphBuilder:
         # refresh (ASE's atoms.wrap()); the skin test and the wrap delta remove the jump
         # (fixed_capacity_builder.py:1071-1074,2233-2245)
         self.minimum_image = bool(minimum_image)
+        # several systems in one union (the slot-union builder sets these): the system of each row
+        # and each system's far self-loop image; None for one system
+        self._system_of = None
+        self._pad_images = None
         n, dev = self.n_real, self.device
         i32 = dict(dtype=torch.int32, device=dev)
         f32 = dict(dtype=torch.float32, device=dev)
@@ -291,7 +295,7 @@ class FixedCapacityGraphBuilder:
                   _abi.array(_abi._i32, self._reach), self.buffer_max, self._cell_count.data_ptr(),
                   self._cell_start.data_ptr(), self._cell_atoms.data_ptr(), self.neighbor_matrix.data_ptr(),
                   self.neighbor_shifts.data_ptr(), self.num_neighbors.data_ptr(),
-                  self._candidate_capacity_valid.data_ptr(), self.system_size, self._stream())
+                  self._candidate_capacity_valid.data_ptr(), self.system_size, 0, self._stream())
         self._candidate_owner._candidate_initialized = True
 
     def assert_candidate_capacity(self) -> None:
@@ -328,8 +332,8 @@ class FixedCapacityGraphBuilder:
                   self.n_real, self.neighbor_matrix.data_ptr(), self.neighbor_shifts.data_ptr(),
                   self.num_neighbors.data_ptr(), self.buffer_max, self.reference_positions.data_ptr(),
                   self.reference_wraps.data_ptr(), self._candidate_capacity_valid.data_ptr(), self._rc2,
-                  self._skin_limit, 1 if self.minimum_image else 0, image[0], image[1], image[2], self.e_capacity,
-                  self._work.data_ptr(),
+                  self._skin_limit, 1 if self.minimum_image else 0, image[0], image[1], image[2],
+                  _abi.ptr(self._system_of), _abi.ptr(self._pad_images), self.e_capacity, self._work.data_ptr(),
                   self.frac_coords.data_ptr(), self.wrap_delta.data_ptr(), self.positions.data_ptr(),
                   self.edge_counts.data_ptr(), self.edge_offsets.data_ptr(), self.center.data_ptr(),
                   self.neighbor.data_ptr(), self.images.data_ptr(), self.distances.data_ptr(),

@@ -16,7 +16,7 @@ from torch import Tensor, nn
 from torch.autograd import Function
 
 from fastmd_amd import _abi
-from fastmd_amd.adapters.protocol import CapacityStep, GraphBatch, PaddingRule, TopologySpec
+from fastmd_amd.adapters.protocol import CapacityStep, GraphBatch, PaddingRule, TopologySpec, system_rows
 from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr
 
 
@@ -47,7 +47,8 @@ class _MorseEnergy(Function):
         ef = torch.empty(e_cap, 1, dtype=torch.float32, device=dev)
         de = torch.empty(e_cap, 1, dtype=torch.float32, device=dev)
         s = _abi.stream_handle()
-        _abi.call("fmd_edge_geometry_f32", positions.data_ptr(), cell.data_ptr(), batch.edge_index.data_ptr(),
+        _abi.call("fmd_edge_geometry_f32", positions.data_ptr(), cell.data_ptr(), system_rows(batch),
+                  batch.edge_index.data_ptr(),
                   batch.edge_image.data_ptr(), batch.n_edges.data_ptr(), e_cap, model.cutoff, 1, geo.data_ptr(),
                   ef.data_ptr(), de.data_ptr(), s)
         energy = torch.empty(n, dtype=torch.float32, device=dev)

@@ -41,7 +41,8 @@ from torch import Tensor, nn
 from torch.autograd import Function
 
 from fastmd_amd import _abi
-from fastmd_amd.adapters.protocol import CapacityStep, CaptureContract, GraphBatch, PaddingRule, TopologySpec
+from fastmd_amd.adapters.protocol import (CapacityStep, CaptureContract, GraphBatch, PaddingRule, TopologySpec,
+                                         system_rows)
 from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr
 from fastmd_amd.ops.threebody import LineGraph, fourier_line_vjp
 from fastmd_amd.ops.wide_gemm import gemm, gemm_gather, gemm_group
@@ -176,7 +177,8 @@ def _forward(ctx, positions: Tensor, cell: Tensor, model: ThreeBodyLike, inputs:
     geo = _empty(e_cap, 8, device=dev)
     ef = _empty(e_cap, nb, device=dev)
     de = _empty(e_cap, nb, device=dev)
-    _call("fmd_edge_geometry_f32", positions.data_ptr(), cell.data_ptr(), ei.data_ptr(), batch.edge_image.data_ptr(),
+    _call("fmd_edge_geometry_f32", positions.data_ptr(), cell.data_ptr(), system_rows(batch), ei.data_ptr(),
+          batch.edge_image.data_ptr(),
           n_edges.data_ptr(), e_cap, float(cfg.cutoff), nb, geo.data_ptr(), ef.data_ptr(), de.data_ptr())
     _call("fmd_tb_bond_envelope_f32", geo.data_ptr(), lg.short_flags.data_ptr(), n_edges.data_ptr(), e_cap,
           float(cfg.bond_cutoff))

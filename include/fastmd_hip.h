@@ -51,12 +51,16 @@ const char* fmd_error_string(int status);
  * Replaces nvalchemiops batch_build_cell_list/batch_query_cell_list as called at
  * fastmd/graph/fixed_capacity_builder.py:1519-1554 (FixedCapacityGraphBuilder._build_candidates).
  * system_size > 0: the atoms are replicas of one system, [k S, (k+1) S) each, and pairs across
- * replicas are not candidates (the union graph of replica batching, replica_batch.py:126-180). */
+ * replicas are not candidates (the union graph of replica batching, replica_batch.py:126-180).  * index_offset is added to every stored neighbour index (the pad value becomes
+ * n_atoms + index_offset): a union of systems searches each system on its own slice of rows and
+ * stores union indices. A row with more candidates than the LDS key buffer holds (at least
+ * bmax) is stored empty, so every row's content is deterministic; it is flagged invalid. */
 int fmd_nl_candidates(const float* wrapped, const float* frac, const float* cell, int64_t n_atoms,
                       float cutoff2, const int32_t* ncells, const int32_t* reach, int32_t bmax,
                       int32_t* cell_count, int32_t* cell_start, int32_t* cell_atoms,
                       int32_t* neighbor_matrix, int32_t* neighbor_shifts, int32_t* num_neighbors,
-                      uint8_t* capacity_valid, int64_t system_size, hipStream_t stream);
+                      uint8_t* capacity_valid, int64_t system_size, int64_t index_offset,
+                      hipStream_t stream);
 
 /* Wrap (refresh flavour): float32 positions -> fractional coordinates in [0,1), integer
  * wraps and wrapped Cartesian coordinates; optionally resets the reference positions/wraps
@@ -84,6 +88,10 @@ int fmd_nl_wrap(const void* positions, int32_t pos_is_f64, const float* inv_cell
  *   capacity_valid  uint8[1] from the refresh
  *   rc2             float32 square of the pair cutoff
  *   skin_limit      float32: the build is valid iff 2 * max displacement <= skin_limit
+ *   system_of       null for one system; for a union of systems (system_batch.py:177-444) the
+ *                   system of each row [n] i32: inv_cell and cell are then [systems, 3, 3]
+ *                   tables, each row wraps with its system's cell, and pad_images [systems, 3]
+ *                   i32 gives the far self-loop image of each system's padded rows (pad_i* unused)
  *   minimum_image   1: a lattice jump since the refresh (the caller wrapped an atom) is no
  *                   motion: the skin test takes the minimum-image displacement and the jump
  *                   leaves the wrap delta (fixed_capacity_builder.py:2233-2245); 0: plain
@@ -102,7 +110,7 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,
                  const int32_t* reference_wraps, const uint8_t* capacity_valid, float rc2,
                  float skin_limit, int32_t minimum_image, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz,
-                 int64_t e_cap, int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
+                 const int32_t* system_of, const int32_t* pad_images, int64_t e_cap, int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
                  int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor,
                  int32_t* images, float* distances, int32_t* edge_index, float* edge_image,
                  float* max_displacement, uint8_t* candidate_valid, uint8_t* overflow,
@@ -124,7 +132,8 @@ int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float*
                          const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,
                          const int32_t* reference_wraps, const uint8_t* capacity_valid, float rc2,
                          float skin_limit, int32_t minimum_image, int32_t pad_ix, int32_t pad_iy,
-                         int32_t pad_iz, int64_t e_cap, float* frac, int32_t* wrap_delta, float* wrapped_out, int64_t* edge_counts,
+                         int32_t pad_iz, const int32_t* system_of, const int32_t* pad_images, int64_t e_cap,
+                         float* frac, int32_t* wrap_delta, float* wrapped_out, int64_t* edge_counts,
                          int64_t* edge_offsets, int32_t* center, int32_t* neighbor, int32_t* images,
                          float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
                          uint8_t* candidate_valid, uint8_t* overflow, int32_t* isolated, float line2,
@@ -459,10 +468,11 @@ int fmd_sum_f64(const void* x, int32_t x_is_f64, int64_t n, double* out, hipStre
  * build's own MACE-like model, specified in fastmd_amd/models/mace_like.py.
  * -------------------------------------------------------------------------------------- */
 
-/* geo[e] = (u, r, fcut, dfcut, 0, 0) [E,8]; ef[e,n] = Bessel_n(r) fcut(r), def = d ef / dr [E,nb]. */
-int fmd_edge_geometry_f32(const float* positions, const float* cell, const int32_t* edge_index,
-                          const float* edge_image, const int64_t* n_edges, int64_t e_cap, float rc, int32_t nb,
-                          float* geo, float* ef, float* def, hipStream_t stream);
+/* geo[e] = (u, r, fcut, dfcut, 0, 0) [E,8]; ef[e,n] = Bessel_n(r) fcut(r), def = d ef / dr [E,nb].  * system_of (null: one cell): the system of each atom for a union of systems, cell then a
+ * [systems, 3, 3] table and each edge's image taken in its centre's cell. */
+int fmd_edge_geometry_f32(const float* positions, const float* cell, const int32_t* system_of,
+                          const int32_t* edge_index, const float* edge_image, const int64_t* n_edges, int64_t e_cap,
+                          float rc, int32_t nb, float* geo, float* ef, float* def, hipStream_t stream);
 /* gvec[e] = dE/dvec from dE/def (up to two sources, row strides ld0/ld1) and dE/d(u, fcut) (ggeo [E,4]). */
 int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, const float* gef0, int64_t ld0,
                               const float* gef1, int64_t ld1, const float* ggeo, const int64_t* n_edges,

@@ -31,7 +31,7 @@ def _noalloc_args(builder, positions, out, n_atoms=None):
             builder.neighbor_shifts.data_ptr(), builder.num_neighbors.data_ptr(), builder.buffer_max,
             builder.reference_positions.data_ptr(), builder.reference_wraps.data_ptr(),
             builder._candidate_capacity_valid.data_ptr(), builder._rc2, builder._skin_limit,
-            1 if builder.minimum_image else 0, image[0], image[1], image[2], builder.e_capacity, out["frac_coords"].data_ptr(), out["wrap_delta"].data_ptr(),
+            1 if builder.minimum_image else 0, image[0], image[1], image[2], None, None, builder.e_capacity, out["frac_coords"].data_ptr(), out["wrap_delta"].data_ptr(),
             out["positions"].data_ptr(), out["edge_counts"].data_ptr(), out["edge_offsets"].data_ptr(),
             out["center"].data_ptr(), out["neighbor"].data_ptr(), out["images"].data_ptr(),
             out["distances"].data_ptr(), out["edge_index"].data_ptr(), out["edge_image"].data_ptr(),
