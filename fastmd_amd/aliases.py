@@ -49,6 +49,8 @@ ALIASES = {
     "fastmd.execution.cuda_graph": "fastmd_amd.execution.cuda_graph",
     "fastmd.execution.replica_batch": "fastmd_amd.execution.replica_batch",
     "fastmd.execution.skin_topology": "fastmd_amd.execution.skin_topology",
+    "fastmd.execution.system_batch": "fastmd_amd.execution.system_batch",
+    "fastmd.interfaces.multi_system_md": "fastmd_amd.interfaces.multi_system_md",
     "fastmd.applications.skin_topology": "fastmd_amd.execution.skin_topology",
     "fastmd.execution.gpu_logging": "fastmd_amd.execution.gpu_logging",
     "fastmd.execution.md_protocol": "fastmd_amd.execution.md_protocol",

@@ -47,19 +47,31 @@ def sum_f64_into(x: Tensor) -> Tensor:
     return out
 
 
-def sum_f64_segments(x: Tensor, segments: int) -> Tensor:
-    """Per-segment ``sum_f64_into`` of ``segments`` equal contiguous slices ([segments] float64):
-    each slice summed in the order ``sum_f64`` sums a system of that size, so a replica's energy
+def _ranges(segments, rows: int) -> list:
+    """(start, count) row ranges of ``segments``: an int k (k equal contiguous slices of ``rows``,
+    replicas) or a sequence of (start, count) pairs (systems of a slot union: their occupied rows)."""
+    if isinstance(segments, int):
+        if rows % segments:
+            raise ValueError(f"{rows} rows do not split into {segments} equal segments")
+        n = rows // segments
+        return [(r * n, n) for r in range(segments)]
+    out = [(int(a), int(c)) for a, c in segments]
+    if any(a < 0 or c < 0 or a + c > rows for a, c in out):
+        raise ValueError(f"segment ranges {out} exceed {rows} rows")
+    return out
+
+
+def sum_f64_segments(x: Tensor, segments) -> Tensor:
+    """Per-segment ``sum_f64_into`` ([segments] float64) of ``segments`` (``_ranges``): each range
+    summed in the order ``sum_f64`` sums a system of that size, so a replica's or a system's energy
     is bitwise its single-system energy."""
-    if segments == 1:
+    if isinstance(segments, int) and segments == 1:
         return sum_f64_into(x)
     x = x.detach().contiguous().reshape(-1)
-    if x.numel() % segments:
-        raise ValueError(f"{x.numel()} rows do not split into {segments} equal segments")
-    n = x.numel() // segments
-    out = torch.empty(segments, dtype=torch.float64, device=x.device)
-    for r in range(segments):
-        _abi.call("fmd_sum_f64", x[r * n:(r + 1) * n].data_ptr(), 1 if x.dtype == torch.float64 else 0, n,
+    ranges = _ranges(segments, x.numel())
+    out = torch.empty(len(ranges), dtype=torch.float64, device=x.device)
+    for r, (a, c) in enumerate(ranges):
+        _abi.call("fmd_sum_f64", x[a:a + c].data_ptr(), 1 if x.dtype == torch.float64 else 0, c,
                   out[r:r + 1].data_ptr(), _abi.stream_handle())
     return out
 
@@ -90,9 +102,10 @@ class EnergyDerivative:
 
     def __init__(self, adapter: EnergyTap, segments: int = 1) -> None:
         self.adapter = adapter
-        # replica batching: the rows are this many copies of one system; "e" then holds one energy
-        # per copy (each bitwise its single-system energy), the forces are unchanged
-        self.segments = int(segments)
+        # replica batching: the rows are this many copies of one system; a slot union of systems:
+        # (start, count) ranges of their occupied rows. "e" then holds one energy per copy or system
+        # (each bitwise its single-system energy), the forces are unchanged
+        self.segments = segments if not isinstance(segments, int) else int(segments)
 
     def extensive_energy(self, energy: Tensor, atom_counts) -> Tensor:
         return energy
@@ -104,7 +117,7 @@ class EnergyDerivative:
         if explicit is not None and (n_real is None or n_real == batch.positions.shape[0]):
             # the adapter's explicit VJP: the same kernels as the autograd path below without the
             # autograd seed / cast / negation launches (one graph node each per step)
-            if self.segments == 1:
+            if isinstance(self.segments, int) and self.segments == 1:
                 energy, forces = explicit(inputs, batch.positions, batch.cell)
             else:
                 energy, forces = explicit(inputs, batch.positions, batch.cell, segments=self.segments)
@@ -113,11 +126,10 @@ class EnergyDerivative:
             leaf = batch.positions.detach().requires_grad_(True)
             energies = self.adapter.node_energy(inputs, leaf, batch.cell)
             rows = energies.shape[0] if n_real is None else n_real
-            if self.segments == 1:
+            if isinstance(self.segments, int) and self.segments == 1:
                 energy = sum_f64(energies[:rows])
                 (grad,) = torch.autograd.grad(energy, (leaf,))
                 return {"e": energy.detach().reshape(1), "f": [-grad]}
-            n = rows // self.segments
-            parts = torch.stack([sum_f64(energies[r * n:(r + 1) * n]) for r in range(self.segments)])
+            parts = torch.stack([sum_f64(energies[a:a + c]) for a, c in _ranges(self.segments, rows)])
             (grad,) = torch.autograd.grad(parts.sum(), (leaf,))
         return {"e": parts.detach(), "f": [-grad]}

@@ -87,7 +87,11 @@ class WholeStepGraphRunner:
         self.adapter = model
         self._derivative = engine_derivative(model)
         replicas = int(getattr(integrator, "replicas", 1))
-        if replicas > 1 and self._derivative is not None:
+        ranges = getattr(integrator, "energy_segments", None)
+        if ranges is not None and self._derivative is not None:
+            # a slot union of systems: one energy per system (its occupied rows)
+            self._derivative.segments = tuple(ranges)
+        elif replicas > 1 and self._derivative is not None:
             # a replica batch: one energy per replica for its integrator
             self._derivative.segments = replicas
         if self._derivative is None:

@@ -563,7 +563,7 @@ class MaceLikeAdapter:
         return _MaceLikeEnergy.apply(positions, cell, self.module, inputs)
 
     def energy_and_forces(self, inputs: MaceLikeInput, positions: Tensor, cell: Tensor,
-                          segments: int = 1) -> tuple[Tensor, Tensor]:
+                          segments=1) -> tuple[Tensor, Tensor]:
         """(E [1] float64 = the fixed-order sum of the node energies, F = -dE/dpos [rows, 3]) without
         autograd: the same forward and VJP kernels as ``node_energy`` + ``torch.autograd.grad``, minus
         the autograd seed, cast and negation kernels."""
@@ -571,5 +571,5 @@ class MaceLikeAdapter:
 
         saved = _Saved()
         energies = _MaceLikeEnergy.forward(saved, positions.detach(), cell.detach(), self.module, inputs)
-        energy = sum_f64_segments(energies, segments)  # one energy per replica (segments > 1)
+        energy = sum_f64_segments(energies, segments)  # one energy per replica or system
         return energy, _vjp(saved, None, -1.0)

@@ -353,11 +353,11 @@ class ThreeBodyAdapter:
         return _ThreeBodyEnergy.apply(positions, cell, self.module, inputs)
 
     def energy_and_forces(self, inputs: ThreeBodyInput, positions: Tensor, cell: Tensor,
-                          segments: int = 1) -> tuple[Tensor, Tensor]:
+                          segments=1) -> tuple[Tensor, Tensor]:
         """(E [1] float64, F = -dE/dpos [rows, 3]) by the forward and VJP kernels, without autograd."""
         from fastmd_amd.engine.energy_derivative import sum_f64_segments
 
         saved = _Saved()
         energies = _forward(saved, positions.detach(), cell.detach(), self.module, inputs)
-        energy = sum_f64_segments(energies, segments)  # one energy per replica (segments > 1)
+        energy = sum_f64_segments(energies, segments)  # one energy per replica or system
         return energy, _vjp(saved, None, -1.0)

@@ -32,6 +32,8 @@ REFERENCE_NAMES = {
     "fastmd.execution.cuda_graph": ("BucketedGraphRunner",),
     "fastmd.execution.replica_batch": ("ReplicaNoseHooverChainNVT",),
     "fastmd.execution.skin_topology": ("SkinTopologyRunner", "SkinTopologyUnavailable", "PROACTIVE_REFRESH_FRACTION"),
+    "fastmd.execution.system_batch": ("SlotLayout", "SlotUnionGraphBuilder", "SystemNoseHooverChainNVT"),
+    "fastmd.interfaces.multi_system_md": ("MultiSystemMolecularDynamics",),
     "fastmd.execution.gpu_logging": ("AsyncGPUMDLogger",),
     "fastmd.execution.md_protocol": ("MDOutputs", "ExtxyzTrajectory", "RestartData", "read_restart", "write_restart",
                                      "resume_mismatch"),
