@@ -51,4 +51,6 @@ class InferenceConfig:
 
     @property
     def resolved_execution(self) -> str:
+        """The mode a run starts in: "auto" starts whole-step; the driver falls back to eager
+        on an out-of-memory error in a whole-step capture (gpu_md.py:1720-1774)."""
         return "whole_step" if self.execution in (None, "auto") else self.execution

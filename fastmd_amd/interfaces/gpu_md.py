@@ -34,6 +34,14 @@ from fastmd_amd.graph.gpu_graph_builder import TensorGraphBuilder, raise_if_isol
 from fastmd_amd._roctx import roctx_ranged
 
 
+def _is_out_of_memory(error: BaseException) -> bool:
+    """A device allocation failure (torch's, or the HIP runtime's reported as a RuntimeError)."""
+    if isinstance(error, torch.OutOfMemoryError):
+        return True
+    text = str(error).lower()
+    return isinstance(error, RuntimeError) and ("out of memory" in text or "hiperroroutofmemory" in text)
+
+
 def _atoms_arrays(atoms):
     if hasattr(atoms, "get_positions"):
         positions = np.asarray(atoms.get_positions(), dtype=np.float64)
@@ -83,6 +91,10 @@ class GPUResidentMolecularDynamics:
             raise ValueError("GPUResidentMolecularDynamics: steps_per_launch must be a positive integer")
         self.config = config or InferenceConfig()
         self.execution = self.config.resolved_execution
+        # execution="auto": an out-of-memory error in a whole-step capture (construction or a
+        # capacity growth) continues on the eager path (gpu_md.py:1720-1774); the reason is kept
+        self.auto = self.config.execution in (None, "auto")
+        self.auto_reason = None
         self.device = torch.device(device)
         if self.device.index is None:
             self.device = torch.device("cuda", torch.cuda.current_device())
@@ -156,7 +168,12 @@ class GPUResidentMolecularDynamics:
         if self.logger.should_log(self.steps) and restart is None:
             self._log_current()
         if self.execution == "whole_step":
-            self.enable_whole_step_cuda_graph()
+            try:
+                self.enable_whole_step_cuda_graph()
+            except Exception as error:  # noqa: BLE001 (an out-of-memory error in auto mode only)
+                if not (self.auto and _is_out_of_memory(error)):
+                    raise
+                self._whole_step_to_eager(error)
 
     # ------------------------------------------------------------------ eager evaluation
     def evaluate(self, positions: Tensor | None = None) -> tuple[Tensor, Tensor]:
@@ -397,6 +414,28 @@ class GPUResidentMolecularDynamics:
         self.whole_step_capacity_history.append(self._capacity.u_capacity)
         self.whole_step_triplet_capacity_history.append(self._capacity.t_capacity)
 
+    def _whole_step_to_eager(self, error: BaseException) -> None:
+        """execution="auto": an out-of-memory error while capturing a whole-step window continues
+        on the eager path from the integrator's state, which the capture restored and a capacity
+        overflow rolled back to its window's start (gpu_md.py:1755-1774). The runner, its graph and
+        its pool are released."""
+        import gc
+        import warnings
+
+        runner = self.whole_step_runner
+        if runner is not None:
+            for key, value in runner.stats().items():
+                if key in _CUMULATIVE_STATS:
+                    self._retired_stats[key] = self._retired_stats.get(key, 0) + value
+        self.whole_step_runner = None
+        self._graph_pool = None
+        self.execution = "eager"
+        del runner
+        gc.collect()
+        torch.cuda.empty_cache()
+        self.auto_reason = f"whole_step ran out of GPU memory ({str(error).splitlines()[0][:160]}); eager"
+        warnings.warn(self.auto_reason, RuntimeWarning, stacklevel=3)
+
     def _grow(self, edge_count: int, triplet_count: int = 0) -> None:
         """A larger tier for a window's largest counts (a pair overflow truncates the triplets it
         counted: their tier grows again if the next window still overflows)."""
@@ -467,7 +506,16 @@ class GPUResidentMolecularDynamics:
                 try:
                     runner.settle(stats)
                 except FixedCapacityOverflow as overflow:
-                    self._grow_whole_step_runner(overflow.edge_count, overflow.triplet_count)
+                    try:
+                        self._grow_whole_step_runner(overflow.edge_count, overflow.triplet_count)
+                    except Exception as error:  # noqa: BLE001 (an out-of-memory error in auto mode only)
+                        if not (self.auto and _is_out_of_memory(error)):
+                            raise
+                        # the overflowed window was rolled back to its start: the rest eagerly
+                        self._whole_step_to_eager(error)
+                        for _ in range((windows - done) * self.steps_per_launch):
+                            self.step()
+                        return
                     continue
                 done += 1
                 self.steps += self.steps_per_launch

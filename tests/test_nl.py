@@ -372,6 +372,52 @@ def test_shared_candidates_follow_the_owner(device):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("spacing", [1.1, 1.0])
+def test_truncated_candidate_rows_are_deterministic(device, spacing):
+    """Rows with more candidates than slots (bmax 1 504 at 8 A): at 1.1 A spacing (~1 600 per atom)
+    the row keeps the sorted first bmax, bit-exact vs the oracle; at 1.0 A (~2 140, more than the
+    LDS key buffer of 2 048) it is stored empty. Either way repeated refreshes give the same rows,
+    the counts are the oracle's, the capacity flag is cleared and the builder raises
+    NeighborOverflowError."""
+    import torch
+
+    from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
+    from fastmd_amd.graph.neighbor_list_backend import NeighborOverflowError
+
+    side = 13 if spacing == 1.1 else 14
+    grid = np.stack(np.meshgrid(*(np.arange(side),) * 3, indexing="ij"), -1).reshape(-1, 3)
+    cell = np.eye(3) * side * spacing
+    rng = np.random.default_rng(side)
+    positions = (grid + 0.5) * spacing + rng.uniform(-0.02, 0.02, grid.shape)
+    n = positions.shape[0]
+    builder = FixedCapacityGraphBuilder(cell=torch.tensor(cell, dtype=torch.float32), atomic_numbers=torch.ones(n),
+                                        u_capacity=64, atom_graph_cutoff=6.0, candidate_cutoff=8.0, device=device)
+    bmax = builder.buffer_max
+    pos = torch.tensor(positions, dtype=torch.float64, device=device)
+    rows = []
+    for _ in range(3):
+        builder.refresh_candidates(pos)
+        rows.append((builder.neighbor_matrix.clone(), builder.neighbor_shifts.clone(), builder.num_neighbors.clone()))
+    for other in rows[1:]:
+        assert all(torch.equal(a, b) for a, b in zip(rows[0], other))
+    assert int(builder._candidate_capacity_valid.item()) == 0
+    with pytest.raises(NeighborOverflowError):
+        builder.assert_candidate_capacity()
+    cell32 = cell.astype(F32)
+    _, _, wrapped = onl.wrap(positions, builder.inv_cell.cpu().numpy(), cell32)
+    cand = onl.candidates(wrapped, cell32, F32(64.0), bmax)
+    num = rows[0][2].cpu().numpy()
+    assert np.array_equal(num, cand.num_neighbors)
+    nm = rows[0][0].cpu().numpy()
+    fits = num <= 2048
+    assert fits.all() if spacing == 1.1 else not fits.any()
+    assert (num > bmax).all()
+    assert np.array_equal(nm[fits], cand.neighbor_matrix[fits])
+    assert np.array_equal(rows[0][1].cpu().numpy()[fits], cand.neighbor_shifts[fits])
+    assert (nm[~fits] == n).all() and (rows[0][1].cpu().numpy()[~fits] == 0).all()
+
+
+@pytest.mark.gpu
 def test_window_flags_kernel(device):
     import torch
 

@@ -270,3 +270,51 @@ def test_oracle_morse_forces_match_the_torch_oracle():
         torch.tensor(b.images[:e]))
     assert abs(float(energy) - e_vec) < 1e-6
     assert np.abs(f.numpy() - f_vec).max() < 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("when", ["construction", "growth"])
+def test_auto_mode_falls_back_to_eager_on_out_of_memory(device, monkeypatch, when):
+    """execution="auto" (gpu_md.py:1720-1774): an out-of-memory error injected from the host into a
+    whole-step capture, at construction or at a capacity growth, continues the run on the eager
+    path from the settled state; the trajectory equals a pure eager run bitwise. The same error
+    in execution="whole_step" propagates."""
+    import torch
+
+    from fastmd_amd.execution import whole_step_cuda_graph as ws
+
+    real_capture = ws.WholeStepGraphRunner._capture
+    calls = {"capture": 0, "settle": 0}
+
+    def capture(self):
+        calls["capture"] += 1
+        if when == "construction" or calls["capture"] == 2:
+            raise torch.OutOfMemoryError("injected: HIP out of memory")
+        return real_capture(self)
+
+    real_settle = ws.WholeStepGraphRunner.settle
+
+    def settle(self, stats):
+        calls["settle"] += 1
+        if when == "growth" and calls["settle"] == 2:
+            # what an overflowed window's settle leaves: the window's start, then the overflow
+            self.integrator.restore()
+            raise ws.FixedCapacityOverflow(self.builder.e_capacity + 2, 0)
+        return real_settle(self, stats)
+
+    monkeypatch.setattr(ws.WholeStepGraphRunner, "_capture", capture)
+    monkeypatch.setattr(ws.WholeStepGraphRunner, "settle", settle)
+    with pytest.warns(RuntimeWarning, match="out of GPU memory"):
+        md = _md(_adapter("morse", device), "auto", device, steps_per_launch=5)
+        md.launch_behind = False
+        md.run(30)
+    assert md.execution == "eager" and md.whole_step_runner is None and md.steps == 30
+    eager = _md(_adapter("morse", device), "eager", device)
+    eager.run(30)
+    torch.cuda.synchronize()
+    assert torch.equal(_state(md), _state(eager))
+    calls.update(capture=0, settle=0)
+    with pytest.raises(torch.OutOfMemoryError):
+        strict = _md(_adapter("morse", device), "whole_step", device, steps_per_launch=5)
+        strict.launch_behind = False
+        strict.run(30)
