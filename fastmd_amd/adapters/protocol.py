@@ -117,6 +117,9 @@ class GraphBatch:
     edge_offsets: Tensor | None = None
     edge_reverse: Tensor | None = None
     line: Any = None  # the line graph's arrays (fastmd_amd.ops.threebody.LineGraph) when built
+    # a permutation of the atom rows in a spatial (Morton) order, refreshed with the candidates:
+    # kernels that take one atom per wave visit them in this order (same results, L2 locality)
+    atom_order: Tensor | None = None
 
     @property
     def edge_dst(self) -> Tensor:

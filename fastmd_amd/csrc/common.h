@@ -21,6 +21,17 @@
 
 __host__ __device__ static inline int64_t fmd_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// XCD-aware block order: the hardware hands workgroups to the 8 XCDs round-robin (workgroup w to
+// XCD w % 8), and each XCD has its own L2. The logical block of workgroup w of g is chosen so
+// that every XCD walks one contiguous run of logical blocks (a bijection of [0, g)): blocks that
+// read the same rows (neighbouring atoms, the tiles of one GEMM row) then share an L2.
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int64_t fmd_xcd_block(int64_t w, int64_t g) {
+  const int64_t xcd = w % kXcds, slot = w / kXcds, q = g / kXcds, r = g % kXcds;
+  return xcd * q + (xcd < r ? xcd : r) + slot;
+}
+
 // gfx950 cross-lane moves that bypass the LDS crossbar: v_permlane32_swap / v_permlane16_swap
 // trade the upper half of every 64 / 32 lanes of one register with the lower half of another, and
 // DPP reads a partner lane inside a row of 16 as an operand of the consuming instruction.

@@ -277,12 +277,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_group_kernel(const GemmGrou
 //  * interior wave tiles without bias/accumulate/activation store straight from the
 //    accumulators with incremental row pointers; the general epilogue handles the rest.
 constexpr int NT_PITCH = 36;
-constexpr int kXcds = 8;
-
-__device__ __forceinline__ int64_t xcd_tile(int64_t w, int64_t g) {
-  const int64_t xcd = w % kXcds, slot = w / kXcds, q = g / kXcds, r = g % kXcds;
-  return xcd * q + (xcd < r ? xcd : r) + slot;
-}
+__device__ __forceinline__ int64_t xcd_tile(int64_t w, int64_t g) { return fmd_xcd_block(w, g); }
 
 constexpr int NT_V = 128 * BK32 / 4 / kThreads;  // float4 per thread per operand and slice (4)
 

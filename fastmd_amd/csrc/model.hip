@@ -234,14 +234,15 @@ template <int CPL64, bool H1>
 __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const float* zq, const float* geo,
                                                            const int32_t* edge_index, const int64_t* off,
                                                            const int64_t* n_edges, int64_t e_cap, int64_t n,
-                                                           const float* h0, const float* h1, float inv_avg, float* A0,
-                                                           float* A1) {
+                                                           const int32_t* order, const float* h0, const float* h1,
+                                                           float inv_avg, float* A0, float* A1) {
   constexpr int CPL = 2 * CPL64, C = 32 * CPL;
   constexpr int NZ = H1 ? 4 : 2;  // z blocks in a row
   const int lane = threadIdx.x & 63;
   const bool upper = lane >= 32;
-  const int64_t i = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-  if (i >= n) return;
+  const int64_t il = fmd_xcd_block(blockIdx.x, gridDim.x) * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  if (il >= n) return;
+  const int64_t i = order ? order[il] : il;  // the atom of this wave (a spatial order keeps gathers in L2)
   int64_t lo;
   const int64_t hi = wave_rows(off, n_edges, e_cap, i, lo);
   const int c0 = (lane & 31) * CPL;
@@ -349,9 +350,9 @@ constexpr int kMaxBasis = 16;
 template <int CPL64, bool H1, int RB>
 __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     const float* z, const float* zq, const float* geo, const int32_t* edge_index, const int64_t* off,
-    const int64_t* n_edges, int64_t e_cap, int64_t n, const float* h0, const float* h1, const float* gA0,
-    const float* gA1, float inv_avg, float* gz, float* gzsum, float* ggeo, int accumulate_geo, const float* w1ef,
-    int nb, float* gef) {
+    const int64_t* n_edges, int64_t e_cap, int64_t n, const int32_t* order, const float* h0, const float* h1,
+    const float* gA0, const float* gA1, float inv_avg, float* gz, float* gzsum, float* ggeo, int accumulate_geo,
+    const float* w1ef, int nb, float* gef) {
   constexpr int CPL = 2 * CPL64, C = 32 * CPL;
   constexpr int NZ = H1 ? 4 : 2;
   constexpr int kPairs = H1 ? 1 : 2;  // row pairs per load group (registers: three waves per SIMD)
@@ -363,8 +364,9 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
   const int nbv = w1ef ? nb : 0;
   for (int k = threadIdx.x; k < RB * 4 * C; k += blockDim.x) s_w[k] = k < nbv * 4 * C ? w1ef[k] : 0.f;
   __syncthreads();
-  const int64_t i = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-  if (i >= n) return;
+  const int64_t il = fmd_xcd_block(blockIdx.x, gridDim.x) * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  if (il >= n) return;
+  const int64_t i = order ? order[il] : il;  // the atom of this wave (a spatial order keeps gathers in L2)
   int64_t lo;
   const int64_t hi = wave_rows(off, n_edges, e_cap, i, lo);
   const int c0 = (lane & 31) * CPL;
@@ -553,15 +555,17 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
 template <int CPL64, bool H1>
 __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
     const float* z, const float* zq, const float* geo, const int32_t* edge_index, const int32_t* reverse,
-    const int64_t* off, const int64_t* n_edges, int64_t e_cap, int64_t n, const float* h0, const float* h1,
-    const float* gA0, const float* gA1, float inv_avg, float* gh0, float* gh1, int accumulate, float* gzsum_src) {
+    const int64_t* off, const int64_t* n_edges, int64_t e_cap, int64_t n, const int32_t* order, const float* h0,
+    const float* h1, const float* gA0, const float* gA1, float inv_avg, float* gh0, float* gh1, int accumulate,
+    float* gzsum_src) {
   constexpr int CPL = 2 * CPL64, C = 32 * CPL;
   constexpr int NZ = H1 ? 4 : 2;
   constexpr int kPairs = H1 ? 1 : 2;  // row pairs per load group (registers: three waves per SIMD)
   const int lane = threadIdx.x & 63;
   const bool upper = lane >= 32;
-  const int64_t jn = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-  if (jn >= n) return;
+  const int64_t jl = fmd_xcd_block(blockIdx.x, gridDim.x) * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  if (jl >= n) return;
+  const int64_t jn = order ? order[jl] : jl;  // the atom of this wave (a spatial order keeps gathers in L2)
   int64_t lo;
   const int64_t hi = wave_rows(off, n_edges, e_cap, jn, lo);
   const int c0 = (lane & 31) * CPL;
@@ -859,14 +863,14 @@ __global__ void morse_bwd_kernel(const float* geo, const float* dvdr, const int3
 template <int CPL>
 int launch_message(bool h1, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
                    const int32_t* ei,
-                   const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const float* h0,
-                   const float* h1p, float inv_avg, float* A0, float* A1) {
+                   const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const int32_t* order,
+                   const float* h0, const float* h1p, float inv_avg, float* A0, float* A1) {
   if (h1)
-    hipLaunchKernelGGL((message_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, off, ne, e_cap, n, h0,
-                       h1p, inv_avg, A0, A1);
+    hipLaunchKernelGGL((message_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, off, ne, e_cap, n,
+                       order, h0, h1p, inv_avg, A0, A1);
   else
     hipLaunchKernelGGL((message_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, off, ne, e_cap, n,
-                       h0, h1p, inv_avg, A0, A1);
+                       order, h0, h1p, inv_avg, A0, A1);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -896,14 +900,14 @@ namespace {
 template <int CPL>
 int launch_bwd_edge(bool h1, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
                     const int32_t* ei,
-                    const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const float* h0,
-                    const float* h1p, const float* gA0, const float* gA1, float inv_avg, float* gz, float* gzsum,
-                    float* ggeo, int acc, const float* w1ef, int nb, float* gef) {
+                    const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const int32_t* order,
+                    const float* h0, const float* h1p, const float* gA0, const float* gA1, float inv_avg, float* gz,
+                    float* gzsum, float* ggeo, int acc, const float* w1ef, int nb, float* gef) {
   const bool wide = w1ef && nb > 8;  // radial rows padded to 16 instead of 8
   const size_t lds = (size_t)(wide ? 16 : 8) * 4 * 64 * CPL * sizeof(float);  // RB x 4C floats
 #define FMD_BWD_EDGE(H, RB)                                                                                         \
   hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, H, RB>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne,  \
-                     e_cap, n, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef)
+                     e_cap, n, order, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef)
   if (h1 && wide)
     FMD_BWD_EDGE(true, 16);
   else if (h1)
@@ -920,14 +924,14 @@ int launch_bwd_edge(bool h1, dim3 grid, hipStream_t s, const float* z, const flo
 template <int CPL>
 int launch_bwd_src(bool h1, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
                    const int32_t* ei, const int32_t* rev, const int64_t* off, const int64_t* ne, int64_t e_cap,
-                   int64_t n, const float* h0, const float* h1p, const float* gA0, const float* gA1, float inv_avg,
-                   float* gh0, float* gh1, int acc, float* gzsum_src) {
+                   int64_t n, const int32_t* order, const float* h0, const float* h1p, const float* gA0,
+                   const float* gA1, float inv_avg, float* gh0, float* gh1, int acc, float* gzsum_src) {
   if (h1)
     hipLaunchKernelGGL((message_bwd_src_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, rev, off, ne,
-                       e_cap, n, h0, h1p, gA0, gA1, inv_avg, gh0, gh1, acc, gzsum_src);
+                       e_cap, n, order, h0, h1p, gA0, gA1, inv_avg, gh0, gh1, acc, gzsum_src);
   else
     hipLaunchKernelGGL((message_bwd_src_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, rev, off, ne,
-                       e_cap, n, h0, h1p, gA0, gA1, inv_avg, gh0, gh1, acc, gzsum_src);
+                       e_cap, n, order, h0, h1p, gA0, gA1, inv_avg, gh0, gh1, acc, gzsum_src);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -960,20 +964,21 @@ int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, co
 
 int fmd_mace_message_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
                          const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
-                         int32_t channels, const float* h0, const float* h1, float inv_avg, float* A0, float* A1,
-                         hipStream_t stream) {
+                         const int32_t* order, int32_t channels, const float* h0, const float* h1, float inv_avg,
+                         float* A0, float* A1, hipStream_t stream) {
   FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && A0 && A1 && n_atoms >= 0);
   FMD_REQUIRE(aligned_to(channel_alignment(channels), {z, zq, h0, h1, A0, A1}) && aligned_to(16, {geo}));
   if (n_atoms == 0) return FMD_OK;
   dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
   FMD_CPL_DISPATCH(channels, launch_message, h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets,
-                   n_edges, e_cap, n_atoms, h0, h1, inv_avg, A0, A1);
+                   n_edges, e_cap, n_atoms, order, h0, h1, inv_avg, A0, A1);
 }
 
 int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
                              const int32_t* reverse,
                              const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
-                             int32_t channels, const float* h0, const float* h1, const float* gA0, const float* gA1,
+                             const int32_t* order, int32_t channels, const float* h0, const float* h1,
+                             const float* gA0, const float* gA1,
                              float inv_avg, float* gz, float* gzsum, float* gzsum_src, float* ggeo,
                              int32_t accumulate_geo, float* gh0, float* gh1, int32_t accumulate_h, const float* w1ef,
                              int32_t nb, float* gef, hipStream_t stream) {
@@ -988,21 +993,21 @@ int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, 
   int rc = FMD_OK;
   switch (channels / 64) {
     case 1: rc = launch_bwd_edge<1>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges, e_cap,
-                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
+                                    n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
     case 2: rc = launch_bwd_edge<2>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges, e_cap,
-                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
+                                    n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
     case 4: rc = launch_bwd_edge<4>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges, e_cap,
-                                    n_atoms, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
+                                    n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
     default: return FMD_EUNSUPPORTED;
   }
   if (rc != FMD_OK || !(gh0 || gzsum_src)) return rc;
   switch (channels / 64) {
     case 1: return launch_bwd_src<1>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets, n_edges,
-                                     e_cap, n_atoms, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h, gzsum_src);
+                                     e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h, gzsum_src);
     case 2: return launch_bwd_src<2>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets, n_edges,
-                                     e_cap, n_atoms, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h, gzsum_src);
+                                     e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h, gzsum_src);
     case 4: return launch_bwd_src<4>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets, n_edges,
-                                     e_cap, n_atoms, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h, gzsum_src);
+                                     e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h, gzsum_src);
     default: return FMD_EUNSUPPORTED;
   }
 }

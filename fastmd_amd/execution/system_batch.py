@@ -42,7 +42,7 @@ from fastmd_amd.engine.capacity_policy import JointCapacityPolicy, held_demand, 
 from fastmd_amd.execution.cuda_graph import triplet_demand
 from fastmd_amd.execution.gpu_nhc import GPUNoseHooverChainNVT, NHCState, maxwell_boltzmann_momenta
 from fastmd_amd.execution.whole_step_cuda_graph import FixedCapacityOverflow, WholeStepGraphRunner
-from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder, self_loop_padding
+from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder, morton_order, self_loop_padding
 from fastmd_amd.graph.gpu_graph_builder import TensorGraphBuilder
 from fastmd_amd.graph.neighbor_list_backend import cell_list_shape
 
@@ -171,6 +171,7 @@ class SlotUnionGraphBuilder(FixedCapacityGraphBuilder):
                       self._slice_ptr(self.num_neighbors, start, 1), self._sys_valid[s:s + 1].data_ptr(), 0, start,
                       stream)
         torch.amin(self._sys_valid, dim=0, keepdim=True, out=self._candidate_capacity_valid)
+        self.atom_order.copy_(morton_order(self.frac_coords, self._system_of))
         self._candidate_owner._candidate_initialized = True
 
 

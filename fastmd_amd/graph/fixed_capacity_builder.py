@@ -90,7 +90,26 @@ def _batch_itself(batch: GraphBatch) -> GraphBatch:
 # (fixed_capacity_builder.py:665-675): the cell list, the candidates and the refresh's reference.
 _CANDIDATE_STATE = ("_cell_count", "_cell_start", "_cell_atoms", "neighbor_matrix", "neighbor_shifts",
                     "num_neighbors", "reference_positions", "reference_wraps", "wrap_delta", "_wraps",
-                    "_wrapped_refresh", "_candidate_capacity_valid")
+                    "_wrapped_refresh", "_candidate_capacity_valid", "atom_order")
+
+
+def morton_order(frac: Tensor, system_of: Tensor | None = None) -> Tensor:
+    """The atoms sorted along a Morton (Z-order) curve of their fractional coordinates (10 bits per
+    axis; a union's system index above them), int32 on the device, without a host sync: atoms
+    near in the order are near in space, so kernels that take one atom per wave in this order
+    gather their neighbours' rows from the same L2."""
+    q = (frac.clamp(0.0, 1.0 - 1e-7) * 1024.0).to(torch.int64)
+
+    def spread(v: Tensor) -> Tensor:  # the 10 bits of v at every third position
+        v = (v | (v << 16)) & 0x030000FF
+        v = (v | (v << 8)) & 0x0300F00F
+        v = (v | (v << 4)) & 0x030C30C3
+        return (v | (v << 2)) & 0x09249249
+
+    code = spread(q[:, 0]) | (spread(q[:, 1]) << 1) | (spread(q[:, 2]) << 2)
+    if system_of is not None:
+        code = code | (system_of.to(torch.int64) << 30)
+    return torch.argsort(code, stable=True).to(torch.int32)
 
 
 class FixedCapacityGraphBuilder:
@@ -206,6 +225,7 @@ class FixedCapacityGraphBuilder:
             self._wrapped_refresh = torch.zeros((n, 3), **f32)
             self._candidate_capacity_valid = torch.zeros(1, **u8)
             self._candidate_initialized = False
+            self.atom_order = torch.arange(n, **i32)
         self.frac_coords = torch.zeros((n, 3), **f32)
         self.edge_counts = torch.zeros(n, **i64)
         self.edge_offsets = torch.zeros(n + 1, **i64)
@@ -259,6 +279,7 @@ class FixedCapacityGraphBuilder:
             pair_u2d=self.undirected2directed,
             triplets=self.line_graph,
             line=self._line_layout(),
+            atom_order=self.atom_order,
         )
         self.graph = (prepare or _batch_itself)(self.batch)
 
@@ -296,6 +317,7 @@ class FixedCapacityGraphBuilder:
                   self._cell_start.data_ptr(), self._cell_atoms.data_ptr(), self.neighbor_matrix.data_ptr(),
                   self.neighbor_shifts.data_ptr(), self.num_neighbors.data_ptr(),
                   self._candidate_capacity_valid.data_ptr(), self.system_size, 0, self._stream())
+        self.atom_order.copy_(morton_order(self.frac_coords))
         self._candidate_owner._candidate_initialized = True
 
     def assert_candidate_capacity(self) -> None:

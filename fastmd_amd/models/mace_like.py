@@ -253,6 +253,13 @@ def _empty(*shape, device, dtype=torch.float32):
     return torch.empty(*shape, dtype=dtype, device=device)
 
 
+def _atom_order(batch, n: int) -> int | None:
+    """Device address of the builder's spatial order of the atoms (``batch.atom_order``, a
+    permutation of the n rows) for the message kernels, or None (atom order)."""
+    order = getattr(batch, "atom_order", None)
+    return None if order is None or order.numel() != n else order.data_ptr()
+
+
 def _gather_edge_rows(h0: Tensor, ef: Tensor, edge_index: Tensor, out: Tensor) -> None:
     """out[e] = [h0[src e] | h0[dst e] | ef[e]] (src = neighbour column 1, dst = centre column 0)."""
     C, nb = h0.shape[1], ef.shape[1]
@@ -282,6 +289,7 @@ class _MaceLikeEnergy(Function):
         positions = positions.detach().contiguous()
         cell = cell.detach().to(torch.float32).contiguous()
         n_edges, off, ei = batch.n_edges, batch.edge_offsets, batch.edge_index
+        order = _atom_order(batch, n)
         elem = inputs.elem
         inv_avg = 1.0 / cfg.avg_num_neighbors
         geo = _empty(e_cap, 8, device=dev)
@@ -333,7 +341,8 @@ class _MaceLikeEnergy(Function):
             A0 = _empty(n, C, device=dev)
             A1 = _empty(n, 3, C, device=dev)
             _call("fmd_mace_message_f32", z.data_ptr(), _abi.ptr(q), geo.data_ptr(), ei.data_ptr(), off.data_ptr(),
-                  n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1), inv_avg, A0.data_ptr(), A1.data_ptr())
+                  n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1), inv_avg, A0.data_ptr(),
+                  A1.data_ptr())
             B0 = _empty(n, C, device=dev)
             B1 = None if last else _empty(n, 3, C, device=dev)
             if FUSED_NODE:
@@ -406,6 +415,7 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
     dev = ctx.geo.device
     inv_avg = 1.0 / cfg.avg_num_neighbors
     n_edges, off, ei, rev = batch.n_edges, batch.edge_offsets, batch.edge_index, batch.edge_reverse
+    order = _atom_order(batch, n)
     # readouts: gha = dE/d(first layer's h0 out), gy -> dE/d(last layer's h0 out)
     gy = _empty(n, H, device=dev)
     gha = _empty(n, C, device=dev)
@@ -472,8 +482,9 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
             gef = _empty(e_cap, nb, device=dev)
             w1ef = layer.W1[2 * C:]
             _call("fmd_mace_message_bwd_f32", z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(), ei.data_ptr(),
-                  rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1),
-                  gA0.data_ptr(), gA1.data_ptr(), inv_avg, None, None, None, ggeo.data_ptr(), acc_geo, None, None,
+                  rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(),
+                  _abi.ptr(h1), gA0.data_ptr(), gA1.data_ptr(), inv_avg, None, None, None, ggeo.data_ptr(), acc_geo,
+                  None, None,
                   0, w1ef.data_ptr(), nb, gef.data_ptr())
             gefs.append((gef, nb))
             break
@@ -490,7 +501,7 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
         g_in1 = _empty(n, 3, C, device=dev) if h1 is not None else None
         w1ef = layer.W1[2 * C:]
         _call("fmd_mace_message_bwd_f32", z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(), ei.data_ptr(),
-              rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, C, h0.data_ptr(), _abi.ptr(h1),
+              rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1),
               gA0.data_ptr(), gA1.data_ptr(), inv_avg, None, gzs.data_ptr(), gzs_src.data_ptr(), ggeo.data_ptr(),
               acc_geo, g_in0.data_ptr(), _abi.ptr(g_in1), 1, w1ef.data_ptr(), nb, gef.data_ptr())
         # g_in0 += [gzs_src | gzs] [W1[:C] | W1[C:2C]]^T (sender and receiver blocks, one node GEMM)

@@ -482,11 +482,13 @@ int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, co
  * features, where c and d meet only zeros) z holds a | b only (W = 2C). The pre-activations are
  * z[e] + zq[i] when zq ([N, W], the receiver block of the edge GEMM formed once per atom) is
  * given, else z[e]. z, zq, h0, h1, A0, A1 start on 16-byte boundaries (8 for C = 64), geo on 16.
- * Every row of a centre is taken by a half-wave (C / 32 channels per lane). */
+ * Every row of a centre is taken by a half-wave (C / 32 channels per lane).  * order (may be null): a permutation of the atoms, the order in which the waves take them (each
+ * atom's results are the same in any order; a spatial order keeps the neighbours' rows a wave
+ * gathers in the L2 of its XCD). */
 int fmd_mace_message_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
                          const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
-                         int32_t channels, const float* h0, const float* h1, float inv_avg, float* A0, float* A1,
-                         hipStream_t stream);
+                         const int32_t* order, int32_t channels, const float* h0, const float* h1, float inv_avg,
+                         float* A0, float* A1, hipStream_t stream);
 /* VJP of fmd_mace_message_f32 (z, zq and the width W as there): gz [E,W] (may be null), gzsum
  * [N,W] (may be null: the sum of gz over each centre's rows, in row order), gzsum_src [N,W] (may
  * be null: the sum of gz over the rows whose sender is the node, over the reverse CSR, without gz
@@ -500,8 +502,9 @@ int fmd_mace_message_f32(const float* z, const float* zq, const float* geo, cons
 int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
                              const int32_t* reverse,
                              const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
-                             int32_t channels, const float* h0, const float* h1, const float* gA0, const float* gA1,
-                             float inv_avg, float* gz, float* gzsum, float* gzsum_src, float* ggeo,
+                             const int32_t* order, int32_t channels, const float* h0, const float* h1,
+                             const float* gA0, const float* gA1, float inv_avg, float* gz, float* gzsum,
+                             float* gzsum_src, float* ggeo,
                              int32_t accumulate_geo, float* gh0, float* gh1, int32_t accumulate_h, const float* w1ef,
                              int32_t nb, float* gef, hipStream_t stream);
 /* The node side of one interaction layer fused per 32-atom tile (one launch instead of six),

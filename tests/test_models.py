@@ -317,6 +317,16 @@ def test_mace_like_gpu_matches_oracle(device, n_cells, channels, hoist, fused, g
         (grad,) = torch.autograd.grad(energy, (leaf,))
     assert torch.equal(energy.detach().reshape(1), out["e"])
     assert torch.equal(-grad, out["f"][0])
+    # the message kernels visit the atoms in the builder's spatial order: any order of the atoms
+    # (here none, the index order) gives the same bits
+    assert not torch.equal(builder.atom_order, torch.arange(n, dtype=torch.int32, device=device))
+    saved_order = builder.batch.atom_order
+    builder.batch.atom_order = None
+    try:
+        out3 = deriv(builder.batch, inputs, n_real=n)
+    finally:
+        builder.batch.atom_order = saved_order
+    assert torch.equal(out3["e"], out["e"]) and torch.equal(out3["f"][0], out["f"][0])
 
 
 @pytest.mark.gpu

@@ -204,6 +204,23 @@ def test_minimum_image_build_ignores_lattice_jumps():
     assert all(abs(np.linalg.norm(vec(t)) - 6.0) < 1e-4 for t in ours ^ brute)
 
 
+def test_morton_order_is_a_local_permutation():
+    """The builder's atom order (fixed_capacity_builder.morton_order): a permutation of the rows, a
+    union's systems one after the other, consecutive atoms close in space."""
+    import torch
+
+    from fastmd_amd.graph.fixed_capacity_builder import morton_order
+
+    frac = torch.rand(4000, 3, generator=torch.Generator().manual_seed(0))
+    order = morton_order(frac)
+    assert order.dtype == torch.int32 and sorted(order.tolist()) == list(range(4000))
+    step = (frac[order[1:].long()] - frac[order[:-1].long()]).norm(dim=1).mean()
+    assert float(step) < 0.25 * float((frac[1:] - frac[:-1]).norm(dim=1).mean())
+    system = torch.repeat_interleave(torch.arange(4), 1000).to(torch.int32)
+    order = morton_order(frac, system)
+    assert torch.equal(system[order.long()], system)  # grouped by system, in system order
+
+
 def test_window_fold():
     st = {"overflow": False, "capacity_overflow": False, "max_edges": 0, "max_isolated": 0}
     st = onl.window_fold(st, 10, False, False, 0, 32, True)
