@@ -99,6 +99,8 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_embed_f32": (ctypes.c_int, [_p, _p, _i64, _i32, _p, _p]),
     "fmd_morse_f32": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _f32, _f32, _f32, _f32, _f32, _p, _p, _p]),
     "fmd_morse_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _p, _p]),
+    "fmd_edge_virial_work_size": (_i64, []),
+    "fmd_edge_stress_f32": (ctypes.c_int, [_p, _p, _p, _i64, _p, _p, _p, _p]),
 }
 
 _lock = threading.Lock()

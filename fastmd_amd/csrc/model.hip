@@ -860,6 +860,67 @@ __global__ void morse_bwd_kernel(const float* geo, const float* dvdr, const int3
   gvec[3 * e + 2] = g * geo[8 * e + 2];
 }
 
+// ------------------------------------------------------------------------------------------
+// Virial of the edge vectors: M_ab = sum_e v_e,a * (dE/dv_e)_b, the derivative of the energy
+// under the strain v -> v (I + S) of every edge vector (positions and cell strained together
+// move every edge that way). v = u r from the geometry row (u, r). Float64 products and sums
+// in a fixed order: a fixed grid of kVirialBlocks blocks strides over the real rows, each block
+// writes its 9 partial sums, and one workgroup adds the partials block by block.
+// ------------------------------------------------------------------------------------------
+constexpr int kVirialBlocks = 256;
+
+__global__ void __launch_bounds__(kThreads) edge_virial_kernel(const float* geo, const float* gvec,
+                                                               const int64_t* n_edges, int64_t e_cap, double* part) {
+  __shared__ double red[9][kThreads];
+  const int64_t rows = real_rows(n_edges, e_cap);
+  double m[9];
+#pragma unroll
+  for (int k = 0; k < 9; ++k) m[k] = 0.0;
+  for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < rows; e += (int64_t)kVirialBlocks * kThreads) {
+    const float4 g = reinterpret_cast<const float4*>(geo)[2 * e];
+    const double v[3] = {(double)g.x * (double)g.w, (double)g.y * (double)g.w, (double)g.z * (double)g.w};
+    const double d[3] = {(double)gvec[3 * e], (double)gvec[3 * e + 1], (double)gvec[3 * e + 2]};
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int b = 0; b < 3; ++b) m[3 * a + b] = m[3 * a + b] + v[a] * d[b];
+  }
+#pragma unroll
+  for (int k = 0; k < 9; ++k) red[k][threadIdx.x] = m[k];
+  __syncthreads();
+  for (int width = kThreads / 2; width > 0; width >>= 1) {
+    if ((int)threadIdx.x < width)
+#pragma unroll
+      for (int k = 0; k < 9; ++k) red[k][threadIdx.x] = red[k][threadIdx.x] + red[k][threadIdx.x + width];
+    __syncthreads();
+  }
+  if (threadIdx.x < 9) part[9 * blockIdx.x + threadIdx.x] = red[threadIdx.x][0];
+}
+
+// stress = (M + M^T) / (2 V), V = |c0 . (c1 x c2)| of the unstrained cell (float64 from the
+// float32 rows); one wave
+__global__ void virial_stress_kernel(const double* part, const float* cell, float* stress) {
+  __shared__ double m[9];
+  const int t = threadIdx.x;
+  if (t < 9) {
+    double s = 0.0;
+    for (int b = 0; b < kVirialBlocks; ++b) s = s + part[9 * b + t];
+    m[t] = s;
+  }
+  __syncthreads();
+  if (t < 9) {
+    double c[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) c[k] = (double)cell[k];
+    const double cross0 = c[4] * c[8] - c[5] * c[7];
+    const double cross1 = c[5] * c[6] - c[3] * c[8];
+    const double cross2 = c[3] * c[7] - c[4] * c[6];
+    const double vol = fabs(c[0] * cross0 + c[1] * cross1 + c[2] * cross2);
+    const int a = t / 3, b = t % 3;
+    stress[t] = (float)(0.5 * (m[3 * a + b] + m[3 * b + a]) / vol);
+  }
+}
+
 template <int CPL>
 int launch_message(bool h1, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
                    const int32_t* ei,
@@ -1084,6 +1145,20 @@ int fmd_morse_bwd_f32(const float* geo, const float* dvdr, const int32_t* edge_i
   if (e_cap == 0) return FMD_OK;
   hipLaunchKernelGGL(morse_bwd_kernel, dim3((unsigned)fmd_cdiv(e_cap, 256)), dim3(256), 0, stream, geo, dvdr,
                      edge_index, gE, n_edges, e_cap, gvec);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int64_t fmd_edge_virial_work_size(void) { return 9 * (int64_t)kVirialBlocks; }
+
+int fmd_edge_stress_f32(const float* geo, const float* gvec, const int64_t* n_edges, int64_t e_cap, const float* cell,
+                        double* work, float* stress, hipStream_t stream) {
+  FMD_REQUIRE(geo && gvec && n_edges && cell && work && stress && e_cap >= 0);
+  FMD_REQUIRE(aligned_to(16, {geo}));
+  hipLaunchKernelGGL(edge_virial_kernel, dim3(kVirialBlocks), dim3(kThreads), 0, stream, geo, gvec, n_edges, e_cap,
+                     work);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(virial_stress_kernel, dim3(1), dim3(FMD_WAVE), 0, stream, work, cell, stress);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -76,6 +76,27 @@ def sum_f64_segments(x: Tensor, segments) -> Tensor:
     return out
 
 
+_VIRIAL_WORK = []
+
+
+def edge_stress(geo: Tensor, gvec: Tensor, n_edges: Tensor, cell: Tensor) -> Tensor:
+    """The stress dE/d(strain) / V [3, 3] float32 (energy_derivative.py:110-140) from a model's
+    edge geometry rows ``geo`` [e_cap, 8] (unit vector, length, ...) and the VJP's edge-vector
+    gradient ``gvec`` = dE/dv [e_cap, 3] over the real rows ``n_edges``: a symmetric strain S of
+    positions and cell moves every edge vector as v -> v (I + S), so dE/dS = sym(sum_e v_e gvec_e^T).
+    Float64 sums in a fixed order (one HIP kernel and a one-wave finish), nothing synchronizes."""
+    if not _VIRIAL_WORK:
+        _VIRIAL_WORK.append(int(_abi.load().fmd_edge_virial_work_size()))
+    cell = cell.detach().to(torch.float32).contiguous()
+    if cell.shape != (3, 3):
+        raise ValueError(f"the stress of one system needs a [3, 3] cell, got {tuple(cell.shape)}")
+    work = torch.empty(_VIRIAL_WORK[0], dtype=torch.float64, device=geo.device)
+    out = torch.empty(3, 3, dtype=torch.float32, device=geo.device)
+    _abi.call("fmd_edge_stress_f32", geo.data_ptr(), gvec.data_ptr(), n_edges.data_ptr(), geo.shape[0],
+              cell.data_ptr(), work.data_ptr(), out.data_ptr(), _abi.stream_handle())
+    return out
+
+
 def engine_derivative(adapter) -> "EnergyDerivative | None":
     """The derivative the runtime runs for ``adapter`` (energy_derivative.py:51-60)."""
     if hasattr(adapter, "node_energy"):
@@ -96,7 +117,8 @@ def edges_only_builder_options(adapter) -> dict:
 
 
 class EnergyDerivative:
-    """``derivative(batch, inputs, task="ef", n_real=None) -> {"e": [1] f64, "f": [forces [rows, 3]]}``."""
+    """``derivative(batch, inputs, task="ef", n_real=None) -> {"e": [1] f64, "f": [forces [rows, 3]]}``,
+    plus ``"s": [stress [3, 3] float32, eV/A^3]`` for a task with ``"s"``."""
 
     stress_unit = "eV/A^3"
 
@@ -112,7 +134,7 @@ class EnergyDerivative:
 
     def __call__(self, batch: GraphBatch, inputs, *, task: str = "ef", n_real: int | None = None) -> dict:
         if "s" in task:
-            raise NotImplementedError("stress is not supported by this build's models")
+            return self._with_stress(batch, inputs, n_real)
         explicit = getattr(self.adapter, "energy_and_forces", None)
         if explicit is not None and (n_real is None or n_real == batch.positions.shape[0]):
             # the adapter's explicit VJP: the same kernels as the autograd path below without the
@@ -133,3 +155,19 @@ class EnergyDerivative:
             parts = torch.stack([sum_f64(energies[a:a + c]) for a, c in _ranges(self.segments, rows)])
             (grad,) = torch.autograd.grad(parts.sum(), (leaf,))
         return {"e": parts.detach(), "f": [-grad]}
+
+    def _with_stress(self, batch: GraphBatch, inputs, n_real: int | None) -> dict:
+        """``{"e", "f", "s": [stress [3, 3]]}`` of one system (energy_derivative.py:110-140): the
+        adapter's ``energy_forces_stress`` forms the stress from its VJP's edge-vector gradient,
+        the same kernels as its forces (which are bitwise those of the ``"ef"`` task)."""
+        tap = getattr(self.adapter, "energy_forces_stress", None)
+        name = getattr(self.adapter, "name", type(self.adapter).__name__)
+        if tap is None:
+            raise NotImplementedError(f"model {name!r} has no stress tap (energy_forces_stress)")
+        if not (isinstance(self.segments, int) and self.segments == 1) or (
+                batch.systems is not None and batch.systems.count > 1):
+            raise NotImplementedError("stress is formed for one system per batch, not per replica or system")
+        if n_real is not None and n_real != batch.positions.shape[0]:
+            raise NotImplementedError("stress over a subset of the rows (n_real < rows) is not supported")
+        energy, forces, stress = tap(inputs, batch.positions, batch.cell)
+        return {"e": energy.reshape(1), "f": [forces], "s": [stress]}

@@ -405,8 +405,10 @@ class _Saved:
     """What the forward keeps for the VJP (the autograd ctx, or this holder outside autograd)."""
 
 
-def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
-    """``sign * dE/dpos`` [rows, 3] with E = sum_i gE_i E_i (gE None: all ones), by the VJP kernels."""
+def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None):
+    """``sign * dE/dpos`` [rows, 3] with E = sum_i gE_i E_i (gE None: all ones), by the VJP kernels;
+    with ``stress_cell`` (the unstrained float32 cell) also the stress dE/d(strain) / V [3, 3]:
+    ``(forces, stress)``."""
     model, inputs = ctx.model, ctx.inputs
     cfg = model.config
     batch = inputs.batch
@@ -513,7 +515,12 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
     (g1, ld1) = gefs[1] if len(gefs) > 1 else (None, 0)
     _call("fmd_edge_geometry_bwd_f32", ctx.geo.data_ptr(), ctx.de.data_ptr(), nb, g0.data_ptr(), ld0,
           _abi.ptr(g1), ld1, ggeo.data_ptr(), n_edges.data_ptr(), e_cap, gvec.data_ptr())
-    return segment_sum_csr([(gvec, inputs.csr_src, 0, sign, None), (gvec, inputs.csr_dst, 0, -sign, None)], n, 3)
+    forces = segment_sum_csr([(gvec, inputs.csr_src, 0, sign, None), (gvec, inputs.csr_dst, 0, -sign, None)], n, 3)
+    if stress_cell is None:
+        return forces
+    from fastmd_amd.engine.energy_derivative import edge_stress
+
+    return forces, edge_stress(ctx.geo, gvec, n_edges, stress_cell)
 
 
 class MaceLikeAdapter:
@@ -584,3 +591,14 @@ class MaceLikeAdapter:
         energies = _MaceLikeEnergy.forward(saved, positions.detach(), cell.detach(), self.module, inputs)
         energy = sum_f64_segments(energies, segments)  # one energy per replica or system
         return energy, _vjp(saved, None, -1.0)
+
+    def energy_forces_stress(self, inputs: MaceLikeInput, positions: Tensor, cell: Tensor):
+        """``energy_and_forces`` plus the stress dE/d(strain) / V [3, 3] float32 of one system
+        (energy_derivative.py:110-140), from the same VJP's edge-vector gradient."""
+        from fastmd_amd.engine.energy_derivative import sum_f64_into
+
+        saved = _Saved()
+        energies = _MaceLikeEnergy.forward(saved, positions.detach(), cell.detach(), self.module, inputs)
+        energy = sum_f64_into(energies)
+        forces, stress = _vjp(saved, None, -1.0, stress_cell=cell.detach().to(torch.float32).contiguous())
+        return energy, forces, stress

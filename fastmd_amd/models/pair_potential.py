@@ -60,14 +60,28 @@ class _MorseEnergy(Function):
 
     @staticmethod
     def backward(ctx, gE):
-        batch = ctx.inputs.batch
         gE = gE.detach().to(torch.float32).contiguous()
-        gvec = torch.empty(ctx.e_cap, 3, dtype=torch.float32, device=gE.device)
-        _abi.call("fmd_morse_bwd_f32", ctx.geo.data_ptr(), ctx.dvdr.data_ptr(), batch.edge_index.data_ptr(),
-                  gE.data_ptr(), batch.n_edges.data_ptr(), ctx.e_cap, gvec.data_ptr(), _abi.stream_handle())
-        gpos = segment_sum_csr([(gvec, ctx.inputs.csr_src, 0, 1.0, None), (gvec, ctx.inputs.csr_dst, 0, -1.0, None)],
-                               ctx.n, 3)
-        return gpos, None, None, None
+        return _morse_vjp(ctx, gE, 1.0)[0], None, None, None
+
+
+class _Saved:
+    """What the forward keeps for the VJP outside autograd."""
+
+
+def _morse_vjp(ctx, gE: Tensor, sign: float, stress_cell: Tensor | None = None):
+    """(sign * dE/dpos [rows, 3] with E = sum_i gE_i E_i, and with ``stress_cell`` the stress
+    [3, 3] of the edge-vector gradient, else None)."""
+    batch = ctx.inputs.batch
+    gvec = torch.empty(ctx.e_cap, 3, dtype=torch.float32, device=gE.device)
+    _abi.call("fmd_morse_bwd_f32", ctx.geo.data_ptr(), ctx.dvdr.data_ptr(), batch.edge_index.data_ptr(),
+              gE.data_ptr(), batch.n_edges.data_ptr(), ctx.e_cap, gvec.data_ptr(), _abi.stream_handle())
+    gpos = segment_sum_csr([(gvec, ctx.inputs.csr_src, 0, sign, None), (gvec, ctx.inputs.csr_dst, 0, -sign, None)],
+                           ctx.n, 3)
+    if stress_cell is None:
+        return gpos, None
+    from fastmd_amd.engine.energy_derivative import edge_stress
+
+    return gpos, edge_stress(ctx.geo, gvec, batch.n_edges, stress_cell)
 
 
 class MorsePairAdapter:
@@ -100,5 +114,18 @@ class MorsePairAdapter:
 
     def node_energy(self, inputs: PairInput, positions: Tensor, cell: Tensor) -> Tensor:
         if cell.requires_grad:
-            raise NotImplementedError("stress is not supported by the pair-potential kernels")
+            raise NotImplementedError("a strained cell is not differentiated by the pair-potential kernels: "
+                                      "stress comes from energy_forces_stress")
         return _MorseEnergy.apply(positions, cell, self.module, inputs)
+
+    def energy_forces_stress(self, inputs: PairInput, positions: Tensor, cell: Tensor):
+        """(E [1] float64, F = -dE/dpos [rows, 3], stress dE/d(strain) / V [3, 3] float32) of one
+        system (energy_derivative.py:110-140): the forward and VJP kernels of ``node_energy`` with
+        a unit energy seed, and the virial of the VJP's edge-vector gradient."""
+        from fastmd_amd.engine.energy_derivative import sum_f64_into
+
+        saved = _Saved()
+        energies = _MorseEnergy.forward(saved, positions.detach(), cell.detach(), self.module, inputs)
+        seed = torch.ones_like(energies)
+        forces, stress = _morse_vjp(saved, seed, -1.0, stress_cell=cell.detach().to(torch.float32).contiguous())
+        return sum_f64_into(energies), forces, stress

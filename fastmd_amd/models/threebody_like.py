@@ -218,8 +218,9 @@ def _forward(ctx, positions: Tensor, cell: Tensor, model: ThreeBodyLike, inputs:
     return energy
 
 
-def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
-    """sign * dE/dpos [n, 3] (gE None: the gradient of the plain sum of the node energies)."""
+def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None):
+    """sign * dE/dpos [n, 3] (gE None: the gradient of the plain sum of the node energies); with
+    ``stress_cell`` (the unstrained float32 cell) also the stress [3, 3]: ``(forces, stress)``."""
     model, inputs = ctx.model, ctx.inputs
     cfg = model.config
     lg, batch = inputs.line, inputs.batch
@@ -273,7 +274,14 @@ def _vjp(ctx, gE: Tensor | None, sign: float) -> Tensor:
     gvec = _empty(e_cap, 3, device=dev)
     _call("fmd_tb_geometry_bwd_f32", geo.data_ptr(), ctx.de.data_ptr(), nb, gef.data_ptr(), nb, gu.data_ptr(), 3,
           gfc.data_ptr(), gs.data_ptr(), lg.short_flags.data_ptr(), batch.n_edges.data_ptr(), e_cap, gvec.data_ptr())
-    return segment_sum_csr([(gvec, inputs.csr_src, 0, sign, None), (gvec, inputs.csr_dst, 0, -sign, None)], n, 3)
+    forces = segment_sum_csr([(gvec, inputs.csr_src, 0, sign, None), (gvec, inputs.csr_dst, 0, -sign, None)], n, 3)
+    if stress_cell is None:
+        return forces
+    from fastmd_amd.engine.energy_derivative import edge_stress
+
+    # the angles enter through the bond unit vectors, whose gradient is part of gvec: the virial
+    # of the edge vectors is the whole strain derivative
+    return forces, edge_stress(geo, gvec, batch.n_edges, stress_cell)
 
 
 class _ThreeBodyEnergy(Function):
@@ -361,3 +369,14 @@ class ThreeBodyAdapter:
         energies = _forward(saved, positions.detach(), cell.detach(), self.module, inputs)
         energy = sum_f64_segments(energies, segments)  # one energy per replica or system
         return energy, _vjp(saved, None, -1.0)
+
+    def energy_forces_stress(self, inputs: ThreeBodyInput, positions: Tensor, cell: Tensor):
+        """``energy_and_forces`` plus the stress dE/d(strain) / V [3, 3] float32 of one system
+        (energy_derivative.py:110-140)."""
+        from fastmd_amd.engine.energy_derivative import sum_f64_into
+
+        saved = _Saved()
+        energies = _forward(saved, positions.detach(), cell.detach(), self.module, inputs)
+        energy = sum_f64_into(energies)
+        forces, stress = _vjp(saved, None, -1.0, stress_cell=cell.detach().to(torch.float32).contiguous())
+        return energy, forces, stress

@@ -550,6 +550,16 @@ int fmd_morse_f32(const float* geo, const int64_t* edge_offsets, const int64_t* 
 int fmd_morse_bwd_f32(const float* geo, const float* dvdr, const int32_t* edge_index, const float* gE,
                       const int64_t* n_edges, int64_t e_cap, float* gvec, hipStream_t stream);
 
+/* Stress of the engine-owned derivative (fastmd/engine/energy_derivative.py:110-140: a symmetric
+ * strain of positions and cell, stress = dE/d(strain) / |det cell|) from the edge-vector
+ * gradient a model's VJP forms: strain moves every edge vector as v -> v (I + S), so
+ * dE/dS = sum_e v_e (x) gvec_e over the real rows (v = u r from the geometry rows geo [e_cap, 8]),
+ * symmetrised. stress [3, 3] float32, row-major; cell [3, 3] float32 (the unstrained cell);
+ * work: fmd_edge_virial_work_size() float64 elements. Float64 sums in a fixed order. */
+int64_t fmd_edge_virial_work_size(void);
+int fmd_edge_stress_f32(const float* geo, const float* gvec, const int64_t* n_edges, int64_t e_cap, const float* cell,
+                        double* work, float* stress, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

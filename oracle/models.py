@@ -163,3 +163,21 @@ def energy_and_forces(node_energy_fn, positions, *args, n_real=None, **kwargs):
     energy = energies[:rows].to(torch.float64).sum()
     (grad,) = torch.autograd.grad(energy, leaf)
     return energy.detach(), -grad, energies.detach()
+
+
+def energy_forces_stress(node_energy_fn, positions, cell):
+    """The engine-owned derivative with its strain leaf (energy_derivative.py:110-140): a zero
+    [3, 3] strain e, S = (e + e^T) / 2, the positions and the cell both deformed as x -> x + x S
+    (the row-by-row ``_times`` of energy_derivative.py:76-79), FP64 energy sum, one autograd.grad
+    over (positions, strain); F = -dE/dx and stress = dE/de / |c0 . (c1 x c2)| of the unstrained
+    cell. ``node_energy_fn(positions, cell)`` returns per-atom energies."""
+    leaf = positions.detach().clone().requires_grad_(True)
+    cell = cell.detach().to(leaf.dtype)
+    strain = torch.zeros((3, 3), dtype=leaf.dtype, requires_grad=True)
+    sym = 0.5 * (strain + strain.transpose(0, 1))
+    times = lambda rows: rows[:, 0:1] * sym[0] + rows[:, 1:2] * sym[1] + rows[:, 2:3] * sym[2]  # noqa: E731
+    energies = node_energy_fn(leaf + times(leaf), cell + times(cell))
+    energy = energies.to(torch.float64).sum()
+    grad, gstrain = torch.autograd.grad(energy, (leaf, strain))
+    volume = torch.dot(cell[0], torch.linalg.cross(cell[1], cell[2])).abs()
+    return energy.detach(), -grad, gstrain / volume
