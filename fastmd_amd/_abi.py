@@ -30,14 +30,14 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_nl_wrap": (ctypes.c_int, [_p, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p]),
     "fmd_nl_build_work_size": (_i64, [_i64]),
     "fmd_nl_build": (ctypes.c_int, [_p, _i32, _p, _p, _i64, _p, _p, _p, _i32, _p, _p, _p, _f32, _f32, _i32,
-                                    _i32, _i32, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                                    _i32, _i32, _i32, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                     _p, _p, _p, _p, _p, _f32, _p, _p]),
     "fmd_nl_build_noalloc": (ctypes.c_int, [_p, _i32, _p, _p, _i64, _p, _p, _p, _i32, _p, _p, _p, _f32, _f32, _i32,
-                                            _i32, _i32, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                                            _i32, _i32, _i32, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                             _p, _p, _p, _p, _p, _f32, _p, _p]),
     "fmd_nl_line_graph_work_size": (_i64, [_i64, _i64]),
     "fmd_nl_line_graph": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _p,
-                                         _p, _p, _p, _p, _p, _p, _p, _p, _p]),
+                                         _p, _p, _p, _p, _p, _p, _p, _p, _i32, _p]),
     "fmd_threebody_fourier_f32": (ctypes.c_int, [_p, _i64, _p, _p, _i64, _p, _i32, _f32, _p, _p]),
     "fmd_threebody_fourier_bwd_rows_f32": (ctypes.c_int, [_p, _p, _i64, _p, _p, _i64, _p, _i32, _f32, _p, _p]),
     "fmd_threebody_fourier_line_f32": (ctypes.c_int, [_p, _i64, _p, _p, _p, _i32, _p, _p, _i64, _i64, _p, _i32, _f32,
@@ -100,6 +100,8 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_morse_f32": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _f32, _f32, _f32, _f32, _f32, _p, _p, _p]),
     "fmd_morse_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _p, _p]),
     "fmd_edge_virial_work_size": (_i64, []),
+    "fmd_nl_overflow_rows": (ctypes.c_int, [_p, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p]),
+    "fmd_nl_pad_override": (ctypes.c_int, [_p, _i64, _f32, _f32, _f32, _p, _p]),
     "fmd_edge_stress_f32": (ctypes.c_int, [_p, _p, _p, _i64, _p, _p, _p, _p]),
 }
 

@@ -33,9 +33,14 @@ class PaddingRule:
     """What the padded rows of a fixed-capacity edge list look like (protocol.py:68-119).
 
     ``far_self_loops``: padded row k is a self-loop of real atom ``k mod n_real`` with an integer
-    image along the longest lattice vector, at least ``min_length`` and twice the cutoff long.
-    ``sink_atoms`` / ``exact_rc_loops`` are validated for parity of the interface but the
-    edges-only builder of this package writes far self-loops only.
+    image along the longest lattice vector, at least ``min_length`` and twice the cutoff long
+    (with a line graph a padded triplet joins a padded pair to itself at that pair's atom).
+    ``exact_rc_loops``: padded row k is a self-loop of real atom ``k mod n_real`` with image 0,
+    whose edge vector the model takes from ``GraphBatch.edge_vec_override`` (``pad_vector``,
+    by default (cutoff, 0, 0)); edges only. ``sink_atoms``: the batch has ``n_dummy`` sink rows
+    after the real ones (at the origin, atomic number 1); padded row k is a self-loop of a sink
+    with image (3, 3, 3), both rows of a padded pair on one sink, the padded pairs (and
+    triplets) spread evenly over the sinks; the model leaves the sink rows out (``n_real``).
     """
 
     kind: Literal["sink_atoms", "far_self_loops", "exact_rc_loops"] = "far_self_loops"
@@ -72,6 +77,15 @@ class SystemSegments:
     system_of_row: Tensor  # [rows] int32
     cells: Tensor | None = None
     atoms: Tensor | None = None
+
+
+def require_atom_rows(batch, model: str) -> None:
+    """Raise unless every row of ``batch`` is a model row: this package's HIP models read the
+    padded rows of far self-loop or exact-cutoff padding (which they skip by the edge count) but
+    not the extra rows of sink padding."""
+    if batch.positions is not None and batch.positions.shape[0] != batch.n_real:
+        raise ValueError(f"the {model} model takes far_self_loops or exact_rc_loops padding, not sink rows "
+                         f"({batch.positions.shape[0] - batch.n_real} rows past n_real)")
 
 
 def system_rows(batch) -> int | None:

@@ -16,6 +16,9 @@
 //     triplets use padding pair real_u + (t - t_real) % (u_cap - real_u) on atom pair % n;
 //     on overflow every triplet is the all-loop topology (u = t u_cap / t_cap, row 2 u, atom u % n)
 //     and d2u / u2d are the all-loop pairs (e / 2, 2 u).
+//   Sink padding (n_dummy > 0): a padding triplet sits on sink n + pad_id n_dummy / (t_cap - t_real)
+//     and the overflow topology is all-sink (u = ceil(d u_cap / n_dummy) for d = t n_dummy / t_cap,
+//     atom n + u n_dummy / u_cap); fmd_nl_overflow_rows writes the matching edge rows.
 // The scans are multi-block (block sums, one workgroup over the blocks, block-local scans):
 // deterministic, no atomics.
 #include "common.h"
@@ -244,7 +247,7 @@ __global__ void lg_edge_offsets_kernel(const int32_t* center, const uint8_t* sho
 __global__ void lg_line_graph_kernel(const int64_t* pair_offsets, const int64_t* short_counts, const int32_t* sem,
                                      const int32_t* d2u, const int64_t* edge_offsets, const uint8_t* overflow,
                                      int64_t n, int64_t e_cap, int64_t u_cap, int64_t t_cap, int32_t bmax,
-                                     int32_t* line_graph, int32_t* second_perm) {
+                                     int32_t n_dummy, int32_t* line_graph, int32_t* second_perm) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= t_cap) return;
   int32_t* out = line_graph + t * 5;
@@ -253,9 +256,15 @@ __global__ void lg_line_graph_kernel(const int64_t* pair_offsets, const int64_t*
   const int64_t total_all = pair_offsets[n];
   if (overflow[0] || t >= (total_all < t_cap ? total_all : t_cap)) second_perm[t] = -1;
   if (overflow[0]) {
-    int64_t u = t * u_cap / t_cap;
+    int64_t u;
+    if (n_dummy > 0) {
+      const int64_t d = t * n_dummy / t_cap;
+      u = (d * u_cap + n_dummy - 1) / n_dummy;
+    } else {
+      u = t * u_cap / t_cap;
+    }
     u = u < u_cap - 1 ? u : u_cap - 1;
-    const int32_t atom = (int32_t)(u % n);
+    const int32_t atom = (int32_t)(n_dummy > 0 ? n + u * n_dummy / u_cap : u % n);
     out[0] = atom;
     out[1] = (int32_t)u;
     out[2] = (int32_t)(2 * u);
@@ -301,7 +310,12 @@ __global__ void lg_line_graph_kernel(const int64_t* pair_offsets, const int64_t*
     const int64_t free_u = u_cap - real_u > 1 ? u_cap - real_u : 1;
     const int64_t pad_pair = pad_id % free_u;
     const int32_t pu = (int32_t)(real_u + pad_pair), pde = (int32_t)(ec + 2 * pad_pair);
-    out[0] = (int32_t)(pad_pair % n);
+    if (n_dummy > 0) {
+      const int64_t free_t = t_cap - t_real > 1 ? t_cap - t_real : 1;
+      out[0] = (int32_t)(n + pad_id * n_dummy / free_t);
+    } else {
+      out[0] = (int32_t)(pad_pair % n);
+    }
     out[1] = pu;
     out[2] = pde;
     out[3] = pu;
@@ -309,9 +323,46 @@ __global__ void lg_line_graph_kernel(const int64_t* pair_offsets, const int64_t*
   }
 }
 
+// The all-padding edge rows of an overflowed line-graph build (_allocate_overflow_topology /
+// _substitute_overflow_topology, fixed_capacity_builder.py:1474-1513,2163-2177): row e is a loop
+// of pair u = e / 2's atom (u mod n, or sink n + u n_dummy / u_cap) with image +/- the pad image
+// (+/- (3, 3, 3) for sinks) for even / odd rows. Rows untouched without overflow.
+__global__ void lg_overflow_rows_kernel(const uint8_t* overflow, int64_t n, int64_t e_cap, int32_t n_dummy, int pix,
+                                        int piy, int piz, int32_t* center, int32_t* neighbor, int32_t* images,
+                                        int32_t* edge_index, float* edge_image) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= e_cap || overflow[0] == 0) return;
+  const int64_t u = e / 2, u_cap = e_cap / 2;
+  const int32_t atom = (int32_t)(n_dummy > 0 ? n + u * n_dummy / u_cap : u % n);
+  const int sign = (e % 2 == 0) ? 1 : -1;
+  const int im[3] = {sign * (n_dummy > 0 ? 3 : pix), sign * (n_dummy > 0 ? 3 : piy), sign * (n_dummy > 0 ? 3 : piz)};
+  center[e] = atom;
+  neighbor[e] = atom;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) images[3 * e + k] = im[k];
+  if (edge_index) {
+    edge_index[2 * e] = atom;
+    edge_index[2 * e + 1] = atom;
+  }
+  if (edge_image)
+#pragma unroll
+    for (int k = 0; k < 3; ++k) edge_image[3 * e + k] = (float)im[k];
+}
+
 }  // namespace
 
 extern "C" {
+
+int fmd_nl_overflow_rows(const uint8_t* overflow, int64_t n_atoms, int64_t e_cap, int32_t n_dummy, int32_t pad_ix,
+                         int32_t pad_iy, int32_t pad_iz, int32_t* center, int32_t* neighbor, int32_t* images,
+                         int32_t* edge_index, float* edge_image, hipStream_t stream) {
+  FMD_REQUIRE(overflow && center && neighbor && images && n_atoms > 0 && e_cap > 0 && e_cap % 2 == 0 && n_dummy >= 0);
+  FMD_REQUIRE(n_atoms + n_dummy < (int64_t(1) << 31));
+  hipLaunchKernelGGL(lg_overflow_rows_kernel, dim3((unsigned)fmd_cdiv(e_cap, 256)), dim3(256), 0, stream, overflow,
+                     n_atoms, e_cap, n_dummy, pad_ix, pad_iy, pad_iz, center, neighbor, images, edge_index, edge_image);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
 
 int64_t fmd_nl_line_graph_work_size(int64_t n_atoms, int64_t e_cap) {
   const int64_t nb = fmd_cdiv(e_cap, kLgBlock);
@@ -323,8 +374,10 @@ int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const 
                       int64_t u_cap, int64_t t_cap, int32_t bmax, int64_t* work, int32_t* d2u, int32_t* u2d,
                       uint8_t* invalid_pairs, int64_t* short_counts, int64_t* short_offsets,
                       int32_t* short_edge_matrix, int64_t* pair_offsets, uint8_t* overflow, int32_t* line_graph,
-                      int64_t* edge_triplet_offsets, int32_t* bond_rows, int32_t* second_perm, hipStream_t stream) {
+                      int64_t* edge_triplet_offsets, int32_t* bond_rows, int32_t* second_perm, int32_t n_dummy,
+                      hipStream_t stream) {
   FMD_REQUIRE(n_atoms > 0 && e_cap > 0 && u_cap > 0 && t_cap > 0 && bmax > 0 && e_cap == 2 * u_cap);
+  FMD_REQUIRE(n_dummy >= 0 && n_atoms + n_dummy < (int64_t(1) << 31));
   FMD_REQUIRE(e_cap < (int64_t(1) << 31) && t_cap < (int64_t(1) << 31) && n_atoms < (int64_t(1) << 31));
   FMD_REQUIRE(edge_reverse && short_flags && edge_offsets && candidate_valid && work && d2u && u2d && invalid_pairs);
   FMD_REQUIRE(short_counts && short_offsets && short_edge_matrix && pair_offsets && overflow && line_graph);
@@ -357,7 +410,7 @@ int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const 
   FMD_CHECK_LAUNCH();
   hipLaunchKernelGGL(lg_line_graph_kernel, dim3((unsigned)fmd_cdiv(t_cap, 256)), dim3(256), 0, stream, pair_offsets,
                      short_counts, short_edge_matrix, d2u, edge_offsets, overflow, n_atoms, e_cap, u_cap, t_cap, bmax,
-                     line_graph, second_perm);
+                     n_dummy, line_graph, second_perm);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -310,6 +310,10 @@ struct BuildArgs {
   float skin_limit;
   int minimum_image;  // a lattice jump since the refresh is no motion (see atom_motion)
   int pad_ix, pad_iy, pad_iz;
+  // sink padding (> 0): padded rows are self-loops of the sink rows n .. n + n_dummy - 1 (image
+  // (3, 3, 3), distance 1e6), a padded pair's two rows on one sink, the pairs spread evenly over
+  // the sinks (fixed_capacity_builder.py:291-320); 0: far self-loops with the pad image
+  int n_dummy;
   // several systems in one union (null: one system): the system of each row; then inv_cell and
   // cell are [systems, 9] tables and pad_images [systems, 3] the far self-loop image of each
   const int32_t* system_of;
@@ -420,6 +424,16 @@ __device__ __forceinline__ bool slot_edge(const BuildArgs& a, const Mat3& cm, in
 
 __device__ __forceinline__ void pad_rows(const BuildArgs& a, int64_t total, int64_t start, int64_t step) {
   const int64_t ec = total < a.e_cap ? total : a.e_cap;
+  if (a.n_dummy > 0) {
+    const int64_t free_u = a.e_cap / 2 - ec / 2;
+    for (int64_t row = ec + start; row < a.e_cap; row += step) {
+      const int64_t pair = (row - ec) / 2;
+      const int32_t sink = (int32_t)(a.n + pair * a.n_dummy / (free_u > 1 ? free_u : 1));
+      write_row(a, row, sink, sink, 3, 3, 3, 0.f, false);
+      a.distances[row] = 1.0e6f;
+    }
+    return;
+  }
   for (int64_t row = ec + start; row < a.e_cap; row += step) {
     const int32_t atom = (int32_t)((row - ec) % a.n);
     if (a.system_of) {
@@ -825,6 +839,7 @@ int launch_build(const BuildArgs& a, hipStream_t stream) {
   FMD_REQUIRE(a.edge_counts && a.edge_offsets && a.center && a.neighbor && a.images && a.distances);
   FMD_REQUIRE(a.max_disp && a.cand_valid && a.overflow && a.isolated);
   FMD_REQUIRE(!a.system_of || a.pad_images);
+  FMD_REQUIRE(a.n_dummy >= 0 && (a.n_dummy == 0 || !a.system_of) && a.n + a.n_dummy < (int64_t(1) << 31));
   if (a.n <= kSmallMaxAtoms && a.n <= 1024) {
     hipLaunchKernelGGL(nl_build_small_kernel, dim3(1), dim3(kSmallThreads), 0, stream, a);
     FMD_CHECK_LAUNCH();
@@ -935,7 +950,7 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  const int32_t* neighbor_matrix, const int32_t* neighbor_shifts, const int32_t* num_neighbors,
                  int32_t bmax, const float* reference_positions, const int32_t* reference_wraps,
                  const uint8_t* capacity_valid, float rc2, float skin_limit, int32_t minimum_image, int32_t pad_ix,
-                 int32_t pad_iy, int32_t pad_iz, const int32_t* system_of, const int32_t* pad_images, int64_t e_cap,
+                 int32_t pad_iy, int32_t pad_iz, int32_t n_dummy, const int32_t* system_of, const int32_t* pad_images, int64_t e_cap,
                  int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
                  int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor, int32_t* images,
                  float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
@@ -944,7 +959,7 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
   FMD_REQUIRE(work);
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
               reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, minimum_image, pad_ix, pad_iy, pad_iz,
-              system_of, pad_images, e_cap, work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
+              n_dummy, system_of, pad_images, e_cap, work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
               edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags};
   return launch_build(a, stream);
 }
@@ -953,7 +968,7 @@ int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float*
                          int64_t n_atoms, const int32_t* neighbor_matrix, const int32_t* neighbor_shifts,
                          const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,
                          const int32_t* reference_wraps, const uint8_t* capacity_valid, float rc2, float skin_limit,
-                         int32_t minimum_image, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz,
+                         int32_t minimum_image, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz, int32_t n_dummy,
                          const int32_t* system_of, const int32_t* pad_images, int64_t e_cap, float* frac,
                          int32_t* wrap_delta, float* wrapped_out, int64_t* edge_counts, int64_t* edge_offsets,
                          int32_t* center, int32_t* neighbor, int32_t* images, float* distances, int32_t* edge_index,
@@ -966,7 +981,7 @@ int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float*
   if (status != FMD_OK) return status;
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
               reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, minimum_image, pad_ix, pad_iy, pad_iz,
-              system_of, pad_images, e_cap, work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
+              n_dummy, system_of, pad_images, e_cap, work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
               edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags};
   return launch_build(a, stream);
 }
@@ -992,6 +1007,28 @@ int fmd_nl_pad_rows(int32_t* edge_index, float* edge_image, int32_t* edge_revers
   if (e_real == e_cap) return FMD_OK;
   hipLaunchKernelGGL(nl_pad_rows_kernel, dim3((unsigned)fmd_cdiv(e_cap - e_real, 256)), dim3(256), 0, stream,
                      edge_index, edge_image, edge_reverse, e_real, e_cap, n_atoms, pad_ix, pad_iy, pad_iz);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+// the edge-vector override of exact-cutoff padding (fixed_capacity_builder.py:357-361): the pad
+// vector on rows [min(n_edges, e_cap), e_cap), zero on the real rows
+__global__ void nl_pad_override_kernel(const int64_t* n_edges, int64_t e_cap, float vx, float vy, float vz,
+                                       float* vec_override) {
+  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= e_cap) return;
+  const int64_t total = n_edges[0];
+  const bool pad = row >= (total < e_cap ? total : e_cap);
+  vec_override[3 * row] = pad ? vx : 0.f;
+  vec_override[3 * row + 1] = pad ? vy : 0.f;
+  vec_override[3 * row + 2] = pad ? vz : 0.f;
+}
+
+int fmd_nl_pad_override(const int64_t* n_edges, int64_t e_cap, float vx, float vy, float vz, float* vec_override,
+                        hipStream_t stream) {
+  FMD_REQUIRE(n_edges && vec_override && e_cap > 0);
+  hipLaunchKernelGGL(nl_pad_override_kernel, dim3((unsigned)fmd_cdiv(e_cap, 256)), dim3(256), 0, stream, n_edges,
+                     e_cap, vx, vy, vz, vec_override);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -132,6 +132,8 @@ class BucketedGraphRunner:
         self.cutoff = float(topology.cutoff)
         self.triplet_cutoff = None if topology.triplet_cutoff is None else float(topology.triplet_cutoff)
         self.rule = model.padding_rule() if hasattr(model, "padding_rule") else _FAR_SELF_LOOPS
+        if self.rule.kind != "far_self_loops":
+            raise NotImplementedError(f"model_graph buckets pad with far self-loops, not {self.rule.kind}")
         step = model.capacity_step() if hasattr(model, "capacity_step") else None
         self._factors = (1.0, 1.0) if step is None else (float(step.u_thermal_factor), float(step.t_thermal_factor))
         self.pool = torch.cuda.graph_pool_handle()

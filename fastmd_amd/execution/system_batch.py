@@ -87,6 +87,8 @@ class SlotUnionGraphBuilder(FixedCapacityGraphBuilder):
                  atom_graph_cutoff: float = 6.0, line_graph_cutoff: float | None = None,
                  candidate_cutoff: float | None = None, padding=None, prepare=None,
                  device: torch.device | str = "cuda", minimum_image: bool = False) -> None:
+        if padding is not None and padding.kind == "sink_atoms":
+            raise NotImplementedError("a slot union pads with self-loops (sink rows would sit between slots)")
         cells32 = [_cell32(c) for c in cells]
         atoms = [int(a) for a in atoms]
         if len(cells32) != layout.count or len(atoms) != layout.count:

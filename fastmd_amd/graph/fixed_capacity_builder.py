@@ -118,9 +118,12 @@ class FixedCapacityGraphBuilder:
     pairs, short-bond lists and triplet rows, fmd_nl_line_graph, published as
     ``batch.pair_d2u`` / ``pair_u2d`` / ``triplets``).
 
-    Unsupported reference options (ghost rows, sink padding, float64 published positions) raise
-    ``NotImplementedError``. ``sorted_edges=False`` is
-    accepted: the rows are always in the canonical order, which is also grouped by centre."""
+    Padding (``padding``, protocol.py:68-119): far self-loops (the default here), exact-cutoff
+    loops (edges only: image 0 and ``batch.edge_vec_override``) or sink atoms (``n_dummy`` sink
+    rows after the real ones at the origin, atomic number 1; padded rows, and with a line graph
+    padded triplets, sit on them). Unsupported reference options (ghost rows, float64 published
+    positions) raise ``NotImplementedError``. ``sorted_edges=False`` is accepted: the rows are
+    always in the canonical order, which is also grouped by centre."""
 
     def __init__(self, *, cell: Tensor, atomic_numbers: Tensor, u_capacity: int, t_capacity: int = 0,
                  pbc: Tensor | None = None, atom_graph_cutoff: float = 6.0, line_graph_cutoff: float | None = None,
@@ -140,8 +143,13 @@ class FixedCapacityGraphBuilder:
         if positions_dtype != torch.float32:
             raise NotImplementedError("float64 published positions are not supported")
         padding = _FAR_SELF_LOOPS if padding is None else padding
-        if padding.kind != "far_self_loops":
-            raise NotImplementedError(f"{padding.kind} padding is not supported (far_self_loops only)")
+        if line_graph and padding.kind == "exact_rc_loops":
+            raise ValueError("a builder with a line graph pads with sink atoms, or a single-system builder "
+                             "with far self-loops (padded triplets need padded pairs)")
+        if padding.kind == "sink_atoms" and int(n_dummy) <= 0:
+            raise ValueError("sink padding needs n_dummy > 0")
+        if padding.kind == "sink_atoms" and system_size:
+            raise NotImplementedError("replica unions pad with far self-loops")
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise ValueError("the fixed-capacity builder runs on the GPU")
@@ -163,7 +171,8 @@ class FixedCapacityGraphBuilder:
         self.n_real = int(self.atomic_numbers_real.shape[0])
         if self.n_real <= 0:
             raise ValueError("a builder needs at least one atom")
-        self.n_dummy = 0
+        # sink rows exist only for sink padding (fixed_capacity_builder.py:1144-1145)
+        self.n_dummy = int(n_dummy) if padding.kind == "sink_atoms" else 0
         self.u_capacity = int(u_capacity)
         if self.u_capacity <= 0:
             raise ValueError("a builder needs u_capacity > 0")
@@ -182,7 +191,9 @@ class FixedCapacityGraphBuilder:
         self._rc2 = float(np.float32(self.atom_graph_cutoff * self.atom_graph_cutoff))
         self._cand2 = float(np.float32(self.candidate_cutoff * self.candidate_cutoff))
         self._skin_limit = float(np.float32(self.skin + 1.0e-6))
-        self._pad_loop = self_loop_padding(padding, self.cell, self.atom_graph_cutoff)
+        # (image, length, override vector) of self-loop padding; None for sink padding
+        self._pad_loop = (None if padding.kind == "sink_atoms"
+                          else self_loop_padding(padding, self.cell, self.atom_graph_cutoff))
         self._ncells, self._reach = cell_list_shape(self.cell.cpu().numpy(), self.candidate_cutoff)
         # minimum_image: the caller may hand in coordinates wrapped by any lattice vector since the
         # refresh (ASE's atoms.wrap()); the skin test and the wrap delta remove the jump
@@ -226,7 +237,8 @@ class FixedCapacityGraphBuilder:
             self._candidate_capacity_valid = torch.zeros(1, **u8)
             self._candidate_initialized = False
             self.atom_order = torch.arange(n, **i32)
-        self.frac_coords = torch.zeros((n, 3), **f32)
+        # real rows, then the sink rows (kept at the origin)
+        self.frac_coords = torch.zeros((n + self.n_dummy, 3), **f32)
         self.edge_counts = torch.zeros(n, **i64)
         self.edge_offsets = torch.zeros(n + 1, **i64)
         self.pair_offsets = torch.zeros(1, **i64)
@@ -259,18 +271,23 @@ class FixedCapacityGraphBuilder:
             # with edge_triplet_offsets: the triplets of each row as their second bond
             self.second_perm = torch.full((self.t_capacity,), -1, **i32)
             self._lg_work = torch.zeros(int(_abi.load().fmd_nl_line_graph_work_size(n, e)), **i64)
-        self.positions = torch.zeros((n, 3), **f32)
+        self.positions = torch.zeros((n + self.n_dummy, 3), **f32)
+        self.edge_vec_override = (torch.zeros((e, 3), **f32) if padding.kind == "exact_rc_loops" else None)
+        species = self.atomic_numbers_real
+        if self.n_dummy:
+            species = torch.cat([species, torch.ones(self.n_dummy, **i32)])
         self.batch = GraphBatch(
             positions=self.positions,
             frac_coords=self.frac_coords,
             cell=self.cell,
-            species=self.atomic_numbers_real,
+            species=species,
             n_real=n,
             edge_index=torch.zeros((e, 2), **i32),
             edge_image=torch.zeros((e, 3), **f32),
             n_edges=self.edge_offsets[-1:],
             cutoff=self.atom_graph_cutoff,
             padding=padding,
+            edge_vec_override=self.edge_vec_override,
             composition=self.composition,
             edge_offsets=self.edge_offsets,
             edge_reverse=self.edge_reverse,
@@ -317,7 +334,7 @@ class FixedCapacityGraphBuilder:
                   self._cell_start.data_ptr(), self._cell_atoms.data_ptr(), self.neighbor_matrix.data_ptr(),
                   self.neighbor_shifts.data_ptr(), self.num_neighbors.data_ptr(),
                   self._candidate_capacity_valid.data_ptr(), self.system_size, 0, self._stream())
-        self.atom_order.copy_(morton_order(self.frac_coords))
+        self.atom_order.copy_(morton_order(self.frac_coords[:n]))
         self._candidate_owner._candidate_initialized = True
 
     def assert_candidate_capacity(self) -> None:
@@ -349,12 +366,12 @@ class FixedCapacityGraphBuilder:
         elif not self._candidate_owner._candidate_initialized:
             raise RuntimeError("refresh_candidates must run before candidate reuse")
         is64 = 1 if positions.dtype == torch.float64 else 0
-        image = self._pad_loop[0]
+        image = self._pad_image
         _abi.call("fmd_nl_build", positions.data_ptr(), is64, self.inv_cell.data_ptr(), self.cell.data_ptr(),
                   self.n_real, self.neighbor_matrix.data_ptr(), self.neighbor_shifts.data_ptr(),
                   self.num_neighbors.data_ptr(), self.buffer_max, self.reference_positions.data_ptr(),
                   self.reference_wraps.data_ptr(), self._candidate_capacity_valid.data_ptr(), self._rc2,
-                  self._skin_limit, 1 if self.minimum_image else 0, image[0], image[1], image[2],
+                  self._skin_limit, 1 if self.minimum_image else 0, image[0], image[1], image[2], self.n_dummy,
                   _abi.ptr(self._system_of), _abi.ptr(self._pad_images), self.e_capacity, self._work.data_ptr(),
                   self.frac_coords.data_ptr(), self.wrap_delta.data_ptr(), self.positions.data_ptr(),
                   self.edge_counts.data_ptr(), self.edge_offsets.data_ptr(), self.center.data_ptr(),
@@ -376,10 +393,24 @@ class FixedCapacityGraphBuilder:
                       self.short_counts.data_ptr(), self.short_offsets.data_ptr(),
                       self.short_edge_matrix.data_ptr(), self.pair_offsets.data_ptr(), self._overflow.data_ptr(),
                       self.line_graph.data_ptr(), self.edge_triplet_offsets.data_ptr(), self.bond_rows.data_ptr(),
-                      self.second_perm.data_ptr(), self._stream())
+                      self.second_perm.data_ptr(), self.n_dummy, self._stream())
+            # an overflowed build publishes the all-padding edge rows (_substitute_overflow_topology)
+            _abi.call("fmd_nl_overflow_rows", self._overflow.data_ptr(), self.n_real, self.e_capacity, self.n_dummy,
+                      image[0], image[1], image[2], self.center.data_ptr(), self.neighbor.data_ptr(),
+                      self.images.data_ptr(), self.batch.edge_index.data_ptr(), self.batch.edge_image.data_ptr(),
+                      self._stream())
+        if self.edge_vec_override is not None:
+            v = self._pad_loop[2]
+            _abi.call("fmd_nl_pad_override", self.edge_offsets[-1:].data_ptr(), self.e_capacity, v[0], v[1], v[2],
+                      self.edge_vec_override.data_ptr(), self._stream())
         if self.max_neighbor_count is not None:
             torch.maximum(self.max_neighbor_count, self.edge_counts.max().reshape(1), out=self.max_neighbor_count)
         return self.graph, self.status
+
+    @property
+    def _pad_image(self) -> tuple[int, int, int]:
+        """The self-loop padding image (unused by sink padding)."""
+        return (0, 0, 0) if self._pad_loop is None else self._pad_loop[0]
 
     @property
     def status(self) -> FixedCapacityGraphStatus:

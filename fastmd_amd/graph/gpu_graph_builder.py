@@ -144,7 +144,7 @@ class TensorGraphBuilder:
         isolated = torch.empty(1, **i32)
         _abi.call("fmd_nl_build", positions.data_ptr(), is64, self.inv_cell.data_ptr(), self.cell.data_ptr(), n,
                   nm.data_ptr(), ns.data_ptr(), num.data_ptr(), bmax, ref_pos.data_ptr(), ref_wraps.data_ptr(),
-                  valid.data_ptr(), self._rc2, float(np.float32(1.0e-6)), 0, 0, 0, 1, None, None, e_cap, work.data_ptr(),
+                  valid.data_ptr(), self._rc2, float(np.float32(1.0e-6)), 0, 0, 0, 1, 0, None, None, e_cap, work.data_ptr(),
                   frac.data_ptr(), wrap_delta.data_ptr(), wrapped.data_ptr(), counts.data_ptr(), offsets.data_ptr(),
                   center.data_ptr(), neighbor.data_ptr(), images.data_ptr(), distances.data_ptr(),
                   edge_index.data_ptr(), edge_image.data_ptr(), max_disp.data_ptr(), cand_valid.data_ptr(),

@@ -356,7 +356,8 @@ class GPUResidentMolecularDynamics:
                                          t_capacity=key.t_capacity if self.triplet_cutoff is not None else 0,
                                          atom_graph_cutoff=self.cutoff, line_graph_cutoff=self.triplet_cutoff,
                                          candidate_cutoff=self.cutoff + self.config.capacity.candidate_skin,
-                                         padding=self.adapter.padding_rule(), prepare=prepare, device=self.device)
+                                         padding=self.adapter.padding_rule(), n_dummy=self.config.capacity.n_dummy,
+                                         prepare=prepare, device=self.device)
 
     def _make_runner(self, key, recapture: bool) -> WholeStepGraphRunner:
         builder = self._line_builder(key, prepare=self.adapter.prepare)

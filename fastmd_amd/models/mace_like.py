@@ -38,7 +38,7 @@ from torch.autograd import Function
 
 from fastmd_amd import _abi
 from fastmd_amd.adapters.protocol import (CapacityStep, CaptureContract, GraphBatch, PaddingRule, TopologySpec,
-                                         system_rows)
+                                         require_atom_rows, system_rows)
 from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr
 from fastmd_amd.ops.wide_gemm import (Planes, gemm, gemm_gather, gemm_group, gemm_planes, gemm_splitk,
                                      split_planes)
@@ -565,6 +565,7 @@ class MaceLikeAdapter:
         outside any graph) and the two CSRs of the edge list."""
         if batch.positions is None or batch.edge_offsets is None or batch.edge_reverse is None:
             raise ValueError("the MACE-like model needs an edges-only batch with its CSR (edge_offsets, edge_reverse)")
+        require_atom_rows(batch, "MACE-like")
         species = batch.species.long()
         table = self.module.z_table.to(species.device)
         if bool(((species < 1) | (species > _ELEMENTS)).any()) or bool((table[species.clamp(1, _ELEMENTS)] < 0).any()):

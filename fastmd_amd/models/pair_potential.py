@@ -16,7 +16,8 @@ from torch import Tensor, nn
 from torch.autograd import Function
 
 from fastmd_amd import _abi
-from fastmd_amd.adapters.protocol import CapacityStep, GraphBatch, PaddingRule, TopologySpec, system_rows
+from fastmd_amd.adapters.protocol import (CapacityStep, GraphBatch, PaddingRule, TopologySpec, require_atom_rows,
+                                         system_rows)
 from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr
 
 
@@ -109,6 +110,7 @@ class MorsePairAdapter:
     def prepare(self, batch: GraphBatch) -> PairInput:
         if batch.edge_offsets is None or batch.edge_reverse is None:
             raise ValueError("the pair potential needs an edges-only batch with its CSR")
+        require_atom_rows(batch, "Morse")
         rows = batch.edge_index.shape[0]
         return PairInput(batch, Csr(batch.edge_offsets, None, rows), Csr(batch.edge_offsets, batch.edge_reverse, rows))
 

@@ -42,7 +42,7 @@ from torch.autograd import Function
 
 from fastmd_amd import _abi
 from fastmd_amd.adapters.protocol import (CapacityStep, CaptureContract, GraphBatch, PaddingRule, TopologySpec,
-                                         system_rows)
+                                         require_atom_rows, system_rows)
 from fastmd_amd.ops.csr_segment_sum import Csr, segment_sum_csr
 from fastmd_amd.ops.threebody import LineGraph, fourier_line_vjp
 from fastmd_amd.ops.wide_gemm import gemm, gemm_gather, gemm_group
@@ -341,6 +341,7 @@ class ThreeBodyAdapter:
         the species, outside any graph) and the two CSRs of the edge list."""
         if batch.positions is None or batch.edge_offsets is None or batch.edge_reverse is None:
             raise ValueError("the three-body model needs a fixed-capacity batch with its CSR")
+        require_atom_rows(batch, "three-body")
         if batch.line is None or batch.line.edge_triplet_offsets is None:
             raise ValueError("the three-body model reads a line graph (a builder with line_graph_cutoff)")
         if abs(float(batch.triplet_cutoff) - float(self.module.config.bond_cutoff)) > 1e-12:

@@ -51,7 +51,8 @@ const char* fmd_error_string(int status);
  * Replaces nvalchemiops batch_build_cell_list/batch_query_cell_list as called at
  * fastmd/graph/fixed_capacity_builder.py:1519-1554 (FixedCapacityGraphBuilder._build_candidates).
  * system_size > 0: the atoms are replicas of one system, [k S, (k+1) S) each, and pairs across
- * replicas are not candidates (the union graph of replica batching, replica_batch.py:126-180).  * index_offset is added to every stored neighbour index (the pad value becomes
+ * replicas are not candidates (the union graph of replica batching, replica_batch.py:126-180).
+ * index_offset is added to every stored neighbour index (the pad value becomes
  * n_atoms + index_offset): a union of systems searches each system on its own slice of rows and
  * stores union indices. A row with more candidates than the LDS key buffer holds (at least
  * bmax) is stored empty, so every row's content is deterministic; it is flagged invalid. */
@@ -96,6 +97,10 @@ int fmd_nl_wrap(const void* positions, int32_t pos_is_f64, const float* inv_cell
  *                   motion: the skin test takes the minimum-image displacement and the jump
  *                   leaves the wrap delta (fixed_capacity_builder.py:2233-2245); 0: plain
  *   pad_image       integer image of the padded self-loops
+ *   n_dummy         0: far self-loop padding (pad_image); > 0: sink padding
+ *                   (_pad_edges_kernel, fixed_capacity_builder.py:291-320): padded row r is a
+ *                   self-loop of sink row n + p n_dummy / (e_cap / 2 - ec / 2), p = (r - ec) / 2,
+ *                   ec = min(E, e_cap), image (3, 3, 3), distance 1e6 (one system only)
  *   work            int64 scratch of fmd_nl_build_work_size(n) elements
  * Outputs: frac [n,3] f32, wrap_delta [n,3] i32, wrapped_out [n,3] f32 (published
  * positions, may be null), edge_counts [n] i64, edge_offsets [n+1] i64, center/neighbor
@@ -110,7 +115,8 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,
                  const int32_t* reference_wraps, const uint8_t* capacity_valid, float rc2,
                  float skin_limit, int32_t minimum_image, int32_t pad_ix, int32_t pad_iy, int32_t pad_iz,
-                 const int32_t* system_of, const int32_t* pad_images, int64_t e_cap, int64_t* work, float* frac, int32_t* wrap_delta, float* wrapped_out,
+                 int32_t n_dummy, const int32_t* system_of, const int32_t* pad_images, int64_t e_cap, int64_t* work,
+                 float* frac, int32_t* wrap_delta, float* wrapped_out,
                  int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor,
                  int32_t* images, float* distances, int32_t* edge_index, float* edge_image,
                  float* max_displacement, uint8_t* candidate_valid, uint8_t* overflow,
@@ -132,7 +138,8 @@ int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float*
                          const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,
                          const int32_t* reference_wraps, const uint8_t* capacity_valid, float rc2,
                          float skin_limit, int32_t minimum_image, int32_t pad_ix, int32_t pad_iy,
-                         int32_t pad_iz, const int32_t* system_of, const int32_t* pad_images, int64_t e_cap,
+                         int32_t pad_iz, int32_t n_dummy, const int32_t* system_of, const int32_t* pad_images,
+                         int64_t e_cap,
                          float* frac, int32_t* wrap_delta, float* wrapped_out, int64_t* edge_counts,
                          int64_t* edge_offsets, int32_t* center, int32_t* neighbor, int32_t* images,
                          float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
@@ -153,14 +160,34 @@ int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float*
  * bond (empty for other rows; clamped to t_cap), bond_rows [e_cap] i32, the short rows in
  * (atom, rank) order (then -1), the rows of the CSR short_offsets over the atoms, and second_perm
  * [t_cap] i32, the permutation that with edge_triplet_offsets lists for row e the triplets with e
- * as their second bond, by first bond (-1 past the real triplets and throughout an overflowed build). */
+ * as their second bond, by first bond (-1 past the real triplets and throughout an overflowed build).
+ * n_dummy > 0 (sink padding): padding triplet t sits on sink n + (t - t_real) n_dummy /
+ * (t_cap - t_real), and the overflow topology is all-sink (_line_graph_kernel without
+ * LOOP_PADDING and _allocate_overflow_topology, fixed_capacity_builder.py:745-749,1474-1513). */
 int64_t fmd_nl_line_graph_work_size(int64_t n_atoms, int64_t e_cap);
 int fmd_nl_line_graph(const int32_t* center, const int32_t* edge_reverse, const uint8_t* short_flags,
                       const int64_t* edge_offsets, const uint8_t* candidate_valid, int64_t n_atoms, int64_t e_cap,
                       int64_t u_cap, int64_t t_cap, int32_t bmax, int64_t* work, int32_t* d2u, int32_t* u2d,
                       uint8_t* invalid_pairs, int64_t* short_counts, int64_t* short_offsets,
                       int32_t* short_edge_matrix, int64_t* pair_offsets, uint8_t* overflow, int32_t* line_graph,
-                      int64_t* edge_triplet_offsets, int32_t* bond_rows, int32_t* second_perm, hipStream_t stream);
+                      int64_t* edge_triplet_offsets, int32_t* bond_rows, int32_t* second_perm, int32_t n_dummy,
+                      hipStream_t stream);
+
+/* The edge rows of an overflowed line-graph build, after fmd_nl_line_graph (overflow its flag):
+ * row e becomes a loop of pair u = e / 2's atom, u mod n (far self-loops) or sink
+ * n + u n_dummy / (e_cap / 2), image + or - the pad image ((3, 3, 3) for sinks) for even / odd e;
+ * nothing is written without overflow. Replaces _substitute_overflow_topology with the edge part
+ * of _allocate_overflow_topology (fixed_capacity_builder.py:2163-2177,1474-1496). edge_index
+ * [e_cap, 2] i32 and edge_image [e_cap, 3] f32 (the published copies) may be null. */
+int fmd_nl_overflow_rows(const uint8_t* overflow, int64_t n_atoms, int64_t e_cap, int32_t n_dummy, int32_t pad_ix,
+                         int32_t pad_iy, int32_t pad_iz, int32_t* center, int32_t* neighbor, int32_t* images,
+                         int32_t* edge_index, float* edge_image, hipStream_t stream);
+
+/* The edge-vector override of exact-cutoff padding (PaddingRule("exact_rc_loops"),
+ * fixed_capacity_builder.py:323-366 with HAS_OVERRIDE): vec_override [e_cap, 3] f32 holds
+ * (vx, vy, vz) on the padded rows [min(*n_edges, e_cap), e_cap) and 0 on the real rows. */
+int fmd_nl_pad_override(const int64_t* n_edges, int64_t e_cap, float vx, float vy, float vz, float* vec_override,
+                        hipStream_t stream);
 
 /* The three-body Fourier angle basis (threebody_fourier_basis, triton_threebody_fourier.py:45-80,
  * :230-260): out[t] = [1/sqrt(2), sin(theta f_k), cos(theta f_k)] / scale (1 + 2 n_freq columns),

@@ -8,13 +8,15 @@ Restates, in NumPy float32 with the operation order of ``fastmd_amd/csrc/nl.hip`
     cutoff, sorted by (j, sx, sy, sz), first bmax stored, all counted
   * _count_neighbors_kernel / _materialize_neighbors_kernel (:97-288), the exclusive scan
     (:1814-1815), far self-loop padding (_pad_self_loops_kernel :323-366, self_loop_padding
-    :1004-1027), the canonical sort (_sort_edges :1968-1999) and the overflow flag
+    :1004-1027), sink padding (_pad_edges_kernel :291-320), the exact-cutoff override
+    (HAS_OVERRIDE, :357-361), the canonical sort (_sort_edges :1968-1999) and the overflow flag
   * fixed_capacity_exceeded (:796-814) and the window flag fold (:430-455)
   * the three-body line graph: the short-bond flags of the materialization (:258-260), the
     undirected pairs of _materialize_pairs (:2001-2084), the short lists, pair offsets and
     overflow rule of _materialize_line_graph (:2086-2161) and the triplet rows of
-    _line_graph_kernel (:680-753), far self-loop padding (LOOP_PADDING), with the all-loop
-    overflow topology of _allocate_overflow_topology (:1474-1513)
+    _line_graph_kernel (:680-753), far self-loop padding (LOOP_PADDING) or sink padding, with
+    the all-loop / all-sink overflow topology of _allocate_overflow_topology (:1474-1513) and
+    its edge rows (_substitute_overflow_topology :2163-2177)
   * estimate_max_neighbors (fastmd/graph/neighbor_list_backend.py:77-88) and the ragged
     builder's slot growth rule (fastmd/graph/gpu_graph_builder.py:74-85)
 and an FP64 brute-force pair set (tests/test_fixed_capacity_boundary.py:86-102) that pins it.
@@ -185,9 +187,11 @@ class Build:
 
 
 def build(positions, inv_cell, cell, cand: Candidates, reference_positions, reference_wraps, rc2, skin_limit,
-          pad_image, e_cap: int, line2: float | None = None, minimum_image: bool = False) -> Build:
+          pad_image, e_cap: int, line2: float | None = None, minimum_image: bool = False, n_dummy: int = 0) -> Build:
     """One build over the candidate list (see module docstring); with ``line2`` (the float32
-    square of the bond cutoff) also the short-bond flag of every row. ``minimum_image``
+    square of the bond cutoff) also the short-bond flag of every row. ``n_dummy`` > 0: sink
+    padding (padded row r on sink n + p n_dummy // max(e_cap // 2 - ec // 2, 1), p = (r - ec) // 2,
+    image (3, 3, 3), distance 1e6); otherwise far self-loops with ``pad_image``. ``minimum_image``
     (fixed_capacity_builder.py:2233-2245): a lattice jump since the refresh is no motion; the
     displacement d loses jumps = round(d @ inv_cell) (float32, half to even) times the cell, and
     the jumps leave the wrap delta."""
@@ -237,10 +241,16 @@ def build(positions, inv_cell, cell, cand: Candidates, reference_positions, refe
     images[:ec] = img[:ec]
     distances[:ec] = np.sqrt(d2[:ec])
     pad = np.arange(ec, e_cap)
-    atoms = ((pad - ec) % n).astype(np.int32)
+    if n_dummy > 0:
+        pair = (pad - ec) // 2
+        atoms = (n + pair * n_dummy // max(e_cap // 2 - ec // 2, 1)).astype(np.int32)
+        images[ec:] = 3
+        distances[ec:] = F32(1.0e6)
+    else:
+        atoms = ((pad - ec) % n).astype(np.int32)
+        images[ec:] = np.asarray(pad_image, dtype=np.int32)
     center[ec:] = atoms
     neighbor[ec:] = atoms
-    images[ec:] = np.asarray(pad_image, dtype=np.int32)
     short = None
     if line2 is not None:
         short = np.zeros(e_cap, bool)
@@ -249,9 +259,21 @@ def build(positions, inv_cell, cell, cand: Candidates, reference_positions, refe
                  bool(total > e_cap or not valid), int((counts == 0).sum()), short)
 
 
-def line_graph(b: Build, rev, n: int, e_cap: int, u_cap: int, t_cap: int, bmax: int) -> dict:
+def pad_override(n_edges: int, e_cap: int, vector) -> np.ndarray:
+    """The exact-cutoff padding's edge-vector override [e_cap, 3] float32: ``vector`` on the padded
+    rows [min(n_edges, e_cap), e_cap), 0 on the real rows (fixed_capacity_builder.py:357-361)."""
+    out = np.zeros((e_cap, 3), F32)
+    out[min(n_edges, e_cap):] = np.asarray(vector, dtype=F32)
+    return out
+
+
+def line_graph(b: Build, rev, n: int, e_cap: int, u_cap: int, t_cap: int, bmax: int, n_dummy: int = 0,
+               pad_image=(0, 0, 0)) -> dict:
     """The line graph of a build (module docstring): d2u, u2d, invalid_pairs, short_counts,
-    short_offsets, short_edge_matrix, pair_offsets, overflow and the triplet rows."""
+    short_offsets, short_edge_matrix, pair_offsets, overflow and the triplet rows; with
+    ``n_dummy`` > 0 sink padding. Also the published edge rows center / neighbor / images: the
+    build's, or on overflow the all-padding rows (row e on pair e // 2's loop atom or sink, image
+    +/- ``pad_image`` or +/- (3, 3, 3) for even / odd e)."""
     total = b.n_edges
     ec = min(total, e_cap)
     ids = np.arange(e_cap, dtype=np.int64)
@@ -283,11 +305,22 @@ def line_graph(b: Build, rev, n: int, e_cap: int, u_cap: int, t_cap: int, bmax: 
     overflow = bool(total >= e_cap or pair_offsets[-1] > t_cap or invalid or not b.candidate_valid)
     lg = np.zeros((t_cap, 5), np.int64)
     t_ids = np.arange(t_cap, dtype=np.int64)
+    def overflow_atom(pair):
+        return n + pair * n_dummy // u_cap if n_dummy > 0 else pair % n
+
+    center, neighbor, images = b.center.copy(), b.neighbor.copy(), b.images.copy()
     if overflow:
-        lu = np.minimum(t_ids * u_cap // t_cap, u_cap - 1)
-        lg[:] = np.stack([lu % n, lu, 2 * lu, lu, 2 * lu], 1)
+        if n_dummy > 0:
+            lu = (t_ids * n_dummy // t_cap * u_cap + n_dummy - 1) // n_dummy
+        else:
+            lu = t_ids * u_cap // t_cap
+        lu = np.minimum(lu, u_cap - 1)
+        lg[:] = np.stack([overflow_atom(lu), lu, 2 * lu, lu, 2 * lu], 1)
         d2u = ids // 2
         u2d = 2 * u
+        center[:] = neighbor[:] = overflow_atom(ids // 2)
+        sign = np.where(ids % 2 == 0, 1, -1)[:, None]
+        images[:] = sign * (np.full(3, 3) if n_dummy > 0 else np.asarray(pad_image, dtype=np.int64))
     else:
         t_real = min(int(pair_offsets[-1]), t_cap)
         tr = t_ids[:t_real]
@@ -304,7 +337,8 @@ def line_graph(b: Build, rev, n: int, e_cap: int, u_cap: int, t_cap: int, bmax: 
         pad_id = t_ids[t_real:] - t_real
         pad_pair = pad_id % max(u_cap - real_u, 1)
         pu, pde = real_u + pad_pair, ec + 2 * pad_pair
-        lg[t_real:] = np.stack([pad_pair % n, pu, pde, pu, pde], 1)
+        pad_atom = n + pad_id * n_dummy // max(t_cap - t_real, 1) if n_dummy > 0 else pad_pair % n
+        lg[t_real:] = np.stack([pad_atom, pu, pde, pu, pde], 1)
     # segment layouts of the angle -> bond -> atom sums: row e (short, rank r among its atom's short
     # rows) is the first bond of triplets pair_offsets[i] + r (s_i - 1) + [0, s_i - 1)
     before = np.concatenate([[0], np.cumsum(short.astype(np.int64))])[:e_cap]  # short rows before e
@@ -327,7 +361,8 @@ def line_graph(b: Build, rev, n: int, e_cap: int, u_cap: int, t_cap: int, bmax: 
             "short_counts": s, "short_offsets": short_offsets, "short_edge_matrix": sem.astype(np.int32),
             "pair_offsets": pair_offsets, "overflow": overflow, "line_graph": lg.astype(np.int32),
             "edge_triplet_offsets": eto, "bond_rows": bond_rows.astype(np.int32),
-            "second_perm": second_perm.astype(np.int32)}
+            "second_perm": second_perm.astype(np.int32), "center": center.astype(np.int32),
+            "neighbor": neighbor.astype(np.int32), "images": images.astype(np.int32)}
 
 
 def triplet_set(center, neighbor, images, short, n_edges: int) -> set:

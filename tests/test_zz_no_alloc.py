@@ -25,13 +25,14 @@ def _outputs(builder):
 def _noalloc_args(builder, positions, out, n_atoms=None):
     from fastmd_amd import _abi
 
-    image = builder._pad_loop[0]
+    image = builder._pad_image
     return (positions.data_ptr(), 1, builder.inv_cell.data_ptr(), builder.cell.data_ptr(),
             builder.n_real if n_atoms is None else n_atoms, builder.neighbor_matrix.data_ptr(),
             builder.neighbor_shifts.data_ptr(), builder.num_neighbors.data_ptr(), builder.buffer_max,
             builder.reference_positions.data_ptr(), builder.reference_wraps.data_ptr(),
             builder._candidate_capacity_valid.data_ptr(), builder._rc2, builder._skin_limit,
-            1 if builder.minimum_image else 0, image[0], image[1], image[2], None, None, builder.e_capacity, out["frac_coords"].data_ptr(), out["wrap_delta"].data_ptr(),
+            1 if builder.minimum_image else 0, image[0], image[1], image[2], builder.n_dummy, None, None,
+            builder.e_capacity, out["frac_coords"].data_ptr(), out["wrap_delta"].data_ptr(),
             out["positions"].data_ptr(), out["edge_counts"].data_ptr(), out["edge_offsets"].data_ptr(),
             out["center"].data_ptr(), out["neighbor"].data_ptr(), out["images"].data_ptr(),
             out["distances"].data_ptr(), out["edge_index"].data_ptr(), out["edge_image"].data_ptr(),
