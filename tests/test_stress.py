@@ -137,8 +137,8 @@ def _gpu_adapter(name, device):
 @pytest.mark.parametrize("name,n_cells", [("morse", 3), ("mace_like", 3), ("threebody", 3), ("mace_like", (6, 6, 6))])
 def test_stress_gpu_matches_oracle(device, name, n_cells):
     """The "efs" task through the fixed-capacity builder (padding rows present) on a sheared,
-    rotated cell: stress within 1e-6 eV/A^3 + 1e-4 of the largest component of the FP64 oracle's
-    (the float32 edge gradients summed in float64; 1e-6 eV/A^3 is 0.16 MPa), symmetric, bitwise
+    rotated cell: stress within 1e-5 of the largest component of the FP64 oracle's (the float32
+    edge gradients summed in float64; measured 2e-7 .. 4e-7 of it), symmetric, bitwise
     reproducible; energy and forces bitwise those of the "ef" task."""
     from fastmd_amd.engine.energy_derivative import EnergyDerivative
 
@@ -167,4 +167,4 @@ def test_stress_gpu_matches_oracle(device, name, n_cells):
     err = float((stress.cpu().double() - ref).abs().max())
     scale = float(ref.abs().max())
     print(f"[stress] {name} cells={n_cells}: max|s| {scale:.3e} eV/A^3, max err {err:.3e}", flush=True)
-    assert err < 1e-6 + 1e-4 * scale
+    assert err < 1e-5 * scale
