@@ -28,7 +28,7 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 SPLIT_PRODUCTS = 6  # fp32-accurate GEMM: three bf16 planes per operand, six MFMA products
 SPIN_CYCLES = 20_000_000  # GPU clock cycles of torch.cuda._sleep (several ms)
-ROOFLINE_KERNEL = "gemm_x3p_dma_kernel"
+ROOFLINE_KERNEL = "message_bwd_edge_kernel<2, true, 8, true>"
 STEPS_PER_LAUNCH = 10
 
 
@@ -95,62 +95,57 @@ def time_kernel(fn, reps: int = 20) -> float:
     return start.elapsed_time(end) / 1e3 / reps
 
 
-def gemm_roofline(md) -> dict:
-    """The dominant kernel of the 10 000-atom step: the second layer's edge GEMM,
-    z = [h0[src] | ef] @ W1[sender and radial rows] (the receiver block h0[dst] @ W1[C:2C] is formed
-    per atom and added by the message kernels), with the gather-cat fused into the operand load
-    and the operands pre-split into bf16 planes (gemm_x3p_dma_kernel: [e_cap, C+8] x [C+8, 4C],
-    fp32-accurate as six bf16 MFMA products). It is timed in the context of the step: HIP events on
-    torch's current stream (the stream it is launched on) around every edge GEMM of 10 eager force
-    evaluations at the run's final state (its edge list, capacity and features), the model's own
-    timing hook; each evaluation is queued behind a spin kernel so that no host latency falls
-    inside the event pairs. Algorithmic flops = 2 M K N per launch; the ceiling of fp32 work done
-    this way is the dense bf16 MFMA peak over the six products. ``isolated_launch_us`` is the same
-    launch repeated back to back."""
+def message_roofline(md) -> dict:
+    """The dominant kernel of the 10 000-atom step: the second layer's edge-side message VJP
+    (message_bwd_edge_kernel, node-factored pre-activation: per row the sender's P, h0, h1 rows
+    gathered, z rebuilt with the radial term, its gradient, the radial-basis and geometry
+    gradients; per atom the centre's Q, gA0, gA1 read and the sum of g_z written). It is timed
+    in the context of the step: HIP events on torch's current stream (the stream it is launched
+    on) around that launch alone in 10 eager force evaluations at the run's final state (its
+    edge list and features), the model's own timing hook; each evaluation is queued behind a
+    spin kernel so that no host latency falls inside the event pairs.
+    Algorithmic bytes per launch, counted as the gather-cat's formula counts them (every
+    gathered row once per edge that reads it): per real edge row 4 B neighbour index + 20 B
+    geometry (unit vector, length, cutoff) + 4 nb B basis + 4 (NZ + 4) C B of gathered sender
+    rows (P: NZ C, h0: C, h1: 3 C) + 16 B geometry-gradient store + 4 nb B basis-gradient store;
+    per atom 20 B offsets and order + 4 (NZ + 4) C B read (Q, gA0, gA1) + 4 NZ C B stored
+    (the per-centre sum of g_z), NZ = 4 (the last layer has vector features). The
+    ``unique_bytes`` alternative counts every input row once (a perfect cache)."""
     import torch
 
     from fastmd_amd.models import mace_like
-    from fastmd_amd.ops.wide_gemm import gemm_planes, split_planes
 
     runner = md.whole_step_runner
     torch.cuda.synchronize()
     time.sleep(0.03)  # an idle gap that separates the timed steps from these launches in a kernel trace
-    mace_like.EDGE_GEMM_EVENTS = events = []
+    mace_like.MESSAGE_EVENTS = events = []
     try:
         for _ in range(10):
             # a spin kernel ahead of each evaluation keeps the GPU busy while the host enqueues
-            # the evaluation's ~40 launches, so the GPU runs them back to back as in the captured
-            # step (no host-latency gaps inside the event pairs)
+            # the evaluation's launches, so the GPU runs them back to back as in the captured step
             torch.cuda._sleep(SPIN_CYCLES)
             runner._evaluate(md.integrator.positions)
         torch.cuda.synchronize()
     finally:
-        mace_like.EDGE_GEMM_EVENTS = None
-    m, k, n = events[-1][2]
-    durations = [a.elapsed_time(b) / 1e3 for a, b, shape in events if shape == (m, k, n)]
+        mace_like.MESSAGE_EVENTS = None
+    e_cap, n, C = events[-1][2]
+    durations = [a.elapsed_time(b) / 1e3 for a, b, shape in events if shape == (e_cap, n, C)]
     t = sum(durations) / len(durations)
-    time.sleep(0.03)
-    # the same launch back to back (inputs of the same shapes)
-    module = md.adapter.module
-    C = module.config.channels
-    ei = runner.builder.batch.edge_index
-    gen = torch.Generator(device="cpu").manual_seed(0)
-    h0p = split_planes(torch.randn(md.n_atoms, C, generator=gen).to(md.device))
-    efp = split_planes(torch.randn(m, k - C, generator=gen).to(md.device))
-    out = torch.empty(m, n, device=md.device)
-    w = module.w1_planes(len(module.layers) - 1, "sender", n)
-    t_iso = time_kernel(lambda: gemm_planes([(h0p, ei[:, 1]), (efp, None)], w, a_planes=True, out=out), reps=20)
-    flops = 2.0 * m * k * n
-    achieved = flops / t / 1e12
-    peak = BF16_MFMA_PEAK_TFLOPS / SPLIT_PRODUCTS
-    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
-            "frac": round(achieved / peak, 4), "traffic": _traffic(ROOFLINE_KERNEL, [m, k, n]),
+    edges = int(runner.builder.edge_offsets[-1].item())
+    rows = min(edges, e_cap)
+    nb, nz = md.adapter.module.config.n_basis, 4
+    per_row = 4 + 20 + 4 * nb + 4 * (nz + 4) * C + 16 + 4 * nb
+    per_atom = 20 + 4 * (nz + 4) * C + 4 * nz * C
+    algorithmic = rows * per_row + n * per_atom
+    unique = rows * (4 + 20 + 4 * nb + 16 + 4 * nb) + n * (20 + 4 * (nz + 4) * C + 4 * nz * C + 4 * (nz + 4) * C)
+    achieved = algorithmic / t / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _traffic(ROOFLINE_KERNEL, [rows, n, C]),
             "kernel": ROOFLINE_KERNEL, "launch_us": round(t * 1e6, 2), "launches_timed": len(durations),
-            "isolated_launch_us": round(t_iso * 1e6, 2), "flops_per_launch": flops,
-            "peak_basis": f"fp32 GEMM as {SPLIT_PRODUCTS} bf16 MFMA products: dense bf16 peak "
-                          f"{BF16_MFMA_PEAK_TFLOPS} TFLOP/s / {SPLIT_PRODUCTS}",
-            "frac_of_fp32_mfma_peak": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-            "algorithmic_bytes_per_launch": 4 * (m * k + n * k + m * n), "shape_mkn": [m, k, n]}
+            "rows": rows, "atoms": n, "bytes_per_launch": algorithmic,
+            "bytes_basis": f"per real edge row {per_row} B (gathered sender rows counted per row), per atom "
+                           f"{per_atom} B",
+            "unique_bytes_per_launch": unique, "unique_frac": round(unique / t / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
 def _traffic(kernel: str, shape: list):
@@ -533,10 +528,10 @@ def main() -> int:
                           "fp32_mfma_peak_TFLOPs": FP32_MFMA_PEAK_TFLOPS}), flush=True)
         return 0
     if args.roofline_only:
-        # the run profiled with rocprofv3 --pmc for the GEMM's HBM traffic: the dominant kernel at
+        # the run profiled with rocprofv3 --pmc for the dominant kernel's HBM traffic: it at
         # the 10 000-atom shape, then a plain 256 MiB device copy (the counters' calibration)
         md = build_md(10000, STEPS_PER_LAUNCH)
-        roof = gemm_roofline(md)
+        roof = message_roofline(md)
         src = torch.empty(64 << 20, device=md.device)
         dst = torch.empty_like(src)
         for _ in range(5):
@@ -553,7 +548,7 @@ def main() -> int:
     stats_big = md.whole_step_stats()
     events_big = md.timed_events
     log(f"10 000 atoms: {ms_big:.3f} ms/step {events_big}")
-    roof = gemm_roofline(md)
+    roof = message_roofline(md)
     del md
     torch.cuda.empty_cache()
 

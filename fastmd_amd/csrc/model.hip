@@ -229,15 +229,74 @@ __device__ __forceinline__ int64_t wave_rows(const int64_t* off, const int64_t* 
   return hi;
 }
 
-// CPL64 = C / 64 (the dispatch parameter); a lane holds CPL = 2 CPL64 channels of a half-wave's row
-template <int CPL64, bool H1>
+// Node-factored z (FZ): z_e = [h0_j | h0_i | ef_e] W1 is linear in its three blocks, so with
+// P = h0 W1[:C] and Q = h0 W1[C:2C] formed per atom ([N, NZ C] each, node GEMMs) a row is
+//   z_e = (P[j] + sum_n ef_e,n W1[2C + n]) + Q[i]
+// and no [E, NZ C] array is written or read: the kernels gather P by sender (the centre's Q once
+// per wave, or in the sender-side VJP the wave's own P once and Q by receiver) and add the radial
+// term from the edge's basis row and W1's radial rows staged in LDS ([RB, 4C], zero past nb).
+// The radial rows are applied to a group's rows together (each LDS read serves the group).
+template <int KP, int NZ, int CPL, int RB>
+__device__ __forceinline__ void add_radial(const float* s_w, int woff, const float (&er)[KP][RB],
+                                           float (&zr)[KP][NZ][CPL]) {
+  constexpr int C = 32 * CPL;
+  // two radial rows per step: unrolled whole, the scheduler would issue every LDS read up front
+  // and hold all RB * NZ * CPL weights in registers
+#pragma unroll 2
+  for (int t = 0; t < RB; ++t) {
+#pragma unroll
+    for (int b = 0; b < NZ; ++b) {
+      float wv[CPL];
+      load_ch<CPL>(s_w + t * 4 * C + b * C + woff, wv);
+#pragma unroll
+      for (int g = 0; g < KP; ++g)
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) zr[g][b][q] += er[g][t] * wv[q];
+    }
+  }
+}
+
+// the basis row of edge e (nb <= RB values, zero past nb)
+template <int RB>
+__device__ __forceinline__ void load_basis(const float* ef, int nb, int64_t e, float (&v)[RB]) {
+  const float* p = ef + e * nb;
+  if (nb == RB) {
+#pragma unroll
+    for (int t = 0; t < RB; t += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(p + t);
+      v[t] = x.x;
+      v[t + 1] = x.y;
+      v[t + 2] = x.z;
+      v[t + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < RB; ++t) v[t] = t < nb ? p[t] : 0.f;
+  }
+}
+
+// W1's radial rows [nb, 4C] into LDS as [RB, 4C], zero rows past nb (all threads of the block)
+__device__ __forceinline__ void stage_radial(float* s_w, const float* w1ef, int nb, int rb, int C) {
+  const int nbv = w1ef ? nb : 0;
+  for (int k = threadIdx.x; k < rb * 4 * C; k += blockDim.x) s_w[k] = k < nbv * 4 * C ? w1ef[k] : 0.f;
+  __syncthreads();
+}
+
+// CPL64 = C / 64 (the dispatch parameter); a lane holds CPL = 2 CPL64 channels of a half-wave's row.
+// FZ: z is node-factored (P = z, Q = zq, radial rows w1ef and basis ef; RB > 0), else z holds
+// the edge rows and zq, when given, the receiver block per atom.
+template <int CPL64, bool H1, bool FZ, int RB>
 __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const float* zq, const float* geo,
                                                            const int32_t* edge_index, const int64_t* off,
                                                            const int64_t* n_edges, int64_t e_cap, int64_t n,
                                                            const int32_t* order, const float* h0, const float* h1,
-                                                           float inv_avg, float* A0, float* A1) {
+                                                           float inv_avg, float* A0, float* A1, const float* ef,
+                                                           const float* w1ef, int nb) {
   constexpr int CPL = 2 * CPL64, C = 32 * CPL;
   constexpr int NZ = H1 ? 4 : 2;  // z blocks in a row
+  constexpr int RBV = FZ ? RB : 1;
+  extern __shared__ float s_w[];  // FZ: [RB, 4C]
+  if constexpr (FZ) stage_radial(s_w, w1ef, nb, RB, C);
   const int lane = threadIdx.x & 63;
   const bool upper = lane >= 32;
   const int64_t il = fmd_xcd_block(blockIdx.x, gridDim.x) * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
@@ -268,6 +327,7 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
     for (int u0 = 0; u0 < cnt; u0 += 2 * kPairs) {
       float zr[kPairs][NZ][CPL], hj[kPairs][CPL], hv[kPairs][3][CPL];
       float ux[kPairs], uy[kPairs], uz[kPairs], fc[kPairs];
+      float er[kPairs][RBV];
 #pragma unroll
       for (int g = 0; g < kPairs; ++g) {
         const int r0 = u0 + 2 * g, s0 = r0 < cnt ? r0 : cnt - 1, s1 = r0 + 1 < cnt ? r0 + 1 : cnt - 1;
@@ -279,14 +339,20 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
         uz[g] = bcast2(m.uz, s0, s1, upper);
         const float f = bcast2(m.fc, s0, s1, upper);
         fc[g] = valid ? f : 0.f;  // a row past the end adds exact zeros
-        const float* ze = z + (base + s) * (NZ * C) + c0;
+        const float* ze = FZ ? z + j * (NZ * C) + c0 : z + (base + s) * (NZ * C) + c0;
 #pragma unroll
         for (int b = 0; b < NZ; ++b) load_ch<CPL>(ze + b * C, zr[g][b]);
+        if constexpr (FZ) load_basis<RBV>(ef, nb, base + s, er[g]);
         load_ch<CPL>(h0 + j * C + c0, hj[g]);
         if (H1) {
 #pragma unroll
           for (int x = 0; x < 3; ++x) load_ch<CPL>(h1 + (j * 3 + x) * C + c0, hv[g][x]);
         }
+      }
+      if constexpr (FZ) {
+        int woff = c0;
+        asm volatile("" : "+v"(woff));  // keeps the radial rows in LDS, not in registers
+        add_radial<kPairs, NZ, CPL, RBV>(s_w, woff, er, zr);
       }
 #pragma unroll
       for (int g = 0; g < kPairs; ++g) {
@@ -347,23 +413,22 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
 // row (radial gradients and geometry) are reduced over its half-wave.
 constexpr int kMaxBasis = 16;
 
-template <int CPL64, bool H1, int RB>
+template <int CPL64, bool H1, int RB, bool FZ>
 __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     const float* z, const float* zq, const float* geo, const int32_t* edge_index, const int64_t* off,
     const int64_t* n_edges, int64_t e_cap, int64_t n, const int32_t* order, const float* h0, const float* h1,
     const float* gA0, const float* gA1, float inv_avg, float* gz, float* gzsum, float* ggeo, int accumulate_geo,
-    const float* w1ef, int nb, float* gef) {
+    const float* w1ef, int nb, float* gef, const float* ef) {
   constexpr int CPL = 2 * CPL64, C = 32 * CPL;
   constexpr int NZ = H1 ? 4 : 2;
   constexpr int kPairs = H1 ? 1 : 2;  // row pairs per load group (registers: three waves per SIMD)
   // w1ef's rows padded to RB (8 or 16) with zero rows (all zero without w1ef): the radial sums
-  // run over RB rows without a branch per row
+  // run over RB rows without a branch per row; FZ: the same rows form z's radial term
   extern __shared__ float s_w[];  // [RB, 4C]
   const int lane = threadIdx.x & 63;
   const bool upper = lane >= 32;
   const int nbv = w1ef ? nb : 0;
-  for (int k = threadIdx.x; k < RB * 4 * C; k += blockDim.x) s_w[k] = k < nbv * 4 * C ? w1ef[k] : 0.f;
-  __syncthreads();
+  stage_radial(s_w, w1ef, nb, RB, C);
   const int64_t il = fmd_xcd_block(blockIdx.x, gridDim.x) * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   if (il >= n) return;
   const int64_t i = order ? order[il] : il;  // the atom of this wave (a spatial order keeps gathers in L2)
@@ -410,6 +475,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     for (int u0 = 0; u0 < cnt; u0 += 2 * kPairs) {
       float zr[kPairs][NZ][CPL], hj[kPairs][CPL], hv[kPairs][3][CPL];
       float ux[kPairs], uy[kPairs], uz[kPairs], fc[kPairs];
+      float er[kPairs][FZ ? RB : 1];
 #pragma unroll
       for (int g = 0; g < kPairs; ++g) {
         const int r0 = u0 + 2 * g, s0 = r0 < cnt ? r0 : cnt - 1, s1 = r0 + 1 < cnt ? r0 + 1 : cnt - 1;
@@ -421,14 +487,20 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
         uz[g] = bcast2(m.uz, s0, s1, upper);
         const float f = bcast2(m.fc, s0, s1, upper);
         fc[g] = valid ? f : 0.f;  // a row past the end adds exact zeros
-        const float* ze = z + (base + s) * (NZ * C) + c0;
+        const float* ze = FZ ? z + j * (NZ * C) + c0 : z + (base + s) * (NZ * C) + c0;
 #pragma unroll
         for (int b = 0; b < NZ; ++b) load_ch<CPL>(ze + b * C, zr[g][b]);
+        if constexpr (FZ) load_basis<RB>(ef, nb, base + s, er[g]);
         load_ch<CPL>(h0 + j * C + c0, hj[g]);
         if (H1) {
 #pragma unroll
           for (int x = 0; x < 3; ++x) load_ch<CPL>(h1 + (j * 3 + x) * C + c0, hv[g][x]);
         }
+      }
+      if constexpr (FZ) {
+        int woff = c0;
+        asm volatile("" : "+v"(woff));
+        add_radial<kPairs, NZ, CPL, RB>(s_w, woff, er, zr);
       }
 #pragma unroll
       for (int g = 0; g < kPairs; ++g) {
@@ -552,15 +624,18 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
 // row as in message_kernel: per 64 rows the wave loads reverse[e'], the receiver and the
 // geometry of e once (a lane per row); each group of kPairs row pairs issues its z[e], zq[i],
 // gA0[i] and gA1[i] loads before any arithmetic.
-template <int CPL64, bool H1>
+template <int CPL64, bool H1, bool FZ, int RB>
 __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
     const float* z, const float* zq, const float* geo, const int32_t* edge_index, const int32_t* reverse,
     const int64_t* off, const int64_t* n_edges, int64_t e_cap, int64_t n, const int32_t* order, const float* h0,
     const float* h1, const float* gA0, const float* gA1, float inv_avg, float* gh0, float* gh1, int accumulate,
-    float* gzsum_src) {
+    float* gzsum_src, const float* ef, const float* w1ef, int nb) {
   constexpr int CPL = 2 * CPL64, C = 32 * CPL;
   constexpr int NZ = H1 ? 4 : 2;
   constexpr int kPairs = H1 ? 1 : 2;  // row pairs per load group (registers: three waves per SIMD)
+  constexpr int RBV = FZ ? RB : 1;
+  extern __shared__ float s_w[];  // FZ: [RB, 4C]
+  if constexpr (FZ) stage_radial(s_w, w1ef, nb, RB, C);
   const int lane = threadIdx.x & 63;
   const bool upper = lane >= 32;
   const int64_t jl = fmd_xcd_block(blockIdx.x, gridDim.x) * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
@@ -587,6 +662,11 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
       for (int x = 0; x < 3; ++x) load_ch<CPL>(h1 + (jn * 3 + x) * C + c0, hsv[x]);
     }
   }
+  float pz[FZ ? NZ : 1][CPL];  // FZ: the sender block of z of every row here (P[jn])
+  if constexpr (FZ) {
+#pragma unroll
+    for (int b = 0; b < NZ; ++b) load_ch<CPL>(z + jn * (NZ * C) + b * C + c0, pz[b]);
+  }
   for (int64_t base = lo; base < hi; base += 64) {
     const int cnt = (int)(hi - base < 64 ? hi - base : 64);
     int me = -1, mi = 0;
@@ -606,6 +686,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
     for (int u0 = 0; u0 < cnt; u0 += 2 * kPairs) {
       float zr[kPairs][NZ][CPL], qe[kPairs][NZ][CPL], ga[kPairs][4][CPL];
       float ux[kPairs], uy[kPairs], uz[kPairs], fc[kPairs];
+      float eb[kPairs][RBV];
 #pragma unroll
       for (int g = 0; g < kPairs; ++g) {
         const int r0 = u0 + 2 * g, s0 = r0 < cnt ? r0 : cnt - 1, s1 = r0 + 1 < cnt ? r0 + 1 : cnt - 1;
@@ -620,9 +701,15 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
         // rows past the end and missing reverse rows add exact zeros (fc = 0)
         fc[g] = valid && er >= 0 ? f : 0.f;
         const float* ze = z + e * (NZ * C) + c0;
+        if constexpr (FZ) load_basis<RBV>(ef, nb, e, eb[g]);  // the basis of row e (its own length)
 #pragma unroll
         for (int b = 0; b < NZ; ++b) {
-          load_ch<CPL>(ze + b * C, zr[g][b]);
+          if constexpr (FZ) {
+#pragma unroll
+            for (int q = 0; q < CPL; ++q) zr[g][b][q] = pz[b][q];
+          } else {
+            load_ch<CPL>(ze + b * C, zr[g][b]);
+          }
           if (zq) {
             load_ch<CPL>(zq + i * (NZ * C) + b * C + c0, qe[g][b]);  // the receiver block of z[e] (row i)
           } else {
@@ -633,6 +720,11 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
         load_ch<CPL>(gA0 + i * C + c0, ga[g][0]);
 #pragma unroll
         for (int x = 0; x < 3; ++x) load_ch<CPL>(gA1 + (i * 3 + x) * C + c0, ga[g][1 + x]);
+      }
+      if constexpr (FZ) {
+        int woff = c0;
+        asm volatile("" : "+v"(woff));
+        add_radial<kPairs, NZ, CPL, RBV>(s_w, woff, eb, zr);
       }
 #pragma unroll
       for (int g = 0; g < kPairs; ++g) {
@@ -922,16 +1014,31 @@ __global__ void virial_stress_kernel(const double* part, const float* cell, floa
 }
 
 template <int CPL>
-int launch_message(bool h1, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
-                   const int32_t* ei,
-                   const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const int32_t* order,
-                   const float* h0, const float* h1p, float inv_avg, float* A0, float* A1) {
-  if (h1)
-    hipLaunchKernelGGL((message_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, off, ne, e_cap, n,
-                       order, h0, h1p, inv_avg, A0, A1);
-  else
-    hipLaunchKernelGGL((message_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, off, ne, e_cap, n,
-                       order, h0, h1p, inv_avg, A0, A1);
+int launch_message(bool h1, bool fz, int rb, dim3 grid, hipStream_t s, const float* z, const float* zq,
+                   const float* geo, const int32_t* ei, const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n,
+                   const int32_t* order, const float* h0, const float* h1p, float inv_avg, float* A0, float* A1,
+                   const float* ef, const float* w1ef, int nb) {
+  const size_t lds = fz ? (size_t)rb * 4 * 64 * CPL * sizeof(float) : 0;  // [RB, 4C]
+#define FMD_MSG(H, F, R)                                                                                          \
+  hipLaunchKernelGGL((message_kernel<CPL, H, F, R>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne, e_cap, n, \
+                     order, h0, h1p, inv_avg, A0, A1, ef, w1ef, nb)
+  if (!fz) {
+    if (h1)
+      FMD_MSG(true, false, 0);
+    else
+      FMD_MSG(false, false, 0);
+  } else if (rb == 8) {
+    if (h1)
+      FMD_MSG(true, true, 8);
+    else
+      FMD_MSG(false, true, 8);
+  } else {
+    if (h1)
+      FMD_MSG(true, true, 16);
+    else
+      FMD_MSG(false, true, 16);
+  }
+#undef FMD_MSG
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -959,40 +1066,63 @@ static uintptr_t channel_alignment(int channels) { return channels <= 64 ? 8 : 1
 
 namespace {
 template <int CPL>
-int launch_bwd_edge(bool h1, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
-                    const int32_t* ei,
-                    const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n, const int32_t* order,
-                    const float* h0, const float* h1p, const float* gA0, const float* gA1, float inv_avg, float* gz,
-                    float* gzsum, float* ggeo, int acc, const float* w1ef, int nb, float* gef) {
+int launch_bwd_edge(bool h1, bool fz, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
+                    const int32_t* ei, const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n,
+                    const int32_t* order, const float* h0, const float* h1p, const float* gA0, const float* gA1,
+                    float inv_avg, float* gz, float* gzsum, float* ggeo, int acc, const float* w1ef, int nb, float* gef,
+                    const float* ef) {
   const bool wide = w1ef && nb > 8;  // radial rows padded to 16 instead of 8
   const size_t lds = (size_t)(wide ? 16 : 8) * 4 * 64 * CPL * sizeof(float);  // RB x 4C floats
-#define FMD_BWD_EDGE(H, RB)                                                                                         \
-  hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, H, RB>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne,  \
-                     e_cap, n, order, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef)
-  if (h1 && wide)
-    FMD_BWD_EDGE(true, 16);
-  else if (h1)
-    FMD_BWD_EDGE(true, 8);
-  else if (wide)
-    FMD_BWD_EDGE(false, 16);
-  else
-    FMD_BWD_EDGE(false, 8);
+#define FMD_BWD_EDGE(H, RB, F)                                                                                       \
+  hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, H, RB, F>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne, \
+                     e_cap, n, order, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef, ef)
+#define FMD_BWD_EDGE_F(H, RB) \
+  if (fz)                     \
+    FMD_BWD_EDGE(H, RB, true); \
+  else                        \
+    FMD_BWD_EDGE(H, RB, false)
+  if (h1 && wide) {
+    FMD_BWD_EDGE_F(true, 16);
+  } else if (h1) {
+    FMD_BWD_EDGE_F(true, 8);
+  } else if (wide) {
+    FMD_BWD_EDGE_F(false, 16);
+  } else {
+    FMD_BWD_EDGE_F(false, 8);
+  }
+#undef FMD_BWD_EDGE_F
 #undef FMD_BWD_EDGE
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
 
 template <int CPL>
-int launch_bwd_src(bool h1, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
-                   const int32_t* ei, const int32_t* rev, const int64_t* off, const int64_t* ne, int64_t e_cap,
-                   int64_t n, const int32_t* order, const float* h0, const float* h1p, const float* gA0,
-                   const float* gA1, float inv_avg, float* gh0, float* gh1, int acc, float* gzsum_src) {
-  if (h1)
-    hipLaunchKernelGGL((message_bwd_src_kernel<CPL, true>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, rev, off, ne,
-                       e_cap, n, order, h0, h1p, gA0, gA1, inv_avg, gh0, gh1, acc, gzsum_src);
-  else
-    hipLaunchKernelGGL((message_bwd_src_kernel<CPL, false>), grid, dim3(kThreads), 0, s, z, zq, geo, ei, rev, off, ne,
-                       e_cap, n, order, h0, h1p, gA0, gA1, inv_avg, gh0, gh1, acc, gzsum_src);
+int launch_bwd_src(bool h1, bool fz, int rb, dim3 grid, hipStream_t s, const float* z, const float* zq,
+                   const float* geo, const int32_t* ei, const int32_t* rev, const int64_t* off, const int64_t* ne,
+                   int64_t e_cap, int64_t n, const int32_t* order, const float* h0, const float* h1p, const float* gA0,
+                   const float* gA1, float inv_avg, float* gh0, float* gh1, int acc, float* gzsum_src, const float* ef,
+                   const float* w1ef, int nb) {
+  const size_t lds = fz ? (size_t)rb * 4 * 64 * CPL * sizeof(float) : 0;
+#define FMD_BWD_SRC(H, F, R)                                                                                        \
+  hipLaunchKernelGGL((message_bwd_src_kernel<CPL, H, F, R>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, rev, off, \
+                     ne, e_cap, n, order, h0, h1p, gA0, gA1, inv_avg, gh0, gh1, acc, gzsum_src, ef, w1ef, nb)
+  if (!fz) {
+    if (h1)
+      FMD_BWD_SRC(true, false, 0);
+    else
+      FMD_BWD_SRC(false, false, 0);
+  } else if (rb == 8) {
+    if (h1)
+      FMD_BWD_SRC(true, true, 8);
+    else
+      FMD_BWD_SRC(false, true, 8);
+  } else {
+    if (h1)
+      FMD_BWD_SRC(true, true, 16);
+    else
+      FMD_BWD_SRC(false, true, 16);
+  }
+#undef FMD_BWD_SRC
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -1026,13 +1156,16 @@ int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, co
 int fmd_mace_message_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
                          const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
                          const int32_t* order, int32_t channels, const float* h0, const float* h1, float inv_avg,
-                         float* A0, float* A1, hipStream_t stream) {
+                         float* A0, float* A1, int32_t z_per_node, const float* ef, const float* w1ef, int32_t nb,
+                         hipStream_t stream) {
   FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && A0 && A1 && n_atoms >= 0);
-  FMD_REQUIRE(aligned_to(channel_alignment(channels), {z, zq, h0, h1, A0, A1}) && aligned_to(16, {geo}));
+  FMD_REQUIRE(!z_per_node || (zq && ef && w1ef && nb > 0 && nb <= kMaxBasis));
+  FMD_REQUIRE(aligned_to(channel_alignment(channels), {z, zq, h0, h1, A0, A1}) && aligned_to(16, {geo, ef}));
   if (n_atoms == 0) return FMD_OK;
   dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
-  FMD_CPL_DISPATCH(channels, launch_message, h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets,
-                   n_edges, e_cap, n_atoms, order, h0, h1, inv_avg, A0, A1);
+  const int rb = nb > 8 ? 16 : 8;
+  FMD_CPL_DISPATCH(channels, launch_message, h1 != nullptr, z_per_node != 0, rb, grid, stream, z, zq, geo, edge_index,
+                   edge_offsets, n_edges, e_cap, n_atoms, order, h0, h1, inv_avg, A0, A1, ef, w1ef, nb);
 }
 
 int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
@@ -1042,33 +1175,45 @@ int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, 
                              const float* gA0, const float* gA1,
                              float inv_avg, float* gz, float* gzsum, float* gzsum_src, float* ggeo,
                              int32_t accumulate_geo, float* gh0, float* gh1, int32_t accumulate_h, const float* w1ef,
-                             int32_t nb, float* gef, hipStream_t stream) {
+                             int32_t nb, float* gef, int32_t z_per_node, const float* ef, hipStream_t stream) {
   FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && gA0 && gA1 && ggeo && n_atoms >= 0);
   FMD_REQUIRE(gz || w1ef || gzsum);
   FMD_REQUIRE(!w1ef || (gef && nb > 0 && nb <= kMaxBasis));
+  FMD_REQUIRE(!z_per_node || (zq && ef && w1ef && !gz));
   FMD_REQUIRE(!(gh0 || gzsum_src) || reverse);
   FMD_REQUIRE(aligned_to(channel_alignment(channels), {z, zq, h0, h1, gA0, gA1, gz, gzsum, gzsum_src, gh0, gh1}) &&
-              aligned_to(16, {geo, ggeo}));
+              aligned_to(16, {geo, ggeo, ef}));
   if (n_atoms == 0) return FMD_OK;
   dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
+  const bool fz = z_per_node != 0;
+  const int rb = nb > 8 ? 16 : 8;
+  // accumulate_h bit 2: the sender-side kernel alone (the edge side ran in a call before)
+  const bool sender_only = (accumulate_h & 4) != 0;
+  accumulate_h &= 3;
   int rc = FMD_OK;
-  switch (channels / 64) {
-    case 1: rc = launch_bwd_edge<1>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges, e_cap,
-                                    n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
-    case 2: rc = launch_bwd_edge<2>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges, e_cap,
-                                    n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
-    case 4: rc = launch_bwd_edge<4>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges, e_cap,
-                                    n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo, w1ef, nb, gef); break;
+  if (!sender_only) switch (channels / 64) {
+    case 1: rc = launch_bwd_edge<1>(h1 != nullptr, fz, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges,
+                                    e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo,
+                                    w1ef, nb, gef, ef); break;
+    case 2: rc = launch_bwd_edge<2>(h1 != nullptr, fz, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges,
+                                    e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo,
+                                    w1ef, nb, gef, ef); break;
+    case 4: rc = launch_bwd_edge<4>(h1 != nullptr, fz, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges,
+                                    e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo,
+                                    w1ef, nb, gef, ef); break;
     default: return FMD_EUNSUPPORTED;
   }
   if (rc != FMD_OK || !(gh0 || gzsum_src)) return rc;
   switch (channels / 64) {
-    case 1: return launch_bwd_src<1>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets, n_edges,
-                                     e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h, gzsum_src);
-    case 2: return launch_bwd_src<2>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets, n_edges,
-                                     e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h, gzsum_src);
-    case 4: return launch_bwd_src<4>(h1 != nullptr, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets, n_edges,
-                                     e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h, gzsum_src);
+    case 1: return launch_bwd_src<1>(h1 != nullptr, fz, rb, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets,
+                                     n_edges, e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h,
+                                     gzsum_src, ef, w1ef, nb);
+    case 2: return launch_bwd_src<2>(h1 != nullptr, fz, rb, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets,
+                                     n_edges, e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h,
+                                     gzsum_src, ef, w1ef, nb);
+    case 4: return launch_bwd_src<4>(h1 != nullptr, fz, rb, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets,
+                                     n_edges, e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h,
+                                     gzsum_src, ef, w1ef, nb);
     default: return FMD_EUNSUPPORTED;
   }
 }

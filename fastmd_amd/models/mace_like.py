@@ -54,10 +54,20 @@ HOIST_MIN_ROWS = 16384
 # at 135 atoms, 73 / 117 us at 10 000) than the six short launches it replaces; kept tested
 # against the oracle beside the chain.
 FUSED_NODE = False
+# Node-factored edge pre-activation: z_e = [h0_j | h0_i | ef_e] W1 is linear in its blocks, so the
+# layer forms P = h0 W1[:C] and Q = h0 W1[C:2C] per atom (node GEMMs; the first layer's, of the
+# element embedding, as per-element tables) and the message kernels add the radial term
+# ef_e W1[2C:] per row: no [E, 4C] edge array is written or read and no edge GEMM runs. Off: z
+# is the edge GEMM over the gather-cat rows (the configs' wide-GEMM operator on the path), kept
+# tested against the oracle beside the factored form.
+FACTORED_Z = True
 # Timing hook of the edge GEMM launches: when a list, each eager (uncaptured) forward appends
 # (start event, end event, (M, K, N)) recorded around its edge GEMMs on the current stream. The
 # benchmark uses it to time the dominant kernel in the context of the step; None in normal runs.
 EDGE_GEMM_EVENTS: list | None = None
+# Timing hook of the last layer's edge-side message VJP (the step's longest launch): when a list,
+# each eager VJP appends (start event, end event, (e_cap, n, C)) recorded around that launch alone.
+MESSAGE_EVENTS: list | None = None
 
 
 @dataclass(frozen=True)
@@ -198,10 +208,39 @@ class MaceLike(nn.Module):
             cache[t] = hit
         return hit[1]
 
+    def w1_sender_node_t(self, t: int) -> Tensor:
+        """The sender rows of W1 ([0, C)) stored K-contiguous ([4C, C]): the B operand of the
+        node-factored P = h0 W1[:C]."""
+        w = self.layers[t].W1
+        C = self.config.channels
+        key = (w.data_ptr(), w._version, w.device)
+        cache = self.__dict__.setdefault("_w1sn_cache", {})
+        hit = cache.get(t)
+        if hit is None or hit[0] != key:
+            hit = (key, w.detach()[:C].t().contiguous())
+            cache[t] = hit
+        return hit[1]
+
+    def first_layer_pq(self) -> tuple[Tensor, Tensor]:
+        """The first layer's node-factored blocks per element, embedding @ W1[:C, :2C] and
+        embedding @ W1[C:2C, :2C] ([elements, 2C] each; the first layer's input is the embedding,
+        so P and Q of an atom depend on its element only), formed in float64 and rounded once;
+        rebuilt when either weight changes in place."""
+        mats = (self.embedding, self.layers[0].W1)
+        key = tuple((w.data_ptr(), w._version, w.device) for w in mats)
+        hit = self.__dict__.get("_pq0_cache")
+        if hit is None or hit[0] != key:
+            C = self.config.channels
+            emb, w1 = self.embedding.detach().double(), self.layers[0].W1.detach().double()
+            tables = ((emb @ w1[:C, :2 * C]).float().contiguous(), (emb @ w1[C:2 * C, :2 * C]).float().contiguous())
+            hit = (key, tables)
+            self.__dict__["_pq0_cache"] = hit
+        return hit[1]
+
     def w1_planes(self, t: int, which: str, nz: int = 0) -> Planes:
         """bf16 planes (split once per W1 version) of the weights of layer t's edge GEMMs when the
-        operands come pre-split: "receiver" / "sender" = the first nz rows of w1_receiver_t /
-        w1_sender_t (the forward's [nz, K] B operands)."""
+        operands come pre-split: "receiver" / "sender" / "sender_node" = the first nz rows of
+        w1_receiver_t / w1_sender_t / w1_sender_node_t (the forward's [nz, K] B operands)."""
         w = self.layers[t].W1
         key = (w.data_ptr(), w._version, w.device)
         cache = self.__dict__.setdefault("_w1p_cache", {})
@@ -212,6 +251,8 @@ class MaceLike(nn.Module):
                 src = self.w1_receiver_t(t)[:nz]
             elif which == "sender":
                 src = self.w1_sender_t(t)[:nz]
+            elif which == "sender_node":
+                src = self.w1_sender_node_t(t)[:nz]
             else:
                 raise ValueError(f"unknown W1 block {which!r}")
             hit = (key, split_planes(src))
@@ -273,6 +314,24 @@ def _gather_edge_rows(h0: Tensor, ef: Tensor, edge_index: Tensor, out: Tensor) -
               out.stride(0), _abi.stream_handle())
 
 
+def _factored_blocks(model: MaceLike, t: int, h0: Tensor, elem: Tensor, n: int, nz: int, dev) -> tuple:
+    """(P, Q) = (h0 W1[:C, :nz], h0 W1[C:2C, :nz]) of layer t ([n, nz] each): the first layer's
+    rows from the per-element tables, later layers' by one grouped node GEMM on pre-split weights."""
+    P = _empty(n, nz, device=dev)
+    Q = _empty(n, nz, device=dev)
+    if t == 0:
+        tp, tq = model.first_layer_pq()
+        if nz != tp.shape[1]:
+            raise ValueError("the first layer's pre-activation has the a | b blocks only")
+        _call("fmd_embed_f32", elem.data_ptr(), tp.data_ptr(), n, nz, P.data_ptr())
+        _call("fmd_embed_f32", elem.data_ptr(), tq.data_ptr(), n, nz, Q.data_ptr())
+        return P, Q
+    ws, wr = model.w1_sender_node_t(t)[:nz], model.w1_receiver_t(t)[:nz]
+    gemm_group([{"a": h0, "b": ws, "b_planes": model.w1_planes(t, "sender_node", nz), "out": P},
+                {"a": h0, "b": wr, "b_planes": model.w1_planes(t, "receiver", nz), "out": Q}], b_layout=0)
+    return P, Q
+
+
 class _MaceLikeEnergy(Function):
     """positions -> node energies [rows]; backward: dE/dpos by the VJP kernels."""
 
@@ -307,8 +366,10 @@ class _MaceLikeEnergy(Function):
         # On large edge lists the edge GEMMs take pre-split operands: the radial rows once per
         # evaluation here, h0 once per layer, the weights once per version (bitwise the same z as
         # splitting inside the GEMM, without the splitting arithmetic per output tile)
-        hoist = e_cap >= HOIST_MIN_ROWS
+        factored = FACTORED_Z
+        hoist = e_cap >= HOIST_MIN_ROWS and not factored
         efp = split_planes(ef) if hoist else None
+        w1ef_all = [layer.W1[2 * C:] for layer in model.layers]
         for t, layer in enumerate(model.layers):
             last = t == L - 1
             # z = [h0[src] | h0[dst] | ef] @ W1 ([E, 4C]), the gather-cat fused into the edge GEMM's
@@ -316,10 +377,18 @@ class _MaceLikeEnergy(Function):
             # every row of a centre, is formed once per atom (q, [N, 4C]) and added by the message
             # kernels, and the edge GEMM multiplies [h0[src] | ef] (K = C + nb).
             # Without vector features (h1 = 0, the first layer) wc and wd multiply only zeros: z keeps
-            # just its a | b blocks ([E, 2C], the first 2C columns of W1).
+            # just its a | b blocks ([E, 2C], the first 2C columns of W1). Node-factored (the
+            # default): z = P, q = Q per atom and the kernels add the radial term per row.
             timed = EDGE_GEMM_EVENTS is not None and not torch.cuda.is_current_stream_capturing()
             nz = 4 * C if h1 is not None else 2 * C
-            if hoist:
+            if factored:
+                z, q = _factored_blocks(model, t, h0, elem, n, nz, dev)
+                A0 = _empty(n, C, device=dev)
+                A1 = _empty(n, 3, C, device=dev)
+                _call("fmd_mace_message_f32", z.data_ptr(), q.data_ptr(), geo.data_ptr(), ei.data_ptr(),
+                      off.data_ptr(), n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1), inv_avg,
+                      A0.data_ptr(), A1.data_ptr(), 1, ef.data_ptr(), w1ef_all[t].data_ptr(), nb)
+            elif hoist:
                 h0p = split_planes(h0)
                 q = gemm_planes([(h0p, None)], model.w1_planes(t, "receiver", nz), a_planes=True)
                 w1p = model.w1_planes(t, "sender", nz)
@@ -328,21 +397,22 @@ class _MaceLikeEnergy(Function):
                 q = None
                 parts, w1 = [(h0, ei[:, 1]), (h0, ei[:, 0]), (ef, None)], model.w1_t(t)[:nz]
                 shape = (e_cap, w1.shape[1], nz)
-            if timed:
-                ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                ev[0].record()
-            if hoist:
-                z = gemm_planes([(h0p, ei[:, 1]), (efp, None)], w1p, a_planes=True)
-            else:
-                z = gemm_gather(parts, w1)
-            if timed:
-                ev[1].record()
-                EDGE_GEMM_EVENTS.append((ev[0], ev[1], shape))
-            A0 = _empty(n, C, device=dev)
-            A1 = _empty(n, 3, C, device=dev)
-            _call("fmd_mace_message_f32", z.data_ptr(), _abi.ptr(q), geo.data_ptr(), ei.data_ptr(), off.data_ptr(),
-                  n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1), inv_avg, A0.data_ptr(),
-                  A1.data_ptr())
+            if not factored:
+                if timed:
+                    ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                    ev[0].record()
+                if hoist:
+                    z = gemm_planes([(h0p, ei[:, 1]), (efp, None)], w1p, a_planes=True)
+                else:
+                    z = gemm_gather(parts, w1)
+                if timed:
+                    ev[1].record()
+                    EDGE_GEMM_EVENTS.append((ev[0], ev[1], shape))
+                A0 = _empty(n, C, device=dev)
+                A1 = _empty(n, 3, C, device=dev)
+                _call("fmd_mace_message_f32", z.data_ptr(), _abi.ptr(q), geo.data_ptr(), ei.data_ptr(),
+                      off.data_ptr(), n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1), inv_avg,
+                      A0.data_ptr(), A1.data_ptr(), 0, None, None, 0)
             B0 = _empty(n, C, device=dev)
             B1 = None if last else _empty(n, 3, C, device=dev)
             if FUSED_NODE:
@@ -391,7 +461,7 @@ class _MaceLikeEnergy(Function):
         _call("fmd_mace_energy_f32", h_first.data_ptr(), model.wr1.data_ptr(), y.data_ptr(), model.wr2b.data_ptr(),
               C, H, elem.data_ptr(), model.e0.data_ptr(), float(cfg.scale), float(cfg.shift), n, energy.data_ptr())
         ctx.model, ctx.inputs, ctx.saved = model, inputs, saved
-        ctx.geo, ctx.de, ctx.y = geo, de, y
+        ctx.geo, ctx.de, ctx.y, ctx.ef, ctx.factored = geo, de, y, ef, factored
         ctx.n, ctx.e_cap = n, e_cap
         return energy
 
@@ -487,7 +557,7 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
                   rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(),
                   _abi.ptr(h1), gA0.data_ptr(), gA1.data_ptr(), inv_avg, None, None, None, ggeo.data_ptr(), acc_geo,
                   None, None,
-                  0, w1ef.data_ptr(), nb, gef.data_ptr())
+                  0, w1ef.data_ptr(), nb, gef.data_ptr(), 1 if ctx.factored else 0, ctx.ef.data_ptr())
             gefs.append((gef, nb))
             break
         # the gather-cat row gradient's node blocks come from per-node sums of g_z (never stored):
@@ -502,10 +572,23 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
             g_in0 = gemm(g_out0, layer.Wsc0, b_layout=0, out=gha if t == 1 else None, accumulate=t == 1)
         g_in1 = _empty(n, 3, C, device=dev) if h1 is not None else None
         w1ef = layer.W1[2 * C:]
-        _call("fmd_mace_message_bwd_f32", z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(), ei.data_ptr(),
-              rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1),
-              gA0.data_ptr(), gA1.data_ptr(), inv_avg, None, gzs.data_ptr(), gzs_src.data_ptr(), ggeo.data_ptr(),
-              acc_geo, g_in0.data_ptr(), _abi.ptr(g_in1), 1, w1ef.data_ptr(), nb, gef.data_ptr())
+        head = (z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(), ei.data_ptr(), rev.data_ptr(), off.data_ptr(),
+                n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(), gA1.data_ptr(),
+                inv_avg, None, gzs.data_ptr())
+        tail = (w1ef.data_ptr(), nb, gef.data_ptr(), 1 if ctx.factored else 0, ctx.ef.data_ptr())
+        if MESSAGE_EVENTS is not None and not torch.cuda.is_current_stream_capturing():
+            # timed: the edge side alone between events, then the sender side alone (the same two
+            # kernels and results as the single call)
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            ev[0].record()
+            _call("fmd_mace_message_bwd_f32", *head, None, ggeo.data_ptr(), acc_geo, None, None, 0, *tail)
+            ev[1].record()
+            MESSAGE_EVENTS.append((ev[0], ev[1], (e_cap, n, C)))
+            _call("fmd_mace_message_bwd_f32", *head, gzs_src.data_ptr(), ggeo.data_ptr(), acc_geo, g_in0.data_ptr(),
+                  _abi.ptr(g_in1), 1 | 4, *tail)
+        else:
+            _call("fmd_mace_message_bwd_f32", *head, gzs_src.data_ptr(), ggeo.data_ptr(), acc_geo, g_in0.data_ptr(),
+                  _abi.ptr(g_in1), 1, *tail)
         # g_in0 += [gzs_src | gzs] [W1[:C] | W1[C:2C]]^T (sender and receiver blocks, one node GEMM)
         gemm_splitk(gzs_src, model.w1_node_blocks(t), b_layout=0, out=g_in0, a2=gzs, accumulate=True)
         gefs.append((gef, nb))

@@ -261,13 +261,14 @@ def _gpu_builder(s, u_cap, device):
     (3, 128, None, False, "cubic"), (3, 256, None, False, "cubic"), ((6, 6, 6), 128, None, False, "cubic"),
     ((10, 10, 10), 128, None, False, "cubic"),
     (3, 128, None, False, "triclinic_rotated"), ((6, 6, 6), 128, None, False, "triclinic_rotated"),
-    ((6, 6, 6), 128, 0, False, "triclinic_rotated"),
-    ((10, 10, 20), 128, None, False, "cubic")])
+    ((6, 6, 6), 128, 0, False, "triclinic_rotated"), ((6, 6, 6), 64, 10 ** 9, False, "cubic"),
+    ((10, 10, 20), 128, None, False, "cubic"), ((10, 10, 20), 128, 0, False, "cubic")])
 def test_mace_like_gpu_matches_oracle(device, n_cells, channels, hoist, fused, geometry, monkeypatch):
     """Energies within 1e-5 eV/atom and forces within 1e-4 eV/A of the FP64 oracle, through the
-    fixed-capacity builder (padding rows present), bitwise reproducible. ``hoist`` overrides the
-    edge-list size from which the receiver block of the edge GEMM is formed per atom (0: always,
-    10**9: never), so both evaluation orders of z are checked at every width; ``fused`` selects the
+    fixed-capacity builder (padding rows present), bitwise reproducible. ``hoist`` None runs the
+    node-factored pre-activation (P, Q per atom, the radial term per row, no edge GEMM); a number
+    runs the edge GEMM form, with the receiver block formed per atom from that edge-list size
+    (0: always, 10**9: never), so every evaluation order of z is checked; ``fused`` selects the
     fused node kernels or the unfused chain of GEMMs and contraction kernels; at 5 000 atoms the
     unfused node GEMMs take their split-plane grouped form. ``triclinic_rotated`` puts the crystal
     in a sheared cell rotated as a whole (no cell axis along x, y or z); 10 x 10 x 20 cells is the
@@ -276,6 +277,7 @@ def test_mace_like_gpu_matches_oracle(device, n_cells, channels, hoist, fused, g
     from fastmd_amd.models import mace_like
     from fastmd_amd.models.mace_like import MaceLikeAdapter
 
+    monkeypatch.setattr(mace_like, "FACTORED_Z", hoist is None)
     if hoist is not None:
         monkeypatch.setattr(mace_like, "HOIST_MIN_ROWS", hoist)
     monkeypatch.setattr(mace_like, "FUSED_NODE", fused)
