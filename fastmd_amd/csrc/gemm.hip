@@ -620,8 +620,29 @@ __device__ __forceinline__ void x3_finish(f32x16 (&acc)[MB][2], const X3Part& ra
         }
       }
   }
-  if (!bias && !accumulate && act == 0 && row0 + 32 * MB <= m && col0 + 64 <= n) {
+  if (!bias && act == 0 && row0 + 32 * MB <= m && col0 + 64 <= n) {
     float* base = c + (row0 + h * 4) * ldc + col0 + rr;
+    if (accumulate) {
+      // every old value loaded before any store: one memory round trip, not one per row (the
+      // stores could alias the loads, so the compiler keeps a load-add-store chain in order)
+#pragma unroll
+      for (int bi = 0; bi < MB; ++bi) {
+        float old[16][2];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float* rp = base + (int64_t)(bi * 32 + (v / 4) * 8 + (v % 4)) * ldc;
+          old[v][0] = rp[0];
+          old[v][1] = rp[32];
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          float* rp = base + (int64_t)(bi * 32 + (v / 4) * 8 + (v % 4)) * ldc;
+          rp[0] = old[v][0] + acc[bi][0][v];
+          rp[32] = old[v][1] + acc[bi][1][v];
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int bi = 0; bi < MB; ++bi)
 #pragma unroll
@@ -965,7 +986,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
   const int64_t t = w - d.tile0;
   const X3Part none{};
   x3p_tile<MB>(d.p0, d.p1, d.p1, d.np, d.b, d.ldb, none, d.bias, d.c, d.ldc, d.m, d.n, d.k, d.accumulate,
-                      grp.act, (t / d.n_tiles) * (64 * MB), (t % d.n_tiles) * 128);
+               grp.act, (t / d.n_tiles) * (64 * MB), (t % d.n_tiles) * 128);
 }
 
 #undef XP_LOAD

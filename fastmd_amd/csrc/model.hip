@@ -907,6 +907,31 @@ __global__ void embed_kernel(const int32_t* elem, const float* table, int64_t n,
   h0[k] = table[(int64_t)elem[i] * C + (k - i * C)];
 }
 
+// Several per-element tables gathered in one launch: out_g[i] = table_g[elem[i]] (widths in
+// float4 units); one thread per float4 of the concatenated rows of an atom.
+constexpr int kMaxEmbed = 8;
+struct EmbedSet {
+  const float4* table[kMaxEmbed];
+  float4* out[kMaxEmbed];
+  int width4[kMaxEmbed];
+  int start4[kMaxEmbed + 1];
+  int count;
+};
+
+__global__ void embed_rows_kernel(const int32_t* elem, int64_t n, const EmbedSet s) {
+  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int total = s.start4[s.count];
+  if (k >= n * total) return;
+  const int64_t i = k / total;
+  int c = (int)(k - i * total);
+  int g = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxEmbed; ++q)
+    if (q < s.count && c >= s.start4[q]) g = q;
+  c -= s.start4[g];
+  s.out[g][i * s.width4[g] + c] = s.table[g][(int64_t)elem[i] * s.width4[g] + c];
+}
+
 // ------------------------------------------------------------------------------------------
 // Morse pair potential, shifted to zero at the cutoff: per centre node (one thread per node):
 //   E_i = 1/2 sum_e V(r_e),  V = D[(1 - exp(-a(r - r0)))^2 - 1] - V_rc (r < rc, else 0)
@@ -1269,6 +1294,27 @@ int fmd_embed_f32(const int32_t* elem, const float* table, int64_t n_atoms, int3
   if (n_atoms == 0) return FMD_OK;
   hipLaunchKernelGGL(embed_kernel, dim3((unsigned)fmd_cdiv(n_atoms * channels, 256)), dim3(256), 0, stream, elem,
                      table, n_atoms, channels, h0);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_embed_rows_f32(const int32_t* elem, int64_t n_atoms, int32_t count, const float* const* tables,
+                       const int32_t* widths, float* const* outs, hipStream_t stream) {
+  FMD_REQUIRE(elem && n_atoms >= 0 && count >= 1 && count <= kMaxEmbed && tables && widths && outs);
+  EmbedSet set{};
+  set.count = count;
+  set.start4[0] = 0;
+  for (int g = 0; g < count; ++g) {
+    FMD_REQUIRE(tables[g] && outs[g] && widths[g] > 0 && widths[g] % 4 == 0);
+    FMD_REQUIRE(aligned_to(16, {tables[g], outs[g]}));
+    set.table[g] = reinterpret_cast<const float4*>(tables[g]);
+    set.out[g] = reinterpret_cast<float4*>(outs[g]);
+    set.width4[g] = widths[g] / 4;
+    set.start4[g + 1] = set.start4[g] + widths[g] / 4;
+  }
+  if (n_atoms == 0) return FMD_OK;
+  hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)fmd_cdiv(n_atoms * set.start4[count], 256)), dim3(256), 0,
+                     stream, elem, n_atoms, set);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -61,6 +61,11 @@ FUSED_NODE = False
 # is the edge GEMM over the gather-cat rows (the configs' wide-GEMM operator on the path), kept
 # tested against the oracle beside the factored form.
 FACTORED_Z = True
+# Merged node side (node-factored, unfused, two or more layers): a layer's output GEMM launch
+# also forms the next layer's P and Q, the last one the readout's first product (its h0n is
+# never formed), and the first layer's per-element rows come from one gather launch. Off: one
+# launch per product, as the unmerged chain (kept tested against the oracle).
+MERGED_NODE = True
 # Timing hook of the edge GEMM launches: when a list, each eager (uncaptured) forward appends
 # (start event, end event, (M, K, N)) recorded around its edge GEMMs on the current stream. The
 # benchmark uses it to time the dominant kernel in the context of the step; None in normal runs.
@@ -221,6 +226,50 @@ class MaceLike(nn.Module):
             cache[t] = hit
         return hit[1]
 
+    def merged_weights(self) -> dict:
+        """Products of consecutive weights for the merged node side (float64, rounded once, with
+        the bf16 planes of the GEMM operands; rebuilt when any weight changes in place):
+          "pq_next"[t] (t < L - 1): the next layer's P and Q straight from this layer's
+            [B0 | h0] (h0n = B0 Wo0 + h0 Wsc0, so h0n W1' = B0 (Wo0 W1') + h0 (Wsc0 W1')), as
+            [N, K] operands: (Wo0 W1'[:, :4C])^T ([4C, C]) in the first layer, whose residual
+            enters as a per-element table, and ([Wo0; Wsc0] W1'[:, :4C])^T ([4C, 2C]) later;
+          "y": the readout's first product from the last layer's [B0 | h0], ([Wo0; Wsc0] Wr2a)^T
+            ([H, 2C]), so the last h0n is never formed;
+          "gy": (Wo0 Wr2a, Wsc0 Wr2a) of the last layer ([C, H] each): its VJP's first products
+            straight from dE/dy;
+          "tables": the first layer's per-element rows: the residual embedding Wsc0 ([nel, C]) and
+            its next-layer blocks (embedding Wsc0) W1'[:C / C:2C, :4C] ([nel, 4C] each)."""
+        mats = [self.embedding, self.Wr2a] + [w for layer in self.layers for w in (layer.W1, layer.Wo0, layer.Wsc0)]
+        key = tuple((w.data_ptr(), w._version, w.device) for w in mats)
+        hit = self.__dict__.get("_merged_cache")
+        if hit is None or hit[0] != key:
+            C, L = self.config.channels, len(self.layers)
+            d64 = lambda w: w.detach().double()  # noqa: E731
+            f32 = lambda x: x.float().contiguous()  # noqa: E731
+            out = {"pq_next": {}, "tables": {}}
+            skip64 = d64(self.embedding) @ d64(self.layers[0].Wsc0)
+            for t in range(L - 1):
+                w1n = d64(self.layers[t + 1].W1)
+                ws, wr = w1n[:C, :4 * C], w1n[C:2 * C, :4 * C]
+                wo0, wsc0 = d64(self.layers[t].Wo0), d64(self.layers[t].Wsc0)
+                if t == 0:
+                    bp, bq = f32((wo0 @ ws).t()), f32((wo0 @ wr).t())
+                    out["tables"]["p_next"] = f32(skip64 @ ws)
+                    out["tables"]["q_next"] = f32(skip64 @ wr)
+                else:
+                    stack = torch.cat([wo0, wsc0], 0)
+                    bp, bq = f32((stack @ ws).t()), f32((stack @ wr).t())
+                out["pq_next"][t] = (bp, bq, split_planes(bp), split_planes(bq))
+            last = self.layers[L - 1]
+            wr2a = d64(self.Wr2a)
+            out["y"] = f32((torch.cat([d64(last.Wo0), d64(last.Wsc0)], 0) @ wr2a).t())
+            gb, gs = f32(d64(last.Wo0) @ wr2a), f32(d64(last.Wsc0) @ wr2a)
+            out["gy"] = (gb, gs)
+            out["tables"]["skip"] = f32(skip64)
+            hit = (key, out)
+            self.__dict__["_merged_cache"] = hit
+        return hit[1]
+
     def first_layer_pq(self) -> tuple[Tensor, Tensor]:
         """The first layer's node-factored blocks per element, embedding @ W1[:C, :2C] and
         embedding @ W1[C:2C, :2C] ([elements, 2C] each; the first layer's input is the embedding,
@@ -357,16 +406,38 @@ class _MaceLikeEnergy(Function):
         _call("fmd_edge_geometry_f32", positions.data_ptr(), cell.data_ptr(), system_rows(batch), ei.data_ptr(),
               batch.edge_image.data_ptr(), n_edges.data_ptr(), e_cap, float(cfg.cutoff), nb, geo.data_ptr(),
               ef.data_ptr(), de.data_ptr())
-        h0 = _empty(n, C, device=dev)
-        _call("fmd_embed_f32", elem.data_ptr(), model.embedding.data_ptr(), n, C, h0.data_ptr())
         h1 = None
         saved = []
         h_first = None
         L = len(model.layers)
+        factored = FACTORED_Z
+        # merged node side (node-factored, unfused, two or more layers): each layer's output GEMM
+        # launch also forms the next layer's P and Q (from [B0 | h0] with the products of
+        # consecutive weights), the last one the readout's y instead of h0n; the first layer's
+        # per-element rows (embedding, its P and Q, the residual table and its next-layer blocks,
+        # the prefills of h0n and of the next P and Q) come from one gather launch
+        merged = MERGED_NODE and factored and not FUSED_NODE and L >= 2
+        h0 = _empty(n, C, device=dev)
+        pq_next = None
+        if merged:
+            mw = model.merged_weights()
+            tp, tq = model.first_layer_pq()
+            tabs = mw["tables"]
+            P = _empty(n, 2 * C, device=dev)
+            Q = _empty(n, 2 * C, device=dev)
+            h0n_first = _empty(n, C, device=dev)
+            pq_next = (_empty(n, 4 * C, device=dev), _empty(n, 4 * C, device=dev))
+            rows = [(model.embedding, C, h0), (tp, 2 * C, P), (tq, 2 * C, Q), (tabs["skip"], C, h0n_first),
+                    (tabs["p_next"], 4 * C, pq_next[0]), (tabs["q_next"], 4 * C, pq_next[1])]
+            _call("fmd_embed_rows_f32", elem.data_ptr(), n, len(rows), _abi.ptr_array([r[0].data_ptr() for r in rows]),
+                  _abi.array(_abi._i32, [r[1] for r in rows]), _abi.ptr_array([r[2].data_ptr() for r in rows]))
+            z, q = P, Q
+        else:
+            _call("fmd_embed_f32", elem.data_ptr(), model.embedding.data_ptr(), n, C, h0.data_ptr())
+        y = None
         # On large edge lists the edge GEMMs take pre-split operands: the radial rows once per
         # evaluation here, h0 once per layer, the weights once per version (bitwise the same z as
         # splitting inside the GEMM, without the splitting arithmetic per output tile)
-        factored = FACTORED_Z
         hoist = e_cap >= HOIST_MIN_ROWS and not factored
         efp = split_planes(ef) if hoist else None
         w1ef_all = [layer.W1[2 * C:] for layer in model.layers]
@@ -382,7 +453,8 @@ class _MaceLikeEnergy(Function):
             timed = EDGE_GEMM_EVENTS is not None and not torch.cuda.is_current_stream_capturing()
             nz = 4 * C if h1 is not None else 2 * C
             if factored:
-                z, q = _factored_blocks(model, t, h0, elem, n, nz, dev)
+                if not merged:
+                    z, q = _factored_blocks(model, t, h0, elem, n, nz, dev)
                 A0 = _empty(n, C, device=dev)
                 A1 = _empty(n, 3, C, device=dev)
                 _call("fmd_mace_message_f32", z.data_ptr(), q.data_ptr(), geo.data_ptr(), ei.data_ptr(),
@@ -439,29 +511,53 @@ class _MaceLikeEnergy(Function):
                              "out": P1.view(3 * n, C)}], b_layout=0)
                 _call("fmd_mace_symcon_f32", P0.data_ptr(), P1.data_ptr(), elem.data_ptr(), layer.Wc.data_ptr(),
                       layer.Wd.data_ptr(), n, C, B0.data_ptr(), _abi.ptr(B1))
-                h0n = _empty(n, C, device=dev)
+                h0n = None if merged and last else (h0n_first if merged and t == 0 else _empty(n, C, device=dev))
                 h1n = None if last else _empty(n, 3, C, device=dev)
-                if t == 0:
+                if merged and last:
+                    # the readout's first product from [B0 | h0]: the last layer's h0n is not formed
+                    y = _empty(n, H, device=dev)
+                    gemm_group([{"a": B0, "a2": h0, "b": mw["y"], "out": y}], b_layout=0)
+                elif merged:
+                    # h0n, h1n and the next layer's P and Q in one launch (the first layer's h0n and
+                    # P, Q prefilled with their per-element residual rows)
+                    bp, bq, bpp, bqp = mw["pq_next"][t]
+                    P_n, Q_n = pq_next if t == 0 else (_empty(n, 4 * C, device=dev), _empty(n, 4 * C, device=dev))
+                    if t == 0:
+                        probs = [{"a": B0, "b": w["wo0t"], "b_planes": wp["wo0t"], "out": h0n, "accumulate": True},
+                                 {"a": B0, "b": bp, "b_planes": bpp, "out": P_n, "accumulate": True},
+                                 {"a": B0, "b": bq, "b_planes": bqp, "out": Q_n, "accumulate": True}]
+                    else:
+                        probs = [{"a": B0, "a2": h0, "b": w["wout0"], "b_planes": wp["wout0"], "out": h0n},
+                                 {"a": B0, "a2": h0, "b": bp, "b_planes": bpp, "out": P_n},
+                                 {"a": B0, "a2": h0, "b": bq, "b_planes": bqp, "out": Q_n}]
+                    probs.append({"a": B1.view(3 * n, C), "b": w["wo1t"], "b_planes": wp["wo1t"],
+                                  "out": h1n.view(3 * n, C)})
+                    gemm_group(probs, b_layout=0)
+                elif t == 0:
                     # h0 is the embedding: the residual h0 Wsc0 is a per-element table (rounded
                     # once), added to B0 Wo0 in the GEMM's epilogue
                     _call("fmd_embed_f32", elem.data_ptr(), model.skip_table().data_ptr(), n, C, h0n.data_ptr())
                     probs = [{"a": B0, "b": w["wo0t"], "b_planes": wp["wo0t"], "out": h0n, "accumulate": True}]
                 else:
                     probs = [{"a": B0, "a2": h0, "b": w["wout0"], "b_planes": wp["wout0"], "out": h0n}]
-                if not last:
-                    probs.append({"a": B1.view(3 * n, C), "b": w["wo1t"], "b_planes": wp["wo1t"],
-                                  "out": h1n.view(3 * n, C)})
-                gemm_group(probs, b_layout=0)
+                if not merged:
+                    if not last:
+                        probs.append({"a": B1.view(3 * n, C), "b": w["wo1t"], "b_planes": wp["wo1t"],
+                                      "out": h1n.view(3 * n, C)})
+                    gemm_group(probs, b_layout=0)
             saved.append((h0, h1, z, q, P0, P1))
             if t == 0:
                 h_first = h0n
+            if merged and not last:
+                z, q = P_n, Q_n
             h0, h1 = h0n, h1n
-        y = gemm(h0, model.Wr2a, b_layout=1)  # [N, H]
+        if y is None:
+            y = gemm(h0, model.Wr2a, b_layout=1)  # [N, H]
         energy = _empty(n, device=dev)
         _call("fmd_mace_energy_f32", h_first.data_ptr(), model.wr1.data_ptr(), y.data_ptr(), model.wr2b.data_ptr(),
               C, H, elem.data_ptr(), model.e0.data_ptr(), float(cfg.scale), float(cfg.shift), n, energy.data_ptr())
         ctx.model, ctx.inputs, ctx.saved = model, inputs, saved
-        ctx.geo, ctx.de, ctx.y, ctx.ef, ctx.factored = geo, de, y, ef, factored
+        ctx.geo, ctx.de, ctx.y, ctx.ef, ctx.factored, ctx.merged = geo, de, y, ef, factored, merged
         ctx.n, ctx.e_cap = n, e_cap
         return energy
 
@@ -495,7 +591,9 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
           C, H, float(cfg.scale), n, gha.data_ptr(), gy.data_ptr())
     # dE/dh0 out of the last layer (with one layer, the first readout's gradient joins here)
     L = len(model.layers)
-    g_out0 = gemm(gy, model.Wr2a, b_layout=0, out=gha if L == 1 else None, accumulate=L == 1)
+    # merged: the last layer's h0n was never formed; its VJP's first products start from gy
+    g_out0 = None if ctx.merged else gemm(gy, model.Wr2a, b_layout=0, out=gha if L == 1 else None,
+                                          accumulate=L == 1)
     g_out1 = None  # dE/dh1 out of the current layer (the last layer's h1 out is unused)
     ggeo = _empty(e_cap, 4, device=dev)
     gefs = []
@@ -529,14 +627,22 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
             wp = model.node_weights(t)["planes"]
             gB0 = _empty(n, C, device=dev)
             gB1 = None if g_out1 is None else _empty(n, 3, C, device=dev)
-            probs = [{"a": g_out0, "b": layer.Wo0, "b_planes": wp["Wo0"], "out": gB0}]
-            if gB1 is not None:
-                probs.append({"a": g_out1.reshape(3 * n, C), "b": layer.Wo1, "b_planes": wp["Wo1"],
-                              "out": gB1.view(3 * n, C)})
-            if t > 0:
+            if g_out0 is None:
+                # the last layer under the merged node side: gB0 = gy (Wo0 Wr2a)^T and the residual's
+                # g_in0 = gy (Wsc0 Wr2a)^T (gy [N, H]: K = H)
+                gb, gs = model.merged_weights()["gy"]
                 g_in0 = gha if t == 1 else _empty(n, C, device=dev)
-                probs.append({"a": g_out0, "b": layer.Wsc0, "b_planes": wp["Wsc0"], "out": g_in0,
-                              "accumulate": t == 1})
+                probs = [{"a": gy, "b": gb, "out": gB0},
+                         {"a": gy, "b": gs, "out": g_in0, "accumulate": t == 1}]
+            else:
+                probs = [{"a": g_out0, "b": layer.Wo0, "b_planes": wp["Wo0"], "out": gB0}]
+                if gB1 is not None:
+                    probs.append({"a": g_out1.reshape(3 * n, C), "b": layer.Wo1, "b_planes": wp["Wo1"],
+                                  "out": gB1.view(3 * n, C)})
+                if t > 0:
+                    g_in0 = gha if t == 1 else _empty(n, C, device=dev)
+                    probs.append({"a": g_out0, "b": layer.Wsc0, "b_planes": wp["Wsc0"], "out": g_in0,
+                                  "accumulate": t == 1})
             gemm_group(probs, b_layout=0)
             _call("fmd_mace_symcon_bwd_f32", P0.data_ptr(), P1.data_ptr(), inputs.elem.data_ptr(),
                   layer.Wc.data_ptr(), layer.Wd.data_ptr(), gB0.data_ptr(), _abi.ptr(gB1), n, C, gP0.data_ptr(),

@@ -578,6 +578,11 @@ int fmd_mace_energy_bwd_f32(const float* gE, const float* wr1, const float* y, c
 /* h0[i] = table[elem[i]]. */
 int fmd_embed_f32(const int32_t* elem, const float* table, int64_t n_atoms, int32_t channels, float* h0,
                   hipStream_t stream);
+/* Up to eight per-element tables gathered in one launch: outs[g][i, :] = tables[g][elem[i], :]
+ * ([n_atoms, widths[g]] each; widths a multiple of 4, every pointer 16-byte aligned): the first
+ * layer's per-element rows (embedding, node-factored pre-activation blocks, residual tables). */
+int fmd_embed_rows_f32(const int32_t* elem, int64_t n_atoms, int32_t count, const float* const* tables,
+                       const int32_t* widths, float* const* outs, hipStream_t stream);
 /* Morse pair potential (shifted to 0 at rc): E_i = 1/2 sum V(r_e) over the rows of centre i,
  * dvdr[e] = V'(r_e); VJP gvec[e] = 1/2 gE[centre] V'(r) u. */
 int fmd_morse_f32(const float* geo, const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap,
