@@ -86,9 +86,9 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_edge_geometry_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _f32, _i32, _p, _p, _p, _p]),
     "fmd_edge_geometry_bwd_f32": (ctypes.c_int, [_p, _p, _i32, _p, _i64, _p, _i64, _p, _p, _i64, _p, _p]),
     "fmd_mace_message_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _i64, _p, _i32, _p, _p, _f32, _p, _p, _i32,
-                                            _p, _p, _i32, _p]),
+                                            _p, _p, _i32, _i32, _p]),
     "fmd_mace_message_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _i32, _p, _p, _p, _p, _f32,
-                                                _p, _p, _p, _p, _i32, _p, _p, _i32, _p, _i32, _p, _i32, _p, _p]),
+                                                _p, _p, _p, _p, _i32, _p, _p, _i32, _p, _i32, _p, _i32, _p, _i32, _p]),
     "fmd_mace_node_fwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p, _p, _p,
                                              _p, _p]),
     "fmd_mace_node_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32,

@@ -134,6 +134,9 @@ class GraphBatch:
     # a permutation of the atom rows in a spatial (Morton) order, refreshed with the candidates:
     # kernels that take one atom per wave visit them in this order (same results, L2 locality)
     atom_order: Tensor | None = None
+    # rows of the largest system in the batch (replica or slot union; 0: all rows one system):
+    # kernels whose arithmetic is chosen by system size choose it by this
+    max_system_rows: int = 0
 
     @property
     def edge_dst(self) -> Tensor:

@@ -229,6 +229,38 @@ __device__ __forceinline__ int64_t wave_rows(const int64_t* off, const int64_t* 
   return hi;
 }
 
+// Several waves per atom (WPA > 1, small systems, where one wave per atom leaves most of the
+// chip idle and each wave walks its rows one after the other): wave `sub` of an atom takes the
+// row pairs sub, sub + WPA, ... of each 64-row chunk, and the per-atom sums are added over the
+// atom's waves in wave order through LDS (fixed order: deterministic; a different association
+// than one wave per atom, so the choice is made per system size, not per launch).
+// v[k][q] (channels c0 + q of vector k, the same in both halves) becomes the sum over the waves.
+template <int WPA, int NV, int CPL>
+__device__ __forceinline__ void reduce_waves(float (&v)[NV][CPL], float* s_red, int wib, int sub, int lane) {
+  if constexpr (WPA > 1) {
+    constexpr int C = 32 * CPL;
+    const int c0 = (lane & 31) * CPL;
+    float* mine = s_red + wib * NV * C;
+    if (lane < 32) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) mine[k * C + c0 + q] = v[k][q];
+    }
+    __syncthreads();
+    const float* first = s_red + (wib - sub) * NV * C;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int q = 0; q < CPL; ++q) {
+        float t = first[k * C + c0 + q];
+#pragma unroll
+        for (int w = 1; w < WPA; ++w) t += first[(w * NV + k) * C + c0 + q];
+        v[k][q] = t;
+      }
+  }
+}
+
 // Node-factored z (FZ): z_e = [h0_j | h0_i | ef_e] W1 is linear in its three blocks, so with
 // P = h0 W1[:C] and Q = h0 W1[C:2C] formed per atom ([N, NZ C] each, node GEMMs) a row is
 //   z_e = (P[j] + sum_n ef_e,n W1[2C + n]) + Q[i]
@@ -285,7 +317,7 @@ __device__ __forceinline__ void stage_radial(float* s_w, const float* w1ef, int 
 // CPL64 = C / 64 (the dispatch parameter); a lane holds CPL = 2 CPL64 channels of a half-wave's row.
 // FZ: z is node-factored (P = z, Q = zq, radial rows w1ef and basis ef; RB > 0), else z holds
 // the edge rows and zq, when given, the receiver block per atom.
-template <int CPL64, bool H1, bool FZ, int RB>
+template <int CPL64, bool H1, bool FZ, int RB, int WPA>
 __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const float* zq, const float* geo,
                                                            const int32_t* edge_index, const int64_t* off,
                                                            const int64_t* n_edges, int64_t e_cap, int64_t n,
@@ -296,14 +328,18 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
   constexpr int NZ = H1 ? 4 : 2;  // z blocks in a row
   constexpr int RBV = FZ ? RB : 1;
   extern __shared__ float s_w[];  // FZ: [RB, 4C]
+  __shared__ float s_red[WPA > 1 ? kWaves * 4 * C : 1];
   if constexpr (FZ) stage_radial(s_w, w1ef, nb, RB, C);
   const int lane = threadIdx.x & 63;
   const bool upper = lane >= 32;
-  const int64_t il = fmd_xcd_block(blockIdx.x, gridDim.x) * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-  if (il >= n) return;
-  const int64_t i = order ? order[il] : il;  // the atom of this wave (a spatial order keeps gathers in L2)
+  const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), sub = wib % WPA;
+  const int64_t il = fmd_xcd_block(blockIdx.x, gridDim.x) * (kWaves / WPA) + wib / WPA;
+  if (WPA == 1 && il >= n) return;
+  const bool active = il < n;  // WPA > 1: an idle wave still takes part in the reduction
+  const int64_t i = active ? (order ? order[il] : il) : 0;  // a spatial order keeps gathers in L2
   int64_t lo;
-  const int64_t hi = wave_rows(off, n_edges, e_cap, i, lo);
+  int64_t hi = wave_rows(off, n_edges, e_cap, i, lo);
+  if (!active) hi = lo;
   const int c0 = (lane & 31) * CPL;
   float a0[CPL], a1[3][CPL];
 #pragma unroll
@@ -324,7 +360,7 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
   for (int64_t base = lo; base < hi; base += 64) {
     const int cnt = (int)(hi - base < 64 ? hi - base : 64);
     const RowGeo m = row_geo(geo, edge_index, base + lane, lane < cnt);
-    for (int u0 = 0; u0 < cnt; u0 += 2 * kPairs) {
+    for (int u0 = 2 * kPairs * sub; u0 < cnt; u0 += 2 * kPairs * WPA) {
       float zr[kPairs][NZ][CPL], hj[kPairs][CPL], hv[kPairs][3][CPL];
       float ux[kPairs], uy[kPairs], uz[kPairs], fc[kPairs];
       float er[kPairs][RBV];
@@ -384,13 +420,23 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
       }
     }
   }
+  float red[4][CPL];
 #pragma unroll
   for (int q = 0; q < CPL; ++q) {
-    a0[q] = add_halves(a0[q]) * inv_avg;
-    a1[0][q] = add_halves(a1[0][q]) * inv_avg;
-    a1[1][q] = add_halves(a1[1][q]) * inv_avg;
-    a1[2][q] = add_halves(a1[2][q]) * inv_avg;
+    red[0][q] = add_halves(a0[q]);
+    red[1][q] = add_halves(a1[0][q]);
+    red[2][q] = add_halves(a1[1][q]);
+    red[3][q] = add_halves(a1[2][q]);
   }
+  reduce_waves<WPA, 4, CPL>(red, s_red, wib, sub, lane);
+#pragma unroll
+  for (int q = 0; q < CPL; ++q) {
+    a0[q] = red[0][q] * inv_avg;
+    a1[0][q] = red[1][q] * inv_avg;
+    a1[1][q] = red[2][q] * inv_avg;
+    a1[2][q] = red[3][q] * inv_avg;
+  }
+  if (!active || sub != 0) return;
   // the lower half writes A0 and the x row of A1, the upper half the y and z rows
   if (!upper) {
     store_ch<CPL>(A0 + i * C + c0, a0);
@@ -413,7 +459,7 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
 // row (radial gradients and geometry) are reduced over its half-wave.
 constexpr int kMaxBasis = 16;
 
-template <int CPL64, bool H1, int RB, bool FZ>
+template <int CPL64, bool H1, int RB, bool FZ, int WPA>
 __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     const float* z, const float* zq, const float* geo, const int32_t* edge_index, const int64_t* off,
     const int64_t* n_edges, int64_t e_cap, int64_t n, const int32_t* order, const float* h0, const float* h1,
@@ -425,15 +471,19 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
   // w1ef's rows padded to RB (8 or 16) with zero rows (all zero without w1ef): the radial sums
   // run over RB rows without a branch per row; FZ: the same rows form z's radial term
   extern __shared__ float s_w[];  // [RB, 4C]
+  __shared__ float s_red[WPA > 1 ? kWaves * NZ * C : 1];
   const int lane = threadIdx.x & 63;
   const bool upper = lane >= 32;
   const int nbv = w1ef ? nb : 0;
   stage_radial(s_w, w1ef, nb, RB, C);
-  const int64_t il = fmd_xcd_block(blockIdx.x, gridDim.x) * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-  if (il >= n) return;
-  const int64_t i = order ? order[il] : il;  // the atom of this wave (a spatial order keeps gathers in L2)
+  const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), sub = wib % WPA;
+  const int64_t il = fmd_xcd_block(blockIdx.x, gridDim.x) * (kWaves / WPA) + wib / WPA;
+  if (WPA == 1 && il >= n) return;
+  const bool active = il < n;  // WPA > 1: an idle wave still takes part in the reduction
+  const int64_t i = active ? (order ? order[il] : il) : 0;  // a spatial order keeps gathers in L2
   int64_t lo;
-  const int64_t hi = wave_rows(off, n_edges, e_cap, i, lo);
+  int64_t hi = wave_rows(off, n_edges, e_cap, i, lo);
+  if (!active) hi = lo;
   const int c0 = (lane & 31) * CPL;
   float g0[CPL], g1[3][CPL];
   load_ch<CPL>(gA0 + i * C + c0, g0);
@@ -472,7 +522,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
       og[2] = t.z;
       og[3] = t.w;
     }
-    for (int u0 = 0; u0 < cnt; u0 += 2 * kPairs) {
+    for (int u0 = 2 * kPairs * sub; u0 < cnt; u0 += 2 * kPairs * WPA) {
       float zr[kPairs][NZ][CPL], hj[kPairs][CPL], hv[kPairs][3][CPL];
       float ux[kPairs], uy[kPairs], uz[kPairs], fc[kPairs];
       float er[kPairs][FZ ? RB : 1];
@@ -603,6 +653,8 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
     for (int b = 0; b < NZ; ++b)
 #pragma unroll
       for (int q = 0; q < CPL; ++q) gs[b][q] = add_halves(gs[b][q]);
+    reduce_waves<WPA, NZ, CPL>(gs, s_red, wib, sub, lane);
+    if (!active || sub != 0) return;
     // the lower half writes blocks 0 .. NZ / 2 - 1, the upper half the rest
     float* d = gzsum + i * NZ * C + c0;
 #pragma unroll
@@ -624,7 +676,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
 // row as in message_kernel: per 64 rows the wave loads reverse[e'], the receiver and the
 // geometry of e once (a lane per row); each group of kPairs row pairs issues its z[e], zq[i],
 // gA0[i] and gA1[i] loads before any arithmetic.
-template <int CPL64, bool H1, bool FZ, int RB>
+template <int CPL64, bool H1, bool FZ, int RB, int WPA>
 __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
     const float* z, const float* zq, const float* geo, const int32_t* edge_index, const int32_t* reverse,
     const int64_t* off, const int64_t* n_edges, int64_t e_cap, int64_t n, const int32_t* order, const float* h0,
@@ -635,14 +687,18 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
   constexpr int kPairs = H1 ? 1 : 2;  // row pairs per load group (registers: three waves per SIMD)
   constexpr int RBV = FZ ? RB : 1;
   extern __shared__ float s_w[];  // FZ: [RB, 4C]
+  __shared__ float s_red[WPA > 1 ? kWaves * (4 + NZ) * C : 1];
   if constexpr (FZ) stage_radial(s_w, w1ef, nb, RB, C);
   const int lane = threadIdx.x & 63;
   const bool upper = lane >= 32;
-  const int64_t jl = fmd_xcd_block(blockIdx.x, gridDim.x) * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-  if (jl >= n) return;
-  const int64_t jn = order ? order[jl] : jl;  // the atom of this wave (a spatial order keeps gathers in L2)
+  const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), sub = wib % WPA;
+  const int64_t jl = fmd_xcd_block(blockIdx.x, gridDim.x) * (kWaves / WPA) + wib / WPA;
+  if (WPA == 1 && jl >= n) return;
+  const bool active = jl < n;  // WPA > 1: an idle wave still takes part in the reduction
+  const int64_t jn = active ? (order ? order[jl] : jl) : 0;  // a spatial order keeps gathers in L2
   int64_t lo;
-  const int64_t hi = wave_rows(off, n_edges, e_cap, jn, lo);
+  int64_t hi = wave_rows(off, n_edges, e_cap, jn, lo);
+  if (!active) hi = lo;
   const int c0 = (lane & 31) * CPL;
   float a0[CPL], a1[3][CPL], gsum[NZ][CPL];
 #pragma unroll
@@ -683,7 +739,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
         mfc = geo[8 * (int64_t)me + 4];
       }
     }
-    for (int u0 = 0; u0 < cnt; u0 += 2 * kPairs) {
+    for (int u0 = 2 * kPairs * sub; u0 < cnt; u0 += 2 * kPairs * WPA) {
       float zr[kPairs][NZ][CPL], qe[kPairs][NZ][CPL], ga[kPairs][4][CPL];
       float ux[kPairs], uy[kPairs], uz[kPairs], fc[kPairs];
       float eb[kPairs][RBV];
@@ -763,14 +819,29 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
       }
     }
   }
+  // the per-node sums: a0, a1 and (with gzsum_src) gsum, over the halves and the atom's waves
+  float red[4 + NZ][CPL];
 #pragma unroll
   for (int q = 0; q < CPL; ++q) {
-    a0[q] = add_halves(a0[q]) * inv_avg;
+    red[0][q] = add_halves(a0[q]);
+    red[1][q] = H1 ? add_halves(a1[0][q]) : 0.f;
+    red[2][q] = H1 ? add_halves(a1[1][q]) : 0.f;
+    red[3][q] = H1 ? add_halves(a1[2][q]) : 0.f;
+#pragma unroll
+    for (int b = 0; b < NZ; ++b) red[4 + b][q] = gzsum_src ? add_halves(gsum[b][q]) : 0.f;
+  }
+  reduce_waves<WPA, 4 + NZ, CPL>(red, s_red, wib, sub, lane);
+  if (!active || sub != 0) return;
+#pragma unroll
+  for (int q = 0; q < CPL; ++q) {
+    a0[q] = red[0][q] * inv_avg;
     if (H1) {
-      a1[0][q] = add_halves(a1[0][q]) * inv_avg;
-      a1[1][q] = add_halves(a1[1][q]) * inv_avg;
-      a1[2][q] = add_halves(a1[2][q]) * inv_avg;
+      a1[0][q] = red[1][q] * inv_avg;
+      a1[1][q] = red[2][q] * inv_avg;
+      a1[2][q] = red[3][q] * inv_avg;
     }
+#pragma unroll
+    for (int b = 0; b < NZ; ++b) gsum[b][q] = red[4 + b][q];
   }
   // the lower half writes gh0 and the x row of gh1, the upper half the y and z rows
   if (gh0 && !upper) {
@@ -807,7 +878,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
 #pragma unroll
     for (int b = 0; b < NZ; ++b)
 #pragma unroll
-      for (int q = 0; q < CPL; ++q) gsum[b][q] = add_halves(gsum[b][q]) * inv_avg;
+      for (int q = 0; q < CPL; ++q) gsum[b][q] = gsum[b][q] * inv_avg;
     // the lower half writes blocks 0 .. NZ / 2 - 1, the upper half the rest
     float* d = gzsum_src + jn * NZ * C + c0;
 #pragma unroll
@@ -1038,15 +1109,16 @@ __global__ void virial_stress_kernel(const double* part, const float* cell, floa
   }
 }
 
-template <int CPL>
-int launch_message(bool h1, bool fz, int rb, dim3 grid, hipStream_t s, const float* z, const float* zq,
+template <int CPL, int WPA>
+int launch_message(bool h1, bool fz, int rb, hipStream_t s, const float* z, const float* zq,
                    const float* geo, const int32_t* ei, const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n,
                    const int32_t* order, const float* h0, const float* h1p, float inv_avg, float* A0, float* A1,
                    const float* ef, const float* w1ef, int nb) {
   const size_t lds = fz ? (size_t)rb * 4 * 64 * CPL * sizeof(float) : 0;  // [RB, 4C]
-#define FMD_MSG(H, F, R)                                                                                          \
-  hipLaunchKernelGGL((message_kernel<CPL, H, F, R>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne, e_cap, n, \
-                     order, h0, h1p, inv_avg, A0, A1, ef, w1ef, nb)
+  const dim3 grid((unsigned)fmd_cdiv(n * WPA, kWaves));
+#define FMD_MSG(H, F, R)                                                                                       \
+  hipLaunchKernelGGL((message_kernel<CPL, H, F, R, WPA>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne, \
+                     e_cap, n, order, h0, h1p, inv_avg, A0, A1, ef, w1ef, nb)
   if (!fz) {
     if (h1)
       FMD_MSG(true, false, 0);
@@ -1090,17 +1162,18 @@ static uintptr_t channel_alignment(int channels) { return channels <= 64 ? 8 : 1
   }
 
 namespace {
-template <int CPL>
-int launch_bwd_edge(bool h1, bool fz, dim3 grid, hipStream_t s, const float* z, const float* zq, const float* geo,
+template <int CPL, int WPA>
+int launch_bwd_edge(bool h1, bool fz, hipStream_t s, const float* z, const float* zq, const float* geo,
                     const int32_t* ei, const int64_t* off, const int64_t* ne, int64_t e_cap, int64_t n,
                     const int32_t* order, const float* h0, const float* h1p, const float* gA0, const float* gA1,
                     float inv_avg, float* gz, float* gzsum, float* ggeo, int acc, const float* w1ef, int nb, float* gef,
                     const float* ef) {
   const bool wide = w1ef && nb > 8;  // radial rows padded to 16 instead of 8
   const size_t lds = (size_t)(wide ? 16 : 8) * 4 * 64 * CPL * sizeof(float);  // RB x 4C floats
-#define FMD_BWD_EDGE(H, RB, F)                                                                                       \
-  hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, H, RB, F>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, off, ne, \
-                     e_cap, n, order, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef, ef)
+  const dim3 grid((unsigned)fmd_cdiv(n * WPA, kWaves));
+#define FMD_BWD_EDGE(H, RB, F)                                                                                   \
+  hipLaunchKernelGGL((message_bwd_edge_kernel<CPL, H, RB, F, WPA>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, \
+                     off, ne, e_cap, n, order, h0, h1p, gA0, gA1, inv_avg, gz, gzsum, ggeo, acc, w1ef, nb, gef, ef)
 #define FMD_BWD_EDGE_F(H, RB) \
   if (fz)                     \
     FMD_BWD_EDGE(H, RB, true); \
@@ -1121,16 +1194,17 @@ int launch_bwd_edge(bool h1, bool fz, dim3 grid, hipStream_t s, const float* z, 
   return FMD_OK;
 }
 
-template <int CPL>
-int launch_bwd_src(bool h1, bool fz, int rb, dim3 grid, hipStream_t s, const float* z, const float* zq,
+template <int CPL, int WPA>
+int launch_bwd_src(bool h1, bool fz, int rb, hipStream_t s, const float* z, const float* zq,
                    const float* geo, const int32_t* ei, const int32_t* rev, const int64_t* off, const int64_t* ne,
                    int64_t e_cap, int64_t n, const int32_t* order, const float* h0, const float* h1p, const float* gA0,
                    const float* gA1, float inv_avg, float* gh0, float* gh1, int acc, float* gzsum_src, const float* ef,
                    const float* w1ef, int nb) {
   const size_t lds = fz ? (size_t)rb * 4 * 64 * CPL * sizeof(float) : 0;
-#define FMD_BWD_SRC(H, F, R)                                                                                        \
-  hipLaunchKernelGGL((message_bwd_src_kernel<CPL, H, F, R>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, rev, off, \
-                     ne, e_cap, n, order, h0, h1p, gA0, gA1, inv_avg, gh0, gh1, acc, gzsum_src, ef, w1ef, nb)
+  const dim3 grid((unsigned)fmd_cdiv(n * WPA, kWaves));
+#define FMD_BWD_SRC(H, F, R)                                                                                       \
+  hipLaunchKernelGGL((message_bwd_src_kernel<CPL, H, F, R, WPA>), grid, dim3(kThreads), lds, s, z, zq, geo, ei, rev, \
+                     off, ne, e_cap, n, order, h0, h1p, gA0, gA1, inv_avg, gh0, gh1, acc, gzsum_src, ef, w1ef, nb)
   if (!fz) {
     if (h1)
       FMD_BWD_SRC(true, false, 0);
@@ -1178,19 +1252,31 @@ int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, co
   return FMD_OK;
 }
 
+// one or four waves per atom (the launchers' WPA)
+#define FMD_WPA_DISPATCH(WPA_ARG, FN, CPLV, ...)                 \
+  ((WPA_ARG) == 4 ? FN<CPLV, 4>(__VA_ARGS__) : FN<CPLV, 1>(__VA_ARGS__))
+
 int fmd_mace_message_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
                          const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
                          const int32_t* order, int32_t channels, const float* h0, const float* h1, float inv_avg,
                          float* A0, float* A1, int32_t z_per_node, const float* ef, const float* w1ef, int32_t nb,
-                         hipStream_t stream) {
+                         int32_t waves_per_atom, hipStream_t stream) {
   FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && A0 && A1 && n_atoms >= 0);
   FMD_REQUIRE(!z_per_node || (zq && ef && w1ef && nb > 0 && nb <= kMaxBasis));
+  FMD_REQUIRE(waves_per_atom == 1 || waves_per_atom == 4);
   FMD_REQUIRE(aligned_to(channel_alignment(channels), {z, zq, h0, h1, A0, A1}) && aligned_to(16, {geo, ef}));
   if (n_atoms == 0) return FMD_OK;
-  dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
   const int rb = nb > 8 ? 16 : 8;
-  FMD_CPL_DISPATCH(channels, launch_message, h1 != nullptr, z_per_node != 0, rb, grid, stream, z, zq, geo, edge_index,
-                   edge_offsets, n_edges, e_cap, n_atoms, order, h0, h1, inv_avg, A0, A1, ef, w1ef, nb);
+  const bool fz = z_per_node != 0, hv = h1 != nullptr;
+  switch (channels / 64) {
+    case 1: return FMD_WPA_DISPATCH(waves_per_atom, launch_message, 1, hv, fz, rb, stream, z, zq, geo, edge_index,
+                                    edge_offsets, n_edges, e_cap, n_atoms, order, h0, h1, inv_avg, A0, A1, ef, w1ef, nb);
+    case 2: return FMD_WPA_DISPATCH(waves_per_atom, launch_message, 2, hv, fz, rb, stream, z, zq, geo, edge_index,
+                                    edge_offsets, n_edges, e_cap, n_atoms, order, h0, h1, inv_avg, A0, A1, ef, w1ef, nb);
+    case 4: return FMD_WPA_DISPATCH(waves_per_atom, launch_message, 4, hv, fz, rb, stream, z, zq, geo, edge_index,
+                                    edge_offsets, n_edges, e_cap, n_atoms, order, h0, h1, inv_avg, A0, A1, ef, w1ef, nb);
+    default: return FMD_EUNSUPPORTED;
+  }
 }
 
 int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
@@ -1200,45 +1286,47 @@ int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, 
                              const float* gA0, const float* gA1,
                              float inv_avg, float* gz, float* gzsum, float* gzsum_src, float* ggeo,
                              int32_t accumulate_geo, float* gh0, float* gh1, int32_t accumulate_h, const float* w1ef,
-                             int32_t nb, float* gef, int32_t z_per_node, const float* ef, hipStream_t stream) {
+                             int32_t nb, float* gef, int32_t z_per_node, const float* ef, int32_t waves_per_atom,
+                             hipStream_t stream) {
   FMD_REQUIRE(z && geo && edge_index && edge_offsets && n_edges && h0 && gA0 && gA1 && ggeo && n_atoms >= 0);
   FMD_REQUIRE(gz || w1ef || gzsum);
   FMD_REQUIRE(!w1ef || (gef && nb > 0 && nb <= kMaxBasis));
   FMD_REQUIRE(!z_per_node || (zq && ef && w1ef && !gz));
   FMD_REQUIRE(!(gh0 || gzsum_src) || reverse);
+  FMD_REQUIRE(waves_per_atom == 1 || waves_per_atom == 4);
   FMD_REQUIRE(aligned_to(channel_alignment(channels), {z, zq, h0, h1, gA0, gA1, gz, gzsum, gzsum_src, gh0, gh1}) &&
               aligned_to(16, {geo, ggeo, ef}));
   if (n_atoms == 0) return FMD_OK;
-  dim3 grid((unsigned)fmd_cdiv(n_atoms, kWaves));
-  const bool fz = z_per_node != 0;
+  const bool fz = z_per_node != 0, hv = h1 != nullptr;
   const int rb = nb > 8 ? 16 : 8;
   // accumulate_h bit 2: the sender-side kernel alone (the edge side ran in a call before)
   const bool sender_only = (accumulate_h & 4) != 0;
   accumulate_h &= 3;
+  const int w = waves_per_atom;
   int rc = FMD_OK;
   if (!sender_only) switch (channels / 64) {
-    case 1: rc = launch_bwd_edge<1>(h1 != nullptr, fz, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges,
-                                    e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo,
-                                    w1ef, nb, gef, ef); break;
-    case 2: rc = launch_bwd_edge<2>(h1 != nullptr, fz, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges,
-                                    e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo,
-                                    w1ef, nb, gef, ef); break;
-    case 4: rc = launch_bwd_edge<4>(h1 != nullptr, fz, grid, stream, z, zq, geo, edge_index, edge_offsets, n_edges,
-                                    e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo, accumulate_geo,
-                                    w1ef, nb, gef, ef); break;
+    case 1: rc = FMD_WPA_DISPATCH(w, launch_bwd_edge, 1, hv, fz, stream, z, zq, geo, edge_index, edge_offsets,
+                                  n_edges, e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo,
+                                  accumulate_geo, w1ef, nb, gef, ef); break;
+    case 2: rc = FMD_WPA_DISPATCH(w, launch_bwd_edge, 2, hv, fz, stream, z, zq, geo, edge_index, edge_offsets,
+                                  n_edges, e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo,
+                                  accumulate_geo, w1ef, nb, gef, ef); break;
+    case 4: rc = FMD_WPA_DISPATCH(w, launch_bwd_edge, 4, hv, fz, stream, z, zq, geo, edge_index, edge_offsets,
+                                  n_edges, e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gz, gzsum, ggeo,
+                                  accumulate_geo, w1ef, nb, gef, ef); break;
     default: return FMD_EUNSUPPORTED;
   }
   if (rc != FMD_OK || !(gh0 || gzsum_src)) return rc;
   switch (channels / 64) {
-    case 1: return launch_bwd_src<1>(h1 != nullptr, fz, rb, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets,
-                                     n_edges, e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h,
-                                     gzsum_src, ef, w1ef, nb);
-    case 2: return launch_bwd_src<2>(h1 != nullptr, fz, rb, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets,
-                                     n_edges, e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h,
-                                     gzsum_src, ef, w1ef, nb);
-    case 4: return launch_bwd_src<4>(h1 != nullptr, fz, rb, grid, stream, z, zq, geo, edge_index, reverse, edge_offsets,
-                                     n_edges, e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1, accumulate_h,
-                                     gzsum_src, ef, w1ef, nb);
+    case 1: return FMD_WPA_DISPATCH(w, launch_bwd_src, 1, hv, fz, rb, stream, z, zq, geo, edge_index, reverse,
+                                    edge_offsets, n_edges, e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1,
+                                    accumulate_h, gzsum_src, ef, w1ef, nb);
+    case 2: return FMD_WPA_DISPATCH(w, launch_bwd_src, 2, hv, fz, rb, stream, z, zq, geo, edge_index, reverse,
+                                    edge_offsets, n_edges, e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1,
+                                    accumulate_h, gzsum_src, ef, w1ef, nb);
+    case 4: return FMD_WPA_DISPATCH(w, launch_bwd_src, 4, hv, fz, rb, stream, z, zq, geo, edge_index, reverse,
+                                    edge_offsets, n_edges, e_cap, n_atoms, order, h0, h1, gA0, gA1, inv_avg, gh0, gh1,
+                                    accumulate_h, gzsum_src, ef, w1ef, nb);
     default: return FMD_EUNSUPPORTED;
   }
 }

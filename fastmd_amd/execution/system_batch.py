@@ -122,6 +122,7 @@ class SlotUnionGraphBuilder(FixedCapacityGraphBuilder):
         self.batch.cell = self._sys_cells
         self.batch.systems = SystemSegments(count=layout.count, row_ptr=self._row_ptr,
                                             system_of_row=self._system_of, cells=self._sys_cells, atoms=self._atoms)
+        self.batch.max_system_rows = max(layout.ceilings)
         self.graph = self.batch if prepare is None else prepare(self.batch)
 
     def _set_cell(self, slot: int, cell32: np.ndarray) -> None:

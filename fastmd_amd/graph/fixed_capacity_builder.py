@@ -297,6 +297,7 @@ class FixedCapacityGraphBuilder:
             triplets=self.line_graph,
             line=self._line_layout(),
             atom_order=self.atom_order,
+            max_system_rows=self.system_size or n,
         )
         self.graph = (prepare or _batch_itself)(self.batch)
 

@@ -66,6 +66,10 @@ FACTORED_Z = True
 # never formed), and the first layer's per-element rows come from one gather launch. Off: one
 # launch per product, as the unmerged chain (kept tested against the oracle).
 MERGED_NODE = True
+# Systems of at most this many atoms (the largest system of a replica or slot union) split each
+# atom's rows over four waves in the message kernels (one wave per atom leaves a small system's
+# chip idle while each wave walks its rows); the per-atom sums are then added over the waves.
+SPLIT_ROWS_MAX_ATOMS = 2048
 # Timing hook of the edge GEMM launches: when a list, each eager (uncaptured) forward appends
 # (start event, end event, (M, K, N)) recorded around its edge GEMMs on the current stream. The
 # benchmark uses it to time the dominant kernel in the context of the step; None in normal runs.
@@ -350,6 +354,13 @@ def _atom_order(batch, n: int) -> int | None:
     return None if order is None or order.numel() != n else order.data_ptr()
 
 
+def _waves_per_atom(batch, n: int) -> int:
+    """Waves per atom of the message kernels: by the largest system of the batch, so that a
+    system batched with others sums its rows as it does alone."""
+    size = getattr(batch, "max_system_rows", 0) or n
+    return 4 if size <= SPLIT_ROWS_MAX_ATOMS else 1
+
+
 def _gather_edge_rows(h0: Tensor, ef: Tensor, edge_index: Tensor, out: Tensor) -> None:
     """out[e] = [h0[src e] | h0[dst e] | ef[e]] (src = neighbour column 1, dst = centre column 0)."""
     C, nb = h0.shape[1], ef.shape[1]
@@ -398,6 +409,7 @@ class _MaceLikeEnergy(Function):
         cell = cell.detach().to(torch.float32).contiguous()
         n_edges, off, ei = batch.n_edges, batch.edge_offsets, batch.edge_index
         order = _atom_order(batch, n)
+        wpa = _waves_per_atom(batch, n)
         elem = inputs.elem
         inv_avg = 1.0 / cfg.avg_num_neighbors
         geo = _empty(e_cap, 8, device=dev)
@@ -459,7 +471,7 @@ class _MaceLikeEnergy(Function):
                 A1 = _empty(n, 3, C, device=dev)
                 _call("fmd_mace_message_f32", z.data_ptr(), q.data_ptr(), geo.data_ptr(), ei.data_ptr(),
                       off.data_ptr(), n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1), inv_avg,
-                      A0.data_ptr(), A1.data_ptr(), 1, ef.data_ptr(), w1ef_all[t].data_ptr(), nb)
+                      A0.data_ptr(), A1.data_ptr(), 1, ef.data_ptr(), w1ef_all[t].data_ptr(), nb, wpa)
             elif hoist:
                 h0p = split_planes(h0)
                 q = gemm_planes([(h0p, None)], model.w1_planes(t, "receiver", nz), a_planes=True)
@@ -484,7 +496,7 @@ class _MaceLikeEnergy(Function):
                 A1 = _empty(n, 3, C, device=dev)
                 _call("fmd_mace_message_f32", z.data_ptr(), _abi.ptr(q), geo.data_ptr(), ei.data_ptr(),
                       off.data_ptr(), n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1), inv_avg,
-                      A0.data_ptr(), A1.data_ptr(), 0, None, None, 0)
+                      A0.data_ptr(), A1.data_ptr(), 0, None, None, 0, wpa)
             B0 = _empty(n, C, device=dev)
             B1 = None if last else _empty(n, 3, C, device=dev)
             if FUSED_NODE:
@@ -584,6 +596,7 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
     inv_avg = 1.0 / cfg.avg_num_neighbors
     n_edges, off, ei, rev = batch.n_edges, batch.edge_offsets, batch.edge_index, batch.edge_reverse
     order = _atom_order(batch, n)
+    wpa = _waves_per_atom(batch, n)
     # readouts: gha = dE/d(first layer's h0 out), gy -> dE/d(last layer's h0 out)
     gy = _empty(n, H, device=dev)
     gha = _empty(n, C, device=dev)
@@ -663,7 +676,7 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
                   rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(),
                   _abi.ptr(h1), gA0.data_ptr(), gA1.data_ptr(), inv_avg, None, None, None, ggeo.data_ptr(), acc_geo,
                   None, None,
-                  0, w1ef.data_ptr(), nb, gef.data_ptr(), 1 if ctx.factored else 0, ctx.ef.data_ptr())
+                  0, w1ef.data_ptr(), nb, gef.data_ptr(), 1 if ctx.factored else 0, ctx.ef.data_ptr(), wpa)
             gefs.append((gef, nb))
             break
         # the gather-cat row gradient's node blocks come from per-node sums of g_z (never stored):
@@ -681,7 +694,7 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
         head = (z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(), ei.data_ptr(), rev.data_ptr(), off.data_ptr(),
                 n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(), gA1.data_ptr(),
                 inv_avg, None, gzs.data_ptr())
-        tail = (w1ef.data_ptr(), nb, gef.data_ptr(), 1 if ctx.factored else 0, ctx.ef.data_ptr())
+        tail = (w1ef.data_ptr(), nb, gef.data_ptr(), 1 if ctx.factored else 0, ctx.ef.data_ptr(), wpa)
         if MESSAGE_EVENTS is not None and not torch.cuda.is_current_stream_capturing():
             # timed: the edge side alone between events, then the sender side alone (the same two
             # kernels and results as the single call)

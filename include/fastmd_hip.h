@@ -516,12 +516,15 @@ int fmd_edge_geometry_bwd_f32(const float* geo, const float* def, int32_t nb, co
  * z_per_node = 1 (node-factored pre-activation): z is P = h0 W1[:C] per atom ([N, W]) and zq is
  * Q = h0 W1[C:2C] ([N, W], required); row e of centre i and sender j takes
  * (P[j] + sum_n ef[e, n] w1ef[n, :W]) + Q[i], with ef [E, nb] the radial basis rows (16-byte
- * aligned) and w1ef [nb, 4C] the radial rows of W1 (nb <= 16): no [E, W] array exists. */
+ * aligned) and w1ef [nb, 4C] the radial rows of W1 (nb <= 16): no [E, W] array exists.
+ * waves_per_atom (1 or 4): the rows of an atom are taken by one wave, or split over four waves
+ * whose per-atom sums are added in wave order (for small systems; a different association of
+ * the sums, so the choice belongs to the system size, not to the call). */
 int fmd_mace_message_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
                          const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
                          const int32_t* order, int32_t channels, const float* h0, const float* h1, float inv_avg,
                          float* A0, float* A1, int32_t z_per_node, const float* ef, const float* w1ef, int32_t nb,
-                         hipStream_t stream);
+                         int32_t waves_per_atom, hipStream_t stream);
 /* VJP of fmd_mace_message_f32 (z, zq and the width W as there): gz [E,W] (may be null), gzsum
  * [N,W] (may be null: the sum of gz over each centre's rows, in row order), gzsum_src [N,W] (may
  * be null: the sum of gz over the rows whose sender is the node, over the reverse CSR, without gz
@@ -534,7 +537,7 @@ int fmd_mace_message_f32(const float* z, const float* zq, const float* geo, cons
  * on 16 bytes). z_per_node = 1: z, zq as in the node-factored forward (P, Q), with its ef; w1ef
  * is then required and gz must be null. accumulate_h bit 2 (4): launch the sender-side kernel
  * only (its arguments as in the full call; the edge side having run in an earlier call), so
- * that each side can be timed on its own. */
+ * that each side can be timed on its own. waves_per_atom as in the forward. */
 int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, const int32_t* edge_index,
                              const int32_t* reverse,
                              const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap, int64_t n_atoms,
@@ -542,7 +545,8 @@ int fmd_mace_message_bwd_f32(const float* z, const float* zq, const float* geo, 
                              const float* gA0, const float* gA1, float inv_avg, float* gz, float* gzsum,
                              float* gzsum_src, float* ggeo,
                              int32_t accumulate_geo, float* gh0, float* gh1, int32_t accumulate_h, const float* w1ef,
-                             int32_t nb, float* gef, int32_t z_per_node, const float* ef, hipStream_t stream);
+                             int32_t nb, float* gef, int32_t z_per_node, const float* ef, int32_t waves_per_atom,
+                             hipStream_t stream);
 /* The node side of one interaction layer fused per 32-atom tile (one launch instead of six),
  * fp32-accurate on the bf16 matrix cores: P0 = A0 Wm0, P1_x = A1_x Wm1, the symmetric
  * contraction (B0, B1: workspace, [N,C] and [N,3,C]), h0n = B0 Wo0 + h0 Wsc0, h1n_x = B1_x Wo1
