@@ -255,41 +255,15 @@ __device__ __forceinline__ double block_sum_mb(double v, double* red) {
   return s;
 }
 
-// p += kick (post half: kick first, cache F) then the block partial of p*p/m
-__global__ void __launch_bounds__(kMbThreads) nhc_mb_partials_kernel(double* p, const void* f_in, int f_in_64,
-                                                                     double* f_cache, const double* masses,
-                                                                     const double* consts, int kick,
-                                                                     int f32_kick, int64_t n, double* work) {
-  __shared__ double red[kMbThreads / FMD_WAVE];
-  const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// ke2 from the partials (lane-strided, then the wave sum: a fixed order), the chain half step
+// and the scale factors; run by one wave (its lane 0 does the chain)
+__device__ __forceinline__ void mb_chain(double* eta, double* pe, const double* consts, int M, int tloop,
+                                         int64_t nblocks, double* work) {
+  const int lane = threadIdx.x & (FMD_WAVE - 1);
   double s = 0.0;
-  if (a < n) {
-    const double m = masses[a];
-    const double dt2 = consts[1];
-#pragma unroll
-    for (int d = 0; d < 3; ++d) {
-      double pv = p[3 * a + d];
-      if (kick) {
-        const double fv = f_in_64 ? static_cast<const double*>(f_in)[3 * a + d]
-                                  : (double)static_cast<const float*>(f_in)[3 * a + d];
-        pv = pv + kick_of(dt2, fv, f32_kick);
-        p[3 * a + d] = pv;
-        f_cache[3 * a + d] = fv;
-      }
-      s = s + (pv * pv) / m;
-    }
-  }
-  s = block_sum_mb(s, red);
-  if (threadIdx.x == 0) work[kMaxScales + blockIdx.x] = s;
-}
-
-// one workgroup: ke2 from the partials, the chain half step, the scale factors
-__global__ void __launch_bounds__(FMD_WAVE) nhc_mb_chain_kernel(double* eta, double* pe, const double* consts, int M,
-                                                                int tloop, int64_t nblocks, double* work) {
-  double s = 0.0;
-  for (int64_t b = threadIdx.x; b < nblocks; b += FMD_WAVE) s = s + work[kMaxScales + b];
+  for (int64_t b = lane; b < nblocks; b += FMD_WAVE) s = s + work[kMaxScales + b];
   s = wave_sum(s);
-  if (threadIdx.x != 0) return;
+  if (lane != 0) return;
   Chain c;
   c.M = M;
   for (int j = 0; j < kMaxChain; ++j) {
@@ -318,6 +292,47 @@ __global__ void __launch_bounds__(FMD_WAVE) nhc_mb_chain_kernel(double* eta, dou
   }
 }
 
+// p += kick (post half: kick first, cache F) then the block partial of p*p/m; the chain half
+// step is run by the workgroup that finishes last (a completion counter after the partials; every workgroup publishes its partial
+// with a device-scope fence before it counts itself, the last one fences again before it reads
+// them, then sets the counter back to zero for the next launch): a half step is this launch and
+// the elementwise pass.
+__global__ void __launch_bounds__(kMbThreads) nhc_mb_partials_chain_kernel(
+    double* p, const void* f_in, int f_in_64, double* f_cache, const double* masses, const double* consts, int kick,
+    int f32_kick, int64_t n, double* work, unsigned int* counter, double* eta, double* pe, int M, int tloop) {
+  __shared__ double red[kMbThreads / FMD_WAVE];
+  __shared__ int last;
+  const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  double s = 0.0;
+  if (a < n) {
+    const double m = masses[a];
+    const double dt2 = consts[1];
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+      double pv = p[3 * a + d];
+      if (kick) {
+        const double fv = f_in_64 ? static_cast<const double*>(f_in)[3 * a + d]
+                                  : (double)static_cast<const float*>(f_in)[3 * a + d];
+        pv = pv + kick_of(dt2, fv, f32_kick);
+        p[3 * a + d] = pv;
+        f_cache[3 * a + d] = fv;
+      }
+      s = s + (pv * pv) / m;
+    }
+  }
+  s = block_sum_mb(s, red);
+  if (threadIdx.x == 0) {
+    work[kMaxScales + blockIdx.x] = s;
+    __threadfence();
+    last = atomicAdd(counter, 1u) == gridDim.x - 1 ? 1 : 0;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  if (threadIdx.x < FMD_WAVE) mb_chain(eta, pe, consts, M, tloop, gridDim.x, work);
+  if (threadIdx.x == 0) atomicExch(counter, 0u);
+}
+
 // p *= scale factors in sequence; pre half: then kick with the cached F and drift
 __global__ void __launch_bounds__(kMbThreads) nhc_mb_apply_kernel(double* q, double* p, const double* f,
                                                                   const double* masses, const double* consts,
@@ -340,6 +355,10 @@ __global__ void __launch_bounds__(kMbThreads) nhc_mb_apply_kernel(double* q, dou
     }
     p[3 * a + d] = pv;
   }
+}
+
+unsigned int* mb_counter(double* work, int64_t n) {
+  return reinterpret_cast<unsigned int*>(work + kMaxScales + fmd_cdiv(n > 0 ? n : 1, kMbThreads));
 }
 
 int pick_kpt(int64_t n, int threads) {
@@ -367,7 +386,11 @@ int nhc_threads(int64_t n) {
 
 extern "C" {
 
-int64_t fmd_nhc_work_size(int64_t n_atoms) { return kMaxScales + fmd_cdiv(n_atoms > 0 ? n_atoms : 1, kMbThreads); }
+// the completion counter of nhc_mb_partials_chain_kernel: the last float64 slot of `work`
+// (zero-initialized by the caller, and zero again after every launch)
+int64_t fmd_nhc_work_size(int64_t n_atoms) {
+  return kMaxScales + fmd_cdiv(n_atoms > 0 ? n_atoms : 1, kMbThreads) + 1;
+}
 
 int fmd_nhc_pre_force(double* q, double* p, const double* f, const double* masses, double* eta, double* p_eta,
                       const double* consts, int64_t n_atoms, int32_t tchain, int32_t tloop, int32_t f32_kick,
@@ -379,11 +402,9 @@ int fmd_nhc_pre_force(double* q, double* p, const double* f, const double* masse
   if (kpt == 0) {
     FMD_REQUIRE(work && 3 * tloop <= kMaxScales);
     const int64_t nb = fmd_cdiv(n_atoms, kMbThreads);
-    hipLaunchKernelGGL(nhc_mb_partials_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, p, (const void*)f, 1,
-                       (double*)nullptr, masses, consts, 0, f32_kick, n_atoms, work);
-    FMD_CHECK_LAUNCH();
-    hipLaunchKernelGGL(nhc_mb_chain_kernel, dim3(1), dim3(FMD_WAVE), 0, stream, eta, p_eta, consts, tchain, tloop, nb,
-                       work);
+    hipLaunchKernelGGL(nhc_mb_partials_chain_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, p,
+                       (const void*)f, 1, (double*)nullptr, masses, consts, 0, f32_kick, n_atoms, work,
+                       mb_counter(work, n_atoms), eta, p_eta, tchain, tloop);
     FMD_CHECK_LAUNCH();
     hipLaunchKernelGGL(nhc_mb_apply_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, q, p, f, masses, consts,
                        3 * tloop, 1, f32_kick, n_atoms, (const double*)work, (const void*)nullptr, 0, (double*)nullptr);
@@ -407,11 +428,9 @@ int fmd_nhc_post_force(double* p, const void* f_in, int32_t f_in_is_f64, double*
   if (kpt == 0) {
     FMD_REQUIRE(work && 3 * tloop <= kMaxScales);
     const int64_t nb = fmd_cdiv(n_atoms, kMbThreads);
-    hipLaunchKernelGGL(nhc_mb_partials_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, p, f_in, f_in_is_f64,
-                       f_cache, masses, consts, 1, f32_kick, n_atoms, work);
-    FMD_CHECK_LAUNCH();
-    hipLaunchKernelGGL(nhc_mb_chain_kernel, dim3(1), dim3(FMD_WAVE), 0, stream, eta, p_eta, consts, tchain, tloop, nb,
-                       work);
+    hipLaunchKernelGGL(nhc_mb_partials_chain_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, p, f_in,
+                       f_in_is_f64, f_cache, masses, consts, 1, f32_kick, n_atoms, work, mb_counter(work, n_atoms),
+                       eta, p_eta, tchain, tloop);
     FMD_CHECK_LAUNCH();
     hipLaunchKernelGGL(nhc_mb_apply_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, (double*)nullptr, p,
                        (const double*)nullptr, masses, consts, 3 * tloop, 0, f32_kick, n_atoms, (const double*)work,

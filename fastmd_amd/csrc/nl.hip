@@ -654,16 +654,19 @@ __global__ void __launch_bounds__(kBlock) nl_count_kernel(BuildArgs a) {
 }
 
 // Kernel 2 (one workgroup): exclusive scan of the counts, the flags and the reductions.
+// The counts are scanned in tiles of kScanTile staged through LDS (coalesced loads, all in
+// flight together; each thread then scans kScanPer consecutive counts), with a carry between
+// tiles: a thread's own serial chunk of global loads would wait out one memory round trip per
+// atom.
+constexpr int kScanPer = 8, kScanTile = 1024 * kScanPer;
+
 __global__ void __launch_bounds__(1024) nl_scan_kernel(BuildArgs a, int64_t nblocks) {
   __shared__ float s_max[1024 / FMD_WAVE];
   __shared__ int32_t s_iso[1024 / FMD_WAVE];
+  __shared__ int64_t s_cnt[kScanTile];
   const int t = threadIdx.x, T = blockDim.x;
   const int lane = t & (FMD_WAVE - 1), wave = t / FMD_WAVE;
   const int64_t n = a.n;
-  const int64_t chunk = fmd_cdiv(n, T);
-  const int64_t lo = t * chunk, hi = lo + chunk < n ? lo + chunk : n;
-  int64_t s = 0;
-  for (int64_t k = lo; k < hi; ++k) s += a.edge_counts[k];
   // block partials of kernel 1 (max displacement, isolated atoms): strided per thread, then
   // over the wave and over the waves, in a fixed order
   {
@@ -684,8 +687,31 @@ __global__ void __launch_bounds__(1024) nl_scan_kernel(BuildArgs a, int64_t nblo
   }
   __syncthreads();
   __shared__ int64_t s_wtot[17];
-  int64_t total = 0;
-  const int64_t mine = block_exclusive_scan<int64_t>(s, s_wtot, &total);
+  int64_t carry = 0;
+  for (int64_t base = 0; base < n; base += kScanTile) {
+    const int64_t cnt = n - base < kScanTile ? n - base : kScanTile;
+#pragma unroll
+    for (int j = 0; j < kScanPer; ++j) {
+      const int64_t k = (int64_t)j * T + t;
+      s_cnt[k] = k < cnt ? a.edge_counts[base + k] : 0;
+    }
+    __syncthreads();
+    int64_t s = 0;
+#pragma unroll
+    for (int j = 0; j < kScanPer; ++j) s += s_cnt[t * kScanPer + j];
+    int64_t tile_total = 0;
+    const int64_t mine = block_exclusive_scan<int64_t>(s, s_wtot, &tile_total);
+    int64_t run = carry + mine;
+#pragma unroll
+    for (int j = 0; j < kScanPer; ++j) {
+      const int64_t k = (int64_t)t * kScanPer + j;
+      if (k < cnt) a.edge_offsets[base + k] = run;
+      run += s_cnt[k];
+    }
+    carry += tile_total;
+    __syncthreads();  // s_cnt and s_wtot are reused by the next tile
+  }
+  const int64_t total = carry;
   if (t == 0) {
     float m = s_max[0];
     int32_t isol = s_iso[0];
@@ -699,12 +725,6 @@ __global__ void __launch_bounds__(1024) nl_scan_kernel(BuildArgs a, int64_t nblo
     a.overflow[0] = (total > a.e_cap || !valid) ? 1 : 0;
     a.isolated[0] = isol;
     a.edge_offsets[n] = total;
-  }
-  int64_t run = mine;
-  for (int64_t k = lo; k < hi; ++k) {
-    const int64_t v = a.edge_counts[k];
-    a.edge_offsets[k] = run;
-    run += v;
   }
 }
 

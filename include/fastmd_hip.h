@@ -473,9 +473,12 @@ int fmd_nhc_post_force(double* p, const void* f_in, int32_t f_in_is_f64, double*
                        int32_t tchain, int32_t tloop, int32_t f32_kick, double* work, hipStream_t stream);
 
 /* float64 elements of the `work` buffer the NHC entry points need for n_atoms (systems of more
- * than 4096 atoms run the multi-block path: per-block partial sums, one chain workgroup, an
- * elementwise pass; after each momentum scaling ke2 is updated as ke2 * s^2, the reference's
- * "scaled" update of gpu_nhc.py:520-706, instead of a fresh reduction). May be null below. */
+ * than 4096 atoms run the multi-block path: per-block partial sums with the chain half step run
+ * by the last workgroup to finish (a completion counter in the last slot of `work`, which must be
+ * zero when the buffer is first used and is left at zero by every call), then an elementwise
+ * pass: two launches per half step; after each momentum scaling ke2 is updated as ke2 * s^2,
+ * the reference's "scaled" update of gpu_nhc.py:520-706, instead of a fresh reduction). May be
+ * null below. */
 int64_t fmd_nhc_work_size(int64_t n_atoms);
 
 /* ----------------------------------------------------------------------------------------
