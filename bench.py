@@ -28,7 +28,7 @@ FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 SPLIT_PRODUCTS = 6  # fp32-accurate GEMM: three bf16 planes per operand, six MFMA products
 SPIN_CYCLES = 20_000_000  # GPU clock cycles of torch.cuda._sleep (several ms)
-ROOFLINE_KERNEL = "message_bwd_edge_kernel<2, true, 8, true>"
+ROOFLINE_KERNEL = "message_bwd_edge_kernel<2, true, 8, true, 1>"
 STEPS_PER_LAUNCH = 10
 
 

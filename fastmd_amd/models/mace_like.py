@@ -11,8 +11,10 @@ Model (per interaction layer t, node features h0 [N, C] scalars and h1 [N, 3, C]
   edge e = (centre i <- neighbour j), vec = pos_j + image @ cell - pos_i, r = |vec|, u = vec / r
   ef_n   = sqrt(2/rc) sin(n pi r / rc) / r * fcut(r),  n = 1..8;  fcut = 1 - 21x^5 + 35x^6 - 15x^7
   a_e    = [h0_j | h0_i | ef_e]                                 (gather-cat, [E, 2C + 8])
-  z_e    = a_e @ W1                                              (edge GEMM, [2C+8, 4C]; the
-                                                                  gather-cat is fused into its load)
+  z_e    = a_e @ W1                                              ([2C+8, 4C]) evaluated as
+         = P_j + Q_i + ef_e @ W1[2C:],  P = h0 W1[:C], Q = h0 W1[C:2C]  (node-factored, the default:
+           node GEMMs, the radial term added per row in the message kernels), or as the edge GEMM
+           over the gather-cat rows (fused into its operand load; FACTORED_Z off)
   w_e    = silu(z_e) * fcut(r)  = (wa | wb | wc | wd)             (h1 = 0: wa | wb only)
   m0     = wa h0_j + wc (h1_j . u),  m1_x = wb h0_j u_x + wd h1_j,x
   A0_i, A1_i = (1 / avg_num_neighbors) * sum over the rows of i   (segment sums)
