@@ -8,7 +8,7 @@ model, NVT Nose-Hoover chain at 500 K (tdamp 25 fs, tchain 3, tloop 1, dt 0.25 f
 F = 128) are reported beside it, with the dominant kernel's roofline and the CPU baseline (the
 PyTorch-CPU eager oracle on this host's cores, a bounded sample of the same workload).
 
-  python bench.py [--gpus 1] [--steps 1000] [--warmup 1000] [--no-cpu] [--quick] [--ops] [--scaling]
+  python bench.py [--gpus 1] [--steps 1000] [--warmup 1000] [--no-cpu] [--quick] [--ops] [--scaling] [--nhc]
 """
 from __future__ import annotations
 
@@ -101,9 +101,11 @@ def message_roofline(md) -> dict:
     gathered, z rebuilt with the radial term, its gradient, the radial-basis and geometry
     gradients; per atom the centre's Q, gA0, gA1 read and the sum of g_z written). It is timed
     in the context of the step: HIP events on torch's current stream (the stream it is launched
-    on) around that launch alone in 10 eager force evaluations at the run's final state (its
-    edge list and features), the model's own timing hook; each evaluation is queued behind a
-    spin kernel so that no host latency falls inside the event pairs.
+    on) around that launch alone in eager force evaluations at the run's final state (its edge
+    list and features), the model's own timing hook. Ten times, a spin kernel is queued and then
+    two evaluations behind it, so that no host latency falls inside the event pairs; the second
+    evaluation of each pair is timed (its launch follows the same kernels as in the captured
+    step, with their data in L2), the first is reported as ``first_launch_us``.
     Algorithmic bytes per launch, counted as the gather-cat's formula counts them (every
     gathered row once per edge that reads it): per real edge row 4 B neighbour index + 20 B
     geometry (unit vector, length, cutoff) + 4 nb B basis + 4 (NZ + 4) C B of gathered sender
@@ -121,15 +123,20 @@ def message_roofline(md) -> dict:
     mace_like.MESSAGE_EVENTS = events = []
     try:
         for _ in range(10):
-            # a spin kernel ahead of each evaluation keeps the GPU busy while the host enqueues
-            # the evaluation's launches, so the GPU runs them back to back as in the captured step
+            # a spin kernel ahead of each pair of evaluations keeps the GPU busy while the host
+            # enqueues their launches, so the GPU runs them back to back as in the captured step
             torch.cuda._sleep(SPIN_CYCLES)
+            runner._evaluate(md.integrator.positions)
             runner._evaluate(md.integrator.positions)
         torch.cuda.synchronize()
     finally:
         mace_like.MESSAGE_EVENTS = None
     e_cap, n, C = events[-1][2]
-    durations = [a.elapsed_time(b) / 1e3 for a, b, shape in events if shape == (e_cap, n, C)]
+    if len(events) != 20 or any(shape != (e_cap, n, C) for _, _, shape in events):
+        raise RuntimeError("the roofline evaluations ran on different edge capacities")
+    durations = [a.elapsed_time(b) / 1e3 for a, b, _ in events]
+    first = durations[0::2]
+    durations = durations[1::2]
     t = sum(durations) / len(durations)
     edges = int(runner.builder.edge_offsets[-1].item())
     rows = min(edges, e_cap)
@@ -142,6 +149,7 @@ def message_roofline(md) -> dict:
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _traffic(ROOFLINE_KERNEL, [rows, n, C]),
             "kernel": ROOFLINE_KERNEL, "launch_us": round(t * 1e6, 2), "launches_timed": len(durations),
+            "first_launch_us": round(sum(first) / len(first) * 1e6, 2),
             "rows": rows, "atoms": n, "bytes_per_launch": algorithmic,
             "bytes_basis": f"per real edge row {per_row} B (gathered sender rows counted per row), per atom "
                            f"{per_atom} B",
@@ -392,6 +400,66 @@ def model_graph_bench(steps: int, warmup: int) -> list:
     return out
 
 
+def nhc_bench(sizes=(135, 10000, 40000), steps: int = 100, reps: int = 5) -> list:
+    """The fused NHC velocity-Verlet halves alone (configs[0]/[2] 135 atoms, configs[3] 10 000 and
+    40 000): ``steps`` pre-force + post-force pairs (500 K, dt 0.25 fs, tdamp 25 fs, tchain 3,
+    tloop 1, float32 forces) captured in one HIP graph and replayed ``reps`` times between HIP
+    events, so the time is the kernels' alone. Bytes per step as the survey counts them,
+    220 N (f64 positions, momenta, cached forces and masses read and written by the two halves,
+    f32 forces read); one workgroup up to 4 096 atoms (one launch per half), block partials with
+    the chain run by the last workgroup above (two launches per half)."""
+    import numpy as np
+    import torch
+
+    from fastmd_amd import systems, units
+    from fastmd_amd.execution.gpu_nhc import GPUNoseHooverChainNVT, maxwell_boltzmann_momenta
+
+    device = torch.device("cuda", 0)
+    out = []
+    for n in sizes:
+        s = systems.perovskite_atoms(n)
+        p0 = maxwell_boltzmann_momenta(s.masses, 500.0, seed=0)
+        nhc = GPUNoseHooverChainNVT(s.masses, s.positions, np.asarray(p0, dtype=np.float64), temperature_K=500.0,
+                                    timestep=0.25 * units.fs, tdamp=25.0 * units.fs, tchain=3, tloop=1,
+                                    device=device, force_dtype=torch.float32)
+        gen = torch.Generator(device="cpu").manual_seed(0)
+        forces = (0.1 * torch.randn(n, 3, generator=gen)).to(device)
+        energy = torch.zeros(1, dtype=torch.float64, device=device)
+
+        def pair():
+            nhc.step_pre_force()
+            nhc.step_post_force(forces, energy=energy)
+
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                pair()
+        torch.cuda.current_stream(device).wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(steps):
+                pair()
+        graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            graph.replay()
+        end.record()
+        end.synchronize()
+        us = start.elapsed_time(end) * 1e3 / (reps * steps)
+        nbytes = 220 * n
+        out.append({"atoms": n, "us_per_step": round(us, 2), "launches_per_step": 2 if n <= 4096 else 4,
+                    "bytes_per_step": nbytes, "GBps": round(nbytes / us / 1e3, 1),
+                    "frac_of_hbm_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4)})
+        log(f"NHC {n} atoms: {us:.2f} us per step ({out[-1]['GBps']} GB/s)")
+        del graph, nhc
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(n_atoms: int, budget_s: float) -> dict:
     """The CPU oracle (PyTorch-CPU eager model forward+backward with index_select/index_add_/matmul,
     NumPy neighbour list and NHC) on this host, whole MD steps until ``budget_s`` elapsed."""
@@ -495,6 +563,8 @@ def main() -> int:
                         help="only replica batching (8 and 32 replicas of the 135-atom system)")
     parser.add_argument("--model-graph", action="store_true",
                         help="only the model_graph execution mode (MACE-like, 135 and 10 000 atoms)")
+    parser.add_argument("--nhc", action="store_true",
+                        help="only the NHC halves alone (135, 10 000 and 40 000 atoms)")
     parser.add_argument("--roofline-only", action="store_true",
                         help="only the dominant kernel at the 10 000-atom shape plus a 256 MiB copy (--pmc runs)")
     args = parser.parse_args()
@@ -522,6 +592,9 @@ def main() -> int:
         return 0
     if args.replicas:
         print(json.dumps({"replicas_135": replica_bench(1000, 1000)}), flush=True)
+        return 0
+    if args.nhc:
+        print(json.dumps({"nhc": nhc_bench()}), flush=True)
         return 0
     if args.ops:
         print(json.dumps({"ops_sweep": ops_sweep(), "hbm_peak_GBps": HBM_PEAK_GBPS,
@@ -578,6 +651,8 @@ def main() -> int:
 
     log("memory-bound operator microbenchmarks")
     seg = hbm_ops_bench()
+    log("NHC halves alone")
+    nhc = nhc_bench()
     cpu = None
     if not (args.no_cpu or args.quick):
         log("CPU baseline (oracle)")
@@ -616,6 +691,7 @@ def main() -> int:
         "replicas_135": replicas,
         "segment_sum_GBps": seg["segment_sum"]["GBps"],
         "hbm_ops_40k": seg,
+        "nhc": nhc,
         "whole_step_stats_10k": {**{k: stats_big[k] for k in ("candidate_refreshes", "fallback_windows",
                                                               "max_edge_count", "capacity_history")},
                                  "timed_events": events_big},

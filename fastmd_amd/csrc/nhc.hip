@@ -1,15 +1,16 @@
 // (e) Nose-Hoover chain velocity Verlet (ASE NoseHooverChainNVT) on the float64 state.
 //
 // One workgroup integrates all atoms (no inter-block synchronization): the thermostat chain
-// is a handful of fp64 scalars in LDS that thread 0 advances (the other threads read the
-// momentum scale factor it publishes), and the only reduction, ke2 = sum(p*p/m), is formed per
-// thread in a fixed order, then over the wave by a butterfly and over the waves in wave order,
-// so every thread sees the same bits. The operation order follows ASE / the reference port
+// is a handful of fp64 scalars in registers that every thread advances alike, and the only
+// reduction, ke2 = sum(p*p/m), is formed per thread in a fixed order, then over the wave by a
+// butterfly and over the waves in wave order, so every thread sees the same bits (and computes
+// the same chain and momentum scale factor). The operation order follows ASE / the reference port
 // (gpu_nhc.py:315-425): p_eta_j sweeps backward, eta update, p scaling by exp(-delta p_eta0/Q0),
 // ke2 recomputed, p_eta_j sweep forward; per Suzuki-Yoshida coefficient, tloop times.
 // FP contraction is off (each op rounded like NumPy); exp is the HIP device library's.
-// Momenta live in registers (KPT <= 4 atoms per thread, no spills) up to 4096 atoms; beyond
-// that the multi-block path below runs (three grid kernels per half step).
+// Momenta live in registers (KPT <= 4 atoms per thread; at KPT = 4, 1 024 threads, the 128-VGPR
+// budget spills a few chain temporaries) up to 4096 atoms; beyond that the multi-block path
+// below runs (two grid kernels per half step).
 #pragma clang fp contract(off)
 
 #include "common.h"
@@ -20,10 +21,15 @@ constexpr int kMaxChain = 8;
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / FMD_WAVE;
 
-// Thermostat chain in LDS; thread 0 advances it, the other threads read the scale factor.
+// Thermostat chain in registers. Every thread of the single-workgroup kernels advances its own
+// copy from the same inputs (ke2 reaches every thread with the same bits), so no thread waits
+// for another to publish the momentum scale factor. The loops run over the constant index range
+// of the arrays with the chain length M as a predicate: every array access has a constant index
+// and the arrays stay in registers (one spare slot for the j + 1 read of the last link). The
+// masses Q are read from the constants vector (uniform loads; only Q[0 .. M-1] are read).
 struct Chain {
-  double eta[kMaxChain], pe[kMaxChain], Q[kMaxChain];
-  double scale;
+  double eta[kMaxChain + 1], pe[kMaxChain + 1];
+  const double* Q;
   int M;
 };
 
@@ -39,7 +45,7 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
   return s;
 }
 
-// ASE _integrate_p_eta_j (thread 0 only)
+// ASE _integrate_p_eta_j; j is a constant after unrolling
 __device__ __forceinline__ void p_eta_j(Chain& c, int j, double ke2, double kT, double ndof_kT, double delta2,
                                         double neg_delta4) {
   double pj = c.pe[j];
@@ -57,6 +63,51 @@ __device__ __forceinline__ void p_eta_j(Chain& c, int j, double ke2, double kT, 
   pj = pj + delta2 * g;
   if (inner) pj = pj * s;
   c.pe[j] = pj;
+}
+
+__device__ __forceinline__ void load_chain(Chain& c, int M, const double* eta, const double* pe,
+                                           const double* consts) {
+  c.M = M;
+  c.Q = consts + 16;
+#pragma unroll
+  for (int j = 0; j <= kMaxChain; ++j) {
+    c.eta[j] = j < M ? eta[j] : 0.0;
+    c.pe[j] = j < M ? pe[j] : 0.0;
+  }
+}
+
+__device__ __forceinline__ void store_chain(const Chain& c, double* eta, double* pe) {
+#pragma unroll
+  for (int j = 0; j < kMaxChain; ++j) {
+    if (j < c.M) {
+      eta[j] = c.eta[j];
+      pe[j] = c.pe[j];
+    }
+  }
+}
+
+// Suzuki-Yoshida sub-step k before the momentum scaling: the p_eta_j sweep backward (j = M-1 .. 0),
+// the eta update; returns the momentum scale factor exp(-delta p_eta_0 / Q_0)
+__device__ __forceinline__ double chain_before_scale(Chain& c, double ke2, const double* consts, int k) {
+  const double kT = consts[2], ndof_kT = consts[3];
+  const double delta = consts[4 + 4 * k], delta2 = consts[5 + 4 * k];
+  const double neg_delta4 = consts[6 + 4 * k], neg_delta = consts[7 + 4 * k];
+#pragma unroll
+  for (int j = kMaxChain - 1; j >= 0; --j)
+    if (j < c.M) p_eta_j(c, j, ke2, kT, ndof_kT, delta2, neg_delta4);
+#pragma unroll
+  for (int j = 0; j < kMaxChain; ++j)
+    if (j < c.M) c.eta[j] = c.eta[j] + (delta * c.pe[j]) / c.Q[j];
+  return exp((neg_delta * c.pe[0]) / c.Q[0]);
+}
+
+// ... and after it, with the new ke2: the p_eta_j sweep forward (j = 0 .. M-1)
+__device__ __forceinline__ void chain_after_scale(Chain& c, double ke2, const double* consts, int k) {
+  const double kT = consts[2], ndof_kT = consts[3];
+  const double delta2 = consts[5 + 4 * k], neg_delta4 = consts[6 + 4 * k];
+#pragma unroll
+  for (int j = 0; j < kMaxChain; ++j)
+    if (j < c.M) p_eta_j(c, j, ke2, kT, ndof_kT, delta2, neg_delta4);
 }
 
 // Momentum storage: registers (KPT > 0) or global memory (KPT == 0).
@@ -124,54 +175,20 @@ __device__ double ke2_of(Momenta<KPT>& mom, double* red) {
   return block_sum(s, red);
 }
 
-// ASE integrate_nhc over half a time step.
+// ASE integrate_nhc over half a time step (every thread advances its copy of the chain).
 template <int KPT>
 __device__ void nhc_half(Momenta<KPT>& mom, Chain& c, const double* consts, int tloop, double* red) {
-  const double kT = consts[2], ndof_kT = consts[3];
-  const bool lead = threadIdx.x == 0;
   double ke2 = ke2_of(mom, red);
   for (int tl = 0; tl < tloop; ++tl) {
     for (int k = 0; k < 3; ++k) {
-      const double delta = consts[4 + 4 * k], delta2 = consts[5 + 4 * k];
-      const double neg_delta4 = consts[6 + 4 * k], neg_delta = consts[7 + 4 * k];
-      if (lead) {
-        for (int jj = 0; jj < c.M; ++jj) p_eta_j(c, c.M - 1 - jj, ke2, kT, ndof_kT, delta2, neg_delta4);
-        for (int j = 0; j < c.M; ++j) c.eta[j] = c.eta[j] + (delta * c.pe[j]) / c.Q[j];
-        c.scale = exp((neg_delta * c.pe[0]) / c.Q[0]);
-      }
-      __syncthreads();
-      const double scale = c.scale;
+      const double scale = chain_before_scale(c, ke2, consts, k);
       mom.for_each([&](int64_t, double (&p)[3]) {
         p[0] = p[0] * scale;
         p[1] = p[1] * scale;
         p[2] = p[2] * scale;
       });
-      ke2 = ke2_of(mom, red);  // its barriers also order the read of c.scale before the next write
-      if (lead)
-        for (int j = 0; j < c.M; ++j) p_eta_j(c, j, ke2, kT, ndof_kT, delta2, neg_delta4);
-    }
-  }
-  __syncthreads();
-}
-
-__device__ __forceinline__ void load_chain(Chain& c, int M, const double* eta, const double* pe,
-                                           const double* consts) {
-  if (threadIdx.x == 0) {
-    c.M = M;
-    for (int j = 0; j < kMaxChain; ++j) {
-      c.eta[j] = j < M ? eta[j] : 0.0;
-      c.pe[j] = j < M ? pe[j] : 0.0;
-      c.Q[j] = j < M ? consts[16 + j] : 1.0;
-    }
-  }
-  __syncthreads();
-}
-
-__device__ __forceinline__ void store_chain(const Chain& c, double* eta, double* pe) {
-  if (threadIdx.x == 0) {
-    for (int j = 0; j < c.M; ++j) {
-      eta[j] = c.eta[j];
-      pe[j] = c.pe[j];
+      ke2 = ke2_of(mom, red);
+      chain_after_scale(c, ke2, consts, k);
     }
   }
 }
@@ -186,7 +203,7 @@ __global__ void __launch_bounds__(kThreads) nhc_pre_kernel(double* q, double* p,
                                                            double* eta, double* pe, const double* consts, int64_t n,
                                                            int M, int tloop, int f32_kick) {
   __shared__ double red[kWaves];
-  __shared__ Chain c;
+  Chain c;
   load_chain(c, M, eta, pe, consts);
   Momenta<KPT> mom;
   mom.load(p, masses, n);
@@ -201,7 +218,7 @@ __global__ void __launch_bounds__(kThreads) nhc_pre_kernel(double* q, double* p,
     }
   });
   mom.store();
-  store_chain(c, eta, pe);
+  if (threadIdx.x == 0) store_chain(c, eta, pe);
 }
 
 template <int KPT>
@@ -210,7 +227,7 @@ __global__ void __launch_bounds__(kThreads) nhc_post_kernel(double* p, const voi
                                                             const double* consts, const void* e_in, int e_kind,
                                                             double* e_out, int64_t n, int M, int tloop, int f32_kick) {
   __shared__ double red[kWaves];
-  __shared__ Chain c;
+  Chain c;
   load_chain(c, M, eta, pe, consts);
   Momenta<KPT> mom;
   mom.load(p, masses, n);
@@ -226,18 +243,18 @@ __global__ void __launch_bounds__(kThreads) nhc_post_kernel(double* p, const voi
   });
   nhc_half(mom, c, consts, tloop, red);
   mom.store();
-  store_chain(c, eta, pe);
+  if (threadIdx.x == 0) store_chain(c, eta, pe);
   if (threadIdx.x == 0 && e_kind != 0)
     e_out[0] = e_kind == 2 ? static_cast<const double*>(e_in)[0] : (double)static_cast<const float*>(e_in)[0];
 }
 
 
 // ------------------------------------------------------------------------------------------
-// Multi-block path (systems beyond the register path): a half step is three grid kernels --
-// per-block partial sums of p*p/m (fixed order) -> one workgroup reduces them in block order
-// and integrates the chain, recording the momentum scale factor of every Suzuki-Yoshida
-// sub-step -> an elementwise pass multiplies p by those factors in sequence (the same roundings
-// as the single-workgroup path). After a scaling, ke2 is updated as ke2 * s^2 instead of a new
+// Multi-block path (systems beyond the register path): a half step is two grid kernels --
+// per-block partial sums of p*p/m (fixed order), after which the last workgroup to finish
+// reduces them in block order and integrates the chain, recording the momentum scale factor of
+// every Suzuki-Yoshida sub-step -> an elementwise pass multiplies p by those factors in sequence
+// (the same roundings as the single-workgroup path). After a scaling, ke2 is updated as ke2 * s^2 instead of a new
 // reduction (the reference's "scaled" ke2 update, gpu_nhc.py:520-706), which differs from the
 // recomputed sum in the last bits only.
 // work layout (float64): [0, kMaxScales) scale factors, then the block partials.
@@ -265,31 +282,18 @@ __device__ __forceinline__ void mb_chain(double* eta, double* pe, const double* 
   s = wave_sum(s);
   if (lane != 0) return;
   Chain c;
-  c.M = M;
-  for (int j = 0; j < kMaxChain; ++j) {
-    c.eta[j] = j < M ? eta[j] : 0.0;
-    c.pe[j] = j < M ? pe[j] : 0.0;
-    c.Q[j] = j < M ? consts[16 + j] : 1.0;
-  }
-  const double kT = consts[2], ndof_kT = consts[3];
+  load_chain(c, M, eta, pe, consts);
   double ke2 = s;
   int ns = 0;
   for (int tl = 0; tl < tloop; ++tl) {
     for (int k = 0; k < 3; ++k) {
-      const double delta = consts[4 + 4 * k], delta2 = consts[5 + 4 * k];
-      const double neg_delta4 = consts[6 + 4 * k], neg_delta = consts[7 + 4 * k];
-      for (int jj = 0; jj < c.M; ++jj) p_eta_j(c, c.M - 1 - jj, ke2, kT, ndof_kT, delta2, neg_delta4);
-      for (int j = 0; j < c.M; ++j) c.eta[j] = c.eta[j] + (delta * c.pe[j]) / c.Q[j];
-      const double scale = exp((neg_delta * c.pe[0]) / c.Q[0]);
+      const double scale = chain_before_scale(c, ke2, consts, k);
       work[ns++] = scale;
       ke2 = ke2 * (scale * scale);
-      for (int j = 0; j < c.M; ++j) p_eta_j(c, j, ke2, kT, ndof_kT, delta2, neg_delta4);
+      chain_after_scale(c, ke2, consts, k);
     }
   }
-  for (int j = 0; j < M; ++j) {
-    eta[j] = c.eta[j];
-    pe[j] = c.pe[j];
-  }
+  store_chain(c, eta, pe);
 }
 
 // p += kick (post half: kick first, cache F) then the block partial of p*p/m; the chain half
