@@ -182,6 +182,100 @@ __device__ __forceinline__ void gemm_f32_tile(const float* __restrict__ a, int64
   epilogue<WM, WN>(acc, row_blk + wm * (BM / 2), col_blk + wn * (BN / 2), m, n, bias, c, ldc, accumulate, act);
 }
 
+// The 64 x 64 tile of gemm_f32_tile for short K (NS = ceil(K / 32) <= 8 slices): every slice's
+// global loads are issued up front into registers, so the tile waits for one memory round trip
+// instead of one per slice (small systems, where a launch is a few workgroups, each latency-bound).
+// Slices then go through the two LDS buffers as in gemm_f32_tile, with the same MFMA sequence: the
+// same C, bit for bit.
+template <int NS, int BLAYOUT>
+__device__ __forceinline__ void gemm_f32_tile_deep(const float* __restrict__ a, int64_t lda,
+                                                   const float* __restrict__ a2, int64_t lda2, int64_t ksplit,
+                                                   const float* __restrict__ b, int64_t ldb,
+                                                   const float* __restrict__ bias, float* c, int64_t ldc, int64_t m,
+                                                   int64_t n, int64_t k, int accumulate, int act, int64_t row_blk,
+                                                   int64_t col_blk) {
+  constexpr int TB = 64, LDA = TB + 4, V = TB * BK32 / 4 / kThreads;  // 2 float4 per operand and slice
+  __shared__ float As[2][BK32][LDA];
+  __shared__ float Bs[2][BK32][LDA];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  auto load4 = [&](const float* p, bool in_rows, int64_t kk, int64_t kmax) -> float4 {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (!in_rows) return v;
+    if (kk + 3 < kmax && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) return *reinterpret_cast<const float4*>(p);
+    v.x = kk < kmax ? p[0] : 0.f;
+    v.y = kk + 1 < kmax ? p[1] : 0.f;
+    v.z = kk + 2 < kmax ? p[2] : 0.f;
+    v.w = kk + 3 < kmax ? p[3] : 0.f;
+    return v;
+  };
+  float4 ra[NS][V], rb[NS][V];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int64_t k0 = (int64_t)s * BK32;
+#pragma unroll
+    for (int q = 0; q < V; ++q) {
+      const int id = t + q * kThreads;
+      {
+        const int r = id >> 3, kc = (id & 7) * 4;
+        const int64_t gr = row_blk + r, gk = k0 + kc;
+        const float* src = k0 < ksplit ? a + gr * lda + gk : a2 + gr * lda2 + (gk - ksplit);
+        ra[s][q] = load4(src, gr < m && k0 < k, gk, k);
+      }
+      if (BLAYOUT == 0) {
+        const int r = id >> 3, kc = (id & 7) * 4;
+        const int64_t gj = col_blk + r, gk = k0 + kc;
+        rb[s][q] = load4(b + gj * ldb + gk, gj < n && k0 < k, gk, k);
+      } else {
+        constexpr int JV = TB / 4;
+        const int kr = id / JV, jc = (id % JV) * 4;
+        const int64_t gk = k0 + kr, gj = col_blk + jc;
+        rb[s][q] = load4(b + gk * ldb + gj, gk < k, gj, n);
+      }
+    }
+  }
+  auto store_slice = [&](int s, int st) {
+#pragma unroll
+    for (int q = 0; q < V; ++q) {
+      const int id = t + q * kThreads;
+      const int r = id >> 3, kc = (id & 7) * 4;
+      As[st][kc + 0][r] = ra[s][q].x;
+      As[st][kc + 1][r] = ra[s][q].y;
+      As[st][kc + 2][r] = ra[s][q].z;
+      As[st][kc + 3][r] = ra[s][q].w;
+      if (BLAYOUT == 0) {
+        Bs[st][kc + 0][r] = rb[s][q].x;
+        Bs[st][kc + 1][r] = rb[s][q].y;
+        Bs[st][kc + 2][r] = rb[s][q].z;
+        Bs[st][kc + 3][r] = rb[s][q].w;
+      } else {
+        constexpr int JV = TB / 4;
+        const int kr = id / JV, jc = (id % JV) * 4;
+        *reinterpret_cast<float4*>(&Bs[st][kr][jc]) = rb[s][q];
+      }
+    }
+  };
+  f32x16 acc[1][1];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[0][0][v] = 0.f;
+  const int nk = (int)fmd_cdiv(k, BK32);
+  store_slice(0, 0);
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    if (s >= nk) break;
+    if (s + 1 < nk && s + 1 < NS) store_slice(s + 1, (s + 1) & 1);
+#pragma unroll
+    for (int kk = 0; kk < BK32; kk += 2) {
+      const int kr = kk + (lane >> 5);
+      const float av = As[s & 1][kr][wm * 32 + (lane & 31)], bv = Bs[s & 1][kr][wn * 32 + (lane & 31)];
+      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[0][0], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  epilogue<1, 1>(acc, row_blk + wm * 32, col_blk + wn * 32, m, n, bias, c, ldc, accumulate, act);
+}
+
 template <int BM, int BN, int BLAYOUT>
 __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restrict__ a, int64_t lda,
                                                             const float* __restrict__ b, int64_t ldb,
@@ -196,6 +290,8 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restr
 // tile (w - tile0[g]) in row-major order of its 64 x 64 tiles. Each problem's result is the one
 // fmd_gemm_f32's 64 x 64 kernel gives (same K order), with [a | a2] when a2 is set.
 constexpr int kMaxGroup = 4;
+// launches of at most this many 64 x 64 tiles (four workgroups per CU) take the deep-prefetch tile
+constexpr int64_t kDeepMaxTiles = 1024;
 struct GemmDesc {
   const float* a;
   const float* a2;
@@ -241,6 +337,41 @@ __global__ void splitk_sum_kernel(const float* __restrict__ ws, int splits, int6
   if (bias) x += bias[col];
   float* d = c + r * ldc + col;
   *d = accumulate ? *d + x : x;
+}
+
+// The group with every problem's K in at most NS slices, on gemm_f32_tile_deep (the same C as
+// gemm_f32_group_kernel, bit for bit): launches of a few tiles each (small systems).
+template <int NS, int BLAYOUT>
+__global__ void __launch_bounds__(kThreads) gemm_f32_group_deep_kernel(const GemmGroup grp) {
+  const int64_t w = blockIdx.x;
+  int g = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxGroup; ++q)
+    if (q < grp.count && w >= grp.d[q].tile0) g = q;
+  const GemmDesc& d = grp.d[g];
+  const int64_t t = w - d.tile0;
+  const int64_t tm = t / d.tiles_n, tn = t - tm * d.tiles_n;
+  gemm_f32_tile_deep<NS, BLAYOUT>(d.a, d.lda, d.a2 ? d.a2 : d.a, d.a2 ? d.lda2 : d.lda, d.a2 ? d.ksplit : d.k, d.b,
+                                  d.ldb, d.bias, d.c, d.ldc, d.m, d.n, d.k, d.accumulate, grp.act, tm * 64, tn * 64);
+}
+
+// Split-K slices of at most NS * 32 k on gemm_f32_tile_deep (the partials of
+// gemm_f32_splitk_kernel, bit for bit).
+template <int NS, int BLAYOUT>
+__global__ void __launch_bounds__(kThreads) gemm_f32_splitk_deep_kernel(const float* __restrict__ a, int64_t lda,
+                                                                        const float* __restrict__ a2, int64_t lda2,
+                                                                        int64_t ksplit, const float* __restrict__ b,
+                                                                        int64_t ldb, float* ws, int64_t m, int64_t n,
+                                                                        int64_t ks, int64_t tiles_n, int64_t tiles) {
+  const int64_t w = blockIdx.x, s = w / tiles, t = w - s * tiles;
+  const int64_t tm = t / tiles_n, tn = t - tm * tiles_n;
+  const int64_t k0 = s * ks;
+  const bool second = k0 >= ksplit;
+  const float* ap = second ? a2 + (k0 - ksplit) : a + k0;
+  const int64_t la = second ? lda2 : lda;
+  const float* bp = BLAYOUT == 0 ? b + k0 : b + k0 * ldb;
+  gemm_f32_tile_deep<NS, BLAYOUT>(ap, la, ap, la, ks, bp, ldb, nullptr, ws + s * m * n, n, m, n, ks, 0, 0, tm * 64,
+                                  tn * 64);
 }
 
 template <int BLAYOUT>
@@ -955,6 +1086,118 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 
 #undef XD_ISSUE
 
+// ---------------------------------------------------- bf16 operands, copied straight into LDS
+// C = A B^T (+ bias) (+ C) with bf16 A [M, K] and B [N, K], both K-contiguous (rows 16-byte
+// aligned, K % 8 == 0): the HBM-bound form of the edge GEMM (bf16 in, fp32 out). Every 16-byte
+// chunk of an operand slice goes from global memory straight into LDS (global_load_lds_dwordx4:
+// no register stage, no VALU). Four LDS stages of 32 k (64 KB, two workgroups per CU) keep the
+// loads of slices kt + 1 .. kt + 3 in flight over slice kt's MFMAs; one v_mfma_f32_32x32x16_bf16
+// per 32 x 32 block and 16 k, K in order (the products and their order of the register-staged
+// gemm_bf16_kernel: the same C). An operand stage is 512 slots of 16 bytes: wave w's load j fills
+// slots (2 w + j) * 64 + lane, slot s holds row s / 4 of the tile and its k chunk
+// (s % 4) ^ ((row / 4) % 4), so the sixteen 16-byte operand reads of a quarter wave (16
+// consecutive rows, one chunk) fall on distinct banks. Chunks past K, and every chunk of a slice
+// past the last one (the loads are issued unconditionally so the vmcnt waits stay exact), are read
+// from a zero chunk. Rows past M / N are clamped to the last row (computed, never stored).
+// 128 x 128 tiles in XCD-aware order (the column tiles of one row block share an XCD's L2),
+// streaming stores for interior tiles.
+constexpr int BD_K = 32, BD_OP = 128 * BD_K, BD_STAGE = 2 * BD_OP;  // bf16 elements
+constexpr int kVmcnt8 = 8 | (7 << 4) | (15 << 8);                  // s_waitcnt vmcnt(8)
+__device__ __attribute__((aligned(16))) uint32_t g_bf16_zero_chunk[4];
+
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) gemm_bf16_dma_kernel(
+    const __bf16* __restrict__ a, int64_t lda, const __bf16* __restrict__ b, int64_t ldb,
+    const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int accumulate, int act,
+    int64_t n_tiles) {
+  __shared__ __attribute__((aligned(16))) __bf16 st0[BD_STAGE];
+  __shared__ __attribute__((aligned(16))) __bf16 st1[BD_STAGE];
+  __shared__ __attribute__((aligned(16))) __bf16 st2[BD_STAGE];
+  __shared__ __attribute__((aligned(16))) __bf16 st3[BD_STAGE];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, rr = lane & 31;
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t row_blk = (tile / n_tiles) * 128, col_blk = (tile % n_tiles) * 128;
+  const __bf16* zero = reinterpret_cast<const __bf16*>(g_bf16_zero_chunk);
+  // this lane's two slots per operand: row offsets and the chunk's k
+  int64_t ao[2], bo[2];
+  int kc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int s = (wave * 2 + j) * 64 + lane, r = s >> 2;
+    kc[j] = ((s & 3) ^ ((r >> 2) & 3)) * 8;
+    ao[j] = min(row_blk + r, m - 1) * lda + kc[j];
+    bo[j] = min(col_blk + r, n - 1) * ldb + kc[j];
+  }
+  const int dst0 = wave * 2 * 512;  // element offset of this wave's first slot in an operand region
+  // this lane's operand reads: row (32-row block base + rr), logical chunk 2 kk + h
+  int rdo[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) rdo[kk] = rr * BD_K + (((2 * kk + h) ^ ((rr >> 2) & 3)) * 8);
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int64_t nk = fmd_cdiv(k, BD_K);
+#define BD_ISSUE(SLICE, STAGE)                                                                      \
+  do {                                                                                              \
+    const int64_t s_ = (SLICE), k0_ = s_ * BD_K;                                                    \
+    const bool live_ = s_ < nk;                                                                     \
+    _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                                 \
+      const bool ok_ = live_ && k0_ + kc[j] < k;                                                    \
+      const __bf16* src_ = ok_ ? a + ao[j] + k0_ : zero;                                            \
+      asm volatile("" : "+v"(src_)); /* one load instruction with a per-lane address */             \
+      lds_dma16(src_, (STAGE) + dst0 + j * 512);                                                    \
+    }                                                                                               \
+    _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                                 \
+      const bool ok_ = live_ && k0_ + kc[j] < k;                                                    \
+      const __bf16* src_ = ok_ ? b + bo[j] + k0_ : zero;                                            \
+      asm volatile("" : "+v"(src_));                                                                \
+      lds_dma16(src_, (STAGE) + BD_OP + dst0 + j * 512);                                            \
+    }                                                                                               \
+  } while (0)
+#define BD_BLOCK(NEXT, ISSUE_STAGE, STAGE)                                                          \
+  do {                                                                                              \
+    __builtin_amdgcn_s_waitcnt(kVmcnt8); /* this wave's loads of the slice landed */                \
+    __builtin_amdgcn_s_barrier();        /* everyone's, and the stage to refill is read */          \
+    BD_ISSUE(NEXT, ISSUE_STAGE);                                                                    \
+    const __bf16* as_ = (STAGE) + (wm * 64) * BD_K;                                                 \
+    const __bf16* bs_ = (STAGE) + BD_OP + (wn * 64) * BD_K;                                         \
+    _Pragma("unroll") for (int kk = 0; kk < 2; ++kk) {                                              \
+      bf16x8 av_[2], bv_[2];                                                                        \
+      _Pragma("unroll") for (int i = 0; i < 2; ++i)                                                 \
+        av_[i] = *reinterpret_cast<const bf16x8*>(as_ + i * 32 * BD_K + rdo[kk]);                   \
+      _Pragma("unroll") for (int j = 0; j < 2; ++j)                                                 \
+        bv_[j] = *reinterpret_cast<const bf16x8*>(bs_ + j * 32 * BD_K + rdo[kk]);                   \
+      _Pragma("unroll") for (int i = 0; i < 2; ++i) _Pragma("unroll") for (int j = 0; j < 2; ++j)  \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av_[i], bv_[j], acc[i][j], 0, 0, 0);    \
+    }                                                                                               \
+  } while (0)
+  BD_ISSUE(0, st0);
+  BD_ISSUE(1, st1);
+  BD_ISSUE(2, st2);
+  // stage q holds slice kt with kt % 4 == q; each block refills the stage the block before read
+  int64_t kt = 0;
+  for (; kt + 4 <= nk; kt += 4) {
+    BD_BLOCK(kt + 3, st3, st0);
+    BD_BLOCK(kt + 4, st0, st1);
+    BD_BLOCK(kt + 5, st1, st2);
+    BD_BLOCK(kt + 6, st2, st3);
+  }
+  if (kt < nk) BD_BLOCK(kt + 3, st3, st0);
+  if (kt + 1 < nk) BD_BLOCK(kt + 4, st0, st1);
+  if (kt + 2 < nk) BD_BLOCK(kt + 5, st1, st2);
+#undef BD_BLOCK
+#undef BD_ISSUE
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);  // no load into LDS outlives the workgroup
+  const X3Part none{};
+  x3_finish<2>(acc, none, bias, c, ldc, m, n, accumulate, act, row_blk + wm * 64, col_blk + wn * 64, h, rr);
+}
+
 // Several independent GEMMs with pre-split weights in one launch (the node side of an interaction
 // layer at thousands of atoms): problem g owns the tiles [tile0[g], tile0[g + 1]) of the XCD-aware
 // order, (64 MB) x 128 each; A = [a | a2] fp32 (a's width a multiple of 16), split as it is
@@ -1227,6 +1470,24 @@ int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda,
   }
   if (grp.count == 0) return FMD_OK;
   FMD_REQUIRE(tiles < (int64_t(1) << 31));
+  int64_t kmax = 0;
+  for (int g = 0; g < grp.count; ++g) kmax = grp.d[g].k > kmax ? grp.d[g].k : kmax;
+  if (tiles <= kDeepMaxTiles && kmax <= 8 * BK32) {
+    // few tiles, short K: every slice's loads in flight at once (the same C)
+    if (kmax <= 4 * BK32) {
+      if (b_layout == 0)
+        hipLaunchKernelGGL((gemm_f32_group_deep_kernel<4, 0>), dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
+      else
+        hipLaunchKernelGGL((gemm_f32_group_deep_kernel<4, 1>), dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
+    } else {
+      if (b_layout == 0)
+        hipLaunchKernelGGL((gemm_f32_group_deep_kernel<8, 0>), dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
+      else
+        hipLaunchKernelGGL((gemm_f32_group_deep_kernel<8, 1>), dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
+    }
+    FMD_CHECK_LAUNCH();
+    return FMD_OK;
+  }
   if (b_layout == 0)
     hipLaunchKernelGGL(gemm_f32_group_kernel<0>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
   else
@@ -1302,7 +1563,15 @@ int fmd_gemm_splitk_f32(const float* a, int64_t lda, const float* a2, int64_t ld
   FMD_REQUIRE(tiles * splits < (int64_t(1) << 31));
   const float* a2p = a2 ? a2 : a;
   const int64_t lda2p = a2 ? lda2 : lda;
-  if (b_layout == 0)
+  if (tiles * splits <= kDeepMaxTiles && ks <= 4 * BK32) {
+    // few tiles, short slices: every slice's loads in flight at once (the same partials)
+    if (b_layout == 0)
+      hipLaunchKernelGGL((gemm_f32_splitk_deep_kernel<4, 0>), dim3((unsigned)(tiles * splits)), dim3(kThreads), 0,
+                         stream, a, lda, a2p, lda2p, ksp, b, ldb, workspace, m, n, ks, tiles_n, tiles);
+    else
+      hipLaunchKernelGGL((gemm_f32_splitk_deep_kernel<4, 1>), dim3((unsigned)(tiles * splits)), dim3(kThreads), 0,
+                         stream, a, lda, a2p, lda2p, ksp, b, ldb, workspace, m, n, ks, tiles_n, tiles);
+  } else if (b_layout == 0)
     hipLaunchKernelGGL(gemm_f32_splitk_kernel<0>, dim3((unsigned)(tiles * splits)), dim3(kThreads), 0, stream, a, lda,
                        a2p, lda2p, ksp, b, ldb, workspace, m, n, ks, tiles_n, tiles);
   else
@@ -1337,6 +1606,16 @@ int fmd_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb
   if (m == 0 || n == 0) return FMD_OK;
   FMD_REQUIRE(k == 0 || (a && b && lda >= k && ldb >= (b_layout == 0 ? k : n)));
   FMD_REQUIRE(fmd_cdiv(m, BM) < (int64_t(1) << 31) && fmd_cdiv(n, BN) < 65536);
+  if (b_layout == 0 && k > 0 && k % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(a) && aligned16(b) &&
+      fmd_cdiv(m, 128) * fmd_cdiv(n, 128) < (int64_t(1) << 31)) {
+    // K-contiguous operands with 16-byte aligned rows: the direct-to-LDS pipeline
+    const int64_t n_tiles = fmd_cdiv(n, 128), tiles = fmd_cdiv(m, 128) * n_tiles;
+    hipLaunchKernelGGL(gemm_bf16_dma_kernel, dim3((unsigned)tiles), dim3(kThreads), 0, stream,
+                       reinterpret_cast<const __bf16*>(a), lda, reinterpret_cast<const __bf16*>(b), ldb, bias, c, ldc,
+                       m, n, k, accumulate, epilogue_kind, n_tiles);
+    FMD_CHECK_LAUNCH();
+    return FMD_OK;
+  }
   dim3 grid((unsigned)fmd_cdiv(m, BM), (unsigned)fmd_cdiv(n, BN));
   if (b_layout == 0)
     hipLaunchKernelGGL(gemm_bf16_kernel<0>, grid, dim3(kThreads), 0, stream, a, lda, b, ldb, bias, c, ldc, m, n, k,

@@ -411,7 +411,9 @@ def edge_gemm(a: Tensor, w: Tensor, dtype: torch.dtype = torch.float32, *, bias:
     (b_layout 1); ``dtype`` float32 or bfloat16 operands, float32 output. No autograd."""
     with torch.no_grad():
         if dtype == torch.bfloat16:
-            return gemm(a.to(torch.bfloat16), w.to(torch.bfloat16), b_layout=1, bias=bias, epilogue=epilogue)
+            # the weight transposed once to K-contiguous [4F, 2F+8]: the direct-to-LDS bf16 kernel
+            return gemm(a.to(torch.bfloat16), w.t().contiguous().to(torch.bfloat16), b_layout=0, bias=bias,
+                        epilogue=epilogue)
         if dtype != torch.float32:
             raise ValueError(f"edge_gemm dtype must be float32 or bfloat16, got {dtype}")
         # the weight transposed once to K-contiguous [4F, 2F+8]: the layout of the fp32-accurate

@@ -316,6 +316,48 @@ def test_gemm_group_matches_single_gemms_and_fp64(device, b_layout):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("b_layout", [0, 1])
+def test_gemm_group_and_splitk_deep_prefetch_bitwise(device, b_layout):
+    """Launches of at most 1 024 tiles of 64 x 64 with K <= 256 take the tile whose slice loads are
+    all issued up front; larger launches the streaming tile. Both give the same bits: the first
+    rows of a 1 200-tile group (streaming) equal the same rows as a small group (deep), for
+    K = 96, 128, 200 and a K split [a | a2]; likewise the split-K partials (K slices of 128)."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm_group, gemm_splitk
+
+    g = torch.Generator().manual_seed(17)
+    big, small = 1200 * 64, 333
+    for k, ka in ((96, None), (128, None), (200, None), (256, 128)):
+        n = 64
+        a = torch.randn(big, k, generator=g).to(device)
+        w = (torch.randn(k, n, generator=g) / k ** 0.5).to(device)
+        wb = w if b_layout == 1 else w.t().contiguous()
+
+        def run(rows):
+            out = torch.empty(rows, n, device=device)
+            p = {"a": a[:rows], "b": wb, "out": out}
+            if ka is not None:
+                p = {"a": a[:rows, :ka], "a2": a[:rows, ka:], "b": wb, "out": out}
+            gemm_group([p], b_layout=b_layout)
+            return out
+
+        full, part = run(big), run(small)
+        assert torch.equal(full[:small], part), k
+        ref = a[:small].double() @ w.double()
+        assert oops.relative(part.cpu().numpy(), ref.cpu().numpy()) < 1e-5
+    # split-K: [N, 8C] x [8C, C] in eight slices of 128 (tall K, the VJP's node GEMM)
+    k, n = 1024, 128
+    a = torch.randn(big // 8, k, generator=g).to(device)
+    w = (torch.randn(k, n, generator=g) / k ** 0.5).to(device)
+    wb = w if b_layout == 1 else w.t().contiguous()
+    full = gemm_splitk(a, wb, b_layout=b_layout, out=torch.empty(big // 8, n, device=device))
+    part = gemm_splitk(a[:small], wb, b_layout=b_layout, out=torch.empty(small, n, device=device))
+    assert torch.equal(full[:small], part)
+    assert oops.relative(part.cpu().numpy(), (a[:small].double() @ w.double()).cpu().numpy()) < 1e-5
+
+
+@pytest.mark.gpu
 def test_gemm_group_split_plane_form(device):
     """A large fmd_gemm_group_f32 group with B [N, K] and the weights' planes (the node side of a
     layer at 10 000 atoms: >= 128 tiles of 128 x 128) runs as split-plane GEMMs
@@ -376,6 +418,40 @@ def test_gemm_bf16_against_fp64_of_rounded_inputs(device, F):
     y = edge_gemm(a.to(device), w.to(device), dtype=torch.bfloat16)
     ref = a.bfloat16().double() @ w.bfloat16().double()  # products of bf16 values are exact in fp32
     assert oops.relative(y.cpu().numpy(), ref.numpy()) < 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m,k,n", [(777, 136, 256), (1000, 72, 200), (4099, 264, 512), (300, 520, 1024),
+                                   (129, 8, 130), (5, 40, 7)])
+def test_gemm_bf16_direct_to_lds(device, m, k, n):
+    """The direct-to-LDS bf16 kernel (K-contiguous operands, aligned rows, K % 8 == 0): K tails of
+    8 / 16 / 24 past a 32-k slice, fewer slices than stages, ragged M and N, against fp64 of the
+    bf16 values; bitwise the register-staged kernel (taken when a row stride is not a multiple of
+    8 elements), with bias, accumulation and the SiLU epilogue."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm
+
+    g = torch.Generator().manual_seed(m + k + n)
+    a = torch.randn(m, k, generator=g).bfloat16()
+    b = torch.randn(n, k, generator=g).bfloat16() / k ** 0.5
+    bias = torch.randn(n, generator=g)
+    ref = a.double() @ b.double().t()
+    y = gemm(a.to(device), b.to(device), b_layout=0)
+    assert oops.relative(y.cpu().numpy(), ref.numpy()) < 1e-5
+    # the same operands at row strides of k + 4: the register-staged kernel
+    a_pad = torch.zeros(m, k + 4, dtype=torch.bfloat16)
+    a_pad[:, :k] = a
+    b_pad = torch.zeros(n, k + 4, dtype=torch.bfloat16)
+    b_pad[:, :k] = b
+    a_s, b_s = a_pad.to(device)[:, :k], b_pad.to(device)[:, :k]
+    assert torch.equal(gemm(a_s, b_s, b_layout=0), y)
+    c0 = torch.randn(m, n, generator=g).to(device)
+    for kw in ({"bias": bias.to(device)}, {"epilogue": "silu"}, {"accumulate": True}):
+        out_d, out_s = c0.clone(), c0.clone()
+        gemm(a.to(device), b.to(device), b_layout=0, out=out_d, **kw)
+        gemm(a_s, b_s, b_layout=0, out=out_s, **kw)
+        assert torch.equal(out_d, out_s), kw
 
 
 @pytest.mark.gpu
