@@ -182,100 +182,6 @@ __device__ __forceinline__ void gemm_f32_tile(const float* __restrict__ a, int64
   epilogue<WM, WN>(acc, row_blk + wm * (BM / 2), col_blk + wn * (BN / 2), m, n, bias, c, ldc, accumulate, act);
 }
 
-// The 64 x 64 tile of gemm_f32_tile for short K (NS = ceil(K / 32) <= 8 slices): every slice's
-// global loads are issued up front into registers, so the tile waits for one memory round trip
-// instead of one per slice (small systems, where a launch is a few workgroups, each latency-bound).
-// Slices then go through the two LDS buffers as in gemm_f32_tile, with the same MFMA sequence: the
-// same C, bit for bit.
-template <int NS, int BLAYOUT>
-__device__ __forceinline__ void gemm_f32_tile_deep(const float* __restrict__ a, int64_t lda,
-                                                   const float* __restrict__ a2, int64_t lda2, int64_t ksplit,
-                                                   const float* __restrict__ b, int64_t ldb,
-                                                   const float* __restrict__ bias, float* c, int64_t ldc, int64_t m,
-                                                   int64_t n, int64_t k, int accumulate, int act, int64_t row_blk,
-                                                   int64_t col_blk) {
-  constexpr int TB = 64, LDA = TB + 4, V = TB * BK32 / 4 / kThreads;  // 2 float4 per operand and slice
-  __shared__ float As[2][BK32][LDA];
-  __shared__ float Bs[2][BK32][LDA];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  auto load4 = [&](const float* p, bool in_rows, int64_t kk, int64_t kmax) -> float4 {
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (!in_rows) return v;
-    if (kk + 3 < kmax && ((reinterpret_cast<uintptr_t>(p) & 15) == 0)) return *reinterpret_cast<const float4*>(p);
-    v.x = kk < kmax ? p[0] : 0.f;
-    v.y = kk + 1 < kmax ? p[1] : 0.f;
-    v.z = kk + 2 < kmax ? p[2] : 0.f;
-    v.w = kk + 3 < kmax ? p[3] : 0.f;
-    return v;
-  };
-  float4 ra[NS][V], rb[NS][V];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const int64_t k0 = (int64_t)s * BK32;
-#pragma unroll
-    for (int q = 0; q < V; ++q) {
-      const int id = t + q * kThreads;
-      {
-        const int r = id >> 3, kc = (id & 7) * 4;
-        const int64_t gr = row_blk + r, gk = k0 + kc;
-        const float* src = k0 < ksplit ? a + gr * lda + gk : a2 + gr * lda2 + (gk - ksplit);
-        ra[s][q] = load4(src, gr < m && k0 < k, gk, k);
-      }
-      if (BLAYOUT == 0) {
-        const int r = id >> 3, kc = (id & 7) * 4;
-        const int64_t gj = col_blk + r, gk = k0 + kc;
-        rb[s][q] = load4(b + gj * ldb + gk, gj < n && k0 < k, gk, k);
-      } else {
-        constexpr int JV = TB / 4;
-        const int kr = id / JV, jc = (id % JV) * 4;
-        const int64_t gk = k0 + kr, gj = col_blk + jc;
-        rb[s][q] = load4(b + gk * ldb + gj, gk < k, gj, n);
-      }
-    }
-  }
-  auto store_slice = [&](int s, int st) {
-#pragma unroll
-    for (int q = 0; q < V; ++q) {
-      const int id = t + q * kThreads;
-      const int r = id >> 3, kc = (id & 7) * 4;
-      As[st][kc + 0][r] = ra[s][q].x;
-      As[st][kc + 1][r] = ra[s][q].y;
-      As[st][kc + 2][r] = ra[s][q].z;
-      As[st][kc + 3][r] = ra[s][q].w;
-      if (BLAYOUT == 0) {
-        Bs[st][kc + 0][r] = rb[s][q].x;
-        Bs[st][kc + 1][r] = rb[s][q].y;
-        Bs[st][kc + 2][r] = rb[s][q].z;
-        Bs[st][kc + 3][r] = rb[s][q].w;
-      } else {
-        constexpr int JV = TB / 4;
-        const int kr = id / JV, jc = (id % JV) * 4;
-        *reinterpret_cast<float4*>(&Bs[st][kr][jc]) = rb[s][q];
-      }
-    }
-  };
-  f32x16 acc[1][1];
-#pragma unroll
-  for (int v = 0; v < 16; ++v) acc[0][0][v] = 0.f;
-  const int nk = (int)fmd_cdiv(k, BK32);
-  store_slice(0, 0);
-  __syncthreads();
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    if (s >= nk) break;
-    if (s + 1 < nk && s + 1 < NS) store_slice(s + 1, (s + 1) & 1);
-#pragma unroll
-    for (int kk = 0; kk < BK32; kk += 2) {
-      const int kr = kk + (lane >> 5);
-      const float av = As[s & 1][kr][wm * 32 + (lane & 31)], bv = Bs[s & 1][kr][wn * 32 + (lane & 31)];
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[0][0], 0, 0, 0);
-    }
-    __syncthreads();
-  }
-  epilogue<1, 1>(acc, row_blk + wm * 32, col_blk + wn * 32, m, n, bias, c, ldc, accumulate, act);
-}
-
 template <int BM, int BN, int BLAYOUT>
 __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restrict__ a, int64_t lda,
                                                             const float* __restrict__ b, int64_t ldb,
@@ -290,8 +196,6 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(const float* __restr
 // tile (w - tile0[g]) in row-major order of its 64 x 64 tiles. Each problem's result is the one
 // fmd_gemm_f32's 64 x 64 kernel gives (same K order), with [a | a2] when a2 is set.
 constexpr int kMaxGroup = 4;
-// launches of at most this many 64 x 64 tiles (four workgroups per CU) take the deep-prefetch tile
-constexpr int64_t kDeepMaxTiles = 1024;
 struct GemmDesc {
   const float* a;
   const float* a2;
@@ -337,41 +241,6 @@ __global__ void splitk_sum_kernel(const float* __restrict__ ws, int splits, int6
   if (bias) x += bias[col];
   float* d = c + r * ldc + col;
   *d = accumulate ? *d + x : x;
-}
-
-// The group with every problem's K in at most NS slices, on gemm_f32_tile_deep (the same C as
-// gemm_f32_group_kernel, bit for bit): launches of a few tiles each (small systems).
-template <int NS, int BLAYOUT>
-__global__ void __launch_bounds__(kThreads) gemm_f32_group_deep_kernel(const GemmGroup grp) {
-  const int64_t w = blockIdx.x;
-  int g = 0;
-#pragma unroll
-  for (int q = 1; q < kMaxGroup; ++q)
-    if (q < grp.count && w >= grp.d[q].tile0) g = q;
-  const GemmDesc& d = grp.d[g];
-  const int64_t t = w - d.tile0;
-  const int64_t tm = t / d.tiles_n, tn = t - tm * d.tiles_n;
-  gemm_f32_tile_deep<NS, BLAYOUT>(d.a, d.lda, d.a2 ? d.a2 : d.a, d.a2 ? d.lda2 : d.lda, d.a2 ? d.ksplit : d.k, d.b,
-                                  d.ldb, d.bias, d.c, d.ldc, d.m, d.n, d.k, d.accumulate, grp.act, tm * 64, tn * 64);
-}
-
-// Split-K slices of at most NS * 32 k on gemm_f32_tile_deep (the partials of
-// gemm_f32_splitk_kernel, bit for bit).
-template <int NS, int BLAYOUT>
-__global__ void __launch_bounds__(kThreads) gemm_f32_splitk_deep_kernel(const float* __restrict__ a, int64_t lda,
-                                                                        const float* __restrict__ a2, int64_t lda2,
-                                                                        int64_t ksplit, const float* __restrict__ b,
-                                                                        int64_t ldb, float* ws, int64_t m, int64_t n,
-                                                                        int64_t ks, int64_t tiles_n, int64_t tiles) {
-  const int64_t w = blockIdx.x, s = w / tiles, t = w - s * tiles;
-  const int64_t tm = t / tiles_n, tn = t - tm * tiles_n;
-  const int64_t k0 = s * ks;
-  const bool second = k0 >= ksplit;
-  const float* ap = second ? a2 + (k0 - ksplit) : a + k0;
-  const int64_t la = second ? lda2 : lda;
-  const float* bp = BLAYOUT == 0 ? b + k0 : b + k0 * ldb;
-  gemm_f32_tile_deep<NS, BLAYOUT>(ap, la, ap, la, ks, bp, ldb, nullptr, ws + s * m * n, n, m, n, ks, 0, 0, tm * 64,
-                                  tn * 64);
 }
 
 template <int BLAYOUT>
@@ -1470,24 +1339,6 @@ int fmd_gemm_group_f32(int32_t count, const float* const* a, const int64_t* lda,
   }
   if (grp.count == 0) return FMD_OK;
   FMD_REQUIRE(tiles < (int64_t(1) << 31));
-  int64_t kmax = 0;
-  for (int g = 0; g < grp.count; ++g) kmax = grp.d[g].k > kmax ? grp.d[g].k : kmax;
-  if (tiles <= kDeepMaxTiles && kmax <= 8 * BK32) {
-    // few tiles, short K: every slice's loads in flight at once (the same C)
-    if (kmax <= 4 * BK32) {
-      if (b_layout == 0)
-        hipLaunchKernelGGL((gemm_f32_group_deep_kernel<4, 0>), dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
-      else
-        hipLaunchKernelGGL((gemm_f32_group_deep_kernel<4, 1>), dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
-    } else {
-      if (b_layout == 0)
-        hipLaunchKernelGGL((gemm_f32_group_deep_kernel<8, 0>), dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
-      else
-        hipLaunchKernelGGL((gemm_f32_group_deep_kernel<8, 1>), dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
-    }
-    FMD_CHECK_LAUNCH();
-    return FMD_OK;
-  }
   if (b_layout == 0)
     hipLaunchKernelGGL(gemm_f32_group_kernel<0>, dim3((unsigned)tiles), dim3(kThreads), 0, stream, grp);
   else
@@ -1563,15 +1414,7 @@ int fmd_gemm_splitk_f32(const float* a, int64_t lda, const float* a2, int64_t ld
   FMD_REQUIRE(tiles * splits < (int64_t(1) << 31));
   const float* a2p = a2 ? a2 : a;
   const int64_t lda2p = a2 ? lda2 : lda;
-  if (tiles * splits <= kDeepMaxTiles && ks <= 4 * BK32) {
-    // few tiles, short slices: every slice's loads in flight at once (the same partials)
-    if (b_layout == 0)
-      hipLaunchKernelGGL((gemm_f32_splitk_deep_kernel<4, 0>), dim3((unsigned)(tiles * splits)), dim3(kThreads), 0,
-                         stream, a, lda, a2p, lda2p, ksp, b, ldb, workspace, m, n, ks, tiles_n, tiles);
-    else
-      hipLaunchKernelGGL((gemm_f32_splitk_deep_kernel<4, 1>), dim3((unsigned)(tiles * splits)), dim3(kThreads), 0,
-                         stream, a, lda, a2p, lda2p, ksp, b, ldb, workspace, m, n, ks, tiles_n, tiles);
-  } else if (b_layout == 0)
+  if (b_layout == 0)
     hipLaunchKernelGGL(gemm_f32_splitk_kernel<0>, dim3((unsigned)(tiles * splits)), dim3(kThreads), 0, stream, a, lda,
                        a2p, lda2p, ksp, b, ldb, workspace, m, n, ks, tiles_n, tiles);
   else

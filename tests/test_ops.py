@@ -316,48 +316,6 @@ def test_gemm_group_matches_single_gemms_and_fp64(device, b_layout):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("b_layout", [0, 1])
-def test_gemm_group_and_splitk_deep_prefetch_bitwise(device, b_layout):
-    """Launches of at most 1 024 tiles of 64 x 64 with K <= 256 take the tile whose slice loads are
-    all issued up front; larger launches the streaming tile. Both give the same bits: the first
-    rows of a 1 200-tile group (streaming) equal the same rows as a small group (deep), for
-    K = 96, 128, 200 and a K split [a | a2]; likewise the split-K partials (K slices of 128)."""
-    import torch
-
-    from fastmd_amd.ops.wide_gemm import gemm_group, gemm_splitk
-
-    g = torch.Generator().manual_seed(17)
-    big, small = 1200 * 64, 333
-    for k, ka in ((96, None), (128, None), (200, None), (256, 128)):
-        n = 64
-        a = torch.randn(big, k, generator=g).to(device)
-        w = (torch.randn(k, n, generator=g) / k ** 0.5).to(device)
-        wb = w if b_layout == 1 else w.t().contiguous()
-
-        def run(rows):
-            out = torch.empty(rows, n, device=device)
-            p = {"a": a[:rows], "b": wb, "out": out}
-            if ka is not None:
-                p = {"a": a[:rows, :ka], "a2": a[:rows, ka:], "b": wb, "out": out}
-            gemm_group([p], b_layout=b_layout)
-            return out
-
-        full, part = run(big), run(small)
-        assert torch.equal(full[:small], part), k
-        ref = a[:small].double() @ w.double()
-        assert oops.relative(part.cpu().numpy(), ref.cpu().numpy()) < 1e-5
-    # split-K: [N, 8C] x [8C, C] in eight slices of 128 (tall K, the VJP's node GEMM)
-    k, n = 1024, 128
-    a = torch.randn(big // 8, k, generator=g).to(device)
-    w = (torch.randn(k, n, generator=g) / k ** 0.5).to(device)
-    wb = w if b_layout == 1 else w.t().contiguous()
-    full = gemm_splitk(a, wb, b_layout=b_layout, out=torch.empty(big // 8, n, device=device))
-    part = gemm_splitk(a[:small], wb, b_layout=b_layout, out=torch.empty(small, n, device=device))
-    assert torch.equal(full[:small], part)
-    assert oops.relative(part.cpu().numpy(), (a[:small].double() @ w.double()).cpu().numpy()) < 1e-5
-
-
-@pytest.mark.gpu
 def test_gemm_group_split_plane_form(device):
     """A large fmd_gemm_group_f32 group with B [N, K] and the weights' planes (the node side of a
     layer at 10 000 atoms: >= 128 tiles of 128 x 128) runs as split-plane GEMMs
