@@ -565,6 +565,8 @@ def main() -> int:
                         help="only the model_graph execution mode (MACE-like, 135 and 10 000 atoms)")
     parser.add_argument("--nhc", action="store_true",
                         help="only the NHC halves alone (135, 10 000 and 40 000 atoms)")
+    parser.add_argument("--gemm-only", action="store_true",
+                        help="only the configs[1] edge GEMMs at 40 000 atoms, F = 128 (the --pmc runs of the matrix cores)")
     parser.add_argument("--roofline-only", action="store_true",
                         help="only the dominant kernel at the 10 000-atom shape plus a 256 MiB copy (--pmc runs)")
     args = parser.parse_args()
@@ -599,6 +601,11 @@ def main() -> int:
     if args.ops:
         print(json.dumps({"ops_sweep": ops_sweep(), "hbm_peak_GBps": HBM_PEAK_GBPS,
                           "fp32_mfma_peak_TFLOPs": FP32_MFMA_PEAK_TFLOPS}), flush=True)
+        return 0
+    if args.gemm_only:
+        r = hbm_ops_bench(40000, 128, gemm=True)
+        print(json.dumps({k: r[k] for k in ("atoms", "edges", "F", "edge_gemm_f32", "gather_cat_edge_gemm_f32_fused",
+                                              "edge_gemm_bf16")}), flush=True)
         return 0
     if args.roofline_only:
         # the run profiled with rocprofv3 --pmc for the dominant kernel's HBM traffic: it at

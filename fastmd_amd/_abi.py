@@ -81,6 +81,8 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_nhc_pre_force": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _p, _p]),
     "fmd_nhc_post_force": (ctypes.c_int, [_p, _p, _i32, _p, _p, _p, _p, _p, _p, _i32, _p, _i64, _i32, _i32,
                                           _i32, _p, _p]),
+    "fmd_nhc_post_pre": (ctypes.c_int, [_p, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _i32, _p, _i64, _i32, _i32, _i32,
+                                        _p, _p]),
     "fmd_nhc_work_size": (_i64, [_i64]),
     "fmd_sum_f64": (ctypes.c_int, [_p, _i32, _i64, _p, _p]),
     "fmd_edge_geometry_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _f32, _i32, _p, _p, _p, _p]),
@@ -97,6 +99,8 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_mace_symcon_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p]),
     "fmd_mace_energy_f32": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _p, _p, _f32, _f32, _i64, _p, _p]),
     "fmd_mace_energy_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _f32, _i64, _p, _p, _p]),
+    "fmd_mace_energy_grad_f32": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _p, _p, _f32, _f32, _i64, _p, _p, _p,
+                                                _p]),
     "fmd_embed_f32": (ctypes.c_int, [_p, _p, _i64, _i32, _p, _p]),
     "fmd_embed_rows_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p]),
     "fmd_morse_f32": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _f32, _f32, _f32, _f32, _f32, _p, _p, _p]),

@@ -94,16 +94,11 @@ __global__ void edge_geometry_kernel(const float* pos, const float* cell, const 
 
 // g_vec[e] = g_r u + (g_u - (g_u . u) u) / r with g_r = sum_n g_ef[e,n] def[e,n] (over up to two
 // g_ef sources) + g_fcut dfcut; g_geo[e] = (g_ux, g_uy, g_uz, g_fcut).
-__global__ void edge_geometry_bwd_kernel(const float* geo, const float* def, int nb, const float* gef0, int64_t ld0,
-                                         const float* gef1, int64_t ld1, const float* ggeo, const int64_t* n_edges,
-                                         int64_t e_cap, float* gvec) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= e_cap) return;
-  const int64_t rows = real_rows(n_edges, e_cap);
-  if (e >= rows) {
-    gvec[3 * e] = gvec[3 * e + 1] = gvec[3 * e + 2] = 0.f;
-    return;
-  }
+// dE/d(edge vector) of row e from the gradients of its geometry: the radial-basis gradients of
+// up to two layers (gef0, gef1, times d ef / dr), the unit-vector and cutoff gradients (ggeo).
+__device__ __forceinline__ void edge_vec_grad(const float* geo, const float* def, int nb, const float* gef0,
+                                              int64_t ld0, const float* gef1, int64_t ld1, const float* ggeo,
+                                              int64_t e, float (&out)[3]) {
   const float* g = geo + 8 * e;
   float gr = 0.f;
   for (int n = 0; n < nb; ++n) {
@@ -122,7 +117,23 @@ __global__ void edge_geometry_bwd_kernel(const float* geo, const float* def, int
   const float inv_r = 1.0f / g[3];
   const float gdotu = gu[0] * g[0] + gu[1] * g[1] + gu[2] * g[2];
 #pragma unroll
-  for (int k = 0; k < 3; ++k) gvec[3 * e + k] = gr * g[k] + (gu[k] - gdotu * g[k]) * inv_r;
+  for (int k = 0; k < 3; ++k) out[k] = gr * g[k] + (gu[k] - gdotu * g[k]) * inv_r;
+}
+
+__global__ void edge_geometry_bwd_kernel(const float* geo, const float* def, int nb, const float* gef0, int64_t ld0,
+                                         const float* gef1, int64_t ld1, const float* ggeo, const int64_t* n_edges,
+                                         int64_t e_cap, float* gvec) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= e_cap) return;
+  const int64_t rows = real_rows(n_edges, e_cap);
+  if (e >= rows) {
+    gvec[3 * e] = gvec[3 * e + 1] = gvec[3 * e + 2] = 0.f;
+    return;
+  }
+  float v[3];
+  edge_vec_grad(geo, def, nb, gef0, ld0, gef1, ld1, ggeo, e, v);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) gvec[3 * e + k] = v[k];
 }
 
 // ------------------------------------------------------------------------------------------
@@ -952,6 +963,36 @@ __global__ void energy_kernel(const float* ha, const float* wr1, const float* y,
   if (lane == 0) energy[i] = e0[elem[i]] + scale * s + shift;
 }
 
+// gy of one readout unit: g wr2b_k silu'(y_k) (shared by the VJP kernel and the fused forward)
+__device__ __forceinline__ float readout_gy(float g, float w, float v) {
+  const float sg = sigmoid(v);
+  return g * w * sg * (1.0f + v * (1.0f - sg));
+}
+
+// The forward with the VJP for dE/dE_i = 1 (the explicit force path: no seed to wait for): E_i as
+// energy_kernel, and in the same wave gha_i = scale wr1, gy_i = scale wr2b silu'(y_i) (the values
+// energy_bwd_kernel writes for a null gE), one launch instead of two.
+__global__ void energy_grad_kernel(const float* ha, const float* wr1, const float* y, const float* wr2b, int C, int H,
+                                   const int32_t* elem, const float* e0, float scale, float shift, int64_t n,
+                                   float* energy, float* gha, float* gy) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64;
+  if (i >= n) return;
+  float s = 0.f;
+  for (int c = lane; c < C; c += 64) {
+    const float w = wr1[c];
+    s += ha[i * C + c] * w;
+    gha[i * C + c] = scale * w;
+  }
+  for (int k = lane; k < H; k += 64) {
+    const float v = y[i * H + k], w = wr2b[k];
+    s += v * sigmoid(v) * w;
+    gy[i * H + k] = readout_gy(scale, w, v);
+  }
+  s = wave_sum(s);
+  if (lane == 0) energy[i] = e0[elem[i]] + scale * s + shift;
+}
+
 __global__ void energy_bwd_kernel(const float* gE, const float* wr1, const float* y, const float* wr2b, int C, int H,
                                   float scale, int64_t n, float* gha, float* gy) {
   const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -964,9 +1005,7 @@ __global__ void energy_bwd_kernel(const float* gE, const float* wr1, const float
     gha[i * C + c] = g * wr1[c];
   } else {
     const int h = c - C;
-    const float v = y[i * H + h];
-    const float sg = sigmoid(v);
-    gy[i * H + h] = g * wr2b[h] * sg * (1.0f + v * (1.0f - sg));
+    gy[i * H + h] = readout_gy(g, wr2b[h], y[i * H + h]);
   }
 }
 
@@ -1361,6 +1400,17 @@ int fmd_mace_energy_f32(const float* ha, const float* wr1, const float* y, const
   if (n_atoms == 0) return FMD_OK;
   hipLaunchKernelGGL(energy_kernel, dim3((unsigned)fmd_cdiv(n_atoms, kWaves)), dim3(kThreads), 0, stream, ha, wr1, y,
                      wr2b, channels, hidden, elem, e0, scale, shift, n_atoms, energy);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_mace_energy_grad_f32(const float* ha, const float* wr1, const float* y, const float* wr2b, int32_t channels,
+                             int32_t hidden, const int32_t* elem, const float* e0, float scale, float shift,
+                             int64_t n_atoms, float* energy, float* gha, float* gy, hipStream_t stream) {
+  FMD_REQUIRE(ha && wr1 && y && wr2b && elem && e0 && energy && gha && gy && n_atoms >= 0);
+  if (n_atoms == 0) return FMD_OK;
+  hipLaunchKernelGGL(energy_grad_kernel, dim3((unsigned)fmd_cdiv(n_atoms, kWaves)), dim3(kThreads), 0, stream, ha,
+                     wr1, y, wr2b, channels, hidden, elem, e0, scale, shift, n_atoms, energy, gha, gy);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

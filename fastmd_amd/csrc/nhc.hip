@@ -249,6 +249,48 @@ __global__ void __launch_bounds__(kThreads) nhc_post_kernel(double* p, const voi
 }
 
 
+// Step n's post-force half followed by step n + 1's pre-force half in one launch (consecutive in a
+// window of steps): momenta and chain stay in registers between the halves; every operation is
+// the one nhc_post_kernel and nhc_pre_kernel perform, in the same order (the same bits), the pre
+// half's kick reading the forces the post half just cached.
+template <int KPT>
+__global__ void __launch_bounds__(kThreads) nhc_post_pre_kernel(double* q, double* p, const void* f_in, int f_in_64,
+                                                                double* f_cache, const double* masses, double* eta,
+                                                                double* pe, const double* consts, const void* e_in,
+                                                                int e_kind, double* e_out, int64_t n, int M, int tloop,
+                                                                int f32_kick) {
+  __shared__ double red[kWaves];
+  Chain c;
+  load_chain(c, M, eta, pe, consts);
+  Momenta<KPT> mom;
+  mom.load(p, masses, n);
+  const double dt = consts[0], dt2 = consts[1];
+  mom.for_each([&](int64_t a, double (&pv)[3]) {
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+      const double fv = f_in_64 ? static_cast<const double*>(f_in)[3 * a + d]
+                                : (double)static_cast<const float*>(f_in)[3 * a + d];
+      pv[d] = pv[d] + kick_of(dt2, fv, f32_kick);
+      f_cache[3 * a + d] = fv;
+    }
+  });
+  nhc_half(mom, c, consts, tloop, red);
+  if (threadIdx.x == 0 && e_kind != 0)
+    e_out[0] = e_kind == 2 ? static_cast<const double*>(e_in)[0] : (double)static_cast<const float*>(e_in)[0];
+  nhc_half(mom, c, consts, tloop, red);
+  mom.for_each([&](int64_t a, double (&pv)[3]) {
+    const double m = masses[a];
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+      pv[d] = pv[d] + kick_of(dt2, f_cache[3 * a + d], f32_kick);
+      q[3 * a + d] = q[3 * a + d] + (dt * pv[d]) / m;
+    }
+  });
+  mom.store();
+  if (threadIdx.x == 0) store_chain(c, eta, pe);
+}
+
+
 // ------------------------------------------------------------------------------------------
 // Multi-block path (systems beyond the register path): a half step is two grid kernels --
 // per-block partial sums of p*p/m (fixed order), after which the last workgroup to finish
@@ -361,6 +403,44 @@ __global__ void __launch_bounds__(kMbThreads) nhc_mb_apply_kernel(double* q, dou
   }
 }
 
+// The multi-block form of the same pair: between nhc_mb_partials_chain_kernel (post half: kick,
+// partials, chain) and nhc_mb_apply_kernel (pre half: scales, kick, drift), one launch applies the
+// post half's scales to p and forms the pre half's partials from the scaled p, its last workgroup
+// running the pre half's chain (the work the post half's apply launch and the pre half's partials
+// launch did, in the same order: the same bits). The last workgroup overwrites the scale factors
+// only after every workgroup has read them (each reads them before it counts itself).
+__global__ void __launch_bounds__(kMbThreads) nhc_mb_apply_partials_chain_kernel(
+    double* p, const double* masses, const double* consts, int nscale, int64_t n, double* work, unsigned int* counter,
+    double* eta, double* pe, int M, int tloop, const void* e_in, int e_kind, double* e_out) {
+  __shared__ double red[kMbThreads / FMD_WAVE];
+  __shared__ int last;
+  const int64_t a = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (a == 0 && e_kind != 0)
+    e_out[0] = e_kind == 2 ? static_cast<const double*>(e_in)[0] : (double)static_cast<const float*>(e_in)[0];
+  double s = 0.0;
+  if (a < n) {
+    const double m = masses[a];
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+      double pv = p[3 * a + d];
+      for (int k = 0; k < nscale; ++k) pv = pv * work[k];
+      p[3 * a + d] = pv;
+      s = s + (pv * pv) / m;
+    }
+  }
+  s = block_sum_mb(s, red);
+  if (threadIdx.x == 0) {
+    work[kMaxScales + blockIdx.x] = s;
+    __threadfence();
+    last = atomicAdd(counter, 1u) == gridDim.x - 1 ? 1 : 0;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  if (threadIdx.x < FMD_WAVE) mb_chain(eta, pe, consts, M, tloop, gridDim.x, work);
+  if (threadIdx.x == 0) atomicExch(counter, 0u);
+}
+
 unsigned int* mb_counter(double* work, int64_t n) {
   return reinterpret_cast<unsigned int*>(work + kMaxScales + fmd_cdiv(n > 0 ? n : 1, kMbThreads));
 }
@@ -444,6 +524,38 @@ int fmd_nhc_post_force(double* p, const void* f_in, int32_t f_in_is_f64, double*
   }
   FMD_NHC_DISPATCH(nhc_post_kernel, p, f_in, f_in_is_f64, f_cache, masses, eta, p_eta, consts, e_in, e_kind, e_out,
                    n_atoms, tchain, tloop, f32_kick);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_nhc_post_pre(double* q, double* p, const void* f_in, int32_t f_in_is_f64, double* f_cache,
+                     const double* masses, double* eta, double* p_eta, const double* consts, const void* e_in,
+                     int32_t e_kind, double* e_out, int64_t n_atoms, int32_t tchain, int32_t tloop, int32_t f32_kick,
+                     double* work, hipStream_t stream) {
+  FMD_REQUIRE(q && p && f_in && f_cache && masses && eta && p_eta && consts && n_atoms > 0);
+  FMD_REQUIRE(tchain >= 1 && tchain <= kMaxChain && tloop >= 1);
+  FMD_REQUIRE(e_kind == 0 || (e_in && e_out && (e_kind == 1 || e_kind == 2)));
+  const int threads = nhc_threads(n_atoms);
+  const int kpt = pick_kpt(n_atoms, threads);
+  if (kpt == 0) {
+    FMD_REQUIRE(work && 3 * tloop <= kMaxScales);
+    const int64_t nb = fmd_cdiv(n_atoms, kMbThreads);
+    unsigned int* counter = mb_counter(work, n_atoms);
+    hipLaunchKernelGGL(nhc_mb_partials_chain_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, p, f_in,
+                       f_in_is_f64, f_cache, masses, consts, 1, f32_kick, n_atoms, work, counter, eta, p_eta, tchain,
+                       tloop);
+    FMD_CHECK_LAUNCH();
+    hipLaunchKernelGGL(nhc_mb_apply_partials_chain_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, p, masses,
+                       consts, 3 * tloop, n_atoms, work, counter, eta, p_eta, tchain, tloop, e_in, e_kind, e_out);
+    FMD_CHECK_LAUNCH();
+    hipLaunchKernelGGL(nhc_mb_apply_kernel, dim3((unsigned)nb), dim3(kMbThreads), 0, stream, q, p,
+                       (const double*)f_cache, masses, consts, 3 * tloop, 1, f32_kick, n_atoms, (const double*)work,
+                       (const void*)nullptr, 0, (double*)nullptr);
+    FMD_CHECK_LAUNCH();
+    return FMD_OK;
+  }
+  FMD_NHC_DISPATCH(nhc_post_pre_kernel, q, p, f_in, f_in_is_f64, f_cache, masses, eta, p_eta, consts, e_in, e_kind,
+                   e_out, n_atoms, tchain, tloop, f32_kick);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -281,10 +281,8 @@ class GPUNoseHooverChainNVT(StatefulIntegrator):
                   _abi.stream_handle(self.device))
         return st.positions
 
-    @roctx_ranged("gpu_integrator")
-    def step_post_force(self, forces: Tensor, energy: Tensor | None = None, state: NHCState | None = None) -> None:
-        """p += dt/2 * F(q_{n+1}); NHC(dt/2); cache F (float64) and the energy."""
-        st = self.state if state is None else state
+    def _post_inputs(self, forces: Tensor, energy: Tensor | None):
+        """Forces as a contiguous float32/float64 [N, 3] on this device and the energy's kind."""
         forces = forces.reshape(self.n_atoms, 3)
         if forces.dtype not in (torch.float32, torch.float64):
             forces = forces.to(torch.float32)
@@ -298,11 +296,31 @@ class GPUNoseHooverChainNVT(StatefulIntegrator):
             if energy.dtype not in (torch.float32, torch.float64):
                 energy = energy.to(torch.float64)
             e_kind = 2 if energy.dtype == torch.float64 else 1
-        _abi.call("fmd_nhc_post_force", st.momenta.data_ptr(), forces.data_ptr(),
-                  1 if forces.dtype == torch.float64 else 0, st.forces.data_ptr(), self.masses.data_ptr(),
+        return forces, 1 if forces.dtype == torch.float64 else 0, energy, e_kind
+
+    @roctx_ranged("gpu_integrator")
+    def step_post_force(self, forces: Tensor, energy: Tensor | None = None, state: NHCState | None = None) -> None:
+        """p += dt/2 * F(q_{n+1}); NHC(dt/2); cache F (float64) and the energy."""
+        st = self.state if state is None else state
+        forces, f64, energy, e_kind = self._post_inputs(forces, energy)
+        _abi.call("fmd_nhc_post_force", st.momenta.data_ptr(), forces.data_ptr(), f64, st.forces.data_ptr(),
+                  self.masses.data_ptr(),
                   st.eta.data_ptr(), st.p_eta.data_ptr(), self.consts.data_ptr(), _abi.ptr(energy), e_kind,
                   st.potential_energy.data_ptr(), self.n_atoms, self.tchain, self.tloop,
                   1 if self.f32_kick else 0, self._work.data_ptr(), _abi.stream_handle(self.device))
+
+    @roctx_ranged("gpu_integrator")
+    def step_post_pre(self, forces: Tensor, energy: Tensor | None = None, state: NHCState | None = None) -> Tensor:
+        """``step_post_force(forces, energy)`` then the next step's ``step_pre_force()`` in one launch
+        (fmd_nhc_post_pre; the same state bit for bit). Returns the float64 positions view."""
+        st = self.state if state is None else state
+        forces, f64, energy, e_kind = self._post_inputs(forces, energy)
+        _abi.call("fmd_nhc_post_pre", st.positions.data_ptr(), st.momenta.data_ptr(), forces.data_ptr(), f64,
+                  st.forces.data_ptr(), self.masses.data_ptr(), st.eta.data_ptr(), st.p_eta.data_ptr(),
+                  self.consts.data_ptr(), _abi.ptr(energy), e_kind, st.potential_energy.data_ptr(), self.n_atoms,
+                  self.tchain, self.tloop, 1 if self.f32_kick else 0, self._work.data_ptr(),
+                  _abi.stream_handle(self.device))
+        return st.positions
 
     def step(self, force_fn, state: NHCState | None = None):
         st = self.state if state is None else state

@@ -164,12 +164,16 @@ class WholeStepGraphRunner:
         energy = out["e"].reshape(-1)  # one energy (or one per replica of a replica batch)
         return forces, energy, status
 
-    def _step_body(self, last: bool) -> None:
+    def _step_body(self, last: bool, positions: Tensor | None = None, fuse_next: bool = False):
+        """One step. ``positions``: this step's pre-force half already ran (fused into the step
+        before). ``fuse_next``: the next step's pre-force half runs fused with this step's post-force
+        half (one integrator launch); its positions are returned."""
         integrator = self.integrator
-        positions = integrator.step_pre_force()
+        if positions is None:
+            positions = integrator.step_pre_force()
         forces, energy, status = self._evaluate(positions)
-        with torch.no_grad():
-            integrator.step_post_force(forces.detach(), energy=energy.detach())
+        # the flag fold reads only the build's status: it goes before the integrator, so that
+        # the post-force half and the next pre-force half are adjacent
         self.builder.accumulate_window(status, window_overflow=self.window_overflow,
                                        window_capacity_overflow=self.window_capacity_overflow,
                                        window_max_edges=self.window_max_edges,
@@ -177,6 +181,11 @@ class WholeStepGraphRunner:
                                        check_isolated=self.validate_isolated_atoms,
                                        stats=self._window_stats if last else None,
                                        window_max_triplets=self.window_max_triplets)
+        with torch.no_grad():
+            if fuse_next:
+                return integrator.step_post_pre(forces.detach(), energy=energy.detach())
+            integrator.step_post_force(forces.detach(), energy=energy.detach())
+        return None
 
     def _window_body(self) -> None:
         self.integrator.backup()
@@ -185,8 +194,11 @@ class WholeStepGraphRunner:
         self.window_max_edges.zero_()
         self.window_max_isolated.zero_()
         self.window_max_triplets.zero_()
+        fuse = hasattr(self.integrator, "step_post_pre")
+        positions = None
         for k in range(self.steps_per_launch):
-            self._step_body(last=k == self.steps_per_launch - 1)
+            last = k == self.steps_per_launch - 1
+            positions = self._step_body(last=last, positions=positions, fuse_next=fuse and not last)
 
     def _capture(self) -> None:
         integrator = self.integrator

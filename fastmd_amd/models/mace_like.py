@@ -568,8 +568,16 @@ class _MaceLikeEnergy(Function):
         if y is None:
             y = gemm(h0, model.Wr2a, b_layout=1)  # [N, H]
         energy = _empty(n, device=dev)
-        _call("fmd_mace_energy_f32", h_first.data_ptr(), model.wr1.data_ptr(), y.data_ptr(), model.wr2b.data_ptr(),
-              C, H, elem.data_ptr(), model.e0.data_ptr(), float(cfg.scale), float(cfg.shift), n, energy.data_ptr())
+        if getattr(ctx, "seed_ones", False):
+            # the explicit force path (seed dE/dE_i = 1): the readout's gradients in the same launch
+            ctx.gha, ctx.gy = _empty(n, C, device=dev), _empty(n, H, device=dev)
+            _call("fmd_mace_energy_grad_f32", h_first.data_ptr(), model.wr1.data_ptr(), y.data_ptr(),
+                  model.wr2b.data_ptr(), C, H, elem.data_ptr(), model.e0.data_ptr(), float(cfg.scale),
+                  float(cfg.shift), n, energy.data_ptr(), ctx.gha.data_ptr(), ctx.gy.data_ptr())
+        else:
+            _call("fmd_mace_energy_f32", h_first.data_ptr(), model.wr1.data_ptr(), y.data_ptr(),
+                  model.wr2b.data_ptr(), C, H, elem.data_ptr(), model.e0.data_ptr(), float(cfg.scale),
+                  float(cfg.shift), n, energy.data_ptr())
         ctx.model, ctx.inputs, ctx.saved = model, inputs, saved
         ctx.geo, ctx.de, ctx.y, ctx.ef, ctx.factored, ctx.merged = geo, de, y, ef, factored, merged
         ctx.n, ctx.e_cap = n, e_cap
@@ -582,7 +590,10 @@ class _MaceLikeEnergy(Function):
 
 
 class _Saved:
-    """What the forward keeps for the VJP (the autograd ctx, or this holder outside autograd)."""
+    """What the forward keeps for the VJP (the autograd ctx, or this holder outside autograd). The
+    explicit force path seeds dE/dE_i = 1, so its forward also forms the readout's gradients."""
+
+    seed_ones = True
 
 
 def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None):
@@ -600,10 +611,13 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
     order = _atom_order(batch, n)
     wpa = _waves_per_atom(batch, n)
     # readouts: gha = dE/d(first layer's h0 out), gy -> dE/d(last layer's h0 out)
-    gy = _empty(n, H, device=dev)
-    gha = _empty(n, C, device=dev)
-    _call("fmd_mace_energy_bwd_f32", _abi.ptr(gE), model.wr1.data_ptr(), ctx.y.data_ptr(), model.wr2b.data_ptr(),
-          C, H, float(cfg.scale), n, gha.data_ptr(), gy.data_ptr())
+    if gE is None and getattr(ctx, "gha", None) is not None:
+        gha, gy = ctx.gha, ctx.gy  # formed by the forward's energy launch
+    else:
+        gy = _empty(n, H, device=dev)
+        gha = _empty(n, C, device=dev)
+        _call("fmd_mace_energy_bwd_f32", _abi.ptr(gE), model.wr1.data_ptr(), ctx.y.data_ptr(),
+              model.wr2b.data_ptr(), C, H, float(cfg.scale), n, gha.data_ptr(), gy.data_ptr())
     # dE/dh0 out of the last layer (with one layer, the first readout's gradient joins here)
     L = len(model.layers)
     # merged: the last layer's h0n was never formed; its VJP's first products start from gy

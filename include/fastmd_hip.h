@@ -472,6 +472,15 @@ int fmd_nhc_post_force(double* p, const void* f_in, int32_t f_in_is_f64, double*
                        const void* e_in, int32_t e_kind, double* e_out, int64_t n_atoms,
                        int32_t tchain, int32_t tloop, int32_t f32_kick, double* work, hipStream_t stream);
 
+/* fmd_nhc_post_force of step n then fmd_nhc_pre_force of step n + 1 (the pre half's kick with the
+ * forces just cached in f_cache), as one launch (multi-block: three instead of four); the same
+ * state, bit for bit. Consecutive steps of a window (whole_step_cuda_graph.py:56-736 runs
+ * _nhc_post_force_kernel and _nhc_pre_force_kernel back to back there, gpu_nhc.py:359-425). */
+int fmd_nhc_post_pre(double* q, double* p, const void* f_in, int32_t f_in_is_f64, double* f_cache,
+                     const double* masses, double* eta, double* p_eta, const double* consts, const void* e_in,
+                     int32_t e_kind, double* e_out, int64_t n_atoms, int32_t tchain, int32_t tloop, int32_t f32_kick,
+                     double* work, hipStream_t stream);
+
 /* float64 elements of the `work` buffer the NHC entry points need for n_atoms (systems of more
  * than 4096 atoms run the multi-block path: per-block partial sums with the chain half step run
  * by the last workgroup to finish (a completion counter in the last slot of `work`, which must be
@@ -582,6 +591,12 @@ int fmd_mace_energy_f32(const float* ha, const float* wr1, const float* y, const
                         int64_t n_atoms, float* energy, hipStream_t stream);
 int fmd_mace_energy_bwd_f32(const float* gE, const float* wr1, const float* y, const float* wr2b, int32_t channels,
                             int32_t hidden, float scale, int64_t n_atoms, float* gha, float* gy, hipStream_t stream);
+/* fmd_mace_energy_f32 together with fmd_mace_energy_bwd_f32's gha and gy for a null gE, in one
+ * launch (the explicit force path of EnergyDerivative, energy_derivative.py:110-140, whose seed is
+ * dE/dE_i = 1). */
+int fmd_mace_energy_grad_f32(const float* ha, const float* wr1, const float* y, const float* wr2b, int32_t channels,
+                             int32_t hidden, const int32_t* elem, const float* e0, float scale, float shift,
+                             int64_t n_atoms, float* energy, float* gha, float* gy, hipStream_t stream);
 /* h0[i] = table[elem[i]]. */
 int fmd_embed_f32(const int32_t* elem, const float* table, int64_t n_atoms, int32_t channels, float* h0,
                   hipStream_t stream);

@@ -172,6 +172,54 @@ def test_gpu_nhc_large_systems(device, n_cells):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("n_cells", [3, (8, 10, 10), (10, 10, 20)])
+@pytest.mark.parametrize("force_dtype", ["float32", "float64"])
+def test_gpu_nhc_post_pre_fused_bitwise(device, n_cells, force_dtype):
+    """fmd_nhc_post_pre (step n's post-force half and step n + 1's pre-force half in one launch;
+    three launches instead of four on the multi-block path) leaves the same state, bit for bit, as
+    the two halves called one after the other: 135, 4 000 and 10 000 atoms, float32 and float64
+    forces, with the energy copied; and the integration stays within 1e-12 of the oracle."""
+    import torch
+
+    from fastmd_amd.execution.gpu_nhc import GPUNoseHooverChainNVT, maxwell_boltzmann_momenta
+
+    print(f"[nhc-fused] {n_cells} {force_dtype}", flush=True)
+    s = systems.perovskite(n_cells)
+    p = maxwell_boltzmann_momenta(s.masses, 500.0, seed=0)
+    f = onhc.harmonic(s.positions, 0.3)
+    f0, e0 = f(s.positions)
+    kw = dict(temperature_K=500.0, timestep=0.25 * units.fs, tdamp=25 * units.fs)
+    o = onhc.NHC(s.masses, s.positions, p, forces=f0, energy=e0, **kw)
+    sep = GPUNoseHooverChainNVT(s.masses, s.positions, p, forces=f0, potential_energy=e0, device=device, **kw)
+    fus = GPUNoseHooverChainNVT(s.masses, s.positions, p, forces=f0, potential_energy=e0, device=device, **kw)
+    q0 = torch.tensor(s.positions, device=device)
+    dt = getattr(torch, force_dtype)
+    q_f = fus.step_pre_force()
+    steps = 12
+    for k in range(steps):
+        o.step(f)
+        q_s = sep.step_pre_force()
+        e = torch.tensor([o.e], device=device, dtype=torch.float64)
+        sep.step_post_force((-0.3 * (q_s - q0)).to(dt), energy=e)
+        forces = (-0.3 * (q_f - q0)).to(dt)
+        if k + 1 < steps:
+            q_f = fus.step_post_pre(forces, energy=e)
+        else:
+            fus.step_post_force(forces, energy=e)
+        if k + 1 < steps:  # the fused integrator is half a step ahead: compare after its pre half
+            sep_next = sep.state.numpy()
+            fus_now = fus.state.numpy()
+            assert np.array_equal(sep_next["forces"], fus_now["forces"])
+    a, b = sep.state.numpy(), fus.state.numpy()
+    for name in ("positions", "momenta", "forces", "eta", "p_eta", "potential_energy"):
+        assert np.array_equal(a[name], b[name]), name
+    if force_dtype == "float64":
+        for name, ref in (("positions", o.q), ("momenta", o.p), ("p_eta", o.p_eta)):
+            rel = np.max(np.abs(a[name] - ref)) / np.max(np.abs(ref))
+            assert rel < 1e-12, (name, rel)
+
+
+@pytest.mark.gpu
 def test_gpu_nhc_set_temperature_and_rollback(device):
     import torch
 
