@@ -1067,6 +1067,91 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   x3_finish<2>(acc, none, bias, c, ldc, m, n, accumulate, act, row_blk + wm * 64, col_blk + wn * 64, h, rr);
 }
 
+// bf16 GEMM for tall A (tens of thousands of edge rows and more, K <= 272) with a column slab of
+// B resident in LDS. Each workgroup has 8 waves, at most two per SIMD, so that the whole K extent
+// of a wave's A rows and its 32 x 32 NCB accumulators fit in registers. It copies NSL slabs of
+// 32 NCB of B's rows (columns of C) once, zero-padded to Kp = 16 ceil(K / 16), with a row stride
+// of Kp + 8 elements (odd multiples of 4 dwords: conflict-free 16-byte reads). It then walks row
+// blocks of 256 rows, a wave per 32 rows. A wave loads its rows' whole K extent straight into
+// registers (one 16-byte load per lane and k-step, issued together), then, slab by slab, runs the
+// k-steps in order over the NCB column blocks and stores them. Each A row is read once per
+// workgroup column range (N / (32 NCB NSL) times) and B once per workgroup;
+// the 128 x 128 tiles read both operands per tile. Workgroup w runs on XCD w % 8, and the slabs of
+// one row walker are placed on the same XCD, so the walker's rows come from HBM once per XCD L2.
+// Per element it runs the same MFMA sequence over the same k-steps as the 128 x 128 kernels
+// (k-steps of 16 in order, zero chunk past K): bitwise their result.
+constexpr int BR_WAVES = 8, BR_ROWS = 32 * BR_WAVES;
+
+template <int NCB, int NKS, int NSL>
+__global__ void __launch_bounds__(64 * BR_WAVES) __attribute__((amdgpu_waves_per_eu(1, 2))) gemm_bf16_bres_kernel(
+    const __bf16* __restrict__ a, int64_t lda, const __bf16* __restrict__ b, int64_t ldb,
+    const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int accumulate, int act,
+    int n_slabs, int walkers) {
+  constexpr int NB = 32 * NCB, SKMAX = 16 * NKS + 8;
+  __shared__ __attribute__((aligned(16))) __bf16 sb[NSL * NB * SKMAX];
+  const int t = threadIdx.x, lane = t & 63, h = lane >> 5, rr = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int w = blockIdx.x, xcd = w & 7, u = w >> 3;
+  const int slab = u % n_slabs, walker = xcd + 8 * (u / n_slabs);
+  const int nks = (int)fmd_cdiv(k, 16), sk = 16 * nks + 8;
+  const int64_t col_blk = (int64_t)slab * NSL * NB;
+  // the slab of B: 16-byte chunks, rows past N clamped (their columns are never stored)
+  const int cpr = sk / 8;  // chunks per LDS row (the last one is padding, left unwritten)
+  for (int q = t; q < NSL * NB * cpr; q += 64 * BR_WAVES) {
+    const int r = q / cpr, kq = (q - r * cpr) * 8;
+    if (kq >= 16 * nks) continue;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (kq < k) v = *reinterpret_cast<const uint4*>(b + min(col_blk + r, n - 1) * ldb + kq);
+    *reinterpret_cast<uint4*>(sb + r * sk + kq) = v;
+  }
+  __syncthreads();
+  const __bf16* zero = reinterpret_cast<const __bf16*>(g_bf16_zero_chunk);
+  const int64_t n_rb = fmd_cdiv(m, BR_ROWS);
+  const X3Part none{};
+  for (int64_t rb = walker; rb < n_rb; rb += walkers) {
+    const int64_t row0 = rb * BR_ROWS + wave * 32;
+    if (row0 >= m) break;  // uniform per wave; the wave's later row blocks start further on
+    const __bf16* ap = a + min(row0 + rr, m - 1) * lda + 8 * h;
+    bf16x8 av[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      if (ks < nks) {
+        const __bf16* src = 16 * ks + 8 * h < k ? ap + 16 * ks : zero;
+        asm volatile("" : "+v"(src));  // one load with a per-lane address, no branch
+        av[ks] = *reinterpret_cast<const bf16x8*>(src);
+      }
+    }
+    // the slabs one after the other on the same A registers (one accumulator set live)
+#pragma unroll 1
+    for (int sl = 0; sl < NSL; ++sl) {
+      const int64_t col0 = col_blk + (int64_t)sl * NB;
+      if (col0 >= n) break;
+      f32x16 acc[NCB / 2][1][2];
+#pragma unroll
+      for (int p = 0; p < NCB / 2; ++p)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[p][0][j][v] = 0.f;
+      const __bf16* bs = sb + (sl * NB + rr) * sk + 8 * h;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        if (ks < nks) {
+#pragma unroll
+          for (int cb = 0; cb < NCB; ++cb) {
+            const bf16x8 bv = *reinterpret_cast<const bf16x8*>(bs + cb * 32 * sk + 16 * ks);
+            acc[cb / 2][0][cb % 2] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[ks], bv, acc[cb / 2][0][cb % 2], 0, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < NCB / 2; ++p)
+        x3_finish<1>(acc[p], none, bias, c, ldc, m, n, accumulate, act, row0, col0 + 64 * p, h, rr);
+    }
+  }
+}
+
 // Several independent GEMMs with pre-split weights in one launch (the node side of an interaction
 // layer at thousands of atoms): problem g owns the tiles [tile0[g], tile0[g + 1]) of the XCD-aware
 // order, (64 MB) x 128 each; A = [a | a2] fp32 (a's width a multiple of 16), split as it is
@@ -1133,6 +1218,11 @@ __global__ void split3_kernel(const float* __restrict__ src, int64_t ld, int64_t
 #undef X3_COMPUTE
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// the resident-B bf16 kernel: taken from this many rows (below, the 128 x 128 tiles fill the chip
+// with fewer re-reads to save); one workgroup per CU of MI355X's 256
+constexpr int64_t kBresMinRows = 32768;
+constexpr int kBresWorkgroups = 256;
 
 bool k_fits_int(int32_t n_parts, const int32_t* widths) {
   if (n_parts < 1 || n_parts > 3) return false;
@@ -1451,6 +1541,28 @@ int fmd_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb
   FMD_REQUIRE(fmd_cdiv(m, BM) < (int64_t(1) << 31) && fmd_cdiv(n, BN) < 65536);
   if (b_layout == 0 && k > 0 && k % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(a) && aligned16(b) &&
       fmd_cdiv(m, 128) * fmd_cdiv(n, 128) < (int64_t(1) << 31)) {
+    const int64_t nks = fmd_cdiv(k, 16);
+    if (m >= kBresMinRows && nks <= 17) {
+      // tall A, K <= 272 (A's whole K extent in a wave's registers beside its accumulators):
+      // B's column slabs resident in LDS. Two 128-column slabs per workgroup (A loaded once for
+      // both) when there are row blocks enough for every workgroup at half the slab count, else one
+      const int nsl = fmd_cdiv(m, BR_ROWS) >= 2 * kBresWorkgroups ? 2 : 1;
+      const int n_slabs = (int)fmd_cdiv(n, nsl * 32 * 4);
+      const int walkers = max(8, (kBresWorkgroups / n_slabs) & ~7);
+      const dim3 grid((unsigned)(walkers * n_slabs)), block(64 * BR_WAVES);
+      const __bf16 *ab = reinterpret_cast<const __bf16*>(a), *bb = reinterpret_cast<const __bf16*>(b);
+#define BRES_LAUNCH(KS, SL)                                                                                   \
+  hipLaunchKernelGGL((gemm_bf16_bres_kernel<4, KS, SL>), grid, block, 0, stream, ab, lda, bb, ldb, bias, c, ldc, m, \
+                     n, k, accumulate, epilogue_kind, n_slabs, walkers)
+      if (nks <= 9) {
+        if (nsl == 2) BRES_LAUNCH(9, 2); else BRES_LAUNCH(9, 1);
+      } else {
+        if (nsl == 2) BRES_LAUNCH(17, 2); else BRES_LAUNCH(17, 1);
+      }
+#undef BRES_LAUNCH
+      FMD_CHECK_LAUNCH();
+      return FMD_OK;
+    }
     // K-contiguous operands with 16-byte aligned rows: the direct-to-LDS pipeline
     const int64_t n_tiles = fmd_cdiv(n, 128), tiles = fmd_cdiv(m, 128) * n_tiles;
     hipLaunchKernelGGL(gemm_bf16_dma_kernel, dim3((unsigned)tiles), dim3(kThreads), 0, stream,

@@ -413,6 +413,40 @@ def test_gemm_bf16_direct_to_lds(device, m, k, n):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m,k,n", [(40000, 264, 512), (33001, 136, 256), (32768, 40, 130), (50000, 272, 200),
+                                   (140000, 264, 512), (131073, 136, 300)])
+def test_gemm_bf16_resident_b(device, m, k, n):
+    """The resident-B bf16 kernel (at least 32 768 rows, K <= 272, aligned K-contiguous operands):
+    K tails of 8 past a 16-k step, a ragged last row block and column slab, one slab or several,
+    one or two slabs per workgroup (from 131 072 rows);
+    against fp64 of the bf16 values on a row sample, and bitwise the register-staged kernel with
+    bias, accumulation and the SiLU epilogue."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm
+
+    g = torch.Generator().manual_seed(m + k + n)
+    a = torch.randn(m, k, generator=g).bfloat16()
+    b = torch.randn(n, k, generator=g).bfloat16() / k ** 0.5
+    bias = torch.randn(n, generator=g)
+    y = gemm(a.to(device), b.to(device), b_layout=0)
+    rows = torch.cat([torch.arange(0, 700), torch.arange(m - 300, m)])
+    ref = a[rows].double() @ b.double().t()
+    assert oops.relative(y.cpu()[rows].numpy(), ref.numpy()) < 1e-5
+    # row strides of k + 4: the register-staged kernel, the same k-steps in the same order
+    a_pad = torch.zeros(m, k + 4, dtype=torch.bfloat16)
+    a_pad[:, :k] = a
+    a_s = a_pad.to(device)[:, :k]
+    assert torch.equal(gemm(a_s, b.to(device), b_layout=0), y)
+    c0 = torch.randn(m, n, generator=g).to(device)
+    for kw in ({"bias": bias.to(device)}, {"epilogue": "silu"}, {"accumulate": True}):
+        out_d, out_s = c0.clone(), c0.clone()
+        gemm(a.to(device), b.to(device), b_layout=0, out=out_d, **kw)
+        gemm(a_s, b.to(device), b_layout=0, out=out_s, **kw)
+        assert torch.equal(out_d, out_s), kw
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("F", [64, 128])
 def test_gemm_gather_against_fp64(device, F):
     """The fused gather-cat + edge GEMM (fmd_gemm_gather_f32) on a real neighbour list: parts
