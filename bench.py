@@ -197,7 +197,7 @@ def hbm_ops_bench(n_atoms: int = 40000, F: int = 128, gemm: bool = False) -> dic
     device = torch.device("cuda", 0)
     s = systems.perovskite_atoms(n_atoms)
     g = TensorGraphBuilder(cell=torch.tensor(s.cell), atomic_numbers=torch.tensor(s.numbers), atom_graph_cutoff=6.0,
-                           device=device, check_isolated_atoms=False).build(torch.tensor(s.positions, device=device))
+                           line_graph_cutoff=None, device=device, check_isolated_atoms=False).build(torch.tensor(s.positions, device=device))
     e = int(g.n_edges.item())
     gen = torch.Generator(device="cpu").manual_seed(0)
     v = torch.randn(e, F, generator=gen).to(device)
@@ -283,7 +283,8 @@ def scaling_sweep(steps: int, warmup: int) -> list:
         for slots, key in ((96, "ragged_build_96"), (8, "ragged_build_overflow_from_8")):
             def build(slots=slots):
                 b = TensorGraphBuilder(cell=torch.tensor(s.cell), atomic_numbers=torch.tensor(s.numbers),
-                                       atom_graph_cutoff=6.0, device="cuda", max_neighbors=slots)
+                                       atom_graph_cutoff=6.0, line_graph_cutoff=None, device="cuda",
+                                       max_neighbors=slots)
                 g = b.build(pos)
                 return b, g
             build()
@@ -572,7 +573,7 @@ def main() -> int:
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs the MD step on one MI355X; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is a design only, see DESIGN.md)", file=sys.stderr)
+              "(multi-GPU sharding is a design only in this build)", file=sys.stderr)
         return 2
     if args.steps % STEPS_PER_LAUNCH:
         print(f"--steps must be a multiple of {STEPS_PER_LAUNCH}", file=sys.stderr)

@@ -22,7 +22,7 @@ import sys
 import types
 
 ALIASES = {
-    # operators (SURVEY 8(b) operator API)
+    # operators
     "fastmd.ops.triton_gather_cat": "fastmd_amd.ops.gather_cat",
     "fastmd.models.matris.op.triton_gather_cat": "fastmd_amd.ops.gather_cat",
     "fastmd.ops.triton_csr_segment_sum": "fastmd_amd.ops.csr_segment_sum",
@@ -35,12 +35,13 @@ ALIASES = {
     "fastmd.models.matris.op.triton_wide_gemm": "fastmd_amd.ops.wide_gemm",
     "fastmd.ops.triton_threebody_fourier": "fastmd_amd.ops.threebody",
     "fastmd.models.matris.op.triton_threebody_fourier": "fastmd_amd.ops.threebody",
-    # builder, engine, integrator, runners, driver, outputs (SURVEY 8(b) builder / integrator API)
+    # builder, engine, dispatcher, integrator, runners, driver, outputs
     "fastmd.adapters.protocol": "fastmd_amd.adapters.protocol",
     "fastmd.graph.fixed_capacity_builder": "fastmd_amd.graph.fixed_capacity_builder",
     "fastmd.graph.gpu_graph_builder": "fastmd_amd.graph.gpu_graph_builder",
     "fastmd.graph.neighbor_list_backend": "fastmd_amd.graph.neighbor_list_backend",
     "fastmd.engine.energy_derivative": "fastmd_amd.engine.energy_derivative",
+    "fastmd.engine.dispatch": "fastmd_amd.engine.dispatch",
     "fastmd.engine.capacity_policy": "fastmd_amd.engine.capacity_policy",
     "fastmd.engine._graph_capture": "fastmd_amd.execution.graph_capture",
     "fastmd.execution.gpu_integrator": "fastmd_amd.execution.gpu_integrator",

@@ -226,7 +226,8 @@ class ReplicaBatchedMD:
         self.triplet_cutoff = None if topology.triplet_cutoff is None else float(topology.triplet_cutoff)
         # demand: R times one replica's ragged build
         single = TensorGraphBuilder(cell=self.cell, atomic_numbers=torch.tensor(numbers, dtype=torch.int32),
-                                    atom_graph_cutoff=self.cutoff, device=self.device, check_isolated_atoms=False)
+                                    atom_graph_cutoff=self.cutoff, line_graph_cutoff=None, device=self.device,
+                                    check_isolated_atoms=False)
         sample = single.build(torch.as_tensor(positions, dtype=torch.float64, device=self.device))
         u = self.replicas * (int(sample.edge_index.shape[0]) // 2)
         t = self.replicas * triplet_demand(sample, self.triplet_cutoff) if self.triplet_cutoff is not None else 0

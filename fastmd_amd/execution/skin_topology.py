@@ -29,6 +29,7 @@ import numpy as np
 import torch
 
 from fastmd_amd._roctx import roctx_range
+from fastmd_amd.adapters.protocol import PaddingRule
 from fastmd_amd.engine.capacity_policy import held_demand, tier
 from fastmd_amd.engine.energy_derivative import engine_derivative
 from fastmd_amd.execution.graph_capture import capture_graph
@@ -83,8 +84,9 @@ class SkinTopologyRunner:
         self._factors = (1.0, 1.0) if step is None else (float(step.u_thermal_factor), float(step.t_thermal_factor))
         self._builder_args = dict(cell=torch.tensor(self.cell, dtype=torch.float32), atomic_numbers=numbers,
                                   atom_graph_cutoff=self.cutoff, candidate_cutoff=self.cutoff + self.skin,
-                                  minimum_image=True, device=self.device,
-                                  padding=model.padding_rule() if hasattr(model, "padding_rule") else None)
+                                  minimum_image=True, device=self.device, t_capacity=0, line_graph_cutoff=None,
+                                  padding=(model.padding_rule() if hasattr(model, "padding_rule")
+                                           else PaddingRule("far_self_loops")))
         # the owner holds the candidate list and counts a refresh's exact edge demand (its own
         # capacity is irrelevant: the count covers every row)
         self.owner = FixedCapacityGraphBuilder(u_capacity=1, **self._builder_args)

@@ -423,7 +423,8 @@ class SystemBatchedMD:
         for positions, cell, numbers, _ in arrays:
             single = TensorGraphBuilder(cell=torch.tensor(cell, dtype=torch.float64),
                                         atomic_numbers=torch.tensor(numbers, dtype=torch.int32),
-                                        atom_graph_cutoff=self.cutoff, device=self.device, check_isolated_atoms=False)
+                                        atom_graph_cutoff=self.cutoff, line_graph_cutoff=None, device=self.device,
+                                        check_isolated_atoms=False)
             sample = single.build(torch.as_tensor(positions, dtype=torch.float64, device=self.device))
             u += int(sample.edge_index.shape[0]) // 2
             if self.triplet_cutoff is not None:

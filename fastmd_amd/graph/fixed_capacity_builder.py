@@ -30,6 +30,7 @@ from fastmd_amd.graph.neighbor_list_backend import (NeighborOverflowError, cell_
                                                     estimate_max_neighbors)
 
 _FAR_SELF_LOOPS = PaddingRule("far_self_loops")
+_SINK_PADDING = PaddingRule("sink_atoms")  # the reference's default (fixed_capacity_builder.py:937,1109)
 
 
 @dataclass
@@ -113,20 +114,22 @@ def morton_order(frac: Tensor, system_of: Tensor | None = None) -> Tensor:
 
 
 class FixedCapacityGraphBuilder:
-    """Single-system fixed-capacity builder (see the module docstring): edges only, or with the
-    three-body line graph when ``line_graph_cutoff`` and ``t_capacity`` are given (undirected
-    pairs, short-bond lists and triplet rows, fmd_nl_line_graph, published as
-    ``batch.pair_d2u`` / ``pair_u2d`` / ``triplets``).
+    """Single-system fixed-capacity builder (see the module docstring): with the three-body line
+    graph (undirected pairs, short-bond lists and triplet rows, fmd_nl_line_graph, published as
+    ``batch.pair_d2u`` / ``pair_u2d`` / ``triplets``), or edges only with
+    ``line_graph_cutoff=None`` and ``t_capacity=0``.
 
-    Padding (``padding``, protocol.py:68-119): far self-loops (the default here), exact-cutoff
-    loops (edges only: image 0 and ``batch.edge_vec_override``) or sink atoms (``n_dummy`` sink
-    rows after the real ones at the origin, atomic number 1; padded rows, and with a line graph
-    padded triplets, sit on them). Unsupported reference options (ghost rows, float64 published
+    The defaults are the reference's (fixed_capacity_builder.py:1047-1070,1109): ``t_capacity``
+    has none, ``line_graph_cutoff=4.5`` and ``padding=None`` means sink atoms. Padding
+    (``padding``, protocol.py:68-119): sink atoms (``n_dummy`` sink rows after the real ones at
+    the origin, atomic number 1; padded rows, and with a line graph padded triplets, sit on them),
+    far self-loops (what this build's HIP models take) or exact-cutoff loops (edges only: image 0
+    and ``batch.edge_vec_override``). Unsupported reference options (ghost rows, float64 published
     positions) raise ``NotImplementedError``. ``sorted_edges=False`` is accepted: the rows are
     always in the canonical order, which is also grouped by centre."""
 
-    def __init__(self, *, cell: Tensor, atomic_numbers: Tensor, u_capacity: int, t_capacity: int = 0,
-                 pbc: Tensor | None = None, atom_graph_cutoff: float = 6.0, line_graph_cutoff: float | None = None,
+    def __init__(self, *, cell: Tensor, atomic_numbers: Tensor, u_capacity: int, t_capacity: int,
+                 pbc: Tensor | None = None, atom_graph_cutoff: float = 6.0, line_graph_cutoff: float | None = 4.5,
                  n_dummy: int = 64, device: torch.device | str = "cuda", composition: str | None = None,
                  candidate_cutoff: float | None = None, ghosts=None, minimum_image: bool = False,
                  candidates_from=None, padding: PaddingRule | None = None,
@@ -142,7 +145,7 @@ class FixedCapacityGraphBuilder:
             raise NotImplementedError("ghost rows are not supported")
         if positions_dtype != torch.float32:
             raise NotImplementedError("float64 published positions are not supported")
-        padding = _FAR_SELF_LOOPS if padding is None else padding
+        padding = _SINK_PADDING if padding is None else padding
         if line_graph and padding.kind == "exact_rc_loops":
             raise ValueError("a builder with a line graph pads with sink atoms, or a single-system builder "
                              "with far self-loops (padded triplets need padded pairs)")

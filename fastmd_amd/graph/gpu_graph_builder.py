@@ -49,12 +49,15 @@ class TensorGraphBuilder:
     slot count (None: the volume estimate); the grown value is kept for later builds."""
 
     def __init__(self, *, cell: Tensor, atomic_numbers: Tensor, pbc: Tensor | None = None,
-                 atom_graph_cutoff: float = 6.0, line_graph_cutoff: float | None = None,
+                 atom_graph_cutoff: float = 6.0, line_graph_cutoff: float | None = 4.5,
                  device: torch.device | str = "cuda", composition: str | None = None,
                  check_isolated_atoms: bool = True, max_neighbors: int | None = None,
                  positions_dtype: torch.dtype = torch.float32) -> None:
         if line_graph_cutoff is not None:
-            raise NotImplementedError("line graphs are not built by this builder")
+            # the reference's default (gpu_graph_builder.py:953) asks for a 4.5 A ragged line graph
+            raise NotImplementedError(
+                f"TensorGraphBuilder builds the edges only: pass line_graph_cutoff=None (got {line_graph_cutoff}; "
+                "the reference's default is a 4.5 A line graph). FixedCapacityGraphBuilder builds line graphs")
         if positions_dtype != torch.float32:
             raise NotImplementedError("float64 published positions are not supported")
         self.device = torch.device(device)

@@ -134,8 +134,8 @@ class GPUResidentMolecularDynamics:
         # a three-body model reads the line graph of bonds shorter than this (None: edges only)
         self.triplet_cutoff = None if topology.triplet_cutoff is None else float(topology.triplet_cutoff)
         self.graph_builder = TensorGraphBuilder(cell=self.cell, atomic_numbers=self.numbers,
-                                                atom_graph_cutoff=self.cutoff, device=self.device,
-                                                check_isolated_atoms=False)
+                                                atom_graph_cutoff=self.cutoff, line_graph_cutoff=None,
+                                                device=self.device, check_isolated_atoms=False)
         self._eager_line = None  # the eager path's line-graph builder and its capacity
         self.model_runner = None  # model_graph: the bucketed model graphs
         self.steps = 0

@@ -1,7 +1,9 @@
 """(b) Fused gather + concatenate on the GPU (HIP kernel), with a deterministic VJP.
 
 * ``aligned_gather_cat3(aligned, gathered, index_a, index_b) = cat([aligned, gathered[index_a],
-  gathered[index_b]], 1)`` and ``aligned_gather_cat4`` keep the reference's signatures
+  gathered[index_b]], 1)`` and ``aligned_gather_cat4(aligned, gathered_a, index_a, gathered_b,
+  index_b, index_c) = cat([aligned, gathered_a[index_a], gathered_b[index_b],
+  gathered_b[index_c]], 1)`` keep the reference's signatures
   (fastmd/models/matris/op/triton_gather_cat.py:181-199, 353-374); widths may differ.
 * ``gather_cat(x, src, dst, rbf) = cat([x[src], x[dst], rbf], 1)``: the edge-row form of the
   MD step, ``[E, 2F + R]``.
@@ -132,11 +134,12 @@ def aligned_gather_cat3(aligned: Tensor, gathered: Tensor, index_a: Tensor, inde
     return _apply([(aligned, None), (gathered, index_a), (gathered, index_b)])
 
 
-def aligned_gather_cat4(aligned: Tensor, gathered: Tensor, index_a: Tensor, index_b: Tensor,
-                        index_c: Tensor) -> Tensor:
-    """``cat([aligned, gathered[index_a], gathered[index_b], gathered[index_c]], 1)``
-    (triton_gather_cat.py:353-374)."""
-    return _apply([(aligned, None), (gathered, index_a), (gathered, index_b), (gathered, index_c)])
+def aligned_gather_cat4(aligned: Tensor, gathered_a: Tensor, index_a: Tensor, gathered_b: Tensor,
+                        index_b: Tensor, index_c: Tensor) -> Tensor:
+    """``cat([aligned, gathered_a[index_a], gathered_b[index_b], gathered_b[index_c]], 1)``
+    (triton_gather_cat.py:353-374). The VJP of ``gathered_b`` sums both of its blocks in one
+    two-term CSR launch (and ``gathered_a`` joins them when it is the same tensor)."""
+    return _apply([(aligned, None), (gathered_a, index_a), (gathered_b, index_b), (gathered_b, index_c)])
 
 
 def gather_cat(x: Tensor, src: Tensor, dst: Tensor, rbf: Tensor, *, src_csr: Csr | None = None,

@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 
 from fastmd_amd.aliases import ALIASES, install_fastmd_aliases, uninstall_fastmd_aliases
+from fastmd_amd.adapters.protocol import PaddingRule
 
 REFERENCE_NAMES = {
     "fastmd.ops.triton_gather_cat": ("aligned_gather_cat3", "aligned_gather_cat4"),
@@ -121,7 +122,8 @@ def test_reference_paths_run_the_builder_and_integrator(device, aliases):
 
     s = systems.perovskite(3)
     builder = FixedCapacityGraphBuilder(cell=torch.tensor(s.cell), atomic_numbers=torch.tensor(s.numbers),
-                                        u_capacity=1088, atom_graph_cutoff=6.0, candidate_cutoff=8.0, device=device)
+                                        u_capacity=1088, t_capacity=0, line_graph_cutoff=None, atom_graph_cutoff=6.0,
+                                        candidate_cutoff=8.0, padding=PaddingRule("far_self_loops"), device=device)
     _, status = builder.build(torch.tensor(s.positions, device=device))
     assert not bool(status.overflow.item()) and int(status.edge_count.item()) == 2054
     from fastmd_amd import units

@@ -12,6 +12,7 @@ import torch
 from oracle import models as om
 from oracle import nl as onl
 from fastmd_amd import systems
+from fastmd_amd.adapters.protocol import PaddingRule
 
 F32 = np.float32
 
@@ -250,7 +251,8 @@ def _gpu_builder(s, u_cap, device):
     from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
 
     return FixedCapacityGraphBuilder(cell=torch.tensor(s.cell), atomic_numbers=torch.tensor(s.numbers),
-                                     u_capacity=u_cap, atom_graph_cutoff=6.0, candidate_cutoff=8.0, device=device)
+                                     u_capacity=u_cap, t_capacity=0, line_graph_cutoff=None, atom_graph_cutoff=6.0,
+                                     candidate_cutoff=8.0, padding=PaddingRule("far_self_loops"), device=device)
 
 
 @pytest.mark.gpu

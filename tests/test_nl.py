@@ -7,6 +7,7 @@ import pytest
 
 from oracle import nl as onl
 from fastmd_amd import systems
+from fastmd_amd.adapters.protocol import PaddingRule
 
 F32 = np.float32
 
@@ -235,8 +236,8 @@ def _gpu_builder(cell, n, cutoff, skin, u_cap, device):
     from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
 
     return FixedCapacityGraphBuilder(cell=torch.tensor(cell, dtype=torch.float32), atomic_numbers=torch.ones(n),
-                                     u_capacity=u_cap, atom_graph_cutoff=cutoff, candidate_cutoff=cutoff + skin,
-                                     device=device)
+                                     u_capacity=u_cap, t_capacity=0, line_graph_cutoff=None, atom_graph_cutoff=cutoff,
+                                     candidate_cutoff=cutoff + skin, padding=PaddingRule("far_self_loops"), device=device)
 
 
 def _assert_build_equal(builder, ob, cand=None):
@@ -335,9 +336,9 @@ def test_builder_minimum_image_bit_exact(device, n_atoms):
     print(f"[nl minimum image] n_atoms={n_atoms}", flush=True)
     s = systems.perovskite_atoms(n_atoms)
     builder = FixedCapacityGraphBuilder(cell=torch.tensor(s.cell, dtype=torch.float32),
-                                        atomic_numbers=torch.ones(n_atoms), u_capacity=9 * n_atoms + 64,
-                                        atom_graph_cutoff=6.0, candidate_cutoff=8.0, minimum_image=True,
-                                        device=device)
+                                        atomic_numbers=torch.ones(n_atoms), u_capacity=9 * n_atoms + 64, t_capacity=0,
+                                        line_graph_cutoff=None, atom_graph_cutoff=6.0, candidate_cutoff=8.0,
+                                        minimum_image=True, padding=PaddingRule("far_self_loops"), device=device)
     builder.build(torch.tensor(s.positions, dtype=torch.float64, device=device), rebuild_candidates=True)
     inv = builder.inv_cell.cpu().numpy()
     cell32 = s.cell.astype(F32)
@@ -367,7 +368,8 @@ def test_shared_candidates_follow_the_owner(device):
     s = systems.perovskite(6)
     n = s.n_atoms
     kw = dict(cell=torch.tensor(s.cell, dtype=torch.float32), atomic_numbers=torch.ones(n), atom_graph_cutoff=6.0,
-              candidate_cutoff=8.0, device=device)
+              candidate_cutoff=8.0, t_capacity=0, line_graph_cutoff=None, padding=PaddingRule("far_self_loops"),
+              device=device)
     owner = FixedCapacityGraphBuilder(u_capacity=9 * n, **kw)
     follower = FixedCapacityGraphBuilder(u_capacity=9 * n + 512, candidates_from=owner, **kw)
     assert follower.neighbor_matrix.data_ptr() == owner.neighbor_matrix.data_ptr()
@@ -408,7 +410,8 @@ def test_truncated_candidate_rows_are_deterministic(device, spacing):
     positions = (grid + 0.5) * spacing + rng.uniform(-0.02, 0.02, grid.shape)
     n = positions.shape[0]
     builder = FixedCapacityGraphBuilder(cell=torch.tensor(cell, dtype=torch.float32), atomic_numbers=torch.ones(n),
-                                        u_capacity=64, atom_graph_cutoff=6.0, candidate_cutoff=8.0, device=device)
+                                        u_capacity=64, t_capacity=0, line_graph_cutoff=None, atom_graph_cutoff=6.0,
+                                        candidate_cutoff=8.0, padding=PaddingRule("far_self_loops"), device=device)
     bmax = builder.buffer_max
     pos = torch.tensor(positions, dtype=torch.float64, device=device)
     rows = []
@@ -466,7 +469,7 @@ def test_ragged_builder_growth_is_bitwise_identical(device, max_neighbors):
 
     s = systems.perovskite(3)
     b = TensorGraphBuilder(cell=torch.tensor(s.cell), atomic_numbers=torch.tensor(s.numbers), atom_graph_cutoff=6.0,
-                           max_neighbors=max_neighbors, device=device)
+                           line_graph_cutoff=None, max_neighbors=max_neighbors, device=device)
     g = b.build(torch.tensor(s.positions, device=device))
     assert max_neighbors is None or b.max_neighbors >= 20
     cell32 = s.cell.astype(F32)
@@ -573,7 +576,8 @@ def _gpu_line_builder(cell, n, cutoff, skin, u_cap, t_cap, line_cutoff, device):
 
     return FixedCapacityGraphBuilder(cell=torch.tensor(cell, dtype=torch.float32), atomic_numbers=torch.ones(n),
                                      u_capacity=u_cap, t_capacity=t_cap, atom_graph_cutoff=cutoff,
-                                     line_graph_cutoff=line_cutoff, candidate_cutoff=cutoff + skin, device=device)
+                                     line_graph_cutoff=line_cutoff, candidate_cutoff=cutoff + skin,
+                                     padding=PaddingRule("far_self_loops"), device=device)
 
 
 def _assert_line_equal(builder, b, lg):

@@ -463,7 +463,7 @@ def test_gemm_gather_against_fp64(device, F):
     print(f"[gemm_gather] F={F}", flush=True)
     s = systems.perovskite(4)
     g = TensorGraphBuilder(cell=torch.tensor(s.cell), atomic_numbers=torch.tensor(s.numbers), atom_graph_cutoff=6.0,
-                           device=device).build(torch.tensor(s.positions, device=device))
+                           line_graph_cutoff=None, device=device).build(torch.tensor(s.positions, device=device))
     e = int(g.n_edges.item())
     ei = g.edge_index[:e]
     gen = torch.Generator().manual_seed(11)

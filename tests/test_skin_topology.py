@@ -54,7 +54,7 @@ def _fresh(adapter, s, positions, u_cap, device, t_cap=0):
     from fastmd_amd.engine.energy_derivative import engine_derivative
     from fastmd_amd.graph.fixed_capacity_builder import FixedCapacityGraphBuilder
 
-    line = {} if not t_cap else dict(line_graph_cutoff=adapter.topology_spec().triplet_cutoff, t_capacity=t_cap)
+    line = dict(line_graph_cutoff=None, t_capacity=0) if not t_cap else dict(line_graph_cutoff=adapter.topology_spec().triplet_cutoff, t_capacity=t_cap)
     b = FixedCapacityGraphBuilder(cell=torch.tensor(s.cell, dtype=torch.float32),
                                   atomic_numbers=torch.tensor(s.numbers), u_capacity=u_cap, atom_graph_cutoff=6.0,
                                   candidate_cutoff=8.0, minimum_image=True, device=device,

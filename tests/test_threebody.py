@@ -9,6 +9,7 @@ import pytest
 
 from oracle import threebody as otb
 from fastmd_amd import systems
+from fastmd_amd.adapters.protocol import PaddingRule
 
 REF_FREQS = np.array([0.833447, 1.5861181, 2.5042067], np.float32)  # the reference's self-check frequencies
 SCALE = math.sqrt(math.pi)  # FourierExpansion's scale (basis_function.py:120)
@@ -223,7 +224,7 @@ def _line(device, n_atoms, line_cutoff, t_cap=None, u_cap=None):
     builder = FixedCapacityGraphBuilder(cell=torch.tensor(s.cell, dtype=torch.float32),
                                         atomic_numbers=torch.ones(n_atoms), u_capacity=u_cap, t_capacity=t_cap,
                                         atom_graph_cutoff=6.0, line_graph_cutoff=line_cutoff, candidate_cutoff=8.0,
-                                        device=device)
+                                        padding=PaddingRule("far_self_loops"), device=device)
     builder.build(torch.tensor(s.positions, dtype=torch.float64, device=device))
     return builder
 

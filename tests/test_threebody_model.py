@@ -11,6 +11,7 @@ import torch
 from oracle import models as om
 from oracle import nl as onl
 from fastmd_amd import systems
+from fastmd_amd.adapters.protocol import PaddingRule
 
 F32 = np.float32
 
@@ -130,7 +131,7 @@ def _builder(s, bond_cutoff, device, u_cap=None, t_cap=None):
     return FixedCapacityGraphBuilder(cell=torch.tensor(s.cell), atomic_numbers=torch.tensor(s.numbers),
                                      u_capacity=u_cap or int(n * 18 / 2) + 100, t_capacity=t_cap or 40 * n,
                                      atom_graph_cutoff=6.0, line_graph_cutoff=bond_cutoff, candidate_cutoff=8.0,
-                                     device=device)
+                                     padding=PaddingRule("far_self_loops"), device=device)
 
 
 @pytest.mark.gpu

@@ -29,7 +29,7 @@ def test_capacity_tiers_known_answers():
     assert whole_step_headroom(77000, 32) == 576 and whole_step_headroom(1027, 32) == 0
     p = JointCapacityPolicy(u_step=32, min_pad_u=32)
     k = p.start(held_demand(1027, 0, 1.02))
-    assert k.u_capacity == 1088  # 135-atom perovskite, MACE capacity step (1 088)
+    assert k.u_capacity == 1088  # 135-atom perovskite (1 027 undirected edges), MACE capacity step
     assert p.grow(k, 900).u_capacity == 1088 and p.grow(k, 1100).u_capacity > 1088
     # joint tiers: pairs and triplets each take their own tier, growth keeps the larger of each
     j = JointCapacityPolicy(u_step=128, min_pad_u=128, t_step=128, min_pad_t=128)

@@ -7,6 +7,7 @@ import numpy as np
 import pytest
 
 from fastmd_amd import systems
+from fastmd_amd.adapters.protocol import PaddingRule
 
 # the builder's output buffers of one build (persistent tensors the C ABI writes)
 OUTPUTS = ("frac_coords", "wrap_delta", "positions", "edge_counts", "edge_offsets", "center", "neighbor", "images",
@@ -53,8 +54,9 @@ def test_noalloc_build_equals_the_build_with_a_work_buffer(device):
         n = s.n_atoms
         print(f"[noalloc] {n} atoms", flush=True)
         builder = FixedCapacityGraphBuilder(cell=torch.tensor(s.cell, dtype=torch.float32),
-                                            atomic_numbers=torch.ones(n), u_capacity=9 * n + 64,
-                                            atom_graph_cutoff=6.0, candidate_cutoff=8.0, device=device)
+                                            atomic_numbers=torch.ones(n), u_capacity=9 * n + 64, t_capacity=0,
+                                            line_graph_cutoff=None, atom_graph_cutoff=6.0, candidate_cutoff=8.0,
+                                            padding=PaddingRule("far_self_loops"), device=device)
         pos = torch.tensor(s.positions, dtype=torch.float64, device=device)
         builder.build(pos, rebuild_candidates=True)
         # a step later: atoms moved (wraps change near the cell faces), the candidates reused
