@@ -24,6 +24,9 @@ if ROOT not in sys.path:
 
 METRIC = "MD ms/step & atom-steps/s (whole_step) at 135/10k atoms; segment_sum HBM GB/s"
 HBM_PEAK_GBPS = 8000.0
+# VALU issue peak: 256 CUs x 4 SIMDs x 2.4 GHz, one wave64 VALU instruction per 4 cycles per SIMD
+# (16 lanes wide; full-rate 32-bit operations)
+VALU_ISSUE_PEAK_GINSTS = 256 * 4 * 2.4 / 4
 FP32_MFMA_PEAK_TFLOPS = 157.3
 BF16_MFMA_PEAK_TFLOPS = 2500.0
 SPLIT_PRODUCTS = 6  # fp32-accurate GEMM: three bf16 planes per operand, six MFMA products
@@ -58,12 +61,16 @@ def build_md(n_atoms: int, steps_per_launch: int, bond_cutoff: float | None = No
                                         steps_per_launch=steps_per_launch, **outputs)
 
 
-def time_md(md, steps: int, warmup_steps: int) -> float:
-    """Seconds for exactly ``steps`` MD steps after ``warmup_steps`` untimed ones (rounded up to
-    whole windows), synchronized on both sides (one process, one GPU: no barrier to take)."""
+def time_md(md, steps: int, warmup_steps: int, thermalise: int = 0) -> float:
+    """Seconds for exactly ``steps`` MD steps after ``thermalise`` untimed equilibration steps (the
+    random-init potential keeps adding edges for about 2 000 steps from the jittered lattice, each
+    growth a recapture) and then ``warmup_steps`` untimed ones (each rounded up to whole windows),
+    synchronized on both sides (one process, one GPU: no barrier to take)."""
     import torch
 
     spl = md.steps_per_launch
+    if thermalise > 0:
+        md.run(-(-thermalise // spl) * spl)
     md.run(-(-warmup_steps // spl) * spl)
     before = md.whole_step_stats()
     torch.cuda.synchronize()
@@ -102,7 +109,7 @@ def message_roofline(md) -> dict:
     gradients; per atom the centre's Q, gA0, gA1 read and the sum of g_z written). It is timed
     in the context of the step: HIP events on torch's current stream (the stream it is launched
     on) around that launch alone in eager force evaluations at the run's final state (its edge
-    list and features), the model's own timing hook. Ten times, a spin kernel is queued and then
+    list and features), the launch split out of the model's combined VJP call here. Ten times, a spin kernel is queued and then
     two evaluations behind it, so that no host latency falls inside the event pairs; the second
     evaluation of each pair is timed (its launch follows the same kernels as in the captured
     step, with their data in L2), the first is reported as ``first_launch_us``.
@@ -112,7 +119,12 @@ def message_roofline(md) -> dict:
     rows (P: NZ C, h0: C, h1: 3 C) + 16 B geometry-gradient store + 4 nb B basis-gradient store;
     per atom 20 B offsets and order + 4 (NZ + 4) C B read (Q, gA0, gA1) + 4 NZ C B stored
     (the per-centre sum of g_z), NZ = 4 (the last layer has vector features). The
-    ``unique_bytes`` alternative counts every input row once (a perfect cache)."""
+    ``unique_bytes`` alternative counts every input row once (a perfect cache).
+    The kernel is bound by instruction issue, not by HBM: ``bound`` "valu", ``achieved`` its VALU
+    wave-instructions per second (the committed SQ_INSTS_VALU count per launch over the live
+    launch time) against the issue peak of one wave64 VALU instruction per 4 cycles per SIMD;
+    ``hbm_frac`` is its measured HBM traffic (FETCH_SIZE + WRITE_SIZE) over the launch time and
+    ``gather_bytes_frac`` the gather-cat byte count's rate, both as fractions of 8 TB/s."""
     import torch
 
     from fastmd_amd.models import mace_like
@@ -120,7 +132,30 @@ def message_roofline(md) -> dict:
     runner = md.whole_step_runner
     torch.cuda.synchronize()
     time.sleep(0.03)  # an idle gap that separates the timed steps from these launches in a kernel trace
-    mace_like.MESSAGE_EVENTS = events = []
+    events = []
+    launch = mace_like._call
+
+    def timed_call(name, *args):
+        # The model's VJP launches both message VJP kernels in one fmd_mace_message_bwd_f32 call
+        # (arguments as in include/fastmd_hip.h: 18 gzsum_src, 21 gh0, 22 gh1, 23 accumulate_h).
+        # The call that carries gzsum_src (the last layer's) is split here into the edge-side
+        # kernel alone between HIP events (no gzsum_src, gh0, gh1) and then the sender-side kernel
+        # alone (accumulate_h bit 2): the same kernels and results as the single call.
+        if name != "fmd_mace_message_bwd_f32" or args[18] is None or torch.cuda.is_current_stream_capturing():
+            return launch(name, *args)
+        edge = list(args)
+        edge[18] = edge[21] = edge[22] = None
+        edge[23] = 0
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        ev[0].record()
+        launch(name, *edge)
+        ev[1].record()
+        events.append((ev[0], ev[1], (args[7], args[8], args[10])))
+        src = list(args)
+        src[23] = args[23] | 4
+        return launch(name, *src)
+
+    mace_like._call = timed_call
     try:
         for _ in range(10):
             # a spin kernel ahead of each pair of evaluations keeps the GPU busy while the host
@@ -130,7 +165,7 @@ def message_roofline(md) -> dict:
             runner._evaluate(md.integrator.positions)
         torch.cuda.synchronize()
     finally:
-        mace_like.MESSAGE_EVENTS = None
+        mace_like._call = launch
     e_cap, n, C = events[-1][2]
     if len(events) != 20 or any(shape != (e_cap, n, C) for _, _, shape in events):
         raise RuntimeError("the roofline evaluations ran on different edge capacities")
@@ -143,33 +178,51 @@ def message_roofline(md) -> dict:
     nb, nz = md.adapter.module.config.n_basis, 4
     per_row = 4 + 20 + 4 * nb + 4 * (nz + 4) * C + 16 + 4 * nb
     per_atom = 20 + 4 * (nz + 4) * C + 4 * nz * C
-    algorithmic = rows * per_row + n * per_atom
+    gathered = rows * per_row + n * per_atom
     unique = rows * (4 + 20 + 4 * nb + 16 + 4 * nb) + n * (20 + 4 * (nz + 4) * C + 4 * nz * C + 4 * (nz + 4) * C)
-    achieved = algorithmic / t / 1e9
-    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": _traffic(ROOFLINE_KERNEL, [rows, n, C]),
-            "kernel": ROOFLINE_KERNEL, "launch_us": round(t * 1e6, 2), "launches_timed": len(durations),
-            "first_launch_us": round(sum(first) / len(first) * 1e6, 2),
-            "rows": rows, "atoms": n, "bytes_per_launch": algorithmic,
-            "bytes_basis": f"per real edge row {per_row} B (gathered sender rows counted per row), per atom "
-                           f"{per_atom} B",
-            "unique_bytes_per_launch": unique, "unique_frac": round(unique / t / 1e9 / HBM_PEAK_GBPS, 4)}
+    counters = _counters(ROOFLINE_KERNEL, [rows, n, C])
+    traffic = counters.get("bytes_per_launch")
+    insts = counters.get("valu_insts_per_launch")
+    out = {"kernel": ROOFLINE_KERNEL, "launch_us": round(t * 1e6, 2), "launches_timed": len(durations),
+           "first_launch_us": round(sum(first) / len(first) * 1e6, 2), "rows": rows, "atoms": n,
+           "traffic": traffic,
+           "hbm_frac": None if traffic is None else round(traffic / t / 1e9 / HBM_PEAK_GBPS, 4),
+           "gather_bytes_per_launch": gathered,
+           "gather_bytes_frac": round(gathered / t / 1e9 / HBM_PEAK_GBPS, 4),
+           "gather_bytes_basis": f"per real edge row {per_row} B (gathered sender rows counted per row), per atom "
+                                 f"{per_atom} B",
+           "unique_bytes_per_launch": unique, "unique_frac": round(unique / t / 1e9 / HBM_PEAK_GBPS, 4)}
+    if insts is not None:
+        # the kernel is bound by instruction issue (its HBM traffic is a small fraction of the peak)
+        achieved = insts / t / 1e9
+        out.update(bound="valu", achieved=round(achieved, 1), peak=VALU_ISSUE_PEAK_GINSTS, unit="Ginst/s",
+                   frac=round(achieved / VALU_ISSUE_PEAK_GINSTS, 4), valu_insts_per_launch=insts,
+                   mfma_insts_per_launch=counters.get("mfma_insts_per_launch"))
+    else:
+        achieved = unique / t / 1e9
+        out.update(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBPS, unit="GB/s",
+                   frac=round(achieved / HBM_PEAK_GBPS, 4))
+    return out
 
 
-def _traffic(kernel: str, shape: list):
-    """HBM bytes per launch of ``kernel`` at ``shape`` from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration), or None if none matches."""
+def _counters(kernel: str, shape: list) -> dict:
+    """Per-launch counter figures of ``kernel`` at ``shape`` from the committed rocprofv3 --pmc
+    summary (profiles/traffic.json): HBM bytes (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel
+    calibration) and, where measured, VALU and MFMA instructions (SQ_INSTS_VALU, SQ_INSTS_MFMA),
+    each scaled from the measured shape to this launch's rows; {} if no entry matches."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
     try:
         with open(path) as f:
             table = json.load(f)
     except (OSError, ValueError):
-        return None
+        return {}
     row = table.get(kernel)
     if not row or row.get("shape", [None])[1:] != shape[1:]:
-        return None
-    # the measured shape's HBM bytes, scaled to this launch's M (the A read and C write are per row)
-    return int(row["bytes_per_launch"] * shape[0] / row["shape"][0])
+        return {}
+    scale = shape[0] / row["shape"][0]  # the per-row work scales with the rows of the launch
+    return {key: int(row[src] * scale) for key, src in (("bytes_per_launch", "bytes_per_launch"),
+                                                        ("valu_insts_per_launch", "valu_insts"),
+                                                        ("mfma_insts_per_launch", "mfma_insts")) if src in row}
 
 
 def hbm_ops_bench(n_atoms: int = 40000, F: int = 128, gemm: bool = False) -> dict:
@@ -545,6 +598,9 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=1000)
     parser.add_argument("--warmup", type=int, default=1000,
                         help="untimed MD steps before timing (thermalisation: the edge count settles)")
+    parser.add_argument("--thermalise", type=int, default=2000,
+                        help="untimed equilibration steps before the warm-up (the random-init potential "
+                             "keeps adding edges for ~2 000 steps from the jittered lattice)")
     parser.add_argument("--steps-small", type=int, default=2000)
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -624,7 +680,8 @@ def main() -> int:
     log("10 000 atoms: capture")
     md = build_md(10000, STEPS_PER_LAUNCH)
     log("10 000 atoms: timing")
-    t_big = time_md(md, args.steps, args.warmup)
+    thermalise = 200 if args.quick else args.thermalise
+    t_big = time_md(md, args.steps, args.warmup, thermalise)
     ms_big = t_big / args.steps * 1e3
     stats_big = md.whole_step_stats()
     events_big = md.timed_events
@@ -635,7 +692,7 @@ def main() -> int:
 
     log("135 atoms: capture")
     md = build_md(135, STEPS_PER_LAUNCH)
-    t_small = time_md(md, steps_small, args.warmup)
+    t_small = time_md(md, steps_small, args.warmup, thermalise)
     ms_small = t_small / steps_small * 1e3
     stats_small = md.whole_step_stats()
     events_small = md.timed_events
@@ -657,8 +714,11 @@ def main() -> int:
     log("model_graph mode")
     model_graph = model_graph_bench(50 if args.quick else 200, 50 if args.quick else 200)
 
-    log("memory-bound operator microbenchmarks")
-    seg = hbm_ops_bench()
+    log("memory-bound operator microbenchmarks and the edge GEMM")
+    seg = hbm_ops_bench(gemm=True)
+    gemm_40k = {"atoms": seg["atoms"], "edges": seg["edges"], "F": seg["F"],
+                "shape": [seg["edges"], 2 * seg["F"] + 8, 4 * seg["F"]],
+                **{k: seg.pop(k) for k in ("edge_gemm_f32", "gather_cat_edge_gemm_f32_fused", "edge_gemm_bf16")}}
     log("NHC halves alone")
     nhc = nhc_bench()
     cpu = None
@@ -686,7 +746,8 @@ def main() -> int:
                    "atoms": 10000, "steps_per_launch": STEPS_PER_LAUNCH,
                    "e_capacity": stats_big["e_capacity"],
                    "max_edges": stats_big["max_edge_count"],
-                   "thermalised": f"{args.warmup} untimed steps before the timed ones"},
+                   "thermalised": f"{thermalise} untimed equilibration steps, then {args.warmup} untimed "
+                                  "warm-up steps, before the timed ones"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "md_steps_per_s": round(1e3 / ms_big, 2),
@@ -699,6 +760,7 @@ def main() -> int:
         "replicas_135": replicas,
         "segment_sum_GBps": seg["segment_sum"]["GBps"],
         "hbm_ops_40k": seg,
+        "gemm_40k": gemm_40k,
         "nhc": nhc,
         "whole_step_stats_10k": {**{k: stats_big[k] for k in ("candidate_refreshes", "fallback_windows",
                                                               "max_edge_count", "capacity_history")},

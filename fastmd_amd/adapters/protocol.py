@@ -137,6 +137,9 @@ class GraphBatch:
     # rows of the largest system in the batch (replica or slot union; 0: all rows one system):
     # kernels whose arithmetic is chosen by system size choose it by this
     max_system_rows: int = 0
+    # slot unions: (first row, rows, atoms) of every slot, host ints; kernels whose arithmetic is
+    # chosen by system size choose it per slot from its atoms (empty: one system or equal replicas)
+    system_slots: tuple = ()
 
     @property
     def edge_dst(self) -> Tensor:

@@ -590,10 +590,12 @@ __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs
 __global__ void __launch_bounds__(kBlock) nl_count_kernel(BuildArgs a) {
   __shared__ float s_red[kBlock / FMD_WAVE];
   __shared__ int32_t s_iso[kBlock / FMD_WAVE];
+  __shared__ int32_t s_cnt[kBlock / FMD_WAVE];
   const int lane = threadIdx.x & (FMD_WAVE - 1), wave = threadIdx.x / FMD_WAVE;
   const int64_t i = (int64_t)blockIdx.x * (kBlock / FMD_WAVE) + wave;
   float dmax = 0.f;
   int iso = 0;
+  int ecount = 0;  // the atom's edge count (uniform over the wave)
   if (i < a.n) {
     Mat3 inv, cm;
     atom_frame(a, i, inv, cm);  // atom i's system's; its neighbours are of the same system
@@ -633,10 +635,12 @@ __global__ void __launch_bounds__(kBlock) nl_count_kernel(BuildArgs a) {
     }
     if (lane == 0) a.edge_counts[i] = total;
     iso = (total == 0);
+    ecount = total;
   }
   if (lane == 0) {
     s_red[wave] = dmax;
     s_iso[wave] = iso;
+    s_cnt[wave] = ecount;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -650,34 +654,63 @@ __global__ void __launch_bounds__(kBlock) nl_count_kernel(BuildArgs a) {
     float* red = reinterpret_cast<float*>(a.work);
     red[blockIdx.x] = m;
     reinterpret_cast<int32_t*>(a.work + fmd_cdiv(nb, 2))[blockIdx.x] = isol;
+    // the block's edge count, for the scan's prefixes
+    int32_t sum = 0;
+    for (int k = 0; k < kBlock / FMD_WAVE; ++k) sum += s_cnt[k];
+    reinterpret_cast<int32_t*>(a.work + 2 * fmd_cdiv(nb, 2))[blockIdx.x] = sum;
   }
 }
 
-// Kernel 2 (one workgroup): exclusive scan of the counts, the flags and the reductions.
-// The counts are scanned in tiles of kScanTile staged through LDS (coalesced loads, all in
-// flight together; each thread then scans kScanPer consecutive counts), with a carry between
-// tiles: a thread's own serial chunk of global loads would wait out one memory round trip per
-// atom.
-constexpr int kScanPer = 8, kScanTile = 1024 * kScanPer;
+// Kernel 2: exclusive scan of the counts, the flags and the reductions, over several
+// workgroups with no waits between them. Workgroup b scans the counts of atoms
+// [b kScanTile, (b + 1) kScanTile): each thread loads kScanPer consecutive counts and the
+// workgroup's offset is the sum of the count kernel's per-block edge counts before its range
+// (blocks of kAtomsPerCountBlock atoms; kScanTile is a multiple of it), read by every thread
+// strided and added in a fixed order. All of a thread's loads are issued before any use (one
+// memory round trip). The last workgroup also reduces the count kernel's partials (maximum
+// displacement, isolated atoms) and writes the total, the flags and edge_offsets[n]. Integer
+// sums are exact, so the offsets are the same in any grouping.
+constexpr int kScanThreads = 256, kScanPer = 8, kScanTile = kScanThreads * kScanPer;
+constexpr int kAtomsPerCountBlock = kBlock / FMD_WAVE;
+static_assert(kScanTile % kAtomsPerCountBlock == 0, "scan tiles cover whole count blocks");
 
-__global__ void __launch_bounds__(1024) nl_scan_kernel(BuildArgs a, int64_t nblocks) {
-  __shared__ float s_max[1024 / FMD_WAVE];
-  __shared__ int32_t s_iso[1024 / FMD_WAVE];
-  __shared__ int64_t s_cnt[kScanTile];
+__global__ void __launch_bounds__(kScanThreads) nl_scan_kernel(BuildArgs a, int64_t nblocks) {
+  __shared__ int64_t s_wtot[17];
+  __shared__ int64_t s_pre[kScanThreads / FMD_WAVE];
+  __shared__ float s_max[kScanThreads / FMD_WAVE];
+  __shared__ int32_t s_iso[kScanThreads / FMD_WAVE];
   const int t = threadIdx.x, T = blockDim.x;
   const int lane = t & (FMD_WAVE - 1), wave = t / FMD_WAVE;
   const int64_t n = a.n;
-  // block partials of kernel 1 (max displacement, isolated atoms): strided per thread, then
-  // over the wave and over the waves, in a fixed order
-  {
+  const int64_t base = (int64_t)blockIdx.x * kScanTile;
+  const int64_t cnt = n - base < kScanTile ? n - base : kScanTile;
+  const bool last = blockIdx.x == gridDim.x - 1;
+  // this thread's counts (consecutive atoms)
+  int64_t c[kScanPer];
+#pragma unroll
+  for (int j = 0; j < kScanPer; ++j) {
+    const int64_t k = (int64_t)t * kScanPer + j;
+    c[j] = k < cnt ? a.edge_counts[base + k] : 0;
+  }
+  // the edge count of every atom before this tile: the count blocks [0, base / kAtomsPerCountBlock)
+  const int32_t* bsum = reinterpret_cast<const int32_t*>(a.work + 2 * fmd_cdiv(nblocks, 2));
+  const int64_t nbefore = base / kAtomsPerCountBlock;
+  int64_t pre = 0;
+  for (int64_t b = t; b < nbefore; b += T) pre += bsum[b];
+  // the last workgroup: the count kernel's partials over all its blocks
+  float m = 0.f;
+  int32_t iso = 0;
+  if (last) {
     const float* red = reinterpret_cast<const float*>(a.work);
     const int32_t* isop = reinterpret_cast<const int32_t*>(a.work + fmd_cdiv(nblocks, 2));
-    float m = 0.f;
-    int32_t iso = 0;
     for (int64_t b = t; b < nblocks; b += T) {
       m = nan_max(m, red[b]);
       iso += isop[b];
     }
+  }
+  pre = wave_sum(pre);
+  if (lane == 0) s_pre[wave] = pre;
+  if (last) {
     m = wave_nan_max(m);
     iso = wave_sum(iso);
     if (lane == 0) {
@@ -685,42 +718,30 @@ __global__ void __launch_bounds__(1024) nl_scan_kernel(BuildArgs a, int64_t nblo
       s_iso[wave] = iso;
     }
   }
-  __syncthreads();
-  __shared__ int64_t s_wtot[17];
-  int64_t carry = 0;
-  for (int64_t base = 0; base < n; base += kScanTile) {
-    const int64_t cnt = n - base < kScanTile ? n - base : kScanTile;
+  int64_t s = 0;
 #pragma unroll
-    for (int j = 0; j < kScanPer; ++j) {
-      const int64_t k = (int64_t)j * T + t;
-      s_cnt[k] = k < cnt ? a.edge_counts[base + k] : 0;
-    }
-    __syncthreads();
-    int64_t s = 0;
+  for (int j = 0; j < kScanPer; ++j) s += c[j];
+  int64_t tile_total = 0;
+  const int64_t mine = block_exclusive_scan<int64_t>(s, s_wtot, &tile_total);  // synchronizes
+  int64_t prefix = 0;
+  for (int w = 0; w < T / FMD_WAVE; ++w) prefix += s_pre[w];
+  int64_t run = prefix + mine;
 #pragma unroll
-    for (int j = 0; j < kScanPer; ++j) s += s_cnt[t * kScanPer + j];
-    int64_t tile_total = 0;
-    const int64_t mine = block_exclusive_scan<int64_t>(s, s_wtot, &tile_total);
-    int64_t run = carry + mine;
-#pragma unroll
-    for (int j = 0; j < kScanPer; ++j) {
-      const int64_t k = (int64_t)t * kScanPer + j;
-      if (k < cnt) a.edge_offsets[base + k] = run;
-      run += s_cnt[k];
-    }
-    carry += tile_total;
-    __syncthreads();  // s_cnt and s_wtot are reused by the next tile
+  for (int j = 0; j < kScanPer; ++j) {
+    const int64_t k = (int64_t)t * kScanPer + j;
+    if (k < cnt) a.edge_offsets[base + k] = run;
+    run += c[j];
   }
-  const int64_t total = carry;
-  if (t == 0) {
-    float m = s_max[0];
+  if (last && t == 0) {
+    const int64_t total = prefix + tile_total;
+    float mm = s_max[0];
     int32_t isol = s_iso[0];
     for (int w = 1; w < T / FMD_WAVE; ++w) {
-      m = nan_max(m, s_max[w]);
+      mm = nan_max(mm, s_max[w]);
       isol += s_iso[w];
     }
-    const bool valid = (m * 2.0f <= a.skin_limit) && (a.capacity_valid[0] != 0);
-    a.max_disp[0] = m;
+    const bool valid = (mm * 2.0f <= a.skin_limit) && (a.capacity_valid[0] != 0);
+    a.max_disp[0] = mm;
     a.cand_valid[0] = valid ? 1 : 0;
     a.overflow[0] = (total > a.e_cap || !valid) ? 1 : 0;
     a.isolated[0] = isol;
@@ -868,7 +889,8 @@ int launch_build(const BuildArgs& a, hipStream_t stream) {
   const int64_t atom_blocks = fmd_cdiv(a.n, kBlock / FMD_WAVE);
   hipLaunchKernelGGL(nl_count_kernel, dim3((unsigned)atom_blocks), dim3(kBlock), 0, stream, a);
   FMD_CHECK_LAUNCH();
-  hipLaunchKernelGGL(nl_scan_kernel, dim3(1), dim3(1024), 0, stream, a, atom_blocks);
+  hipLaunchKernelGGL(nl_scan_kernel, dim3((unsigned)fmd_cdiv(a.n, kScanTile)), dim3(kScanThreads), 0, stream, a,
+                     atom_blocks);
   FMD_CHECK_LAUNCH();
   int64_t pad_blocks = fmd_cdiv(a.e_cap, (int64_t)kBlock * 4);
   pad_blocks = pad_blocks < 1 ? 1 : (pad_blocks > 1024 ? 1024 : pad_blocks);
@@ -963,7 +985,7 @@ int fmd_nl_candidates(const float* wrapped, const float* frac, const float* cell
 
 int64_t fmd_nl_build_work_size(int64_t n_atoms) {
   const int64_t nb = fmd_cdiv(n_atoms > 0 ? n_atoms : 1, kBlock / FMD_WAVE);
-  return 2 * fmd_cdiv(nb, 2) + 2;
+  return 3 * fmd_cdiv(nb, 2) + 2;  // per count block: maximum displacement, isolated atoms, edge count
 }
 
 int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cell, const float* cell, int64_t n_atoms,

@@ -7,7 +7,10 @@ fixed-capacity build over the R·N atoms whose candidate search takes no pair ac
 (``system_size``), so each replica's rows are its own edge list, in the canonical order, with
 the union's atom indices; the model sees one batch, the engine derivative sums one energy per
 replica (``EnergyDerivative.segments``), and each replica's NHC chain integrates its own rows.
-A replica's trajectory is therefore bitwise the single-system run with its momenta (tested).
+A replica's trajectory is therefore bitwise the single-system run with its momenta (tested)
+while the union's node GEMMs take the form the single system's take (fp32 tiles below a
+launch-size threshold, about 4 000 rows for the MACE-like model; above it the split-plane form,
+and the replicas match their single runs to float32 rounding).
 """
 from __future__ import annotations
 

@@ -24,8 +24,14 @@ The single-system whole-step runner runs the union unchanged; these parts make i
   over its occupied rows.
 * ``SystemBatchedMD``: the driver (capacity growth, replays, per-system observables).
 
-Every system's trajectory is bitwise its single-system run (tested for Morse, the MACE-like and the
-three-body model).
+A system's trajectory is bitwise its single-system run whenever every launch over the union takes
+the form the single run takes (tested for Morse, the MACE-like and the three-body model on unions of
+a few hundred rows). Launches whose form follows the system size follow each system's own atom
+count (the message kernels' waves per atom, per slot); the node GEMMs take their form from the
+launch's row count (fp32 tiles below a size threshold, the split-plane form above it, about 4 000
+rows for the MACE-like model), so in a union that crosses the threshold a small system's node
+products round differently and its trajectory matches its single run to float32 rounding instead
+(tested: a 135-atom system beside the 5 000-atom perovskite, which itself stays bitwise).
 """
 from __future__ import annotations
 
@@ -123,6 +129,7 @@ class SlotUnionGraphBuilder(FixedCapacityGraphBuilder):
         self.batch.systems = SystemSegments(count=layout.count, row_ptr=self._row_ptr,
                                             system_of_row=self._system_of, cells=self._sys_cells, atoms=self._atoms)
         self.batch.max_system_rows = max(layout.ceilings)
+        self.batch.system_slots = tuple(zip(layout.starts, layout.ceilings, atoms))
         self.graph = self.batch if prepare is None else prepare(self.batch)
 
     def _set_cell(self, slot: int, cell32: np.ndarray) -> None:

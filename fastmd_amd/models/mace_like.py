@@ -68,17 +68,10 @@ FACTORED_Z = True
 # never formed), and the first layer's per-element rows come from one gather launch. Off: one
 # launch per product, as the unmerged chain (kept tested against the oracle).
 MERGED_NODE = True
-# Systems of at most this many atoms (the largest system of a replica or slot union) split each
+# Systems of at most this many atoms (each system of a slot union by its own count) split each
 # atom's rows over four waves in the message kernels (one wave per atom leaves a small system's
 # chip idle while each wave walks its rows); the per-atom sums are then added over the waves.
 SPLIT_ROWS_MAX_ATOMS = 2048
-# Timing hook of the edge GEMM launches: when a list, each eager (uncaptured) forward appends
-# (start event, end event, (M, K, N)) recorded around its edge GEMMs on the current stream. The
-# benchmark uses it to time the dominant kernel in the context of the step; None in normal runs.
-EDGE_GEMM_EVENTS: list | None = None
-# Timing hook of the last layer's edge-side message VJP (the step's longest launch): when a list,
-# each eager VJP appends (start event, end event, (e_cap, n, C)) recorded around that launch alone.
-MESSAGE_EVENTS: list | None = None
 
 
 @dataclass(frozen=True)
@@ -356,11 +349,42 @@ def _atom_order(batch, n: int) -> int | None:
     return None if order is None or order.numel() != n else order.data_ptr()
 
 
-def _waves_per_atom(batch, n: int) -> int:
-    """Waves per atom of the message kernels: by the largest system of the batch, so that a
-    system batched with others sums its rows as it does alone."""
-    size = getattr(batch, "max_system_rows", 0) or n
-    return 4 if size <= SPLIT_ROWS_MAX_ATOMS else 1
+def _wave_groups(batch, n: int) -> list:
+    """The message kernels' launches as ``(order address, atoms, waves per atom)``: the waves per
+    atom of a system are chosen by its own atom count, so that a system batched with others sums
+    its rows as it does alone. One launch for one system or equal replicas; for a slot union one
+    per run of consecutive slots with the same choice, over the slots' range of the spatial order
+    (sorted by system first: slot s holds entries [first row, first row + rows) of it)."""
+    order = _atom_order(batch, n)
+    slots = getattr(batch, "system_slots", ())
+    if not slots:
+        size = getattr(batch, "max_system_rows", 0) or n
+        return [(order, n, 4 if size <= SPLIT_ROWS_MAX_ATOMS else 1)]
+    if order is None:
+        raise ValueError("a slot union needs the builder's atom order")
+    groups: list = []
+    end = 0
+    for start, rows, atoms in slots:
+        wpa = 4 if atoms <= SPLIT_ROWS_MAX_ATOMS else 1
+        if start != end:
+            raise ValueError("slot union rows must be consecutive")
+        if groups and groups[-1][2] == wpa:
+            groups[-1][1] += rows
+        else:
+            groups.append([order + 4 * start, rows, wpa])
+        end = start + rows
+    if end != n:
+        raise ValueError(f"the slots cover {end} rows of {n}")
+    return [tuple(g) for g in groups]
+
+
+def _call_groups(name: str, groups: list, n_at: int, *args) -> None:
+    """One ``name`` call per wave group: ``args`` with the atom count at ``n_at``, the order right
+    after it and the waves per atom last (placeholders, replaced per group)."""
+    for order, count, wpa in groups:
+        a = list(args)
+        a[n_at], a[n_at + 1], a[-1] = count, order, wpa
+        _call(name, *a)
 
 
 def _gather_edge_rows(h0: Tensor, ef: Tensor, edge_index: Tensor, out: Tensor) -> None:
@@ -410,8 +434,7 @@ class _MaceLikeEnergy(Function):
         positions = positions.detach().contiguous()
         cell = cell.detach().to(torch.float32).contiguous()
         n_edges, off, ei = batch.n_edges, batch.edge_offsets, batch.edge_index
-        order = _atom_order(batch, n)
-        wpa = _waves_per_atom(batch, n)
+        groups = _wave_groups(batch, n)
         elem = inputs.elem
         inv_avg = 1.0 / cfg.avg_num_neighbors
         geo = _empty(e_cap, 8, device=dev)
@@ -464,41 +487,33 @@ class _MaceLikeEnergy(Function):
             # Without vector features (h1 = 0, the first layer) wc and wd multiply only zeros: z keeps
             # just its a | b blocks ([E, 2C], the first 2C columns of W1). Node-factored (the
             # default): z = P, q = Q per atom and the kernels add the radial term per row.
-            timed = EDGE_GEMM_EVENTS is not None and not torch.cuda.is_current_stream_capturing()
             nz = 4 * C if h1 is not None else 2 * C
             if factored:
                 if not merged:
                     z, q = _factored_blocks(model, t, h0, elem, n, nz, dev)
                 A0 = _empty(n, C, device=dev)
                 A1 = _empty(n, 3, C, device=dev)
-                _call("fmd_mace_message_f32", z.data_ptr(), q.data_ptr(), geo.data_ptr(), ei.data_ptr(),
-                      off.data_ptr(), n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1), inv_avg,
-                      A0.data_ptr(), A1.data_ptr(), 1, ef.data_ptr(), w1ef_all[t].data_ptr(), nb, wpa)
+                _call_groups("fmd_mace_message_f32", groups, 7, z.data_ptr(), q.data_ptr(), geo.data_ptr(),
+                             ei.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, None, C, h0.data_ptr(),
+                             _abi.ptr(h1), inv_avg, A0.data_ptr(), A1.data_ptr(), 1, ef.data_ptr(),
+                             w1ef_all[t].data_ptr(), nb, 0)
             elif hoist:
                 h0p = split_planes(h0)
                 q = gemm_planes([(h0p, None)], model.w1_planes(t, "receiver", nz), a_planes=True)
                 w1p = model.w1_planes(t, "sender", nz)
-                shape = (e_cap, w1p.width, nz)
             else:
                 q = None
                 parts, w1 = [(h0, ei[:, 1]), (h0, ei[:, 0]), (ef, None)], model.w1_t(t)[:nz]
-                shape = (e_cap, w1.shape[1], nz)
             if not factored:
-                if timed:
-                    ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                    ev[0].record()
                 if hoist:
                     z = gemm_planes([(h0p, ei[:, 1]), (efp, None)], w1p, a_planes=True)
                 else:
                     z = gemm_gather(parts, w1)
-                if timed:
-                    ev[1].record()
-                    EDGE_GEMM_EVENTS.append((ev[0], ev[1], shape))
                 A0 = _empty(n, C, device=dev)
                 A1 = _empty(n, 3, C, device=dev)
-                _call("fmd_mace_message_f32", z.data_ptr(), _abi.ptr(q), geo.data_ptr(), ei.data_ptr(),
-                      off.data_ptr(), n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1), inv_avg,
-                      A0.data_ptr(), A1.data_ptr(), 0, None, None, 0, wpa)
+                _call_groups("fmd_mace_message_f32", groups, 7, z.data_ptr(), _abi.ptr(q), geo.data_ptr(),
+                             ei.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, None, C, h0.data_ptr(),
+                             _abi.ptr(h1), inv_avg, A0.data_ptr(), A1.data_ptr(), 0, None, None, 0, 0)
             B0 = _empty(n, C, device=dev)
             B1 = None if last else _empty(n, 3, C, device=dev)
             if FUSED_NODE:
@@ -608,8 +623,7 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
     dev = ctx.geo.device
     inv_avg = 1.0 / cfg.avg_num_neighbors
     n_edges, off, ei, rev = batch.n_edges, batch.edge_offsets, batch.edge_index, batch.edge_reverse
-    order = _atom_order(batch, n)
-    wpa = _waves_per_atom(batch, n)
+    groups = _wave_groups(batch, n)
     # readouts: gha = dE/d(first layer's h0 out), gy -> dE/d(last layer's h0 out)
     if gE is None and getattr(ctx, "gha", None) is not None:
         gha, gy = ctx.gha, ctx.gy  # formed by the forward's energy launch
@@ -688,11 +702,11 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
             # kernel from W1's radial rows (gz is not stored)
             gef = _empty(e_cap, nb, device=dev)
             w1ef = layer.W1[2 * C:]
-            _call("fmd_mace_message_bwd_f32", z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(), ei.data_ptr(),
-                  rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(),
-                  _abi.ptr(h1), gA0.data_ptr(), gA1.data_ptr(), inv_avg, None, None, None, ggeo.data_ptr(), acc_geo,
-                  None, None,
-                  0, w1ef.data_ptr(), nb, gef.data_ptr(), 1 if ctx.factored else 0, ctx.ef.data_ptr(), wpa)
+            _call_groups("fmd_mace_message_bwd_f32", groups, 8, z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(),
+                         ei.data_ptr(), rev.data_ptr(), off.data_ptr(), n_edges.data_ptr(), e_cap, n, None, C,
+                         h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(), gA1.data_ptr(), inv_avg, None, None, None,
+                         ggeo.data_ptr(), acc_geo, None, None, 0, w1ef.data_ptr(), nb, gef.data_ptr(),
+                         1 if ctx.factored else 0, ctx.ef.data_ptr(), 0)
             gefs.append((gef, nb))
             break
         # the gather-cat row gradient's node blocks come from per-node sums of g_z (never stored):
@@ -708,22 +722,11 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
         g_in1 = _empty(n, 3, C, device=dev) if h1 is not None else None
         w1ef = layer.W1[2 * C:]
         head = (z.data_ptr(), _abi.ptr(q), ctx.geo.data_ptr(), ei.data_ptr(), rev.data_ptr(), off.data_ptr(),
-                n_edges.data_ptr(), e_cap, n, order, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(), gA1.data_ptr(),
+                n_edges.data_ptr(), e_cap, n, None, C, h0.data_ptr(), _abi.ptr(h1), gA0.data_ptr(), gA1.data_ptr(),
                 inv_avg, None, gzs.data_ptr())
-        tail = (w1ef.data_ptr(), nb, gef.data_ptr(), 1 if ctx.factored else 0, ctx.ef.data_ptr(), wpa)
-        if MESSAGE_EVENTS is not None and not torch.cuda.is_current_stream_capturing():
-            # timed: the edge side alone between events, then the sender side alone (the same two
-            # kernels and results as the single call)
-            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            ev[0].record()
-            _call("fmd_mace_message_bwd_f32", *head, None, ggeo.data_ptr(), acc_geo, None, None, 0, *tail)
-            ev[1].record()
-            MESSAGE_EVENTS.append((ev[0], ev[1], (e_cap, n, C)))
-            _call("fmd_mace_message_bwd_f32", *head, gzs_src.data_ptr(), ggeo.data_ptr(), acc_geo, g_in0.data_ptr(),
-                  _abi.ptr(g_in1), 1 | 4, *tail)
-        else:
-            _call("fmd_mace_message_bwd_f32", *head, gzs_src.data_ptr(), ggeo.data_ptr(), acc_geo, g_in0.data_ptr(),
-                  _abi.ptr(g_in1), 1, *tail)
+        tail = (w1ef.data_ptr(), nb, gef.data_ptr(), 1 if ctx.factored else 0, ctx.ef.data_ptr(), 0)
+        _call_groups("fmd_mace_message_bwd_f32", groups, 8, *head, gzs_src.data_ptr(), ggeo.data_ptr(), acc_geo,
+                     g_in0.data_ptr(), _abi.ptr(g_in1), 1, *tail)
         # g_in0 += [gzs_src | gzs] [W1[:C] | W1[C:2C]]^T (sender and receiver blocks, one node GEMM)
         gemm_splitk(gzs_src, model.w1_node_blocks(t), b_layout=0, out=g_in0, a2=gzs, accumulate=True)
         gefs.append((gef, nb))

@@ -126,13 +126,16 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
  * callers that cannot call hipMalloc (code under HIP graph capture, tight serving loops,
  * harnesses that forbid allocation). Same arguments, kernels and results as fmd_nl_build,
  * without `work`: the per-block partials go to a static device array of
- * FMD_NL_BUILD_NOALLOC_SCRATCH int64 words (2 MiB) that each GPU the library runs on holds until
+ * FMD_NL_BUILD_NOALLOC_SCRATCH int64 words (3 MiB) that each GPU the library runs on holds until
  * the process ends. n_atoms above FMD_NL_BUILD_NOALLOC_MAX_ATOMS returns FMD_ETOOLARGE with
  * nothing launched. Every call on one GPU shares that GPU's array, which keeps the last call's
- * contents (nothing in it must start at zero: each block writes its slot before it is read),
- * so calls that overlap on one GPU (unordered streams) race. */
+ * contents (nothing in it must start at zero: each block writes its slot before it is read).
+ * It must not be called concurrently on one device: two calls whose kernels can overlap (on
+ * streams the caller has not ordered, or from two host threads) overwrite each other's partials
+ * and both return wrong edge offsets and flags, with no error reported. Calls on one stream, or
+ * on streams ordered by events, are safe. */
 #define FMD_NL_BUILD_NOALLOC_MAX_ATOMS (1 << 20)
-#define FMD_NL_BUILD_NOALLOC_SCRATCH 262146 /* fmd_nl_build_work_size(FMD_NL_BUILD_NOALLOC_MAX_ATOMS) */
+#define FMD_NL_BUILD_NOALLOC_SCRATCH 393218 /* fmd_nl_build_work_size(FMD_NL_BUILD_NOALLOC_MAX_ATOMS) */
 int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float* inv_cell, const float* cell,
                          int64_t n_atoms, const int32_t* neighbor_matrix, const int32_t* neighbor_shifts,
                          const int32_t* num_neighbors, int32_t bmax, const float* reference_positions,

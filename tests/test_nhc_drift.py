@@ -49,15 +49,14 @@ def _gate(gpu, oracle):
     return float(gpu.mean()), float(oracle.mean() + (oracle.max() - oracle.min()))
 
 
-def _record(name, rows):
-    """Writes the per-seed drift figures of one gate to gpurun_out/ (the summary under profiles/
-    quotes them)."""
-    out = os.path.join(os.path.dirname(GOLDEN), os.pardir, "gpurun_out")
-    os.makedirs(out, exist_ok=True)
-    with open(os.path.join(out, f"drift_{name}.txt"), "w") as fh:
-        fh.write("seed run drift_|b|T_eV resid_std_eV max_excursion_eV\n")
-        for row in rows:
-            fh.write(" ".join(str(v) for v in row) + "\n")
+def _record(name, rows, directory):
+    """Prints the per-seed drift figures of one gate (run pytest with -s to see them) and writes
+    them to ``directory`` (the test's tmp_path)."""
+    lines = ["seed run drift_|b|T_eV resid_std_eV max_excursion_eV"]
+    lines += [" ".join(str(v) for v in row) for row in rows]
+    with open(os.path.join(directory, f"drift_{name}.txt"), "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print(f"[drift {name}]\n" + "\n".join(lines), flush=True)
 
 
 def _mace_params():
@@ -153,7 +152,7 @@ def _md(system, adapter, momenta, device):
 
 
 @pytest.mark.gpu
-def test_nhc_conserved_quantity_drift_10k_steps_morse(device):
+def test_nhc_conserved_quantity_drift_10k_steps_morse(device, tmp_path):
     """10 000 whole-step NHC steps of Morse on the 135-atom perovskite at 500 K."""
     from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
     from fastmd_amd.models.pair_potential import MorsePairAdapter
@@ -176,14 +175,14 @@ def test_nhc_conserved_quantity_drift_10k_steps_morse(device):
         print(f"[drift morse] seed {seed}: |b|T gpu {g[0]:.3e} eV, oracle {o[0]:.3e} eV; "
               f"residual std gpu {g[1]:.3e}, oracle {o[1]:.3e}; excursion gpu {g[2]:.3e}, oracle {o[2]:.3e}",
               flush=True)
-    _record("morse_135_10000", rows)
+    _record("morse_135_10000", rows, tmp_path)
     got, bound = _gate(gpu, oracle)
     print(f"[drift morse] mean gpu {got:.3e} eV <= bound {bound:.3e} eV", flush=True)
     assert got <= bound, (gpu, oracle)
 
 
 @pytest.mark.gpu
-def test_mace_like_nhc_2000_steps_vs_oracle(device):
+def test_mace_like_nhc_2000_steps_vs_oracle(device, tmp_path):
     """the MACE-like model (random init, seed 0) on the 135-atom perovskite, 2 000
     whole-step NHC steps per seed. Positions follow the float64 oracle's trajectory over the first
     50 steps (1e-4 A); the drift over the whole run is gated against the oracle's float32 runs (the
@@ -215,7 +214,61 @@ def test_mace_like_nhc_2000_steps_vs_oracle(device):
         print(f"[mace 2000] seed {seed}: |b|T gpu {g[0]:.3e} eV, oracle f32 {f32[0]:.3e} eV, oracle f64 "
               f"{f64[0]:.3e} eV; residual std gpu {g[1]:.3e}, oracle f32 {f32[1]:.3e}; excursion gpu "
               f"{g[2]:.3e}, oracle f32 {f32[2]:.3e}", flush=True)
-    _record("mace_like_135_2000", rows)
+    _record("mace_like_135_2000", rows, tmp_path)
     got, bound = _gate(gpu, o32)
     print(f"[mace 2000] mean gpu {got:.3e} eV <= bound {bound:.3e} eV", flush=True)
+    assert got <= bound, (gpu, o32)
+
+
+def test_mace_like_10k_fixture_is_the_oracle_integration():
+    import torch
+
+    import md_oracle
+    from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
+
+    fx = _fixture("nhc_drift_mace_like_135_10k.npz")
+    s = systems.perovskite(3)
+    assert tuple(fx["seeds"]) == (0, 1, 2) and fx["steps"][-1] == 10_000
+    assert fx["conserved_f32"].shape == (3, 201) and fx["conserved_f64"].shape == (3, 201)
+    params, cfg = _mace_params()
+    live = md_oracle.run_nhc(s, md_oracle.mace_like_forces(s, params, cfg, dtype=torch.float32),
+                             maxwell_boltzmann_momenta(s.masses, 500.0, 2), 100, sample_every=50)
+    np.testing.assert_allclose(live["conserved"], fx["conserved_f32"][2, :3], rtol=0, atol=1e-9)
+    # the 2 000-step fixture is the same integration, sampled more often
+    short = _fixture("nhc_drift_mace_like_135.npz")
+    np.testing.assert_allclose(fx["conserved_f64"][:, :41], short["conserved_f64"][:, ::5], rtol=0, atol=1e-9)
+
+
+@pytest.mark.gpu
+def test_mace_like_nhc_drift_10k_steps(device, tmp_path):
+    """The north-star drift gate on configs[2]: 10 000 whole-step NHC steps of the MACE-like model
+    (random init, seed 0) on the 135-atom perovskite per momenta seed, C(t) every 50 steps, the
+    fitted drift gated against the oracle's float32 runs of the same 10 000 steps (float64 runs
+    reported beside them)."""
+    from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
+    from fastmd_amd.models.mace_like import MaceLikeAdapter
+
+    fx = _fixture("nhc_drift_mace_like_135_10k.npz")
+    s = systems.perovskite(3)
+    gpu, o32, rows = [], [], []
+    for k, seed in enumerate(fx["seeds"]):
+        md = _md(s, MaceLikeAdapter(device=device), maxwell_boltzmann_momenta(s.masses, 500.0, int(seed)), device)
+        c0 = md.conserved_energy()
+        assert abs(c0 - fx["conserved_f64"][k, 0]) < 1e-5 * s.n_atoms
+        series = [c0]
+        for _ in range(200):
+            md.run(50)
+            series.append(md.conserved_energy())
+        g = drift_stats(fx["steps"], series)
+        f32 = drift_stats(fx["steps"], fx["conserved_f32"][k])
+        f64 = drift_stats(fx["steps"], fx["conserved_f64"][k])
+        gpu.append(g[0])
+        o32.append(f32[0])
+        rows += [(int(seed), "gpu", *g), (int(seed), "oracle_f32", *f32), (int(seed), "oracle_f64", *f64)]
+        print(f"[mace 10k] seed {seed}: |b|T gpu {g[0]:.3e} eV, oracle f32 {f32[0]:.3e} eV, oracle f64 "
+              f"{f64[0]:.3e} eV; residual std gpu {g[1]:.3e}, oracle f32 {f32[1]:.3e}; excursion gpu "
+              f"{g[2]:.3e}, oracle f32 {f32[2]:.3e}", flush=True)
+    _record("mace_like_135_10000", rows, tmp_path)
+    got, bound = _gate(gpu, o32)
+    print(f"[mace 10k] mean gpu {got:.3e} eV <= bound {bound:.3e} eV", flush=True)
     assert got <= bound, (gpu, o32)

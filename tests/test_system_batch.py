@@ -96,6 +96,74 @@ def test_systems_equal_single_runs_bitwise(device, model_name):
 
 
 @pytest.mark.gpu
+def test_small_and_large_systems_against_single_runs(device):
+    """A 135-atom system in a slot of 2 200 rows next to the 5 000-atom perovskite, 10 steps. The
+    message kernels take the small system's atoms four waves each and the large one's one wave
+    each, as their single runs do (chosen per system, not per slot or union), and the large
+    system's chain runs on the multi-block NHC path (more than 4 096 atoms): the large system
+    equals its single run bitwise. The small system's node GEMMs run inside launches of the
+    union's 7 200 rows, which take the split-plane form its 135-atom single run does not (the
+    form is chosen per launch size), so it matches its single run to float32 rounding, not
+    bitwise."""
+    import torch
+
+    from fastmd_amd.execution.gpu_nhc import maxwell_boltzmann_momenta
+    from fastmd_amd.execution.system_batch import SystemBatchedMD
+    from fastmd_amd.models.mace_like import SPLIT_ROWS_MAX_ATOMS
+
+    print("[systems] 135 + 5000 atoms, mace_like", flush=True)
+    sys_list = [systems.perovskite(3), systems.perovskite(10, seed=3)]
+    assert sys_list[0].n_atoms <= SPLIT_ROWS_MAX_ATOMS < 2200 < sys_list[1].n_atoms
+    momenta = [maxwell_boltzmann_momenta(s.masses, 500.0, 40 + k) for k, s in enumerate(sys_list)]
+    batch = SystemBatchedMD(sys_list, _adapter("mace_like", device), ceilings=(2200, 5000), device=device,
+                            temperature=500.0, timestep=0.25, tdamp=25.0, momenta=momenta, steps_per_launch=5)
+    assert batch.runner.builder.batch.system_slots == ((0, 2200, 135), (2200, 5000, 5000))
+    batch.run(10)
+    torch.cuda.synchronize()
+    for k, s in enumerate(sys_list):
+        single = _single(s, _adapter("mace_like", device), momenta[k], device, 10)
+        torch.cuda.synchronize()
+        got = batch.system_state(k)
+        th = single.integrator
+        if k == 1:
+            for key in ("positions", "momenta", "forces"):
+                assert torch.equal(got[key], getattr(th, key)), (k, key)
+            assert torch.equal(got["potential_energy"].reshape(1), th.potential_energy.reshape(1))
+            assert torch.equal(batch.integrator.eta[k], th.eta) and torch.equal(batch.integrator.p_eta[k], th.p_eta)
+        else:
+            dq = float((got["positions"] - th.positions).abs().max())
+            df = float((got["forces"] - th.forces).abs().max())
+            de = abs(float(got["potential_energy"]) - float(th.potential_energy)) / s.n_atoms
+            print(f"[systems] 135-atom system vs its single run: |dq| {dq:.2e} A, |dF| {df:.2e} eV/A, "
+                  f"|dE| {de:.2e} eV/atom", flush=True)
+            assert dq < 1e-6 and df < 1e-4 and de < 1e-6
+        del single
+        torch.cuda.empty_cache()
+
+
+def test_wave_groups_follow_each_systems_size():
+    """The message kernels' launches of a slot union: one per run of slots with the same waves per
+    atom, over that run's range of the atom order."""
+    import types
+
+    import torch
+
+    from fastmd_amd.models.mace_like import _wave_groups
+
+    order = torch.arange(7400, dtype=torch.int32)
+    base = order.data_ptr()
+    batch = types.SimpleNamespace(atom_order=order, max_system_rows=5000,
+                                  system_slots=((0, 2200, 135), (2200, 5000, 5000), (7200, 200, 180)))
+    assert _wave_groups(batch, 7400) == [(base, 2200, 4), (base + 4 * 2200, 5000, 1), (base + 4 * 7200, 200, 4)]
+    batch.system_slots = ((0, 2200, 135), (2200, 200, 180), (2400, 5000, 5000))
+    assert _wave_groups(batch, 7400) == [(base, 2400, 4), (base + 4 * 2400, 5000, 1)]
+    single = types.SimpleNamespace(atom_order=None, max_system_rows=0)
+    assert _wave_groups(single, 135) == [(None, 135, 4)] and _wave_groups(single, 3000) == [(None, 3000, 1)]
+    replicas = types.SimpleNamespace(atom_order=None, max_system_rows=135)
+    assert _wave_groups(replicas, 135 * 32) == [(None, 135 * 32, 4)]
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("model_name", ["morse", "mace_like"])
 def test_systems_follow_the_oracle_md(device, model_name):
     """Each system of the union follows the CPU oracle's NHC integration of that system alone
