@@ -670,7 +670,7 @@ __global__ void __launch_bounds__(kBlock) nl_count_kernel(BuildArgs a) {
 // memory round trip). The last workgroup also reduces the count kernel's partials (maximum
 // displacement, isolated atoms) and writes the total, the flags and edge_offsets[n]. Integer
 // sums are exact, so the offsets are the same in any grouping.
-constexpr int kScanThreads = 256, kScanPer = 8, kScanTile = kScanThreads * kScanPer;
+constexpr int kScanThreads = 256, kScanPer = 8, kScanTile = kScanThreads * kScanPer, kScanLoads = 8;
 constexpr int kAtomsPerCountBlock = kBlock / FMD_WAVE;
 static_assert(kScanTile % kAtomsPerCountBlock == 0, "scan tiles cover whole count blocks");
 
@@ -693,19 +693,43 @@ __global__ void __launch_bounds__(kScanThreads) nl_scan_kernel(BuildArgs a, int6
     c[j] = k < cnt ? a.edge_counts[base + k] : 0;
   }
   // the edge count of every atom before this tile: the count blocks [0, base / kAtomsPerCountBlock)
+  // (16-byte loads, kScanLoads of them in flight per thread: a loop of single loads would wait out
+  // one memory round trip per iteration)
   const int32_t* bsum = reinterpret_cast<const int32_t*>(a.work + 2 * fmd_cdiv(nblocks, 2));
-  const int64_t nbefore = base / kAtomsPerCountBlock;
+  const int4* bsum4 = reinterpret_cast<const int4*>(bsum);
+  const int64_t nbefore = base / kAtomsPerCountBlock, nbefore4 = nbefore / 4;
   int64_t pre = 0;
-  for (int64_t b = t; b < nbefore; b += T) pre += bsum[b];
+  for (int64_t q0 = t; q0 < nbefore4; q0 += (int64_t)T * kScanLoads) {
+    int4 v[kScanLoads];
+#pragma unroll
+    for (int u = 0; u < kScanLoads; ++u) {
+      const int64_t q = q0 + (int64_t)u * T;
+      v[u] = q < nbefore4 ? bsum4[q] : make_int4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < kScanLoads; ++u) pre += (int64_t)v[u].x + v[u].y + v[u].z + v[u].w;
+  }
+  for (int64_t b = nbefore4 * 4 + t; b < nbefore; b += T) pre += bsum[b];
   // the last workgroup: the count kernel's partials over all its blocks
   float m = 0.f;
   int32_t iso = 0;
   if (last) {
     const float* red = reinterpret_cast<const float*>(a.work);
     const int32_t* isop = reinterpret_cast<const int32_t*>(a.work + fmd_cdiv(nblocks, 2));
-    for (int64_t b = t; b < nblocks; b += T) {
-      m = nan_max(m, red[b]);
-      iso += isop[b];
+    for (int64_t b0 = t; b0 < nblocks; b0 += (int64_t)T * kScanLoads) {
+      float r[kScanLoads];
+      int32_t z[kScanLoads];
+#pragma unroll
+      for (int u = 0; u < kScanLoads; ++u) {
+        const int64_t b = b0 + (int64_t)u * T;
+        r[u] = b < nblocks ? red[b] : 0.f;
+        z[u] = b < nblocks ? isop[b] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < kScanLoads; ++u) {
+        m = nan_max(m, r[u]);
+        iso += z[u];
+      }
     }
   }
   pre = wave_sum(pre);
@@ -998,7 +1022,7 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
                  uint8_t* candidate_valid, uint8_t* overflow, int32_t* isolated, float line2, uint8_t* short_flags,
                  hipStream_t stream) {
-  FMD_REQUIRE(work);
+  FMD_REQUIRE(work && reinterpret_cast<uintptr_t>(work) % 16 == 0);  // the scan reads it 16 bytes at a time
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
               reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, minimum_image, pad_ix, pad_iy, pad_iz,
               n_dummy, system_of, pad_images, e_cap, work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,

@@ -101,7 +101,7 @@ int fmd_nl_wrap(const void* positions, int32_t pos_is_f64, const float* inv_cell
  *                   (_pad_edges_kernel, fixed_capacity_builder.py:291-320): padded row r is a
  *                   self-loop of sink row n + p n_dummy / (e_cap / 2 - ec / 2), p = (r - ec) / 2,
  *                   ec = min(E, e_cap), image (3, 3, 3), distance 1e6 (one system only)
- *   work            int64 scratch of fmd_nl_build_work_size(n) elements
+ *   work            int64 scratch of fmd_nl_build_work_size(n) elements, 16-byte aligned
  * Outputs: frac [n,3] f32, wrap_delta [n,3] i32, wrapped_out [n,3] f32 (published
  * positions, may be null), edge_counts [n] i64, edge_offsets [n+1] i64, center/neighbor
  * [e_cap] i32, images [e_cap,3] i32, distances [e_cap] f32, edge_index [e_cap,2] i32 and

@@ -220,6 +220,12 @@ def test_mace_like_nhc_2000_steps_vs_oracle(device, tmp_path):
     assert got <= bound, (gpu, o32)
 
 
+_LONG = os.path.join(GOLDEN, "nhc_drift_mace_like_135_10k.npz")
+_needs_long = pytest.mark.skipif(not os.path.exists(_LONG), reason="tests/golden/make_nhc_drift.py mace_like_10k "
+                                 "has not written its fixture")
+
+
+@_needs_long
 def test_mace_like_10k_fixture_is_the_oracle_integration():
     import torch
 
@@ -231,8 +237,13 @@ def test_mace_like_10k_fixture_is_the_oracle_integration():
     assert tuple(fx["seeds"]) == (0, 1, 2) and fx["steps"][-1] == 10_000
     assert fx["conserved_f32"].shape == (3, 201) and fx["conserved_f64"].shape == (3, 201)
     params, cfg = _mace_params()
-    live = md_oracle.run_nhc(s, md_oracle.mace_like_forces(s, params, cfg, dtype=torch.float32),
-                             maxwell_boltzmann_momenta(s.masses, 500.0, 2), 100, sample_every=50)
+    threads = torch.get_num_threads()
+    torch.set_num_threads(1)  # the generator's workers run one thread each (float32 sums follow the thread count)
+    try:
+        live = md_oracle.run_nhc(s, md_oracle.mace_like_forces(s, params, cfg, dtype=torch.float32),
+                                 maxwell_boltzmann_momenta(s.masses, 500.0, 2), 100, sample_every=50)
+    finally:
+        torch.set_num_threads(threads)
     np.testing.assert_allclose(live["conserved"], fx["conserved_f32"][2, :3], rtol=0, atol=1e-9)
     # the 2 000-step fixture is the same integration, sampled more often
     short = _fixture("nhc_drift_mace_like_135.npz")
@@ -240,6 +251,7 @@ def test_mace_like_10k_fixture_is_the_oracle_integration():
 
 
 @pytest.mark.gpu
+@_needs_long
 def test_mace_like_nhc_drift_10k_steps(device, tmp_path):
     """The north-star drift gate on configs[2]: 10 000 whole-step NHC steps of the MACE-like model
     (random init, seed 0) on the 135-atom perovskite per momenta seed, C(t) every 50 steps, the
