@@ -68,6 +68,8 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_gemm_f32": (ctypes.c_int, [_p, _i64, _p, _i64, _i32, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _p]),
     "fmd_gemm_group_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _i32,
                                           _p]),
+    "fmd_gemm_group_ks_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32,
+                                             _p]),
     "fmd_gemm_group_x3_planes_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                                     _i32, _p]),
     "fmd_split3_f32": (ctypes.c_int, [_p, _i64, _i64, _i32, _p, _p]),
@@ -95,6 +97,9 @@ SIGNATURES: dict[str, tuple] = {
                                              _p, _p]),
     "fmd_mace_node_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p, _i32,
                                              _p, _p, _p, _p, _p]),
+    "fmd_mace_mix_symcon_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p, _p, _p]),
+    "fmd_mace_mix_symcon_bwd_f32": (ctypes.c_int, [_p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p,
+                                                   _p]),
     "fmd_mace_symcon_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p]),
     "fmd_mace_symcon_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p]),
     "fmd_mace_energy_f32": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _p, _p, _f32, _f32, _i64, _p, _p]),

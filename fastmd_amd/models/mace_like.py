@@ -72,6 +72,12 @@ MERGED_NODE = True
 # atom's rows over four waves in the message kernels (one wave per atom leaves a small system's
 # chip idle while each wave walks its rows); the per-atom sums are then added over the waves.
 SPLIT_ROWS_MAX_ATOMS = 2048
+# Launches of at most this many atoms (unfused node side) form P0, P1 and the contraction in one
+# launch (fmd_mace_mix_symcon_f32: 16 atoms x 16 channels per workgroup, the scalar and vector
+# rows of a tile in its four waves), and in the VJP gB0, gB1 and the contraction's VJP in one
+# (fmd_mace_mix_symcon_bwd_f32), the residual's input gradient then joining the gA group. Above,
+# the grouped GEMMs and the contraction kernels run as separate launches.
+SMALL_NODE_MAX_ATOMS = 2048
 
 
 @dataclass(frozen=True)
@@ -535,11 +541,16 @@ class _MaceLikeEnergy(Function):
                 wp = w["planes"]
                 P0 = _empty(n, C, device=dev)
                 P1 = _empty(n, 3, C, device=dev)
-                gemm_group([{"a": A0, "b": w["wm0t"], "b_planes": wp["wm0t"], "out": P0},
-                            {"a": A1.view(3 * n, C), "b": w["wm1t"], "b_planes": wp["wm1t"],
-                             "out": P1.view(3 * n, C)}], b_layout=0)
-                _call("fmd_mace_symcon_f32", P0.data_ptr(), P1.data_ptr(), elem.data_ptr(), layer.Wc.data_ptr(),
-                      layer.Wd.data_ptr(), n, C, B0.data_ptr(), _abi.ptr(B1))
+                if n <= SMALL_NODE_MAX_ATOMS:
+                    _call("fmd_mace_mix_symcon_f32", A0.data_ptr(), A1.data_ptr(), w["wm0t"].data_ptr(),
+                          w["wm1t"].data_ptr(), elem.data_ptr(), layer.Wc.data_ptr(), layer.Wd.data_ptr(), n, C,
+                          P0.data_ptr(), P1.data_ptr(), B0.data_ptr(), _abi.ptr(B1))
+                else:
+                    gemm_group([{"a": A0, "b": w["wm0t"], "b_planes": wp["wm0t"], "out": P0},
+                                {"a": A1.view(3 * n, C), "b": w["wm1t"], "b_planes": wp["wm1t"],
+                                 "out": P1.view(3 * n, C)}], b_layout=0)
+                    _call("fmd_mace_symcon_f32", P0.data_ptr(), P1.data_ptr(), elem.data_ptr(), layer.Wc.data_ptr(),
+                          layer.Wd.data_ptr(), n, C, B0.data_ptr(), _abi.ptr(B1))
                 h0n = None if merged and last else (h0n_first if merged and t == 0 else _empty(n, C, device=dev))
                 h1n = None if last else _empty(n, 3, C, device=dev)
                 if merged and last:
@@ -663,38 +674,51 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
                   _abi.ptr(gB1), _abi.ptr(g_in0), 1 if t == 1 else 0, gP0.data_ptr(), gP1.data_ptr(),
                   gA0.data_ptr(), gA1.data_ptr())
         else:
-            # two grouped GEMM launches around the contraction's VJP: (gB0 = g_out0 Wo0^T,
-            # gB1 = g_out1 Wo1^T, and with t > 0 this layer's input gradient through the residual,
-            # g_in0 = g_out0 Wsc0^T, added to the first readout's gradient in the second layer),
-            # then (gA0 = gP0 Wm0^T, gA1 = gP1 Wm1^T)
+            # gB0 = g_out0 Wo0^T, gB1 = g_out1 Wo1^T, the contraction's VJP (gP0, gP1), then
+            # gA0 = gP0 Wm0^T, gA1 = gP1 Wm1^T; with t > 0 also this layer's input gradient through
+            # the residual, g_in0 = g_out0 Wsc0^T, added to the first readout's gradient in the second
+            # layer. Small launches: the first three in one kernel, g_in0 in the gA group; else
+            # grouped GEMM launches around the contraction's VJP kernel, g_in0 in the first group.
             wp = model.node_weights(t)["planes"]
-            gB0 = _empty(n, C, device=dev)
-            gB1 = None if g_out1 is None else _empty(n, 3, C, device=dev)
+            gA0 = _empty(n, C, device=dev)
+            gA1 = _empty(n, 3, C, device=dev)
+            gA_probs = [{"a": gP0, "b": layer.Wm0, "b_planes": wp["Wm0"], "out": gA0},
+                        {"a": gP1.view(3 * n, C), "b": layer.Wm1, "b_planes": wp["Wm1"], "out": gA1.view(3 * n, C)}]
             if g_out0 is None:
                 # the last layer under the merged node side: gB0 = gy (Wo0 Wr2a)^T and the residual's
                 # g_in0 = gy (Wsc0 Wr2a)^T (gy [N, H]: K = H)
                 gb, gs = model.merged_weights()["gy"]
-                g_in0 = gha if t == 1 else _empty(n, C, device=dev)
-                probs = [{"a": gy, "b": gb, "out": gB0},
-                         {"a": gy, "b": gs, "out": g_in0, "accumulate": t == 1}]
+                g0, wb0, k0, ws, wsp = gy, gb, H, gs, None
             else:
-                probs = [{"a": g_out0, "b": layer.Wo0, "b_planes": wp["Wo0"], "out": gB0}]
+                g0, wb0, k0, ws, wsp = g_out0, layer.Wo0, C, layer.Wsc0, wp["Wsc0"]
+            if t > 0:
+                g_in0 = gha if t == 1 else _empty(n, C, device=dev)
+                res = {"a": g0, "b": ws, "out": g_in0, "accumulate": t == 1}
+                if wsp is not None:
+                    res["b_planes"] = wsp
+            if n <= SMALL_NODE_MAX_ATOMS:
+                # gB0, gB1 and the contraction's VJP in one launch; the residual's input gradient
+                # joins the gA group
+                _call("fmd_mace_mix_symcon_bwd_f32", g0.data_ptr(), k0, wb0.data_ptr(), _abi.ptr(g_out1),
+                      layer.Wo1.data_ptr(), P0.data_ptr(), P1.data_ptr(), inputs.elem.data_ptr(), layer.Wc.data_ptr(),
+                      layer.Wd.data_ptr(), n, C, gP0.data_ptr(), gP1.data_ptr())
+                gemm_group(gA_probs + ([res] if t > 0 else []), b_layout=0)
+            else:
+                gB0 = _empty(n, C, device=dev)
+                gB1 = None if g_out1 is None else _empty(n, 3, C, device=dev)
+                probs = [{"a": g0, "b": wb0, "out": gB0}]
+                if g_out0 is not None:
+                    probs[0]["b_planes"] = wp["Wo0"]
                 if gB1 is not None:
                     probs.append({"a": g_out1.reshape(3 * n, C), "b": layer.Wo1, "b_planes": wp["Wo1"],
                                   "out": gB1.view(3 * n, C)})
                 if t > 0:
-                    g_in0 = gha if t == 1 else _empty(n, C, device=dev)
-                    probs.append({"a": g_out0, "b": layer.Wsc0, "b_planes": wp["Wsc0"], "out": g_in0,
-                                  "accumulate": t == 1})
-            gemm_group(probs, b_layout=0)
-            _call("fmd_mace_symcon_bwd_f32", P0.data_ptr(), P1.data_ptr(), inputs.elem.data_ptr(),
-                  layer.Wc.data_ptr(), layer.Wd.data_ptr(), gB0.data_ptr(), _abi.ptr(gB1), n, C, gP0.data_ptr(),
-                  gP1.data_ptr())
-            gA0 = _empty(n, C, device=dev)
-            gA1 = _empty(n, 3, C, device=dev)
-            gemm_group([{"a": gP0, "b": layer.Wm0, "b_planes": wp["Wm0"], "out": gA0},
-                        {"a": gP1.view(3 * n, C), "b": layer.Wm1, "b_planes": wp["Wm1"],
-                         "out": gA1.view(3 * n, C)}], b_layout=0)
+                    probs.append(res)
+                gemm_group(probs, b_layout=0)
+                _call("fmd_mace_symcon_bwd_f32", P0.data_ptr(), P1.data_ptr(), inputs.elem.data_ptr(),
+                      layer.Wc.data_ptr(), layer.Wd.data_ptr(), gB0.data_ptr(), _abi.ptr(gB1), n, C, gP0.data_ptr(),
+                      gP1.data_ptr())
+                gemm_group(gA_probs, b_layout=0)
         acc_geo = 1 if t < L - 1 else 0
         if t == 0:
             # the first layer's inputs are the element embedding (no position dependence): only

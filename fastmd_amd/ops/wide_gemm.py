@@ -60,6 +60,10 @@ def gemm(a: Tensor, b: Tensor, *, b_layout: int, bias: Tensor | None = None, out
 # 128 x 128 tiles from which a group with pre-split weights takes the split-plane form (below,
 # the fp32 kernel's 64 x 64 tiles give four times more workgroups)
 GROUP_X3_MIN_TILES = 128
+# 64 x 64 tiles below which a b_layout 0 group (and a split-K product) takes the K-split form
+# (fmd_gemm_group_ks_f32: 16 x 16 tiles, K shared by the four waves of a workgroup): a group
+# that small leaves most of the chip idle while each 64 x 64 tile walks its K slices
+GROUP_KS_MAX_TILES = 256
 
 
 def gemm_group(problems, *, b_layout: int, epilogue: str | None = None) -> list:
@@ -116,6 +120,16 @@ def gemm_group(problems, *, b_layout: int, epilogue: str | None = None) -> list:
         cols["acc"].append(1 if p.get("accumulate") else 0)
     i64 = lambda key: _abi.array(_abi._i64, cols[key])  # noqa: E731
     planes = [p.get("b_planes") for p in problems]
+    tiles64 = sum(-(-m // 64) * -(-n // 64) for m, n in zip(cols["m"], cols["n"]))
+    if b_layout == 0 and tiles64 < GROUP_KS_MAX_TILES:
+        status = _abi.load().fmd_gemm_group_ks_f32(
+            len(problems), _abi.ptr_array(cols["a"]), i64("lda"), _abi.ptr_array(cols["a2"]), i64("lda2"),
+            i64("ksplit"), _abi.ptr_array(cols["b"]), i64("ldb"), _abi.ptr_array(cols["bias"]),
+            _abi.ptr_array(cols["c"]), i64("ldc"), i64("m"), i64("n"), i64("k"), _abi.array(_abi._i32, cols["acc"]),
+            _EPILOGUES[epilogue], stream())
+        if status != _EUNSUPPORTED:
+            _abi.check(status, "fmd_gemm_group_ks_f32")
+            return [p["out"] for p in problems]
     tiles = sum(-(-m // 128) * -(-n // 128) for m, n in zip(cols["m"], cols["n"]))
     if b_layout == 0 and all(q is not None for q in planes) and tiles >= GROUP_X3_MIN_TILES:
         for q, p in zip(planes, problems):
@@ -141,8 +155,20 @@ def gemm_group(problems, *, b_layout: int, epilogue: str | None = None) -> list:
 def gemm_splitk(a: Tensor, b: Tensor, *, b_layout: int, out: Tensor, a2: Tensor | None = None,
                 bias: Tensor | None = None, accumulate: bool = False, splits: int = 8) -> Tensor:
     """``out (+)= [a | a2] @ op(b) (+ bias)`` with K cut into ``splits`` slices multiplied by separate
-    workgroups and summed in slice order (fmd_gemm_splitk_f32): tall-K, few-tile GEMMs."""
+    workgroups and summed in slice order (fmd_gemm_splitk_f32): tall-K, few-tile GEMMs. Products
+    of fewer than ``GROUP_KS_MAX_TILES`` 64 x 64 tiles (b_layout 0) run as a one-problem K-split
+    group instead (one launch, no workspace)."""
     require_cuda(a, b, out, a2, bias)
+    n_out = b.shape[0] if b_layout == 0 else b.shape[1]
+    if b_layout == 0 and -(-a.shape[0] // 64) * -(-n_out // 64) < GROUP_KS_MAX_TILES and (
+            a2 is None or a.shape[1] % 32 == 0):
+        prob = {"a": a, "b": b, "out": out, "accumulate": accumulate}
+        if a2 is not None:
+            prob["a2"] = a2
+        if bias is not None:
+            prob["bias"] = bias
+        gemm_group([prob], b_layout=0)
+        return out
     a, lda = rows_view(a)
     b, ldb = rows_view(b)
     m, ka = a.shape

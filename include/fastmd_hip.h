@@ -394,6 +394,19 @@ int fmd_gemm_group_x3_planes_f32(int32_t count, const float* const* a, const int
                                  const int64_t* m, const int64_t* n, const int64_t* k,
                                  const int32_t* accumulate, int32_t epilogue, hipStream_t stream);
 
+/* fmd_gemm_group_f32 with b_layout 0 (B_g [N_g, K_g] K-contiguous) for groups too small to fill
+ * the chip (small systems' node side): 16 x 16 output tiles, one workgroup each, whose four
+ * waves multiply a contiguous quarter of the K slices of 32 each with fp32 MFMAs and add their
+ * partial tiles in wave order (deterministic; not fmd_gemm_f32's K order, so not its bits).
+ * Conditions: A_g, A2_g and B_g 16-byte aligned, lda_g, lda2_g and ldb_g multiples of 4,
+ * ksplit_g a multiple of 32 when A2_g is set; FMD_EUNSUPPORTED otherwise (nothing launched).
+ * Replaces the same linear / matmul calls as fmd_gemm_group_f32 (triton_wide_gemm.py:482-553). */
+int fmd_gemm_group_ks_f32(int32_t count, const float* const* a, const int64_t* lda, const float* const* a2,
+                          const int64_t* lda2, const int64_t* ksplit, const float* const* b, const int64_t* ldb,
+                          const float* const* bias, float* const* c, const int64_t* ldc, const int64_t* m,
+                          const int64_t* n, const int64_t* k, const int32_t* accumulate, int32_t epilogue,
+                          hipStream_t stream);
+
 /* C = [A | A2] op(B) (+ bias) (+ C if accumulate) as fmd_gemm_f32, with K cut into `splits` equal
  * slices (multiples of 32, none straddling ksplit, the width of A; A2 may be null) multiplied by
  * separate workgroups into workspace [splits, M, N] and then summed in slice order
@@ -581,6 +594,27 @@ int fmd_mace_node_bwd_f32(const float* g0, const float* g1, const float* P0, con
                           const float* wo0st, const float* wo1st, const float* Wc, const float* Wd, const float* wm0,
                           const float* wm1, int64_t n_atoms, int32_t channels, float* gB0, float* gB1, float* gin0,
                           int32_t accumulate_in0, float* gP0, float* gP1, float* gA0, float* gA1, hipStream_t stream);
+/* The first half of a layer's node side for small systems, one launch: P0 = A0 Wm0, P1_x = A1_x
+ * Wm1 (A1 [N,3,C]) and the symmetric contraction B0, B1 (B1 null: last layer, no vector output)
+ * of every (atom, channel), P0 and P1 written too (the VJP reads them). A workgroup takes 16 atoms
+ * x 16 channels: one wave per row kind (the scalar row, the vector rows x, y, z) over all of K =
+ * C with fp32 MFMAs, the contraction from the four tiles in LDS. wm0t = Wm0^T, wm1t = Wm1^T [C, C]
+ * (K-contiguous), 16-byte aligned like A0, A1; channels a multiple of 32. Same results as
+ * fmd_gemm_group_ks_f32 + fmd_mace_symcon_f32 up to the K order of the products. No reference
+ * counterpart: it replaces two launches of the model's node-side chain (mace.py:386 runs
+ * mace-torch there). */
+int fmd_mace_mix_symcon_f32(const float* A0, const float* A1, const float* wm0t, const float* wm1t,
+                            const int32_t* elem, const float* Wc, const float* Wd, int64_t n_atoms, int32_t channels,
+                            float* P0, float* P1, float* B0, float* B1, hipStream_t stream);
+/* The VJP's matching half, one launch: gB0 = g0 wb0^T (g0 [N, k0], wb0 [C, k0]; k0 = C with
+ * wb0 = Wo0, or the readout width with the merged last layer's weight), gB1_x = g1_x wb1^T (g1
+ * [N,3,C], wb1 = Wo1 [C, C]; g1 null: no vector output gradient) and the contraction's VJP from
+ * them -> gP0 [N,C], gP1 [N,3,C] (gB0 and gB1 are never written). Layout and conditions as
+ * fmd_mace_mix_symcon_f32, k0 a multiple of 4. No reference counterpart (see there). */
+int fmd_mace_mix_symcon_bwd_f32(const float* g0, int64_t k0, const float* wb0, const float* g1, const float* wb1,
+                                const float* P0, const float* P1, const int32_t* elem, const float* Wc,
+                                const float* Wd, int64_t n_atoms, int32_t channels, float* gP0, float* gP1,
+                                hipStream_t stream);
 /* Symmetric contraction (correlation 3, L <= 1) and its VJP. */
 int fmd_mace_symcon_f32(const float* P0, const float* P1, const int32_t* elem, const float* Wc, const float* Wd,
                         int64_t n_atoms, int32_t channels, float* B0, float* B1, hipStream_t stream);

@@ -334,6 +334,57 @@ def test_mace_like_gpu_matches_oracle(device, n_cells, channels, hoist, fused, g
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("n,C", [(135, 128), (1080, 64), (37, 256)])
+def test_mix_symcon_kernels(device, n, C):
+    """fmd_mace_mix_symcon_f32 and its VJP half (small systems' node side, one launch each): P0 =
+    A0 Wm0 and P1 = A1 Wm1 within fp32 of float64, the contraction B0, B1 the standalone kernel's on
+    those P to fp32 rounding; gP0, gP1 the contraction VJP kernel's on float64 gB0 = g0 Wo0^T and
+    gB1 = g1 Wo1^T (rounded to float32), with and without the vector gradient, with K = C and with
+    the readout width 16 (the merged last layer); a ragged last tile of atoms (n % 16 != 0)."""
+    from fastmd_amd import _abi
+    from fastmd_amd.models.mace_like import MaceLike, MaceLikeConfig
+
+    m = MaceLike(MaceLikeConfig(channels=C)).to(device)
+    layer = m.layers[1]
+    g = torch.Generator().manual_seed(5)
+    d = lambda t: t.to(device).contiguous()  # noqa: E731
+    A0, A1 = torch.randn(n, C, generator=g), torch.randn(n, 3, C, generator=g)
+    elem = torch.randint(0, 3, (n,), generator=g, dtype=torch.int32)
+    wm0t, wm1t = layer.Wm0.t().contiguous(), layer.Wm1.t().contiguous()
+    P0, P1, B0, B1 = (torch.empty(n, C, device=device), torch.empty(n, 3, C, device=device),
+                      torch.empty(n, C, device=device), torch.empty(n, 3, C, device=device))
+    A0d, A1d, elemd = d(A0), d(A1), d(elem)  # (held: the kernels read them after the call returns)
+    _abi.call("fmd_mace_mix_symcon_f32", A0d.data_ptr(), A1d.data_ptr(), wm0t.data_ptr(), wm1t.data_ptr(),
+              elemd.data_ptr(), layer.Wc.data_ptr(), layer.Wd.data_ptr(), n, C, P0.data_ptr(), P1.data_ptr(),
+              B0.data_ptr(), B1.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    r0 = A0.double() @ layer.Wm0.cpu().double()
+    r1 = A1.double() @ layer.Wm1.cpu().double()
+    rel = lambda x, r: float((x.cpu().double() - r).abs().max() / r.abs().max())  # noqa: E731
+    assert rel(P0, r0) < 1e-5 and rel(P1, r1) < 1e-5
+    B0s, B1s = torch.empty_like(B0), torch.empty_like(B1)
+    _abi.call("fmd_mace_symcon_f32", P0.data_ptr(), P1.data_ptr(), elemd.data_ptr(), layer.Wc.data_ptr(),
+              layer.Wd.data_ptr(), n, C, B0s.data_ptr(), B1s.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert rel(B0, B0s.cpu().double()) < 1e-6 and rel(B1, B1s.cpu().double()) < 1e-6
+    # VJP half
+    for k0, with_vec in ((C, True), (C, False), (16, False)):
+        g0 = torch.randn(n, k0, generator=g)
+        wb0 = torch.randn(C, k0, generator=g) / k0 ** 0.5
+        g1 = torch.randn(n, 3, C, generator=g) if with_vec else None
+        gP0, gP1 = torch.empty(n, C, device=device), torch.empty(n, 3, C, device=device)
+        g0d, wb0d, g1d = d(g0), d(wb0), (d(g1) if with_vec else None)
+        _abi.call("fmd_mace_mix_symcon_bwd_f32", g0d.data_ptr(), k0, wb0d.data_ptr(), _abi.ptr(g1d),
+                  layer.Wo1.data_ptr(), P0.data_ptr(), P1.data_ptr(), elemd.data_ptr(), layer.Wc.data_ptr(),
+                  layer.Wd.data_ptr(), n, C, gP0.data_ptr(), gP1.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        gB0 = d((g0.double() @ wb0.double().t()).float())
+        gB1 = d((g1.double() @ layer.Wo1.cpu().double().t()).float()) if with_vec else None
+        rP0, rP1 = torch.empty_like(gP0), torch.empty_like(gP1)
+        _abi.call("fmd_mace_symcon_bwd_f32", P0.data_ptr(), P1.data_ptr(), elemd.data_ptr(), layer.Wc.data_ptr(),
+                  layer.Wd.data_ptr(), gB0.data_ptr(), _abi.ptr(gB1), n, C, rP0.data_ptr(), rP1.data_ptr(),
+                  torch.cuda.current_stream().cuda_stream)
+        assert rel(gP0, rP0.cpu().double()) < 1e-5 and rel(gP1, rP1.cpu().double()) < 1e-5
+
+
+@pytest.mark.gpu
 def test_morse_gpu_matches_oracle(device):
     from fastmd_amd.engine.energy_derivative import EnergyDerivative
     from fastmd_amd.models.pair_potential import MorsePairAdapter

@@ -261,13 +261,17 @@ def test_gemm_fp32_large_tiles(device):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("b_layout", [0, 1])
-def test_gemm_group_matches_single_gemms_and_fp64(device, b_layout):
+def test_gemm_group_matches_single_gemms_and_fp64(device, b_layout, monkeypatch):
     """fmd_gemm_group_f32: four problems of mixed shapes (ragged M, an empty one, a K split
     [a | a2], accumulate and bias) in one launch, each bitwise equal to the same problem through
-    fmd_gemm_f32's 64 x 64 kernel (same K order) and within fp32 of float64."""
+    fmd_gemm_f32's 64 x 64 kernel (same K order) and within fp32 of float64 (groups this small
+    otherwise take the K-split form: switched off here)."""
     import torch
 
+    from fastmd_amd.ops import wide_gemm
     from fastmd_amd.ops.wide_gemm import gemm, gemm_group
+
+    monkeypatch.setattr(wide_gemm, "GROUP_KS_MAX_TILES", 0)
 
     g = torch.Generator().manual_seed(11)
 
@@ -313,6 +317,86 @@ def test_gemm_group_matches_single_gemms_and_fp64(device, b_layout):
     single = gemm(torch.cat([a, a2], 1).to(device), w.to(device), b_layout=b_layout)
     assert torch.equal(out, single)
     assert oops.relative(out.cpu().numpy(), ref_of(torch.cat([a, a2], 1), w).numpy()) < 1e-5
+
+
+@pytest.mark.gpu
+def test_gemm_group_ks_form(device):
+    """fmd_gemm_group_ks_f32 (small groups, B [N, K]: 16 x 16 tiles, K shared by four waves):
+    ragged M and N, K = 4, 16, 136 (a partial last slice), 1 024 and a split [a | a2], accumulate,
+    bias and the SiLU epilogue, each within fp32 of float64; every problem's result the same bits
+    alone as in the group and on a second call; gemm_group picks it below GROUP_KS_MAX_TILES
+    64 x 64 tiles and gemm_splitk for small products."""
+    import torch
+
+    from fastmd_amd.ops import wide_gemm
+    from fastmd_amd.ops.wide_gemm import gemm_group, gemm_splitk
+
+    g = torch.Generator().manual_seed(31)
+    d = lambda t: t.to(device)  # noqa: E731
+    shapes = [(135, 128, 512), (405, 136, 128), (1, 4, 16), (17, 16, 130)]
+    mats = []
+    for (m, k, n) in shapes:
+        mats.append((torch.randn(m, k, generator=g), torch.randn(n, k, generator=g) / k ** 0.5))
+    c3 = torch.randn(17, 130, generator=g)
+    bias = torch.randn(128, generator=g)
+
+    def problems():
+        ps = [{"a": d(a), "b": d(w), "out": torch.empty(a.shape[0], w.shape[0], device=device)} for a, w in mats]
+        ps[1]["bias"] = d(bias)
+        ps[3]["out"] = d(c3)
+        ps[3]["accumulate"] = True
+        return ps
+
+    ref = [a.double() @ w.double().t() for a, w in mats]
+    ref[1] = ref[1] + bias.double()
+    ref[3] = ref[3] + c3.double()
+    runs = []
+    for _ in range(2):
+        ps = problems()
+        gemm_group(ps, b_layout=0)
+        runs.append([p["out"].clone() for p in ps])
+    for out, r in zip(runs[0], ref):
+        assert oops.relative(out.cpu().numpy(), r.numpy()) < 1e-5
+    for x, y in zip(runs[0], runs[1]):
+        assert torch.equal(x, y)
+    for i, p in enumerate(problems()):
+        gemm_group([p], b_layout=0)
+        assert torch.equal(p["out"], runs[0][i])
+    # the K-split form, not the 64 x 64 tiles: the same problems with the K-split form switched off
+    # give other bits (a different K order)
+    saved = wide_gemm.GROUP_KS_MAX_TILES
+    try:
+        wide_gemm.GROUP_KS_MAX_TILES = 0
+        ps = problems()
+        gemm_group(ps, b_layout=0)
+        assert not torch.equal(ps[0]["out"], runs[0][0])
+    finally:
+        wide_gemm.GROUP_KS_MAX_TILES = saved
+    # SiLU epilogue
+    a, w = mats[0]
+    out = torch.empty(135, 512, device=device)
+    gemm_group([{"a": d(a), "b": d(w), "out": out}], b_layout=0, epilogue="silu")
+    assert oops.relative(out.cpu().numpy(), torch.nn.functional.silu(ref[0]).numpy()) < 1e-5
+    # [a | a2] with K = 512 + 512 through gemm_splitk (small: the K-split group), accumulate
+    a1, a2 = torch.randn(135, 512, generator=g), torch.randn(135, 512, generator=g)
+    w = torch.randn(128, 1024, generator=g) / 32.0
+    c0 = torch.randn(135, 128, generator=g)
+    outs = []
+    for _ in range(2):
+        out = d(c0)
+        gemm_splitk(d(a1), d(w), b_layout=0, out=out, a2=d(a2), accumulate=True)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+    r = torch.cat([a1, a2], 1).double() @ w.double().t() + c0.double()
+    assert oops.relative(outs[0].cpu().numpy(), r.numpy()) < 1e-5
+    # the split operand gives the concatenated operand's bits (the same slices in the same order),
+    # and accumulating adds C to the same sum
+    out = torch.empty(135, 128, device=device)
+    gemm_group([{"a": d(a1), "a2": d(a2), "b": d(w), "out": out}], b_layout=0)
+    out_cat = torch.empty(135, 128, device=device)
+    gemm_group([{"a": d(torch.cat([a1, a2], 1)), "b": d(w), "out": out_cat}], b_layout=0)
+    assert torch.equal(out, out_cat)
+    assert torch.equal(out + d(c0), outs[0])
 
 
 @pytest.mark.gpu
