@@ -84,6 +84,33 @@ __device__ __forceinline__ float wave_sum<float>(float v) {
   return v;
 }
 
+// double: the same six lane moves on both 32-bit halves (the same fixed order; no LDS crossbar)
+__device__ __forceinline__ double f64_from(uint32_t lo, uint32_t hi) { return __hiloint2double((int)hi, (int)lo); }
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_read_f64(double v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, 0xf, 0xf, false);
+  return __hiloint2double(hi, lo);
+}
+
+template <>
+__device__ __forceinline__ double wave_sum<double>(double v) {
+  const uint32_t l0 = (uint32_t)__double2loint(v), h0 = (uint32_t)__double2hiint(v);
+  const auto a = __builtin_amdgcn_permlane32_swap(l0, l0, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(h0, h0, false, false);
+  v = f64_from(a[0], b[0]) + f64_from(a[1], b[1]);
+  const uint32_t l1 = (uint32_t)__double2loint(v), h1 = (uint32_t)__double2hiint(v);
+  const auto c = __builtin_amdgcn_permlane16_swap(l1, l1, false, false);
+  const auto d = __builtin_amdgcn_permlane16_swap(h1, h1, false, false);
+  v = f64_from(c[0], d[0]) + f64_from(c[1], d[1]);
+  v = v + dpp_read_f64<kDppRowRor8>(v);
+  v = v + dpp_read_f64<kDppHalfMirror>(v);
+  v = v + dpp_read_f64<kDppQuadXor1>(v);
+  v = v + dpp_read_f64<kDppQuadXor2>(v);
+  return v;
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_max(T v) {
 #pragma unroll

@@ -175,10 +175,11 @@ __device__ double ke2_of(Momenta<KPT>& mom, double* red) {
   return block_sum(s, red);
 }
 
-// ASE integrate_nhc over half a time step (every thread advances its copy of the chain).
+// ASE integrate_nhc over half a time step (every thread advances its copy of the chain), from
+// ke2 = sum(p*p/m) of the momenta on entry; returns that sum of the momenta on return (the
+// recomputation after the last scaling: a pre half that follows directly starts from it).
 template <int KPT>
-__device__ void nhc_half(Momenta<KPT>& mom, Chain& c, const double* consts, int tloop, double* red) {
-  double ke2 = ke2_of(mom, red);
+__device__ double nhc_half(Momenta<KPT>& mom, Chain& c, const double* consts, int tloop, double* red, double ke2) {
   for (int tl = 0; tl < tloop; ++tl) {
     for (int k = 0; k < 3; ++k) {
       const double scale = chain_before_scale(c, ke2, consts, k);
@@ -191,6 +192,7 @@ __device__ void nhc_half(Momenta<KPT>& mom, Chain& c, const double* consts, int 
       chain_after_scale(c, ke2, consts, k);
     }
   }
+  return ke2;
 }
 
 __device__ __forceinline__ double kick_of(double dt2, double f, int f32_kick) {
@@ -207,7 +209,7 @@ __global__ void __launch_bounds__(kThreads) nhc_pre_kernel(double* q, double* p,
   load_chain(c, M, eta, pe, consts);
   Momenta<KPT> mom;
   mom.load(p, masses, n);
-  nhc_half(mom, c, consts, tloop, red);
+  nhc_half(mom, c, consts, tloop, red, ke2_of(mom, red));
   const double dt = consts[0], dt2 = consts[1];
   mom.for_each([&](int64_t a, double (&pv)[3]) {
     const double m = masses[a];
@@ -241,7 +243,7 @@ __global__ void __launch_bounds__(kThreads) nhc_post_kernel(double* p, const voi
       f_cache[3 * a + d] = fv;
     }
   });
-  nhc_half(mom, c, consts, tloop, red);
+  nhc_half(mom, c, consts, tloop, red, ke2_of(mom, red));
   mom.store();
   if (threadIdx.x == 0) store_chain(c, eta, pe);
   if (threadIdx.x == 0 && e_kind != 0)
@@ -274,10 +276,10 @@ __global__ void __launch_bounds__(kThreads) nhc_post_pre_kernel(double* q, doubl
       f_cache[3 * a + d] = fv;
     }
   });
-  nhc_half(mom, c, consts, tloop, red);
+  const double ke2 = nhc_half(mom, c, consts, tloop, red, ke2_of(mom, red));
   if (threadIdx.x == 0 && e_kind != 0)
     e_out[0] = e_kind == 2 ? static_cast<const double*>(e_in)[0] : (double)static_cast<const float*>(e_in)[0];
-  nhc_half(mom, c, consts, tloop, red);
+  nhc_half(mom, c, consts, tloop, red, ke2);  // the same momenta: the post half's last sum
   mom.for_each([&](int64_t a, double (&pv)[3]) {
     const double m = masses[a];
 #pragma unroll

@@ -25,6 +25,9 @@ namespace {
 
 constexpr int kSmallThreads = 1024;   // fused single-workgroup build
 constexpr int kSmallMaxAtoms = 1024;  // LDS-resident wrapped coordinates up to this many atoms
+constexpr int kSmallBatch = 4;        // atoms per wave whose candidate loads are issued together
+constexpr int kSmallMaxEdges = 8192;  // rows whose reverse search runs on LDS copies of their keys
+constexpr int kImageBias = 512;       // packed image fields: component + 512 in 10 bits
 constexpr int kBlock = 256;           // multi-block kernels: 4 waves, one atom per wave
 
 struct Mat3 {
@@ -337,6 +340,7 @@ struct BuildArgs {
   int32_t* isolated;
   float line2;           // line-graph (bond) cutoff squared, float32
   uint8_t* short_flags;  // [e_cap]: real row with d2 < line2 (null: not written)
+  int32_t* reverse;      // [e_cap]: the reverse row of every real row, -1 past them (null: not formed)
 };
 
 // The cell and inverse cell of atom i (its system's, in a union of systems).
@@ -406,13 +410,12 @@ __device__ __forceinline__ void write_row(const BuildArgs& a, int64_t row, int32
 
 // Validity of candidate slot s of atom i, given the atom's wrapped position and wrap delta and
 // a functor giving (wrapped_j, wrap_delta_j).
+// The same test from the slot's candidate entry (j_raw) and lattice shift (sh), loaded beforehand.
 template <typename NeighborFn>
-__device__ __forceinline__ bool slot_edge(const BuildArgs& a, const Mat3& cm, int64_t i, int s, float xi, float yi,
-                                          float zi, const int wdi[3], NeighborFn nbr_state, int32_t& j, int img[3],
-                                          float& d2) {
-  j = a.nbr[i * a.bmax + s];
-  j = j < (int32_t)a.n - 1 ? j : (int32_t)a.n - 1;
-  const int32_t* sh = a.shifts + (i * a.bmax + s) * 3;
+__device__ __forceinline__ bool slot_edge_of(const BuildArgs& a, const Mat3& cm, int32_t j_raw, const int32_t sh[3],
+                                             float xi, float yi, float zi, const int wdi[3], NeighborFn nbr_state,
+                                             int32_t& j, int img[3], float& d2) {
+  j = j_raw < (int32_t)a.n - 1 ? j_raw : (int32_t)a.n - 1;
   float xj, yj, zj;
   int wdj[3];
   nbr_state(j, xj, yj, zj, wdj);
@@ -420,6 +423,77 @@ __device__ __forceinline__ bool slot_edge(const BuildArgs& a, const Mat3& cm, in
   for (int k = 0; k < 3; ++k) img[k] = sh[k] + wdj[k] - wdi[k];
   d2 = pair_d2(xi, yi, zi, xj, yj, zj, (float)img[0], (float)img[1], (float)img[2], cm);
   return d2 < a.rc2;
+}
+
+template <typename NeighborFn>
+__device__ __forceinline__ bool slot_edge(const BuildArgs& a, const Mat3& cm, int64_t i, int s, float xi, float yi,
+                                          float zi, const int wdi[3], NeighborFn nbr_state, int32_t& j, int img[3],
+                                          float& d2) {
+  const int32_t* sh = a.shifts + (i * a.bmax + s) * 3;
+  const int32_t shv[3] = {sh[0], sh[1], sh[2]};
+  return slot_edge_of(a, cm, a.nbr[i * a.bmax + s], shv, xi, yi, zi, wdi, nbr_state, j, img, d2);
+}
+
+// Reverse rows of a build (the search of nl_reverse_kernel) over rows start, start + step, ...:
+// row e (i -> j, image) finds the first row of j's block [off[j], off[j + 1]) at or after
+// (i, -image) in (neighbor, image) order and takes it when it is that pair, else -1; rows past
+// the real ones get -1. Four rows per thread at a time, so that their loads overlap.
+template <typename OffFn>
+__device__ __forceinline__ void reverse_rows(const BuildArgs& a, int64_t ec, OffFn off_of, int64_t start,
+                                             int64_t step) {
+  constexpr int R = 4;
+  for (int64_t e0 = start; e0 < a.e_cap; e0 += R * step) {
+    int64_t e[R], lo[R], hi[R], end[R];
+    int32_t c[R];
+    int ix[R], iy[R], iz[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      e[k] = e0 + k * step;
+      lo[k] = hi[k] = end[k] = 0;
+      c[k] = 0;
+      ix[k] = iy[k] = iz[k] = 0;
+      if (e[k] < ec) {
+        c[k] = a.center[e[k]];
+        const int32_t j = a.neighbor[e[k]];
+        ix[k] = -a.images[3 * e[k]];
+        iy[k] = -a.images[3 * e[k] + 1];
+        iz[k] = -a.images[3 * e[k] + 2];
+        const int64_t o1 = off_of(j + 1);
+        end[k] = o1 < ec ? o1 : ec;
+        hi[k] = end[k];
+        const int64_t o0 = off_of(j);
+        lo[k] = o0 < hi[k] ? o0 : hi[k];
+      }
+    }
+    bool any = true;
+    while (any) {
+      any = false;
+#pragma unroll
+      for (int k = 0; k < R; ++k) {
+        if (lo[k] < hi[k]) {
+          const int64_t mid = (lo[k] + hi[k]) >> 1;
+          const int32_t mj = a.neighbor[mid];
+          const int mx = a.images[3 * mid], my = a.images[3 * mid + 1], mz = a.images[3 * mid + 2];
+          const bool less = (mj < c[k]) || (mj == c[k] && (mx < ix[k] || (mx == ix[k] && (my < iy[k] ||
+                                                                                       (my == iy[k] && mz < iz[k])))));
+          if (less)
+            lo[k] = mid + 1;
+          else
+            hi[k] = mid;
+          any = true;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      if (e[k] >= a.e_cap) continue;
+      int32_t r = -1;
+      if (e[k] < ec && lo[k] < end[k] && a.neighbor[lo[k]] == c[k] && a.images[3 * lo[k]] == ix[k] &&
+          a.images[3 * lo[k] + 1] == iy[k] && a.images[3 * lo[k] + 2] == iz[k])
+        r = (int32_t)lo[k];
+      a.reverse[e[k]] = r;
+    }
+  }
 }
 
 __device__ __forceinline__ void pad_rows(const BuildArgs& a, int64_t total, int64_t start, int64_t step) {
@@ -454,7 +528,14 @@ __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs
   __shared__ float s_red[kSmallThreads / FMD_WAVE];
   __shared__ int32_t s_iso[kSmallThreads / FMD_WAVE];
   __shared__ int32_t s_scan[kSmallThreads];
+  // the keys of the real rows for the reverse search (row < kSmallMaxEdges): centre, neighbour and
+  // the image packed as three 10-bit fields of component + 512 (field order = lexicographic order)
+  __shared__ int16_t s_rc[kSmallMaxEdges];
+  __shared__ int32_t s_rn[kSmallMaxEdges];
+  __shared__ uint32_t s_ri[kSmallMaxEdges];
+  __shared__ int s_wide_image;  // some real row has an image component outside [-511, 511]
   const int t = threadIdx.x, T = blockDim.x;
+  if (t == 0) s_wide_image = 0;
   const int lane = t & (FMD_WAVE - 1), wave = t / FMD_WAVE, nwaves = T / FMD_WAVE;
   const int n = (int)a.n;
 
@@ -492,31 +573,64 @@ __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs
     wdj[2] = s_wd[3 * j + 2];
   };
 
+  // The first 64 candidate slots of kSmallBatch atoms of a wave (atoms i0 + u nwaves) with their
+  // loads issued together: one memory round trip per batch instead of one per atom. Slots past
+  // the candidate count are loaded (in bounds: the matrix has bmax slots per atom) and ignored.
+  struct SlotBatch {
+    int cnt[kSmallBatch];
+    int32_t j[kSmallBatch];
+    int32_t sh[kSmallBatch][3];
+  };
+  auto load_batch = [&](int i0, SlotBatch& b) {
+#pragma unroll
+    for (int u = 0; u < kSmallBatch; ++u) {
+      const int i = i0 + u * nwaves;
+      b.cnt[u] = 0;
+      b.j[u] = 0;
+      b.sh[u][0] = b.sh[u][1] = b.sh[u][2] = 0;
+      if (i < n) {
+        const int c = a.num[i];
+        b.cnt[u] = c < a.bmax ? c : a.bmax;
+        if (lane < a.bmax) {
+          const int64_t q = (int64_t)i * a.bmax + lane;
+          b.j[u] = a.nbr[q];
+          b.sh[u][0] = a.shifts[3 * q];
+          b.sh[u][1] = a.shifts[3 * q + 1];
+          b.sh[u][2] = a.shifts[3 * q + 2];
+        }
+      }
+    }
+  };
+
   // (2) counts, one wave per atom
   int iso = 0;
-  for (int i = wave; i < n; i += nwaves) {
-    const float xi = s_pos[3 * i], yi = s_pos[3 * i + 1], zi = s_pos[3 * i + 2];
-    const int wdi[3] = {s_wd[3 * i], s_wd[3 * i + 1], s_wd[3 * i + 2]};
-    Mat3 inv, cm;
-    atom_frame(a, i, inv, cm);
-    int cnt = a.num[i];
-    cnt = cnt < a.bmax ? cnt : a.bmax;
-    int total = 0;
-    for (int base = 0; base < cnt; base += FMD_WAVE) {
-      const int s = base + lane;
-      bool e = false;
-      if (s < cnt) {
-        int32_t j;
-        int img[3];
-        float d2;
-        e = slot_edge(a, cm, i, s, xi, yi, zi, wdi, nbr_state, j, img, d2);
+  for (int i0 = wave; i0 < n; i0 += nwaves * kSmallBatch) {
+    SlotBatch b;
+    load_batch(i0, b);
+#pragma unroll
+    for (int u = 0; u < kSmallBatch; ++u) {
+      const int i = i0 + u * nwaves;
+      if (i >= n) break;
+      const float xi = s_pos[3 * i], yi = s_pos[3 * i + 1], zi = s_pos[3 * i + 2];
+      const int wdi[3] = {s_wd[3 * i], s_wd[3 * i + 1], s_wd[3 * i + 2]};
+      Mat3 inv, cm;
+      atom_frame(a, i, inv, cm);
+      const int cnt = b.cnt[u];
+      int32_t j;
+      int img[3];
+      float d2;
+      bool e = lane < cnt && slot_edge_of(a, cm, b.j[u], b.sh[u], xi, yi, zi, wdi, nbr_state, j, img, d2);
+      int total = __popcll(__ballot(e));
+      for (int base = FMD_WAVE; base < cnt; base += FMD_WAVE) {
+        const int s = base + lane;
+        e = s < cnt && slot_edge(a, cm, i, s, xi, yi, zi, wdi, nbr_state, j, img, d2);
+        total += __popcll(__ballot(e));
       }
-      total += __popcll(__ballot(e));
-    }
-    if (lane == 0) {
-      s_cnt[i] = total;
-      a.edge_counts[i] = total;
-      iso += (total == 0);
+      if (lane == 0) {
+        s_cnt[i] = total;
+        a.edge_counts[i] = total;
+        iso += (total == 0);
+      }
     }
   }
   if (lane == 0) s_iso[wave] = iso;
@@ -559,29 +673,86 @@ __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs
   const int64_t total = s_cnt[kSmallMaxAtoms];
 
   // (4) materialize in candidate (= canonical) order
-  for (int i = wave; i < n; i += nwaves) {
-    const float xi = s_pos[3 * i], yi = s_pos[3 * i + 1], zi = s_pos[3 * i + 2];
-    const int wdi[3] = {s_wd[3 * i], s_wd[3 * i + 1], s_wd[3 * i + 2]};
-    Mat3 inv, cm;
-    atom_frame(a, i, inv, cm);
-    int cnt = a.num[i];
-    cnt = cnt < a.bmax ? cnt : a.bmax;
-    int64_t row0 = s_cnt[i];
-    for (int base = 0; base < cnt; base += FMD_WAVE) {
-      const int s = base + lane;
-      bool e = false;
-      int32_t j = 0;
-      int img[3] = {0, 0, 0};
-      float d2 = 0.f;
-      if (s < cnt) e = slot_edge(a, cm, i, s, xi, yi, zi, wdi, nbr_state, j, img, d2);
-      const uint64_t m = __ballot(e);
-      const int64_t row = row0 + lane_prefix(m);
-      if (e && row < a.e_cap) write_row(a, row, (int32_t)i, j, img[0], img[1], img[2], d2, true);
-      row0 += __popcll(m);
+  for (int i0 = wave; i0 < n; i0 += nwaves * kSmallBatch) {
+    SlotBatch b;
+    load_batch(i0, b);
+#pragma unroll
+    for (int u = 0; u < kSmallBatch; ++u) {
+      const int i = i0 + u * nwaves;
+      if (i >= n) break;
+      const float xi = s_pos[3 * i], yi = s_pos[3 * i + 1], zi = s_pos[3 * i + 2];
+      const int wdi[3] = {s_wd[3 * i], s_wd[3 * i + 1], s_wd[3 * i + 2]};
+      Mat3 inv, cm;
+      atom_frame(a, i, inv, cm);
+      const int cnt = b.cnt[u];
+      int64_t row0 = s_cnt[i];
+      for (int base = 0; base < cnt; base += FMD_WAVE) {
+        const int s = base + lane;
+        bool e = false;
+        int32_t j = 0;
+        int img[3] = {0, 0, 0};
+        float d2 = 0.f;
+        if (s < cnt) {
+          e = base == 0 ? slot_edge_of(a, cm, b.j[u], b.sh[u], xi, yi, zi, wdi, nbr_state, j, img, d2)
+                        : slot_edge(a, cm, i, s, xi, yi, zi, wdi, nbr_state, j, img, d2);
+        }
+        const uint64_t m = __ballot(e);
+        const int64_t row = row0 + lane_prefix(m);
+        if (e && row < a.e_cap) {
+          write_row(a, row, (int32_t)i, j, img[0], img[1], img[2], d2, true);
+          if (row < kSmallMaxEdges) {
+            const bool narrow = img[0] > -kImageBias && img[0] < kImageBias && img[1] > -kImageBias &&
+                                img[1] < kImageBias && img[2] > -kImageBias && img[2] < kImageBias;
+            if (!narrow) s_wide_image = 1;
+            s_rc[row] = (int16_t)i;
+            s_rn[row] = j;
+            s_ri[row] = ((uint32_t)(img[0] + kImageBias) << 20) | ((uint32_t)(img[1] + kImageBias) << 10) |
+                        (uint32_t)(img[2] + kImageBias);
+          }
+        }
+        row0 += __popcll(m);
+      }
     }
   }
   // (5) padding rows
   pad_rows(a, total, t, T);
+  // (6) reverse rows: the search of nl_reverse_kernel on the LDS keys, or (more rows than the
+  // LDS holds, or a wide image) on the rows this workgroup has written (visible after the barrier)
+  if (a.reverse) {
+    __syncthreads();
+    const int64_t ec = total < a.e_cap ? total : a.e_cap;
+    auto off_of = [&](int64_t k) -> int64_t { return k < n ? s_cnt[k] : total; };
+    if (ec > kSmallMaxEdges || s_wide_image) {
+      reverse_rows(a, ec, off_of, t, T);
+      return;
+    }
+    constexpr uint32_t kField = 2 * kImageBias, kMask = kField - 1;
+    for (int64_t e = t; e < a.e_cap; e += T) {
+      int32_t r = -1;
+      if (e < ec) {
+        const int32_t c = s_rc[e], j = s_rn[e];
+        const uint32_t p = s_ri[e];
+        // (c, -image): each field f = component + 512 in [1, 1023] becomes 1024 - f
+        const uint32_t want = ((kField - (p >> 20)) << 20) | ((kField - ((p >> 10) & kMask)) << 10) |
+                              (kField - (p & kMask));
+        const int64_t o1 = off_of(j + 1);
+        const int64_t end = o1 < ec ? o1 : ec;
+        int64_t hi = end;
+        const int64_t o0 = off_of(j);
+        int64_t lo = o0 < hi ? o0 : hi;
+        while (lo < hi) {
+          const int64_t mid = (lo + hi) >> 1;
+          const int32_t mj = s_rn[mid];
+          if (mj < c || (mj == c && s_ri[mid] < want))
+            lo = mid + 1;
+          else
+            hi = mid;
+        }
+        if (lo < end && s_rn[lo] == c && s_ri[lo] == want) r = (int32_t)lo;
+      }
+      a.reverse[e] = r;
+    }
+  }
 }
 
 // Multi-block path, kernel 1: prologue of atom i (own wrap) and its edge count; the
@@ -921,6 +1092,11 @@ int launch_build(const BuildArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(nl_materialize_kernel, dim3((unsigned)(atom_blocks + pad_blocks)), dim3(kBlock), 0, stream, a,
                      atom_blocks);
   FMD_CHECK_LAUNCH();
+  if (a.reverse) {
+    hipLaunchKernelGGL(nl_reverse_kernel, dim3((unsigned)fmd_cdiv(a.e_cap, 256)), dim3(256), 0, stream, a.center,
+                       a.neighbor, a.images, a.edge_offsets, a.n, a.e_cap, a.reverse);
+    FMD_CHECK_LAUNCH();
+  }
   return FMD_OK;
 }
 
@@ -1021,12 +1197,13 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor, int32_t* images,
                  float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
                  uint8_t* candidate_valid, uint8_t* overflow, int32_t* isolated, float line2, uint8_t* short_flags,
-                 hipStream_t stream) {
+                 int32_t* edge_reverse, hipStream_t stream) {
   FMD_REQUIRE(work && reinterpret_cast<uintptr_t>(work) % 16 == 0);  // the scan reads it 16 bytes at a time
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
               reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, minimum_image, pad_ix, pad_iy, pad_iz,
               n_dummy, system_of, pad_images, e_cap, work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
-              edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags};
+              edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags,
+              edge_reverse};
   return launch_build(a, stream);
 }
 
@@ -1048,7 +1225,8 @@ int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float*
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
               reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, minimum_image, pad_ix, pad_iy, pad_iz,
               n_dummy, system_of, pad_images, e_cap, work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
-              edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags};
+              edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags,
+              nullptr};
   return launch_build(a, stream);
 }
 

@@ -382,10 +382,8 @@ class FixedCapacityGraphBuilder:
                   self.neighbor.data_ptr(), self.images.data_ptr(), self.distances.data_ptr(),
                   self.batch.edge_index.data_ptr(), self.batch.edge_image.data_ptr(),
                   self._max_displacement.data_ptr(), self._candidate_valid.data_ptr(), self._overflow.data_ptr(),
-                  self._isolated_atom_count.data_ptr(), self._line2, _abi.ptr(self.short_flags), self._stream())
-        _abi.call("fmd_nl_reverse", self.center.data_ptr(), self.neighbor.data_ptr(), self.images.data_ptr(),
-                  self.edge_offsets.data_ptr(), self.n_real, self.e_capacity, self.edge_reverse.data_ptr(),
-                  self._stream())
+                  self._isolated_atom_count.data_ptr(), self._line2, _abi.ptr(self.short_flags),
+                  self.edge_reverse.data_ptr(), self._stream())
         if not self.edges_only:
             # pairs, short-bond lists and triplets; the overflow flag becomes the line-graph rule
             # (edges >= e_capacity | triplets > t_capacity | invalid pairs | invalid candidates)

@@ -108,7 +108,9 @@ int fmd_nl_wrap(const void* positions, int32_t pos_is_f64, const float* inv_cell
  * edge_image [e_cap,3] f32 (published, may be null), status: max_displacement f32[1],
  * candidate_valid u8[1], overflow u8[1], isolated i32[1]; short_flags [e_cap] u8 (may be null:
  * a line-graph build's short-bond flag, real rows with the same d2 < line2, line2 the float32
- * square of the bond cutoff, fixed_capacity_builder.py:258-260; padding rows 0). */
+ * square of the bond cutoff, fixed_capacity_builder.py:258-260; padding rows 0); edge_reverse
+ * [e_cap] i32 (may be null: not formed) the reverse rows of fmd_nl_reverse on this build's rows,
+ * formed in the same launch for small systems (one workgroup), else by one more launch. */
 int64_t fmd_nl_build_work_size(int64_t n_atoms);
 int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cell, const float* cell,
                  int64_t n_atoms, const int32_t* neighbor_matrix, const int32_t* neighbor_shifts,
@@ -120,12 +122,14 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor,
                  int32_t* images, float* distances, int32_t* edge_index, float* edge_image,
                  float* max_displacement, uint8_t* candidate_valid, uint8_t* overflow,
-                 int32_t* isolated, float line2, uint8_t* short_flags, hipStream_t stream);
+                 int32_t* isolated, float line2, uint8_t* short_flags, int32_t* edge_reverse,
+                 hipStream_t stream);
 
 /* Allocation-free variant of fmd_nl_build. It has no counterpart in the reference: it is for
  * callers that cannot call hipMalloc (code under HIP graph capture, tight serving loops,
  * harnesses that forbid allocation). Same arguments, kernels and results as fmd_nl_build,
- * without `work`: the per-block partials go to a static device array of
+ * without `work` (and without edge_reverse: fmd_nl_reverse forms it): the per-block partials go
+ * to a static device array of
  * FMD_NL_BUILD_NOALLOC_SCRATCH int64 words (3 MiB) that each GPU the library runs on holds until
  * the process ends. n_atoms above FMD_NL_BUILD_NOALLOC_MAX_ATOMS returns FMD_ETOOLARGE with
  * nothing launched. Every call on one GPU shares that GPU's array, which keeps the last call's

@@ -136,7 +136,7 @@ def _builder(s, bond_cutoff, device, u_cap=None, t_cap=None):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("n_cells,bond_cutoff", [(3, 3.5), (3, 3.0), ((6, 6, 6), 3.5), ((6, 6, 6), 3.0),
-                                                 (10, 3.5)])
+                                                 (10, 3.5), (10, 3.0)])
 def test_threebody_gpu_matches_oracle(device, n_cells, bond_cutoff):
     """Energies within 1e-5 eV/atom and forces within 1e-4 eV/A of the FP64 oracle through the
     line-graph builder (padding pairs and triplets present); bitwise reproducible; the autograd
