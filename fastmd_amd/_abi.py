@@ -105,9 +105,11 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_mace_energy_f32": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _p, _p, _f32, _f32, _i64, _p, _p]),
     "fmd_mace_energy_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _f32, _i64, _p, _p, _p]),
     "fmd_mace_energy_grad_f32": (ctypes.c_int, [_p, _p, _p, _p, _i32, _i32, _p, _p, _f32, _f32, _i64, _p, _p, _p,
-                                                _p]),
+                                                _p, _p, _p]),
     "fmd_embed_f32": (ctypes.c_int, [_p, _p, _i64, _i32, _p, _p]),
     "fmd_embed_rows_f32": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p]),
+    "fmd_edge_geometry_embed_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _i64, _f32, _i32, _p, _p, _p, _p, _i64,
+                                                   _i32, _p, _p, _p, _p]),
     "fmd_morse_f32": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _f32, _f32, _f32, _f32, _f32, _p, _p, _p]),
     "fmd_morse_bwd_f32": (ctypes.c_int, [_p, _p, _p, _p, _p, _i64, _p, _p]),
     "fmd_edge_virial_work_size": (_i64, []),

@@ -35,12 +35,31 @@ __device__ __forceinline__ float sigmoid(float x) { return __builtin_amdgcn_rcpf
 // polynomial envelope 1 - 21 x^5 + 35 x^6 - 15 x^7 (x = r / rc < 1, else 0).
 // vec = (pos[j] + image @ cell) - pos[c], image @ cell formed row by row.
 // ------------------------------------------------------------------------------------------
-__global__ void edge_geometry_kernel(const float* pos, const float* cell, const int32_t* system_of,
-                                     const int32_t* edge_index, const float* edge_image, const int64_t* n_edges,
-                                     int64_t e_cap, float rc, int nb, float* geo, float* ef, float* def) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= e_cap) return;
-  const int64_t rows = real_rows(n_edges, e_cap);
+struct GeoArgs {
+  const float* pos;
+  const float* cell;
+  const int32_t* system_of;
+  const int32_t* edge_index;
+  const float* edge_image;
+  const int64_t* n_edges;
+  int64_t e_cap;
+  float rc;
+  int nb;
+  float* geo;
+  float* ef;
+  float* def;
+};
+
+__device__ __forceinline__ void edge_geometry_row(const GeoArgs& a, int64_t e) {
+  const float* pos = a.pos;
+  const float* cell = a.cell;
+  const int32_t *system_of = a.system_of, *edge_index = a.edge_index;
+  const float* edge_image = a.edge_image;
+  const int64_t e_cap = a.e_cap;
+  const float rc = a.rc;
+  const int nb = a.nb;
+  float *geo = a.geo, *ef = a.ef, *def = a.def;
+  const int64_t rows = real_rows(a.n_edges, e_cap);
   float* g = geo + 8 * e;
   if (e >= rows) {
 #pragma unroll
@@ -90,6 +109,11 @@ __global__ void edge_geometry_kernel(const float* pos, const float* cell, const 
     ef[e * nb + (n - 1)] = b * fc;
     def[e * nb + (n - 1)] = db * fc + b * dfc;
   }
+}
+
+__global__ void edge_geometry_kernel(const GeoArgs a) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < a.e_cap) edge_geometry_row(a, e);
 }
 
 // g_vec[e] = g_r u + (g_u - (g_u . u) u) / r with g_r = sum_n g_ef[e,n] def[e,n] (over up to two
@@ -972,25 +996,63 @@ __device__ __forceinline__ float readout_gy(float g, float w, float v) {
 // The forward with the VJP for dE/dE_i = 1 (the explicit force path: no seed to wait for): E_i as
 // energy_kernel, and in the same wave gha_i = scale wr1, gy_i = scale wr2b silu'(y_i) (the values
 // energy_bwd_kernel writes for a null gE), one launch instead of two.
+__global__ void zero_f64_kernel(double* x) { x[0] = 0.0; }
+
+// The float64 total of x[0 .. n) in fmd_sum_f64's fixed order (1 024 strided partials in index
+// order, then a pairwise tree over them), formed by the threads of one block.
+__device__ void sum_f64_order(const float* x, int64_t n, double* out, double* part) {
+  constexpr int kParts = 1024;
+  for (int v = threadIdx.x; v < kParts; v += blockDim.x) {
+    double s = 0.0;
+    for (int64_t k = v; k < n; k += kParts) s = s + (double)x[k];
+    part[v] = s;
+  }
+  __syncthreads();
+  for (int width = kParts / 2; width > 0; width >>= 1) {
+    for (int v = threadIdx.x; v < width; v += blockDim.x) part[v] = part[v] + part[v + width];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[0] = part[0];
+}
+
+// With total (and its completion counter): every block publishes its energies with a
+// device-scope fence before it counts itself; the last block to count fences again, forms the
+// fixed-order float64 total of all n energies and sets the counter back to zero for the next
+// launch (no separate summing launch). A device-scope fence writes back the L2, so this is for
+// small launches (a few hundred blocks); large ones sum in a launch of their own.
 __global__ void energy_grad_kernel(const float* ha, const float* wr1, const float* y, const float* wr2b, int C, int H,
                                    const int32_t* elem, const float* e0, float scale, float shift, int64_t n,
-                                   float* energy, float* gha, float* gy) {
+                                   float* energy, float* gha, float* gy, double* total, unsigned int* counter) {
   const int lane = threadIdx.x & 63;
   const int64_t i = (int64_t)blockIdx.x * kWaves + threadIdx.x / 64;
-  if (i >= n) return;
-  float s = 0.f;
-  for (int c = lane; c < C; c += 64) {
-    const float w = wr1[c];
-    s += ha[i * C + c] * w;
-    gha[i * C + c] = scale * w;
+  if (i < n) {
+    float s = 0.f;
+    for (int c = lane; c < C; c += 64) {
+      const float w = wr1[c];
+      s += ha[i * C + c] * w;
+      gha[i * C + c] = scale * w;
+    }
+    for (int k = lane; k < H; k += 64) {
+      const float v = y[i * H + k], w = wr2b[k];
+      s += v * sigmoid(v) * w;
+      gy[i * H + k] = readout_gy(scale, w, v);
+    }
+    s = wave_sum(s);
+    if (lane == 0) energy[i] = e0[elem[i]] + scale * s + shift;
   }
-  for (int k = lane; k < H; k += 64) {
-    const float v = y[i * H + k], w = wr2b[k];
-    s += v * sigmoid(v) * w;
-    gy[i * H + k] = readout_gy(scale, w, v);
+  if (!total) return;
+  __shared__ int last;
+  __shared__ double part[1024];
+  __syncthreads();  // the block's energies are written; thread 0's device-scope fence publishes them
+  if (threadIdx.x == 0) {
+    __threadfence();
+    last = atomicAdd(counter, 1u) == gridDim.x - 1 ? 1 : 0;
   }
-  s = wave_sum(s);
-  if (lane == 0) energy[i] = e0[elem[i]] + scale * s + shift;
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  sum_f64_order(energy, n, total, part);
+  if (threadIdx.x == 0) atomicExch(counter, 0u);
 }
 
 __global__ void energy_bwd_kernel(const float* gE, const float* wr1, const float* y, const float* wr2b, int C, int H,
@@ -1028,8 +1090,7 @@ struct EmbedSet {
   int count;
 };
 
-__global__ void embed_rows_kernel(const int32_t* elem, int64_t n, const EmbedSet s) {
-  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void embed_row(const int32_t* elem, int64_t n, const EmbedSet& s, int64_t k) {
   const int total = s.start4[s.count];
   if (k >= n * total) return;
   const int64_t i = k / total;
@@ -1040,6 +1101,22 @@ __global__ void embed_rows_kernel(const int32_t* elem, int64_t n, const EmbedSet
     if (q < s.count && c >= s.start4[q]) g = q;
   c -= s.start4[g];
   s.out[g][i * s.width4[g] + c] = s.table[g][(int64_t)elem[i] * s.width4[g] + c];
+}
+
+__global__ void embed_rows_kernel(const int32_t* elem, int64_t n, const EmbedSet s) {
+  embed_row(elem, n, s, (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+}
+
+// The edge geometry (blocks [0, geo_blocks)) and the per-element gathers (the rest) in one launch:
+// two independent passes at the start of a force evaluation.
+__global__ void geometry_embed_kernel(const GeoArgs a, int64_t geo_blocks, const int32_t* elem, int64_t n,
+                                      const EmbedSet s) {
+  if ((int64_t)blockIdx.x < geo_blocks) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < a.e_cap) edge_geometry_row(a, e);
+  } else {
+    embed_row(elem, n, s, ((int64_t)blockIdx.x - geo_blocks) * blockDim.x + threadIdx.x);
+  }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1274,8 +1351,8 @@ int fmd_edge_geometry_f32(const float* positions, const float* cell, const int32
   FMD_REQUIRE(positions && cell && edge_index && edge_image && n_edges && geo && ef && def);
   FMD_REQUIRE(e_cap >= 0 && nb > 0 && rc > 0.f);
   if (e_cap == 0) return FMD_OK;
-  hipLaunchKernelGGL(edge_geometry_kernel, dim3((unsigned)fmd_cdiv(e_cap, 256)), dim3(256), 0, stream, positions,
-                     cell, system_of, edge_index, edge_image, n_edges, e_cap, rc, nb, geo, ef, def);
+  const GeoArgs a{positions, cell, system_of, edge_index, edge_image, n_edges, e_cap, rc, nb, geo, ef, def};
+  hipLaunchKernelGGL(edge_geometry_kernel, dim3((unsigned)fmd_cdiv(e_cap, 256)), dim3(256), 0, stream, a);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -1406,11 +1483,19 @@ int fmd_mace_energy_f32(const float* ha, const float* wr1, const float* y, const
 
 int fmd_mace_energy_grad_f32(const float* ha, const float* wr1, const float* y, const float* wr2b, int32_t channels,
                              int32_t hidden, const int32_t* elem, const float* e0, float scale, float shift,
-                             int64_t n_atoms, float* energy, float* gha, float* gy, hipStream_t stream) {
-  FMD_REQUIRE(ha && wr1 && y && wr2b && elem && e0 && energy && gha && gy && n_atoms >= 0);
-  if (n_atoms == 0) return FMD_OK;
+                             int64_t n_atoms, float* energy, float* gha, float* gy, double* total,
+                             uint32_t* counter, hipStream_t stream) {
+  FMD_REQUIRE(ha && wr1 && y && wr2b && elem && e0 && energy && gha && gy && n_atoms >= 0 && (!total || counter));
+  if (n_atoms == 0) {
+    if (total) {  // the empty sum (a kernel, not a memset node: callers capture this launch)
+      hipLaunchKernelGGL(zero_f64_kernel, dim3(1), dim3(1), 0, stream, total);
+      FMD_CHECK_LAUNCH();
+    }
+    return FMD_OK;
+  }
   hipLaunchKernelGGL(energy_grad_kernel, dim3((unsigned)fmd_cdiv(n_atoms, kWaves)), dim3(kThreads), 0, stream, ha,
-                     wr1, y, wr2b, channels, hidden, elem, e0, scale, shift, n_atoms, energy, gha, gy);
+                     wr1, y, wr2b, channels, hidden, elem, e0, scale, shift, n_atoms, energy, gha, gy, total,
+                     reinterpret_cast<unsigned int*>(counter));
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -1436,10 +1521,12 @@ int fmd_embed_f32(const int32_t* elem, const float* table, int64_t n_atoms, int3
   return FMD_OK;
 }
 
-int fmd_embed_rows_f32(const int32_t* elem, int64_t n_atoms, int32_t count, const float* const* tables,
-                       const int32_t* widths, float* const* outs, hipStream_t stream) {
-  FMD_REQUIRE(elem && n_atoms >= 0 && count >= 1 && count <= kMaxEmbed && tables && widths && outs);
-  EmbedSet set{};
+}  // extern "C"
+
+namespace {
+int embed_set(int32_t count, const float* const* tables, const int32_t* widths, float* const* outs, EmbedSet& set) {
+  FMD_REQUIRE(count >= 1 && count <= kMaxEmbed && tables && widths && outs);
+  set = EmbedSet{};
   set.count = count;
   set.start4[0] = 0;
   for (int g = 0; g < count; ++g) {
@@ -1450,9 +1537,41 @@ int fmd_embed_rows_f32(const int32_t* elem, int64_t n_atoms, int32_t count, cons
     set.width4[g] = widths[g] / 4;
     set.start4[g + 1] = set.start4[g] + widths[g] / 4;
   }
+  return FMD_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int fmd_embed_rows_f32(const int32_t* elem, int64_t n_atoms, int32_t count, const float* const* tables,
+                       const int32_t* widths, float* const* outs, hipStream_t stream) {
+  FMD_REQUIRE(elem && n_atoms >= 0);
+  EmbedSet set;
+  const int rc = embed_set(count, tables, widths, outs, set);
+  if (rc != FMD_OK) return rc;
   if (n_atoms == 0) return FMD_OK;
   hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)fmd_cdiv(n_atoms * set.start4[count], 256)), dim3(256), 0,
                      stream, elem, n_atoms, set);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
+int fmd_edge_geometry_embed_f32(const float* positions, const float* cell, const int32_t* system_of,
+                                const int32_t* edge_index, const float* edge_image, const int64_t* n_edges,
+                                int64_t e_cap, float rc, int32_t nb, float* geo, float* ef, float* def,
+                                const int32_t* elem, int64_t n_atoms, int32_t count, const float* const* tables,
+                                const int32_t* widths, float* const* outs, hipStream_t stream) {
+  FMD_REQUIRE(positions && cell && edge_index && edge_image && n_edges && geo && ef && def);
+  FMD_REQUIRE(e_cap >= 0 && nb > 0 && rc > 0.f && elem && n_atoms >= 0);
+  EmbedSet set;
+  const int st = embed_set(count, tables, widths, outs, set);
+  if (st != FMD_OK) return st;
+  const int64_t geo_blocks = fmd_cdiv(e_cap, 256), emb_blocks = fmd_cdiv(n_atoms * set.start4[count], 256);
+  if (geo_blocks + emb_blocks == 0) return FMD_OK;
+  FMD_REQUIRE(geo_blocks + emb_blocks < (int64_t(1) << 31));
+  const GeoArgs a{positions, cell, system_of, edge_index, edge_image, n_edges, e_cap, rc, nb, geo, ef, def};
+  hipLaunchKernelGGL(geometry_embed_kernel, dim3((unsigned)(geo_blocks + emb_blocks)), dim3(256), 0, stream, a,
+                     geo_blocks, elem, n_atoms, set);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

@@ -338,6 +338,9 @@ class MaceLikeInput:
     elem: Tensor  # int32 [rows] element index of every atom row
     csr_dst: Csr = field(default=None)
     csr_src: Csr = field(default=None)
+    # the energy launch's completion counter (uint32 [1], zero between launches): the explicit
+    # force path forms the float64 total in that launch's last workgroup
+    sum_counter: Tensor = field(default=None)
 
 
 def _call(name, *args):
@@ -446,9 +449,9 @@ class _MaceLikeEnergy(Function):
         geo = _empty(e_cap, 8, device=dev)
         ef = _empty(e_cap, nb, device=dev)
         de = _empty(e_cap, nb, device=dev)
-        _call("fmd_edge_geometry_f32", positions.data_ptr(), cell.data_ptr(), system_rows(batch), ei.data_ptr(),
-              batch.edge_image.data_ptr(), n_edges.data_ptr(), e_cap, float(cfg.cutoff), nb, geo.data_ptr(),
-              ef.data_ptr(), de.data_ptr())
+        geo_args = (positions.data_ptr(), cell.data_ptr(), system_rows(batch), ei.data_ptr(),
+                    batch.edge_image.data_ptr(), n_edges.data_ptr(), e_cap, float(cfg.cutoff), nb, geo.data_ptr(),
+                    ef.data_ptr(), de.data_ptr())
         h1 = None
         saved = []
         h_first = None
@@ -472,10 +475,13 @@ class _MaceLikeEnergy(Function):
             pq_next = (_empty(n, 4 * C, device=dev), _empty(n, 4 * C, device=dev))
             rows = [(model.embedding, C, h0), (tp, 2 * C, P), (tq, 2 * C, Q), (tabs["skip"], C, h0n_first),
                     (tabs["p_next"], 4 * C, pq_next[0]), (tabs["q_next"], 4 * C, pq_next[1])]
-            _call("fmd_embed_rows_f32", elem.data_ptr(), n, len(rows), _abi.ptr_array([r[0].data_ptr() for r in rows]),
-                  _abi.array(_abi._i32, [r[1] for r in rows]), _abi.ptr_array([r[2].data_ptr() for r in rows]))
+            # the edge geometry and these gathers in one launch
+            _call("fmd_edge_geometry_embed_f32", *geo_args, elem.data_ptr(), n, len(rows),
+                  _abi.ptr_array([r[0].data_ptr() for r in rows]), _abi.array(_abi._i32, [r[1] for r in rows]),
+                  _abi.ptr_array([r[2].data_ptr() for r in rows]))
             z, q = P, Q
         else:
+            _call("fmd_edge_geometry_f32", *geo_args)
             _call("fmd_embed_f32", elem.data_ptr(), model.embedding.data_ptr(), n, C, h0.data_ptr())
         y = None
         # On large edge lists the edge GEMMs take pre-split operands: the radial rows once per
@@ -597,9 +603,11 @@ class _MaceLikeEnergy(Function):
         if getattr(ctx, "seed_ones", False):
             # the explicit force path (seed dE/dE_i = 1): the readout's gradients in the same launch
             ctx.gha, ctx.gy = _empty(n, C, device=dev), _empty(n, H, device=dev)
+            total = getattr(ctx, "total", None)
             _call("fmd_mace_energy_grad_f32", h_first.data_ptr(), model.wr1.data_ptr(), y.data_ptr(),
                   model.wr2b.data_ptr(), C, H, elem.data_ptr(), model.e0.data_ptr(), float(cfg.scale),
-                  float(cfg.shift), n, energy.data_ptr(), ctx.gha.data_ptr(), ctx.gy.data_ptr())
+                  float(cfg.shift), n, energy.data_ptr(), ctx.gha.data_ptr(), ctx.gy.data_ptr(), _abi.ptr(total),
+                  _abi.ptr(inputs.sum_counter if total is not None else None))
         else:
             _call("fmd_mace_energy_f32", h_first.data_ptr(), model.wr1.data_ptr(), y.data_ptr(),
                   model.wr2b.data_ptr(), C, H, elem.data_ptr(), model.e0.data_ptr(), float(cfg.scale),
@@ -818,7 +826,8 @@ class MaceLikeAdapter:
         elem = table[species].to(torch.int32).contiguous()
         rows = batch.edge_index.shape[0]
         return MaceLikeInput(batch=batch, elem=elem, csr_dst=Csr(batch.edge_offsets, None, rows),
-                             csr_src=Csr(batch.edge_offsets, batch.edge_reverse, rows))
+                             csr_src=Csr(batch.edge_offsets, batch.edge_reverse, rows),
+                             sum_counter=torch.zeros(1, dtype=torch.int32, device=elem.device))
 
     def node_energy(self, inputs: MaceLikeInput, positions: Tensor, cell: Tensor) -> Tensor:
         """Per-atom energies [rows] (float32) at ``positions``; differentiable w.r.t. positions."""
@@ -834,8 +843,15 @@ class MaceLikeAdapter:
         from fastmd_amd.engine.energy_derivative import sum_f64_segments
 
         saved = _Saved()
+        # (small launches only: each of the energy launch's blocks fences at device scope)
+        one = (isinstance(segments, int) and segments == 1 and inputs.sum_counter is not None
+               and positions.shape[0] <= SMALL_NODE_MAX_ATOMS)
+        if one:
+            # the fixed-order total of all rows, formed by the energy launch itself
+            saved.total = torch.empty(1, dtype=torch.float64, device=positions.device)
         energies = _MaceLikeEnergy.forward(saved, positions.detach(), cell.detach(), self.module, inputs)
-        energy = sum_f64_segments(energies, segments)  # one energy per replica or system
+        # one energy per replica or system
+        energy = saved.total if one else sum_f64_segments(energies, segments)
         return energy, _vjp(saved, None, -1.0)
 
     def energy_forces_stress(self, inputs: MaceLikeInput, positions: Tensor, cell: Tensor):

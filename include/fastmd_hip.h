@@ -634,10 +634,13 @@ int fmd_mace_energy_bwd_f32(const float* gE, const float* wr1, const float* y, c
                             int32_t hidden, float scale, int64_t n_atoms, float* gha, float* gy, hipStream_t stream);
 /* fmd_mace_energy_f32 together with fmd_mace_energy_bwd_f32's gha and gy for a null gE, in one
  * launch (the explicit force path of EnergyDerivative, energy_derivative.py:110-140, whose seed is
- * dE/dE_i = 1). */
+ * dE/dE_i = 1). total (may be null) [1] f64: also the sum of the n_atoms energies, bitwise
+ * fmd_sum_f64's, formed by the last workgroup to finish; counter: a uint32 that is zero before
+ * the first call and that the call leaves at zero (calls sharing one counter must not overlap). */
 int fmd_mace_energy_grad_f32(const float* ha, const float* wr1, const float* y, const float* wr2b, int32_t channels,
                              int32_t hidden, const int32_t* elem, const float* e0, float scale, float shift,
-                             int64_t n_atoms, float* energy, float* gha, float* gy, hipStream_t stream);
+                             int64_t n_atoms, float* energy, float* gha, float* gy, double* total,
+                             uint32_t* counter, hipStream_t stream);
 /* h0[i] = table[elem[i]]. */
 int fmd_embed_f32(const int32_t* elem, const float* table, int64_t n_atoms, int32_t channels, float* h0,
                   hipStream_t stream);
@@ -646,6 +649,14 @@ int fmd_embed_f32(const int32_t* elem, const float* table, int64_t n_atoms, int3
  * layer's per-element rows (embedding, node-factored pre-activation blocks, residual tables). */
 int fmd_embed_rows_f32(const int32_t* elem, int64_t n_atoms, int32_t count, const float* const* tables,
                        const int32_t* widths, float* const* outs, hipStream_t stream);
+/* fmd_edge_geometry_f32 and fmd_embed_rows_f32 (the same arguments, the same results) in one
+ * launch: the two independent passes that open a force evaluation. No reference counterpart: it
+ * saves a launch where a step is launch-bound (small systems). */
+int fmd_edge_geometry_embed_f32(const float* positions, const float* cell, const int32_t* system_of,
+                                const int32_t* edge_index, const float* edge_image, const int64_t* n_edges,
+                                int64_t e_cap, float rc, int32_t nb, float* geo, float* ef, float* def,
+                                const int32_t* elem, int64_t n_atoms, int32_t count, const float* const* tables,
+                                const int32_t* widths, float* const* outs, hipStream_t stream);
 /* Morse pair potential (shifted to 0 at rc): E_i = 1/2 sum V(r_e) over the rows of centre i,
  * dvdr[e] = V'(r_e); VJP gvec[e] = 1/2 gE[centre] V'(r) u. */
 int fmd_morse_f32(const float* geo, const int64_t* edge_offsets, const int64_t* n_edges, int64_t e_cap,
