@@ -31,7 +31,7 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_nl_build_work_size": (_i64, [_i64]),
     "fmd_nl_build": (ctypes.c_int, [_p, _i32, _p, _p, _i64, _p, _p, _p, _i32, _p, _p, _p, _f32, _f32, _i32,
                                     _i32, _i32, _i32, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
-                                    _p, _p, _p, _p, _p, _f32, _p, _p, _p]),
+                                    _p, _p, _p, _p, _p, _f32, _p, _p, _p, _p, _p, _p, _p, _i32, _p]),
     "fmd_nl_build_noalloc": (ctypes.c_int, [_p, _i32, _p, _p, _i64, _p, _p, _p, _i32, _p, _p, _p, _f32, _f32, _i32,
                                             _i32, _i32, _i32, _i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                             _p, _p, _p, _p, _p, _f32, _p, _p]),

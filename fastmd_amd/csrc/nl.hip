@@ -341,6 +341,13 @@ struct BuildArgs {
   float line2;           // line-graph (bond) cutoff squared, float32
   uint8_t* short_flags;  // [e_cap]: real row with d2 < line2 (null: not written)
   int32_t* reverse;      // [e_cap]: the reverse row of every real row, -1 past them (null: not formed)
+  // a whole-step window's flags, folded with this build's status (w_over null: not folded)
+  uint8_t* w_over;
+  uint8_t* w_cap;
+  int64_t* w_edges;
+  int32_t* w_iso;
+  double* w_stats;
+  int w_check_iso;
 };
 
 // The cell and inverse cell of atom i (its system's, in a union of systems).
@@ -519,6 +526,43 @@ __device__ __forceinline__ void pad_rows(const BuildArgs& a, int64_t total, int6
   }
 }
 
+// One build's status folded into a whole-step window's flags (one thread).
+__device__ __forceinline__ void window_fold(int64_t edges, int32_t iso, bool overflowed, const uint8_t* invalid_pairs,
+                                           int64_t e_cap, int check_isolated, uint8_t* w_over, uint8_t* w_cap,
+                                           int64_t* w_edges, int32_t* w_iso, float max_disp, double* stats,
+                                           const int64_t* triplet_count, int64_t t_cap, int64_t* w_triplets) {
+  bool flag = overflowed;
+  if (check_isolated) flag = flag || iso > 0;
+  const uint8_t wo = (w_over[0] != 0 || flag) ? 1 : 0;
+  w_over[0] = wo;
+  // a line-graph build (triplet_count given) overflows its pairs at edges == e_cap (no padding
+  // pair left), and its triplets above t_cap
+  const int64_t triplets = triplet_count ? triplet_count[0] : 0;
+  const bool cap = (triplet_count ? edges >= e_cap : edges > e_cap) || (invalid_pairs && invalid_pairs[0] != 0) ||
+                   (triplet_count && triplets > t_cap);
+  int64_t wt = 0;
+  if (w_triplets) {
+    wt = triplets > w_triplets[0] ? triplets : w_triplets[0];
+    w_triplets[0] = wt;
+  }
+  const uint8_t wc = (w_cap[0] != 0 || cap) ? 1 : 0;
+  w_cap[0] = wc;
+  const int64_t we = edges > w_edges[0] ? edges : w_edges[0];
+  w_edges[0] = we;
+  w_iso[0] = iso > w_iso[0] ? iso : w_iso[0];
+  if (stats) {
+    // the window's statistics after this build: (overflow, edges, triplets, max displacement,
+    // capacity overflow, max edges, max isolated)
+    stats[0] = (double)wo;
+    stats[1] = (double)edges;
+    stats[2] = (double)wt;
+    stats[3] = (double)max_disp;
+    stats[4] = (double)wc;
+    stats[5] = (double)we;
+    stats[6] = (double)w_iso[0];
+  }
+}
+
 // Fused build of small systems in ONE workgroup (no inter-block dependency): prologue, counts,
 // scan, materialization, padding and flags, with the wrapped coordinates in LDS.
 __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs a) {
@@ -654,11 +698,15 @@ __global__ void __launch_bounds__(kSmallThreads) nl_build_small_kernel(BuildArgs
         isol += s_iso[k];
       }
       const bool valid = (m * 2.0f <= a.skin_limit) && (a.capacity_valid[0] != 0);
+      const bool over = (int64_t)run > a.e_cap || !valid;
       a.max_disp[0] = m;
       a.cand_valid[0] = valid ? 1 : 0;
-      a.overflow[0] = ((int64_t)run > a.e_cap || !valid) ? 1 : 0;
+      a.overflow[0] = over ? 1 : 0;
       a.isolated[0] = isol;
       a.edge_offsets[n] = run;
+      if (a.w_over)
+        window_fold(run, isol, over, nullptr, a.e_cap, a.w_check_iso, a.w_over, a.w_cap, a.w_edges, a.w_iso, m,
+                    a.w_stats, nullptr, 0, nullptr);
     }
     __syncthreads();
     int run = mine;
@@ -1032,38 +1080,8 @@ __global__ void nl_window_flags_kernel(const int64_t* edge_count, const uint8_t*
                                        int32_t* w_iso, const float* max_disp, double* stats,
                                        const int64_t* triplet_count, int64_t t_cap, int64_t* w_triplets) {
   if (threadIdx.x != 0) return;
-  const int64_t edges = edge_count[0];
-  const int32_t iso = isolated[0];
-  bool flag = overflow[0] != 0;
-  if (check_isolated) flag = flag || iso > 0;
-  const uint8_t wo = (w_over[0] != 0 || flag) ? 1 : 0;
-  w_over[0] = wo;
-  // a line-graph build (triplet_count given) overflows its pairs at edges == e_cap (no padding
-  // pair left), and its triplets above t_cap
-  const int64_t triplets = triplet_count ? triplet_count[0] : 0;
-  const bool cap = (triplet_count ? edges >= e_cap : edges > e_cap) || (invalid_pairs && invalid_pairs[0] != 0) ||
-                   (triplet_count && triplets > t_cap);
-  int64_t wt = 0;
-  if (w_triplets) {
-    wt = triplets > w_triplets[0] ? triplets : w_triplets[0];
-    w_triplets[0] = wt;
-  }
-  const uint8_t wc = (w_cap[0] != 0 || cap) ? 1 : 0;
-  w_cap[0] = wc;
-  const int64_t we = edges > w_edges[0] ? edges : w_edges[0];
-  w_edges[0] = we;
-  w_iso[0] = iso > w_iso[0] ? iso : w_iso[0];
-  if (stats) {
-    // the window's statistics after this build: (overflow, edges, triplets, max displacement,
-    // capacity overflow, max edges, max isolated)
-    stats[0] = (double)wo;
-    stats[1] = (double)edges;
-    stats[2] = (double)wt;
-    stats[3] = max_disp ? (double)max_disp[0] : 0.0;
-    stats[4] = (double)wc;
-    stats[5] = (double)we;
-    stats[6] = (double)w_iso[0];
-  }
+  window_fold(edge_count[0], isolated[0], overflow[0] != 0, invalid_pairs, e_cap, check_isolated, w_over, w_cap,
+              w_edges, w_iso, max_disp ? max_disp[0] : 0.f, stats, triplet_count, t_cap, w_triplets);
 }
 
 // The build's launches (small systems: one fused workgroup; otherwise count -> scan ->
@@ -1095,6 +1113,13 @@ int launch_build(const BuildArgs& a, hipStream_t stream) {
   if (a.reverse) {
     hipLaunchKernelGGL(nl_reverse_kernel, dim3((unsigned)fmd_cdiv(a.e_cap, 256)), dim3(256), 0, stream, a.center,
                        a.neighbor, a.images, a.edge_offsets, a.n, a.e_cap, a.reverse);
+    FMD_CHECK_LAUNCH();
+  }
+  if (a.w_over) {
+    hipLaunchKernelGGL(nl_window_flags_kernel, dim3(1), dim3(64), 0, stream, a.edge_offsets + a.n,
+                       (const uint8_t*)nullptr, (const uint8_t*)a.overflow, (const int32_t*)a.isolated, a.e_cap,
+                       a.w_check_iso, a.w_over, a.w_cap, a.w_edges, a.w_iso, (const float*)a.max_disp, a.w_stats,
+                       (const int64_t*)nullptr, (int64_t)0, (int64_t*)nullptr);
     FMD_CHECK_LAUNCH();
   }
   return FMD_OK;
@@ -1197,13 +1222,17 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  int64_t* edge_counts, int64_t* edge_offsets, int32_t* center, int32_t* neighbor, int32_t* images,
                  float* distances, int32_t* edge_index, float* edge_image, float* max_displacement,
                  uint8_t* candidate_valid, uint8_t* overflow, int32_t* isolated, float line2, uint8_t* short_flags,
-                 int32_t* edge_reverse, hipStream_t stream) {
+                 int32_t* edge_reverse, uint8_t* window_overflow, uint8_t* window_capacity,
+                 int64_t* window_max_edges, int32_t* window_max_isolated, double* window_stats,
+                 int32_t window_check_isolated, hipStream_t stream) {
   FMD_REQUIRE(work && reinterpret_cast<uintptr_t>(work) % 16 == 0);  // the scan reads it 16 bytes at a time
+  FMD_REQUIRE(!window_overflow || (window_capacity && window_max_edges && window_max_isolated));
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
               reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, minimum_image, pad_ix, pad_iy, pad_iz,
               n_dummy, system_of, pad_images, e_cap, work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
               edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags,
-              edge_reverse};
+              edge_reverse, window_overflow, window_capacity, window_max_edges, window_max_isolated, window_stats,
+              window_check_isolated};
   return launch_build(a, stream);
 }
 
@@ -1226,7 +1255,7 @@ int fmd_nl_build_noalloc(const void* positions, int32_t pos_is_f64, const float*
               reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, minimum_image, pad_ix, pad_iy, pad_iz,
               n_dummy, system_of, pad_images, e_cap, work, frac, wrap_delta, wrapped_out, edge_counts, edge_offsets, center, neighbor, images, distances,
               edge_index, edge_image, max_displacement, candidate_valid, overflow, isolated, line2, short_flags,
-              nullptr};
+              nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
   return launch_build(a, stream);
 }
 

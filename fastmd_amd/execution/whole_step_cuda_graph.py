@@ -157,8 +157,8 @@ class WholeStepGraphRunner:
             self._capture()
 
     # ------------------------------------------------------------------ body
-    def _evaluate(self, positions: Tensor):
-        graph, status = self.builder.build(positions, rebuild_candidates=False)
+    def _evaluate(self, positions: Tensor, window: dict | None = None):
+        graph, status = self.builder.build(positions, rebuild_candidates=False, window=window)
         out = self._derivative(self.builder.batch, graph, task=self.task, n_real=self.n_real)
         forces = out["f"][0][: self.n_real]
         energy = out["e"].reshape(-1)  # one energy (or one per replica of a replica batch)
@@ -171,16 +171,14 @@ class WholeStepGraphRunner:
         integrator = self.integrator
         if positions is None:
             positions = integrator.step_pre_force()
-        forces, energy, status = self._evaluate(positions)
-        # the flag fold reads only the build's status: it goes before the integrator, so that
-        # the post-force half and the next pre-force half are adjacent
-        self.builder.accumulate_window(status, window_overflow=self.window_overflow,
-                                       window_capacity_overflow=self.window_capacity_overflow,
-                                       window_max_edges=self.window_max_edges,
-                                       window_max_isolated=self.window_max_isolated,
-                                       check_isolated=self.validate_isolated_atoms,
-                                       stats=self._window_stats if last else None,
-                                       window_max_triplets=self.window_max_triplets)
+        # the window's flag fold reads only the build's status: the build does it (an edges-only
+        # build in its own launch), so that the post-force half and the next pre-force half stay
+        # adjacent
+        window = dict(window_overflow=self.window_overflow, window_capacity_overflow=self.window_capacity_overflow,
+                      window_max_edges=self.window_max_edges, window_max_isolated=self.window_max_isolated,
+                      check_isolated=self.validate_isolated_atoms, stats=self._window_stats if last else None,
+                      window_max_triplets=self.window_max_triplets)
+        forces, energy, status = self._evaluate(positions, window)
         with torch.no_grad():
             if fuse_next:
                 return integrator.step_post_pre(forces.detach(), energy=energy.detach())

@@ -359,11 +359,18 @@ class FixedCapacityGraphBuilder:
     # ------------------------------------------------------------------ build
     @torch.no_grad()
     @roctx_ranged("fixed_capacity_graph_build")
-    def build(self, positions: Tensor, *, rebuild_candidates: bool = True, predicate=None):
+    def build(self, positions: Tensor, *, rebuild_candidates: bool = True, predicate=None, window: dict | None = None):
         """Build into the persistent buffers; returns ``(prepare(batch), status)``
-        (fixed_capacity_builder.py:2180-2298). ``positions`` float32 or float64 [N, 3]."""
+        (fixed_capacity_builder.py:2180-2298). ``positions`` float32 or float64 [N, 3]. ``window``
+        (the keyword arguments of ``accumulate_window``): this build's status is also folded into
+        a whole-step window's flags, by the build's own launch for an edges-only build."""
         if predicate is not None:
             raise NotImplementedError("caller predicates belong to ghost-row builders")
+        fold = None
+        if window is not None:
+            self._check_window(**window)
+            if self.line_graph is None:
+                fold = window
         positions = self._positions_arg(positions)
         if rebuild_candidates:
             self.refresh_candidates(positions)
@@ -383,7 +390,7 @@ class FixedCapacityGraphBuilder:
                   self.batch.edge_index.data_ptr(), self.batch.edge_image.data_ptr(),
                   self._max_displacement.data_ptr(), self._candidate_valid.data_ptr(), self._overflow.data_ptr(),
                   self._isolated_atom_count.data_ptr(), self._line2, _abi.ptr(self.short_flags),
-                  self.edge_reverse.data_ptr(), self._stream())
+                  self.edge_reverse.data_ptr(), *self._window_ptrs(fold), self._stream())
         if not self.edges_only:
             # pairs, short-bond lists and triplets; the overflow flag becomes the line-graph rule
             # (edges >= e_capacity | triplets > t_capacity | invalid pairs | invalid candidates)
@@ -407,7 +414,32 @@ class FixedCapacityGraphBuilder:
                       self.edge_vec_override.data_ptr(), self._stream())
         if self.max_neighbor_count is not None:
             torch.maximum(self.max_neighbor_count, self.edge_counts.max().reshape(1), out=self.max_neighbor_count)
+        if window is not None and fold is None:
+            self.accumulate_window(self.status, **window)
         return self.graph, self.status
+
+    @staticmethod
+    def _window_ptrs(window: dict | None) -> tuple:
+        """fmd_nl_build's window arguments (all null: no fold)."""
+        if window is None:
+            return (None, None, None, None, None, 0)
+        stats = window.get("stats")
+        return (window["window_overflow"].data_ptr(), window["window_capacity_overflow"].data_ptr(),
+                window["window_max_edges"].data_ptr(), window["window_max_isolated"].data_ptr(),
+                None if stats is None else stats.data_ptr(), 1 if window["check_isolated"] else 0)
+
+    @staticmethod
+    def _check_window(*, window_overflow: Tensor, window_capacity_overflow: Tensor, window_max_edges: Tensor,
+                      window_max_isolated: Tensor, check_isolated: bool, stats: Tensor | None = None,
+                      window_max_triplets: Tensor | None = None) -> None:
+        if window_max_triplets is not None and window_max_triplets.dtype != torch.int64:
+            raise ValueError("window_max_triplets must be int64")
+        if stats is not None and (stats.dtype != torch.float64 or stats.numel() < 7):
+            raise ValueError("stats must be a float64 tensor of at least 7 entries")
+        for t, dt in ((window_overflow, torch.uint8), (window_capacity_overflow, torch.uint8),
+                      (window_max_edges, torch.int64), (window_max_isolated, torch.int32)):
+            if t.dtype != dt:
+                raise ValueError(f"window flag dtype {t.dtype}, expected {dt}")
 
     @property
     def _pad_image(self) -> tuple[int, int, int]:
@@ -436,15 +468,10 @@ class FixedCapacityGraphBuilder:
         receives the window's statistics after this build. A line-graph build also folds its
         triplet count (capacity overflow above t_capacity, pairs full at e_capacity edges) and
         its invalid-pair flag."""
-        if window_max_triplets is not None and window_max_triplets.dtype != torch.int64:
-            raise ValueError("window_max_triplets must be int64")
+        self._check_window(window_overflow=window_overflow, window_capacity_overflow=window_capacity_overflow,
+                           window_max_edges=window_max_edges, window_max_isolated=window_max_isolated,
+                           check_isolated=check_isolated, stats=stats, window_max_triplets=window_max_triplets)
         line = self.line_graph is not None
-        if stats is not None and (stats.dtype != torch.float64 or stats.numel() < 7):
-            raise ValueError("stats must be a float64 tensor of at least 7 entries")
-        for t, dt in ((window_overflow, torch.uint8), (window_capacity_overflow, torch.uint8),
-                      (window_max_edges, torch.int64), (window_max_isolated, torch.int32)):
-            if t.dtype != dt:
-                raise ValueError(f"window flag dtype {t.dtype}, expected {dt}")
         _abi.call("fmd_nl_window_flags", status.edge_count.data_ptr(),
                   status.invalid_pairs.data_ptr() if line else None, status.overflow.data_ptr(),
                   status.isolated_atom_count.data_ptr(), self.e_capacity, 1 if check_isolated else 0,

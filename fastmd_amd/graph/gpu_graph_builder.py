@@ -151,7 +151,8 @@ class TensorGraphBuilder:
                   frac.data_ptr(), wrap_delta.data_ptr(), wrapped.data_ptr(), counts.data_ptr(), offsets.data_ptr(),
                   center.data_ptr(), neighbor.data_ptr(), images.data_ptr(), distances.data_ptr(),
                   edge_index.data_ptr(), edge_image.data_ptr(), max_disp.data_ptr(), cand_valid.data_ptr(),
-                  overflow.data_ptr(), isolated.data_ptr(), 0.0, None, None, stream)
+                  overflow.data_ptr(), isolated.data_ptr(), 0.0, None, None, None, None, None, None, None, 0,
+                  stream)
         edges, iso = torch.stack([offsets[-1], isolated[0].long()]).tolist()
         if self.check_isolated_atoms:
             raise_if_isolated_atoms(iso)

@@ -110,7 +110,10 @@ int fmd_nl_wrap(const void* positions, int32_t pos_is_f64, const float* inv_cell
  * a line-graph build's short-bond flag, real rows with the same d2 < line2, line2 the float32
  * square of the bond cutoff, fixed_capacity_builder.py:258-260; padding rows 0); edge_reverse
  * [e_cap] i32 (may be null: not formed) the reverse rows of fmd_nl_reverse on this build's rows,
- * formed in the same launch for small systems (one workgroup), else by one more launch. */
+ * formed in the same launch for small systems (one workgroup), else by one more launch.
+ * window_* (window_overflow null: not folded; window_stats may be null): this build's status folded
+ * into a whole-step window's flags as fmd_nl_window_flags does for an edges-only build (in the same
+ * launch for small systems, else by one more launch). */
 int64_t fmd_nl_build_work_size(int64_t n_atoms);
 int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cell, const float* cell,
                  int64_t n_atoms, const int32_t* neighbor_matrix, const int32_t* neighbor_shifts,
@@ -123,6 +126,8 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  int32_t* images, float* distances, int32_t* edge_index, float* edge_image,
                  float* max_displacement, uint8_t* candidate_valid, uint8_t* overflow,
                  int32_t* isolated, float line2, uint8_t* short_flags, int32_t* edge_reverse,
+                 uint8_t* window_overflow, uint8_t* window_capacity, int64_t* window_max_edges,
+                 int32_t* window_max_isolated, double* window_stats, int32_t window_check_isolated,
                  hipStream_t stream);
 
 /* Allocation-free variant of fmd_nl_build. It has no counterpart in the reference: it is for
