@@ -1067,7 +1067,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
   x3_finish<2>(acc, none, bias, c, ldc, m, n, accumulate, act, row_blk + wm * 64, col_blk + wn * 64, h, rr);
 }
 
-// bf16 GEMM for tall A (tens of thousands of edge rows and more, K <= 272) with a column slab of
+// bf16 GEMM for tall A (tens of thousands of edge rows and more, K <= 544) with a column slab of
 // B resident in LDS. Each workgroup has 8 waves, at most two per SIMD, so that the whole K extent
 // of a wave's A rows and its 32 x 32 NCB accumulators fit in registers. It copies NSL slabs of
 // 32 NCB of B's rows (columns of C) once, zero-padded to Kp = 16 ceil(K / 16), with a row stride
@@ -1082,12 +1082,16 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2
 // (k-steps of 16 in order, zero chunk past K): bitwise their result.
 constexpr int BR_WAVES = 8, BR_ROWS = 32 * BR_WAVES;
 
-template <int NCB, int NKS, int NSL>
+// KR = 2 (one slab only, K up to 2 NKS k-steps): a wave holds NKS k-steps of its rows at a time;
+// as each k-step's MFMAs are issued its register is refilled with k-step NKS + ks, and a second
+// round runs those (K still in order, the same result as one round over all k-steps).
+template <int NCB, int NKS, int NSL, int KR = 1>
 __global__ void __launch_bounds__(64 * BR_WAVES) __attribute__((amdgpu_waves_per_eu(1, 2))) gemm_bf16_bres_kernel(
     const __bf16* __restrict__ a, int64_t lda, const __bf16* __restrict__ b, int64_t ldb,
     const float* __restrict__ bias, float* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int accumulate, int act,
     int n_slabs, int walkers) {
-  constexpr int NB = 32 * NCB, SKMAX = 16 * NKS + 8;
+  static_assert(KR == 1 || (KR == 2 && NSL == 1), "a second round of k-steps overwrites the first: one slab");
+  constexpr int NB = 32 * NCB, SKMAX = 16 * NKS * KR + 8;
   __shared__ __attribute__((aligned(16))) __bf16 sb[NSL * NB * SKMAX];
   const int t = threadIdx.x, lane = t & 63, h = lane >> 5, rr = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -1142,6 +1146,26 @@ __global__ void __launch_bounds__(64 * BR_WAVES) __attribute__((amdgpu_waves_per
             const bf16x8 bv = *reinterpret_cast<const bf16x8*>(bs + cb * 32 * sk + 16 * ks);
             acc[cb / 2][0][cb % 2] =
                 __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[ks], bv, acc[cb / 2][0][cb % 2], 0, 0, 0);
+          }
+          if constexpr (KR == 2) {
+            if (NKS + ks < nks) {
+              const __bf16* src = 16 * (NKS + ks) + 8 * h < k ? ap + 16 * (NKS + ks) : zero;
+              asm volatile("" : "+v"(src));
+              av[ks] = *reinterpret_cast<const bf16x8*>(src);
+            }
+          }
+        }
+      }
+      if constexpr (KR == 2) {
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          if (NKS + ks < nks) {
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+              const bf16x8 bv = *reinterpret_cast<const bf16x8*>(bs + cb * 32 * sk + 16 * (NKS + ks));
+              acc[cb / 2][0][cb % 2] =
+                  __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[ks], bv, acc[cb / 2][0][cb % 2], 0, 0, 0);
+            }
           }
         }
       }
@@ -1542,22 +1566,24 @@ int fmd_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb
   if (b_layout == 0 && k > 0 && k % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 && aligned16(a) && aligned16(b) &&
       fmd_cdiv(m, 128) * fmd_cdiv(n, 128) < (int64_t(1) << 31)) {
     const int64_t nks = fmd_cdiv(k, 16);
-    if (m >= kBresMinRows && nks <= 17) {
+    if (m >= kBresMinRows && nks <= 34) {
       // tall A, K <= 272 (A's whole K extent in a wave's registers beside its accumulators):
       // B's column slabs resident in LDS. Two 128-column slabs per workgroup (A loaded once for
       // both) when there are row blocks enough for every workgroup at half the slab count, else one
-      const int nsl = fmd_cdiv(m, BR_ROWS) >= 2 * kBresWorkgroups ? 2 : 1;
+      const int nsl = nks <= 17 && fmd_cdiv(m, BR_ROWS) >= 2 * kBresWorkgroups ? 2 : 1;
       const int n_slabs = (int)fmd_cdiv(n, nsl * 32 * 4);
       const int walkers = max(8, (kBresWorkgroups / n_slabs) & ~7);
       const dim3 grid((unsigned)(walkers * n_slabs)), block(64 * BR_WAVES);
       const __bf16 *ab = reinterpret_cast<const __bf16*>(a), *bb = reinterpret_cast<const __bf16*>(b);
-#define BRES_LAUNCH(KS, SL)                                                                                   \
-  hipLaunchKernelGGL((gemm_bf16_bres_kernel<4, KS, SL>), grid, block, 0, stream, ab, lda, bb, ldb, bias, c, ldc, m, \
-                     n, k, accumulate, epilogue_kind, n_slabs, walkers)
+#define BRES_LAUNCH(KS, SL, KR)                                                                              \
+  hipLaunchKernelGGL((gemm_bf16_bres_kernel<4, KS, SL, KR>), grid, block, 0, stream, ab, lda, bb, ldb, bias, c, ldc, \
+                     m, n, k, accumulate, epilogue_kind, n_slabs, walkers)
       if (nks <= 9) {
-        if (nsl == 2) BRES_LAUNCH(9, 2); else BRES_LAUNCH(9, 1);
+        if (nsl == 2) BRES_LAUNCH(9, 2, 1); else BRES_LAUNCH(9, 1, 1);
+      } else if (nks <= 17) {
+        if (nsl == 2) BRES_LAUNCH(17, 2, 1); else BRES_LAUNCH(17, 1, 1);
       } else {
-        if (nsl == 2) BRES_LAUNCH(17, 2); else BRES_LAUNCH(17, 1);
+        BRES_LAUNCH(17, 1, 2);  // K <= 544: one 128-column slab (137-140 KB of LDS), two k-rounds
       }
 #undef BRES_LAUNCH
       FMD_CHECK_LAUNCH();

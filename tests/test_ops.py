@@ -498,11 +498,12 @@ def test_gemm_bf16_direct_to_lds(device, m, k, n):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("m,k,n", [(40000, 264, 512), (33001, 136, 256), (32768, 40, 130), (50000, 272, 200),
-                                   (140000, 264, 512), (131073, 136, 300)])
+                                   (140000, 264, 512), (131073, 136, 300), (40000, 520, 1024), (33001, 280, 200),
+                                   (50000, 544, 130)])
 def test_gemm_bf16_resident_b(device, m, k, n):
-    """The resident-B bf16 kernel (at least 32 768 rows, K <= 272, aligned K-contiguous operands):
+    """The resident-B bf16 kernel (at least 32 768 rows, K <= 544, aligned K-contiguous operands):
     K tails of 8 past a 16-k step, a ragged last row block and column slab, one slab or several,
-    one or two slabs per workgroup (from 131 072 rows);
+    one or two slabs per workgroup (from 131 072 rows), and past K = 272 the two k-rounds form;
     against fp64 of the bf16 values on a row sample, and bitwise the register-staged kernel with
     bias, accumulation and the SiLU epilogue."""
     import torch
