@@ -456,12 +456,14 @@ def model_graph_bench(steps: int, warmup: int) -> list:
 
 def nhc_bench(sizes=(135, 10000, 40000), steps: int = 100, reps: int = 5) -> list:
     """The fused NHC velocity-Verlet halves alone (configs[0]/[2] 135 atoms, configs[3] 10 000 and
-    40 000): ``steps`` pre-force + post-force pairs (500 K, dt 0.25 fs, tdamp 25 fs, tchain 3,
-    tloop 1, float32 forces) captured in one HIP graph and replayed ``reps`` times between HIP
-    events, so the time is the kernels' alone. Bytes per step as the survey counts them,
-    220 N (f64 positions, momenta, cached forces and masses read and written by the two halves,
-    f32 forces read); one workgroup up to 4 096 atoms (one launch per half), block partials with
-    the chain run by the last workgroup above (two launches per half)."""
+    40 000): ``steps`` steps (500 K, dt 0.25 fs, tdamp 25 fs, tchain 3, tloop 1, float32 forces)
+    captured in one HIP graph and replayed ``reps`` times between HIP events, so the time is the
+    kernels' alone. As the whole step runs them, a step's post-force half and the next step's
+    pre-force half share a launch (``step_post_pre``: one workgroup up to 4 096 atoms, one launch;
+    above, block partials with the chain run by the last workgroup, three launches); the separate
+    pre-force + post-force pair is timed beside it (``us_per_step_separate``: two launches, or four
+    above 4 096 atoms). Bytes per step as the survey counts them, 220 N (f64 positions, momenta,
+    cached forces and masses read and written by the two halves, f32 forces read)."""
     import numpy as np
     import torch
 
@@ -484,32 +486,41 @@ def nhc_bench(sizes=(135, 10000, 40000), steps: int = 100, reps: int = 5) -> lis
             nhc.step_pre_force()
             nhc.step_post_force(forces, energy=energy)
 
-        side = torch.cuda.Stream(device)
-        side.wait_stream(torch.cuda.current_stream(device))
-        with torch.cuda.stream(side):
-            for _ in range(3):
-                pair()
-        torch.cuda.current_stream(device).wait_stream(side)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            for _ in range(steps):
-                pair()
-        graph.replay()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(reps):
+        def fused():
+            nhc.step_post_pre(forces, energy=energy)
+
+        def per_step_us(body) -> float:
+            side = torch.cuda.Stream(device)
+            side.wait_stream(torch.cuda.current_stream(device))
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    body()
+            torch.cuda.current_stream(device).wait_stream(side)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(steps):
+                    body()
             graph.replay()
-        end.record()
-        end.synchronize()
-        us = start.elapsed_time(end) * 1e3 / (reps * steps)
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(reps):
+                graph.replay()
+            end.record()
+            end.synchronize()
+            del graph
+            return start.elapsed_time(end) * 1e3 / (reps * steps)
+
+        us_sep = per_step_us(pair)
+        nhc.step_pre_force()  # the fused calls run a step's post half and the next step's pre half
+        us = per_step_us(fused)
         nbytes = 220 * n
-        out.append({"atoms": n, "us_per_step": round(us, 2), "launches_per_step": 2 if n <= 4096 else 4,
-                    "bytes_per_step": nbytes, "GBps": round(nbytes / us / 1e3, 1),
-                    "frac_of_hbm_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4)})
-        log(f"NHC {n} atoms: {us:.2f} us per step ({out[-1]['GBps']} GB/s)")
-        del graph, nhc
+        out.append({"atoms": n, "us_per_step": round(us, 2), "launches_per_step": 1 if n <= 4096 else 3,
+                    "us_per_step_separate": round(us_sep, 2), "bytes_per_step": nbytes,
+                    "GBps": round(nbytes / us / 1e3, 1), "frac_of_hbm_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4)})
+        log(f"NHC {n} atoms: {us:.2f} us per step fused, {us_sep:.2f} separate ({out[-1]['GBps']} GB/s)")
+        del nhc
         torch.cuda.empty_cache()
     return out
 
