@@ -303,22 +303,69 @@ __device__ __forceinline__ void reduce_waves(float (&v)[NV][CPL], float* s_red, 
 // per wave, or in the sender-side VJP the wave's own P once and Q by receiver) and add the radial
 // term from the edge's basis row and W1's radial rows staged in LDS ([RB, 4C], zero past nb).
 // The radial rows are applied to a group's rows together (each LDS read serves the group).
-template <int KP, int NZ, int CPL, int RB>
+// The radial products in one of three loop forms, chosen per kernel by measurement (the same
+// products in the same order: the same bits):
+//  kRadialFull: unrolled whole (the basis values are registers with constant indices), one radial
+//    row per scheduling region (without the barrier the scheduler would issue every LDS read up
+//    front and hold all RB * NZ * CPL weights in registers);
+//  kRadialShift: a loop over the radial rows, the basis values moved down the row's registers after
+//    each step (constant register indices);
+//  kRadialPairs: a loop of two radial rows per step, each step's basis value selected among the
+//    row's registers (the fewest registers).
+constexpr int kRadialPairs = 0, kRadialShift = 1, kRadialFull = 2;
+
+template <int KP, int NZ, int CPL, int RB, int FORM>
 __device__ __forceinline__ void add_radial(const float* s_w, int woff, const float (&er)[KP][RB],
                                            float (&zr)[KP][NZ][CPL]) {
   constexpr int C = 32 * CPL;
-  // two radial rows per step: unrolled whole, the scheduler would issue every LDS read up front
-  // and hold all RB * NZ * CPL weights in registers
-#pragma unroll 2
-  for (int t = 0; t < RB; ++t) {
+  if constexpr (FORM == kRadialFull) {
 #pragma unroll
-    for (int b = 0; b < NZ; ++b) {
-      float wv[CPL];
-      load_ch<CPL>(s_w + t * 4 * C + b * C + woff, wv);
+    for (int t = 0; t < RB; ++t) {
+      float wv[NZ][CPL];
+#pragma unroll
+      for (int b = 0; b < NZ; ++b) load_ch<CPL>(s_w + t * 4 * C + b * C + woff, wv[b]);
+#pragma unroll
+      for (int b = 0; b < NZ; ++b)
+#pragma unroll
+        for (int g = 0; g < KP; ++g)
+#pragma unroll
+          for (int q = 0; q < CPL; ++q) zr[g][b][q] += er[g][t] * wv[b][q];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else if constexpr (FORM == kRadialShift) {
+    float eb[KP][RB];
+#pragma unroll
+    for (int g = 0; g < KP; ++g)
+#pragma unroll
+      for (int k = 0; k < RB; ++k) eb[g][k] = er[g][k];
+#pragma unroll 1
+    for (int t = 0; t < RB; ++t) {
+#pragma unroll
+      for (int b = 0; b < NZ; ++b) {
+        float wv[CPL];
+        load_ch<CPL>(s_w + t * 4 * C + b * C + woff, wv);
+#pragma unroll
+        for (int g = 0; g < KP; ++g)
+#pragma unroll
+          for (int q = 0; q < CPL; ++q) zr[g][b][q] += eb[g][0] * wv[q];
+      }
 #pragma unroll
       for (int g = 0; g < KP; ++g)
 #pragma unroll
-        for (int q = 0; q < CPL; ++q) zr[g][b][q] += er[g][t] * wv[q];
+        for (int k = 0; k + 1 < RB; ++k) eb[g][k] = eb[g][k + 1];
+    }
+  } else {
+#pragma unroll 2
+    for (int t = 0; t < RB; ++t) {
+#pragma unroll
+      for (int b = 0; b < NZ; ++b) {
+        float wv[CPL];
+        load_ch<CPL>(s_w + t * 4 * C + b * C + woff, wv);
+#pragma unroll
+        for (int g = 0; g < KP; ++g)
+#pragma unroll
+          for (int q = 0; q < CPL; ++q) zr[g][b][q] += er[g][t] * wv[q];
+      }
     }
   }
 }
@@ -423,7 +470,7 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
       if constexpr (FZ) {
         int woff = c0;
         asm volatile("" : "+v"(woff));  // keeps the radial rows in LDS, not in registers
-        add_radial<kPairs, NZ, CPL, RBV>(s_w, woff, er, zr);
+        add_radial<kPairs, NZ, CPL, RBV, kRadialFull>(s_w, woff, er, zr);
       }
 #pragma unroll
       for (int g = 0; g < kPairs; ++g) {
@@ -585,7 +632,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
       if constexpr (FZ) {
         int woff = c0;
         asm volatile("" : "+v"(woff));
-        add_radial<kPairs, NZ, CPL, RB>(s_w, woff, er, zr);
+        add_radial<kPairs, NZ, CPL, RB, H1 ? kRadialFull : kRadialPairs>(s_w, woff, er, zr);
       }
 #pragma unroll
       for (int g = 0; g < kPairs; ++g) {
@@ -815,7 +862,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
       if constexpr (FZ) {
         int woff = c0;
         asm volatile("" : "+v"(woff));
-        add_radial<kPairs, NZ, CPL, RBV>(s_w, woff, eb, zr);
+        add_radial<kPairs, NZ, CPL, RBV, kRadialShift>(s_w, woff, eb, zr);
       }
 #pragma unroll
       for (int g = 0; g < kPairs; ++g) {
