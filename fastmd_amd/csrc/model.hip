@@ -389,10 +389,34 @@ __device__ __forceinline__ void load_basis(const float* ef, int nb, int64_t e, f
   }
 }
 
-// W1's radial rows [nb, 4C] into LDS as [RB, 4C], zero rows past nb (all threads of the block)
-__device__ __forceinline__ void stage_radial(float* s_w, const float* w1ef, int nb, int rb, int C) {
-  const int nbv = w1ef ? nb : 0;
-  for (int k = threadIdx.x; k < rb * 4 * C; k += blockDim.x) s_w[k] = k < nbv * 4 * C ? w1ef[k] : 0.f;
+// W1's radial rows [nb, 4C] into LDS as [RB, 4C], zero rows past nb (all threads of the block, which
+// has kThreads). Every thread issues all of its loads before its first store (one memory round trip
+// per block, not one per element), 16-byte loads when w1ef is 16-byte aligned.
+template <int RB, int C>
+__device__ __forceinline__ void stage_radial(float* s_w, const float* w1ef, int nb) {
+  constexpr int N4 = RB * C, PER = (N4 + kThreads - 1) / kThreads;  // float4s of [RB, 4C]
+  const int real4 = w1ef ? nb * C : 0;                               // float4s of the real rows
+  const int tid = threadIdx.x;
+  float4 v[PER];
+  if (((uintptr_t)w1ef & 15) == 0) {
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int k = tid + r * kThreads;
+      v[r] = k < real4 ? reinterpret_cast<const float4*>(w1ef)[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int k = tid + r * kThreads;
+      v[r] = k < real4 ? make_float4(w1ef[4 * k], w1ef[4 * k + 1], w1ef[4 * k + 2], w1ef[4 * k + 3])
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    const int k = tid + r * kThreads;
+    if (k < N4) reinterpret_cast<float4*>(s_w)[k] = v[r];
+  }
   __syncthreads();
 }
 
@@ -411,7 +435,7 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
   constexpr int RBV = FZ ? RB : 1;
   extern __shared__ float s_w[];  // FZ: [RB, 4C]
   __shared__ float s_red[WPA > 1 ? kWaves * 4 * C : 1];
-  if constexpr (FZ) stage_radial(s_w, w1ef, nb, RB, C);
+  if constexpr (FZ) stage_radial<RB, C>(s_w, w1ef, nb);
   const int lane = threadIdx.x & 63;
   const bool upper = lane >= 32;
   const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), sub = wib % WPA;
@@ -557,7 +581,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
   const int lane = threadIdx.x & 63;
   const bool upper = lane >= 32;
   const int nbv = w1ef ? nb : 0;
-  stage_radial(s_w, w1ef, nb, RB, C);
+  stage_radial<RB, C>(s_w, w1ef, nb);
   const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), sub = wib % WPA;
   const int64_t il = fmd_xcd_block(blockIdx.x, gridDim.x) * (kWaves / WPA) + wib / WPA;
   if (WPA == 1 && il >= n) return;
@@ -770,7 +794,7 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
   constexpr int RBV = FZ ? RB : 1;
   extern __shared__ float s_w[];  // FZ: [RB, 4C]
   __shared__ float s_red[WPA > 1 ? kWaves * (4 + NZ) * C : 1];
-  if constexpr (FZ) stage_radial(s_w, w1ef, nb, RB, C);
+  if constexpr (FZ) stage_radial<RB, C>(s_w, w1ef, nb);
   const int lane = threadIdx.x & 63;
   const bool upper = lane >= 32;
   const int wib = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), sub = wib % WPA;
