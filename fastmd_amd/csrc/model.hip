@@ -193,6 +193,14 @@ __device__ __forceinline__ float bcast2(float v, int s0, int s1, bool upper) {
   return upper ? b : a;
 }
 
+// the same exchange for row data that is not on the path to the gathers' addresses: ds_bpermute
+// (the LDS crossbar) moves a value per instruction with no VALU work; bperm_addr is the byte
+// address of lane s0 in the lower half-wave and of lane s1 in the upper one, shared by the values
+__device__ __forceinline__ int bperm_addr(int s0, int s1, bool upper) { return (upper ? s1 : s0) << 2; }
+__device__ __forceinline__ float bperm(float v, int addr) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(v)));
+}
+
 // CPL consecutive floats (CPL 2: 8-byte, 4 and 8: 16-byte aligned)
 template <int CPL>
 __device__ __forceinline__ void load_ch(const float* p, float (&v)[CPL]) {
@@ -476,10 +484,11 @@ __global__ void __launch_bounds__(kThreads) message_kernel(const float* z, const
         const bool valid = r0 + (upper ? 1 : 0) < cnt;
         const int s = upper ? s1 : s0;
         const int64_t j = bcast2(m.j, s0, s1, upper);
-        ux[g] = bcast2(m.ux, s0, s1, upper);
-        uy[g] = bcast2(m.uy, s0, s1, upper);
-        uz[g] = bcast2(m.uz, s0, s1, upper);
-        const float f = bcast2(m.fc, s0, s1, upper);
+        const int ba = bperm_addr(s0, s1, upper);
+        ux[g] = bperm(m.ux, ba);
+        uy[g] = bperm(m.uy, ba);
+        uz[g] = bperm(m.uz, ba);
+        const float f = bperm(m.fc, ba);
         fc[g] = valid ? f : 0.f;  // a row past the end adds exact zeros
         const float* ze = FZ ? z + j * (NZ * C) + c0 : z + (base + s) * (NZ * C) + c0;
 #pragma unroll
@@ -638,10 +647,11 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
         const bool valid = r0 + (upper ? 1 : 0) < cnt;
         const int s = upper ? s1 : s0;
         const int64_t j = bcast2(m.j, s0, s1, upper);
-        ux[g] = bcast2(m.ux, s0, s1, upper);
-        uy[g] = bcast2(m.uy, s0, s1, upper);
-        uz[g] = bcast2(m.uz, s0, s1, upper);
-        const float f = bcast2(m.fc, s0, s1, upper);
+        const int ba = bperm_addr(s0, s1, upper);
+        ux[g] = bperm(m.ux, ba);
+        uy[g] = bperm(m.uy, ba);
+        uz[g] = bperm(m.uz, ba);
+        const float f = bperm(m.fc, ba);
         fc[g] = valid ? f : 0.f;  // a row past the end adds exact zeros
         const float* ze = FZ ? z + j * (NZ * C) + c0 : z + (base + s) * (NZ * C) + c0;
 #pragma unroll
@@ -669,29 +679,32 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
         float sf = 0.f, su0 = 0.f, su1 = 0.f, su2 = 0.f;
 #pragma unroll
         for (int q = 0; q < CPL; ++q) {
+          // with t = z s (the SiLU) its derivative is s (1 + z (1 - s)) = s + t - t s
           const float hjq = hj[g][q];
           const float gu = g1[0][q] * ux[g] + g1[1][q] * uy[g] + g1[2][q] * uz[g];
           const float za = zr[g][0][q] + qz[0][q], zb = zr[g][1][q] + qz[1][q];
           const float sa = sigmoid(za), sb = sigmoid(zb);
+          const float ta = za * sa, tb = zb * sb;
           const float gwa = g0[q] * hjq, gwb = hjq * gu;
-          gzl[0][q] = gwa * fc[g] * sa * (1.0f + za * (1.0f - sa));
-          gzl[1][q] = gwb * fc[g] * sb * (1.0f + zb * (1.0f - sb));
-          sf += gwa * za * sa + gwb * zb * sb;
-          const float wb = zb * sb * fc[g];
-          su0 += g1[0][q] * wb * hjq;
-          su1 += g1[1][q] * wb * hjq;
-          su2 += g1[2][q] * wb * hjq;
+          gzl[0][q] = gwa * fc[g] * __builtin_fmaf(-ta, sa, sa + ta);
+          gzl[1][q] = gwb * fc[g] * __builtin_fmaf(-tb, sb, sb + tb);
+          sf += gwa * ta + gwb * tb;
+          const float wbh = tb * fc[g] * hjq;
+          su0 += g1[0][q] * wbh;
+          su1 += g1[1][q] * wbh;
+          su2 += g1[2][q] * wbh;
           if (H1) {
             constexpr int BC = NZ > 2 ? 2 : 0, BD = NZ > 2 ? 3 : 0;
             const float hx = hv[g][0][q], hy = hv[g][1][q], hz = hv[g][2][q];
             const float zc = zr[g][BC][q] + qz[BC][q], zd = zr[g][BD][q] + qz[BD][q];
             const float sc = sigmoid(zc), sd = sigmoid(zd);
+            const float tc = zc * sc, td = zd * sd;
             const float proj = hx * ux[g] + hy * uy[g] + hz * uz[g];
             const float gwc = g0[q] * proj, gwd = g1[0][q] * hx + g1[1][q] * hy + g1[2][q] * hz;
-            gzl[BC][q] = gwc * fc[g] * sc * (1.0f + zc * (1.0f - sc));
-            gzl[BD][q] = gwd * fc[g] * sd * (1.0f + zd * (1.0f - sd));
-            sf += gwc * zc * sc + gwd * zd * sd;
-            const float t = g0[q] * zc * sc * fc[g];
+            gzl[BC][q] = gwc * fc[g] * __builtin_fmaf(-tc, sc, sc + tc);
+            gzl[BD][q] = gwd * fc[g] * __builtin_fmaf(-td, sd, sd + td);
+            sf += gwc * tc + gwd * td;
+            const float t = g0[q] * tc * fc[g];
             su0 += t * hx;
             su1 += t * hy;
             su2 += t * hz;
@@ -726,8 +739,8 @@ __global__ void __launch_bounds__(kThreads) message_bwd_edge_kernel(
             for (int q = 0; q < CPL; ++q) red[t] += gzl[b][q] * wv[q];
           }
         }
-        const float o0 = bcast2(og[0], s0, s1, upper), o1 = bcast2(og[1], s0, s1, upper),
-                    o2 = bcast2(og[2], s0, s1, upper), o3 = bcast2(og[3], s0, s1, upper);
+        const int ba = bperm_addr(s0, s1, upper);
+        const float o0 = bperm(og[0], ba), o1 = bperm(og[1], ba), o2 = bperm(og[2], ba), o3 = bperm(og[3], ba);
         float tg;  // the geometry sum this lane writes (index tgi), if any
         int tgi;
         if constexpr (RB == 8) {
@@ -856,10 +869,11 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
         const int er = bcast2(me, s0, s1, upper);
         const int64_t i = bcast2(mi, s0, s1, upper);
         const int64_t e = er < 0 ? 0 : er;  // a missing reverse row reads row 0, weight 0
-        ux[g] = bcast2(mux, s0, s1, upper);
-        uy[g] = bcast2(muy, s0, s1, upper);
-        uz[g] = bcast2(muz, s0, s1, upper);
-        const float f = bcast2(mfc, s0, s1, upper);
+        const int ba = bperm_addr(s0, s1, upper);
+        ux[g] = bperm(mux, ba);
+        uy[g] = bperm(muy, ba);
+        uz[g] = bperm(muz, ba);
+        const float f = bperm(mfc, ba);
         // rows past the end and missing reverse rows add exact zeros (fc = 0)
         fc[g] = valid && er >= 0 ? f : 0.f;
         const float* ze = z + e * (NZ * C) + c0;
@@ -895,20 +909,23 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
         for (int q = 0; q < CPL; ++q) {
           const float g0 = ga[g][0][q], gx = ga[g][1][q], gy = ga[g][2][q], gzv = ga[g][3][q];
           const float za = zr[g][0][q] + qe[g][0][q], zb = zr[g][1][q] + qe[g][1][q];
+          // with t = z s (the SiLU) its derivative is s (1 + z (1 - s)) = s + t - t s
           const float sa = sigmoid(za), sb = sigmoid(zb);
-          const float wa = za * sa * fc[g], wb = zb * sb * fc[g];
+          const float ta = za * sa, tb = zb * sb;
+          const float wa = ta * fc[g], wb = tb * fc[g];
           const float gu = gx * ux[g] + gy * uy[g] + gzv * uz[g];
           a0[q] += g0 * wa + wb * gu;
           if (gzsum_src) {
             const float gwa = g0 * hs[q], gwb = hs[q] * gu;
-            gsum[0][q] += gwa * fc[g] * sa * (1.0f + za * (1.0f - sa));
-            gsum[1][q] += gwb * fc[g] * sb * (1.0f + zb * (1.0f - sb));
+            gsum[0][q] += gwa * fc[g] * __builtin_fmaf(-ta, sa, sa + ta);
+            gsum[1][q] += gwb * fc[g] * __builtin_fmaf(-tb, sb, sb + tb);
           }
           if (H1) {
             constexpr int BC = NZ > 2 ? 2 : 0, BD = NZ > 2 ? 3 : 0;
             const float zc = zr[g][BC][q] + qe[g][BC][q], zd = zr[g][BD][q] + qe[g][BD][q];
             const float sc = sigmoid(zc), sd = sigmoid(zd);
-            const float wc = zc * sc * fc[g], wd = zd * sd * fc[g];
+            const float tc = zc * sc, td = zd * sd;
+            const float wc = tc * fc[g], wd = td * fc[g];
             const float t = g0 * wc;
             a1[0][q] += t * ux[g] + gx * wd;
             a1[1][q] += t * uy[g] + gy * wd;
@@ -917,8 +934,8 @@ __global__ void __launch_bounds__(kThreads) message_bwd_src_kernel(
               const float hx = hsv[0][q], hy = hsv[1][q], hz = hsv[2][q];
               const float gwc = g0 * (hx * ux[g] + hy * uy[g] + hz * uz[g]);
               const float gwd = gx * hx + gy * hy + gzv * hz;
-              gsum[BC][q] += gwc * fc[g] * sc * (1.0f + zc * (1.0f - sc));
-              gsum[BD][q] += gwd * fc[g] * sd * (1.0f + zd * (1.0f - sd));
+              gsum[BC][q] += gwc * fc[g] * __builtin_fmaf(-tc, sc, sc + tc);
+              gsum[BD][q] += gwd * fc[g] * __builtin_fmaf(-td, sd, sd + td);
             }
           }
         }
