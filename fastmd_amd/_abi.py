@@ -72,6 +72,8 @@ SIGNATURES: dict[str, tuple] = {
                                              _p]),
     "fmd_gemm_group_x3_planes_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                                     _i32, _p]),
+    "fmd_gemm_group_x3_planes_rows_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                                                         _p, _p, _p, _p, _i32, _p]),
     "fmd_split3_f32": (ctypes.c_int, [_p, _i64, _i64, _i32, _p, _p]),
     "fmd_gemm_x3_planes_f32": (ctypes.c_int, [_i32, _i32, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _p, _p, _i64,
                                               _i64, _p, _p, _i64, _i64, _i32, _i32, _p]),

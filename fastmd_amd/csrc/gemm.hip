@@ -1189,6 +1189,7 @@ struct X3PGroupDesc {
   float* c;
   int64_t ldb, ldc, m, n, k, n_tiles, tile0;
   int accumulate;
+  X3Part radd;  // a gathered row added to every row of C (src null: none)
 };
 struct X3PGroup {
   X3PGroupDesc d[kMaxGroup];
@@ -1205,8 +1206,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3
     if (q < grp.count && w >= grp.d[q].tile0) g = q;
   const X3PGroupDesc& d = grp.d[g];
   const int64_t t = w - d.tile0;
-  const X3Part none{};
-  x3p_tile<MB>(d.p0, d.p1, d.p1, d.np, d.b, d.ldb, none, d.bias, d.c, d.ldc, d.m, d.n, d.k, d.accumulate,
+  x3p_tile<MB>(d.p0, d.p1, d.p1, d.np, d.b, d.ldb, d.radd, d.bias, d.c, d.ldc, d.m, d.n, d.k, d.accumulate,
                grp.act, (t / d.n_tiles) * (64 * MB), (t % d.n_tiles) * 128);
 }
 
@@ -1466,6 +1466,17 @@ int fmd_gemm_group_x3_planes_f32(int32_t count, const float* const* a, const int
                                  const int64_t* ldb, const float* const* bias, float* const* c, const int64_t* ldc,
                                  const int64_t* m, const int64_t* n, const int64_t* k, const int32_t* accumulate,
                                  int32_t epilogue_kind, hipStream_t stream) {
+  return fmd_gemm_group_x3_planes_rows_f32(count, a, lda, a2, lda2, ksplit, b_planes, ldb, bias, c, ldc, m, n, k,
+                                           accumulate, nullptr, nullptr, nullptr, epilogue_kind, stream);
+}
+
+int fmd_gemm_group_x3_planes_rows_f32(int32_t count, const float* const* a, const int64_t* lda,
+                                      const float* const* a2, const int64_t* lda2, const int64_t* ksplit,
+                                      const uint16_t* const* b_planes, const int64_t* ldb, const float* const* bias,
+                                      float* const* c, const int64_t* ldc, const int64_t* m, const int64_t* n,
+                                      const int64_t* k, const int32_t* accumulate, const float* const* row_add,
+                                      const int32_t* const* row_index, const int64_t* row_ld, int32_t epilogue_kind,
+                                      hipStream_t stream) {
   FMD_REQUIRE(count >= 1 && count <= kMaxGroup && a && lda && b_planes && ldb && c && ldc && m && n && k);
   FMD_REQUIRE(epilogue_kind == 0 || epilogue_kind == 1);
   X3PGroup grp{};
@@ -1496,6 +1507,11 @@ int fmd_gemm_group_x3_planes_f32(int32_t count, const float* const* a, const int
     d.k = k[g];
     d.n_tiles = fmd_cdiv(n[g], 128);
     d.accumulate = accumulate ? accumulate[g] : 0;
+    d.radd = X3Part{};
+    if (row_add && row_add[g]) {
+      FMD_REQUIRE(row_index && row_index[g] && row_ld && row_ld[g] >= n[g]);
+      d.radd = X3Part{row_add[g], row_index[g], row_ld[g], 1, 0};
+    }
     big += fmd_cdiv(m[g], 128) * d.n_tiles;
   }
   if (grp.count == 0) return FMD_OK;

@@ -63,6 +63,9 @@ FUSED_NODE = False
 # is the edge GEMM over the gather-cat rows (the configs' wide-GEMM operator on the path), kept
 # tested against the oracle beside the factored form.
 FACTORED_Z = True
+# The first layer's output GEMM adds the per-element residual and next-layer rows in its epilogue
+# (above the small-system sizes) instead of accumulating onto outputs prefilled with them.
+ROWS_IN_EPILOGUE = True
 # Merged node side (node-factored, unfused, two or more layers): a layer's output GEMM launch
 # also forms the next layer's P and Q, the last one the readout's first product (its h0n is
 # never formed), and the first layer's per-element rows come from one gather launch. Off: one
@@ -473,8 +476,14 @@ class _MaceLikeEnergy(Function):
             Q = _empty(n, 2 * C, device=dev)
             h0n_first = _empty(n, C, device=dev)
             pq_next = (_empty(n, 4 * C, device=dev), _empty(n, 4 * C, device=dev))
-            rows = [(model.embedding, C, h0), (tp, 2 * C, P), (tq, 2 * C, Q), (tabs["skip"], C, h0n_first),
-                    (tabs["p_next"], 4 * C, pq_next[0]), (tabs["q_next"], 4 * C, pq_next[1])]
+            rows = [(model.embedding, C, h0), (tp, 2 * C, P), (tq, 2 * C, Q)]
+            # the first layer's output rows start from per-element rows (residual, next P and Q):
+            # added in the output GEMM's epilogue above the small-system sizes (no prefill written
+            # and read back), prefilled here by the same launch below them
+            rows_in_epilogue = ROWS_IN_EPILOGUE and n > SMALL_NODE_MAX_ATOMS
+            if not rows_in_epilogue:
+                rows += [(tabs["skip"], C, h0n_first), (tabs["p_next"], 4 * C, pq_next[0]),
+                         (tabs["q_next"], 4 * C, pq_next[1])]
             # the edge geometry and these gathers in one launch
             _call("fmd_edge_geometry_embed_f32", *geo_args, elem.data_ptr(), n, len(rows),
                   _abi.ptr_array([r[0].data_ptr() for r in rows]), _abi.array(_abi._i32, [r[1] for r in rows]),
@@ -569,9 +578,14 @@ class _MaceLikeEnergy(Function):
                     bp, bq, bpp, bqp = mw["pq_next"][t]
                     P_n, Q_n = pq_next if t == 0 else (_empty(n, 4 * C, device=dev), _empty(n, 4 * C, device=dev))
                     if t == 0:
-                        probs = [{"a": B0, "b": w["wo0t"], "b_planes": wp["wo0t"], "out": h0n, "accumulate": True},
-                                 {"a": B0, "b": bp, "b_planes": bpp, "out": P_n, "accumulate": True},
-                                 {"a": B0, "b": bq, "b_planes": bqp, "out": Q_n, "accumulate": True}]
+                        probs = [{"a": B0, "b": w["wo0t"], "b_planes": wp["wo0t"], "out": h0n},
+                                 {"a": B0, "b": bp, "b_planes": bpp, "out": P_n},
+                                 {"a": B0, "b": bq, "b_planes": bqp, "out": Q_n}]
+                        for prob, tab in zip(probs, ("skip", "p_next", "q_next")):
+                            if rows_in_epilogue:
+                                prob["row_add"] = (tabs[tab], elem)
+                            else:
+                                prob["accumulate"] = True
                     else:
                         probs = [{"a": B0, "a2": h0, "b": w["wout0"], "b_planes": wp["wout0"], "out": h0n},
                                  {"a": B0, "a2": h0, "b": bp, "b_planes": bpp, "out": P_n},

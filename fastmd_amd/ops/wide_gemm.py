@@ -70,13 +70,18 @@ def gemm_group(problems, *, b_layout: int, epilogue: str | None = None) -> list:
     """Up to four independent ``gemm`` problems of one ``b_layout`` in one launch
     (fmd_gemm_group_f32). Each problem is a dict with ``a``, ``b``, ``out`` (float32, preallocated,
     unit column stride) and optionally ``a2`` (extra K columns: ``[a | a2] @ op(b)``, a's width a
-    multiple of 32), ``bias``, ``accumulate``, and ``b_planes`` (``split_planes(b)`` of a
-    ``b_layout`` 0 weight): when every problem has them and the group is large enough for the
-    split-plane form, the launch reads the planes (fmd_gemm_group_x3_planes_f32; the same bits
-    as splitting ``b`` in the kernel). Returns the outputs."""
+    multiple of 32), ``bias``, ``accumulate``, ``row_add`` (``(table, index)``: row ``index[r]`` of the
+    float32 ``table`` [*, N] added to output row r, int32 ``index`` [M]; the bits of a prefill of
+    those rows and an accumulating launch), and ``b_planes``
+    (``split_planes(b)`` of a ``b_layout`` 0 weight): when every problem has them and the group is
+    large enough for the split-plane form, the launch reads the planes
+    (fmd_gemm_group_x3_planes_rows_f32; the same bits as splitting ``b`` in the kernel, the rows
+    added in the epilogue). On the other forms ``row_add`` becomes a prefill of the output
+    (fmd_embed_f32) and an accumulating launch: the same bits. Returns the outputs."""
     if not 1 <= len(problems) <= 4:
         raise ValueError("gemm_group takes one to four problems")
-    cols = {k: [] for k in ("a", "lda", "a2", "lda2", "ksplit", "b", "ldb", "bias", "c", "ldc", "m", "n", "k", "acc")}
+    cols = {k: [] for k in ("a", "lda", "a2", "lda2", "ksplit", "b", "ldb", "bias", "c", "ldc", "m", "n", "k", "acc",
+                            "radd", "ridx", "rld")}
     keep = []
     for p in problems:
         a, b, out, a2, bias = p["a"], p["b"], p["out"], p.get("a2"), p.get("bias")
@@ -118,10 +123,38 @@ def gemm_group(problems, *, b_layout: int, epilogue: str | None = None) -> list:
         cols["n"].append(n)
         cols["k"].append(k)
         cols["acc"].append(1 if p.get("accumulate") else 0)
+        ra = p.get("row_add")
+        if ra is not None:
+            table, index = ra
+            require_cuda(table, index)
+            if (table.dtype != torch.float32 or table.dim() != 2 or table.shape[1] != n or table.stride(1) != 1
+                    or index.dtype != torch.int32 or index.shape != (m,) or not index.is_contiguous()):
+                raise ValueError(f"gemm_group: row_add must be a float32 [*, {n}] table and an int32 [{m}] index")
+            keep += [table, index]
+        cols["radd"].append(None if ra is None else ra[0].data_ptr())
+        cols["ridx"].append(None if ra is None else ra[1].data_ptr())
+        cols["rld"].append(0 if ra is None else ra[0].stride(0))
     i64 = lambda key: _abi.array(_abi._i64, cols[key])  # noqa: E731
+
+    def prefill_rows() -> None:
+        """The forms without the row epilogue: the rows written into the outputs first, then added to."""
+        for j, p in enumerate(problems):
+            if p.get("row_add") is None:
+                continue
+            table, index = p["row_add"]
+            out = p["out"]
+            if p.get("accumulate") or not out.is_contiguous() or not table.is_contiguous():
+                raise ValueError("gemm_group: row_add on this form needs a contiguous output and table, no accumulate")
+            _abi.call("fmd_embed_f32", index.data_ptr(), table.data_ptr(), out.shape[0], out.shape[1], out.data_ptr(),
+                      stream())
+            cols["acc"][j] = 1
     planes = [p.get("b_planes") for p in problems]
     tiles64 = sum(-(-m // 64) * -(-n // 64) for m, n in zip(cols["m"], cols["n"]))
+    rows_added = any(r is not None for r in cols["radd"])
     if b_layout == 0 and tiles64 < GROUP_KS_MAX_TILES:
+        if rows_added:
+            prefill_rows()
+            rows_added = False
         status = _abi.load().fmd_gemm_group_ks_f32(
             len(problems), _abi.ptr_array(cols["a"]), i64("lda"), _abi.ptr_array(cols["a2"]), i64("lda2"),
             i64("ksplit"), _abi.ptr_array(cols["b"]), i64("ldb"), _abi.ptr_array(cols["bias"]),
@@ -136,15 +169,18 @@ def gemm_group(problems, *, b_layout: int, epilogue: str | None = None) -> list:
             require_cuda(q.data)
             if q.width != p["b"].shape[1] or q.data.shape[0] != p["b"].shape[0]:
                 raise ValueError("gemm_group: b_planes are not the planes of b")
-        status = _abi.load().fmd_gemm_group_x3_planes_f32(
+        status = _abi.load().fmd_gemm_group_x3_planes_rows_f32(
             len(problems), _abi.ptr_array(cols["a"]), i64("lda"), _abi.ptr_array(cols["a2"]), i64("lda2"),
             i64("ksplit"), _abi.ptr_array([q.data.data_ptr() for q in planes]),
             _abi.array(_abi._i64, [q.ld for q in planes]), _abi.ptr_array(cols["bias"]), _abi.ptr_array(cols["c"]),
-            i64("ldc"), i64("m"), i64("n"), i64("k"), _abi.array(_abi._i32, cols["acc"]), _EPILOGUES[epilogue],
-            stream())
+            i64("ldc"), i64("m"), i64("n"), i64("k"), _abi.array(_abi._i32, cols["acc"]),
+            _abi.ptr_array(cols["radd"]) if rows_added else None, _abi.ptr_array(cols["ridx"]) if rows_added else None,
+            i64("rld") if rows_added else None, _EPILOGUES[epilogue], stream())
         if status != _EUNSUPPORTED:
-            _abi.check(status, "fmd_gemm_group_x3_planes_f32")
+            _abi.check(status, "fmd_gemm_group_x3_planes_rows_f32")
             return [p["out"] for p in problems]
+    if rows_added:
+        prefill_rows()
     _abi.call("fmd_gemm_group_f32", len(problems), _abi.ptr_array(cols["a"]), i64("lda"), _abi.ptr_array(cols["a2"]),
               i64("lda2"), i64("ksplit"), _abi.ptr_array(cols["b"]), i64("ldb"), b_layout,
               _abi.ptr_array(cols["bias"]), _abi.ptr_array(cols["c"]), i64("ldc"), i64("m"), i64("n"), i64("k"),

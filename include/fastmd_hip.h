@@ -402,6 +402,20 @@ int fmd_gemm_group_x3_planes_f32(int32_t count, const float* const* a, const int
                                  const float* const* bias, float* const* c, const int64_t* ldc,
                                  const int64_t* m, const int64_t* n, const int64_t* k,
                                  const int32_t* accumulate, int32_t epilogue, hipStream_t stream);
+/* fmd_gemm_group_x3_planes_f32 with a gathered row added to each output row: for a problem with
+ * row_add[g] non-null, C[r, :] = (A B)[r, :] + row_add[g][row_index[g][r] * row_ld[g] + (0 .. n)]
+ * (+ the old C when accumulate, then bias and the activation): the sum a launch on a C prefilled
+ * with those rows and accumulate = 1 gives, bitwise, without the prefill's write and read (the
+ * model's per-element residual and next-layer tables, indexed by element). row_add, row_index,
+ * row_ld may be null (no row added anywhere). No reference counterpart: a fused epilogue of this
+ * build's node side (the reference adds those terms in PyTorch). */
+int fmd_gemm_group_x3_planes_rows_f32(int32_t count, const float* const* a, const int64_t* lda,
+                                      const float* const* a2, const int64_t* lda2, const int64_t* ksplit,
+                                      const uint16_t* const* b_planes, const int64_t* ldb, const float* const* bias,
+                                      float* const* c, const int64_t* ldc, const int64_t* m, const int64_t* n,
+                                      const int64_t* k, const int32_t* accumulate, const float* const* row_add,
+                                      const int32_t* const* row_index, const int64_t* row_ld, int32_t epilogue_kind,
+                                      hipStream_t stream);
 
 /* fmd_gemm_group_f32 with b_layout 0 (B_g [N_g, K_g] K-contiguous) for groups too small to fill
  * the chip (small systems' node side): 16 x 16 output tiles, one workgroup each, whose four

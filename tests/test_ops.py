@@ -447,6 +447,55 @@ def test_gemm_group_split_plane_form(device):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m", [33000, 3000, 200])
+def test_gemm_group_row_add_is_a_prefill(device, m):
+    """gemm_group's row_add (row index[r] of a table added to output row r): on the split-plane
+    form (fmd_gemm_group_x3_planes_rows_f32, the rows added in the epilogue; m = 33 000), on the
+    fp32 grouped tiles (no planes) and on the small K-split form (m = 200) bitwise the result of
+    prefilling the output with those rows (fmd_embed_f32) and accumulating; a problem without
+    row_add in the same group is unchanged; within fp32 of float64."""
+    import torch
+
+    from fastmd_amd import _abi
+    from fastmd_amd.ops.wide_gemm import gemm_group, split_planes
+
+    print(f"[row_add] m={m}", flush=True)
+    g = torch.Generator().manual_seed(m)
+    C = 128
+    d = lambda t: t.to(device)  # noqa: E731
+    a = d(torch.randn(m, C, generator=g))
+    w0 = d(torch.randn(C, C, generator=g) / C ** 0.5)
+    w1 = d(torch.randn(4 * C, C, generator=g) / C ** 0.5)
+    tab0 = d(torch.randn(3, C, generator=g))
+    tab1 = d(torch.randn(5, 4 * C, generator=g))
+    idx = d(torch.randint(0, 3, (m,), generator=g, dtype=torch.int32))
+    idx1 = d(torch.randint(0, 5, (m,), generator=g, dtype=torch.int32))
+    for planes in (True, False):
+        o0, o1, o2 = torch.empty(m, C, device=device), torch.empty(m, 4 * C, device=device), torch.empty(m, C,
+                                                                                                       device=device)
+        probs = [{"a": a, "b": w0, "out": o0, "row_add": (tab0, idx)}, {"a": a, "b": w1, "out": o1,
+                                                                        "row_add": (tab1, idx1)},
+                 {"a": a, "b": w0, "out": o2}]
+        if planes:
+            for p in probs:
+                p["b_planes"] = split_planes(p["b"])
+        gemm_group(probs, b_layout=0)
+        p0, p1, p2 = torch.empty_like(o0), torch.empty_like(o1), torch.empty_like(o2)
+        for tab, ix, out in ((tab0, idx, p0), (tab1, idx1, p1)):
+            _abi.call("fmd_embed_f32", ix.data_ptr(), tab.data_ptr(), m, tab.shape[1], out.data_ptr(),
+                      _abi.stream_handle(device))
+        refs = [{"a": a, "b": w0, "out": p0, "accumulate": True}, {"a": a, "b": w1, "out": p1, "accumulate": True},
+                {"a": a, "b": w0, "out": p2}]
+        if planes:
+            for p in refs:
+                p["b_planes"] = split_planes(p["b"])
+        gemm_group(refs, b_layout=0)
+        assert torch.equal(o0, p0) and torch.equal(o1, p1) and torch.equal(o2, p2)
+        ref1 = a.cpu().double() @ w1.cpu().double().t() + tab1.cpu().double()[idx1.cpu().long()]
+        assert oops.relative(o1.cpu().numpy(), ref1.numpy()) < 1e-5
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("F", [64, 128])
 def test_gemm_bf16_against_fp64_of_rounded_inputs(device, F):
     import torch
