@@ -1,6 +1,6 @@
 // (a) Neighbour list of the GPU-resident MD step: candidate cell list (rare refresh path) and
-// the per-step exact re-filter build over the candidates (count -> scan -> materialize ->
-// pad -> flags), bit-exact against the CPU oracle.
+// the per-step exact re-filter build over the candidates (count -> offsets + materialize + pad ->
+// reverse rows + flags), bit-exact against the CPU oracle.
 //
 // Arithmetic contract (shared with oracle/nl.py): every float32 operation below is a single
 // IEEE round-to-nearest operation in the written order, with no contraction into FMAs (this
@@ -873,76 +873,60 @@ __global__ void __launch_bounds__(kBlock) nl_count_kernel(BuildArgs a) {
     float* red = reinterpret_cast<float*>(a.work);
     red[blockIdx.x] = m;
     reinterpret_cast<int32_t*>(a.work + fmd_cdiv(nb, 2))[blockIdx.x] = isol;
-    // the block's edge count, for the scan's prefixes
+    // the block's edge count, for the materialize kernel's row offsets
     int32_t sum = 0;
     for (int k = 0; k < kBlock / FMD_WAVE; ++k) sum += s_cnt[k];
     reinterpret_cast<int32_t*>(a.work + 2 * fmd_cdiv(nb, 2))[blockIdx.x] = sum;
   }
 }
 
-// Kernel 2: exclusive scan of the counts, the flags and the reductions, over several
-// workgroups with no waits between them. Workgroup b scans the counts of atoms
-// [b kScanTile, (b + 1) kScanTile): each thread loads kScanPer consecutive counts and the
-// workgroup's offset is the sum of the count kernel's per-block edge counts before its range
-// (blocks of kAtomsPerCountBlock atoms; kScanTile is a multiple of it), read by every thread
-// strided and added in a fixed order. All of a thread's loads are issued before any use (one
-// memory round trip). The last workgroup also reduces the count kernel's partials (maximum
-// displacement, isolated atoms) and writes the total, the flags and edge_offsets[n]. Integer
-// sums are exact, so the offsets are the same in any grouping.
-constexpr int kScanThreads = 256, kScanPer = 8, kScanTile = kScanThreads * kScanPer, kScanLoads = 8;
-constexpr int kAtomsPerCountBlock = kBlock / FMD_WAVE;
-static_assert(kScanTile % kAtomsPerCountBlock == 0, "scan tiles cover whole count blocks");
+// Loads each thread keeps in flight when it sums the count kernel's per-workgroup partials.
+constexpr int kScanLoads = 8;
 
-__global__ void __launch_bounds__(kScanThreads) nl_scan_kernel(BuildArgs a, int64_t nblocks) {
-  __shared__ int64_t s_wtot[17];
-  __shared__ int64_t s_pre[kScanThreads / FMD_WAVE];
-  __shared__ float s_max[kScanThreads / FMD_WAVE];
-  __shared__ int32_t s_iso[kScanThreads / FMD_WAVE];
-  const int t = threadIdx.x, T = blockDim.x;
-  const int lane = t & (FMD_WAVE - 1), wave = t / FMD_WAVE;
-  const int64_t n = a.n;
-  const int64_t base = (int64_t)blockIdx.x * kScanTile;
-  const int64_t cnt = n - base < kScanTile ? n - base : kScanTile;
-  const bool last = blockIdx.x == gridDim.x - 1;
-  // this thread's counts (consecutive atoms)
-  int64_t c[kScanPer];
-#pragma unroll
-  for (int j = 0; j < kScanPer; ++j) {
-    const int64_t k = (int64_t)t * kScanPer + j;
-    c[j] = k < cnt ? a.edge_counts[base + k] : 0;
-  }
-  // the edge count of every atom before this tile: the count blocks [0, base / kAtomsPerCountBlock)
-  // (16-byte loads, kScanLoads of them in flight per thread: a loop of single loads would wait out
-  // one memory round trip per iteration)
-  const int32_t* bsum = reinterpret_cast<const int32_t*>(a.work + 2 * fmd_cdiv(nblocks, 2));
+// Kernel 2: the offsets and the materialization in one launch (one wave per atom, neighbours'
+// state from kernel 1's output) and, in the trailing workgroups, the padding rows. An atom
+// workgroup takes the atoms of the count kernel's workgroup of the same index (kBlock / 64
+// each): its first row is the sum of that kernel's per-workgroup edge counts before it, read by
+// every thread strided (16-byte loads, all of a thread's loads issued before any use), and its
+// atoms follow in atom order. The first padding workgroup sums every count workgroup's edges (the
+// total, edge_offsets[n]) and reduces the count kernel's partials (maximum displacement, isolated
+// atoms) into the build's flags. Integer sums are exact: the offsets are those of any grouping.
+__global__ void __launch_bounds__(kBlock) nl_materialize_kernel(BuildArgs a, int64_t atom_blocks) {
+  __shared__ int64_t s_pre[kBlock / FMD_WAVE];
+  __shared__ int32_t s_cnt[kBlock / FMD_WAVE];
+  __shared__ float s_max[kBlock / FMD_WAVE];
+  __shared__ int32_t s_iso[kBlock / FMD_WAVE];
+  const int t = threadIdx.x, lane = t & (FMD_WAVE - 1), wave = t / FMD_WAVE;
+  const bool pad = (int64_t)blockIdx.x >= atom_blocks, first_pad = (int64_t)blockIdx.x == atom_blocks;
+  const int64_t before = pad ? atom_blocks : (int64_t)blockIdx.x;  // count workgroups before this one's rows
+  const int32_t* bsum = reinterpret_cast<const int32_t*>(a.work + 2 * fmd_cdiv(atom_blocks, 2));
   const int4* bsum4 = reinterpret_cast<const int4*>(bsum);
-  const int64_t nbefore = base / kAtomsPerCountBlock, nbefore4 = nbefore / 4;
+  const int64_t before4 = before / 4;
   int64_t pre = 0;
-  for (int64_t q0 = t; q0 < nbefore4; q0 += (int64_t)T * kScanLoads) {
+  for (int64_t q0 = t; q0 < before4; q0 += (int64_t)kBlock * kScanLoads) {
     int4 v[kScanLoads];
 #pragma unroll
     for (int u = 0; u < kScanLoads; ++u) {
-      const int64_t q = q0 + (int64_t)u * T;
-      v[u] = q < nbefore4 ? bsum4[q] : make_int4(0, 0, 0, 0);
+      const int64_t q = q0 + (int64_t)u * kBlock;
+      v[u] = q < before4 ? bsum4[q] : make_int4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < kScanLoads; ++u) pre += (int64_t)v[u].x + v[u].y + v[u].z + v[u].w;
   }
-  for (int64_t b = nbefore4 * 4 + t; b < nbefore; b += T) pre += bsum[b];
-  // the last workgroup: the count kernel's partials over all its blocks
+  for (int64_t b = before4 * 4 + t; b < before; b += kBlock) pre += bsum[b];
   float m = 0.f;
   int32_t iso = 0;
-  if (last) {
+  if (first_pad) {
     const float* red = reinterpret_cast<const float*>(a.work);
-    const int32_t* isop = reinterpret_cast<const int32_t*>(a.work + fmd_cdiv(nblocks, 2));
-    for (int64_t b0 = t; b0 < nblocks; b0 += (int64_t)T * kScanLoads) {
+    const int32_t* isop = reinterpret_cast<const int32_t*>(a.work + fmd_cdiv(atom_blocks, 2));
+    for (int64_t b0 = t; b0 < atom_blocks; b0 += (int64_t)kBlock * kScanLoads) {
       float r[kScanLoads];
       int32_t z[kScanLoads];
 #pragma unroll
       for (int u = 0; u < kScanLoads; ++u) {
-        const int64_t b = b0 + (int64_t)u * T;
-        r[u] = b < nblocks ? red[b] : 0.f;
-        z[u] = b < nblocks ? isop[b] : 0;
+        const int64_t b = b0 + (int64_t)u * kBlock;
+        r[u] = b < atom_blocks ? red[b] : 0.f;
+        z[u] = b < atom_blocks ? isop[b] : 0;
       }
 #pragma unroll
       for (int u = 0; u < kScanLoads; ++u) {
@@ -951,59 +935,46 @@ __global__ void __launch_bounds__(kScanThreads) nl_scan_kernel(BuildArgs a, int6
       }
     }
   }
+  const int64_t i = (int64_t)blockIdx.x * (kBlock / FMD_WAVE) + wave;  // this wave's atom (atom workgroups)
   pre = wave_sum(pre);
-  if (lane == 0) s_pre[wave] = pre;
-  if (last) {
+  if (first_pad) {
     m = wave_nan_max(m);
     iso = wave_sum(iso);
-    if (lane == 0) {
-      s_max[wave] = m;
-      s_iso[wave] = iso;
-    }
   }
-  int64_t s = 0;
-#pragma unroll
-  for (int j = 0; j < kScanPer; ++j) s += c[j];
-  int64_t tile_total = 0;
-  const int64_t mine = block_exclusive_scan<int64_t>(s, s_wtot, &tile_total);  // synchronizes
+  if (lane == 0) {
+    s_pre[wave] = pre;
+    s_max[wave] = m;
+    s_iso[wave] = iso;
+    s_cnt[wave] = !pad && i < a.n ? a.edge_counts[i] : 0;
+  }
+  __syncthreads();
   int64_t prefix = 0;
-  for (int w = 0; w < T / FMD_WAVE; ++w) prefix += s_pre[w];
-  int64_t run = prefix + mine;
 #pragma unroll
-  for (int j = 0; j < kScanPer; ++j) {
-    const int64_t k = (int64_t)t * kScanPer + j;
-    if (k < cnt) a.edge_offsets[base + k] = run;
-    run += c[j];
-  }
-  if (last && t == 0) {
-    const int64_t total = prefix + tile_total;
-    float mm = s_max[0];
-    int32_t isol = s_iso[0];
-    for (int w = 1; w < T / FMD_WAVE; ++w) {
-      mm = nan_max(mm, s_max[w]);
-      isol += s_iso[w];
+  for (int w = 0; w < kBlock / FMD_WAVE; ++w) prefix += s_pre[w];
+  if (pad) {
+    const int64_t total = prefix;
+    if (first_pad && t == 0) {
+      float mm = s_max[0];
+      int32_t isol = s_iso[0];
+      for (int w = 1; w < kBlock / FMD_WAVE; ++w) {
+        mm = nan_max(mm, s_max[w]);
+        isol += s_iso[w];
+      }
+      const bool valid = (mm * 2.0f <= a.skin_limit) && (a.capacity_valid[0] != 0);
+      a.max_disp[0] = mm;
+      a.cand_valid[0] = valid ? 1 : 0;
+      a.overflow[0] = (total > a.e_cap || !valid) ? 1 : 0;
+      a.isolated[0] = isol;
+      a.edge_offsets[a.n] = total;
     }
-    const bool valid = (mm * 2.0f <= a.skin_limit) && (a.capacity_valid[0] != 0);
-    a.max_disp[0] = mm;
-    a.cand_valid[0] = valid ? 1 : 0;
-    a.overflow[0] = (total > a.e_cap || !valid) ? 1 : 0;
-    a.isolated[0] = isol;
-    a.edge_offsets[n] = total;
-  }
-}
-
-// Kernel 3: materialization (one wave per atom, neighbours' state from kernel 1's output)
-// and, in the trailing blocks, the padding rows.
-__global__ void __launch_bounds__(kBlock) nl_materialize_kernel(BuildArgs a, int64_t atom_blocks) {
-  const int lane = threadIdx.x & (FMD_WAVE - 1), wave = threadIdx.x / FMD_WAVE;
-  if ((int64_t)blockIdx.x >= atom_blocks) {
-    const int64_t total = a.edge_offsets[a.n];
     const int64_t pb = blockIdx.x - atom_blocks, npb = gridDim.x - atom_blocks;
-    pad_rows(a, total, pb * kBlock + threadIdx.x, npb * kBlock);
+    pad_rows(a, total, pb * kBlock + t, npb * kBlock);
     return;
   }
-  const int64_t i = (int64_t)blockIdx.x * (kBlock / FMD_WAVE) + wave;
   if (i >= a.n) return;
+  int64_t row0 = prefix;
+  for (int w = 0; w < wave; ++w) row0 += s_cnt[w];
+  if (lane == 0) a.edge_offsets[i] = row0;
   Mat3 inv, cm;
   atom_frame(a, i, inv, cm);
   // atom i's own wrapped position: recomputed (kernel 1 may not have published it)
@@ -1026,7 +997,6 @@ __global__ void __launch_bounds__(kBlock) nl_materialize_kernel(BuildArgs a, int
   };
   int cnt = a.num[i];
   cnt = cnt < a.bmax ? cnt : a.bmax;
-  int64_t row0 = a.edge_offsets[i];
   for (int base = 0; base < cnt; base += FMD_WAVE) {
     const int s = base + lane;
     bool e = false;
@@ -1041,8 +1011,27 @@ __global__ void __launch_bounds__(kBlock) nl_materialize_kernel(BuildArgs a, int
   }
 }
 
+// The window fold of a build whose reverse rows are formed: run by the first thread of the reverse
+// kernel (its inputs, the count, the overflow and isolated flags and the maximum displacement, are
+// final once materialize has run), so no launch of its own. w_over null: none.
+struct RevWindow {
+  const int64_t* edge_count;
+  const uint8_t* overflow;
+  const int32_t* isolated;
+  int check_isolated;
+  uint8_t* w_over;
+  uint8_t* w_cap;
+  int64_t* w_edges;
+  int32_t* w_iso;
+  const float* max_disp;
+  double* stats;
+};
+
 __global__ void nl_reverse_kernel(const int32_t* center, const int32_t* neighbor, const int32_t* images,
-                                  const int64_t* off, int64_t n, int64_t e_cap, int32_t* reverse) {
+                                  const int64_t* off, int64_t n, int64_t e_cap, int32_t* reverse, const RevWindow w) {
+  if (w.w_over && blockIdx.x == 0 && threadIdx.x == 0)
+    window_fold(w.edge_count[0], w.isolated[0], w.overflow[0] != 0, nullptr, e_cap, w.check_isolated, w.w_over,
+                w.w_cap, w.w_edges, w.w_iso, w.max_disp ? w.max_disp[0] : 0.f, w.stats, nullptr, 0, nullptr);
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = off[n];
   const int64_t ec = total < e_cap ? total : e_cap;
@@ -1084,8 +1073,9 @@ __global__ void nl_window_flags_kernel(const int64_t* edge_count, const uint8_t*
               w_edges, w_iso, max_disp ? max_disp[0] : 0.f, stats, triplet_count, t_cap, w_triplets);
 }
 
-// The build's launches (small systems: one fused workgroup; otherwise count -> scan ->
-// materialize, with the count kernel's per-block partials in a.work).
+// The build's launches (small systems: one fused workgroup; otherwise count -> offsets and
+// materialize (one launch) -> reverse rows with the window flags, with the count kernel's
+// per-block partials in a.work).
 int launch_build(const BuildArgs& a, hipStream_t stream) {
   FMD_REQUIRE(a.n > 0 && a.n < (int64_t(1) << 31) && a.e_cap > 0 && a.bmax > 0);
   FMD_REQUIRE(a.positions && a.inv_cell && a.cell && a.nbr && a.shifts && a.num);
@@ -1102,20 +1092,19 @@ int launch_build(const BuildArgs& a, hipStream_t stream) {
   const int64_t atom_blocks = fmd_cdiv(a.n, kBlock / FMD_WAVE);
   hipLaunchKernelGGL(nl_count_kernel, dim3((unsigned)atom_blocks), dim3(kBlock), 0, stream, a);
   FMD_CHECK_LAUNCH();
-  hipLaunchKernelGGL(nl_scan_kernel, dim3((unsigned)fmd_cdiv(a.n, kScanTile)), dim3(kScanThreads), 0, stream, a,
-                     atom_blocks);
-  FMD_CHECK_LAUNCH();
   int64_t pad_blocks = fmd_cdiv(a.e_cap, (int64_t)kBlock * 4);
   pad_blocks = pad_blocks < 1 ? 1 : (pad_blocks > 1024 ? 1024 : pad_blocks);
   hipLaunchKernelGGL(nl_materialize_kernel, dim3((unsigned)(atom_blocks + pad_blocks)), dim3(kBlock), 0, stream, a,
                      atom_blocks);
   FMD_CHECK_LAUNCH();
   if (a.reverse) {
+    const RevWindow w = a.w_over ? RevWindow{a.edge_offsets + a.n, a.overflow, a.isolated, a.w_check_iso, a.w_over,
+                                             a.w_cap, a.w_edges, a.w_iso, a.max_disp, a.w_stats}
+                                 : RevWindow{};
     hipLaunchKernelGGL(nl_reverse_kernel, dim3((unsigned)fmd_cdiv(a.e_cap, 256)), dim3(256), 0, stream, a.center,
-                       a.neighbor, a.images, a.edge_offsets, a.n, a.e_cap, a.reverse);
+                       a.neighbor, a.images, a.edge_offsets, a.n, a.e_cap, a.reverse, w);
     FMD_CHECK_LAUNCH();
-  }
-  if (a.w_over) {
+  } else if (a.w_over) {
     hipLaunchKernelGGL(nl_window_flags_kernel, dim3(1), dim3(64), 0, stream, a.edge_offsets + a.n,
                        (const uint8_t*)nullptr, (const uint8_t*)a.overflow, (const int32_t*)a.isolated, a.e_cap,
                        a.w_check_iso, a.w_over, a.w_cap, a.w_edges, a.w_iso, (const float*)a.max_disp, a.w_stats,
@@ -1127,7 +1116,7 @@ int launch_build(const BuildArgs& a, hipStream_t stream) {
 
 // Scratch of fmd_nl_build_noalloc: the count kernel's per-block partials (max displacement,
 // isolated atoms) for up to FMD_NL_BUILD_NOALLOC_MAX_ATOMS atoms. Every block writes its own
-// slot before the scan kernel reads it, so nothing in it has to start at zero. Host code never
+// slot before the materialize kernel reads it, so nothing in it has to start at zero. Host code never
 // passes the array's name to a kernel (on the host it is only a stand-in for the symbol): its
 // device address is looked up once per device and kept in scratch_ptr.
 static __device__ __align__(256) int64_t scratch[FMD_NL_BUILD_NOALLOC_SCRATCH];
@@ -1225,7 +1214,7 @@ int fmd_nl_build(const void* positions, int32_t pos_is_f64, const float* inv_cel
                  int32_t* edge_reverse, uint8_t* window_overflow, uint8_t* window_capacity,
                  int64_t* window_max_edges, int32_t* window_max_isolated, double* window_stats,
                  int32_t window_check_isolated, hipStream_t stream) {
-  FMD_REQUIRE(work && reinterpret_cast<uintptr_t>(work) % 16 == 0);  // the scan reads it 16 bytes at a time
+  FMD_REQUIRE(work && reinterpret_cast<uintptr_t>(work) % 16 == 0);  // its partials are read 16 bytes at a time
   FMD_REQUIRE(!window_overflow || (window_capacity && window_max_edges && window_max_isolated));
   BuildArgs a{positions, pos_is_f64, inv_cell, cell, n_atoms, neighbor_matrix, neighbor_shifts, num_neighbors, bmax,
               reference_positions, reference_wraps, capacity_valid, rc2, skin_limit, minimum_image, pad_ix, pad_iy, pad_iz,
@@ -1311,7 +1300,7 @@ int fmd_nl_reverse(const int32_t* center, const int32_t* neighbor, const int32_t
   FMD_REQUIRE(n_atoms > 0 && e_cap > 0 && center && neighbor && images && edge_offsets && reverse);
   const int threads = 256;
   hipLaunchKernelGGL(nl_reverse_kernel, dim3((unsigned)fmd_cdiv(e_cap, threads)), dim3(threads), 0, stream, center,
-                     neighbor, images, edge_offsets, n_atoms, e_cap, reverse);
+                     neighbor, images, edge_offsets, n_atoms, e_cap, reverse, RevWindow{});
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
