@@ -1089,10 +1089,19 @@ __global__ void zero_f64_kernel(double* x) { x[0] = 0.0; }
 // The float64 total of x[0 .. n) in fmd_sum_f64's fixed order (1 024 strided partials in index
 // order, then a pairwise tree over them), formed by the threads of one block.
 __device__ void sum_f64_order(const float* x, int64_t n, double* out, double* part) {
-  constexpr int kParts = 1024;
+  constexpr int kParts = 1024, kU = 8;
   for (int v = threadIdx.x; v < kParts; v += blockDim.x) {
+    // the same adds in the same order; eight loads in flight before their adds
     double s = 0.0;
-    for (int64_t k = v; k < n; k += kParts) s = s + (double)x[k];
+    int64_t k = v;
+    for (; k + (kU - 1) * kParts < n; k += kU * kParts) {
+      float t[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) t[u] = x[k + u * kParts];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) s = s + (double)t[u];
+    }
+    for (; k < n; k += kParts) s = s + (double)x[k];
     part[v] = s;
   }
   __syncthreads();

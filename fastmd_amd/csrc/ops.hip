@@ -242,8 +242,19 @@ __global__ void zero_rows_kernel(float* a, float* b, const int64_t* first_ptr, i
 template <typename T>
 __global__ void __launch_bounds__(1024) sum_f64_kernel(const T* x, int64_t n, double* out) {
   __shared__ double part[1024];
+  // the same adds in the same order; eight loads in flight before their adds
+  constexpr int kU = 8;
+  const int64_t step = blockDim.x;
   double s = 0.0;
-  for (int64_t k = threadIdx.x; k < n; k += blockDim.x) s = s + (double)x[k];
+  int64_t k = threadIdx.x;
+  for (; k + (kU - 1) * step < n; k += kU * step) {
+    T t[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) t[u] = x[k + u * step];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) s = s + (double)t[u];
+  }
+  for (; k < n; k += step) s = s + (double)x[k];
   part[threadIdx.x] = s;
   __syncthreads();
   for (int width = blockDim.x / 2; width > 0; width >>= 1) {

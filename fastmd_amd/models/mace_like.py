@@ -63,6 +63,10 @@ FUSED_NODE = False
 # is the edge GEMM over the gather-cat rows (the configs' wide-GEMM operator on the path), kept
 # tested against the oracle beside the factored form.
 FACTORED_Z = True
+# The energy launch forms the float64 total itself (its last workgroup) up to this many atoms; above,
+# a separate one-workgroup sum: each of the energy launch's workgroups fences at device scope, which
+# took that launch from 7 to 60 us at 10 000 atoms (2 500 workgroups).
+ENERGY_TOTAL_MAX_ATOMS = 2048
 # The first layer's output GEMM adds the per-element residual and next-layer rows in its epilogue
 # (above the small-system sizes) instead of accumulating onto outputs prefilled with them.
 ROWS_IN_EPILOGUE = True
@@ -859,7 +863,7 @@ class MaceLikeAdapter:
         saved = _Saved()
         # (small launches only: each of the energy launch's blocks fences at device scope)
         one = (isinstance(segments, int) and segments == 1 and inputs.sum_counter is not None
-               and positions.shape[0] <= SMALL_NODE_MAX_ATOMS)
+               and positions.shape[0] <= ENERGY_TOTAL_MAX_ATOMS)
         if one:
             # the fixed-order total of all rows, formed by the energy launch itself
             saved.total = torch.empty(1, dtype=torch.float64, device=positions.device)
