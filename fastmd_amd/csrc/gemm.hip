@@ -20,6 +20,11 @@
 //   D: lane l, register v holds D[(v/4)*8 + (l/32)*4 + v%4][l%32]
 #include "common.h"
 
+// thin.hip: the K <= 16 and N <= 16 shapes of fmd_gemm_f32; FMD_EUNSUPPORTED for the others
+__attribute__((visibility("hidden"))) int launch_gemm_thin(const float* a, int64_t lda, const float* b, int64_t ldb, int32_t b_layout, const float* bias,
+                     float* c, int64_t ldc, int64_t m, int64_t n, int64_t k, int32_t accumulate, int32_t act,
+                     hipStream_t stream);
+
 namespace {
 
 constexpr int BM = 128, BN = 128, kThreads = 256;
@@ -1387,6 +1392,11 @@ int fmd_gemm_f32(const float* a, int64_t lda, const float* b, int64_t ldb, int32
   if (m == 0 || n == 0) return FMD_OK;
   FMD_REQUIRE(k == 0 || (a && b && lda >= k && ldb >= (b_layout == 0 ? k : n)));
   FMD_REQUIRE(fmd_cdiv(m, 64) < (int64_t(1) << 31) && fmd_cdiv(n, 64) < 65536);
+  {
+    // K <= 16 or N <= 16: fp32 FMA chains on the vector ALUs (thin.hip)
+    const int st = launch_gemm_thin(a, lda, b, ldb, b_layout, bias, c, ldc, m, n, k, accumulate, epilogue_kind, stream);
+    if (st != FMD_EUNSUPPORTED) return st;
+  }
   const int64_t big_tiles = fmd_cdiv(m, 128) * fmd_cdiv(n, 128);
   if (big_tiles >= 256 && b_layout == 0 && k > 0 && k % 4 == 0) {
     // fp32-accurate on the bf16 matrix cores when the operands allow 16-byte loads (from 256

@@ -32,20 +32,35 @@ __device__ __forceinline__ int64_t real_rows_of(const int64_t* edge_offsets, int
   return t < e_cap ? t : e_cap;
 }
 
-// block-wide inclusive scan of one int64 per thread (1024 threads), through LDS
-__device__ __forceinline__ int64_t block_inclusive_scan(int64_t v, int64_t* sh) {
-  const int t = threadIdx.x;
-  sh[t] = v;
-  __syncthreads();
-  for (int off = 1; off < kLgBlock; off <<= 1) {
-    const int64_t add = t >= off ? sh[t - off] : 0;
-    __syncthreads();
-    sh[t] += add;
-    __syncthreads();
+// wave-wide inclusive scan of one int64 per lane (six shuffle steps)
+__device__ __forceinline__ int64_t wave_inclusive_scan(int64_t v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t u = __shfl_up(v, off, 64);
+    v += lane >= off ? u : 0;
   }
-  const int64_t r = sh[t];
+  return v;
+}
+
+// block-wide inclusive scan of one int64 per thread (1024 threads): scans within the waves, the
+// wave totals through LDS (sh: at least 16 entries), two barriers; integer sums, so the result is
+// the serial prefix whatever the order. `total` (optional): the block's sum.
+__device__ __forceinline__ int64_t block_inclusive_scan(int64_t v, int64_t* sh, int64_t* total = nullptr) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_inclusive_scan(v);
+  if (lane == 63) sh[wave] = v;
   __syncthreads();
-  return r;
+  int64_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kLgBlock / 64; ++w) {
+    const int64_t t = sh[w];
+    before += w < wave ? t : 0;
+    all += t;
+  }
+  if (total) *total = all;
+  __syncthreads();
+  return before + v;
 }
 
 __device__ __forceinline__ void leader_of(const int32_t* reverse, int64_t e, int64_t ec, bool& leader, bool& unmatched,
@@ -62,7 +77,7 @@ __device__ __forceinline__ void leader_of(const int32_t* reverse, int64_t e, int
 __global__ void __launch_bounds__(kLgBlock) lg_leader_count_kernel(const int32_t* reverse, const int64_t* edge_offsets,
                                                                     int64_t n, int64_t e_cap, int64_t nb,
                                                                     int64_t* work) {
-  __shared__ int64_t sh[kLgBlock];
+  __shared__ int64_t sh[kLgBlock / 64];
   const int64_t e = (int64_t)blockIdx.x * kLgBlock + threadIdx.x;
   const int64_t ec = real_rows_of(edge_offsets, n, e_cap);
   bool leader, unmatched;
@@ -79,7 +94,7 @@ __global__ void __launch_bounds__(kLgBlock) lg_leader_count_kernel(const int32_t
 // K2: one workgroup: exclusive scan of the block leader counts (in place), the invalid-pairs flag
 __global__ void __launch_bounds__(kLgBlock) lg_leader_scan_kernel(const int64_t* edge_offsets, int64_t n, int64_t nb,
                                                                    int64_t* work, uint8_t* invalid_pairs) {
-  __shared__ int64_t sh[kLgBlock];
+  __shared__ int64_t sh[kLgBlock / 64];
   __shared__ int64_t chunk;
   int64_t carry = 0, unmatched = 0;
   for (int64_t base = 0; base < nb; base += kLgBlock) {
@@ -105,7 +120,7 @@ __global__ void __launch_bounds__(kLgBlock) lg_leader_scan_kernel(const int64_t*
 __global__ void __launch_bounds__(kLgBlock) lg_leader_apply_kernel(const int32_t* reverse, const int64_t* edge_offsets,
                                                                     int64_t n, int64_t e_cap, const int64_t* work,
                                                                     int64_t* pfx) {
-  __shared__ int64_t sh[kLgBlock];
+  __shared__ int64_t sh[kLgBlock / 64];
   const int64_t e = (int64_t)blockIdx.x * kLgBlock + threadIdx.x;
   const int64_t ec = real_rows_of(edge_offsets, n, e_cap);
   bool leader, unmatched;
@@ -141,31 +156,41 @@ __global__ void __launch_bounds__(256) lg_short_kernel(const uint8_t* short_flag
   if (lane == 0) short_counts[i] = s;
 }
 
-// K5: one workgroup: exclusive scans of s and s (s - 1) over the atoms, the overflow flag
+// K5: one workgroup: exclusive scans of s and s (s - 1) over the atoms, the overflow flag. Each
+// thread takes kPairsPer consecutive atoms per pass (their loads in flight together), the block
+// scans the per-thread sums.
+constexpr int kPairsPer = 8;
+
 __global__ void __launch_bounds__(kLgBlock) lg_pairs_scan_kernel(const int64_t* short_counts, const int64_t* edge_offsets,
                                                                   const uint8_t* invalid_pairs,
                                                                   const uint8_t* candidate_valid, int64_t n,
                                                                   int64_t e_cap, int64_t t_cap, int64_t* short_offsets,
                                                                   int64_t* pair_offsets, uint8_t* overflow) {
-  __shared__ int64_t sh[kLgBlock];
-  __shared__ int64_t tot[2];
+  __shared__ int64_t sh[2][kLgBlock / 64];
   int64_t carry_s = 0, carry_p = 0;
-  for (int64_t base = 0; base < n; base += kLgBlock) {
-    const int64_t i = base + threadIdx.x;
-    const int64_t s = i < n ? short_counts[i] : 0;
-    const int64_t p = s * (s - 1);
-    const int64_t inc_s = block_inclusive_scan(s, sh);
-    if (threadIdx.x == kLgBlock - 1) tot[0] = inc_s;
-    const int64_t inc_p = block_inclusive_scan(p, sh);
-    if (threadIdx.x == kLgBlock - 1) tot[1] = inc_p;
-    __syncthreads();
-    if (i < n) {
-      short_offsets[i] = carry_s + inc_s - s;
-      pair_offsets[i] = carry_p + inc_p - p;
+  for (int64_t base = 0; base < n; base += (int64_t)kLgBlock * kPairsPer) {
+    const int64_t i0 = base + (int64_t)threadIdx.x * kPairsPer;
+    int64_t sv[kPairsPer], ts = 0, tp = 0;
+#pragma unroll
+    for (int k = 0; k < kPairsPer; ++k) sv[k] = i0 + k < n ? short_counts[i0 + k] : 0;
+#pragma unroll
+    for (int k = 0; k < kPairsPer; ++k) {
+      ts += sv[k];
+      tp += sv[k] * (sv[k] - 1);
     }
-    carry_s += tot[0];
-    carry_p += tot[1];
-    __syncthreads();
+    int64_t tot_s, tot_p;
+    int64_t ex_s = carry_s + block_inclusive_scan(ts, sh[0], &tot_s) - ts;
+    int64_t ex_p = carry_p + block_inclusive_scan(tp, sh[1], &tot_p) - tp;
+#pragma unroll
+    for (int k = 0; k < kPairsPer; ++k)
+      if (i0 + k < n) {
+        short_offsets[i0 + k] = ex_s;
+        pair_offsets[i0 + k] = ex_p;
+        ex_s += sv[k];
+        ex_p += sv[k] * (sv[k] - 1);
+      }
+    carry_s += tot_s;
+    carry_p += tot_p;
   }
   if (threadIdx.x == 0) {
     short_offsets[n] = carry_s;

@@ -59,45 +59,94 @@ __device__ __forceinline__ void run_of(const int64_t* off, int64_t s, int64_t ro
   lo = lo < hi ? lo : hi;
 }
 
+// The channel columns of a lane: c = lane + 64 cc (cc < NC); lanes past C read column C - 1 (a
+// real column, so every load stays in the row) and store nothing.
+template <int NC>
+struct LaneCols {
+  int col[NC];
+  bool live[NC];
+  __device__ __forceinline__ explicit LaneCols(int C) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int cc = 0; cc < NC; ++cc) {
+      const int c = lane + 64 * cc;
+      live[cc] = c < C;
+      col[cc] = c < C ? c : C - 1;
+    }
+  }
+};
+
+// the value of lane j (j wave-uniform)
+__device__ __forceinline__ float lane_value(float v, int j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+}
+
+// Rows per batch of the gated sums: a batch's loads (clamped to the run's last row) are all issued
+// before its arithmetic, and the rows past the run are masked out of the sums; a run of up to R
+// rows costs one memory round trip instead of one per four rows.
+template <int NC>
+constexpr int gated_batch() {
+  return NC == 1 ? 16 : 8;
+}
+
+template <int NC>
 __global__ void __launch_bounds__(256) tb_gated_sum_kernel(const float* z, int64_t ldz, int64_t rows, int C,
                                                             RowWeight rw, const int64_t* off, int64_t n_seg,
                                                             float scale, float* out, int64_t ldo, int accumulate) {
+  constexpr int R = gated_batch<NC>();
   const int lane = threadIdx.x & 63;
   const int64_t s = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   if (s >= n_seg) return;
   int64_t lo, hi;
   run_of(off, s, rows, lo, hi);
-  for (int c = lane; c < C; c += 64) {
-    float acc = 0.f;
-    // four rows' loads in flight before their arithmetic (the sum stays in row order)
-    for (int64_t r = lo; r < hi; r += 4) {
-      const int m = hi - r >= 4 ? 4 : (int)(hi - r);
-      float x[4], w[4];
+  const LaneCols<NC> lc(C);
+  float* o = out + s * ldo;
+  float old[NC], acc[NC];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (j < m) {
-          x[j] = z[(r + j) * ldz + c];
-          w[j] = rw.w1(r + j) * rw.w2(r + j);
-        }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (j < m) acc += x[j] * tb_sigmoid(x[j]) * w[j];
-    }
-    float* o = out + s * ldo + c;
-    *o = accumulate ? *o + scale * acc : scale * acc;
+  for (int cc = 0; cc < NC; ++cc) {
+    old[cc] = accumulate ? o[lc.col[cc]] : 0.f;
+    acc[cc] = 0.f;
   }
+  for (int64_t r0 = lo; r0 < hi; r0 += R) {
+    const int m = hi - r0 >= R ? R : (int)(hi - r0);
+    // the batch's row weights one per lane (lane j: row j), read back per row from that lane
+    const int64_t rl = r0 + (lane < m ? lane : m - 1);
+    const float wl = rw.w1(rl) * rw.w2(rl);
+    float x[R][NC];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int64_t r = r0 + (j < m ? j : m - 1);
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) x[j][cc] = z[r * ldz + lc.col[cc]];
+    }
+    // rows in order; the masked rows leave the sum as it is
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const float w = lane_value(wl, j);
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) {
+        const float v = x[j][cc] * tb_sigmoid(x[j][cc]) * w;
+        acc[cc] = j < m ? acc[cc] + v : acc[cc];
+      }
+    }
+  }
+#pragma unroll
+  for (int cc = 0; cc < NC; ++cc)
+    if (lc.live[cc]) o[lc.col[cc]] = accumulate ? old[cc] + scale * acc[cc] : scale * acc[cc];
 }
 
 // VJP: per row of run s, with g = scale * gout[s]: gz[r] = g w(r) silu'(z[r]) and
 // gw(r) = sum_c g silu(z[r]) (the weight's gradient; with two indices written as the two
 // envelopes' terms (gw w2, gw w1); added to gw with acc_gw); gsum[s] = sum_r gz[r]. Rows past the
 // last run: gz = 0, gw = 0 (left as they are with acc_gw).
+template <int NC>
 __global__ void __launch_bounds__(256) tb_gated_sum_bwd_kernel(const float* gout, int64_t ldg, const float* z,
                                                                 int64_t ldz, int64_t rows, int C, RowWeight rw,
                                                                 const int64_t* off, int64_t n_seg, float scale,
                                                                 float* gz, int64_t ldgz, float* gsum, int64_t ldgs,
                                                                 float* gw, int64_t ldgw, int acc_gw,
                                                                 int64_t seg_blocks) {
+  constexpr int R = gated_batch<NC>();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   if ((int64_t)blockIdx.x >= seg_blocks) {
@@ -114,57 +163,55 @@ __global__ void __launch_bounds__(256) tb_gated_sum_bwd_kernel(const float* gout
   if (s >= n_seg) return;
   int64_t lo, hi;
   run_of(off, s, rows, lo, hi);
-  // C <= 256: up to four channels per lane
-  float g[4], acc[4];
-  const int nc = (C + 63) / 64;
+  const LaneCols<NC> lc(C);
+  const bool two = rw.i2 != nullptr, old_gw = gw && acc_gw;
+  float g[NC], acc[NC];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int c = lane + 64 * k;
-    g[k] = (k < nc && c < C) ? scale * gout[s * ldg + c] : 0.f;
-    acc[k] = 0.f;
+  for (int cc = 0; cc < NC; ++cc) {
+    g[cc] = lc.live[cc] ? scale * gout[s * ldg + lc.col[cc]] : 0.f;
+    acc[cc] = 0.f;
   }
-  for (int64_t r0 = lo; r0 < hi; r0 += 4) {
-    // four rows' loads in flight before their arithmetic (rows still handled in order)
-    const int m = hi - r0 >= 4 ? 4 : (int)(hi - r0);
-    float xs[4][4], wa[4], wb[4];
+  for (int64_t r0 = lo; r0 < hi; r0 += R) {
+    const int m = hi - r0 >= R ? R : (int)(hi - r0);
+    // every load of the batch before its arithmetic: the rows, and one per lane (lane j: row j)
+    // the row's weights and old weight gradients, read back per row from that lane
+    const int64_t rl = r0 + (lane < m ? lane : m - 1);
+    const float wal = rw.w1(rl), wbl = rw.w2(rl);
+    const float go0 = old_gw ? gw[rl * ldgw] : 0.f, go1 = old_gw && two ? gw[rl * ldgw + 1] : 0.f;
+    float xs[R][NC];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (j < m) {
-        wa[j] = rw.w1(r0 + j);
-        wb[j] = rw.w2(r0 + j);
+    for (int j = 0; j < R; ++j) {
+      const int64_t r = r0 + (j < m ? j : m - 1);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int c = lane + 64 * k;
-          xs[j][k] = (k < nc && c < C) ? z[(r0 + j) * ldz + c] : 0.f;
-        }
-      }
+      for (int cc = 0; cc < NC; ++cc) xs[j][cc] = z[r * ldz + lc.col[cc]];
+    }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j >= m) break;
+    for (int j = 0; j < R; ++j) {
       const int64_t r = r0 + j;
-      const float a = wa[j], b = wb[j], w = a * b;
-      float p = 0.f;
+      const float a = lane_value(wal, j), b = lane_value(wbl, j), w = a * b;
+      float p = 0.f, v[NC];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int c = lane + 64 * k;
-        if (k < nc && c < C) {
-          const float x = xs[j][k];
-          const float sg = tb_sigmoid(x);
-          const float si = x * sg;
-          const float v = g[k] * w * (sg + si * (1.0f - sg));
-          gz[r * ldgz + c] = v;
-          acc[k] += v;
-          p += g[k] * si;
-        }
+      for (int cc = 0; cc < NC; ++cc) {
+        const float x = xs[j][cc];
+        const float sg = tb_sigmoid(x);
+        const float si = x * sg;
+        v[cc] = g[cc] * w * (sg + si * (1.0f - sg));
+        acc[cc] = j < m ? acc[cc] + v[cc] : acc[cc];
+        p += g[cc] * si;  // g = 0 on the lanes past C
+      }
+      if (j < m) {
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc)
+          if (lc.live[cc]) gz[r * ldgz + lc.col[cc]] = v[cc];
       }
       if (gw) {
         const float t = wave_sum(p);
-        if (lane == 0) {
-          if (rw.i2) {
-            gw[r * ldgw] = (acc_gw ? gw[r * ldgw] : 0.f) + t * b;
-            gw[r * ldgw + 1] = (acc_gw ? gw[r * ldgw + 1] : 0.f) + t * a;
+        if (j < m && lane == 0) {
+          if (two) {
+            gw[r * ldgw] = lane_value(go0, j) + t * b;
+            gw[r * ldgw + 1] = lane_value(go1, j) + t * a;
           } else {
-            gw[r * ldgw] = (acc_gw ? gw[r * ldgw] : 0.f) + t;
+            gw[r * ldgw] = lane_value(go0, j) + t;
           }
         }
       }
@@ -172,10 +219,8 @@ __global__ void __launch_bounds__(256) tb_gated_sum_bwd_kernel(const float* gout
   }
   if (gsum) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int c = lane + 64 * k;
-      if (k < nc && c < C) gsum[s * ldgs + c] = acc[k];
-    }
+    for (int cc = 0; cc < NC; ++cc)
+      if (lc.live[cc]) gsum[s * ldgs + lc.col[cc]] = acc[cc];
   }
 }
 
@@ -236,9 +281,10 @@ __global__ void tb_geometry_bwd_kernel(const float* geo, const float* def, int n
 // ---- angle -> bond sums over the line graph. The work is a few bonds and triplets per atom, far
 // fewer than the edge rows: each kernel runs a fixed grid of waves that strides over the real
 // bonds (bond_rows[0, short_offsets[n])) or triplets ([0, pair_offsets[n])), counts read on the
-// device, one bond or triplet per wave at a time (channels across the lanes). A bond's triplets
-// as first bond are the run [eto[b], eto[b+1]) of the line graph (contiguous), as second bond
-// the same run through second_perm.
+// device, several bonds or triplets per wave and pass (channels across the lanes) whose loads are
+// all issued before their arithmetic: one chain of dependent loads per pass, not per item. A
+// bond's triplets as first bond are the run [eto[b], eto[b+1]) of the line graph (contiguous), as
+// second bond the same run through second_perm.
 struct LineCsr {
   const int64_t* short_offsets;  // [n + 1]: the bond count at [n]
   const int32_t* bond_rows;      // [e_cap]
@@ -256,145 +302,315 @@ __device__ __forceinline__ int64_t wave_id() {
   return (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
 }
 
+// The index work of a pass runs across the lanes (one load instruction per level of the chain
+// bond_rows -> eto -> line graph / second_perm -> envelope for all of the pass's bonds or
+// triplets), the channel rows across the wave with the indices read back per lane: a pass costs
+// one chain of dependent loads, whatever the number of bonds or triplets in it.
+__device__ __forceinline__ int lane_int(int v, int j) { return __builtin_amdgcn_readlane(v, j); }
+
+// Lane q < U: bond slot q of the pass (bond j0 + q NW of bond_rows; past the count the pass's
+// first bond again, loaded and not stored) with its run [lo, hi) of triplets as first bond,
+// clamped to t_cap.
+template <int U>
+struct BondSlots {
+  int b, lo, hi;
+  bool ok;
+  __device__ __forceinline__ BondSlots(const LineCsr& lc, int64_t j0, int64_t nw, int64_t nb) {
+    const int lane = threadIdx.x & 63;
+    const int64_t j = j0 + (lane < U ? lane : 0) * nw;
+    ok = j < nb;
+    b = lc.bond_rows[ok ? j : j0];
+    int64_t l = lc.eto[b], h = lc.eto[(int64_t)b + 1];
+    h = h < lc.t_cap ? h : lc.t_cap;
+    l = l < h ? l : h;
+    lo = (int)l;
+    hi = (int)h;
+  }
+  __device__ __forceinline__ int64_t bond(int q) const { return lane_int(b, q); }
+  __device__ __forceinline__ int64_t count(int q) const { return lane_int(hi, q) - lane_int(lo, q); }
+  __device__ __forceinline__ bool stored(int q) const { return lane_int(ok ? 1 : 0, q) != 0; }
+  // on lane l: triplet t of bond q's run, clamped to its last triplet (row 0 for an empty run,
+  // whose loads are then not used as addresses)
+  __device__ __forceinline__ int64_t slot_row(int q, int t, bool& empty) const {
+    const int l = __shfl(lo, q, 64), h = __shfl(hi, q, 64);
+    empty = h <= l;
+    return l + t < h ? l + t : (h > l ? h - 1 : 0);
+  }
+};
+
+// bonds per pass and triplets per bond whose loads go out together (longer runs finish in a loop)
+template <int NC>
+constexpr int bond_pass() {
+  return NC == 1 ? 4 : 2;
+}
+constexpr int kRunBatch = 4;
+
 // eps[b] += scale * sum over b's triplets (first bond), in order, of silu(z3[k]) s_b s_b2
+template <int NC>
 __global__ void __launch_bounds__(256) tb_bond_sum_kernel(LineCsr lc, const float* z3, int64_t ldz, int C,
                                                            const float* geo, float scale, float* eps, int64_t lde) {
+  constexpr int U = bond_pass<NC>(), TQ = kRunBatch;
   const int lane = threadIdx.x & 63;
-  const int nc = (C + 63) / 64;
-  const int64_t nb = lc.short_offsets[lc.n];
-  for (int64_t j = wave_id(); j < nb; j += (int64_t)gridDim.x * 4) {
-    const int64_t b = lc.bond_rows[j];
-    const float w1 = geo[8 * b + 6];
-    int64_t lo = lc.eto[b], hi = lc.eto[b + 1];
-    hi = hi < lc.t_cap ? hi : lc.t_cap;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    // four triplets' loads in flight before their arithmetic (the sum stays in triplet order)
-    for (int64_t k0 = lo; k0 < hi; k0 += 4) {
-      const int m = hi - k0 >= 4 ? 4 : (int)(hi - k0);
-      float x[4][4], w[4];
+  const LaneCols<NC> cols(C);
+  const int64_t nb = lc.short_offsets[lc.n], nw = (int64_t)gridDim.x * 4;
+  for (int64_t j0 = wave_id(); j0 < nb; j0 += U * nw) {
+    const BondSlots<U> bs(lc, j0, nw, nb);
+    float old[U][NC], x[U][TQ][NC];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (q < m) {
-          w[q] = w1 * geo[8 * (int64_t)lc.line[5 * (k0 + q) + 4] + 6];
+    for (int q = 0; q < U; ++q)
 #pragma unroll
-          for (int cc = 0; cc < 4; ++cc) {
-            const int c = lane + 64 * cc;
-            x[q][cc] = (cc < nc && c < C) ? z3[(k0 + q) * ldz + c] : 0.f;
-          }
+      for (int cc = 0; cc < NC; ++cc) old[q][cc] = eps[bs.bond(q) * lde + cols.col[cc]];
+    // lane l < U TQ: triplet slot (l / TQ, l % TQ) and its weight s_b s_b2
+    const int qs = lane < U * TQ ? lane / TQ : 0;
+    bool empty;
+    const int64_t ks = bs.slot_row(qs, lane % TQ, empty);
+    const int b2raw = lc.line[5 * ks + 4];
+#pragma unroll
+    for (int q = 0; q < U; ++q)
+#pragma unroll
+      for (int t = 0; t < TQ; ++t) {
+        const int64_t k = lane_int((int)ks, q * TQ + t);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) x[q][t][cc] = z3[k * ldz + cols.col[cc]];
+      }
+    const int bq = __shfl(bs.b, qs, 64);
+    const float w1 = geo[8 * (int64_t)bq + 6];
+    const float ws = w1 * geo[8 * (int64_t)(empty ? bq : b2raw) + 6];
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      float acc[NC];
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) acc[cc] = 0.f;
+      const int64_t cnt = bs.count(q);
+#pragma unroll
+      for (int t = 0; t < TQ; ++t) {
+        const float w = lane_value(ws, q * TQ + t);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+          const float v = x[q][t][cc] * tb_sigmoid(x[q][t][cc]) * w;
+          acc[cc] = t < cnt ? acc[cc] + v : acc[cc];
+        }
+      }
+      // the rest of a longer run, four triplets' loads at a time
+      const int64_t lo = lane_int(bs.lo, q), hi = lane_int(bs.hi, q);
+      const float w1q = lane_value(w1, q * TQ);
+      for (int64_t k0 = lo + TQ; k0 < hi; k0 += 4) {
+        const int m = hi - k0 >= 4 ? 4 : (int)(hi - k0);
+        float y[4][NC], wy[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int64_t k = k0 + (t < m ? t : m - 1);
+          wy[t] = w1q * geo[8 * (int64_t)lc.line[5 * k + 4] + 6];
+#pragma unroll
+          for (int cc = 0; cc < NC; ++cc) y[t][cc] = z3[k * ldz + cols.col[cc]];
         }
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (q < m)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int cc = 0; cc < 4; ++cc) acc[cc] += x[q][cc] * tb_sigmoid(x[q][cc]) * w[q];
-    }
+          for (int cc = 0; cc < NC; ++cc) {
+            const float v = y[t][cc] * tb_sigmoid(y[t][cc]) * wy[t];
+            acc[cc] = t < m ? acc[cc] + v : acc[cc];
+          }
+      }
+      if (bs.stored(q)) {
+        const int64_t b = bs.bond(q);
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      const int c = lane + 64 * cc;
-      if (cc < nc && c < C) eps[b * lde + c] += scale * acc[cc];
+        for (int cc = 0; cc < NC; ++cc)
+          if (cols.live[cc]) eps[b * lde + cols.col[cc]] = old[q][cc] + scale * acc[cc];
+      }
     }
   }
 }
 
-// Per triplet k (one wave): with g = scale geps[b1], gz3[k] = g s_b1 s_b2 silu'(z3[k]) and
+// triplets per pass of the triplet VJP
+template <int NC>
+constexpr int triplet_pass() {
+  return NC == 1 ? 8 : 4;
+}
+
+// Per triplet k: with g = scale geps[b1], gz3[k] = g s_b1 s_b2 silu'(z3[k]) and
 // gw = sum_c g silu(z3[k]), stored as the envelope terms gsw[k] = (gw s_b2, gw s_b1). Rows past
 // the real triplets: gz3 = 0.
+template <int NC>
 __global__ void __launch_bounds__(256) tb_triplet_bwd_kernel(LineCsr lc, const float* geps, int64_t ldg,
                                                               const float* z3, int64_t ldz, int C, const float* geo,
                                                               float scale, float* gz3, int64_t ldgz, float* gsw) {
+  constexpr int U = triplet_pass<NC>();
   const int lane = threadIdx.x & 63;
-  const int nc = (C + 63) / 64;
+  const LaneCols<NC> cols(C);
   const int64_t t_all = lc.pair_offsets[lc.n];
   const int64_t t_real = t_all < lc.t_cap ? t_all : lc.t_cap;
-  for (int64_t k = wave_id(); k < lc.t_cap; k += (int64_t)gridDim.x * 4) {
-    if (k >= t_real) {
-      for (int c = lane; c < C; c += 64) gz3[k * ldgz + c] = 0.f;
-      continue;
-    }
-    const int64_t b1 = lc.line[5 * k + 2], b2 = lc.line[5 * k + 4];
-    const float w1 = geo[8 * b1 + 6], w2 = geo[8 * b2 + 6], w = w1 * w2;
-    float g[4], x[4];
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  for (int64_t k0 = wave_id(); k0 < lc.t_cap; k0 += U * nw) {
+    // lane q < U: triplet slot q (k0 + q NW); a slot past the real triplets loads line-graph row 0
+    // and edge row 0 (in bounds, unused)
+    const int64_t kl = k0 + (lane < U ? lane : 0) * nw;
+    const bool real = kl < t_real;
+    const int64_t kr = real ? kl : 0;
+    const int r1 = lc.line[5 * kr + 2], r2 = lc.line[5 * kr + 4];
+    float x[U][NC], g[U][NC];
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      const int c = lane + 64 * cc;
-      const bool ok = cc < nc && c < C;
-      g[cc] = ok ? scale * geps[b1 * ldg + c] : 0.f;
-      x[cc] = ok ? z3[k * ldz + c] : 0.f;
-    }
-    float p = 0.f;
+    for (int q = 0; q < U; ++q) {
+      const int64_t kq = k0 + q * nw < t_real ? k0 + q * nw : 0;
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      const int c = lane + 64 * cc;
-      if (cc < nc && c < C) {
-        const float sg = tb_sigmoid(x[cc]);
-        const float si = x[cc] * sg;
-        gz3[k * ldgz + c] = g[cc] * w * (sg + si * (1.0f - sg));
-        p += g[cc] * si;
+      for (int cc = 0; cc < NC; ++cc) x[q][cc] = z3[kq * ldz + cols.col[cc]];
+    }
+    const int b1 = real ? r1 : 0, b2 = real ? r2 : 0;
+    const float w1l = geo[8 * (int64_t)b1 + 6], w2l = geo[8 * (int64_t)b2 + 6];
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      const int64_t b = lane_int(b1, q);
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) g[q][cc] = scale * geps[b * ldg + cols.col[cc]];
+    }
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      const int64_t kq = k0 + q * nw;
+      if (kq >= lc.t_cap) continue;
+      float* out = gz3 + kq * ldgz;
+      if (kq >= t_real) {
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc)
+          if (cols.live[cc]) out[cols.col[cc]] = 0.f;
+        continue;
       }
-    }
-    const float gw = wave_sum(p);
-    if (lane == 0) {
-      gsw[2 * k] = gw * w2;
-      gsw[2 * k + 1] = gw * w1;
+      const float w1 = lane_value(w1l, q), w2 = lane_value(w2l, q), w = w1 * w2;
+      float p = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) {
+        const float sg = tb_sigmoid(x[q][cc]);
+        const float si = x[q][cc] * sg;
+        if (cols.live[cc]) {
+          out[cols.col[cc]] = g[q][cc] * w * (sg + si * (1.0f - sg));
+          p += g[q][cc] * si;
+        }
+      }
+      const float gw = wave_sum(p);
+      if (lane == 0) {
+        gsw[2 * kq] = gw * w2;
+        gsw[2 * kq + 1] = gw * w1;
+      }
     }
   }
 }
 
-// Per bond b (one wave): geps[b] += sum over b's triplets as first bond of ga3[k, 0:C], then as
-// second bond of ga3[k, C:2C]; gs[b] (+)= the same sums of gsw[k, 0] and gsw[k, 1] (stored, or
-// added with acc_gs).
+// Per bond b: geps[b] += sum over b's triplets as first bond of ga3[k, 0:C], then as second bond
+// of ga3[k, C:2C]; gs[b] (+)= the same sums of gsw[k, 0] and gsw[k, 1] (stored, or added with
+// acc_gs). A second-bond slot of -1 (no triplet) adds zeros.
+template <int NC>
 __global__ void __launch_bounds__(256) tb_bond_reduce_kernel(LineCsr lc, const float* ga3, int64_t lda, int C,
                                                               const float* gsw, float* geps, int64_t ldg, float* gs,
                                                               int acc_gs) {
+  constexpr int U = bond_pass<NC>(), TQ = kRunBatch;
   const int lane = threadIdx.x & 63;
-  const int nc = (C + 63) / 64;
-  const int64_t nb = lc.short_offsets[lc.n];
-  for (int64_t j = wave_id(); j < nb; j += (int64_t)gridDim.x * 4) {
-    const int64_t b = lc.bond_rows[j];
-    int64_t lo = lc.eto[b], hi = lc.eto[b + 1];
-    hi = hi < lc.t_cap ? hi : lc.t_cap;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    float gsum = 0.f;
-    for (int role = 0; role < 2; ++role) {
-      for (int64_t p0 = lo; p0 < hi; p0 += 4) {
-        const int m = hi - p0 >= 4 ? 4 : (int)(hi - p0);
-        int64_t kk[4];
-        float x[4][4], sw[4];
+  const LaneCols<NC> cols(C);
+  const int64_t nb = lc.short_offsets[lc.n], nw = (int64_t)gridDim.x * 4;
+  for (int64_t j0 = wave_id(); j0 < nb; j0 += U * nw) {
+    const BondSlots<U> bs(lc, j0, nw, nb);
+    const float gs_l = acc_gs ? gs[bs.b] : 0.f;
+    float old[U][NC], x[U][2][TQ][NC];
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (q < m) kk[q] = role == 0 ? p0 + q : (int64_t)lc.second_perm[p0 + q];
+    for (int q = 0; q < U; ++q)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (q < m) {
-            const bool real = kk[q] >= 0;
-            sw[q] = real ? gsw[2 * kk[q] + role] : 0.f;
+      for (int cc = 0; cc < NC; ++cc) old[q][cc] = geps[bs.bond(q) * ldg + cols.col[cc]];
+    // lane l < 2 U TQ: role l / (U TQ), slot ((l % U TQ) / TQ, l % TQ); role 1 through second_perm
+    const int sl = lane % (U * TQ), role_l = lane < U * TQ ? 0 : 1;
+    bool empty;
+    const int64_t pl = bs.slot_row(lane < 2 * U * TQ ? sl / TQ : 0, sl % TQ, empty);
+    const int sp = lc.second_perm[pl];
 #pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
-              const int c = lane + 64 * cc;
-              x[q][cc] = (real && cc < nc && c < C) ? ga3[kk[q] * lda + role * C + c] : 0.f;
+    for (int q = 0; q < U; ++q)
+#pragma unroll
+      for (int t = 0; t < TQ; ++t) {
+        const int64_t k = lane_int((int)pl, q * TQ + t);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) x[q][0][t][cc] = ga3[k * lda + cols.col[cc]];
+      }
+    const int kk = role_l == 0 ? (int)pl : (empty ? -1 : sp);
+    const float sw = gsw[2 * (int64_t)(kk >= 0 ? kk : 0) + role_l];
+#pragma unroll
+    for (int q = 0; q < U; ++q)
+#pragma unroll
+      for (int t = 0; t < TQ; ++t) {
+        const int k = lane_int(kk, U * TQ + q * TQ + t);
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) x[q][1][t][cc] = ga3[(int64_t)(k >= 0 ? k : 0) * lda + C + cols.col[cc]];
+      }
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      float acc[NC], gsum = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) acc[cc] = 0.f;
+      const int64_t cnt = bs.count(q), lo = lane_int(bs.lo, q), hi = lane_int(bs.hi, q);
+#pragma unroll
+      for (int role = 0; role < 2; ++role) {
+#pragma unroll
+        for (int t = 0; t < TQ; ++t) {
+          const int l = role * U * TQ + q * TQ + t;
+          const bool use = t < cnt, ok = lane_int(kk, l) >= 0;
+#pragma unroll
+          for (int cc = 0; cc < NC; ++cc) {
+            const float v = ok ? x[q][role][t][cc] : 0.f;
+            acc[cc] = use ? acc[cc] + v : acc[cc];
+          }
+          const float v = ok ? lane_value(sw, l) : 0.f;
+          gsum = use ? gsum + v : gsum;
+        }
+        // the rest of a longer run, four slots' loads at a time
+        for (int64_t p0 = lo + TQ; p0 < hi; p0 += 4) {
+          const int m = hi - p0 >= 4 ? 4 : (int)(hi - p0);
+          int64_t ky[4];
+          float y[4][NC], sy[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int64_t p = p0 + (t < m ? t : m - 1);
+            ky[t] = role == 0 ? p : (int64_t)lc.second_perm[p];
+          }
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int64_t k = ky[t] >= 0 ? ky[t] : 0;
+            sy[t] = gsw[2 * k + role];
+#pragma unroll
+            for (int cc = 0; cc < NC; ++cc) y[t][cc] = ga3[k * lda + role * C + cols.col[cc]];
+          }
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const bool use = t < m, ok = ky[t] >= 0;
+#pragma unroll
+            for (int cc = 0; cc < NC; ++cc) {
+              const float v = ok ? y[t][cc] : 0.f;
+              acc[cc] = use ? acc[cc] + v : acc[cc];
             }
+            const float v = ok ? sy[t] : 0.f;
+            gsum = use ? gsum + v : gsum;
           }
+        }
+      }
+      if (bs.stored(q)) {
+        const int64_t b = bs.bond(q);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (q < m) {
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) acc[cc] += x[q][cc];
-            gsum += sw[q];
-          }
+        for (int cc = 0; cc < NC; ++cc)
+          if (cols.live[cc]) geps[b * ldg + cols.col[cc]] = old[q][cc] + acc[cc];
+        if (lane == 0) gs[b] = lane_value(gs_l, q) + gsum;
       }
     }
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      const int c = lane + 64 * cc;
-      if (cc < nc && c < C) geps[b * ldg + c] += acc[cc];
-    }
-    if (lane == 0) gs[b] = (acc_gs ? gs[b] : 0.f) + gsum;
   }
 }
 
 RowWeight make_weight(const float* w, int64_t ldw, const int32_t* i1, const int32_t* i2, int64_t ld_idx) {
   return RowWeight{w, ldw, i1, i2, ld_idx};
 }
+
+// launch of KERNEL<NC> with NC = ceil(channels / 64) (channels <= 256)
+#define TB_LAUNCH_NC(KERNEL, CHANNELS, GRID, ...)                                              \
+  do {                                                                                        \
+    switch (fmd_cdiv((CHANNELS), 64)) {                                                       \
+      case 1: hipLaunchKernelGGL(KERNEL<1>, GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+      case 2: hipLaunchKernelGGL(KERNEL<2>, GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+      case 3: hipLaunchKernelGGL(KERNEL<3>, GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+      default: hipLaunchKernelGGL(KERNEL<4>, GRID, dim3(256), 0, stream, __VA_ARGS__); break; \
+    }                                                                                         \
+  } while (0)
 
 }  // namespace
 
@@ -419,9 +635,8 @@ int fmd_tb_gated_sum_f32(const float* z, int64_t ldz, int64_t rows, int32_t chan
               ldo >= channels && (index1 || !index2));
   if (n_segments == 0) return FMD_OK;
   FMD_REQUIRE(z && w && offsets && out);
-  hipLaunchKernelGGL(tb_gated_sum_kernel, dim3((unsigned)fmd_cdiv(n_segments, 4)), dim3(256), 0, stream, z, ldz, rows,
-                     channels, make_weight(w, ldw, index1, index2, ld_index), offsets, n_segments, scale, out, ldo,
-                     accumulate);
+  TB_LAUNCH_NC(tb_gated_sum_kernel, channels, dim3((unsigned)fmd_cdiv(n_segments, 4)), z, ldz, rows, channels,
+               make_weight(w, ldw, index1, index2, ld_index), offsets, n_segments, scale, out, ldo, accumulate);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -440,9 +655,9 @@ int fmd_tb_gated_sum_bwd_f32(const float* gout, int64_t ldg, const float* z, int
   const int64_t seg_blocks = fmd_cdiv(n_segments, 4);
   int64_t tail_blocks = fmd_cdiv(rows, 4);
   tail_blocks = tail_blocks < 1 ? 1 : (tail_blocks > 512 ? 512 : tail_blocks);
-  hipLaunchKernelGGL(tb_gated_sum_bwd_kernel, dim3((unsigned)(seg_blocks + tail_blocks)), dim3(256), 0, stream, gout,
-                     ldg, z, ldz, rows, channels, make_weight(w, ldw, index1, index2, ld_index), offsets, n_segments,
-                     scale, gz, ldgz, gsum, ldgs, gw, ldgw, accumulate_gw, seg_blocks);
+  TB_LAUNCH_NC(tb_gated_sum_bwd_kernel, channels, dim3((unsigned)(seg_blocks + tail_blocks)), gout, ldg, z, ldz, rows,
+               channels, make_weight(w, ldw, index1, index2, ld_index), offsets, n_segments, scale, gz, ldgz, gsum,
+               ldgs, gw, ldgw, accumulate_gw, seg_blocks);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -454,8 +669,7 @@ int fmd_tb_bond_sum_f32(const float* z3, int64_t ldz, int32_t channels, const fl
   if (n_atoms == 0 || t_cap == 0) return FMD_OK;
   FMD_REQUIRE(z3 && geo && short_offsets && bond_rows && edge_triplet_offsets && line_graph && eps);
   LineCsr lc{short_offsets, bond_rows, edge_triplet_offsets, nullptr, line_graph, nullptr, n_atoms, t_cap};
-  hipLaunchKernelGGL(tb_bond_sum_kernel, dim3(kStrideBlocks), dim3(256), 0, stream, lc, z3, ldz, channels, geo, scale,
-                     eps, lde);
+  TB_LAUNCH_NC(tb_bond_sum_kernel, channels, dim3(kStrideBlocks), lc, z3, ldz, channels, geo, scale, eps, lde);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -468,8 +682,8 @@ int fmd_tb_triplet_bwd_f32(const float* geps, int64_t ldg, const float* z3, int6
   if (n_atoms == 0 || t_cap == 0) return FMD_OK;
   FMD_REQUIRE(geps && z3 && geo && line_graph && pair_offsets && gz3 && gsw);
   LineCsr lc{nullptr, nullptr, nullptr, nullptr, line_graph, pair_offsets, n_atoms, t_cap};
-  hipLaunchKernelGGL(tb_triplet_bwd_kernel, dim3(kStrideBlocks), dim3(256), 0, stream, lc, geps, ldg, z3, ldz,
-                     channels, geo, scale, gz3, ldgz, gsw);
+  TB_LAUNCH_NC(tb_triplet_bwd_kernel, channels, dim3(kStrideBlocks), lc, geps, ldg, z3, ldz, channels, geo, scale, gz3,
+               ldgz, gsw);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -483,8 +697,8 @@ int fmd_tb_bond_reduce_f32(const float* ga3, int64_t lda, int32_t channels, cons
   if (n_atoms == 0 || t_cap == 0) return FMD_OK;
   FMD_REQUIRE(ga3 && gsw && short_offsets && bond_rows && edge_triplet_offsets && second_perm && geps && gs);
   LineCsr lc{short_offsets, bond_rows, edge_triplet_offsets, second_perm, nullptr, nullptr, n_atoms, t_cap};
-  hipLaunchKernelGGL(tb_bond_reduce_kernel, dim3(kStrideBlocks), dim3(256), 0, stream, lc, ga3, lda, channels, gsw, geps,
-                     ldg, gs, accumulate_gs);
+  TB_LAUNCH_NC(tb_bond_reduce_kernel, channels, dim3(kStrideBlocks), lc, ga3, lda, channels, gsw, geps, ldg, gs,
+               accumulate_gs);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }

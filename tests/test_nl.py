@@ -594,10 +594,11 @@ def _assert_line_equal(builder, b, lg):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("n_atoms,line_cutoff", [(135, 3.5), (1080, 3.0), (5000, 3.0), (5000, 3.5)])
+@pytest.mark.parametrize("n_atoms,line_cutoff", [(135, 3.5), (1080, 3.0), (5000, 3.0), (5000, 3.5), (10000, 3.5)])
 def test_line_graph_builder_bit_exact(device, n_atoms, line_cutoff):
     """The HIP line graph (short-bond flags, undirected pairs, short lists, pair offsets, triplet
-    rows, flags) bit-exact vs the oracle on the fused (<= 1 024 atoms) and multi-block builds."""
+    rows, flags) bit-exact vs the oracle on the fused (<= 1 024 atoms) and multi-block builds
+    (10 000 atoms: the pair scan's workgroup takes two passes of 8 192 atoms)."""
     import torch
 
     print(f"[line graph] n_atoms={n_atoms} cutoff={line_cutoff}", flush=True)

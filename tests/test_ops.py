@@ -223,6 +223,46 @@ def test_gemm_fp32_against_fp64(device, F, m):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("b_layout", [0, 1])
+def test_gemm_thin_shapes_against_fp64(device, b_layout):
+    """fmd_gemm_f32 on K <= 16 (outer-product form) and N <= 16 (row-dot form): ragged M, every K
+    bucket, N up to 256, a row pitch that is not a multiple of 4 (scalar loads), bias, accumulate
+    and the SiLU epilogue, within 1e-6 of float64 (fp32 FMA chains; 1e-5 past K = 256, where K = 1 000
+    with N = 16 exceeds the row-dot form's LDS and takes the matrix-core path); rows are independent
+    of the launch's other rows (the same bits for a slice) and run-to-run bitwise."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm
+
+    g = torch.Generator().manual_seed(21)
+    shapes = [(1, 1, 1), (37, 3, 5), (1000, 8, 64), (38401, 9, 256), (777, 16, 200), (500, 12, 130),
+              (100, 3, 9), (5000, 64, 8), (38401, 256, 9), (333, 800, 16), (333, 1000, 16), (777, 130, 4),
+              (64, 17, 1)]
+    for i, (m, k, n) in enumerate(shapes):
+        print(f"[gemm thin] m={m} k={k} n={n} layout={b_layout}", flush=True)
+        a = torch.randn(m, k + 3, generator=g)[:, :k] if i % 3 == 2 else torch.randn(m, k, generator=g)
+        w = torch.randn(k, n, generator=g) / k ** 0.5
+        wb = w if b_layout == 1 else w.t().contiguous()
+        bias = torch.randn(n, generator=g) if i % 2 else None
+        c0 = torch.randn(m, n, generator=g)
+        ref = a.double() @ w.double() + (bias.double() if bias is not None else 0.0)
+        ad, wd = a.to(device), wb.to(device)
+        bd = bias.to(device) if bias is not None else None
+        tol = 1e-6 if k <= 256 else 1e-5
+        y = gemm(ad, wd, b_layout=b_layout, bias=bd)
+        assert oops.relative(y.cpu().numpy(), ref.numpy()) < tol
+        assert torch.equal(gemm(ad, wd, b_layout=b_layout, bias=bd), y)
+        ys = gemm(ad, wd, b_layout=b_layout, bias=bd, epilogue="silu")
+        assert oops.relative(ys.cpu().numpy(), torch.nn.functional.silu(ref).numpy()) < tol
+        out = c0.to(device)
+        gemm(ad, wd, b_layout=b_layout, bias=bd, out=out, accumulate=True)
+        assert oops.relative(out.cpu().numpy(), (ref + c0.double()).numpy()) < tol
+        if m > 40:
+            part = gemm(ad[13:40], wd, b_layout=b_layout, bias=bd)
+            assert torch.equal(part, y[13:40])
+
+
+@pytest.mark.gpu
 def test_gemm_fp32_large_tiles(device):
     """The 10k-atom edge GEMM shape (ragged M, K = 2F+8, N = 4F) takes the 128x128 tile path:
     both B layouts, the bias/SiLU epilogue and accumulate against float64."""
