@@ -32,6 +32,14 @@ constexpr int BM = 128, BN = 128, kThreads = 256;
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// A 16-byte load through the global address space. A pointer whose origin the compiler cannot see
+// (behind an empty asm, a select with another object) is loaded as generic (flat) memory, and a
+// flat load counts against the LDS counter too: every wait for an LDS read would then also wait
+// for it.
+__device__ __forceinline__ bf16x8 load_global(const __bf16* p) {
+  return *(const __attribute__((address_space(1))) bf16x8*)(p);
+}
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 
 template <int WM, int WN>
@@ -1121,14 +1129,14 @@ __global__ void __launch_bounds__(64 * BR_WAVES) __attribute__((amdgpu_waves_per
     const int64_t row0 = rb * BR_ROWS + wave * 32;
     if (row0 >= m) break;  // uniform per wave; the wave's later row blocks start further on
     const __bf16* ap = a + min(row0 + rr, m - 1) * lda + 8 * h;
+    // every load unconditional (the zero chunk past K) and in one straight run: the wait before a
+    // k-step's MFMAs then covers that k-step's load only
     bf16x8 av[NKS];
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      if (ks < nks) {
-        const __bf16* src = 16 * ks + 8 * h < k ? ap + 16 * ks : zero;
-        asm volatile("" : "+v"(src));  // one load with a per-lane address, no branch
-        av[ks] = *reinterpret_cast<const bf16x8*>(src);
-      }
+      const __bf16* src = 16 * ks + 8 * h < k ? ap + 16 * ks : zero;
+      asm volatile("" : "+v"(src));  // one load with a per-lane address, no branch
+      av[ks] = load_global(src);
     }
     // the slabs one after the other on the same A registers (one accumulator set live)
 #pragma unroll 1
@@ -1152,13 +1160,12 @@ __global__ void __launch_bounds__(64 * BR_WAVES) __attribute__((amdgpu_waves_per
             acc[cb / 2][0][cb % 2] =
                 __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[ks], bv, acc[cb / 2][0][cb % 2], 0, 0, 0);
           }
-          if constexpr (KR == 2) {
-            if (NKS + ks < nks) {
-              const __bf16* src = 16 * (NKS + ks) + 8 * h < k ? ap + 16 * (NKS + ks) : zero;
-              asm volatile("" : "+v"(src));
-              av[ks] = *reinterpret_cast<const bf16x8*>(src);
-            }
-          }
+        }
+        if constexpr (KR == 2) {
+          // k-step NKS + ks into the register k-step ks has just been used from
+          const __bf16* src = 16 * (NKS + ks) + 8 * h < k ? ap + 16 * (NKS + ks) : zero;
+          asm volatile("" : "+v"(src));
+          av[ks] = load_global(src);
         }
       }
       if constexpr (KR == 2) {
