@@ -264,7 +264,8 @@ def _gpu_builder(s, u_cap, device):
     ((10, 10, 10), 128, None, False, "cubic"),
     (3, 128, None, False, "triclinic_rotated"), ((6, 6, 6), 128, None, False, "triclinic_rotated"),
     ((6, 6, 6), 128, 0, False, "triclinic_rotated"), ((6, 6, 6), 64, 10 ** 9, False, "cubic"),
-    ((10, 10, 20), 128, None, False, "cubic"), ((10, 10, 20), 128, 0, False, "cubic")])
+    ((10, 10, 20), 128, None, False, "cubic"), ((10, 10, 20), 128, 0, False, "cubic"),
+    ((15, 15, 15), 128, None, False, "cubic")])
 def test_mace_like_gpu_matches_oracle(device, n_cells, channels, hoist, fused, geometry, monkeypatch):
     """Energies within 1e-5 eV/atom and forces within 1e-4 eV/A of the FP64 oracle, through the
     fixed-capacity builder (padding rows present), bitwise reproducible. ``hoist`` None runs the
@@ -274,7 +275,7 @@ def test_mace_like_gpu_matches_oracle(device, n_cells, channels, hoist, fused, g
     fused node kernels or the unfused chain of GEMMs and contraction kernels; at 5 000 atoms the
     unfused node GEMMs take their split-plane grouped form. ``triclinic_rotated`` puts the crystal
     in a sheared cell rotated as a whole (no cell axis along x, y or z); 10 x 10 x 20 cells is the
-    10 000-atom headline system."""
+    10 000-atom headline system, 15 x 15 x 15 cells (16 875 atoms) a system above it."""
     from fastmd_amd.engine.energy_derivative import EnergyDerivative
     from fastmd_amd.models import mace_like
     from fastmd_amd.models.mace_like import MaceLikeAdapter
