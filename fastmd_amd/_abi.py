@@ -77,6 +77,8 @@ SIGNATURES: dict[str, tuple] = {
     "fmd_split3_f32": (ctypes.c_int, [_p, _i64, _i64, _i32, _p, _p]),
     "fmd_gemm_x3_planes_f32": (ctypes.c_int, [_i32, _i32, _p, _p, _p, _p, _p, _i64, _p, _i64, _i64, _p, _p, _i64,
                                               _i64, _p, _p, _i64, _i64, _i32, _i32, _p]),
+    "fmd_gemm_splitk_x3_planes_f32": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _p, _i64, _p, _p, _i64, _i64, _i64,
+                                                      _i64, _i32, _i32, _p, _p]),
     "fmd_gemm_splitk_f32": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i64, _i64, _i64, _i64,
                                            _i32, _i32, _p, _p]),
     "fmd_gemm_gather_f32": (ctypes.c_int, [_i32, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _p, _i64, _i64, _p, _p, _i64,

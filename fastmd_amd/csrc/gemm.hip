@@ -1574,6 +1574,58 @@ int fmd_gemm_splitk_f32(const float* a, int64_t lda, const float* a2, int64_t ld
   return FMD_OK;
 }
 
+int fmd_gemm_splitk_x3_planes_f32(const float* a, int64_t lda, const float* a2, int64_t lda2, int64_t ksplit,
+                                  const uint16_t* b_planes, int64_t ldb, const float* bias, float* c, int64_t ldc,
+                                  int64_t m, int64_t n, int64_t k, int32_t accumulate, int32_t splits,
+                                  float* workspace, hipStream_t stream) {
+  FMD_REQUIRE(m >= 0 && n >= 0 && k > 0 && splits >= 1 && splits <= kMaxGroup);
+  if (m == 0 || n == 0) return FMD_OK;
+  FMD_REQUIRE(a && b_planes && c && workspace && ldc >= n && k % splits == 0 && ldb == 48 * fmd_cdiv(k, 16));
+  const int64_t ks = k / splits, ksp = a2 ? ksplit : k;
+  FMD_REQUIRE(ks % 16 == 0 && ksp % ks == 0 && lda >= ksp && (!a2 || (ksp < k && lda2 >= k - ksp)));
+  FMD_REQUIRE(aligned16(a) && lda % 4 == 0 && aligned16(b_planes) && (!a2 || (aligned16(a2) && lda2 % 4 == 0)));
+  FMD_REQUIRE(fmd_cdiv(m, 64) * fmd_cdiv(n, 128) * splits < (int64_t(1) << 31));
+  // split s: columns [s ks, (s + 1) ks) of [a | a2] against the same slices of B's planes (16-k
+  // slices of 48 bf16 per B row), into workspace slice s
+  X3PGroup grp{};
+  grp.act = 0;
+  int64_t big = 0;
+  for (int sp = 0; sp < splits; ++sp) {
+    X3PGroupDesc& d = grp.d[grp.count++];
+    const int64_t k0 = sp * ks;
+    d.p0 = k0 < ksp ? X3PPart{a + k0, nullptr, lda, 1, (int32_t)ks} : X3PPart{a2 + (k0 - ksp), nullptr, lda2, 1, (int32_t)ks};
+    d.p1 = X3PPart{};
+    d.np = 1;
+    d.b = reinterpret_cast<const __bf16*>(b_planes) + (k0 / 16) * 48;
+    d.bias = nullptr;
+    d.c = workspace + sp * m * n;
+    d.ldb = ldb;
+    d.ldc = n;
+    d.m = m;
+    d.n = n;
+    d.k = ks;
+    d.n_tiles = fmd_cdiv(n, 128);
+    d.accumulate = 0;
+    d.radd = X3Part{};
+    big += fmd_cdiv(m, 128) * d.n_tiles;
+  }
+  const int mb = big < kGroupX3HalfTilesBelow ? 1 : 2;
+  int64_t t0 = 0;
+  for (int g = 0; g < grp.count; ++g) {
+    grp.d[g].tile0 = t0;
+    t0 += fmd_cdiv(m, 64 * mb) * grp.d[g].n_tiles;
+  }
+  if (mb == 1)
+    hipLaunchKernelGGL(gemm_x3p_group_kernel<1>, dim3((unsigned)t0), dim3(kThreads), 0, stream, grp);
+  else
+    hipLaunchKernelGGL(gemm_x3p_group_kernel<2>, dim3((unsigned)t0), dim3(kThreads), 0, stream, grp);
+  FMD_CHECK_LAUNCH();
+  hipLaunchKernelGGL(splitk_sum_kernel, dim3((unsigned)fmd_cdiv(m * n, 256)), dim3(256), 0, stream, workspace, splits, m,
+                     n, bias, c, ldc, accumulate);
+  FMD_CHECK_LAUNCH();
+  return FMD_OK;
+}
+
 int fmd_gemm_gather_f32(int32_t n_parts, const float* const* srcs, const int32_t* const* indices,
                         const int64_t* index_strides, const int64_t* lds, const int32_t* widths, int64_t m,
                         const float* b, int64_t ldb, const float* row_add, const int32_t* row_add_index,

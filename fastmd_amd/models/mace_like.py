@@ -334,6 +334,16 @@ class MaceLike(nn.Module):
             cache[t] = hit
         return hit[1]
 
+    def w1_node_blocks_planes(self, t: int):
+        """The bf16 planes of ``w1_node_blocks(t)`` (split once per weight version)."""
+        w = self.w1_node_blocks(t)
+        cache = self.__dict__.setdefault("_w1nb_planes", {})
+        hit = cache.get(t)
+        if hit is None or hit[0] is not w:
+            hit = (w, split_planes(w))
+            cache[t] = hit
+        return hit[1]
+
     @property
     def num_interactions(self) -> int:
         return self.config.num_interactions
@@ -778,7 +788,10 @@ def _vjp(ctx, gE: Tensor | None, sign: float, stress_cell: Tensor | None = None)
         _call_groups("fmd_mace_message_bwd_f32", groups, 8, *head, gzs_src.data_ptr(), ggeo.data_ptr(), acc_geo,
                      g_in0.data_ptr(), _abi.ptr(g_in1), 1, *tail)
         # g_in0 += [gzs_src | gzs] [W1[:C] | W1[C:2C]]^T (sender and receiver blocks, one node GEMM)
-        gemm_splitk(gzs_src, model.w1_node_blocks(t), b_layout=0, out=g_in0, a2=gzs, accumulate=True)
+        # (as four K slices of one split-plane group, the weights split once: 20 us per step less at
+        # 10 000 atoms than eight fp32 MFMA slices)
+        gemm_splitk(gzs_src, model.w1_node_blocks(t), b_layout=0, out=g_in0, a2=gzs, accumulate=True,
+                    b_planes=model.w1_node_blocks_planes(t))
         gefs.append((gef, nb))
         g_out0, g_out1 = g_in0, g_in1
     gvec = _empty(e_cap, 3, device=dev)

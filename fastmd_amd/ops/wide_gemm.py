@@ -189,13 +189,20 @@ def gemm_group(problems, *, b_layout: int, epilogue: str | None = None) -> list:
 
 
 def gemm_splitk(a: Tensor, b: Tensor, *, b_layout: int, out: Tensor, a2: Tensor | None = None,
-                bias: Tensor | None = None, accumulate: bool = False, splits: int = 8) -> Tensor:
+                bias: Tensor | None = None, accumulate: bool = False, splits: int = 8,
+                b_planes: "Planes | None" = None) -> Tensor:
     """``out (+)= [a | a2] @ op(b) (+ bias)`` with K cut into ``splits`` slices multiplied by separate
     workgroups and summed in slice order (fmd_gemm_splitk_f32): tall-K, few-tile GEMMs. Products
     of fewer than ``GROUP_KS_MAX_TILES`` 64 x 64 tiles (b_layout 0) run as a one-problem K-split
-    group instead (one launch, no workspace)."""
+    group instead (one launch, no workspace). With ``b_planes`` (``split_planes(b)``, b_layout 0)
+    and a large enough product: four (or two) K slices as split-plane problems of one grouped
+    launch, summed in order (fmd_gemm_splitk_x3_planes_f32)."""
     require_cuda(a, b, out, a2, bias)
     n_out = b.shape[0] if b_layout == 0 else b.shape[1]
+    if b_planes is not None and b_layout == 0 and -(-a.shape[0] // 64) * -(-n_out // 64) >= GROUP_KS_MAX_TILES:
+        done = _splitk_planes(a, b_planes, out, a2, bias, accumulate)
+        if done:
+            return out
     if b_layout == 0 and -(-a.shape[0] // 64) * -(-n_out // 64) < GROUP_KS_MAX_TILES and (
             a2 is None or a.shape[1] % 32 == 0):
         prob = {"a": a, "b": b, "out": out, "accumulate": accumulate}
@@ -226,6 +233,31 @@ def gemm_splitk(a: Tensor, b: Tensor, *, b_layout: int, out: Tensor, a2: Tensor 
               _abi.ptr(bias), out.data_ptr(), out.stride(0) if m > 1 else n, m, n, k, 1 if accumulate else 0, splits,
               ws.data_ptr(), stream())
     return out
+
+
+def _splitk_planes(a, planes, out, a2, bias, accumulate) -> bool:
+    """fmd_gemm_splitk_x3_planes_f32 when the layout allows it (else False, nothing launched)."""
+    a, lda = rows_view(a)
+    m, ka = a.shape
+    k = ka + (a2.shape[1] if a2 is not None else 0)
+    n = out.shape[1]
+    if planes.width != k or planes.data.shape[0] != n or out.shape[0] != m or out.stride(1) != 1:
+        raise ValueError("gemm_splitk: b_planes do not match")
+    lda2 = 0
+    if a2 is not None:
+        a2, lda2 = rows_view(a2)
+    splits = next((s for s in (4, 2) if k % s == 0 and (k // s) % 16 == 0 and ka % (k // s) == 0), 0)
+    ok = (splits and lda % 4 == 0 and a.data_ptr() % 16 == 0 and
+          (a2 is None or (lda2 % 4 == 0 and a2.data_ptr() % 16 == 0)))
+    if not ok:
+        return False
+    ws = torch.empty((splits, m, n), dtype=torch.float32, device=out.device)
+    if bias is not None:
+        bias = bias.contiguous()
+    _abi.call("fmd_gemm_splitk_x3_planes_f32", a.data_ptr(), lda, _abi.ptr(a2), lda2, ka, planes.data.data_ptr(),
+              48 * planes.data.shape[1], _abi.ptr(bias), out.data_ptr(), out.stride(0) if m > 1 else n, m, n, k,
+              1 if accumulate else 0, splits, ws.data_ptr(), stream())
+    return True
 
 
 class Planes:

@@ -440,6 +440,18 @@ int fmd_gemm_splitk_f32(const float* a, int64_t lda, const float* a2, int64_t ld
                         int64_t ldb, int32_t b_layout, const float* bias, float* c, int64_t ldc, int64_t m, int64_t n,
                         int64_t k, int32_t accumulate, int32_t splits, float* workspace, hipStream_t stream);
 
+/* The same K-split product in the split-plane form: B given as its bf16 planes (fmd_split3_f32
+ * of the [N, K] weight, ldb = 48 ceil(K / 16)); split s (splits <= 4, K / splits a multiple of
+ * 16 that does not straddle [a | a2]) multiplies its K slice as problem s of one grouped
+ * split-plane launch into workspace [splits, M, N], then the slices are summed in order (+ bias)
+ * (+ C). fp32-accurate (six bf16 plane products), deterministic. 16-byte aligned A rows with
+ * lda % 4 == 0. Replaces the reference's matmul (triton_wide_gemm.py:542-553) for the tall-K node
+ * GEMM of the MACE-like VJP. */
+int fmd_gemm_splitk_x3_planes_f32(const float* a, int64_t lda, const float* a2, int64_t lda2, int64_t ksplit,
+                                  const uint16_t* b_planes, int64_t ldb, const float* bias, float* c, int64_t ldc,
+                                  int64_t m, int64_t n, int64_t k, int32_t accumulate, int32_t splits,
+                                  float* workspace, hipStream_t stream);
+
 /* C[M,N] = A[M,K] B[N,K]^T (+ bias) (+ C) with the gather-cat fused into the operand load:
  * A = cat(part_0, ..., part_{n-1}) over n_parts <= 3 column blocks, part p reading row
  * indices_p[r * index_strides_p] of srcs_p (or row r when indices_p is null), width widths_p,

@@ -695,6 +695,38 @@ def test_gemm_splitk_against_fp64_and_run_to_run(device, b_layout):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("m,ka,kb,n", [(10000, 512, 512, 128), (40000, 256, 256, 64), (20011, 1024, 0, 200)])
+def test_gemm_splitk_split_planes(device, m, ka, kb, n):
+    """fmd_gemm_splitk_x3_planes_f32 through gemm_splitk(b_planes=...): [a | a2] @ B^T with K cut
+    into four slices of one grouped split-plane launch, summed in order, accumulate and bias:
+    within 1e-5 of float64 and run-to-run bitwise (each split writes its own workspace slice)."""
+    import torch
+
+    from fastmd_amd.ops.wide_gemm import gemm_splitk, split_planes
+
+    print(f"[splitk planes] m={m} ka={ka} kb={kb} n={n}", flush=True)
+    g = torch.Generator().manual_seed(m + n)
+    k = ka + kb
+    a = torch.randn(m, ka, generator=g)
+    a2 = torch.randn(m, kb, generator=g) if kb else None
+    w = torch.randn(n, k, generator=g) / k ** 0.5
+    bias = torch.randn(n, generator=g)
+    c0 = torch.randn(m, n, generator=g)
+    full = a if a2 is None else torch.cat([a, a2], 1)
+    ref = full.double() @ w.double().t() + bias.double() + c0.double()
+    wd = w.to(device)
+    planes = split_planes(wd)
+    outs = []
+    for _ in range(2):
+        out = c0.to(device)
+        gemm_splitk(a.to(device), wd, b_layout=0, out=out, a2=a2.to(device) if a2 is not None else None,
+                    bias=bias.to(device), accumulate=True, b_planes=planes)
+        outs.append(out)
+    assert oops.relative(outs[0].cpu().numpy(), ref.numpy()) < 1e-5
+    assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.gpu
 def test_gemm_planes_bitwise_equal_to_in_kernel_split(device):
     """fmd_split3_f32 gives x = p0 + p1 + p2 exactly (zero padding past the width), and the GEMM on
     pre-split planes (A gathered from plane rows, or fp32 A with pre-split B) is bitwise the GEMM
