@@ -1138,8 +1138,10 @@ __global__ void __launch_bounds__(64 * BR_WAVES) __attribute__((amdgpu_waves_per
       asm volatile("" : "+v"(src));  // one load with a per-lane address, no branch
       av[ks] = load_global(src);
     }
-    // the slabs one after the other on the same A registers (one accumulator set live)
-#pragma unroll 1
+    // the slabs one after the other on the same A registers (one accumulator set live); unrolled,
+    // so that the first slab's MFMAs wait for their own k-step's load only (a loop header makes the
+    // compiler wait for every A load)
+#pragma unroll
     for (int sl = 0; sl < NSL; ++sl) {
       const int64_t col0 = col_blk + (int64_t)sl * NB;
       if (col0 >= n) break;
