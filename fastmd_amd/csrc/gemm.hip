@@ -1305,9 +1305,10 @@ int launch_gemm_x3(int32_t n_parts, const float* const* srcs, const int32_t* con
   return FMD_OK;
 }
 
-// Grouped split-plane launches use 64-row tiles below this many tiles of 128 x 128 (three
-// workgroups per CU).
-constexpr int64_t kGroupX3HalfTilesBelow = 3 * 256;
+// Grouped split-plane launches use 64-row tiles below this many tiles of 128 x 128 (eight per CU;
+// the MACE-like merged node group at 10 000 / 16 875 / 40 000 atoms, 946 to 3 755 such tiles, ran
+// 16 / 9 / 20 us per step faster on 64-row tiles than with the switch at three per CU).
+constexpr int64_t kGroupX3HalfTilesBelow = 8 * 256;
 
 // Tile choice: 128 x 128 when that still gives two workgroups per CU (256 CUs), else 64 x 64
 // (small node-side GEMMs and the 135-atom edge GEMM: 4x more workgroups, 4x less serial K work

@@ -472,13 +472,14 @@ def test_gemm_group_split_plane_form(device):
     single = d(c1)
     gemm(d(torch.cat([a0, a1], 1)), d(w1), b_layout=0, out=single, accumulate=True, bias=d(bias))
     assert torch.equal(out1, single)
-    # 128-row tiles once a group has three per CU (782 here): the same bits as the 64-row form
-    a2 = torch.randn(100000, C, generator=g)
-    out2 = torch.empty(100000, C, device=device)
-    gemm_group([{"a": d(a2), "b": d(w0), "b_planes": split_planes(d(w0)), "out": out2}], b_layout=0)
-    assert torch.equal(out2, gemm(d(a2), d(w0), b_layout=0))
-    assert torch.equal(out2[:33000], gemm(d(a2[:33000]), d(w0), b_layout=0))
-    assert oops.relative(out2.cpu().numpy(), (a2.double() @ w0.double().t()).numpy()) < 1e-5
+    # 128-row tiles once a group has eight per CU (2 188 here): the same bits as the 64-row form
+    a2 = torch.randn(140000, C, generator=g)
+    w2 = torch.randn(2 * C, C, generator=g) / C ** 0.5
+    out2 = torch.empty(140000, 2 * C, device=device)
+    gemm_group([{"a": d(a2), "b": d(w2), "b_planes": split_planes(d(w2)), "out": out2}], b_layout=0)
+    assert torch.equal(out2, gemm(d(a2), d(w2), b_layout=0))
+    assert torch.equal(out2[:33000], gemm(d(a2[:33000]), d(w2), b_layout=0))
+    assert oops.relative(out2.cpu().numpy(), (a2.double() @ w2.double().t()).numpy()) < 1e-5
     # without planes: the fp32 tiles (within fp32 rounding of the same product, not its bits)
     out0f = torch.empty(33000, C, device=device)
     gemm_group([{"a": d(a0), "b": d(w0), "out": out0f}], b_layout=0)
