@@ -26,12 +26,17 @@ constexpr int kWaves = kThreads / FMD_WAVE;
 // for another to publish the momentum scale factor. The loops run over the constant index range
 // of the arrays with the chain length M as a predicate: every array access has a constant index
 // and the arrays stay in registers (one spare slot for the j + 1 read of the last link). The
-// masses Q are read from the constants vector (uniform loads; only Q[0 .. M-1] are read).
+// chain masses Q and the Suzuki-Yoshida constants are read from the constants vector once, at
+// the start of a kernel (uniform loads ahead of its stores): the chain, a serial sequence of
+// float64 divisions and exponentials, then waits on no memory.
 struct Chain {
-  double eta[kMaxChain + 1], pe[kMaxChain + 1];
-  const double* Q;
+  double eta[kMaxChain + 1], pe[kMaxChain + 1], Q[kMaxChain + 1];
+  double kT, ndof_kT;
+  double delta[3], delta2[3], neg_delta4[3], neg_delta[3];  // per Suzuki-Yoshida sub-step
   int M;
 };
+
+__device__ __forceinline__ double sub_step(const double (&v)[3], int k) { return k == 0 ? v[0] : k == 1 ? v[1] : v[2]; }
 
 __device__ __forceinline__ double block_sum(double v, double* red) {
   v = wave_sum(v);
@@ -46,8 +51,7 @@ __device__ __forceinline__ double block_sum(double v, double* red) {
 }
 
 // ASE _integrate_p_eta_j; j is a constant after unrolling
-__device__ __forceinline__ void p_eta_j(Chain& c, int j, double ke2, double kT, double ndof_kT, double delta2,
-                                        double neg_delta4) {
+__device__ __forceinline__ void p_eta_j(Chain& c, int j, double ke2, double delta2, double neg_delta4) {
   double pj = c.pe[j];
   double s = 1.0;
   const bool inner = j < c.M - 1;
@@ -57,22 +61,35 @@ __device__ __forceinline__ void p_eta_j(Chain& c, int j, double ke2, double kT, 
   }
   double g;
   if (j == 0)
-    g = ke2 - ndof_kT;
+    g = ke2 - c.ndof_kT;
   else
-    g = (c.pe[j - 1] * c.pe[j - 1]) / c.Q[j - 1] - kT;
+    g = (c.pe[j - 1] * c.pe[j - 1]) / c.Q[j - 1] - c.kT;
   pj = pj + delta2 * g;
   if (inner) pj = pj * s;
   c.pe[j] = pj;
 }
 
+// consts: [dt, dt/2, kT, ndof kT, 3 x (delta, delta/2, -delta/4, -delta), Q[0 .. M-1], ...];
+// links past M load link M - 1 (in bounds) and hold zeros
 __device__ __forceinline__ void load_chain(Chain& c, int M, const double* eta, const double* pe,
                                            const double* consts) {
   c.M = M;
-  c.Q = consts + 16;
+  c.kT = consts[2];
+  c.ndof_kT = consts[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    c.delta[k] = consts[4 + 4 * k];
+    c.delta2[k] = consts[5 + 4 * k];
+    c.neg_delta4[k] = consts[6 + 4 * k];
+    c.neg_delta[k] = consts[7 + 4 * k];
+  }
 #pragma unroll
   for (int j = 0; j <= kMaxChain; ++j) {
-    c.eta[j] = j < M ? eta[j] : 0.0;
-    c.pe[j] = j < M ? pe[j] : 0.0;
+    const int jj = j < M ? j : M - 1;
+    const double e = eta[jj], p = pe[jj];
+    c.Q[j] = consts[16 + jj];
+    c.eta[j] = j < M ? e : 0.0;
+    c.pe[j] = j < M ? p : 0.0;
   }
 }
 
@@ -88,13 +105,12 @@ __device__ __forceinline__ void store_chain(const Chain& c, double* eta, double*
 
 // Suzuki-Yoshida sub-step k before the momentum scaling: the p_eta_j sweep backward (j = M-1 .. 0),
 // the eta update; returns the momentum scale factor exp(-delta p_eta_0 / Q_0)
-__device__ __forceinline__ double chain_before_scale(Chain& c, double ke2, const double* consts, int k) {
-  const double kT = consts[2], ndof_kT = consts[3];
-  const double delta = consts[4 + 4 * k], delta2 = consts[5 + 4 * k];
-  const double neg_delta4 = consts[6 + 4 * k], neg_delta = consts[7 + 4 * k];
+__device__ __forceinline__ double chain_before_scale(Chain& c, double ke2, int k) {
+  const double delta = sub_step(c.delta, k), delta2 = sub_step(c.delta2, k);
+  const double neg_delta4 = sub_step(c.neg_delta4, k), neg_delta = sub_step(c.neg_delta, k);
 #pragma unroll
   for (int j = kMaxChain - 1; j >= 0; --j)
-    if (j < c.M) p_eta_j(c, j, ke2, kT, ndof_kT, delta2, neg_delta4);
+    if (j < c.M) p_eta_j(c, j, ke2, delta2, neg_delta4);
 #pragma unroll
   for (int j = 0; j < kMaxChain; ++j)
     if (j < c.M) c.eta[j] = c.eta[j] + (delta * c.pe[j]) / c.Q[j];
@@ -102,18 +118,18 @@ __device__ __forceinline__ double chain_before_scale(Chain& c, double ke2, const
 }
 
 // ... and after it, with the new ke2: the p_eta_j sweep forward (j = 0 .. M-1)
-__device__ __forceinline__ void chain_after_scale(Chain& c, double ke2, const double* consts, int k) {
-  const double kT = consts[2], ndof_kT = consts[3];
-  const double delta2 = consts[5 + 4 * k], neg_delta4 = consts[6 + 4 * k];
+__device__ __forceinline__ void chain_after_scale(Chain& c, double ke2, int k) {
+  const double delta2 = sub_step(c.delta2, k), neg_delta4 = sub_step(c.neg_delta4, k);
 #pragma unroll
   for (int j = 0; j < kMaxChain; ++j)
-    if (j < c.M) p_eta_j(c, j, ke2, kT, ndof_kT, delta2, neg_delta4);
+    if (j < c.M) p_eta_j(c, j, ke2, delta2, neg_delta4);
 }
 
 // Momentum storage: registers (KPT > 0) or global memory (KPT == 0).
 template <int KPT>
 struct Momenta {
   double p[KPT > 0 ? KPT : 1][3];
+  double mv[KPT > 0 ? KPT : 1];  // the atoms' masses (registers: ke2 is summed once per sub-step)
   double* gp;
   const double* m;
   int64_t n;
@@ -128,6 +144,7 @@ struct Momenta {
         const int64_t a = threadIdx.x + (int64_t)r * blockDim.x;
 #pragma unroll
         for (int d = 0; d < 3; ++d) p[r][d] = a < n ? p_ptr[3 * a + d] : 0.0;
+        mv[r] = a < n ? masses[a] : 1.0;
       }
     }
   }
@@ -165,13 +182,18 @@ struct Momenta {
 
 template <int KPT>
 __device__ double ke2_of(Momenta<KPT>& mom, double* red) {
+  static_assert(KPT > 0, "the single-workgroup kernels keep the momenta in registers");
   double s = 0.0;
-  mom.for_each([&](int64_t a, double (&p)[3]) {
-    const double m = mom.m[a];
+#pragma unroll
+  for (int r = 0; r < KPT; ++r) {
+    const int64_t a = threadIdx.x + (int64_t)r * blockDim.x;
+    if (a >= mom.n) continue;
+    const double(&p)[3] = mom.p[r];
+    const double m = mom.mv[r];
     s = s + (p[0] * p[0]) / m;
     s = s + (p[1] * p[1]) / m;
     s = s + (p[2] * p[2]) / m;
-  });
+  }
   return block_sum(s, red);
 }
 
@@ -179,17 +201,17 @@ __device__ double ke2_of(Momenta<KPT>& mom, double* red) {
 // ke2 = sum(p*p/m) of the momenta on entry; returns that sum of the momenta on return (the
 // recomputation after the last scaling: a pre half that follows directly starts from it).
 template <int KPT>
-__device__ double nhc_half(Momenta<KPT>& mom, Chain& c, const double* consts, int tloop, double* red, double ke2) {
+__device__ double nhc_half(Momenta<KPT>& mom, Chain& c, int tloop, double* red, double ke2) {
   for (int tl = 0; tl < tloop; ++tl) {
     for (int k = 0; k < 3; ++k) {
-      const double scale = chain_before_scale(c, ke2, consts, k);
+      const double scale = chain_before_scale(c, ke2, k);
       mom.for_each([&](int64_t, double (&p)[3]) {
         p[0] = p[0] * scale;
         p[1] = p[1] * scale;
         p[2] = p[2] * scale;
       });
       ke2 = ke2_of(mom, red);
-      chain_after_scale(c, ke2, consts, k);
+      chain_after_scale(c, ke2, k);
     }
   }
   return ke2;
@@ -209,7 +231,7 @@ __global__ void __launch_bounds__(kThreads) nhc_pre_kernel(double* q, double* p,
   load_chain(c, M, eta, pe, consts);
   Momenta<KPT> mom;
   mom.load(p, masses, n);
-  nhc_half(mom, c, consts, tloop, red, ke2_of(mom, red));
+  nhc_half(mom, c, tloop, red, ke2_of(mom, red));
   const double dt = consts[0], dt2 = consts[1];
   mom.for_each([&](int64_t a, double (&pv)[3]) {
     const double m = masses[a];
@@ -243,7 +265,7 @@ __global__ void __launch_bounds__(kThreads) nhc_post_kernel(double* p, const voi
       f_cache[3 * a + d] = fv;
     }
   });
-  nhc_half(mom, c, consts, tloop, red, ke2_of(mom, red));
+  nhc_half(mom, c, tloop, red, ke2_of(mom, red));
   mom.store();
   if (threadIdx.x == 0) store_chain(c, eta, pe);
   if (threadIdx.x == 0 && e_kind != 0)
@@ -276,10 +298,10 @@ __global__ void __launch_bounds__(kThreads) nhc_post_pre_kernel(double* q, doubl
       f_cache[3 * a + d] = fv;
     }
   });
-  const double ke2 = nhc_half(mom, c, consts, tloop, red, ke2_of(mom, red));
+  const double ke2 = nhc_half(mom, c, tloop, red, ke2_of(mom, red));
   if (threadIdx.x == 0 && e_kind != 0)
     e_out[0] = e_kind == 2 ? static_cast<const double*>(e_in)[0] : (double)static_cast<const float*>(e_in)[0];
-  nhc_half(mom, c, consts, tloop, red, ke2);  // the same momenta: the post half's last sum
+  nhc_half(mom, c, tloop, red, ke2);  // the same momenta: the post half's last sum
   mom.for_each([&](int64_t a, double (&pv)[3]) {
     const double m = masses[a];
 #pragma unroll
@@ -331,10 +353,10 @@ __device__ __forceinline__ void mb_chain(double* eta, double* pe, const double* 
   int ns = 0;
   for (int tl = 0; tl < tloop; ++tl) {
     for (int k = 0; k < 3; ++k) {
-      const double scale = chain_before_scale(c, ke2, consts, k);
+      const double scale = chain_before_scale(c, ke2, k);
       work[ns++] = scale;
       ke2 = ke2 * (scale * scale);
-      chain_after_scale(c, ke2, consts, k);
+      chain_after_scale(c, ke2, k);
     }
   }
   store_chain(c, eta, pe);
