@@ -256,6 +256,66 @@ __global__ void splitk_sum_kernel(const float* __restrict__ ws, int splits, int6
   *d = accumulate ? *d + x : x;
 }
 
+// The same sums for S slices, four columns per thread (N, ldc multiples of 4, 16-byte aligned
+// workspace and C, M N < 2^32): the S loads all in flight before the adds, which run in slice
+// order as above (the same bits).
+template <int S>
+__global__ void __launch_bounds__(256) splitk_sum4_kernel(const float* __restrict__ ws, uint32_t m, uint32_t n,
+                                                          const float* __restrict__ bias, float* c, int64_t ldc,
+                                                          int accumulate) {
+  const uint32_t id = 4u * (blockIdx.x * 256u + threadIdx.x);
+  const uint32_t mn = m * n;
+  if (id >= mn) return;
+  const uint32_t r = id / n, col = id - r * n;
+  float4 v[S];
+#pragma unroll
+  for (int sp = 0; sp < S; ++sp) v[sp] = *reinterpret_cast<const float4*>(ws + (size_t)sp * mn + id);
+  float4 x = v[0];
+#pragma unroll
+  for (int sp = 1; sp < S; ++sp) {
+    x.x += v[sp].x;
+    x.y += v[sp].y;
+    x.z += v[sp].z;
+    x.w += v[sp].w;
+  }
+  if (bias) {
+    const float4 b = *reinterpret_cast<const float4*>(bias + col);
+    x.x += b.x;
+    x.y += b.y;
+    x.z += b.z;
+    x.w += b.w;
+  }
+  float4* d = reinterpret_cast<float4*>(c + (int64_t)r * ldc + col);
+  if (accumulate) {
+    const float4 o = *d;
+    x.x = o.x + x.x;
+    x.y = o.y + x.y;
+    x.z = o.z + x.z;
+    x.w = o.w + x.w;
+  }
+  *d = x;
+}
+
+void launch_splitk_sum(const float* ws, int splits, int64_t m, int64_t n, const float* bias, float* c, int64_t ldc,
+                       int accumulate, hipStream_t stream) {
+  const auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const bool vec = n % 4 == 0 && ldc % 4 == 0 && m * n < (int64_t(1) << 32) && aligned(ws) && aligned(c) &&
+                   (!bias || aligned(bias)) && (splits == 2 || splits == 4 || splits == 8);
+  if (!vec) {
+    hipLaunchKernelGGL(splitk_sum_kernel, dim3((unsigned)fmd_cdiv(m * n, 256)), dim3(256), 0, stream, ws, splits, m,
+                       n, bias, c, ldc, accumulate);
+    return;
+  }
+  const dim3 grid((unsigned)fmd_cdiv(m * n, 4 * 256));
+  const uint32_t mu = (uint32_t)m, nu = (uint32_t)n;
+  if (splits == 2)
+    hipLaunchKernelGGL(splitk_sum4_kernel<2>, grid, dim3(256), 0, stream, ws, mu, nu, bias, c, ldc, accumulate);
+  else if (splits == 4)
+    hipLaunchKernelGGL(splitk_sum4_kernel<4>, grid, dim3(256), 0, stream, ws, mu, nu, bias, c, ldc, accumulate);
+  else
+    hipLaunchKernelGGL(splitk_sum4_kernel<8>, grid, dim3(256), 0, stream, ws, mu, nu, bias, c, ldc, accumulate);
+}
+
 template <int BLAYOUT>
 __global__ void __launch_bounds__(kThreads) gemm_f32_group_kernel(const GemmGroup grp) {
   const int64_t w = blockIdx.x;
@@ -1571,8 +1631,7 @@ int fmd_gemm_splitk_f32(const float* a, int64_t lda, const float* a2, int64_t ld
     hipLaunchKernelGGL(gemm_f32_splitk_kernel<1>, dim3((unsigned)(tiles * splits)), dim3(kThreads), 0, stream, a, lda,
                        a2p, lda2p, ksp, b, ldb, workspace, m, n, ks, tiles_n, tiles);
   FMD_CHECK_LAUNCH();
-  hipLaunchKernelGGL(splitk_sum_kernel, dim3((unsigned)fmd_cdiv(m * n, 256)), dim3(256), 0, stream, workspace, splits, m,
-                     n, bias, c, ldc, accumulate);
+  launch_splitk_sum(workspace, splits, m, n, bias, c, ldc, accumulate, stream);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
@@ -1623,8 +1682,7 @@ int fmd_gemm_splitk_x3_planes_f32(const float* a, int64_t lda, const float* a2, 
   else
     hipLaunchKernelGGL(gemm_x3p_group_kernel<2>, dim3((unsigned)t0), dim3(kThreads), 0, stream, grp);
   FMD_CHECK_LAUNCH();
-  hipLaunchKernelGGL(splitk_sum_kernel, dim3((unsigned)fmd_cdiv(m * n, 256)), dim3(256), 0, stream, workspace, splits, m,
-                     n, bias, c, ldc, accumulate);
+  launch_splitk_sum(workspace, splits, m, n, bias, c, ldc, accumulate, stream);
   FMD_CHECK_LAUNCH();
   return FMD_OK;
 }
