@@ -328,6 +328,14 @@ __global__ void __launch_bounds__(kThreads) nhc_post_pre_kernel(double* q, doubl
 constexpr int kMbThreads = 256;
 constexpr int kMaxScales = 3 * 16;
 
+// p times the nscale factors in sequence; one Suzuki-Yoshida loop (three factors, the usual
+// case) from registers the caller loaded before its atom's loads
+__device__ __forceinline__ double apply_scales(double pv, const double (&s3)[3], int nscale, const double* work) {
+  if (nscale == 3) return ((pv * s3[0]) * s3[1]) * s3[2];
+  for (int k = 0; k < nscale; ++k) pv = pv * work[k];
+  return pv;
+}
+
 __device__ __forceinline__ double block_sum_mb(double v, double* red) {
   v = wave_sum(v);
   const int lane = threadIdx.x & (FMD_WAVE - 1), wave = threadIdx.x / FMD_WAVE;
@@ -413,12 +421,12 @@ __global__ void __launch_bounds__(kMbThreads) nhc_mb_apply_kernel(double* q, dou
   if (a == 0 && e_kind != 0)
     e_out[0] = e_kind == 2 ? static_cast<const double*>(e_in)[0] : (double)static_cast<const float*>(e_in)[0];
   if (a >= n) return;
+  const double s3[3] = {work[0], work[1], work[2]};
   const double m = masses[a];
   const double dt = consts[0], dt2 = consts[1];
 #pragma unroll
   for (int d = 0; d < 3; ++d) {
-    double pv = p[3 * a + d];
-    for (int k = 0; k < nscale; ++k) pv = pv * work[k];
+    double pv = apply_scales(p[3 * a + d], s3, nscale, work);
     if (pre) {
       pv = pv + kick_of(dt2, f[3 * a + d], f32_kick);
       q[3 * a + d] = q[3 * a + d] + (dt * pv) / m;
@@ -443,11 +451,11 @@ __global__ void __launch_bounds__(kMbThreads) nhc_mb_apply_partials_chain_kernel
     e_out[0] = e_kind == 2 ? static_cast<const double*>(e_in)[0] : (double)static_cast<const float*>(e_in)[0];
   double s = 0.0;
   if (a < n) {
+    const double s3[3] = {work[0], work[1], work[2]};
     const double m = masses[a];
 #pragma unroll
     for (int d = 0; d < 3; ++d) {
-      double pv = p[3 * a + d];
-      for (int k = 0; k < nscale; ++k) pv = pv * work[k];
+      const double pv = apply_scales(p[3 * a + d], s3, nscale, work);
       p[3 * a + d] = pv;
       s = s + (pv * pv) / m;
     }
