@@ -1,6 +1,6 @@
 """The operator boundary as the reference's callers use it: ``aligned_gather_cat4`` in its
 six-argument form, the engine's ``OpDispatcher`` entry points, the builders' reference
-defaults, and the reference-side ctypes binding shown in INTEGRATION.md run as written."""
+defaults, and the reference-side ctypes binding of the integration guide run as written."""
 import inspect
 import os
 import re
@@ -301,7 +301,7 @@ def test_builder_reference_defaults_build_a_sink_padded_line_graph(device):
 def _integration_stub():
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     block = re.search(r"```python\n(# fastmd/engine/kernels/hip_backend\.py.*?)```", text, re.S)
-    assert block is not None, "INTEGRATION.md lost its reference-side binding"
+    assert block is not None, "the integration guide lost its reference-side binding"
     return block.group(1)
 
 
@@ -321,7 +321,7 @@ def test_integration_stub_binds_the_header_signatures():
 
 @pytest.mark.gpu
 def test_integration_stub_runs(device):
-    """The INTEGRATION.md binding, executed as written (library path filled in): its segment sum,
+    """The integration guide's binding, executed as written (library path filled in): its segment sum,
     4-part gather-cat and linear agree with this build's operators."""
     import torch
 
